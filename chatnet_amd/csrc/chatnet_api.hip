@@ -1,0 +1,611 @@
+// chatnet_api.hip — the C ABI of libchatnet_hip (declared in include/chatnet_hip.h).
+//
+// Host-side orchestration of the per-token schedule of LlamaModel.Forward
+// (src/ChatNet.Core/Models/Llama/LlamaModel.cs:93-238), five launches per layer:
+//   1. QKV GEMV   : RMSNorm (fused prologue) -> Wq|Wk|Wv -> RoPE -> K/V cache write
+//   2. attention  : GQA decode attention over the cache
+//   3. O GEMV     : x += Wo * attn           (residual fused)
+//   4. gate/up    : RMSNorm -> Wg|Wu -> silu(g)*u
+//   5. down GEMV  : x += Wd * h              (residual fused)
+// then the LM head (final RMSNorm fused) only for the last token of a span.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/chatnet_hip.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                   \
+  do {                                                                                  \
+    hipError_t e_ = (expr);                                                             \
+    if (e_ != hipSuccess) return fail(CHATNET_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+  } while (0)
+
+struct DevTensor {
+  void* ptr = nullptr;
+  uint32_t type = 0;
+  uint64_t nbytes = 0;
+  uint64_t ne0 = 0, ne1 = 1;  // GGUF dims: ne0 = inner (K), ne1 = rows (M)
+};
+
+struct Layer {
+  DevTensor attn_norm, ffn_norm, wq, wk, wv, wo, wg, wu, wd;
+};
+
+int device_cus(int dev) {
+  static int cache[64] = {0};
+  if (dev >= 0 && dev < 64 && cache[dev]) return cache[dev];
+  hipDeviceProp_t p;
+  if (hipGetDeviceProperties(&p, dev) != hipSuccess) return 256;
+  if (dev >= 0 && dev < 64) cache[dev] = p.multiProcessorCount;
+  return p.multiProcessorCount;
+}
+
+bool is_matrix_type(uint32_t t) {
+  return t == CHATNET_GGML_Q4_0 || t == CHATNET_GGML_Q4_K || t == CHATNET_GGML_Q6_K;
+}
+
+}  // namespace
+
+struct chatnet_model {
+  chatnet_config cfg{};
+  int device = 0;
+  int num_cus = 256;
+  int kv_dim = 0;
+  size_t kv_elt = 4;
+  hipStream_t stream = nullptr;
+  DevTensor emb, out, out_norm;
+  std::vector<Layer> layers;
+  void* kcache = nullptr;
+  void* vcache = nullptr;
+  float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr;
+  int* state = nullptr;  // [0] pos, [1] token, [2] step
+  int* out_tokens = nullptr;
+  int out_cap = 0;
+  hipGraphExec_t graph = nullptr;
+  bool have_logits = false;
+  int next_pos = 0;  // position after the last forwarded token
+  int last_tok = 0;  // last forwarded token
+};
+
+extern "C" {
+
+const char* chatnet_last_error(void) { return g_err.c_str(); }
+
+// GgufTensorInfo.ByteSize (src/ChatNet.Core/Gguf/GgufTensorInfo.cs:30-113).
+uint64_t chatnet_tensor_nbytes(uint32_t t, uint64_t n) {
+  auto blocks = [n](uint64_t b) { return (n + b - 1) / b; };
+  switch (t) {
+    case 0: return n * 4;                 // F32
+    case 1: return n * 2;                 // F16
+    case 2: return blocks(32) * 18;       // Q4_0
+    case 3: return blocks(32) * 20;       // Q4_1
+    case 6: return blocks(32) * 22;       // Q5_0
+    case 7: return blocks(32) * 24;       // Q5_1
+    case 8: return blocks(32) * 34;       // Q8_0
+    case 9: return blocks(32) * 36;       // Q8_1
+    case 10: return blocks(256) * 84;     // Q2_K
+    case 11: return blocks(256) * 110;    // Q3_K
+    case 12: return blocks(256) * 144;    // Q4_K
+    case 13: return blocks(256) * 176;    // Q5_K
+    case 14: return blocks(256) * 210;    // Q6_K
+    case 15: return blocks(256) * 292;    // Q8_K
+    case 16: return blocks(256) * 66;     // IQ2_XXS
+    case 17: return blocks(256) * 74;     // IQ2_XS
+    case 18: return blocks(256) * 98;     // IQ3_XXS
+    case 19: return blocks(256) * 50;     // IQ1_S
+    case 20: return blocks(32) * 18;      // IQ4_NL
+    case 21: return blocks(256) * 110;    // IQ3_S
+    case 22: return blocks(256) * 82;     // IQ2_S
+    case 23: return blocks(256) * 136;    // IQ4_XS
+    case 24: return n;                    // I8
+    case 25: return n * 2;                // I16
+    case 26: return n * 4;                // I32
+    case 27: return n * 8;                // I64
+    case 28: return n * 8;                // F64
+    case 29: return blocks(256) * 56;     // IQ1_M
+    default: return 0;
+  }
+}
+
+int chatnet_create(const chatnet_config* cfg, int device, chatnet_model** out) {
+  if (!cfg || !out) return fail(CHATNET_ERR_INVALID_ARG, "cfg and out must be non-null");
+  *out = nullptr;
+  const chatnet_config& c = *cfg;
+  if (c.dim <= 0 || c.hidden_dim <= 0 || c.n_layers <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 ||
+      c.head_dim <= 0 || c.vocab_size <= 0 || c.context_length <= 0)
+    return fail(CHATNET_ERR_INVALID_ARG, "all dimensions must be positive");
+  if (c.n_heads % c.n_kv_heads != 0)
+    return fail(CHATNET_ERR_INVALID_ARG, "n_heads (%d) must be a multiple of n_kv_heads (%d)", c.n_heads, c.n_kv_heads);
+  if (c.n_heads * c.head_dim != c.dim)
+    return fail(CHATNET_ERR_INVALID_ARG, "n_heads*head_dim (%d) must equal dim (%d)", c.n_heads * c.head_dim, c.dim);
+  if (c.head_dim != 32 && c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256)
+    return fail(CHATNET_ERR_INVALID_ARG, "head_dim %d not supported (32, 64, 128, 256)", c.head_dim);
+  if (c.dim % 64 != 0 || c.hidden_dim % 64 != 0)
+    return fail(CHATNET_ERR_INVALID_ARG, "dim and hidden_dim must be multiples of 64");
+  if (c.context_length > 16384)
+    return fail(CHATNET_ERR_INVALID_ARG, "context_length %d exceeds 16384", c.context_length);
+  if (c.kv_dtype != CHATNET_KV_F32 && c.kv_dtype != CHATNET_KV_F16)
+    return fail(CHATNET_ERR_INVALID_ARG, "kv_dtype %d unknown", c.kv_dtype);
+  if (c.reserved != 0) return fail(CHATNET_ERR_INVALID_ARG, "reserved must be 0");
+  if (!(c.rope_freq_base > 0.f) || !(c.rms_norm_eps >= 0.f))
+    return fail(CHATNET_ERR_INVALID_ARG, "rope_freq_base must be > 0 and rms_norm_eps >= 0");
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+    return fail(CHATNET_ERR_NO_DEVICE, "no HIP device available");
+  if (device < 0 || device >= ndev) return fail(CHATNET_ERR_NO_DEVICE, "device %d out of range (%d devices)", device, ndev);
+  HIP_TRY(hipSetDevice(device));
+
+  chatnet_model* m = new chatnet_model();
+  m->cfg = c;
+  m->device = device;
+  m->num_cus = device_cus(device);
+  m->kv_dim = c.n_kv_heads * c.head_dim;
+  m->kv_elt = c.kv_dtype == CHATNET_KV_F16 ? 2 : 4;
+  m->layers.resize(c.n_layers);
+  const size_t kv_bytes = (size_t)c.n_layers * c.context_length * m->kv_dim * m->kv_elt;
+  auto cleanup = [m]() { chatnet_destroy(m); };
+  if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) {
+    cleanup();
+    return fail(CHATNET_ERR_HIP, "hipStreamCreate failed");
+  }
+  struct { void** p; size_t n; } allocs[] = {
+      {&m->kcache, kv_bytes},
+      {&m->vcache, kv_bytes},
+      {(void**)&m->x, sizeof(float) * c.dim},
+      {(void**)&m->q, sizeof(float) * c.dim},
+      {(void**)&m->att, sizeof(float) * c.dim},
+      {(void**)&m->h, sizeof(float) * c.hidden_dim},
+      {(void**)&m->logits, sizeof(float) * c.vocab_size},
+      {(void**)&m->state, sizeof(int) * 4},
+  };
+  for (auto& a : allocs) {
+    if (hipMalloc(a.p, a.n) != hipSuccess) {
+      cleanup();
+      return fail(CHATNET_ERR_OUT_OF_MEMORY, "hipMalloc of %zu bytes failed", a.n);
+    }
+  }
+  // Zero the caches once so unwritten positions hold 0 like the managed arrays.
+  if (hipMemset(m->kcache, 0, kv_bytes) != hipSuccess || hipMemset(m->vcache, 0, kv_bytes) != hipSuccess ||
+      hipMemset(m->state, 0, sizeof(int) * 4) != hipSuccess) {
+    cleanup();
+    return fail(CHATNET_ERR_HIP, "hipMemset failed");
+  }
+  *out = m;
+  g_err.clear();
+  return CHATNET_OK;
+}
+
+void chatnet_destroy(chatnet_model* m) {
+  if (!m) return;
+  (void)hipSetDevice(m->device);
+  if (m->stream) (void)hipStreamSynchronize(m->stream);
+  if (m->graph) (void)hipGraphExecDestroy(m->graph);
+  auto fr = [](void* p) { if (p) (void)hipFree(p); };
+  fr(m->emb.ptr); fr(m->out.ptr); fr(m->out_norm.ptr);
+  for (auto& l : m->layers) {
+    fr(l.attn_norm.ptr); fr(l.ffn_norm.ptr); fr(l.wq.ptr); fr(l.wk.ptr); fr(l.wv.ptr);
+    fr(l.wo.ptr); fr(l.wg.ptr); fr(l.wu.ptr); fr(l.wd.ptr);
+  }
+  fr(m->kcache); fr(m->vcache); fr(m->x); fr(m->q); fr(m->att); fr(m->h); fr(m->logits);
+  fr(m->state); fr(m->out_tokens);
+  if (m->stream) (void)hipStreamDestroy(m->stream);
+  delete m;
+}
+
+int chatnet_upload_tensor(chatnet_model* m, const char* name, uint32_t type, const uint64_t* dims,
+                          int ndims, const void* host, uint64_t nbytes) {
+  if (!m || !name || !dims || !host || ndims < 1 || ndims > 4)
+    return fail(CHATNET_ERR_INVALID_ARG, "invalid arguments to chatnet_upload_tensor");
+  const chatnet_config& c = m->cfg;
+  uint64_t n = 1;
+  for (int i = 0; i < ndims; i++) n *= dims[i];
+  const uint64_t want = chatnet_tensor_nbytes(type, n);
+  if (want == 0) return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "tensor %s: unknown ggml type %u", name, type);
+  if (want != nbytes)
+    return fail(CHATNET_ERR_SIZE_MISMATCH, "tensor %s: %llu bytes given, ByteSize is %llu", name,
+                (unsigned long long)nbytes, (unsigned long long)want);
+  const uint64_t ne0 = dims[0], ne1 = ndims > 1 ? dims[1] : 1;
+  for (int i = 2; i < ndims; i++)
+    if (dims[i] != 1) return fail(CHATNET_ERR_INVALID_ARG, "tensor %s: more than 2 non-unit dims", name);
+
+  DevTensor* slot = nullptr;
+  uint64_t want0 = 0, want1 = 0;
+  bool matrix = true;
+  int layer = -1;
+  char suffix[64] = {0};
+  if (!strcmp(name, "token_embd.weight")) {
+    slot = &m->emb; want0 = c.dim; want1 = c.vocab_size; matrix = false;
+    if (type != CHATNET_GGML_F32 && type != CHATNET_GGML_F16 && type != CHATNET_GGML_Q4_0)
+      return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "token_embd.weight: type %u not supported (F32, F16, Q4_0)", type);
+  } else if (!strcmp(name, "output.weight")) {
+    slot = &m->out; want0 = c.dim; want1 = c.vocab_size;
+  } else if (!strcmp(name, "output_norm.weight")) {
+    slot = &m->out_norm; want0 = c.dim; want1 = 1; matrix = false;
+  } else if (sscanf(name, "blk.%d.%63s", &layer, suffix) == 2) {
+    if (layer < 0 || layer >= c.n_layers) return fail(CHATNET_ERR_NOT_FOUND, "tensor %s: layer out of range", name);
+    Layer& L = m->layers[layer];
+    const uint64_t kvd = (uint64_t)m->kv_dim;
+    struct { const char* s; DevTensor* t; uint64_t k, r; bool mat; } tab[] = {
+        {"attn_norm.weight", &L.attn_norm, (uint64_t)c.dim, 1, false},
+        {"ffn_norm.weight", &L.ffn_norm, (uint64_t)c.dim, 1, false},
+        {"attn_q.weight", &L.wq, (uint64_t)c.dim, (uint64_t)c.dim, true},
+        {"attn_k.weight", &L.wk, (uint64_t)c.dim, kvd, true},
+        {"attn_v.weight", &L.wv, (uint64_t)c.dim, kvd, true},
+        {"attn_output.weight", &L.wo, (uint64_t)c.dim, (uint64_t)c.dim, true},
+        {"ffn_gate.weight", &L.wg, (uint64_t)c.dim, (uint64_t)c.hidden_dim, true},
+        {"ffn_up.weight", &L.wu, (uint64_t)c.dim, (uint64_t)c.hidden_dim, true},
+        {"ffn_down.weight", &L.wd, (uint64_t)c.hidden_dim, (uint64_t)c.dim, true},
+    };
+    for (auto& e : tab)
+      if (!strcmp(suffix, e.s)) { slot = e.t; want0 = e.k; want1 = e.r; matrix = e.mat; }
+  }
+  if (!slot) return fail(CHATNET_ERR_NOT_FOUND, "tensor %s is not part of the Llama layout", name);
+  if (ne0 != want0 || ne1 != want1)
+    return fail(CHATNET_ERR_SIZE_MISMATCH, "tensor %s: dims [%llu, %llu], expected [%llu, %llu]", name,
+                (unsigned long long)ne0, (unsigned long long)ne1, (unsigned long long)want0,
+                (unsigned long long)want1);
+  if (matrix) {
+    if (!is_matrix_type(type))
+      return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "tensor %s: weight type %u not supported (Q4_0, Q4_K, Q6_K)", name, type);
+    if (!gemv_supports((int)type, (int)ne0))
+      return fail(CHATNET_ERR_INVALID_ARG, "tensor %s: inner dim %llu not a multiple of the block", name,
+                  (unsigned long long)ne0);
+  } else if (slot != &m->emb && type != CHATNET_GGML_F32) {
+    return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "tensor %s: norm weights must be F32", name);
+  }
+  HIP_TRY(hipSetDevice(m->device));
+  if (slot->ptr) {
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    (void)hipFree(slot->ptr);
+    slot->ptr = nullptr;
+  }
+  // 256 bytes of tail padding keep every vector load of the kernels in bounds.
+  if (hipMalloc(&slot->ptr, nbytes + 256) != hipSuccess)
+    return fail(CHATNET_ERR_OUT_OF_MEMORY, "hipMalloc of %llu bytes for %s failed", (unsigned long long)nbytes, name);
+  HIP_TRY(hipMemcpy(slot->ptr, host, nbytes, hipMemcpyHostToDevice));
+  HIP_TRY(hipMemset((char*)slot->ptr + nbytes, 0, 256));
+  slot->type = type;
+  slot->nbytes = nbytes;
+  slot->ne0 = ne0;
+  slot->ne1 = ne1;
+  if (m->graph) {
+    (void)hipGraphExecDestroy(m->graph);
+    m->graph = nullptr;
+  }
+  g_err.clear();
+  return CHATNET_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+int check_complete(const chatnet_model* m) {
+  if (!m->emb.ptr) return fail(CHATNET_ERR_NOT_FOUND, "tensor token_embd.weight not uploaded");
+  if (!m->out_norm.ptr) return fail(CHATNET_ERR_NOT_FOUND, "tensor output_norm.weight not uploaded");
+  if (!m->out.ptr) {
+    // LlamaWeights.cs:89-98 falls back to the tied embedding; only quantized
+    // LM heads run on the device GEMV.
+    return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "output.weight missing: tied F32/F16 embeddings as LM head are not supported");
+  }
+  for (size_t l = 0; l < m->layers.size(); l++) {
+    const Layer& L = m->layers[l];
+    const DevTensor* ts[] = {&L.attn_norm, &L.ffn_norm, &L.wq, &L.wk, &L.wv, &L.wo, &L.wg, &L.wu, &L.wd};
+    const char* nm[] = {"attn_norm", "ffn_norm", "attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"};
+    for (int i = 0; i < 9; i++)
+      if (!ts[i]->ptr) return fail(CHATNET_ERR_NOT_FOUND, "tensor blk.%zu.%s.weight not uploaded", l, nm[i]);
+  }
+  return CHATNET_OK;
+}
+
+GemvArgs base_args(const chatnet_model* m) {
+  GemvArgs a;
+  memset(&a, 0, sizeof(a));
+  a.eps = m->cfg.rms_norm_eps;
+  a.pos = m->state;
+  a.head_dim = m->cfg.head_dim;
+  a.rope_dim_inv = 1.0f / (float)m->cfg.head_dim;
+  a.rope_neg_log_base = -logf(m->cfg.rope_freq_base);
+  a.kv_dim = m->kv_dim;
+  a.kv_f16 = m->cfg.kv_dtype == CHATNET_KV_F16;
+  return a;
+}
+
+// Launches the forward of the token held in m->state (pos, token).
+int launch_token(chatnet_model* m, bool lm_head) {
+  const chatnet_config& c = m->cfg;
+  hipStream_t st = m->stream;
+  const int kvd = m->kv_dim;
+  HIP_TRY(embed_launch(m->emb.ptr, (int)m->emb.type, c.dim, m->state + 1, m->x, st));
+  for (int l = 0; l < c.n_layers; l++) {
+    const Layer& L = m->layers[l];
+    const size_t loff = (size_t)l * c.context_length * kvd * m->kv_elt;
+    GemvArgs a = base_args(m);
+    a.K = c.dim;
+    a.x = m->x;
+    a.norm_w = (const float*)L.attn_norm.ptr;
+    a.out[0] = m->q;
+    a.kcache = (char*)m->kcache + loff;
+    a.vcache = (char*)m->vcache + loff;
+    if (L.wq.type == L.wk.type && L.wk.type == L.wv.type) {
+      a.w[0] = (const uint8_t*)L.wq.ptr;
+      a.w[1] = (const uint8_t*)L.wk.ptr;
+      a.w[2] = (const uint8_t*)L.wv.ptr;
+      a.seg_rows[0] = c.dim;
+      a.seg_rows[1] = kvd;
+      a.seg_rows[2] = kvd;
+      a.n_vrows = c.dim + 2 * kvd;
+      HIP_TRY(gemv_launch((int)L.wq.type, GEMV_EPI_QKV, a, m->num_cus, st));
+    } else {
+      const DevTensor* ts[3] = {&L.wq, &L.wk, &L.wv};
+      const int rows[3] = {c.dim, kvd, kvd};
+      for (int s = 0; s < 3; s++) {
+        GemvArgs b = a;
+        b.w[0] = b.w[1] = b.w[2] = (const uint8_t*)ts[s]->ptr;
+        b.seg_rows[0] = s == 0 ? rows[0] : 0;
+        b.seg_rows[1] = s == 1 ? rows[1] : 0;
+        b.seg_rows[2] = s == 2 ? rows[2] : 0;
+        b.n_vrows = rows[s];
+        HIP_TRY(gemv_launch((int)ts[s]->type, GEMV_EPI_QKV, b, m->num_cus, st));
+      }
+    }
+    AttnArgs at;
+    memset(&at, 0, sizeof(at));
+    at.q = m->q;
+    at.kc = a.kcache;
+    at.vc = a.vcache;
+    at.out = m->att;
+    at.pos = m->state;
+    at.n_heads = c.n_heads;
+    at.kv_mul = c.n_heads / c.n_kv_heads;
+    at.head_dim = c.head_dim;
+    at.kv_dim = kvd;
+    at.ctx = c.context_length;
+    at.kv_f16 = a.kv_f16;
+    at.scale = 1.0f / sqrtf((float)c.head_dim);  // LlamaModel.cs:248
+    at.splits = 1;
+    HIP_TRY(attn_decode_launch(at, st));
+
+    GemvArgs o = base_args(m);
+    o.K = c.dim;
+    o.x = m->att;
+    o.w[0] = (const uint8_t*)L.wo.ptr;
+    o.seg_rows[0] = c.dim;
+    o.n_vrows = c.dim;
+    o.out[0] = m->x;
+    HIP_TRY(gemv_launch((int)L.wo.type, GEMV_EPI_ADD, o, m->num_cus, st));
+
+    if (L.wg.type != L.wu.type)
+      return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "layer %d: ffn_gate and ffn_up types differ", l);
+    GemvArgs g = base_args(m);
+    g.K = c.dim;
+    g.x = m->x;
+    g.norm_w = (const float*)L.ffn_norm.ptr;
+    g.w[0] = (const uint8_t*)L.wg.ptr;
+    g.w[1] = (const uint8_t*)L.wu.ptr;
+    g.seg_rows[0] = c.hidden_dim;
+    g.seg_rows[1] = c.hidden_dim;
+    g.n_vrows = 2 * c.hidden_dim;
+    g.out[0] = m->h;
+    HIP_TRY(gemv_launch((int)L.wg.type, GEMV_EPI_SWIGLU, g, m->num_cus, st));
+
+    GemvArgs d = base_args(m);
+    d.K = c.hidden_dim;
+    d.x = m->h;
+    d.w[0] = (const uint8_t*)L.wd.ptr;
+    d.seg_rows[0] = c.dim;
+    d.n_vrows = c.dim;
+    d.out[0] = m->x;
+    HIP_TRY(gemv_launch((int)L.wd.type, GEMV_EPI_ADD, d, m->num_cus, st));
+  }
+  if (lm_head) {
+    GemvArgs o = base_args(m);  // final RMSNorm fused (LlamaModel.cs:203-213)
+    o.K = c.dim;
+    o.x = m->x;
+    o.norm_w = (const float*)m->out_norm.ptr;
+    o.w[0] = (const uint8_t*)m->out.ptr;
+    o.seg_rows[0] = c.vocab_size;
+    o.n_vrows = c.vocab_size;
+    o.out[0] = m->logits;
+    HIP_TRY(gemv_launch((int)m->out.type, GEMV_EPI_LOGITS, o, m->num_cus, st));
+  }
+  return CHATNET_OK;
+}
+
+int ensure_out_tokens(chatnet_model* m, int cap) {
+  if (m->out_cap >= cap) return CHATNET_OK;
+  if (m->out_tokens) {
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    (void)hipFree(m->out_tokens);
+    m->out_tokens = nullptr;
+    m->out_cap = 0;
+  }
+  if (hipMalloc(&m->out_tokens, sizeof(int) * (size_t)cap) != hipSuccess)
+    return fail(CHATNET_ERR_OUT_OF_MEMORY, "hipMalloc of token buffer failed");
+  m->out_cap = cap;
+  if (m->graph) {  // the captured argmax node points at the old buffer
+    (void)hipGraphExecDestroy(m->graph);
+    m->graph = nullptr;
+  }
+  return CHATNET_OK;
+}
+
+int run_prompt(chatnet_model* m, const int32_t* tokens, int n, int position) {
+  for (int t = 0; t < n; t++) {
+    HIP_TRY(set_state_launch(m->state, position + t, tokens[t], -1, m->stream));
+    int rc = launch_token(m, t == n - 1);
+    if (rc) return rc;
+  }
+  m->have_logits = true;
+  m->next_pos = position + n;
+  m->last_tok = tokens[n - 1];
+  return CHATNET_OK;
+}
+
+int validate_tokens(const chatnet_model* m, const int32_t* tokens, int n, int position) {
+  if (!tokens || n <= 0) return fail(CHATNET_ERR_INVALID_ARG, "tokens must be non-empty");
+  if (position < 0 || (long long)position + n > m->cfg.context_length)
+    return fail(CHATNET_ERR_OUT_OF_RANGE, "positions %d..%d exceed context_length %d", position,
+                position + n - 1, m->cfg.context_length);
+  for (int i = 0; i < n; i++)
+    if (tokens[i] < 0 || tokens[i] >= m->cfg.vocab_size)
+      return fail(CHATNET_ERR_OUT_OF_RANGE, "token id %d at index %d outside [0, %d)", tokens[i], i, m->cfg.vocab_size);
+  return CHATNET_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int chatnet_forward(chatnet_model* m, const int32_t* tokens, int n, int position, float* logits_host) {
+  if (!m) return fail(CHATNET_ERR_INVALID_ARG, "null model");
+  int rc = validate_tokens(m, tokens, n, position);
+  if (rc) return rc;
+  if ((rc = check_complete(m))) return rc;
+  HIP_TRY(hipSetDevice(m->device));
+  if ((rc = run_prompt(m, tokens, n, position))) return rc;
+  if (logits_host)
+    HIP_TRY(hipMemcpyAsync(logits_host, m->logits, sizeof(float) * m->cfg.vocab_size, hipMemcpyDeviceToHost, m->stream));
+  HIP_TRY(hipStreamSynchronize(m->stream));
+  g_err.clear();
+  return CHATNET_OK;
+}
+
+int chatnet_get_logits(chatnet_model* m, float* logits_host) {
+  if (!m || !logits_host) return fail(CHATNET_ERR_INVALID_ARG, "null argument");
+  if (!m->have_logits) return fail(CHATNET_ERR_INVALID_ARG, "no forward has produced logits yet");
+  HIP_TRY(hipSetDevice(m->device));
+  HIP_TRY(hipMemcpyAsync(logits_host, m->logits, sizeof(float) * m->cfg.vocab_size, hipMemcpyDeviceToHost, m->stream));
+  HIP_TRY(hipStreamSynchronize(m->stream));
+  return CHATNET_OK;
+}
+
+int chatnet_argmax(chatnet_model* m, int32_t* out_token) {
+  if (!m || !out_token) return fail(CHATNET_ERR_INVALID_ARG, "null argument");
+  if (!m->have_logits) return fail(CHATNET_ERR_INVALID_ARG, "no forward has produced logits yet");
+  HIP_TRY(hipSetDevice(m->device));
+  HIP_TRY(argmax_launch(m->logits, m->cfg.vocab_size, m->state, nullptr, 0, m->stream));
+  int st[4];
+  HIP_TRY(hipMemcpyAsync(st, m->state, sizeof(st), hipMemcpyDeviceToHost, m->stream));
+  HIP_TRY(hipStreamSynchronize(m->stream));
+  *out_token = st[1];
+  return CHATNET_OK;
+}
+
+int chatnet_decode_greedy(chatnet_model* m, int max_tokens, int32_t eos_token, int32_t* out_tokens, int* n_out) {
+  if (!m || !out_tokens || !n_out) return fail(CHATNET_ERR_INVALID_ARG, "null argument");
+  *n_out = 0;
+  if (max_tokens < 0) return fail(CHATNET_ERR_INVALID_ARG, "max_tokens must be >= 0");
+  if (!m->have_logits) return fail(CHATNET_ERR_INVALID_ARG, "no forward has produced logits yet");
+  int rc = check_complete(m);
+  if (rc) return rc;
+  HIP_TRY(hipSetDevice(m->device));
+  const int ctx = m->cfg.context_length;
+  const int p0 = m->next_pos;  // position of the first generated token
+  // InferenceEngine.cs:256-307: token i is emitted, then the loop stops if its
+  // position p0+i >= ctx-1; otherwise it is forwarded there and the next sampled.
+  const int room = ctx - 1 - p0;
+  int forwards = max_tokens < room ? max_tokens : (room > 0 ? room : 0);
+  int emitted = max_tokens < room + 1 ? max_tokens : room + 1;
+  if (emitted < 0) emitted = 0;
+  if ((rc = ensure_out_tokens(m, max_tokens + 2))) return rc;
+  // step counter = 0, then sample the first token from the last forward's logits
+  HIP_TRY(set_state_launch(m->state, p0 - 1, m->last_tok, 0, m->stream));
+  HIP_TRY(argmax_launch(m->logits, m->cfg.vocab_size, m->state, m->out_tokens, m->out_cap, m->stream));
+  if (forwards > 0) {
+    if (!m->graph) {
+      hipGraph_t g;
+      HIP_TRY(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+      int lrc = launch_token(m, true);
+      hipError_t ae = argmax_launch(m->logits, m->cfg.vocab_size, m->state, m->out_tokens, m->out_cap, m->stream);
+      hipError_t ee = hipStreamEndCapture(m->stream, &g);
+      if (lrc) return lrc;
+      if (ae != hipSuccess) return fail(CHATNET_ERR_HIP, "argmax capture: %s", hipGetErrorString(ae));
+      if (ee != hipSuccess) return fail(CHATNET_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(ee));
+      hipError_t ie = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(g);
+      if (ie != hipSuccess) {
+        m->graph = nullptr;
+        return fail(CHATNET_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(ie));
+      }
+    }
+    for (int i = 0; i < forwards; i++) HIP_TRY(hipGraphLaunch(m->graph, m->stream));
+  }
+  std::vector<int> buf((size_t)emitted + 2);
+  HIP_TRY(hipMemcpyAsync(buf.data(), m->out_tokens, sizeof(int) * (emitted + 1), hipMemcpyDeviceToHost, m->stream));
+  HIP_TRY(hipStreamSynchronize(m->stream));
+  int nout = 0;
+  for (int i = 0; i < emitted; i++) {
+    if (eos_token >= 0 && buf[i] == eos_token) break;  // InferenceEngine.cs:258-261
+    out_tokens[nout++] = buf[i];
+  }
+  *n_out = nout;
+  // the cache now holds positions < p0+forwards; the logits are those of the
+  // last forwarded token
+  if (forwards > 0) {
+    m->next_pos = p0 + forwards;
+    m->last_tok = buf[forwards - 1];
+  }
+  g_err.clear();
+  return CHATNET_OK;
+}
+
+int chatnet_generate_greedy(chatnet_model* m, const int32_t* prompt, int n_prompt, int max_tokens,
+                            int32_t eos_token, int32_t* out_tokens, int* n_out) {
+  if (!m || !out_tokens || !n_out) return fail(CHATNET_ERR_INVALID_ARG, "null argument");
+  *n_out = 0;
+  if (max_tokens < 0) return fail(CHATNET_ERR_INVALID_ARG, "max_tokens must be >= 0");
+  int rc = validate_tokens(m, prompt, n_prompt, 0);
+  if (rc) return rc;
+  if ((rc = check_complete(m))) return rc;
+  HIP_TRY(hipSetDevice(m->device));
+  if ((rc = run_prompt(m, prompt, n_prompt, 0))) return rc;  // InferenceEngine.cs:235-239
+  return chatnet_decode_greedy(m, max_tokens, eos_token, out_tokens, n_out);
+}
+
+int chatnet_matmul(uint32_t type, const void* w_dev, const float* x_dev, float* y_dev, int M, int K, int N,
+                   void* stream) {
+  if (!w_dev || !x_dev || !y_dev) return fail(CHATNET_ERR_INVALID_ARG, "null device pointer");
+  if (M <= 0 || K <= 0 || N <= 0) return fail(CHATNET_ERR_INVALID_ARG, "M, K, N must be positive");
+  if (!is_matrix_type(type)) return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "matmul type %u not supported", type);
+  if (!gemv_supports((int)type, K)) return fail(CHATNET_ERR_INVALID_ARG, "K=%d not a multiple of the block size", K);
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  const int cus = device_cus(dev);
+  hipStream_t st = (hipStream_t)stream;
+  for (int n = 0; n < N; n++) {
+    GemvArgs a;
+    memset(&a, 0, sizeof(a));
+    a.w[0] = a.w[1] = a.w[2] = (const uint8_t*)w_dev;
+    a.seg_rows[0] = M;
+    a.n_vrows = M;
+    a.K = K;
+    a.x = x_dev + (size_t)n * K;
+    a.out[0] = y_dev + (size_t)n * M;
+    HIP_TRY(gemv_launch((int)type, GEMV_EPI_STORE, a, cus, st));
+  }
+  g_err.clear();
+  return CHATNET_OK;
+}
+
+}  // extern "C"

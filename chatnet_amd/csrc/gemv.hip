@@ -1,0 +1,528 @@
+// gemv.hip — fused dequant-GEMV for batch-1 decode on gfx950.
+//
+// Replaces TensorMath.MatVecMulQ4_0 / MatVecMulQ6K / MatVecMulGeneric
+// (src/ChatNet.Core/Tensors/TensorMath.cs:548-656) and the fused row dots
+// DequantQ4_0.DotProduct (DequantQ4_0.cs:80-149), DequantQ4K.DotProduct
+// (DequantQ4K.cs:89-163) and DequantQ6K.DotProduct (DequantQ6K.cs:104-188).
+//
+// Weights stay in their raw GGUF block layout in HBM.  One lane owns one
+// "unit" of a row — two Q4_0 blocks (64 weights, 36 B, dword aligned), or one
+// Q4_K super-block (256 weights, 144 B), or one Q6_K super-block (256 weights,
+// 210 B, realigned in registers) — and LPR lanes cover a row, so a wave reads
+// each row as one contiguous stretch.  Every lane works on RPW rows at once so
+// each x value it reads from LDS feeds RPW rows.  The input vector is staged
+// in LDS once per workgroup (with RMSNorm fused in when a norm weight is
+// given, TensorMath.RmsNorm TensorMath.cs:97-165), padded by 4 floats per unit
+// so the 16-byte LDS reads of neighbouring lanes hit distinct banks.
+// Products are fp32 (exact nibble -> float conversion), sums fp32; the
+// per-block offset (q-8 for Q4_0, dmin*m for Q4_K, q-32 for Q6_K) is applied
+// once per block through precomputed block sums of x.  Partial row sums are
+// reduced across the LPR lanes with cross-lane shuffles.
+//
+// Epilogues (fused into the lane that finishes a row pair):
+//   STORE   y[r]  = dot                          (LM head, matmul API)
+//   ADD     y[r] += dot                          (O / down + residual, TensorMath.Add :712-733)
+//   QKV     RoPE on q/k pairs + K/V cache write  (TensorMath.ApplyRoPE :408-458, LlamaModel.cs:146-153)
+//   SWIGLU  h[r] = silu(gate[r]) * up[r]         (TensorMath.SiluElementwiseMul :253-286)
+#include "device_common.h"
+#include "kernels.h"
+
+namespace {
+
+constexpr int QT_Q4_0 = 2, QT_Q4_K = 12, QT_Q6_K = 14;
+
+template <int QT> struct QTraits;
+template <> struct QTraits<QT_Q4_0> {
+  static constexpr int UNIT = 64;        // weights per lane unit
+  static constexpr int NDW = 9;          // dwords held per unit
+  static constexpr int BLOCK_BYTES = 18, BLOCK = 32;
+};
+template <> struct QTraits<QT_Q4_K> {
+  static constexpr int UNIT = 256, NDW = 36;
+  static constexpr int BLOCK_BYTES = 144, BLOCK = 256;
+};
+template <> struct QTraits<QT_Q6_K> {
+  static constexpr int UNIT = 256, NDW = 53;
+  static constexpr int BLOCK_BYTES = 210, BLOCK = 256;
+};
+
+// LDS index of x[k] for a given unit size (4 floats of padding per unit).
+template <int UNIT>
+__device__ __forceinline__ int xidx(int k) {
+  return k + (k / UNIT) * 4;
+}
+
+// ---------------------------------------------------------------------------
+// Unit loads
+// ---------------------------------------------------------------------------
+template <int QT>
+__device__ __forceinline__ void load_unit(const uint8_t* row, int u, uint32_t* w);
+
+template <>
+__device__ __forceinline__ void load_unit<QT_Q4_0>(const uint8_t* row, int u, uint32_t* w) {
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(row + (size_t)u * 36);
+#pragma unroll
+  for (int k = 0; k < 9; k++) w[k] = __builtin_nontemporal_load(p + k);
+}
+
+template <>
+__device__ __forceinline__ void load_unit<QT_Q4_K>(const uint8_t* row, int u, uint32_t* w) {
+  const cn_u32x4* p = reinterpret_cast<const cn_u32x4*>(row + (size_t)u * 144);
+#pragma unroll
+  for (int k = 0; k < 9; k++) {
+    cn_u32x4 t = __builtin_nontemporal_load(p + k);
+    w[4 * k + 0] = t.x;
+    w[4 * k + 1] = t.y;
+    w[4 * k + 2] = t.z;
+    w[4 * k + 3] = t.w;
+  }
+}
+
+// Q6_K super-blocks start on 2-byte boundaries.  Load the dword-aligned window
+// and realign so that canonical byte i of w[] is super-block byte i (w[52]
+// holds d in its low half).  Never touches bytes outside the super-block
+// except the 2 bytes before it, which belong to the same allocation whenever
+// the super-block is not the first one (a misaligned super-block never is).
+template <>
+__device__ __forceinline__ void load_unit<QT_Q6_K>(const uint8_t* row, int u, uint32_t* w) {
+  const uint8_t* s = row + (size_t)u * 210;
+  const uintptr_t a = reinterpret_cast<uintptr_t>(s);
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(a & ~(uintptr_t)3);
+  const uint32_t sh = (uint32_t)(a & 3);  // 0 or 2
+  uint32_t r[53];
+#pragma unroll
+  for (int k = 0; k < 52; k++) r[k] = __builtin_nontemporal_load(p + k);
+  if (sh) {
+    r[52] = __builtin_nontemporal_load(p + 52);
+#pragma unroll
+    for (int k = 0; k < 52; k++) w[k] = __builtin_amdgcn_alignbyte(r[k + 1], r[k], 2);
+    w[52] = r[52] >> 16;
+  } else {
+#pragma unroll
+    for (int k = 0; k < 52; k++) w[k] = r[k];
+    w[52] = *reinterpret_cast<const uint16_t*>(s + 208);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Unit dot products for RPW rows sharing the same x slice.
+// xs: LDS (padded) already offset to the unit's first element; sx: block sums.
+// ---------------------------------------------------------------------------
+
+// Byte j (0..15) of the qs of block A (pair bytes 2..17) / block B (20..35).
+template <int RPW>
+__device__ __forceinline__ void dot_unit_q4_0(const uint32_t (*w)[9], const float* xs,
+                                              const float* sx, float* acc) {
+  float sa[RPW], sb[RPW];
+#pragma unroll
+  for (int i = 0; i < RPW; i++) sa[i] = sb[i] = 0.f;
+  // Block A: x[0..31]; Block B: x[32..63].
+#pragma unroll
+  for (int blk = 0; blk < 2; blk++) {
+    float xl[16], xh[16];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      float4 t0 = *reinterpret_cast<const float4*>(xs + blk * 32 + 4 * c);
+      float4 t1 = *reinterpret_cast<const float4*>(xs + blk * 32 + 16 + 4 * c);
+      xl[4 * c + 0] = t0.x; xl[4 * c + 1] = t0.y; xl[4 * c + 2] = t0.z; xl[4 * c + 3] = t0.w;
+      xh[4 * c + 0] = t1.x; xh[4 * c + 1] = t1.y; xh[4 * c + 2] = t1.z; xh[4 * c + 3] = t1.w;
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        const int P = (blk ? 20 : 2) + j;  // byte position inside the 36-byte pair
+        const uint32_t dw = w[i][P >> 2];
+        const uint32_t lo = dw & 0x0F0F0F0Fu;
+        const uint32_t hi = (dw >> 4) & 0x0F0F0F0Fu;
+        const int b = P & 3;
+        s0 += (float)((lo >> (8 * b)) & 0xFFu) * xl[j];
+        s1 += (float)((hi >> (8 * b)) & 0xFFu) * xh[j];
+      }
+      if (blk == 0) sa[i] = s0 + s1; else sb[i] = s0 + s1;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RPW; i++) {
+    const float da = cn_h2f(w[i][0]);
+    const float db = cn_h2f(w[i][4] >> 16);
+    acc[i] += da * (sa[i] - 8.f * sx[0]) + db * (sb[i] - 8.f * sx[1]);
+  }
+}
+
+// Q4_K super-block in the reference's order (DequantQ4K.cs:59-72): sub-block s
+// uses qs[16s..16s+15]; low nibbles -> elements 32s+0..15, high -> 32s+16..31.
+// value = d*sc[s]*q - dmin*m[s]  =>  dot = sum_s d*sc[s]*S_s - dmin*m[s]*X_s.
+template <int RPW>
+__device__ __forceinline__ void dot_unit_q4_k(const uint32_t (*w)[36], const float* xs,
+                                              const float* sx, float* acc) {
+  float dsc[RPW][8], dmm[RPW][8];
+#pragma unroll
+  for (int i = 0; i < RPW; i++) {
+    const float d = cn_h2f(w[i][0]), dmin = cn_h2f(w[i][0] >> 16);
+    const uint32_t q0 = w[i][1], q1 = w[i][2], q2 = w[i][3];  // scale bytes 0..11
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      int sc, m;
+      if (j < 4) {
+        sc = (q0 >> (8 * j)) & 63;
+        m = (q1 >> (8 * j)) & 63;
+      } else {
+        const uint32_t b8 = (q2 >> (8 * (j - 4))) & 0xFF;
+        sc = (b8 & 0xF) | (((q0 >> (8 * (j - 4) + 6)) & 3) << 4);
+        m = (b8 >> 4) | (((q1 >> (8 * (j - 4) + 6)) & 3) << 4);
+      }
+      dsc[i][j] = d * (float)sc;
+      dmm[i][j] = dmin * (float)m;
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < 8; s++) {
+    float xl[16], xh[16];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      float4 t0 = *reinterpret_cast<const float4*>(xs + 32 * s + 4 * c);
+      float4 t1 = *reinterpret_cast<const float4*>(xs + 32 * s + 16 + 4 * c);
+      xl[4 * c + 0] = t0.x; xl[4 * c + 1] = t0.y; xl[4 * c + 2] = t0.z; xl[4 * c + 3] = t0.w;
+      xh[4 * c + 0] = t1.x; xh[4 * c + 1] = t1.y; xh[4 * c + 2] = t1.z; xh[4 * c + 3] = t1.w;
+    }
+    const float xsum = sx[s];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const uint32_t dw = w[i][4 + 4 * s + k];
+        const uint32_t lo = dw & 0x0F0F0F0Fu, hi = (dw >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+          s0 += (float)((lo >> (8 * b)) & 0xFFu) * xl[4 * k + b];
+          s1 += (float)((hi >> (8 * b)) & 0xFFu) * xh[4 * k + b];
+        }
+      }
+      acc[i] += dsc[i][s] * (s0 + s1) - dmm[i][s] * xsum;
+    }
+  }
+}
+
+// Q6_K super-block (DequantQ6K.cs:53-83): for half h and l < 32,
+//   q1 = ql[64h+l]&15 | (qh[32h+l]&3)<<4          -> element 128h+l,    scale sc[8h+l/16]
+//   q2 = ql[64h+l+32]&15 | ((qh>>2)&3)<<4         -> element 128h+32+l, scale sc[8h+l/16+2]
+//   q3 = ql[64h+l]>>4 | ((qh>>4)&3)<<4            -> element 128h+64+l, scale sc[8h+l/16+4]
+//   q4 = ql[64h+l+32]>>4 | ((qh>>6)&3)<<4         -> element 128h+96+l, scale sc[8h+l/16+6]
+// value = d*sc*(q-32): per 16-element group g, dot = d*sc[g]*(S_g - 32*X_g).
+template <int RPW>
+__device__ __forceinline__ void dot_unit_q6_k(const uint32_t (*w)[53], const float* xs,
+                                              const float* sx16, float* acc) {
+  float part[RPW];
+#pragma unroll
+  for (int i = 0; i < RPW; i++) part[i] = 0.f;
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+#pragma unroll
+    for (int qi = 0; qi < 4; qi++) {        // q1..q4 -> element offset 32*qi
+#pragma unroll
+      for (int lb = 0; lb < 2; lb++) {      // l in [16lb, 16lb+16)
+        const int e0 = 128 * h + 32 * qi + 16 * lb;  // first element of this 16-group
+        float xv[16];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          float4 t = *reinterpret_cast<const float4*>(xs + e0 + 4 * c);
+          xv[4 * c + 0] = t.x; xv[4 * c + 1] = t.y; xv[4 * c + 2] = t.z; xv[4 * c + 3] = t.w;
+        }
+        const float xsum = sx16[e0 >> 4];
+#pragma unroll
+        for (int i = 0; i < RPW; i++) {
+          float s = 0.f;
+#pragma unroll
+          for (int k = 0; k < 4; k++) {  // 4 dwords = 16 consecutive l
+            const int l = 16 * lb + 4 * k;
+            const uint32_t qlw = w[i][(64 * h + l + ((qi & 1) ? 32 : 0)) >> 2];
+            const uint32_t qhw = w[i][(128 + 32 * h + l) >> 2];
+            const uint32_t nib = (qi < 2) ? (qlw & 0x0F0F0F0Fu) : ((qlw >> 4) & 0x0F0F0F0Fu);
+            const uint32_t two = ((qhw >> (2 * qi)) & 0x03030303u) << 4;
+            const uint32_t q = nib | two;
+#pragma unroll
+            for (int b = 0; b < 4; b++) s += (float)((q >> (8 * b)) & 0xFFu) * xv[4 * k + b];
+          }
+          const int g = 8 * h + 2 * qi + lb;  // scale index = element / 16
+          const int8_t scv = (int8_t)((w[i][(192 + g) >> 2] >> (8 * ((192 + g) & 3))) & 0xFF);
+          part[i] += (float)scv * (s - 32.f * xsum);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RPW; i++) acc[i] += cn_h2f(w[i][52]) * part[i];
+}
+
+template <int QT, int RPW>
+__device__ __forceinline__ void dot_unit(const uint32_t (*w)[QTraits<QT>::NDW], const float* xs,
+                                         const float* sx, const float* sx16, float* acc) {
+  if constexpr (QT == QT_Q4_0) dot_unit_q4_0<RPW>(w, xs, sx, acc);
+  else if constexpr (QT == QT_Q4_K) dot_unit_q4_k<RPW>(w, xs, sx, acc);
+  else dot_unit_q6_k<RPW>(w, xs, sx16, acc);
+}
+
+// Virtual row -> (segment, row-in-segment).
+template <int EPI>
+__device__ __forceinline__ void map_row(const GemvArgs& a, int vr, int& seg, int& r) {
+  if constexpr (EPI == GEMV_EPI_SWIGLU) {
+    seg = vr & 1;
+    r = vr >> 1;
+  } else if constexpr (EPI == GEMV_EPI_QKV) {
+    if (vr < a.seg_rows[0]) { seg = 0; r = vr; }
+    else if (vr < a.seg_rows[0] + a.seg_rows[1]) { seg = 1; r = vr - a.seg_rows[0]; }
+    else { seg = 2; r = vr - a.seg_rows[0] - a.seg_rows[1]; }
+  } else {
+    seg = 0;
+    r = vr;
+  }
+}
+
+// RoPE angle of pair index i (even) at position pos, TensorMath.cs:418-432:
+//   theta = pos * exp(i * (1/hd) * (-ln base)).
+__device__ __forceinline__ void rope_cs(int i, int pos, float dim_inv, float neg_log_base,
+                                        float& c, float& s) {
+  const float theta = (float)pos * expf((float)i * dim_inv * neg_log_base);
+  sincosf(theta, &s, &c);
+}
+
+template <int EPI, int RPW>
+__device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, const float* v) {
+#pragma unroll
+  for (int i = 0; i < RPW; i += 2) {
+    const int vr = vr0 + i;
+    if (vr >= a.n_vrows) return;
+    int seg, r;
+    map_row<EPI>(a, vr, seg, r);
+    if constexpr (EPI == GEMV_EPI_STORE || EPI == GEMV_EPI_LOGITS) {
+      a.out[0][r] = v[i];
+      if (vr + 1 < a.n_vrows) a.out[0][r + 1] = v[i + 1];
+    } else if constexpr (EPI == GEMV_EPI_ADD) {
+      a.out[0][r] += v[i];
+      if (vr + 1 < a.n_vrows) a.out[0][r + 1] += v[i + 1];
+    } else if constexpr (EPI == GEMV_EPI_SWIGLU) {
+      const float g = v[i], u = v[i + 1];
+      a.out[0][r] = (g / (1.0f + expf(-g))) * u;
+    } else {  // QKV
+      const int pos = *a.pos;
+      float x0 = v[i], x1 = v[i + 1];
+      if (seg < 2) {
+        float c, s;
+        rope_cs(r % a.head_dim, pos, a.rope_dim_inv, a.rope_neg_log_base, c, s);
+        const float y0 = x0 * c - x1 * s;
+        const float y1 = x0 * s + x1 * c;
+        x0 = y0;
+        x1 = y1;
+      }
+      if (seg == 0) {
+        a.out[0][r] = x0;
+        a.out[0][r + 1] = x1;
+      } else {
+        const size_t off = (size_t)pos * a.kv_dim + r;
+        if (a.kv_f16) {
+          _Float16* dst = reinterpret_cast<_Float16*>(seg == 1 ? a.kcache : a.vcache) + off;
+          dst[0] = (_Float16)x0;
+          dst[1] = (_Float16)x1;
+        } else {
+          float* dst = reinterpret_cast<float*>(seg == 1 ? a.kcache : a.vcache) + off;
+          dst[0] = x0;
+          dst[1] = x1;
+        }
+      }
+    }
+  }
+}
+
+template <int QT, int RPW, int LPR, int EPI>
+__global__ __launch_bounds__(CN_BLOCK) void gemv_kernel(GemvArgs a) {
+  using T = QTraits<QT>;
+  constexpr int UNIT = T::UNIT;
+  extern __shared__ float smem[];
+  const int K = a.K;
+  const int nunits = K / UNIT;
+  float* xs = smem;                                    // nunits*(UNIT+4)
+  float* sx = xs + nunits * (UNIT + 4);                // K/32 block sums
+  float* sx16 = sx + (K >> 5);                         // K/16 group sums (Q6_K)
+  float* red = sx16 + ((QT == QT_Q6_K) ? (K >> 4) : 0);  // 4 floats
+
+  // ---- prologue: stage x (optionally RMS-normalised) into LDS ----
+  float rms = 1.0f;
+  if (a.norm_w) {
+    float ss = 0.f;
+    for (int k = threadIdx.x * 4; k < K; k += CN_BLOCK * 4) {
+      const float4 t = *reinterpret_cast<const float4*>(a.x + k);
+      ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
+    }
+    ss = cn_block_sum(ss, red);
+    rms = 1.0f / sqrtf(ss / (float)K + a.eps);  // TensorMath.cs:142
+  }
+  for (int k = threadIdx.x * 4; k < K; k += CN_BLOCK * 4) {
+    float4 t = *reinterpret_cast<const float4*>(a.x + k);
+    if (a.norm_w) {
+      const float4 g = *reinterpret_cast<const float4*>(a.norm_w + k);
+      t.x = t.x * rms * g.x; t.y = t.y * rms * g.y; t.z = t.z * rms * g.z; t.w = t.w * rms * g.w;
+    }
+    *reinterpret_cast<float4*>(xs + xidx<UNIT>(k)) = t;
+  }
+  __syncthreads();
+  if constexpr (QT == QT_Q6_K) {
+    for (int g = threadIdx.x; g < (K >> 4); g += CN_BLOCK) {
+      const float* p = xs + xidx<UNIT>(g * 16);
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; j++) s += p[j];
+      sx16[g] = s;
+    }
+  } else {
+    for (int b = threadIdx.x; b < (K >> 5); b += CN_BLOCK) {
+      const float* p = xs + xidx<UNIT>(b * 32);
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < 32; j++) s += p[j];
+      sx[b] = s;
+    }
+  }
+  __syncthreads();
+
+  // ---- main loop: wave-strided over row groups ----
+  constexpr int GPW = CN_WAVE / LPR;  // row groups per wave
+  constexpr int RW = RPW * GPW;       // rows per wave iteration
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane / LPR, li = lane % LPR;
+  const int n_iters = (a.n_vrows + RW - 1) / RW;
+  const size_t bpr = (size_t)(K / T::BLOCK) * T::BLOCK_BYTES;
+
+  for (int it = blockIdx.x * (CN_BLOCK / CN_WAVE) + wave; it < n_iters;
+       it += gridDim.x * (CN_BLOCK / CN_WAVE)) {
+    const int vr0 = it * RW + sub * RPW;
+    const uint8_t* rp[RPW];
+    bool ok[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      const int vr = vr0 + i;
+      ok[i] = vr < a.n_vrows;
+      int seg, r;
+      map_row<EPI>(a, ok[i] ? vr : 0, seg, r);
+      rp[i] = a.w[seg] + (size_t)r * bpr;
+    }
+    float acc[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) acc[i] = 0.f;
+
+    for (int u = li; u < nunits; u += LPR) {
+      uint32_t w[RPW][T::NDW];
+#pragma unroll
+      for (int i = 0; i < RPW; i++) {
+        if (ok[i]) {
+          load_unit<QT>(rp[i], u, w[i]);
+        } else {
+#pragma unroll
+          for (int k = 0; k < T::NDW; k++) w[i][k] = 0;
+        }
+      }
+      const float* xu = xs + u * (UNIT + 4);
+      dot_unit<QT, RPW>(w, xu, sx + u * (UNIT / 32), sx16 + u * (UNIT / 16), acc);
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+#pragma unroll
+      for (int off = LPR / 2; off > 0; off >>= 1) acc[i] += __shfl_xor(acc[i], off, CN_WAVE);
+    }
+    if (li == 0) epilogue<EPI, RPW>(a, vr0, acc);
+  }
+}
+
+template <int QT>
+size_t gemv_smem_bytes(int K) {
+  using T = QTraits<QT>;
+  const int nunits = K / T::UNIT;
+  size_t f = (size_t)nunits * (T::UNIT + 4) + (K >> 5) + (QT == QT_Q6_K ? (K >> 4) : 0) + 4;
+  return f * sizeof(float);
+}
+
+// Lanes per row: the power of two in {16, 32, 64} that wastes the fewest lanes
+// on the last unit sweep (ties go to the wider choice).
+inline int pick_lpr(int nunits) {
+  int best = 64;
+  double best_eff = -1.0;
+  for (int lpr = 64; lpr >= 16; lpr >>= 1) {
+    const int sweeps = (nunits + lpr - 1) / lpr;
+    const double eff = (double)nunits / (double)(sweeps * lpr);
+    if (eff > best_eff + 1e-9) {
+      best_eff = eff;
+      best = lpr;
+    }
+  }
+  return best;
+}
+
+template <int QT, int RPW, int EPI>
+hipError_t launch_lpr(const GemvArgs& a, int lpr, int grid, size_t smem, hipStream_t st) {
+  switch (lpr) {
+    case 16: hipLaunchKernelGGL((gemv_kernel<QT, RPW, 16, EPI>), dim3(grid), dim3(CN_BLOCK), smem, st, a); break;
+    case 32: hipLaunchKernelGGL((gemv_kernel<QT, RPW, 32, EPI>), dim3(grid), dim3(CN_BLOCK), smem, st, a); break;
+    default: hipLaunchKernelGGL((gemv_kernel<QT, RPW, 64, EPI>), dim3(grid), dim3(CN_BLOCK), smem, st, a); break;
+  }
+  return hipGetLastError();
+}
+
+template <int QT, int EPI>
+hipError_t launch_qt(const GemvArgs& a, int num_cus, hipStream_t st) {
+  using T = QTraits<QT>;
+  constexpr int RPW = 2;
+  const int nunits = a.K / T::UNIT;
+  const int lpr = pick_lpr(nunits);
+  const int rw = RPW * (CN_WAVE / lpr);
+  const int n_iters = (a.n_vrows + rw - 1) / rw;
+  const int waves_per_block = CN_BLOCK / CN_WAVE;
+  int grid = (n_iters + waves_per_block - 1) / waves_per_block;
+  const int cap = num_cus * 8;
+  if (grid > cap) grid = cap;
+  if (grid < 1) grid = 1;
+  const size_t smem = gemv_smem_bytes<QT>(a.K);
+  return launch_lpr<QT, RPW, EPI>(a, lpr, grid, smem, st);
+}
+
+template <int EPI>
+hipError_t launch_epi(int qtype, const GemvArgs& a, int num_cus, hipStream_t st) {
+  switch (qtype) {
+    case QT_Q4_0: return launch_qt<QT_Q4_0, EPI>(a, num_cus, st);
+    case QT_Q4_K: return launch_qt<QT_Q4_K, EPI>(a, num_cus, st);
+    case QT_Q6_K: return launch_qt<QT_Q6_K, EPI>(a, num_cus, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+size_t gemv_lds_bytes(int qtype, int K) {
+  switch (qtype) {
+    case QT_Q4_0: return gemv_smem_bytes<QT_Q4_0>(K);
+    case QT_Q4_K: return gemv_smem_bytes<QT_Q4_K>(K);
+    case QT_Q6_K: return gemv_smem_bytes<QT_Q6_K>(K);
+    default: return 0;
+  }
+}
+
+bool gemv_supports(int qtype, int K) {
+  switch (qtype) {
+    case QT_Q4_0: return K > 0 && K % 64 == 0;
+    case QT_Q4_K:
+    case QT_Q6_K: return K > 0 && K % 256 == 0;
+    default: return false;
+  }
+}
+
+hipError_t gemv_launch(int qtype, int epi, const GemvArgs& a, int num_cus, hipStream_t st) {
+  switch (epi) {
+    case GEMV_EPI_STORE: return launch_epi<GEMV_EPI_STORE>(qtype, a, num_cus, st);
+    case GEMV_EPI_ADD: return launch_epi<GEMV_EPI_ADD>(qtype, a, num_cus, st);
+    case GEMV_EPI_QKV: return launch_epi<GEMV_EPI_QKV>(qtype, a, num_cus, st);
+    case GEMV_EPI_SWIGLU: return launch_epi<GEMV_EPI_SWIGLU>(qtype, a, num_cus, st);
+    case GEMV_EPI_LOGITS: return launch_epi<GEMV_EPI_LOGITS>(qtype, a, num_cus, st);
+    default: return hipErrorInvalidValue;
+  }
+}

@@ -1,0 +1,65 @@
+// kernels.h — host-side launch interface of the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+// STORE and LOGITS write y = W x; LOGITS is the LM-head instance (a separate
+// kernel so its launches are told apart from stand-alone GEMVs in profiles).
+enum { GEMV_EPI_STORE = 0, GEMV_EPI_ADD = 1, GEMV_EPI_QKV = 2, GEMV_EPI_SWIGLU = 3, GEMV_EPI_LOGITS = 4 };
+
+// One fused GEMV launch over up to three weight segments of the same type.
+// Virtual rows: STORE/ADD use segment 0 only; QKV concatenates q|k|v rows;
+// SWIGLU interleaves gate (even) and up (odd) rows.
+struct GemvArgs {
+  const uint8_t* w[3];
+  int seg_rows[3];
+  int n_vrows;
+  int K;
+  const float* x;       // K fp32 inputs
+  const float* norm_w;  // optional fused RMSNorm weight (K), nullptr = none
+  float eps;
+  float* out[3];  // out[0]: y / q / h
+  // QKV epilogue
+  const int* pos;  // device position of the token
+  int head_dim;
+  float rope_dim_inv;       // 1/head_dim
+  float rope_neg_log_base;  // -ln(freq_base)
+  void* kcache;             // layer base of the K cache
+  void* vcache;             // layer base of the V cache
+  int kv_dim;
+  int kv_f16;
+};
+
+bool gemv_supports(int qtype, int K);
+size_t gemv_lds_bytes(int qtype, int K);
+hipError_t gemv_launch(int qtype, int epi, const GemvArgs& a, int num_cus, hipStream_t st);
+
+// Embedding row gather (LlamaModel.LoadEmbedding, LlamaModel.cs:365-394).
+hipError_t embed_launch(const void* emb, int type, int dim, const int* tok, float* x, hipStream_t st);
+
+// GQA decode attention over the device KV cache (LlamaModel.ComputeAttention,
+// LlamaModel.cs:241-346).  Reads pos from device memory; seq = pos+1.
+struct AttnArgs {
+  const float* q;     // n_heads*head_dim
+  const void* kc;     // layer base, [ctx][kv_dim]
+  const void* vc;
+  float* out;         // n_heads*head_dim
+  const int* pos;
+  int n_heads, kv_mul, head_dim, kv_dim, ctx, kv_f16;
+  float scale;
+  float* part_o;      // split-K scratch: [n_heads][splits][head_dim]
+  float* part_ml;     // [n_heads][splits][2] (max, sum)
+  int splits;         // chunks of positions processed in parallel
+};
+hipError_t attn_decode_launch(const AttnArgs& a, hipStream_t st);
+
+// Greedy argmax (GreedySampler.Sample, GreedySampler.cs:13-26); writes the
+// winner to state[1] and appends it to out_tokens[state[2]++], and advances
+// state[0] (the position) by one.
+hipError_t argmax_launch(const float* logits, int n, int* state, int* out_tokens, int out_cap,
+                         hipStream_t st);
+
+// Sets state[0] = pos, state[1] = tok and, when step >= 0, state[2] = step.
+hipError_t set_state_launch(int* state, int pos, int tok, int step, hipStream_t st);

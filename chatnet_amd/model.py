@@ -1,0 +1,103 @@
+"""HipLlamaModel — the IModel of ChatNet backed by libchatnet_hip.
+
+Mirrors the reference's interface (src/ChatNet.Core/Abstractions/IModel.cs:8-19):
+    config                                   IModel.Config
+    forward(token_ids, position, logits)     IModel.Forward(ReadOnlySpan<int>, int, Span<float>)
+    close() / context manager                IDisposable.Dispose
+Every call goes through the C ABI of include/chatnet_hip.h; the weights live
+in HBM in their raw GGUF block layout (uploaded once, never dequantized on the
+host).  Like the reference (TensorMath.cs:30-37), a model is not thread-safe.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Mapping, Optional
+
+import numpy as np
+
+from . import _native
+from .config import LlamaConfig
+
+
+class HipLlamaModel:
+    def __init__(self, config: LlamaConfig, weights: Optional[Mapping] = None, device: int = 0):
+        self._lib = _native.hip_lib()
+        self._cfg = config
+        self._h = ctypes.c_void_p()
+        c = config.to_c()
+        _native.check(self._lib.chatnet_create(ctypes.byref(c), device, ctypes.byref(self._h)))
+        if weights is not None:
+            for name, t in weights.items():
+                self.upload_tensor(name, t.type, t.dims, t.data)
+
+    # -- IModel -----------------------------------------------------------
+    @property
+    def config(self) -> LlamaConfig:
+        return self._cfg
+
+    def forward(self, token_ids, position: int, logits: Optional[np.ndarray] = None) -> np.ndarray:
+        """LlamaModel.Forward (LlamaModel.cs:93-238): runs every token of the span,
+        fills `logits` (vocab floats) with the last token's logits and returns it."""
+        toks = np.ascontiguousarray(np.asarray(token_ids, dtype=np.int32).ravel())
+        if logits is None:
+            logits = np.empty(self._cfg.vocab_size, dtype=np.float32)
+        if logits.dtype != np.float32 or logits.size < self._cfg.vocab_size or not logits.flags.c_contiguous:
+            raise ValueError("logits must be a contiguous float32 array of at least vocab_size elements")
+        _native.check(self._lib.chatnet_forward(
+            self._h, toks.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), int(toks.size), int(position),
+            logits.ctypes.data))
+        return logits
+
+    # -- extras over the reference interface -----------------------------
+    def upload_tensor(self, name: str, ggml_type: int, dims, data: np.ndarray) -> None:
+        arr = np.ascontiguousarray(data).view(np.uint8).ravel()
+        d = (ctypes.c_uint64 * len(dims))(*[int(x) for x in dims])
+        _native.check(self._lib.chatnet_upload_tensor(
+            self._h, name.encode(), int(ggml_type), d, len(dims), arr.ctypes.data, int(arr.nbytes)))
+
+    def argmax(self) -> int:
+        """Device-side GreedySampler.Sample over the last logits."""
+        out = ctypes.c_int32()
+        _native.check(self._lib.chatnet_argmax(self._h, ctypes.byref(out)))
+        return int(out.value)
+
+    def get_logits(self) -> np.ndarray:
+        out = np.empty(self._cfg.vocab_size, dtype=np.float32)
+        _native.check(self._lib.chatnet_get_logits(self._h, out.ctypes.data))
+        return out
+
+    def generate_greedy(self, prompt, max_tokens: int, eos_token: int = -1) -> np.ndarray:
+        """InferenceEngine.Generate's greedy loop (InferenceEngine.cs:234-307) on the device."""
+        p = np.ascontiguousarray(np.asarray(prompt, dtype=np.int32).ravel())
+        out = np.empty(max(max_tokens, 1), dtype=np.int32)
+        n = ctypes.c_int()
+        _native.check(self._lib.chatnet_generate_greedy(
+            self._h, p.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), int(p.size), int(max_tokens),
+            int(eos_token), out.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), ctypes.byref(n)))
+        return out[: n.value].copy()
+
+    def decode_greedy(self, max_tokens: int, eos_token: int = -1) -> np.ndarray:
+        """Greedy continuation after forward() (InferenceEngine.cs:241-307) on the device."""
+        out = np.empty(max(max_tokens, 1), dtype=np.int32)
+        n = ctypes.c_int()
+        _native.check(self._lib.chatnet_decode_greedy(
+            self._h, int(max_tokens), int(eos_token), out.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+            ctypes.byref(n)))
+        return out[: n.value].copy()
+
+    def close(self) -> None:
+        if self._h:
+            self._lib.chatnet_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

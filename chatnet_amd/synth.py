@@ -1,0 +1,121 @@
+"""Seeded synthetic Llama checkpoints in GGUF block layouts.
+
+A checkpoint is a dict: GGUF tensor name -> SynthTensor(type, dims, data),
+with dims in GGUF order (ne0 = inner dimension) and data the raw bytes the
+reference would mmap (MemoryMappedWeights.GetTensorPointer,
+MemoryMappedWeights.cs:76-84).  Weights are N(0, 0.02) quantized by
+libchatnet_synth; embeddings are F32 N(0, 0.02); norm weights are 1.0.
+"""
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+
+import numpy as np
+
+from . import _native
+from .config import LlamaConfig
+
+SIGMA = 0.02
+
+# Quantization mixes.  "q4_0": every matrix Q4_0.  "q4_k_m": Q4_K for the
+# attention and ffn_gate/up matrices, Q6_K for ffn_down and output.
+MIXES = {
+    "q4_0": {"attn": _native.GGML_Q4_0, "gate_up": _native.GGML_Q4_0, "down": _native.GGML_Q4_0,
+             "output": _native.GGML_Q4_0},
+    "q4_k_m": {"attn": _native.GGML_Q4_K, "gate_up": _native.GGML_Q4_K, "down": _native.GGML_Q6_K,
+               "output": _native.GGML_Q6_K},
+    "q4_k": {"attn": _native.GGML_Q4_K, "gate_up": _native.GGML_Q4_K, "down": _native.GGML_Q4_K,
+             "output": _native.GGML_Q4_K},
+    "q6_k": {"attn": _native.GGML_Q6_K, "gate_up": _native.GGML_Q6_K, "down": _native.GGML_Q6_K,
+             "output": _native.GGML_Q6_K},
+}
+
+
+@dataclasses.dataclass
+class SynthTensor:
+    type: int
+    dims: tuple  # GGUF order: (ne0, ne1)
+    data: np.ndarray  # uint8 raw bytes (float32 view for F32)
+
+    @property
+    def n_elements(self) -> int:
+        n = 1
+        for d in self.dims:
+            n *= int(d)
+        return n
+
+
+def stream_id(name: str) -> int:
+    return int(_native.synth_lib().chatnet_synth_stream_id(name.encode()))
+
+
+def normal(seed: int, name: str, n: int, sigma: float = SIGMA, start: int = 0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    _native.synth_lib().chatnet_synth_normal(seed, stream_id(name), start, n, sigma, out.ctypes.data)
+    return out
+
+
+def quantize(ggml_type: int, w: np.ndarray) -> np.ndarray:
+    """Quantizes a float32 array (length a multiple of the block) to raw bytes."""
+    w = np.ascontiguousarray(w, dtype=np.float32).ravel()
+    nbytes = _native.tensor_nbytes(ggml_type, w.size) if ggml_type != _native.GGML_F32 else w.size * 4
+    out = np.empty(nbytes, dtype=np.uint8)
+    wrote = _native.synth_lib().chatnet_synth_quantize(ggml_type, w.ctypes.data, w.size, out.ctypes.data)
+    if wrote != nbytes:
+        raise ValueError(f"quantize: type {ggml_type} cannot hold {w.size} elements")
+    return out
+
+
+def float_to_half(f: float) -> int:
+    return int(_native.synth_lib().chatnet_float_to_half(ctypes.c_float(f)))
+
+
+def tensor(ggml_type: int, seed: int, name: str, rows: int, cols: int, sigma: float = SIGMA) -> SynthTensor:
+    """rows x cols matrix (GGUF dims (cols, rows)) of N(0, sigma) weights in `ggml_type`."""
+    n = rows * cols
+    if ggml_type == _native.GGML_F32:
+        data = normal(seed, name, n, sigma).view(np.uint8)
+    else:
+        nbytes = _native.tensor_nbytes(ggml_type, n)
+        data = np.empty(nbytes, dtype=np.uint8)
+        wrote = _native.synth_lib().chatnet_synth_tensor(ggml_type, seed, stream_id(name), sigma, n,
+                                                         data.ctypes.data)
+        if wrote != nbytes:
+            raise ValueError(f"synth_tensor failed for {name}")
+    return SynthTensor(ggml_type, (cols, rows), data)
+
+
+def tokens(seed: int, name: str, n: int, vocab: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.int32)
+    _native.synth_lib().chatnet_synth_tokens(seed, stream_id(name), n, vocab, out.ctypes.data)
+    return out
+
+
+def llama_checkpoint(cfg: LlamaConfig, seed: int = 1234, mix: str = "q4_0",
+                     with_output: bool = True) -> dict:
+    """All tensors LlamaWeights.ResolveAll (LlamaWeights.cs:78-145) looks up."""
+    q = MIXES[mix]
+    ck = {}
+    ck["token_embd.weight"] = tensor(_native.GGML_F32, seed, "token_embd.weight", cfg.vocab_size, cfg.dim)
+    ones = np.ones(cfg.dim, dtype=np.float32)
+    ck["output_norm.weight"] = SynthTensor(_native.GGML_F32, (cfg.dim,), ones.view(np.uint8).copy())
+    if with_output:
+        ck["output.weight"] = tensor(q["output"], seed, "output.weight", cfg.vocab_size, cfg.dim)
+    kvd = cfg.kv_dim
+    for l in range(cfg.n_layers):
+        p = f"blk.{l}."
+        ck[p + "attn_norm.weight"] = SynthTensor(_native.GGML_F32, (cfg.dim,), ones.view(np.uint8).copy())
+        ck[p + "ffn_norm.weight"] = SynthTensor(_native.GGML_F32, (cfg.dim,), ones.view(np.uint8).copy())
+        ck[p + "attn_q.weight"] = tensor(q["attn"], seed, p + "attn_q.weight", cfg.dim, cfg.dim)
+        ck[p + "attn_k.weight"] = tensor(q["attn"], seed, p + "attn_k.weight", kvd, cfg.dim)
+        ck[p + "attn_v.weight"] = tensor(q["attn"], seed, p + "attn_v.weight", kvd, cfg.dim)
+        ck[p + "attn_output.weight"] = tensor(q["attn"], seed, p + "attn_output.weight", cfg.dim, cfg.dim)
+        ck[p + "ffn_gate.weight"] = tensor(q["gate_up"], seed, p + "ffn_gate.weight", cfg.hidden_dim, cfg.dim)
+        ck[p + "ffn_up.weight"] = tensor(q["gate_up"], seed, p + "ffn_up.weight", cfg.hidden_dim, cfg.dim)
+        ck[p + "ffn_down.weight"] = tensor(q["down"], seed, p + "ffn_down.weight", cfg.dim, cfg.hidden_dim)
+    return ck
+
+
+def checkpoint_bytes(ck: dict) -> int:
+    return sum(int(t.data.nbytes) for t in ck.values())

@@ -1,0 +1,168 @@
+/*
+ * chatnet_hip.h — C ABI of libchatnet_hip.so, the MI355X (gfx950) quantized
+ * Llama forward pass that stands in for ChatNet's CPU hot path.
+ *
+ * The reference has no FFI; its hot path sits behind the C# interface
+ * IModel (src/ChatNet.Core/Abstractions/IModel.cs:8-19) implemented by
+ * LlamaModel (src/ChatNet.Core/Models/Llama/LlamaModel.cs:18-611).  Each entry
+ * point below names the reference member whose behaviour it takes over.
+ *
+ * Conventions
+ *   - Every function returns CHATNET_OK (0) or a negative chatnet_status.
+ *     chatnet_last_error() returns a thread-local message for the last
+ *     failure on the calling thread.
+ *   - The library owns all device memory of a model handle.  Host pointers
+ *     are borrowed for the duration of the call only.
+ *   - One HIP stream per model handle.  A handle is not thread-safe, which is
+ *     the reference's contract too (static per-kernel state in
+ *     src/ChatNet.Core/Tensors/TensorMath.cs:30-37).
+ *   - Only types, pointers and sizes cross the boundary; no torch types.
+ */
+#ifndef CHATNET_HIP_H
+#define CHATNET_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define CHATNET_API __attribute__((visibility("default")))
+#else
+#define CHATNET_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  Each maps to the .NET exception the reference throws for
+ * the same condition, so a P/Invoke adapter can rethrow it. */
+typedef enum chatnet_status {
+  CHATNET_OK = 0,
+  CHATNET_ERR_INVALID_ARG = -1,      /* ArgumentException */
+  CHATNET_ERR_NOT_FOUND = -2,        /* KeyNotFoundException, MemoryMappedWeights.cs:50-53 */
+  CHATNET_ERR_UNSUPPORTED_TYPE = -3, /* NotSupportedException, LlamaModel.cs:564-565 */
+  CHATNET_ERR_SIZE_MISMATCH = -4,    /* byte count differs from GgufTensorInfo.ByteSize */
+  CHATNET_ERR_OUT_OF_RANGE = -5,     /* IndexOutOfRangeException (position >= context, token >= vocab) */
+  CHATNET_ERR_NO_DEVICE = -6,        /* no usable HIP device */
+  CHATNET_ERR_HIP = -7,              /* a HIP runtime call failed */
+  CHATNET_ERR_OUT_OF_MEMORY = -8     /* OutOfMemoryException */
+} chatnet_status;
+
+/* GGML tensor type codes, identical to GgmlType
+ * (src/ChatNet.Core/Gguf/GgufConstants.cs:41-71). */
+enum {
+  CHATNET_GGML_F32 = 0,
+  CHATNET_GGML_F16 = 1,
+  CHATNET_GGML_Q4_0 = 2,
+  CHATNET_GGML_Q4_K = 12,
+  CHATNET_GGML_Q6_K = 14
+};
+
+/* KV-cache element type. */
+enum { CHATNET_KV_F32 = 0, CHATNET_KV_F16 = 1 };
+
+/* Model hyper-parameters.  Mirrors LlamaConfig
+ * (src/ChatNet.Core/Models/Llama/LlamaConfig.cs:8-38), which is derived from
+ * ModelConfig (src/ChatNet.Core/Abstractions/ModelConfig.cs:6-27). */
+typedef struct chatnet_config {
+  int32_t dim;            /* LlamaConfig.Dim        (embedding_length)      */
+  int32_t hidden_dim;     /* LlamaConfig.HiddenDim  (feed_forward_length)   */
+  int32_t n_layers;       /* LlamaConfig.LayerCount                         */
+  int32_t n_heads;        /* LlamaConfig.HeadCount                          */
+  int32_t n_kv_heads;     /* LlamaConfig.KvHeadCount                        */
+  int32_t head_dim;       /* LlamaConfig.HeadDim                            */
+  int32_t vocab_size;     /* LlamaConfig.VocabSize                          */
+  int32_t context_length; /* LlamaConfig.ContextLength = KV-cache capacity  */
+  float rope_freq_base;   /* LlamaConfig.RopeFreqBase                       */
+  float rms_norm_eps;     /* LlamaConfig.RmsNormEps                         */
+  int32_t kv_dtype;       /* CHATNET_KV_F32 (reference) or CHATNET_KV_F16   */
+  int32_t reserved;       /* must be 0                                      */
+} chatnet_config;
+
+typedef struct chatnet_model chatnet_model;
+
+/* Creates a model on HIP device `device`: allocates the KV cache
+ * (n_layers x context_length x n_kv_heads*head_dim per K and V) and all
+ * activation scratch in HBM.  Replaces the constructor
+ * LlamaModel(ModelConfig, LlamaWeights) (LlamaModel.cs:48-88). */
+CHATNET_API int chatnet_create(const chatnet_config* cfg, int device, chatnet_model** out);
+
+/* Copies one GGUF tensor's raw bytes host->device once, in its on-disk block
+ * layout (no host-side dequantization).  `name` is the GGUF tensor name the
+ * reference resolves in LlamaWeights.ResolveAll (LlamaWeights.cs:78-145):
+ * token_embd.weight, output.weight, output_norm.weight and
+ * blk.{l}.{attn_norm,ffn_norm,attn_q,attn_k,attn_v,attn_output,
+ * ffn_gate,ffn_up,ffn_down}.weight.  `dims` is GGUF order (ne0 = inner).
+ * `nbytes` must equal GgufTensorInfo.ByteSize (GgufTensorInfo.cs:30-113).
+ * Replaces MemoryMappedWeights.GetTensorPointer (MemoryMappedWeights.cs:76-84)
+ * as the source of weight bytes for the forward pass. */
+CHATNET_API int chatnet_upload_tensor(chatnet_model* m, const char* name, uint32_t ggml_type,
+                          const uint64_t* dims, int ndims, const void* host,
+                          uint64_t nbytes);
+
+/* IModel.Forward(ReadOnlySpan<int> tokenIds, int position, Span<float> logits)
+ * (IModel.cs:18, LlamaModel.cs:93-238).  Processes tokens[0..n) at positions
+ * position..position+n-1, writing their K/V into the cache; logits of the last
+ * token stay on the device and are copied to `logits_host` (vocab_size
+ * floats) when it is non-NULL.  Spans of n > 1 run as one batched prefill. */
+CHATNET_API int chatnet_forward(chatnet_model* m, const int32_t* tokens, int n, int position,
+                    float* logits_host);
+
+/* GreedySampler.Sample (src/ChatNet.Core/Samplers/GreedySampler.cs:13-26) on
+ * the device-resident logits of the last forward: index of the first maximum. */
+CHATNET_API int chatnet_argmax(chatnet_model* m, int32_t* out_token);
+
+/* Greedy generation loop of InferenceEngine.Generate
+ * (src/ChatNet.Core/InferenceEngine.cs:234-307) with the tokenizer, EOS and
+ * stop-string checks left to the caller: forwards the prompt at positions
+ * 0..n_prompt-1, then emits up to max_tokens greedy tokens, feeding each back
+ * at the next position; stops early when the next position would reach
+ * context_length - 1 (InferenceEngine.cs:295-298).  The decode loop stays on
+ * the device (one HIP graph per step, token fed back through device memory).
+ * Output stops before the first `eos_token` (InferenceEngine.cs:258-261);
+ * eos_token < 0 disables the check.  Writes the generated ids to out_tokens
+ * (room for max_tokens ids) and their count to *n_out. */
+CHATNET_API int chatnet_generate_greedy(chatnet_model* m, const int32_t* prompt, int n_prompt,
+                            int max_tokens, int32_t eos_token, int32_t* out_tokens,
+                            int* n_out);
+
+/* The decode half of InferenceEngine.Generate (InferenceEngine.cs:241-307):
+ * continues after a chatnet_forward of positions ..p-1 by sampling greedily
+ * from its logits, emitting the token, forwarding it at position p, and so on,
+ * with the same context and EOS rules as chatnet_generate_greedy.  Every
+ * decode step is one replay of a captured HIP graph; the host synchronizes
+ * once, at the end. */
+CHATNET_API int chatnet_decode_greedy(chatnet_model* m, int max_tokens, int32_t eos_token,
+                                      int32_t* out_tokens, int* n_out);
+
+/* Copies the device logits of the last forward to the host (vocab_size floats). */
+CHATNET_API int chatnet_get_logits(chatnet_model* m, float* logits_host);
+
+/* Quantized matrix product on caller-owned device buffers, the batched form of
+ * TensorMath.MatVecMulQ4_0 / MatVecMulQ6K / MatVecMulGeneric
+ * (TensorMath.cs:548-656) as dispatched by LlamaModel.MatVecMulByType
+ * (LlamaModel.cs:470-567):
+ *   y[n][m] = sum_k W[m][k] * x[n][k],  0 <= n < N, 0 <= m < M
+ * W is M rows of raw GGUF blocks (row stride K/block*bytes_per_block), x is
+ * N x K fp32 row-major, y is N x M fp32 row-major.  N == 1 runs the fused
+ * dequant-GEMV; N > 1 runs the dequant-to-LDS bf16 MFMA GEMM.  `stream` is a
+ * hipStream_t (NULL = default stream).  Asynchronous on `stream`. */
+CHATNET_API int chatnet_matmul(uint32_t ggml_type, const void* w_dev, const float* x_dev,
+                   float* y_dev, int M, int K, int N, void* stream);
+
+/* Bytes of one GGUF tensor of `ggml_type` with `n_elements` elements, per
+ * GgufTensorInfo.ByteSize (GgufTensorInfo.cs:30-113); 0 for an unknown type. */
+CHATNET_API uint64_t chatnet_tensor_nbytes(uint32_t ggml_type, uint64_t n_elements);
+
+/* Frees every device buffer of the model.  Replaces LlamaModel.Dispose
+ * (LlamaModel.cs:606-609).  NULL is accepted. */
+CHATNET_API void chatnet_destroy(chatnet_model* m);
+
+/* Thread-local message describing the last error on this thread ("" if none). */
+CHATNET_API const char* chatnet_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CHATNET_HIP_H */

@@ -1,0 +1,611 @@
+/*
+ * chatnet_oracle.c — CPU oracle (TEST INFRASTRUCTURE ONLY; see the header).
+ *
+ * Plain-C restatement of ChatNet's quantized Llama forward pass.  Citations
+ * are path:line into the ChatNet sources.  Build with -ffp-contract=off so
+ * that every `a*b + c` rounds twice, as RyuJIT's Vector128/Vector<T> code does.
+ */
+#include "chatnet_oracle.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* TensorMath.cs:28 — rows below this run serially. */
+#define PARALLEL_ROW_THRESHOLD 512
+/* Vector<float>.Count on AVX2 hardware (256-bit Vector<T>). */
+#define VLEN 8
+
+static int g_threads = 1;
+
+void oracle_set_threads(int n) { g_threads = n > 0 ? n : 1; }
+int oracle_get_threads(void) { return g_threads; }
+
+/* ---------------------------------------------------------------------------
+ * DequantQ4_0.HalfToFloat (DequantQ4_0.cs:190-194): exact IEEE binary16 ->
+ * binary32, subnormals, infinities and NaN payloads included.
+ * ------------------------------------------------------------------------- */
+float oracle_half_to_float(uint16_t h) {
+  uint32_t sign = (uint32_t)(h >> 15) << 31;
+  uint32_t exp = (h >> 10) & 0x1F;
+  uint32_t man = h & 0x3FF;
+  uint32_t bits;
+  if (exp == 0) {
+    if (man == 0) {
+      bits = sign;
+    } else { /* subnormal: value = man * 2^-24, exact in binary32 */
+      int e = -1;
+      do {
+        man <<= 1;
+        e++;
+      } while ((man & 0x400) == 0);
+      man &= 0x3FF;
+      bits = sign | ((uint32_t)(127 - 15 - e) << 23) | (man << 13);
+    }
+  } else if (exp == 31) {
+    bits = sign | 0x7F800000u | (man << 13);
+  } else {
+    bits = sign | ((exp - 15 + 127) << 23) | (man << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+static inline float h2f(const uint8_t* p) { return oracle_half_to_float((uint16_t)(p[0] | (p[1] << 8))); }
+
+/* Vector128.Sum for float: ((v0 + v1) + (v2 + v3)).  The JIT's lane order is
+ * not visible in the C# source: parity unpinned at the last ulp. */
+static inline float vsum4(const float v[4]) { return (v[0] + v[1]) + (v[2] + v[3]); }
+
+/* TensorMath.VectorSum (TensorMath.cs:750-758) / LlamaModel.VectorSumFast
+ * (LlamaModel.cs:353-362): sequential lane sum starting from 0. */
+static inline float vsum8(const float v[VLEN]) {
+  float s = 0.0f;
+  for (int i = 0; i < VLEN; i++) s += v[i];
+  return s;
+}
+
+/* ---------------------------------------------------------------------------
+ * Q4_0 (DequantQ4_0.cs)
+ * ------------------------------------------------------------------------- */
+
+/* DequantQ4_0.Dequantize (DequantQ4_0.cs:28-58), partial last block included. */
+void oracle_dequant_q4_0(const uint8_t* src, float* out, int n) {
+  int blocks = (n + 31) / 32;
+  int so = 0, dst = 0;
+  for (int b = 0; b < blocks; b++) {
+    float scale = h2f(src + so);
+    so += 2;
+    int remaining = n - dst;
+    int half = remaining < 16 ? remaining : 16;
+    for (int j = 0; j < half; j++) out[dst + j] = (float)((src[so + j] & 0x0F) - 8) * scale;
+    int second = remaining < 32 ? (remaining > 16 ? remaining - 16 : 0) : 16;
+    for (int j = 0; j < second; j++) out[dst + 16 + j] = (float)(((src[so + j] >> 4) & 0x0F) - 8) * scale;
+    so += 16;
+    dst += half + second;
+  }
+}
+
+/* DequantQ4_0.DotProductVec128 (DequantQ4_0.cs:80-149). */
+float oracle_dot_q4_0(const uint8_t* row, const float* x, int n) {
+  int blocks = n / 32;
+  float acc0[4] = {0, 0, 0, 0}, acc1[4] = {0, 0, 0, 0};
+  const uint8_t* src = row;
+  const float* in = x;
+  for (int b = 0; b < blocks; b++) {
+    float scale = h2f(src);
+    src += 2;
+    float lo[16], hi[16];
+    for (int j = 0; j < 16; j++) {
+      lo[j] = (float)((int)(src[j] & 0x0F) - 8);
+      hi[j] = (float)((int)((src[j] >> 4) & 0x0F) - 8);
+    }
+    float ba0[4] = {0, 0, 0, 0}, ba1[4] = {0, 0, 0, 0};
+    /* :121-124 then :135-138 — the accumulator alternates every 4 lanes */
+    for (int l = 0; l < 4; l++) ba0[l] = ba0[l] + lo[l] * in[l];
+    for (int l = 0; l < 4; l++) ba1[l] = ba1[l] + lo[4 + l] * in[4 + l];
+    for (int l = 0; l < 4; l++) ba0[l] = ba0[l] + lo[8 + l] * in[8 + l];
+    for (int l = 0; l < 4; l++) ba1[l] = ba1[l] + lo[12 + l] * in[12 + l];
+    for (int l = 0; l < 4; l++) ba0[l] = ba0[l] + hi[l] * in[16 + l];
+    for (int l = 0; l < 4; l++) ba1[l] = ba1[l] + hi[4 + l] * in[20 + l];
+    for (int l = 0; l < 4; l++) ba0[l] = ba0[l] + hi[8 + l] * in[24 + l];
+    for (int l = 0; l < 4; l++) ba1[l] = ba1[l] + hi[12 + l] * in[28 + l];
+    /* :141-142 */
+    for (int l = 0; l < 4; l++) {
+      acc0[l] = acc0[l] + ba0[l] * scale;
+      acc1[l] = acc1[l] + ba1[l] * scale;
+    }
+    src += 16;
+    in += 32;
+  }
+  float s[4];
+  for (int l = 0; l < 4; l++) s[l] = acc0[l] + acc1[l];
+  return vsum4(s); /* :148 */
+}
+
+/* ---------------------------------------------------------------------------
+ * Q4_K (DequantQ4K.cs) — the reference's own nibble order: sub-block s uses
+ * qs[16s..16s+15]; low nibbles are elements 32s+0..15, high nibbles 32s+16..31.
+ * ------------------------------------------------------------------------- */
+
+/* DequantQ4K.DecodeScales / DecodeScalesUnsafe (DequantQ4K.cs:218-264),
+ * llama.cpp get_scale_min_k4. */
+static void q4k_scales(const uint8_t* q, int sc[8], int m[8]) {
+  for (int j = 0; j < 4; j++) {
+    sc[j] = q[j] & 63;
+    m[j] = q[j + 4] & 63;
+  }
+  for (int j = 4; j < 8; j++) {
+    sc[j] = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+    m[j] = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+  }
+}
+
+/* DequantQ4K.Dequantize (DequantQ4K.cs:37-77). */
+void oracle_dequant_q4_k(const uint8_t* src, float* out, int n) {
+  int blocks = n / 256;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = src + (size_t)b * 144;
+    float d = h2f(blk + 0), dmin = h2f(blk + 2);
+    int sc[8], m[8];
+    q4k_scales(blk + 4, sc, m);
+    for (int s = 0; s < 8; s++) {
+      float dsc = d * (float)sc[s];
+      float dm = dmin * (float)m[s];
+      const uint8_t* qs = blk + 16 + s * 16;
+      float* o = out + (size_t)b * 256 + s * 32;
+      for (int j = 0; j < 16; j++) {
+        o[j] = dsc * (float)(qs[j] & 0x0F) - dm;
+        o[j + 16] = dsc * (float)((qs[j] >> 4) & 0x0F) - dm;
+      }
+    }
+  }
+}
+
+/* DequantQ4K.DotProductVec128 (DequantQ4K.cs:89-163). */
+float oracle_dot_q4_k(const uint8_t* row, const float* x, int n) {
+  int blocks = n / 256;
+  float acc[4] = {0, 0, 0, 0};
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = row + (size_t)b * 144;
+    const float* in = x + (size_t)b * 256;
+    float d = h2f(blk + 0), dmin = h2f(blk + 2);
+    int sc[8], m[8];
+    q4k_scales(blk + 4, sc, m);
+    float ba[4] = {0, 0, 0, 0};
+    for (int s = 0; s < 8; s++) {
+      float dsc = d * (float)sc[s];
+      float dm = dmin * (float)m[s];
+      const uint8_t* qs = blk + 16 + s * 16;
+      const float* xi = in + s * 32;
+      /* :137-140 low nibbles, then :151-154 high nibbles, 4 lanes at a time */
+      for (int c = 0; c < 4; c++)
+        for (int l = 0; l < 4; l++)
+          ba[l] = ba[l] + ((float)(qs[4 * c + l] & 0x0F) * dsc - dm) * xi[4 * c + l];
+      for (int c = 0; c < 4; c++)
+        for (int l = 0; l < 4; l++)
+          ba[l] = ba[l] + ((float)((qs[4 * c + l] >> 4) & 0x0F) * dsc - dm) * xi[16 + 4 * c + l];
+    }
+    for (int l = 0; l < 4; l++) acc[l] = acc[l] + ba[l]; /* :157 */
+  }
+  return vsum4(acc); /* :162 */
+}
+
+/* ---------------------------------------------------------------------------
+ * Q6_K (DequantQ6K.cs): ql[128] @0, qh[64] @128, int8 scales[16] @192, d @208.
+ * ------------------------------------------------------------------------- */
+
+/* DequantQ6K.Dequantize (DequantQ6K.cs:37-88). */
+void oracle_dequant_q6_k(const uint8_t* src, float* out, int n) {
+  int blocks = n / 256;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = src + (size_t)b * 210;
+    float d = h2f(blk + 208);
+    const int8_t* sc = (const int8_t*)(blk + 192);
+    for (int h = 0; h < 2; h++) {
+      const uint8_t* ql = blk + h * 64;
+      const uint8_t* qh = blk + 128 + h * 32;
+      float* o = out + (size_t)b * 256 + h * 128;
+      for (int l = 0; l < 32; l++) {
+        int si = h * 8 + l / 16;
+        int q1 = ((ql[l] & 0x0F) | (((qh[l] >> 0) & 3) << 4)) - 32;
+        int q2 = ((ql[l + 32] & 0x0F) | (((qh[l] >> 2) & 3) << 4)) - 32;
+        int q3 = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+        int q4 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+        o[l] = d * (float)sc[si] * (float)q1;
+        o[l + 32] = d * (float)sc[si + 2] * (float)q2;
+        o[l + 64] = d * (float)sc[si + 4] * (float)q3;
+        o[l + 96] = d * (float)sc[si + 6] * (float)q4;
+      }
+    }
+  }
+}
+
+/* DequantQ6K.DotProductVec128 (DequantQ6K.cs:104-188). */
+float oracle_dot_q6_k(const uint8_t* row, const float* x, int n) {
+  int blocks = n / 256;
+  float acc[4] = {0, 0, 0, 0};
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = row + (size_t)b * 210;
+    float d = h2f(blk + 208);
+    const int8_t* sc = (const int8_t*)(blk + 192);
+    float ba[4] = {0, 0, 0, 0};
+    for (int h = 0; h < 2; h++) {
+      const uint8_t* ql = blk + h * 64;
+      const uint8_t* qh = blk + 128 + h * 32;
+      const float* in = x + (size_t)b * 256 + h * 128;
+      for (int lb = 0; lb < 2; lb++) {
+        int si = h * 8 + lb;
+        float s0 = (float)sc[si], s2 = (float)sc[si + 2], s4 = (float)sc[si + 4], s6 = (float)sc[si + 6];
+        for (int l = lb * 16; l < lb * 16 + 16; l += 4) {
+          for (int i = 0; i < 4; i++) {
+            float q1 = (float)(((ql[l + i] & 0xF) | (((qh[l + i] >> 0) & 3) << 4)) - 32);
+            ba[i] = ba[i] + q1 * s0 * in[l + i];
+          }
+          for (int i = 0; i < 4; i++) {
+            float q2 = (float)(((ql[l + 32 + i] & 0xF) | (((qh[l + i] >> 2) & 3) << 4)) - 32);
+            ba[i] = ba[i] + q2 * s2 * in[l + 32 + i];
+          }
+          for (int i = 0; i < 4; i++) {
+            float q3 = (float)(((ql[l + i] >> 4) | (((qh[l + i] >> 4) & 3) << 4)) - 32);
+            ba[i] = ba[i] + q3 * s4 * in[l + 64 + i];
+          }
+          for (int i = 0; i < 4; i++) {
+            float q4 = (float)(((ql[l + 32 + i] >> 4) | (((qh[l + i] >> 6) & 3) << 4)) - 32);
+            ba[i] = ba[i] + q4 * s6 * in[l + 96 + i];
+          }
+        }
+      }
+    }
+    for (int i = 0; i < 4; i++) acc[i] = acc[i] + ba[i] * d; /* :182 */
+  }
+  return vsum4(acc);
+}
+
+/* ---------------------------------------------------------------------------
+ * fp32 ops (TensorMath.cs)
+ * ------------------------------------------------------------------------- */
+
+/* TensorMath.DotProductSimd (TensorMath.cs:666-702). */
+float oracle_dot_f32(const float* a, const float* b, int n) {
+  float sum = 0.0f;
+  int i = 0;
+  float v0[VLEN] = {0}, v1[VLEN] = {0};
+  int lim2 = n - 2 * VLEN + 1;
+  for (; i < lim2; i += 2 * VLEN)
+    for (int l = 0; l < VLEN; l++) {
+      v0[l] = v0[l] + a[i + l] * b[i + l];
+      v1[l] = v1[l] + a[i + VLEN + l] * b[i + VLEN + l];
+    }
+  int lim1 = n - VLEN + 1;
+  for (; i < lim1; i += VLEN)
+    for (int l = 0; l < VLEN; l++) v0[l] = v0[l] + a[i + l] * b[i + l];
+  float s[VLEN];
+  for (int l = 0; l < VLEN; l++) s[l] = v0[l] + v1[l];
+  sum = vsum8(s);
+  for (; i < n; i++) sum += a[i] * b[i];
+  return sum;
+}
+
+/* LlamaModel.MatVecMulF16 (LlamaModel.cs:570-598): dequantize the row, then a
+ * sequential scalar dot. */
+static float dot_f16_row(const uint8_t* row, const float* x, int n, float* buf) {
+  for (int i = 0; i < n; i++) buf[i] = h2f(row + 2 * i);
+  float dot = 0.0f;
+  for (int i = 0; i < n; i++) dot += buf[i] * x[i];
+  return dot;
+}
+
+/* TensorMath.MatVecMulQ4_0 / MatVecMulQ6K / MatVecMulGeneric / MatVecMul
+ * (TensorMath.cs:527-656) dispatched as LlamaModel.MatVecMulByType
+ * (LlamaModel.cs:470-567).  Rows are independent (TensorMath.cs:47-51), so the
+ * thread count never changes a result. */
+int oracle_matvec(uint32_t type, const void* W, const float* x, float* y, int M, int K) {
+  const uint8_t* w = (const uint8_t*)W;
+  size_t bpr;
+  float (*dot)(const uint8_t*, const float*, int) = NULL;
+  switch (type) {
+    case ORACLE_Q4_0: bpr = (size_t)(K / 32) * 18; dot = oracle_dot_q4_0; break;
+    case ORACLE_Q4_K: bpr = (size_t)(K / 256) * 144; dot = oracle_dot_q4_k; break;
+    case ORACLE_Q6_K: bpr = (size_t)(K / 256) * 210; dot = oracle_dot_q6_k; break;
+    case ORACLE_F32: {
+      const float* wf = (const float*)W;
+      for (int r = 0; r < M; r++) y[r] = oracle_dot_f32(wf + (size_t)r * K, x, K);
+      return 0;
+    }
+    case ORACLE_F16: {
+      float* buf = (float*)malloc(sizeof(float) * (size_t)K);
+      for (int r = 0; r < M; r++) y[r] = dot_f16_row(w + (size_t)r * K * 2, x, K, buf);
+      free(buf);
+      return 0;
+    }
+    default: return -3;
+  }
+  if (M >= PARALLEL_ROW_THRESHOLD && g_threads > 1) {
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (int r = 0; r < M; r++) y[r] = dot(w + (size_t)r * bpr, x, K);
+  } else {
+    for (int r = 0; r < M; r++) y[r] = dot(w + (size_t)r * bpr, x, K);
+  }
+  return 0;
+}
+
+/* TensorMath.RmsNorm (TensorMath.cs:97-165). */
+void oracle_rmsnorm(const float* x, const float* w, float* out, int n, float eps) {
+  float sumSq = 0.0f;
+  int i = 0;
+  if (n >= VLEN) {
+    float a0[VLEN] = {0}, a1[VLEN] = {0};
+    int lim2 = n - 2 * VLEN + 1;
+    for (; i < lim2; i += 2 * VLEN)
+      for (int l = 0; l < VLEN; l++) {
+        a0[l] = a0[l] + x[i + l] * x[i + l];
+        a1[l] = a1[l] + x[i + VLEN + l] * x[i + VLEN + l];
+      }
+    int lim1 = n - VLEN + 1;
+    for (; i < lim1; i += VLEN)
+      for (int l = 0; l < VLEN; l++) a0[l] = a0[l] + x[i + l] * x[i + l];
+    float s[VLEN];
+    for (int l = 0; l < VLEN; l++) s[l] = a0[l] + a1[l];
+    sumSq = vsum8(s);
+  }
+  for (; i < n; i++) sumSq += x[i] * x[i];
+  float rms = 1.0f / sqrtf(sumSq / (float)n + eps); /* :142 */
+  for (i = 0; i < n; i++) out[i] = x[i] * rms * w[i]; /* :155, :162 */
+}
+
+/* TensorMath.Softmax (TensorMath.cs:177-241). */
+void oracle_softmax(float* d, int n) {
+  float mx = -INFINITY;
+  for (int i = 0; i < n; i++)
+    if (d[i] > mx) mx = d[i];
+  float sum = 0.0f;
+  for (int i = 0; i < n; i++) {
+    float v = expf(d[i] - mx);
+    d[i] = v;
+    sum += v;
+  }
+  if (sum > 0.0f) {
+    float inv = 1.0f / sum;
+    for (int i = 0; i < n; i++) d[i] = d[i] * inv;
+  }
+}
+
+/* TensorMath.SiluElementwiseMul (TensorMath.cs:253-286). */
+void oracle_silu_mul(float* gate, const float* up, int n) {
+  for (int i = 0; i < n; i++) {
+    float xv = gate[i];
+    gate[i] = (xv / (1.0f + expf(-xv))) * up[i];
+  }
+}
+
+/* TensorMath.Add (TensorMath.cs:712-733). */
+void oracle_add(float* a, const float* b, int n) {
+  for (int i = 0; i < n; i++) a[i] = a[i] + b[i];
+}
+
+/* TensorMath.ApplyRoPE (TensorMath.cs:408-458), rotaryDim = headDim. */
+void oracle_rope(float* q, float* k, int position, int hd, int nh, int nkv, float base) {
+  float negLogBase = -logf(base);
+  float dimInv = 1.0f / (float)hd;
+  for (int pass = 0; pass < 2; pass++) {
+    float* v = pass == 0 ? q : k;
+    int heads = pass == 0 ? nh : nkv;
+    for (int h = 0; h < heads; h++) {
+      float* vec = v + (size_t)h * hd;
+      for (int i = 0; i < hd; i += 2) {
+        float theta = (float)position * expf((float)i * dimInv * negLogBase);
+        float c = cosf(theta), s = sinf(theta);
+        float x0 = vec[i], x1 = vec[i + 1];
+        vec[i] = x0 * c - x1 * s;
+        vec[i + 1] = x0 * s + x1 * c;
+      }
+    }
+  }
+}
+
+/* GreedySampler.Sample (GreedySampler.cs:13-26): first maximum wins. */
+int oracle_argmax(const float* logits, int n) {
+  int best = 0;
+  float bv = logits[0];
+  for (int i = 1; i < n; i++)
+    if (logits[i] > bv) {
+      bv = logits[i];
+      best = i;
+    }
+  return best;
+}
+
+/* ---------------------------------------------------------------------------
+ * Llama model (LlamaModel.cs, LlamaWeights.cs)
+ * ------------------------------------------------------------------------- */
+
+typedef struct tensor_ref {
+  const void* data;
+  uint32_t type;
+} tensor_ref;
+
+struct oracle_llama {
+  oracle_config c;
+  int kv_dim, kv_mul;
+  tensor_ref emb, out, out_norm;
+  tensor_ref *attn_norm, *ffn_norm, *wq, *wk, *wv, *wo, *wg, *wu, *wd;
+  float *kcache, *vcache;
+  float *x, *xn, *q, *k, *v, *att, *gate, *up, *ffo, *scores, *rowbuf;
+};
+
+oracle_llama* oracle_llama_create(const oracle_config* cfg) {
+  oracle_llama* m = (oracle_llama*)calloc(1, sizeof(oracle_llama));
+  if (!m) return NULL;
+  m->c = *cfg;
+  int L = cfg->n_layers;
+  m->kv_dim = cfg->n_kv_heads * cfg->head_dim; /* LlamaConfig.cs:34 */
+  m->kv_mul = cfg->n_heads / cfg->n_kv_heads;  /* LlamaConfig.cs:37 */
+  tensor_ref** arrs[] = {&m->attn_norm, &m->ffn_norm, &m->wq, &m->wk, &m->wv,
+                         &m->wo,        &m->wg,       &m->wu, &m->wd};
+  for (size_t i = 0; i < sizeof(arrs) / sizeof(arrs[0]); i++)
+    *arrs[i] = (tensor_ref*)calloc((size_t)L, sizeof(tensor_ref));
+  size_t kv = (size_t)L * cfg->context_length * m->kv_dim; /* LlamaModel.cs:60-61 */
+  m->kcache = (float*)calloc(kv, sizeof(float));
+  m->vcache = (float*)calloc(kv, sizeof(float));
+  int dim = cfg->dim, hid = cfg->hidden_dim;
+  m->x = (float*)calloc((size_t)dim, 4);
+  m->xn = (float*)calloc((size_t)dim, 4);
+  m->q = (float*)calloc((size_t)dim, 4);
+  m->k = (float*)calloc((size_t)m->kv_dim, 4);
+  m->v = (float*)calloc((size_t)m->kv_dim, 4);
+  m->att = (float*)calloc((size_t)dim, 4);
+  m->gate = (float*)calloc((size_t)hid, 4);
+  m->up = (float*)calloc((size_t)hid, 4);
+  m->ffo = (float*)calloc((size_t)dim, 4);
+  m->scores = (float*)calloc((size_t)cfg->context_length, 4);
+  m->rowbuf = (float*)calloc((size_t)(dim > hid ? dim : hid), 4);
+  if (!m->kcache || !m->vcache) {
+    oracle_llama_destroy(m);
+    return NULL;
+  }
+  return m;
+}
+
+/* Name resolution of LlamaWeights.ResolveAll (LlamaWeights.cs:78-145). */
+int oracle_llama_set_tensor(oracle_llama* m, const char* name, uint32_t type, const void* data) {
+  tensor_ref t = {data, type};
+  if (!strcmp(name, "token_embd.weight")) { m->emb = t; return 0; }
+  if (!strcmp(name, "output.weight")) { m->out = t; return 0; }
+  if (!strcmp(name, "output_norm.weight")) { m->out_norm = t; return 0; }
+  int l;
+  char suffix[64];
+  if (sscanf(name, "blk.%d.%63s", &l, suffix) != 2 || l < 0 || l >= m->c.n_layers) return -2;
+  struct { const char* s; tensor_ref* a; } tab[] = {
+      {"attn_norm.weight", m->attn_norm}, {"ffn_norm.weight", m->ffn_norm},
+      {"attn_q.weight", m->wq},           {"attn_k.weight", m->wk},
+      {"attn_v.weight", m->wv},           {"attn_output.weight", m->wo},
+      {"ffn_gate.weight", m->wg},         {"ffn_up.weight", m->wu},
+      {"ffn_down.weight", m->wd}};
+  for (size_t i = 0; i < sizeof(tab) / sizeof(tab[0]); i++)
+    if (!strcmp(suffix, tab[i].s)) {
+      tab[i].a[l] = t;
+      return 0;
+    }
+  return -2;
+}
+
+/* LlamaModel.LoadEmbedding (LlamaModel.cs:365-394) for F32 / F16 / Q4_0. */
+static int load_embedding(oracle_llama* m, int token, float* out) {
+  int dim = m->c.dim;
+  const uint8_t* e = (const uint8_t*)m->emb.data;
+  switch (m->emb.type) {
+    case ORACLE_F32: memcpy(out, e + (size_t)token * dim * 4, (size_t)dim * 4); return 0;
+    case ORACLE_F16:
+      for (int i = 0; i < dim; i++) out[i] = h2f(e + ((size_t)token * dim + i) * 2);
+      return 0;
+    case ORACLE_Q4_0: oracle_dequant_q4_0(e + (size_t)token * (dim / 32) * 18, out, dim); return 0;
+    default: return -3;
+  }
+}
+
+/* LlamaModel.ComputeAttention (LlamaModel.cs:241-346). */
+static void attention(oracle_llama* m, int layer, int pos) {
+  int hd = m->c.head_dim, kvd = m->kv_dim, ctx = m->c.context_length;
+  size_t loff = (size_t)layer * ctx * kvd;
+  int seq = pos + 1;
+  float scale = 1.0f / sqrtf((float)hd);
+  memset(m->att, 0, sizeof(float) * (size_t)m->c.dim);
+  for (int h = 0; h < m->c.n_heads; h++) {
+    const float* qp = m->q + (size_t)h * hd;
+    int kvh = h / m->kv_mul;
+    for (int p = 0; p < seq; p++) {
+      const float* kp = m->kcache + loff + (size_t)p * kvd + (size_t)kvh * hd;
+      float score = 0.0f;
+      int d = 0;
+      if (hd >= VLEN) {
+        float a0[VLEN] = {0}, a1[VLEN] = {0};
+        int lim = hd - 2 * VLEN + 1;
+        for (; d < lim; d += 2 * VLEN)
+          for (int l = 0; l < VLEN; l++) {
+            a0[l] = a0[l] + qp[d + l] * kp[d + l];
+            a1[l] = a1[l] + qp[d + VLEN + l] * kp[d + VLEN + l];
+          }
+        int lim1 = hd - VLEN + 1;
+        for (; d < lim1; d += VLEN)
+          for (int l = 0; l < VLEN; l++) a0[l] = a0[l] + qp[d + l] * kp[d + l];
+        float s[VLEN];
+        for (int l = 0; l < VLEN; l++) s[l] = a0[l] + a1[l];
+        score = vsum8(s);
+      }
+      for (; d < hd; d++) score += qp[d] * kp[d];
+      m->scores[p] = score * scale;
+    }
+    oracle_softmax(m->scores, seq);
+    float* op = m->att + (size_t)h * hd;
+    for (int p = 0; p < seq; p++) {
+      float w = m->scores[p];
+      if (w == 0.0f) continue; /* :322 */
+      const float* vp = m->vcache + loff + (size_t)p * kvd + (size_t)kvh * hd;
+      for (int d = 0; d < hd; d++) op[d] = op[d] + vp[d] * w;
+    }
+  }
+}
+
+/* LlamaModel.Forward (LlamaModel.cs:93-238). */
+int oracle_llama_forward(oracle_llama* m, const int32_t* tokens, int n, int position, float* logits) {
+  const oracle_config* c = &m->c;
+  int dim = c->dim, kvd = m->kv_dim, hid = c->hidden_dim;
+  const tensor_ref* out = m->out.data ? &m->out : &m->emb; /* LlamaWeights.cs:89-98 */
+  if (!m->emb.data || !m->out_norm.data) return -2;
+  for (int t = 0; t < n; t++) {
+    int pos = position + t;
+    if (tokens[t] < 0 || tokens[t] >= c->vocab_size || pos < 0 || pos >= c->context_length) return -5;
+    int rc = load_embedding(m, tokens[t], m->x);
+    if (rc) return rc;
+    for (int l = 0; l < c->n_layers; l++) {
+      if (!m->wq[l].data || !m->wk[l].data || !m->wv[l].data || !m->wo[l].data || !m->wg[l].data ||
+          !m->wu[l].data || !m->wd[l].data || !m->attn_norm[l].data || !m->ffn_norm[l].data)
+        return -2;
+      oracle_rmsnorm(m->x, (const float*)m->attn_norm[l].data, m->xn, dim, c->rms_norm_eps);
+      if ((rc = oracle_matvec(m->wq[l].type, m->wq[l].data, m->xn, m->q, dim, dim))) return rc;
+      if ((rc = oracle_matvec(m->wk[l].type, m->wk[l].data, m->xn, m->k, kvd, dim))) return rc;
+      if ((rc = oracle_matvec(m->wv[l].type, m->wv[l].data, m->xn, m->v, kvd, dim))) return rc;
+      oracle_rope(m->q, m->k, pos, c->head_dim, c->n_heads, c->n_kv_heads, c->rope_freq_base);
+      size_t off = (size_t)l * c->context_length * kvd + (size_t)pos * kvd; /* :150-153 */
+      memcpy(m->kcache + off, m->k, sizeof(float) * (size_t)kvd);
+      memcpy(m->vcache + off, m->v, sizeof(float) * (size_t)kvd);
+      attention(m, l, pos);
+      if ((rc = oracle_matvec(m->wo[l].type, m->wo[l].data, m->att, m->ffo, dim, dim))) return rc;
+      oracle_add(m->x, m->ffo, dim);
+      oracle_rmsnorm(m->x, (const float*)m->ffn_norm[l].data, m->xn, dim, c->rms_norm_eps);
+      if ((rc = oracle_matvec(m->wg[l].type, m->wg[l].data, m->xn, m->gate, hid, dim))) return rc;
+      if ((rc = oracle_matvec(m->wu[l].type, m->wu[l].data, m->xn, m->up, hid, dim))) return rc;
+      oracle_silu_mul(m->gate, m->up, hid);
+      if ((rc = oracle_matvec(m->wd[l].type, m->wd[l].data, m->gate, m->ffo, dim, hid))) return rc;
+      oracle_add(m->x, m->ffo, dim);
+    }
+    oracle_rmsnorm(m->x, (const float*)m->out_norm.data, m->xn, dim, c->rms_norm_eps);
+    if (t == n - 1 && logits) { /* :207 — LM head only for the last token */
+      if ((rc = oracle_matvec(out->type, out->data, m->xn, logits, c->vocab_size, dim))) return rc;
+    }
+  }
+  return 0;
+}
+
+int oracle_llama_kv(oracle_llama* m, int layer, int position, int which, float* out) {
+  if (layer < 0 || layer >= m->c.n_layers || position < 0 || position >= m->c.context_length) return -5;
+  size_t off = (size_t)layer * m->c.context_length * m->kv_dim + (size_t)position * m->kv_dim;
+  memcpy(out, (which ? m->vcache : m->kcache) + off, sizeof(float) * (size_t)m->kv_dim);
+  return 0;
+}
+
+void oracle_llama_destroy(oracle_llama* m) {
+  if (!m) return;
+  free(m->attn_norm); free(m->ffn_norm); free(m->wq); free(m->wk); free(m->wv);
+  free(m->wo); free(m->wg); free(m->wu); free(m->wd);
+  free(m->kcache); free(m->vcache);
+  free(m->x); free(m->xn); free(m->q); free(m->k); free(m->v); free(m->att);
+  free(m->gate); free(m->up); free(m->ffo); free(m->scores); free(m->rowbuf);
+  free(m);
+}

@@ -1,0 +1,86 @@
+/*
+ * chatnet_oracle.h — CPU oracle for the quantized Llama forward pass.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This is a plain-C restatement of ChatNet's CPU
+ * algorithm (C#, not buildable here: no .NET toolchain in the image), used as
+ * the parity checker for libchatnet_hip and as the CPU baseline timer.  Only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
+ * The product path (chatnet_amd/) never links, loads or calls it.
+ *
+ * Every function cites the reference file:line it restates.  The restatement
+ * keeps the reference's accumulation structure: Vector128<float> (4 lanes) in
+ * the fused quant dots, Vector<float> (8 lanes, AVX2 width) in the other ops,
+ * separate multiply and add (compiled with -ffp-contract=off), glibc
+ * expf/sinf/cosf/logf/sqrtf for MathF.*.
+ *
+ * Pinning (how each function is checked; see tests/test_oracle_*.py):
+ *   half_to_float     IEEE closed form, all 65536 inputs vs numpy float16.
+ *   q4_0 dequant/dot  reference KATs QuantizationTests.cs:23-87,704-726 and a
+ *                     float64 brute force on random blocks.
+ *   q4_k dequant/dot  reference KATs QuantizationTests.cs:445-489,728-759,
+ *                     a hand-derived single-sub-block nibble-order KAT, and
+ *                     float64 brute force.
+ *   q6_k dequant/dot  reference KATs QuantizationTests.cs:302-345, a
+ *                     hand-derived element-position KAT, float64 brute force.
+ *   rmsnorm/rope/softmax/silu/add/attention/argmax: invariants (closed forms,
+ *                     identity at pos 0, norm preservation, shift invariance,
+ *                     tie rule) and a float64 numpy restatement of a tiny model.
+ *   Order of Vector128.Sum / MathF last-ulp results: parity unpinned (only
+ *                     running .NET could pin them; covered by tolerance).
+ */
+#ifndef CHATNET_ORACLE_H
+#define CHATNET_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ORACLE_F32 = 0, ORACLE_F16 = 1, ORACLE_Q4_0 = 2, ORACLE_Q4_K = 12, ORACLE_Q6_K = 14 };
+
+void oracle_set_threads(int n);
+int oracle_get_threads(void);
+
+float oracle_half_to_float(uint16_t h);
+
+void oracle_dequant_q4_0(const uint8_t* src, float* out, int n);
+float oracle_dot_q4_0(const uint8_t* row, const float* x, int n);
+void oracle_dequant_q4_k(const uint8_t* src, float* out, int n);
+float oracle_dot_q4_k(const uint8_t* row, const float* x, int n);
+void oracle_dequant_q6_k(const uint8_t* src, float* out, int n);
+float oracle_dot_q6_k(const uint8_t* row, const float* x, int n);
+float oracle_dot_f32(const float* a, const float* b, int n);
+
+/* y[m] = dot(W row m, x) for m < M (MatVecMulByType semantics). Returns 0 or -3
+ * for an unsupported type. */
+int oracle_matvec(uint32_t type, const void* W, const float* x, float* y, int M, int K);
+
+void oracle_rmsnorm(const float* x, const float* w, float* out, int n, float eps);
+void oracle_softmax(float* data, int n);
+void oracle_silu_mul(float* gate, const float* up, int n);
+void oracle_add(float* a, const float* b, int n);
+void oracle_rope(float* q, float* k, int position, int head_dim, int n_heads, int n_kv_heads,
+                 float freq_base);
+int oracle_argmax(const float* logits, int n);
+
+/* Whole model.  Tensor pointers are borrowed host pointers (like the mmap). */
+typedef struct oracle_config {
+  int32_t dim, hidden_dim, n_layers, n_heads, n_kv_heads, head_dim, vocab_size, context_length;
+  float rope_freq_base, rms_norm_eps;
+} oracle_config;
+
+typedef struct oracle_llama oracle_llama;
+oracle_llama* oracle_llama_create(const oracle_config* cfg);
+int oracle_llama_set_tensor(oracle_llama* m, const char* name, uint32_t type, const void* data);
+int oracle_llama_forward(oracle_llama* m, const int32_t* tokens, int n, int position, float* logits);
+/* Copies layer `layer`'s cached K (which=0) or V (which=1) at `position`
+ * (kv_dim floats) to out. */
+int oracle_llama_kv(oracle_llama* m, int layer, int position, int which, float* out);
+void oracle_llama_destroy(oracle_llama* m);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,140 @@
+"""Independent float64 numpy restatement used to pin the C oracle.
+
+Written from the ChatNet sources (not from the oracle): block decoders of
+DequantQ4_0.cs:28-58, DequantQ4K.cs:37-77 / :218-241 and DequantQ6K.cs:37-88,
+and the per-token Llama schedule of LlamaModel.cs:93-346.  Everything here is
+vectorised and evaluated in float64, so it shares no accumulation order with
+the oracle; agreement to ~1e-5 relative pins the oracle's arithmetic, and a
+wrong index, sign or dropped term shows up as an O(1) mismatch.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def half(u16: np.ndarray) -> np.ndarray:
+    return np.asarray(u16, dtype=np.uint16).view(np.float16).astype(np.float64)
+
+
+def dequant_q4_0(raw: np.ndarray, n: int) -> np.ndarray:
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, 18)
+    d = half(b[:, 0].astype(np.uint16) | (b[:, 1].astype(np.uint16) << 8))
+    qs = b[:, 2:]
+    q = np.concatenate([qs & 0x0F, qs >> 4], axis=1).astype(np.float64) - 8.0
+    return (q * d[:, None]).ravel()[:n]
+
+
+def q4k_scales(s12: np.ndarray):
+    s = np.asarray(s12, dtype=np.int64).reshape(-1, 12)
+    sc = np.zeros((s.shape[0], 8), dtype=np.int64)
+    m = np.zeros((s.shape[0], 8), dtype=np.int64)
+    sc[:, :4] = s[:, 0:4] & 63
+    m[:, :4] = s[:, 4:8] & 63
+    sc[:, 4:] = (s[:, 8:12] & 0xF) | ((s[:, 0:4] >> 6) << 4)
+    m[:, 4:] = (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)
+    return sc, m
+
+
+def dequant_q4_k(raw: np.ndarray, n: int) -> np.ndarray:
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, 144)
+    d = half(b[:, 0].astype(np.uint16) | (b[:, 1].astype(np.uint16) << 8))
+    dmin = half(b[:, 2].astype(np.uint16) | (b[:, 3].astype(np.uint16) << 8))
+    sc, m = q4k_scales(b[:, 4:16])
+    qs = b[:, 16:].reshape(-1, 8, 16)  # sub-block s owns qs[16s:16s+16]
+    q = np.concatenate([qs & 0x0F, qs >> 4], axis=2).astype(np.float64)  # [blk, 8, 32]
+    val = d[:, None, None] * sc[:, :, None] * q - dmin[:, None, None] * m[:, :, None]
+    return val.reshape(-1)[:n]
+
+
+def dequant_q6_k(raw: np.ndarray, n: int) -> np.ndarray:
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, 210)
+    d = half(b[:, 208].astype(np.uint16) | (b[:, 209].astype(np.uint16) << 8))
+    sc = b[:, 192:208].view(np.int8).astype(np.float64)
+    out = np.zeros((b.shape[0], 256))
+    for h in range(2):
+        ql = b[:, 64 * h: 64 * h + 64].astype(np.int64)
+        qh = b[:, 128 + 32 * h: 128 + 32 * h + 32].astype(np.int64)
+        l = np.arange(32)
+        q1 = (ql[:, l] & 15) | ((qh[:, l] & 3) << 4)
+        q2 = (ql[:, l + 32] & 15) | (((qh[:, l] >> 2) & 3) << 4)
+        q3 = (ql[:, l] >> 4) | (((qh[:, l] >> 4) & 3) << 4)
+        q4 = (ql[:, l + 32] >> 4) | (((qh[:, l] >> 6) & 3) << 4)
+        for k, q in enumerate((q1, q2, q3, q4)):
+            e = 128 * h + 32 * k + l
+            out[:, e] = (q - 32) * sc[:, e // 16]
+    return (out * d[:, None]).ravel()[:n]
+
+
+DEQUANT = {2: dequant_q4_0, 12: dequant_q4_k, 14: dequant_q6_k}
+
+
+def matrix(t) -> np.ndarray:
+    """Dense float64 [rows, cols] of a SynthTensor."""
+    cols, rows = int(t.dims[0]), int(t.dims[1]) if len(t.dims) > 1 else 1
+    if t.type == 0:
+        return t.data.view(np.float32).astype(np.float64).reshape(rows, cols)
+    return DEQUANT[t.type](t.data, rows * cols).reshape(rows, cols)
+
+
+def rmsnorm(x, w, eps):
+    return x / np.sqrt(np.mean(x * x) + eps) * w
+
+
+def rope(v, pos, hd, base):
+    v = v.copy().reshape(-1, hd)
+    i = np.arange(0, hd, 2)
+    theta = pos * base ** (-i / hd)
+    c, s = np.cos(theta), np.sin(theta)
+    x0, x1 = v[:, 0::2].copy(), v[:, 1::2].copy()
+    v[:, 0::2] = x0 * c - x1 * s
+    v[:, 1::2] = x0 * s + x1 * c
+    return v.ravel()
+
+
+class Llama64:
+    """float64 LlamaModel: same schedule, none of the float32 roundings."""
+
+    def __init__(self, cfg, ck):
+        self.cfg = cfg
+        self.emb = matrix(ck["token_embd.weight"])
+        self.out = matrix(ck["output.weight"])
+        self.out_norm = ck["output_norm.weight"].data.view(np.float32).astype(np.float64)
+        self.L = []
+        for l in range(cfg.n_layers):
+            p = f"blk.{l}."
+            self.L.append({k: matrix(ck[p + k + ".weight"]) for k in
+                           ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")})
+            self.L[-1]["attn_norm"] = ck[p + "attn_norm.weight"].data.view(np.float32).astype(np.float64)
+            self.L[-1]["ffn_norm"] = ck[p + "ffn_norm.weight"].data.view(np.float32).astype(np.float64)
+        self.kc = np.zeros((cfg.n_layers, cfg.context_length, cfg.kv_dim))
+        self.vc = np.zeros_like(self.kc)
+
+    def forward(self, tokens, position):
+        c = self.cfg
+        hd = c.head_dim
+        logits = None
+        for t, tok in enumerate(tokens):
+            pos = position + t
+            x = self.emb[tok].copy()
+            for l, W in enumerate(self.L):
+                xn = rmsnorm(x, W["attn_norm"], c.rms_norm_eps)
+                q = rope(W["attn_q"] @ xn, pos, hd, c.rope_freq_base)
+                k = rope(W["attn_k"] @ xn, pos, hd, c.rope_freq_base)
+                v = W["attn_v"] @ xn
+                self.kc[l, pos], self.vc[l, pos] = k, v
+                att = np.zeros(c.dim)
+                for h in range(c.n_heads):
+                    kvh = h // c.kv_mul
+                    K = self.kc[l, : pos + 1, kvh * hd:(kvh + 1) * hd]
+                    V = self.vc[l, : pos + 1, kvh * hd:(kvh + 1) * hd]
+                    s = K @ q[h * hd:(h + 1) * hd] / np.sqrt(hd)
+                    p = np.exp(s - s.max())
+                    p /= p.sum()
+                    att[h * hd:(h + 1) * hd] = p @ V
+                x = x + W["attn_output"] @ att
+                xn = rmsnorm(x, W["ffn_norm"], c.rms_norm_eps)
+                g, u = W["ffn_gate"] @ xn, W["ffn_up"] @ xn
+                x = x + W["ffn_down"] @ (g / (1 + np.exp(-g)) * u)
+            if t == len(tokens) - 1:
+                logits = self.out @ rmsnorm(x, self.out_norm, c.rms_norm_eps)
+        return logits

@@ -1,0 +1,99 @@
+"""GPU parity of the fused dequant-GEMV (chatnet_matmul, N=1) against the
+oracle's MatVecMulByType on identical seeded blocks.  Bar: normwise error
+max|y-r|/max|r| <= 1e-3 (fp32 accumulate)."""
+import numpy as np
+import pytest
+
+import oracle
+from chatnet_amd import synth
+from gpu_util import announce, gpu_matmul, normwise
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+# Isolated Q4_0 sweep shapes (out x in) and the K-quant shapes of the
+# Q4_K_M-style mix.
+Q4_0_SHAPES = [(2048, 2048), (256, 2048), (5632, 2048), (2048, 5632), (32000, 2048), (4096, 4096),
+               (11008, 4096)]
+KQ_SHAPES = [(12, 4096, 4096), (12, 11008, 4096), (14, 4096, 11008), (14, 32000, 4096)]
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _threads():
+    oracle.set_threads(16)
+    yield
+    oracle.set_threads(1)
+
+
+def run_case(qtype, M, K, seed=1):
+    announce(f"gemv type={qtype} M={M} K={K} seed={seed}")
+    t = synth.tensor(qtype, seed, f"w{qtype}_{M}_{K}", M, K)
+    x = synth.normal(seed, f"x{K}", K, 1.0)
+    y = gpu_matmul(qtype, t.data, x, M, K)[0]
+    r = oracle.matvec(qtype, t.data, x, M, K)
+    assert np.all(np.isfinite(y))
+    err = normwise(y, r)
+    assert err <= TOL, (qtype, M, K, err)
+    return err
+
+
+@pytest.mark.parametrize("M,K", Q4_0_SHAPES)
+def test_q4_0_gemv_sweep_shapes(M, K):
+    run_case(2, M, K)
+
+
+@pytest.mark.parametrize("qtype,M,K", KQ_SHAPES)
+def test_kquant_gemv_shapes(qtype, M, K):
+    run_case(qtype, M, K)
+
+
+@pytest.mark.parametrize("qtype,M,K", [
+    (2, 1, 64), (2, 3, 64), (2, 17, 192), (2, 33, 2048), (2, 130, 5632), (2, 7, 11008),
+    (12, 1, 256), (12, 5, 768), (12, 31, 11008),
+    (14, 1, 256), (14, 9, 768), (14, 18, 1280),   # 768/1280: rows start 2 bytes off a dword
+])
+def test_ragged_and_misaligned_shapes(qtype, M, K):
+    run_case(qtype, M, K, seed=5)
+
+
+def test_q6_k_rows_off_dword_alignment_are_exact_per_row():
+    # K=768 gives a 630-byte row stride: odd rows start at 2 mod 4.
+    M, K = 64, 768
+    t = synth.tensor(14, 9, "q6mis", M, K)
+    x = synth.normal(9, "q6mis-x", K, 1.0)
+    announce("q6_k misaligned rows")
+    y = gpu_matmul(14, t.data, x, M, K)[0]
+    r = oracle.matvec(14, t.data, x, M, K)
+    rel = np.abs(y - r) / np.maximum(np.abs(r), 1e-3)
+    assert np.max(rel[1::2]) < 1e-3 and np.max(rel[0::2]) < 1e-3
+
+
+def test_subnormal_fp16_scales_are_not_flushed():
+    # K-quant and Q4_0 scales of N(0, 0.02) weights sit near fp16's min normal;
+    # the kernel must convert subnormal halves exactly (DequantQ4_0.cs:190-194).
+    M, K = 4, 64
+    blk = bytearray()
+    for r in range(M):
+        for b in range(K // 32):
+            blk += np.uint16(0x0001 + 0x0100 * r + b).tobytes()  # subnormal d (< 0x0400)
+            blk += bytes([(0x1F * (r + 3 * b + j)) & 0xFF for j in range(16)])
+    w = np.frombuffer(bytes(blk), np.uint8)
+    x = synth.normal(4, "sub-x", K, 1.0)
+    announce("q4_0 subnormal scales")
+    y = gpu_matmul(2, w, x, M, K)[0]
+    r = oracle.matvec(2, w, x, M, K)
+    assert np.all(r != 0)
+    assert normwise(y, r) < 1e-5
+
+
+@pytest.mark.parametrize("N", [8, 64])
+def test_batched_columns_match_per_column_gemv(N):
+    M, K = 2048, 2048
+    t = synth.tensor(2, 2, "batch", M, K)
+    x = synth.normal(2, "batch-x", N * K, 1.0).reshape(N, K)
+    announce(f"q4_0 matmul N={N}")
+    y = gpu_matmul(2, t.data, x, M, K)
+    for n in range(0, N, max(1, N // 4)):
+        r = oracle.matvec(2, t.data, x[n], M, K)
+        assert normwise(y[n], r) <= 1e-2

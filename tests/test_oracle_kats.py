@@ -1,0 +1,247 @@
+"""Pins the CPU oracle before it is trusted as the parity checker.
+
+Known-answer vectors come from the reference's own tests
+(tests/ChatNet.Tests/QuantizationTests.cs), closed forms and hand-derived
+byte-position cases; random blocks are checked against the independent
+float64 restatement in npref.py.
+"""
+import numpy as np
+import pytest
+
+import npref
+import oracle
+from chatnet_amd import synth
+
+
+def h16(f: float) -> bytes:
+    """QuantizationTests.WriteHalf (:768-773): fp32 -> System.Half -> LE bytes."""
+    return np.array([f], dtype=np.float16).view(np.uint16).astype("<u2").tobytes()
+
+
+# ---------------------------------------------------------------- half -> float
+def test_half_to_float_all_65536_inputs():
+    bits = np.arange(65536, dtype=np.uint32)
+    want = bits.astype(np.uint16).view(np.float16).astype(np.float32)
+    got = np.array([oracle.half_to_float(int(b)) for b in bits], dtype=np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    # subnormal KATs: smallest subnormal and largest subnormal
+    assert oracle.half_to_float(0x0001) == 2.0 ** -24
+    assert oracle.half_to_float(0x03FF) == 1023 * 2.0 ** -24
+    assert oracle.half_to_float(0x8001) == -(2.0 ** -24)
+
+
+# ---------------------------------------------------------------- Q4_0
+def test_q4_0_dequantize_all_zero_is_minus_8():  # QuantizationTests.cs:23-41
+    blk = np.frombuffer(h16(1.0) + bytes(16), dtype=np.uint8)
+    assert np.all(oracle.dequant(oracle.Q4_0, blk, 32) == -8.0)
+
+
+def test_q4_0_dequantize_midpoint_is_zero():  # QuantizationTests.cs:43-60
+    blk = np.frombuffer(h16(0.5) + bytes([0x88] * 16), dtype=np.uint8)
+    assert np.all(oracle.dequant(oracle.Q4_0, blk, 32) == 0.0)
+
+
+def test_q4_0_dot_closed_form():  # QuantizationTests.cs:62-87
+    blk = np.frombuffer(h16(2.0) + bytes([0x37] * 16), dtype=np.uint8)
+    # 16 * (7 - 8) * 2 + 16 * (3 - 8) * 2 = -192
+    assert oracle.dot(oracle.Q4_0, blk, np.ones(32, np.float32)) == -192.0
+    deq = oracle.dequant(oracle.Q4_0, blk, 32)
+    assert np.all(deq[:16] == -2.0) and np.all(deq[16:] == -10.0)
+
+
+def test_q4_0_multiblock_dequantize():  # QuantizationTests.cs:704-726
+    data = np.frombuffer(h16(1.0) + bytes([0x88] * 16) + h16(2.0) + bytes([0x88] * 16), dtype=np.uint8)
+    assert np.all(oracle.dequant(oracle.Q4_0, data, 64) == 0.0)
+
+
+def test_q4_0_nibble_positions():
+    # low nibble of qs[j] -> element j, high nibble -> element 16+j (DequantQ4_0.cs:12-14)
+    qs = bytearray([0x88] * 16)
+    qs[5] = 0x8B   # low nibble 11 -> element 5 = +3
+    qs[9] = 0x18   # high nibble 1 -> element 25 = -7
+    blk = np.frombuffer(h16(1.0) + bytes(qs), dtype=np.uint8)
+    deq = oracle.dequant(oracle.Q4_0, blk, 32)
+    want = np.zeros(32, np.float32)
+    want[5], want[25] = 3.0, -7.0
+    assert np.array_equal(deq, want)
+
+
+def test_q4_0_partial_final_block():
+    # DequantQ4_0.Dequantize handles elementCount not a multiple of 32 (:39-56)
+    blk = np.frombuffer(h16(1.0) + bytes([0x9A] * 16), dtype=np.uint8)
+    deq = oracle.dequant(oracle.Q4_0, blk, 20)
+    assert np.array_equal(deq, np.array([2.0] * 16 + [1.0] * 4, np.float32))
+
+
+# ---------------------------------------------------------------- Q4_K
+def q4k_block(d, dmin, scale_byte, qs_byte):
+    return np.frombuffer(h16(d) + h16(dmin) + bytes([scale_byte] * 12) + bytes([qs_byte] * 128), np.uint8)
+
+
+def test_q4_k_dot_closed_form():  # QuantizationTests.cs:464-489
+    blk = q4k_block(0.5, 0.25, 0x11, 0x33)
+    # sc/m = 17 for s<4 and 1 for s>=4: values 21.25 and 1.25; dot = 2880
+    deq = oracle.dequant(oracle.Q4_K, blk, 256)
+    assert np.all(deq[:128] == 21.25) and np.all(deq[128:] == 1.25)
+    assert oracle.dot(oracle.Q4_K, blk, np.ones(256, np.float32)) == 2880.0
+
+
+def test_q4_k_two_block_dot():  # QuantizationTests.cs:728-759
+    blk = np.concatenate([q4k_block(0.5, 0.25, 0x11, 0x55)] * 2)
+    assert oracle.dot(oracle.Q4_K, blk, np.full(512, 0.5, np.float32)) == 5184.0
+
+
+def test_q4_k_finite():  # QuantizationTests.cs:445-462
+    blk = np.frombuffer(h16(1.0) + h16(0.5) + bytes([0x11] * 12) + bytes(128), np.uint8)
+    assert np.all(np.isfinite(oracle.dequant(oracle.Q4_K, blk, 256)))
+
+
+def test_q4_k_reference_nibble_order():
+    # ChatNet's own order (DequantQ4K.cs:59-72): sub-block s owns qs[16s..16s+15];
+    # byte 3 of sub-block 2 carries element 67 (low) and element 83 (high).
+    # llama.cpp's order would put these bytes at elements 3 / 35 of sub-blocks 0/1.
+    scales = bytes([1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1])  # sc = 1, m = 0 for all 8
+    qs = bytearray(128)
+    qs[16 * 2 + 3] = 0x5A
+    blk = np.frombuffer(h16(1.0) + h16(0.0) + scales + bytes(qs), np.uint8)
+    deq = oracle.dequant(oracle.Q4_K, blk, 256)
+    want = np.zeros(256, np.float32)
+    want[67], want[83] = 10.0, 5.0
+    assert np.array_equal(deq, want)
+
+
+def test_q4_k_scale_decode_high_bits():
+    # get_scale_min_k4 (DequantQ4K.cs:218-241): 6-bit sc/m for s>=4 take their
+    # top two bits from bytes 0..7.
+    s = bytearray(12)
+    s[0] = 0xC0 | 5      # sc[0] = 5, top bits of sc[4] = 3
+    s[4] = 0x40 | 7      # m[0] = 7, top bits of m[4] = 1
+    s[8] = 0x92          # sc[4] low = 2, m[4] low = 9
+    sc, m = npref.q4k_scales(np.frombuffer(bytes(s), np.uint8))
+    assert sc[0, 0] == 5 and m[0, 0] == 7 and sc[0, 4] == 2 + (3 << 4) and m[0, 4] == 9 + (1 << 4)
+    qs = bytes([0x11] * 128)
+    blk = np.frombuffer(h16(1.0) + h16(1.0) + bytes(s) + qs, np.uint8)
+    deq = oracle.dequant(oracle.Q4_K, blk, 256)
+    assert deq[0] == 5 * 1 - 7 and deq[32 * 4] == (2 + 48) * 1 - (9 + 16)
+
+
+# ---------------------------------------------------------------- Q6_K
+def test_q6_k_dot_closed_form():  # QuantizationTests.cs:321-345
+    raw = bytearray(210)
+    raw[0:128] = bytes([0x22] * 128)
+    raw[192:208] = bytes([2] * 16)
+    raw[208:210] = h16(0.1)
+    blk = np.frombuffer(bytes(raw), np.uint8)
+    d = float(np.float16(0.1))
+    assert d == 0.0999755859375
+    deq = oracle.dequant(oracle.Q6_K, blk, 256)
+    assert np.all(deq == np.float32(d * 2 * -30))
+    assert oracle.dot(oracle.Q6_K, blk, np.ones(256, np.float32)) == 256 * 2 * -30 * d  # -1535.625
+
+
+def test_q6_k_finite():  # QuantizationTests.cs:302-319
+    raw = bytearray(210)
+    raw[192:208] = bytes([1] * 16)
+    raw[208:210] = h16(1.0)
+    assert np.all(np.isfinite(oracle.dequant(oracle.Q6_K, np.frombuffer(bytes(raw), np.uint8), 256)))
+
+
+def test_q6_k_element_positions_and_signed_scales():
+    # Background: ql nibbles 0 and qh bit-pairs 2 -> q = 32 -> value 0.
+    raw = bytearray(210)
+    raw[128:192] = bytes([0xAA] * 64)
+    sc = np.arange(1, 17, dtype=np.int8)
+    sc[4] = -3
+    raw[192:208] = sc.tobytes()
+    raw[208:210] = h16(1.0)
+    raw[64 + 32 + 5] = 0x71   # h=1, l=5: q2 low nibble 1 -> elem 165; q4 high nibble 7 -> elem 229
+    raw[128 + 7] = 0xBA       # h=0, l=7: q3 high bits 3 -> elem 71 = (48 - 32) * sc[4]
+    deq = oracle.dequant(oracle.Q6_K, np.frombuffer(bytes(raw), np.uint8), 256)
+    want = np.zeros(256, np.float32)
+    want[165] = 1 * sc[10]   # scale index 8h + l/16 + 2
+    want[229] = 7 * sc[14]   # 8h + l/16 + 6
+    want[71] = 16 * sc[4]    # 8h + l/16 + 4, a negative int8 scale
+    assert np.array_equal(deq, want)
+
+
+# ---------------------------------------------------------------- brute force
+@pytest.mark.parametrize("qtype", [oracle.Q4_0, oracle.Q4_K, oracle.Q6_K])
+def test_dequant_and_dot_match_float64_restatement(qtype):
+    rows, K = 48, 512
+    t = synth.tensor(qtype, 7, f"bf{qtype}", rows, K)
+    x = synth.normal(8, "bf-x", K, 1.0)
+    W64 = npref.matrix(t)
+    got_deq = oracle.dequant(qtype, t.data, rows * K).reshape(rows, K)
+    np.testing.assert_allclose(got_deq, W64, rtol=1e-6, atol=1e-12)
+    y = oracle.matvec(qtype, t.data, x, rows, K)
+    ref = W64 @ x.astype(np.float64)
+    assert np.max(np.abs(y - ref)) / np.max(np.abs(ref)) < 1e-5
+
+
+def test_matvec_threads_do_not_change_results():
+    M, K = 1024, 512  # above ParallelRowThreshold (TensorMath.cs:28)
+    t = synth.tensor(oracle.Q4_0, 3, "thr", M, K)
+    x = synth.normal(3, "thr-x", K, 1.0)
+    oracle.set_threads(1)
+    a = oracle.matvec(oracle.Q4_0, t.data, x, M, K)
+    oracle.set_threads(4)
+    b = oracle.matvec(oracle.Q4_0, t.data, x, M, K)
+    oracle.set_threads(1)
+    assert np.array_equal(a, b)
+
+
+def test_dot_f32_matches_float64():
+    a = synth.normal(1, "fa", 1000, 1.0)
+    b = synth.normal(1, "fb", 1000, 1.0)
+    r = float(np.dot(a.astype(np.float64), b.astype(np.float64)))
+    assert abs(float(oracle.lib().oracle_dot_f32(a.ctypes.data, b.ctypes.data, 1000)) - r) < 1e-4
+
+
+# ---------------------------------------------------------------- fp32 ops
+def test_rmsnorm_closed_form():
+    n, c, eps = 2048, 0.75, 1e-5
+    w = synth.normal(2, "rw", n, 1.0)
+    out = oracle.rmsnorm(np.full(n, c, np.float32), w, eps)
+    np.testing.assert_allclose(out, w * c / np.sqrt(c * c + eps), rtol=2e-6)
+    x = synth.normal(2, "rx", 1000, 1.0)  # 1000: exercises the 8-lane remainder and scalar tail
+    np.testing.assert_allclose(oracle.rmsnorm(x, w[:1000], eps), npref.rmsnorm(x.astype(np.float64), w[:1000], eps),
+                               rtol=2e-6, atol=1e-7)
+
+
+def test_rope_identity_at_zero_and_norm_preserving():
+    hd, nh, nkv = 64, 4, 2
+    q = synth.normal(4, "rq", nh * hd, 1.0)
+    k = synth.normal(4, "rk", nkv * hd, 1.0)
+    q0, k0 = oracle.rope(q, k, 0, hd, nh, nkv, 10000.0)
+    assert np.array_equal(q0, q) and np.array_equal(k0, k)
+    q5, k5 = oracle.rope(q, k, 517, hd, nh, nkv, 10000.0)
+    pn = lambda v: np.hypot(v[0::2], v[1::2])
+    np.testing.assert_allclose(pn(q5), pn(q), rtol=1e-5)
+    np.testing.assert_allclose(q5, npref.rope(q.astype(np.float64), 517, hd, 10000.0), atol=5e-4)
+    np.testing.assert_allclose(k5, npref.rope(k.astype(np.float64), 517, hd, 10000.0), atol=5e-4)
+
+
+def test_softmax_sums_to_one_and_is_shift_invariant():
+    x = synth.normal(5, "sm", 300, 3.0)
+    p = oracle.softmax(x)
+    assert abs(float(p.astype(np.float64).sum()) - 1.0) < 1e-5
+    np.testing.assert_allclose(oracle.softmax(x + 7.0), p, rtol=1e-4, atol=1e-7)
+    e = np.exp(x.astype(np.float64) - x.max())
+    np.testing.assert_allclose(p, e / e.sum(), rtol=1e-5, atol=1e-9)
+
+
+def test_silu_mul():
+    g = synth.normal(6, "sg", 999, 2.0)
+    u = synth.normal(6, "su", 999, 1.0)
+    g64 = g.astype(np.float64)
+    np.testing.assert_allclose(oracle.silu_mul(g, u), g64 / (1 + np.exp(-g64)) * u, rtol=1e-5, atol=1e-7)
+    assert oracle.silu_mul(np.zeros(4, np.float32), np.ones(4, np.float32)).tolist() == [0.0] * 4
+
+
+def test_argmax_tie_rule():  # GreedySampler.cs:13-26
+    assert oracle.argmax(np.array([1, 5, 5, 2], np.float32)) == 1
+    assert oracle.argmax(np.array([np.nan, 5, 9], np.float32)) == 0
+    assert oracle.argmax(np.array([1, np.nan, 9, 9], np.float32)) == 2
+    assert oracle.argmax(np.array([-np.inf, -np.inf], np.float32)) == 0
