@@ -48,28 +48,24 @@ def gemv_algorithmic_bytes(M: int, K: int) -> int:
 
 
 def decode_run(cfg, ck, prompt, steps, warmup):
-    import torch
-
-    from chatnet_amd import HipLlamaModel
+    from chatnet_amd import HipLlamaModel, hiprt
 
     with HipLlamaModel(cfg, ck) as m:
         m.forward(prompt, 0)
         m.decode_greedy(max(warmup, 1))             # warm-up (also captures the graph)
-        m.forward(prompt, 0)                         # reset to the 128-token prompt
-        torch.cuda.synchronize()
+        m.forward(prompt, 0)                         # reset to the prompt
+        hiprt.synchronize()
         t0 = time.perf_counter()
-        toks = m.decode_greedy(steps)
-        torch.cuda.synchronize()
+        toks = m.decode_greedy(steps)                # synchronizes before returning
+        hiprt.synchronize()
         dt = time.perf_counter() - t0
     assert len(toks) == steps, (len(toks), steps)
     return dt, toks
 
 
 def gemv_sweep(shapes, launches_per_shape=64, rotate_bytes=1 << 30):
-    """Cold per-launch GEMV time via HIP events on torch's current stream."""
-    import torch
-
-    from chatnet_amd import ops, synth
+    """Cold per-launch GEMV time via HIP events on the stream of the launches."""
+    from chatnet_amd import hiprt, ops, synth
 
     res = {}
     for (M, K) in shapes:
@@ -77,29 +73,29 @@ def gemv_sweep(shapes, launches_per_shape=64, rotate_bytes=1 << 30):
         stride = (nb + 256 + 4095) // 4096 * 4096
         copies = max(4, min(256, -(-rotate_bytes // stride)))
         t = synth.tensor(2, 99, f"sweep{M}x{K}", M, K)
-        base = torch.from_numpy(t.data).to("cuda:0")
-        pool = torch.zeros(copies * stride, dtype=torch.uint8, device="cuda:0")
+        base = hiprt.DeviceBuffer.from_numpy(t.data)
+        pool = hiprt.DeviceBuffer(copies * stride)
+        pool.fill(0)
         for c in range(copies):
-            pool[c * stride: c * stride + nb].copy_(base)
-        x = torch.randn(K, dtype=torch.float32, device="cuda:0")
-        y = torch.empty(M, dtype=torch.float32, device="cuda:0")
-        st = torch.cuda.current_stream().cuda_stream
+            pool.copy_from(base, nb, dst_offset=c * stride)
+        x = hiprt.DeviceBuffer.from_numpy(synth.normal(99, f"sweepx{K}", K, 1.0))
+        y = hiprt.DeviceBuffer(4 * M)
+        stream = 0  # launches and events share the null stream
         for c in range(min(copies, 8)):  # warm-up
-            ops.matmul_ptr(2, pool.data_ptr() + c * stride, x.data_ptr(), y.data_ptr(), M, K, 1, st)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
+            ops.matmul_ptr(2, pool.ptr + c * stride, x.ptr, y.ptr, M, K, 1, stream)
+        hiprt.synchronize()
+        e0, e1 = hiprt.Event(), hiprt.Event()
+        e0.record(stream)
         for i in range(launches_per_shape):
             c = i % copies
-            ops.matmul_ptr(2, pool.data_ptr() + c * stride, x.data_ptr(), y.data_ptr(), M, K, 1, st)
-        e1.record()
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1000.0 / launches_per_shape
+            ops.matmul_ptr(2, pool.ptr + c * stride, x.ptr, y.ptr, M, K, 1, stream)
+        e1.record(stream)
+        us = e0.elapsed_ms(e1) * 1000.0 / launches_per_shape
         alg = gemv_algorithmic_bytes(M, K)
         res[f"{M}x{K}"] = {"us": round(us, 3), "GB/s": round(alg / us / 1e3, 1),
                            "frac": round(alg / us / 1e3 / HBM_PEAK_GBS, 4), "alg_bytes": alg}
-        del pool, base
-        torch.cuda.empty_cache()
+        for b in (pool, base, x, y):
+            b.free()
     return res
 
 
@@ -108,7 +104,7 @@ def cpu_baseline(cfg, ck, prompt_len=4, decode=8):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
 
-    cores = len(os.sched_getaffinity(0))
+    cores = int(os.environ.get("OMP_NUM_THREADS") or len(os.sched_getaffinity(0)))
     oracle.set_threads(cores)
     ora = oracle.OracleLlama(cfg, ck)
     prompt = list(range(1, prompt_len + 1))
@@ -143,15 +139,12 @@ def main():
               "multi-GPU sharding is design-only", file=sys.stderr)
         sys.exit(2)
 
-    import torch
+    from chatnet_amd import LLAMA2_7B, TINYLLAMA_1B, hiprt, synth
 
-    from chatnet_amd import LLAMA2_7B, TINYLLAMA_1B, synth
-
-    if not torch.cuda.is_available():
+    if hiprt.device_count() < 1:
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
 
-    out = {}
     log("gemv sweep (cold, rotating >= 1 GiB)")
     sweep = gemv_sweep(SWEEP)
     roof = sweep[f"{ROOF_SHAPE[0]}x{ROOF_SHAPE[1]}"]

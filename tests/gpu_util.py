@@ -1,4 +1,4 @@
-"""Shared helpers of the GPU tests (torch is used only for device buffers)."""
+"""Shared helpers of the GPU tests (device buffers through chatnet_amd.hiprt)."""
 import sys
 
 import numpy as np
@@ -7,12 +7,6 @@ import numpy as np
 def announce(msg: str) -> None:
     print(f"[gpu-case] {msg}", flush=True)
     sys.stdout.flush()
-
-
-def device_tensor(arr: np.ndarray):
-    import torch
-
-    return torch.from_numpy(np.ascontiguousarray(arr)).to("cuda:0")
 
 
 def normwise(y: np.ndarray, r: np.ndarray) -> float:
@@ -24,18 +18,18 @@ def normwise(y: np.ndarray, r: np.ndarray) -> float:
 
 def gpu_matmul(qtype: int, w_bytes: np.ndarray, x: np.ndarray, M: int, K: int) -> np.ndarray:
     """Runs chatnet_matmul on device copies and returns y as [N, M]."""
-    import torch
-
-    from chatnet_amd import ops
+    from chatnet_amd import hiprt, ops
 
     x = np.ascontiguousarray(x, np.float32).reshape(-1, K)
     N = x.shape[0]
     # 256 bytes of slack behind the weights, as the model's own uploads have
-    padded = np.zeros(w_bytes.size + 256, np.uint8)
-    padded[: w_bytes.size] = w_bytes
-    w_d = device_tensor(padded)
-    x_d = device_tensor(x)
-    y_d = torch.full((N, M), float("nan"), dtype=torch.float32, device="cuda:0")
-    ops.matmul(qtype, w_d, x_d, y_d, M, K)
-    torch.cuda.synchronize()
-    return y_d.cpu().numpy()
+    w_d = hiprt.DeviceBuffer.from_numpy(np.ascontiguousarray(w_bytes, np.uint8), pad=256)
+    x_d = hiprt.DeviceBuffer.from_numpy(x)
+    y_d = hiprt.DeviceBuffer(4 * N * M)
+    y_d.fill(0xFF)  # NaN pattern: rows the kernel fails to write stay NaN
+    ops.matmul(qtype, w_d, x_d, y_d, M, K, N)
+    hiprt.synchronize()
+    y = y_d.to_numpy(np.float32, N * M).reshape(N, M)
+    for b in (w_d, x_d, y_d):
+        b.free()
+    return y
