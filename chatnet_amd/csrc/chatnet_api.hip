@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstdlib>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -79,6 +80,10 @@ struct chatnet_model {
   void* vcache = nullptr;
   float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr;
   int* state = nullptr;  // [0] pos, [1] token, [2] step
+  float* attn_part_o = nullptr;   // split partials of the decode attention
+  float* attn_part_ml = nullptr;
+  int* attn_counters = nullptr;
+  int attn_splits = 1;
   int* out_tokens = nullptr;
   int out_cap = 0;
   hipGraphExec_t graph = nullptr;
@@ -163,6 +168,10 @@ int chatnet_create(const chatnet_config* cfg, int device, chatnet_model** out) {
   m->kv_elt = c.kv_dtype == CHATNET_KV_F16 ? 2 : 4;
   m->layers.resize(c.n_layers);
   const size_t kv_bytes = (size_t)c.n_layers * c.context_length * m->kv_dim * m->kv_elt;
+  // Attention splits: about two workgroups per CU over the KV heads.
+  int splits = 1;
+  while (splits < 64 && splits * c.n_kv_heads < 2 * m->num_cus && splits * 2 <= c.context_length) splits *= 2;
+  m->attn_splits = splits;
   auto cleanup = [m]() { chatnet_destroy(m); };
   if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) {
     cleanup();
@@ -177,6 +186,9 @@ int chatnet_create(const chatnet_config* cfg, int device, chatnet_model** out) {
       {(void**)&m->h, sizeof(float) * c.hidden_dim},
       {(void**)&m->logits, sizeof(float) * c.vocab_size},
       {(void**)&m->state, sizeof(int) * 4},
+      {(void**)&m->attn_part_o, sizeof(float) * (size_t)c.n_heads * splits * c.head_dim},
+      {(void**)&m->attn_part_ml, sizeof(float) * (size_t)c.n_heads * splits * 2},
+      {(void**)&m->attn_counters, sizeof(int) * (size_t)c.n_kv_heads},
   };
   for (auto& a : allocs) {
     if (hipMalloc(a.p, a.n) != hipSuccess) {
@@ -184,9 +196,11 @@ int chatnet_create(const chatnet_config* cfg, int device, chatnet_model** out) {
       return fail(CHATNET_ERR_OUT_OF_MEMORY, "hipMalloc of %zu bytes failed", a.n);
     }
   }
-  // Zero the caches once so unwritten positions hold 0 like the managed arrays.
+  // Zero the caches once so unwritten positions hold 0 like the managed arrays;
+  // the attention tickets start (and are left by every launch) at 0.
   if (hipMemset(m->kcache, 0, kv_bytes) != hipSuccess || hipMemset(m->vcache, 0, kv_bytes) != hipSuccess ||
-      hipMemset(m->state, 0, sizeof(int) * 4) != hipSuccess) {
+      hipMemset(m->state, 0, sizeof(int) * 4) != hipSuccess ||
+      hipMemset(m->attn_counters, 0, sizeof(int) * c.n_kv_heads) != hipSuccess) {
     cleanup();
     return fail(CHATNET_ERR_HIP, "hipMemset failed");
   }
@@ -208,6 +222,7 @@ void chatnet_destroy(chatnet_model* m) {
   }
   fr(m->kcache); fr(m->vcache); fr(m->x); fr(m->q); fr(m->att); fr(m->h); fr(m->logits);
   fr(m->state); fr(m->out_tokens);
+  fr(m->attn_part_o); fr(m->attn_part_ml); fr(m->attn_counters);
   if (m->stream) (void)hipStreamDestroy(m->stream);
   delete m;
 }
@@ -383,7 +398,11 @@ int launch_token(chatnet_model* m, bool lm_head) {
     at.ctx = c.context_length;
     at.kv_f16 = a.kv_f16;
     at.scale = 1.0f / sqrtf((float)c.head_dim);  // LlamaModel.cs:248
-    at.splits = 1;
+    at.splits = m->attn_splits;
+    at.chunk_cap = (c.context_length + m->attn_splits - 1) / m->attn_splits;
+    at.part_o = m->attn_part_o;
+    at.part_ml = m->attn_part_ml;
+    at.counters = m->attn_counters;
     HIP_TRY(attn_decode_launch(at, st));
 
     GemvArgs o = base_args(m);
@@ -532,7 +551,17 @@ int chatnet_decode_greedy(chatnet_model* m, int max_tokens, int32_t eos_token, i
   // step counter = 0, then sample the first token from the last forward's logits
   HIP_TRY(set_state_launch(m->state, p0 - 1, m->last_tok, 0, m->stream));
   HIP_TRY(argmax_launch(m->logits, m->cfg.vocab_size, m->state, m->out_tokens, m->out_cap, m->stream));
-  if (forwards > 0) {
+  // CHATNET_DECODE_GRAPH=0 issues the same per-step launches directly instead
+  // of replaying the captured graph (profilers that cannot trace graph
+  // launches need this; the kernels and their order are identical).
+  const char* ge = getenv("CHATNET_DECODE_GRAPH");
+  const bool use_graph = !(ge && ge[0] == '0');
+  if (forwards > 0 && !use_graph) {
+    for (int i = 0; i < forwards; i++) {
+      if ((rc = launch_token(m, true))) return rc;
+      HIP_TRY(argmax_launch(m->logits, m->cfg.vocab_size, m->state, m->out_tokens, m->out_cap, m->stream));
+    }
+  } else if (forwards > 0) {
     if (!m->graph) {
       hipGraph_t g;
       HIP_TRY(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));

@@ -33,80 +33,142 @@ __device__ __forceinline__ float kv_load(const void* base, size_t idx) {
   else return reinterpret_cast<const float*>(base)[idx];
 }
 
-// One workgroup per query head (LlamaModel.cs:262-344):
-//   s[p] = (q_h . K[p][kvh]) * scale, p <= pos;  softmax;  out_h = sum_p s[p] V[p][kvh]
-// kvh = h / kv_mul (LlamaModel.cs:265).  Scores live in LDS (ctx floats).
-template <int HD, bool F16>
+// Split-position GQA decode attention (LlamaModel.ComputeAttention,
+// LlamaModel.cs:241-346):  for query head h with kvh = h / kv_mul (:265),
+//   s[p] = (q_h . K[p][kvh]) * scale  for p <= pos,  w = softmax(s),
+//   out_h = sum_p w[p] V[p][kvh].
+// Grid = n_kv_heads x splits.  Workgroup (kvh, c) takes positions
+// [c*chunk, (c+1)*chunk) of seq = pos+1 and every query head of the group, so
+// each K/V row is read once for all kv_mul heads; waves take positions, lanes
+// take head_dim elements (coalesced rows).  Each split leaves (max, sum, o) and
+// the workgroup that arrives last for its KV head (atomic ticket after a
+// device-scope release fence) merges the splits:
+//   M = max_c m_c,  L = sum_c l_c e^(m_c - M),  out = sum_c o_c e^(m_c - M) / L.
+template <int HD, bool F16, int GMAX>
 __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
+  constexpr int EPL = HD >= 64 ? HD / 64 : 1;  // head elements per lane
+  constexpr int G = CN_BLOCK / HD;             // position groups in the V pass
   extern __shared__ float sm[];
-  float* qs = sm;             // HD
-  float* sc = qs + HD;        // ctx
-  float* red = sc + a.ctx;    // 4
-  float* opart = red + 4;     // CN_BLOCK
-  const int h = blockIdx.x;
-  const int kvh = h / a.kv_mul;
+  const int kvh = blockIdx.x / a.splits;
+  const int split = blockIdx.x % a.splits;
+  const int kv_mul = a.kv_mul;
   const int seq = *a.pos + 1;
+  const int chunk = (seq + a.splits - 1) / a.splits;
+  const int p0 = split * chunk;
+  const int p1 = min(seq, p0 + chunk);
+  const int cap = a.chunk_cap;
+  float* qs = sm;                       // kv_mul * HD
+  float* sc = qs + kv_mul * HD;         // kv_mul * cap
+  float* ml = sc + kv_mul * cap;        // kv_mul * 2
+  float* op = ml + 2 * kv_mul;          // G * GMAX * HD
+  __shared__ int ticket;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const size_t koff = (size_t)kvh * HD;
-  for (int d = threadIdx.x; d < HD; d += CN_BLOCK) qs[d] = a.q[(size_t)h * HD + d];
+  const int h0 = kvh * kv_mul;
+
+  for (int i = threadIdx.x; i < kv_mul * HD; i += CN_BLOCK) qs[i] = a.q[(size_t)h0 * HD + i];
   __syncthreads();
 
-  // scores: one position per thread
-  float mx = -INFINITY;
-  for (int p = threadIdx.x; p < seq; p += CN_BLOCK) {
-    const size_t base = (size_t)p * a.kv_dim + koff;
-    float s = 0.f;
-    if constexpr (F16) {
-      const uint4* kp = reinterpret_cast<const uint4*>(reinterpret_cast<const _Float16*>(a.kc) + base);
+  // scores
+  for (int p = p0 + wave; p < p1; p += CN_BLOCK / CN_WAVE) {
+    float kv[EPL];
 #pragma unroll
-      for (int c = 0; c < HD / 8; c++) {
-        uint4 t = kp[c];
-        const uint32_t u[4] = {t.x, t.y, t.z, t.w};
+    for (int e = 0; e < EPL; e++) {
+      const int d = lane * EPL + e;
+      kv[e] = d < HD ? kv_load<F16>(a.kc, (size_t)p * a.kv_dim + koff + d) : 0.f;
+    }
+    for (int j = 0; j < kv_mul; j++) {
+      float s = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          s += cn_h2f(u[e]) * qs[8 * c + 2 * e];
-          s += cn_h2f(u[e] >> 16) * qs[8 * c + 2 * e + 1];
+      for (int e = 0; e < EPL; e++) {
+        const int d = lane * EPL + e;
+        if (d < HD) s += qs[j * HD + d] * kv[e];
+      }
+      s = cn_wave_sum(s);
+      if (lane == 0) sc[j * cap + (p - p0)] = s * a.scale;
+    }
+  }
+  __syncthreads();
+
+  // per-head max and exp-sum of this split (one wave per head)
+  for (int j = wave; j < kv_mul; j += CN_BLOCK / CN_WAVE) {
+    float m = -INFINITY;
+    for (int i = lane; i < p1 - p0; i += CN_WAVE) m = fmaxf(m, sc[j * cap + i]);
+    m = cn_wave_max(m);
+    float l = 0.f;
+    for (int i = lane; i < p1 - p0; i += CN_WAVE) {
+      const float e = expf(sc[j * cap + i] - m);
+      sc[j * cap + i] = e;
+      l += e;
+    }
+    l = cn_wave_sum(l);
+    if (lane == 0) {
+      ml[2 * j] = m;
+      ml[2 * j + 1] = l;
+    }
+  }
+  __syncthreads();
+
+  // o_j[d] = sum_p e_j[p] V[p][d], GMAX heads at a time
+  const int d = threadIdx.x % HD, g = threadIdx.x / HD;
+  for (int jb = 0; jb < kv_mul; jb += GMAX) {
+    float o[GMAX];
+#pragma unroll
+    for (int j = 0; j < GMAX; j++) o[j] = 0.f;
+    for (int p = p0 + g; p < p1; p += G) {
+      const float v = kv_load<F16>(a.vc, (size_t)p * a.kv_dim + koff + d);
+#pragma unroll
+      for (int j = 0; j < GMAX; j++)
+        if (jb + j < kv_mul) o[j] += sc[(jb + j) * cap + (p - p0)] * v;
+    }
+#pragma unroll
+    for (int j = 0; j < GMAX; j++) op[(g * GMAX + j) * HD + d] = o[j];
+    __syncthreads();
+    if (g == 0) {
+#pragma unroll
+      for (int j = 0; j < GMAX; j++) {
+        if (jb + j >= kv_mul) break;
+        float t = 0.f;
+#pragma unroll
+        for (int k = 0; k < G; k++) t += op[(k * GMAX + j) * HD + d];
+        const size_t slot = (size_t)(h0 + jb + j) * a.splits + split;
+        a.part_o[slot * HD + d] = t;
+        if (d == 0) {
+          a.part_ml[2 * slot] = ml[2 * (jb + j)];
+          a.part_ml[2 * slot + 1] = ml[2 * (jb + j) + 1];
         }
       }
-    } else {
-      const float4* kp = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.kc) + base);
-#pragma unroll
-      for (int c = 0; c < HD / 4; c++) {
-        const float4 t = kp[c];
-        s += t.x * qs[4 * c] + t.y * qs[4 * c + 1] + t.z * qs[4 * c + 2] + t.w * qs[4 * c + 3];
-      }
     }
-    s *= a.scale;
-    sc[p] = s;
-    mx = fmaxf(mx, s);
+    __syncthreads();
   }
-  mx = cn_block_max(mx, red);
-  // TensorMath.Softmax (TensorMath.cs:177-241): exp(x - max), sum, * (1/sum)
-  float sum = 0.f;
-  for (int p = threadIdx.x; p < seq; p += CN_BLOCK) {
-    const float e = expf(sc[p] - mx);
-    sc[p] = e;
-    sum += e;
-  }
-  sum = cn_block_sum(sum, red);
-  const float inv = 1.0f / sum;
-  __syncthreads();
 
-  // out[d] = sum_p w_p V[p][d]: G groups of HD threads split the positions.
-  constexpr int G = CN_BLOCK / HD;
-  const int d = threadIdx.x % HD, g = threadIdx.x / HD;
-  float acc = 0.f;
-  for (int p = g; p < seq; p += G) {
-    const float wgt = sc[p] * inv;
-    acc += wgt * kv_load<F16>(a.vc, (size_t)p * a.kv_dim + koff + d);
-  }
-  opart[threadIdx.x] = acc;
+  // last workgroup of this KV head merges the splits: every thread releases its
+  // partial stores before thread 0 takes the ticket
+  __threadfence();
   __syncthreads();
-  if (g == 0) {
-    float o = acc;
-#pragma unroll
-    for (int k = 1; k < G; k++) o += opart[k * HD + d];
-    a.out[(size_t)h * HD + d] = o;
+  if (threadIdx.x == 0)
+    ticket = __hip_atomic_fetch_add(a.counters + kvh, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (ticket != a.splits - 1) return;
+  __threadfence();
+  for (int i = threadIdx.x; i < kv_mul * HD; i += CN_BLOCK) {
+    const int j = i / HD, dd = i % HD;
+    const size_t base = (size_t)(h0 + j) * a.splits;
+    float M = -INFINITY;
+    for (int c = 0; c < a.splits; c++) M = fmaxf(M, __builtin_nontemporal_load(a.part_ml + 2 * (base + c)));
+    float L = 0.f, acc = 0.f;
+    for (int c = 0; c < a.splits; c++) {
+      const float mc = __builtin_nontemporal_load(a.part_ml + 2 * (base + c));
+      const float lc = __builtin_nontemporal_load(a.part_ml + 2 * (base + c) + 1);
+      if (lc == 0.f) continue;  // empty split
+      const float f = expf(mc - M);
+      L += lc * f;
+      acc += __builtin_nontemporal_load(a.part_o + (base + c) * HD + dd) * f;
+    }
+    a.out[(size_t)(h0 + j) * HD + dd] = acc / L;
   }
+  if (threadIdx.x == 0)
+    __hip_atomic_store(a.counters + kvh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // GreedySampler.Sample: strict '>' scan => the lowest index of the maximum;
@@ -164,8 +226,12 @@ __global__ void set_state_kernel(int* state, int pos, int tok, int step) {
 
 template <int HD, bool F16>
 hipError_t attn_launch_t(const AttnArgs& a, hipStream_t st) {
-  const size_t smem = sizeof(float) * ((size_t)HD + a.ctx + 4 + CN_BLOCK);
-  hipLaunchKernelGGL((attn_decode_kernel<HD, F16>), dim3(a.n_heads), dim3(CN_BLOCK), smem, st, a);
+  constexpr int GMAX = 8;
+  const int G = CN_BLOCK / HD;
+  const size_t smem = sizeof(float) * ((size_t)a.kv_mul * HD + (size_t)a.kv_mul * a.chunk_cap + 2 * a.kv_mul +
+                                       (size_t)G * GMAX * HD);
+  const int n_kv = a.n_heads / a.kv_mul;
+  hipLaunchKernelGGL((attn_decode_kernel<HD, F16, GMAX>), dim3(n_kv * a.splits), dim3(CN_BLOCK), smem, st, a);
   return hipGetLastError();
 }
 
@@ -178,6 +244,7 @@ hipError_t embed_launch(const void* emb, int type, int dim, const int* tok, floa
 }
 
 hipError_t attn_decode_launch(const AttnArgs& a, hipStream_t st) {
+  if (a.splits < 1 || a.chunk_cap * a.splits < a.ctx) return hipErrorInvalidValue;
   if (a.head_dim == 64) return a.kv_f16 ? attn_launch_t<64, true>(a, st) : attn_launch_t<64, false>(a, st);
   if (a.head_dim == 128) return a.kv_f16 ? attn_launch_t<128, true>(a, st) : attn_launch_t<128, false>(a, st);
   if (a.head_dim == 32) return a.kv_f16 ? attn_launch_t<32, true>(a, st) : attn_launch_t<32, false>(a, st);

@@ -336,17 +336,59 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, const float
   }
 }
 
-template <int QT, int RPW, int LPR, int EPI>
+// Issues the loads of one wave iteration: RPW rows x NU units per lane.
+template <int QT, int RPW, int LPR, int NU, int EPI>
+__device__ __forceinline__ void issue_loads(const GemvArgs& a, int it, int sub, int li, int nunits, size_t bpr,
+                                            uint32_t (&w)[RPW][NU][QTraits<QT>::NDW]) {
+  constexpr int RW = RPW * (CN_WAVE / LPR);
+  const int vr0 = it * RW + sub * RPW;
+#pragma unroll
+  for (int i = 0; i < RPW; i++) {
+    const int vr = vr0 + i;
+    const bool ok = vr < a.n_vrows;
+    int seg, r;
+    map_row<EPI>(a, ok ? vr : 0, seg, r);
+    const uint8_t* rp = a.w[seg] + (size_t)r * bpr;
+#pragma unroll
+    for (int n = 0; n < NU; n++) {
+      const int u = li + LPR * n;
+      if (ok && u < nunits) {
+        load_unit<QT>(rp, u, w[i][n]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < QTraits<QT>::NDW; k++) w[i][n][k] = 0;
+      }
+    }
+  }
+}
+
+// One launch streams n_vrows rows.  A wave iteration covers RW = RPW*(64/LPR)
+// rows; every lane holds RPW rows x NU units in registers.  The first
+// iteration's loads are issued before x is staged, so HBM latency overlaps the
+// prologue, and each next iteration's loads are issued before the current
+// reduction and epilogue.
+template <int QT, int RPW, int LPR, int NU, int EPI>
 __global__ __launch_bounds__(CN_BLOCK) void gemv_kernel(GemvArgs a) {
   using T = QTraits<QT>;
   constexpr int UNIT = T::UNIT;
+  constexpr int RW = RPW * (CN_WAVE / LPR);
   extern __shared__ float smem[];
   const int K = a.K;
   const int nunits = K / UNIT;
-  float* xs = smem;                                    // nunits*(UNIT+4)
-  float* sx = xs + nunits * (UNIT + 4);                // K/32 block sums
-  float* sx16 = sx + (K >> 5);                         // K/16 group sums (Q6_K)
+  float* xs = smem;                                      // nunits*(UNIT+4)
+  float* sx = xs + nunits * (UNIT + 4);                  // K/32 block sums
+  float* sx16 = sx + (K >> 5);                           // K/16 group sums (Q6_K)
   float* red = sx16 + ((QT == QT_Q6_K) ? (K >> 4) : 0);  // 4 floats
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane / LPR, li = lane % LPR;
+  const int n_iters = (a.n_vrows + RW - 1) / RW;
+  const size_t bpr = (size_t)(K / T::BLOCK) * T::BLOCK_BYTES;
+  const int wstride = gridDim.x * (CN_BLOCK / CN_WAVE);
+  int it = blockIdx.x * (CN_BLOCK / CN_WAVE) + wave;
+
+  uint32_t w[RPW][NU][T::NDW];
+  if (it < n_iters) issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
 
   // ---- prologue: stage x (optionally RMS-normalised) into LDS ----
   float rms = 1.0f;
@@ -387,51 +429,32 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_kernel(GemvArgs a) {
   }
   __syncthreads();
 
-  // ---- main loop: wave-strided over row groups ----
-  constexpr int GPW = CN_WAVE / LPR;  // row groups per wave
-  constexpr int RW = RPW * GPW;       // rows per wave iteration
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int sub = lane / LPR, li = lane % LPR;
-  const int n_iters = (a.n_vrows + RW - 1) / RW;
-  const size_t bpr = (size_t)(K / T::BLOCK) * T::BLOCK_BYTES;
-
-  for (int it = blockIdx.x * (CN_BLOCK / CN_WAVE) + wave; it < n_iters;
-       it += gridDim.x * (CN_BLOCK / CN_WAVE)) {
-    const int vr0 = it * RW + sub * RPW;
-    const uint8_t* rp[RPW];
-    bool ok[RPW];
-#pragma unroll
-    for (int i = 0; i < RPW; i++) {
-      const int vr = vr0 + i;
-      ok[i] = vr < a.n_vrows;
-      int seg, r;
-      map_row<EPI>(a, ok[i] ? vr : 0, seg, r);
-      rp[i] = a.w[seg] + (size_t)r * bpr;
-    }
+  // ---- main loop ----
+  while (it < n_iters) {
     float acc[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; i++) acc[i] = 0.f;
-
-    for (int u = li; u < nunits; u += LPR) {
-      uint32_t w[RPW][T::NDW];
 #pragma unroll
-      for (int i = 0; i < RPW; i++) {
-        if (ok[i]) {
-          load_unit<QT>(rp[i], u, w[i]);
-        } else {
+    for (int n = 0; n < NU; n++) {
+      const int u = li + LPR * n;
+      if (u < nunits) {
+        uint32_t wu[RPW][T::NDW];
 #pragma unroll
-          for (int k = 0; k < T::NDW; k++) w[i][k] = 0;
-        }
+        for (int i = 0; i < RPW; i++)
+#pragma unroll
+          for (int k = 0; k < T::NDW; k++) wu[i][k] = w[i][n][k];
+        dot_unit<QT, RPW>(wu, xs + u * (UNIT + 4), sx + u * (UNIT / 32), sx16 + u * (UNIT / 16), acc);
       }
-      const float* xu = xs + u * (UNIT + 4);
-      dot_unit<QT, RPW>(w, xu, sx + u * (UNIT / 32), sx16 + u * (UNIT / 16), acc);
     }
+    const int cur = it;
+    it += wstride;
+    if (it < n_iters) issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
 #pragma unroll
       for (int off = LPR / 2; off > 0; off >>= 1) acc[i] += __shfl_xor(acc[i], off, CN_WAVE);
     }
-    if (li == 0) epilogue<EPI, RPW>(a, vr0, acc);
+    if (li == 0) epilogue<EPI, RPW>(a, cur * RW + sub * RPW, acc);
   }
 }
 
@@ -443,47 +466,73 @@ size_t gemv_smem_bytes(int K) {
   return f * sizeof(float);
 }
 
-// Lanes per row: the power of two in {16, 32, 64} that wastes the fewest lanes
-// on the last unit sweep (ties go to the wider choice).
-inline int pick_lpr(int nunits) {
-  int best = 64;
-  double best_eff = -1.0;
-  for (int lpr = 64; lpr >= 16; lpr >>= 1) {
-    const int sweeps = (nunits + lpr - 1) / lpr;
-    const double eff = (double)nunits / (double)(sweeps * lpr);
-    if (eff > best_eff + 1e-9) {
-      best_eff = eff;
-      best = lpr;
-    }
+// Launch shape of one GEMV: lanes per row, units per lane, rows per lane.
+struct GemvShape {
+  int lpr, nu, rpw;
+};
+
+// Q4_0: the (LPR, NU) pair that wastes the fewest lanes (NU <= 4, ties to the
+// wider LPR); 4 rows per lane when that still leaves >= 12 waves per CU, else 2.
+// K-quants: one super-block per lane (NU = 1) and 2 rows, LPR the smallest
+// power of two covering the row (min 16).
+template <int QT>
+GemvShape pick_shape(int K, int n_vrows, int num_cus) {
+  using T = QTraits<QT>;
+  const int nunits = K / T::UNIT;
+  GemvShape s{64, 1, 2};
+  if (QT == QT_Q4_0) {
+    double best = -1.0;
+    for (int lpr = 64; lpr >= 32; lpr >>= 1)
+      for (int nu = 1; nu <= 4; nu++) {
+        if (lpr * nu < nunits) continue;
+        const double eff = (double)nunits / (double)(lpr * nu);
+        if (eff > best + 1e-9) { best = eff; s.lpr = lpr; s.nu = nu; }
+        break;  // larger nu only adds idle lanes
+      }
+    if (best < 0) { s.lpr = 64; s.nu = 4; }  // K beyond 16384: loop over the max
+    const int iters4 = (n_vrows + 4 * (64 / s.lpr) - 1) / (4 * (64 / s.lpr));
+    s.rpw = (s.nu <= 2 && iters4 >= num_cus * 12) ? 4 : 2;
+  } else {
+    s.nu = 1;
+    s.rpw = 2;
+    s.lpr = nunits <= 16 ? 16 : (nunits <= 32 ? 32 : 64);
   }
-  return best;
+  return s;
 }
 
-template <int QT, int RPW, int EPI>
-hipError_t launch_lpr(const GemvArgs& a, int lpr, int grid, size_t smem, hipStream_t st) {
-  switch (lpr) {
-    case 16: hipLaunchKernelGGL((gemv_kernel<QT, RPW, 16, EPI>), dim3(grid), dim3(CN_BLOCK), smem, st, a); break;
-    case 32: hipLaunchKernelGGL((gemv_kernel<QT, RPW, 32, EPI>), dim3(grid), dim3(CN_BLOCK), smem, st, a); break;
-    default: hipLaunchKernelGGL((gemv_kernel<QT, RPW, 64, EPI>), dim3(grid), dim3(CN_BLOCK), smem, st, a); break;
-  }
+template <int QT, int RPW, int NU, int EPI>
+hipError_t launch_k(const GemvArgs& a, int lpr, int grid, size_t smem, hipStream_t st) {
+  if (lpr == 16) hipLaunchKernelGGL((gemv_kernel<QT, RPW, 16, NU, EPI>), dim3(grid), dim3(CN_BLOCK), smem, st, a);
+  else if (lpr == 32) hipLaunchKernelGGL((gemv_kernel<QT, RPW, 32, NU, EPI>), dim3(grid), dim3(CN_BLOCK), smem, st, a);
+  else hipLaunchKernelGGL((gemv_kernel<QT, RPW, 64, NU, EPI>), dim3(grid), dim3(CN_BLOCK), smem, st, a);
   return hipGetLastError();
 }
 
 template <int QT, int EPI>
 hipError_t launch_qt(const GemvArgs& a, int num_cus, hipStream_t st) {
   using T = QTraits<QT>;
-  constexpr int RPW = 2;
-  const int nunits = a.K / T::UNIT;
-  const int lpr = pick_lpr(nunits);
-  const int rw = RPW * (CN_WAVE / lpr);
+  const GemvShape s = pick_shape<QT>(a.K, a.n_vrows, num_cus);
+  const int rw = s.rpw * (CN_WAVE / s.lpr);
   const int n_iters = (a.n_vrows + rw - 1) / rw;
   const int waves_per_block = CN_BLOCK / CN_WAVE;
+  // One iteration per wave while that fits 16 waves per CU, else a grid-stride loop.
   int grid = (n_iters + waves_per_block - 1) / waves_per_block;
-  const int cap = num_cus * 8;
+  const int cap = num_cus * 4;
   if (grid > cap) grid = cap;
   if (grid < 1) grid = 1;
   const size_t smem = gemv_smem_bytes<QT>(a.K);
-  return launch_lpr<QT, RPW, EPI>(a, lpr, grid, smem, st);
+  (void)T::NDW;
+  if constexpr (QT == QT_Q4_0) {
+    if (s.rpw == 4) return launch_k<QT, 4, 1, EPI>(a, s.lpr, grid, smem, st);
+    switch (s.nu) {
+      case 1: return launch_k<QT, 2, 1, EPI>(a, s.lpr, grid, smem, st);
+      case 2: return launch_k<QT, 2, 2, EPI>(a, s.lpr, grid, smem, st);
+      case 3: return launch_k<QT, 2, 3, EPI>(a, s.lpr, grid, smem, st);
+      default: return launch_k<QT, 2, 4, EPI>(a, s.lpr, grid, smem, st);
+    }
+  } else {
+    return launch_k<QT, 2, 1, EPI>(a, s.lpr, grid, smem, st);
+  }
 }
 
 template <int EPI>
@@ -507,11 +556,12 @@ size_t gemv_lds_bytes(int qtype, int K) {
   }
 }
 
+// The launch shapes cover rows of up to 256 lanes x units: K <= 16384.
 bool gemv_supports(int qtype, int K) {
   switch (qtype) {
-    case QT_Q4_0: return K > 0 && K % 64 == 0;
+    case QT_Q4_0: return K > 0 && K % 64 == 0 && K <= 16384;
     case QT_Q4_K:
-    case QT_Q6_K: return K > 0 && K % 256 == 0;
+    case QT_Q6_K: return K > 0 && K % 256 == 0 && K <= 16384;
     default: return false;
   }
 }

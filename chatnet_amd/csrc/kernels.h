@@ -49,9 +49,11 @@ struct AttnArgs {
   const int* pos;
   int n_heads, kv_mul, head_dim, kv_dim, ctx, kv_f16;
   float scale;
-  float* part_o;      // split-K scratch: [n_heads][splits][head_dim]
+  float* part_o;      // split scratch: [n_heads][splits][head_dim]
   float* part_ml;     // [n_heads][splits][2] (max, sum)
-  int splits;         // chunks of positions processed in parallel
+  int* counters;      // [n_kv_heads] arrival tickets, zero between launches
+  int splits;         // position chunks processed in parallel
+  int chunk_cap;      // ceil(ctx / splits): LDS rows reserved per head
 };
 hipError_t attn_decode_launch(const AttnArgs& a, hipStream_t st);
 
