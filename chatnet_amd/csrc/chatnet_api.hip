@@ -82,7 +82,6 @@ struct chatnet_model {
   int* state = nullptr;  // [0] pos, [1] token, [2] step
   float* attn_part_o = nullptr;   // split partials of the decode attention
   float* attn_part_ml = nullptr;
-  int* attn_counters = nullptr;
   int attn_splits = 1;
   int* out_tokens = nullptr;
   int out_cap = 0;
@@ -188,7 +187,6 @@ int chatnet_create(const chatnet_config* cfg, int device, chatnet_model** out) {
       {(void**)&m->state, sizeof(int) * 4},
       {(void**)&m->attn_part_o, sizeof(float) * (size_t)c.n_heads * splits * c.head_dim},
       {(void**)&m->attn_part_ml, sizeof(float) * (size_t)c.n_heads * splits * 2},
-      {(void**)&m->attn_counters, sizeof(int) * (size_t)c.n_kv_heads},
   };
   for (auto& a : allocs) {
     if (hipMalloc(a.p, a.n) != hipSuccess) {
@@ -196,11 +194,9 @@ int chatnet_create(const chatnet_config* cfg, int device, chatnet_model** out) {
       return fail(CHATNET_ERR_OUT_OF_MEMORY, "hipMalloc of %zu bytes failed", a.n);
     }
   }
-  // Zero the caches once so unwritten positions hold 0 like the managed arrays;
-  // the attention tickets start (and are left by every launch) at 0.
+  // Zero the caches once so unwritten positions hold 0 like the managed arrays.
   if (hipMemset(m->kcache, 0, kv_bytes) != hipSuccess || hipMemset(m->vcache, 0, kv_bytes) != hipSuccess ||
-      hipMemset(m->state, 0, sizeof(int) * 4) != hipSuccess ||
-      hipMemset(m->attn_counters, 0, sizeof(int) * c.n_kv_heads) != hipSuccess) {
+      hipMemset(m->state, 0, sizeof(int) * 4) != hipSuccess) {
     cleanup();
     return fail(CHATNET_ERR_HIP, "hipMemset failed");
   }
@@ -222,7 +218,7 @@ void chatnet_destroy(chatnet_model* m) {
   }
   fr(m->kcache); fr(m->vcache); fr(m->x); fr(m->q); fr(m->att); fr(m->h); fr(m->logits);
   fr(m->state); fr(m->out_tokens);
-  fr(m->attn_part_o); fr(m->attn_part_ml); fr(m->attn_counters);
+  fr(m->attn_part_o); fr(m->attn_part_ml);
   if (m->stream) (void)hipStreamDestroy(m->stream);
   delete m;
 }
@@ -402,7 +398,6 @@ int launch_token(chatnet_model* m, bool lm_head) {
     at.chunk_cap = (c.context_length + m->attn_splits - 1) / m->attn_splits;
     at.part_o = m->attn_part_o;
     at.part_ml = m->attn_part_ml;
-    at.counters = m->attn_counters;
     HIP_TRY(attn_decode_launch(at, st));
 
     GemvArgs o = base_args(m);

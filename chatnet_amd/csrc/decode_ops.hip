@@ -40,10 +40,8 @@ __device__ __forceinline__ float kv_load(const void* base, size_t idx) {
 // Grid = n_kv_heads x splits.  Workgroup (kvh, c) takes positions
 // [c*chunk, (c+1)*chunk) of seq = pos+1 and every query head of the group, so
 // each K/V row is read once for all kv_mul heads; waves take positions, lanes
-// take head_dim elements (coalesced rows).  Each split leaves (max, sum, o) and
-// the workgroup that arrives last for its KV head (atomic ticket after a
-// device-scope release fence) merges the splits:
-//   M = max_c m_c,  L = sum_c l_c e^(m_c - M),  out = sum_c o_c e^(m_c - M) / L.
+// take head_dim elements (coalesced rows).  Each split leaves (max, sum, o)
+// for attn_merge_kernel.
 template <int HD, bool F16, int GMAX>
 __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
   constexpr int EPL = HD >= 64 ? HD / 64 : 1;  // head elements per lane
@@ -61,7 +59,6 @@ __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
   float* sc = qs + kv_mul * HD;         // kv_mul * cap
   float* ml = sc + kv_mul * cap;        // kv_mul * 2
   float* op = ml + 2 * kv_mul;          // G * GMAX * HD
-  __shared__ int ticket;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const size_t koff = (size_t)kvh * HD;
   const int h0 = kvh * kv_mul;
@@ -131,6 +128,10 @@ __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
         float t = 0.f;
 #pragma unroll
         for (int k = 0; k < G; k++) t += op[(k * GMAX + j) * HD + d];
+        if (a.splits == 1) {  // single split: normalise in place
+          a.out[(size_t)(h0 + jb + j) * HD + d] = t / ml[2 * (jb + j) + 1];
+          continue;
+        }
         const size_t slot = (size_t)(h0 + jb + j) * a.splits + split;
         a.part_o[slot * HD + d] = t;
         if (d == 0) {
@@ -142,33 +143,27 @@ __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
     __syncthreads();
   }
 
-  // last workgroup of this KV head merges the splits: every thread releases its
-  // partial stores before thread 0 takes the ticket
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0)
-    ticket = __hip_atomic_fetch_add(a.counters + kvh, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  if (ticket != a.splits - 1) return;
-  __threadfence();
-  for (int i = threadIdx.x; i < kv_mul * HD; i += CN_BLOCK) {
-    const int j = i / HD, dd = i % HD;
-    const size_t base = (size_t)(h0 + j) * a.splits;
-    float M = -INFINITY;
-    for (int c = 0; c < a.splits; c++) M = fmaxf(M, __builtin_nontemporal_load(a.part_ml + 2 * (base + c)));
-    float L = 0.f, acc = 0.f;
-    for (int c = 0; c < a.splits; c++) {
-      const float mc = __builtin_nontemporal_load(a.part_ml + 2 * (base + c));
-      const float lc = __builtin_nontemporal_load(a.part_ml + 2 * (base + c) + 1);
-      if (lc == 0.f) continue;  // empty split
-      const float f = expf(mc - M);
-      L += lc * f;
-      acc += __builtin_nontemporal_load(a.part_o + (base + c) * HD + dd) * f;
-    }
-    a.out[(size_t)(h0 + j) * HD + dd] = acc / L;
+}
+
+// Merges the split partials of one query head (grid = n_heads, block = HD):
+//   M = max_c m_c,  L = sum_c l_c e^(m_c - M),  out = sum_c o_c e^(m_c - M) / L.
+// Empty splits (l_c = 0) contribute nothing.
+template <int HD>
+__global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs a) {
+  const int h = blockIdx.x, d = threadIdx.x;
+  const size_t base = (size_t)h * a.splits;
+  float M = -INFINITY;
+  for (int c = 0; c < a.splits; c++)
+    if (a.part_ml[2 * (base + c) + 1] > 0.f) M = fmaxf(M, a.part_ml[2 * (base + c)]);
+  float L = 0.f, acc = 0.f;
+  for (int c = 0; c < a.splits; c++) {
+    const float lc = a.part_ml[2 * (base + c) + 1];
+    if (lc == 0.f) continue;
+    const float f = expf(a.part_ml[2 * (base + c)] - M);
+    L += lc * f;
+    acc += a.part_o[(base + c) * HD + d] * f;
   }
-  if (threadIdx.x == 0)
-    __hip_atomic_store(a.counters + kvh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  a.out[(size_t)h * HD + d] = acc / L;
 }
 
 // GreedySampler.Sample: strict '>' scan => the lowest index of the maximum;
@@ -232,6 +227,7 @@ hipError_t attn_launch_t(const AttnArgs& a, hipStream_t st) {
                                        (size_t)G * GMAX * HD);
   const int n_kv = a.n_heads / a.kv_mul;
   hipLaunchKernelGGL((attn_decode_kernel<HD, F16, GMAX>), dim3(n_kv * a.splits), dim3(CN_BLOCK), smem, st, a);
+  if (a.splits > 1) hipLaunchKernelGGL((attn_merge_kernel<HD>), dim3(a.n_heads), dim3(HD), 0, st, a);
   return hipGetLastError();
 }
 

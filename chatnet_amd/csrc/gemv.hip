@@ -53,6 +53,89 @@ __device__ __forceinline__ int xidx(int k) {
 }
 
 // ---------------------------------------------------------------------------
+// Q4_0 inputs as signed 4-bit digits.
+//
+// For the Q4_0 GEMV, x is staged in LDS as integers so that v_dot8_i32_i4 can
+// multiply raw weight nibbles exactly: per 32-element block b,
+//   s_b = 18 - e_b  with max|x_b| = f * 2^e_b, f in [0.5, 1)   (so |X| <= 2^18)
+//   X_j = rint(x_j * 2^s_b) = sum_{d<5} D_{j,d} 16^d,  D in [-8, 7]
+// A weight dword XOR 0x88888888 holds (q - 8) as eight signed nibbles, so
+//   sum_j (q_j - 8) X_j = Horner over d of dot8(qs ^ 0x88888888, D_d)
+// is exact in int32 (|.| <= 32 * 8 * 2^18), and the block contributes
+// fp16(d_b) * 2^-s_b * that integer.  X carries 19 significant bits relative
+// to the block maximum; the GEMV's normwise deviation from an fp32 dot is
+// about 4e-6.
+// LDS record of unit u (blocks 2u and 2u+1): 44 dwords,
+//   dword blk*20 + d*4 + k: nibble 2i = digit d of element 4k+i, nibble 2i+1 =
+//   digit d of element 16+4k+i (the nibble order of qs dword k);
+//   dword 40 + blk = s_b.  The 44-dword stride keeps 16-byte reads of 16
+//   neighbouring lanes on distinct banks.
+// ---------------------------------------------------------------------------
+constexpr int XD_UNIT_DW = 44;
+
+__device__ __forceinline__ uint32_t digit_nibble(int& v) {
+  const int d = ((v + 8) & 15) - 8;
+  v = (v - d) >> 4;
+  return (uint32_t)(d & 15);
+}
+
+// Stages x (times rms * norm_w when norm_w is given) as digit records.
+// Work item t = (block t/4, dword k = t%4); the four items of a block sit in
+// adjacent lanes and share the block maximum through two xor-shuffles.
+__device__ __forceinline__ void stage_x_digits(const float* __restrict__ x, const float* __restrict__ norm_w,
+                                               float rms, int K, uint32_t* xd) {
+  const int ntask = K >> 3;
+  for (int t0 = 0; t0 < ntask; t0 += CN_BLOCK) {
+    const int t = t0 + threadIdx.x;
+    const bool on = t < ntask;
+    const int b = t >> 2, k = t & 3;
+    float v[8];
+    if (on) {
+      const float4 lo = *reinterpret_cast<const float4*>(x + 32 * b + 4 * k);
+      const float4 hi = *reinterpret_cast<const float4*>(x + 32 * b + 16 + 4 * k);
+      v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+      v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+      if (norm_w) {
+        const float4 gl = *reinterpret_cast<const float4*>(norm_w + 32 * b + 4 * k);
+        const float4 gh = *reinterpret_cast<const float4*>(norm_w + 32 * b + 16 + 4 * k);
+        const float g[8] = {gl.x, gl.y, gl.z, gl.w, gh.x, gh.y, gh.z, gh.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = v[i] * rms * g[i];  // TensorMath.cs:155
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = 0.f;
+    }
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) m = fmaxf(m, fabsf(v[i]));
+    m = fmaxf(m, __shfl_xor(m, 1, CN_WAVE));
+    m = fmaxf(m, __shfl_xor(m, 2, CN_WAVE));
+    int e = 0;
+    (void)frexpf(m, &e);
+    const int s = m > 0.f ? 18 - e : 0;
+    uint32_t dw[5] = {0, 0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      int xl = __float2int_rn(ldexpf(v[i], s));
+      int xh = __float2int_rn(ldexpf(v[4 + i], s));
+#pragma unroll
+      for (int d = 0; d < 5; d++) {
+        dw[d] |= digit_nibble(xl) << (8 * i);
+        dw[d] |= digit_nibble(xh) << (8 * i + 4);
+      }
+    }
+    if (on) {
+      uint32_t* rec = xd + (b >> 1) * XD_UNIT_DW;
+      const int blk = b & 1;
+#pragma unroll
+      for (int d = 0; d < 5; d++) rec[blk * 20 + d * 4 + k] = dw[d];
+      if (k == 0) rec[40 + blk] = (uint32_t)s;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Unit loads
 // ---------------------------------------------------------------------------
 template <int QT>
@@ -148,6 +231,46 @@ __device__ __forceinline__ void dot_unit_q4_0(const uint32_t (*w)[9], const floa
     const float da = cn_h2f(w[i][0]);
     const float db = cn_h2f(w[i][4] >> 16);
     acc[i] += da * (sa[i] - 8.f * sx[0]) + db * (sb[i] - 8.f * sx[1]);
+  }
+}
+
+// Q4_0 unit against the digit record xd (see stage_x_digits): block A's qs
+// (pair bytes 2..17) is realigned with alignbyte, block B's (bytes 20..35)
+// is dword aligned.
+template <int RPW>
+__device__ __forceinline__ void dot_unit_q4_0_dig(const uint32_t (*w)[9], const uint32_t* xd, float* acc) {
+  uint32_t X[40];
+#pragma unroll
+  for (int c = 0; c < 10; c++) {
+    const uint4 t = *reinterpret_cast<const uint4*>(xd + 4 * c);
+    X[4 * c + 0] = t.x; X[4 * c + 1] = t.y; X[4 * c + 2] = t.z; X[4 * c + 3] = t.w;
+  }
+  const uint2 se = *reinterpret_cast<const uint2*>(xd + 40);
+  const int sA = (int)se.x, sB = (int)se.y;
+#pragma unroll
+  for (int i = 0; i < RPW; i++) {
+    uint32_t qa[4], qb[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      qa[k] = __builtin_amdgcn_alignbyte(w[i][k + 1], w[i][k], 2) ^ 0x88888888u;
+      qb[k] = w[i][5 + k] ^ 0x88888888u;
+    }
+    int ta = 0, tb = 0;
+#pragma unroll
+    for (int d = 4; d >= 0; d--) {
+      if (d < 4) {
+        ta <<= 4;
+        tb <<= 4;
+      }
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        ta = __builtin_amdgcn_sdot8((int)qa[k], (int)X[d * 4 + k], ta, false);
+        tb = __builtin_amdgcn_sdot8((int)qb[k], (int)X[20 + d * 4 + k], tb, false);
+      }
+    }
+    const float da = ldexpf(cn_h2f(w[i][0]), -sA);
+    const float db = ldexpf(cn_h2f(w[i][4] >> 16), -sB);
+    acc[i] += (float)ta * da + (float)tb * db;
   }
 }
 
@@ -398,8 +521,44 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_kernel(GemvArgs a) {
       const float4 t = *reinterpret_cast<const float4*>(a.x + k);
       ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
     }
-    ss = cn_block_sum(ss, red);
+    if constexpr (QT == QT_Q4_0) {
+      ss = cn_block_sum(ss, reinterpret_cast<float*>(smem) + (size_t)nunits * XD_UNIT_DW);
+    } else {
+      ss = cn_block_sum(ss, red);
+    }
     rms = 1.0f / sqrtf(ss / (float)K + a.eps);  // TensorMath.cs:142
+  }
+  if constexpr (QT == QT_Q4_0) {
+    uint32_t* xd = reinterpret_cast<uint32_t*>(smem);
+    stage_x_digits(a.x, a.norm_w, rms, K, xd);
+    __syncthreads();
+    while (it < n_iters) {
+      float acc[RPW];
+#pragma unroll
+      for (int i = 0; i < RPW; i++) acc[i] = 0.f;
+#pragma unroll
+      for (int n = 0; n < NU; n++) {
+        const int u = li + LPR * n;
+        if (u < nunits) {
+          uint32_t wu[RPW][9];
+#pragma unroll
+          for (int i = 0; i < RPW; i++)
+#pragma unroll
+            for (int k = 0; k < 9; k++) wu[i][k] = w[i][n][k];
+          dot_unit_q4_0_dig<RPW>(wu, xd + u * XD_UNIT_DW, acc);
+        }
+      }
+      const int cur = it;
+      it += wstride;
+      if (it < n_iters) issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
+#pragma unroll
+      for (int i = 0; i < RPW; i++) {
+#pragma unroll
+        for (int off = LPR / 2; off > 0; off >>= 1) acc[i] += __shfl_xor(acc[i], off, CN_WAVE);
+      }
+      if (li == 0) epilogue<EPI, RPW>(a, cur * RW + sub * RPW, acc);
+    }
+    return;
   }
   for (int k = threadIdx.x * 4; k < K; k += CN_BLOCK * 4) {
     float4 t = *reinterpret_cast<const float4*>(a.x + k);
@@ -462,6 +621,7 @@ template <int QT>
 size_t gemv_smem_bytes(int K) {
   using T = QTraits<QT>;
   const int nunits = K / T::UNIT;
+  if (QT == QT_Q4_0) return ((size_t)nunits * XD_UNIT_DW + 4) * sizeof(uint32_t);
   size_t f = (size_t)nunits * (T::UNIT + 4) + (K >> 5) + (QT == QT_Q6_K ? (K >> 4) : 0) + 4;
   return f * sizeof(float);
 }

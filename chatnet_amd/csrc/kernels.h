@@ -51,7 +51,6 @@ struct AttnArgs {
   float scale;
   float* part_o;      // split scratch: [n_heads][splits][head_dim]
   float* part_ml;     // [n_heads][splits][2] (max, sum)
-  int* counters;      // [n_kv_heads] arrival tickets, zero between launches
   int splits;         // position chunks processed in parallel
   int chunk_cap;      // ceil(ctx / splits): LDS rows reserved per head
 };
