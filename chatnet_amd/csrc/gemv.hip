@@ -79,12 +79,18 @@ __device__ __forceinline__ uint32_t digit_nibble(int& v) {
   return (uint32_t)(d & 15);
 }
 
-// Stages x (times rms * norm_w when norm_w is given) as digit records.
-// Work item t = (block t/4, dword k = t%4); the four items of a block sit in
-// adjacent lanes and share the block maximum through two xor-shuffles.
+// Stages x * norm_w (x alone when norm_w is null) as digit records in one
+// read of x.  RMSNorm's scale rms = 1/sqrt(sum x^2 / K + eps) (TensorMath.cs:142)
+// is a single positive factor per token, so it is applied to the finished dot
+// products instead of to every element; each wave leaves its share of sum x^2
+// in red[wave] for the caller to combine after its __syncthreads().
+// Work item t = (block t/4, dword k = t%4) holds x[32b+4k..+3] and
+// x[32b+16+4k..+3]; the four items of a block sit in adjacent lanes and share
+// the block maximum through two xor-shuffles.
 __device__ __forceinline__ void stage_x_digits(const float* __restrict__ x, const float* __restrict__ norm_w,
-                                               float rms, int K, uint32_t* xd) {
+                                               int K, uint32_t* xd, float* red) {
   const int ntask = K >> 3;
+  float ss = 0.f;
   for (int t0 = 0; t0 < ntask; t0 += CN_BLOCK) {
     const int t = t0 + threadIdx.x;
     const bool on = t < ntask;
@@ -95,12 +101,14 @@ __device__ __forceinline__ void stage_x_digits(const float* __restrict__ x, cons
       const float4 hi = *reinterpret_cast<const float4*>(x + 32 * b + 16 + 4 * k);
       v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
       v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+#pragma unroll
+      for (int i = 0; i < 8; i++) ss += v[i] * v[i];
       if (norm_w) {
         const float4 gl = *reinterpret_cast<const float4*>(norm_w + 32 * b + 4 * k);
         const float4 gh = *reinterpret_cast<const float4*>(norm_w + 32 * b + 16 + 4 * k);
         const float g[8] = {gl.x, gl.y, gl.z, gl.w, gh.x, gh.y, gh.z, gh.w};
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = v[i] * rms * g[i];  // TensorMath.cs:155
+        for (int i = 0; i < 8; i++) v[i] = v[i] * g[i];
       }
     } else {
 #pragma unroll
@@ -133,6 +141,8 @@ __device__ __forceinline__ void stage_x_digits(const float* __restrict__ x, cons
       if (k == 0) rec[40 + blk] = (uint32_t)s;
     }
   }
+  ss = cn_wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
 }
 
 // ---------------------------------------------------------------------------
@@ -145,7 +155,7 @@ template <>
 __device__ __forceinline__ void load_unit<QT_Q4_0>(const uint8_t* row, int u, uint32_t* w) {
   const uint32_t* p = reinterpret_cast<const uint32_t*>(row + (size_t)u * 36);
 #pragma unroll
-  for (int k = 0; k < 9; k++) w[k] = __builtin_nontemporal_load(p + k);
+  for (int k = 0; k < 9; k++) w[k] = p[k];
 }
 
 template <>
@@ -153,7 +163,7 @@ __device__ __forceinline__ void load_unit<QT_Q4_K>(const uint8_t* row, int u, ui
   const cn_u32x4* p = reinterpret_cast<const cn_u32x4*>(row + (size_t)u * 144);
 #pragma unroll
   for (int k = 0; k < 9; k++) {
-    cn_u32x4 t = __builtin_nontemporal_load(p + k);
+    cn_u32x4 t = p[k];
     w[4 * k + 0] = t.x;
     w[4 * k + 1] = t.y;
     w[4 * k + 2] = t.z;
@@ -174,9 +184,9 @@ __device__ __forceinline__ void load_unit<QT_Q6_K>(const uint8_t* row, int u, ui
   const uint32_t sh = (uint32_t)(a & 3);  // 0 or 2
   uint32_t r[53];
 #pragma unroll
-  for (int k = 0; k < 52; k++) r[k] = __builtin_nontemporal_load(p + k);
+  for (int k = 0; k < 52; k++) r[k] = p[k];
   if (sh) {
-    r[52] = __builtin_nontemporal_load(p + 52);
+    r[52] = p[52];
 #pragma unroll
     for (int k = 0; k < 52; k++) w[k] = __builtin_amdgcn_alignbyte(r[k + 1], r[k], 2);
     w[52] = r[52] >> 16;
@@ -514,24 +524,12 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_kernel(GemvArgs a) {
   if (it < n_iters) issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
 
   // ---- prologue: stage x (optionally RMS-normalised) into LDS ----
-  float rms = 1.0f;
-  if (a.norm_w) {
-    float ss = 0.f;
-    for (int k = threadIdx.x * 4; k < K; k += CN_BLOCK * 4) {
-      const float4 t = *reinterpret_cast<const float4*>(a.x + k);
-      ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
-    }
-    if constexpr (QT == QT_Q4_0) {
-      ss = cn_block_sum(ss, reinterpret_cast<float*>(smem) + (size_t)nunits * XD_UNIT_DW);
-    } else {
-      ss = cn_block_sum(ss, red);
-    }
-    rms = 1.0f / sqrtf(ss / (float)K + a.eps);  // TensorMath.cs:142
-  }
   if constexpr (QT == QT_Q4_0) {
     uint32_t* xd = reinterpret_cast<uint32_t*>(smem);
-    stage_x_digits(a.x, a.norm_w, rms, K, xd);
+    float* xred = reinterpret_cast<float*>(smem) + (size_t)nunits * XD_UNIT_DW;
+    stage_x_digits(a.x, a.norm_w, K, xd, xred);
     __syncthreads();
+    const float rms = a.norm_w ? 1.0f / sqrtf((xred[0] + xred[1] + xred[2] + xred[3]) / (float)K + a.eps) : 1.0f;
     while (it < n_iters) {
       float acc[RPW];
 #pragma unroll
@@ -555,10 +553,21 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_kernel(GemvArgs a) {
       for (int i = 0; i < RPW; i++) {
 #pragma unroll
         for (int off = LPR / 2; off > 0; off >>= 1) acc[i] += __shfl_xor(acc[i], off, CN_WAVE);
+        acc[i] *= rms;
       }
       if (li == 0) epilogue<EPI, RPW>(a, cur * RW + sub * RPW, acc);
     }
     return;
+  }
+  float rms = 1.0f;
+  if (a.norm_w) {
+    float ss = 0.f;
+    for (int k = threadIdx.x * 4; k < K; k += CN_BLOCK * 4) {
+      const float4 t = *reinterpret_cast<const float4*>(a.x + k);
+      ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
+    }
+    ss = cn_block_sum(ss, red);
+    rms = 1.0f / sqrtf(ss / (float)K + a.eps);  // TensorMath.cs:142
   }
   for (int k = threadIdx.x * 4; k < K; k += CN_BLOCK * 4) {
     float4 t = *reinterpret_cast<const float4*>(a.x + k);
@@ -632,7 +641,10 @@ struct GemvShape {
 };
 
 // Q4_0: the (LPR, NU) pair that wastes the fewest lanes (NU <= 4, ties to the
-// wider LPR); 4 rows per lane when that still leaves >= 12 waves per CU, else 2.
+// wider LPR).  Rows per lane: the smallest of 2, 4, 8 (register budget
+// permitting) whose waves all fit on the chip at once, so every weight load of
+// the launch is issued in the first round; resident waves per CU assumed 20,
+// 16 and 12 for 2, 4 and 8 rows.
 // K-quants: one super-block per lane (NU = 1) and 2 rows, LPR the smallest
 // power of two covering the row (min 16).
 template <int QT>
@@ -649,9 +661,18 @@ GemvShape pick_shape(int K, int n_vrows, int num_cus) {
         if (eff > best + 1e-9) { best = eff; s.lpr = lpr; s.nu = nu; }
         break;  // larger nu only adds idle lanes
       }
-    if (best < 0) { s.lpr = 64; s.nu = 4; }  // K beyond 16384: loop over the max
-    const int iters4 = (n_vrows + 4 * (64 / s.lpr) - 1) / (4 * (64 / s.lpr));
-    s.rpw = (s.nu <= 2 && iters4 >= num_cus * 12) ? 4 : 2;
+    if (best < 0) { s.lpr = 64; s.nu = 4; }
+    const int max_rpw = s.nu == 1 ? 8 : (s.nu == 2 ? 4 : 2);
+    const int resident[9] = {0, 0, 20, 0, 16, 0, 0, 0, 12};
+    s.rpw = max_rpw;
+    for (int rpw = 2; rpw <= max_rpw; rpw *= 2) {
+      const int rw = rpw * (64 / s.lpr);
+      const int waves = (n_vrows + rw - 1) / rw;
+      if (waves <= num_cus * resident[rpw]) {
+        s.rpw = rpw;
+        break;
+      }
+    }
   } else {
     s.nu = 1;
     s.rpw = 2;
@@ -675,21 +696,25 @@ hipError_t launch_qt(const GemvArgs& a, int num_cus, hipStream_t st) {
   const int rw = s.rpw * (CN_WAVE / s.lpr);
   const int n_iters = (a.n_vrows + rw - 1) / rw;
   const int waves_per_block = CN_BLOCK / CN_WAVE;
-  // One iteration per wave while that fits 16 waves per CU, else a grid-stride loop.
+  // One iteration per wave while the waves fit the chip, else a grid-stride loop.
   int grid = (n_iters + waves_per_block - 1) / waves_per_block;
-  const int cap = num_cus * 4;
+  const int cap = num_cus * 5;
   if (grid > cap) grid = cap;
   if (grid < 1) grid = 1;
   const size_t smem = gemv_smem_bytes<QT>(a.K);
   (void)T::NDW;
   if constexpr (QT == QT_Q4_0) {
-    if (s.rpw == 4) return launch_k<QT, 4, 1, EPI>(a, s.lpr, grid, smem, st);
-    switch (s.nu) {
-      case 1: return launch_k<QT, 2, 1, EPI>(a, s.lpr, grid, smem, st);
-      case 2: return launch_k<QT, 2, 2, EPI>(a, s.lpr, grid, smem, st);
-      case 3: return launch_k<QT, 2, 3, EPI>(a, s.lpr, grid, smem, st);
-      default: return launch_k<QT, 2, 4, EPI>(a, s.lpr, grid, smem, st);
+    if (s.nu == 1) {
+      if (s.rpw == 8) return launch_k<QT, 8, 1, EPI>(a, s.lpr, grid, smem, st);
+      if (s.rpw == 4) return launch_k<QT, 4, 1, EPI>(a, s.lpr, grid, smem, st);
+      return launch_k<QT, 2, 1, EPI>(a, s.lpr, grid, smem, st);
     }
+    if (s.nu == 2) {
+      if (s.rpw == 4) return launch_k<QT, 4, 2, EPI>(a, s.lpr, grid, smem, st);
+      return launch_k<QT, 2, 2, EPI>(a, s.lpr, grid, smem, st);
+    }
+    if (s.nu == 3) return launch_k<QT, 2, 3, EPI>(a, s.lpr, grid, smem, st);
+    return launch_k<QT, 2, 4, EPI>(a, s.lpr, grid, smem, st);
   } else {
     return launch_k<QT, 2, 1, EPI>(a, s.lpr, grid, smem, st);
   }
