@@ -73,46 +73,80 @@ __device__ __forceinline__ int xidx(int k) {
 // ---------------------------------------------------------------------------
 constexpr int XD_UNIT_DW = 44;
 
-__device__ __forceinline__ uint32_t digit_nibble(int& v) {
-  const int d = ((v + 8) & 15) - 8;
-  v = (v - d) >> 4;
-  return (uint32_t)(d & 15);
+// Balanced base-16 digits without carries: with E_d = D_d + 8 in [0, 15],
+// sum_d 16^d E_d = X + 0x88888, so the nibbles of (X + 0x88888) are the E_d and
+// XOR 0x88888 turns each into D_d = E_d - 8 as a signed nibble.  Valid for
+// X in [-0x88888, 0x77777], which |X| <= 2^18 satisfies.
+__device__ __forceinline__ uint32_t digit_word(int X) {
+  return (uint32_t)(X + 0x88888) ^ 0x88888u;
 }
 
-// Stages x * norm_w (x alone when norm_w is null) as digit records in one
-// read of x.  RMSNorm's scale rms = 1/sqrt(sum x^2 / K + eps) (TensorMath.cs:142)
-// is a single positive factor per token, so it is applied to the finished dot
-// products instead of to every element; each wave leaves its share of sum x^2
-// in red[wave] for the caller to combine after its __syncthreads().
+// x (and the RMSNorm weight) of the MAXT work items a thread stages.
 // Work item t = (block t/4, dword k = t%4) holds x[32b+4k..+3] and
-// x[32b+16+4k..+3]; the four items of a block sit in adjacent lanes and share
-// the block maximum through two xor-shuffles.
-__device__ __forceinline__ void stage_x_digits(const float* __restrict__ x, const float* __restrict__ norm_w,
-                                               int K, uint32_t* xd, float* red) {
+// x[32b+16+4k..+3]; thread i owns items i, i+256, ...
+template <int MAXT, bool NORM>
+struct XStage {
+  float x[MAXT][8];
+  float g[MAXT][8];
+};
+template <int MAXT>
+struct XStage<MAXT, false> {
+  float x[MAXT][8];
+};
+
+// Issues every load of the staged x before the caller issues its weight
+// loads: vector-memory counters retire in order, so loads issued after the
+// weight stream could not be consumed before the whole stream had landed.
+template <int MAXT, bool NORM>
+__device__ __forceinline__ void stage_load(const float* __restrict__ x, const float* __restrict__ norm_w, int K,
+                                           XStage<MAXT, NORM>& st) {
+  const int ntask = K >> 3;
+#pragma unroll
+  for (int j = 0; j < MAXT; j++) {
+    const int t = threadIdx.x + CN_BLOCK * j;
+    const int b = t >> 2, k = t & 3;
+    float4 lo = make_float4(0.f, 0.f, 0.f, 0.f), hi = lo, glo = lo, ghi = lo;
+    if (t < ntask) {
+      lo = *reinterpret_cast<const float4*>(x + 32 * b + 4 * k);
+      hi = *reinterpret_cast<const float4*>(x + 32 * b + 16 + 4 * k);
+      if constexpr (NORM) {
+        glo = *reinterpret_cast<const float4*>(norm_w + 32 * b + 4 * k);
+        ghi = *reinterpret_cast<const float4*>(norm_w + 32 * b + 16 + 4 * k);
+      }
+    }
+    st.x[j][0] = lo.x; st.x[j][1] = lo.y; st.x[j][2] = lo.z; st.x[j][3] = lo.w;
+    st.x[j][4] = hi.x; st.x[j][5] = hi.y; st.x[j][6] = hi.z; st.x[j][7] = hi.w;
+    if constexpr (NORM) {
+      st.g[j][0] = glo.x; st.g[j][1] = glo.y; st.g[j][2] = glo.z; st.g[j][3] = glo.w;
+      st.g[j][4] = ghi.x; st.g[j][5] = ghi.y; st.g[j][6] = ghi.z; st.g[j][7] = ghi.w;
+    }
+  }
+}
+
+// Writes the digit records of x * norm_w (x alone without NORM).  RMSNorm's
+// scale rms = 1/sqrt(sum x^2 / K + eps) (TensorMath.cs:142) is one positive
+// factor per token, so it is applied to the finished dot products instead of
+// to every element; each wave leaves its share of sum x^2 in red[wave] for the
+// caller to combine after its __syncthreads().  The four items of a block sit
+// in adjacent lanes and share the block maximum through two xor-shuffles.
+template <int MAXT, bool NORM>
+__device__ __forceinline__ void stage_digitize(const XStage<MAXT, NORM>& st, int K, uint32_t* xd, float* red) {
   const int ntask = K >> 3;
   float ss = 0.f;
-  for (int t0 = 0; t0 < ntask; t0 += CN_BLOCK) {
-    const int t = t0 + threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < MAXT; j++) {
+    const int t = threadIdx.x + CN_BLOCK * j;
     const bool on = t < ntask;
     const int b = t >> 2, k = t & 3;
     float v[8];
-    if (on) {
-      const float4 lo = *reinterpret_cast<const float4*>(x + 32 * b + 4 * k);
-      const float4 hi = *reinterpret_cast<const float4*>(x + 32 * b + 16 + 4 * k);
-      v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
-      v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
 #pragma unroll
-      for (int i = 0; i < 8; i++) ss += v[i] * v[i];
-      if (norm_w) {
-        const float4 gl = *reinterpret_cast<const float4*>(norm_w + 32 * b + 4 * k);
-        const float4 gh = *reinterpret_cast<const float4*>(norm_w + 32 * b + 16 + 4 * k);
-        const float g[8] = {gl.x, gl.y, gl.z, gl.w, gh.x, gh.y, gh.z, gh.w};
+    for (int i = 0; i < 8; i++) {
+      v[i] = st.x[j][i];
+      ss += v[i] * v[i];
+    }
+    if constexpr (NORM) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = v[i] * g[i];
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; i++) v[i] = 0.f;
+      for (int i = 0; i < 8; i++) v[i] = v[i] * st.g[j][i];
     }
     float m = 0.f;
 #pragma unroll
@@ -125,12 +159,12 @@ __device__ __forceinline__ void stage_x_digits(const float* __restrict__ x, cons
     uint32_t dw[5] = {0, 0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      int xl = __float2int_rn(ldexpf(v[i], s));
-      int xh = __float2int_rn(ldexpf(v[4 + i], s));
+      const uint32_t tl = digit_word(__float2int_rn(ldexpf(v[i], s)));
+      const uint32_t th = digit_word(__float2int_rn(ldexpf(v[4 + i], s)));
 #pragma unroll
       for (int d = 0; d < 5; d++) {
-        dw[d] |= digit_nibble(xl) << (8 * i);
-        dw[d] |= digit_nibble(xh) << (8 * i + 4);
+        dw[d] |= ((tl >> (4 * d)) & 15u) << (8 * i);
+        dw[d] |= ((th >> (4 * d)) & 15u) << (8 * i + 4);
       }
     }
     if (on) {
@@ -244,7 +278,7 @@ __device__ __forceinline__ void dot_unit_q4_0(const uint32_t (*w)[9], const floa
   }
 }
 
-// Q4_0 unit against the digit record xd (see stage_x_digits): block A's qs
+// Q4_0 unit against the digit record xd (see stage_digitize): block A's qs
 // (pair bytes 2..17) is realigned with alignbyte, block B's (bytes 20..35)
 // is dword aligned.
 template <int RPW>
@@ -521,15 +555,21 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_kernel(GemvArgs a) {
   int it = blockIdx.x * (CN_BLOCK / CN_WAVE) + wave;
 
   uint32_t w[RPW][NU][T::NDW];
-  if (it < n_iters) issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
 
   // ---- prologue: stage x (optionally RMS-normalised) into LDS ----
   if constexpr (QT == QT_Q4_0) {
+    // items per thread: K <= 64 * LPR * NU, K/8 items over 256 threads
+    constexpr int MAXT = (LPR * NU) / 32 > 0 ? (LPR * NU) / 32 : 1;
+    constexpr bool NORM = EPI == GEMV_EPI_QKV || EPI == GEMV_EPI_SWIGLU || EPI == GEMV_EPI_LOGITS;
+    XStage<MAXT, NORM> st;
+    stage_load<MAXT, NORM>(a.x, a.norm_w, K, st);
+    // rows past n_vrows come back as zeros, so idle waves need no branch here
+    issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
     uint32_t* xd = reinterpret_cast<uint32_t*>(smem);
     float* xred = reinterpret_cast<float*>(smem) + (size_t)nunits * XD_UNIT_DW;
-    stage_x_digits(a.x, a.norm_w, K, xd, xred);
+    stage_digitize<MAXT, NORM>(st, K, xd, xred);
     __syncthreads();
-    const float rms = a.norm_w ? 1.0f / sqrtf((xred[0] + xred[1] + xred[2] + xred[3]) / (float)K + a.eps) : 1.0f;
+    const float rms = NORM ? 1.0f / sqrtf((xred[0] + xred[1] + xred[2] + xred[3]) / (float)K + a.eps) : 1.0f;
     while (it < n_iters) {
       float acc[RPW];
 #pragma unroll
@@ -559,6 +599,7 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_kernel(GemvArgs a) {
     }
     return;
   }
+  if (it < n_iters) issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
   float rms = 1.0f;
   if (a.norm_w) {
     float ss = 0.f;
@@ -648,7 +689,7 @@ struct GemvShape {
 // K-quants: one super-block per lane (NU = 1) and 2 rows, LPR the smallest
 // power of two covering the row (min 16).
 template <int QT>
-GemvShape pick_shape(int K, int n_vrows, int num_cus) {
+GemvShape pick_shape(int K, int n_vrows, int num_cus, bool allow8) {
   using T = QTraits<QT>;
   const int nunits = K / T::UNIT;
   GemvShape s{64, 1, 2};
@@ -662,7 +703,7 @@ GemvShape pick_shape(int K, int n_vrows, int num_cus) {
         break;  // larger nu only adds idle lanes
       }
     if (best < 0) { s.lpr = 64; s.nu = 4; }
-    const int max_rpw = s.nu == 1 ? 8 : (s.nu == 2 ? 4 : 2);
+    const int max_rpw = s.nu == 1 ? (allow8 ? 8 : 4) : (s.nu == 2 ? 4 : 2);
     const int resident[9] = {0, 0, 20, 0, 16, 0, 0, 0, 12};
     s.rpw = max_rpw;
     for (int rpw = 2; rpw <= max_rpw; rpw *= 2) {
@@ -692,7 +733,10 @@ hipError_t launch_k(const GemvArgs& a, int lpr, int grid, size_t smem, hipStream
 template <int QT, int EPI>
 hipError_t launch_qt(const GemvArgs& a, int num_cus, hipStream_t st) {
   using T = QTraits<QT>;
-  const GemvShape s = pick_shape<QT>(a.K, a.n_vrows, num_cus);
+  // 8 rows per lane only for the norm-fused epilogues (the wide QKV, gate/up
+  // and LM-head launches); hipcc 7.2 fails to compile the 8-row STORE/ADD forms.
+  constexpr bool kAllow8 = EPI == GEMV_EPI_QKV || EPI == GEMV_EPI_SWIGLU || EPI == GEMV_EPI_LOGITS;
+  const GemvShape s = pick_shape<QT>(a.K, a.n_vrows, num_cus, kAllow8);
   const int rw = s.rpw * (CN_WAVE / s.lpr);
   const int n_iters = (a.n_vrows + rw - 1) / rw;
   const int waves_per_block = CN_BLOCK / CN_WAVE;
@@ -705,7 +749,9 @@ hipError_t launch_qt(const GemvArgs& a, int num_cus, hipStream_t st) {
   (void)T::NDW;
   if constexpr (QT == QT_Q4_0) {
     if (s.nu == 1) {
-      if (s.rpw == 8) return launch_k<QT, 8, 1, EPI>(a, s.lpr, grid, smem, st);
+      if constexpr (kAllow8) {
+        if (s.rpw == 8) return launch_k<QT, 8, 1, EPI>(a, s.lpr, grid, smem, st);
+      }
       if (s.rpw == 4) return launch_k<QT, 4, 1, EPI>(a, s.lpr, grid, smem, st);
       return launch_k<QT, 2, 1, EPI>(a, s.lpr, grid, smem, st);
     }
