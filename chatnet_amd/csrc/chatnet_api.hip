@@ -167,10 +167,12 @@ int chatnet_create(const chatnet_config* cfg, int device, chatnet_model** out) {
   m->kv_elt = c.kv_dtype == CHATNET_KV_F16 ? 2 : 4;
   m->layers.resize(c.n_layers);
   const size_t kv_bytes = (size_t)c.n_layers * c.context_length * m->kv_dim * m->kv_elt;
-  // Attention splits: about two workgroups per CU over the KV heads.
+  // Attention splits: about one workgroup per CU over the KV heads (at most 16
+  // splits); each workgroup leaves one partial per query head.
   int splits = 1;
-  while (splits < 64 && splits * c.n_kv_heads < 2 * m->num_cus && splits * 2 <= c.context_length) splits *= 2;
+  while (splits < 16 && splits * 2 * c.n_kv_heads <= m->num_cus && splits * 2 <= c.context_length) splits *= 2;
   m->attn_splits = splits;
+  const size_t attn_slots = (size_t)c.n_heads * splits;
   auto cleanup = [m]() { chatnet_destroy(m); };
   if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) {
     cleanup();
@@ -185,8 +187,8 @@ int chatnet_create(const chatnet_config* cfg, int device, chatnet_model** out) {
       {(void**)&m->h, sizeof(float) * c.hidden_dim},
       {(void**)&m->logits, sizeof(float) * c.vocab_size},
       {(void**)&m->state, sizeof(int) * 4},
-      {(void**)&m->attn_part_o, sizeof(float) * (size_t)c.n_heads * splits * c.head_dim},
-      {(void**)&m->attn_part_ml, sizeof(float) * (size_t)c.n_heads * splits * 2},
+      {(void**)&m->attn_part_o, sizeof(float) * attn_slots * c.head_dim},
+      {(void**)&m->attn_part_ml, sizeof(float) * attn_slots * 2},
   };
   for (auto& a : allocs) {
     if (hipMalloc(a.p, a.n) != hipSuccess) {
@@ -395,7 +397,6 @@ int launch_token(chatnet_model* m, bool lm_head) {
     at.kv_f16 = a.kv_f16;
     at.scale = 1.0f / sqrtf((float)c.head_dim);  // LlamaModel.cs:248
     at.splits = m->attn_splits;
-    at.chunk_cap = (c.context_length + m->attn_splits - 1) / m->attn_splits;
     at.part_o = m->attn_part_o;
     at.part_ml = m->attn_part_ml;
     HIP_TRY(attn_decode_launch(at, st));

@@ -34,134 +34,152 @@ __device__ __forceinline__ float kv_load(const void* base, size_t idx) {
 }
 
 // Split-position GQA decode attention (LlamaModel.ComputeAttention,
-// LlamaModel.cs:241-346):  for query head h with kvh = h / kv_mul (:265),
-//   s[p] = (q_h . K[p][kvh]) * scale  for p <= pos,  w = softmax(s),
+// LlamaModel.cs:241-346): for query head h with kvh = h / kv_mul (:265),
+//   s[p] = (q_h . K[p][kvh]) * scale  for p <= pos,  w = softmax(s) (TensorMath.cs:177-241),
 //   out_h = sum_p w[p] V[p][kvh].
-// Grid = n_kv_heads x splits.  Workgroup (kvh, c) takes positions
-// [c*chunk, (c+1)*chunk) of seq = pos+1 and every query head of the group, so
-// each K/V row is read once for all kv_mul heads; waves take positions, lanes
-// take head_dim elements (coalesced rows).  Each split leaves (max, sum, o)
+// Grid = n_kv_heads x splits; workgroup (kvh, c) takes positions
+// [c*chunk, (c+1)*chunk) of seq = pos+1, and wave w of it the positions
+// p = c*chunk + w + 4i.  A wave issues the K and V row loads of PW positions
+// at once (lane l owns head elements l*EPL..), keeps q of up to KVM query
+// heads of the group in registers, reduces each score across the wave and
+// folds it into a running (max, sum, o) per head (online softmax).  The four
+// wave partials of a head are folded through LDS into one partial per split
 // for attn_merge_kernel.
-template <int HD, bool F16, int GMAX>
+template <int HD, bool F16, int KVM>
 __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
   constexpr int EPL = HD >= 64 ? HD / 64 : 1;  // head elements per lane
-  constexpr int G = CN_BLOCK / HD;             // position groups in the V pass
-  extern __shared__ float sm[];
+  constexpr int PW = 8;                        // positions whose loads are in flight together
+  constexpr int NW = CN_BLOCK / CN_WAVE;
   const int kvh = blockIdx.x / a.splits;
   const int split = blockIdx.x % a.splits;
-  const int kv_mul = a.kv_mul;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int seq = *a.pos + 1;
   const int chunk = (seq + a.splits - 1) / a.splits;
   const int p0 = split * chunk;
   const int p1 = min(seq, p0 + chunk);
-  const int cap = a.chunk_cap;
-  float* qs = sm;                       // kv_mul * HD
-  float* sc = qs + kv_mul * HD;         // kv_mul * cap
-  float* ml = sc + kv_mul * cap;        // kv_mul * 2
-  float* op = ml + 2 * kv_mul;          // G * GMAX * HD
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const size_t koff = (size_t)kvh * HD;
-  const int h0 = kvh * kv_mul;
+  const int h0 = kvh * a.kv_mul;
+  __shared__ float so[KVM * NW * HD];
+  __shared__ float sml[KVM * NW * 2];
 
-  for (int i = threadIdx.x; i < kv_mul * HD; i += CN_BLOCK) qs[i] = a.q[(size_t)h0 * HD + i];
-  __syncthreads();
-
-  // scores
-  for (int p = p0 + wave; p < p1; p += CN_BLOCK / CN_WAVE) {
-    float kv[EPL];
+  for (int jg = 0; jg < a.kv_mul; jg += KVM) {
+    const int nj = min(KVM, a.kv_mul - jg);
+    float q[KVM][EPL], m[KVM], l[KVM], o[KVM][EPL];
 #pragma unroll
-    for (int e = 0; e < EPL; e++) {
-      const int d = lane * EPL + e;
-      kv[e] = d < HD ? kv_load<F16>(a.kc, (size_t)p * a.kv_dim + koff + d) : 0.f;
-    }
-    for (int j = 0; j < kv_mul; j++) {
-      float s = 0.f;
+    for (int j = 0; j < KVM; j++) {
+      m[j] = -INFINITY;
+      l[j] = 0.f;
 #pragma unroll
       for (int e = 0; e < EPL; e++) {
         const int d = lane * EPL + e;
-        if (d < HD) s += qs[j * HD + d] * kv[e];
+        q[j][e] = (j < nj && d < HD) ? a.q[(size_t)(h0 + jg + j) * HD + d] : 0.f;
+        o[j][e] = 0.f;
       }
-      s = cn_wave_sum(s);
-      if (lane == 0) sc[j * cap + (p - p0)] = s * a.scale;
     }
-  }
-  __syncthreads();
-
-  // per-head max and exp-sum of this split (one wave per head)
-  for (int j = wave; j < kv_mul; j += CN_BLOCK / CN_WAVE) {
-    float m = -INFINITY;
-    for (int i = lane; i < p1 - p0; i += CN_WAVE) m = fmaxf(m, sc[j * cap + i]);
-    m = cn_wave_max(m);
-    float l = 0.f;
-    for (int i = lane; i < p1 - p0; i += CN_WAVE) {
-      const float e = expf(sc[j * cap + i] - m);
-      sc[j * cap + i] = e;
-      l += e;
-    }
-    l = cn_wave_sum(l);
-    if (lane == 0) {
-      ml[2 * j] = m;
-      ml[2 * j + 1] = l;
-    }
-  }
-  __syncthreads();
-
-  // o_j[d] = sum_p e_j[p] V[p][d], GMAX heads at a time
-  const int d = threadIdx.x % HD, g = threadIdx.x / HD;
-  for (int jb = 0; jb < kv_mul; jb += GMAX) {
-    float o[GMAX];
+    for (int pb = p0 + wave; pb < p1; pb += NW * PW) {
+      float kr[PW][EPL], vr[PW][EPL];
 #pragma unroll
-    for (int j = 0; j < GMAX; j++) o[j] = 0.f;
-    for (int p = p0 + g; p < p1; p += G) {
-      const float v = kv_load<F16>(a.vc, (size_t)p * a.kv_dim + koff + d);
+      for (int i = 0; i < PW; i++) {
+        const int p = pb + NW * i;
 #pragma unroll
-      for (int j = 0; j < GMAX; j++)
-        if (jb + j < kv_mul) o[j] += sc[(jb + j) * cap + (p - p0)] * v;
-    }
-#pragma unroll
-    for (int j = 0; j < GMAX; j++) op[(g * GMAX + j) * HD + d] = o[j];
-    __syncthreads();
-    if (g == 0) {
-#pragma unroll
-      for (int j = 0; j < GMAX; j++) {
-        if (jb + j >= kv_mul) break;
-        float t = 0.f;
-#pragma unroll
-        for (int k = 0; k < G; k++) t += op[(k * GMAX + j) * HD + d];
-        if (a.splits == 1) {  // single split: normalise in place
-          a.out[(size_t)(h0 + jb + j) * HD + d] = t / ml[2 * (jb + j) + 1];
-          continue;
+        for (int e = 0; e < EPL; e++) {
+          const int d = lane * EPL + e;
+          const bool ok = p < p1 && d < HD;
+          const size_t idx = (size_t)p * a.kv_dim + koff + d;
+          kr[i][e] = ok ? kv_load<F16>(a.kc, idx) : 0.f;
+          vr[i][e] = ok ? kv_load<F16>(a.vc, idx) : 0.f;
         }
-        const size_t slot = (size_t)(h0 + jb + j) * a.splits + split;
-        a.part_o[slot * HD + d] = t;
-        if (d == 0) {
-          a.part_ml[2 * slot] = ml[2 * (jb + j)];
-          a.part_ml[2 * slot + 1] = ml[2 * (jb + j) + 1];
+      }
+#pragma unroll
+      for (int i = 0; i < PW; i++) {
+        if (pb + NW * i >= p1) break;  // uniform across the wave
+#pragma unroll
+        for (int j = 0; j < KVM; j++) {
+          if (j >= nj) break;
+          float sdot = 0.f;
+#pragma unroll
+          for (int e = 0; e < EPL; e++) sdot += q[j][e] * kr[i][e];
+          const float sc = cn_wave_sum(sdot) * a.scale;
+          const float mn = fmaxf(m[j], sc);
+          const float c = expf(m[j] - mn);
+          const float pe = expf(sc - mn);
+          l[j] = l[j] * c + pe;
+#pragma unroll
+          for (int e = 0; e < EPL; e++) o[j][e] = o[j][e] * c + pe * vr[i][e];
+          m[j] = mn;
         }
       }
     }
+    // fold the NW wave partials of each head through LDS, one partial per split
+#pragma unroll
+    for (int j = 0; j < KVM; j++) {
+      if (j >= nj) break;
+#pragma unroll
+      for (int e = 0; e < EPL; e++) {
+        const int d = lane * EPL + e;
+        if (d < HD) so[(j * NW + wave) * HD + d] = o[j][e];
+      }
+      if (lane == 0) {
+        sml[2 * (j * NW + wave)] = m[j];
+        sml[2 * (j * NW + wave) + 1] = l[j];
+      }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < nj * HD; i += CN_BLOCK) {
+      const int j = i / HD, d = i % HD;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < NW; w++)
+        if (sml[2 * (j * NW + w) + 1] > 0.f) M = fmaxf(M, sml[2 * (j * NW + w)]);
+      float L = 0.f, acc = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; w++) {
+        const float lw = sml[2 * (j * NW + w) + 1];
+        if (lw > 0.f) {
+          const float f = expf(sml[2 * (j * NW + w)] - M);
+          L += lw * f;
+          acc += so[(j * NW + w) * HD + d] * f;
+        }
+      }
+      const size_t slot = (size_t)(h0 + jg + j) * a.splits + split;
+      a.part_o[slot * HD + d] = acc;
+      if (d == 0) {
+        a.part_ml[2 * slot] = M;
+        a.part_ml[2 * slot + 1] = L;
+      }
+    }
     __syncthreads();
   }
-
 }
 
 // Merges the split partials of one query head (grid = n_heads, block = HD):
-//   M = max_c m_c,  L = sum_c l_c e^(m_c - M),  out = sum_c o_c e^(m_c - M) / L.
-// Empty splits (l_c = 0) contribute nothing.
-template <int HD>
+//   M = max_c m_c,  L = sum_c l_c e^(m_c - M),  out = sum_c o_c e^(m_c - M) / L,
+// empty splits (l_c = 0) contributing nothing.  All loads are issued in one
+// round (at most SMAX splits).
+template <int HD, int SMAX>
 __global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs a) {
   const int h = blockIdx.x, d = threadIdx.x;
   const size_t base = (size_t)h * a.splits;
+  float mc[SMAX], lc[SMAX], oc[SMAX];
+#pragma unroll
+  for (int c = 0; c < SMAX; c++) {
+    const bool on = c < a.splits;
+    mc[c] = on ? a.part_ml[2 * (base + c)] : 0.f;
+    lc[c] = on ? a.part_ml[2 * (base + c) + 1] : 0.f;
+    oc[c] = on ? a.part_o[(base + c) * HD + d] : 0.f;
+  }
   float M = -INFINITY;
-  for (int c = 0; c < a.splits; c++)
-    if (a.part_ml[2 * (base + c) + 1] > 0.f) M = fmaxf(M, a.part_ml[2 * (base + c)]);
+#pragma unroll
+  for (int c = 0; c < SMAX; c++)
+    if (lc[c] > 0.f) M = fmaxf(M, mc[c]);
   float L = 0.f, acc = 0.f;
-  for (int c = 0; c < a.splits; c++) {
-    const float lc = a.part_ml[2 * (base + c) + 1];
-    if (lc == 0.f) continue;
-    const float f = expf(a.part_ml[2 * (base + c)] - M);
-    L += lc * f;
-    acc += a.part_o[(base + c) * HD + d] * f;
+#pragma unroll
+  for (int c = 0; c < SMAX; c++) {
+    if (lc[c] > 0.f) {
+      const float f = expf(mc[c] - M);
+      L += lc[c] * f;
+      acc += oc[c] * f;
+    }
   }
   a.out[(size_t)h * HD + d] = acc / L;
 }
@@ -221,13 +239,12 @@ __global__ void set_state_kernel(int* state, int pos, int tok, int step) {
 
 template <int HD, bool F16>
 hipError_t attn_launch_t(const AttnArgs& a, hipStream_t st) {
-  constexpr int GMAX = 8;
-  const int G = CN_BLOCK / HD;
-  const size_t smem = sizeof(float) * ((size_t)a.kv_mul * HD + (size_t)a.kv_mul * a.chunk_cap + 2 * a.kv_mul +
-                                       (size_t)G * GMAX * HD);
   const int n_kv = a.n_heads / a.kv_mul;
-  hipLaunchKernelGGL((attn_decode_kernel<HD, F16, GMAX>), dim3(n_kv * a.splits), dim3(CN_BLOCK), smem, st, a);
-  if (a.splits > 1) hipLaunchKernelGGL((attn_merge_kernel<HD>), dim3(a.n_heads), dim3(HD), 0, st, a);
+  if (a.kv_mul == 1)
+    hipLaunchKernelGGL((attn_decode_kernel<HD, F16, 1>), dim3(n_kv * a.splits), dim3(CN_BLOCK), 0, st, a);
+  else
+    hipLaunchKernelGGL((attn_decode_kernel<HD, F16, 8>), dim3(n_kv * a.splits), dim3(CN_BLOCK), 0, st, a);
+  hipLaunchKernelGGL((attn_merge_kernel<HD, 16>), dim3(a.n_heads), dim3(HD), 0, st, a);
   return hipGetLastError();
 }
 
@@ -240,7 +257,7 @@ hipError_t embed_launch(const void* emb, int type, int dim, const int* tok, floa
 }
 
 hipError_t attn_decode_launch(const AttnArgs& a, hipStream_t st) {
-  if (a.splits < 1 || a.chunk_cap * a.splits < a.ctx) return hipErrorInvalidValue;
+  if (a.splits < 1 || a.splits > 16) return hipErrorInvalidValue;
   if (a.head_dim == 64) return a.kv_f16 ? attn_launch_t<64, true>(a, st) : attn_launch_t<64, false>(a, st);
   if (a.head_dim == 128) return a.kv_f16 ? attn_launch_t<128, true>(a, st) : attn_launch_t<128, false>(a, st);
   if (a.head_dim == 32) return a.kv_f16 ? attn_launch_t<32, true>(a, st) : attn_launch_t<32, false>(a, st);

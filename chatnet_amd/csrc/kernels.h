@@ -49,10 +49,9 @@ struct AttnArgs {
   const int* pos;
   int n_heads, kv_mul, head_dim, kv_dim, ctx, kv_f16;
   float scale;
-  float* part_o;      // split scratch: [n_heads][splits][head_dim]
+  float* part_o;      // split partials: [n_heads][splits][head_dim]
   float* part_ml;     // [n_heads][splits][2] (max, sum)
-  int splits;         // position chunks processed in parallel
-  int chunk_cap;      // ceil(ctx / splits): LDS rows reserved per head
+  int splits;         // position chunks processed in parallel (<= 16)
 };
 hipError_t attn_decode_launch(const AttnArgs& a, hipStream_t st);
 
