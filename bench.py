@@ -63,8 +63,10 @@ def decode_run(cfg, ck, prompt, steps, warmup):
     return dt, toks
 
 
-def gemv_sweep(shapes, launches_per_shape=64, rotate_bytes=1 << 30):
-    """Cold per-launch GEMV time via HIP events on the stream of the launches."""
+def gemv_sweep(shapes, launches_per_shape=64, replays=5, rotate_bytes=1 << 30):
+    """Cold per-launch GEMV time: `launches_per_shape` launches over distinct
+    weight copies are captured into one HIP graph, so the device runs them
+    back to back, and HIP events on that stream time `replays` replays."""
     from chatnet_amd import hiprt, ops, synth
 
     res = {}
@@ -80,17 +82,25 @@ def gemv_sweep(shapes, launches_per_shape=64, rotate_bytes=1 << 30):
             pool.copy_from(base, nb, dst_offset=c * stride)
         x = hiprt.DeviceBuffer.from_numpy(synth.normal(99, f"sweepx{K}", K, 1.0))
         y = hiprt.DeviceBuffer(4 * M)
-        stream = 0  # launches and events share the null stream
-        for c in range(min(copies, 8)):  # warm-up
-            ops.matmul_ptr(2, pool.ptr + c * stride, x.ptr, y.ptr, M, K, 1, stream)
         hiprt.synchronize()
+        stream = hiprt.Stream()
+
+        def issue():
+            for i in range(launches_per_shape):
+                c = i % copies
+                ops.matmul_ptr(2, pool.ptr + c * stride, x.ptr, y.ptr, M, K, 1, stream.h)
+
+        graph = hiprt.Graph(stream, issue)
+        graph.launch()  # warm-up
+        stream.synchronize()
         e0, e1 = hiprt.Event(), hiprt.Event()
-        e0.record(stream)
-        for i in range(launches_per_shape):
-            c = i % copies
-            ops.matmul_ptr(2, pool.ptr + c * stride, x.ptr, y.ptr, M, K, 1, stream)
-        e1.record(stream)
-        us = e0.elapsed_ms(e1) * 1000.0 / launches_per_shape
+        e0.record(stream.h)
+        for _ in range(replays):
+            graph.launch()
+        e1.record(stream.h)
+        us = e0.elapsed_ms(e1) * 1000.0 / (launches_per_shape * replays)
+        del graph
+        stream.synchronize()
         alg = gemv_algorithmic_bytes(M, K)
         res[f"{M}x{K}"] = {"us": round(us, 3), "GB/s": round(alg / us / 1e3, 1),
                            "frac": round(alg / us / 1e3 / HBM_PEAK_GBS, 4), "alg_bytes": alg}

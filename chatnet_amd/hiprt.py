@@ -37,6 +37,15 @@ def rt() -> ctypes.CDLL:
             "hipEventElapsedTime": [ctypes.POINTER(ctypes.c_float), vp, vp],
             "hipEventDestroy": [vp],
             "hipGetErrorString": [ctypes.c_int],
+            "hipStreamCreate": [ctypes.POINTER(vp)],
+            "hipStreamDestroy": [vp],
+            "hipStreamSynchronize": [vp],
+            "hipStreamBeginCapture": [vp, ctypes.c_int],
+            "hipStreamEndCapture": [vp, ctypes.POINTER(vp)],
+            "hipGraphInstantiate": [ctypes.POINTER(vp), vp, vp, vp, sz],
+            "hipGraphLaunch": [vp, vp],
+            "hipGraphExecDestroy": [vp],
+            "hipGraphDestroy": [vp],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -98,6 +107,50 @@ class DeviceBuffer:
     def __del__(self):
         try:
             self.free()
+        except Exception:
+            pass
+
+
+class Stream:
+    """A non-default stream (default priority)."""
+
+    def __init__(self):
+        s = ctypes.c_void_p()
+        _ok(rt().hipStreamCreate(ctypes.byref(s)), "hipStreamCreate")
+        self.h = s.value
+
+    def synchronize(self) -> None:
+        _ok(rt().hipStreamSynchronize(self.h), "hipStreamSynchronize")
+
+    def __del__(self):
+        try:
+            rt().hipStreamDestroy(self.h)
+        except Exception:
+            pass
+
+
+class Graph:
+    """Captures the work issued on a stream by `fn()` into a replayable graph."""
+
+    def __init__(self, stream: Stream, fn):
+        _ok(rt().hipStreamBeginCapture(stream.h, 0), "hipStreamBeginCapture")
+        try:
+            fn()
+        finally:
+            g = ctypes.c_void_p()
+            _ok(rt().hipStreamEndCapture(stream.h, ctypes.byref(g)), "hipStreamEndCapture")
+        e = ctypes.c_void_p()
+        _ok(rt().hipGraphInstantiate(ctypes.byref(e), g, None, None, 0), "hipGraphInstantiate")
+        rt().hipGraphDestroy(g)
+        self.exec = e.value
+        self.stream = stream
+
+    def launch(self) -> None:
+        _ok(rt().hipGraphLaunch(self.exec, self.stream.h), "hipGraphLaunch")
+
+    def __del__(self):
+        try:
+            rt().hipGraphExecDestroy(self.exec)
         except Exception:
             pass
 
