@@ -109,6 +109,22 @@ def gemv_sweep(shapes, launches_per_shape=64, replays=5, rotate_bytes=1 << 30):
     return res
 
 
+def measured_traffic(shape):
+    """HBM bytes per launch of the roofline GEMV, from the committed
+    rocprofv3 FETCH_SIZE + WRITE_SIZE summary (counters scaled by the same
+    counters read on a copy kernel of known size), or None if absent."""
+    path = os.path.join(ROOT, "profiles", "gemv_q4_0_sweep_roofline.md")
+    key = f"traffic_bytes_per_launch {shape[0]}x{shape[1]}:"
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith(key):
+                    return int(line[len(key):].strip())
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(cfg, ck, prompt_len=4, decode=8):
     """The oracle (C restatement of the reference's CPU path) on the host cores."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -207,7 +223,8 @@ def main():
                    "tinyllama_1b_q4_0_decode_tok_s": tiny},
         "gemv_sweep_q4_0_n1_cold": sweep,
         "roofline": {"bound": "hbm", "achieved": roof["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": roof["frac"], "traffic": None,
+                     "frac": roof["frac"], "traffic": measured_traffic(ROOF_SHAPE),
+                     "traffic_source": "profiles/gemv_q4_0_sweep_roofline.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
                      "kernel": "gemv_kernel<Q4_0> (chatnet_matmul N=1) at 11008x4096, cold",
                      "alg_bytes_per_launch": roof["alg_bytes"], "avg_launch_us": roof["us"]},
         "cpu_baseline": cpu,
