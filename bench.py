@@ -29,6 +29,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16
 METRIC = "decode tok/s bs1 (1.1B & 7B Q4_0); Q4_0 GEMV achieved HBM GB/s vs peak"
 SWEEP = [(2048, 2048), (256, 2048), (5632, 2048), (2048, 5632), (32000, 2048), (4096, 4096), (11008, 4096)]
 ROOF_SHAPE = (11008, 4096)
@@ -109,6 +110,81 @@ def gemv_sweep(shapes, launches_per_shape=64, replays=5, rotate_bytes=1 << 30):
     return res
 
 
+def gemm_sweep(shapes, ns, rotate_bytes=1 << 30):
+    """Batched chatnet_matmul (x fp32 -> bf16, MFMA GEMM, split-K reduce when
+    used) per call, cold weights as in gemv_sweep; HIP events on the stream the
+    calls are captured on."""
+    from chatnet_amd import hiprt, ops, synth
+
+    res = {}
+    for (M, K) in shapes:
+        nb = q4_0_bytes(M, K)
+        stride = (nb + 256 + 4095) // 4096 * 4096
+        copies = max(4, min(64, -(-rotate_bytes // stride)))
+        t = synth.tensor(2, 99, f"sweep{M}x{K}", M, K)
+        base = hiprt.DeviceBuffer.from_numpy(t.data)
+        pool = hiprt.DeviceBuffer(copies * stride)
+        pool.fill(0)
+        for c in range(copies):
+            pool.copy_from(base, nb, dst_offset=c * stride)
+        per = {}
+        for N in ns:
+            x = hiprt.DeviceBuffer.from_numpy(synth.normal(99, f"gemmx{N}x{K}", N * K, 1.0))
+            y = hiprt.DeviceBuffer(4 * M * N)
+            stream = hiprt.Stream()
+            launches = 32 if N <= 64 else 8
+            ops.matmul_ptr(2, pool.ptr, x.ptr, y.ptr, M, K, N, stream.h)  # sizes the workspace
+            stream.synchronize()
+
+            def issue():
+                for i in range(launches):
+                    ops.matmul_ptr(2, pool.ptr + (i % copies) * stride, x.ptr, y.ptr, M, K, N, stream.h)
+
+            graph = hiprt.Graph(stream, issue)
+            graph.launch()
+            stream.synchronize()
+            e0, e1 = hiprt.Event(), hiprt.Event()
+            replays = 3
+            e0.record(stream.h)
+            for _ in range(replays):
+                graph.launch()
+            e1.record(stream.h)
+            us = e0.elapsed_ms(e1) * 1000.0 / (launches * replays)
+            del graph
+            stream.synchronize()
+            alg = nb + 4 * K * N + 4 * M * N
+            tflops = 2.0 * M * N * K / us / 1e6
+            per[str(N)] = {"us": round(us, 2), "GB/s": round(alg / us / 1e3, 1), "TFLOP/s": round(tflops, 1),
+                           "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+            x.free()
+            y.free()
+        res[f"{M}x{K}"] = per
+        pool.free()
+        base.free()
+    return res
+
+
+def prefill_run(cfg, ck, n_prompt, n_decode):
+    """Time to first token of an n_prompt-token prompt forwarded as one span,
+    then n_decode greedy decode tokens."""
+    from chatnet_amd import HipLlamaModel, hiprt, synth
+
+    prompt = synth.tokens(77, "prefill", n_prompt, cfg.vocab_size)
+    with HipLlamaModel(cfg, ck) as m:
+        m.forward(prompt, 0)  # warm-up: span buffers, kernel attributes
+        m.decode_greedy(4)
+        hiprt.synchronize()
+        t0 = time.perf_counter()
+        m.forward(prompt, 0)  # returns after the logits are on the host
+        t1 = time.perf_counter()
+        toks = m.decode_greedy(n_decode)
+        t2 = time.perf_counter()
+    assert len(toks) == n_decode
+    return {"prompt_tokens": n_prompt, "ttft_ms": round((t1 - t0) * 1e3, 3),
+            "prefill_tok_s": round(n_prompt / (t1 - t0), 1), "decode_tokens": n_decode,
+            "decode_tok_s": round(n_decode / (t2 - t1), 1)}
+
+
 def measured_traffic(shape):
     """HBM bytes per launch of the roofline GEMV, from the committed
     rocprofv3 FETCH_SIZE + WRITE_SIZE summary (counters scaled by the same
@@ -158,6 +234,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-tinyllama", action="store_true")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the batched GEMM sweep")
     ap.add_argument("--roofline-only", action="store_true", help="only the isolated GEMV legs")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -180,6 +257,12 @@ def main():
     toks7 = None
     cpu = None
     tiny = None
+    gsweep = None
+    prefill = None
+    if not args.roofline_only and not args.no_gemm:
+        log("gemm sweep N = 8, 64, 512 (cold)")
+        gsweep = gemm_sweep(SWEEP, (8, 64, 512))
+        log(f"gemm sweep: {json.dumps(gsweep)}")
     if not args.roofline_only:
         cfg7 = LLAMA2_7B.replace(context_length=2048)
         log("generating Llama-2-7B-shaped Q4_0 checkpoint")
@@ -204,6 +287,9 @@ def main():
             dt1, _ = decode_run(cfg1, ck1, p1, 128, 8)
             tiny = round(128 / dt1, 1)
             log(f"TinyLlama decode: {tiny} tok/s")
+            log("TinyLlama 512-token prefill + 128 decode")
+            prefill = prefill_run(cfg1, ck1, 512, 128)
+            log(f"  {json.dumps(prefill)}")
 
     res = {
         "metric": METRIC,
@@ -222,6 +308,8 @@ def main():
                    "kv_cache": "f32", "context_length": 2048, "weights": "Q4_0 (all matrices)",
                    "tinyllama_1b_q4_0_decode_tok_s": tiny},
         "gemv_sweep_q4_0_n1_cold": sweep,
+        "gemm_sweep_q4_0_cold": gsweep,
+        "tinyllama_q4_0_prefill": prefill,
         "roofline": {"bound": "hbm", "achieved": roof["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": roof["frac"], "traffic": measured_traffic(ROOF_SHAPE),
                      "traffic_source": "profiles/gemv_q4_0_sweep_roofline.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",

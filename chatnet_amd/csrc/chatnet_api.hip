@@ -15,7 +15,10 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "../../include/chatnet_hip.h"
@@ -65,6 +68,32 @@ bool is_matrix_type(uint32_t t) {
   return t == CHATNET_GGML_Q4_0 || t == CHATNET_GGML_Q4_K || t == CHATNET_GGML_Q6_K;
 }
 
+// Workspace of chatnet_matmul's batched path (bf16 copy of x + K-split
+// partials), one per (device, stream): work queued on one stream runs in
+// order, so calls sharing a stream can share it.  Grown on demand (after
+// draining that stream) and kept until the process ends.
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, std::pair<char*, size_t>> g_ws;
+
+int matmul_workspace(int dev, hipStream_t st, size_t bytes, char** out) {
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  auto& e = g_ws[{dev, st}];
+  if (e.second < bytes) {
+    if (e.first) {
+      HIP_TRY(hipStreamSynchronize(st));
+      (void)hipFree(e.first);
+      e = {nullptr, 0};
+    }
+    if (hipMalloc((void**)&e.first, bytes) != hipSuccess) {
+      e = {nullptr, 0};
+      return fail(CHATNET_ERR_OUT_OF_MEMORY, "hipMalloc of %zu bytes (matmul workspace) failed", bytes);
+    }
+    e.second = bytes;
+  }
+  *out = e.first;
+  return CHATNET_OK;
+}
+
 }  // namespace
 
 struct chatnet_model {
@@ -89,6 +118,17 @@ struct chatnet_model {
   bool have_logits = false;
   int next_pos = 0;  // position after the last forwarded token
   int last_tok = 0;  // last forwarded token
+  // Batched span buffers (allocated by the first span of >= kSpanMin tokens):
+  // up to span_cap tokens per pass.
+  int span_cap = 0;
+  float* sp_x = nullptr;       // [cap][dim] residual stream
+  // GEMM inputs as bf16 hi + lo planes (x = hi + lo to ~2^-17)
+  uint16_t* sp_xb = nullptr;   // [2][cap][dim]: normed x, then attention output
+  uint16_t* sp_hb = nullptr;   // [2][cap][hidden]: silu(gate)*up
+  float* sp_qkv = nullptr;     // [cap][dim + 2*kv_dim]
+  int* sp_tok = nullptr;       // [cap]
+  float* sp_part = nullptr;    // GEMM K-split partials
+  size_t sp_part_bytes = 0;
 };
 
 extern "C" {
@@ -221,6 +261,7 @@ void chatnet_destroy(chatnet_model* m) {
   fr(m->kcache); fr(m->vcache); fr(m->x); fr(m->q); fr(m->att); fr(m->h); fr(m->logits);
   fr(m->state); fr(m->out_tokens);
   fr(m->attn_part_o); fr(m->attn_part_ml);
+  fr(m->sp_x); fr(m->sp_xb); fr(m->sp_hb); fr(m->sp_qkv); fr(m->sp_tok); fr(m->sp_part);
   if (m->stream) (void)hipStreamDestroy(m->stream);
   delete m;
 }
@@ -465,7 +506,210 @@ int ensure_out_tokens(chatnet_model* m, int cap) {
   return CHATNET_OK;
 }
 
+// Spans of at least this many tokens run as one batch on the MFMA GEMM.
+constexpr int kSpanMin = 8;
+constexpr int kSpanCap = 512;
+
+bool span_batchable(const chatnet_model* m, int n) {
+  if (n < kSpanMin) return false;
+  const char* e = getenv("CHATNET_SPAN_BATCH");  // "0": per-token schedule for every span
+  if (e && e[0] == '0') return false;
+  const chatnet_config& c = m->cfg;
+  if (!attn_prefill_supports(c.head_dim, c.n_heads / c.n_kv_heads)) return false;
+  if (!gemm_supports(CHATNET_GGML_Q4_0, c.dim) || !gemm_supports(CHATNET_GGML_Q4_0, c.hidden_dim)) return false;
+  for (const Layer& L : m->layers) {
+    const DevTensor* ts[] = {&L.wq, &L.wk, &L.wv, &L.wo, &L.wg, &L.wu, &L.wd};
+    for (const DevTensor* t : ts)
+      if (t->type != CHATNET_GGML_Q4_0) return false;
+  }
+  return true;
+}
+
+int ensure_span_buffers(chatnet_model* m) {
+  if (m->span_cap) return CHATNET_OK;
+  const chatnet_config& c = m->cfg;
+  const int cap = c.context_length < kSpanCap ? c.context_length : kSpanCap;
+  struct { void** p; size_t n; } allocs[] = {
+      {(void**)&m->sp_x, sizeof(float) * cap * c.dim},
+      {(void**)&m->sp_xb, sizeof(uint16_t) * 2 * cap * c.dim},
+      {(void**)&m->sp_hb, sizeof(uint16_t) * 2 * cap * c.hidden_dim},
+      {(void**)&m->sp_qkv, sizeof(float) * cap * (c.dim + 2 * m->kv_dim)},
+      {(void**)&m->sp_tok, sizeof(int) * cap},
+  };
+  for (auto& a : allocs) {
+    if (hipMalloc(a.p, a.n) != hipSuccess) return fail(CHATNET_ERR_OUT_OF_MEMORY, "hipMalloc of %zu bytes failed", a.n);
+  }
+  m->span_cap = cap;
+  return CHATNET_OK;
+}
+
+int span_gemm(chatnet_model* m, GemmArgs& g) {
+  g.precise = 1;
+  const size_t need = gemm_workspace_bytes(g.M, g.N, g.K, m->num_cus, true);
+  if (need > m->sp_part_bytes) {
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    if (m->sp_part) (void)hipFree(m->sp_part);
+    m->sp_part = nullptr;
+    m->sp_part_bytes = 0;
+    if (hipMalloc(&m->sp_part, need) != hipSuccess)
+      return fail(CHATNET_ERR_OUT_OF_MEMORY, "hipMalloc of %zu bytes failed", need);
+    m->sp_part_bytes = need;
+  }
+  g.part = m->sp_part;
+  HIP_TRY(gemm_launch(g, m->num_cus, m->stream));
+  return CHATNET_OK;
+}
+
+// LlamaModel.Forward (LlamaModel.cs:93-238) over tokens[0..n) at positions
+// position.. as batches of up to span_cap tokens: every projection is one
+// MFMA GEMM over the batch, attention is causal over the cache, and the LM
+// head runs for the last token only (LlamaModel.cs:207).
+int run_span(chatnet_model* m, const int32_t* tokens, int n, int position) {
+  int rc = ensure_span_buffers(m);
+  if (rc) return rc;
+  const chatnet_config& c = m->cfg;
+  hipStream_t st = m->stream;
+  const int kvd = m->kv_dim, qkv_ld = c.dim + 2 * kvd;
+  uint16_t* xb_lo = m->sp_xb + (size_t)m->span_cap * c.dim;
+  uint16_t* hb_lo = m->sp_hb + (size_t)m->span_cap * c.hidden_dim;
+  int last_rows = 0;
+  for (int s0 = 0; s0 < n; s0 += m->span_cap) {
+    const int cn = n - s0 < m->span_cap ? n - s0 : m->span_cap;
+    const int p0 = position + s0;
+    HIP_TRY(hipMemcpyAsync(m->sp_tok, tokens + s0, sizeof(int) * cn, hipMemcpyHostToDevice, st));
+    HIP_TRY(embed_launch(m->emb.ptr, (int)m->emb.type, c.dim, m->sp_tok, m->sp_x, st, cn));
+    for (int l = 0; l < c.n_layers; l++) {
+      const Layer& L = m->layers[l];
+      const size_t loff = (size_t)l * c.context_length * kvd * m->kv_elt;
+      void* kc = (char*)m->kcache + loff;
+      void* vc = (char*)m->vcache + loff;
+      HIP_TRY(rmsnorm_bf16_launch(m->sp_x, (const float*)L.attn_norm.ptr, c.rms_norm_eps, m->sp_xb, xb_lo, cn, c.dim,
+                                  st));
+      GemmArgs g;
+      memset(&g, 0, sizeof(g));
+      g.qtype = CHATNET_GGML_Q4_0;
+      g.w[0] = (const uint8_t*)L.wq.ptr;
+      g.w[1] = (const uint8_t*)L.wk.ptr;
+      g.w[2] = (const uint8_t*)L.wv.ptr;
+      g.seg_rows[0] = c.dim;
+      g.seg_rows[1] = kvd;
+      g.seg_rows[2] = kvd;
+      g.seg_mode = GEMM_SEG_CONCAT;
+      g.M = qkv_ld;
+      g.K = c.dim;
+      g.N = cn;
+      g.xb = m->sp_xb;
+      g.xb_lo = xb_lo;
+      g.epi = GEMV_EPI_STORE;
+      g.y = m->sp_qkv;
+      g.ldy = qkv_ld;
+      if ((rc = span_gemm(m, g))) return rc;
+
+      RopeKvArgs r;
+      memset(&r, 0, sizeof(r));
+      r.qkv = m->sp_qkv;
+      r.ld = qkv_ld;
+      r.dim = c.dim;
+      r.kv_dim = kvd;
+      r.head_dim = c.head_dim;
+      r.p0 = p0;
+      r.rope_dim_inv = 1.0f / (float)c.head_dim;
+      r.rope_neg_log_base = -logf(c.rope_freq_base);
+      r.kcache = kc;
+      r.vcache = vc;
+      r.kv_f16 = c.kv_dtype == CHATNET_KV_F16;
+      HIP_TRY(rope_kv_launch(r, cn, st));
+
+      PrefillAttnArgs at;
+      memset(&at, 0, sizeof(at));
+      at.qkv = m->sp_qkv;
+      at.ld = qkv_ld;
+      at.kc = kc;
+      at.vc = vc;
+      at.out = m->sp_xb;
+      at.out_lo = xb_lo;
+      at.ldo = c.dim;
+      at.n = cn;
+      at.p0 = p0;
+      at.n_heads = c.n_heads;
+      at.kv_mul = c.n_heads / c.n_kv_heads;
+      at.head_dim = c.head_dim;
+      at.kv_dim = kvd;
+      at.kv_f16 = r.kv_f16;
+      at.scale = 1.0f / sqrtf((float)c.head_dim);  // LlamaModel.cs:248
+      HIP_TRY(attn_prefill_launch(at, st));
+
+      GemmArgs o;
+      memset(&o, 0, sizeof(o));
+      o.qtype = CHATNET_GGML_Q4_0;
+      o.w[0] = (const uint8_t*)L.wo.ptr;
+      o.seg_rows[0] = c.dim;
+      o.M = c.dim;
+      o.K = c.dim;
+      o.N = cn;
+      o.xb = m->sp_xb;
+      o.xb_lo = xb_lo;
+      o.epi = GEMV_EPI_ADD;
+      o.y = m->sp_x;
+      o.ldy = c.dim;
+      if ((rc = span_gemm(m, o))) return rc;
+
+      HIP_TRY(rmsnorm_bf16_launch(m->sp_x, (const float*)L.ffn_norm.ptr, c.rms_norm_eps, m->sp_xb, xb_lo, cn, c.dim,
+                                  st));
+      GemmArgs gu;
+      memset(&gu, 0, sizeof(gu));
+      gu.qtype = CHATNET_GGML_Q4_0;
+      gu.w[0] = (const uint8_t*)L.wg.ptr;
+      gu.w[1] = (const uint8_t*)L.wu.ptr;
+      gu.seg_rows[0] = c.hidden_dim;
+      gu.seg_rows[1] = c.hidden_dim;
+      gu.seg_mode = GEMM_SEG_INTERLEAVE;
+      gu.M = 2 * c.hidden_dim;
+      gu.K = c.dim;
+      gu.N = cn;
+      gu.xb = m->sp_xb;
+      gu.xb_lo = xb_lo;
+      gu.epi = GEMV_EPI_SWIGLU;
+      gu.hb = m->sp_hb;
+      gu.hb_lo = hb_lo;
+      gu.ldh = c.hidden_dim;
+      if ((rc = span_gemm(m, gu))) return rc;
+
+      GemmArgs d;
+      memset(&d, 0, sizeof(d));
+      d.qtype = CHATNET_GGML_Q4_0;
+      d.w[0] = (const uint8_t*)L.wd.ptr;
+      d.seg_rows[0] = c.dim;
+      d.M = c.dim;
+      d.K = c.hidden_dim;
+      d.N = cn;
+      d.xb = m->sp_hb;
+      d.xb_lo = hb_lo;
+      d.epi = GEMV_EPI_ADD;
+      d.y = m->sp_x;
+      d.ldy = c.dim;
+      if ((rc = span_gemm(m, d))) return rc;
+    }
+    last_rows = cn;
+  }
+  // final RMSNorm + LM head of the last token (LlamaModel.cs:203-213)
+  GemvArgs o = base_args(m);
+  o.K = c.dim;
+  o.x = m->sp_x + (size_t)(last_rows - 1) * c.dim;
+  o.norm_w = (const float*)m->out_norm.ptr;
+  o.w[0] = (const uint8_t*)m->out.ptr;
+  o.seg_rows[0] = c.vocab_size;
+  o.n_vrows = c.vocab_size;
+  o.out[0] = m->logits;
+  HIP_TRY(gemv_launch((int)m->out.type, GEMV_EPI_LOGITS, o, m->num_cus, st));
+  m->have_logits = true;
+  m->next_pos = position + n;
+  m->last_tok = tokens[n - 1];
+  return CHATNET_OK;
+}
+
 int run_prompt(chatnet_model* m, const int32_t* tokens, int n, int position) {
+  if (span_batchable(m, n)) return run_span(m, tokens, n, position);
   for (int t = 0; t < n; t++) {
     HIP_TRY(set_state_launch(m->state, position + t, tokens[t], -1, m->stream));
     int rc = launch_token(m, t == n - 1);
@@ -618,6 +862,32 @@ int chatnet_matmul(uint32_t type, const void* w_dev, const float* x_dev, float* 
   HIP_TRY(hipGetDevice(&dev));
   const int cus = device_cus(dev);
   hipStream_t st = (hipStream_t)stream;
+  if (N >= 8 && gemm_supports((int)type, K)) {
+    // x -> bf16 into the stream's workspace, then the MFMA GEMM.
+    const size_t xb_bytes = ((size_t)N * K * sizeof(uint16_t) + 255) & ~(size_t)255;
+    const size_t part_bytes = gemm_workspace_bytes(M, N, K, cus, false);
+    char* ws = nullptr;
+    int rc = matmul_workspace(dev, st, xb_bytes + part_bytes, &ws);
+    if (rc) return rc;
+    HIP_TRY(to_bf16_launch(x_dev, (uint16_t*)ws, (size_t)N * K, st));
+    GemmArgs g;
+    memset(&g, 0, sizeof(g));
+    g.qtype = (int)type;
+    g.w[0] = g.w[1] = g.w[2] = (const uint8_t*)w_dev;
+    g.seg_rows[0] = M;
+    g.seg_mode = GEMM_SEG_SINGLE;
+    g.M = M;
+    g.K = K;
+    g.N = N;
+    g.xb = (const uint16_t*)ws;
+    g.epi = GEMV_EPI_STORE;
+    g.y = y_dev;
+    g.ldy = M;
+    g.part = part_bytes ? (float*)(ws + xb_bytes) : nullptr;
+    HIP_TRY(gemm_launch(g, cus, st));
+    g_err.clear();
+    return CHATNET_OK;
+  }
   for (int n = 0; n < N; n++) {
     GemvArgs a;
     memset(&a, 0, sizeof(a));

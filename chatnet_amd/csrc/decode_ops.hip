@@ -9,7 +9,8 @@ namespace {
 // per-element conversion, Q4_0 row dequantization (DequantQ4_0.cs:28-58).
 __global__ __launch_bounds__(CN_BLOCK) void embed_kernel(const void* emb, int type, int dim,
                                                          const int* tok, float* x) {
-  const int t = *tok;
+  const int t = tok[blockIdx.y];
+  x += (size_t)blockIdx.y * dim;
   const int i = blockIdx.x * CN_BLOCK + threadIdx.x;
   if (i >= dim) return;
   if (type == 0) {
@@ -250,8 +251,9 @@ hipError_t attn_launch_t(const AttnArgs& a, hipStream_t st) {
 
 }  // namespace
 
-hipError_t embed_launch(const void* emb, int type, int dim, const int* tok, float* x, hipStream_t st) {
-  hipLaunchKernelGGL(embed_kernel, dim3((dim + CN_BLOCK - 1) / CN_BLOCK), dim3(CN_BLOCK), 0, st, emb,
+hipError_t embed_launch(const void* emb, int type, int dim, const int* tok, float* x, hipStream_t st, int n) {
+  if (n < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(embed_kernel, dim3((dim + CN_BLOCK - 1) / CN_BLOCK, n), dim3(CN_BLOCK), 0, st, emb,
                      type, dim, tok, x);
   return hipGetLastError();
 }

@@ -36,8 +36,66 @@ bool gemv_supports(int qtype, int K);
 size_t gemv_lds_bytes(int qtype, int K);
 hipError_t gemv_launch(int qtype, int epi, const GemvArgs& a, int num_cus, hipStream_t st);
 
-// Embedding row gather (LlamaModel.LoadEmbedding, LlamaModel.cs:365-394).
-hipError_t embed_launch(const void* emb, int type, int dim, const int* tok, float* x, hipStream_t st);
+// Batched quantized GEMM on the matrix cores (gemm.hip):
+//   acc[n][vr] = sum_k W_vr[k] * xb[n][k],  0 <= n < N, 0 <= vr < M
+// epilogue `epi`: GEMV_EPI_STORE y[n*ldy+vr] = acc, GEMV_EPI_ADD y += acc,
+// GEMV_EPI_SWIGLU hb[n*ldh+vr/2] = bf16(silu(acc[vr even]) * acc[vr odd]).
+enum { GEMM_SEG_SINGLE = 0, GEMM_SEG_CONCAT = 1, GEMM_SEG_INTERLEAVE = 2 };
+struct GemmArgs {
+  int qtype;
+  const uint8_t* w[3];
+  int seg_rows[3];
+  int seg_mode;
+  int M, K, N;            // M = virtual rows
+  const uint16_t* xb;     // N x K bf16, row stride K
+  const uint16_t* xb_lo;  // precise: low parts, x = xb + xb_lo
+  int precise;            // exact-weight two-plane kernel
+  int epi;
+  float* y;               // STORE / ADD target
+  int ldy;
+  uint16_t* hb;           // SWIGLU target (bf16)
+  uint16_t* hb_lo;        // optional low parts of h
+  int ldh;
+  float* part;            // K-split partials, gemm_workspace_bytes() bytes
+  int splits;             // set by gemm_launch
+};
+bool gemm_supports(int qtype, int K);
+size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool precise);
+hipError_t gemm_launch(const GemmArgs& a, int num_cus, hipStream_t st);
+hipError_t to_bf16_launch(const float* x, uint16_t* xb, size_t n, hipStream_t st);
+// xb = bf16(RMSNorm(x) * g) per row; with xb_lo also the low parts.
+hipError_t rmsnorm_bf16_launch(const float* x, const float* g, float eps, uint16_t* xb, uint16_t* xb_lo, int rows,
+                               int dim, hipStream_t st);
+
+// Span kernels (prefill.hip).  qkv is [n][ld] fp32 with q | k | v columns.
+struct RopeKvArgs {
+  float* qkv;
+  int ld, dim, kv_dim, head_dim, p0;
+  float rope_dim_inv, rope_neg_log_base;
+  void* kcache;  // layer base
+  void* vcache;
+  int kv_f16;
+};
+hipError_t rope_kv_launch(const RopeKvArgs& a, int n, hipStream_t st);
+
+struct PrefillAttnArgs {
+  const float* qkv;  // q at column 0 of each row
+  int ld;
+  const void* kc;    // layer base, [ctx][kv_dim]
+  const void* vc;
+  uint16_t* out;     // bf16 [n][ldo]
+  uint16_t* out_lo;  // optional low parts
+  int ldo;
+  int n, p0, n_heads, kv_mul, head_dim, kv_dim, kv_f16;
+  float scale;
+};
+bool attn_prefill_supports(int head_dim, int kv_mul);
+hipError_t attn_prefill_launch(const PrefillAttnArgs& a, hipStream_t st);
+
+// Embedding row gather (LlamaModel.LoadEmbedding, LlamaModel.cs:365-394) of
+// n tokens read from device memory: x[i] = row tok[i].
+hipError_t embed_launch(const void* emb, int type, int dim, const int* tok, float* x, hipStream_t st,
+                        int n = 1);
 
 // GQA decode attention over the device KV cache (LlamaModel.ComputeAttention,
 // LlamaModel.cs:241-346).  Reads pos from device memory; seq = pos+1.

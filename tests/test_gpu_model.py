@@ -137,3 +137,61 @@ def test_error_paths():
         with pytest.raises(_native.ChatnetOutOfRange):
             m.forward([cfg.vocab_size], 0)
         m.forward([1, 2], 0)  # still usable after errors
+
+
+# -- batched spans (>= 8 tokens: MFMA GEMM projections + causal span attention) --
+SPAN_SMALL = TINY_TEST.replace(dim=256, hidden_dim=512, n_heads=4, n_kv_heads=2, head_dim=64,
+                               context_length=1100)
+
+
+def span_case(cfg, seed, n_prompt, n_next=8):
+    ck = synth.llama_checkpoint(cfg, seed=seed, mix="q4_0")
+    toks = synth.tokens(seed, "prompt", n_prompt + n_next, cfg.vocab_size)
+    with HipLlamaModel(cfg, ck) as m:
+        g = m.forward(toks[:n_prompt], 0)
+        g2 = m.forward(toks[n_prompt:], n_prompt)  # a second span continuing the sequence
+    ora = oracle.OracleLlama(cfg, ck)
+    r = ora.forward(toks[:n_prompt], 0)
+    r2 = ora.forward(toks[n_prompt:], n_prompt)
+    tol = LOGIT_TOL if cfg.kv_dtype == _native.KV_F32 else 2 * LOGIT_TOL
+    e1, e2 = float(np.max(np.abs(g - r))), float(np.max(np.abs(g2 - r2)))
+    print(f"span logits max-abs err {e1:.3g} / {e2:.3g} (logit scale {float(np.max(np.abs(r))):.3g})", flush=True)
+    assert e1 <= tol and e2 <= tol
+
+
+def test_span_tinyllama_layers_match_oracle():
+    announce("span: tinyllama-shaped 2 layers, 24 + 8 tokens")
+    span_case(TINYLLAMA_1B.replace(n_layers=2, context_length=128), 31, 24)
+
+
+def test_span_llama7b_layer_matches_oracle():
+    from chatnet_amd import LLAMA2_7B
+    announce("span: llama-7b-shaped 1 layer, 16 + 8 tokens")
+    span_case(LLAMA2_7B.replace(n_layers=1, context_length=64), 32, 16)
+
+
+def test_span_fp16_kv_matches_oracle():
+    announce("span: fp16 kv cache")
+    span_case(SPAN_SMALL.replace(kv_dtype=_native.KV_F16, context_length=96), 33, 40)
+
+
+def test_span_longer_than_batch_cap_matches_oracle_and_token_schedule(monkeypatch):
+    """600 tokens run as batches of 512 + 88; logits and the greedy tokens that
+    follow agree with the oracle and with the per-token schedule."""
+    cfg = SPAN_SMALL
+    ck = synth.llama_checkpoint(cfg, seed=34, mix="q4_0")
+    toks = synth.tokens(34, "prompt", 600, cfg.vocab_size)
+    announce("span: 600 tokens (two batches)")
+    with HipLlamaModel(cfg, ck) as m:
+        g = m.forward(toks, 0)
+        gt = m.decode_greedy(16)
+    monkeypatch.setenv("CHATNET_SPAN_BATCH", "0")
+    announce("span: 600 tokens per-token schedule")
+    with HipLlamaModel(cfg, ck) as m:
+        h = m.forward(toks, 0)
+    ora = oracle.OracleLlama(cfg, ck)
+    r = ora.forward(toks, 0)
+    assert np.max(np.abs(g - r)) <= LOGIT_TOL
+    assert np.max(np.abs(h - r)) <= LOGIT_TOL
+    o, margins = oracle.OracleLlama(cfg, ck).generate_greedy(list(toks), 16)
+    compare_greedy(list(gt), o, margins)
