@@ -33,19 +33,30 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16
 METRIC = "decode tok/s bs1 (1.1B & 7B Q4_0); Q4_0 GEMV achieved HBM GB/s vs peak"
 SWEEP = [(2048, 2048), (256, 2048), (5632, 2048), (2048, 5632), (32000, 2048), (4096, 4096), (11008, 4096)]
 ROOF_SHAPE = (11008, 4096)
+# Q4_K_M-style mix on Llama-2-7B shapes: Q4_K attention + gate/up, Q6_K down + output
+KQ4_SHAPES = [(4096, 4096), (11008, 4096)]
+KQ6_SHAPES = [(4096, 11008), (32000, 4096)]
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+BLOCK = {2: (32, 18), 12: (256, 144), 14: (256, 210)}  # ggml type -> (weights, bytes) per block
+
+
+def weight_bytes(M: int, K: int, qtype: int = 2) -> int:
+    w, b = BLOCK[qtype]
+    return M * K // w * b
+
+
 def q4_0_bytes(M: int, K: int) -> int:
-    return M * K // 32 * 18
+    return weight_bytes(M, K, 2)
 
 
-def gemv_algorithmic_bytes(M: int, K: int) -> int:
+def gemv_algorithmic_bytes(M: int, K: int, qtype: int = 2) -> int:
     # weights + x (fp32) + y (fp32)
-    return q4_0_bytes(M, K) + 4 * K + 4 * M
+    return weight_bytes(M, K, qtype) + 4 * K + 4 * M
 
 
 def decode_run(cfg, ck, prompt, steps, warmup):
@@ -64,7 +75,7 @@ def decode_run(cfg, ck, prompt, steps, warmup):
     return dt, toks
 
 
-def gemv_sweep(shapes, launches_per_shape=64, replays=5, rotate_bytes=1 << 30):
+def gemv_sweep(shapes, launches_per_shape=64, replays=5, rotate_bytes=1 << 30, qtype=2):
     """Cold per-launch GEMV time: `launches_per_shape` launches over distinct
     weight copies are captured into one HIP graph, so the device runs them
     back to back, and HIP events on that stream time `replays` replays."""
@@ -72,10 +83,10 @@ def gemv_sweep(shapes, launches_per_shape=64, replays=5, rotate_bytes=1 << 30):
 
     res = {}
     for (M, K) in shapes:
-        nb = q4_0_bytes(M, K)
+        nb = weight_bytes(M, K, qtype)
         stride = (nb + 256 + 4095) // 4096 * 4096
         copies = max(4, min(256, -(-rotate_bytes // stride)))
-        t = synth.tensor(2, 99, f"sweep{M}x{K}", M, K)
+        t = synth.tensor(qtype, 99, f"sweep{M}x{K}", M, K)
         base = hiprt.DeviceBuffer.from_numpy(t.data)
         pool = hiprt.DeviceBuffer(copies * stride)
         pool.fill(0)
@@ -89,7 +100,7 @@ def gemv_sweep(shapes, launches_per_shape=64, replays=5, rotate_bytes=1 << 30):
         def issue():
             for i in range(launches_per_shape):
                 c = i % copies
-                ops.matmul_ptr(2, pool.ptr + c * stride, x.ptr, y.ptr, M, K, 1, stream.h)
+                ops.matmul_ptr(qtype, pool.ptr + c * stride, x.ptr, y.ptr, M, K, 1, stream.h)
 
         graph = hiprt.Graph(stream, issue)
         graph.launch()  # warm-up
@@ -102,7 +113,7 @@ def gemv_sweep(shapes, launches_per_shape=64, replays=5, rotate_bytes=1 << 30):
         us = e0.elapsed_ms(e1) * 1000.0 / (launches_per_shape * replays)
         del graph
         stream.synchronize()
-        alg = gemv_algorithmic_bytes(M, K)
+        alg = gemv_algorithmic_bytes(M, K, qtype)
         res[f"{M}x{K}"] = {"us": round(us, 3), "GB/s": round(alg / us / 1e3, 1),
                            "frac": round(alg / us / 1e3 / HBM_PEAK_GBS, 4), "alg_bytes": alg}
         for b in (pool, base, x, y):
@@ -235,6 +246,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-tinyllama", action="store_true")
     ap.add_argument("--no-gemm", action="store_true", help="skip the batched GEMM sweep")
+    ap.add_argument("--no-kquant", action="store_true", help="skip the Q4_K / Q6_K legs")
     ap.add_argument("--roofline-only", action="store_true", help="only the isolated GEMV legs")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -259,6 +271,19 @@ def main():
     tiny = None
     gsweep = None
     prefill = None
+    kq = None
+    if not args.roofline_only and not args.no_kquant:
+        log("Q4_K / Q6_K gemv (cold) and 7B Q4_K_M-style 64-token decode")
+        kq = {"gemv_q4_k_cold": gemv_sweep(KQ4_SHAPES, qtype=12),
+              "gemv_q6_k_cold": gemv_sweep(KQ6_SHAPES, qtype=14)}
+        cfgk = LLAMA2_7B.replace(context_length=2048)
+        ckk = synth.llama_checkpoint(cfgk, seed=11, mix="q4_k_m")
+        pk = synth.tokens(11, "prompt", 16, cfgk.vocab_size)
+        dtk, _ = decode_run(cfgk, ckk, pk, 64, 4)
+        kq["llama2_7b_q4_k_m_decode_tok_s"] = round(64 / dtk, 1)
+        kq["weights_GB"] = round(synth.checkpoint_bytes(ckk) / 1e9, 3)
+        del ckk
+        log(f"  {json.dumps(kq)}")
     if not args.roofline_only and not args.no_gemm:
         log("gemm sweep N = 8, 64, 512 (cold)")
         gsweep = gemm_sweep(SWEEP, (8, 64, 512))
@@ -310,6 +335,7 @@ def main():
         "gemv_sweep_q4_0_n1_cold": sweep,
         "gemm_sweep_q4_0_cold": gsweep,
         "tinyllama_q4_0_prefill": prefill,
+        "llama2_7b_q4_k_m": kq,
         "roofline": {"bound": "hbm", "achieved": roof["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": roof["frac"], "traffic": measured_traffic(ROOF_SHAPE),
                      "traffic_source": "profiles/gemv_q4_0_sweep_roofline.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",

@@ -1,28 +1,20 @@
-// gemm.hip — quantized-weight GEMM on the bf16 matrix cores of gfx950 (N > 1).
+// gemm.hip — quantized-weight GEMM on the matrix cores of gfx950 (N >= 8).
 //
 // y[n][m] = sum_k W[m][k] * x[n][k] for a batch of N inputs: the batched form
 // of TensorMath.MatVecMulQ4_0 (src/ChatNet.Core/Tensors/TensorMath.cs:548-578)
-// that a multi-token LlamaModel.Forward span (LlamaModel.cs:93-238) needs.
+// that chatnet_matmul with N >= 8 and a multi-token LlamaModel.Forward span
+// (LlamaModel.cs:93-238) need.
 //
-// Operands: W stays in its raw Q4_0 blocks in HBM; x arrives as bf16 [N][K]
-// (converted, or RMS-normalised and converted, by the producer kernel).
-// Each Q4_0 block (32 weights along K) is exactly the K extent of one
-// v_mfma_f32_16x16x32_bf16, so a wave dequantizes a block of 16 rows straight
-// into the MFMA A operand in registers: lane l holds row l%16 and the 8
-// consecutive k in [8g, 8g+8), g = l/16, which are the low (g < 2) or high
-// (g >= 2) nibbles of qs[8(g&1) .. 8(g&1)+7].  Each value is d*(q-8) computed
-// exactly in fp32 (one fma) and rounded once to bf16.  W needs no LDS: every
-// W element is used by exactly one wave.  The x tile (BN columns x KC of K) is
-// shared by the 4 waves through LDS, double-buffered; the next chunk's x and W
-// loads are issued before the current chunk's MFMAs.  Accumulation is fp32.
-//
-// Tiles: a workgroup owns BM = 64*MT rows (16*MT per wave) x BN = 16*NT
-// columns; when that leaves the chip under-filled the K range is split and
-// the partial tiles are summed by gemm_reduce_kernel, which then applies the
-// epilogue.  Epilogues: STORE y = acc, ADD y += acc (residual), SWIGLU (rows
-// interleave gate/up, h = silu(gate)*up written as bf16 for the next GEMM).
-// A second, exact-weight kernel (gemm_q4_0_x2_kernel, below) serves the
-// forward pass of multi-token spans.
+// W stays in its raw Q4_0 blocks in HBM; x arrives as bf16 [N][K] (one
+// plane, or hi + lo planes for the exact-weight variant) from the producer
+// kernel (conversion, RMSNorm, attention or the SwiGLU epilogue).  W bytes
+// and x tiles stream through an LDS ring by direct global->LDS loads; each
+// wave dequantizes its W rows into v_mfma_f32_32x32x16_bf16 operands in
+// registers and accumulates in fp32.  When the tile grid leaves the chip
+// under-filled the K range is split and gemm_reduce_kernel sums the partial
+// tiles and applies the epilogue.  Epilogues: STORE y = acc, ADD y += acc
+// (residual), SWIGLU (rows interleave gate/up; h = silu(gate)*up is written
+// as bf16 (hi + lo) for the next GEMM).
 #include "device_common.h"
 #include "kernels.h"
 
@@ -52,51 +44,6 @@ __device__ __forceinline__ const uint32_t* gemm_row_ptr(const GemmArgs& a, int v
     }
   }
   return reinterpret_cast<const uint32_t*>(a.w[seg]) + (size_t)r * row_dw;
-}
-
-// The 7 dwords of a 36-byte unit that lane group g needs: d of both blocks
-// and 8 bytes of qs per block (qs[0..7] for even g, qs[8..15] for odd g).
-struct UnitRegs {
-  uint32_t a0, a1, a2, a3, b0, b1, b2;
-};
-
-__device__ __forceinline__ void load_unit(const uint32_t* p, int h, UnitRegs& u) {
-  if (p) {
-    u.a0 = p[0];
-    u.a1 = p[2 * h];
-    u.a2 = p[2 * h + 1];
-    u.a3 = p[2 * h + 2];
-    u.b0 = p[4];
-    u.b1 = p[5 + 2 * h];
-    u.b2 = p[6 + 2 * h];
-  } else {
-    u.a0 = u.a1 = u.a2 = u.a3 = u.b0 = u.b1 = u.b2 = 0u;
-  }
-}
-
-// 8 weights d*(q-8) as bf16 from 8 nibbles held in bytes of q0 (k 0..3), q1 (k 4..7).
-__device__ __forceinline__ bf16x8 dequant8(uint32_t q0, uint32_t q1, float d) {
-  const float nd = -8.0f * d;
-  bf16x8 r;
-  r[0] = (__bf16)fmaf(cn_ubyte<0>(q0), d, nd);
-  r[1] = (__bf16)fmaf(cn_ubyte<1>(q0), d, nd);
-  r[2] = (__bf16)fmaf(cn_ubyte<2>(q0), d, nd);
-  r[3] = (__bf16)fmaf(cn_ubyte<3>(q0), d, nd);
-  r[4] = (__bf16)fmaf(cn_ubyte<0>(q1), d, nd);
-  r[5] = (__bf16)fmaf(cn_ubyte<1>(q1), d, nd);
-  r[6] = (__bf16)fmaf(cn_ubyte<2>(q1), d, nd);
-  r[7] = (__bf16)fmaf(cn_ubyte<3>(q1), d, nd);
-  return r;
-}
-
-// A operands of block A (first 32 weights) and block B of a unit for lane group g.
-__device__ __forceinline__ void dequant_unit(const UnitRegs& u, int nshift, bf16x8& fa, bf16x8& fb) {
-  const uint32_t qa0 = (__builtin_amdgcn_alignbyte(u.a2, u.a1, 2) >> nshift) & 0x0F0F0F0Fu;
-  const uint32_t qa1 = (__builtin_amdgcn_alignbyte(u.a3, u.a2, 2) >> nshift) & 0x0F0F0F0Fu;
-  const uint32_t qb0 = (u.b1 >> nshift) & 0x0F0F0F0Fu;
-  const uint32_t qb1 = (u.b2 >> nshift) & 0x0F0F0F0Fu;
-  fa = dequant8(qa0, qa1, cn_h2f(u.a0));
-  fb = dequant8(qb0, qb1, cn_h2f(u.b0 >> 16));
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
@@ -152,331 +99,322 @@ __device__ __forceinline__ void write_out4(const GemmArgs& a, int epi, int n, in
   }
 }
 
-template <int MT, int NT, int KC>
-__global__ __launch_bounds__(CN_BLOCK) void gemm_q4_0_kernel(GemmArgs a) {
-  constexpr int BN = 16 * NT;
-  constexpr int XS = KC + 8;             // LDS row stride (bf16): 16 B pad -> conflict-free b128 reads
-  constexpr int XV = BN * KC / 8;        // 16-byte x vectors per chunk
-  constexpr int XR = (XV + CN_BLOCK - 1) / CN_BLOCK;
-  constexpr int UPC = KC / 64;           // units per chunk
-  __shared__ __attribute__((aligned(16))) uint16_t xs[2][BN * XS];
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int g = lane >> 4, li = lane & 15;
-  const int h = g & 1, nshift = (g >> 1) * 4;
-
-  // Workgroup -> (m tile, n tile, K split); the n tiles of one m tile are
-  // adjacent so their W reads meet in L2.
-  const int n_nt = (a.N + BN - 1) / BN;
-  int bid = blockIdx.x;
-  const int ks = bid % a.splits;
-  bid /= a.splits;
-  const int nt = bid % n_nt;
-  const int mt = bid / n_nt;
-  const int m_wave = mt * 64 * MT + wave * 16 * MT;
-  const int n0 = nt * BN;
-
-  const int nchunks = a.K / KC;
-  const int cps = (nchunks + a.splits - 1) / a.splits;
-  const int c_begin = ks * cps;
-  const int c_end = min(nchunks, c_begin + cps);
-
-  const int row_dw = a.K / 64 * Q4_0_UNIT_DW;
-  const uint32_t* wrow[MT];
+// 16 weights d*(q-8) of one lane as bf16: 8 per MFMA step (low nibbles of
+// q0/q1 for the first, high nibbles for the second).  w = d*(q-8) is exact in
+// fp32 (at most 14 significant bits); `hi` is bf16(w) and, when `precise`,
+// `lo` = bf16(w - hi) makes hi + lo == w exactly.
+__device__ __forceinline__ void dequant_w16(uint32_t q0, uint32_t q1, float d, bool precise, bf16x8 (&hi)[2],
+                                            bf16x8 (&lo)[2]) {
+  const float nd = -8.0f * d;
+  uint32_t n[2][2] = {{q0 & 0x0F0F0F0Fu, q1 & 0x0F0F0F0Fu}, {(q0 >> 4) & 0x0F0F0F0Fu, (q1 >> 4) & 0x0F0F0F0Fu}};
+  // Opaque to the optimizer: without this it folds the masks into one
+  // bit-field extract per element instead of v_cvt_f32_ubyte{0..3}.
+  asm volatile("" : "+v"(n[0][0]), "+v"(n[0][1]), "+v"(n[1][0]), "+v"(n[1][1]));
 #pragma unroll
-  for (int r = 0; r < MT; r++) wrow[r] = gemm_row_ptr(a, m_wave + 16 * r + li, row_dw);
-
-  f32x4 acc[MT][NT];
+  for (int s = 0; s < 2; s++) {
+    float w[8];
+    w[0] = fmaf(cn_ubyte<0>(n[s][0]), d, nd);
+    w[1] = fmaf(cn_ubyte<1>(n[s][0]), d, nd);
+    w[2] = fmaf(cn_ubyte<2>(n[s][0]), d, nd);
+    w[3] = fmaf(cn_ubyte<3>(n[s][0]), d, nd);
+    w[4] = fmaf(cn_ubyte<0>(n[s][1]), d, nd);
+    w[5] = fmaf(cn_ubyte<1>(n[s][1]), d, nd);
+    w[6] = fmaf(cn_ubyte<2>(n[s][1]), d, nd);
+    w[7] = fmaf(cn_ubyte<3>(n[s][1]), d, nd);
 #pragma unroll
-  for (int r = 0; r < MT; r++)
-#pragma unroll
-    for (int c = 0; c < NT; c++) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  if (c_begin >= c_end) {
-    // empty split: contributes zeros
-  } else {
-    uint4 xr[XR];
-    UnitRegs wr[MT][UPC];
-
-    auto load_x = [&](int c) {
-      const int k0 = c * KC;
-#pragma unroll
-      for (int j = 0; j < XR; j++) {
-        const int i = threadIdx.x + CN_BLOCK * j;
-        const int n = i / (KC / 8), k8 = i % (KC / 8);
-        uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        if (i < XV && n0 + n < a.N)
-          v = *reinterpret_cast<const uint4*>(a.xb + (size_t)(n0 + n) * a.K + k0 + 8 * k8);
-        xr[j] = v;
-      }
-    };
-    auto store_x = [&](int buf) {
-#pragma unroll
-      for (int j = 0; j < XR; j++) {
-        const int i = threadIdx.x + CN_BLOCK * j;
-        if (i < XV) {
-          const int n = i / (KC / 8), k8 = i % (KC / 8);
-          *reinterpret_cast<uint4*>(&xs[buf][n * XS + 8 * k8]) = xr[j];
-        }
-      }
-    };
-    auto load_w = [&](int c) {
-#pragma unroll
-      for (int r = 0; r < MT; r++)
-#pragma unroll
-        for (int u = 0; u < UPC; u++)
-          load_unit(wrow[r] ? wrow[r] + (size_t)(c * UPC + u) * Q4_0_UNIT_DW : nullptr, h, wr[r][u]);
-    };
-
-    load_x(c_begin);
-    load_w(c_begin);
-    store_x(0);
-    __syncthreads();
-
-    for (int c = c_begin; c < c_end; c++) {
-      const int buf = (c - c_begin) & 1;
-      UnitRegs cur[MT][UPC];
-#pragma unroll
-      for (int r = 0; r < MT; r++)
-#pragma unroll
-        for (int u = 0; u < UPC; u++) cur[r][u] = wr[r][u];
-      const bool more = c + 1 < c_end;
-      if (more) {
-        load_x(c + 1);  // x first: vector-memory counters retire in order
-        load_w(c + 1);
-      }
-      const uint16_t* xt = xs[buf];
-#pragma unroll
-      for (int u = 0; u < UPC; u++) {
-        bf16x8 fa[MT], fb[MT];
-#pragma unroll
-        for (int r = 0; r < MT; r++) dequant_unit(cur[r][u], nshift, fa[r], fb[r]);
-#pragma unroll
-        for (int half = 0; half < 2; half++) {
-          const int kofs = u * 64 + half * 32 + 8 * g;
-#pragma unroll
-          for (int cc = 0; cc < NT; cc++) {
-            const uint4 bv = *reinterpret_cast<const uint4*>(&xt[(16 * cc + li) * XS + kofs]);
-            const bf16x8 bfr = __builtin_bit_cast(bf16x8, bv);
-#pragma unroll
-            for (int r = 0; r < MT; r++)
-              acc[r][cc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(half ? fb[r] : fa[r], bfr, acc[r][cc], 0, 0, 0);
-          }
-        }
-      }
-      if (more) store_x(buf ^ 1);
-      __syncthreads();
-    }
-  }
-
-  // D layout: lane holds rows 4g..4g+3 of column li of each 16x16 tile.
-#pragma unroll
-  for (int r = 0; r < MT; r++) {
-    const int m = m_wave + 16 * r + 4 * g;
-#pragma unroll
-    for (int cc = 0; cc < NT; cc++) {
-      const int n = n0 + 16 * cc + li;
-      if (a.splits > 1) {
-        if (n < a.N && m < a.M) {
-          float* p = a.part + ((size_t)ks * a.N + n) * a.M + m;
-          if (m + 3 < a.M && (a.M & 3) == 0) *reinterpret_cast<f32x4*>(p) = acc[r][cc];
-          else
-            for (int i = 0; i < 4 && m + i < a.M; i++) p[i] = acc[r][cc][i];
-        }
-      } else {
-        write_out4(a, a.epi, n, m, acc[r][cc]);
-      }
+    for (int t = 0; t < 8; t++) {
+      const __bf16 b = (__bf16)w[t];
+      hi[s][t] = b;
+      if (precise) lo[s][t] = (__bf16)(w[t] - (float)b);
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Exact-weight variant for multi-token LlamaModel.Forward spans.
+// Pipelined 32x32 tile kernel: raw W bytes and the x tile stream into an
+// S-stage LDS ring through direct global->LDS loads (global_load_lds_dwordx4,
+// no registers held), so S-1 chunks of 64 K are in flight while one is
+// computed.  A workgroup waits only for the chunk it needs
+// (s_waitcnt vmcnt(n) + a bare s_barrier), not for the whole queue.
 //
-// The single-pass kernel rounds both operands to bf16 (2^-9 each), which
-// leaves ~3e-3 relative noise per projection; over a 22-layer stack that moves
-// logits by ~1e-2 and can flip greedy near-ties.  Here the weights enter the
-// MFMA exactly — (q - 8) is a small integer — and x as two bf16 planes
-// hi + lo (~2^-17 relative): per Q4_0 block and output
-//   p = sum_k x_hi[k] (q_k - 8) + sum_k x_lo[k] (q_k - 8)    (two MFMAs, fp32)
-//   acc += d * p
-// The operands are swapped relative to the single-pass kernel (x is A, W is
-// B) so that a lane's four outputs (columns 4g..4g+3 of the x rows, one W row
-// m = li) all need the block scale d of the row that lane itself loaded.
+// Per chunk (one 36-byte Q4_0 unit per W row) lane half h of row li takes
+// block h of the unit: its 8 k of MFMA step s are the low (s < 2) or high
+// nibbles of qs[8(s&1) .. +7], i.e. k = 32h + 8s .. +7 of the chunk.  The
+// x fragment of the same lane reads exactly those k, so the K order inside a
+// chunk is permuted consistently for both operands.
+// LDS layout per stage: x planes [BN rows][8 x 16 B] with the 16-byte chunk
+// of logical index c of row r stored at c ^ ((r >> 1) & 7) (reads of 32 rows
+// stay 2-way per bank), then W [BM rows][48 B] holding unit bytes [0,16),
+// [16,32) and [20,36).
+// A wave owns 32*TM W rows x 32*TN columns; the 4 waves stack along M and
+// share the x tile.  PRECISE (spans of the forward pass) runs three MFMAs per
+// step, Wh*xh + Wh*xl + Wl*xh, with W = Wh + Wl exact and x = xh + xl to
+// ~2^-17; the dropped Wl*xl term is below 2^-16 relative.  Output layout of a
+// 32x32 tile: lane l, accumulator v holds row 8*(v/4) + 4*(l/32) + v%4,
+// column l%32.
 // ---------------------------------------------------------------------------
-
-// Exact (q - 8) of 8 nibbles as bf16.
-__device__ __forceinline__ bf16x8 qm8(uint32_t q0, uint32_t q1) {
-  bf16x8 r;
-  r[0] = (__bf16)(cn_ubyte<0>(q0) - 8.0f);
-  r[1] = (__bf16)(cn_ubyte<1>(q0) - 8.0f);
-  r[2] = (__bf16)(cn_ubyte<2>(q0) - 8.0f);
-  r[3] = (__bf16)(cn_ubyte<3>(q0) - 8.0f);
-  r[4] = (__bf16)(cn_ubyte<0>(q1) - 8.0f);
-  r[5] = (__bf16)(cn_ubyte<1>(q1) - 8.0f);
-  r[6] = (__bf16)(cn_ubyte<2>(q1) - 8.0f);
-  r[7] = (__bf16)(cn_ubyte<3>(q1) - 8.0f);
-  return r;
+// 16 bytes from global memory straight into LDS: lane i of the wave writes
+// lds_wave_base + 16*i (lds_wave_base must be the same for the whole wave).
+// The builtin exists only for the device; the host pass sees an empty body.
+__device__ __forceinline__ void lds_dma16(const void* g, void* lds_wave_base) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0, 0);
+#endif
 }
 
-__device__ __forceinline__ void exact_unit(const UnitRegs& u, int nshift, bf16x8& fa, bf16x8& fb, float& da,
-                                           float& db) {
-  const uint32_t qa0 = (__builtin_amdgcn_alignbyte(u.a2, u.a1, 2) >> nshift) & 0x0F0F0F0Fu;
-  const uint32_t qa1 = (__builtin_amdgcn_alignbyte(u.a3, u.a2, 2) >> nshift) & 0x0F0F0F0Fu;
-  const uint32_t qb0 = (u.b1 >> nshift) & 0x0F0F0F0Fu;
-  const uint32_t qb1 = (u.b2 >> nshift) & 0x0F0F0F0Fu;
-  fa = qm8(qa0, qa1);
-  fb = qm8(qb0, qb1);
-  da = cn_h2f(u.a0);
-  db = cn_h2f(u.b0 >> 16);
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int MT, int NT, int KC>
-__global__ __launch_bounds__(CN_BLOCK) void gemm_q4_0_x2_kernel(GemmArgs a) {
-  constexpr int BN = 16 * NT;
-  constexpr int XS = KC + 8;
-  constexpr int XV = BN * KC / 8;
-  constexpr int XR = (XV + CN_BLOCK - 1) / CN_BLOCK;
-  constexpr int UPC = KC / 64;
-  __shared__ __attribute__((aligned(16))) uint16_t xs[2][2][BN * XS];  // [buffer][hi, lo]
+__device__ __forceinline__ void wg_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <bool PRECISE, int TM, int TN, int S>
+struct PipeCfg {
+  static constexpr int PL = PRECISE ? 2 : 1;
+  static constexpr int BM = 128 * TM, BN = 32 * TN;
+  static constexpr int XB = BN * 128;          // bytes per x plane per stage
+  static constexpr int WB = BM * 48;           // bytes of W per stage
+  static constexpr int STAGE = PL * XB + WB;
+  static constexpr int XPW = BN * 8 / 4;       // x pieces (16 B) per wave per plane
+  static constexpr int XI = XPW / 64;
+  static constexpr int WPW = BM * 3 / 4;       // W pieces per wave
+  static constexpr int WI = (WPW + 63) / 64;
+  static constexpr int VPS = PL * XI + WI;     // vector-memory instructions per stage per wave
+  static_assert(XPW % 64 == 0, "x pieces per wave must fill whole instructions");
+};
+
+template <bool PRECISE, int TM, int TN, int S>
+__global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
+  using C = PipeCfg<PRECISE, TM, TN, S>;
+  extern __shared__ __attribute__((aligned(16))) char lds[];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int g = lane >> 4, li = lane & 15;
-  const int h = g & 1, nshift = (g >> 1) * 4;
+  const int h = lane >> 5, li = lane & 31;
 
-  const int n_nt = (a.N + BN - 1) / BN;
+  const int n_nt = (a.N + C::BN - 1) / C::BN;
   int bid = blockIdx.x;
   const int ks = bid % a.splits;
   bid /= a.splits;
   const int nt = bid % n_nt;
   const int mt = bid / n_nt;
-  const int m_wave = mt * 64 * MT + wave * 16 * MT;
-  const int n0 = nt * BN;
+  const int m0 = mt * C::BM;
+  const int n0 = nt * C::BN;
+  const int m_wave = m0 + wave * 32 * TM;
 
-  const int nchunks = a.K / KC;
+  const int nchunks = a.K / 64;
   const int cps = (nchunks + a.splits - 1) / a.splits;
   const int c_begin = ks * cps;
   const int c_end = min(nchunks, c_begin + cps);
-
   const int row_dw = a.K / 64 * Q4_0_UNIT_DW;
-  const uint32_t* wrow[MT];
-#pragma unroll
-  for (int r = 0; r < MT; r++) wrow[r] = gemm_row_ptr(a, m_wave + 16 * r + li, row_dw);
 
-  f32x4 acc[MT][NT];
+  // Per-lane source pointers of the stage loads (chunk-independent parts).
+  const uint16_t* xsrc[C::PL][C::XI];
 #pragma unroll
-  for (int r = 0; r < MT; r++)
+  for (int p = 0; p < C::PL; p++)
 #pragma unroll
-    for (int c = 0; c < NT; c++) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < C::XI; j++) {
+      const int piece = wave * C::XPW + 64 * j + lane;
+      const int row = piece >> 3, ch = piece & 7;
+      const int n = min(n0 + row, a.N - 1);
+      const int logical = ch ^ ((row >> 1) & 7);
+      xsrc[p][j] = (p ? a.xb_lo : a.xb) + (size_t)n * a.K + 8 * logical;
+    }
+  const char* wsrc[C::WI];
+  bool wact[C::WI];
+#pragma unroll
+  for (int j = 0; j < C::WI; j++) {
+    const int q = 64 * j + lane;
+    wact[j] = q < C::WPW;
+    const int piece = wave * C::WPW + (wact[j] ? q : 0);
+    const int row = piece / 3, part = piece % 3;
+    const int vr = min(m0 + row, a.M - 1);
+    // pieces at unit bytes 0, 16 and 20: exactly the 36 bytes, no read past the unit
+    wsrc[j] = reinterpret_cast<const char*>(gemm_row_ptr(a, vr, row_dw)) + (part == 2 ? 20 : 16 * part);
+  }
+
+  auto issue = [&](int c, int slot) {
+    char* st = lds + slot * C::STAGE;
+#pragma unroll
+    for (int p = 0; p < C::PL; p++)
+#pragma unroll
+      for (int j = 0; j < C::XI; j++)
+        lds_dma16(xsrc[p][j] + c * 64, st + p * C::XB + (wave * C::XPW + 64 * j) * 16);
+#pragma unroll
+    for (int j = 0; j < C::WI; j++)
+      if (wact[j])
+        lds_dma16(wsrc[j] + c * 36, st + C::PL * C::XB + (wave * C::WPW + 64 * j) * 16);
+    asm volatile("" ::: "memory");
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int r = 0; r < TM; r++)
+#pragma unroll
+    for (int cc = 0; cc < TN; cc++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) acc[r][cc][v] = 0.f;
 
   if (c_begin < c_end) {
-    uint4 xr[2][XR];
-    UnitRegs wr[MT][UPC];
-
-    auto load_x = [&](int c) {
-      const int k0 = c * KC;
-#pragma unroll
-      for (int j = 0; j < XR; j++) {
-        const int i = threadIdx.x + CN_BLOCK * j;
-        const int n = i / (KC / 8), k8 = i % (KC / 8);
-        uint4 vh = make_uint4(0u, 0u, 0u, 0u), vl = vh;
-        if (i < XV && n0 + n < a.N) {
-          const size_t off = (size_t)(n0 + n) * a.K + k0 + 8 * k8;
-          vh = *reinterpret_cast<const uint4*>(a.xb + off);
-          vl = *reinterpret_cast<const uint4*>(a.xb_lo + off);
-        }
-        xr[0][j] = vh;
-        xr[1][j] = vl;
+    auto slot_of = [&](int c) { return lds + ((c - c_begin) % S) * C::STAGE; };
+    // The 5 dwords of a lane's W block from a stage slot: the slot holds unit
+    // bytes [0,16) [16,32) [20,36): block A's d + qs at dwords 0..4, block B's
+    // d in the high half of dword 4 and its qs at dwords 8..11.
+    auto wraw = [&](const char* st, int r, uint32_t (&w)[5]) {
+      const uint32_t* wb = reinterpret_cast<const uint32_t*>(st + C::PL * C::XB + (wave * 32 * TM + 32 * r + li) * 48);
+      w[0] = wb[8 * h];
+      w[1] = wb[8 * h + 1];
+      w[2] = wb[8 * h + 2];
+      w[3] = wb[8 * h + 3];
+      w[4] = wb[4];
+    };
+    // half 0: steps 0 and 2 (low/high nibbles of qs[0..7]); half 1: steps 1 and 3
+    auto deq = [&](const uint32_t (&w)[5], int half, bf16x8 (&fh)[4], bf16x8 (&fl)[4]) {
+      const uint32_t sh = h ? 0u : 2u;
+      const float d = cn_h2f(h ? (w[4] >> 16) : w[0]);
+      const uint32_t qa = __builtin_amdgcn_alignbyte(half ? w[3] : w[1], half ? w[2] : w[0], sh);
+      const uint32_t qb = __builtin_amdgcn_alignbyte(half ? w[4] : w[2], half ? w[3] : w[1], sh);
+      bf16x8 th[2], tl[2];
+      dequant_w16(qa, qb, d, PRECISE, th, tl);
+      fh[half] = th[0];
+      fh[half + 2] = th[1];
+      if constexpr (PRECISE) {
+        fl[half] = tl[0];
+        fl[half + 2] = tl[1];
       }
     };
-    auto store_x = [&](int buf) {
-#pragma unroll
-      for (int j = 0; j < XR; j++) {
-        const int i = threadIdx.x + CN_BLOCK * j;
-        if (i < XV) {
-          const int n = i / (KC / 8), k8 = i % (KC / 8);
-          *reinterpret_cast<uint4*>(&xs[buf][0][n * XS + 8 * k8]) = xr[0][j];
-          *reinterpret_cast<uint4*>(&xs[buf][1][n * XS + 8 * k8]) = xr[1][j];
-        }
+    // Waits until stage t has landed, given that stages up to `issued` are in flight.
+    auto wait_stage = [&](int t, int issued) {
+      const int later = issued - t;
+      if constexpr (S >= 4) {
+        if (later >= 2) vm_wait<2 * C::VPS>();
+        else if (later == 1) vm_wait<C::VPS>();
+        else vm_wait<0>();
+      } else {
+        if (later >= 1) vm_wait<C::VPS>();
+        else vm_wait<0>();
       }
     };
-    auto load_w = [&](int c) {
-#pragma unroll
-      for (int r = 0; r < MT; r++)
-#pragma unroll
-        for (int u = 0; u < UPC; u++)
-          load_unit(wrow[r] ? wrow[r] + (size_t)(c * UPC + u) * Q4_0_UNIT_DW : nullptr, h, wr[r][u]);
-    };
 
-    load_x(c_begin);
-    load_w(c_begin);
-    store_x(0);
-    __syncthreads();
+    int issued = c_begin - 1;
+#pragma unroll
+    for (int i = 0; i < S - 1; i++)
+      if (c_begin + i < c_end) {
+        issue(c_begin + i, i);
+        issued = c_begin + i;
+      }
+    wait_stage(c_begin, issued);
+    wg_barrier();
+    bf16x8 wh[TM][4], wl[TM][4];
+#pragma unroll
+    for (int r = 0; r < TM; r++) {
+      uint32_t w[5];
+      wraw(slot_of(c_begin), r, w);
+      deq(w, 0, wh[r], wl[r]);
+      deq(w, 1, wh[r], wl[r]);
+    }
 
     for (int c = c_begin; c < c_end; c++) {
-      const int buf = (c - c_begin) & 1;
-      UnitRegs cur[MT][UPC];
-#pragma unroll
-      for (int r = 0; r < MT; r++)
-#pragma unroll
-        for (int u = 0; u < UPC; u++) cur[r][u] = wr[r][u];
-      const bool more = c + 1 < c_end;
-      if (more) {
-        load_x(c + 1);
-        load_w(c + 1);
+      const bool has_next = c + 1 < c_end;
+      // Stage c+1 (whose W is dequantized during this chunk) must have landed,
+      // and every wave must be done with chunk c-1 before its slot is reused.
+      wait_stage(has_next ? c + 1 : c, issued);
+      wg_barrier();
+      if (c + S - 1 < c_end) {
+        issue(c + S - 1, (c + S - 1 - c_begin) % S);
+        issued = c + S - 1;
       }
+      // Unconditional (branch-free, so it interleaves with the MFMAs): on the
+      // last chunk this reads a stale slot whose result is never used.
+      uint32_t nw[TM][5];
 #pragma unroll
-      for (int u = 0; u < UPC; u++) {
-        bf16x8 fa[MT], fb[MT];
-        float da[MT], db[MT];
+      for (int r = 0; r < TM; r++) wraw(slot_of(c + 1), r, nw[r]);
+      bf16x8 nwh[TM][4], nwl[TM][4];
+
+      const char* st = slot_of(c);
+      bf16x8 xh[2][TN], xl[2][TN];
+      auto load_x = [&](int s, int b) {
 #pragma unroll
-        for (int r = 0; r < MT; r++) exact_unit(cur[r][u], nshift, fa[r], fb[r], da[r], db[r]);
+        for (int cc = 0; cc < TN; cc++) {
+          const int xrow = 32 * cc + li;
+          const int phys = (4 * h + s) ^ ((xrow >> 1) & 7);
+          const char* xp = st + xrow * 128 + phys * 16;
+          xh[b][cc] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(xp));
+          if constexpr (PRECISE) xl[b][cc] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(xp + C::XB));
+        }
+      };
+      load_x(0, 0);
 #pragma unroll
-        for (int half = 0; half < 2; half++) {
-          const int kofs = u * 64 + half * 32 + 8 * g;
+      for (int s = 0; s < 4; s++) {
+        if (s < 3) load_x(s + 1, (s + 1) & 1);  // next step's fragments in flight during this step
+        // one pass over all accumulators per product, so consecutive MFMAs
+        // never wait on each other's result
 #pragma unroll
-          for (int cc = 0; cc < NT; cc++) {
-            const int xo = (16 * cc + li) * XS + kofs;
-            const bf16x8 xh = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&xs[buf][0][xo]));
-            const bf16x8 xl = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&xs[buf][1][xo]));
+        for (int cc = 0; cc < TN; cc++)
 #pragma unroll
-            for (int r = 0; r < MT; r++) {
-              const bf16x8 wf = half ? fb[r] : fa[r];
-              f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wf, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-              p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wf, p, 0, 0, 0);
-              const float d = half ? db[r] : da[r];
-              acc[r][cc] += d * p;
-            }
-          }
+          for (int r = 0; r < TM; r++)
+            acc[r][cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wh[r][s], xh[s & 1][cc], acc[r][cc], 0, 0, 0);
+        if constexpr (PRECISE) {
+#pragma unroll
+          for (int cc = 0; cc < TN; cc++)
+#pragma unroll
+            for (int r = 0; r < TM; r++)
+              acc[r][cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wh[r][s], xl[s & 1][cc], acc[r][cc], 0, 0, 0);
+#pragma unroll
+          for (int cc = 0; cc < TN; cc++)
+#pragma unroll
+            for (int r = 0; r < TM; r++)
+              acc[r][cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wl[r][s], xh[s & 1][cc], acc[r][cc], 0, 0, 0);
+        }
+        // the next chunk's W is dequantized while these MFMAs run
+        if (s == 0 || s == 2) {
+#pragma unroll
+          for (int r = 0; r < TM; r++) deq(nw[r], s >> 1, nwh[r], nwl[r]);
         }
       }
-      if (more) store_x(buf ^ 1);
-      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < TM; r++)
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+          wh[r][s] = nwh[r][s];
+          if constexpr (PRECISE) wl[r][s] = nwl[r][s];
+        }
     }
   }
 
-  // D layout: lane holds x rows 4g..4g+3 of tile column li = W row m.
 #pragma unroll
-  for (int r = 0; r < MT; r++) {
-    const int m = m_wave + 16 * r + li;
+  for (int r = 0; r < TM; r++) {
 #pragma unroll
-    for (int cc = 0; cc < NT; cc++) {
+    for (int cc = 0; cc < TN; cc++) {
+      const int n = n0 + 32 * cc + li;
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int n = n0 + 16 * cc + 4 * g + i;
-        const float v = acc[r][cc][i];
+      for (int v4 = 0; v4 < 4; v4++) {
+        const int m = m_wave + 32 * r + 8 * v4 + 4 * h;
+        const f32x4 v = {acc[r][cc][4 * v4], acc[r][cc][4 * v4 + 1], acc[r][cc][4 * v4 + 2], acc[r][cc][4 * v4 + 3]};
         if (a.splits > 1) {
-          if (n < a.N && m < a.M) a.part[((size_t)ks * a.N + n) * a.M + m] = v;
-        } else if (a.epi == GEMV_EPI_SWIGLU) {
-          const float up = __shfl_xor(v, 1, CN_WAVE);  // row m+1 sits in lane li+1
-          if ((m & 1) == 0 && m + 1 < a.M && n < a.N) write_h(a, n, m >> 1, silu_mul(v, up));
-        } else if (n < a.N && m < a.M) {
-          float* y = a.y + (size_t)n * a.ldy + m;
-          *y = (a.epi == GEMV_EPI_ADD) ? *y + v : v;
+          if (n < a.N && m < a.M) {
+            float* p = a.part + ((size_t)ks * a.N + n) * a.M + m;
+            if (m + 3 < a.M && (a.M & 3) == 0) *reinterpret_cast<f32x4*>(p) = v;
+            else
+              for (int i = 0; i < 4 && m + i < a.M; i++) p[i] = v[i];
+          }
+        } else {
+          write_out4(a, a.epi, n, m, v);
         }
       }
     }
   }
+}
+
+template <bool PRECISE, int TM, int TN, int S>
+constexpr size_t gemm_p_lds() {
+  return (size_t)S * PipeCfg<PRECISE, TM, TN, S>::STAGE;
 }
 
 // Sums the K-split partials [splits][N][M] and applies the epilogue; one
@@ -548,68 +486,54 @@ __global__ __launch_bounds__(CN_BLOCK) void rmsnorm_bf16_kernel(const float* __r
   }
 }
 
+// Column tile by batch size (32, 64 or 128 columns per workgroup, 128 rows);
+// K is split while the tile grid covers fewer than two workgroups per CU,
+// keeping at least 8 chunks of 64 per split so the LDS ring stays full.
 struct GemmShape {
-  int mt, nt, kc, splits;
+  int tn, splits;
 };
 
-GemmShape pick_gemm(int M, int N, int K, int num_cus, bool precise) {
+GemmShape pick_gemm(int M, int N, int K, int num_cus) {
   GemmShape s;
-  // Column tile: up to 128 columns so each dequantized W operand feeds NT MFMAs.
-  s.nt = N <= 16 ? 1 : (N <= 32 ? 2 : (N <= 64 ? 4 : 8));
-  s.mt = (N >= 256 && M >= 128 * num_cus / 2) ? 2 : 1;
-  // K chunk staged in LDS per step; the two-plane variant halves it at 128
-  // columns to stay within 80 KB of LDS.
-  s.kc = (K % 128 == 0 && !(precise && s.nt == 8)) ? 128 : 64;
-  const int bm = 64 * s.mt, bn = 16 * s.nt;
-  const long long tiles = (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
-  const int nchunks = K / s.kc;
+  s.tn = N <= 32 ? 1 : (N <= 64 ? 2 : 4);
+  const long long tiles = (long long)((M + 127) / 128) * ((N + 32 * s.tn - 1) / (32 * s.tn));
+  const int nchunks = K / 64;
   s.splits = 1;
-  // Split K until the grid covers the chip twice, keeping >= 4 chunks per split.
-  while (tiles * s.splits < 2LL * num_cus && nchunks / (s.splits * 2) >= 4 && s.splits < 16) s.splits *= 2;
+  while (tiles * s.splits < 2LL * num_cus && nchunks / (s.splits * 2) >= 8 && s.splits < 16) s.splits *= 2;
   return s;
 }
 
-template <bool PRECISE, int MT, int NT, int KC>
-hipError_t launch_gemm_t(const GemmArgs& a, int grid, hipStream_t st) {
-  if constexpr (PRECISE)
-    hipLaunchKernelGGL((gemm_q4_0_x2_kernel<MT, NT, KC>), dim3(grid), dim3(CN_BLOCK), 0, st, a);
-  else
-    hipLaunchKernelGGL((gemm_q4_0_kernel<MT, NT, KC>), dim3(grid), dim3(CN_BLOCK), 0, st, a);
+constexpr int kStages = 3;
+
+template <bool PRECISE, int TN>
+hipError_t launch_p(const GemmArgs& a, int grid, hipStream_t st) {
+  constexpr size_t lds = gemm_p_lds<PRECISE, 1, TN, kStages>();
+  // Dynamic LDS above 64 KB must be allowed per kernel; every caller sets the
+  // same value, so a race on the flag is harmless.
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_p_kernel<PRECISE, 1, TN, kStages>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((gemm_p_kernel<PRECISE, 1, TN, kStages>), dim3(grid), dim3(CN_BLOCK), lds, st, a);
   return hipGetLastError();
 }
 
-template <bool PRECISE, int MT, int NT>
-hipError_t launch_gemm_kc(const GemmArgs& a, int kc, int grid, hipStream_t st) {
-  if constexpr (PRECISE && NT == 8) {
-    return launch_gemm_t<PRECISE, MT, NT, 64>(a, grid, st);
-  } else {
-    if (kc == 128) return launch_gemm_t<PRECISE, MT, NT, 128>(a, grid, st);
-    return launch_gemm_t<PRECISE, MT, NT, 64>(a, grid, st);
-  }
-}
-
-template <bool PRECISE, int MT>
-hipError_t launch_gemm_nt(const GemmArgs& a, int nt, int kc, int grid, hipStream_t st) {
-  switch (nt) {
-    case 1: return launch_gemm_kc<PRECISE, MT, 1>(a, kc, grid, st);
-    case 2: return launch_gemm_kc<PRECISE, MT, 2>(a, kc, grid, st);
-    case 4: return launch_gemm_kc<PRECISE, MT, 4>(a, kc, grid, st);
-    default: return launch_gemm_kc<PRECISE, MT, 8>(a, kc, grid, st);
-  }
-}
-
 template <bool PRECISE>
-hipError_t launch_gemm(const GemmArgs& a, const GemmShape& s, int grid, hipStream_t st) {
-  return s.mt == 2 ? launch_gemm_nt<PRECISE, 2>(a, s.nt, s.kc, grid, st)
-                   : launch_gemm_nt<PRECISE, 1>(a, s.nt, s.kc, grid, st);
+hipError_t launch_tn(const GemmArgs& a, int tn, int grid, hipStream_t st) {
+  if (tn == 1) return launch_p<PRECISE, 1>(a, grid, st);
+  if (tn == 2) return launch_p<PRECISE, 2>(a, grid, st);
+  return launch_p<PRECISE, 4>(a, grid, st);
 }
 
 }  // namespace
 
 bool gemm_supports(int qtype, int K) { return qtype == 2 && K > 0 && K % 64 == 0; }
 
-size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool precise) {
-  const GemmShape s = pick_gemm(M, N, K, num_cus, precise);
+size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool /*precise*/) {
+  const GemmShape s = pick_gemm(M, N, K, num_cus);
   return s.splits > 1 ? (size_t)s.splits * N * M * sizeof(float) : 0;
 }
 
@@ -617,14 +541,13 @@ hipError_t gemm_launch(const GemmArgs& a_in, int num_cus, hipStream_t st) {
   if (!gemm_supports(a_in.qtype, a_in.K) || a_in.M <= 0 || a_in.N <= 0) return hipErrorInvalidValue;
   const bool precise = a_in.precise != 0;
   if (precise && !a_in.xb_lo) return hipErrorInvalidValue;
-  const GemmShape s = pick_gemm(a_in.M, a_in.N, a_in.K, num_cus, precise);
+  const GemmShape s = pick_gemm(a_in.M, a_in.N, a_in.K, num_cus);
   GemmArgs a = a_in;
   a.splits = s.splits;
   if (s.splits > 1 && !a.part) return hipErrorInvalidValue;
-  const int bm = 64 * s.mt, bn = 16 * s.nt;
-  const long long grid = (long long)((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn) * s.splits;
+  const long long grid = (long long)((a.M + 127) / 128) * ((a.N + 32 * s.tn - 1) / (32 * s.tn)) * s.splits;
   if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
-  hipError_t e = precise ? launch_gemm<true>(a, s, (int)grid, st) : launch_gemm<false>(a, s, (int)grid, st);
+  hipError_t e = precise ? launch_tn<true>(a, s.tn, (int)grid, st) : launch_tn<false>(a, s.tn, (int)grid, st);
   if (e != hipSuccess || s.splits == 1) return e;
   const long long work = (long long)((a.M + 3) / 4) * a.N;
   hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((work + CN_BLOCK - 1) / CN_BLOCK)), dim3(CN_BLOCK), 0, st, a);
