@@ -207,10 +207,12 @@ int chatnet_create(const chatnet_config* cfg, int device, chatnet_model** out) {
   m->kv_elt = c.kv_dtype == CHATNET_KV_F16 ? 2 : 4;
   m->layers.resize(c.n_layers);
   const size_t kv_bytes = (size_t)c.n_layers * c.context_length * m->kv_dim * m->kv_elt;
-  // Attention splits: about one workgroup per CU over the KV heads (at most 16
-  // splits); each workgroup leaves one partial per query head.
+  // Attention splits: up to two workgroups per CU over the KV heads (at most 64
+  // splits); the kernels use only as many as hold 4 or more positions at the
+  // current position.  Each workgroup leaves one partial per query head.
   int splits = 1;
-  while (splits < 16 && splits * 2 * c.n_kv_heads <= m->num_cus && splits * 2 <= c.context_length) splits *= 2;
+  while (splits < 64 && splits * 2 * c.n_kv_heads <= 2 * m->num_cus && splits * 2 * 4 <= c.context_length)
+    splits *= 2;
   m->attn_splits = splits;
   const size_t attn_slots = (size_t)c.n_heads * splits;
   auto cleanup = [m]() { chatnet_destroy(m); };

@@ -28,6 +28,18 @@ __global__ __launch_bounds__(CN_BLOCK) void embed_kernel(const void* emb, int ty
   }
 }
 
+// Fewest positions a decode-attention split takes: one per wave.  Decode
+// attention is latency-bound, so short contexts still spread over many
+// workgroups; the cap on splits bounds the merge.
+constexpr int kAttnMinChunk = 4;
+
+// Splits that carry positions at sequence length seq: min(splits, ceil(seq / kAttnMinChunk)).
+// The decode kernel and the merge both derive it from the device-side position,
+// so one captured decode step serves every position.
+__device__ __forceinline__ int attn_active_splits(int splits, int seq) {
+  return min(splits, (seq + kAttnMinChunk - 1) / kAttnMinChunk);
+}
+
 template <bool F16>
 __device__ __forceinline__ float kv_load(const void* base, size_t idx) {
   if constexpr (F16) return (float)reinterpret_cast<const _Float16*>(base)[idx];
@@ -55,7 +67,11 @@ __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
   const int split = blockIdx.x % a.splits;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int seq = *a.pos + 1;
-  const int chunk = (seq + a.splits - 1) / a.splits;
+  // Active splits for this position: at least kAttnMinChunk positions each, so
+  // short contexts use few workgroups and long ones spread over many.
+  const int s_eff = attn_active_splits(a.splits, seq);
+  if (split >= s_eff) return;  // uniform over the workgroup, before any barrier
+  const int chunk = (seq + s_eff - 1) / s_eff;
   const int p0 = split * chunk;
   const int p1 = min(seq, p0 + chunk);
   const size_t koff = (size_t)kvh * HD;
@@ -153,34 +169,44 @@ __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
   }
 }
 
-// Merges the split partials of one query head (grid = n_heads, block = HD):
+// Merges the active split partials of one query head (grid = n_heads, block = HD):
 //   M = max_c m_c,  L = sum_c l_c e^(m_c - M),  out = sum_c o_c e^(m_c - M) / L,
-// empty splits (l_c = 0) contributing nothing.  All loads are issued in one
-// round (at most SMAX splits).
-template <int HD, int SMAX>
+// empty splits (l_c = 0) contributing nothing.  Partials are read in rounds of
+// R, all loads of a round in flight together, with the running (M, L, acc)
+// rescaled when a round raises the maximum.
+template <int HD>
 __global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs a) {
+  constexpr int R = 16;
   const int h = blockIdx.x, d = threadIdx.x;
+  const int s_eff = attn_active_splits(a.splits, *a.pos + 1);
   const size_t base = (size_t)h * a.splits;
-  float mc[SMAX], lc[SMAX], oc[SMAX];
+  float M = -INFINITY, L = 0.f, acc = 0.f;
+  for (int c0 = 0; c0 < s_eff; c0 += R) {
+    float mc[R], lc[R], oc[R];
 #pragma unroll
-  for (int c = 0; c < SMAX; c++) {
-    const bool on = c < a.splits;
-    mc[c] = on ? a.part_ml[2 * (base + c)] : 0.f;
-    lc[c] = on ? a.part_ml[2 * (base + c) + 1] : 0.f;
-    oc[c] = on ? a.part_o[(base + c) * HD + d] : 0.f;
-  }
-  float M = -INFINITY;
-#pragma unroll
-  for (int c = 0; c < SMAX; c++)
-    if (lc[c] > 0.f) M = fmaxf(M, mc[c]);
-  float L = 0.f, acc = 0.f;
-#pragma unroll
-  for (int c = 0; c < SMAX; c++) {
-    if (lc[c] > 0.f) {
-      const float f = expf(mc[c] - M);
-      L += lc[c] * f;
-      acc += oc[c] * f;
+    for (int c = 0; c < R; c++) {
+      const bool on = c0 + c < s_eff;
+      mc[c] = on ? a.part_ml[2 * (base + c0 + c)] : 0.f;
+      lc[c] = on ? a.part_ml[2 * (base + c0 + c) + 1] : 0.f;
+      oc[c] = on ? a.part_o[(base + c0 + c) * HD + d] : 0.f;
     }
+    float Mn = M;
+#pragma unroll
+    for (int c = 0; c < R; c++)
+      if (lc[c] > 0.f) Mn = fmaxf(Mn, mc[c]);
+    if (Mn == -INFINITY) continue;  // nothing in this round or before it
+    const float r = (M == -INFINITY) ? 0.f : expf(M - Mn);
+    L *= r;
+    acc *= r;
+#pragma unroll
+    for (int c = 0; c < R; c++) {
+      if (lc[c] > 0.f) {
+        const float f = expf(mc[c] - Mn);
+        L += lc[c] * f;
+        acc += oc[c] * f;
+      }
+    }
+    M = Mn;
   }
   a.out[(size_t)h * HD + d] = acc / L;
 }
@@ -245,7 +271,7 @@ hipError_t attn_launch_t(const AttnArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((attn_decode_kernel<HD, F16, 1>), dim3(n_kv * a.splits), dim3(CN_BLOCK), 0, st, a);
   else
     hipLaunchKernelGGL((attn_decode_kernel<HD, F16, 8>), dim3(n_kv * a.splits), dim3(CN_BLOCK), 0, st, a);
-  hipLaunchKernelGGL((attn_merge_kernel<HD, 16>), dim3(a.n_heads), dim3(HD), 0, st, a);
+  hipLaunchKernelGGL((attn_merge_kernel<HD>), dim3(a.n_heads), dim3(HD), 0, st, a);
   return hipGetLastError();
 }
 
@@ -259,7 +285,7 @@ hipError_t embed_launch(const void* emb, int type, int dim, const int* tok, floa
 }
 
 hipError_t attn_decode_launch(const AttnArgs& a, hipStream_t st) {
-  if (a.splits < 1 || a.splits > 16) return hipErrorInvalidValue;
+  if (a.splits < 1 || a.splits > 64) return hipErrorInvalidValue;
   if (a.head_dim == 64) return a.kv_f16 ? attn_launch_t<64, true>(a, st) : attn_launch_t<64, false>(a, st);
   if (a.head_dim == 128) return a.kv_f16 ? attn_launch_t<128, true>(a, st) : attn_launch_t<128, false>(a, st);
   if (a.head_dim == 32) return a.kv_f16 ? attn_launch_t<32, true>(a, st) : attn_launch_t<32, false>(a, st);

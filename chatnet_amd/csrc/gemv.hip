@@ -474,8 +474,21 @@ __device__ __forceinline__ void rope_cs(int i, int pos, float dim_inv, float neg
   sincosf(theta, &s, &c);
 }
 
+// ADD: the residual rows an epilogue will update, loaded by the lane that
+// finishes them together with the weights of the same iteration, so the
+// epilogue does not wait on a load issued behind the next iteration's weights.
 template <int EPI, int RPW>
-__device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, const float* v) {
+__device__ __forceinline__ void load_residual(const GemvArgs& a, int vr0, int li, float (&res)[RPW]) {
+#pragma unroll
+  for (int i = 0; i < RPW; i++) {
+    const int vr = vr0 + i;
+    res[i] = (EPI == GEMV_EPI_ADD && li == 0 && vr < a.n_vrows) ? a.out[0][vr] : 0.f;
+  }
+}
+
+// pos: the device-side position (QKV), read at kernel start.
+template <int EPI, int RPW>
+__device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, const float* v, const float* res, int pos) {
 #pragma unroll
   for (int i = 0; i < RPW; i += 2) {
     const int vr = vr0 + i;
@@ -486,13 +499,12 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, const float
       a.out[0][r] = v[i];
       if (vr + 1 < a.n_vrows) a.out[0][r + 1] = v[i + 1];
     } else if constexpr (EPI == GEMV_EPI_ADD) {
-      a.out[0][r] += v[i];
-      if (vr + 1 < a.n_vrows) a.out[0][r + 1] += v[i + 1];
+      a.out[0][r] = res[i] + v[i];
+      if (vr + 1 < a.n_vrows) a.out[0][r + 1] = res[i + 1] + v[i + 1];
     } else if constexpr (EPI == GEMV_EPI_SWIGLU) {
       const float g = v[i], u = v[i + 1];
       a.out[0][r] = (g / (1.0f + expf(-g))) * u;
     } else {  // QKV
-      const int pos = *a.pos;
       float x0 = v[i], x1 = v[i + 1];
       if (seg < 2) {
         float c, s;
@@ -573,6 +585,8 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_kernel(GemvArgs a) {
   int it = blockIdx.x * (CN_BLOCK / CN_WAVE) + wave;
 
   uint32_t w[RPW][NU][T::NDW];
+  float res[RPW];
+  const int pos = EPI == GEMV_EPI_QKV ? *a.pos : 0;
 
   // ---- prologue: stage x (optionally RMS-normalised) into LDS ----
   if constexpr (QT == QT_Q4_0) {
@@ -583,6 +597,7 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_kernel(GemvArgs a) {
     stage_load<MAXT, NORM>(a.x, a.norm_w, K, st);
     // rows past n_vrows come back as zeros, so idle waves need no branch here
     issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
+    load_residual<EPI, RPW>(a, it * RW + sub * RPW, li, res);
     uint32_t* xd = reinterpret_cast<uint32_t*>(smem);
     float* xred = reinterpret_cast<float*>(smem) + (size_t)nunits * XD_UNIT_DW;
     stage_digitize<MAXT, NORM>(st, K, xd, xred);
@@ -605,19 +620,28 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_kernel(GemvArgs a) {
         }
       }
       const int cur = it;
+      float res_cur[RPW];
+#pragma unroll
+      for (int i = 0; i < RPW; i++) res_cur[i] = res[i];
       it += wstride;
-      if (it < n_iters) issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
+      if (it < n_iters) {
+        issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
+        load_residual<EPI, RPW>(a, it * RW + sub * RPW, li, res);
+      }
 #pragma unroll
       for (int i = 0; i < RPW; i++) {
 #pragma unroll
         for (int off = LPR / 2; off > 0; off >>= 1) acc[i] += __shfl_xor(acc[i], off, CN_WAVE);
         acc[i] *= rms;
       }
-      if (li == 0) epilogue<EPI, RPW>(a, cur * RW + sub * RPW, acc);
+      if (li == 0) epilogue<EPI, RPW>(a, cur * RW + sub * RPW, acc, res_cur, pos);
     }
     return;
   }
-  if (it < n_iters) issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
+  if (it < n_iters) {
+    issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
+    load_residual<EPI, RPW>(a, it * RW + sub * RPW, li, res);
+  }
   float rms = 1.0f;
   if (a.norm_w) {
     float ss = 0.f;
@@ -674,14 +698,20 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_kernel(GemvArgs a) {
       }
     }
     const int cur = it;
+    float res_cur[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) res_cur[i] = res[i];
     it += wstride;
-    if (it < n_iters) issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
+    if (it < n_iters) {
+      issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
+      load_residual<EPI, RPW>(a, it * RW + sub * RPW, li, res);
+    }
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
 #pragma unroll
       for (int off = LPR / 2; off > 0; off >>= 1) acc[i] += __shfl_xor(acc[i], off, CN_WAVE);
     }
-    if (li == 0) epilogue<EPI, RPW>(a, cur * RW + sub * RPW, acc);
+    if (li == 0) epilogue<EPI, RPW>(a, cur * RW + sub * RPW, acc, res_cur, pos);
   }
 }
 

@@ -109,7 +109,7 @@ struct AttnArgs {
   float scale;
   float* part_o;      // split partials: [n_heads][splits][head_dim]
   float* part_ml;     // [n_heads][splits][2] (max, sum)
-  int splits;         // position chunks processed in parallel (<= 16)
+  int splits;         // most position chunks processed in parallel (<= 64)
 };
 hipError_t attn_decode_launch(const AttnArgs& a, hipStream_t st);
 

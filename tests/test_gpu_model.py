@@ -195,3 +195,22 @@ def test_span_longer_than_batch_cap_matches_oracle_and_token_schedule(monkeypatc
     assert np.max(np.abs(h - r)) <= LOGIT_TOL
     o, margins = oracle.OracleLlama(cfg, ck).generate_greedy(list(toks), 16)
     compare_greedy(list(gt), o, margins)
+
+
+def test_long_context_decode_attention_matches_oracle():
+    """2000-token prompt, then greedy decode: the decode attention runs with up
+    to 64 position splits (63 active at 2000 positions, merged in rounds)."""
+    cfg = SPAN_SMALL.replace(context_length=2100)
+    ck = synth.llama_checkpoint(cfg, seed=35, mix="q4_0")
+    toks = synth.tokens(35, "prompt", 2000, cfg.vocab_size)
+    announce("decode attention: 2000-token context, 64 splits")
+    with HipLlamaModel(cfg, ck) as m:
+        m.forward(toks, 0)
+        gt = m.decode_greedy(8)
+        logits_g = m.get_logits()
+    o, margins = oracle.OracleLlama(cfg, ck).generate_greedy(list(toks), 8)
+    n = compare_greedy(list(gt), o, margins)
+    if n == 8:
+        # the 8th decode step forwarded the 8th token at position 2007
+        r = oracle.OracleLlama(cfg, ck).forward(list(toks) + list(o), 0)
+        assert np.max(np.abs(logits_g - r)) <= LOGIT_TOL
