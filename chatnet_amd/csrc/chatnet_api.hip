@@ -1,9 +1,10 @@
 // chatnet_api.hip — the C ABI of libchatnet_hip (declared in include/chatnet_hip.h).
 //
 // Host-side orchestration of the per-token schedule of LlamaModel.Forward
-// (src/ChatNet.Core/Models/Llama/LlamaModel.cs:93-238), five launches per layer:
+// (src/ChatNet.Core/Models/Llama/LlamaModel.cs:93-238), six launches per layer:
 //   1. QKV GEMV   : RMSNorm (fused prologue) -> Wq|Wk|Wv -> RoPE -> K/V cache write
-//   2. attention  : GQA decode attention over the cache
+//   2. attention  : GQA decode attention over the cache, split over positions,
+//                   then a merge of the splits
 //   3. O GEMV     : x += Wo * attn           (residual fused)
 //   4. gate/up    : RMSNorm -> Wg|Wu -> silu(g)*u
 //   5. down GEMV  : x += Wd * h              (residual fused)
@@ -112,6 +113,7 @@ struct chatnet_model {
   float* attn_part_o = nullptr;   // split partials of the decode attention
   float* attn_part_ml = nullptr;
   int attn_splits = 1;
+  float2* rope = nullptr;  // [context_length][head_dim/2] (cos, sin), filled at creation
   int* out_tokens = nullptr;
   int out_cap = 0;
   hipGraphExec_t graph = nullptr;
@@ -231,6 +233,7 @@ int chatnet_create(const chatnet_config* cfg, int device, chatnet_model** out) {
       {(void**)&m->state, sizeof(int) * 4},
       {(void**)&m->attn_part_o, sizeof(float) * attn_slots * c.head_dim},
       {(void**)&m->attn_part_ml, sizeof(float) * attn_slots * 2},
+      {(void**)&m->rope, sizeof(float2) * (size_t)c.context_length * (c.head_dim / 2)},
   };
   for (auto& a : allocs) {
     if (hipMalloc(a.p, a.n) != hipSuccess) {
@@ -243,6 +246,13 @@ int chatnet_create(const chatnet_config* cfg, int device, chatnet_model** out) {
       hipMemset(m->state, 0, sizeof(int) * 4) != hipSuccess) {
     cleanup();
     return fail(CHATNET_ERR_HIP, "hipMemset failed");
+  }
+  // RoPE angles of every position (TensorMath.cs:418-432), computed once.
+  if (rope_table_launch(m->rope, c.context_length, c.head_dim, 1.0f / (float)c.head_dim, -logf(c.rope_freq_base),
+                        m->stream) != hipSuccess ||
+      hipStreamSynchronize(m->stream) != hipSuccess) {
+    cleanup();
+    return fail(CHATNET_ERR_HIP, "RoPE table initialisation failed");
   }
   *out = m;
   g_err.clear();
@@ -262,7 +272,7 @@ void chatnet_destroy(chatnet_model* m) {
   }
   fr(m->kcache); fr(m->vcache); fr(m->x); fr(m->q); fr(m->att); fr(m->h); fr(m->logits);
   fr(m->state); fr(m->out_tokens);
-  fr(m->attn_part_o); fr(m->attn_part_ml);
+  fr(m->attn_part_o); fr(m->attn_part_ml); fr(m->rope);
   fr(m->sp_x); fr(m->sp_xb); fr(m->sp_hb); fr(m->sp_qkv); fr(m->sp_tok); fr(m->sp_part);
   if (m->stream) (void)hipStreamDestroy(m->stream);
   delete m;
@@ -380,8 +390,7 @@ GemvArgs base_args(const chatnet_model* m) {
   a.eps = m->cfg.rms_norm_eps;
   a.pos = m->state;
   a.head_dim = m->cfg.head_dim;
-  a.rope_dim_inv = 1.0f / (float)m->cfg.head_dim;
-  a.rope_neg_log_base = -logf(m->cfg.rope_freq_base);
+  a.rope = m->rope;
   a.kv_dim = m->kv_dim;
   a.kv_f16 = m->cfg.kv_dtype == CHATNET_KV_F16;
   return a;
@@ -615,8 +624,7 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position) {
       r.kv_dim = kvd;
       r.head_dim = c.head_dim;
       r.p0 = p0;
-      r.rope_dim_inv = 1.0f / (float)c.head_dim;
-      r.rope_neg_log_base = -logf(c.rope_freq_base);
+      r.rope = m->rope;
       r.kcache = kc;
       r.vcache = vc;
       r.kv_f16 = c.kv_dtype == CHATNET_KV_F16;

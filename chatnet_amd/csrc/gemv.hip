@@ -94,13 +94,14 @@ struct XStage<MAXT, false> {
 // Issues every load of the staged x before the caller issues its weight
 // loads: vector-memory counters retire in order, so loads issued after the
 // weight stream could not be consumed before the whole stream had landed.
-template <int MAXT, bool NORM>
+// BS threads stage the K/8 items, item t on thread t % BS.
+template <int MAXT, bool NORM, int BS>
 __device__ __forceinline__ void stage_load(const float* __restrict__ x, const float* __restrict__ norm_w, int K,
                                            XStage<MAXT, NORM>& st) {
   const int ntask = K >> 3;
 #pragma unroll
   for (int j = 0; j < MAXT; j++) {
-    const int t = threadIdx.x + CN_BLOCK * j;
+    const int t = threadIdx.x + BS * j;
     const int b = t >> 2, k = t & 3;
     float4 lo = make_float4(0.f, 0.f, 0.f, 0.f), hi = lo, glo = lo, ghi = lo;
     if (t < ntask) {
@@ -126,13 +127,13 @@ __device__ __forceinline__ void stage_load(const float* __restrict__ x, const fl
 // to every element; each wave leaves its share of sum x^2 in red[wave] for the
 // caller to combine after its __syncthreads().  The four items of a block sit
 // in adjacent lanes and share the block maximum through two xor-shuffles.
-template <int MAXT, bool NORM>
+template <int MAXT, bool NORM, int BS>
 __device__ __forceinline__ void stage_digitize(const XStage<MAXT, NORM>& st, int K, uint32_t* xd, float* red) {
   const int ntask = K >> 3;
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < MAXT; j++) {
-    const int t = threadIdx.x + CN_BLOCK * j;
+    const int t = threadIdx.x + BS * j;
     const bool on = t < ntask;
     const int b = t >> 2, k = t & 3;
     float v[8];
@@ -466,27 +467,41 @@ __device__ __forceinline__ void map_row(const GemvArgs& a, int vr, int& seg, int
   }
 }
 
-// RoPE angle of pair index i (even) at position pos, TensorMath.cs:418-432:
-//   theta = pos * exp(i * (1/hd) * (-ln base)).
-__device__ __forceinline__ void rope_cs(int i, int pos, float dim_inv, float neg_log_base,
-                                        float& c, float& s) {
-  const float theta = (float)pos * expf((float)i * dim_inv * neg_log_base);
-  sincosf(theta, &s, &c);
-}
-
-// ADD: the residual rows an epilogue will update, loaded by the lane that
-// finishes them together with the weights of the same iteration, so the
-// epilogue does not wait on a load issued behind the next iteration's weights.
+// What an epilogue reads besides the dot products, loaded by the lane that
+// finishes the rows together with the weights of the same iteration, so the
+// epilogue does not wait on a load issued behind the next iteration's weights:
+//   ADD: the residual rows;
+//   QKV: (cos, sin) of each q/k row pair at position pos from the RoPE table
+//        (TensorMath.ApplyRoPE's angle, TensorMath.cs:418-432), the pair index
+//        being the row's offset within its head.
 template <int EPI, int RPW>
-__device__ __forceinline__ void load_residual(const GemvArgs& a, int vr0, int li, float (&res)[RPW]) {
+__device__ __forceinline__ void load_residual(const GemvArgs& a, int vr0, int li, int pos, float (&res)[RPW]) {
 #pragma unroll
-  for (int i = 0; i < RPW; i++) {
-    const int vr = vr0 + i;
-    res[i] = (EPI == GEMV_EPI_ADD && li == 0 && vr < a.n_vrows) ? a.out[0][vr] : 0.f;
+  for (int i = 0; i < RPW; i++) res[i] = 0.f;
+  if (li != 0) return;
+  if constexpr (EPI == GEMV_EPI_ADD) {
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      const int vr = vr0 + i;
+      if (vr < a.n_vrows) res[i] = a.out[0][vr];
+    }
+  } else if constexpr (EPI == GEMV_EPI_QKV) {
+#pragma unroll
+    for (int i = 0; i < RPW; i += 2) {
+      const int vr = vr0 + i;
+      int seg, r;
+      map_row<EPI>(a, vr, seg, r);
+      if (vr < a.n_vrows && seg < 2) {
+        const float2 cs = a.rope[(size_t)pos * (a.head_dim / 2) + (r % a.head_dim) / 2];
+        res[i] = cs.x;
+        res[i + 1] = cs.y;
+      }
+    }
   }
 }
 
-// pos: the device-side position (QKV), read at kernel start.
+// pos: the device-side position (QKV), read at kernel start; res: what
+// load_residual fetched for these rows.
 template <int EPI, int RPW>
 __device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, const float* v, const float* res, int pos) {
 #pragma unroll
@@ -507,8 +522,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, const float
     } else {  // QKV
       float x0 = v[i], x1 = v[i + 1];
       if (seg < 2) {
-        float c, s;
-        rope_cs(r % a.head_dim, pos, a.rope_dim_inv, a.rope_neg_log_base, c, s);
+        const float c = res[i], s = res[i + 1];
         const float y0 = x0 * c - x1 * s;
         const float y1 = x0 * s + x1 * c;
         x0 = y0;
@@ -563,10 +577,14 @@ __device__ __forceinline__ void issue_loads(const GemvArgs& a, int it, int sub, 
 // rows; every lane holds RPW rows x NU units in registers.  The first
 // iteration's loads are issued before x is staged, so HBM latency overlaps the
 // prologue, and each next iteration's loads are issued before the current
-// reduction and epilogue.
-template <int QT, int RPW, int LPR, int NU, int EPI>
-__global__ __launch_bounds__(CN_BLOCK) void gemv_kernel(GemvArgs a) {
+// reduction and epilogue.  BS threads per workgroup (Q4_0: 256, 512 or 1024;
+// K-quants 256): the launch picks BS so that one workgroup per CU holds every
+// row of the launch in flight where the register budget allows.
+template <int QT, int RPW, int LPR, int NU, int EPI, int BS>
+__global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
   using T = QTraits<QT>;
+  static_assert(QT == QT_Q4_0 || BS == CN_BLOCK, "K-quant GEMVs run 256-thread workgroups");
+  constexpr int NWV = BS / CN_WAVE;
   constexpr int UNIT = T::UNIT;
   constexpr int RW = RPW * (CN_WAVE / LPR);
   extern __shared__ float smem[];
@@ -581,8 +599,8 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_kernel(GemvArgs a) {
   const int sub = lane / LPR, li = lane % LPR;
   const int n_iters = (a.n_vrows + RW - 1) / RW;
   const size_t bpr = (size_t)(K / T::BLOCK) * T::BLOCK_BYTES;
-  const int wstride = gridDim.x * (CN_BLOCK / CN_WAVE);
-  int it = blockIdx.x * (CN_BLOCK / CN_WAVE) + wave;
+  const int wstride = gridDim.x * NWV;
+  int it = blockIdx.x * NWV + wave;
 
   uint32_t w[RPW][NU][T::NDW];
   float res[RPW];
@@ -590,19 +608,22 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_kernel(GemvArgs a) {
 
   // ---- prologue: stage x (optionally RMS-normalised) into LDS ----
   if constexpr (QT == QT_Q4_0) {
-    // items per thread: K <= 64 * LPR * NU, K/8 items over 256 threads
-    constexpr int MAXT = (LPR * NU) / 32 > 0 ? (LPR * NU) / 32 : 1;
+    // items per thread: K <= 64 * LPR * NU, so K/8 <= 8 * LPR * NU items over BS threads
+    constexpr int MAXT = (8 * LPR * NU + BS - 1) / BS;
     constexpr bool NORM = EPI == GEMV_EPI_QKV || EPI == GEMV_EPI_SWIGLU || EPI == GEMV_EPI_LOGITS;
     XStage<MAXT, NORM> st;
-    stage_load<MAXT, NORM>(a.x, a.norm_w, K, st);
+    stage_load<MAXT, NORM, BS>(a.x, a.norm_w, K, st);
     // rows past n_vrows come back as zeros, so idle waves need no branch here
     issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
-    load_residual<EPI, RPW>(a, it * RW + sub * RPW, li, res);
+    load_residual<EPI, RPW>(a, it * RW + sub * RPW, li, pos, res);
     uint32_t* xd = reinterpret_cast<uint32_t*>(smem);
     float* xred = reinterpret_cast<float*>(smem) + (size_t)nunits * XD_UNIT_DW;
-    stage_digitize<MAXT, NORM>(st, K, xd, xred);
+    stage_digitize<MAXT, NORM, BS>(st, K, xd, xred);
     __syncthreads();
-    const float rms = NORM ? 1.0f / sqrtf((xred[0] + xred[1] + xred[2] + xred[3]) / (float)K + a.eps) : 1.0f;
+    float ss = 0.f;
+#pragma unroll
+    for (int v = 0; v < NWV; v++) ss += xred[v];
+    const float rms = NORM ? 1.0f / sqrtf(ss / (float)K + a.eps) : 1.0f;
     while (it < n_iters) {
       float acc[RPW];
 #pragma unroll
@@ -626,7 +647,7 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_kernel(GemvArgs a) {
       it += wstride;
       if (it < n_iters) {
         issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
-        load_residual<EPI, RPW>(a, it * RW + sub * RPW, li, res);
+        load_residual<EPI, RPW>(a, it * RW + sub * RPW, li, pos, res);
       }
 #pragma unroll
       for (int i = 0; i < RPW; i++) {
@@ -640,7 +661,7 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_kernel(GemvArgs a) {
   }
   if (it < n_iters) {
     issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
-    load_residual<EPI, RPW>(a, it * RW + sub * RPW, li, res);
+    load_residual<EPI, RPW>(a, it * RW + sub * RPW, li, pos, res);
   }
   float rms = 1.0f;
   if (a.norm_w) {
@@ -704,7 +725,7 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_kernel(GemvArgs a) {
     it += wstride;
     if (it < n_iters) {
       issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
-      load_residual<EPI, RPW>(a, it * RW + sub * RPW, li, res);
+      load_residual<EPI, RPW>(a, it * RW + sub * RPW, li, pos, res);
     }
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
@@ -719,28 +740,34 @@ template <int QT>
 size_t gemv_smem_bytes(int K) {
   using T = QTraits<QT>;
   const int nunits = K / T::UNIT;
-  if (QT == QT_Q4_0) return ((size_t)nunits * XD_UNIT_DW + 4) * sizeof(uint32_t);
+  if (QT == QT_Q4_0) return ((size_t)nunits * XD_UNIT_DW + 16) * sizeof(uint32_t);  // + one float per wave
   size_t f = (size_t)nunits * (T::UNIT + 4) + (K >> 5) + (QT == QT_Q6_K ? (K >> 4) : 0) + 4;
   return f * sizeof(float);
 }
 
-// Launch shape of one GEMV: lanes per row, units per lane, rows per lane.
+// Launch shape of one GEMV: lanes per row, units per lane, rows per lane,
+// threads per workgroup and workgroups.
 struct GemvShape {
-  int lpr, nu, rpw;
+  int lpr, nu, rpw, bs, grid;
 };
 
 // Q4_0: the (LPR, NU) pair that wastes the fewest lanes (NU <= 4, ties to the
 // wider LPR).  Rows per lane: the smallest of 2, 4, 8 (register budget
-// permitting) whose waves all fit on the chip at once, so every weight load of
-// the launch is issued in the first round; resident waves per CU assumed 20,
-// 16 and 12 for 2, 4 and 8 rows.
-// K-quants: one super-block per lane (NU = 1) and 2 rows, LPR the smallest
-// power of two covering the row (min 16).
+// permitting) whose waves would all be resident at once (20, 16 and 12 waves
+// per CU assumed for 2, 4 and 8 rows).  256-thread workgroups, at most two per
+// CU, with further rows taken by a grid-stride loop; when 512-thread
+// workgroups bring the launch to one workgroup per CU they are used instead,
+// so x is staged once per CU (measured on 4096x4096 and 4096x11008: 4.85 ->
+// 4.52 us and 10.1 -> 9.1 us).  Single-round shapes with more rows per lane,
+// and 1024- or 128-thread workgroups, measured slower on every decode GEMV of
+// the 1.1B and 7B shapes.
+// K-quants: one super-block per lane (NU = 1), 2 rows, LPR the smallest power
+// of two covering the row (min 16), 256 threads, at most two workgroups per CU.
 template <int QT>
 GemvShape pick_shape(int K, int n_vrows, int num_cus, bool allow8) {
   using T = QTraits<QT>;
   const int nunits = K / T::UNIT;
-  GemvShape s{64, 1, 2};
+  GemvShape s{64, 1, 2, CN_BLOCK, 1};
   if (QT == QT_Q4_0) {
     double best = -1.0;
     for (int lpr = 64; lpr >= 32; lpr >>= 1)
@@ -756,8 +783,7 @@ GemvShape pick_shape(int K, int n_vrows, int num_cus, bool allow8) {
     s.rpw = max_rpw;
     for (int rpw = 2; rpw <= max_rpw; rpw *= 2) {
       const int rw = rpw * (64 / s.lpr);
-      const int waves = (n_vrows + rw - 1) / rw;
-      if (waves <= num_cus * resident[rpw]) {
+      if ((n_vrows + rw - 1) / rw <= num_cus * resident[rpw]) {
         s.rpw = rpw;
         break;
       }
@@ -767,53 +793,60 @@ GemvShape pick_shape(int K, int n_vrows, int num_cus, bool allow8) {
     s.rpw = 2;
     s.lpr = nunits <= 16 ? 16 : (nunits <= 32 ? 32 : 64);
   }
+  const int rw = s.rpw * (64 / s.lpr);
+  const int waves = (n_vrows + rw - 1) / rw;
+  s.grid = (waves + 3) / 4;
+  if (QT == QT_Q4_0 && s.grid > num_cus && (waves + 7) / 8 <= num_cus) {
+    s.bs = 512;
+    s.grid = (waves + 7) / 8;
+  }
+  if (s.grid > 2 * num_cus) s.grid = 2 * num_cus;
+  if (s.grid < 1) s.grid = 1;
   return s;
 }
 
-template <int QT, int RPW, int NU, int EPI>
+template <int QT, int RPW, int NU, int EPI, int BS>
 hipError_t launch_k(const GemvArgs& a, int lpr, int grid, size_t smem, hipStream_t st) {
-  if (lpr == 16) hipLaunchKernelGGL((gemv_kernel<QT, RPW, 16, NU, EPI>), dim3(grid), dim3(CN_BLOCK), smem, st, a);
-  else if (lpr == 32) hipLaunchKernelGGL((gemv_kernel<QT, RPW, 32, NU, EPI>), dim3(grid), dim3(CN_BLOCK), smem, st, a);
-  else hipLaunchKernelGGL((gemv_kernel<QT, RPW, 64, NU, EPI>), dim3(grid), dim3(CN_BLOCK), smem, st, a);
+  if constexpr (QT != QT_Q4_0) {
+    if (lpr == 16) {
+      hipLaunchKernelGGL((gemv_kernel<QT, RPW, 16, NU, EPI, BS>), dim3(grid), dim3(BS), smem, st, a);
+      return hipGetLastError();
+    }
+  }
+  if (lpr == 32) hipLaunchKernelGGL((gemv_kernel<QT, RPW, 32, NU, EPI, BS>), dim3(grid), dim3(BS), smem, st, a);
+  else hipLaunchKernelGGL((gemv_kernel<QT, RPW, 64, NU, EPI, BS>), dim3(grid), dim3(BS), smem, st, a);
   return hipGetLastError();
+}
+
+template <int QT, int RPW, int NU, int EPI>
+hipError_t launch_bs(const GemvArgs& a, const GemvShape& s, size_t smem, hipStream_t st) {
+  if (s.bs == 512) return launch_k<QT, RPW, NU, EPI, 512>(a, s.lpr, s.grid, smem, st);
+  return launch_k<QT, RPW, NU, EPI, 256>(a, s.lpr, s.grid, smem, st);
 }
 
 template <int QT, int EPI>
 hipError_t launch_qt(const GemvArgs& a, int num_cus, hipStream_t st) {
-  using T = QTraits<QT>;
   // 8 rows per lane only for the norm-fused epilogues (the wide QKV, gate/up
   // and LM-head launches); hipcc 7.2 fails to compile the 8-row STORE/ADD forms.
   constexpr bool kAllow8 = EPI == GEMV_EPI_QKV || EPI == GEMV_EPI_SWIGLU || EPI == GEMV_EPI_LOGITS;
   const GemvShape s = pick_shape<QT>(a.K, a.n_vrows, num_cus, kAllow8);
-  const int rw = s.rpw * (CN_WAVE / s.lpr);
-  const int n_iters = (a.n_vrows + rw - 1) / rw;
-  const int waves_per_block = CN_BLOCK / CN_WAVE;
-  // At most two workgroups per CU; further rows run as a grid-stride loop whose
-  // next-iteration loads are issued before the current rows are reduced.  Every
-  // workgroup re-stages x, so fewer, longer-lived workgroups beat one short
-  // workgroup per row group (measured: 11008x4096 8.4 -> 7.9 us).
-  int grid = (n_iters + waves_per_block - 1) / waves_per_block;
-  const int cap = num_cus * 2;
-  if (grid > cap) grid = cap;
-  if (grid < 1) grid = 1;
   const size_t smem = gemv_smem_bytes<QT>(a.K);
-  (void)T::NDW;
   if constexpr (QT == QT_Q4_0) {
     if (s.nu == 1) {
       if constexpr (kAllow8) {
-        if (s.rpw == 8) return launch_k<QT, 8, 1, EPI>(a, s.lpr, grid, smem, st);
+        if (s.rpw == 8) return launch_bs<QT, 8, 1, EPI>(a, s, smem, st);
       }
-      if (s.rpw == 4) return launch_k<QT, 4, 1, EPI>(a, s.lpr, grid, smem, st);
-      return launch_k<QT, 2, 1, EPI>(a, s.lpr, grid, smem, st);
+      if (s.rpw == 4) return launch_bs<QT, 4, 1, EPI>(a, s, smem, st);
+      return launch_bs<QT, 2, 1, EPI>(a, s, smem, st);
     }
     if (s.nu == 2) {
-      if (s.rpw == 4) return launch_k<QT, 4, 2, EPI>(a, s.lpr, grid, smem, st);
-      return launch_k<QT, 2, 2, EPI>(a, s.lpr, grid, smem, st);
+      if (s.rpw == 4) return launch_bs<QT, 4, 2, EPI>(a, s, smem, st);
+      return launch_bs<QT, 2, 2, EPI>(a, s, smem, st);
     }
-    if (s.nu == 3) return launch_k<QT, 2, 3, EPI>(a, s.lpr, grid, smem, st);
-    return launch_k<QT, 2, 4, EPI>(a, s.lpr, grid, smem, st);
+    if (s.nu == 3) return launch_bs<QT, 2, 3, EPI>(a, s, smem, st);
+    return launch_bs<QT, 2, 4, EPI>(a, s, smem, st);
   } else {
-    return launch_k<QT, 2, 1, EPI>(a, s.lpr, grid, smem, st);
+    return launch_k<QT, 2, 1, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
   }
 }
 

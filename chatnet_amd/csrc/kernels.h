@@ -24,8 +24,7 @@ struct GemvArgs {
   // QKV epilogue
   const int* pos;  // device position of the token
   int head_dim;
-  float rope_dim_inv;       // 1/head_dim
-  float rope_neg_log_base;  // -ln(freq_base)
+  const float2* rope;       // RoPE table [context][head_dim/2] of (cos, sin)
   void* kcache;             // layer base of the K cache
   void* vcache;             // layer base of the V cache
   int kv_dim;
@@ -71,12 +70,15 @@ hipError_t rmsnorm_bf16_launch(const float* x, const float* g, float eps, uint16
 struct RopeKvArgs {
   float* qkv;
   int ld, dim, kv_dim, head_dim, p0;
-  float rope_dim_inv, rope_neg_log_base;
+  const float2* rope;  // RoPE table [context][head_dim/2] of (cos, sin)
   void* kcache;  // layer base
   void* vcache;
   int kv_f16;
 };
 hipError_t rope_kv_launch(const RopeKvArgs& a, int n, hipStream_t st);
+// Fills tab[p][j] = (cos, sin) of theta = p * exp(2j * dim_inv * neg_log_base),
+// p < ctx, j < head_dim/2 (TensorMath.ApplyRoPE's angle, TensorMath.cs:418-432).
+hipError_t rope_table_launch(float2* tab, int ctx, int head_dim, float dim_inv, float neg_log_base, hipStream_t st);
 
 struct PrefillAttnArgs {
   const float* qkv;  // q at column 0 of each row

@@ -8,13 +8,25 @@
 
 namespace {
 
-// RoPE (TensorMath.ApplyRoPE, TensorMath.cs:408-458) of the pair (i, i+1) of a
-// head at position pos, theta = pos * exp(i * (1/hd) * (-ln base)); the same
-// expression as the decode path's QKV epilogue.
-__device__ __forceinline__ void rope_pair(float& x0, float& x1, int i, int pos, float dim_inv, float neg_log_base) {
+// The RoPE table (TensorMath.ApplyRoPE, TensorMath.cs:418-432): one thread per
+// (position, pair), theta = pos * exp(i * (1/hd) * (-ln base)) for the pair's
+// even index i = 2j.  Built once per model, so the per-token kernels read the
+// angles instead of evaluating expf and sincosf (whose large-argument
+// reduction would give them a scratch allocation).
+__global__ __launch_bounds__(CN_BLOCK) void rope_table_kernel(float2* tab, int ctx, int half, float dim_inv,
+                                                              float neg_log_base) {
+  const int idx = blockIdx.x * CN_BLOCK + threadIdx.x;
+  if (idx >= ctx * half) return;
+  const int pos = idx / half, i = 2 * (idx % half);
   const float theta = (float)pos * expf((float)i * dim_inv * neg_log_base);
   float s, c;
   sincosf(theta, &s, &c);
+  tab[idx] = make_float2(c, s);
+}
+
+// RoPE of the pair (x0, x1) with the table entry cs = (cos, sin).
+__device__ __forceinline__ void rope_pair(float& x0, float& x1, float2 cs) {
+  const float c = cs.x, s = cs.y;
   const float y0 = x0 * c - x1 * s;
   const float y1 = x0 * s + x1 * c;
   x0 = y0;
@@ -33,14 +45,14 @@ __global__ __launch_bounds__(CN_BLOCK) void rope_kv_kernel(RopeKvArgs a) {
   if (i < pairs_q) {
     float2* p = reinterpret_cast<float2*>(row) + i;
     float2 v = *p;
-    rope_pair(v.x, v.y, (2 * i) % a.head_dim, pos, a.rope_dim_inv, a.rope_neg_log_base);
+    rope_pair(v.x, v.y, a.rope[(size_t)pos * (a.head_dim / 2) + i % (a.head_dim / 2)]);
     *p = v;
     return;
   }
   const bool is_k = i < pairs_q + pairs_kv;
   const int j = is_k ? i - pairs_q : i - pairs_q - pairs_kv;  // pair index within k or v
   float2 v = reinterpret_cast<const float2*>(row + a.dim + (is_k ? 0 : a.kv_dim))[j];
-  if (is_k) rope_pair(v.x, v.y, (2 * j) % a.head_dim, pos, a.rope_dim_inv, a.rope_neg_log_base);
+  if (is_k) rope_pair(v.x, v.y, a.rope[(size_t)pos * (a.head_dim / 2) + j % (a.head_dim / 2)]);
   const size_t off = (size_t)pos * a.kv_dim + 2 * j;
   void* base = is_k ? a.kcache : a.vcache;
   if (a.kv_f16) {
@@ -270,6 +282,14 @@ hipError_t attn_prefill_launch(const PrefillAttnArgs& a, hipStream_t st) {
   if (!attn_prefill_supports(a.head_dim, a.kv_mul) || a.n <= 0) return hipErrorInvalidValue;
   if (a.head_dim == 64) return a.kv_f16 ? attn_prefill_t<64, true>(a, st) : attn_prefill_t<64, false>(a, st);
   return a.kv_f16 ? attn_prefill_t<128, true>(a, st) : attn_prefill_t<128, false>(a, st);
+}
+
+hipError_t rope_table_launch(float2* tab, int ctx, int head_dim, float dim_inv, float neg_log_base, hipStream_t st) {
+  if (ctx <= 0 || head_dim <= 0 || (head_dim & 1)) return hipErrorInvalidValue;
+  const int n = ctx * (head_dim / 2);
+  hipLaunchKernelGGL(rope_table_kernel, dim3((n + CN_BLOCK - 1) / CN_BLOCK), dim3(CN_BLOCK), 0, st, tab, ctx,
+                     head_dim / 2, dim_inv, neg_log_base);
+  return hipGetLastError();
 }
 
 hipError_t rope_kv_launch(const RopeKvArgs& a, int n, hipStream_t st) {
