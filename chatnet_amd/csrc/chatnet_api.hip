@@ -112,11 +112,15 @@ struct chatnet_model {
   int* state = nullptr;  // [0] pos, [1] token, [2] step
   float* attn_part_o = nullptr;   // split partials of the decode attention
   float* attn_part_ml = nullptr;
-  int attn_splits = 1;
+  int attn_splits_max = 1;  // most chunks any decode-attention launch uses
+
   float2* rope = nullptr;  // [context_length][head_dim/2] (cos, sin), filled at creation
   int* out_tokens = nullptr;
   int out_cap = 0;
-  hipGraphExec_t graph = nullptr;
+  // Decode-step graphs, one per position bucket (sequence lengths up to
+  // min(ctx, 64 << k) for bucket k), captured on first use.
+  static constexpr int kBuckets = 16;
+  hipGraphExec_t graphs[kBuckets] = {};
   bool have_logits = false;
   int next_pos = 0;  // position after the last forwarded token
   int last_tok = 0;  // last forwarded token
@@ -132,6 +136,52 @@ struct chatnet_model {
   float* sp_part = nullptr;    // GEMM K-split partials
   size_t sp_part_bytes = 0;
 };
+
+namespace {
+
+// Most decode-attention chunks per kv head: up to two workgroups per CU over
+// the kv heads, at most 64.
+int attn_max_splits(int n_kv_heads, int num_cus) {
+  int s = 1;
+  while (s < 64 && s * 2 * n_kv_heads <= 2 * num_cus) s *= 2;
+  return s;
+}
+
+// Position bucket of a sequence length: bucket k covers lengths up to
+// min(ctx, 64 << k).  A decode graph serves one bucket; its attention launch is
+// sized for the bucket's largest length.
+int bucket_index(const chatnet_model* m, int seq) {
+  int k = 0;
+  while ((64 << k) < seq && (64 << k) < m->cfg.context_length && k + 1 < chatnet_model::kBuckets) k++;
+  return k;
+}
+
+int bucket_cap(const chatnet_model* m, int seq) {
+  const int cap = 64 << bucket_index(m, seq);
+  return cap < m->cfg.context_length ? cap : m->cfg.context_length;
+}
+
+// Decode-attention launch for sequence lengths up to cap: chunks of at least
+// 32 positions (one step of the four waves), as many as attn_max_splits
+// allows.  chunk * splits >= cap, and every chunk starts below cap.
+struct AttnPlan {
+  int splits, chunk;
+};
+AttnPlan attn_plan(const chatnet_model* m, int cap) {
+  const int smax = m->attn_splits_max;
+  int chunk = (cap + smax - 1) / smax;
+  if (chunk < 32) chunk = 32;
+  return {(cap + chunk - 1) / chunk, chunk};
+}
+
+void drop_graphs(chatnet_model* m) {
+  for (auto& g : m->graphs) {
+    if (g) (void)hipGraphExecDestroy(g);
+    g = nullptr;
+  }
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -209,14 +259,8 @@ int chatnet_create(const chatnet_config* cfg, int device, chatnet_model** out) {
   m->kv_elt = c.kv_dtype == CHATNET_KV_F16 ? 2 : 4;
   m->layers.resize(c.n_layers);
   const size_t kv_bytes = (size_t)c.n_layers * c.context_length * m->kv_dim * m->kv_elt;
-  // Attention splits: up to two workgroups per CU over the KV heads (at most 64
-  // splits); the kernels use only as many as hold 4 or more positions at the
-  // current position.  Each workgroup leaves one partial per query head.
-  int splits = 1;
-  while (splits < 64 && splits * 2 * c.n_kv_heads <= 2 * m->num_cus && splits * 2 * 4 <= c.context_length)
-    splits *= 2;
-  m->attn_splits = splits;
-  const size_t attn_slots = (size_t)c.n_heads * splits;
+  m->attn_splits_max = attn_max_splits(c.n_kv_heads, m->num_cus);
+  const size_t attn_slots = (size_t)c.n_heads * m->attn_splits_max;
   auto cleanup = [m]() { chatnet_destroy(m); };
   if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) {
     cleanup();
@@ -263,7 +307,7 @@ void chatnet_destroy(chatnet_model* m) {
   if (!m) return;
   (void)hipSetDevice(m->device);
   if (m->stream) (void)hipStreamSynchronize(m->stream);
-  if (m->graph) (void)hipGraphExecDestroy(m->graph);
+  drop_graphs(m);
   auto fr = [](void* p) { if (p) (void)hipFree(p); };
   fr(m->emb.ptr); fr(m->out.ptr); fr(m->out_norm.ptr);
   for (auto& l : m->layers) {
@@ -354,10 +398,7 @@ int chatnet_upload_tensor(chatnet_model* m, const char* name, uint32_t type, con
   slot->nbytes = nbytes;
   slot->ne0 = ne0;
   slot->ne1 = ne1;
-  if (m->graph) {
-    (void)hipGraphExecDestroy(m->graph);
-    m->graph = nullptr;
-  }
+  drop_graphs(m);
   g_err.clear();
   return CHATNET_OK;
 }
@@ -396,8 +437,9 @@ GemvArgs base_args(const chatnet_model* m) {
   return a;
 }
 
-// Launches the forward of the token held in m->state (pos, token).
-int launch_token(chatnet_model* m, bool lm_head) {
+// Launches the forward of the token held in m->state (pos, token); the
+// attention covers sequence lengths up to cap (the position's bucket).
+int launch_token(chatnet_model* m, bool lm_head, int cap) {
   const chatnet_config& c = m->cfg;
   hipStream_t st = m->stream;
   const int kvd = m->kv_dim;
@@ -448,7 +490,9 @@ int launch_token(chatnet_model* m, bool lm_head) {
     at.ctx = c.context_length;
     at.kv_f16 = a.kv_f16;
     at.scale = 1.0f / sqrtf((float)c.head_dim);  // LlamaModel.cs:248
-    at.splits = m->attn_splits;
+    const AttnPlan plan = attn_plan(m, cap);
+    at.splits = plan.splits;
+    at.chunk = plan.chunk;
     at.part_o = m->attn_part_o;
     at.part_ml = m->attn_part_ml;
     HIP_TRY(attn_decode_launch(at, st));
@@ -510,10 +554,7 @@ int ensure_out_tokens(chatnet_model* m, int cap) {
   if (hipMalloc(&m->out_tokens, sizeof(int) * (size_t)cap) != hipSuccess)
     return fail(CHATNET_ERR_OUT_OF_MEMORY, "hipMalloc of token buffer failed");
   m->out_cap = cap;
-  if (m->graph) {  // the captured argmax node points at the old buffer
-    (void)hipGraphExecDestroy(m->graph);
-    m->graph = nullptr;
-  }
+  drop_graphs(m);  // the captured argmax nodes point at the old buffer
   return CHATNET_OK;
 }
 
@@ -722,7 +763,7 @@ int run_prompt(chatnet_model* m, const int32_t* tokens, int n, int position) {
   if (span_batchable(m, n)) return run_span(m, tokens, n, position);
   for (int t = 0; t < n; t++) {
     HIP_TRY(set_state_launch(m->state, position + t, tokens[t], -1, m->stream));
-    int rc = launch_token(m, t == n - 1);
+    int rc = launch_token(m, t == n - 1, bucket_cap(m, position + t + 1));
     if (rc) return rc;
   }
   m->have_logits = true;
@@ -806,29 +847,33 @@ int chatnet_decode_greedy(chatnet_model* m, int max_tokens, int32_t eos_token, i
   // launches need this; the kernels and their order are identical).
   const char* ge = getenv("CHATNET_DECODE_GRAPH");
   const bool use_graph = !(ge && ge[0] == '0');
+  // Step i forwards the token at position p0+i (sequence length p0+i+1).
   if (forwards > 0 && !use_graph) {
     for (int i = 0; i < forwards; i++) {
-      if ((rc = launch_token(m, true))) return rc;
+      if ((rc = launch_token(m, true, bucket_cap(m, p0 + i + 1)))) return rc;
       HIP_TRY(argmax_launch(m->logits, m->cfg.vocab_size, m->state, m->out_tokens, m->out_cap, m->stream));
     }
   } else if (forwards > 0) {
-    if (!m->graph) {
-      hipGraph_t g;
-      HIP_TRY(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
-      int lrc = launch_token(m, true);
-      hipError_t ae = argmax_launch(m->logits, m->cfg.vocab_size, m->state, m->out_tokens, m->out_cap, m->stream);
-      hipError_t ee = hipStreamEndCapture(m->stream, &g);
-      if (lrc) return lrc;
-      if (ae != hipSuccess) return fail(CHATNET_ERR_HIP, "argmax capture: %s", hipGetErrorString(ae));
-      if (ee != hipSuccess) return fail(CHATNET_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(ee));
-      hipError_t ie = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
-      (void)hipGraphDestroy(g);
-      if (ie != hipSuccess) {
-        m->graph = nullptr;
-        return fail(CHATNET_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(ie));
+    for (int i = 0; i < forwards; i++) {
+      const int k = bucket_index(m, p0 + i + 1);
+      if (!m->graphs[k]) {
+        hipGraph_t g;
+        HIP_TRY(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+        int lrc = launch_token(m, true, bucket_cap(m, p0 + i + 1));
+        hipError_t ae = argmax_launch(m->logits, m->cfg.vocab_size, m->state, m->out_tokens, m->out_cap, m->stream);
+        hipError_t ee = hipStreamEndCapture(m->stream, &g);
+        if (lrc) return lrc;
+        if (ae != hipSuccess) return fail(CHATNET_ERR_HIP, "argmax capture: %s", hipGetErrorString(ae));
+        if (ee != hipSuccess) return fail(CHATNET_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(ee));
+        hipError_t ie = hipGraphInstantiate(&m->graphs[k], g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (ie != hipSuccess) {
+          m->graphs[k] = nullptr;
+          return fail(CHATNET_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(ie));
+        }
       }
+      HIP_TRY(hipGraphLaunch(m->graphs[k], m->stream));
     }
-    for (int i = 0; i < forwards; i++) HIP_TRY(hipGraphLaunch(m->graph, m->stream));
   }
   std::vector<int> buf((size_t)emitted + 2);
   HIP_TRY(hipMemcpyAsync(buf.data(), m->out_tokens, sizeof(int) * (emitted + 1), hipMemcpyDeviceToHost, m->stream));

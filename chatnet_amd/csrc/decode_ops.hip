@@ -28,113 +28,195 @@ __global__ __launch_bounds__(CN_BLOCK) void embed_kernel(const void* emb, int ty
   }
 }
 
-// Fewest positions a decode-attention split takes: one per wave.  Decode
-// attention is latency-bound, so short contexts still spread over many
-// workgroups; the cap on splits bounds the merge.
-constexpr int kAttnMinChunk = 4;
-
-// Splits that carry positions at sequence length seq: min(splits, ceil(seq / kAttnMinChunk)).
-// The decode kernel and the merge both derive it from the device-side position,
-// so one captured decode step serves every position.
-__device__ __forceinline__ int attn_active_splits(int splits, int seq) {
-  return min(splits, (seq + kAttnMinChunk - 1) / kAttnMinChunk);
+// Splits that carry positions at sequence length seq: the launch covers
+// a.splits fixed chunks of a.chunk positions, and chunk c is active while
+// c * chunk < seq.
+__device__ __forceinline__ int attn_active_splits(const AttnArgs& a, int seq) {
+  return min(a.splits, (seq + a.chunk - 1) / a.chunk);
 }
 
-template <bool F16>
-__device__ __forceinline__ float kv_load(const void* base, size_t idx) {
-  if constexpr (F16) return (float)reinterpret_cast<const _Float16*>(base)[idx];
-  else return reinterpret_cast<const float*>(base)[idx];
+// n consecutive floats of a K/V cache row (fp32 or fp16) starting at idx.
+template <bool F16, int N>
+__device__ __forceinline__ void kv_load_n(const void* base, size_t idx, float* out) {
+  if constexpr (F16) {
+    const _Float16* p = reinterpret_cast<const _Float16*>(base) + idx;
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < N; i += 4) {
+        const uint2 u = *reinterpret_cast<const uint2*>(p + i);
+        out[i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u.x & 0xFFFFu));
+        out[i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u.x >> 16));
+        out[i + 2] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u.y & 0xFFFFu));
+        out[i + 3] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u.y >> 16));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; i++) out[i] = (float)p[i];
+    }
+  } else {
+    const float* p = reinterpret_cast<const float*>(base) + idx;
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < N; i += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(p + i);
+        out[i] = v.x; out[i + 1] = v.y; out[i + 2] = v.z; out[i + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; i++) out[i] = p[i];
+    }
+  }
+}
+
+// Sum over the 16 lanes of a row (DPP: quad xor 1, quad xor 2, half-row
+// mirror, row mirror); every lane of the row gets the sum.
+__device__ __forceinline__ float row_sum16(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, true));
+  return v;
 }
 
 // Split-position GQA decode attention (LlamaModel.ComputeAttention,
 // LlamaModel.cs:241-346): for query head h with kvh = h / kv_mul (:265),
 //   s[p] = (q_h . K[p][kvh]) * scale  for p <= pos,  w = softmax(s) (TensorMath.cs:177-241),
 //   out_h = sum_p w[p] V[p][kvh].
-// Grid = n_kv_heads x splits; workgroup (kvh, c) takes positions
-// [c*chunk, (c+1)*chunk) of seq = pos+1, and wave w of it the positions
-// p = c*chunk + w + 4i.  A wave issues the K and V row loads of PW positions
-// at once (lane l owns head elements l*EPL..), keeps q of up to KVM query
-// heads of the group in registers, reduces each score across the wave and
-// folds it into a running (max, sum, o) per head (online softmax).  The four
-// wave partials of a head are folded through LDS into one partial per split
-// for attn_merge_kernel.
+// Grid = n_kv_heads x a.splits; workgroup (kvh, c) takes the positions
+// [c*chunk, (c+1)*chunk) below seq = pos+1.  A wave is 4 rows of 16 lanes: row
+// r holds one position, lane i of the row the head elements [i*EPL, (i+1)*EPL)
+// (EPL = HD/16).  A wave step covers 8 consecutive positions (two per row) for
+// KVM query heads of the group at once: 16-lane dot products reduced with DPP
+// inside the row, one max over the step's positions per head, one rescale of
+// the running (max, sum, o) per head (online softmax; sums and o stay per row
+// until the end).  The first step's K/V loads depend only on the chunk, so
+// they are in flight before the position arrives.  Rows, then the four waves
+// (through LDS), fold into one partial per split for attn_merge_kernel.
 template <int HD, bool F16, int KVM>
 __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
-  constexpr int EPL = HD >= 64 ? HD / 64 : 1;  // head elements per lane
-  constexpr int PW = 8;                        // positions whose loads are in flight together
+  constexpr int EPL = HD / 16;   // head elements per lane
+  constexpr int PG = 2;          // positions per row in a step
   constexpr int NW = CN_BLOCK / CN_WAVE;
+  constexpr int SP = 4 * PG;     // positions per wave step
   const int kvh = blockIdx.x / a.splits;
   const int split = blockIdx.x % a.splits;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int seq = *a.pos + 1;
-  // Active splits for this position: at least kAttnMinChunk positions each, so
-  // short contexts use few workgroups and long ones spread over many.
-  const int s_eff = attn_active_splits(a.splits, seq);
-  if (split >= s_eff) return;  // uniform over the workgroup, before any barrier
-  const int chunk = (seq + s_eff - 1) / s_eff;
-  const int p0 = split * chunk;
-  const int p1 = min(seq, p0 + chunk);
-  const size_t koff = (size_t)kvh * HD;
+  const int row = lane >> 4, col = lane & 15;
   const int h0 = kvh * a.kv_mul;
+  const int p0 = split * a.chunk;
+  const int pcap = min(p0 + a.chunk, a.ctx);  // this split's positions, all inside the cache
+  const size_t koff = (size_t)kvh * HD + col * EPL;
   __shared__ float so[KVM * NW * HD];
   __shared__ float sml[KVM * NW * 2];
+  const int seq = *a.pos + 1;
 
   for (int jg = 0; jg < a.kv_mul; jg += KVM) {
     const int nj = min(KVM, a.kv_mul - jg);
     float q[KVM][EPL], m[KVM], l[KVM], o[KVM][EPL];
 #pragma unroll
     for (int j = 0; j < KVM; j++) {
+      if (j < nj) {
+        kv_load_n<false, EPL>(a.q, (size_t)(h0 + jg + j) * HD + col * EPL, q[j]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPL; e++) q[j][e] = 0.f;
+      }
       m[j] = -INFINITY;
       l[j] = 0.f;
 #pragma unroll
-      for (int e = 0; e < EPL; e++) {
-        const int d = lane * EPL + e;
-        q[j][e] = (j < nj && d < HD) ? a.q[(size_t)(h0 + jg + j) * HD + d] : 0.f;
-        o[j][e] = 0.f;
+      for (int e = 0; e < EPL; e++) o[j][e] = 0.f;
+    }
+    // first step: positions below pcap regardless of seq
+    int pb = p0 + wave * SP;
+    float kr[PG][EPL], vr[PG][EPL];
+#pragma unroll
+    for (int g = 0; g < PG; g++) {
+      const int p = pb + 4 * g + row;
+      if (p < pcap) {
+        kv_load_n<F16, EPL>(a.kc, (size_t)p * a.kv_dim + koff, kr[g]);
+        kv_load_n<F16, EPL>(a.vc, (size_t)p * a.kv_dim + koff, vr[g]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPL; e++) kr[g][e] = vr[g][e] = 0.f;
       }
     }
-    for (int pb = p0 + wave; pb < p1; pb += NW * PW) {
-      float kr[PW][EPL], vr[PW][EPL];
+    const int p1 = min(seq, pcap);
+    while (pb < p1) {  // uniform across the wave
+      float sc[PG][KVM];
 #pragma unroll
-      for (int i = 0; i < PW; i++) {
-        const int p = pb + NW * i;
+      for (int g = 0; g < PG; g++) {
+        const bool on = pb + 4 * g + row < p1;
+        // rows past the sequence may hold anything the speculative first loads
+        // found: their scores become -inf and their V rows 0 by selection
 #pragma unroll
-        for (int e = 0; e < EPL; e++) {
-          const int d = lane * EPL + e;
-          const bool ok = p < p1 && d < HD;
-          const size_t idx = (size_t)p * a.kv_dim + koff + d;
-          kr[i][e] = ok ? kv_load<F16>(a.kc, idx) : 0.f;
-          vr[i][e] = ok ? kv_load<F16>(a.vc, idx) : 0.f;
+        for (int e = 0; e < EPL; e++) vr[g][e] = on ? vr[g][e] : 0.f;
+#pragma unroll
+        for (int j = 0; j < KVM; j++) {
+          float t = 0.f;
+#pragma unroll
+          for (int e = 0; e < EPL; e++) t += q[j][e] * kr[g][e];
+          t = row_sum16(t) * a.scale;
+          sc[g][j] = on ? t : -INFINITY;
         }
       }
 #pragma unroll
-      for (int i = 0; i < PW; i++) {
-        if (pb + NW * i >= p1) break;  // uniform across the wave
+      for (int j = 0; j < KVM; j++) {
+        if (j >= nj) break;
+        float mx = sc[0][j];
 #pragma unroll
-        for (int j = 0; j < KVM; j++) {
-          if (j >= nj) break;
-          float sdot = 0.f;
+        for (int g = 1; g < PG; g++) mx = fmaxf(mx, sc[g][j]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, CN_WAVE));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, CN_WAVE));
+        const float mn = fmaxf(m[j], mx);  // finite: position pb (row 0, g 0) is below p1
+        const float c = expf(m[j] - mn);
+        float pe[PG], ps = 0.f;
 #pragma unroll
-          for (int e = 0; e < EPL; e++) sdot += q[j][e] * kr[i][e];
-          const float sc = cn_wave_sum(sdot) * a.scale;
-          const float mn = fmaxf(m[j], sc);
-          const float c = expf(m[j] - mn);
-          const float pe = expf(sc - mn);
-          l[j] = l[j] * c + pe;
-#pragma unroll
-          for (int e = 0; e < EPL; e++) o[j][e] = o[j][e] * c + pe * vr[i][e];
-          m[j] = mn;
+        for (int g = 0; g < PG; g++) {
+          pe[g] = expf(sc[g][j] - mn);
+          ps += pe[g];
         }
+        l[j] = l[j] * c + ps;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) {
+          float t = o[j][e] * c;
+#pragma unroll
+          for (int g = 0; g < PG; g++) t += pe[g] * vr[g][e];
+          o[j][e] = t;
+        }
+        m[j] = mn;
+      }
+      pb += NW * SP;
+      if (pb >= p1) break;
+#pragma unroll
+      for (int g = 0; g < PG; g++) {
+        const int p = pb + 4 * g + row;
+        if (p < p1) {
+          kv_load_n<F16, EPL>(a.kc, (size_t)p * a.kv_dim + koff, kr[g]);
+          kv_load_n<F16, EPL>(a.vc, (size_t)p * a.kv_dim + koff, vr[g]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < EPL; e++) kr[g][e] = vr[g][e] = 0.f;
+        }
+      }
+    }
+    // rows -> wave: sums and o add across the 4 rows (common running max)
+#pragma unroll
+    for (int j = 0; j < KVM; j++) {
+      l[j] += __shfl_xor(l[j], 16, CN_WAVE);
+      l[j] += __shfl_xor(l[j], 32, CN_WAVE);
+#pragma unroll
+      for (int e = 0; e < EPL; e++) {
+        o[j][e] += __shfl_xor(o[j][e], 16, CN_WAVE);
+        o[j][e] += __shfl_xor(o[j][e], 32, CN_WAVE);
       }
     }
     // fold the NW wave partials of each head through LDS, one partial per split
 #pragma unroll
     for (int j = 0; j < KVM; j++) {
       if (j >= nj) break;
+      if (row == 0) {
 #pragma unroll
-      for (int e = 0; e < EPL; e++) {
-        const int d = lane * EPL + e;
-        if (d < HD) so[(j * NW + wave) * HD + d] = o[j][e];
+        for (int e = 0; e < EPL; e++) so[(j * NW + wave) * HD + col * EPL + e] = o[j][e];
       }
       if (lane == 0) {
         sml[2 * (j * NW + wave)] = m[j];
@@ -169,26 +251,39 @@ __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
   }
 }
 
-// Merges the active split partials of one query head (grid = n_heads, block = HD):
+// Merges the active split partials of one query head (grid = n_heads,
+// block = CN_BLOCK = G groups of HD threads):
 //   M = max_c m_c,  L = sum_c l_c e^(m_c - M),  out = sum_c o_c e^(m_c - M) / L,
-// empty splits (l_c = 0) contributing nothing.  Partials are read in rounds of
-// R, all loads of a round in flight together, with the running (M, L, acc)
-// rescaled when a round raises the maximum.
+// empty splits (l_c = 0) contributing nothing.  Group g takes splits
+// g, g+G, ... in rounds of R (all loads of a round in flight together, the
+// running (M, L, acc) rescaled when a round raises the maximum), so up to G*R
+// splits cost one memory round trip; the G group states are then combined the
+// same way through LDS.
 template <int HD>
-__global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs a) {
+__global__ __launch_bounds__(CN_BLOCK) void attn_merge_kernel(AttnArgs a) {
   constexpr int R = 16;
-  const int h = blockIdx.x, d = threadIdx.x;
-  const int s_eff = attn_active_splits(a.splits, *a.pos + 1);
+  constexpr int G = CN_BLOCK / HD;
+  __shared__ float sm[G][HD], sl[G], so[G][HD];
+  const int h = blockIdx.x, d = threadIdx.x % HD, g = threadIdx.x / HD;
+  const int s_eff = attn_active_splits(a, *a.pos + 1);
   const size_t base = (size_t)h * a.splits;
   float M = -INFINITY, L = 0.f, acc = 0.f;
-  for (int c0 = 0; c0 < s_eff; c0 += R) {
+  // The loads cover every split of the launch (their addresses do not depend
+  // on the position), so they are in flight before s_eff is known; inactive
+  // splits hold stale values and are masked out.
+  for (int c0 = g; c0 < a.splits; c0 += G * R) {
     float mc[R], lc[R], oc[R];
 #pragma unroll
     for (int c = 0; c < R; c++) {
-      const bool on = c0 + c < s_eff;
-      mc[c] = on ? a.part_ml[2 * (base + c0 + c)] : 0.f;
-      lc[c] = on ? a.part_ml[2 * (base + c0 + c) + 1] : 0.f;
-      oc[c] = on ? a.part_o[(base + c0 + c) * HD + d] : 0.f;
+      const int cs = c0 + G * c;
+      const bool in = cs < a.splits;
+      const float mr = in ? a.part_ml[2 * (base + cs)] : 0.f;
+      const float lr = in ? a.part_ml[2 * (base + cs) + 1] : 0.f;
+      const float orr = in ? a.part_o[(base + cs) * HD + d] : 0.f;
+      const bool on = cs < s_eff;
+      mc[c] = on ? mr : 0.f;
+      lc[c] = on ? lr : 0.f;
+      oc[c] = on ? orr : 0.f;
     }
     float Mn = M;
 #pragma unroll
@@ -208,7 +303,25 @@ __global__ __launch_bounds__(HD) void attn_merge_kernel(AttnArgs a) {
     }
     M = Mn;
   }
-  a.out[(size_t)h * HD + d] = acc / L;
+  sm[g][d] = M;
+  so[g][d] = acc;
+  if (d == 0) sl[g] = L;
+  __syncthreads();
+  if (g != 0) return;
+  float Mt = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < G; k++)
+    if (sl[k] > 0.f) Mt = fmaxf(Mt, sm[k][d]);
+  float Lt = 0.f, at = 0.f;
+#pragma unroll
+  for (int k = 0; k < G; k++) {
+    if (sl[k] > 0.f) {
+      const float f = expf(sm[k][d] - Mt);
+      Lt += sl[k] * f;
+      at += so[k][d] * f;
+    }
+  }
+  a.out[(size_t)h * HD + d] = at / Lt;
 }
 
 // GreedySampler.Sample: strict '>' scan => the lowest index of the maximum;
@@ -271,7 +384,7 @@ hipError_t attn_launch_t(const AttnArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((attn_decode_kernel<HD, F16, 1>), dim3(n_kv * a.splits), dim3(CN_BLOCK), 0, st, a);
   else
     hipLaunchKernelGGL((attn_decode_kernel<HD, F16, 8>), dim3(n_kv * a.splits), dim3(CN_BLOCK), 0, st, a);
-  hipLaunchKernelGGL((attn_merge_kernel<HD>), dim3(a.n_heads), dim3(HD), 0, st, a);
+  hipLaunchKernelGGL((attn_merge_kernel<HD>), dim3(a.n_heads), dim3(CN_BLOCK), 0, st, a);
   return hipGetLastError();
 }
 
@@ -285,7 +398,7 @@ hipError_t embed_launch(const void* emb, int type, int dim, const int* tok, floa
 }
 
 hipError_t attn_decode_launch(const AttnArgs& a, hipStream_t st) {
-  if (a.splits < 1 || a.splits > 64) return hipErrorInvalidValue;
+  if (a.splits < 1 || a.splits > 64 || a.chunk < 1 || a.head_dim % 16 != 0) return hipErrorInvalidValue;
   if (a.head_dim == 64) return a.kv_f16 ? attn_launch_t<64, true>(a, st) : attn_launch_t<64, false>(a, st);
   if (a.head_dim == 128) return a.kv_f16 ? attn_launch_t<128, true>(a, st) : attn_launch_t<128, false>(a, st);
   if (a.head_dim == 32) return a.kv_f16 ? attn_launch_t<32, true>(a, st) : attn_launch_t<32, false>(a, st);

@@ -111,7 +111,8 @@ struct AttnArgs {
   float scale;
   float* part_o;      // split partials: [n_heads][splits][head_dim]
   float* part_ml;     // [n_heads][splits][2] (max, sum)
-  int splits;         // most position chunks processed in parallel (<= 64)
+  int splits;         // position chunks of the launch (<= 64), one workgroup per kv head each
+  int chunk;          // positions per chunk: chunk c covers [c*chunk, (c+1)*chunk) below pos+1
 };
 hipError_t attn_decode_launch(const AttnArgs& a, hipStream_t st);
 
