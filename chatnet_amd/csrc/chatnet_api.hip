@@ -162,16 +162,21 @@ int bucket_cap(const chatnet_model* m, int seq) {
 }
 
 // Decode-attention launch for sequence lengths up to cap: chunks of at least
-// 32 positions (one step of the four waves), as many as attn_max_splits
-// allows.  chunk * splits >= cap, and every chunk starts below cap.
+// one round of the workgroup's wave steps, as many as attn_max_splits allows;
+// chunk * splits >= cap, and every chunk starts below cap.  Where two chunks
+// would do, one chunk of two rounds is used instead: its second round costs
+// less than the merge launch a second chunk needs.
 struct AttnPlan {
   int splits, chunk;
 };
 AttnPlan attn_plan(const chatnet_model* m, int cap) {
   const int smax = m->attn_splits_max;
+  const int round = attn_decode_round(m->cfg.head_dim, m->cfg.n_heads / m->cfg.n_kv_heads);
   int chunk = (cap + smax - 1) / smax;
-  if (chunk < 32) chunk = 32;
-  return {(cap + chunk - 1) / chunk, chunk};
+  if (chunk < round) chunk = round;
+  const int splits = (cap + chunk - 1) / chunk;
+  if (splits <= 2 && cap <= 2 * round) return {1, cap};
+  return {splits, chunk};
 }
 
 void drop_graphs(chatnet_model* m) {

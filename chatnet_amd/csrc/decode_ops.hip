@@ -78,45 +78,68 @@ __device__ __forceinline__ float row_sum16(float v) {
   return v;
 }
 
+// One (head, element) result of a split: the final output when the launch
+// has a single chunk (nothing to merge), else the split's partial.
+template <int HD>
+__device__ __forceinline__ void attn_put(const AttnArgs& a, int h, int split, int d, float M, float L, float acc) {
+  if (a.splits == 1) {
+    a.out[(size_t)h * HD + d] = acc / L;
+    return;
+  }
+  const size_t slot = (size_t)h * a.splits + split;
+  a.part_o[slot * HD + d] = acc;
+  if (d == 0) {
+    a.part_ml[2 * slot] = M;
+    a.part_ml[2 * slot + 1] = L;
+  }
+}
+
 // Split-position GQA decode attention (LlamaModel.ComputeAttention,
 // LlamaModel.cs:241-346): for query head h with kvh = h / kv_mul (:265),
 //   s[p] = (q_h . K[p][kvh]) * scale  for p <= pos,  w = softmax(s) (TensorMath.cs:177-241),
 //   out_h = sum_p w[p] V[p][kvh].
 // Grid = n_kv_heads x a.splits; workgroup (kvh, c) takes the positions
-// [c*chunk, (c+1)*chunk) below seq = pos+1.  A wave is 4 rows of 16 lanes: row
-// r holds one position, lane i of the row the head elements [i*EPL, (i+1)*EPL)
-// (EPL = HD/16).  A wave step covers 8 consecutive positions (two per row) for
-// KVM query heads of the group at once: 16-lane dot products reduced with DPP
-// inside the row, one max over the step's positions per head, one rescale of
-// the running (max, sum, o) per head (online softmax; sums and o stay per row
-// until the end).  The first step's K/V loads depend only on the chunk, so
-// they are in flight before the position arrives.  Rows, then the four waves
-// (through LDS), fold into one partial per split for attn_merge_kernel.
-template <int HD, bool F16, int KVM>
+// [c*chunk, (c+1)*chunk) below seq = pos+1.  Its four waves split the kv_mul
+// query heads WH ways (WH = 4, 2 or 1 as kv_mul allows, HPW heads per wave
+// and pass) and the positions WP = 4/WH ways.  A wave is 4 rows of 16 lanes:
+// row r holds one position, lane i of the row the head elements
+// [i*EPL, (i+1)*EPL) (EPL = HD/16).  A wave step covers SP = 4*PG consecutive
+// positions for the wave's heads: 16-lane dot products reduced with DPP inside
+// the row, one max over the step's positions per head, one rescale of the
+// running (max, sum, o) per head (online softmax; sums and o stay per row
+// until the end, then add across rows).  The first step's K/V loads depend
+// only on the chunk, so they are in flight before the position arrives.  With
+// WP = 1 each wave holds its heads' complete result for the chunk; otherwise
+// the WP waves of a head fold through LDS.  A launch of one chunk writes the
+// output itself; more chunks leave partials for attn_merge_kernel.
+template <int HD, bool F16, int HPW, int PG>
 __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
   constexpr int EPL = HD / 16;   // head elements per lane
-  constexpr int PG = 2;          // positions per row in a step
   constexpr int NW = CN_BLOCK / CN_WAVE;
   constexpr int SP = 4 * PG;     // positions per wave step
   const int kvh = blockIdx.x / a.splits;
   const int split = blockIdx.x % a.splits;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row = lane >> 4, col = lane & 15;
+  const int WH = a.kv_mul >= 4 ? 4 : (a.kv_mul >= 2 ? 2 : 1);
+  const int WP = NW / WH;
+  const int hw = wave % WH, pw = wave / WH;
   const int h0 = kvh * a.kv_mul;
   const int p0 = split * a.chunk;
   const int pcap = min(p0 + a.chunk, a.ctx);  // this split's positions, all inside the cache
   const size_t koff = (size_t)kvh * HD + col * EPL;
-  __shared__ float so[KVM * NW * HD];
-  __shared__ float sml[KVM * NW * 2];
+  __shared__ float so[NW * HPW * HD];
+  __shared__ float sml[NW * HPW * 2];
   const int seq = *a.pos + 1;
 
-  for (int jg = 0; jg < a.kv_mul; jg += KVM) {
-    const int nj = min(KVM, a.kv_mul - jg);
-    float q[KVM][EPL], m[KVM], l[KVM], o[KVM][EPL];
+  for (int jg = 0; jg < a.kv_mul; jg += WH * HPW) {
+    const int jb = jg + hw * HPW;                      // the wave's first head of this pass
+    const int nj = max(0, min(HPW, a.kv_mul - jb));    // its heads in this pass
+    float q[HPW][EPL], m[HPW], l[HPW], o[HPW][EPL];
 #pragma unroll
-    for (int j = 0; j < KVM; j++) {
+    for (int j = 0; j < HPW; j++) {
       if (j < nj) {
-        kv_load_n<false, EPL>(a.q, (size_t)(h0 + jg + j) * HD + col * EPL, q[j]);
+        kv_load_n<false, EPL>(a.q, (size_t)(h0 + jb + j) * HD + col * EPL, q[j]);
       } else {
 #pragma unroll
         for (int e = 0; e < EPL; e++) q[j][e] = 0.f;
@@ -127,12 +150,12 @@ __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
       for (int e = 0; e < EPL; e++) o[j][e] = 0.f;
     }
     // first step: positions below pcap regardless of seq
-    int pb = p0 + wave * SP;
+    int pb = p0 + pw * SP;
     float kr[PG][EPL], vr[PG][EPL];
 #pragma unroll
     for (int g = 0; g < PG; g++) {
       const int p = pb + 4 * g + row;
-      if (p < pcap) {
+      if (nj > 0 && p < pcap) {
         kv_load_n<F16, EPL>(a.kc, (size_t)p * a.kv_dim + koff, kr[g]);
         kv_load_n<F16, EPL>(a.vc, (size_t)p * a.kv_dim + koff, vr[g]);
       } else {
@@ -140,9 +163,9 @@ __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
         for (int e = 0; e < EPL; e++) kr[g][e] = vr[g][e] = 0.f;
       }
     }
-    const int p1 = min(seq, pcap);
+    const int p1 = nj > 0 ? min(seq, pcap) : 0;
     while (pb < p1) {  // uniform across the wave
-      float sc[PG][KVM];
+      float sc[PG][HPW];
 #pragma unroll
       for (int g = 0; g < PG; g++) {
         const bool on = pb + 4 * g + row < p1;
@@ -151,7 +174,7 @@ __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
 #pragma unroll
         for (int e = 0; e < EPL; e++) vr[g][e] = on ? vr[g][e] : 0.f;
 #pragma unroll
-        for (int j = 0; j < KVM; j++) {
+        for (int j = 0; j < HPW; j++) {
           float t = 0.f;
 #pragma unroll
           for (int e = 0; e < EPL; e++) t += q[j][e] * kr[g][e];
@@ -160,7 +183,7 @@ __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
         }
       }
 #pragma unroll
-      for (int j = 0; j < KVM; j++) {
+      for (int j = 0; j < HPW; j++) {
         if (j >= nj) break;
         float mx = sc[0][j];
 #pragma unroll
@@ -185,7 +208,7 @@ __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
         }
         m[j] = mn;
       }
-      pb += NW * SP;
+      pb += WP * SP;
       if (pb >= p1) break;
 #pragma unroll
       for (int g = 0; g < PG; g++) {
@@ -201,7 +224,8 @@ __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
     }
     // rows -> wave: sums and o add across the 4 rows (common running max)
 #pragma unroll
-    for (int j = 0; j < KVM; j++) {
+    for (int j = 0; j < HPW; j++) {
+      if (j >= nj) break;
       l[j] += __shfl_xor(l[j], 16, CN_WAVE);
       l[j] += __shfl_xor(l[j], 32, CN_WAVE);
 #pragma unroll
@@ -210,42 +234,51 @@ __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
         o[j][e] += __shfl_xor(o[j][e], 32, CN_WAVE);
       }
     }
-    // fold the NW wave partials of each head through LDS, one partial per split
-#pragma unroll
-    for (int j = 0; j < KVM; j++) {
-      if (j >= nj) break;
+    if (WP == 1) {
+      // the wave's heads are complete over the chunk (a split with positions
+      // has them all in wave step 0, so l > 0)
       if (row == 0) {
 #pragma unroll
-        for (int e = 0; e < EPL; e++) so[(j * NW + wave) * HD + col * EPL + e] = o[j][e];
+        for (int j = 0; j < HPW; j++) {
+          if (j >= nj) break;
+#pragma unroll
+          for (int e = 0; e < EPL; e++) attn_put<HD>(a, h0 + jb + j, split, col * EPL + e, m[j], l[j], o[j][e]);
+        }
+      }
+      continue;
+    }
+    // fold the WP position waves of each head through LDS (uniform branch)
+#pragma unroll
+    for (int j = 0; j < HPW; j++) {
+      if (row == 0) {
+#pragma unroll
+        for (int e = 0; e < EPL; e++) so[(wave * HPW + j) * HD + col * EPL + e] = o[j][e];
       }
       if (lane == 0) {
-        sml[2 * (j * NW + wave)] = m[j];
-        sml[2 * (j * NW + wave) + 1] = l[j];
+        sml[2 * (wave * HPW + j)] = j < nj ? m[j] : -INFINITY;
+        sml[2 * (wave * HPW + j) + 1] = j < nj ? l[j] : 0.f;
       }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < nj * HD; i += CN_BLOCK) {
-      const int j = i / HD, d = i % HD;
+    for (int i = threadIdx.x; i < WH * HPW * HD; i += CN_BLOCK) {
+      const int d = i % HD, jj = (i / HD) % HPW, hh = i / (HD * HPW);  // head jg + hh*HPW + jj
+      if (jg + hh * HPW + jj >= a.kv_mul) continue;
       float M = -INFINITY;
-#pragma unroll
-      for (int w = 0; w < NW; w++)
-        if (sml[2 * (j * NW + w) + 1] > 0.f) M = fmaxf(M, sml[2 * (j * NW + w)]);
+      for (int w = 0; w < WP; w++) {
+        const int sl = (w * WH + hh) * HPW + jj;
+        if (sml[2 * sl + 1] > 0.f) M = fmaxf(M, sml[2 * sl]);
+      }
       float L = 0.f, acc = 0.f;
-#pragma unroll
-      for (int w = 0; w < NW; w++) {
-        const float lw = sml[2 * (j * NW + w) + 1];
+      for (int w = 0; w < WP; w++) {
+        const int sl = (w * WH + hh) * HPW + jj;
+        const float lw = sml[2 * sl + 1];
         if (lw > 0.f) {
-          const float f = expf(sml[2 * (j * NW + w)] - M);
+          const float f = expf(sml[2 * sl] - M);
           L += lw * f;
-          acc += so[(j * NW + w) * HD + d] * f;
+          acc += so[sl * HD + d] * f;
         }
       }
-      const size_t slot = (size_t)(h0 + jg + j) * a.splits + split;
-      a.part_o[slot * HD + d] = acc;
-      if (d == 0) {
-        a.part_ml[2 * slot] = M;
-        a.part_ml[2 * slot + 1] = L;
-      }
+      attn_put<HD>(a, h0 + jg + hh * HPW + jj, split, d, M, L, acc);
     }
     __syncthreads();
   }
@@ -377,14 +410,34 @@ __global__ void set_state_kernel(int* state, int pos, int tok, int step) {
   if (step >= 0) state[2] = step;
 }
 
+// Heads per wave and pass for a group of kv_mul query heads (four waves split
+// the group when kv_mul >= 4), and positions per row per step (register
+// budget: K and V rows of the step, q and o of the wave's heads).
+int attn_hpw(int kv_mul) {
+  const int wh = kv_mul >= 4 ? 4 : (kv_mul >= 2 ? 2 : 1);
+  const int need = (kv_mul + wh - 1) / wh;
+  return need <= 1 ? 1 : (need <= 2 ? 2 : 4);
+}
+// (One head per wave at head_dim 128 keeps 8-position steps: four waves then
+// cover 32 positions a round, and more chunks spread the work.)
+constexpr int attn_pg(int hd, int hpw) {
+  return hd <= 64 ? (hpw <= 2 ? 8 : 4) : (hd == 128 ? (hpw == 1 ? 2 : 4) : 2);
+}
+
+template <int HD, bool F16, int HPW>
+void attn_launch_k(const AttnArgs& a, hipStream_t st) {
+  const int n_kv = a.n_heads / a.kv_mul;
+  hipLaunchKernelGGL((attn_decode_kernel<HD, F16, HPW, attn_pg(HD, HPW)>), dim3(n_kv * a.splits), dim3(CN_BLOCK), 0,
+                     st, a);
+}
+
 template <int HD, bool F16>
 hipError_t attn_launch_t(const AttnArgs& a, hipStream_t st) {
-  const int n_kv = a.n_heads / a.kv_mul;
-  if (a.kv_mul == 1)
-    hipLaunchKernelGGL((attn_decode_kernel<HD, F16, 1>), dim3(n_kv * a.splits), dim3(CN_BLOCK), 0, st, a);
-  else
-    hipLaunchKernelGGL((attn_decode_kernel<HD, F16, 8>), dim3(n_kv * a.splits), dim3(CN_BLOCK), 0, st, a);
-  hipLaunchKernelGGL((attn_merge_kernel<HD>), dim3(a.n_heads), dim3(CN_BLOCK), 0, st, a);
+  const int hpw = attn_hpw(a.kv_mul);
+  if (hpw == 1) attn_launch_k<HD, F16, 1>(a, st);
+  else if (hpw == 2 || HD > 128) attn_launch_k<HD, F16, 2>(a, st);
+  else attn_launch_k<HD, F16, 4>(a, st);
+  if (a.splits > 1) hipLaunchKernelGGL((attn_merge_kernel<HD>), dim3(a.n_heads), dim3(CN_BLOCK), 0, st, a);
   return hipGetLastError();
 }
 
@@ -395,6 +448,13 @@ hipError_t embed_launch(const void* emb, int type, int dim, const int* tok, floa
   hipLaunchKernelGGL(embed_kernel, dim3((dim + CN_BLOCK - 1) / CN_BLOCK, n), dim3(CN_BLOCK), 0, st, emb,
                      type, dim, tok, x);
   return hipGetLastError();
+}
+
+int attn_decode_round(int head_dim, int kv_mul) {
+  const int wh = kv_mul >= 4 ? 4 : (kv_mul >= 2 ? 2 : 1);
+  int hpw = attn_hpw(kv_mul);
+  if (head_dim > 128 && hpw > 2) hpw = 2;
+  return (4 / wh) * 4 * attn_pg(head_dim, hpw);
 }
 
 hipError_t attn_decode_launch(const AttnArgs& a, hipStream_t st) {

@@ -115,6 +115,8 @@ struct AttnArgs {
   int chunk;          // positions per chunk: chunk c covers [c*chunk, (c+1)*chunk) below pos+1
 };
 hipError_t attn_decode_launch(const AttnArgs& a, hipStream_t st);
+// Positions one decode-attention workgroup covers per round of wave steps.
+int attn_decode_round(int head_dim, int kv_mul);
 
 // Greedy argmax (GreedySampler.Sample, GreedySampler.cs:13-26); writes the
 // winner to state[1] and appends it to out_tokens[state[2]++], and advances
