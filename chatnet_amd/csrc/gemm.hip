@@ -43,7 +43,9 @@ __device__ __forceinline__ const uint32_t* gemm_row_ptr(const GemmArgs& a, int v
       }
     }
   }
-  return reinterpret_cast<const uint32_t*>(a.w[seg]) + (size_t)r * row_dw;
+  // a select, not a[seg]: indexing the argument array would copy it to scratch
+  const uint8_t* w = seg == 0 ? a.w[0] : (seg == 1 ? a.w[1] : a.w[2]);
+  return reinterpret_cast<const uint32_t*>(w) + (size_t)r * row_dw;
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }

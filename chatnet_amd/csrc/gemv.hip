@@ -301,15 +301,8 @@ __device__ __forceinline__ void dot_unit_q4_0(const uint32_t (*w)[9], const floa
 // (pair bytes 2..17) is realigned with alignbyte, block B's (bytes 20..35)
 // is dword aligned.
 template <int RPW>
-__device__ __forceinline__ void dot_unit_q4_0_dig(const uint32_t (*w)[9], const uint32_t* xd, float* acc) {
-  uint32_t X[40];
-#pragma unroll
-  for (int c = 0; c < 10; c++) {
-    const uint4 t = *reinterpret_cast<const uint4*>(xd + 4 * c);
-    X[4 * c + 0] = t.x; X[4 * c + 1] = t.y; X[4 * c + 2] = t.z; X[4 * c + 3] = t.w;
-  }
-  const uint2 se = *reinterpret_cast<const uint2*>(xd + 40);
-  const int sA = (int)se.x, sB = (int)se.y;
+__device__ __forceinline__ void dot_q4_0_digits(const uint32_t (*w)[9], const uint32_t (&X)[40], int sA, int sB,
+                                                float* acc) {
 #pragma unroll
   for (int i = 0; i < RPW; i++) {
     uint32_t qa[4], qb[4];
@@ -335,6 +328,18 @@ __device__ __forceinline__ void dot_unit_q4_0_dig(const uint32_t (*w)[9], const 
     const float db = ldexpf(cn_h2f(w[i][4] >> 16), -sB);
     acc[i] += (float)ta * da + (float)tb * db;
   }
+}
+
+template <int RPW>
+__device__ __forceinline__ void dot_unit_q4_0_dig(const uint32_t (*w)[9], const uint32_t* xd, float* acc) {
+  uint32_t X[40];
+#pragma unroll
+  for (int c = 0; c < 10; c++) {
+    const uint4 t = *reinterpret_cast<const uint4*>(xd + 4 * c);
+    X[4 * c + 0] = t.x; X[4 * c + 1] = t.y; X[4 * c + 2] = t.z; X[4 * c + 3] = t.w;
+  }
+  const uint2 se = *reinterpret_cast<const uint2*>(xd + 40);
+  dot_q4_0_digits<RPW>(w, X, (int)se.x, (int)se.y, acc);
 }
 
 // Q4_K super-block in the reference's order (DequantQ4K.cs:59-72): sub-block s
@@ -451,6 +456,21 @@ __device__ __forceinline__ void dot_unit(const uint32_t (*w)[QTraits<QT>::NDW], 
   else dot_unit_q6_k<RPW>(w, xs, sx16, acc);
 }
 
+// Segment base pointer and row count by run-time segment index, chosen with
+// masks: indexing the kernel-argument arrays (or a select chain, which the
+// compiler turns into a table) would copy them to scratch, and a scratch load
+// waits on every vector-memory operation in flight.
+__device__ __forceinline__ const uint8_t* seg_w(const GemvArgs& a, int seg) {
+  const uintptr_t w0 = reinterpret_cast<uintptr_t>(a.w[0]);
+  const uintptr_t w1 = reinterpret_cast<uintptr_t>(a.w[1]);
+  const uintptr_t w2 = reinterpret_cast<uintptr_t>(a.w[2]);
+  const uintptr_t m1 = 0 - (uintptr_t)(seg == 1), m2 = 0 - (uintptr_t)(seg == 2);
+  return reinterpret_cast<const uint8_t*>(w0 ^ ((w0 ^ w1) & m1) ^ ((w0 ^ w2) & m2));
+}
+__device__ __forceinline__ int seg_n(const GemvArgs& a, int seg) {
+  return seg == 0 ? a.seg_rows[0] : (seg == 1 ? a.seg_rows[1] : a.seg_rows[2]);
+}
+
 // Virtual row -> (segment, row-in-segment).
 template <int EPI>
 __device__ __forceinline__ void map_row(const GemvArgs& a, int vr, int& seg, int& r) {
@@ -533,12 +553,17 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, const float
         a.out[0][r + 1] = x1;
       } else {
         const size_t off = (size_t)pos * a.kv_dim + r;
+        // K or V cache base chosen arithmetically: a select of the two pointer
+        // arguments compiles to a scratch table whose load waits on every
+        // vector-memory operation in flight
+        const uintptr_t kb = reinterpret_cast<uintptr_t>(a.kcache), vb = reinterpret_cast<uintptr_t>(a.vcache);
+        const uintptr_t base = vb + ((kb - vb) & (uintptr_t)(0 - (uintptr_t)(seg == 1)));
         if (a.kv_f16) {
-          _Float16* dst = reinterpret_cast<_Float16*>(seg == 1 ? a.kcache : a.vcache) + off;
+          _Float16* dst = reinterpret_cast<_Float16*>(base) + off;
           dst[0] = (_Float16)x0;
           dst[1] = (_Float16)x1;
         } else {
-          float* dst = reinterpret_cast<float*>(seg == 1 ? a.kcache : a.vcache) + off;
+          float* dst = reinterpret_cast<float*>(base) + off;
           dst[0] = x0;
           dst[1] = x1;
         }
@@ -559,7 +584,7 @@ __device__ __forceinline__ void issue_loads(const GemvArgs& a, int it, int sub, 
     const bool ok = vr < a.n_vrows;
     int seg, r;
     map_row<EPI>(a, ok ? vr : 0, seg, r);
-    const uint8_t* rp = a.w[seg] + (size_t)r * bpr;
+    const uint8_t* rp = seg_w(a, seg) + (size_t)r * bpr;
 #pragma unroll
     for (int n = 0; n < NU; n++) {
       const int u = li + LPR * n;

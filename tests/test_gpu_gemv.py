@@ -97,3 +97,4 @@ def test_batched_columns_match_per_column_gemv(N):
     for n in range(0, N, max(1, N // 4)):
         r = oracle.matvec(2, t.data, x[n], M, K)
         assert normwise(y[n], r) <= 1e-2
+

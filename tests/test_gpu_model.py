@@ -214,3 +214,54 @@ def test_long_context_decode_attention_matches_oracle():
         # the 8th decode step forwarded the 8th token at position 2007
         r = oracle.OracleLlama(cfg, ck).forward(list(toks) + list(o), 0)
         assert np.max(np.abs(logits_g - r)) <= LOGIT_TOL
+
+
+# -- decode attention layouts: the four waves of a workgroup split the query
+# heads of a kv head (kv_mul >= 4: 1, 2 or 4 heads per wave), or split the
+# positions and fold through LDS (kv_mul 1, 2); buckets of one chunk write the
+# output directly, larger ones merge chunks.  The prompt runs as one span and
+# the decode crosses the 64 and 128 position buckets.
+@pytest.mark.parametrize("head_dim,n_heads,n_kv,kv", [
+    (128, 4, 4, _native.KV_F32),   # kv_mul 1: positions over four waves
+    (128, 4, 2, _native.KV_F32),   # kv_mul 2: two head waves x two position waves
+    (64, 8, 2, _native.KV_F32),    # kv_mul 4: one head per wave
+    (64, 16, 1, _native.KV_F32),   # kv_mul 16: four heads per wave
+    (32, 8, 1, _native.KV_F32),    # kv_mul 8, head_dim 32
+    (128, 4, 4, _native.KV_F16),
+])
+def test_decode_attention_layouts_match_oracle(head_dim, n_heads, n_kv, kv):
+    cfg = TINY_TEST.replace(dim=head_dim * n_heads, hidden_dim=512, n_heads=n_heads, n_kv_heads=n_kv,
+                            head_dim=head_dim, context_length=300, kv_dtype=kv)
+    ck = synth.llama_checkpoint(cfg, seed=36, mix="q4_0")
+    prompt = synth.tokens(36, "prompt", 60, cfg.vocab_size)
+    announce(f"decode attention layout hd={head_dim} heads={n_heads} kv={n_kv} kvtype={kv}")
+    with HipLlamaModel(cfg, ck) as m:
+        m.forward(prompt, 0)
+        g = m.decode_greedy(80)
+        logits_g = m.get_logits()
+    o, margins = oracle.OracleLlama(cfg, ck).generate_greedy(list(prompt), 80)
+    n = compare_greedy(list(g), o, margins)
+    if n == 80:
+        r = oracle.OracleLlama(cfg, ck).forward(list(prompt) + list(o), 0)
+        tol = LOGIT_TOL if kv == _native.KV_F32 else 2 * LOGIT_TOL
+        assert np.max(np.abs(logits_g - r)) <= tol
+
+
+def test_llama7b_layer_decode_matches_oracle():
+    """7B-shaped layer decode: QKV 12288x4096, O, gate/up 22016x4096, down
+    4096x11008 and the LM head at their real shapes; tokens and logits match
+    the oracle."""
+    from chatnet_amd import LLAMA2_7B
+    cfg = LLAMA2_7B.replace(n_layers=1, context_length=64)
+    ck = synth.llama_checkpoint(cfg, seed=37, mix="q4_0")
+    prompt = synth.tokens(37, "prompt", 8, cfg.vocab_size)
+    announce("7b layer decode")
+    with HipLlamaModel(cfg, ck) as m:
+        m.forward(prompt, 0)
+        g = m.decode_greedy(8)
+        lg = m.get_logits()
+    o, margins = oracle.OracleLlama(cfg, ck).generate_greedy(list(prompt), 8)
+    n = compare_greedy(list(g), o, margins)
+    if n == 8:
+        r = oracle.OracleLlama(cfg, ck).forward(list(prompt) + list(o), 0)
+        assert np.max(np.abs(lg - r)) <= LOGIT_TOL
