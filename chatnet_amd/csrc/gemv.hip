@@ -67,9 +67,11 @@ __device__ __forceinline__ int xidx(int k) {
 // about 4e-6.
 // LDS record of unit u (blocks 2u and 2u+1): 44 dwords,
 //   dword blk*20 + d*4 + k: nibble 2i = digit d of element 4k+i, nibble 2i+1 =
-//   digit d of element 16+4k+i (the nibble order of qs dword k);
-//   dword 40 + blk = s_b.  The 44-dword stride keeps 16-byte reads of 16
-//   neighbouring lanes on distinct banks.
+//   digit d of element 16+4k+i (the nibble order of qs dword k, and of a Q4_K
+//   sub-block's 16 qs bytes, DequantQ4K.cs:59-72);
+//   dword 40 + blk = s_b;  dword 42 + blk = sum_j X_j of the block (written
+//   for the Q4_K dot, whose per-block min term needs it).  The 44-dword stride
+//   keeps 16-byte reads of 16 neighbouring lanes on distinct banks.
 // ---------------------------------------------------------------------------
 constexpr int XD_UNIT_DW = 44;
 
@@ -127,7 +129,7 @@ __device__ __forceinline__ void stage_load(const float* __restrict__ x, const fl
 // to every element; each wave leaves its share of sum x^2 in red[wave] for the
 // caller to combine after its __syncthreads().  The four items of a block sit
 // in adjacent lanes and share the block maximum through two xor-shuffles.
-template <int MAXT, bool NORM, int BS>
+template <int MAXT, bool NORM, int BS, bool BSUM = false>
 __device__ __forceinline__ void stage_digitize(const XStage<MAXT, NORM>& st, int K, uint32_t* xd, float* red) {
   const int ntask = K >> 3;
   float ss = 0.f;
@@ -186,12 +188,23 @@ __device__ __forceinline__ void stage_digitize(const XStage<MAXT, NORM>& st, int
     dw[2] = __builtin_amdgcn_perm(eb, ea, 0x07060302u) ^ 0x88888888u;
     dw[3] = __builtin_amdgcn_perm(ob, oa, 0x07060302u) ^ 0x88888888u;
     dw[4] = __builtin_amdgcn_perm(ed, ec, 0x05040100u) ^ 0x88888888u;
+    int bs = 0;
+    if constexpr (BSUM) {
+      // X_i = (low 20 bits of tl/th) - 0x88888; the block sum over its 4 items
+#pragma unroll
+      for (int i = 0; i < 4; i++) bs += (int)(tl[i] & 0xFFFFFu) + (int)(th[i] & 0xFFFFFu) - 2 * 0x88888;
+      bs += __shfl_xor(bs, 1, CN_WAVE);
+      bs += __shfl_xor(bs, 2, CN_WAVE);
+    }
     if (on) {
       uint32_t* rec = xd + (b >> 1) * XD_UNIT_DW;
       const int blk = b & 1;
 #pragma unroll
       for (int d = 0; d < 5; d++) rec[blk * 20 + d * 4 + k] = dw[d];
-      if (k == 0) rec[40 + blk] = (uint32_t)s;
+      if (k == 0) {
+        rec[40 + blk] = (uint32_t)s;
+        if constexpr (BSUM) rec[42 + blk] = (uint32_t)bs;
+      }
     }
   }
   ss = cn_wave_sum(ss);
@@ -340,6 +353,63 @@ __device__ __forceinline__ void dot_unit_q4_0_dig(const uint32_t (*w)[9], const 
   }
   const uint2 se = *reinterpret_cast<const uint2*>(xd + 40);
   dot_q4_0_digits<RPW>(w, X, (int)se.x, (int)se.y, acc);
+}
+
+// Q4_K super-block (reference order, DequantQ4K.cs:59-72) against the digit
+// records of its 8 blocks (4 records).  Sub-block s's qs dwords XOR 0x88888888
+// are (q - 8) as signed nibbles in the digit records' nibble order, so with
+// T_s = sum_j (q_j - 8) X_j from the Horner sum of sdot8 over the 5 digits,
+//   sum_j q_j X_j = T_s + 8 SX_s   (SX_s = sum_j X_j, exact in int32),
+// and the sub-block contributes 2^-e_s (d sc_s (T_s + 8 SX_s) - dmin m_s SX_s):
+// d sc q - dmin m per weight (DequantQ4K.cs:59-72) against x rounded to its
+// digits, as the Q4_0 digit dot.
+template <int RPW>
+__device__ __forceinline__ void dot_unit_q4_k_dig(const uint32_t (*w)[36], const uint32_t* xd, float* acc) {
+  float dsc[RPW][8], dmm[RPW][8];
+#pragma unroll
+  for (int i = 0; i < RPW; i++) {
+    const float d = cn_h2f(w[i][0]), dmin = cn_h2f(w[i][0] >> 16);
+    const uint32_t q0 = w[i][1], q1 = w[i][2], q2 = w[i][3];  // scale bytes 0..11
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      int sc, m;
+      if (j < 4) {
+        sc = (q0 >> (8 * j)) & 63;
+        m = (q1 >> (8 * j)) & 63;
+      } else {
+        const uint32_t b8 = (q2 >> (8 * (j - 4))) & 0xFF;
+        sc = (b8 & 0xF) | (((q0 >> (8 * (j - 4) + 6)) & 3) << 4);
+        m = (b8 >> 4) | (((q1 >> (8 * (j - 4) + 6)) & 3) << 4);
+      }
+      dsc[i][j] = d * (float)sc;
+      dmm[i][j] = dmin * (float)m;
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < 8; s++) {
+    const uint32_t* rec = xd + (s >> 1) * XD_UNIT_DW;
+    const int blk = s & 1;
+    uint32_t X[20];
+#pragma unroll
+    for (int c = 0; c < 5; c++) {
+      const uint4 t = *reinterpret_cast<const uint4*>(rec + blk * 20 + 4 * c);
+      X[4 * c + 0] = t.x; X[4 * c + 1] = t.y; X[4 * c + 2] = t.z; X[4 * c + 3] = t.w;
+    }
+    const int e = (int)rec[40 + blk];
+    const int sx = (int)rec[42 + blk];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      int t = 0;
+#pragma unroll
+      for (int dg = 4; dg >= 0; dg--) {
+        if (dg < 4) t <<= 4;
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+          t = __builtin_amdgcn_sdot8((int)(w[i][4 + 4 * s + k] ^ 0x88888888u), (int)X[dg * 4 + k], t, false);
+      }
+      acc[i] += ldexpf(dsc[i][s] * (float)(t + 8 * sx) - dmm[i][s] * (float)sx, -e);
+    }
+  }
 }
 
 // Q4_K super-block in the reference's order (DequantQ4K.cs:59-72): sub-block s
@@ -632,9 +702,12 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
   const int pos = EPI == GEMV_EPI_QKV ? *a.pos : 0;
 
   // ---- prologue: stage x (optionally RMS-normalised) into LDS ----
-  if constexpr (QT == QT_Q4_0) {
-    // items per thread: K <= 64 * LPR * NU, so K/8 <= 8 * LPR * NU items over BS threads
-    constexpr int MAXT = (8 * LPR * NU + BS - 1) / BS;
+  // Integer digit path: Q4_0, and Q4_K for K <= 8192 (the register budget of
+  // the staged x at 32 items per super-block lane).
+  constexpr bool kDigits = QT == QT_Q4_0 || (QT == QT_Q4_K && LPR <= 32);
+  if constexpr (kDigits) {
+    // items per thread: K <= UNIT * LPR * NU, so K/8 <= (UNIT/8) * LPR * NU items over BS threads
+    constexpr int MAXT = ((UNIT / 8) * LPR * NU + BS - 1) / BS;
     constexpr bool NORM = EPI == GEMV_EPI_QKV || EPI == GEMV_EPI_SWIGLU || EPI == GEMV_EPI_LOGITS;
     XStage<MAXT, NORM> st;
     stage_load<MAXT, NORM, BS>(a.x, a.norm_w, K, st);
@@ -642,8 +715,8 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
     issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
     load_residual<EPI, RPW>(a, it * RW + sub * RPW, li, pos, res);
     uint32_t* xd = reinterpret_cast<uint32_t*>(smem);
-    float* xred = reinterpret_cast<float*>(smem) + (size_t)nunits * XD_UNIT_DW;
-    stage_digitize<MAXT, NORM, BS>(st, K, xd, xred);
+    float* xred = reinterpret_cast<float*>(smem) + (size_t)(K >> 6) * XD_UNIT_DW;
+    stage_digitize<MAXT, NORM, BS, QT == QT_Q4_K>(st, K, xd, xred);
     __syncthreads();
     float ss = 0.f;
 #pragma unroll
@@ -657,12 +730,13 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
       for (int n = 0; n < NU; n++) {
         const int u = li + LPR * n;
         if (u < nunits) {
-          uint32_t wu[RPW][9];
+          uint32_t wu[RPW][T::NDW];
 #pragma unroll
           for (int i = 0; i < RPW; i++)
 #pragma unroll
-            for (int k = 0; k < 9; k++) wu[i][k] = w[i][n][k];
-          dot_unit_q4_0_dig<RPW>(wu, xd + u * XD_UNIT_DW, acc);
+            for (int k = 0; k < T::NDW; k++) wu[i][k] = w[i][n][k];
+          if constexpr (QT == QT_Q4_0) dot_unit_q4_0_dig<RPW>(wu, xd + u * XD_UNIT_DW, acc);
+          else dot_unit_q4_k_dig<RPW>(wu, xd + 4 * u * XD_UNIT_DW, acc);
         }
       }
       const int cur = it;
@@ -765,7 +839,8 @@ template <int QT>
 size_t gemv_smem_bytes(int K) {
   using T = QTraits<QT>;
   const int nunits = K / T::UNIT;
-  if (QT == QT_Q4_0) return ((size_t)nunits * XD_UNIT_DW + 16) * sizeof(uint32_t);  // + one float per wave
+  // digit records (Q4_0; Q4_K up to 32 super-blocks per row) + one float per wave
+  if (QT == QT_Q4_0 || (QT == QT_Q4_K && nunits <= 32)) return ((size_t)(K >> 6) * XD_UNIT_DW + 16) * sizeof(uint32_t);
   size_t f = (size_t)nunits * (T::UNIT + 4) + (K >> 5) + (QT == QT_Q6_K ? (K >> 4) : 0) + 4;
   return f * sizeof(float);
 }
