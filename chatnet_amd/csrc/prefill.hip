@@ -64,6 +64,9 @@ __global__ __launch_bounds__(CN_BLOCK) void rope_kv_kernel(RopeKvArgs a) {
   }
 }
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 template <bool F16>
 __device__ __forceinline__ float4 kv_load4(const void* base, size_t idx) {
   if constexpr (F16) {
@@ -74,15 +77,25 @@ __device__ __forceinline__ float4 kv_load4(const void* base, size_t idx) {
   }
 }
 
-__device__ __forceinline__ float group16_max(float v) {
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, CN_WAVE));
-  return v;
+__device__ __forceinline__ uint32_t bf16_bits(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
+
+// (a, b) as packed bf16 high parts and packed bf16 low parts (hi + lo carries
+// ~16 significant bits; an f16 value is represented exactly).
+__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  const __bf16 ha = (__bf16)a, hb = (__bf16)b;
+  hi = (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+  lo = bf16_bits(a - (float)ha) | (bf16_bits(b - (float)hb) << 16);
 }
-__device__ __forceinline__ float group16_sum(float v) {
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, CN_WAVE);
-  return v;
+
+__device__ __forceinline__ void split4(float a, float b, float c, float d, uint2& hi, uint2& lo) {
+  split2(a, b, hi.x, lo.x);
+  split2(c, d, hi.y, lo.y);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
 // Causal GQA attention of a span (LlamaModel.ComputeAttention,
@@ -90,171 +103,262 @@ __device__ __forceinline__ float group16_sum(float v) {
 // p0+t, query head h, kv head h / kv_mul,
 //   out[t][h] = softmax_p<=p0+t( q . K[p] * scale ) . V[p].
 // A workgroup owns 64 rows = QB consecutive tokens x the kv_mul query heads of
-// one kv head (QB = 64 / kv_mul), so each K/V chunk of 64 positions staged in
-// LDS serves all of them.  Thread (tr, tc) = (tid / 16, tid % 16) scores rows
-// 4tr..4tr+3 against keys tc + 16j, keeps the online-softmax state of its rows
-// (the 16 threads of a row group reduce with shuffles), and accumulates
-// out[rows][4tc + 64e .. +3].  fp32 throughout; output written as bf16 (and
-// its low part, when out_lo is given) for the O-projection GEMM.
+// one kv head (QB = 64 / kv_mul); wave w owns rows 16w..16w+15, lane l the
+// row 16w + l%16.  K/V are walked in chunks of 64 positions, staged in LDS as
+// bf16 high and low parts (K row-major, V transposed), and both products run
+// on v_mfma_f32_16x16x32_bf16 with three passes (hi*hi + hi*lo + lo*hi):
+//  - S^T = K Q^T: 16 keys x 16 rows per tile, q held in registers as the B
+//    operand; lane l gets the scores of its row against keys 4*(l/16)+0..3 of
+//    each tile, so the online softmax (exp2 of scores prescaled by
+//    scale*log2 e) is per lane, with two shuffles for the chunk maximum;
+//  - O^T = V^T P^T: the probabilities stay in registers as the B operand (the
+//    8 k-values of lane l are the 8 keys it scored in two adjacent tiles, and
+//    V^T is stored in LDS with its keys in that same order), and lane l
+//    accumulates dims 16i + 4*(l/16)+0..3 of its row.
+// The workgroup's 8 waves form two groups of 4 that walk alternate chunks
+// (group 0 the even ones) with LDS buffers of their own, so two waves share
+// each SIMD and the chain of chunks per group is half as long; group 1 hands
+// its softmax state and unnormalised output to group 0 through LDS at the end.
+// Each group's next chunk is loaded into registers while it computes the
+// current one.  The output is written as bf16 (and its low part, when out_lo
+// is given) for the O-projection GEMM.
+constexpr int kSpanThreads = 512;
+
+template <int HD>
+constexpr int span_group_lds() {  // bf16 elements of one group's K/V buffers
+  return 2 * 64 * (HD + 8) + 2 * HD * (64 + 8);
+}
+
 template <int HD, bool F16>
-__global__ __launch_bounds__(CN_BLOCK) void attn_prefill_kernel(PrefillAttnArgs a) {
-  constexpr int R = 64, KB = 64;
-  constexpr int S = HD + 4;   // padded LDS row (floats)
-  constexpr int OE = HD / 64; // float4 output groups per thread (HD 64 -> 1, 128 -> 2)
-  extern __shared__ float lds[];
-  float* Qs = lds;            // [R][S]
-  float* Ks = Qs + R * S;     // [KB][S]
-  float* Vs = Ks + KB * S;    // [KB][S]
-  float* Ps = Vs + KB * S;    // [R][KB + 4]
-  constexpr int PS = KB + 4;
+__global__ __launch_bounds__(kSpanThreads) void attn_prefill_kernel(PrefillAttnArgs a) {
+  constexpr int KB = 64;                               // positions per chunk
+  constexpr int KP = HD + 8;                           // K row pitch (bf16)
+  constexpr int VP = KB + 8;                           // V^T row pitch (bf16)
+  constexpr int NS = HD / 32;                          // k-steps of q . k
+  constexpr int NT = HD / 16;                          // 16-dim output tiles
+  constexpr int GT = kSpanThreads / 2;                 // threads per group
+  constexpr int KU = KB * (HD / 4) / GT;               // K float4 loads per thread
+  constexpr int VU = (KB / 4) * (HD / 4) / GT;         // V 4x4 blocks per thread
+  extern __shared__ __align__(16) uint16_t lds_b[];
+  const int grp = threadIdx.x / GT;
+  uint16_t* Kh = lds_b + grp * span_group_lds<HD>();
+  uint16_t* Kl = Kh + KB * KP;
+  uint16_t* Vh = Kl + KB * KP;
+  uint16_t* Vl = Vh + HD * VP;
 
+  const int tid = threadIdx.x % GT, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 4, c = lane & 15;
   const int kvh = blockIdx.x;
-  const int qb = blockIdx.y;
-  const int QB = R / a.kv_mul;
-  const int t0 = qb * QB;
-  const int tid = threadIdx.x;
-  const int tr = tid >> 4, tc = tid & 15;
-
-  // Q rows: r -> token t0 + r / kv_mul, head kvh*kv_mul + r % kv_mul
-  for (int i = tid; i < R * (HD / 4); i += CN_BLOCK) {
-    const int r = i / (HD / 4), d4 = i % (HD / 4);
-    const int t = t0 + r / a.kv_mul, hh = kvh * a.kv_mul + r % a.kv_mul;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (t < a.n) v = *reinterpret_cast<const float4*>(a.qkv + (size_t)t * a.ld + hh * HD + 4 * d4);
-    *reinterpret_cast<float4*>(&Qs[r * S + 4 * d4]) = v;
-  }
-
-  int qpos[4];
-#pragma unroll
-  for (int k = 0; k < 4; k++) {
-    const int r = 4 * tr + k;
-    const int t = t0 + r / a.kv_mul;
-    qpos[k] = t < a.n ? a.p0 + t : -1;  // -1: padding row, every key masked
-  }
+  const int QB = 64 / a.kv_mul;
+  const int t0 = (gridDim.y - 1 - blockIdx.y) * QB;  // longest key ranges dispatched first
+  const int r = 16 * w + c;
+  const int t = t0 + r / a.kv_mul, hh = kvh * a.kv_mul + r % a.kv_mul;
+  const int qpos = t < a.n ? a.p0 + t : -1;  // -1: padding row, every key masked
   const int t_last = min(a.n, t0 + QB) - 1;
-  const int kend = a.p0 + t_last + 1;  // keys [0, kend)
+  const int kend = a.p0 + t_last + 1;        // keys [0, kend)
 
-  float m_run[4], l_run[4];
-  float4 o[4][OE];
+  // q of row r: k-step s, lane group g holds dims 32s + 8g .. +7
+  float4 qr[NS][2];
 #pragma unroll
-  for (int k = 0; k < 4; k++) {
-    m_run[k] = -INFINITY;
-    l_run[k] = 0.f;
-#pragma unroll
-    for (int e = 0; e < OE; e++) o[k][e] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-
-  for (int c0 = 0; c0 < kend; c0 += KB) {
-    __syncthreads();  // previous chunk's readers are done (and Q is staged)
-    for (int i = tid; i < KB * (HD / 4); i += CN_BLOCK) {
-      const int kk = i / (HD / 4), d4 = i % (HD / 4);
-      const int p = c0 + kk;
-      float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-      if (p < kend) {
-        const size_t idx = (size_t)p * a.kv_dim + kvh * HD + 4 * d4;
-        kv = kv_load4<F16>(a.kc, idx);
-        vv = kv_load4<F16>(a.vc, idx);
-      }
-      *reinterpret_cast<float4*>(&Ks[kk * S + 4 * d4]) = kv;
-      *reinterpret_cast<float4*>(&Vs[kk * S + 4 * d4]) = vv;
-    }
-    __syncthreads();
-
-    // scores of rows 4tr..+3 x keys tc + 16j
-    float s[4][4];
-#pragma unroll
-    for (int k = 0; k < 4; k++)
-#pragma unroll
-      for (int j = 0; j < 4; j++) s[k][j] = 0.f;
-#pragma unroll 4
-    for (int d = 0; d < HD; d += 4) {
-      float4 q[4], kk[4];
-#pragma unroll
-      for (int k = 0; k < 4; k++) q[k] = *reinterpret_cast<const float4*>(&Qs[(4 * tr + k) * S + d]);
-#pragma unroll
-      for (int j = 0; j < 4; j++) kk[j] = *reinterpret_cast<const float4*>(&Ks[(tc + 16 * j) * S + d]);
-#pragma unroll
-      for (int k = 0; k < 4; k++)
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-          s[k][j] += q[k].x * kk[j].x + q[k].y * kk[j].y + q[k].z * kk[j].z + q[k].w * kk[j].w;
-    }
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      float mx = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int p = c0 + tc + 16 * j;
-        s[k][j] = (p <= qpos[k]) ? s[k][j] * a.scale : -INFINITY;
-        mx = fmaxf(mx, s[k][j]);
-      }
-      mx = group16_max(mx);
-      const float m_new = fmaxf(m_run[k], mx);
-      // rows with every key so far masked keep m = -inf and contribute nothing
-      const float alpha = (m_new == -INFINITY) ? 1.f : expf(m_run[k] - m_new);
-      float sum = 0.f;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const float p = (m_new == -INFINITY) ? 0.f : expf(s[k][j] - m_new);
-        s[k][j] = p;
-        sum += p;
-      }
-      sum = group16_sum(sum);
-      l_run[k] = l_run[k] * alpha + sum;
-      m_run[k] = m_new;
-#pragma unroll
-      for (int e = 0; e < OE; e++) {
-        o[k][e].x *= alpha; o[k][e].y *= alpha; o[k][e].z *= alpha; o[k][e].w *= alpha;
-      }
-#pragma unroll
-      for (int j = 0; j < 4; j++) Ps[(4 * tr + k) * PS + tc + 16 * j] = s[k][j];
-    }
-    __syncthreads();
-    const int nk = min(KB, kend - c0);
-    for (int kk = 0; kk < nk; kk++) {
-      float p[4];
-#pragma unroll
-      for (int k = 0; k < 4; k++) p[k] = Ps[(4 * tr + k) * PS + kk];
-#pragma unroll
-      for (int e = 0; e < OE; e++) {
-        const float4 v = *reinterpret_cast<const float4*>(&Vs[kk * S + 64 * e + 4 * tc]);
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-          o[k][e].x += p[k] * v.x; o[k][e].y += p[k] * v.y;
-          o[k][e].z += p[k] * v.z; o[k][e].w += p[k] * v.w;
-        }
-      }
+  for (int s = 0; s < NS; s++) {
+    qr[s][0] = qr[s][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t < a.n) {
+      const float* qp = a.qkv + (size_t)t * a.ld + hh * HD + 32 * s + 8 * g;
+      qr[s][0] = *reinterpret_cast<const float4*>(qp);
+      qr[s][1] = *reinterpret_cast<const float4*>(qp + 4);
     }
   }
 
+  // K/V of one chunk in registers: K as float4 (key, 4 dims), V as 4x4 blocks
+  // (4 keys x 4 dims) so the transposed LDS store writes 4 keys at once.
+  float4 kr[KU], vr[VU][4];
+  const size_t head_off = (size_t)kvh * HD;
+  auto load_chunk = [&](int c0) {
 #pragma unroll
-  for (int k = 0; k < 4; k++) {
-    const int r = 4 * tr + k;
-    const int t = t0 + r / a.kv_mul, hh = kvh * a.kv_mul + r % a.kv_mul;
-    if (t >= a.n) continue;
-    const float inv = 1.0f / l_run[k];
-    const size_t base = (size_t)t * a.ldo + hh * HD;
+    for (int u = 0; u < KU; u++) {
+      const int i = tid + GT * u, key = i / (HD / 4), d4 = i % (HD / 4);
+      const int p = c0 + key;
+      kr[u] = p < kend ? kv_load4<F16>(a.kc, (size_t)p * a.kv_dim + head_off + 4 * d4)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
 #pragma unroll
-    for (int e = 0; e < OE; e++) {
-      const int d = 64 * e + 4 * tc;
-      const float v[4] = {o[k][e].x * inv, o[k][e].y * inv, o[k][e].z * inv, o[k][e].w * inv};
-      uint32_t hi[4], lo[4];
+    for (int u = 0; u < VU; u++) {
+      const int i = tid + GT * u, dq = i % (HD / 4), kq = i / (HD / 4);
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int p = c0 + 4 * kq + k;
+        vr[u][k] = p < kend ? kv_load4<F16>(a.vc, (size_t)p * a.kv_dim + head_off + 4 * dq)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  };
+  // Key kk = 32s + 16h + 4g + v of the chunk sits at V^T column 32s + 8g + 4h + v.
+  auto store_chunk = [&]() {
+#pragma unroll
+    for (int u = 0; u < KU; u++) {
+      const int i = tid + GT * u, key = i / (HD / 4), d4 = i % (HD / 4);
+      uint2 hi, lo;
+      split4(kr[u].x, kr[u].y, kr[u].z, kr[u].w, hi, lo);
+      *reinterpret_cast<uint2*>(&Kh[key * KP + 4 * d4]) = hi;
+      *reinterpret_cast<uint2*>(&Kl[key * KP + 4 * d4]) = lo;
+    }
+#pragma unroll
+    for (int u = 0; u < VU; u++) {
+      const int i = tid + GT * u, dq = i % (HD / 4), kq = i / (HD / 4);
+      const int col = 32 * (kq >> 3) + 8 * (kq & 3) + 4 * ((kq >> 2) & 1);
+      uint2 hi, lo;
+      split4(vr[u][0].x, vr[u][1].x, vr[u][2].x, vr[u][3].x, hi, lo);
+      *reinterpret_cast<uint2*>(&Vh[(4 * dq + 0) * VP + col]) = hi;
+      *reinterpret_cast<uint2*>(&Vl[(4 * dq + 0) * VP + col]) = lo;
+      split4(vr[u][0].y, vr[u][1].y, vr[u][2].y, vr[u][3].y, hi, lo);
+      *reinterpret_cast<uint2*>(&Vh[(4 * dq + 1) * VP + col]) = hi;
+      *reinterpret_cast<uint2*>(&Vl[(4 * dq + 1) * VP + col]) = lo;
+      split4(vr[u][0].z, vr[u][1].z, vr[u][2].z, vr[u][3].z, hi, lo);
+      *reinterpret_cast<uint2*>(&Vh[(4 * dq + 2) * VP + col]) = hi;
+      *reinterpret_cast<uint2*>(&Vl[(4 * dq + 2) * VP + col]) = lo;
+      split4(vr[u][0].w, vr[u][1].w, vr[u][2].w, vr[u][3].w, hi, lo);
+      *reinterpret_cast<uint2*>(&Vh[(4 * dq + 3) * VP + col]) = hi;
+      *reinterpret_cast<uint2*>(&Vl[(4 * dq + 3) * VP + col]) = lo;
+    }
+  };
+
+  f32x4 o[NT];
+#pragma unroll
+  for (int i = 0; i < NT; i++) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_part = 0.f;  // l_part: this lane's keys only
+
+  // group grp walks chunks grp, grp + 2, ...; both groups run the same number
+  // of rounds, a group past the last chunk only keeps the barriers
+  const int rounds = (kend + 2 * KB - 1) / (2 * KB);
+  int c0 = grp * KB;
+  if (c0 < kend) load_chunk(c0);
+
+  // q * scale * log2(e) as bf16 hi/lo B operands
+  const float qscale = a.scale * 1.4426950408889634f;
+  bf16x8 qh[NS], ql[NS];
+#pragma unroll
+  for (int s = 0; s < NS; s++) {
+    uint2 h0, l0, h1, l1;
+    split4(qr[s][0].x * qscale, qr[s][0].y * qscale, qr[s][0].z * qscale, qr[s][0].w * qscale, h0, l0);
+    split4(qr[s][1].x * qscale, qr[s][1].y * qscale, qr[s][1].z * qscale, qr[s][1].w * qscale, h1, l1);
+    qh[s] = as_bf16x8(make_uint4(h0.x, h0.y, h1.x, h1.y));
+    ql[s] = as_bf16x8(make_uint4(l0.x, l0.y, l1.x, l1.y));
+  }
+
+  for (int it = 0; it < rounds; it++, c0 += 2 * KB) {
+    __syncthreads();  // the previous chunk's LDS readers are done
+    if (c0 < kend) store_chunk();
+    __syncthreads();
+    if (c0 >= kend) continue;
+    if (c0 + 2 * KB < kend) load_chunk(c0 + 2 * KB);
+
+    f32x4 sc[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) sc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const __bf16 b = (__bf16)v[j];
-        hi[j] = __builtin_bit_cast(uint16_t, b);
-        lo[j] = __builtin_bit_cast(uint16_t, (__bf16)(v[j] - (float)b));
+        const uint16_t* kp = Kh + (16 * j + c) * KP + 32 * s + 8 * g;
+        const bf16x8 kh = as_bf16x8(*reinterpret_cast<const uint4*>(kp));
+        const bf16x8 kl = as_bf16x8(*reinterpret_cast<const uint4*>(kp + KB * KP));
+        sc[j] = mfma16(kh, qh[s], sc[j]);
+        sc[j] = mfma16(kh, ql[s], sc[j]);
+        sc[j] = mfma16(kl, qh[s], sc[j]);
       }
-      *reinterpret_cast<uint2*>(a.out + base + d) = make_uint2(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16));
-      if (a.out_lo)
-        *reinterpret_cast<uint2*>(a.out_lo + base + d) = make_uint2(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16));
     }
+
+    // sc[j][v]: key c0 + 16j + 4g + v of row r (log2 domain)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        if (c0 + 16 * j + 4 * g + v > qpos) sc[j][v] = -INFINITY;
+        mx = fmaxf(mx, sc[j][v]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, CN_WAVE));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, CN_WAVE));
+    const float m_new = fmaxf(m_run, mx);
+    // a row with every key so far masked keeps m = -inf; its sums stay 0
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    m_run = m_new;
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        sc[j][v] = __builtin_amdgcn_exp2f(sc[j][v] - m_use);
+        sum += sc[j][v];
+      }
+    l_part = l_part * alpha + sum;
+#pragma unroll
+    for (int i = 0; i < NT; i++) o[i] *= alpha;
+
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+      uint2 h0, l0, h1, l1;
+      split4(sc[2 * s][0], sc[2 * s][1], sc[2 * s][2], sc[2 * s][3], h0, l0);
+      split4(sc[2 * s + 1][0], sc[2 * s + 1][1], sc[2 * s + 1][2], sc[2 * s + 1][3], h1, l1);
+      const bf16x8 ph = as_bf16x8(make_uint4(h0.x, h0.y, h1.x, h1.y));
+      const bf16x8 pl = as_bf16x8(make_uint4(l0.x, l0.y, l1.x, l1.y));
+#pragma unroll
+      for (int i = 0; i < NT; i++) {
+        const uint16_t* vp = Vh + (16 * i + c) * VP + 32 * s + 8 * g;
+        const bf16x8 vh = as_bf16x8(*reinterpret_cast<const uint4*>(vp));
+        const bf16x8 vl = as_bf16x8(*reinterpret_cast<const uint4*>(vp + HD * VP));
+        o[i] = mfma16(vh, ph, o[i]);
+        o[i] = mfma16(vh, pl, o[i]);
+        o[i] = mfma16(vl, ph, o[i]);
+      }
+    }
+  }
+
+  float l = l_part + __shfl_xor(l_part, 16, CN_WAVE);
+  l += __shfl_xor(l, 32, CN_WAVE);
+
+  // group 1's state to group 0 through LDS (the K/V buffers are free now):
+  // xs[row][HD + 4] unnormalised output, then m[64] and l[64]
+  constexpr int XP = HD + 4;
+  float* xs = reinterpret_cast<float*>(lds_b);
+  __syncthreads();
+  if (grp == 1) {
+#pragma unroll
+    for (int i = 0; i < NT; i++)
+      *reinterpret_cast<float4*>(&xs[r * XP + 16 * i + 4 * g]) = make_float4(o[i][0], o[i][1], o[i][2], o[i][3]);
+    if (g == 0) {
+      xs[64 * XP + r] = m_run;
+      xs[64 * XP + 64 + r] = l;
+    }
+  }
+  __syncthreads();
+  if (grp == 1 || t >= a.n) return;
+  // group 0 scored key 0 of every real row, so m is finite; a row group 1 never
+  // scored has m1 = -inf and weight 0
+  const float m1 = xs[64 * XP + r], l1 = xs[64 * XP + 64 + r];
+  const float m = fmaxf(m_run, m1);
+  const float a0 = __builtin_amdgcn_exp2f(m_run - m), a1 = __builtin_amdgcn_exp2f(m1 - m);
+  const float inv = 1.0f / (l * a0 + l1 * a1);
+  const float s0 = a0 * inv, s1 = a1 * inv;
+  const size_t base = (size_t)t * a.ldo + hh * HD + 4 * g;
+#pragma unroll
+  for (int i = 0; i < NT; i++) {
+    const float4 o1 = *reinterpret_cast<const float4*>(&xs[r * XP + 16 * i + 4 * g]);
+    uint2 hi, lo;
+    split4(o[i][0] * s0 + o1.x * s1, o[i][1] * s0 + o1.y * s1, o[i][2] * s0 + o1.z * s1,
+           o[i][3] * s0 + o1.w * s1, hi, lo);
+    *reinterpret_cast<uint2*>(a.out + base + 16 * i) = hi;
+    if (a.out_lo) *reinterpret_cast<uint2*>(a.out_lo + base + 16 * i) = lo;
   }
 }
 
 template <int HD>
 size_t prefill_lds_bytes() {
-  return sizeof(float) * (size_t)(3 * 64 * (HD + 4) + 64 * 68);
+  // the end-of-kernel exchange (64 rows of HD + 4 floats, then m and l) fits in
+  // group 0's buffers
+  static_assert(sizeof(float) * (64 * (HD + 4) + 128) <= sizeof(uint16_t) * span_group_lds<HD>(), "exchange area");
+  return sizeof(uint16_t) * (size_t)(2 * span_group_lds<HD>());
 }
 
 template <int HD, bool F16>
@@ -268,7 +372,7 @@ hipError_t attn_prefill_t(const PrefillAttnArgs& a, hipStream_t st) {
     if (e != hipSuccess) return e;
     lds_set = true;
   }
-  hipLaunchKernelGGL((attn_prefill_kernel<HD, F16>), grid, dim3(CN_BLOCK), prefill_lds_bytes<HD>(), st, a);
+  hipLaunchKernelGGL((attn_prefill_kernel<HD, F16>), grid, dim3(kSpanThreads), prefill_lds_bytes<HD>(), st, a);
   return hipGetLastError();
 }
 
