@@ -77,14 +77,17 @@ __device__ __forceinline__ float4 kv_load4(const void* base, size_t idx) {
   }
 }
 
-__device__ __forceinline__ uint32_t bf16_bits(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 // (a, b) as packed bf16 high parts and packed bf16 low parts (hi + lo carries
-// ~16 significant bits; an f16 value is represented exactly).
+// ~16 significant bits; an f16 value is represented exactly).  Pair
+// conversions (v_cvt_pk_bf16_f32) and the high parts read back with a shift
+// and a mask: three instructions per value.
 __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
-  const __bf16 ha = (__bf16)a, hb = (__bf16)b;
-  hi = (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
-  lo = bf16_bits(a - (float)ha) | (bf16_bits(b - (float)hb) << 16);
+  hi = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+  const float ha = __builtin_bit_cast(float, hi << 16), hb = __builtin_bit_cast(float, hi & 0xFFFF0000u);
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a - ha, b - hb}, bf16x2));
 }
 
 __device__ __forceinline__ void split4(float a, float b, float c, float d, uint2& hi, uint2& lo) {
@@ -173,6 +176,15 @@ __global__ __launch_bounds__(kSpanThreads) void attn_prefill_kernel(PrefillAttnA
   // (4 keys x 4 dims) so the transposed LDS store writes 4 keys at once.
   float4 kr[KU], vr[VU][4];
   const size_t head_off = (size_t)kvh * HD;
+  // V block u of this thread: dims 4dq.., keys 4kq...  Each quarter-wave takes
+  // 2 dim quads of opposite parity x 8 key quads and each half-wave 4 dim quads,
+  // so the transposed 8-byte stores (V^T rows 4dq + e, pitch 36 dwords, 8
+  // distinct columns) fall on distinct banks per 16 and per 32 lanes.
+  auto vblock = [&](int u, int& dq, int& kq) {
+    const int i = tid + GT * u, l = i & 63;
+    dq = 4 * (i >> 6) + (l & 1) + 2 * ((l >> 4) & 1);
+    kq = 8 * (l >> 5) + ((l >> 1) & 7);
+  };
   auto load_chunk = [&](int c0) {
 #pragma unroll
     for (int u = 0; u < KU; u++) {
@@ -183,7 +195,8 @@ __global__ __launch_bounds__(kSpanThreads) void attn_prefill_kernel(PrefillAttnA
     }
 #pragma unroll
     for (int u = 0; u < VU; u++) {
-      const int i = tid + GT * u, dq = i % (HD / 4), kq = i / (HD / 4);
+      int dq, kq;
+      vblock(u, dq, kq);
 #pragma unroll
       for (int k = 0; k < 4; k++) {
         const int p = c0 + 4 * kq + k;
@@ -204,7 +217,8 @@ __global__ __launch_bounds__(kSpanThreads) void attn_prefill_kernel(PrefillAttnA
     }
 #pragma unroll
     for (int u = 0; u < VU; u++) {
-      const int i = tid + GT * u, dq = i % (HD / 4), kq = i / (HD / 4);
+      int dq, kq;
+      vblock(u, dq, kq);
       const int col = 32 * (kq >> 3) + 8 * (kq & 3) + 4 * ((kq >> 2) & 1);
       uint2 hi, lo;
       split4(vr[u][0].x, vr[u][1].x, vr[u][2].x, vr[u][3].x, hi, lo);
@@ -268,15 +282,21 @@ __global__ __launch_bounds__(kSpanThreads) void attn_prefill_kernel(PrefillAttnA
       }
     }
 
-    // sc[j][v]: key c0 + 16j + 4g + v of row r (log2 domain)
+    // sc[j][v]: key c0 + 16j + 4g + v of row r (log2 domain).  Chunks below
+    // the diagonal of the workgroup's first token need no mask (padding rows
+    // past n are never written, so they may score anything).
+    if (c0 + KB - 1 > a.p0 + t0) {
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int v = 0; v < 4; v++)
+          if (c0 + 16 * j + 4 * g + v > qpos) sc[j][v] = -INFINITY;
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (int j = 0; j < 4; j++)
 #pragma unroll
-      for (int v = 0; v < 4; v++) {
-        if (c0 + 16 * j + 4 * g + v > qpos) sc[j][v] = -INFINITY;
-        mx = fmaxf(mx, sc[j][v]);
-      }
+      for (int v = 0; v < 4; v++) mx = fmaxf(mx, sc[j][v]);
     mx = fmaxf(mx, __shfl_xor(mx, 16, CN_WAVE));
     mx = fmaxf(mx, __shfl_xor(mx, 32, CN_WAVE));
     const float m_new = fmaxf(m_run, mx);
@@ -319,24 +339,25 @@ __global__ __launch_bounds__(kSpanThreads) void attn_prefill_kernel(PrefillAttnA
   l += __shfl_xor(l, 32, CN_WAVE);
 
   // group 1's state to group 0 through LDS (the K/V buffers are free now):
-  // xs[row][HD + 4] unnormalised output, then m[64] and l[64]
-  constexpr int XP = HD + 4;
+  // the unnormalised output as float4 slots [tile i][lane group g][row], so
+  // 16 lanes touch 256 consecutive bytes, then m[64] and l[64]
   float* xs = reinterpret_cast<float*>(lds_b);
+  float* xm = xs + 64 * HD;
   __syncthreads();
   if (grp == 1) {
 #pragma unroll
     for (int i = 0; i < NT; i++)
-      *reinterpret_cast<float4*>(&xs[r * XP + 16 * i + 4 * g]) = make_float4(o[i][0], o[i][1], o[i][2], o[i][3]);
+      *reinterpret_cast<float4*>(&xs[4 * ((4 * i + g) * 64 + r)]) = make_float4(o[i][0], o[i][1], o[i][2], o[i][3]);
     if (g == 0) {
-      xs[64 * XP + r] = m_run;
-      xs[64 * XP + 64 + r] = l;
+      xm[r] = m_run;
+      xm[64 + r] = l;
     }
   }
   __syncthreads();
   if (grp == 1 || t >= a.n) return;
   // group 0 scored key 0 of every real row, so m is finite; a row group 1 never
   // scored has m1 = -inf and weight 0
-  const float m1 = xs[64 * XP + r], l1 = xs[64 * XP + 64 + r];
+  const float m1 = xm[r], l1 = xm[64 + r];
   const float m = fmaxf(m_run, m1);
   const float a0 = __builtin_amdgcn_exp2f(m_run - m), a1 = __builtin_amdgcn_exp2f(m1 - m);
   const float inv = 1.0f / (l * a0 + l1 * a1);
@@ -344,7 +365,7 @@ __global__ __launch_bounds__(kSpanThreads) void attn_prefill_kernel(PrefillAttnA
   const size_t base = (size_t)t * a.ldo + hh * HD + 4 * g;
 #pragma unroll
   for (int i = 0; i < NT; i++) {
-    const float4 o1 = *reinterpret_cast<const float4*>(&xs[r * XP + 16 * i + 4 * g]);
+    const float4 o1 = *reinterpret_cast<const float4*>(&xs[4 * ((4 * i + g) * 64 + r)]);
     uint2 hi, lo;
     split4(o[i][0] * s0 + o1.x * s1, o[i][1] * s0 + o1.y * s1, o[i][2] * s0 + o1.z * s1,
            o[i][3] * s0 + o1.w * s1, hi, lo);
@@ -355,9 +376,9 @@ __global__ __launch_bounds__(kSpanThreads) void attn_prefill_kernel(PrefillAttnA
 
 template <int HD>
 size_t prefill_lds_bytes() {
-  // the end-of-kernel exchange (64 rows of HD + 4 floats, then m and l) fits in
+  // the end-of-kernel exchange (64 rows of HD floats, then m and l) fits in
   // group 0's buffers
-  static_assert(sizeof(float) * (64 * (HD + 4) + 128) <= sizeof(uint16_t) * span_group_lds<HD>(), "exchange area");
+  static_assert(sizeof(float) * (64 * HD + 128) <= sizeof(uint16_t) * span_group_lds<HD>(), "exchange area");
   return sizeof(uint16_t) * (size_t)(2 * span_group_lds<HD>());
 }
 
