@@ -197,6 +197,22 @@ def test_span_longer_than_batch_cap_matches_oracle_and_token_schedule(monkeypatc
     compare_greedy(list(gt), o, margins)
 
 
+@pytest.mark.parametrize("head_dim,n_heads,n_kv,kv", [
+    (64, 8, 2, _native.KV_F32),    # kv_mul 4: 16 tokens per workgroup
+    (64, 16, 1, _native.KV_F32),   # kv_mul 16: 4 tokens per workgroup
+    (128, 4, 4, _native.KV_F32),   # head_dim 128 without grouping
+    (128, 8, 2, _native.KV_F16),   # head_dim 128, kv_mul 4, fp16 cache
+])
+def test_span_attention_layouts_match_oracle(head_dim, n_heads, n_kv, kv):
+    """Causal span attention across GQA ratios and head sizes: a 150-token
+    span (three chunks of 64 positions, ragged last workgroup) and a 37-token
+    span continuing at position 150."""
+    cfg = TINY_TEST.replace(dim=head_dim * n_heads, hidden_dim=512, n_heads=n_heads, n_kv_heads=n_kv,
+                            head_dim=head_dim, context_length=256, kv_dtype=kv)
+    announce(f"span attention layout hd={head_dim} heads={n_heads} kv={n_kv} kvtype={kv}")
+    span_case(cfg, 38, 150, n_next=37)
+
+
 def test_long_context_decode_attention_matches_oracle():
     """2000-token prompt, then greedy decode: the decode attention runs with up
     to 64 position splits (63 active at 2000 positions, merged in rounds)."""
