@@ -30,6 +30,34 @@ class HipLlamaModel:
             for name, t in weights.items():
                 self.upload_tensor(name, t.type, t.dims, t.data)
 
+    @classmethod
+    def from_gguf(cls, path: str, kv_dtype: int = _native.KV_F32, context_length: Optional[int] = None,
+                  device: int = 0) -> "HipLlamaModel":
+        """InferenceEngine.LoadFromGguf (InferenceEngine.cs:57-110) for the Llama
+        path: the config from the file's metadata (GgufReader.ExtractModelConfig),
+        then the tensors LlamaWeights.ResolveAll resolves (LlamaWeights.cs:78-145)
+        uploaded straight from the read-only mapping of the file; any other
+        tensors in the file are left alone, as the reference leaves them."""
+        from .gguf import GgufFile
+
+        g = GgufFile(path)
+        cfg = g.config(kv_dtype=kv_dtype, context_length=context_length)
+        names = ["token_embd.weight", "output_norm.weight", "output.weight"]
+        for l in range(cfg.n_layers):
+            names += [f"blk.{l}.{n}.weight" for n in ("attn_norm", "ffn_norm", "attn_q", "attn_k", "attn_v",
+                                                     "attn_output", "ffn_gate", "ffn_up", "ffn_down")]
+        m = cls(cfg, device=device)
+        try:
+            for name in names:
+                if name == "output.weight" and not g.has_tensor(name):
+                    continue  # the tied-embedding fallback is decided at the first forward
+                t = g.tensor_info(name)
+                m.upload_tensor(name, t.type, t.dims, g.tensor_bytes(name))
+        except BaseException:
+            m.close()
+            raise
+        return m
+
     # -- IModel -----------------------------------------------------------
     @property
     def config(self) -> LlamaConfig:

@@ -80,6 +80,30 @@ def test_tiny_greedy_generation_matches_oracle():
     assert list(g) == list(h)
 
 
+def test_from_gguf_matches_uploaded_checkpoint(tmp_path):
+    """A GGUF file written by chatnet_amd.gguf and loaded with
+    HipLlamaModel.from_gguf (InferenceEngine.LoadFromGguf's path) gives the
+    same logits and greedy tokens, bit for bit, as the checkpoint uploaded
+    directly, and matches the oracle."""
+    from chatnet_amd import gguf
+    cfg = TINY_TEST
+    ck = synth.llama_checkpoint(cfg, seed=39, mix="q4_k_m")
+    path = str(tmp_path / "tiny.gguf")
+    gguf.write_llama(path, cfg, ck)
+    toks = synth.tokens(39, "prompt", 10, cfg.vocab_size)
+    announce("gguf load")
+    with HipLlamaModel.from_gguf(path) as m:
+        assert m.config == cfg.replace(rms_norm_eps=float(np.float32(cfg.rms_norm_eps)))
+        g = m.forward(toks, 0).copy()
+        gt = list(m.decode_greedy(16))
+    with HipLlamaModel(cfg, ck) as m2:
+        r = m2.forward(toks, 0).copy()
+        rt = list(m2.decode_greedy(16))
+    assert np.array_equal(g, r) and gt == rt
+    o = oracle.OracleLlama(cfg, ck).forward(toks, 0)
+    assert np.max(np.abs(g - o)) <= LOGIT_TOL
+
+
 def test_context_limit_and_eos():
     cfg = TINY_TEST.replace(context_length=12)
     ck = synth.llama_checkpoint(cfg, seed=24)
