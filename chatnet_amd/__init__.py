@@ -7,7 +7,7 @@ ctypes bindings, the IModel-shaped wrapper and the synthetic-weight tools.
 """
 from . import _native
 from .config import LLAMA2_7B, TINY_TEST, TINYLLAMA_1B, LlamaConfig
-from .engine import GreedySampler, generate
+from .engine import GreedySampler, TemperatureSampler, generate, net_random
 from .model import HipLlamaModel
 
 __all__ = [
@@ -18,5 +18,7 @@ __all__ = [
     "TINY_TEST",
     "HipLlamaModel",
     "GreedySampler",
+    "TemperatureSampler",
     "generate",
+    "net_random",
 ]

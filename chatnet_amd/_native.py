@@ -121,6 +121,15 @@ _SIGNATURES = {
         ctypes.c_int,
         [_P, ctypes.c_int, ctypes.c_int32, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int)],
     ),
+    "chatnet_sample": (
+        ctypes.c_int, [_P, ctypes.c_float, ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.POINTER(ctypes.c_int32)],
+    ),
+    "chatnet_generate_sampled": (
+        ctypes.c_int,
+        [_P, ctypes.POINTER(ctypes.c_int32), ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_float,
+         ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int)],
+    ),
+    "chatnet_net_random": (ctypes.c_int, [ctypes.c_int32, ctypes.c_int, _P]),
     "chatnet_get_logits": (ctypes.c_int, [_P, _P]),
     "chatnet_matmul": (
         ctypes.c_int,

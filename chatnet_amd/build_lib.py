@@ -17,7 +17,7 @@ CSRC = os.path.join(PKG, "csrc")
 LIBDIR = os.path.join(PKG, "lib")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
-HIP_SOURCES = ["chatnet_api.hip", "gemv.hip", "gemm.hip", "prefill.hip", "decode_ops.hip"]
+HIP_SOURCES = ["chatnet_api.hip", "gemv.hip", "gemm.hip", "prefill.hip", "decode_ops.hip", "sample.hip"]
 HIP_HEADERS = ["device_common.h", "kernels.h"]
 
 HIPCC_FLAGS = [

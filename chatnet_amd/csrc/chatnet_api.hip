@@ -18,6 +18,7 @@
 #include <cstring>
 #include <map>
 #include <mutex>
+#include <random>
 #include <string>
 #include <utility>
 #include <vector>
@@ -121,6 +122,13 @@ struct chatnet_model {
   // min(ctx, 64 << k) for bucket k), captured on first use.
   static constexpr int kBuckets = 16;
   hipGraphExec_t graphs[kBuckets] = {};
+  // The same steps with the temperature sampler in place of the argmax; the
+  // sampler's parameters and draws are read from device memory at replay.
+  hipGraphExec_t sgraphs[kBuckets] = {};
+  SampleParams* sparams = nullptr;  // device
+  float* sample_p = nullptr;        // [vocab] probabilities scratch
+  float* draws = nullptr;           // [draws_cap] draw of each step
+  int draws_cap = 0;
   bool have_logits = false;
   int next_pos = 0;  // position after the last forwarded token
   int last_tok = 0;  // last forwarded token
@@ -181,6 +189,10 @@ AttnPlan attn_plan(const chatnet_model* m, int cap) {
 
 void drop_graphs(chatnet_model* m) {
   for (auto& g : m->graphs) {
+    if (g) (void)hipGraphExecDestroy(g);
+    g = nullptr;
+  }
+  for (auto& g : m->sgraphs) {
     if (g) (void)hipGraphExecDestroy(g);
     g = nullptr;
   }
@@ -283,6 +295,8 @@ int chatnet_create(const chatnet_config* cfg, int device, chatnet_model** out) {
       {(void**)&m->attn_part_o, sizeof(float) * attn_slots * c.head_dim},
       {(void**)&m->attn_part_ml, sizeof(float) * attn_slots * 2},
       {(void**)&m->rope, sizeof(float2) * (size_t)c.context_length * (c.head_dim / 2)},
+      {(void**)&m->sparams, sizeof(SampleParams)},
+      {(void**)&m->sample_p, sizeof(float) * c.vocab_size},
   };
   for (auto& a : allocs) {
     if (hipMalloc(a.p, a.n) != hipSuccess) {
@@ -322,6 +336,7 @@ void chatnet_destroy(chatnet_model* m) {
   fr(m->kcache); fr(m->vcache); fr(m->x); fr(m->q); fr(m->att); fr(m->h); fr(m->logits);
   fr(m->state); fr(m->out_tokens);
   fr(m->attn_part_o); fr(m->attn_part_ml); fr(m->rope);
+  fr(m->sparams); fr(m->sample_p); fr(m->draws);
   fr(m->sp_x); fr(m->sp_xb); fr(m->sp_hb); fr(m->sp_qkv); fr(m->sp_tok); fr(m->sp_part);
   if (m->stream) (void)hipStreamDestroy(m->stream);
   delete m;
@@ -827,10 +842,12 @@ int chatnet_argmax(chatnet_model* m, int32_t* out_token) {
   return CHATNET_OK;
 }
 
-int chatnet_decode_greedy(chatnet_model* m, int max_tokens, int32_t eos_token, int32_t* out_tokens, int* n_out) {
-  if (!m || !out_tokens || !n_out) return fail(CHATNET_ERR_INVALID_ARG, "null argument");
+// The decode half of InferenceEngine.Generate (InferenceEngine.cs:241-307):
+// each token is picked by the argmax or, when `sampled`, by the temperature
+// sampler (parameters in m->sparams, the i-th pick's draw in m->draws[i]).
+static int decode_loop(chatnet_model* m, int max_tokens, int32_t eos_token, int32_t* out_tokens, int* n_out,
+                       bool sampled) {
   *n_out = 0;
-  if (max_tokens < 0) return fail(CHATNET_ERR_INVALID_ARG, "max_tokens must be >= 0");
   if (!m->have_logits) return fail(CHATNET_ERR_INVALID_ARG, "no forward has produced logits yet");
   int rc = check_complete(m);
   if (rc) return rc;
@@ -845,8 +862,14 @@ int chatnet_decode_greedy(chatnet_model* m, int max_tokens, int32_t eos_token, i
   if (emitted < 0) emitted = 0;
   if ((rc = ensure_out_tokens(m, max_tokens + 2))) return rc;
   // step counter = 0, then sample the first token from the last forward's logits
+  auto pick = [m, sampled]() {
+    return sampled ? sample_launch(m->logits, m->cfg.vocab_size, m->sparams, m->draws, m->state, m->out_tokens,
+                                   m->out_cap, m->sample_p, m->stream)
+                   : argmax_launch(m->logits, m->cfg.vocab_size, m->state, m->out_tokens, m->out_cap, m->stream);
+  };
+  hipGraphExec_t* graphs = sampled ? m->sgraphs : m->graphs;
   HIP_TRY(set_state_launch(m->state, p0 - 1, m->last_tok, 0, m->stream));
-  HIP_TRY(argmax_launch(m->logits, m->cfg.vocab_size, m->state, m->out_tokens, m->out_cap, m->stream));
+  HIP_TRY(pick());
   // CHATNET_DECODE_GRAPH=0 issues the same per-step launches directly instead
   // of replaying the captured graph (profilers that cannot trace graph
   // launches need this; the kernels and their order are identical).
@@ -856,28 +879,28 @@ int chatnet_decode_greedy(chatnet_model* m, int max_tokens, int32_t eos_token, i
   if (forwards > 0 && !use_graph) {
     for (int i = 0; i < forwards; i++) {
       if ((rc = launch_token(m, true, bucket_cap(m, p0 + i + 1)))) return rc;
-      HIP_TRY(argmax_launch(m->logits, m->cfg.vocab_size, m->state, m->out_tokens, m->out_cap, m->stream));
+      HIP_TRY(pick());
     }
   } else if (forwards > 0) {
     for (int i = 0; i < forwards; i++) {
       const int k = bucket_index(m, p0 + i + 1);
-      if (!m->graphs[k]) {
+      if (!graphs[k]) {
         hipGraph_t g;
         HIP_TRY(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
         int lrc = launch_token(m, true, bucket_cap(m, p0 + i + 1));
-        hipError_t ae = argmax_launch(m->logits, m->cfg.vocab_size, m->state, m->out_tokens, m->out_cap, m->stream);
+        hipError_t ae = pick();
         hipError_t ee = hipStreamEndCapture(m->stream, &g);
         if (lrc) return lrc;
-        if (ae != hipSuccess) return fail(CHATNET_ERR_HIP, "argmax capture: %s", hipGetErrorString(ae));
+        if (ae != hipSuccess) return fail(CHATNET_ERR_HIP, "sampler capture: %s", hipGetErrorString(ae));
         if (ee != hipSuccess) return fail(CHATNET_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(ee));
-        hipError_t ie = hipGraphInstantiate(&m->graphs[k], g, nullptr, nullptr, 0);
+        hipError_t ie = hipGraphInstantiate(&graphs[k], g, nullptr, nullptr, 0);
         (void)hipGraphDestroy(g);
         if (ie != hipSuccess) {
-          m->graphs[k] = nullptr;
+          graphs[k] = nullptr;
           return fail(CHATNET_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(ie));
         }
       }
-      HIP_TRY(hipGraphLaunch(m->graphs[k], m->stream));
+      HIP_TRY(hipGraphLaunch(graphs[k], m->stream));
     }
   }
   std::vector<int> buf((size_t)emitted + 2);
@@ -899,6 +922,13 @@ int chatnet_decode_greedy(chatnet_model* m, int max_tokens, int32_t eos_token, i
   return CHATNET_OK;
 }
 
+int chatnet_decode_greedy(chatnet_model* m, int max_tokens, int32_t eos_token, int32_t* out_tokens, int* n_out) {
+  if (!m || !out_tokens || !n_out) return fail(CHATNET_ERR_INVALID_ARG, "null argument");
+  *n_out = 0;
+  if (max_tokens < 0) return fail(CHATNET_ERR_INVALID_ARG, "max_tokens must be >= 0");
+  return decode_loop(m, max_tokens, eos_token, out_tokens, n_out, false);
+}
+
 int chatnet_generate_greedy(chatnet_model* m, const int32_t* prompt, int n_prompt, int max_tokens,
                             int32_t eos_token, int32_t* out_tokens, int* n_out) {
   if (!m || !out_tokens || !n_out) return fail(CHATNET_ERR_INVALID_ARG, "null argument");
@@ -910,6 +940,65 @@ int chatnet_generate_greedy(chatnet_model* m, const int32_t* prompt, int n_promp
   HIP_TRY(hipSetDevice(m->device));
   if ((rc = run_prompt(m, prompt, n_prompt, 0))) return rc;  // InferenceEngine.cs:235-239
   return chatnet_decode_greedy(m, max_tokens, eos_token, out_tokens, n_out);
+}
+
+int chatnet_sample(chatnet_model* m, float temperature, int top_k, float top_p, float r, int32_t* out_token) {
+  if (!m || !out_token) return fail(CHATNET_ERR_INVALID_ARG, "null argument");
+  if (temperature <= 0.0f) return chatnet_argmax(m, out_token);  // TemperatureSampler.cs:37-41
+  if (!m->have_logits) return fail(CHATNET_ERR_INVALID_ARG, "no forward has produced logits yet");
+  if (top_k < 1 || top_k > kSampleMaxK) return fail(CHATNET_ERR_INVALID_ARG, "top_k must be in [1, %d]", kSampleMaxK);
+  HIP_TRY(hipSetDevice(m->device));
+  const SampleParams sp{1.0f / temperature, top_k, top_p, r};  // invTemp as TemperatureSampler.cs:50
+  HIP_TRY(hipMemcpyAsync(m->sparams, &sp, sizeof(sp), hipMemcpyHostToDevice, m->stream));
+  HIP_TRY(sample_launch(m->logits, m->cfg.vocab_size, m->sparams, nullptr, m->state, nullptr, 0, m->sample_p,
+                        m->stream));
+  int st[4];
+  HIP_TRY(hipMemcpyAsync(st, m->state, sizeof(st), hipMemcpyDeviceToHost, m->stream));
+  HIP_TRY(hipStreamSynchronize(m->stream));
+  *out_token = st[1];
+  return CHATNET_OK;
+}
+
+int chatnet_generate_sampled(chatnet_model* m, const int32_t* prompt, int n_prompt, int max_tokens, float temperature,
+                             int top_k, float top_p, int32_t seed, int32_t eos_token, int32_t* out_tokens,
+                             int* n_out) {
+  if (temperature <= 0.0f)  // greedy fallback, no draws consumed (TemperatureSampler.cs:37-41)
+    return chatnet_generate_greedy(m, prompt, n_prompt, max_tokens, eos_token, out_tokens, n_out);
+  if (!m || !out_tokens || !n_out) return fail(CHATNET_ERR_INVALID_ARG, "null argument");
+  *n_out = 0;
+  if (max_tokens < 0) return fail(CHATNET_ERR_INVALID_ARG, "max_tokens must be >= 0");
+  if (top_k < 1 || top_k > kSampleMaxK) return fail(CHATNET_ERR_INVALID_ARG, "top_k must be in [1, %d]", kSampleMaxK);
+  int rc = validate_tokens(m, prompt, n_prompt, 0);
+  if (rc) return rc;
+  if ((rc = check_complete(m))) return rc;
+  HIP_TRY(hipSetDevice(m->device));
+  // pick i takes the i-th NextDouble of the sampler's Random (TemperatureSampler.cs:29, :97)
+  const int ndraw = max_tokens + 2;
+  if (m->draws_cap < ndraw) {
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    if (m->draws) (void)hipFree(m->draws);
+    m->draws = nullptr;
+    m->draws_cap = 0;
+    if (hipMalloc(&m->draws, sizeof(float) * (size_t)ndraw) != hipSuccess)
+      return fail(CHATNET_ERR_OUT_OF_MEMORY, "hipMalloc of the draw buffer failed");
+    m->draws_cap = ndraw;
+    drop_graphs(m);  // captured sampler nodes point at the old buffer
+  }
+  NetRandom rng(seed >= 0 ? seed : (int32_t)(std::random_device{}() & 0x7FFFFFFFu));
+  std::vector<float> d((size_t)ndraw);
+  for (auto& v : d) v = (float)rng.next_double();
+  const SampleParams sp{1.0f / temperature, top_k, top_p, 0.0f};
+  HIP_TRY(hipMemcpyAsync(m->draws, d.data(), sizeof(float) * d.size(), hipMemcpyHostToDevice, m->stream));
+  HIP_TRY(hipMemcpyAsync(m->sparams, &sp, sizeof(sp), hipMemcpyHostToDevice, m->stream));
+  if ((rc = run_prompt(m, prompt, n_prompt, 0))) return rc;  // InferenceEngine.cs:235-239
+  return decode_loop(m, max_tokens, eos_token, out_tokens, n_out, true);
+}
+
+int chatnet_net_random(int32_t seed, int n, double* out) {
+  if (n < 0 || (n > 0 && !out)) return fail(CHATNET_ERR_INVALID_ARG, "invalid arguments to chatnet_net_random");
+  NetRandom rng(seed);
+  for (int i = 0; i < n; i++) out[i] = rng.next_double();
+  return CHATNET_OK;
 }
 
 int chatnet_matmul(uint32_t type, const void* w_dev, const float* x_dev, float* y_dev, int M, int K, int N,

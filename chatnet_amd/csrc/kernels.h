@@ -124,5 +124,33 @@ int attn_decode_round(int head_dim, int kv_mul);
 hipError_t argmax_launch(const float* logits, int n, int* state, int* out_tokens, int out_cap,
                          hipStream_t st);
 
+// TemperatureSampler.Sample (TemperatureSampler.cs:33-112) over the logits with
+// the parameters in device memory (so captured graphs read the current ones):
+// the draw is draws[state[2]] when draws is given, else params->draw; the
+// token is written like argmax_launch's.  top_k must be in [1, kSampleMaxK]
+// (clamped to n); scratch holds n floats.
+constexpr int kSampleMaxK = 1024;
+struct SampleParams {
+  float inv_temp;  // 1.0f / temperature, temperature > 0
+  int top_k;
+  float top_p;
+  float draw;
+};
+hipError_t sample_launch(const float* logits, int n, const SampleParams* params, const float* draws, int* state,
+                         int* out_tokens, int out_cap, float* scratch, hipStream_t st);
+
+// System.Random(seed) of the .NET BCL, the seeded compat generator
+// (TemperatureSampler.cs:29 constructs it, :97 draws NextDouble).
+class NetRandom {
+ public:
+  explicit NetRandom(int32_t seed);
+  double next_double();
+
+ private:
+  int32_t internal_sample();
+  int32_t a_[56];
+  int inext_, inextp_;
+};
+
 // Sets state[0] = pos, state[1] = tok and, when step >= 0, state[2] = step.
 hipError_t set_state_launch(int* state, int pos, int tok, int step, hipStream_t st);

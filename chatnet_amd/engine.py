@@ -1,11 +1,14 @@
-"""Host-side mirrors of ChatNet's sampler and generation loop.
+"""Host-side mirrors of ChatNet's samplers and generation loop.
 
-GreedySampler   src/ChatNet.Core/Samplers/GreedySampler.cs:13-26
-generate        InferenceEngine.Generate's token loop, InferenceEngine.cs:234-307,
-                with token ids in and out (no tokenizer, no stop strings).
+GreedySampler       src/ChatNet.Core/Samplers/GreedySampler.cs:13-26
+TemperatureSampler  src/ChatNet.Core/Samplers/TemperatureSampler.cs:19-112 (runs
+                    on the device through HipLlamaModel.sample)
+generate            InferenceEngine.Generate's token loop, InferenceEngine.cs:234-307,
+                    with token ids in and out (no tokenizer, no stop strings).
 """
 from __future__ import annotations
 
+import os
 from typing import Callable, List, Optional
 
 import numpy as np
@@ -22,6 +25,44 @@ class GreedySampler:
         if np.isnan(arr[0]):
             return 0
         return int(np.argmax(np.where(np.isnan(arr), -np.inf, arr)))
+
+
+def net_random(seed: int, n: int) -> np.ndarray:
+    """The first n values of System.Random(seed).NextDouble(), the .NET BCL's
+    seeded generator TemperatureSampler draws from (TemperatureSampler.cs:29)."""
+    from . import _native
+
+    out = np.empty(max(n, 1), dtype=np.float64)
+    _native.check(_native.hip_lib().chatnet_net_random(int(seed), int(n), out.ctypes.data))
+    return out[:n]
+
+
+class TemperatureSampler:
+    """TemperatureSampler (TemperatureSampler.cs:19-112) for a HipLlamaModel:
+    Sample runs on the device over the model's last logits, with the draws of
+    System.Random(seed) taken in order, one per Sample when temperature > 0
+    (TemperatureSampler.cs:97); temperature <= 0 is the greedy fallback.  A
+    negative seed stands for the reference's unseeded Random."""
+
+    def __init__(self, model, temperature: float, top_k: int = 40, top_p: float = 0.9, seed: int = -1):
+        self.model = model
+        self.temperature = float(temperature)
+        self.top_k = int(top_k)
+        self.top_p = float(top_p)
+        self.seed = int(seed) if seed >= 0 else int.from_bytes(os.urandom(4), "little") & 0x7FFFFFFF
+        self._draws = net_random(self.seed, 256)
+        self._next = 0
+
+    def sample(self, logits=None) -> int:
+        """ISampler.Sample; the logits are those the model last produced (a host
+        copy passed here is not read)."""
+        if self.temperature <= 0.0:
+            return self.model.argmax()
+        if self._next >= len(self._draws):
+            self._draws = net_random(self.seed, 2 * len(self._draws))
+        draw = float(np.float32(self._draws[self._next]))
+        self._next += 1
+        return self.model.sample(self.temperature, self.top_k, self.top_p, draw)
 
 
 def generate(model, prompt_ids, max_tokens: int, sampler=None, eos_token: Optional[int] = None,

@@ -89,6 +89,27 @@ class HipLlamaModel:
         _native.check(self._lib.chatnet_argmax(self._h, ctypes.byref(out)))
         return int(out.value)
 
+    def sample(self, temperature: float, top_k: int, top_p: float, draw: float) -> int:
+        """Device-side TemperatureSampler.Sample (TemperatureSampler.cs:33-112)
+        over the last logits with the draw (float)Random.NextDouble()."""
+        out = ctypes.c_int32()
+        _native.check(self._lib.chatnet_sample(self._h, float(temperature), int(top_k), float(top_p), float(draw),
+                                               ctypes.byref(out)))
+        return int(out.value)
+
+    def generate_sampled(self, prompt, max_tokens: int, temperature: float, top_k: int = 40, top_p: float = 0.9,
+                         seed: int = -1, eos_token: int = -1) -> np.ndarray:
+        """InferenceEngine.Generate with TemperatureSampler(temperature, top_k,
+        top_p, seed) on the device (draw i = i-th NextDouble of Random(seed))."""
+        p = np.ascontiguousarray(np.asarray(prompt, dtype=np.int32).ravel())
+        out = np.empty(max(max_tokens, 1), dtype=np.int32)
+        n = ctypes.c_int()
+        _native.check(self._lib.chatnet_generate_sampled(
+            self._h, p.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), int(p.size), int(max_tokens),
+            float(temperature), int(top_k), float(top_p), int(seed), int(eos_token),
+            out.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), ctypes.byref(n)))
+        return out[: n.value].copy()
+
     def get_logits(self) -> np.ndarray:
         out = np.empty(self._cfg.vocab_size, dtype=np.float32)
         _native.check(self._lib.chatnet_get_logits(self._h, out.ctypes.data))

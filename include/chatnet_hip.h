@@ -138,6 +138,34 @@ CHATNET_API int chatnet_generate_greedy(chatnet_model* m, const int32_t* prompt,
 CHATNET_API int chatnet_decode_greedy(chatnet_model* m, int max_tokens, int32_t eos_token,
                                       int32_t* out_tokens, int* n_out);
 
+/* TemperatureSampler.Sample (src/ChatNet.Core/Samplers/TemperatureSampler.cs:33-112)
+ * on the device-resident logits of the last forward, with the draw `r` that the
+ * reference takes from its Random, (float)NextDouble() (:97).  temperature <= 0
+ * is the reference's greedy fallback (:37-41, same result as chatnet_argmax);
+ * otherwise softmax(logits / temperature), the top_k most probable tokens
+ * (1 <= top_k <= 1024; the reference throws for top_k < 1), the shortest prefix
+ * reaching top_p, renormalised, and the first token whose running sum exceeds r. */
+CHATNET_API int chatnet_sample(chatnet_model* m, float temperature, int top_k, float top_p, float r,
+                               int32_t* out_token);
+
+/* InferenceEngine.Generate (InferenceEngine.cs:234-307) with
+ * TemperatureSampler(temperature, top_k, top_p, seed)
+ * (TemperatureSampler.cs:25-31): like chatnet_generate_greedy, but every token
+ * is drawn by chatnet_sample's rule, the k-th draw being the k-th NextDouble()
+ * of System.Random(seed) (seed < 0: a nondeterministic seed, as
+ * `new Random()`).  The draws are made on the host before the loop (they do
+ * not depend on the logits); the loop itself stays on the device. */
+CHATNET_API int chatnet_generate_sampled(chatnet_model* m, const int32_t* prompt, int n_prompt,
+                                         int max_tokens, float temperature, int top_k, float top_p,
+                                         int32_t seed, int32_t eos_token, int32_t* out_tokens,
+                                         int* n_out);
+
+/* The first n values of System.Random(seed).NextDouble() (the .NET BCL's seeded
+ * generator that TemperatureSampler uses, TemperatureSampler.cs:29), for callers
+ * that drive chatnet_sample one token at a time.  No counterpart to bind in the
+ * reference (it is the BCL's); provided so a host loop can reproduce the draws. */
+CHATNET_API int chatnet_net_random(int32_t seed, int n, double* out);
+
 /* Copies the device logits of the last forward to the host (vocab_size floats). */
 CHATNET_API int chatnet_get_logits(chatnet_model* m, float* logits_host);
 

@@ -422,6 +422,173 @@ int oracle_argmax(const float* logits, int n) {
 }
 
 /* ---------------------------------------------------------------------------
+ * System.Random(int seed) (TemperatureSampler.cs:29 constructs it; :97 draws
+ * NextDouble once per Sample).  The generator lives in the .NET BCL (net10.0,
+ * ChatNet.Core.csproj:3), which the reference does not vendor; a seeded
+ * Random keeps the compat implementation: Knuth's subtractive method as in
+ * Numerical Recipes in C (2nd ed.) "ran3", MBIG = int.MaxValue,
+ * MSEED = 161803398, 55-entry table with lags 21/55, NextDouble =
+ * InternalSample * (1.0 / MBIG).  Restated from that published algorithm.
+ * ------------------------------------------------------------------------- */
+#define NR_MBIG 2147483647
+#define NR_MSEED 161803398
+
+void oracle_net_random_init(oracle_net_random* r, int32_t seed) {
+  int32_t subtraction = seed == INT32_MIN ? INT32_MAX : (seed < 0 ? -seed : seed);
+  int32_t mj = NR_MSEED - subtraction;
+  r->seed_array[0] = 0;
+  r->seed_array[55] = mj;
+  int32_t mk = 1;
+  for (int i = 1; i < 55; i++) {
+    int ii = (21 * i) % 55;
+    r->seed_array[ii] = mk;
+    mk = mj - mk;
+    if (mk < 0) mk += NR_MBIG;
+    mj = r->seed_array[ii];
+  }
+  for (int k = 1; k < 5; k++)
+    for (int i = 1; i < 56; i++) {
+      r->seed_array[i] -= r->seed_array[1 + (i + 30) % 55];
+      if (r->seed_array[i] < 0) r->seed_array[i] += NR_MBIG;
+    }
+  r->inext = 0;
+  r->inextp = 21;
+}
+
+int32_t oracle_net_random_sample(oracle_net_random* r) {
+  int32_t a = r->inext, b = r->inextp;
+  if (++a >= 56) a = 1;
+  if (++b >= 56) b = 1;
+  int32_t v = r->seed_array[a] - r->seed_array[b];
+  if (v == NR_MBIG) v--;
+  if (v < 0) v += NR_MBIG;
+  r->seed_array[a] = v;
+  r->inext = a;
+  r->inextp = b;
+  return v;
+}
+
+double oracle_net_random_next_double(oracle_net_random* r) {
+  return oracle_net_random_sample(r) * (1.0 / NR_MBIG);
+}
+
+/* ---------------------------------------------------------------------------
+ * TemperatureSampler (TemperatureSampler.cs:33-222)
+ * ------------------------------------------------------------------------- */
+static void ts_swap(float* p, int* idx, int a, int b) { /* :167-172 */
+  float t = p[a];
+  p[a] = p[b];
+  p[b] = t;
+  int u = idx[a];
+  idx[a] = idx[b];
+  idx[b] = u;
+}
+
+/* PartialSortDescending (:118-165): median-of-three quickselect. */
+static void ts_partial_sort(float* p, int* idx, int left, int right, int k) {
+  while (left < right) {
+    int mid = left + (right - left) / 2;
+    if (p[mid] > p[left]) ts_swap(p, idx, left, mid);
+    if (p[right] > p[left]) ts_swap(p, idx, left, right);
+    if (p[mid] > p[right]) ts_swap(p, idx, mid, right);
+    float pivot = p[right];
+    int store = left;
+    for (int i = left; i < right; i++)
+      if (p[i] > pivot) {
+        ts_swap(p, idx, i, store);
+        store++;
+      }
+    ts_swap(p, idx, store, right);
+    if (store == k - 1) return;
+    if (store < k - 1) left = store + 1;
+    else right = store - 1;
+  }
+}
+
+/* InsertionSortDescending (:177-194). */
+static void ts_insertion_sort(float* p, int* idx, int count) {
+  for (int i = 1; i < count; i++) {
+    float kp = p[i];
+    int ki = idx[i];
+    int j = i - 1;
+    while (j >= 0 && p[j] < kp) {
+      p[j + 1] = p[j];
+      idx[j + 1] = idx[j];
+      j--;
+    }
+    p[j + 1] = kp;
+    idx[j + 1] = ki;
+  }
+}
+
+static float fminabs(float m, float d) {
+  d = fabsf(d);
+  return d < m ? d : m;
+}
+
+int oracle_temperature_sample(const float* logits, int n, float temperature, int top_k, float top_p, float r,
+                              float* margin) {
+  float mg = INFINITY;
+  if (temperature <= 0.0f) { /* :37-41 */
+    if (margin) *margin = mg;
+    return oracle_argmax(logits, n);
+  }
+  if (top_k < 1) return -1;
+  float* p = (float*)malloc(sizeof(float) * (size_t)n);
+  int* idx = (int*)malloc(sizeof(int) * (size_t)n);
+  float invTemp = 1.0f / temperature; /* :50-55 */
+  for (int i = 0; i < n; i++) {
+    p[i] = logits[i] * invTemp;
+    idx[i] = i;
+  }
+  oracle_softmax(p, n); /* :58 */
+  int k = top_k < n ? top_k : n; /* :62-63 */
+  /* the k-th / (k+1)-th gap decides the set, relative to the k-th (a copy
+   * keeps p's order intact) */
+  if (k < n) {
+    float* s = (float*)malloc(sizeof(float) * (size_t)n);
+    int* si = (int*)malloc(sizeof(int) * (size_t)n);
+    memcpy(s, p, sizeof(float) * (size_t)n);
+    memcpy(si, idx, sizeof(int) * (size_t)n);
+    ts_partial_sort(s, si, 0, n - 1, k + 1);
+    ts_insertion_sort(s, si, k + 1);
+    if (s[k - 1] > 0.0f) mg = fminabs(mg, (s[k - 1] - s[k]) / s[k - 1]);
+    free(s);
+    free(si);
+  }
+  ts_partial_sort(p, idx, 0, n - 1, k);
+  ts_insertion_sort(p, idx, k); /* :67 */
+  float cumulative = 0.0f; /* :70-80 */
+  int cutoff = k;
+  for (int i = 0; i < k; i++) {
+    cumulative += p[i];
+    mg = fminabs(mg, cumulative - top_p);
+    if (cumulative >= top_p) {
+      cutoff = i + 1;
+      break;
+    }
+  }
+  float sum = 0.0f; /* :83-92 */
+  for (int i = 0; i < cutoff; i++) sum += p[i];
+  float invSum = 1.0f / sum;
+  for (int i = 0; i < cutoff; i++) p[i] *= invSum;
+  float acc = 0.0f; /* :95-106 */
+  int tok = idx[cutoff - 1];
+  for (int i = 0; i < cutoff; i++) {
+    acc += p[i];
+    mg = fminabs(mg, r - acc);
+    if (r < acc) {
+      tok = idx[i];
+      break;
+    }
+  }
+  free(p);
+  free(idx);
+  if (margin) *margin = mg;
+  return tok;
+}
+
+/* ---------------------------------------------------------------------------
  * Llama model (LlamaModel.cs, LlamaWeights.cs)
  * ------------------------------------------------------------------------- */
 

@@ -25,6 +25,13 @@
  *   rmsnorm/rope/softmax/silu/add/attention/argmax: invariants (closed forms,
  *                     identity at pos 0, norm preservation, shift invariance,
  *                     tie rule) and a float64 numpy restatement of a tiny model.
+ *   net_random        published outputs of .NET's Random (Random(0), Random(42))
+ *                     and the |seed| / int.MinValue rules of its constructor.
+ *   temperature_sample a float64 restatement of the sampling rule on random
+ *                     logits, hand-derived special cases (greedy fallback,
+ *                     top-1, nucleus of one, a top-2 split) and draw
+ *                     frequencies.  The order the quickselect leaves equal
+ *                     probabilities in: parity unpinned.
  *   Order of Vector128.Sum / MathF last-ulp results: parity unpinned (only
  *                     running .NET could pin them; covered by tolerance).
  */
@@ -63,6 +70,24 @@ void oracle_add(float* a, const float* b, int n);
 void oracle_rope(float* q, float* k, int position, int head_dim, int n_heads, int n_kv_heads,
                  float freq_base);
 int oracle_argmax(const float* logits, int n);
+
+/* System.Random(int seed) of the .NET BCL (the seeded compat generator). */
+typedef struct oracle_net_random {
+  int32_t seed_array[56];
+  int32_t inext, inextp;
+} oracle_net_random;
+void oracle_net_random_init(oracle_net_random* r, int32_t seed);
+int32_t oracle_net_random_sample(oracle_net_random* r); /* InternalSample, [0, int.MaxValue) */
+double oracle_net_random_next_double(oracle_net_random* r);
+
+/* TemperatureSampler.Sample with the draw r = (float)Random.NextDouble() passed
+ * in.  Returns the token (-1 for top_k < 1, where the reference indexes out of
+ * range); *margin (nullable) receives the smallest distance between a quantity
+ * the result depends on and the threshold it was compared with: the gap of the
+ * k-th to the (k+1)-th probability relative to the k-th, and in probability
+ * units cumulative vs top_p and draw vs running sum. */
+int oracle_temperature_sample(const float* logits, int n, float temperature, int top_k, float top_p, float r,
+                              float* margin);
 
 /* Whole model.  Tensor pointers are borrowed host pointers (like the mmap). */
 typedef struct oracle_config {

@@ -56,6 +56,14 @@ def lib() -> ctypes.CDLL:
         L.oracle_rope.argtypes = [_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float]
         L.oracle_argmax.argtypes = [_P, ctypes.c_int]
         L.oracle_argmax.restype = ctypes.c_int
+        L.oracle_net_random_init.argtypes = [_P, ctypes.c_int32]
+        L.oracle_net_random_sample.argtypes = [_P]
+        L.oracle_net_random_sample.restype = ctypes.c_int32
+        L.oracle_net_random_next_double.argtypes = [_P]
+        L.oracle_net_random_next_double.restype = ctypes.c_double
+        L.oracle_temperature_sample.argtypes = [_P, ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_float,
+                                                ctypes.c_float, _P]
+        L.oracle_temperature_sample.restype = ctypes.c_int
         L.oracle_llama_create.argtypes = [ctypes.POINTER(OracleConfig)]
         L.oracle_llama_create.restype = _P
         L.oracle_llama_set_tensor.argtypes = [_P, ctypes.c_char_p, ctypes.c_uint32, _P]
@@ -131,6 +139,30 @@ def rope(q, k, pos, head_dim, n_heads, n_kv_heads, base):
 def argmax(logits) -> int:
     l = _f32(logits)
     return int(lib().oracle_argmax(l.ctypes.data, l.size))
+
+
+class NetRandom(ctypes.Structure):
+    """System.Random(seed) of the .NET BCL (the seeded compat generator)."""
+    _fields_ = [("seed_array", ctypes.c_int32 * 56), ("inext", ctypes.c_int32), ("inextp", ctypes.c_int32)]
+
+    def __init__(self, seed: int):
+        super().__init__()
+        lib().oracle_net_random_init(ctypes.addressof(self), int(seed))
+
+    def sample(self) -> int:
+        return int(lib().oracle_net_random_sample(ctypes.addressof(self)))
+
+    def next_double(self) -> float:
+        return float(lib().oracle_net_random_next_double(ctypes.addressof(self)))
+
+
+def temperature_sample(logits, temperature: float, top_k: int, top_p: float, draw: float):
+    """TemperatureSampler.Sample with the draw given: (token, margin)."""
+    l = _f32(logits)
+    m = ctypes.c_float()
+    tok = lib().oracle_temperature_sample(l.ctypes.data, l.size, temperature, top_k, top_p, draw,
+                                          ctypes.addressof(m))
+    return int(tok), float(m.value)
 
 
 class OracleLlama:
