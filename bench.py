@@ -175,6 +175,22 @@ def gemm_sweep(shapes, ns, rotate_bytes=1 << 30):
     return res
 
 
+def sampled_run(cfg, ck, prompt, steps):
+    """Decode tok/s with the device temperature sampler (T 0.8, top-k 40,
+    top-p 0.9, seed 1) in place of the argmax, prompt included in the call."""
+    from chatnet_amd import HipLlamaModel
+
+    with HipLlamaModel(cfg, ck) as m:
+        m.generate_sampled(prompt, 8, 0.8, 40, 0.9, 1)  # warm-up, graph capture
+        t0 = time.perf_counter()
+        m.forward(prompt, 0)
+        t1 = time.perf_counter()
+        toks = m.generate_sampled(prompt, steps, 0.8, 40, 0.9, 1)
+        t2 = time.perf_counter()
+    assert len(toks) == steps
+    return round(steps / ((t2 - t1) - (t1 - t0)), 1)
+
+
 def prefill_run(cfg, ck, n_prompt, n_decode):
     """Time to first token of an n_prompt-token prompt forwarded as one span,
     then n_decode greedy decode tokens."""
@@ -269,6 +285,7 @@ def main():
     toks7 = None
     cpu = None
     tiny = None
+    tiny_sampled = None
     gsweep = None
     prefill = None
     kq = None
@@ -312,6 +329,8 @@ def main():
             dt1, _ = decode_run(cfg1, ck1, p1, 128, 8)
             tiny = round(128 / dt1, 1)
             log(f"TinyLlama decode: {tiny} tok/s")
+            tiny_sampled = sampled_run(cfg1, ck1, p1, 128)
+            log(f"TinyLlama decode, temperature sampler on the device: {tiny_sampled} tok/s")
             log("TinyLlama 512-token prefill + 128 decode")
             prefill = prefill_run(cfg1, ck1, 512, 128)
             log(f"  {json.dumps(prefill)}")
@@ -331,7 +350,8 @@ def main():
         "data": "synthetic (seeded N(0,0.02) weights quantized to Q4_0, seeded prompt ids)",
         "config": {"workload": "llama2-7b-q4_0-decode-bs1", "prompt_tokens": 128, "decode_tokens": args.steps,
                    "kv_cache": "f32", "context_length": 2048, "weights": "Q4_0 (all matrices)",
-                   "tinyllama_1b_q4_0_decode_tok_s": tiny},
+                   "tinyllama_1b_q4_0_decode_tok_s": tiny,
+                   "tinyllama_1b_q4_0_sampled_decode_tok_s": tiny_sampled},
         "gemv_sweep_q4_0_n1_cold": sweep,
         "gemm_sweep_q4_0_cold": gsweep,
         "tinyllama_q4_0_prefill": prefill,

@@ -10,9 +10,10 @@
 //   renormalise the cutoff tokens, first i with r < acc         (:83-106)
 // The reference finds the top k by quickselect and insertion sort; here a
 // 4-pass radix select on the float bit patterns (p >= 0, so they order like
-// the values) finds the k-th largest key, the k winners are gathered in index
-// order, and a bitonic sort in LDS orders them by (p descending, index
-// ascending).  Equal probabilities may therefore come out in another order
+// the values) finds the k-th largest key, the keys at or above it are
+// gathered (an index-ordered scan instead when more than 1024 tie with it),
+// and a bitonic sort in LDS orders them by (p descending, index ascending),
+// the first k being the winners.  Equal probabilities may therefore come out in another order
 // than the reference's quickselect leaves them.  The softmax sum is a tree
 // here and a left-to-right sum in the reference (a few ulps apart); the
 // top-p, renormalisation and draw loops run on one thread in the reference's
@@ -49,14 +50,19 @@ __device__ __forceinline__ float st_sum(float v, float* red) {
   return s;
 }
 
-// p is a scratch array of n floats; each thread only ever touches its own
-// elements i = tid + 1024j, so no barrier is needed between the passes over it.
+// Element i = tid + 1024j of the vocabulary belongs to thread tid.  REG keeps
+// a thread's (at most kRegPerThread) probabilities in registers; otherwise
+// they live in the scratch array p (n floats), where each thread only ever
+// touches its own elements, so no barrier is needed between the passes.
+constexpr int kRegPerThread = 32;
+
+template <bool REG>
 __global__ __launch_bounds__(kST) void sample_kernel(const float* __restrict__ logits, int n,
                                                      const SampleParams* __restrict__ prm,
                                                      const float* __restrict__ draws, int* state,
                                                      int* out_tokens, int out_cap, float* __restrict__ p) {
   __shared__ float red[kSW];
-  __shared__ int hist[256];
+  __shared__ int hist[256 * 8];
   __shared__ int sel[2];
   __shared__ int wcnt[2][kSW];
   __shared__ float cp[kSampleMaxK];
@@ -65,46 +71,87 @@ __global__ __launch_bounds__(kST) void sample_kernel(const float* __restrict__ l
   const float inv_temp = prm->inv_temp;
   const float top_p = prm->top_p;
   const int k = prm->top_k < n ? prm->top_k : n;
+  const int nj = REG ? kRegPerThread : (n + kST - 1) / kST;
+  float rv[REG ? kRegPerThread : 1];
+  auto get = [&](int j) -> float {
+    if constexpr (REG) return rv[j];
+    else return p[tid + kST * j];
+  };
+  auto put = [&](int j, float x) {
+    if constexpr (REG) rv[j] = x;
+    else p[tid + kST * j] = x;
+  };
 
   // temperature and softmax
   float mx = -INFINITY;
-  for (int i = tid; i < n; i += kST) {
-    const float v = __fmul_rn(logits[i], inv_temp);
-    p[i] = v;
+#pragma unroll
+  for (int j = 0; j < nj; j++) {
+    const int i = tid + kST * j;
+    const float v = i < n ? __fmul_rn(logits[i], inv_temp) : -INFINITY;
+    if (REG || i < n) put(j, v);
     mx = fmaxf(mx, v);
   }
   mx = st_max(mx, red);
   float s = 0.f;
-  for (int i = tid; i < n; i += kST) {
-    const float e = expf(p[i] - mx);
-    p[i] = e;
-    s += e;
+#pragma unroll
+  for (int j = 0; j < nj; j++) {
+    if (tid + kST * j < n) {
+      const float e = expf(get(j) - mx);
+      put(j, e);
+      s += e;
+    }
   }
   s = st_sum(s, red);
   if (s > 0.f) {
     const float inv = 1.0f / s;
-    for (int i = tid; i < n; i += kST) p[i] = __fmul_rn(p[i], inv);
+#pragma unroll
+    for (int j = 0; j < nj; j++)
+      if (tid + kST * j < n) put(j, __fmul_rn(get(j), inv));
   }
 
-  // radix select of the k-th largest key, most significant byte first
+  // radix select of the k-th largest key, most significant byte first.  Each
+  // bin is counted in 8 lane-striped copies: probabilities share a handful of
+  // exponents, and single counters would serialise the LDS atomics.
   uint32_t prefix = 0, pmask = 0;
   int remaining = k;
   for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int b = tid; b < 256; b += kST) hist[b] = 0;
+    for (int b = tid; b < 256 * 8; b += kST) hist[b] = 0;
     __syncthreads();
-    for (int i = tid; i < n; i += kST) {
-      const uint32_t key = __float_as_uint(p[i]);
-      if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255], 1);
+#pragma unroll
+    for (int j = 0; j < nj; j++) {
+      const uint32_t key = __float_as_uint(get(j));
+      if (tid + kST * j < n && (key & pmask) == prefix)
+        atomicAdd(&hist[(((key >> shift) & 255) << 3) | (lane & 7)], 1);
     }
     __syncthreads();
-    if (tid == 0) {
-      int cum = 0, d = 255;
-      for (; d > 0; d--) {
-        if (cum + hist[d] >= remaining) break;
-        cum += hist[d];
+    if (wave == 0) {
+      // lane l holds bins 255-4l .. 252-4l; running sums from the top bin down
+      int c[4], s4 = 0;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int b = 255 - 4 * lane - j;
+        int v = 0;
+#pragma unroll
+        for (int r = 0; r < 8; r++) v += hist[(b << 3) | r];
+        c[j] = v;
+        s4 += v;
       }
-      sel[0] = d;
-      sel[1] = remaining - cum;
+      int incl = s4;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(incl, o, CN_WAVE);
+        if (lane >= o) incl += t;
+      }
+      const int excl = incl - s4;
+      if (excl < remaining && remaining <= incl) {  // exactly one lane
+        int cum = excl, j = 0;
+        for (; j < 3; j++) {
+          if (cum + c[j] >= remaining) break;
+          cum += c[j];
+        }
+        sel[0] = 255 - 4 * lane - j;
+        sel[1] = remaining - cum;
+      }
     }
     __syncthreads();
     prefix |= (uint32_t)sel[0] << shift;
@@ -115,44 +162,68 @@ __global__ __launch_bounds__(kST) void sample_kernel(const float* __restrict__ l
   // keys above `prefix` are all taken; of those equal to it, the first
   // `remaining` in index order
 
-  // gather the k winners in index order
-  const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
-  int eq_seen = 0, taken = 0;
-  for (int base = 0; base < n; base += kST) {
-    const int i = base + tid;
-    const uint32_t key = i < n ? __float_as_uint(p[i]) : 0u;
-    const bool gt = i < n && key > prefix;
-    const bool eq = i < n && key == prefix;
-    const uint64_t beq = __ballot(eq);
-    if (lane == 0) wcnt[0][wave] = __popcll(beq);
-    __syncthreads();
-    int eq_before = eq_seen + __popcll(beq & below), eq_tot = 0;
-    for (int w = 0; w < kSW; w++) {
-      if (w < wave) eq_before += wcnt[0][w];
-      eq_tot += wcnt[0][w];
+  // Gather every key >= prefix in any order: the sort below orders them by
+  // (p descending, index ascending), so its first k entries are the winners.
+  if (tid == 0) sel[0] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < nj; j++) {
+    const int i = tid + kST * j;
+    const float v = get(j);
+    if (i < n && __float_as_uint(v) >= prefix) {
+      const int pos = atomicAdd(&sel[0], 1);
+      if (pos < kSampleMaxK) {
+        cp[pos] = v;
+        ci[pos] = i;
+      }
     }
-    const bool take = gt || (eq && eq_before < remaining);
-    const uint64_t bt = __ballot(take);
-    if (lane == 0) wcnt[1][wave] = __popcll(bt);
-    __syncthreads();
-    int pos = taken + __popcll(bt & below), t_tot = 0;
-    for (int w = 0; w < kSW; w++) {
-      if (w < wave) pos += wcnt[1][w];
-      t_tot += wcnt[1][w];
+  }
+  __syncthreads();
+  int m = sel[0];
+  if (m > kSampleMaxK) {
+    // more keys tie at the k-th value than fit: an ordered scan keeps exactly
+    // the k winners, the tied ones with the lowest indices
+    const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+    int eq_seen = 0, taken = 0;
+#pragma unroll
+    for (int j = 0; j < nj; j++) {
+      const int i = tid + kST * j;
+      const float v = get(j);
+      const uint32_t key = i < n ? __float_as_uint(v) : 0u;
+      const bool gt = i < n && key > prefix;
+      const bool eq = i < n && key == prefix;
+      const uint64_t beq = __ballot(eq);
+      if (lane == 0) wcnt[0][wave] = __popcll(beq);
+      __syncthreads();
+      int eq_before = eq_seen + __popcll(beq & below), eq_tot = 0;
+      for (int w = 0; w < kSW; w++) {
+        if (w < wave) eq_before += wcnt[0][w];
+        eq_tot += wcnt[0][w];
+      }
+      const bool take = gt || (eq && eq_before < remaining);
+      const uint64_t bt = __ballot(take);
+      if (lane == 0) wcnt[1][wave] = __popcll(bt);
+      __syncthreads();
+      int pos = taken + __popcll(bt & below), t_tot = 0;
+      for (int w = 0; w < kSW; w++) {
+        if (w < wave) pos += wcnt[1][w];
+        t_tot += wcnt[1][w];
+      }
+      if (take && pos < kSampleMaxK) {
+        cp[pos] = v;
+        ci[pos] = i;
+      }
+      eq_seen += eq_tot;
+      taken += t_tot;
+      __syncthreads();
     }
-    if (take && pos < kSampleMaxK) {
-      cp[pos] = p[i];
-      ci[pos] = i;
-    }
-    eq_seen += eq_tot;
-    taken += t_tot;
-    __syncthreads();
+    m = k;
   }
 
-  // bitonic sort of the winners: p descending, then index ascending
+  // bitonic sort of the gathered keys: p descending, then index ascending
   int k2 = 1;
-  while (k2 < k) k2 <<= 1;
-  for (int j = k + tid; j < k2; j += kST) {
+  while (k2 < m) k2 <<= 1;
+  for (int j = m + tid; j < k2; j += kST) {
     cp[j] = -1.0f;
     ci[j] = 0x7FFFFFFF;
   }
@@ -211,8 +282,12 @@ __global__ __launch_bounds__(kST) void sample_kernel(const float* __restrict__ l
 
 hipError_t sample_launch(const float* logits, int n, const SampleParams* params, const float* draws, int* state,
                          int* out_tokens, int out_cap, float* scratch, hipStream_t st) {
-  hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(kST), 0, st, logits, n, params, draws, state, out_tokens, out_cap,
-                     scratch);
+  if (n <= kST * kRegPerThread)
+    hipLaunchKernelGGL(sample_kernel<true>, dim3(1), dim3(kST), 0, st, logits, n, params, draws, state, out_tokens,
+                       out_cap, scratch);
+  else
+    hipLaunchKernelGGL(sample_kernel<false>, dim3(1), dim3(kST), 0, st, logits, n, params, draws, state, out_tokens,
+                       out_cap, scratch);
   return hipGetLastError();
 }
 

@@ -8,7 +8,8 @@ import numpy as np
 import pytest
 
 import oracle
-from chatnet_amd import TINY_TEST, TINYLLAMA_1B, HipLlamaModel, TemperatureSampler, _native, generate, net_random, synth
+from chatnet_amd import (TINY_TEST, TINYLLAMA_1B, HipLlamaModel, TemperatureSampler, _native, generate, net_random,
+                         synth)
 from gpu_util import announce
 
 pytestmark = pytest.mark.gpu
@@ -24,10 +25,12 @@ def _check(tok, logits, t, k, p, draw, where):
     return True
 
 
-@pytest.mark.parametrize("cfg_name", ["tinyllama-vocab", "tiny"])
+@pytest.mark.parametrize("cfg_name", ["tinyllama-vocab", "tiny", "vocab-40000"])
 def test_sample_matches_oracle(cfg_name):
-    cfg = (TINYLLAMA_1B.replace(n_layers=1, context_length=64) if cfg_name == "tinyllama-vocab"
-           else TINY_TEST)
+    """Vocabularies up to 32768 keep the probabilities in registers, larger
+    ones (40000 here) in a scratch array."""
+    cfg = {"tinyllama-vocab": TINYLLAMA_1B.replace(n_layers=1, context_length=64), "tiny": TINY_TEST,
+           "vocab-40000": TINY_TEST.replace(vocab_size=40000)}[cfg_name]
     ck = synth.llama_checkpoint(cfg, seed=41, mix="q4_0")
     toks = synth.tokens(41, "prompt", 12, cfg.vocab_size)
     draws = net_random(41, 400).astype(np.float32)
