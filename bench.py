@@ -36,13 +36,15 @@ ROOF_SHAPE = (11008, 4096)
 # Q4_K_M-style mix on Llama-2-7B shapes: Q4_K attention + gate/up, Q6_K down + output
 KQ4_SHAPES = [(4096, 4096), (11008, 4096)]
 KQ6_SHAPES = [(4096, 11008), (32000, 4096)]
+# MatVecMulGeneric types on the 7B projection shapes
+GENERIC_SHAPES = [(4096, 4096), (11008, 4096), (4096, 11008)]
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-BLOCK = {2: (32, 18), 12: (256, 144), 14: (256, 210)}  # ggml type -> (weights, bytes) per block
+BLOCK = {2: (32, 18), 8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}  # ggml type -> (weights, bytes) per block
 
 
 def weight_bytes(M: int, K: int, qtype: int = 2) -> int:
@@ -262,7 +264,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-tinyllama", action="store_true")
     ap.add_argument("--no-gemm", action="store_true", help="skip the batched GEMM sweep")
-    ap.add_argument("--no-kquant", action="store_true", help="skip the Q4_K / Q6_K legs")
+    ap.add_argument("--no-kquant", action="store_true", help="skip the Q4_K / Q6_K / Q8_0 / Q5_K legs")
     ap.add_argument("--roofline-only", action="store_true", help="only the isolated GEMV legs")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -290,9 +292,11 @@ def main():
     prefill = None
     kq = None
     if not args.roofline_only and not args.no_kquant:
-        log("Q4_K / Q6_K gemv (cold) and 7B Q4_K_M-style 64-token decode")
+        log("Q4_K / Q6_K / Q8_0 / Q5_K gemv (cold) and 7B Q4_K_M-style 64-token decode")
         kq = {"gemv_q4_k_cold": gemv_sweep(KQ4_SHAPES, qtype=12),
-              "gemv_q6_k_cold": gemv_sweep(KQ6_SHAPES, qtype=14)}
+              "gemv_q6_k_cold": gemv_sweep(KQ6_SHAPES, qtype=14),
+              "gemv_q8_0_cold": gemv_sweep(GENERIC_SHAPES, qtype=8),
+              "gemv_q5_k_cold": gemv_sweep(GENERIC_SHAPES, qtype=13)}
         cfgk = LLAMA2_7B.replace(context_length=2048)
         ckk = synth.llama_checkpoint(cfgk, seed=11, mix="q4_k_m")
         pk = synth.tokens(11, "prompt", 16, cfgk.vocab_size)

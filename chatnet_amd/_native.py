@@ -24,7 +24,9 @@ ERR_OUT_OF_MEMORY = -8
 GGML_F32 = 0
 GGML_F16 = 1
 GGML_Q4_0 = 2
+GGML_Q8_0 = 8
 GGML_Q4_K = 12
+GGML_Q5_K = 13
 GGML_Q6_K = 14
 
 KV_F32 = 0

@@ -66,8 +66,10 @@ int device_cus(int dev) {
   return p.multiProcessorCount;
 }
 
+// Weight types the GEMV serves (LlamaModel.MatVecMulByType, LlamaModel.cs:470-567).
 bool is_matrix_type(uint32_t t) {
-  return t == CHATNET_GGML_Q4_0 || t == CHATNET_GGML_Q4_K || t == CHATNET_GGML_Q6_K;
+  return t == CHATNET_GGML_Q4_0 || t == CHATNET_GGML_Q8_0 || t == CHATNET_GGML_Q4_K || t == CHATNET_GGML_Q5_K ||
+         t == CHATNET_GGML_Q6_K;
 }
 
 // Workspace of chatnet_matmul's batched path (bf16 copy of x + K-split
@@ -396,7 +398,8 @@ int chatnet_upload_tensor(chatnet_model* m, const char* name, uint32_t type, con
                 (unsigned long long)want1);
   if (matrix) {
     if (!is_matrix_type(type))
-      return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "tensor %s: weight type %u not supported (Q4_0, Q4_K, Q6_K)", name, type);
+      return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "tensor %s: weight type %u not supported (Q4_0, Q8_0, Q4_K, Q5_K, Q6_K)",
+                  name, type);
     if (!gemv_supports((int)type, (int)ne0))
       return fail(CHATNET_ERR_INVALID_ARG, "tensor %s: inner dim %llu not a multiple of the block", name,
                   (unsigned long long)ne0);

@@ -29,7 +29,7 @@
 
 namespace {
 
-constexpr int QT_Q4_0 = 2, QT_Q4_K = 12, QT_Q6_K = 14;
+constexpr int QT_Q4_0 = 2, QT_Q8_0 = 8, QT_Q4_K = 12, QT_Q5_K = 13, QT_Q6_K = 14;
 
 template <int QT> struct QTraits;
 template <> struct QTraits<QT_Q4_0> {
@@ -44,6 +44,14 @@ template <> struct QTraits<QT_Q4_K> {
 template <> struct QTraits<QT_Q6_K> {
   static constexpr int UNIT = 256, NDW = 53;
   static constexpr int BLOCK_BYTES = 210, BLOCK = 256;
+};
+template <> struct QTraits<QT_Q8_0> {
+  static constexpr int UNIT = 64, NDW = 17;  // two 34-byte blocks
+  static constexpr int BLOCK_BYTES = 34, BLOCK = 32;
+};
+template <> struct QTraits<QT_Q5_K> {
+  static constexpr int UNIT = 256, NDW = 44;
+  static constexpr int BLOCK_BYTES = 176, BLOCK = 256;
 };
 
 // LDS index of x[k] for a given unit size (4 floats of padding per unit).
@@ -229,6 +237,28 @@ __device__ __forceinline__ void load_unit<QT_Q4_K>(const uint8_t* row, int u, ui
   const cn_u32x4* p = reinterpret_cast<const cn_u32x4*>(row + (size_t)u * 144);
 #pragma unroll
   for (int k = 0; k < 9; k++) {
+    cn_u32x4 t = p[k];
+    w[4 * k + 0] = t.x;
+    w[4 * k + 1] = t.y;
+    w[4 * k + 2] = t.z;
+    w[4 * k + 3] = t.w;
+  }
+}
+
+// Two Q8_0 blocks, 68 bytes: rows hold whole pairs (K % 64 == 0), so a unit
+// starts on a 4-byte boundary.
+template <>
+__device__ __forceinline__ void load_unit<QT_Q8_0>(const uint8_t* row, int u, uint32_t* w) {
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(row + (size_t)u * 68);
+#pragma unroll
+  for (int k = 0; k < 17; k++) w[k] = p[k];
+}
+
+template <>
+__device__ __forceinline__ void load_unit<QT_Q5_K>(const uint8_t* row, int u, uint32_t* w) {
+  const cn_u32x4* p = reinterpret_cast<const cn_u32x4*>(row + (size_t)u * 176);
+#pragma unroll
+  for (int k = 0; k < 11; k++) {
     cn_u32x4 t = p[k];
     w[4 * k + 0] = t.x;
     w[4 * k + 1] = t.y;
@@ -518,11 +548,103 @@ __device__ __forceinline__ void dot_unit_q6_k(const uint32_t (*w)[53], const flo
   for (int i = 0; i < RPW; i++) acc[i] += cn_h2f(w[i][52]) * part[i];
 }
 
+// Q8_0 pair of blocks (DequantQ8_0.cs:51-90): block A is unit bytes 0..33 (d,
+// then 32 int8), block B bytes 34..67.  The int8s are read as the unsigned
+// bytes q + 128 (q ^ 0x80) and 128 times the block's x sum is taken off.
+template <int RPW>
+__device__ __forceinline__ void dot_unit_q8_0(const uint32_t (*w)[17], const float* xs, const float* sx,
+                                              float* acc) {
+#pragma unroll
+  for (int b = 0; b < 2; b++) {
+    float xv[32];
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      const float4 t = *reinterpret_cast<const float4*>(xs + 32 * b + 4 * c);
+      xv[4 * c + 0] = t.x; xv[4 * c + 1] = t.y; xv[4 * c + 2] = t.z; xv[4 * c + 3] = t.w;
+    }
+    const float xsum = sx[b];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      const float d = b == 0 ? cn_h2f(w[i][0]) : cn_h2f(w[i][8] >> 16);
+      float s = 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const uint32_t q =
+            (b == 0 ? __builtin_amdgcn_alignbyte(w[i][k + 1], w[i][k], 2) : w[i][9 + k]) ^ 0x80808080u;
+        s += cn_ubyte<0>(q) * xv[4 * k] + cn_ubyte<1>(q) * xv[4 * k + 1] + cn_ubyte<2>(q) * xv[4 * k + 2] +
+             cn_ubyte<3>(q) * xv[4 * k + 3];
+      }
+      acc[i] += d * (s - 128.f * xsum);
+    }
+  }
+}
+
+// Q5_K super-block (DequantQ5K.cs:37-88): Q4_K's scales and nibble order, plus
+// qh[32] at byte 16 whose bit e%8 of byte e/8 is bit 4 of element e.  For
+// sub-block s that is bit j of dword 4+s for element 32s+j, so four high bits
+// at a time are spread into byte lanes (t * 0x00204081 puts bit b of t at bit
+// 8b) and or-ed above the nibbles: q5 bytes, exact as floats.
+template <int RPW>
+__device__ __forceinline__ void dot_unit_q5_k(const uint32_t (*w)[44], const float* xs, const float* sx,
+                                              float* acc) {
+  float dsc[RPW][8], dmm[RPW][8];
+#pragma unroll
+  for (int i = 0; i < RPW; i++) {
+    const float d = cn_h2f(w[i][0]), dmin = cn_h2f(w[i][0] >> 16);
+    const uint32_t q0 = w[i][1], q1 = w[i][2], q2 = w[i][3];  // scale bytes 0..11
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      int sc, m;
+      if (j < 4) {
+        sc = (q0 >> (8 * j)) & 63;
+        m = (q1 >> (8 * j)) & 63;
+      } else {
+        const uint32_t b8 = (q2 >> (8 * (j - 4))) & 0xFF;
+        sc = (b8 & 0xF) | (((q0 >> (8 * (j - 4) + 6)) & 3) << 4);
+        m = (b8 >> 4) | (((q1 >> (8 * (j - 4) + 6)) & 3) << 4);
+      }
+      dsc[i][j] = d * (float)sc;
+      dmm[i][j] = dmin * (float)m;
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < 8; s++) {
+    float xl[16], xh[16];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const float4 t0 = *reinterpret_cast<const float4*>(xs + 32 * s + 4 * c);
+      const float4 t1 = *reinterpret_cast<const float4*>(xs + 32 * s + 16 + 4 * c);
+      xl[4 * c + 0] = t0.x; xl[4 * c + 1] = t0.y; xl[4 * c + 2] = t0.z; xl[4 * c + 3] = t0.w;
+      xh[4 * c + 0] = t1.x; xh[4 * c + 1] = t1.y; xh[4 * c + 2] = t1.z; xh[4 * c + 3] = t1.w;
+    }
+    const float xsum = sx[s];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      const uint32_t hb = w[i][4 + s];
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const uint32_t dw = w[i][12 + 4 * s + k];
+        const uint32_t tl = (hb >> (4 * k)) & 0xFu, th = (hb >> (16 + 4 * k)) & 0xFu;
+        const uint32_t ql = (dw & 0x0F0F0F0Fu) | (((tl * 0x00204081u) & 0x01010101u) << 4);
+        const uint32_t qh = ((dw >> 4) & 0x0F0F0F0Fu) | (((th * 0x00204081u) & 0x01010101u) << 4);
+        s0 += cn_ubyte<0>(ql) * xl[4 * k] + cn_ubyte<1>(ql) * xl[4 * k + 1] + cn_ubyte<2>(ql) * xl[4 * k + 2] +
+              cn_ubyte<3>(ql) * xl[4 * k + 3];
+        s1 += cn_ubyte<0>(qh) * xh[4 * k] + cn_ubyte<1>(qh) * xh[4 * k + 1] + cn_ubyte<2>(qh) * xh[4 * k + 2] +
+              cn_ubyte<3>(qh) * xh[4 * k + 3];
+      }
+      acc[i] += dsc[i][s] * (s0 + s1) - dmm[i][s] * xsum;
+    }
+  }
+}
+
 template <int QT, int RPW>
 __device__ __forceinline__ void dot_unit(const uint32_t (*w)[QTraits<QT>::NDW], const float* xs,
                                          const float* sx, const float* sx16, float* acc) {
   if constexpr (QT == QT_Q4_0) dot_unit_q4_0<RPW>(w, xs, sx, acc);
   else if constexpr (QT == QT_Q4_K) dot_unit_q4_k<RPW>(w, xs, sx, acc);
+  else if constexpr (QT == QT_Q8_0) dot_unit_q8_0<RPW>(w, xs, sx, acc);
+  else if constexpr (QT == QT_Q5_K) dot_unit_q5_k<RPW>(w, xs, sx, acc);
   else dot_unit_q6_k<RPW>(w, xs, sx16, acc);
 }
 
@@ -863,12 +985,23 @@ struct GemvShape {
 // the 1.1B and 7B shapes.
 // K-quants: one super-block per lane (NU = 1), 2 rows, LPR the smallest power
 // of two covering the row (min 16), 256 threads, at most two workgroups per CU.
+// Q8_0: Q4_0's (LPR, NU) with 2 rows per lane and 256 threads.
 template <int QT>
 GemvShape pick_shape(int K, int n_vrows, int num_cus, bool allow8) {
   using T = QTraits<QT>;
   const int nunits = K / T::UNIT;
   GemvShape s{64, 1, 2, CN_BLOCK, 1};
-  if (QT == QT_Q4_0) {
+  if (QT == QT_Q8_0) {  // Q4_0's (LPR, NU) rule, two rows per lane
+    double best = -1.0;
+    for (int lpr = 64; lpr >= 32; lpr >>= 1)
+      for (int nu = 1; nu <= 4; nu++) {
+        if (lpr * nu < nunits) continue;
+        const double eff = (double)nunits / (double)(lpr * nu);
+        if (eff > best + 1e-9) { best = eff; s.lpr = lpr; s.nu = nu; }
+        break;
+      }
+    if (best < 0) { s.lpr = 64; s.nu = 4; }
+  } else if (QT == QT_Q4_0) {
     double best = -1.0;
     for (int lpr = 64; lpr >= 32; lpr >>= 1)
       for (int nu = 1; nu <= 4; nu++) {
@@ -945,6 +1078,11 @@ hipError_t launch_qt(const GemvArgs& a, int num_cus, hipStream_t st) {
     }
     if (s.nu == 3) return launch_bs<QT, 2, 3, EPI>(a, s, smem, st);
     return launch_bs<QT, 2, 4, EPI>(a, s, smem, st);
+  } else if constexpr (QT == QT_Q8_0) {
+    if (s.nu == 1) return launch_k<QT, 2, 1, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
+    if (s.nu == 2) return launch_k<QT, 2, 2, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
+    if (s.nu == 3) return launch_k<QT, 2, 3, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
+    return launch_k<QT, 2, 4, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
   } else {
     return launch_k<QT, 2, 1, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
   }
@@ -956,6 +1094,8 @@ hipError_t launch_epi(int qtype, const GemvArgs& a, int num_cus, hipStream_t st)
     case QT_Q4_0: return launch_qt<QT_Q4_0, EPI>(a, num_cus, st);
     case QT_Q4_K: return launch_qt<QT_Q4_K, EPI>(a, num_cus, st);
     case QT_Q6_K: return launch_qt<QT_Q6_K, EPI>(a, num_cus, st);
+    case QT_Q8_0: return launch_qt<QT_Q8_0, EPI>(a, num_cus, st);
+    case QT_Q5_K: return launch_qt<QT_Q5_K, EPI>(a, num_cus, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -967,6 +1107,8 @@ size_t gemv_lds_bytes(int qtype, int K) {
     case QT_Q4_0: return gemv_smem_bytes<QT_Q4_0>(K);
     case QT_Q4_K: return gemv_smem_bytes<QT_Q4_K>(K);
     case QT_Q6_K: return gemv_smem_bytes<QT_Q6_K>(K);
+    case QT_Q8_0: return gemv_smem_bytes<QT_Q8_0>(K);
+    case QT_Q5_K: return gemv_smem_bytes<QT_Q5_K>(K);
     default: return 0;
   }
 }
@@ -974,8 +1116,10 @@ size_t gemv_lds_bytes(int qtype, int K) {
 // The launch shapes cover rows of up to 256 lanes x units: K <= 16384.
 bool gemv_supports(int qtype, int K) {
   switch (qtype) {
-    case QT_Q4_0: return K > 0 && K % 64 == 0 && K <= 16384;
+    case QT_Q4_0:
+    case QT_Q8_0: return K > 0 && K % 64 == 0 && K <= 16384;
     case QT_Q4_K:
+    case QT_Q5_K:
     case QT_Q6_K: return K > 0 && K % 256 == 0 && K <= 16384;
     default: return false;
   }

@@ -11,6 +11,10 @@
  *                                  sub-block s owns qs[16s..16s+15] (low nibbles
  *                                  = elements 32s..32s+15, high = 32s+16..31)
  *   Q6_K  DequantQ6K.cs:11-32,53-83 ql[128], qh[64], int8 scales[16], fp16 d
+ *   Q8_0  DequantQ8_0.cs:7-16      fp16 d, 32 int8
+ *   Q5_K  DequantQ5K.cs:7-34,58-83 fp16 d, fp16 dmin, 12 B scales/mins, qh[32]
+ *                                  (bit e%8 of qh[e/8] = bit 4 of element e),
+ *                                  qs[128] in Q4_K's nibble order
  * Every element is a pure function of (seed, stream, index): a splitmix64
  * counter hash feeds a Box-Muller transform, so any tensor can be regenerated
  * bit-identically, in any order, on any number of threads.
@@ -234,12 +238,95 @@ static void quant_block_q6_k(const float* w, uint8_t* out) {
   put16(out + 208, dh);
 }
 
+/* Q8_0: d = max|w| / 127 as fp16, q = round(w / d) clamped to [-127, 127]. */
+static void quant_block_q8_0(const float* w, uint8_t* out) {
+  float amax = 0.f;
+  for (int j = 0; j < 32; j++)
+    if (fabsf(w[j]) > amax) amax = fabsf(w[j]);
+  uint16_t dh = chatnet_float_to_half(amax / 127.0f);
+  float d = half_to_float(dh), id = d != 0.f ? 1.0f / d : 0.f;
+  put16(out, dh);
+  for (int j = 0; j < 32; j++) {
+    int q = nearest_int(w[j] * id);
+    if (q > 127) q = 127;
+    if (q < -127) q = -127;
+    out[2 + j] = (uint8_t)(int8_t)q;
+  }
+}
+
+/* Q5_K: as Q4_K with 5-bit quants (scale = (max - min) / 31), written in the
+ * reference's layout (DequantQ5K.cs:30-34, :58-83): d, dmin, 12 scale bytes,
+ * qh[32] with the high bit of element e at qh[e/8] bit e%8, qs[128] where
+ * sub-block s keeps elements 32s+j / 32s+16+j in the low / high nibble of
+ * qs[16s+j]. */
+static void quant_block_q5_k(const float* w, uint8_t* out) {
+  float scale[8], mins[8], ms = 0.f, mm = 0.f;
+  for (int s = 0; s < 8; s++) {
+    float lo = 0.f, hi = w[32 * s];
+    for (int j = 0; j < 32; j++) {
+      float v = w[32 * s + j];
+      if (v < lo) lo = v;
+      if (v > hi) hi = v;
+    }
+    if (hi < lo) hi = lo;
+    scale[s] = (hi - lo) / 31.0f;
+    mins[s] = -lo;
+    if (scale[s] > ms) ms = scale[s];
+    if (mins[s] > mm) mm = mins[s];
+  }
+  uint16_t dh = chatnet_float_to_half(ms / 63.0f), mh = chatnet_float_to_half(mm / 63.0f);
+  float d = half_to_float(dh), dmin = half_to_float(mh);
+  int sc[8], m[8];
+  for (int s = 0; s < 8; s++) {
+    sc[s] = d > 0.f ? nearest_int(scale[s] / d) : 0;
+    m[s] = dmin > 0.f ? nearest_int(mins[s] / dmin) : 0;
+    if (sc[s] > 63) sc[s] = 63;
+    if (sc[s] < 0) sc[s] = 0;
+    if (m[s] > 63) m[s] = 63;
+    if (m[s] < 0) m[s] = 0;
+  }
+  memset(out, 0, 176);
+  put16(out, dh);
+  put16(out + 2, mh);
+  uint8_t* q = out + 4;
+  for (int j = 0; j < 4; j++) {
+    q[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+    q[j + 4] = (uint8_t)((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+    q[j + 8] = (uint8_t)((sc[j + 4] & 0xF) | ((m[j + 4] & 0xF) << 4));
+  }
+  uint8_t* qh = out + 16;
+  uint8_t* qs = out + 48;
+  for (int s = 0; s < 8; s++) {
+    float ds = d * (float)sc[s], dm = dmin * (float)m[s];
+    for (int j = 0; j < 32; j++) {
+      int e = 32 * s + j;
+      int v = ds > 0.f ? nearest_int((w[e] + dm) / ds) : 0;
+      v = v < 0 ? 0 : (v > 31 ? 31 : v);
+      if (j < 16) qs[16 * s + j] |= (uint8_t)(v & 0xF);
+      else qs[16 * s + j - 16] |= (uint8_t)((v & 0xF) << 4);
+      if (v & 16) qh[e / 8] |= (uint8_t)(1u << (e % 8));
+    }
+  }
+}
+
 static int block_info(uint32_t type, int* blk, int* bytes) {
   switch (type) {
     case 2: *blk = 32; *bytes = 18; return 0;
+    case 8: *blk = 32; *bytes = 34; return 0;
     case 12: *blk = 256; *bytes = 144; return 0;
+    case 13: *blk = 256; *bytes = 176; return 0;
     case 14: *blk = 256; *bytes = 210; return 0;
     default: return -1;
+  }
+}
+
+static void quant_block(uint32_t type, const float* src, uint8_t* dst) {
+  switch (type) {
+    case 2: quant_block_q4_0(src, dst); break;
+    case 8: quant_block_q8_0(src, dst); break;
+    case 12: quant_block_q4_k(src, dst); break;
+    case 13: quant_block_q5_k(src, dst); break;
+    default: quant_block_q6_k(src, dst); break;
   }
 }
 
@@ -253,9 +340,7 @@ EXPORT uint64_t chatnet_synth_quantize(uint32_t type, const float* w, uint64_t n
   for (int64_t b = 0; b < (int64_t)nb; b++) {
     const float* src = w + (uint64_t)b * blk;
     uint8_t* dst = o + (uint64_t)b * bytes;
-    if (type == 2) quant_block_q4_0(src, dst);
-    else if (type == 12) quant_block_q4_k(src, dst);
-    else quant_block_q6_k(src, dst);
+    quant_block(type, src, dst);
   }
   return nb * (uint64_t)bytes;
 }
@@ -285,9 +370,7 @@ EXPORT uint64_t chatnet_synth_tensor(uint32_t type, uint64_t seed, uint64_t stre
       w[j + 1] = (float)(z1 * sigma);
     }
     uint8_t* dst = o + (uint64_t)b * bytes;
-    if (type == 2) quant_block_q4_0(w, dst);
-    else if (type == 12) quant_block_q4_k(w, dst);
-    else quant_block_q6_k(w, dst);
+    quant_block(type, w, dst);
   }
   return nb * (uint64_t)bytes;
 }

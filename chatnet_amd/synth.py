@@ -19,7 +19,8 @@ from .config import LlamaConfig
 SIGMA = 0.02
 
 # Quantization mixes.  "q4_0": every matrix Q4_0.  "q4_k_m": Q4_K for the
-# attention and ffn_gate/up matrices, Q6_K for ffn_down and output.
+# attention and ffn_gate/up matrices, Q6_K for ffn_down and output; "q5_k_m"
+# likewise with Q5_K; "q4_k", "q6_k", "q8_0": every matrix of that type.
 MIXES = {
     "q4_0": {"attn": _native.GGML_Q4_0, "gate_up": _native.GGML_Q4_0, "down": _native.GGML_Q4_0,
              "output": _native.GGML_Q4_0},
@@ -29,6 +30,11 @@ MIXES = {
              "output": _native.GGML_Q4_K},
     "q6_k": {"attn": _native.GGML_Q6_K, "gate_up": _native.GGML_Q6_K, "down": _native.GGML_Q6_K,
              "output": _native.GGML_Q6_K},
+    "q8_0": {"attn": _native.GGML_Q8_0, "gate_up": _native.GGML_Q8_0, "down": _native.GGML_Q8_0,
+             "output": _native.GGML_Q8_0},
+    # Q5_K_M-style: Q5_K attention and ffn_gate/up, Q6_K ffn_down and output
+    "q5_k_m": {"attn": _native.GGML_Q5_K, "gate_up": _native.GGML_Q5_K, "down": _native.GGML_Q6_K,
+               "output": _native.GGML_Q6_K},
 }
 
 

@@ -54,7 +54,9 @@ enum {
   CHATNET_GGML_F32 = 0,
   CHATNET_GGML_F16 = 1,
   CHATNET_GGML_Q4_0 = 2,
+  CHATNET_GGML_Q8_0 = 8,
   CHATNET_GGML_Q4_K = 12,
+  CHATNET_GGML_Q5_K = 13,
   CHATNET_GGML_Q6_K = 14
 };
 

@@ -301,6 +301,92 @@ static float dot_f16_row(const uint8_t* row, const float* x, int n, float* buf) 
   return dot;
 }
 
+/* ---------------------------------------------------------------------------
+ * Q8_0 (DequantQ8_0.cs): fp16 d + 32 int8; value = (sbyte)q * d.
+ * ------------------------------------------------------------------------- */
+
+/* DequantQ8_0.Dequantize (DequantQ8_0.cs:18-41), partial last block included. */
+void oracle_dequant_q8_0(const uint8_t* src, float* out, int n) {
+  int blocks = (n + 31) / 32;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = src + (size_t)b * 34;
+    float scale = h2f(blk);
+    int count = n - 32 * b < 32 ? n - 32 * b : 32;
+    for (int i = 0; i < count; i++) out[32 * b + i] = (float)(int8_t)blk[2 + i] * scale;
+  }
+}
+
+/* DequantQ8_0.DotProductVec128 (DequantQ8_0.cs:51-90): acc0 takes lanes
+ * i..i+3, acc1 lanes i+4..i+7 of each group of 8, as (v * scale) * x. */
+float oracle_dot_q8_0(const uint8_t* row, const float* x, int n) {
+  int blocks = n / 32;
+  float acc0[4] = {0, 0, 0, 0}, acc1[4] = {0, 0, 0, 0};
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* src = row + (size_t)b * 34;
+    const float* in = x + (size_t)b * 32;
+    float scale = h2f(src);
+    for (int i = 0; i < 32; i += 8)
+      for (int l = 0; l < 4; l++) {
+        acc0[l] = acc0[l] + ((float)(int8_t)src[2 + i + l] * scale) * in[i + l];
+        acc1[l] = acc1[l] + ((float)(int8_t)src[2 + i + 4 + l] * scale) * in[i + 4 + l];
+      }
+  }
+  float s[4];
+  for (int l = 0; l < 4; l++) s[l] = acc0[l] + acc1[l];
+  return vsum4(s);
+}
+
+/* ---------------------------------------------------------------------------
+ * Q5_K (DequantQ5K.cs): d, dmin, 12 B scales/mins (Q4_K packing), qh[32] @16,
+ * qs[128] @48 in Q4_K's nibble order; q5 = nibble | (bit e%8 of qh[e/8]) << 4,
+ * value = d*sc[s]*q5 - dmin*m[s].
+ * ------------------------------------------------------------------------- */
+static inline int q5k_q(const uint8_t* blk, int e) {
+  int s = e / 32, j = e % 32;
+  int nib = j < 16 ? (blk[48 + 16 * s + j] & 0x0F) : ((blk[48 + 16 * s + j - 16] >> 4) & 0x0F);
+  int hb = (blk[16 + e / 8] >> (e % 8)) & 1;
+  return nib | (hb << 4);
+}
+
+/* DequantQ5K.Dequantize (DequantQ5K.cs:37-88). */
+void oracle_dequant_q5_k(const uint8_t* src, float* out, int n) {
+  int blocks = n / 256;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = src + (size_t)b * 176;
+    float d = h2f(blk + 0), dmin = h2f(blk + 2);
+    int sc[8], m[8];
+    q4k_scales(blk + 4, sc, m);
+    for (int e = 0; e < 256; e++) {
+      float dsc = d * (float)sc[e / 32], dm = dmin * (float)m[e / 32];
+      out[(size_t)b * 256 + e] = dsc * (float)q5k_q(blk, e) - dm;
+    }
+  }
+}
+
+/* DequantQ5K.DotProductScalar (DequantQ5K.cs:97-151): one sequential sum per
+ * super-block, added to the row sum. */
+float oracle_dot_q5_k(const uint8_t* row, const float* x, int n) {
+  int blocks = n / 256;
+  float sum = 0.0f;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = row + (size_t)b * 176;
+    const float* in = x + (size_t)b * 256;
+    float d = h2f(blk + 0), dmin = h2f(blk + 2);
+    int sc[8], m[8];
+    q4k_scales(blk + 4, sc, m);
+    float blockSum = 0.0f;
+    for (int s = 0; s < 8; s++) {
+      float dsc = d * (float)sc[s], dm = dmin * (float)m[s];
+      for (int j = 0; j < 32; j++) {
+        int e = 32 * s + j;
+        blockSum = blockSum + (dsc * (float)q5k_q(blk, e) - dm) * in[e];
+      }
+    }
+    sum = sum + blockSum;
+  }
+  return sum;
+}
+
 /* TensorMath.MatVecMulQ4_0 / MatVecMulQ6K / MatVecMulGeneric / MatVecMul
  * (TensorMath.cs:527-656) dispatched as LlamaModel.MatVecMulByType
  * (LlamaModel.cs:470-567).  Rows are independent (TensorMath.cs:47-51), so the
@@ -313,6 +399,8 @@ int oracle_matvec(uint32_t type, const void* W, const float* x, float* y, int M,
     case ORACLE_Q4_0: bpr = (size_t)(K / 32) * 18; dot = oracle_dot_q4_0; break;
     case ORACLE_Q4_K: bpr = (size_t)(K / 256) * 144; dot = oracle_dot_q4_k; break;
     case ORACLE_Q6_K: bpr = (size_t)(K / 256) * 210; dot = oracle_dot_q6_k; break;
+    case ORACLE_Q8_0: bpr = (size_t)(K / 32) * 34; dot = oracle_dot_q8_0; break;
+    case ORACLE_Q5_K: bpr = (size_t)(K / 256) * 176; dot = oracle_dot_q5_k; break;
     case ORACLE_F32: {
       const float* wf = (const float*)W;
       for (int r = 0; r < M; r++) y[r] = oracle_dot_f32(wf + (size_t)r * K, x, K);

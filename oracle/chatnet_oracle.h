@@ -22,6 +22,10 @@
  *                     float64 brute force.
  *   q6_k dequant/dot  reference KATs QuantizationTests.cs:302-345, a
  *                     hand-derived element-position KAT, float64 brute force.
+ *   q8_0 dequant/dot  reference KATs QuantizationTests.cs:235-295 and float64
+ *                     brute force.
+ *   q5_k dequant/dot  reference KAT QuantizationTests.cs:513-537 (dot 5184),
+ *                     a hand-derived high-bit position KAT, float64 brute force.
  *   rmsnorm/rope/softmax/silu/add/attention/argmax: invariants (closed forms,
  *                     identity at pos 0, norm preservation, shift invariance,
  *                     tie rule) and a float64 numpy restatement of a tiny model.
@@ -44,7 +48,8 @@
 extern "C" {
 #endif
 
-enum { ORACLE_F32 = 0, ORACLE_F16 = 1, ORACLE_Q4_0 = 2, ORACLE_Q4_K = 12, ORACLE_Q6_K = 14 };
+enum { ORACLE_F32 = 0, ORACLE_F16 = 1, ORACLE_Q4_0 = 2, ORACLE_Q8_0 = 8, ORACLE_Q4_K = 12, ORACLE_Q5_K = 13,
+       ORACLE_Q6_K = 14 };
 
 void oracle_set_threads(int n);
 int oracle_get_threads(void);
@@ -57,6 +62,10 @@ void oracle_dequant_q4_k(const uint8_t* src, float* out, int n);
 float oracle_dot_q4_k(const uint8_t* row, const float* x, int n);
 void oracle_dequant_q6_k(const uint8_t* src, float* out, int n);
 float oracle_dot_q6_k(const uint8_t* row, const float* x, int n);
+void oracle_dequant_q8_0(const uint8_t* src, float* out, int n);
+float oracle_dot_q8_0(const uint8_t* row, const float* x, int n);
+void oracle_dequant_q5_k(const uint8_t* src, float* out, int n);
+float oracle_dot_q5_k(const uint8_t* row, const float* x, int n);
 float oracle_dot_f32(const float* a, const float* b, int n);
 
 /* y[m] = dot(W row m, x) for m < M (MatVecMulByType semantics). Returns 0 or -3

@@ -15,7 +15,8 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(HERE, "liboracle.so")
 
-F32, F16, Q4_0, Q4_K, Q6_K = 0, 1, 2, 12, 14
+F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 2, 8, 12, 13, 14
+_NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q5_K: "q5_k", Q6_K: "q6_k"}
 _P = ctypes.c_void_p
 _lib = None
 
@@ -41,7 +42,7 @@ def lib() -> ctypes.CDLL:
         L.oracle_get_threads.restype = ctypes.c_int
         L.oracle_half_to_float.restype = ctypes.c_float
         L.oracle_half_to_float.argtypes = [ctypes.c_uint16]
-        for q in ("q4_0", "q4_k", "q6_k"):
+        for q in ("q4_0", "q4_k", "q6_k", "q8_0", "q5_k"):
             getattr(L, f"oracle_dequant_{q}").argtypes = [_P, _P, ctypes.c_int]
             getattr(L, f"oracle_dequant_{q}").restype = None
             getattr(L, f"oracle_dot_{q}").argtypes = [_P, _P, ctypes.c_int]
@@ -88,14 +89,14 @@ def half_to_float(h: int) -> float:
 
 def dequant(qtype: int, data: np.ndarray, n: int) -> np.ndarray:
     out = np.empty(n, dtype=np.float32)
-    name = {Q4_0: "q4_0", Q4_K: "q4_k", Q6_K: "q6_k"}[qtype]
+    name = _NAMES[qtype]
     d = np.ascontiguousarray(data, dtype=np.uint8)
     getattr(lib(), f"oracle_dequant_{name}")(d.ctypes.data, out.ctypes.data, n)
     return out
 
 
 def dot(qtype: int, row: np.ndarray, x: np.ndarray) -> float:
-    name = {Q4_0: "q4_0", Q4_K: "q4_k", Q6_K: "q6_k"}[qtype]
+    name = _NAMES[qtype]
     r = np.ascontiguousarray(row, dtype=np.uint8)
     xx = _f32(x)
     return float(getattr(lib(), f"oracle_dot_{name}")(r.ctypes.data, xx.ctypes.data, xx.size))

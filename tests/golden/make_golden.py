@@ -1,7 +1,7 @@
 """Writes the golden fixtures of tests/golden/ (run from the repository root).
 
 Fixtures are data only: seeded inputs and the CPU oracle's outputs for them.
-  blocks_q4_0.npz / blocks_q4_k.npz / blocks_q6_k.npz
+  blocks_{q4_0,q4_k,q6_k,q8_0,q5_k}.npz
       raw blocks of 16 rows x 512 weights, an x vector, and the oracle's
       dequantized rows and row dots (DequantQ*.Dequantize / DotProduct).
   tiny_llama_q4_0.npz
@@ -9,6 +9,8 @@ Fixtures are data only: seeded inputs and the CPU oracle's outputs for them.
       prompt, the logits after the prompt and 16 greedy tokens.
 The weights of the tiny model are not stored: they are a pure function of the
 seed (chatnet_amd.synth), and the test regenerates and checksums them.
+Existing fixtures are kept (their bytes would only differ in zip timestamps);
+pass --force to rewrite them.
 """
 import hashlib
 import os
@@ -34,7 +36,11 @@ def checkpoint_digest(ck) -> str:
 
 
 def main():
-    for qtype, tag in ((oracle.Q4_0, "q4_0"), (oracle.Q4_K, "q4_k"), (oracle.Q6_K, "q6_k")):
+    force = "--force" in sys.argv[1:]
+    for qtype, tag in ((oracle.Q4_0, "q4_0"), (oracle.Q4_K, "q4_k"), (oracle.Q6_K, "q6_k"), (oracle.Q8_0, "q8_0"),
+                       (oracle.Q5_K, "q5_k")):
+        if os.path.exists(os.path.join(OUT, f"blocks_{tag}.npz")) and not force:
+            continue
         rows, K = 16, 512
         t = synth.tensor(qtype, 2024, f"golden-{tag}", rows, K)
         x = synth.normal(2024, f"golden-x-{tag}", K, 1.0)
@@ -42,6 +48,9 @@ def main():
         dots = oracle.matvec(qtype, t.data, x, rows, K)
         np.savez_compressed(os.path.join(OUT, f"blocks_{tag}.npz"), raw=t.data, x=x, dequant=deq, dots=dots,
                             rows=rows, K=K, ggml_type=qtype)
+    if os.path.exists(os.path.join(OUT, "tiny_llama_q4_0.npz")) and not force:
+        print("fixtures written to", OUT)
+        return
     cfg = TINY_TEST
     ck = synth.llama_checkpoint(cfg, seed=77, mix="q4_0")
     prompt = synth.tokens(77, "golden-prompt", 8, cfg.vocab_size)

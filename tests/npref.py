@@ -65,7 +65,26 @@ def dequant_q6_k(raw: np.ndarray, n: int) -> np.ndarray:
     return (out * d[:, None]).ravel()[:n]
 
 
-DEQUANT = {2: dequant_q4_0, 12: dequant_q4_k, 14: dequant_q6_k}
+def dequant_q8_0(raw: np.ndarray, n: int) -> np.ndarray:
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, 34)
+    d = half(b[:, 0].astype(np.uint16) | (b[:, 1].astype(np.uint16) << 8))
+    q = b[:, 2:].view(np.int8).astype(np.float64)
+    return (q * d[:, None]).ravel()[:n]
+
+
+def dequant_q5_k(raw: np.ndarray, n: int) -> np.ndarray:
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, 176)
+    d = half(b[:, 0].astype(np.uint16) | (b[:, 1].astype(np.uint16) << 8))
+    dmin = half(b[:, 2].astype(np.uint16) | (b[:, 3].astype(np.uint16) << 8))
+    sc, m = q4k_scales(b[:, 4:16])
+    qh = np.unpackbits(b[:, 16:48], axis=1, bitorder="little").reshape(-1, 8, 32)  # bit e of qh
+    qs = b[:, 48:].reshape(-1, 8, 16)
+    q = np.concatenate([qs & 0x0F, qs >> 4], axis=2).astype(np.float64) + 16.0 * qh
+    val = d[:, None, None] * sc[:, :, None] * q - dmin[:, None, None] * m[:, :, None]
+    return val.reshape(-1)[:n]
+
+
+DEQUANT = {2: dequant_q4_0, 8: dequant_q8_0, 12: dequant_q4_k, 13: dequant_q5_k, 14: dequant_q6_k}
 
 
 def matrix(t) -> np.ndarray:

@@ -17,7 +17,7 @@ def load(name):
     return np.load(os.path.join(GOLD, name), allow_pickle=False)
 
 
-@pytest.mark.parametrize("tag", ["q4_0", "q4_k", "q6_k"])
+@pytest.mark.parametrize("tag", ["q4_0", "q4_k", "q6_k", "q8_0", "q5_k"])
 def test_block_fixtures_reproduce(tag):
     g = load(f"blocks_{tag}.npz")
     qtype, rows, K = int(g["ggml_type"]), int(g["rows"]), int(g["K"])
@@ -52,7 +52,7 @@ def test_tiny_model_fixture_reproduces():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("tag", ["q4_0", "q4_k", "q6_k"])
+@pytest.mark.parametrize("tag", ["q4_0", "q4_k", "q6_k", "q8_0", "q5_k"])
 def test_gpu_matches_block_fixtures(tag):
     from gpu_util import announce, gpu_matmul, normwise
 

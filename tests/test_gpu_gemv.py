@@ -17,6 +17,9 @@ TOL = 1e-3
 Q4_0_SHAPES = [(2048, 2048), (256, 2048), (5632, 2048), (2048, 5632), (32000, 2048), (4096, 4096),
                (11008, 4096)]
 KQ_SHAPES = [(12, 4096, 4096), (12, 11008, 4096), (14, 4096, 11008), (14, 32000, 4096)]
+# Q8_0 and Q5_K (MatVecMulGeneric types, LlamaModel.cs:501-519) on the 7B shapes.
+GENERIC_SHAPES = [(8, 4096, 4096), (8, 11008, 4096), (8, 4096, 11008), (8, 32000, 4096),
+                  (13, 4096, 4096), (13, 11008, 4096), (13, 4096, 11008)]
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -48,8 +51,15 @@ def test_kquant_gemv_shapes(qtype, M, K):
     run_case(qtype, M, K)
 
 
+@pytest.mark.parametrize("qtype,M,K", GENERIC_SHAPES)
+def test_generic_type_gemv_shapes(qtype, M, K):
+    run_case(qtype, M, K)
+
+
 @pytest.mark.parametrize("qtype,M,K", [
     (2, 1, 64), (2, 3, 64), (2, 17, 192), (2, 33, 2048), (2, 130, 5632), (2, 7, 11008),
+    (8, 1, 64), (8, 3, 128), (8, 17, 192), (8, 33, 2048), (8, 5, 16384),   # 1..4 units per lane
+    (13, 1, 256), (13, 9, 768), (13, 40, 2816),
     (12, 1, 256), (12, 5, 768), (12, 31, 11008),
     (14, 1, 256), (14, 9, 768), (14, 18, 1280),   # 768/1280: rows start 2 bytes off a dword
 ])

@@ -35,7 +35,8 @@ def compare_greedy(gpu_tokens, ora_tokens, margins):
 
 
 @pytest.mark.parametrize("mix,kv", [("q4_0", _native.KV_F32), ("q4_k_m", _native.KV_F32),
-                                    ("q4_0", _native.KV_F16)])
+                                    ("q4_0", _native.KV_F16), ("q8_0", _native.KV_F32),
+                                    ("q5_k_m", _native.KV_F32)])
 def test_tiny_model_logits_token_by_token(mix, kv):
     cfg = TINY_TEST.replace(kv_dtype=kv)
     ck = synth.llama_checkpoint(cfg, seed=21, mix=mix)
@@ -151,7 +152,7 @@ def test_error_paths():
         with pytest.raises(_native.ChatnetSizeMismatch):
             m.upload_tensor("blk.0.attn_q.weight", t.type, (cfg.dim, cfg.dim // 2), t.data[: t.data.size // 2])
         with pytest.raises(_native.ChatnetNotSupported):
-            m.upload_tensor("blk.0.attn_q.weight", 8, t.dims, np.zeros(cfg.dim * cfg.dim // 32 * 34, np.uint8))
+            m.upload_tensor("blk.0.attn_q.weight", 6, t.dims, np.zeros(cfg.dim * cfg.dim // 32 * 22, np.uint8))  # Q5_0
         with pytest.raises(_native.ChatnetKeyNotFound):
             m.upload_tensor("blk.9.attn_q.weight", t.type, t.dims, t.data)
         for name, tt in ck.items():

@@ -166,8 +166,71 @@ def test_q6_k_element_positions_and_signed_scales():
     assert np.array_equal(deq, want)
 
 
+# ---------------------------------------------------------------- Q8_0
+def test_q8_0_dequantize():  # QuantizationTests.cs:237-270
+    blk = np.frombuffer(h16(0.5) + bytes([10] * 32), np.uint8)
+    assert np.all(oracle.dequant(oracle.Q8_0, blk, 32) == 5.0)
+    blk = np.frombuffer(h16(1.0) + bytes([0xF6] * 32), np.uint8)
+    assert np.all(oracle.dequant(oracle.Q8_0, blk, 32) == -10.0)
+
+
+def test_q8_0_dot():  # QuantizationTests.cs:273-295: 0.25 * (0 + 1 + ... + 31)
+    blk = np.frombuffer(h16(0.25) + bytes(range(32)), np.uint8)
+    assert oracle.dot(oracle.Q8_0, blk, np.ones(32, np.float32)) == 124.0
+
+
+def test_q8_0_element_positions_and_partial_block():
+    q = bytes([0] * 32)
+    blk = bytearray(h16(2.0) + q + h16(-1.0) + q)
+    blk[2 + 5] = 0x81        # block 0 element 5 = -127 * 2
+    blk[34 + 2 + 31] = 3     # block 1 element 31 = 3 * -1
+    deq = oracle.dequant(oracle.Q8_0, np.frombuffer(bytes(blk), np.uint8), 64)
+    want = np.zeros(64, np.float32)
+    want[5], want[63] = -254.0, -3.0
+    assert np.array_equal(deq, want)
+    assert np.array_equal(oracle.dequant(oracle.Q8_0, np.frombuffer(bytes(blk), np.uint8), 40), want[:40])
+
+
+# ---------------------------------------------------------------- Q5_K
+def q5k_block(d, dmin, scale_byte, qs_byte, qh=bytes(32)):
+    return np.frombuffer(h16(d) + h16(dmin) + bytes([scale_byte] * 12) + qh + bytes([qs_byte] * 128), np.uint8)
+
+
+def test_q5_k_dot_closed_form():  # QuantizationTests.cs:513-537
+    # sc = m = 17 for sub-blocks 0..3 and 1 for 4..7, q5 = 5:
+    # 4*32*(0.5*17*5 - 0.25*17) + 4*32*(0.5*1*5 - 0.25*1) = 5184
+    blk = q5k_block(0.5, 0.25, 0x11, 0x55)
+    assert oracle.dot(oracle.Q5_K, blk, np.ones(256, np.float32)) == 5184.0
+
+
+def test_q5_k_finite():  # QuantizationTests.cs:495-511
+    raw = bytearray(176)
+    raw[0:2], raw[2:4], raw[4:16] = h16(1.0), h16(0.5), bytes([0x11] * 12)
+    assert np.all(np.isfinite(oracle.dequant(oracle.Q5_K, np.frombuffer(bytes(raw), np.uint8), 256)))
+
+
+def test_q5_k_high_bit_positions():
+    """Bit e%8 of qh[e/8] adds 16 to element e only (DequantQ5K.cs:67-80), in the
+    reference's nibble order (qs[16s+j] low -> 32s+j, high -> 32s+16+j)."""
+    base = oracle.dequant(oracle.Q5_K, q5k_block(1.0, 0.0, 0x01, 0x00), 256)  # sc = 1, m = 0 -> q5
+    assert np.all(base == 0.0)
+    for e in (0, 7, 8, 31, 32, 47, 100, 255):
+        qh = bytearray(32)
+        qh[e // 8] |= 1 << (e % 8)
+        deq = oracle.dequant(oracle.Q5_K, q5k_block(1.0, 0.0, 0x01, 0x00, bytes(qh)), 256)
+        want = np.zeros(256, np.float32)
+        want[e] = 16.0
+        assert np.array_equal(deq, want), e
+    raw = bytearray(q5k_block(1.0, 0.0, 0x01, 0x00).tobytes())
+    raw[48 + 16 * 3 + 5] = 0x9A  # sub-block 3: element 96+5 gets 0xA, element 96+16+5 gets 0x9
+    deq = oracle.dequant(oracle.Q5_K, np.frombuffer(bytes(raw), np.uint8), 256)
+    want = np.zeros(256, np.float32)
+    want[101], want[117] = 10.0, 9.0
+    assert np.array_equal(deq, want)
+
+
 # ---------------------------------------------------------------- brute force
-@pytest.mark.parametrize("qtype", [oracle.Q4_0, oracle.Q4_K, oracle.Q6_K])
+@pytest.mark.parametrize("qtype", [oracle.Q4_0, oracle.Q4_K, oracle.Q6_K, oracle.Q8_0, oracle.Q5_K])
 def test_dequant_and_dot_match_float64_restatement(qtype):
     rows, K = 48, 512
     t = synth.tensor(qtype, 7, f"bf{qtype}", rows, K)
