@@ -272,7 +272,7 @@ def main():
               "multi-GPU sharding is design-only", file=sys.stderr)
         sys.exit(2)
 
-    from chatnet_amd import LLAMA2_7B, TINYLLAMA_1B, hiprt, synth
+    from chatnet_amd import LLAMA2_7B, QWEN2_0_5B, TINYLLAMA_1B, _native, hiprt, synth
 
     if hiprt.device_count() < 1:
         print("bench.py needs a GPU", file=sys.stderr)
@@ -291,6 +291,7 @@ def main():
     gsweep = None
     prefill = None
     kq = None
+    qwen = None
     if not args.roofline_only and not args.no_kquant:
         log("Q4_K / Q6_K / Q8_0 / Q5_K gemv (cold) and 7B Q4_K_M-style 64-token decode")
         kq = {"gemv_q4_k_cold": gemv_sweep(KQ4_SHAPES, qtype=12),
@@ -338,6 +339,15 @@ def main():
             log("TinyLlama 512-token prefill + 128 decode")
             prefill = prefill_run(cfg1, ck1, 512, 128)
             log(f"  {json.dumps(prefill)}")
+            del ck1
+            cfgq = QWEN2_0_5B.replace(context_length=2048)
+            ckq = synth.llama_checkpoint(cfgq, seed=5, mix="q8_0", with_output=False, embedding=_native.GGML_Q8_0)
+            pq = synth.tokens(5, "prompt", 16, cfgq.vocab_size)
+            dtq, _ = decode_run(cfgq, ckq, pq, 128, 8)
+            qwen = {"qwen2_0_5b_q8_0_decode_tok_s": round(128 / dtq, 1),
+                    "weights_GB": round(synth.checkpoint_bytes(ckq) / 1e9, 3)}
+            log(f"Qwen2-0.5B-shaped Q8_0 (tied embeddings, QKV biases) decode: {json.dumps(qwen)}")
+            del ckq
 
     res = {
         "metric": METRIC,
@@ -360,6 +370,7 @@ def main():
         "gemm_sweep_q4_0_cold": gsweep,
         "tinyllama_q4_0_prefill": prefill,
         "llama2_7b_q4_k_m": kq,
+        "qwen2_0_5b_q8_0": qwen,
         "roofline": {"bound": "hbm", "achieved": roof["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": roof["frac"], "traffic": measured_traffic(ROOF_SHAPE),
                      "traffic_source": "profiles/gemv_q4_0_sweep_roofline.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",

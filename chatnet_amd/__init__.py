@@ -1,12 +1,12 @@
 """chatnet_amd — MI355X-native quantized Llama forward pass for ChatNet.
 
-The hot path of ChatNet (LlamaModel.Forward with the Q4_0 / Q4_K / Q6_K
-dequant-matvecs) as hand-written gfx950 HIP kernels behind a C ABI
+The hot path of ChatNet (LlamaModel.Forward with the Q4_0 / Q8_0 / Q4_K /
+Q5_K / Q6_K dequant-matvecs, and the Mistral and Qwen2 variants of it) as hand-written gfx950 HIP kernels behind a C ABI
 (libchatnet_hip.so, include/chatnet_hip.h).  Python here is a thin host:
 ctypes bindings, the IModel-shaped wrapper and the synthetic-weight tools.
 """
 from . import _native
-from .config import LLAMA2_7B, TINY_TEST, TINYLLAMA_1B, LlamaConfig
+from .config import LLAMA2_7B, QWEN2_0_5B, TINY_TEST, TINYLLAMA_1B, LlamaConfig
 from .engine import GreedySampler, TemperatureSampler, generate, net_random
 from .model import HipLlamaModel
 
@@ -16,6 +16,7 @@ __all__ = [
     "TINYLLAMA_1B",
     "LLAMA2_7B",
     "TINY_TEST",
+    "QWEN2_0_5B",
     "HipLlamaModel",
     "GreedySampler",
     "TemperatureSampler",

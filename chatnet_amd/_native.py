@@ -32,6 +32,10 @@ GGML_Q6_K = 14
 KV_F32 = 0
 KV_F16 = 1
 
+# forward-pass variant (chatnet_config.arch)
+ARCH_LLAMA = 0   # LlamaModel; MistralModel computes the same
+ARCH_QWEN2 = 1   # QwenModel: optional QKV biases, split-half (NeoX) RoPE
+
 
 class ChatnetError(RuntimeError):
     """Base class of errors raised from libchatnet_hip status codes."""
@@ -100,7 +104,7 @@ class ChatnetConfig(ctypes.Structure):
         ("rope_freq_base", ctypes.c_float),
         ("rms_norm_eps", ctypes.c_float),
         ("kv_dtype", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("arch", ctypes.c_int32),
     ]
 
 

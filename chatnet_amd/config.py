@@ -23,6 +23,7 @@ class LlamaConfig:
     rope_freq_base: float = 10000.0
     rms_norm_eps: float = 1e-5
     kv_dtype: int = _native.KV_F32
+    arch: int = _native.ARCH_LLAMA  # ARCH_QWEN2: QwenModel's biases and NeoX RoPE
 
     @property
     def kv_dim(self) -> int:  # LlamaConfig.cs:34
@@ -38,7 +39,7 @@ class LlamaConfig:
     def to_c(self) -> _native.ChatnetConfig:
         return _native.ChatnetConfig(
             self.dim, self.hidden_dim, self.n_layers, self.n_heads, self.n_kv_heads, self.head_dim,
-            self.vocab_size, self.context_length, self.rope_freq_base, self.rms_norm_eps, self.kv_dtype, 0,
+            self.vocab_size, self.context_length, self.rope_freq_base, self.rms_norm_eps, self.kv_dtype, self.arch,
         )
 
 
@@ -51,3 +52,7 @@ LLAMA2_7B = LlamaConfig(dim=4096, hidden_dim=11008, n_layers=32, n_heads=32, n_k
 # A small Llama for tests (GQA, both block sizes usable).
 TINY_TEST = LlamaConfig(dim=256, hidden_dim=512, n_layers=2, n_heads=8, n_kv_heads=2, head_dim=32,
                         vocab_size=512, context_length=64)
+# Qwen2-0.5B architecture (QwenConfig.cs; rope base 1e6, eps 1e-6, tied embeddings).
+QWEN2_0_5B = LlamaConfig(dim=896, hidden_dim=4864, n_layers=24, n_heads=14, n_kv_heads=2, head_dim=64,
+                         vocab_size=151936, context_length=2048, rope_freq_base=1000000.0, rms_norm_eps=1e-6,
+                         arch=_native.ARCH_QWEN2)

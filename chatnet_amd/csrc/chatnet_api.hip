@@ -55,6 +55,10 @@ struct DevTensor {
 
 struct Layer {
   DevTensor attn_norm, ffn_norm, wq, wk, wv, wo, wg, wu, wd;
+  // QKV biases (Qwen2), one fp32 buffer [dim | kv_dim | kv_dim] in the row
+  // order of the stored q/k/v weights; bias_have: bits 0/1/2 = q/k/v uploaded.
+  float* bias = nullptr;
+  unsigned bias_have = 0;
 };
 
 int device_cus(int dev) {
@@ -189,6 +193,20 @@ AttnPlan attn_plan(const chatnet_model* m, int cap) {
   return {splits, chunk};
 }
 
+// Row order of the stored q and k weights of a split-half (NeoX) RoPE model
+// (TensorMath.ApplyRoPENeox, TensorMath.cs:475-520, rotates element j of a head
+// with element j + hd/2): stored row 2j of a head is source row j and stored
+// row 2j+1 is source row j + hd/2.  The interleaved rotation of stored rows
+// (2j, 2j+1), with the angle of pair j, is then the split-half rotation, and
+// ApplyRoPENeox's angle for j, exp(j * (2/hd) * -ln base), equals ApplyRoPE's
+// for the pair at 2j, exp(2j * (1/hd) * -ln base), bit for bit (scaling by 2 is
+// exact).  q and the K cache keep this order: a q.k dot product does not depend
+// on a permutation applied to both.
+int neox_source_row(int r, int hd) {
+  const int t = r % hd;
+  return r - t + t / 2 + (t & 1) * (hd / 2);
+}
+
 void drop_graphs(chatnet_model* m) {
   for (auto& g : m->graphs) {
     if (g) (void)hipGraphExecDestroy(g);
@@ -198,6 +216,35 @@ void drop_graphs(chatnet_model* m) {
     if (g) (void)hipGraphExecDestroy(g);
     g = nullptr;
   }
+}
+
+// QwenWeights' optional biases (QwenWeights.cs:158-170), kept in one buffer
+// per layer [dim | kv_dim | kv_dim] in the stored row order of q/k/v.
+int upload_bias(chatnet_model* m, Layer& L, int which, const char* name, uint32_t type, uint64_t ne0,
+                uint64_t ne1, const void* host) {
+  const chatnet_config& c = m->cfg;
+  if (type != CHATNET_GGML_F32) return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "tensor %s: biases must be F32", name);
+  const int n = which == 0 ? c.dim : m->kv_dim;
+  if (ne0 != (uint64_t)n || ne1 != 1)
+    return fail(CHATNET_ERR_SIZE_MISMATCH, "tensor %s: dims [%llu, %llu], expected [%d]", name,
+                (unsigned long long)ne0, (unsigned long long)ne1, n);
+  HIP_TRY(hipSetDevice(m->device));
+  HIP_TRY(hipStreamSynchronize(m->stream));
+  if (!L.bias) {
+    const size_t bytes = sizeof(float) * (size_t)(c.dim + 2 * m->kv_dim);
+    if (hipMalloc(&L.bias, bytes) != hipSuccess) return fail(CHATNET_ERR_OUT_OF_MEMORY, "hipMalloc of bias failed");
+    HIP_TRY(hipMemset(L.bias, 0, bytes));
+  }
+  const float* src = (const float*)host;
+  std::vector<float> v(src, src + n);
+  if (which < 2)
+    for (int r = 0; r < n; r++) v[r] = src[neox_source_row(r, c.head_dim)];
+  const size_t off = which == 0 ? 0 : (size_t)c.dim + (which == 2 ? m->kv_dim : 0);
+  HIP_TRY(hipMemcpy(L.bias + off, v.data(), sizeof(float) * n, hipMemcpyHostToDevice));
+  L.bias_have |= 1u << which;
+  drop_graphs(m);
+  g_err.clear();
+  return CHATNET_OK;
 }
 
 }  // namespace
@@ -261,7 +308,8 @@ int chatnet_create(const chatnet_config* cfg, int device, chatnet_model** out) {
     return fail(CHATNET_ERR_INVALID_ARG, "context_length %d exceeds 16384", c.context_length);
   if (c.kv_dtype != CHATNET_KV_F32 && c.kv_dtype != CHATNET_KV_F16)
     return fail(CHATNET_ERR_INVALID_ARG, "kv_dtype %d unknown", c.kv_dtype);
-  if (c.reserved != 0) return fail(CHATNET_ERR_INVALID_ARG, "reserved must be 0");
+  if (c.arch != CHATNET_ARCH_LLAMA && c.arch != CHATNET_ARCH_QWEN2)
+    return fail(CHATNET_ERR_INVALID_ARG, "arch %d unknown", c.arch);
   if (!(c.rope_freq_base > 0.f) || !(c.rms_norm_eps >= 0.f))
     return fail(CHATNET_ERR_INVALID_ARG, "rope_freq_base must be > 0 and rms_norm_eps >= 0");
   int ndev = 0;
@@ -333,7 +381,7 @@ void chatnet_destroy(chatnet_model* m) {
   fr(m->emb.ptr); fr(m->out.ptr); fr(m->out_norm.ptr);
   for (auto& l : m->layers) {
     fr(l.attn_norm.ptr); fr(l.ffn_norm.ptr); fr(l.wq.ptr); fr(l.wk.ptr); fr(l.wv.ptr);
-    fr(l.wo.ptr); fr(l.wg.ptr); fr(l.wu.ptr); fr(l.wd.ptr);
+    fr(l.wo.ptr); fr(l.wg.ptr); fr(l.wu.ptr); fr(l.wd.ptr); fr(l.bias);
   }
   fr(m->kcache); fr(m->vcache); fr(m->x); fr(m->q); fr(m->att); fr(m->h); fr(m->logits);
   fr(m->state); fr(m->out_tokens);
@@ -367,8 +415,11 @@ int chatnet_upload_tensor(chatnet_model* m, const char* name, uint32_t type, con
   char suffix[64] = {0};
   if (!strcmp(name, "token_embd.weight")) {
     slot = &m->emb; want0 = c.dim; want1 = c.vocab_size; matrix = false;
-    if (type != CHATNET_GGML_F32 && type != CHATNET_GGML_F16 && type != CHATNET_GGML_Q4_0)
-      return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "token_embd.weight: type %u not supported (F32, F16, Q4_0)", type);
+    if (type != CHATNET_GGML_F32 && type != CHATNET_GGML_F16 && type != CHATNET_GGML_Q4_0 && type != CHATNET_GGML_Q8_0)
+      return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "token_embd.weight: type %u not supported (F32, F16, Q4_0, Q8_0)",
+                  type);
+    if ((type == CHATNET_GGML_Q4_0 || type == CHATNET_GGML_Q8_0) && c.dim % 32 != 0)
+      return fail(CHATNET_ERR_INVALID_ARG, "token_embd.weight: dim %d not a multiple of 32", c.dim);
   } else if (!strcmp(name, "output.weight")) {
     slot = &m->out; want0 = c.dim; want1 = c.vocab_size;
   } else if (!strcmp(name, "output_norm.weight")) {
@@ -390,6 +441,9 @@ int chatnet_upload_tensor(chatnet_model* m, const char* name, uint32_t type, con
     };
     for (auto& e : tab)
       if (!strcmp(suffix, e.s)) { slot = e.t; want0 = e.k; want1 = e.r; matrix = e.mat; }
+    const char* bias_names[3] = {"attn_q.bias", "attn_k.bias", "attn_v.bias"};
+    for (int which = 0; which < 3 && !slot && c.arch == CHATNET_ARCH_QWEN2; which++)
+      if (!strcmp(suffix, bias_names[which])) return upload_bias(m, L, which, name, type, ne0, ne1, host);
   }
   if (!slot) return fail(CHATNET_ERR_NOT_FOUND, "tensor %s is not part of the Llama layout", name);
   if (ne0 != want0 || ne1 != want1)
@@ -415,7 +469,17 @@ int chatnet_upload_tensor(chatnet_model* m, const char* name, uint32_t type, con
   // 256 bytes of tail padding keep every vector load of the kernels in bounds.
   if (hipMalloc(&slot->ptr, nbytes + 256) != hipSuccess)
     return fail(CHATNET_ERR_OUT_OF_MEMORY, "hipMalloc of %llu bytes for %s failed", (unsigned long long)nbytes, name);
-  HIP_TRY(hipMemcpy(slot->ptr, host, nbytes, hipMemcpyHostToDevice));
+  const bool neox_rows = c.arch == CHATNET_ARCH_QWEN2 && layer >= 0 &&
+                         (slot == &m->layers[layer].wq || slot == &m->layers[layer].wk);
+  if (neox_rows) {
+    const size_t bpr = (size_t)(nbytes / ne1);
+    std::vector<uint8_t> rows(nbytes);
+    for (uint64_t r = 0; r < ne1; r++)
+      memcpy(rows.data() + r * bpr, (const uint8_t*)host + (size_t)neox_source_row((int)r, c.head_dim) * bpr, bpr);
+    HIP_TRY(hipMemcpy(slot->ptr, rows.data(), nbytes, hipMemcpyHostToDevice));
+  } else {
+    HIP_TRY(hipMemcpy(slot->ptr, host, nbytes, hipMemcpyHostToDevice));
+  }
   HIP_TRY(hipMemset((char*)slot->ptr + nbytes, 0, 256));
   slot->type = type;
   slot->nbytes = nbytes;
@@ -433,10 +497,12 @@ namespace {
 int check_complete(const chatnet_model* m) {
   if (!m->emb.ptr) return fail(CHATNET_ERR_NOT_FOUND, "tensor token_embd.weight not uploaded");
   if (!m->out_norm.ptr) return fail(CHATNET_ERR_NOT_FOUND, "tensor output_norm.weight not uploaded");
-  if (!m->out.ptr) {
-    // LlamaWeights.cs:89-98 falls back to the tied embedding; only quantized
-    // LM heads run on the device GEMV.
-    return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "output.weight missing: tied F32/F16 embeddings as LM head are not supported");
+  if (!m->out.ptr && (!is_matrix_type(m->emb.type) || !gemv_supports((int)m->emb.type, m->cfg.dim))) {
+    // LlamaWeights.cs:89-98 / QwenWeights.cs:103-112 fall back to the tied
+    // embedding; the LM head runs on the quantized GEMV only.
+    return fail(CHATNET_ERR_UNSUPPORTED_TYPE,
+                "output.weight missing: the tied token_embd.weight (type %u) cannot be the LM head (Q4_0, Q8_0)",
+                m->emb.type);
   }
   for (size_t l = 0; l < m->layers.size(); l++) {
     const Layer& L = m->layers[l];
@@ -444,9 +510,18 @@ int check_complete(const chatnet_model* m) {
     const char* nm[] = {"attn_norm", "ffn_norm", "attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"};
     for (int i = 0; i < 9; i++)
       if (!ts[i]->ptr) return fail(CHATNET_ERR_NOT_FOUND, "tensor blk.%zu.%s.weight not uploaded", l, nm[i]);
+    // QwenWeights.cs:164-169: with the q bias present, k and v are looked up too
+    const char* bn[3] = {"attn_q", "attn_k", "attn_v"};
+    if (L.bias_have)
+      for (int i = 0; i < 3; i++)
+        if (!(L.bias_have & (1u << i)))
+          return fail(CHATNET_ERR_NOT_FOUND, "tensor blk.%zu.%s.bias not uploaded", l, bn[i]);
   }
   return CHATNET_OK;
 }
+
+// output.weight, or the tied embedding when it is absent (LlamaWeights.cs:89-98).
+const DevTensor& lm_head_tensor(const chatnet_model* m) { return m->out.ptr ? m->out : m->emb; }
 
 GemvArgs base_args(const chatnet_model* m) {
   GemvArgs a;
@@ -477,6 +552,7 @@ int launch_token(chatnet_model* m, bool lm_head, int cap) {
     a.out[0] = m->q;
     a.kcache = (char*)m->kcache + loff;
     a.vcache = (char*)m->vcache + loff;
+    a.bias = L.bias_have ? L.bias : nullptr;  // QwenModel.cs:104-120
     if (L.wq.type == L.wk.type && L.wk.type == L.wv.type) {
       a.w[0] = (const uint8_t*)L.wq.ptr;
       a.w[1] = (const uint8_t*)L.wk.ptr;
@@ -496,6 +572,7 @@ int launch_token(chatnet_model* m, bool lm_head, int cap) {
         b.seg_rows[1] = s == 1 ? rows[1] : 0;
         b.seg_rows[2] = s == 2 ? rows[2] : 0;
         b.n_vrows = rows[s];
+        if (b.bias) b.bias += s == 0 ? 0 : c.dim + (s == 2 ? kvd : 0);
         HIP_TRY(gemv_launch((int)ts[s]->type, GEMV_EPI_QKV, b, m->num_cus, st));
       }
     }
@@ -557,11 +634,11 @@ int launch_token(chatnet_model* m, bool lm_head, int cap) {
     o.K = c.dim;
     o.x = m->x;
     o.norm_w = (const float*)m->out_norm.ptr;
-    o.w[0] = (const uint8_t*)m->out.ptr;
+    o.w[0] = (const uint8_t*)lm_head_tensor(m).ptr;
     o.seg_rows[0] = c.vocab_size;
     o.n_vrows = c.vocab_size;
     o.out[0] = m->logits;
-    HIP_TRY(gemv_launch((int)m->out.type, GEMV_EPI_LOGITS, o, m->num_cus, st));
+    HIP_TRY(gemv_launch((int)lm_head_tensor(m).type, GEMV_EPI_LOGITS, o, m->num_cus, st));
   }
   return CHATNET_OK;
 }
@@ -692,6 +769,7 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position) {
       r.kcache = kc;
       r.vcache = vc;
       r.kv_f16 = c.kv_dtype == CHATNET_KV_F16;
+      r.bias = L.bias_have ? L.bias : nullptr;
       HIP_TRY(rope_kv_launch(r, cn, st));
 
       PrefillAttnArgs at;
@@ -771,11 +849,11 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position) {
   o.K = c.dim;
   o.x = m->sp_x + (size_t)(last_rows - 1) * c.dim;
   o.norm_w = (const float*)m->out_norm.ptr;
-  o.w[0] = (const uint8_t*)m->out.ptr;
+  o.w[0] = (const uint8_t*)lm_head_tensor(m).ptr;
   o.seg_rows[0] = c.vocab_size;
   o.n_vrows = c.vocab_size;
   o.out[0] = m->logits;
-  HIP_TRY(gemv_launch((int)m->out.type, GEMV_EPI_LOGITS, o, m->num_cus, st));
+  HIP_TRY(gemv_launch((int)lm_head_tensor(m).type, GEMV_EPI_LOGITS, o, m->num_cus, st));
   m->have_logits = true;
   m->next_pos = position + n;
   m->last_tok = tokens[n - 1];

@@ -18,6 +18,10 @@ __global__ __launch_bounds__(CN_BLOCK) void embed_kernel(const void* emb, int ty
   } else if (type == 1) {
     const uint16_t* e = reinterpret_cast<const uint16_t*>(emb);
     x[i] = cn_h2f(e[(size_t)t * dim + i]);
+  } else if (type == 8) {  // Q8_0: DequantQ8_0.Dequantize (DequantQ8_0.cs:19-41), qs[j] * d
+    const uint8_t* blk = reinterpret_cast<const uint8_t*>(emb) + ((size_t)t * (dim / 32) + i / 32) * 34;
+    const float d = cn_h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+    x[i] = (float)(int8_t)blk[2 + (i & 31)] * d;
   } else {  // Q4_0
     const uint8_t* row = reinterpret_cast<const uint8_t*>(emb) + (size_t)t * (dim / 32) * 18;
     const uint8_t* blk = row + (size_t)(i / 32) * 18;

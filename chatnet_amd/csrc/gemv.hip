@@ -685,11 +685,15 @@ __device__ __forceinline__ void map_row(const GemvArgs& a, int vr, int& seg, int
 //   ADD: the residual rows;
 //   QKV: (cos, sin) of each q/k row pair at position pos from the RoPE table
 //        (TensorMath.ApplyRoPE's angle, TensorMath.cs:418-432), the pair index
-//        being the row's offset within its head.
+//        being the row's offset within its head, in res[0..RPW); with a bias
+//        (QwenModel.cs:104-120) the rows' biases in res[RPW..2*RPW).
 template <int EPI, int RPW>
-__device__ __forceinline__ void load_residual(const GemvArgs& a, int vr0, int li, int pos, float (&res)[RPW]) {
+constexpr int res_count() { return EPI == GEMV_EPI_QKV ? 2 * RPW : RPW; }
+
+template <int EPI, int RPW, int NR>
+__device__ __forceinline__ void load_residual(const GemvArgs& a, int vr0, int li, int pos, float (&res)[NR]) {
 #pragma unroll
-  for (int i = 0; i < RPW; i++) res[i] = 0.f;
+  for (int i = 0; i < NR; i++) res[i] = 0.f;
   if (li != 0) return;
   if constexpr (EPI == GEMV_EPI_ADD) {
 #pragma unroll
@@ -707,6 +711,11 @@ __device__ __forceinline__ void load_residual(const GemvArgs& a, int vr0, int li
         const float2 cs = a.rope[(size_t)pos * (a.head_dim / 2) + (r % a.head_dim) / 2];
         res[i] = cs.x;
         res[i + 1] = cs.y;
+      }
+      if (vr < a.n_vrows && a.bias) {
+        const float2 b = *reinterpret_cast<const float2*>(a.bias + vr);
+        res[RPW + i] = b.x;
+        res[RPW + i + 1] = b.y;
       }
     }
   }
@@ -733,6 +742,10 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, const float
       a.out[0][r] = (g / (1.0f + expf(-g))) * u;
     } else {  // QKV
       float x0 = v[i], x1 = v[i + 1];
+      if (a.bias) {  // q/k/v += bias before RoPE (QwenModel.cs:104-125)
+        x0 += res[RPW + i];
+        x1 += res[RPW + i + 1];
+      }
       if (seg < 2) {
         const float c = res[i], s = res[i + 1];
         const float y0 = x0 * c - x1 * s;
@@ -820,7 +833,8 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
   int it = blockIdx.x * NWV + wave;
 
   uint32_t w[RPW][NU][T::NDW];
-  float res[RPW];
+  constexpr int NR = res_count<EPI, RPW>();
+  float res[NR];
   const int pos = EPI == GEMV_EPI_QKV ? *a.pos : 0;
 
   // ---- prologue: stage x (optionally RMS-normalised) into LDS ----
@@ -835,7 +849,7 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
     stage_load<MAXT, NORM, BS>(a.x, a.norm_w, K, st);
     // rows past n_vrows come back as zeros, so idle waves need no branch here
     issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
-    load_residual<EPI, RPW>(a, it * RW + sub * RPW, li, pos, res);
+    load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, pos, res);
     uint32_t* xd = reinterpret_cast<uint32_t*>(smem);
     float* xred = reinterpret_cast<float*>(smem) + (size_t)(K >> 6) * XD_UNIT_DW;
     stage_digitize<MAXT, NORM, BS, QT == QT_Q4_K>(st, K, xd, xred);
@@ -862,13 +876,13 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
         }
       }
       const int cur = it;
-      float res_cur[RPW];
+      float res_cur[NR];
 #pragma unroll
-      for (int i = 0; i < RPW; i++) res_cur[i] = res[i];
+      for (int i = 0; i < NR; i++) res_cur[i] = res[i];
       it += wstride;
       if (it < n_iters) {
         issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
-        load_residual<EPI, RPW>(a, it * RW + sub * RPW, li, pos, res);
+        load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, pos, res);
       }
 #pragma unroll
       for (int i = 0; i < RPW; i++) {
@@ -882,7 +896,7 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
   }
   if (it < n_iters) {
     issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
-    load_residual<EPI, RPW>(a, it * RW + sub * RPW, li, pos, res);
+    load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, pos, res);
   }
   float rms = 1.0f;
   if (a.norm_w) {
@@ -940,13 +954,13 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
       }
     }
     const int cur = it;
-    float res_cur[RPW];
+    float res_cur[NR];
 #pragma unroll
-    for (int i = 0; i < RPW; i++) res_cur[i] = res[i];
+    for (int i = 0; i < NR; i++) res_cur[i] = res[i];
     it += wstride;
     if (it < n_iters) {
       issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
-      load_residual<EPI, RPW>(a, it * RW + sub * RPW, li, pos, res);
+      load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, pos, res);
     }
 #pragma unroll
     for (int i = 0; i < RPW; i++) {

@@ -29,6 +29,7 @@ struct GemvArgs {
   void* vcache;             // layer base of the V cache
   int kv_dim;
   int kv_f16;
+  const float* bias;  // QKV: optional per-row bias added before RoPE, indexed by virtual row
 };
 
 bool gemv_supports(int qtype, int K);
@@ -74,6 +75,7 @@ struct RopeKvArgs {
   void* kcache;  // layer base
   void* vcache;
   int kv_f16;
+  const float* bias;  // optional [dim | kv_dim | kv_dim] added to q | k | v before RoPE
 };
 hipError_t rope_kv_launch(const RopeKvArgs& a, int n, hipStream_t st);
 // Fills tab[p][j] = (cos, sin) of theta = p * exp(2j * dim_inv * neg_log_base),

@@ -34,7 +34,8 @@ __device__ __forceinline__ void rope_pair(float& x0, float& x1, float2 cs) {
 }
 
 // One thread per (token, pair): q pairs rotated in place, k pairs rotated and
-// stored at cache row p0+t, v pairs copied there (LlamaModel.cs:137-153).
+// stored at cache row p0+t, v pairs copied there (LlamaModel.cs:137-153); with
+// a bias, q/k/v get it added first (QwenModel.cs:104-125).
 __global__ __launch_bounds__(CN_BLOCK) void rope_kv_kernel(RopeKvArgs a) {
   const int t = blockIdx.y;
   const int pairs_q = a.dim / 2, pairs_kv = a.kv_dim / 2;
@@ -42,9 +43,12 @@ __global__ __launch_bounds__(CN_BLOCK) void rope_kv_kernel(RopeKvArgs a) {
   if (i >= pairs_q + 2 * pairs_kv) return;
   float* row = a.qkv + (size_t)t * a.ld;
   const int pos = a.p0 + t;
+  float2 b = make_float2(0.f, 0.f);
+  if (a.bias) b = reinterpret_cast<const float2*>(a.bias)[i];
   if (i < pairs_q) {
     float2* p = reinterpret_cast<float2*>(row) + i;
     float2 v = *p;
+    if (a.bias) { v.x += b.x; v.y += b.y; }
     rope_pair(v.x, v.y, a.rope[(size_t)pos * (a.head_dim / 2) + i % (a.head_dim / 2)]);
     *p = v;
     return;
@@ -52,6 +56,7 @@ __global__ __launch_bounds__(CN_BLOCK) void rope_kv_kernel(RopeKvArgs a) {
   const bool is_k = i < pairs_q + pairs_kv;
   const int j = is_k ? i - pairs_q : i - pairs_q - pairs_kv;  // pair index within k or v
   float2 v = reinterpret_cast<const float2*>(row + a.dim + (is_k ? 0 : a.kv_dim))[j];
+  if (a.bias) { v.x += b.x; v.y += b.y; }
   if (is_k) rope_pair(v.x, v.y, a.rope[(size_t)pos * (a.head_dim / 2) + j % (a.head_dim / 2)]);
   const size_t off = (size_t)pos * a.kv_dim + 2 * j;
   void* base = is_k ? a.kcache : a.vcache;

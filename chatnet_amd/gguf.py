@@ -11,7 +11,7 @@ Reader — the rules of src/ChatNet.Core/Gguf/GgufReader.cs:
   ReadTensorInfo (:298-306)  name, u32 n_dims, u64 dims[n_dims], u32 type,
                              u64 offset relative to the data start
   ReadString (:364-377)      u64 length + UTF-8, at most 1 000 000 bytes
-  ExtractModelConfig (:80-182) the llama.* keys with bare-key fallbacks and the
+  ExtractModelConfig (:80-182) the <architecture>.* keys with bare-key fallbacks and the
                              defaults below; vocabulary size from the
                              tokenizer.ggml.tokens array when present
   GgufMetadata.GetInt32 (GgufMetadata.cs:53-63) accepts int32, uint32, int64
@@ -24,12 +24,13 @@ MemoryMappedWeights.cs:48-57), mapped read-only, never copied on the host.
 
 Writer — the metadata the reference needs to load the file unchanged through
 InferenceEngine.LoadFromGguf (InferenceEngine.cs:57-110): general.architecture
-"llama", the llama.* shape keys, and a tokenizer vocabulary
+("llama", "mistral" or "qwen2"), the shape keys under that prefix, and a tokenizer vocabulary
 (BpeTokenizer.cs:96-117: tokens, scores, token types, BOS/EOS ids, model
 "llama"); tensors in the order given, each at an offset aligned to the file's
 alignment.
 
     python -m chatnet_amd.gguf write OUT.gguf --model tinyllama --mix q4_0 --seed 1234
+    python -m chatnet_amd.gguf write OUT.gguf --model qwen2-0.5b --mix q8_0 --tied
     python -m chatnet_amd.gguf info FILE.gguf
 """
 from __future__ import annotations
@@ -43,7 +44,7 @@ from typing import Dict, List, Mapping, Optional, Tuple
 import numpy as np
 
 from . import _native
-from .config import LLAMA2_7B, TINY_TEST, TINYLLAMA_1B, LlamaConfig
+from .config import LLAMA2_7B, QWEN2_0_5B, TINY_TEST, TINYLLAMA_1B, LlamaConfig
 
 MAGIC = 0x46554747
 VERSION = 3
@@ -211,9 +212,7 @@ class GgufFile:
     # -- GgufReader.ExtractModelConfig -------------------------------------
     def config(self, kv_dtype: int = _native.KV_F32, context_length: Optional[int] = None) -> LlamaConfig:
         arch = self.get_string("general.architecture", "llama")
-        if arch != "llama":
-            raise _native.ChatnetNotSupported(_native.ERR_UNSUPPORTED_TYPE,
-                                              f"architecture '{arch}': only llama runs on this path")
+        variant = architecture_variant(arch)
 
         def arch_int(suffix: str, default: int) -> int:
             val = self.get_int(f"{arch}.{suffix}", -1)
@@ -245,7 +244,7 @@ class GgufFile:
                            context_length=ctx if context_length is None else int(context_length),
                            rope_freq_base=arch_float("rope.freq_base", 10000.0),
                            rms_norm_eps=arch_float("attention.layer_norm_rms_epsilon", 1e-5),
-                           kv_dtype=kv_dtype)
+                           kv_dtype=kv_dtype, arch=variant)
 
     # -- tensor data ---------------------------------------------------------
     def has_tensor(self, name: str) -> bool:
@@ -307,25 +306,49 @@ def vocabulary(n: int) -> Tuple[List[str], np.ndarray, np.ndarray]:
     return tokens, -np.arange(n, dtype=np.float32), np.asarray(types, dtype=np.int32)
 
 
+def architecture_variant(arch: str) -> int:
+    """ModelFactory.DetectArchitecture (ModelFactory.cs:23-39) narrowed to the
+    variants that run here: llama and mistral take LlamaModel's forward
+    (MistralModel computes the same), qwen2 / qwen QwenModel's; gemma and phi
+    are refused; any other name falls back to llama with the reference's
+    warning."""
+    a = arch.lower()
+    if a in ("llama", "mistral"):
+        return _native.ARCH_LLAMA
+    if a in ("qwen2", "qwen"):
+        return _native.ARCH_QWEN2
+    if a in ("gemma", "gemma2", "phi2", "phi3", "phi"):
+        raise _native.ChatnetNotSupported(_native.ERR_UNSUPPORTED_TYPE,
+                                          f"architecture '{arch}': Gemma and Phi do not run on this path")
+    print(f"[WARN] Unknown architecture '{arch}', defaulting to Llama.", file=sys.stderr)
+    return _native.ARCH_LLAMA
+
+
 def llama_metadata(cfg: LlamaConfig, name: str = "chatnet-synthetic",
-                   alignment: int = DEFAULT_ALIGNMENT) -> Dict[str, Value]:
+                   alignment: int = DEFAULT_ALIGNMENT, architecture: Optional[str] = None) -> Dict[str, Value]:
+    """Metadata of a checkpoint of `cfg`; the keys carry the architecture
+    prefix ("llama" or, for ARCH_QWEN2, "qwen2" unless `architecture` names
+    another, e.g. "mistral")."""
+    arch = architecture or ("qwen2" if cfg.arch == _native.ARCH_QWEN2 else "llama")
+    if architecture_variant(arch) != cfg.arch:
+        raise ValueError(f"architecture '{arch}' does not match the config's variant {cfg.arch}")
     tokens, scores, types = vocabulary(cfg.vocab_size)
     md = {
-        "general.architecture": Value(STRING, "llama"),
+        "general.architecture": Value(STRING, arch),
         "general.name": Value(STRING, name),
         "general.alignment": Value(UINT32, alignment),
-        "llama.context_length": Value(UINT32, cfg.context_length),
-        "llama.embedding_length": Value(UINT32, cfg.dim),
-        "llama.block_count": Value(UINT32, cfg.n_layers),
-        "llama.feed_forward_length": Value(UINT32, cfg.hidden_dim),
-        "llama.attention.head_count": Value(UINT32, cfg.n_heads),
-        "llama.attention.head_count_kv": Value(UINT32, cfg.n_kv_heads),
-        "llama.attention.key_length": Value(UINT32, cfg.head_dim),
-        "llama.attention.value_length": Value(UINT32, cfg.head_dim),
-        "llama.rope.dimension_count": Value(UINT32, cfg.head_dim),
-        "llama.rope.freq_base": Value(FLOAT32, float(cfg.rope_freq_base)),
-        "llama.attention.layer_norm_rms_epsilon": Value(FLOAT32, float(cfg.rms_norm_eps)),
-        "llama.vocab_size": Value(UINT32, cfg.vocab_size),
+        f"{arch}.context_length": Value(UINT32, cfg.context_length),
+        f"{arch}.embedding_length": Value(UINT32, cfg.dim),
+        f"{arch}.block_count": Value(UINT32, cfg.n_layers),
+        f"{arch}.feed_forward_length": Value(UINT32, cfg.hidden_dim),
+        f"{arch}.attention.head_count": Value(UINT32, cfg.n_heads),
+        f"{arch}.attention.head_count_kv": Value(UINT32, cfg.n_kv_heads),
+        f"{arch}.attention.key_length": Value(UINT32, cfg.head_dim),
+        f"{arch}.attention.value_length": Value(UINT32, cfg.head_dim),
+        f"{arch}.rope.dimension_count": Value(UINT32, cfg.head_dim),
+        f"{arch}.rope.freq_base": Value(FLOAT32, float(cfg.rope_freq_base)),
+        f"{arch}.attention.layer_norm_rms_epsilon": Value(FLOAT32, float(cfg.rms_norm_eps)),
+        f"{arch}.vocab_size": Value(UINT32, cfg.vocab_size),
         "tokenizer.ggml.model": Value(STRING, "llama"),
         "tokenizer.ggml.tokens": Value(ARRAY, tokens, STRING),
         "tokenizer.ggml.scores": Value(ARRAY, scores, FLOAT32),
@@ -370,14 +393,16 @@ def write(path: str, tensors: Mapping, metadata: Mapping[str, Value],
 
 
 def write_llama(path: str, cfg: LlamaConfig, checkpoint: Mapping, name: str = "chatnet-synthetic",
-                alignment: int = DEFAULT_ALIGNMENT) -> None:
-    """A Llama checkpoint (name -> tensor, e.g. synth.llama_checkpoint) as GGUF."""
-    write(path, checkpoint, llama_metadata(cfg, name, alignment), alignment)
+                alignment: int = DEFAULT_ALIGNMENT, architecture: Optional[str] = None) -> None:
+    """A Llama / Mistral / Qwen2 checkpoint (name -> tensor, e.g.
+    synth.llama_checkpoint) as GGUF."""
+    write(path, checkpoint, llama_metadata(cfg, name, alignment, architecture), alignment)
 
 
 # --------------------------------------------------------------------------
 
-_MODELS = {"tinyllama": TINYLLAMA_1B, "llama2-7b": LLAMA2_7B, "tiny-test": TINY_TEST}
+_MODELS = {"tinyllama": TINYLLAMA_1B, "llama2-7b": LLAMA2_7B, "tiny-test": TINY_TEST,
+           "qwen2-0.5b": QWEN2_0_5B, "tiny-qwen2": TINY_TEST.replace(arch=_native.ARCH_QWEN2)}
 
 
 def main(argv=None) -> int:
@@ -386,7 +411,11 @@ def main(argv=None) -> int:
     w = sub.add_parser("write", help="write a seeded synthetic Llama checkpoint as GGUF")
     w.add_argument("out")
     w.add_argument("--model", choices=sorted(_MODELS), default="tinyllama")
-    w.add_argument("--mix", default="q4_0", help="q4_0, q4_k_m, q4_k or q6_k")
+    w.add_argument("--mix", default="q4_0", help="q4_0, q8_0, q4_k_m, q5_k_m, q4_k or q6_k")
+    w.add_argument("--architecture", default=None, help="general.architecture (e.g. mistral); "
+                   "default llama, or qwen2 for the Qwen2 models")
+    w.add_argument("--tied", action="store_true",
+                   help="no output.weight: Q8_0 token embeddings double as the LM head")
     w.add_argument("--seed", type=int, default=1234)
     w.add_argument("--layers", type=int, default=None, help="override the layer count")
     i = sub.add_parser("info", help="print the config and tensor table of a GGUF file")
@@ -397,8 +426,9 @@ def main(argv=None) -> int:
         cfg = _MODELS[a.model]
         if a.layers is not None:
             cfg = cfg.replace(n_layers=a.layers)
-        ck = synth.llama_checkpoint(cfg, seed=a.seed, mix=a.mix)
-        write_llama(a.out, cfg, ck, name=f"{a.model}-{a.mix}-seed{a.seed}")
+        emb = _native.GGML_Q8_0 if a.tied else _native.GGML_F32
+        ck = synth.llama_checkpoint(cfg, seed=a.seed, mix=a.mix, with_output=not a.tied, embedding=emb)
+        write_llama(a.out, cfg, ck, name=f"{a.model}-{a.mix}-seed{a.seed}", architecture=a.architecture)
         print(f"wrote {a.out}: {len(ck)} tensors")
     else:
         g = GgufFile(a.path)

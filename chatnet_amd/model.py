@@ -33,11 +33,14 @@ class HipLlamaModel:
     @classmethod
     def from_gguf(cls, path: str, kv_dtype: int = _native.KV_F32, context_length: Optional[int] = None,
                   device: int = 0) -> "HipLlamaModel":
-        """InferenceEngine.LoadFromGguf (InferenceEngine.cs:57-110) for the Llama
-        path: the config from the file's metadata (GgufReader.ExtractModelConfig),
-        then the tensors LlamaWeights.ResolveAll resolves (LlamaWeights.cs:78-145)
-        uploaded straight from the read-only mapping of the file; any other
-        tensors in the file are left alone, as the reference leaves them."""
+        """InferenceEngine.LoadFromGguf (InferenceEngine.cs:57-110) for the Llama,
+        Mistral and Qwen2 paths: the config from the file's metadata
+        (GgufReader.ExtractModelConfig, the variant by ModelFactory's
+        architecture rule), then the tensors LlamaWeights.ResolveAll resolves
+        (LlamaWeights.cs:78-145; for Qwen2 also the q/k/v biases of a layer that
+        has attn_q.bias, QwenWeights.cs:158-170) uploaded straight from the
+        read-only mapping of the file; any other tensors in the file are left
+        alone, as the reference leaves them."""
         from .gguf import GgufFile
 
         g = GgufFile(path)
@@ -46,6 +49,8 @@ class HipLlamaModel:
         for l in range(cfg.n_layers):
             names += [f"blk.{l}.{n}.weight" for n in ("attn_norm", "ffn_norm", "attn_q", "attn_k", "attn_v",
                                                      "attn_output", "ffn_gate", "ffn_up", "ffn_down")]
+            if cfg.arch == _native.ARCH_QWEN2 and g.has_tensor(f"blk.{l}.attn_q.bias"):
+                names += [f"blk.{l}.{n}.bias" for n in ("attn_q", "attn_k", "attn_v")]
         m = cls(cfg, device=device)
         try:
             for name in names:

@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import ctypes
 import dataclasses
+from typing import Optional
 
 import numpy as np
 
@@ -98,12 +99,22 @@ def tokens(seed: int, name: str, n: int, vocab: int) -> np.ndarray:
     return out
 
 
+BIAS_SIGMA = 0.25  # N(0, 0.25) QKV biases: comparable to the projections of a normalised x
+
+
 def llama_checkpoint(cfg: LlamaConfig, seed: int = 1234, mix: str = "q4_0",
-                     with_output: bool = True) -> dict:
-    """All tensors LlamaWeights.ResolveAll (LlamaWeights.cs:78-145) looks up."""
+                     with_output: bool = True, embedding: int = _native.GGML_F32,
+                     qkv_bias: Optional[bool] = None) -> dict:
+    """All tensors LlamaWeights.ResolveAll (LlamaWeights.cs:78-145) looks up;
+    for an ARCH_QWEN2 config also the F32 q/k/v biases QwenWeights resolves
+    (QwenWeights.cs:158-170) unless qkv_bias is False.  with_output=False leaves
+    out output.weight (the tied-embedding fallback); `embedding` is the type of
+    token_embd.weight."""
     q = MIXES[mix]
+    if qkv_bias is None:
+        qkv_bias = cfg.arch == _native.ARCH_QWEN2
     ck = {}
-    ck["token_embd.weight"] = tensor(_native.GGML_F32, seed, "token_embd.weight", cfg.vocab_size, cfg.dim)
+    ck["token_embd.weight"] = tensor(embedding, seed, "token_embd.weight", cfg.vocab_size, cfg.dim)
     ones = np.ones(cfg.dim, dtype=np.float32)
     ck["output_norm.weight"] = SynthTensor(_native.GGML_F32, (cfg.dim,), ones.view(np.uint8).copy())
     if with_output:
@@ -120,6 +131,10 @@ def llama_checkpoint(cfg: LlamaConfig, seed: int = 1234, mix: str = "q4_0",
         ck[p + "ffn_gate.weight"] = tensor(q["gate_up"], seed, p + "ffn_gate.weight", cfg.hidden_dim, cfg.dim)
         ck[p + "ffn_up.weight"] = tensor(q["gate_up"], seed, p + "ffn_up.weight", cfg.hidden_dim, cfg.dim)
         ck[p + "ffn_down.weight"] = tensor(q["down"], seed, p + "ffn_down.weight", cfg.dim, cfg.hidden_dim)
+        if qkv_bias:
+            for nm, n in (("attn_q.bias", cfg.dim), ("attn_k.bias", kvd), ("attn_v.bias", kvd)):
+                ck[p + nm] = SynthTensor(_native.GGML_F32, (n,),
+                                         normal(seed, p + nm, n, BIAS_SIGMA).view(np.uint8).copy())
     return ck
 
 

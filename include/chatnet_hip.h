@@ -63,6 +63,20 @@ enum {
 /* KV-cache element type. */
 enum { CHATNET_KV_F32 = 0, CHATNET_KV_F16 = 1 };
 
+/* Forward-pass variant, chosen by GGUF general.architecture the way
+ * ModelFactory.DetectArchitecture / CreateModel do
+ * (src/ChatNet.Core/Models/ModelFactory.cs:23-82):
+ *   CHATNET_ARCH_LLAMA  "llama" and "mistral": LlamaModel.Forward
+ *                       (LlamaModel.cs:93-238); MistralModel.Forward
+ *                       (Models/Mistral/MistralModel.cs:67-154) is the same
+ *                       computation (no sliding window).
+ *   CHATNET_ARCH_QWEN2  "qwen2" and "qwen": QwenModel.Forward
+ *                       (Models/Qwen/QwenModel.cs:69-178): optional F32 biases
+ *                       added to q, k and v after their projections, and
+ *                       split-half (NeoX) RoPE, TensorMath.ApplyRoPENeox
+ *                       (TensorMath.cs:475-520). */
+enum { CHATNET_ARCH_LLAMA = 0, CHATNET_ARCH_QWEN2 = 1 };
+
 /* Model hyper-parameters.  Mirrors LlamaConfig
  * (src/ChatNet.Core/Models/Llama/LlamaConfig.cs:8-38), which is derived from
  * ModelConfig (src/ChatNet.Core/Abstractions/ModelConfig.cs:6-27). */
@@ -78,7 +92,7 @@ typedef struct chatnet_config {
   float rope_freq_base;   /* LlamaConfig.RopeFreqBase                       */
   float rms_norm_eps;     /* LlamaConfig.RmsNormEps                         */
   int32_t kv_dtype;       /* CHATNET_KV_F32 (reference) or CHATNET_KV_F16   */
-  int32_t reserved;       /* must be 0                                      */
+  int32_t arch;           /* CHATNET_ARCH_LLAMA or CHATNET_ARCH_QWEN2       */
 } chatnet_config;
 
 typedef struct chatnet_model chatnet_model;
@@ -94,7 +108,12 @@ CHATNET_API int chatnet_create(const chatnet_config* cfg, int device, chatnet_mo
  * reference resolves in LlamaWeights.ResolveAll (LlamaWeights.cs:78-145):
  * token_embd.weight, output.weight, output_norm.weight and
  * blk.{l}.{attn_norm,ffn_norm,attn_q,attn_k,attn_v,attn_output,
- * ffn_gate,ffn_up,ffn_down}.weight.  `dims` is GGUF order (ne0 = inner).
+ * ffn_gate,ffn_up,ffn_down}.weight, plus for CHATNET_ARCH_QWEN2 the optional
+ * F32 biases blk.{l}.{attn_q,attn_k,attn_v}.bias (QwenWeights.cs:158-170: a
+ * layer that has the q bias must have all three).  Without output.weight the
+ * LM head is token_embd.weight (the tied fallback of LlamaWeights.cs:89-98
+ * and QwenWeights.cs:102-112), which must then be Q4_0 or Q8_0.  Embeddings
+ * may be F32, F16, Q4_0 or Q8_0.  `dims` is GGUF order (ne0 = inner).
  * `nbytes` must equal GgufTensorInfo.ByteSize (GgufTensorInfo.cs:30-113).
  * Replaces MemoryMappedWeights.GetTensorPointer (MemoryMappedWeights.cs:76-84)
  * as the source of weight bytes for the forward pass. */

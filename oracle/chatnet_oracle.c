@@ -497,6 +497,29 @@ void oracle_rope(float* q, float* k, int position, int hd, int nh, int nkv, floa
   }
 }
 
+/* TensorMath.ApplyRoPENeox (TensorMath.cs:475-520), rotaryDim = headDim:
+ * element i of a head is rotated with element i + hd/2 by
+ * theta = pos * exp(i * (2/hd) * -ln base). */
+void oracle_rope_neox(float* q, float* k, int position, int hd, int nh, int nkv, float base) {
+  float negLogBase = -logf(base);
+  float dimInv = 2.0f / (float)hd;
+  int half = hd / 2;
+  for (int pass = 0; pass < 2; pass++) {
+    float* v = pass == 0 ? q : k;
+    int heads = pass == 0 ? nh : nkv;
+    for (int h = 0; h < heads; h++) {
+      float* vec = v + (size_t)h * hd;
+      for (int i = 0; i < half; i++) {
+        float theta = (float)position * expf((float)i * dimInv * negLogBase);
+        float c = cosf(theta), s = sinf(theta);
+        float x0 = vec[i], x1 = vec[i + half];
+        vec[i] = x0 * c - x1 * s;
+        vec[i + half] = x1 * c + x0 * s;
+      }
+    }
+  }
+}
+
 /* GreedySampler.Sample (GreedySampler.cs:13-26): first maximum wins. */
 int oracle_argmax(const float* logits, int n) {
   int best = 0;
@@ -690,6 +713,7 @@ struct oracle_llama {
   int kv_dim, kv_mul;
   tensor_ref emb, out, out_norm;
   tensor_ref *attn_norm, *ffn_norm, *wq, *wk, *wv, *wo, *wg, *wu, *wd;
+  const float **bq, **bk, **bv; /* QwenWeights' optional biases (QwenWeights.cs:158-170) */
   float *kcache, *vcache;
   float *x, *xn, *q, *k, *v, *att, *gate, *up, *ffo, *scores, *rowbuf;
 };
@@ -705,6 +729,9 @@ oracle_llama* oracle_llama_create(const oracle_config* cfg) {
                          &m->wo,        &m->wg,       &m->wu, &m->wd};
   for (size_t i = 0; i < sizeof(arrs) / sizeof(arrs[0]); i++)
     *arrs[i] = (tensor_ref*)calloc((size_t)L, sizeof(tensor_ref));
+  m->bq = (const float**)calloc((size_t)L, sizeof(float*));
+  m->bk = (const float**)calloc((size_t)L, sizeof(float*));
+  m->bv = (const float**)calloc((size_t)L, sizeof(float*));
   size_t kv = (size_t)L * cfg->context_length * m->kv_dim; /* LlamaModel.cs:60-61 */
   m->kcache = (float*)calloc(kv, sizeof(float));
   m->vcache = (float*)calloc(kv, sizeof(float));
@@ -727,7 +754,8 @@ oracle_llama* oracle_llama_create(const oracle_config* cfg) {
   return m;
 }
 
-/* Name resolution of LlamaWeights.ResolveAll (LlamaWeights.cs:78-145). */
+/* Name resolution of LlamaWeights.ResolveAll (LlamaWeights.cs:78-145), and for
+ * ORACLE_ARCH_QWEN2 the F32 q/k/v biases of QwenWeights (QwenWeights.cs:158-170). */
 int oracle_llama_set_tensor(oracle_llama* m, const char* name, uint32_t type, const void* data) {
   tensor_ref t = {data, type};
   if (!strcmp(name, "token_embd.weight")) { m->emb = t; return 0; }
@@ -747,10 +775,21 @@ int oracle_llama_set_tensor(oracle_llama* m, const char* name, uint32_t type, co
       tab[i].a[l] = t;
       return 0;
     }
+  if (m->c.arch == ORACLE_ARCH_QWEN2) {
+    const float** b = !strcmp(suffix, "attn_q.bias")   ? m->bq
+                      : !strcmp(suffix, "attn_k.bias") ? m->bk
+                      : !strcmp(suffix, "attn_v.bias") ? m->bv
+                                                       : NULL;
+    if (b) {
+      if (type != ORACLE_F32) return -3;
+      b[l] = (const float*)data;
+      return 0;
+    }
+  }
   return -2;
 }
 
-/* LlamaModel.LoadEmbedding (LlamaModel.cs:365-394) for F32 / F16 / Q4_0. */
+/* LlamaModel.LoadEmbedding (LlamaModel.cs:365-394) for F32 / F16 / Q4_0 / Q8_0. */
 static int load_embedding(oracle_llama* m, int token, float* out) {
   int dim = m->c.dim;
   const uint8_t* e = (const uint8_t*)m->emb.data;
@@ -760,6 +799,7 @@ static int load_embedding(oracle_llama* m, int token, float* out) {
       for (int i = 0; i < dim; i++) out[i] = h2f(e + ((size_t)token * dim + i) * 2);
       return 0;
     case ORACLE_Q4_0: oracle_dequant_q4_0(e + (size_t)token * (dim / 32) * 18, out, dim); return 0;
+    case ORACLE_Q8_0: oracle_dequant_q8_0(e + (size_t)token * (dim / 32) * 34, out, dim); return 0;
     default: return -3;
   }
 }
@@ -807,7 +847,10 @@ static void attention(oracle_llama* m, int layer, int pos) {
   }
 }
 
-/* LlamaModel.Forward (LlamaModel.cs:93-238). */
+/* LlamaModel.Forward (LlamaModel.cs:93-238); MistralModel.Forward
+ * (MistralModel.cs:67-154) is the same computation.  ORACLE_ARCH_QWEN2 is
+ * QwenModel.Forward (QwenModel.cs:69-178): biases added after the q/k/v
+ * projections (:104-120), split-half RoPE (:124-126). */
 int oracle_llama_forward(oracle_llama* m, const int32_t* tokens, int n, int position, float* logits) {
   const oracle_config* c = &m->c;
   int dim = c->dim, kvd = m->kv_dim, hid = c->hidden_dim;
@@ -826,7 +869,17 @@ int oracle_llama_forward(oracle_llama* m, const int32_t* tokens, int n, int posi
       if ((rc = oracle_matvec(m->wq[l].type, m->wq[l].data, m->xn, m->q, dim, dim))) return rc;
       if ((rc = oracle_matvec(m->wk[l].type, m->wk[l].data, m->xn, m->k, kvd, dim))) return rc;
       if ((rc = oracle_matvec(m->wv[l].type, m->wv[l].data, m->xn, m->v, kvd, dim))) return rc;
-      oracle_rope(m->q, m->k, pos, c->head_dim, c->n_heads, c->n_kv_heads, c->rope_freq_base);
+      if (c->arch == ORACLE_ARCH_QWEN2) {
+        if (m->bq[l]) {
+          if (!m->bk[l] || !m->bv[l]) return -2; /* GetTensorPointer throws for the missing one */
+          for (int i = 0; i < dim; i++) m->q[i] += m->bq[l][i];
+          for (int i = 0; i < kvd; i++) m->k[i] += m->bk[l][i];
+          for (int i = 0; i < kvd; i++) m->v[i] += m->bv[l][i];
+        }
+        oracle_rope_neox(m->q, m->k, pos, c->head_dim, c->n_heads, c->n_kv_heads, c->rope_freq_base);
+      } else {
+        oracle_rope(m->q, m->k, pos, c->head_dim, c->n_heads, c->n_kv_heads, c->rope_freq_base);
+      }
       size_t off = (size_t)l * c->context_length * kvd + (size_t)pos * kvd; /* :150-153 */
       memcpy(m->kcache + off, m->k, sizeof(float) * (size_t)kvd);
       memcpy(m->vcache + off, m->v, sizeof(float) * (size_t)kvd);
@@ -859,6 +912,7 @@ void oracle_llama_destroy(oracle_llama* m) {
   if (!m) return;
   free(m->attn_norm); free(m->ffn_norm); free(m->wq); free(m->wk); free(m->wv);
   free(m->wo); free(m->wg); free(m->wu); free(m->wd);
+  free(m->bq); free(m->bk); free(m->bv);
   free(m->kcache); free(m->vcache);
   free(m->x); free(m->xn); free(m->q); free(m->k); free(m->v); free(m->att);
   free(m->gate); free(m->up); free(m->ffo); free(m->scores); free(m->rowbuf);

@@ -26,6 +26,11 @@
  *                     brute force.
  *   q5_k dequant/dot  reference KAT QuantizationTests.cs:513-537 (dot 5184),
  *                     a hand-derived high-bit position KAT, float64 brute force.
+ *   rope_neox         closed form at hd 4, identity at pos 0, pair norms, and
+ *                     the exact identity neox = P^-1 . rope . P with P the
+ *                     split-half -> interleaved permutation of each head.
+ *   Qwen2 forward     the float64 numpy restatement of a tiny model with biases
+ *                     and split-half RoPE (tests/npref.py).
  *   rmsnorm/rope/softmax/silu/add/attention/argmax: invariants (closed forms,
  *                     identity at pos 0, norm preservation, shift invariance,
  *                     tie rule) and a float64 numpy restatement of a tiny model.
@@ -78,6 +83,8 @@ void oracle_silu_mul(float* gate, const float* up, int n);
 void oracle_add(float* a, const float* b, int n);
 void oracle_rope(float* q, float* k, int position, int head_dim, int n_heads, int n_kv_heads,
                  float freq_base);
+void oracle_rope_neox(float* q, float* k, int position, int head_dim, int n_heads, int n_kv_heads,
+                      float freq_base);
 int oracle_argmax(const float* logits, int n);
 
 /* System.Random(int seed) of the .NET BCL (the seeded compat generator). */
@@ -99,9 +106,11 @@ int oracle_temperature_sample(const float* logits, int n, float temperature, int
                               float* margin);
 
 /* Whole model.  Tensor pointers are borrowed host pointers (like the mmap). */
+enum { ORACLE_ARCH_LLAMA = 0, ORACLE_ARCH_QWEN2 = 1 };
 typedef struct oracle_config {
   int32_t dim, hidden_dim, n_layers, n_heads, n_kv_heads, head_dim, vocab_size, context_length;
   float rope_freq_base, rms_norm_eps;
+  int32_t arch; /* ORACLE_ARCH_LLAMA (Llama, Mistral) or ORACLE_ARCH_QWEN2 */
 } oracle_config;
 
 typedef struct oracle_llama oracle_llama;

@@ -24,7 +24,8 @@ _lib = None
 class OracleConfig(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in
                 ("dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads", "head_dim", "vocab_size",
-                 "context_length")] + [("rope_freq_base", ctypes.c_float), ("rms_norm_eps", ctypes.c_float)]
+                 "context_length")] + [("rope_freq_base", ctypes.c_float), ("rms_norm_eps", ctypes.c_float),
+                                       ("arch", ctypes.c_int32)]
 
 
 def build() -> str:
@@ -55,6 +56,7 @@ def lib() -> ctypes.CDLL:
         L.oracle_silu_mul.argtypes = [_P, _P, ctypes.c_int]
         L.oracle_add.argtypes = [_P, _P, ctypes.c_int]
         L.oracle_rope.argtypes = [_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float]
+        L.oracle_rope_neox.argtypes = [_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float]
         L.oracle_argmax.argtypes = [_P, ctypes.c_int]
         L.oracle_argmax.restype = ctypes.c_int
         L.oracle_net_random_init.argtypes = [_P, ctypes.c_int32]
@@ -137,6 +139,12 @@ def rope(q, k, pos, head_dim, n_heads, n_kv_heads, base):
     return q, k
 
 
+def rope_neox(q, k, pos, head_dim, n_heads, n_kv_heads, base):
+    q, k = _f32(q).copy(), _f32(k).copy()
+    lib().oracle_rope_neox(q.ctypes.data, k.ctypes.data, pos, head_dim, n_heads, n_kv_heads, base)
+    return q, k
+
+
 def argmax(logits) -> int:
     l = _f32(logits)
     return int(lib().oracle_argmax(l.ctypes.data, l.size))
@@ -167,11 +175,14 @@ def temperature_sample(logits, temperature: float, top_k: int, top_p: float, dra
 
 
 class OracleLlama:
-    """LlamaModel (LlamaModel.cs) on the CPU over borrowed host tensors."""
+    """LlamaModel (LlamaModel.cs; MistralModel computes the same) or, for an
+    ARCH_QWEN2 config, QwenModel (QwenModel.cs) on the CPU over borrowed host
+    tensors."""
 
     def __init__(self, cfg, checkpoint: dict):
         c = OracleConfig(cfg.dim, cfg.hidden_dim, cfg.n_layers, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
-                         cfg.vocab_size, cfg.context_length, cfg.rope_freq_base, cfg.rms_norm_eps)
+                         cfg.vocab_size, cfg.context_length, cfg.rope_freq_base, cfg.rms_norm_eps,
+                         getattr(cfg, "arch", 0))
         self.cfg = cfg
         self._h = lib().oracle_llama_create(ctypes.byref(c))
         if not self._h:

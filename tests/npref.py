@@ -110,13 +110,27 @@ def rope(v, pos, hd, base):
     return v.ravel()
 
 
+def rope_neox(v, pos, hd, base):
+    """Split-half rotary embedding: element i of a head turns with element
+    i + hd/2 by the angle pos * base^(-2i/hd)."""
+    v = v.copy().reshape(-1, hd)
+    half = hd // 2
+    theta = pos * base ** (-2.0 * np.arange(half) / hd)
+    c, s = np.cos(theta), np.sin(theta)
+    x0, x1 = v[:, :half].copy(), v[:, half:].copy()
+    v[:, :half] = x0 * c - x1 * s
+    v[:, half:] = x1 * c + x0 * s
+    return v.ravel()
+
+
 class Llama64:
-    """float64 LlamaModel: same schedule, none of the float32 roundings."""
+    """float64 LlamaModel (or, for arch 1, QwenModel: q/k/v biases and
+    split-half RoPE): same schedule, none of the float32 roundings."""
 
     def __init__(self, cfg, ck):
         self.cfg = cfg
         self.emb = matrix(ck["token_embd.weight"])
-        self.out = matrix(ck["output.weight"])
+        self.out = matrix(ck["output.weight"]) if "output.weight" in ck else self.emb
         self.out_norm = ck["output_norm.weight"].data.view(np.float32).astype(np.float64)
         self.L = []
         for l in range(cfg.n_layers):
@@ -125,6 +139,9 @@ class Llama64:
                            ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")})
             self.L[-1]["attn_norm"] = ck[p + "attn_norm.weight"].data.view(np.float32).astype(np.float64)
             self.L[-1]["ffn_norm"] = ck[p + "ffn_norm.weight"].data.view(np.float32).astype(np.float64)
+            for b in ("attn_q", "attn_k", "attn_v"):
+                t = ck.get(p + b + ".bias")
+                self.L[-1][b + ".bias"] = np.zeros(0) if t is None else t.data.view(np.float32).astype(np.float64)
         self.kc = np.zeros((cfg.n_layers, cfg.context_length, cfg.kv_dim))
         self.vc = np.zeros_like(self.kc)
 
@@ -137,9 +154,13 @@ class Llama64:
             x = self.emb[tok].copy()
             for l, W in enumerate(self.L):
                 xn = rmsnorm(x, W["attn_norm"], c.rms_norm_eps)
-                q = rope(W["attn_q"] @ xn, pos, hd, c.rope_freq_base)
-                k = rope(W["attn_k"] @ xn, pos, hd, c.rope_freq_base)
-                v = W["attn_v"] @ xn
+                q, k, v = W["attn_q"] @ xn, W["attn_k"] @ xn, W["attn_v"] @ xn
+                if getattr(c, "arch", 0) == 1:
+                    if W["attn_q.bias"].size:
+                        q, k, v = q + W["attn_q.bias"], k + W["attn_k.bias"], v + W["attn_v.bias"]
+                    q, k = rope_neox(q, pos, hd, c.rope_freq_base), rope_neox(k, pos, hd, c.rope_freq_base)
+                else:
+                    q, k = rope(q, pos, hd, c.rope_freq_base), rope(k, pos, hd, c.rope_freq_base)
                 self.kc[l, pos], self.vc[l, pos] = k, v
                 att = np.zeros(c.dim)
                 for h in range(c.n_heads):

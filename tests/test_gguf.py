@@ -143,6 +143,37 @@ def test_round_trip(tmp_path, mix, alignment):
     assert g.get_int("tokenizer.ggml.eos_token_id", 0) == 2
 
 
+@pytest.mark.parametrize("architecture,variant", [("mistral", _native.ARCH_LLAMA), ("qwen2", _native.ARCH_QWEN2),
+                                                  ("Qwen", _native.ARCH_QWEN2)])
+def test_variants_round_trip(tmp_path, architecture, variant):
+    # ModelFactory.DetectArchitecture (ModelFactory.cs:23-39) lower-cases the name;
+    # ExtractModelConfig reads the keys under the name as written (GgufReader.cs:82-110)
+    cfg = TINY_TEST.replace(arch=variant, rope_freq_base=1e6)
+    ck = synth.llama_checkpoint(cfg, seed=8, mix="q8_0", with_output=False, embedding=_native.GGML_Q8_0)
+    assert ("blk.0.attn_q.bias" in ck) == (variant == _native.ARCH_QWEN2)
+    p = str(tmp_path / "v.gguf")
+    gguf.write_llama(p, cfg, ck, architecture=architecture)
+    g = gguf.GgufFile(p)
+    assert g.get_string("general.architecture") == architecture
+    assert g.get_int(f"{architecture}.block_count", -1) == cfg.n_layers
+    assert g.config() == cfg.replace(rms_norm_eps=float(np.float32(cfg.rms_norm_eps)))
+    assert not g.has_tensor("output.weight")
+    for t in g.tensors:
+        assert np.array_equal(g.tensor_bytes(t.name), np.asarray(ck[t.name].data).view(np.uint8).ravel())
+    with pytest.raises(ValueError):   # a Qwen2 config under a Llama name, or the reverse
+        gguf.llama_metadata(cfg, architecture="llama" if variant == _native.ARCH_QWEN2 else "qwen2")
+
+
+def test_unknown_architecture_defaults_to_llama(tmp_path, capsys):
+    # ModelFactory.cs:36-37: an unknown name runs LlamaModel after a warning
+    body = _handmade(extra_kv=[_kv("general.architecture", 8, _s("yi"))])[0]
+    p = tmp_path / "yi.gguf"
+    p.write_bytes(body)
+    cfg = gguf.GgufFile(str(p)).config()
+    assert cfg.arch == _native.ARCH_LLAMA
+    assert "Unknown architecture 'yi', defaulting to Llama" in capsys.readouterr().err
+
+
 def test_writer_rejects_wrong_sizes(tmp_path):
     t = synth.SynthTensor(_native.GGML_Q4_0, (64, 2), np.zeros(35, np.uint8))   # ByteSize is 72
     with pytest.raises(ValueError):

@@ -52,6 +52,97 @@ def test_tiny_model_logits_token_by_token(mix, kv):
         assert m.argmax() == GreedySampler().sample(g)
 
 
+# -- Qwen2 variant (QwenModel.Forward): QKV biases, split-half RoPE, tied LM head --
+TINY_QWEN = TINY_TEST.replace(arch=_native.ARCH_QWEN2, rope_freq_base=1e6, rms_norm_eps=1e-6)
+
+
+@pytest.mark.parametrize("mix,bias,tied", [("q8_0", True, False), ("q4_0", False, False), ("q4_k_m", True, False),
+                                           ("q4_0", True, True)])
+def test_tiny_qwen2_logits_token_by_token(mix, bias, tied):
+    cfg = TINY_QWEN
+    emb = _native.GGML_Q8_0 if tied else _native.GGML_F32
+    ck = synth.llama_checkpoint(cfg, seed=41, mix=mix, qkv_bias=bias, with_output=not tied, embedding=emb)
+    ora = oracle.OracleLlama(cfg, ck)
+    toks = synth.tokens(41, "prompt", 12, cfg.vocab_size)
+    announce(f"tiny qwen2 mix={mix} bias={bias} tied={tied}")
+    with HipLlamaModel(cfg, ck) as m:
+        for pos, t in enumerate(toks):
+            g = m.forward([t], pos)
+            r = ora.forward([t], pos)
+            assert np.max(np.abs(g - r)) <= LOGIT_TOL, (pos, float(np.max(np.abs(g - r))))
+
+
+def test_qwen2_span_and_greedy_match_oracle():
+    """A 40-token Qwen2 span on the batched path (bias and split-half RoPE in
+    the span kernels), a continuing 8-token span, then 32 greedy tokens from
+    the device loop."""
+    cfg = SPAN_SMALL.replace(arch=_native.ARCH_QWEN2, rope_freq_base=1e6, context_length=128)
+    ck = synth.llama_checkpoint(cfg, seed=42, mix="q4_0")
+    toks = synth.tokens(42, "prompt", 48, cfg.vocab_size)
+    announce("qwen2 span 40 + 8, greedy 32")
+    with HipLlamaModel(cfg, ck) as m:
+        g = m.forward(toks[:40], 0).copy()
+        g2 = m.forward(toks[40:], 40).copy()
+        gt = list(m.decode_greedy(32))
+    ora = oracle.OracleLlama(cfg, ck)
+    r = ora.forward(toks[:40], 0)
+    r2 = ora.forward(toks[40:], 40)
+    assert np.max(np.abs(g - r)) <= LOGIT_TOL and np.max(np.abs(g2 - r2)) <= LOGIT_TOL
+    o, margins = oracle.OracleLlama(cfg, ck).generate_greedy(list(toks), 32)
+    compare_greedy(gt, o, margins)
+
+
+def test_qwen2_from_gguf_matches_uploaded_checkpoint(tmp_path):
+    from chatnet_amd import gguf
+    cfg = TINY_QWEN
+    ck = synth.llama_checkpoint(cfg, seed=43, mix="q8_0", with_output=False, embedding=_native.GGML_Q8_0)
+    path = str(tmp_path / "qwen.gguf")
+    gguf.write_llama(path, cfg, ck)
+    toks = synth.tokens(43, "prompt", 10, cfg.vocab_size)
+    announce("qwen2 gguf load")
+    with HipLlamaModel.from_gguf(path) as m:
+        assert m.config.arch == _native.ARCH_QWEN2
+        g = m.forward(toks, 0).copy()
+    with HipLlamaModel(cfg, ck) as m2:
+        r = m2.forward(toks, 0).copy()
+    assert np.array_equal(g, r)
+    o = oracle.OracleLlama(cfg, ck).forward(toks, 0)
+    assert np.max(np.abs(g - o)) <= LOGIT_TOL
+
+
+def test_qwen2_upload_rules():
+    cfg = TINY_QWEN
+    ck = synth.llama_checkpoint(cfg, seed=44, mix="q4_0")
+    announce("qwen2 upload rules")
+    qb = ck["blk.0.attn_q.bias"]
+    with HipLlamaModel(TINY_TEST) as m:   # Llama has no biases (LlamaWeights.cs:105-144)
+        with pytest.raises(_native.ChatnetKeyNotFound):
+            m.upload_tensor("blk.0.attn_q.bias", qb.type, qb.dims, qb.data)
+    with HipLlamaModel(cfg) as m:
+        with pytest.raises(_native.ChatnetNotSupported):
+            m.upload_tensor("blk.0.attn_q.bias", _native.GGML_F16, qb.dims, qb.data[: qb.data.size // 2])
+        with pytest.raises(_native.ChatnetSizeMismatch):
+            m.upload_tensor("blk.0.attn_k.bias", qb.type, qb.dims, qb.data)   # dim floats where kv_dim are due
+        for name, t in ck.items():
+            if name not in ("blk.1.attn_k.bias", "blk.1.attn_v.bias"):
+                m.upload_tensor(name, t.type, t.dims, t.data)
+        with pytest.raises(_native.ChatnetKeyNotFound):   # q bias without k/v (QwenWeights.cs:164-169)
+            m.forward([1], 0)
+        for name in ("blk.1.attn_k.bias", "blk.1.attn_v.bias"):
+            t = ck[name]
+            m.upload_tensor(name, t.type, t.dims, t.data)
+        r = oracle.OracleLlama(cfg, ck).forward([1, 2], 0)
+        assert np.max(np.abs(m.forward([1, 2], 0) - r)) <= LOGIT_TOL
+
+
+def test_tied_f32_embedding_lm_head_is_refused():
+    ck = synth.llama_checkpoint(TINY_TEST, seed=45, with_output=False)
+    announce("tied f32 lm head")
+    with HipLlamaModel(TINY_TEST, ck) as m:
+        with pytest.raises(_native.ChatnetNotSupported):
+            m.forward([1], 0)
+
+
 def test_span_forward_matches_oracle_span():
     cfg = TINY_TEST
     ck = synth.llama_checkpoint(cfg, seed=22)
@@ -268,6 +359,7 @@ def test_long_context_decode_attention_matches_oracle():
     (64, 8, 2, _native.KV_F32),    # kv_mul 4: one head per wave
     (64, 16, 1, _native.KV_F32),   # kv_mul 16: four heads per wave
     (32, 8, 1, _native.KV_F32),    # kv_mul 8, head_dim 32
+    (64, 14, 2, _native.KV_F32),   # kv_mul 7 (Qwen2-0.5B): a ragged second pass of heads
     (128, 4, 4, _native.KV_F16),
 ])
 def test_decode_attention_layouts_match_oracle(head_dim, n_heads, n_kv, kv):
@@ -286,6 +378,26 @@ def test_decode_attention_layouts_match_oracle(head_dim, n_heads, n_kv, kv):
         r = oracle.OracleLlama(cfg, ck).forward(list(prompt) + list(o), 0)
         tol = LOGIT_TOL if kv == _native.KV_F32 else 2 * LOGIT_TOL
         assert np.max(np.abs(logits_g - r)) <= tol
+
+
+def test_qwen2_0_5b_layer_decode_matches_oracle():
+    """Qwen2-0.5B-shaped layer (dim 896, 14 heads over 2 kv heads, QKV biases,
+    split-half RoPE at base 1e6) with Q8_0 weights and the tied Q8_0 embedding
+    as a 151936-row LM head."""
+    from chatnet_amd import QWEN2_0_5B
+    cfg = QWEN2_0_5B.replace(n_layers=1, context_length=64)
+    ck = synth.llama_checkpoint(cfg, seed=46, mix="q8_0", with_output=False, embedding=_native.GGML_Q8_0)
+    prompt = synth.tokens(46, "prompt", 8, cfg.vocab_size)
+    announce("qwen2-0.5b layer decode")
+    with HipLlamaModel(cfg, ck) as m:
+        m.forward(prompt, 0)
+        g = m.decode_greedy(8)
+        lg = m.get_logits()
+    o, margins = oracle.OracleLlama(cfg, ck).generate_greedy(list(prompt), 8)
+    n = compare_greedy(list(g), o, margins)
+    if n == 8:
+        r = oracle.OracleLlama(cfg, ck).forward(list(prompt) + list(o), 0)
+        assert np.max(np.abs(lg - r)) <= LOGIT_TOL
 
 
 def test_llama7b_layer_decode_matches_oracle():

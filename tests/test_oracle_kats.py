@@ -286,6 +286,52 @@ def test_rope_identity_at_zero_and_norm_preserving():
     np.testing.assert_allclose(k5, npref.rope(k.astype(np.float64), 517, hd, 10000.0), atol=5e-4)
 
 
+def _split_half_to_pairs(v, hd):
+    # per head: element j -> 2j and element j + hd/2 -> 2j + 1
+    h = v.reshape(-1, 2, hd // 2)
+    return np.stack([h[:, 0], h[:, 1]], axis=-1).reshape(-1)
+
+
+def test_rope_neox_closed_form_and_invariants():
+    # TensorMath.ApplyRoPENeox (TensorMath.cs:475-520), hd 4: pairs (0, 2) and (1, 3)
+    # with angles pos * base^0 and pos * base^(-1/2)
+    q = np.array([1.0, 2.0, 3.0, 4.0], dtype=np.float32)
+    k = np.array([0.5, -1.0, 0.25, 2.0], dtype=np.float32)
+    pos, base = 3, 100.0
+    t0, t1 = pos * 1.0, pos * base ** -0.5
+    want = np.array([1 * np.cos(t0) - 3 * np.sin(t0), 2 * np.cos(t1) - 4 * np.sin(t1),
+                     3 * np.cos(t0) + 1 * np.sin(t0), 4 * np.cos(t1) + 2 * np.sin(t1)])
+    qn, kn = oracle.rope_neox(q, k, pos, 4, 1, 1, base)
+    np.testing.assert_allclose(qn, want, atol=2e-6)
+    np.testing.assert_allclose(kn[0], 0.5 * np.cos(t0) - 0.25 * np.sin(t0), atol=2e-6)
+    # identity at position 0, pair norms kept, float64 restatement
+    hd, nh, nkv = 64, 4, 2
+    q = synth.normal(4, "nq", nh * hd, 1.0)
+    k = synth.normal(4, "nk", nkv * hd, 1.0)
+    q0, k0 = oracle.rope_neox(q, k, 0, hd, nh, nkv, 1e6)
+    assert np.array_equal(q0, q) and np.array_equal(k0, k)
+    q5, k5 = oracle.rope_neox(q, k, 517, hd, nh, nkv, 1e6)
+    pn = lambda v: np.hypot(v.reshape(-1, 2, hd // 2)[:, 0], v.reshape(-1, 2, hd // 2)[:, 1])
+    np.testing.assert_allclose(pn(q5), pn(q), rtol=1e-5)
+    np.testing.assert_allclose(q5, npref.rope_neox(q.astype(np.float64), 517, hd, 1e6), atol=5e-4)
+    np.testing.assert_allclose(k5, npref.rope_neox(k.astype(np.float64), 517, hd, 1e6), atol=5e-4)
+
+
+def test_rope_neox_is_interleaved_rope_of_the_permuted_head():
+    # Exact in float32: ApplyRoPENeox's angle for element j equals ApplyRoPE's for
+    # the pair at 2j (j*(2/hd) and 2j*(1/hd) differ by an exact factor 2), and
+    # x1*c + x0*s is x0*s + x1*c.  This is the identity the device path relies on
+    # when it stores q/k rows of a split-half model in pair order.
+    hd, nh, nkv = 64, 14, 2
+    q = synth.normal(9, "pq", nh * hd, 1.0)
+    k = synth.normal(9, "pk", nkv * hd, 1.0)
+    for pos in (1, 7, 1000, 4095):
+        qn, kn = oracle.rope_neox(q, k, pos, hd, nh, nkv, 1e6)
+        qi, ki = oracle.rope(_split_half_to_pairs(q, hd), _split_half_to_pairs(k, hd), pos, hd, nh, nkv, 1e6)
+        assert np.array_equal(_split_half_to_pairs(qn, hd), qi)
+        assert np.array_equal(_split_half_to_pairs(kn, hd), ki)
+
+
 def test_softmax_sums_to_one_and_is_shift_invariant():
     x = synth.normal(5, "sm", 300, 3.0)
     p = oracle.softmax(x)
