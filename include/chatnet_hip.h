@@ -126,7 +126,8 @@ CHATNET_API int chatnet_upload_tensor(chatnet_model* m, const char* name, uint32
  * position..position+n-1, writing their K/V into the cache; logits of the last
  * token stay on the device and are copied to `logits_host` (vocab_size
  * floats) when it is non-NULL.  Spans of 8 or more tokens (Q4_0 weights,
- * head_dim 64 or 128) run as batches of up to 512 tokens: exact-weight MFMA
+ * head_dim 64 or 128, n_heads/n_kv_heads dividing 64) run as batches of up
+ * to 512 tokens: exact-weight MFMA
  * GEMMs over two-plane bf16 activations and causal attention over the cache;
  * shorter spans run token by token. */
 CHATNET_API int chatnet_forward(chatnet_model* m, const int32_t* tokens, int n, int position,
