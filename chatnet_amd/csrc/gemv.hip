@@ -1040,23 +1040,29 @@ GemvShape pick_shape(int K, int n_vrows, int num_cus, bool allow8, bool isolated
     s.rpw = 2;
     s.lpr = nunits <= 16 ? 16 : (nunits <= 32 ? 32 : 64);
   }
-  if (QT == QT_Q4_0 && isolated) {
-    // A stand-alone product (chatnet_matmul, nothing fused): two rows per lane
-    // and, once there are 16 waves per CU, 512-thread workgroups at most two per
-    // CU, else 256-thread ones at most three per CU (cold sweep on the
-    // 2048..32000-row shapes: 11008x4096 7.9 -> 7.2 us, 32000x2048 9.3 -> 8.5 us).
-    s.rpw = 2;
-    const int rw = s.rpw * (64 / s.lpr);
-    const int waves = (n_vrows + rw - 1) / rw;
-    if (waves >= 16 * num_cus) {
+  if (QT == QT_Q4_0) {
+    // Launches that reach 16 waves per CU at two rows per lane run that way, in
+    // 512-thread workgroups at most two per CU: more waves in flight beat fewer
+    // wider ones (7B QKV and gate/up each +3.4 % decode tok/s, the stand-alone
+    // 11008x4096 product 7.9 -> 7.2 us).  Smaller stand-alone products (nothing
+    // fused) also take two rows per lane, in 256-thread workgroups at most three
+    // per CU; smaller fused launches keep the rule above, measured in the
+    // TinyLlama decode graph.
+    const int rw2 = 2 * (64 / s.lpr);
+    const int waves2 = (n_vrows + rw2 - 1) / rw2;
+    if (waves2 >= 16 * num_cus) {
+      s.rpw = 2;
       s.bs = 512;
-      s.grid = (waves + 7) / 8;
+      s.grid = (waves2 + 7) / 8;
       if (s.grid > 2 * num_cus) s.grid = 2 * num_cus;
-    } else {
-      s.grid = (waves + 3) / 4;
-      if (s.grid > 3 * num_cus) s.grid = 3 * num_cus;
+      return s;
     }
-    return s;
+    if (isolated) {
+      s.rpw = 2;
+      s.grid = (waves2 + 3) / 4;
+      if (s.grid > 3 * num_cus) s.grid = 3 * num_cus;
+      return s;
+    }
   }
   const int rw = s.rpw * (64 / s.lpr);
   const int waves = (n_vrows + rw - 1) / rw;
