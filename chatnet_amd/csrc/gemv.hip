@@ -220,6 +220,116 @@ __device__ __forceinline__ void stage_digitize(const XStage<MAXT, NORM>& st, int
 }
 
 // ---------------------------------------------------------------------------
+// Q6_K inputs as signed base-256 digits (v_dot4_i32_i8).
+//
+// Per 16-element group g (the span of one Q6_K scale):
+//   s_g = 18 - e_g  with max|x_g| = f * 2^e_g, f in [0.5, 1)   (so |X| <= 2^18)
+//   X_j = rint(x_j * 2^s_g) = sum_{d<3} D_{j,d} 256^d,  D in [-128, 127]
+// The 6-bit weights q in [0, 63] are non-negative int8s, so
+//   sum_j q_j X_j = Horner over d of dot4(q bytes, D_d bytes)
+// is exact in int32 (|.| <= 16 * 63 * 2^18), and the group contributes
+// sc_g * 2^-s_g * (that - 32 * sum_j X_j).
+// LDS record of unit u (one 256-element super-block): XD6_UNIT_DW dwords,
+// group g at dword 16g: dwords 4d..4d+3 = digit plane d (byte b of dword k is
+// the digit of element 16g + 4k + b), dword 12 = sum_j X_j, dword 13 = s_g.
+// The 260-dword unit stride puts the 16-byte reads of neighbouring lanes
+// (different units, same group) on different banks.
+// ---------------------------------------------------------------------------
+constexpr int XD6_UNIT_DW = 260;
+
+template <int MAXT, bool NORM>
+struct XStage16 {
+  float x[MAXT][16];
+  float g[MAXT][16];
+};
+template <int MAXT>
+struct XStage16<MAXT, false> {
+  float x[MAXT][16];
+};
+
+// Group t of x (and of the RMSNorm weight) on thread t % BS, loads issued
+// before the caller's weight loads (see stage_load).
+template <int MAXT, bool NORM, int BS>
+__device__ __forceinline__ void stage_load16(const float* __restrict__ x, const float* __restrict__ norm_w, int K,
+                                             XStage16<MAXT, NORM>& st) {
+  const int ngroups = K >> 4;
+#pragma unroll
+  for (int j = 0; j < MAXT; j++) {
+    const int t = threadIdx.x + BS * j;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f), g = v;
+      if (t < ngroups) {
+        v = *reinterpret_cast<const float4*>(x + 16 * t + 4 * c);
+        if constexpr (NORM) g = *reinterpret_cast<const float4*>(norm_w + 16 * t + 4 * c);
+      }
+      st.x[j][4 * c + 0] = v.x; st.x[j][4 * c + 1] = v.y; st.x[j][4 * c + 2] = v.z; st.x[j][4 * c + 3] = v.w;
+      if constexpr (NORM) {
+        st.g[j][4 * c + 0] = g.x; st.g[j][4 * c + 1] = g.y; st.g[j][4 * c + 2] = g.z; st.g[j][4 * c + 3] = g.w;
+      }
+    }
+  }
+}
+
+// Writes the base-256 digit records of x * norm_w (x alone without NORM) and,
+// as stage_digitize, leaves each wave's share of sum x^2 in red[wave].
+template <int MAXT, bool NORM, int BS>
+__device__ __forceinline__ void stage_digitize16(const XStage16<MAXT, NORM>& st, int K, uint32_t* xd, float* red) {
+  const int ngroups = K >> 4;
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < MAXT; j++) {
+    const int t = threadIdx.x + BS * j;
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      v[i] = st.x[j][i];
+      ss += v[i] * v[i];
+    }
+    if constexpr (NORM) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) v[i] = v[i] * st.g[j][i];
+    }
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(v[i]));
+    int e = 0;
+    (void)frexpf(m, &e);
+    const int sc = m > 0.f ? 18 - e : 0;
+    // U = X + 0x808080 in [0x7C8080, 0x848080]: its bytes 0..2 are D_d + 128
+    uint32_t U[16];
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const int X = (int)rintf(ldexpf(v[i], sc));
+      sum += X;
+      U[i] = (uint32_t)(X + 0x808080);
+    }
+    if (t < ngroups) {
+      uint32_t* rec = xd + (t >> 4) * XD6_UNIT_DW + 16 * (t & 15);
+      uint32_t P[3][4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const uint32_t a01 = __builtin_amdgcn_perm(U[4 * k + 1], U[4 * k], 0x05010400u);  // U0.b0 U1.b0 U0.b1 U1.b1
+        const uint32_t a23 = __builtin_amdgcn_perm(U[4 * k + 3], U[4 * k + 2], 0x05010400u);
+        const uint32_t c01 = __builtin_amdgcn_perm(U[4 * k + 1], U[4 * k], 0x00000602u);  // U0.b2 U1.b2
+        const uint32_t c23 = __builtin_amdgcn_perm(U[4 * k + 3], U[4 * k + 2], 0x00000602u);
+        P[0][k] = __builtin_amdgcn_perm(a23, a01, 0x05040100u) ^ 0x80808080u;
+        P[1][k] = __builtin_amdgcn_perm(a23, a01, 0x07060302u) ^ 0x80808080u;
+        P[2][k] = __builtin_amdgcn_perm(c23, c01, 0x05040100u) ^ 0x80808080u;
+      }
+#pragma unroll
+      for (int d = 0; d < 3; d++)
+        *reinterpret_cast<uint4*>(rec + 4 * d) = make_uint4(P[d][0], P[d][1], P[d][2], P[d][3]);
+      rec[12] = (uint32_t)sum;
+      rec[13] = (uint32_t)sc;
+    }
+  }
+  ss = cn_wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+}
+
+// ---------------------------------------------------------------------------
 // Unit loads
 // ---------------------------------------------------------------------------
 template <int QT>
@@ -502,44 +612,50 @@ __device__ __forceinline__ void dot_unit_q4_k(const uint32_t (*w)[36], const flo
 //   q2 = ql[64h+l+32]&15 | ((qh>>2)&3)<<4         -> element 128h+32+l, scale sc[8h+l/16+2]
 //   q3 = ql[64h+l]>>4 | ((qh>>4)&3)<<4            -> element 128h+64+l, scale sc[8h+l/16+4]
 //   q4 = ql[64h+l+32]>>4 | ((qh>>6)&3)<<4         -> element 128h+96+l, scale sc[8h+l/16+6]
-// value = d*sc*(q-32): per 16-element group g, dot = d*sc[g]*(S_g - 32*X_g).
+// value = d*sc*(q-32): the 16 elements of group g = 8h + 2*qi + lb are l in
+// [16lb, 16lb+16) of q_{qi+1}; their q bytes, assembled four at a time in
+// element order, meet the digit planes of stage_digitize16 on v_dot4_i32_i8.
 template <int RPW>
-__device__ __forceinline__ void dot_unit_q6_k(const uint32_t (*w)[53], const float* xs,
-                                              const float* sx16, float* acc) {
+__device__ __forceinline__ void dot_unit_q6_k_dig(const uint32_t (*w)[53], const uint32_t* xd, float* acc) {
   float part[RPW];
 #pragma unroll
   for (int i = 0; i < RPW; i++) part[i] = 0.f;
 #pragma unroll
   for (int h = 0; h < 2; h++) {
 #pragma unroll
-    for (int qi = 0; qi < 4; qi++) {        // q1..q4 -> element offset 32*qi
+    for (int qi = 0; qi < 4; qi++) {
 #pragma unroll
-      for (int lb = 0; lb < 2; lb++) {      // l in [16lb, 16lb+16)
-        const int e0 = 128 * h + 32 * qi + 16 * lb;  // first element of this 16-group
-        float xv[16];
+      for (int lb = 0; lb < 2; lb++) {
+        const int g = 8 * h + 2 * qi + lb;  // scale index = element / 16
+        const uint32_t* rec = xd + 16 * g;
+        uint32_t D[3][4];
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-          float4 t = *reinterpret_cast<const float4*>(xs + e0 + 4 * c);
-          xv[4 * c + 0] = t.x; xv[4 * c + 1] = t.y; xv[4 * c + 2] = t.z; xv[4 * c + 3] = t.w;
+        for (int d = 0; d < 3; d++) {
+          const uint4 t = *reinterpret_cast<const uint4*>(rec + 4 * d);
+          D[d][0] = t.x; D[d][1] = t.y; D[d][2] = t.z; D[d][3] = t.w;
         }
-        const float xsum = sx16[e0 >> 4];
+        const int xsum = (int)rec[12];
+        const int e = (int)rec[13];
 #pragma unroll
         for (int i = 0; i < RPW; i++) {
-          float s = 0.f;
+          uint32_t q[4];
 #pragma unroll
-          for (int k = 0; k < 4; k++) {  // 4 dwords = 16 consecutive l
+          for (int k = 0; k < 4; k++) {
             const int l = 16 * lb + 4 * k;
             const uint32_t qlw = w[i][(64 * h + l + ((qi & 1) ? 32 : 0)) >> 2];
             const uint32_t qhw = w[i][(128 + 32 * h + l) >> 2];
             const uint32_t nib = (qi < 2) ? (qlw & 0x0F0F0F0Fu) : ((qlw >> 4) & 0x0F0F0F0Fu);
-            const uint32_t two = ((qhw >> (2 * qi)) & 0x03030303u) << 4;
-            const uint32_t q = nib | two;
-#pragma unroll
-            for (int b = 0; b < 4; b++) s += (float)((q >> (8 * b)) & 0xFFu) * xv[4 * k + b];
+            q[k] = nib | (((qhw >> (2 * qi)) & 0x03030303u) << 4);
           }
-          const int g = 8 * h + 2 * qi + lb;  // scale index = element / 16
+          int t = 0;
+#pragma unroll
+          for (int d = 2; d >= 0; d--) {
+            if (d < 2) t <<= 8;
+#pragma unroll
+            for (int k = 0; k < 4; k++) t = __builtin_amdgcn_sdot4((int)q[k], (int)D[d][k], t, false);
+          }
           const int8_t scv = (int8_t)((w[i][(192 + g) >> 2] >> (8 * ((192 + g) & 3))) & 0xFF);
-          part[i] += (float)scv * (s - 32.f * xsum);
+          part[i] += ldexpf((float)(t - 32 * xsum) * (float)scv, -e);
         }
       }
     }
@@ -640,12 +756,11 @@ __device__ __forceinline__ void dot_unit_q5_k(const uint32_t (*w)[44], const flo
 
 template <int QT, int RPW>
 __device__ __forceinline__ void dot_unit(const uint32_t (*w)[QTraits<QT>::NDW], const float* xs,
-                                         const float* sx, const float* sx16, float* acc) {
+                                         const float* sx, float* acc) {
   if constexpr (QT == QT_Q4_0) dot_unit_q4_0<RPW>(w, xs, sx, acc);
   else if constexpr (QT == QT_Q4_K) dot_unit_q4_k<RPW>(w, xs, sx, acc);
   else if constexpr (QT == QT_Q8_0) dot_unit_q8_0<RPW>(w, xs, sx, acc);
-  else if constexpr (QT == QT_Q5_K) dot_unit_q5_k<RPW>(w, xs, sx, acc);
-  else dot_unit_q6_k<RPW>(w, xs, sx16, acc);
+  else dot_unit_q5_k<RPW>(w, xs, sx, acc);
 }
 
 // Segment base pointer and row count by run-time segment index, chosen with
@@ -820,10 +935,9 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
   extern __shared__ float smem[];
   const int K = a.K;
   const int nunits = K / UNIT;
-  float* xs = smem;                                      // nunits*(UNIT+4)
-  float* sx = xs + nunits * (UNIT + 4);                  // K/32 block sums
-  float* sx16 = sx + (K >> 5);                           // K/16 group sums (Q6_K)
-  float* red = sx16 + ((QT == QT_Q6_K) ? (K >> 4) : 0);  // 4 floats
+  float* xs = smem;                      // fp32 path: nunits*(UNIT+4)
+  float* sx = xs + nunits * (UNIT + 4);  // K/32 block sums
+  float* red = sx + (K >> 5);            // 4 floats
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane / LPR, li = lane % LPR;
@@ -838,21 +952,33 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
   const int pos = EPI == GEMV_EPI_QKV ? *a.pos : 0;
 
   // ---- prologue: stage x (optionally RMS-normalised) into LDS ----
-  // Integer digit path: Q4_0, and Q4_K for K <= 8192 (the register budget of
-  // the staged x at 32 items per super-block lane).
-  constexpr bool kDigits = QT == QT_Q4_0 || (QT == QT_Q4_K && LPR <= 32);
+  // Integer digit paths: Q4_0, Q4_K for K <= 8192 (the register budget of the
+  // staged x at 32 items per super-block lane), and Q6_K.
+  constexpr bool kDigits = QT == QT_Q4_0 || (QT == QT_Q4_K && LPR <= 32) || QT == QT_Q6_K;
   if constexpr (kDigits) {
-    // items per thread: K <= UNIT * LPR * NU, so K/8 <= (UNIT/8) * LPR * NU items over BS threads
-    constexpr int MAXT = ((UNIT / 8) * LPR * NU + BS - 1) / BS;
     constexpr bool NORM = EPI == GEMV_EPI_QKV || EPI == GEMV_EPI_SWIGLU || EPI == GEMV_EPI_LOGITS;
-    XStage<MAXT, NORM> st;
-    stage_load<MAXT, NORM, BS>(a.x, a.norm_w, K, st);
-    // rows past n_vrows come back as zeros, so idle waves need no branch here
-    issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
-    load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, pos, res);
     uint32_t* xd = reinterpret_cast<uint32_t*>(smem);
-    float* xred = reinterpret_cast<float*>(smem) + (size_t)(K >> 6) * XD_UNIT_DW;
-    stage_digitize<MAXT, NORM, BS, QT == QT_Q4_K>(st, K, xd, xred);
+    float* xred;
+    if constexpr (QT == QT_Q6_K) {
+      // groups per thread: K <= 256 * LPR * NU, so K/16 <= 16 * LPR * NU groups over BS threads
+      constexpr int MAXT = (16 * LPR * NU + BS - 1) / BS;
+      XStage16<MAXT, NORM> st;
+      stage_load16<MAXT, NORM, BS>(a.x, a.norm_w, K, st);
+      issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
+      load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, pos, res);
+      xred = reinterpret_cast<float*>(smem) + (size_t)nunits * XD6_UNIT_DW;
+      stage_digitize16<MAXT, NORM, BS>(st, K, xd, xred);
+    } else {
+      // items per thread: K <= UNIT * LPR * NU, so K/8 <= (UNIT/8) * LPR * NU items over BS threads
+      constexpr int MAXT = ((UNIT / 8) * LPR * NU + BS - 1) / BS;
+      XStage<MAXT, NORM> st;
+      stage_load<MAXT, NORM, BS>(a.x, a.norm_w, K, st);
+      // rows past n_vrows come back as zeros, so idle waves need no branch here
+      issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
+      load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, pos, res);
+      xred = reinterpret_cast<float*>(smem) + (size_t)(K >> 6) * XD_UNIT_DW;
+      stage_digitize<MAXT, NORM, BS, QT == QT_Q4_K>(st, K, xd, xred);
+    }
     __syncthreads();
     float ss = 0.f;
 #pragma unroll
@@ -872,7 +998,8 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
 #pragma unroll
             for (int k = 0; k < T::NDW; k++) wu[i][k] = w[i][n][k];
           if constexpr (QT == QT_Q4_0) dot_unit_q4_0_dig<RPW>(wu, xd + u * XD_UNIT_DW, acc);
-          else dot_unit_q4_k_dig<RPW>(wu, xd + 4 * u * XD_UNIT_DW, acc);
+          else if constexpr (QT == QT_Q4_K) dot_unit_q4_k_dig<RPW>(wu, xd + 4 * u * XD_UNIT_DW, acc);
+          else dot_unit_q6_k_dig<RPW>(wu, xd + u * XD6_UNIT_DW, acc);
         }
       }
       const int cur = it;
@@ -892,8 +1019,7 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
       }
       if (li == 0) epilogue<EPI, RPW>(a, cur * RW + sub * RPW, acc, res_cur, pos);
     }
-    return;
-  }
+  } else {
   if (it < n_iters) {
     issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
     load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, pos, res);
@@ -917,22 +1043,12 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
     *reinterpret_cast<float4*>(xs + xidx<UNIT>(k)) = t;
   }
   __syncthreads();
-  if constexpr (QT == QT_Q6_K) {
-    for (int g = threadIdx.x; g < (K >> 4); g += CN_BLOCK) {
-      const float* p = xs + xidx<UNIT>(g * 16);
-      float s = 0.f;
+  for (int b = threadIdx.x; b < (K >> 5); b += CN_BLOCK) {
+    const float* p = xs + xidx<UNIT>(b * 32);
+    float s = 0.f;
 #pragma unroll
-      for (int j = 0; j < 16; j++) s += p[j];
-      sx16[g] = s;
-    }
-  } else {
-    for (int b = threadIdx.x; b < (K >> 5); b += CN_BLOCK) {
-      const float* p = xs + xidx<UNIT>(b * 32);
-      float s = 0.f;
-#pragma unroll
-      for (int j = 0; j < 32; j++) s += p[j];
-      sx[b] = s;
-    }
+    for (int j = 0; j < 32; j++) s += p[j];
+    sx[b] = s;
   }
   __syncthreads();
 
@@ -950,7 +1066,7 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
         for (int i = 0; i < RPW; i++)
 #pragma unroll
           for (int k = 0; k < T::NDW; k++) wu[i][k] = w[i][n][k];
-        dot_unit<QT, RPW>(wu, xs + u * (UNIT + 4), sx + u * (UNIT / 32), sx16 + u * (UNIT / 16), acc);
+        dot_unit<QT, RPW>(wu, xs + u * (UNIT + 4), sx + u * (UNIT / 32), acc);
       }
     }
     const int cur = it;
@@ -969,6 +1085,7 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
     }
     if (li == 0) epilogue<EPI, RPW>(a, cur * RW + sub * RPW, acc, res_cur, pos);
   }
+  }
 }
 
 template <int QT>
@@ -977,7 +1094,8 @@ size_t gemv_smem_bytes(int K) {
   const int nunits = K / T::UNIT;
   // digit records (Q4_0; Q4_K up to 32 super-blocks per row) + one float per wave
   if (QT == QT_Q4_0 || (QT == QT_Q4_K && nunits <= 32)) return ((size_t)(K >> 6) * XD_UNIT_DW + 16) * sizeof(uint32_t);
-  size_t f = (size_t)nunits * (T::UNIT + 4) + (K >> 5) + (QT == QT_Q6_K ? (K >> 4) : 0) + 4;
+  if (QT == QT_Q6_K) return ((size_t)nunits * XD6_UNIT_DW + 16) * sizeof(uint32_t);
+  size_t f = (size_t)nunits * (T::UNIT + 4) + (K >> 5) + 4;
   return f * sizeof(float);
 }
 

@@ -75,7 +75,10 @@ def test_q6_k_rows_off_dword_alignment_are_exact_per_row():
     announce("q6_k misaligned rows")
     y = gpu_matmul(14, t.data, x, M, K)[0]
     r = oracle.matvec(14, t.data, x, M, K)
-    rel = np.abs(y - r) / np.maximum(np.abs(r), 1e-3)
+    # A misread row is off by about its own size.  The floor (1 % of the largest
+    # row) keeps rows that cancel to near zero from failing on the digit path's
+    # rounding of x, ~2^-19 of each 16-element group's maximum.
+    rel = np.abs(y - r) / np.maximum(np.abs(r), 1e-2 * np.max(np.abs(r)))
     assert np.max(rel[1::2]) < 1e-3 and np.max(rel[0::2]) < 1e-3
 
 
