@@ -408,48 +408,6 @@ __device__ __forceinline__ void load_unit<QT_Q6_K>(const uint8_t* row, int u, ui
 // xs: LDS (padded) already offset to the unit's first element; sx: block sums.
 // ---------------------------------------------------------------------------
 
-// Byte j (0..15) of the qs of block A (pair bytes 2..17) / block B (20..35).
-template <int RPW>
-__device__ __forceinline__ void dot_unit_q4_0(const uint32_t (*w)[9], const float* xs,
-                                              const float* sx, float* acc) {
-  float sa[RPW], sb[RPW];
-#pragma unroll
-  for (int i = 0; i < RPW; i++) sa[i] = sb[i] = 0.f;
-  // Block A: x[0..31]; Block B: x[32..63].
-#pragma unroll
-  for (int blk = 0; blk < 2; blk++) {
-    float xl[16], xh[16];
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-      float4 t0 = *reinterpret_cast<const float4*>(xs + blk * 32 + 4 * c);
-      float4 t1 = *reinterpret_cast<const float4*>(xs + blk * 32 + 16 + 4 * c);
-      xl[4 * c + 0] = t0.x; xl[4 * c + 1] = t0.y; xl[4 * c + 2] = t0.z; xl[4 * c + 3] = t0.w;
-      xh[4 * c + 0] = t1.x; xh[4 * c + 1] = t1.y; xh[4 * c + 2] = t1.z; xh[4 * c + 3] = t1.w;
-    }
-#pragma unroll
-    for (int i = 0; i < RPW; i++) {
-      float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-      for (int j = 0; j < 16; j++) {
-        const int P = (blk ? 20 : 2) + j;  // byte position inside the 36-byte pair
-        const uint32_t dw = w[i][P >> 2];
-        const uint32_t lo = dw & 0x0F0F0F0Fu;
-        const uint32_t hi = (dw >> 4) & 0x0F0F0F0Fu;
-        const int b = P & 3;
-        s0 += (float)((lo >> (8 * b)) & 0xFFu) * xl[j];
-        s1 += (float)((hi >> (8 * b)) & 0xFFu) * xh[j];
-      }
-      if (blk == 0) sa[i] = s0 + s1; else sb[i] = s0 + s1;
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < RPW; i++) {
-    const float da = cn_h2f(w[i][0]);
-    const float db = cn_h2f(w[i][4] >> 16);
-    acc[i] += da * (sa[i] - 8.f * sx[0]) + db * (sb[i] - 8.f * sx[1]);
-  }
-}
-
 // Q4_0 unit against the digit record xd (see stage_digitize): block A's qs
 // (pair bytes 2..17) is realigned with alignbyte, block B's (bytes 20..35)
 // is dword aligned.
@@ -552,61 +510,6 @@ __device__ __forceinline__ void dot_unit_q4_k_dig(const uint32_t (*w)[36], const
   }
 }
 
-// Q4_K super-block in the reference's order (DequantQ4K.cs:59-72): sub-block s
-// uses qs[16s..16s+15]; low nibbles -> elements 32s+0..15, high -> 32s+16..31.
-// value = d*sc[s]*q - dmin*m[s]  =>  dot = sum_s d*sc[s]*S_s - dmin*m[s]*X_s.
-template <int RPW>
-__device__ __forceinline__ void dot_unit_q4_k(const uint32_t (*w)[36], const float* xs,
-                                              const float* sx, float* acc) {
-  float dsc[RPW][8], dmm[RPW][8];
-#pragma unroll
-  for (int i = 0; i < RPW; i++) {
-    const float d = cn_h2f(w[i][0]), dmin = cn_h2f(w[i][0] >> 16);
-    const uint32_t q0 = w[i][1], q1 = w[i][2], q2 = w[i][3];  // scale bytes 0..11
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-      int sc, m;
-      if (j < 4) {
-        sc = (q0 >> (8 * j)) & 63;
-        m = (q1 >> (8 * j)) & 63;
-      } else {
-        const uint32_t b8 = (q2 >> (8 * (j - 4))) & 0xFF;
-        sc = (b8 & 0xF) | (((q0 >> (8 * (j - 4) + 6)) & 3) << 4);
-        m = (b8 >> 4) | (((q1 >> (8 * (j - 4) + 6)) & 3) << 4);
-      }
-      dsc[i][j] = d * (float)sc;
-      dmm[i][j] = dmin * (float)m;
-    }
-  }
-#pragma unroll
-  for (int s = 0; s < 8; s++) {
-    float xl[16], xh[16];
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-      float4 t0 = *reinterpret_cast<const float4*>(xs + 32 * s + 4 * c);
-      float4 t1 = *reinterpret_cast<const float4*>(xs + 32 * s + 16 + 4 * c);
-      xl[4 * c + 0] = t0.x; xl[4 * c + 1] = t0.y; xl[4 * c + 2] = t0.z; xl[4 * c + 3] = t0.w;
-      xh[4 * c + 0] = t1.x; xh[4 * c + 1] = t1.y; xh[4 * c + 2] = t1.z; xh[4 * c + 3] = t1.w;
-    }
-    const float xsum = sx[s];
-#pragma unroll
-    for (int i = 0; i < RPW; i++) {
-      float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const uint32_t dw = w[i][4 + 4 * s + k];
-        const uint32_t lo = dw & 0x0F0F0F0Fu, hi = (dw >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-          s0 += (float)((lo >> (8 * b)) & 0xFFu) * xl[4 * k + b];
-          s1 += (float)((hi >> (8 * b)) & 0xFFu) * xh[4 * k + b];
-        }
-      }
-      acc[i] += dsc[i][s] * (s0 + s1) - dmm[i][s] * xsum;
-    }
-  }
-}
-
 // Q6_K super-block (DequantQ6K.cs:53-83): for half h and l < 32,
 //   q1 = ql[64h+l]&15 | (qh[32h+l]&3)<<4          -> element 128h+l,    scale sc[8h+l/16]
 //   q2 = ql[64h+l+32]&15 | ((qh>>2)&3)<<4         -> element 128h+32+l, scale sc[8h+l/16+2]
@@ -695,14 +598,20 @@ __device__ __forceinline__ void dot_unit_q8_0(const uint32_t (*w)[17], const flo
   }
 }
 
-// Q5_K super-block (DequantQ5K.cs:37-88): Q4_K's scales and nibble order, plus
-// qh[32] at byte 16 whose bit e%8 of byte e/8 is bit 4 of element e.  For
-// sub-block s that is bit j of dword 4+s for element 32s+j, so four high bits
-// at a time are spread into byte lanes (t * 0x00204081 puts bit b of t at bit
-// 8b) and or-ed above the nibbles: q5 bytes, exact as floats.
-template <int RPW>
-__device__ __forceinline__ void dot_unit_q5_k(const uint32_t (*w)[44], const float* xs, const float* sx,
-                                              float* acc) {
+// Q4_K / Q5_K super-block against the base-256 digit record of
+// stage_digitize16.  Scales and nibble order of Q4_K (DequantQ4K.cs:59-72):
+// sub-block s uses qs[16s..16s+15], low nibbles -> elements 32s+0..15, high ->
+// 32s+16..31, so digit group g = 2s + hh takes the low (hh = 0) or high nibbles
+// of those 16 bytes, four elements per qs dword in element order.  Q5_K
+// (DequantQ5K.cs:37-88) adds qh[32] at byte 16 whose bit e%8 of byte e/8 is bit
+// 4 of element e: bits 16hh + 4k .. +3 of dword 4+s for the four elements of
+// qs dword k, spread into byte lanes (t * 0x00204081 puts bit b of t at bit
+// 8b) above the nibbles.  With t_g = sum_j q_j X_j (exact, |.| <= 16*31*2^18)
+// the group contributes 2^-e_g (d sc_s t_g - dmin m_s SX_g).
+template <int QT, int RPW>
+__device__ __forceinline__ void dot_unit_k45_dig8(const uint32_t (*w)[QTraits<QT>::NDW], const uint32_t* xd,
+                                                  float* acc) {
+  constexpr int QS = QT == QT_Q5_K ? 12 : 4;  // first qs dword of the super-block
   float dsc[RPW][8], dmm[RPW][8];
 #pragma unroll
   for (int i = 0; i < RPW; i++) {
@@ -724,43 +633,40 @@ __device__ __forceinline__ void dot_unit_q5_k(const uint32_t (*w)[44], const flo
     }
   }
 #pragma unroll
-  for (int s = 0; s < 8; s++) {
-    float xl[16], xh[16];
+  for (int g = 0; g < 16; g++) {
+    const int sb = g >> 1, hh = g & 1;
+    const uint32_t* rec = xd + 16 * g;
+    uint32_t D[3][4];
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-      const float4 t0 = *reinterpret_cast<const float4*>(xs + 32 * s + 4 * c);
-      const float4 t1 = *reinterpret_cast<const float4*>(xs + 32 * s + 16 + 4 * c);
-      xl[4 * c + 0] = t0.x; xl[4 * c + 1] = t0.y; xl[4 * c + 2] = t0.z; xl[4 * c + 3] = t0.w;
-      xh[4 * c + 0] = t1.x; xh[4 * c + 1] = t1.y; xh[4 * c + 2] = t1.z; xh[4 * c + 3] = t1.w;
+    for (int d = 0; d < 3; d++) {
+      const uint4 t = *reinterpret_cast<const uint4*>(rec + 4 * d);
+      D[d][0] = t.x; D[d][1] = t.y; D[d][2] = t.z; D[d][3] = t.w;
     }
-    const float xsum = sx[s];
+    const int xsum = (int)rec[12];
+    const int e = (int)rec[13];
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
-      const uint32_t hb = w[i][4 + s];
-      float s0 = 0.f, s1 = 0.f;
+      uint32_t q[4];
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        const uint32_t dw = w[i][12 + 4 * s + k];
-        const uint32_t tl = (hb >> (4 * k)) & 0xFu, th = (hb >> (16 + 4 * k)) & 0xFu;
-        const uint32_t ql = (dw & 0x0F0F0F0Fu) | (((tl * 0x00204081u) & 0x01010101u) << 4);
-        const uint32_t qh = ((dw >> 4) & 0x0F0F0F0Fu) | (((th * 0x00204081u) & 0x01010101u) << 4);
-        s0 += cn_ubyte<0>(ql) * xl[4 * k] + cn_ubyte<1>(ql) * xl[4 * k + 1] + cn_ubyte<2>(ql) * xl[4 * k + 2] +
-              cn_ubyte<3>(ql) * xl[4 * k + 3];
-        s1 += cn_ubyte<0>(qh) * xh[4 * k] + cn_ubyte<1>(qh) * xh[4 * k + 1] + cn_ubyte<2>(qh) * xh[4 * k + 2] +
-              cn_ubyte<3>(qh) * xh[4 * k + 3];
+        const uint32_t dw = w[i][QS + 4 * sb + k];
+        uint32_t v = hh ? ((dw >> 4) & 0x0F0F0F0Fu) : (dw & 0x0F0F0F0Fu);
+        if constexpr (QT == QT_Q5_K) {
+          const uint32_t t4 = (w[i][4 + sb] >> (16 * hh + 4 * k)) & 0xFu;
+          v |= ((t4 * 0x00204081u) & 0x01010101u) << 4;
+        }
+        q[k] = v;
       }
-      acc[i] += dsc[i][s] * (s0 + s1) - dmm[i][s] * xsum;
+      int t = 0;
+#pragma unroll
+      for (int d = 2; d >= 0; d--) {
+        if (d < 2) t <<= 8;
+#pragma unroll
+        for (int k = 0; k < 4; k++) t = __builtin_amdgcn_sdot4((int)q[k], (int)D[d][k], t, false);
+      }
+      acc[i] += ldexpf(dsc[i][sb] * (float)t - dmm[i][sb] * (float)xsum, -e);
     }
   }
-}
-
-template <int QT, int RPW>
-__device__ __forceinline__ void dot_unit(const uint32_t (*w)[QTraits<QT>::NDW], const float* xs,
-                                         const float* sx, float* acc) {
-  if constexpr (QT == QT_Q4_0) dot_unit_q4_0<RPW>(w, xs, sx, acc);
-  else if constexpr (QT == QT_Q4_K) dot_unit_q4_k<RPW>(w, xs, sx, acc);
-  else if constexpr (QT == QT_Q8_0) dot_unit_q8_0<RPW>(w, xs, sx, acc);
-  else dot_unit_q5_k<RPW>(w, xs, sx, acc);
 }
 
 // Segment base pointer and row count by run-time segment index, chosen with
@@ -952,14 +858,17 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
   const int pos = EPI == GEMV_EPI_QKV ? *a.pos : 0;
 
   // ---- prologue: stage x (optionally RMS-normalised) into LDS ----
-  // Integer digit paths: Q4_0, Q4_K for K <= 8192 (the register budget of the
-  // staged x at 32 items per super-block lane), and Q6_K.
-  constexpr bool kDigits = QT == QT_Q4_0 || (QT == QT_Q4_K && LPR <= 32) || QT == QT_Q6_K;
+  // Integer digit paths: base-16 digits on v_dot8_i32_i4 for Q4_0 and for Q4_K
+  // up to K = 8192 (the register budget of the staged x at 32 items per
+  // super-block lane); base-256 digits on v_dot4_i32_i8 for Q6_K, Q5_K and the
+  // longer Q4_K rows.  Q8_0 runs the fp32 dot below.
+  constexpr bool kDig8 = QT == QT_Q6_K || QT == QT_Q5_K || (QT == QT_Q4_K && LPR > 32);
+  constexpr bool kDigits = QT != QT_Q8_0;
   if constexpr (kDigits) {
     constexpr bool NORM = EPI == GEMV_EPI_QKV || EPI == GEMV_EPI_SWIGLU || EPI == GEMV_EPI_LOGITS;
     uint32_t* xd = reinterpret_cast<uint32_t*>(smem);
     float* xred;
-    if constexpr (QT == QT_Q6_K) {
+    if constexpr (kDig8) {
       // groups per thread: K <= 256 * LPR * NU, so K/16 <= 16 * LPR * NU groups over BS threads
       constexpr int MAXT = (16 * LPR * NU + BS - 1) / BS;
       XStage16<MAXT, NORM> st;
@@ -998,8 +907,9 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
 #pragma unroll
             for (int k = 0; k < T::NDW; k++) wu[i][k] = w[i][n][k];
           if constexpr (QT == QT_Q4_0) dot_unit_q4_0_dig<RPW>(wu, xd + u * XD_UNIT_DW, acc);
-          else if constexpr (QT == QT_Q4_K) dot_unit_q4_k_dig<RPW>(wu, xd + 4 * u * XD_UNIT_DW, acc);
-          else dot_unit_q6_k_dig<RPW>(wu, xd + u * XD6_UNIT_DW, acc);
+          else if constexpr (QT == QT_Q6_K) dot_unit_q6_k_dig<RPW>(wu, xd + u * XD6_UNIT_DW, acc);
+          else if constexpr (kDig8) dot_unit_k45_dig8<QT, RPW>(wu, xd + u * XD6_UNIT_DW, acc);
+          else dot_unit_q4_k_dig<RPW>(wu, xd + 4 * u * XD_UNIT_DW, acc);
         }
       }
       const int cur = it;
@@ -1066,7 +976,7 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
         for (int i = 0; i < RPW; i++)
 #pragma unroll
           for (int k = 0; k < T::NDW; k++) wu[i][k] = w[i][n][k];
-        dot_unit<QT, RPW>(wu, xs + u * (UNIT + 4), sx + u * (UNIT / 32), acc);
+        dot_unit_q8_0<RPW>(wu, xs + u * (UNIT + 4), sx + u * (UNIT / 32), acc);
       }
     }
     const int cur = it;
@@ -1094,7 +1004,7 @@ size_t gemv_smem_bytes(int K) {
   const int nunits = K / T::UNIT;
   // digit records (Q4_0; Q4_K up to 32 super-blocks per row) + one float per wave
   if (QT == QT_Q4_0 || (QT == QT_Q4_K && nunits <= 32)) return ((size_t)(K >> 6) * XD_UNIT_DW + 16) * sizeof(uint32_t);
-  if (QT == QT_Q6_K) return ((size_t)nunits * XD6_UNIT_DW + 16) * sizeof(uint32_t);
+  if (QT == QT_Q6_K || QT == QT_Q5_K || QT == QT_Q4_K) return ((size_t)nunits * XD6_UNIT_DW + 16) * sizeof(uint32_t);
   size_t f = (size_t)nunits * (T::UNIT + 4) + (K >> 5) + 4;
   return f * sizeof(float);
 }
