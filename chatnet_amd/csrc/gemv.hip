@@ -37,12 +37,14 @@ template <> struct QTraits<QT_Q4_0> {
   static constexpr int NDW = 9;          // dwords held per unit
   static constexpr int BLOCK_BYTES = 18, BLOCK = 32;
 };
+// K-quant units are half super-blocks (128 weights): the dwords a lane holds
+// are the super-block header or scales plus that half's quants (load_unit).
 template <> struct QTraits<QT_Q4_K> {
-  static constexpr int UNIT = 256, NDW = 36;
+  static constexpr int UNIT = 128, NDW = 20;
   static constexpr int BLOCK_BYTES = 144, BLOCK = 256;
 };
 template <> struct QTraits<QT_Q6_K> {
-  static constexpr int UNIT = 256, NDW = 53;
+  static constexpr int UNIT = 128, NDW = 27;
   static constexpr int BLOCK_BYTES = 210, BLOCK = 256;
 };
 template <> struct QTraits<QT_Q8_0> {
@@ -50,7 +52,7 @@ template <> struct QTraits<QT_Q8_0> {
   static constexpr int BLOCK_BYTES = 34, BLOCK = 32;
 };
 template <> struct QTraits<QT_Q5_K> {
-  static constexpr int UNIT = 256, NDW = 44;
+  static constexpr int UNIT = 128, NDW = 24;
   static constexpr int BLOCK_BYTES = 176, BLOCK = 256;
 };
 
@@ -229,13 +231,13 @@ __device__ __forceinline__ void stage_digitize(const XStage<MAXT, NORM>& st, int
 //   sum_j q_j X_j = Horner over d of dot4(q bytes, D_d bytes)
 // is exact in int32 (|.| <= 16 * 63 * 2^18), and the group contributes
 // sc_g * 2^-s_g * (that - 32 * sum_j X_j).
-// LDS record of unit u (one 256-element super-block): XD6_UNIT_DW dwords,
-// group g at dword 16g: dwords 4d..4d+3 = digit plane d (byte b of dword k is
-// the digit of element 16g + 4k + b), dword 12 = sum_j X_j, dword 13 = s_g.
-// The 260-dword unit stride puts the 16-byte reads of neighbouring lanes
-// (different units, same group) on different banks.
+// LDS record of unit u (128 elements, half a super-block): XD6_UNIT_DW dwords,
+// local group g at dword 16g: dwords 4d..4d+3 = digit plane d (byte b of dword
+// k is the digit of element 128u + 16g + 4k + b), dword 12 = sum_j X_j,
+// dword 13 = s_g.  The 132-dword unit stride puts the 16-byte reads of
+// neighbouring lanes (different units, same group) on different banks.
 // ---------------------------------------------------------------------------
-constexpr int XD6_UNIT_DW = 260;
+constexpr int XD6_UNIT_DW = 132;
 
 template <int MAXT, bool NORM>
 struct XStage16 {
@@ -306,7 +308,7 @@ __device__ __forceinline__ void stage_digitize16(const XStage16<MAXT, NORM>& st,
       U[i] = (uint32_t)(X + 0x808080);
     }
     if (t < ngroups) {
-      uint32_t* rec = xd + (t >> 4) * XD6_UNIT_DW + 16 * (t & 15);
+      uint32_t* rec = xd + (t >> 3) * XD6_UNIT_DW + 16 * (t & 7);
       uint32_t P[3][4];
 #pragma unroll
       for (int k = 0; k < 4; k++) {
@@ -342,17 +344,23 @@ __device__ __forceinline__ void load_unit<QT_Q4_0>(const uint8_t* row, int u, ui
   for (int k = 0; k < 9; k++) w[k] = p[k];
 }
 
+__device__ __forceinline__ void load_u32x4(const uint8_t* p, uint32_t* w) {
+  const cn_u32x4 t = *reinterpret_cast<const cn_u32x4*>(p);
+  w[0] = t.x;
+  w[1] = t.y;
+  w[2] = t.z;
+  w[3] = t.w;
+}
+
+// Half h = u & 1 of Q4_K super-block u >> 1 (144 bytes, 16-byte aligned):
+// w[0..3] = d, dmin and the 12 scale bytes, w[4..19] = qs[64h .. 64h+63].
 template <>
 __device__ __forceinline__ void load_unit<QT_Q4_K>(const uint8_t* row, int u, uint32_t* w) {
-  const cn_u32x4* p = reinterpret_cast<const cn_u32x4*>(row + (size_t)u * 144);
+  const uint8_t* sb = row + (size_t)(u >> 1) * 144;
+  const int h = u & 1;
+  load_u32x4(sb, w);
 #pragma unroll
-  for (int k = 0; k < 9; k++) {
-    cn_u32x4 t = p[k];
-    w[4 * k + 0] = t.x;
-    w[4 * k + 1] = t.y;
-    w[4 * k + 2] = t.z;
-    w[4 * k + 3] = t.w;
-  }
+  for (int k = 0; k < 4; k++) load_u32x4(sb + 16 + 64 * h + 16 * k, w + 4 + 4 * k);
 }
 
 // Two Q8_0 blocks, 68 bytes: rows hold whole pairs (K % 64 == 0), so a unit
@@ -364,43 +372,50 @@ __device__ __forceinline__ void load_unit<QT_Q8_0>(const uint8_t* row, int u, ui
   for (int k = 0; k < 17; k++) w[k] = p[k];
 }
 
+// Half h = u & 1 of Q5_K super-block u >> 1 (176 bytes, 16-byte aligned):
+// w[0..3] = d, dmin and the scales, w[4..7] = qh[16h .. 16h+15] (the fifth
+// bits of elements 128h ..), w[8..23] = qs[64h .. 64h+63].
 template <>
 __device__ __forceinline__ void load_unit<QT_Q5_K>(const uint8_t* row, int u, uint32_t* w) {
-  const cn_u32x4* p = reinterpret_cast<const cn_u32x4*>(row + (size_t)u * 176);
+  const uint8_t* sb = row + (size_t)(u >> 1) * 176;
+  const int h = u & 1;
+  load_u32x4(sb, w);
+  load_u32x4(sb + 16 + 16 * h, w + 4);
 #pragma unroll
-  for (int k = 0; k < 11; k++) {
-    cn_u32x4 t = p[k];
-    w[4 * k + 0] = t.x;
-    w[4 * k + 1] = t.y;
-    w[4 * k + 2] = t.z;
-    w[4 * k + 3] = t.w;
-  }
+  for (int k = 0; k < 4; k++) load_u32x4(sb + 48 + 64 * h + 16 * k, w + 8 + 4 * k);
 }
 
-// Q6_K super-blocks start on 2-byte boundaries.  Load the dword-aligned window
-// and realign so that canonical byte i of w[] is super-block byte i (w[52]
-// holds d in its low half).  Never touches bytes outside the super-block
-// except the 2 bytes before it, which belong to the same allocation whenever
-// the super-block is not the first one (a misaligned super-block never is).
+// Half h = u & 1 of Q6_K super-block u >> 1 (210 bytes, so super-blocks start
+// on 2-byte boundaries): w[0..15] = ql[64h .. 64h+63], w[16..23] = qh[32h ..
+// 32h+31], w[24..25] = scales[8h .. 8h+7], w[26] = d (low half).  Each piece
+// is read as the dword-aligned window that covers it (one dword more than the
+// piece) and realigned by sh = 0 or 2 bytes, the same for every piece of the
+// super-block, so the loads do not diverge.  The windows of ql and qh end
+// inside the next piece; the scales' window needs its third dword only when
+// sh = 2 (it then ends at byte 209), and d is a 16-bit load, so nothing past
+// the super-block is read.
 template <>
 __device__ __forceinline__ void load_unit<QT_Q6_K>(const uint8_t* row, int u, uint32_t* w) {
-  const uint8_t* s = row + (size_t)u * 210;
-  const uintptr_t a = reinterpret_cast<uintptr_t>(s);
-  const uint32_t* p = reinterpret_cast<const uint32_t*>(a & ~(uintptr_t)3);
-  const uint32_t sh = (uint32_t)(a & 3);  // 0 or 2
-  uint32_t r[53];
+  const uint8_t* sb = row + (size_t)(u >> 1) * 210;
+  const int h = u & 1;
+  const uintptr_t base = reinterpret_cast<uintptr_t>(sb);
+  const uint32_t sh = (uint32_t)(base & 3);  // 0 or 2
+  const uint32_t* q = reinterpret_cast<const uint32_t*>(base & ~(uintptr_t)3);
+  uint32_t r[17], t[9], c[3];
 #pragma unroll
-  for (int k = 0; k < 52; k++) r[k] = p[k];
-  if (sh) {
-    r[52] = p[52];
+  for (int k = 0; k < 17; k++) r[k] = q[16 * h + k];
 #pragma unroll
-    for (int k = 0; k < 52; k++) w[k] = __builtin_amdgcn_alignbyte(r[k + 1], r[k], 2);
-    w[52] = r[52] >> 16;
-  } else {
+  for (int k = 0; k < 9; k++) t[k] = q[32 + 8 * h + k];
+  c[0] = q[48 + 2 * h];
+  c[1] = q[49 + 2 * h];
+  c[2] = sh ? q[50 + 2 * h] : 0u;
 #pragma unroll
-    for (int k = 0; k < 52; k++) w[k] = r[k];
-    w[52] = *reinterpret_cast<const uint16_t*>(s + 208);
-  }
+  for (int k = 0; k < 16; k++) w[k] = __builtin_amdgcn_alignbyte(r[k + 1], r[k], sh);
+#pragma unroll
+  for (int k = 0; k < 8; k++) w[16 + k] = __builtin_amdgcn_alignbyte(t[k + 1], t[k], sh);
+  w[24] = __builtin_amdgcn_alignbyte(c[1], c[0], sh);
+  w[25] = __builtin_amdgcn_alignbyte(c[2], c[1], sh);
+  w[26] = *reinterpret_cast<const uint16_t*>(sb + 208);
 }
 
 // ---------------------------------------------------------------------------
@@ -453,38 +468,40 @@ __device__ __forceinline__ void dot_unit_q4_0_dig(const uint32_t (*w)[9], const 
   dot_q4_0_digits<RPW>(w, X, (int)se.x, (int)se.y, acc);
 }
 
-// Q4_K super-block (reference order, DequantQ4K.cs:59-72) against the digit
-// records of its 8 blocks (4 records).  Sub-block s's qs dwords XOR 0x88888888
-// are (q - 8) as signed nibbles in the digit records' nibble order, so with
-// T_s = sum_j (q_j - 8) X_j from the Horner sum of sdot8 over the 5 digits,
+// d*sc and dmin*m of sub-blocks 4h .. 4h+3 of a Q4_K / Q5_K super-block from
+// its header dwords (get_scale_min_k4, DequantQ4K.cs:218-241): sub-blocks 0..3
+// take the low six bits of scale bytes 0..3 / 4..7, sub-blocks 4..7 a nibble
+// of bytes 8..11 with the top two bits of bytes 0..3 / 4..7 above it.
+__device__ __forceinline__ void k4_scales_half(const uint32_t* hdr, int h, float (&dsc)[4], float (&dmm)[4]) {
+  const float d = cn_h2f(hdr[0]), dmin = cn_h2f(hdr[0] >> 16);
+  const uint32_t q0 = hdr[1], q1 = hdr[2], q2 = hdr[3];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t b8 = (q2 >> (8 * j)) & 0xFF;
+    const int sc_lo = (q0 >> (8 * j)) & 63, m_lo = (q1 >> (8 * j)) & 63;
+    const int sc_hi = (b8 & 0xF) | (((q0 >> (8 * j + 6)) & 3) << 4);
+    const int m_hi = (b8 >> 4) | (((q1 >> (8 * j + 6)) & 3) << 4);
+    dsc[j] = d * (float)(h ? sc_hi : sc_lo);
+    dmm[j] = dmin * (float)(h ? m_hi : m_lo);
+  }
+}
+
+// Half h of a Q4_K super-block (reference order, DequantQ4K.cs:59-72) against
+// the digit records of its 4 blocks (2 records).  Local sub-block s's qs dwords
+// XOR 0x88888888 are (q - 8) as signed nibbles in the digit records' nibble
+// order, so with T_s = sum_j (q_j - 8) X_j from the Horner sum of sdot8 over
+// the 5 digits,
 //   sum_j q_j X_j = T_s + 8 SX_s   (SX_s = sum_j X_j, exact in int32),
 // and the sub-block contributes 2^-e_s (d sc_s (T_s + 8 SX_s) - dmin m_s SX_s):
-// d sc q - dmin m per weight (DequantQ4K.cs:59-72) against x rounded to its
-// digits, as the Q4_0 digit dot.
+// d sc q - dmin m per weight against x rounded to its digits, as the Q4_0
+// digit dot.
 template <int RPW>
-__device__ __forceinline__ void dot_unit_q4_k_dig(const uint32_t (*w)[36], const uint32_t* xd, float* acc) {
-  float dsc[RPW][8], dmm[RPW][8];
+__device__ __forceinline__ void dot_unit_q4_k_dig(const uint32_t (*w)[20], const uint32_t* xd, int h, float* acc) {
+  float dsc[RPW][4], dmm[RPW][4];
 #pragma unroll
-  for (int i = 0; i < RPW; i++) {
-    const float d = cn_h2f(w[i][0]), dmin = cn_h2f(w[i][0] >> 16);
-    const uint32_t q0 = w[i][1], q1 = w[i][2], q2 = w[i][3];  // scale bytes 0..11
+  for (int i = 0; i < RPW; i++) k4_scales_half(w[i], h, dsc[i], dmm[i]);
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      int sc, m;
-      if (j < 4) {
-        sc = (q0 >> (8 * j)) & 63;
-        m = (q1 >> (8 * j)) & 63;
-      } else {
-        const uint32_t b8 = (q2 >> (8 * (j - 4))) & 0xFF;
-        sc = (b8 & 0xF) | (((q0 >> (8 * (j - 4) + 6)) & 3) << 4);
-        m = (b8 >> 4) | (((q1 >> (8 * (j - 4) + 6)) & 3) << 4);
-      }
-      dsc[i][j] = d * (float)sc;
-      dmm[i][j] = dmin * (float)m;
-    }
-  }
-#pragma unroll
-  for (int s = 0; s < 8; s++) {
+  for (int s = 0; s < 4; s++) {
     const uint32_t* rec = xd + (s >> 1) * XD_UNIT_DW;
     const int blk = s & 1;
     uint32_t X[20];
@@ -519,52 +536,49 @@ __device__ __forceinline__ void dot_unit_q4_k_dig(const uint32_t (*w)[36], const
 // [16lb, 16lb+16) of q_{qi+1}; their q bytes, assembled four at a time in
 // element order, meet the digit planes of stage_digitize16 on v_dot4_i32_i8.
 template <int RPW>
-__device__ __forceinline__ void dot_unit_q6_k_dig(const uint32_t (*w)[53], const uint32_t* xd, float* acc) {
+__device__ __forceinline__ void dot_unit_q6_k_dig(const uint32_t (*w)[27], const uint32_t* xd, float* acc) {
   float part[RPW];
 #pragma unroll
   for (int i = 0; i < RPW; i++) part[i] = 0.f;
 #pragma unroll
-  for (int h = 0; h < 2; h++) {
+  for (int qi = 0; qi < 4; qi++) {
 #pragma unroll
-    for (int qi = 0; qi < 4; qi++) {
+    for (int lb = 0; lb < 2; lb++) {
+      const int g = 2 * qi + lb;  // local group: scale 8h + g of the super-block
+      const uint32_t* rec = xd + 16 * g;
+      uint32_t D[3][4];
 #pragma unroll
-      for (int lb = 0; lb < 2; lb++) {
-        const int g = 8 * h + 2 * qi + lb;  // scale index = element / 16
-        const uint32_t* rec = xd + 16 * g;
-        uint32_t D[3][4];
+      for (int d = 0; d < 3; d++) {
+        const uint4 t = *reinterpret_cast<const uint4*>(rec + 4 * d);
+        D[d][0] = t.x; D[d][1] = t.y; D[d][2] = t.z; D[d][3] = t.w;
+      }
+      const int xsum = (int)rec[12];
+      const int e = (int)rec[13];
 #pragma unroll
-        for (int d = 0; d < 3; d++) {
-          const uint4 t = *reinterpret_cast<const uint4*>(rec + 4 * d);
-          D[d][0] = t.x; D[d][1] = t.y; D[d][2] = t.z; D[d][3] = t.w;
+      for (int i = 0; i < RPW; i++) {
+        uint32_t q[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const int l = 16 * lb + 4 * k;
+          const uint32_t qlw = w[i][(l + ((qi & 1) ? 32 : 0)) >> 2];
+          const uint32_t qhw = w[i][16 + (l >> 2)];
+          const uint32_t nib = (qi < 2) ? (qlw & 0x0F0F0F0Fu) : ((qlw >> 4) & 0x0F0F0F0Fu);
+          q[k] = nib | (((qhw >> (2 * qi)) & 0x03030303u) << 4);
         }
-        const int xsum = (int)rec[12];
-        const int e = (int)rec[13];
+        int t = 0;
 #pragma unroll
-        for (int i = 0; i < RPW; i++) {
-          uint32_t q[4];
+        for (int d = 2; d >= 0; d--) {
+          if (d < 2) t <<= 8;
 #pragma unroll
-          for (int k = 0; k < 4; k++) {
-            const int l = 16 * lb + 4 * k;
-            const uint32_t qlw = w[i][(64 * h + l + ((qi & 1) ? 32 : 0)) >> 2];
-            const uint32_t qhw = w[i][(128 + 32 * h + l) >> 2];
-            const uint32_t nib = (qi < 2) ? (qlw & 0x0F0F0F0Fu) : ((qlw >> 4) & 0x0F0F0F0Fu);
-            q[k] = nib | (((qhw >> (2 * qi)) & 0x03030303u) << 4);
-          }
-          int t = 0;
-#pragma unroll
-          for (int d = 2; d >= 0; d--) {
-            if (d < 2) t <<= 8;
-#pragma unroll
-            for (int k = 0; k < 4; k++) t = __builtin_amdgcn_sdot4((int)q[k], (int)D[d][k], t, false);
-          }
-          const int8_t scv = (int8_t)((w[i][(192 + g) >> 2] >> (8 * ((192 + g) & 3))) & 0xFF);
-          part[i] += ldexpf((float)(t - 32 * xsum) * (float)scv, -e);
+          for (int k = 0; k < 4; k++) t = __builtin_amdgcn_sdot4((int)q[k], (int)D[d][k], t, false);
         }
+        const int8_t scv = (int8_t)((w[i][24 + (g >> 2)] >> (8 * (g & 3))) & 0xFF);
+        part[i] += ldexpf((float)(t - 32 * xsum) * (float)scv, -e);
       }
     }
   }
 #pragma unroll
-  for (int i = 0; i < RPW; i++) acc[i] += cn_h2f(w[i][52]) * part[i];
+  for (int i = 0; i < RPW; i++) acc[i] += cn_h2f(w[i][26]) * part[i];
 }
 
 // Q8_0 pair of blocks (DequantQ8_0.cs:51-90): block A is unit bytes 0..33 (d,
@@ -609,32 +623,15 @@ __device__ __forceinline__ void dot_unit_q8_0(const uint32_t (*w)[17], const flo
 // 8b) above the nibbles.  With t_g = sum_j q_j X_j (exact, |.| <= 16*31*2^18)
 // the group contributes 2^-e_g (d sc_s t_g - dmin m_s SX_g).
 template <int QT, int RPW>
-__device__ __forceinline__ void dot_unit_k45_dig8(const uint32_t (*w)[QTraits<QT>::NDW], const uint32_t* xd,
+__device__ __forceinline__ void dot_unit_k45_dig8(const uint32_t (*w)[QTraits<QT>::NDW], const uint32_t* xd, int h,
                                                   float* acc) {
-  constexpr int QS = QT == QT_Q5_K ? 12 : 4;  // first qs dword of the super-block
-  float dsc[RPW][8], dmm[RPW][8];
+  constexpr int QS = QT == QT_Q5_K ? 8 : 4;  // first qs dword of the half
+  float dsc[RPW][4], dmm[RPW][4];
 #pragma unroll
-  for (int i = 0; i < RPW; i++) {
-    const float d = cn_h2f(w[i][0]), dmin = cn_h2f(w[i][0] >> 16);
-    const uint32_t q0 = w[i][1], q1 = w[i][2], q2 = w[i][3];  // scale bytes 0..11
+  for (int i = 0; i < RPW; i++) k4_scales_half(w[i], h, dsc[i], dmm[i]);
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      int sc, m;
-      if (j < 4) {
-        sc = (q0 >> (8 * j)) & 63;
-        m = (q1 >> (8 * j)) & 63;
-      } else {
-        const uint32_t b8 = (q2 >> (8 * (j - 4))) & 0xFF;
-        sc = (b8 & 0xF) | (((q0 >> (8 * (j - 4) + 6)) & 3) << 4);
-        m = (b8 >> 4) | (((q1 >> (8 * (j - 4) + 6)) & 3) << 4);
-      }
-      dsc[i][j] = d * (float)sc;
-      dmm[i][j] = dmin * (float)m;
-    }
-  }
-#pragma unroll
-  for (int g = 0; g < 16; g++) {
-    const int sb = g >> 1, hh = g & 1;
+  for (int g = 0; g < 8; g++) {
+    const int sb = g >> 1, hh = g & 1;  // local sub-block, low / high nibbles
     const uint32_t* rec = xd + 16 * g;
     uint32_t D[3][4];
 #pragma unroll
@@ -859,9 +856,9 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
 
   // ---- prologue: stage x (optionally RMS-normalised) into LDS ----
   // Integer digit paths: base-16 digits on v_dot8_i32_i4 for Q4_0 and for Q4_K
-  // up to K = 8192 (the register budget of the staged x at 32 items per
-  // super-block lane); base-256 digits on v_dot4_i32_i8 for Q6_K, Q5_K and the
-  // longer Q4_K rows.  Q8_0 runs the fp32 dot below.
+  // up to K = 4096 (the register budget of the staged x at 16 items per
+  // half-super-block lane); base-256 digits on v_dot4_i32_i8 for Q6_K, Q5_K and
+  // the longer Q4_K rows.  Q8_0 runs the fp32 dot below.
   constexpr bool kDig8 = QT == QT_Q6_K || QT == QT_Q5_K || (QT == QT_Q4_K && LPR > 32);
   constexpr bool kDigits = QT != QT_Q8_0;
   if constexpr (kDigits) {
@@ -869,8 +866,8 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
     uint32_t* xd = reinterpret_cast<uint32_t*>(smem);
     float* xred;
     if constexpr (kDig8) {
-      // groups per thread: K <= 256 * LPR * NU, so K/16 <= 16 * LPR * NU groups over BS threads
-      constexpr int MAXT = (16 * LPR * NU + BS - 1) / BS;
+      // groups per thread: K <= UNIT * LPR * NU, so K/16 <= (UNIT/16) * LPR * NU groups over BS threads
+      constexpr int MAXT = ((UNIT / 16) * LPR * NU + BS - 1) / BS;
       XStage16<MAXT, NORM> st;
       stage_load16<MAXT, NORM, BS>(a.x, a.norm_w, K, st);
       issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
@@ -908,8 +905,8 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
             for (int k = 0; k < T::NDW; k++) wu[i][k] = w[i][n][k];
           if constexpr (QT == QT_Q4_0) dot_unit_q4_0_dig<RPW>(wu, xd + u * XD_UNIT_DW, acc);
           else if constexpr (QT == QT_Q6_K) dot_unit_q6_k_dig<RPW>(wu, xd + u * XD6_UNIT_DW, acc);
-          else if constexpr (kDig8) dot_unit_k45_dig8<QT, RPW>(wu, xd + u * XD6_UNIT_DW, acc);
-          else dot_unit_q4_k_dig<RPW>(wu, xd + 4 * u * XD_UNIT_DW, acc);
+          else if constexpr (kDig8) dot_unit_k45_dig8<QT, RPW>(wu, xd + u * XD6_UNIT_DW, u & 1, acc);
+          else dot_unit_q4_k_dig<RPW>(wu, xd + 2 * u * XD_UNIT_DW, u & 1, acc);
         }
       }
       const int cur = it;
@@ -1002,7 +999,7 @@ template <int QT>
 size_t gemv_smem_bytes(int K) {
   using T = QTraits<QT>;
   const int nunits = K / T::UNIT;
-  // digit records (Q4_0; Q4_K up to 32 super-blocks per row) + one float per wave
+  // digit records (Q4_0; Q4_K up to 32 half super-blocks per row) + one float per wave
   if (QT == QT_Q4_0 || (QT == QT_Q4_K && nunits <= 32)) return ((size_t)(K >> 6) * XD_UNIT_DW + 16) * sizeof(uint32_t);
   if (QT == QT_Q6_K || QT == QT_Q5_K || QT == QT_Q4_K) return ((size_t)nunits * XD6_UNIT_DW + 16) * sizeof(uint32_t);
   size_t f = (size_t)nunits * (T::UNIT + 4) + (K >> 5) + 4;
@@ -1063,10 +1060,10 @@ GemvShape pick_shape(int K, int n_vrows, int num_cus, bool allow8, bool isolated
         break;
       }
     }
-  } else {
-    s.nu = 1;
+  } else {  // K-quants: half super-blocks, up to 128 per row (K <= 16384)
     s.rpw = 2;
     s.lpr = nunits <= 16 ? 16 : (nunits <= 32 ? 32 : 64);
+    s.nu = (nunits + s.lpr - 1) / s.lpr;
   }
   if (QT == QT_Q4_0) {
     // Launches that reach 16 waves per CU at two rows per lane run that way, in
@@ -1099,7 +1096,10 @@ GemvShape pick_shape(int K, int n_vrows, int num_cus, bool allow8, bool isolated
     s.bs = 512;
     s.grid = (waves + 7) / 8;
   }
-  if (s.grid > 2 * num_cus) s.grid = 2 * num_cus;
+  // one-unit Q6_K lanes (<= 128 VGPRs) run best at four 256-thread workgroups
+  // per CU (32000x4096 29.2 -> 28.0 us); Q4_K and Q5_K at two
+  const int per_cu = QT == QT_Q6_K && s.nu == 1 ? 4 : 2;
+  if (s.grid > per_cu * num_cus) s.grid = per_cu * num_cus;
   if (s.grid < 1) s.grid = 1;
   return s;
 }
@@ -1150,7 +1150,8 @@ hipError_t launch_qt(const GemvArgs& a, int num_cus, hipStream_t st) {
     if (s.nu == 3) return launch_k<QT, 2, 3, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
     return launch_k<QT, 2, 4, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
   } else {
-    return launch_k<QT, 2, 1, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
+    if (s.nu == 1) return launch_k<QT, 2, 1, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
+    return launch_k<QT, 2, 2, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
   }
 }
 
