@@ -56,6 +56,11 @@ __device__ __forceinline__ float st_sum(float v, float* red) {
 // touches its own elements, so no barrier is needed between the passes.
 constexpr int kRegPerThread = 32;
 
+// The unroll pragmas below keep rv[] in registers for REG (32 iterations known
+// at compile time); in the scratch-array form the trip count is a run-time
+// value and clang reports that it could not unroll, which is expected there.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Wpass-failed"
 template <bool REG>
 __global__ __launch_bounds__(kST) void sample_kernel(const float* __restrict__ logits, int n,
                                                      const SampleParams* __restrict__ prm,
@@ -277,6 +282,7 @@ __global__ __launch_bounds__(kST) void sample_kernel(const float* __restrict__ l
     state[0] = state[0] + 1;
   }
 }
+#pragma clang diagnostic pop
 
 }  // namespace
 
