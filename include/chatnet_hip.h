@@ -199,7 +199,7 @@ CHATNET_API int chatnet_get_logits(chatnet_model* m, float* logits_host);
  * W is M rows of raw GGUF blocks (row stride K/block*bytes_per_block), x is
  * N x K fp32 row-major, y is N x M fp32 row-major.  Types Q4_0, Q8_0 and K %
  * 64 == 0, or Q4_K, Q5_K, Q6_K and K % 256 == 0, with K <= 16384.  N >= 8 with
- * Q4_0 runs the dequant-to-LDS bf16 MFMA GEMM (bf16 x, ~1e-3 normwise); any
+ * Q4_0 runs the dequant-to-LDS bf16 MFMA GEMM (x rounded to bf16); any
  * other call runs the fused dequant-GEMV once per column.  The GEMM's
  * workspace is allocated on first use per (device, stream) and kept.
  * `stream` is a hipStream_t (NULL = default stream).  Asynchronous on
