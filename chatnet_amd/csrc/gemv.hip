@@ -56,12 +56,6 @@ template <> struct QTraits<QT_Q5_K> {
   static constexpr int BLOCK_BYTES = 176, BLOCK = 256;
 };
 
-// LDS index of x[k] for a given unit size (4 floats of padding per unit).
-template <int UNIT>
-__device__ __forceinline__ int xidx(int k) {
-  return k + (k / UNIT) * 4;
-}
-
 // ---------------------------------------------------------------------------
 // Q4_0 inputs as signed 4-bit digits.
 //
@@ -581,33 +575,40 @@ __device__ __forceinline__ void dot_unit_q6_k_dig(const uint32_t (*w)[27], const
   for (int i = 0; i < RPW; i++) acc[i] += cn_h2f(w[i][26]) * part[i];
 }
 
-// Q8_0 pair of blocks (DequantQ8_0.cs:51-90): block A is unit bytes 0..33 (d,
-// then 32 int8), block B bytes 34..67.  The int8s are read as the unsigned
-// bytes q + 128 (q ^ 0x80) and 128 times the block's x sum is taken off.
+// Q8_0 pair of blocks (DequantQ8_0.cs:51-90) against the base-256 digit
+// records of its four 16-element groups: block A is unit bytes 0..33 (d, then
+// 32 int8; its qs realigned with alignbyte), block B bytes 34..67 (d in the
+// high half of dword 8, qs in dwords 9..16).  The int8 weights meet the x
+// digits directly on v_dot4_i32_i8: t_g = sum_j q_j X_j is exact
+// (|.| <= 16 * 128 * 2^18) and the group contributes d * 2^-e_g * t_g.
 template <int RPW>
-__device__ __forceinline__ void dot_unit_q8_0(const uint32_t (*w)[17], const float* xs, const float* sx,
-                                              float* acc) {
+__device__ __forceinline__ void dot_unit_q8_0_dig8(const uint32_t (*w)[17], const uint32_t* xd, float* acc) {
 #pragma unroll
-  for (int b = 0; b < 2; b++) {
-    float xv[32];
+  for (int g = 0; g < 4; g++) {
+    const int b = g >> 1;
+    const uint32_t* rec = xd + 16 * g;
+    uint32_t D[3][4];
 #pragma unroll
-    for (int c = 0; c < 8; c++) {
-      const float4 t = *reinterpret_cast<const float4*>(xs + 32 * b + 4 * c);
-      xv[4 * c + 0] = t.x; xv[4 * c + 1] = t.y; xv[4 * c + 2] = t.z; xv[4 * c + 3] = t.w;
+    for (int d = 0; d < 3; d++) {
+      const uint4 t = *reinterpret_cast<const uint4*>(rec + 4 * d);
+      D[d][0] = t.x; D[d][1] = t.y; D[d][2] = t.z; D[d][3] = t.w;
     }
-    const float xsum = sx[b];
+    const int e = (int)rec[13];
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
-      const float d = b == 0 ? cn_h2f(w[i][0]) : cn_h2f(w[i][8] >> 16);
-      float s = 0.f;
+      int t = 0;
 #pragma unroll
-      for (int k = 0; k < 8; k++) {
-        const uint32_t q =
-            (b == 0 ? __builtin_amdgcn_alignbyte(w[i][k + 1], w[i][k], 2) : w[i][9 + k]) ^ 0x80808080u;
-        s += cn_ubyte<0>(q) * xv[4 * k] + cn_ubyte<1>(q) * xv[4 * k + 1] + cn_ubyte<2>(q) * xv[4 * k + 2] +
-             cn_ubyte<3>(q) * xv[4 * k + 3];
+      for (int dg = 2; dg >= 0; dg--) {
+        if (dg < 2) t <<= 8;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const int kk = 4 * (g & 1) + k;  // qs dword of the block
+          const uint32_t q = b == 0 ? __builtin_amdgcn_alignbyte(w[i][kk + 1], w[i][kk], 2) : w[i][9 + kk];
+          t = __builtin_amdgcn_sdot4((int)q, (int)D[dg][k], t, false);
+        }
       }
-      acc[i] += d * (s - 128.f * xsum);
+      const float d = b == 0 ? cn_h2f(w[i][0]) : cn_h2f(w[i][8] >> 16);
+      acc[i] += d * ldexpf((float)t, -e);
     }
   }
 }
@@ -838,9 +839,6 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
   extern __shared__ float smem[];
   const int K = a.K;
   const int nunits = K / UNIT;
-  float* xs = smem;                      // fp32 path: nunits*(UNIT+4)
-  float* sx = xs + nunits * (UNIT + 4);  // K/32 block sums
-  float* red = sx + (K >> 5);            // 4 floats
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane / LPR, li = lane % LPR;
@@ -857,11 +855,10 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
   // ---- prologue: stage x (optionally RMS-normalised) into LDS ----
   // Integer digit paths: base-16 digits on v_dot8_i32_i4 for Q4_0 and for Q4_K
   // up to K = 4096 (the register budget of the staged x at 16 items per
-  // half-super-block lane); base-256 digits on v_dot4_i32_i8 for Q6_K, Q5_K and
-  // the longer Q4_K rows.  Q8_0 runs the fp32 dot below.
-  constexpr bool kDig8 = QT == QT_Q6_K || QT == QT_Q5_K || (QT == QT_Q4_K && LPR > 32);
-  constexpr bool kDigits = QT != QT_Q8_0;
-  if constexpr (kDigits) {
+  // half-super-block lane); base-256 digits on v_dot4_i32_i8 for Q8_0, Q6_K,
+  // Q5_K and the longer Q4_K rows.
+  constexpr bool kDig8 = QT == QT_Q8_0 || QT == QT_Q6_K || QT == QT_Q5_K || (QT == QT_Q4_K && LPR > 32);
+  {
     constexpr bool NORM = EPI == GEMV_EPI_QKV || EPI == GEMV_EPI_SWIGLU || EPI == GEMV_EPI_LOGITS;
     uint32_t* xd = reinterpret_cast<uint32_t*>(smem);
     float* xred;
@@ -872,7 +869,7 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
       stage_load16<MAXT, NORM, BS>(a.x, a.norm_w, K, st);
       issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
       load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, pos, res);
-      xred = reinterpret_cast<float*>(smem) + (size_t)nunits * XD6_UNIT_DW;
+      xred = reinterpret_cast<float*>(smem) + (size_t)((K + 127) >> 7) * XD6_UNIT_DW;
       stage_digitize16<MAXT, NORM, BS>(st, K, xd, xred);
     } else {
       // items per thread: K <= UNIT * LPR * NU, so K/8 <= (UNIT/8) * LPR * NU items over BS threads
@@ -904,6 +901,7 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
 #pragma unroll
             for (int k = 0; k < T::NDW; k++) wu[i][k] = w[i][n][k];
           if constexpr (QT == QT_Q4_0) dot_unit_q4_0_dig<RPW>(wu, xd + u * XD_UNIT_DW, acc);
+          else if constexpr (QT == QT_Q8_0) dot_unit_q8_0_dig8<RPW>(wu, xd + (u >> 1) * XD6_UNIT_DW + 64 * (u & 1), acc);
           else if constexpr (QT == QT_Q6_K) dot_unit_q6_k_dig<RPW>(wu, xd + u * XD6_UNIT_DW, acc);
           else if constexpr (kDig8) dot_unit_k45_dig8<QT, RPW>(wu, xd + u * XD6_UNIT_DW, u & 1, acc);
           else dot_unit_q4_k_dig<RPW>(wu, xd + 2 * u * XD_UNIT_DW, u & 1, acc);
@@ -926,72 +924,6 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
       }
       if (li == 0) epilogue<EPI, RPW>(a, cur * RW + sub * RPW, acc, res_cur, pos);
     }
-  } else {
-  if (it < n_iters) {
-    issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
-    load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, pos, res);
-  }
-  float rms = 1.0f;
-  if (a.norm_w) {
-    float ss = 0.f;
-    for (int k = threadIdx.x * 4; k < K; k += CN_BLOCK * 4) {
-      const float4 t = *reinterpret_cast<const float4*>(a.x + k);
-      ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
-    }
-    ss = cn_block_sum(ss, red);
-    rms = 1.0f / sqrtf(ss / (float)K + a.eps);  // TensorMath.cs:142
-  }
-  for (int k = threadIdx.x * 4; k < K; k += CN_BLOCK * 4) {
-    float4 t = *reinterpret_cast<const float4*>(a.x + k);
-    if (a.norm_w) {
-      const float4 g = *reinterpret_cast<const float4*>(a.norm_w + k);
-      t.x = t.x * rms * g.x; t.y = t.y * rms * g.y; t.z = t.z * rms * g.z; t.w = t.w * rms * g.w;
-    }
-    *reinterpret_cast<float4*>(xs + xidx<UNIT>(k)) = t;
-  }
-  __syncthreads();
-  for (int b = threadIdx.x; b < (K >> 5); b += CN_BLOCK) {
-    const float* p = xs + xidx<UNIT>(b * 32);
-    float s = 0.f;
-#pragma unroll
-    for (int j = 0; j < 32; j++) s += p[j];
-    sx[b] = s;
-  }
-  __syncthreads();
-
-  // ---- main loop ----
-  while (it < n_iters) {
-    float acc[RPW];
-#pragma unroll
-    for (int i = 0; i < RPW; i++) acc[i] = 0.f;
-#pragma unroll
-    for (int n = 0; n < NU; n++) {
-      const int u = li + LPR * n;
-      if (u < nunits) {
-        uint32_t wu[RPW][T::NDW];
-#pragma unroll
-        for (int i = 0; i < RPW; i++)
-#pragma unroll
-          for (int k = 0; k < T::NDW; k++) wu[i][k] = w[i][n][k];
-        dot_unit_q8_0<RPW>(wu, xs + u * (UNIT + 4), sx + u * (UNIT / 32), acc);
-      }
-    }
-    const int cur = it;
-    float res_cur[NR];
-#pragma unroll
-    for (int i = 0; i < NR; i++) res_cur[i] = res[i];
-    it += wstride;
-    if (it < n_iters) {
-      issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
-      load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, pos, res);
-    }
-#pragma unroll
-    for (int i = 0; i < RPW; i++) {
-#pragma unroll
-      for (int off = LPR / 2; off > 0; off >>= 1) acc[i] += __shfl_xor(acc[i], off, CN_WAVE);
-    }
-    if (li == 0) epilogue<EPI, RPW>(a, cur * RW + sub * RPW, acc, res_cur, pos);
-  }
   }
 }
 
@@ -999,11 +931,10 @@ template <int QT>
 size_t gemv_smem_bytes(int K) {
   using T = QTraits<QT>;
   const int nunits = K / T::UNIT;
-  // digit records (Q4_0; Q4_K up to 32 half super-blocks per row) + one float per wave
+  // digit records (base 16: Q4_0, Q4_K up to 32 half super-blocks per row;
+  // base 256 per 128 elements otherwise) + one float per wave
   if (QT == QT_Q4_0 || (QT == QT_Q4_K && nunits <= 32)) return ((size_t)(K >> 6) * XD_UNIT_DW + 16) * sizeof(uint32_t);
-  if (QT == QT_Q6_K || QT == QT_Q5_K || QT == QT_Q4_K) return ((size_t)nunits * XD6_UNIT_DW + 16) * sizeof(uint32_t);
-  size_t f = (size_t)nunits * (T::UNIT + 4) + (K >> 5) + 4;
-  return f * sizeof(float);
+  return ((size_t)((K + 127) >> 7) * XD6_UNIT_DW + 16) * sizeof(uint32_t);
 }
 
 // Launch shape of one GEMV: lanes per row, units per lane, rows per lane,
