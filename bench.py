@@ -292,6 +292,7 @@ def main():
     prefill = None
     kq = None
     qwen = None
+    fp16kv = None
     if not args.roofline_only and not args.no_kquant:
         log("Q4_K / Q6_K / Q8_0 / Q5_K gemv (cold) and 7B Q4_K_M-style 64-token decode")
         kq = {"gemv_q4_k_cold": gemv_sweep(KQ4_SHAPES, qtype=12),
@@ -322,6 +323,9 @@ def main():
         value = args.steps / dt
         ms = dt * 1000.0 / args.steps
         log(f"  {value:.1f} tok/s ({ms:.3f} ms/token)")
+        dt16, _ = decode_run(cfg7.replace(kv_dtype=_native.KV_F16), ck7, prompt, args.steps, args.warmup)
+        fp16kv = round(args.steps / dt16, 1)
+        log(f"  fp16 KV cache: {fp16kv} tok/s")
         if not args.no_cpu:
             log("cpu baseline (oracle on host cores)")
             cpu = cpu_baseline(cfg7, ck7)
@@ -364,6 +368,7 @@ def main():
         "data": "synthetic (seeded N(0,0.02) weights quantized to Q4_0, seeded prompt ids)",
         "config": {"workload": "llama2-7b-q4_0-decode-bs1", "prompt_tokens": 128, "decode_tokens": args.steps,
                    "kv_cache": "f32", "context_length": 2048, "weights": "Q4_0 (all matrices)",
+                   "llama2_7b_q4_0_fp16_kv_decode_tok_s": fp16kv,
                    "tinyllama_1b_q4_0_decode_tok_s": tiny,
                    "tinyllama_1b_q4_0_sampled_decode_tok_s": tiny_sampled},
         "gemv_sweep_q4_0_n1_cold": sweep,
