@@ -3,21 +3,25 @@
 // Replaces TensorMath.MatVecMulQ4_0 / MatVecMulQ6K / MatVecMulGeneric
 // (src/ChatNet.Core/Tensors/TensorMath.cs:548-656) and the fused row dots
 // DequantQ4_0.DotProduct (DequantQ4_0.cs:80-149), DequantQ4K.DotProduct
-// (DequantQ4K.cs:89-163) and DequantQ6K.DotProduct (DequantQ6K.cs:104-188).
+// (DequantQ4K.cs:89-163), DequantQ6K.DotProduct (DequantQ6K.cs:104-188),
+// DequantQ8_0.DotProduct and DequantQ5K.DotProduct.
 //
 // Weights stay in their raw GGUF block layout in HBM.  One lane owns one
-// "unit" of a row — two Q4_0 blocks (64 weights, 36 B, dword aligned), or one
-// Q4_K super-block (256 weights, 144 B), or one Q6_K super-block (256 weights,
-// 210 B, realigned in registers) — and LPR lanes cover a row, so a wave reads
-// each row as one contiguous stretch.  Every lane works on RPW rows at once so
-// each x value it reads from LDS feeds RPW rows.  The input vector is staged
-// in LDS once per workgroup (with RMSNorm fused in when a norm weight is
-// given, TensorMath.RmsNorm TensorMath.cs:97-165), padded by 4 floats per unit
-// so the 16-byte LDS reads of neighbouring lanes hit distinct banks.
-// Products are fp32 (exact nibble -> float conversion), sums fp32; the
-// per-block offset (q-8 for Q4_0, dmin*m for Q4_K, q-32 for Q6_K) is applied
-// once per block through precomputed block sums of x.  Partial row sums are
-// reduced across the LPR lanes with cross-lane shuffles.
+// "unit" of a row — two Q4_0 or Q8_0 blocks (64 weights, 36 / 68 B, dword
+// aligned), or half a Q4_K / Q5_K / Q6_K super-block (128 weights plus the
+// header or scales it needs; Q6_K realigned in registers) — and LPR lanes
+// cover a row, so a wave reads each row as one contiguous stretch.  Every lane
+// works on RPW rows at once so each x value it reads from LDS feeds RPW rows.
+// The input vector is staged in LDS once per workgroup as integer digits (with
+// RMSNorm's weight fused in when one is given, TensorMath.RmsNorm
+// TensorMath.cs:97-165; the 1/rms factor is applied to the finished sums):
+// x is scaled by a power of two per 32- or 16-element group to 19 significant
+// bits and split into base-16 digits (Q4_0, short Q4_K rows: signed weight
+// nibbles on v_dot8_i32_i4) or base-256 digits (Q8_0, Q5_K, Q6_K, long Q4_K
+// rows: weight bytes on v_dot4_i32_i8).  Each group's dot is exact in int32;
+// the per-group scales, offsets (q-8, q-32, dmin*m) and 2^-e are applied in
+// fp32 once per group.  Partial row sums are reduced across the LPR lanes with
+// cross-lane shuffles.
 //
 // Epilogues (fused into the lane that finishes a row pair):
 //   STORE   y[r]  = dot                          (LM head, matmul API)
