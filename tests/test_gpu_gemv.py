@@ -62,6 +62,10 @@ def test_generic_type_gemv_shapes(qtype, M, K):
     (13, 1, 256), (13, 9, 768), (13, 40, 2816),
     (12, 1, 256), (12, 5, 768), (12, 31, 11008),
     (14, 1, 256), (14, 9, 768), (14, 18, 1280),   # 768/1280: rows start 2 bytes off a dword
+    # half super-blocks per lane: 44 per row (one per lane, base-256 digits for
+    # Q4_K too) and 128 per row (K = 16384, two per lane)
+    (12, 7, 5632), (13, 7, 5632), (14, 7, 5632),
+    (12, 3, 16384), (13, 3, 16384), (14, 3, 16384), (8, 9, 16320),
 ])
 def test_ragged_and_misaligned_shapes(qtype, M, K):
     run_case(qtype, M, K, seed=5)
