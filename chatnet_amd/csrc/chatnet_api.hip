@@ -595,6 +595,8 @@ int launch_token(chatnet_model* m, bool lm_head, int cap) {
     at.chunk = plan.chunk;
     at.part_o = m->attn_part_o;
     at.part_ml = m->attn_part_ml;
+    // a few chunks are combined by the O GEMV as it stages x (no merge launch)
+    at.fold = plan.splits > 1 && plan.splits <= kFoldMaxSplits;
     HIP_TRY(attn_decode_launch(at, st));
 
     GemvArgs o = base_args(m);
@@ -604,7 +606,13 @@ int launch_token(chatnet_model* m, bool lm_head, int cap) {
     o.seg_rows[0] = c.dim;
     o.n_vrows = c.dim;
     o.out[0] = m->x;
-    HIP_TRY(gemv_launch((int)L.wo.type, GEMV_EPI_ADD, o, m->num_cus, st));
+    if (at.fold) {
+      o.part_o = m->attn_part_o;
+      o.part_ml = m->attn_part_ml;
+      o.msplits = plan.splits;
+      o.mchunk = plan.chunk;
+    }
+    HIP_TRY(gemv_launch((int)L.wo.type, at.fold ? GEMV_EPI_ADD_MERGE : GEMV_EPI_ADD, o, m->num_cus, st));
 
     if (L.wg.type != L.wu.type)
       return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "layer %d: ffn_gate and ffn_up types differ", l);

@@ -441,7 +441,7 @@ hipError_t attn_launch_t(const AttnArgs& a, hipStream_t st) {
   if (hpw == 1) attn_launch_k<HD, F16, 1>(a, st);
   else if (hpw == 2 || HD > 128) attn_launch_k<HD, F16, 2>(a, st);
   else attn_launch_k<HD, F16, 4>(a, st);
-  if (a.splits > 1) hipLaunchKernelGGL((attn_merge_kernel<HD>), dim3(a.n_heads), dim3(CN_BLOCK), 0, st, a);
+  if (a.splits > 1 && !a.fold) hipLaunchKernelGGL((attn_merge_kernel<HD>), dim3(a.n_heads), dim3(CN_BLOCK), 0, st, a);
   return hipGetLastError();
 }
 

@@ -88,6 +88,59 @@ constexpr int XD_UNIT_DW = 44;
 // XOR 8 turns each into D_d = E_d - 8 as a signed nibble.  Valid for
 // X in [-0x88888, 0x77777], which |X| <= 2^18 satisfies.
 
+// x read from the decode attention's per-chunk partials (ADD_MERGE): element
+// i belongs to head i / hd; each active chunk c (c < s_eff) holds the running
+// max M_c, sum L_c and unnormalised output O_c of its positions, and
+//   x = sum_c O_c e^(M_c - M) / sum_c L_c e^(M_c - M),  M = max_c M_c
+// (attn_merge_kernel's combination).  Every chunk's loads are issued (their
+// addresses do not depend on the position); inactive ones are masked.
+struct MergeSrc {
+  const float* o;
+  const float* ml;
+  int hd, splits, s_eff;
+};
+
+__device__ __forceinline__ float4 merged_x4(const MergeSrc& m, int i) {
+  const int h = i / m.hd, d = i - h * m.hd;
+  const size_t base = (size_t)h * m.splits;
+  float mc[kFoldMaxSplits], lc[kFoldMaxSplits];
+  float4 oc[kFoldMaxSplits];
+  float M = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < kFoldMaxSplits; c++) {
+    const bool in = c < m.splits;
+    const float mr = in ? m.ml[2 * (base + c)] : 0.f;
+    const float lr = in ? m.ml[2 * (base + c) + 1] : 0.f;
+    const float4 orr = in ? *reinterpret_cast<const float4*>(m.o + (base + c) * m.hd + d)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+    const bool on = c < m.s_eff;
+    mc[c] = mr;
+    lc[c] = on ? lr : 0.f;
+    oc[c] = orr;
+    if (lc[c] > 0.f) M = fmaxf(M, mr);
+  }
+  float L = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int c = 0; c < kFoldMaxSplits; c++) {
+    if (lc[c] > 0.f) {
+      const float f = expf(mc[c] - M);
+      L += lc[c] * f;
+      acc.x += oc[c].x * f;
+      acc.y += oc[c].y * f;
+      acc.z += oc[c].z * f;
+      acc.w += oc[c].w * f;
+    }
+  }
+  return make_float4(acc.x / L, acc.y / L, acc.z / L, acc.w / L);
+}
+
+template <bool MERGE>
+__device__ __forceinline__ float4 load_x4(const float* __restrict__ x, const MergeSrc& m, int i) {
+  if constexpr (MERGE) return merged_x4(m, i);
+  else return *reinterpret_cast<const float4*>(x + i);
+}
+
 // x (and the RMSNorm weight) of the MAXT work items a thread stages.
 // Work item t = (block t/4, dword k = t%4) holds x[32b+4k..+3] and
 // x[32b+16+4k..+3]; thread i owns items i, i+256, ...
@@ -105,9 +158,9 @@ struct XStage<MAXT, false> {
 // loads: vector-memory counters retire in order, so loads issued after the
 // weight stream could not be consumed before the whole stream had landed.
 // BS threads stage the K/8 items, item t on thread t % BS.
-template <int MAXT, bool NORM, int BS>
+template <int MAXT, bool NORM, int BS, bool MERGE = false>
 __device__ __forceinline__ void stage_load(const float* __restrict__ x, const float* __restrict__ norm_w, int K,
-                                           XStage<MAXT, NORM>& st) {
+                                           XStage<MAXT, NORM>& st, const MergeSrc& ms = MergeSrc{}) {
   const int ntask = K >> 3;
 #pragma unroll
   for (int j = 0; j < MAXT; j++) {
@@ -115,8 +168,8 @@ __device__ __forceinline__ void stage_load(const float* __restrict__ x, const fl
     const int b = t >> 2, k = t & 3;
     float4 lo = make_float4(0.f, 0.f, 0.f, 0.f), hi = lo, glo = lo, ghi = lo;
     if (t < ntask) {
-      lo = *reinterpret_cast<const float4*>(x + 32 * b + 4 * k);
-      hi = *reinterpret_cast<const float4*>(x + 32 * b + 16 + 4 * k);
+      lo = load_x4<MERGE>(x, ms, 32 * b + 4 * k);
+      hi = load_x4<MERGE>(x, ms, 32 * b + 16 + 4 * k);
       if constexpr (NORM) {
         glo = *reinterpret_cast<const float4*>(norm_w + 32 * b + 4 * k);
         ghi = *reinterpret_cast<const float4*>(norm_w + 32 * b + 16 + 4 * k);
@@ -249,9 +302,9 @@ struct XStage16<MAXT, false> {
 
 // Group t of x (and of the RMSNorm weight) on thread t % BS, loads issued
 // before the caller's weight loads (see stage_load).
-template <int MAXT, bool NORM, int BS>
+template <int MAXT, bool NORM, int BS, bool MERGE = false>
 __device__ __forceinline__ void stage_load16(const float* __restrict__ x, const float* __restrict__ norm_w, int K,
-                                             XStage16<MAXT, NORM>& st) {
+                                             XStage16<MAXT, NORM>& st, const MergeSrc& ms = MergeSrc{}) {
   const int ngroups = K >> 4;
 #pragma unroll
   for (int j = 0; j < MAXT; j++) {
@@ -260,7 +313,7 @@ __device__ __forceinline__ void stage_load16(const float* __restrict__ x, const 
     for (int c = 0; c < 4; c++) {
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f), g = v;
       if (t < ngroups) {
-        v = *reinterpret_cast<const float4*>(x + 16 * t + 4 * c);
+        v = load_x4<MERGE>(x, ms, 16 * t + 4 * c);
         if constexpr (NORM) g = *reinterpret_cast<const float4*>(norm_w + 16 * t + 4 * c);
       }
       st.x[j][4 * c + 0] = v.x; st.x[j][4 * c + 1] = v.y; st.x[j][4 * c + 2] = v.z; st.x[j][4 * c + 3] = v.w;
@@ -718,7 +771,7 @@ __device__ __forceinline__ void load_residual(const GemvArgs& a, int vr0, int li
 #pragma unroll
   for (int i = 0; i < NR; i++) res[i] = 0.f;
   if (li != 0) return;
-  if constexpr (EPI == GEMV_EPI_ADD) {
+  if constexpr (EPI == GEMV_EPI_ADD || EPI == GEMV_EPI_ADD_MERGE) {
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
       const int vr = vr0 + i;
@@ -757,7 +810,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, const float
     if constexpr (EPI == GEMV_EPI_STORE || EPI == GEMV_EPI_LOGITS) {
       a.out[0][r] = v[i];
       if (vr + 1 < a.n_vrows) a.out[0][r + 1] = v[i + 1];
-    } else if constexpr (EPI == GEMV_EPI_ADD) {
+    } else if constexpr (EPI == GEMV_EPI_ADD || EPI == GEMV_EPI_ADD_MERGE) {
       a.out[0][r] = res[i] + v[i];
       if (vr + 1 < a.n_vrows) a.out[0][r + 1] = res[i + 1] + v[i + 1];
     } else if constexpr (EPI == GEMV_EPI_SWIGLU) {
@@ -855,6 +908,15 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
   constexpr int NR = res_count<EPI, RPW>();
   float res[NR];
   const int pos = EPI == GEMV_EPI_QKV ? *a.pos : 0;
+  constexpr bool MERGE = EPI == GEMV_EPI_ADD_MERGE;
+  MergeSrc ms{};
+  if constexpr (MERGE) {
+    ms.o = a.part_o;
+    ms.ml = a.part_ml;
+    ms.hd = a.head_dim;
+    ms.splits = a.msplits;
+    ms.s_eff = min(a.msplits, (*a.pos + a.mchunk) / a.mchunk);  // chunks below pos + 1
+  }
 
   // ---- prologue: stage x (optionally RMS-normalised) into LDS ----
   // Integer digit paths: base-16 digits on v_dot8_i32_i4 for Q4_0 and for Q4_K
@@ -870,7 +932,7 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
       // groups per thread: K <= UNIT * LPR * NU, so K/16 <= (UNIT/16) * LPR * NU groups over BS threads
       constexpr int MAXT = ((UNIT / 16) * LPR * NU + BS - 1) / BS;
       XStage16<MAXT, NORM> st;
-      stage_load16<MAXT, NORM, BS>(a.x, a.norm_w, K, st);
+      stage_load16<MAXT, NORM, BS, MERGE>(a.x, a.norm_w, K, st, ms);
       issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
       load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, pos, res);
       xred = reinterpret_cast<float*>(smem) + (size_t)((K + 127) >> 7) * XD6_UNIT_DW;
@@ -879,7 +941,7 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
       // items per thread: K <= UNIT * LPR * NU, so K/8 <= (UNIT/8) * LPR * NU items over BS threads
       constexpr int MAXT = ((UNIT / 8) * LPR * NU + BS - 1) / BS;
       XStage<MAXT, NORM> st;
-      stage_load<MAXT, NORM, BS>(a.x, a.norm_w, K, st);
+      stage_load<MAXT, NORM, BS, MERGE>(a.x, a.norm_w, K, st, ms);
       // rows past n_vrows come back as zeros, so idle waves need no branch here
       issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
       load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, pos, res);
@@ -1134,6 +1196,10 @@ hipError_t gemv_launch(int qtype, int epi, const GemvArgs& a, int num_cus, hipSt
     case GEMV_EPI_QKV: return launch_epi<GEMV_EPI_QKV>(qtype, a, num_cus, st);
     case GEMV_EPI_SWIGLU: return launch_epi<GEMV_EPI_SWIGLU>(qtype, a, num_cus, st);
     case GEMV_EPI_LOGITS: return launch_epi<GEMV_EPI_LOGITS>(qtype, a, num_cus, st);
+    case GEMV_EPI_ADD_MERGE:
+      if (a.msplits < 2 || a.msplits > kFoldMaxSplits || a.mchunk < 1 || a.head_dim % 32 != 0)
+        return hipErrorInvalidValue;
+      return launch_epi<GEMV_EPI_ADD_MERGE>(qtype, a, num_cus, st);
     default: return hipErrorInvalidValue;
   }
 }

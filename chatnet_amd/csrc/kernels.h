@@ -7,7 +7,12 @@
 
 // STORE and LOGITS write y = W x; LOGITS is the LM-head instance (a separate
 // kernel so its launches are told apart from stand-alone GEMVs in profiles).
-enum { GEMV_EPI_STORE = 0, GEMV_EPI_ADD = 1, GEMV_EPI_QKV = 2, GEMV_EPI_SWIGLU = 3, GEMV_EPI_LOGITS = 4 };
+// GEMV_EPI_ADD_MERGE: GEMV_EPI_ADD whose x is the decode attention's output,
+// combined from its per-chunk partials while it is staged (the O projection
+// of a position bucket with 2..kFoldMaxSplits chunks; no merge launch).
+enum { GEMV_EPI_STORE = 0, GEMV_EPI_ADD = 1, GEMV_EPI_QKV = 2, GEMV_EPI_SWIGLU = 3, GEMV_EPI_LOGITS = 4,
+       GEMV_EPI_ADD_MERGE = 5 };
+constexpr int kFoldMaxSplits = 8;
 
 // One fused GEMV launch over up to three weight segments of the same type.
 // Virtual rows: STORE/ADD use segment 0 only; QKV concatenates q|k|v rows;
@@ -30,6 +35,11 @@ struct GemvArgs {
   int kv_dim;
   int kv_f16;
   const float* bias;  // QKV: optional per-row bias added before RoPE, indexed by virtual row
+  // ADD_MERGE: attention partials [heads][msplits][head_dim] and (max, sum)
+  // pairs, chunks of mchunk positions of which those below *pos + 1 count
+  const float* part_o;
+  const float* part_ml;
+  int msplits, mchunk;
 };
 
 bool gemv_supports(int qtype, int K);
@@ -115,6 +125,7 @@ struct AttnArgs {
   float* part_ml;     // [n_heads][splits][2] (max, sum)
   int splits;         // position chunks of the launch (<= 64), one workgroup per kv head each
   int chunk;          // positions per chunk: chunk c covers [c*chunk, (c+1)*chunk) below pos+1
+  int fold;           // splits > 1: leave the partials for the O GEMV (GEMV_EPI_ADD_MERGE)
 };
 hipError_t attn_decode_launch(const AttnArgs& a, hipStream_t st);
 // Positions one decode-attention workgroup covers per round of wave steps.
