@@ -93,39 +93,39 @@ constexpr int XD_UNIT_DW = 44;
 // max M_c, sum L_c and unnormalised output O_c of its positions, and
 //   x = sum_c O_c e^(M_c - M) / sum_c L_c e^(M_c - M),  M = max_c M_c
 // (attn_merge_kernel's combination).  Every chunk's loads are issued (their
-// addresses do not depend on the position); inactive ones are masked.
+// addresses do not depend on the position); inactive ones are masked.  The
+// weights e^(M_c - M) and the sum depend on the head only: the base-256
+// staging (16-element groups of one head) computes them once per group.
 struct MergeSrc {
   const float* o;
   const float* ml;
   int hd, splits, s_eff;
 };
 
+// Elements i .. i+3 combined in one round trip: every chunk's (max, sum) and
+// outputs are loaded together, then folded.  Used by the base-16 staging,
+// whose items (two float4 of one head) gain nothing from sharing the weights.
 __device__ __forceinline__ float4 merged_x4(const MergeSrc& m, int i) {
   const int h = i / m.hd, d = i - h * m.hd;
   const size_t base = (size_t)h * m.splits;
-  float mc[kFoldMaxSplits], lc[kFoldMaxSplits];
+  float2 ml[kFoldMaxSplits];
   float4 oc[kFoldMaxSplits];
   float M = -INFINITY;
 #pragma unroll
   for (int c = 0; c < kFoldMaxSplits; c++) {
     const bool in = c < m.splits;
-    const float mr = in ? m.ml[2 * (base + c)] : 0.f;
-    const float lr = in ? m.ml[2 * (base + c) + 1] : 0.f;
-    const float4 orr = in ? *reinterpret_cast<const float4*>(m.o + (base + c) * m.hd + d)
-                          : make_float4(0.f, 0.f, 0.f, 0.f);
-    const bool on = c < m.s_eff;
-    mc[c] = mr;
-    lc[c] = on ? lr : 0.f;
-    oc[c] = orr;
-    if (lc[c] > 0.f) M = fmaxf(M, mr);
+    ml[c] = in ? *reinterpret_cast<const float2*>(m.ml + 2 * (base + c)) : make_float2(0.f, 0.f);
+    oc[c] = in ? *reinterpret_cast<const float4*>(m.o + (base + c) * m.hd + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (c >= m.s_eff) ml[c].y = 0.f;
+    if (ml[c].y > 0.f) M = fmaxf(M, ml[c].x);
   }
   float L = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int c = 0; c < kFoldMaxSplits; c++) {
-    if (lc[c] > 0.f) {
-      const float f = expf(mc[c] - M);
-      L += lc[c] * f;
+    if (ml[c].y > 0.f) {
+      const float f = expf(ml[c].x - M);
+      L += ml[c].y * f;
       acc.x += oc[c].x * f;
       acc.y += oc[c].y * f;
       acc.z += oc[c].z * f;
@@ -135,10 +135,48 @@ __device__ __forceinline__ float4 merged_x4(const MergeSrc& m, int i) {
   return make_float4(acc.x / L, acc.y / L, acc.z / L, acc.w / L);
 }
 
-template <bool MERGE>
-__device__ __forceinline__ float4 load_x4(const float* __restrict__ x, const MergeSrc& m, int i) {
-  if constexpr (MERGE) return merged_x4(m, i);
-  else return *reinterpret_cast<const float4*>(x + i);
+// Chunk weights of head h: f[c] = e^(M_c - M) for active chunks that hold
+// positions (0 otherwise) and their sum L = sum_c L_c f[c].
+struct MergeW {
+  float f[kFoldMaxSplits];
+  float L;
+};
+
+__device__ __forceinline__ MergeW merge_weights(const MergeSrc& m, int h) {
+  const size_t base = (size_t)h * m.splits;
+  float2 ml[kFoldMaxSplits];
+  float M = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < kFoldMaxSplits; c++) {
+    ml[c] = c < m.splits ? *reinterpret_cast<const float2*>(m.ml + 2 * (base + c)) : make_float2(0.f, 0.f);
+    if (c >= m.s_eff) ml[c].y = 0.f;
+    if (ml[c].y > 0.f) M = fmaxf(M, ml[c].x);
+  }
+  MergeW w;
+  w.L = 0.f;
+#pragma unroll
+  for (int c = 0; c < kFoldMaxSplits; c++) {
+    w.f[c] = ml[c].y > 0.f ? expf(ml[c].x - M) : 0.f;
+    w.L += ml[c].y * w.f[c];
+  }
+  return w;
+}
+
+// Elements d .. d+3 of head h combined with the chunk weights.
+__device__ __forceinline__ float4 merge_apply(const MergeSrc& m, const MergeW& w, int h, int d) {
+  const size_t base = (size_t)h * m.splits;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int c = 0; c < kFoldMaxSplits; c++) {
+    if (c < m.splits) {
+      const float4 o = *reinterpret_cast<const float4*>(m.o + (base + c) * m.hd + d);
+      acc.x += o.x * w.f[c];
+      acc.y += o.y * w.f[c];
+      acc.z += o.z * w.f[c];
+      acc.w += o.w * w.f[c];
+    }
+  }
+  return make_float4(acc.x / w.L, acc.y / w.L, acc.z / w.L, acc.w / w.L);
 }
 
 // x (and the RMSNorm weight) of the MAXT work items a thread stages.
@@ -168,8 +206,13 @@ __device__ __forceinline__ void stage_load(const float* __restrict__ x, const fl
     const int b = t >> 2, k = t & 3;
     float4 lo = make_float4(0.f, 0.f, 0.f, 0.f), hi = lo, glo = lo, ghi = lo;
     if (t < ntask) {
-      lo = load_x4<MERGE>(x, ms, 32 * b + 4 * k);
-      hi = load_x4<MERGE>(x, ms, 32 * b + 16 + 4 * k);
+      if constexpr (MERGE) {
+        lo = merged_x4(ms, 32 * b + 4 * k);
+        hi = merged_x4(ms, 32 * b + 16 + 4 * k);
+      } else {
+        lo = *reinterpret_cast<const float4*>(x + 32 * b + 4 * k);
+        hi = *reinterpret_cast<const float4*>(x + 32 * b + 16 + 4 * k);
+      }
       if constexpr (NORM) {
         glo = *reinterpret_cast<const float4*>(norm_w + 32 * b + 4 * k);
         ghi = *reinterpret_cast<const float4*>(norm_w + 32 * b + 16 + 4 * k);
@@ -309,11 +352,19 @@ __device__ __forceinline__ void stage_load16(const float* __restrict__ x, const 
 #pragma unroll
   for (int j = 0; j < MAXT; j++) {
     const int t = threadIdx.x + BS * j;
+    MergeW mw{};
+    int mh = 0, md = 0;
+    if constexpr (MERGE) {  // the group's 16 elements lie in one head
+      mh = (16 * t) / ms.hd;
+      md = 16 * t - mh * ms.hd;
+      if (t < ngroups) mw = merge_weights(ms, mh);
+    }
 #pragma unroll
     for (int c = 0; c < 4; c++) {
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f), g = v;
       if (t < ngroups) {
-        v = load_x4<MERGE>(x, ms, 16 * t + 4 * c);
+        if constexpr (MERGE) v = merge_apply(ms, mw, mh, md + 4 * c);
+        else v = *reinterpret_cast<const float4*>(x + 16 * t + 4 * c);
         if constexpr (NORM) g = *reinterpret_cast<const float4*>(norm_w + 16 * t + 4 * c);
       }
       st.x[j][4 * c + 0] = v.x; st.x[j][4 * c + 1] = v.y; st.x[j][4 * c + 2] = v.z; st.x[j][4 * c + 3] = v.w;
