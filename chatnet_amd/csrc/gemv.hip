@@ -984,10 +984,20 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
       constexpr int MAXT = ((UNIT / 16) * LPR * NU + BS - 1) / BS;
       XStage16<MAXT, NORM> st;
       stage_load16<MAXT, NORM, BS, MERGE>(a.x, a.norm_w, K, st, ms);
-      issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
-      load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, pos, res);
+      // Two units per lane: the staged x would sit beside twice the weight
+      // registers (2 waves per SIMD), so it is digitized before the weight
+      // loads are issued.
+      constexpr bool kLate = NU >= 2;
+      if constexpr (!kLate) {
+        issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
+        load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, pos, res);
+      }
       xred = reinterpret_cast<float*>(smem) + (size_t)((K + 127) >> 7) * XD6_UNIT_DW;
       stage_digitize16<MAXT, NORM, BS>(st, K, xd, xred);
+      if constexpr (kLate) {
+        issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
+        load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, pos, res);
+      }
     } else {
       // items per thread: K <= UNIT * LPR * NU, so K/8 <= (UNIT/8) * LPR * NU items over BS threads
       constexpr int MAXT = ((UNIT / 8) * LPR * NU + BS - 1) / BS;
@@ -1145,8 +1155,11 @@ GemvShape pick_shape(int K, int n_vrows, int num_cus, bool allow8, bool isolated
     s.grid = (waves + 7) / 8;
   }
   // one-unit Q6_K lanes (<= 128 VGPRs) run best at four 256-thread workgroups
-  // per CU (32000x4096 29.2 -> 28.0 us); Q4_K and Q5_K at two
-  const int per_cu = QT == QT_Q6_K && s.nu == 1 ? 4 : 2;
+  // per CU (32000x4096 29.2 -> 28.0 us), two-unit K-quant lanes (~160 VGPRs,
+  // x digitized before the weight loads) at three, Q4_K and Q5_K one-unit
+  // lanes at two
+  const bool kq = QT == QT_Q4_K || QT == QT_Q5_K || QT == QT_Q6_K;
+  const int per_cu = QT == QT_Q6_K && s.nu == 1 ? 4 : (kq && s.nu >= 2 ? 3 : 2);
   if (s.grid > per_cu * num_cus) s.grid = per_cu * num_cus;
   if (s.grid < 1) s.grid = 1;
   return s;
