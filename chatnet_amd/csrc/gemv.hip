@@ -1184,11 +1184,118 @@ hipError_t launch_bs(const GemvArgs& a, const GemvShape& s, size_t smem, hipStre
   return launch_k<QT, RPW, NU, EPI, 256>(a, s.lpr, s.grid, smem, st);
 }
 
+
+// Q4_0 rows of 65..128 units (4096 < K <= 8192) with a store or residual-add
+// epilogue: the row's K is split over KS waves of a workgroup, one 36-byte
+// unit per lane, so the launch has as many waves in flight as a 4096-wide
+// product of the same bytes instead of three units per lane at a third of
+// the waves.  The KS partial sums of a row group meet in LDS; the first wave
+// adds them in ks order and runs the epilogue.  Every wave of a workgroup runs
+// the same number of loop iterations (base is per workgroup, the work is
+// predicated), so the barriers always match.
+template <int RPW, int KS, int EPI, int BS>
+__global__ __launch_bounds__(BS) void gemv_ks_kernel(GemvArgs a) {
+  static_assert(EPI == GEMV_EPI_STORE || EPI == GEMV_EPI_ADD, "K split for store / residual add only");
+  constexpr int NWV = BS / CN_WAVE;
+  static_assert(NWV % KS == 0, "whole row groups per workgroup");
+  constexpr int NRG = NWV / KS;  // row groups per workgroup
+  constexpr int NR = res_count<EPI, RPW>();
+  extern __shared__ float smem[];
+  const int K = a.K;
+  const int nunits = K >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rg = wave / KS, ks = wave % KS;
+  const int u = ks * CN_WAVE + lane;  // this lane's unit
+  const int n_iters = (a.n_vrows + RPW - 1) / RPW;
+  const size_t bpr = (size_t)nunits * 36;
+  const int gstride = gridDim.x * NRG;
+  int base = blockIdx.x * NRG;
+  int it = base + rg;
+
+  uint32_t w[RPW][9];
+  float res[NR];
+  auto load = [&](int itn) {
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      const int vr = itn * RPW + i;
+      if (vr < a.n_vrows && u < nunits) {
+        load_unit<QT_Q4_0>(a.w[0] + (size_t)vr * bpr, u, w[i]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 9; k++) w[i][k] = 0;
+      }
+    }
+  };
+  // items per thread: K/8 <= 8 * 64 * KS items over BS = 64 * KS * NRG threads
+  constexpr int MAXT = (8 * CN_WAVE * KS + BS - 1) / BS;
+  XStage<MAXT, false> st;
+  stage_load<MAXT, false, BS>(a.x, nullptr, K, st);
+  load(it);
+  load_residual<EPI, RPW, NR>(a, it * RPW, lane, 0, res);
+  uint32_t* xd = reinterpret_cast<uint32_t*>(smem);
+  float* xred = smem + (size_t)nunits * XD_UNIT_DW;
+  float* part = xred + 16;  // [NRG][KS-1][RPW]
+  stage_digitize<MAXT, false, BS>(st, K, xd, xred);
+  __syncthreads();
+  while (base < n_iters) {
+    float acc[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) acc[i] = 0.f;
+    if (u < nunits) dot_unit_q4_0_dig<RPW>(w, xd + u * XD_UNIT_DW, acc);
+    const int cur = it;
+    float res_cur[NR];
+#pragma unroll
+    for (int i = 0; i < NR; i++) res_cur[i] = res[i];
+    base += gstride;
+    it += gstride;
+    if (base < n_iters) {
+      load(it);
+      load_residual<EPI, RPW, NR>(a, it * RPW, lane, 0, res);
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+#pragma unroll
+      for (int off = CN_WAVE / 2; off > 0; off >>= 1) acc[i] += __shfl_xor(acc[i], off, CN_WAVE);
+    }
+    if (ks > 0 && lane == 0) {
+#pragma unroll
+      for (int i = 0; i < RPW; i++) part[(rg * (KS - 1) + ks - 1) * RPW + i] = acc[i];
+    }
+    __syncthreads();
+    if (ks == 0 && lane == 0 && cur < n_iters) {
+#pragma unroll
+      for (int k = 1; k < KS; k++)
+#pragma unroll
+        for (int i = 0; i < RPW; i++) acc[i] += part[(rg * (KS - 1) + k - 1) * RPW + i];
+      epilogue<EPI, RPW>(a, cur * RPW, acc, res_cur, 0);
+    }
+    __syncthreads();
+  }
+}
+
+template <int KS, int EPI>
+hipError_t launch_ks(const GemvArgs& a, hipStream_t st) {
+  constexpr int NRG = 2, BS = CN_WAVE * KS * NRG;
+  const int n_iters = (a.n_vrows + 1) / 2;
+  const int grid = (n_iters + NRG - 1) / NRG;
+  const size_t smem = ((size_t)(a.K >> 6) * XD_UNIT_DW + 16 + NRG * (KS - 1) * 2) * sizeof(float);
+  hipLaunchKernelGGL((gemv_ks_kernel<2, KS, EPI, BS>), dim3(grid), dim3(BS), smem, st, a);
+  return hipGetLastError();
+}
+
 template <int QT, int EPI>
 hipError_t launch_qt(const GemvArgs& a, int num_cus, hipStream_t st) {
   // 8 rows per lane only for the norm-fused epilogues (the wide QKV, gate/up
   // and LM-head launches); hipcc 7.2 fails to compile the 8-row STORE/ADD forms.
   constexpr bool kAllow8 = EPI == GEMV_EPI_QKV || EPI == GEMV_EPI_SWIGLU || EPI == GEMV_EPI_LOGITS;
+  if constexpr (QT == QT_Q4_0 && (EPI == GEMV_EPI_STORE || EPI == GEMV_EPI_ADD)) {
+    // 4096 < K <= 8192: K split over two waves (TinyLlama's down projection
+    // 2048x5632: 6.05 -> 5.70 us).  Longer rows keep three or four units per
+    // lane: split three ways, the 7B down projection's 1024 six-wave
+    // workgroups do not all fit at once and decode lost 5 %.
+    const int nunits = a.K >> 6;
+    if (nunits > 64 && nunits <= 128) return launch_ks<2, EPI>(a, st);
+  }
   const GemvShape s = pick_shape<QT>(a.K, a.n_vrows, num_cus, kAllow8, EPI == GEMV_EPI_STORE);
   const size_t smem = gemv_smem_bytes<QT>(a.K);
   if constexpr (QT == QT_Q4_0) {
