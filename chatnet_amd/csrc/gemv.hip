@@ -1273,13 +1273,13 @@ __global__ __launch_bounds__(BS) void gemv_ks_kernel(GemvArgs a) {
   }
 }
 
-template <int KS, int EPI>
+template <int KS, int EPI, int RPW = 2>
 hipError_t launch_ks(const GemvArgs& a, hipStream_t st) {
   constexpr int NRG = 2, BS = CN_WAVE * KS * NRG;
-  const int n_iters = (a.n_vrows + 1) / 2;
+  const int n_iters = (a.n_vrows + RPW - 1) / RPW;
   const int grid = (n_iters + NRG - 1) / NRG;
-  const size_t smem = ((size_t)(a.K >> 6) * XD_UNIT_DW + 16 + NRG * (KS - 1) * 2) * sizeof(float);
-  hipLaunchKernelGGL((gemv_ks_kernel<2, KS, EPI, BS>), dim3(grid), dim3(BS), smem, st, a);
+  const size_t smem = ((size_t)(a.K >> 6) * XD_UNIT_DW + 16 + NRG * (KS - 1) * RPW) * sizeof(float);
+  hipLaunchKernelGGL((gemv_ks_kernel<RPW, KS, EPI, BS>), dim3(grid), dim3(BS), smem, st, a);
   return hipGetLastError();
 }
 
@@ -1291,8 +1291,9 @@ hipError_t launch_qt(const GemvArgs& a, int num_cus, hipStream_t st) {
   if constexpr (QT == QT_Q4_0 && (EPI == GEMV_EPI_STORE || EPI == GEMV_EPI_ADD)) {
     // 4096 < K <= 8192: K split over two waves (TinyLlama's down projection
     // 2048x5632: 6.05 -> 5.70 us).  Longer rows keep three or four units per
-    // lane: split three ways, the 7B down projection's 1024 six-wave
-    // workgroups do not all fit at once and decode lost 5 %.
+    // lane: split three ways, the 7B down projection lost 5 % of decode at two
+    // rows per lane (1024 six-wave workgroups, not all resident) and 2 % at
+    // four.
     const int nunits = a.K >> 6;
     if (nunits > 64 && nunits <= 128) return launch_ks<2, EPI>(a, st);
   }
