@@ -65,6 +65,9 @@ def test_generic_type_gemv_shapes(qtype, M, K):
     # half super-blocks per lane: 44 per row (one per lane, base-256 digits for
     # Q4_K too) and 128 per row (K = 16384, two per lane)
     (12, 7, 5632), (13, 7, 5632), (14, 7, 5632),
+    # Q4_0 rows of 65..128 units: K split over two waves (65: the second wave
+    # holds one unit; 128: both full)
+    (2, 5, 4160), (2, 3, 8192), (2, 1, 8192),
     (12, 3, 16384), (13, 3, 16384), (14, 3, 16384), (8, 9, 16320),
 ])
 def test_ragged_and_misaligned_shapes(qtype, M, K):
