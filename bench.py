@@ -177,6 +177,26 @@ def gemm_sweep(shapes, ns, rotate_bytes=1 << 30):
     return res
 
 
+def copy_rate(nbytes=512 << 20, reps=5):
+    """The box's measured streaming rate: a device-to-device copy of nbytes
+    (read + write bytes per second), HIP events on the null stream."""
+    from chatnet_amd import hiprt
+
+    a, b = hiprt.DeviceBuffer(nbytes), hiprt.DeviceBuffer(nbytes)
+    a.fill(1)
+    b.copy_from(a, nbytes)
+    hiprt.synchronize()
+    e0, e1 = hiprt.Event(), hiprt.Event()
+    e0.record(0)
+    for _ in range(reps):
+        b.copy_from(a, nbytes)
+    e1.record(0)
+    ms = e0.elapsed_ms(e1)
+    a.free()
+    b.free()
+    return round(2 * nbytes * reps / (ms * 1e-3) / 1e9, 1)
+
+
 def sampled_run(cfg, ck, prompt, steps):
     """Decode tok/s with the device temperature sampler (T 0.8, top-k 40,
     top-p 0.9, seed 1) in place of the argmax, prompt included in the call."""
@@ -278,6 +298,8 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
 
+    copy_gbs = copy_rate()
+    log(f"device-to-device copy: {copy_gbs} GB/s (read + write)")
     log("gemv sweep (cold, rotating >= 1 GiB)")
     sweep = gemv_sweep(SWEEP)
     roof = sweep[f"{ROOF_SHAPE[0]}x{ROOF_SHAPE[1]}"]
@@ -380,7 +402,9 @@ def main():
                      "frac": roof["frac"], "traffic": measured_traffic(ROOF_SHAPE),
                      "traffic_source": "profiles/gemv_q4_0_sweep_roofline.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
                      "kernel": "gemv_kernel<Q4_0> (chatnet_matmul N=1) at 11008x4096, cold",
-                     "alg_bytes_per_launch": roof["alg_bytes"], "avg_launch_us": roof["us"]},
+                     "alg_bytes_per_launch": roof["alg_bytes"], "avg_launch_us": roof["us"],
+                     "measured_copy_GBs": copy_gbs,
+                     "measured_copy_note": "512 MiB device-to-device copy, read + write bytes per second"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
