@@ -1,25 +1,31 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized Llama decode path on one MI355X.
 
-Headline (`value`): Llama-2-7B-shaped Q4_0 batch-1 greedy decode, tok/s.
-A step is one decode token (embedding, 32 layers of fused GEMVs + attention,
-LM head, device argmax) replayed as one HIP graph; the 128-token prompt is
-forwarded before the timed region, then exactly --steps decode tokens are
+Headline (`value`): Llama-2-7B-shaped Q4_0 batch-1 greedy decode, tok/s
+(workload llama2_7b_q4_0_decode of chatnet_amd.workloads).  A step is one
+decode token (embedding, 32 layers of fused GEMVs + attention, LM head,
+device argmax) replayed as one HIP graph; the 128-token prompt is forwarded as
+one span before the timed region, then exactly --steps decode tokens are
 timed (KV cache grows 128 -> 128+steps).  Weights are seeded random N(0, 0.02)
 quantized to Q4_0 in HBM; inputs are resident before timing starts.
 
-Extra fields: TinyLlama-1.1B decode tok/s, the isolated Q4_0 GEMV sweep
-(achieved HBM GB/s per shape, cold: every launch reads a different copy of the
-weights, >= 1 GiB in rotation so the 256 MB MALL cannot serve them), the
-roofline object of the dominant kernel (the Q4_0 GEMV at the 11008 x 4096
-ffn shape) and the CPU baseline (the oracle's restatement of the reference's
-C# path on the host cores, bounded sample).
+Every timed run's tokens (and the logits after its prompt) are checked
+against the oracle's expected outputs committed under tests/golden/
+(`parity`).  Extra legs: the TinyLlama-1.1B workloads (16-token prompt + 32
+tokens at context 64; 512-token span + 128 tokens), the 7B Q4_K_M-style
+decode, the isolated GEMV and GEMM sweeps (cold: every launch of a timed
+graph reads its own copy of the weights and each shape cycles at least 1 GiB,
+so the 256 MB MALL cannot serve them), the roofline object of the dominant
+kernel (the Q4_0 GEMV at the 11008 x 4096 ffn shape) and the CPU baseline
+(the oracle's restatement of the reference's C# path on the host cores,
+bounded samples).
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -38,13 +44,16 @@ KQ4_SHAPES = [(4096, 4096), (11008, 4096)]
 KQ6_SHAPES = [(4096, 11008), (32000, 4096)]
 # MatVecMulGeneric types on the 7B projection shapes
 GENERIC_SHAPES = [(4096, 4096), (11008, 4096), (4096, 11008)]
+ROTATE_BYTES = 1 << 30  # weight bytes each cold sweep shape cycles through
+NEAR_TIE = 1e-3
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-BLOCK = {2: (32, 18), 8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}  # ggml type -> (weights, bytes) per block
+BLOCK = {0: (1, 4), 1: (1, 2), 2: (32, 18), 8: (32, 34), 12: (256, 144), 13: (256, 176),
+         14: (256, 210)}  # ggml type -> (weights, bytes) per block
 
 
 def weight_bytes(M: int, K: int, qtype: int = 2) -> int:
@@ -52,20 +61,59 @@ def weight_bytes(M: int, K: int, qtype: int = 2) -> int:
     return M * K // w * b
 
 
-def q4_0_bytes(M: int, K: int) -> int:
-    return weight_bytes(M, K, 2)
-
-
 def gemv_algorithmic_bytes(M: int, K: int, qtype: int = 2) -> int:
     # weights + x (fp32) + y (fp32)
     return weight_bytes(M, K, qtype) + 4 * K + 4 * M
 
 
+def decode_gemv_bytes(cfg, mix_types) -> int:
+    """Algorithmic bytes of one decode step's GEMVs (weights + fp32 x + fp32 y
+    per launch): QKV, O, gate/up and down per layer, then the LM head."""
+    attn, gate_up, down, out = mix_types
+    kvd = cfg.kv_dim
+    per_layer = (gemv_algorithmic_bytes(cfg.dim + 2 * kvd, cfg.dim, attn)
+                 + gemv_algorithmic_bytes(cfg.dim, cfg.dim, attn)
+                 + gemv_algorithmic_bytes(2 * cfg.hidden_dim, cfg.dim, gate_up)
+                 + gemv_algorithmic_bytes(cfg.dim, cfg.hidden_dim, down))
+    return cfg.n_layers * per_layer + gemv_algorithmic_bytes(cfg.vocab_size, cfg.dim, out)
+
+
+# -- parity of the timed runs against the oracle's committed expected outputs --
+def fixture(name: str):
+    path = os.path.join(ROOT, "tests", "golden", f"workload_{name}.npz")
+    return np.load(path) if os.path.exists(path) else None
+
+
+def parity(name: str, tokens, prompt_logits=None):
+    """Leading tokens identical to the oracle's; a first difference is
+    acceptable only at a step whose oracle top-1/top-2 margin is < 1e-3."""
+    fx = fixture(name)
+    if fx is None:
+        return {"fixture": None}
+    exp = [int(t) for t in fx["tokens"]]
+    got = [int(t) for t in tokens]
+    n = min(len(got), len(exp))
+    same = 0
+    while same < n and got[same] == exp[same]:
+        same += 1
+    res = {"checked": n, "identical_prefix": same}
+    if same < n:
+        res["first_difference_oracle_margin"] = round(float(fx["margins"][same]), 6)
+    res["ok"] = same == n or float(fx["margins"][same]) < NEAR_TIE
+    if prompt_logits is not None:
+        err = float(np.max(np.abs(np.asarray(prompt_logits) - fx["logits_prompt"])))
+        res["prompt_logits_max_abs_err"] = float(f"{err:.3g}")
+        res["ok"] = bool(res["ok"] and err <= 1e-2)
+    return res
+
+
 def decode_run(cfg, ck, prompt, steps, warmup):
+    """Forward the prompt, warm up (graph capture), forward the prompt again
+    and time `steps` greedy decode tokens on the device."""
     from chatnet_amd import HipLlamaModel, hiprt
 
     with HipLlamaModel(cfg, ck) as m:
-        m.forward(prompt, 0)
+        lp = m.forward(prompt, 0).copy()
         m.decode_greedy(max(warmup, 1))             # warm-up (also captures the graph)
         m.forward(prompt, 0)                         # reset to the prompt
         hiprt.synchronize()
@@ -74,34 +122,61 @@ def decode_run(cfg, ck, prompt, steps, warmup):
         hiprt.synchronize()
         dt = time.perf_counter() - t0
     assert len(toks) == steps, (len(toks), steps)
-    return dt, toks
+    return dt, toks, lp
 
 
-def gemv_sweep(shapes, launches_per_shape=64, replays=5, rotate_bytes=1 << 30, qtype=2):
-    """Cold per-launch GEMV time: `launches_per_shape` launches over distinct
-    weight copies are captured into one HIP graph, so the device runs them
-    back to back, and HIP events on that stream time `replays` replays."""
+def short_decode_run(cfg, ck, prompt, steps, repeats):
+    """A short workload timed `repeats` times (forward the prompt, then
+    `steps` greedy tokens timed): median decode tok/s and the last tokens."""
+    from chatnet_amd import HipLlamaModel, hiprt
+
+    rates = []
+    with HipLlamaModel(cfg, ck) as m:
+        lp = m.forward(prompt, 0).copy()
+        m.decode_greedy(steps)                       # graph capture
+        for _ in range(repeats):
+            m.forward(prompt, 0)
+            hiprt.synchronize()
+            t0 = time.perf_counter()
+            toks = m.decode_greedy(steps)
+            rates.append(steps / (time.perf_counter() - t0))
+    return statistics.median(rates), toks, lp
+
+
+def _cold_pool(qtype, M, K, rotate_bytes):
+    """Distinct copies of one seeded weight matrix, at least rotate_bytes in all."""
+    from chatnet_amd import hiprt, synth
+
+    nb = weight_bytes(M, K, qtype)
+    stride = (nb + 256 + 4095) // 4096 * 4096
+    copies = max(4, -(-rotate_bytes // stride))
+    t = synth.tensor(qtype, 99, f"sweep{M}x{K}", M, K)
+    base = hiprt.DeviceBuffer.from_numpy(t.data)
+    pool = hiprt.DeviceBuffer(copies * stride)
+    pool.fill(0)
+    for c in range(copies):
+        pool.copy_from(base, nb, dst_offset=c * stride)
+    base.free()
+    return pool, stride, copies
+
+
+def gemv_sweep(shapes, replays=2, rotate_bytes=ROTATE_BYTES, qtype=2):
+    """Cold per-launch GEMV time: one launch per weight copy (at least
+    rotate_bytes of copies, so no launch finds its weights in the 256 MB MALL)
+    captured into one HIP graph, so the device runs them back to back; HIP
+    events on that stream time `replays` replays."""
     from chatnet_amd import hiprt, ops, synth
 
     res = {}
     for (M, K) in shapes:
-        nb = weight_bytes(M, K, qtype)
-        stride = (nb + 256 + 4095) // 4096 * 4096
-        copies = max(4, min(256, -(-rotate_bytes // stride)))
-        t = synth.tensor(qtype, 99, f"sweep{M}x{K}", M, K)
-        base = hiprt.DeviceBuffer.from_numpy(t.data)
-        pool = hiprt.DeviceBuffer(copies * stride)
-        pool.fill(0)
-        for c in range(copies):
-            pool.copy_from(base, nb, dst_offset=c * stride)
+        pool, stride, copies = _cold_pool(qtype, M, K, rotate_bytes)
         x = hiprt.DeviceBuffer.from_numpy(synth.normal(99, f"sweepx{K}", K, 1.0))
         y = hiprt.DeviceBuffer(4 * M)
         hiprt.synchronize()
         stream = hiprt.Stream()
 
         def issue():
-            for i in range(launches_per_shape):
-                c = i % copies
+            for c in range(copies):
                 ops.matmul_ptr(qtype, pool.ptr + c * stride, x.ptr, y.ptr, M, K, 1, stream.h)
 
         graph = hiprt.Graph(stream, issue)
@@ -112,68 +187,60 @@ def gemv_sweep(shapes, launches_per_shape=64, replays=5, rotate_bytes=1 << 30, q
         for _ in range(replays):
             graph.launch()
         e1.record(stream.h)
-        us = e0.elapsed_ms(e1) * 1000.0 / (launches_per_shape * replays)
+        us = e0.elapsed_ms(e1) * 1000.0 / (copies * replays)
         del graph
         stream.synchronize()
         alg = gemv_algorithmic_bytes(M, K, qtype)
         res[f"{M}x{K}"] = {"us": round(us, 3), "GB/s": round(alg / us / 1e3, 1),
-                           "frac": round(alg / us / 1e3 / HBM_PEAK_GBS, 4), "alg_bytes": alg}
-        for b in (pool, base, x, y):
+                           "frac": round(alg / us / 1e3 / HBM_PEAK_GBS, 4), "alg_bytes": alg,
+                           "launches": copies, "rotated_MB": round(copies * stride / 1e6, 1)}
+        for b in (pool, x, y):
             b.free()
     return res
 
 
-def gemm_sweep(shapes, ns, rotate_bytes=1 << 30):
+def gemm_sweep(shapes, ns, rotate_bytes=ROTATE_BYTES):
     """Batched chatnet_matmul (x fp32 -> bf16, MFMA GEMM, split-K reduce when
-    used) per call, cold weights as in gemv_sweep; HIP events on the stream the
-    calls are captured on."""
+    used) per call, cold weights as in gemv_sweep (one call per weight copy);
+    HIP events on the stream the calls are captured on."""
     from chatnet_amd import hiprt, ops, synth
 
     res = {}
     for (M, K) in shapes:
-        nb = q4_0_bytes(M, K)
-        stride = (nb + 256 + 4095) // 4096 * 4096
-        copies = max(4, min(64, -(-rotate_bytes // stride)))
-        t = synth.tensor(2, 99, f"sweep{M}x{K}", M, K)
-        base = hiprt.DeviceBuffer.from_numpy(t.data)
-        pool = hiprt.DeviceBuffer(copies * stride)
-        pool.fill(0)
-        for c in range(copies):
-            pool.copy_from(base, nb, dst_offset=c * stride)
+        pool, stride, copies = _cold_pool(2, M, K, rotate_bytes)
+        nb = weight_bytes(M, K, 2)
         per = {}
         for N in ns:
             x = hiprt.DeviceBuffer.from_numpy(synth.normal(99, f"gemmx{N}x{K}", N * K, 1.0))
             y = hiprt.DeviceBuffer(4 * M * N)
             stream = hiprt.Stream()
-            launches = 32 if N <= 64 else 8
             ops.matmul_ptr(2, pool.ptr, x.ptr, y.ptr, M, K, N, stream.h)  # sizes the workspace
             stream.synchronize()
 
             def issue():
-                for i in range(launches):
-                    ops.matmul_ptr(2, pool.ptr + (i % copies) * stride, x.ptr, y.ptr, M, K, N, stream.h)
+                for c in range(copies):
+                    ops.matmul_ptr(2, pool.ptr + c * stride, x.ptr, y.ptr, M, K, N, stream.h)
 
             graph = hiprt.Graph(stream, issue)
             graph.launch()
             stream.synchronize()
             e0, e1 = hiprt.Event(), hiprt.Event()
-            replays = 3
+            replays = 2
             e0.record(stream.h)
             for _ in range(replays):
                 graph.launch()
             e1.record(stream.h)
-            us = e0.elapsed_ms(e1) * 1000.0 / (launches * replays)
+            us = e0.elapsed_ms(e1) * 1000.0 / (copies * replays)
             del graph
             stream.synchronize()
             alg = nb + 4 * K * N + 4 * M * N
             tflops = 2.0 * M * N * K / us / 1e6
             per[str(N)] = {"us": round(us, 2), "GB/s": round(alg / us / 1e3, 1), "TFLOP/s": round(tflops, 1),
-                           "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+                           "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "launches": copies}
             x.free()
             y.free()
         res[f"{M}x{K}"] = per
         pool.free()
-        base.free()
     return res
 
 
@@ -213,67 +280,96 @@ def sampled_run(cfg, ck, prompt, steps):
     return round(steps / ((t2 - t1) - (t1 - t0)), 1)
 
 
-def prefill_run(cfg, ck, n_prompt, n_decode):
-    """Time to first token of an n_prompt-token prompt forwarded as one span,
-    then n_decode greedy decode tokens."""
-    from chatnet_amd import HipLlamaModel, hiprt, synth
+def prefill_run(w, ck):
+    """Time to first token of the workload's prompt forwarded as one span,
+    then its greedy decode tokens; both checked against the fixture."""
+    from chatnet_amd import HipLlamaModel, hiprt
 
-    prompt = synth.tokens(77, "prefill", n_prompt, cfg.vocab_size)
-    with HipLlamaModel(cfg, ck) as m:
+    prompt = w.prompt()
+    with HipLlamaModel(w.config, ck) as m:
         m.forward(prompt, 0)  # warm-up: span buffers, kernel attributes
         m.decode_greedy(4)
         hiprt.synchronize()
         t0 = time.perf_counter()
-        m.forward(prompt, 0)  # returns after the logits are on the host
+        lp = m.forward(prompt, 0).copy()  # returns after the logits are on the host
         t1 = time.perf_counter()
-        toks = m.decode_greedy(n_decode)
+        toks = m.decode_greedy(w.n_decode)
         t2 = time.perf_counter()
-    assert len(toks) == n_decode
-    return {"prompt_tokens": n_prompt, "ttft_ms": round((t1 - t0) * 1e3, 3),
-            "prefill_tok_s": round(n_prompt / (t1 - t0), 1), "decode_tokens": n_decode,
-            "decode_tok_s": round(n_decode / (t2 - t1), 1)}
+    assert len(toks) == w.n_decode
+    return {"prompt_tokens": w.n_prompt, "ttft_ms": round((t1 - t0) * 1e3, 3),
+            "prefill_tok_s": round(w.n_prompt / (t1 - t0), 1), "decode_tokens": w.n_decode,
+            "decode_tok_s": round(w.n_decode / (t2 - t1), 1), "parity": parity(w.name, toks, lp)}
 
 
-def measured_traffic(shape):
-    """HBM bytes per launch of the roofline GEMV, from the committed
-    rocprofv3 FETCH_SIZE + WRITE_SIZE summary (counters scaled by the same
-    counters read on a copy kernel of known size), or None if absent."""
-    path = os.path.join(ROOT, "profiles", "gemv_q4_0_sweep_roofline.md")
-    key = f"traffic_bytes_per_launch {shape[0]}x{shape[1]}:"
+def profile_figure(path: str, key: str):
+    """A number recorded as `key: value` in a committed profiles/ summary."""
     try:
-        with open(path) as f:
+        with open(os.path.join(ROOT, "profiles", path)) as f:
             for line in f:
-                if line.startswith(key):
-                    return int(line[len(key):].strip())
-    except OSError:
+                if line.startswith(key + ":"):
+                    return float(line.split(":", 1)[1].split()[0])
+    except (OSError, ValueError):
         pass
     return None
 
 
-def cpu_baseline(cfg, ck, prompt_len=4, decode=8):
-    """The oracle (C restatement of the reference's CPU path) on the host cores."""
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(cfg7, ck7, cfg1, ck1):
+    """The oracle (C restatement of the reference's CPU path) on the host
+    cores, bounded samples: the 7B decode (headline unit), the TinyLlama
+    decode at all threads and at one thread, and the isolated Q4_0 GEMV."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
+    from chatnet_amd import synth
 
     cores = int(os.environ.get("OMP_NUM_THREADS") or len(os.sched_getaffinity(0)))
-    oracle.set_threads(cores)
-    ora = oracle.OracleLlama(cfg, ck)
-    prompt = list(range(1, prompt_len + 1))
-    t0 = time.perf_counter()
-    for i, tk in enumerate(prompt):
-        logits = ora.forward([tk], i)
-    t1 = time.perf_counter()
-    tok = oracle.argmax(logits)
-    for j in range(decode):
-        logits = ora.forward([tok], prompt_len + j)
+
+    def decode_rate(cfg, ck, prompt_len, decode, threads):
+        oracle.set_threads(threads)
+        ora = oracle.OracleLlama(cfg, ck)
+        logits = ora.forward(list(range(1, prompt_len + 1)), 0)
         tok = oracle.argmax(logits)
-    t2 = time.perf_counter()
-    ora.close()
+        t0 = time.perf_counter()
+        for j in range(decode):
+            logits = ora.forward([tok], prompt_len + j)
+            tok = oracle.argmax(logits)
+        dt = time.perf_counter() - t0
+        ora.close()
+        return decode / dt
+
+    v7 = decode_rate(cfg7, ck7, 4, 8, cores)
+    legs = {"cpu_model": cpu_model(), "host_threads_visible": os.cpu_count(), "threads_used": cores}
+    if cfg1 is not None:
+        legs["tinyllama_q4_0_decode_tok_s"] = round(decode_rate(cfg1, ck1, 4, 16, cores), 3)
+        legs["tinyllama_q4_0_decode_tok_s_1_thread"] = round(decode_rate(cfg1, ck1, 2, 4, 1), 3)
+    M, K = ROOF_SHAPE
+    t = synth.tensor(2, 99, f"sweep{M}x{K}", M, K)
+    x = synth.normal(99, f"sweepx{K}", K, 1.0)
+    oracle.set_threads(cores)
+    oracle.matvec(2, t.data, x, M, K)
+    reps = 10
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        oracle.matvec(2, t.data, x, M, K)
+    dt = (time.perf_counter() - t0) / reps
+    legs[f"gemv_q4_0_{M}x{K}_GBs"] = round(gemv_algorithmic_bytes(M, K) / dt / 1e9, 2)
     oracle.set_threads(1)
-    return {"value": round(decode / (t2 - t1), 3), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"oracle LlamaModel.Forward restatement, {cfg.n_layers}-layer {cfg.dim}-dim Q4_0, "
-                      f"{prompt_len}-token prompt then {decode} greedy decode tokens timed "
-                      f"(positions {prompt_len}..{prompt_len + decode - 1}), row-parallel over {cores} threads"}
+    return {"value": round(v7, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"oracle LlamaModel.Forward restatement, {cfg7.n_layers}-layer {cfg7.dim}-dim Q4_0, "
+                      f"4-token prompt then 8 greedy decode tokens timed, row-parallel over {cores} threads; "
+                      f"legs: TinyLlama-shaped decode (16 tokens at {cores} threads, 4 at 1 thread) and "
+                      f"{reps} isolated {M}x{K} Q4_0 GEMVs",
+            "legs": legs}
 
 
 def main():
@@ -292,7 +388,8 @@ def main():
               "multi-GPU sharding is design-only", file=sys.stderr)
         sys.exit(2)
 
-    from chatnet_amd import LLAMA2_7B, QWEN2_0_5B, TINYLLAMA_1B, _native, hiprt, synth
+    from chatnet_amd import QWEN2_0_5B, _native, hiprt, synth
+    from chatnet_amd.workloads import WORKLOADS
 
     if hiprt.device_count() < 1:
         print("bench.py needs a GPU", file=sys.stderr)
@@ -300,13 +397,12 @@ def main():
 
     copy_gbs = copy_rate()
     log(f"device-to-device copy: {copy_gbs} GB/s (read + write)")
-    log("gemv sweep (cold, rotating >= 1 GiB)")
+    log("gemv sweep (cold: one launch per weight copy, >= 1 GiB of copies per shape)")
     sweep = gemv_sweep(SWEEP)
     roof = sweep[f"{ROOF_SHAPE[0]}x{ROOF_SHAPE[1]}"]
     log(f"sweep: {json.dumps(sweep)}")
 
     value = ms = None
-    toks7 = None
     cpu = None
     tiny = None
     tiny_sampled = None
@@ -315,18 +411,20 @@ def main():
     kq = None
     qwen = None
     fp16kv = None
+    par = {}
     if not args.roofline_only and not args.no_kquant:
-        log("Q4_K / Q6_K / Q8_0 / Q5_K gemv (cold) and 7B Q4_K_M-style 64-token decode")
+        log("Q4_K / Q6_K / Q8_0 / Q5_K / F16 gemv (cold) and 7B Q4_K_M-style 64-token decode")
         kq = {"gemv_q4_k_cold": gemv_sweep(KQ4_SHAPES, qtype=12),
               "gemv_q6_k_cold": gemv_sweep(KQ6_SHAPES, qtype=14),
               "gemv_q8_0_cold": gemv_sweep(GENERIC_SHAPES, qtype=8),
-              "gemv_q5_k_cold": gemv_sweep(GENERIC_SHAPES, qtype=13)}
-        cfgk = LLAMA2_7B.replace(context_length=2048)
-        ckk = synth.llama_checkpoint(cfgk, seed=11, mix="q4_k_m")
-        pk = synth.tokens(11, "prompt", 16, cfgk.vocab_size)
-        dtk, _ = decode_run(cfgk, ckk, pk, 64, 4)
-        kq["llama2_7b_q4_k_m_decode_tok_s"] = round(64 / dtk, 1)
+              "gemv_q5_k_cold": gemv_sweep(GENERIC_SHAPES, qtype=13),
+              "gemv_f16_cold": gemv_sweep(GENERIC_SHAPES[:2], qtype=1)}
+        wk = WORKLOADS["llama2_7b_q4_k_m_decode"]
+        ckk = wk.checkpoint()
+        dtk, tk, lpk = decode_run(wk.config, ckk, wk.prompt(), wk.n_decode, 4)
+        kq["llama2_7b_q4_k_m_decode_tok_s"] = round(wk.n_decode / dtk, 1)
         kq["weights_GB"] = round(synth.checkpoint_bytes(ckk) / 1e9, 3)
+        par[wk.name] = parity(wk.name, tk, lpk)
         del ckk
         log(f"  {json.dumps(kq)}")
     if not args.roofline_only and not args.no_gemm:
@@ -334,47 +432,53 @@ def main():
         gsweep = gemm_sweep(SWEEP, (8, 64, 512))
         log(f"gemm sweep: {json.dumps(gsweep)}")
     if not args.roofline_only:
-        cfg7 = LLAMA2_7B.replace(context_length=2048)
+        w7 = WORKLOADS["llama2_7b_q4_0_decode"]
+        cfg7 = w7.config
         log("generating Llama-2-7B-shaped Q4_0 checkpoint")
         t0 = time.perf_counter()
-        ck7 = synth.llama_checkpoint(cfg7, seed=7, mix="q4_0")
+        ck7 = w7.checkpoint()
         log(f"  {synth.checkpoint_bytes(ck7) / 1e9:.2f} GB in {time.perf_counter() - t0:.1f} s")
-        prompt = synth.tokens(7, "prompt", 128, cfg7.vocab_size)
-        log(f"7B decode: prompt 128, warmup {args.warmup}, timed {args.steps}")
-        dt, toks7 = decode_run(cfg7, ck7, prompt, args.steps, args.warmup)
+        prompt = w7.prompt()
+        log(f"7B decode: prompt {w7.n_prompt} (one span), warmup {args.warmup}, timed {args.steps}")
+        dt, toks7, lp7 = decode_run(cfg7, ck7, prompt, args.steps, args.warmup)
         value = args.steps / dt
         ms = dt * 1000.0 / args.steps
-        log(f"  {value:.1f} tok/s ({ms:.3f} ms/token)")
-        dt16, _ = decode_run(cfg7.replace(kv_dtype=_native.KV_F16), ck7, prompt, args.steps, args.warmup)
+        par[w7.name] = parity(w7.name, toks7, lp7)
+        log(f"  {value:.1f} tok/s ({ms:.3f} ms/token); parity {json.dumps(par[w7.name])}")
+        dt16, toks16, _ = decode_run(cfg7.replace(kv_dtype=_native.KV_F16), ck7, prompt, args.steps, args.warmup)
         fp16kv = round(args.steps / dt16, 1)
         log(f"  fp16 KV cache: {fp16kv} tok/s")
+        w1 = WORKLOADS["tinyllama_q4_0_decode"]
+        ck1 = w1.checkpoint() if not args.no_tinyllama or not args.no_cpu else None
         if not args.no_cpu:
             log("cpu baseline (oracle on host cores)")
-            cpu = cpu_baseline(cfg7, ck7)
-            log(f"  {cpu['value']} tok/s on {cpu['cores']} threads")
+            cpu = cpu_baseline(cfg7, ck7, w1.config, ck1)
+            log(f"  {cpu['value']} tok/s on {cpu['cores']} threads; {json.dumps(cpu['legs'])}")
         del ck7
         if not args.no_tinyllama:
-            cfg1 = TINYLLAMA_1B.replace(context_length=2048)
-            ck1 = synth.llama_checkpoint(cfg1, seed=1234, mix="q4_0")
-            p1 = synth.tokens(1234, "prompt", 16, cfg1.vocab_size)
-            dt1, _ = decode_run(cfg1, ck1, p1, 128, 8)
-            tiny = round(128 / dt1, 1)
-            log(f"TinyLlama decode: {tiny} tok/s")
-            tiny_sampled = sampled_run(cfg1, ck1, p1, 128)
+            rate1, toks1, lp1 = short_decode_run(w1.config, ck1, w1.prompt(), w1.n_decode, 20)
+            tiny = round(rate1, 1)
+            par[w1.name] = parity(w1.name, toks1, lp1)
+            log(f"TinyLlama decode ({w1.n_prompt}-token prompt, {w1.n_decode} tokens, context "
+                f"{w1.config.context_length}): {tiny} tok/s; parity {json.dumps(par[w1.name])}")
+            tiny_sampled = sampled_run(w1.config.replace(context_length=2048), ck1, w1.prompt(), 128)
             log(f"TinyLlama decode, temperature sampler on the device: {tiny_sampled} tok/s")
-            log("TinyLlama 512-token prefill + 128 decode")
-            prefill = prefill_run(cfg1, ck1, 512, 128)
-            log(f"  {json.dumps(prefill)}")
+            w2 = WORKLOADS["tinyllama_q4_0_prefill"]
+            log(f"TinyLlama {w2.n_prompt}-token prefill + {w2.n_decode} decode")
             del ck1
+            prefill = prefill_run(w2, w2.checkpoint())
+            log(f"  {json.dumps(prefill)}")
             cfgq = QWEN2_0_5B.replace(context_length=2048)
             ckq = synth.llama_checkpoint(cfgq, seed=5, mix="q8_0", with_output=False, embedding=_native.GGML_Q8_0)
             pq = synth.tokens(5, "prompt", 16, cfgq.vocab_size)
-            dtq, _ = decode_run(cfgq, ckq, pq, 128, 8)
+            dtq, _, _ = decode_run(cfgq, ckq, pq, 128, 8)
             qwen = {"qwen2_0_5b_q8_0_decode_tok_s": round(128 / dtq, 1),
                     "weights_GB": round(synth.checkpoint_bytes(ckq) / 1e9, 3)}
             log(f"Qwen2-0.5B-shaped Q8_0 (tied embeddings, QKV biases) decode: {json.dumps(qwen)}")
             del ckq
 
+    tiny_gemv_bytes = decode_gemv_bytes(WORKLOADS["tinyllama_q4_0_decode"].config, (2, 2, 2, 2))
+    tiny_gemv_us = profile_figure("tinyllama_q4_0_decode_kernels.md", "gemv_us_per_token")
     res = {
         "metric": METRIC,
         "value": round(value, 2) if value else None,
@@ -388,18 +492,32 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded N(0,0.02) weights quantized to Q4_0, seeded prompt ids)",
-        "config": {"workload": "llama2-7b-q4_0-decode-bs1", "prompt_tokens": 128, "decode_tokens": args.steps,
-                   "kv_cache": "f32", "context_length": 2048, "weights": "Q4_0 (all matrices)",
+        "config": {"workload": "llama2-7b-q4_0-decode-bs1", "prompt_tokens": 128, "prompt_as": "one span",
+                   "decode_tokens": args.steps, "kv_cache": "f32", "context_length": 2048,
+                   "weights": "Q4_0 (all matrices)",
                    "llama2_7b_q4_0_fp16_kv_decode_tok_s": fp16kv,
                    "tinyllama_1b_q4_0_decode_tok_s": tiny,
+                   "tinyllama_1b_q4_0_decode_workload": "16-token prompt, 32 greedy tokens, context 64, "
+                                                       "median of 20 timed runs",
                    "tinyllama_1b_q4_0_sampled_decode_tok_s": tiny_sampled},
+        "parity": par,
+        "tinyllama_decode": {
+            "step_frac_of_hbm_roofline": (round(tiny * decode_gemv_bytes(
+                WORKLOADS["tinyllama_q4_0_decode"].config, (2, 2, 2, 2)) / 1e9 / HBM_PEAK_GBS, 4) if tiny else None),
+            "gemv_alg_bytes_per_token": tiny_gemv_bytes,
+            "gemv_us_per_token": tiny_gemv_us,
+            "gemv_frac_of_hbm_peak": (round(tiny_gemv_bytes / (tiny_gemv_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+                                      if tiny_gemv_us else None),
+            "gemv_source": "profiles/tinyllama_q4_0_decode_kernels.md (rocprofv3 kernel trace of the workload)"},
         "gemv_sweep_q4_0_n1_cold": sweep,
         "gemm_sweep_q4_0_cold": gsweep,
         "tinyllama_q4_0_prefill": prefill,
         "llama2_7b_q4_k_m": kq,
         "qwen2_0_5b_q8_0": qwen,
         "roofline": {"bound": "hbm", "achieved": roof["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": roof["frac"], "traffic": measured_traffic(ROOF_SHAPE),
+                     "frac": roof["frac"],
+                     "traffic": profile_figure("gemv_q4_0_sweep_roofline.md",
+                                               f"traffic_bytes_per_launch {ROOF_SHAPE[0]}x{ROOF_SHAPE[1]}"),
                      "traffic_source": "profiles/gemv_q4_0_sweep_roofline.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
                      "kernel": "gemv_kernel<Q4_0> (chatnet_matmul N=1) at 11008x4096, cold",
                      "alg_bytes_per_launch": roof["alg_bytes"], "avg_launch_us": roof["us"],
@@ -407,6 +525,10 @@ def main():
                      "measured_copy_note": "512 MiB device-to-device copy, read + write bytes per second"},
         "cpu_baseline": cpu,
     }
+    if res["tinyllama_decode"]["gemv_us_per_token"] is not None:
+        res["tinyllama_decode"]["gemv_us_per_token"] = round(tiny_gemv_us, 2)
+    if res["roofline"]["traffic"] is not None:
+        res["roofline"]["traffic"] = int(res["roofline"]["traffic"])
     print(json.dumps(res), flush=True)
 
 

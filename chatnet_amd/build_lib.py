@@ -17,8 +17,8 @@ CSRC = os.path.join(PKG, "csrc")
 LIBDIR = os.path.join(PKG, "lib")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
-HIP_SOURCES = ["chatnet_api.hip", "gemv.hip", "gemm.hip", "prefill.hip", "decode_ops.hip", "sample.hip"]
-HIP_HEADERS = ["device_common.h", "kernels.h"]
+HIP_SOURCES = ["chatnet_api.hip", "gemv.hip", "gemv_float.hip", "gemm.hip", "prefill.hip", "decode_ops.hip", "sample.hip"]
+HIP_HEADERS = ["device_common.h", "gemv_common.h", "kernels.h"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -47,15 +47,32 @@ def _run(cmd: list[str]) -> None:
 
 
 def build_hip(verbose: bool = False) -> str:
+    """Compiles each translation unit to an object in parallel (no device code
+    crosses translation units), then links the shared library."""
+    from concurrent.futures import ThreadPoolExecutor
+
     hipcc = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
     os.makedirs(LIBDIR, exist_ok=True)
+    objdir = os.path.join(PKG, "_build")
+    os.makedirs(objdir, exist_ok=True)
     out = os.path.join(LIBDIR, "libchatnet_hip.so")
     tmp = out + ".tmp"
     srcs = [os.path.join(CSRC, s) for s in HIP_SOURCES if os.path.exists(os.path.join(CSRC, s))]
-    cmd = [hipcc, *HIPCC_FLAGS, "-I", os.path.join(PKG, "..", "include"), *srcs, "-o", tmp]
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    cmds = []
+    for src in srcs:
+        obj = os.path.join(objdir, os.path.basename(src) + ".o")
+        cmds.append([hipcc, *compile_flags, "-I", os.path.join(PKG, "..", "include"), "-c", src, "-o", obj])
     if verbose:
-        print(" ".join(cmd))
-    _run(cmd)
+        for c in cmds:
+            print(" ".join(c))
+    jobs = max(1, min(len(cmds), int(os.environ.get("MAX_JOBS") or os.cpu_count() or 1)))
+    with ThreadPoolExecutor(jobs) as ex:
+        list(ex.map(_run, cmds))
+    link = [hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *[c[-1] for c in cmds], "-o", tmp]
+    if verbose:
+        print(" ".join(link))
+    _run(link)
     os.replace(tmp, out)
     return out
 

@@ -72,31 +72,37 @@ int device_cus(int dev) {
 
 // Weight types the GEMV serves (LlamaModel.MatVecMulByType, LlamaModel.cs:470-567).
 bool is_matrix_type(uint32_t t) {
-  return t == CHATNET_GGML_Q4_0 || t == CHATNET_GGML_Q8_0 || t == CHATNET_GGML_Q4_K || t == CHATNET_GGML_Q5_K ||
-         t == CHATNET_GGML_Q6_K;
+  return t == CHATNET_GGML_F32 || t == CHATNET_GGML_F16 || t == CHATNET_GGML_Q4_0 || t == CHATNET_GGML_Q8_0 ||
+         t == CHATNET_GGML_Q4_K || t == CHATNET_GGML_Q5_K || t == CHATNET_GGML_Q6_K;
 }
 
 // Workspace of chatnet_matmul's batched path (bf16 copy of x + K-split
 // partials), one per (device, stream): work queued on one stream runs in
-// order, so calls sharing a stream can share it.  Grown on demand (after
-// draining that stream) and kept until the process ends.
+// order, so calls sharing a stream can share it.  Grown on demand and kept
+// until the process ends; a buffer it outgrows is retired, not freed, because
+// a graph the caller captured earlier may still read it.  Growing needs a
+// hipMalloc, which a stream under capture cannot take: a capturing caller gets
+// an error unless an uncaptured call of the same or a larger size came first.
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, std::pair<char*, size_t>> g_ws;
+std::vector<char*> g_ws_retired;
 
 int matmul_workspace(int dev, hipStream_t st, size_t bytes, char** out) {
   std::lock_guard<std::mutex> lk(g_ws_mu);
   auto& e = g_ws[{dev, st}];
   if (e.second < bytes) {
-    if (e.first) {
-      HIP_TRY(hipStreamSynchronize(st));
-      (void)hipFree(e.first);
-      e = {nullptr, 0};
-    }
-    if (hipMalloc((void**)&e.first, bytes) != hipSuccess) {
-      e = {nullptr, 0};
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(st, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+      return fail(CHATNET_ERR_INVALID_ARG,
+                  "chatnet_matmul: the stream is capturing and its workspace (%zu bytes) is smaller than the %zu "
+                  "this call needs; make one uncaptured call of this size first",
+                  e.second, bytes);
+    char* p = nullptr;
+    if (hipMalloc((void**)&p, bytes) != hipSuccess)
       return fail(CHATNET_ERR_OUT_OF_MEMORY, "hipMalloc of %zu bytes (matmul workspace) failed", bytes);
-    }
-    e.second = bytes;
+    if (e.first) g_ws_retired.push_back(e.first);
+    e = {p, bytes};
   }
   *out = e.first;
   return CHATNET_OK;
@@ -116,7 +122,8 @@ struct chatnet_model {
   void* kcache = nullptr;
   void* vcache = nullptr;
   float *x = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr;
-  int* state = nullptr;  // [0] pos, [1] token, [2] step
+  float* gu = nullptr;  // [2][hidden]: gate and up of a layer whose two types differ
+  int* state = nullptr;  // device decode state, kDecWords ints (kernels.h)
   float* attn_part_o = nullptr;   // split partials of the decode attention
   float* attn_part_ml = nullptr;
   int attn_splits_max = 1;  // most chunks any decode-attention launch uses
@@ -340,8 +347,9 @@ int chatnet_create(const chatnet_config* cfg, int device, chatnet_model** out) {
       {(void**)&m->q, sizeof(float) * c.dim},
       {(void**)&m->att, sizeof(float) * c.dim},
       {(void**)&m->h, sizeof(float) * c.hidden_dim},
+      {(void**)&m->gu, sizeof(float) * 2 * c.hidden_dim},
       {(void**)&m->logits, sizeof(float) * c.vocab_size},
-      {(void**)&m->state, sizeof(int) * 4},
+      {(void**)&m->state, sizeof(int) * kDecWords},
       {(void**)&m->attn_part_o, sizeof(float) * attn_slots * c.head_dim},
       {(void**)&m->attn_part_ml, sizeof(float) * attn_slots * 2},
       {(void**)&m->rope, sizeof(float2) * (size_t)c.context_length * (c.head_dim / 2)},
@@ -356,7 +364,7 @@ int chatnet_create(const chatnet_config* cfg, int device, chatnet_model** out) {
   }
   // Zero the caches once so unwritten positions hold 0 like the managed arrays.
   if (hipMemset(m->kcache, 0, kv_bytes) != hipSuccess || hipMemset(m->vcache, 0, kv_bytes) != hipSuccess ||
-      hipMemset(m->state, 0, sizeof(int) * 4) != hipSuccess) {
+      hipMemset(m->state, 0, sizeof(int) * kDecWords) != hipSuccess) {
     cleanup();
     return fail(CHATNET_ERR_HIP, "hipMemset failed");
   }
@@ -383,7 +391,7 @@ void chatnet_destroy(chatnet_model* m) {
     fr(l.attn_norm.ptr); fr(l.ffn_norm.ptr); fr(l.wq.ptr); fr(l.wk.ptr); fr(l.wv.ptr);
     fr(l.wo.ptr); fr(l.wg.ptr); fr(l.wu.ptr); fr(l.wd.ptr); fr(l.bias);
   }
-  fr(m->kcache); fr(m->vcache); fr(m->x); fr(m->q); fr(m->att); fr(m->h); fr(m->logits);
+  fr(m->kcache); fr(m->vcache); fr(m->x); fr(m->q); fr(m->att); fr(m->h); fr(m->gu); fr(m->logits);
   fr(m->state); fr(m->out_tokens);
   fr(m->attn_part_o); fr(m->attn_part_ml); fr(m->rope);
   fr(m->sparams); fr(m->sample_p); fr(m->draws);
@@ -452,8 +460,8 @@ int chatnet_upload_tensor(chatnet_model* m, const char* name, uint32_t type, con
                 (unsigned long long)want1);
   if (matrix) {
     if (!is_matrix_type(type))
-      return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "tensor %s: weight type %u not supported (Q4_0, Q8_0, Q4_K, Q5_K, Q6_K)",
-                  name, type);
+      return fail(CHATNET_ERR_UNSUPPORTED_TYPE,
+                  "tensor %s: weight type %u not supported (F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K)", name, type);
     if (!gemv_supports((int)type, (int)ne0))
       return fail(CHATNET_ERR_INVALID_ARG, "tensor %s: inner dim %llu not a multiple of the block", name,
                   (unsigned long long)ne0);
@@ -499,10 +507,10 @@ int check_complete(const chatnet_model* m) {
   if (!m->out_norm.ptr) return fail(CHATNET_ERR_NOT_FOUND, "tensor output_norm.weight not uploaded");
   if (!m->out.ptr && (!is_matrix_type(m->emb.type) || !gemv_supports((int)m->emb.type, m->cfg.dim))) {
     // LlamaWeights.cs:89-98 / QwenWeights.cs:103-112 fall back to the tied
-    // embedding; the LM head runs on the quantized GEMV only.
-    return fail(CHATNET_ERR_UNSUPPORTED_TYPE,
-                "output.weight missing: the tied token_embd.weight (type %u) cannot be the LM head (Q4_0, Q8_0)",
-                m->emb.type);
+    // embedding, which the GEMV then reads as the LM head
+    return fail(CHATNET_ERR_INVALID_ARG,
+                "output.weight missing: the tied token_embd.weight (type %u) cannot be the LM head at dim %d",
+                m->emb.type, m->cfg.dim);
   }
   for (size_t l = 0; l < m->layers.size(); l++) {
     const Layer& L = m->layers[l];
@@ -523,9 +531,10 @@ int check_complete(const chatnet_model* m) {
 // output.weight, or the tied embedding when it is absent (LlamaWeights.cs:89-98).
 const DevTensor& lm_head_tensor(const chatnet_model* m) { return m->out.ptr ? m->out : m->emb; }
 
-GemvArgs base_args(const chatnet_model* m) {
+GemvArgs base_args(const chatnet_model* m, bool decode = false) {
   GemvArgs a;
   memset(&a, 0, sizeof(a));
+  a.stop = decode ? m->state + kDecStop : nullptr;
   a.eps = m->cfg.rms_norm_eps;
   a.pos = m->state;
   a.head_dim = m->cfg.head_dim;
@@ -536,8 +545,10 @@ GemvArgs base_args(const chatnet_model* m) {
 }
 
 // Launches the forward of the token held in m->state (pos, token); the
-// attention covers sequence lengths up to cap (the position's bucket).
-int launch_token(chatnet_model* m, bool lm_head, int cap) {
+// attention covers sequence lengths up to cap (the position's bucket).  In a
+// decode loop (`decode`) every launch but the embedding gather exits early
+// once the loop's stop flag is set.
+int launch_token(chatnet_model* m, bool lm_head, int cap, bool decode = false) {
   const chatnet_config& c = m->cfg;
   hipStream_t st = m->stream;
   const int kvd = m->kv_dim;
@@ -545,7 +556,7 @@ int launch_token(chatnet_model* m, bool lm_head, int cap) {
   for (int l = 0; l < c.n_layers; l++) {
     const Layer& L = m->layers[l];
     const size_t loff = (size_t)l * c.context_length * kvd * m->kv_elt;
-    GemvArgs a = base_args(m);
+    GemvArgs a = base_args(m, decode);
     a.K = c.dim;
     a.x = m->x;
     a.norm_w = (const float*)L.attn_norm.ptr;
@@ -597,9 +608,10 @@ int launch_token(chatnet_model* m, bool lm_head, int cap) {
     at.part_ml = m->attn_part_ml;
     // a few chunks are combined by the O GEMV as it stages x (no merge launch)
     at.fold = plan.splits > 1 && plan.splits <= kFoldMaxSplits;
+    at.stop = a.stop;
     HIP_TRY(attn_decode_launch(at, st));
 
-    GemvArgs o = base_args(m);
+    GemvArgs o = base_args(m, decode);
     o.K = c.dim;
     o.x = m->att;
     o.w[0] = (const uint8_t*)L.wo.ptr;
@@ -614,21 +626,34 @@ int launch_token(chatnet_model* m, bool lm_head, int cap) {
     }
     HIP_TRY(gemv_launch((int)L.wo.type, at.fold ? GEMV_EPI_ADD_MERGE : GEMV_EPI_ADD, o, m->num_cus, st));
 
-    if (L.wg.type != L.wu.type)
-      return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "layer %d: ffn_gate and ffn_up types differ", l);
-    GemvArgs g = base_args(m);
+    GemvArgs g = base_args(m, decode);
     g.K = c.dim;
     g.x = m->x;
     g.norm_w = (const float*)L.ffn_norm.ptr;
-    g.w[0] = (const uint8_t*)L.wg.ptr;
-    g.w[1] = (const uint8_t*)L.wu.ptr;
-    g.seg_rows[0] = c.hidden_dim;
-    g.seg_rows[1] = c.hidden_dim;
-    g.n_vrows = 2 * c.hidden_dim;
-    g.out[0] = m->h;
-    HIP_TRY(gemv_launch((int)L.wg.type, GEMV_EPI_SWIGLU, g, m->num_cus, st));
+    if (L.wg.type == L.wu.type) {  // one launch, gate and up rows interleaved
+      g.w[0] = (const uint8_t*)L.wg.ptr;
+      g.w[1] = (const uint8_t*)L.wu.ptr;
+      g.seg_rows[0] = c.hidden_dim;
+      g.seg_rows[1] = c.hidden_dim;
+      g.n_vrows = 2 * c.hidden_dim;
+      g.out[0] = m->h;
+      HIP_TRY(gemv_launch((int)L.wg.type, GEMV_EPI_SWIGLU, g, m->num_cus, st));
+    } else {
+      // gate and up of different types (each dispatched on its own type,
+      // LlamaModel.cs:175-179): two normed GEMVs, then SiLU(gate) * up
+      const DevTensor* ts[2] = {&L.wg, &L.wu};
+      for (int s = 0; s < 2; s++) {
+        GemvArgs b = g;
+        b.w[0] = b.w[1] = b.w[2] = (const uint8_t*)ts[s]->ptr;
+        b.seg_rows[0] = c.hidden_dim;
+        b.n_vrows = c.hidden_dim;
+        b.out[0] = m->gu + (size_t)s * c.hidden_dim;
+        HIP_TRY(gemv_launch((int)ts[s]->type, GEMV_EPI_LOGITS, b, m->num_cus, st));
+      }
+      HIP_TRY(silu_mul_launch(m->gu, m->gu + c.hidden_dim, m->h, c.hidden_dim, st));
+    }
 
-    GemvArgs d = base_args(m);
+    GemvArgs d = base_args(m, decode);
     d.K = c.hidden_dim;
     d.x = m->h;
     d.w[0] = (const uint8_t*)L.wd.ptr;
@@ -638,7 +663,7 @@ int launch_token(chatnet_model* m, bool lm_head, int cap) {
     HIP_TRY(gemv_launch((int)L.wd.type, GEMV_EPI_ADD, d, m->num_cus, st));
   }
   if (lm_head) {
-    GemvArgs o = base_args(m);  // final RMSNorm fused (LlamaModel.cs:203-213)
+    GemvArgs o = base_args(m, decode);  // final RMSNorm fused (LlamaModel.cs:203-213)
     o.K = c.dim;
     o.x = m->x;
     o.norm_w = (const float*)m->out_norm.ptr;
@@ -881,6 +906,63 @@ int run_prompt(chatnet_model* m, const int32_t* tokens, int n, int position) {
   return CHATNET_OK;
 }
 
+// chatnet_matmul: the batched path's scratch (bf16 x, then the K-split
+// partials) comes from the per-stream workspace.
+int matmul_impl(uint32_t type, const void* w_dev, const float* x_dev, float* y_dev, int M, int K, int N,
+                void* stream) {
+  if (!w_dev || !x_dev || !y_dev) return fail(CHATNET_ERR_INVALID_ARG, "null device pointer");
+  if (M <= 0 || K <= 0 || N <= 0) return fail(CHATNET_ERR_INVALID_ARG, "M, K, N must be positive");
+  if (!is_matrix_type(type)) return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "matmul type %u not supported", type);
+  if (!gemv_supports((int)type, K))
+    return fail(CHATNET_ERR_INVALID_ARG, "K=%d not supported for type %u (block multiple, at most 16384)", K, type);
+  if ((reinterpret_cast<uintptr_t>(w_dev) & 15) || (reinterpret_cast<uintptr_t>(x_dev) & 15))
+    return fail(CHATNET_ERR_INVALID_ARG, "w_dev and x_dev must be 16-byte aligned");
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  const int cus = device_cus(dev);
+  hipStream_t st = (hipStream_t)stream;
+  if (N >= 8 && gemm_supports((int)type, K)) {
+    // x -> bf16 into the scratch, then the MFMA GEMM (K-split partials after x).
+    const size_t xb_bytes = ((size_t)N * K * sizeof(uint16_t) + 255) & ~(size_t)255;
+    const size_t part_bytes = gemm_workspace_bytes(M, N, K, cus, false);
+    char* ws = nullptr;
+    int rc;
+    rc = matmul_workspace(dev, st, xb_bytes + part_bytes, &ws);
+    if (rc) return rc;
+    HIP_TRY(to_bf16_launch(x_dev, (uint16_t*)ws, (size_t)N * K, st));
+    GemmArgs g;
+    memset(&g, 0, sizeof(g));
+    g.qtype = (int)type;
+    g.w[0] = g.w[1] = g.w[2] = (const uint8_t*)w_dev;
+    g.seg_rows[0] = M;
+    g.seg_mode = GEMM_SEG_SINGLE;
+    g.M = M;
+    g.K = K;
+    g.N = N;
+    g.xb = (const uint16_t*)ws;
+    g.epi = GEMV_EPI_STORE;
+    g.y = y_dev;
+    g.ldy = M;
+    g.part = part_bytes ? (float*)(ws + xb_bytes) : nullptr;
+    HIP_TRY(gemm_launch(g, cus, st));
+    g_err.clear();
+    return CHATNET_OK;
+  }
+  for (int n = 0; n < N; n++) {  // one fused GEMV per column, no scratch
+    GemvArgs a;
+    memset(&a, 0, sizeof(a));
+    a.w[0] = a.w[1] = a.w[2] = (const uint8_t*)w_dev;
+    a.seg_rows[0] = M;
+    a.n_vrows = M;
+    a.K = K;
+    a.x = x_dev + (size_t)n * K;
+    a.out[0] = y_dev + (size_t)n * M;
+    HIP_TRY(gemv_launch((int)type, GEMV_EPI_STORE, a, cus, st));
+  }
+  g_err.clear();
+  return CHATNET_OK;
+}
+
 int validate_tokens(const chatnet_model* m, const int32_t* tokens, int n, int position) {
   if (!tokens || n <= 0) return fail(CHATNET_ERR_INVALID_ARG, "tokens must be non-empty");
   if (position < 0 || (long long)position + n > m->cfg.context_length)
@@ -941,49 +1023,61 @@ static int decode_loop(chatnet_model* m, int max_tokens, int32_t eos_token, int3
   int rc = check_complete(m);
   if (rc) return rc;
   HIP_TRY(hipSetDevice(m->device));
+  if (max_tokens == 0) {  // InferenceEngine.cs:256: the loop body never runs
+    g_err.clear();
+    return CHATNET_OK;
+  }
   const int ctx = m->cfg.context_length;
   const int p0 = m->next_pos;  // position of the first generated token
-  // InferenceEngine.cs:256-307: token i is emitted, then the loop stops if its
-  // position p0+i >= ctx-1; otherwise it is forwarded there and the next sampled.
+  // InferenceEngine.cs:256-307: token i is emitted unless it is EOS, then the
+  // loop stops if its position p0+i >= ctx-1; otherwise it is forwarded there
+  // and the next one sampled.  So at most `room` tokens are forwarded and
+  // room + 1 emitted (one, the first pick, when the cache is already full).
   const int room = ctx - 1 - p0;
-  int forwards = max_tokens < room ? max_tokens : (room > 0 ? room : 0);
-  int emitted = max_tokens < room + 1 ? max_tokens : room + 1;
-  if (emitted < 0) emitted = 0;
+  const int forwards = max_tokens < room ? max_tokens : (room > 0 ? room : 0);
+  const int emitted = max_tokens < (room > 0 ? room : 0) + 1 ? max_tokens : (room > 0 ? room : 0) + 1;
   if ((rc = ensure_out_tokens(m, max_tokens + 2))) return rc;
-  // step counter = 0, then sample the first token from the last forward's logits
+  // step counter = 0, stop flag cleared, then the first pick from the last
+  // forward's logits.  A pick of EOS sets the stop flag: every later launch of
+  // the loop returns early, so the cache, the logits and the state stay those
+  // of the last token forwarded before it (InferenceEngine.cs:258-261 breaks
+  // before forwarding EOS).
   auto pick = [m, sampled]() {
     return sampled ? sample_launch(m->logits, m->cfg.vocab_size, m->sparams, m->draws, m->state, m->out_tokens,
                                    m->out_cap, m->sample_p, m->stream)
                    : argmax_launch(m->logits, m->cfg.vocab_size, m->state, m->out_tokens, m->out_cap, m->stream);
   };
   hipGraphExec_t* graphs = sampled ? m->sgraphs : m->graphs;
-  HIP_TRY(set_state_launch(m->state, p0 - 1, m->last_tok, 0, m->stream));
+  HIP_TRY(set_state_launch(m->state, p0 - 1, m->last_tok, 0, m->stream, eos_token >= 0 ? eos_token : -1));
   HIP_TRY(pick());
   // CHATNET_DECODE_GRAPH=0 issues the same per-step launches directly instead
-  // of replaying the captured graph (profilers that cannot trace graph
-  // launches need this; the kernels and their order are identical).
+  // of replaying the captured graph (the kernels and their order are
+  // identical; kernel-trace profiles of the decode step are taken this way).
   const char* ge = getenv("CHATNET_DECODE_GRAPH");
   const bool use_graph = !(ge && ge[0] == '0');
   // Step i forwards the token at position p0+i (sequence length p0+i+1).
   if (forwards > 0 && !use_graph) {
     for (int i = 0; i < forwards; i++) {
-      if ((rc = launch_token(m, true, bucket_cap(m, p0 + i + 1)))) return rc;
+      if ((rc = launch_token(m, true, bucket_cap(m, p0 + i + 1), true))) return rc;
       HIP_TRY(pick());
     }
   } else if (forwards > 0) {
     for (int i = 0; i < forwards; i++) {
       const int k = bucket_index(m, p0 + i + 1);
       if (!graphs[k]) {
-        hipGraph_t g;
+        hipGraph_t g = nullptr;
         HIP_TRY(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
-        int lrc = launch_token(m, true, bucket_cap(m, p0 + i + 1));
-        hipError_t ae = pick();
-        hipError_t ee = hipStreamEndCapture(m->stream, &g);
+        const int lrc = launch_token(m, true, bucket_cap(m, p0 + i + 1), true);
+        const hipError_t ae = lrc ? hipSuccess : pick();
+        // the capture is always ended, so the stream leaves capture mode, and
+        // the graph it returns is destroyed on every path
+        const hipError_t ee = hipStreamEndCapture(m->stream, &g);
+        hipError_t ie = hipSuccess;
+        if (!lrc && ae == hipSuccess && ee == hipSuccess) ie = hipGraphInstantiate(&graphs[k], g, nullptr, nullptr, 0);
+        if (g) (void)hipGraphDestroy(g);
         if (lrc) return lrc;
         if (ae != hipSuccess) return fail(CHATNET_ERR_HIP, "sampler capture: %s", hipGetErrorString(ae));
         if (ee != hipSuccess) return fail(CHATNET_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(ee));
-        hipError_t ie = hipGraphInstantiate(&graphs[k], g, nullptr, nullptr, 0);
-        (void)hipGraphDestroy(g);
         if (ie != hipSuccess) {
           graphs[k] = nullptr;
           return fail(CHATNET_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(ie));
@@ -993,19 +1087,20 @@ static int decode_loop(chatnet_model* m, int max_tokens, int32_t eos_token, int3
     }
   }
   std::vector<int> buf((size_t)emitted + 2);
-  HIP_TRY(hipMemcpyAsync(buf.data(), m->out_tokens, sizeof(int) * (emitted + 1), hipMemcpyDeviceToHost, m->stream));
+  HIP_TRY(hipMemcpyAsync(buf.data(), m->out_tokens, sizeof(int) * emitted, hipMemcpyDeviceToHost, m->stream));
   HIP_TRY(hipStreamSynchronize(m->stream));
   int nout = 0;
-  for (int i = 0; i < emitted; i++) {
-    if (eos_token >= 0 && buf[i] == eos_token) break;  // InferenceEngine.cs:258-261
-    out_tokens[nout++] = buf[i];
+  while (nout < emitted && !(eos_token >= 0 && buf[nout] == eos_token)) {  // InferenceEngine.cs:258-261
+    out_tokens[nout] = buf[nout];
+    nout++;
   }
   *n_out = nout;
-  // the cache now holds positions < p0+forwards; the logits are those of the
-  // last forwarded token
-  if (forwards > 0) {
-    m->next_pos = p0 + forwards;
-    m->last_tok = buf[forwards - 1];
+  // tokens 0 .. done-1 were forwarded (EOS never is): the cache holds
+  // positions < p0 + done and the logits are those of token done-1
+  const int done = nout < forwards ? nout : forwards;
+  if (done > 0) {
+    m->next_pos = p0 + done;
+    m->last_tok = buf[done - 1];
   }
   g_err.clear();
   return CHATNET_OK;
@@ -1092,53 +1187,7 @@ int chatnet_net_random(int32_t seed, int n, double* out) {
 
 int chatnet_matmul(uint32_t type, const void* w_dev, const float* x_dev, float* y_dev, int M, int K, int N,
                    void* stream) {
-  if (!w_dev || !x_dev || !y_dev) return fail(CHATNET_ERR_INVALID_ARG, "null device pointer");
-  if (M <= 0 || K <= 0 || N <= 0) return fail(CHATNET_ERR_INVALID_ARG, "M, K, N must be positive");
-  if (!is_matrix_type(type)) return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "matmul type %u not supported", type);
-  if (!gemv_supports((int)type, K)) return fail(CHATNET_ERR_INVALID_ARG, "K=%d not a multiple of the block size", K);
-  int dev = 0;
-  HIP_TRY(hipGetDevice(&dev));
-  const int cus = device_cus(dev);
-  hipStream_t st = (hipStream_t)stream;
-  if (N >= 8 && gemm_supports((int)type, K)) {
-    // x -> bf16 into the stream's workspace, then the MFMA GEMM.
-    const size_t xb_bytes = ((size_t)N * K * sizeof(uint16_t) + 255) & ~(size_t)255;
-    const size_t part_bytes = gemm_workspace_bytes(M, N, K, cus, false);
-    char* ws = nullptr;
-    int rc = matmul_workspace(dev, st, xb_bytes + part_bytes, &ws);
-    if (rc) return rc;
-    HIP_TRY(to_bf16_launch(x_dev, (uint16_t*)ws, (size_t)N * K, st));
-    GemmArgs g;
-    memset(&g, 0, sizeof(g));
-    g.qtype = (int)type;
-    g.w[0] = g.w[1] = g.w[2] = (const uint8_t*)w_dev;
-    g.seg_rows[0] = M;
-    g.seg_mode = GEMM_SEG_SINGLE;
-    g.M = M;
-    g.K = K;
-    g.N = N;
-    g.xb = (const uint16_t*)ws;
-    g.epi = GEMV_EPI_STORE;
-    g.y = y_dev;
-    g.ldy = M;
-    g.part = part_bytes ? (float*)(ws + xb_bytes) : nullptr;
-    HIP_TRY(gemm_launch(g, cus, st));
-    g_err.clear();
-    return CHATNET_OK;
-  }
-  for (int n = 0; n < N; n++) {
-    GemvArgs a;
-    memset(&a, 0, sizeof(a));
-    a.w[0] = a.w[1] = a.w[2] = (const uint8_t*)w_dev;
-    a.seg_rows[0] = M;
-    a.n_vrows = M;
-    a.K = K;
-    a.x = x_dev + (size_t)n * K;
-    a.out[0] = y_dev + (size_t)n * M;
-    HIP_TRY(gemv_launch((int)type, GEMV_EPI_STORE, a, cus, st));
-  }
-  g_err.clear();
-  return CHATNET_OK;
+  return matmul_impl(type, w_dev, x_dev, y_dev, M, K, N, stream);
 }
 
 }  // extern "C"

@@ -135,6 +135,7 @@ __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
   __shared__ float so[NW * HPW * HD];
   __shared__ float sml[NW * HPW * 2];
   const int seq = *a.pos + 1;
+  if (a.stop && *a.stop) return;
 
   for (int jg = 0; jg < a.kv_mul; jg += WH * HPW) {
     const int jb = jg + hw * HPW;                      // the wave's first head of this pass
@@ -302,6 +303,7 @@ __global__ __launch_bounds__(CN_BLOCK) void attn_merge_kernel(AttnArgs a) {
   constexpr int G = CN_BLOCK / HD;
   __shared__ float sm[G][HD], sl[G], so[G][HD];
   const int h = blockIdx.x, d = threadIdx.x % HD, g = threadIdx.x / HD;
+  if (a.stop && *a.stop) return;
   const int s_eff = attn_active_splits(a, *a.pos + 1);
   const size_t base = (size_t)h * a.splits;
   float M = -INFINITY, L = 0.f, acc = 0.f;
@@ -363,10 +365,13 @@ __global__ __launch_bounds__(CN_BLOCK) void attn_merge_kernel(AttnArgs a) {
 
 // GreedySampler.Sample: strict '>' scan => the lowest index of the maximum;
 // NaN never wins unless it sits at index 0, in which case the answer is 0.
+// A decode-loop pick (out_tokens given) does nothing once the loop has
+// stopped, and stops it when the winner is the EOS token.
 __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, int n, int* state,
                                                       int* out_tokens, int out_cap) {
   __shared__ float bv[16];
   __shared__ int bi[16];
+  if (out_tokens && state[kDecStop]) return;
   float best = -INFINITY;
   int idx = 0x7FFFFFFF;
   for (int i = threadIdx.x; i < n; i += 1024) {
@@ -400,18 +405,33 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, int n
         idx = bi[w];
       }
     if (idx == 0x7FFFFFFF || logits[0] != logits[0]) idx = 0;
-    state[1] = idx;
-    const int step = state[2];
-    if (out_tokens && step < out_cap) out_tokens[step] = idx;
-    state[2] = step + 1;
-    state[0] = state[0] + 1;
+    state[kDecTok] = idx;
+    if (out_tokens) {
+      const int step = state[kDecStep];
+      if (step < out_cap) out_tokens[step] = idx;
+      state[kDecStep] = step + 1;
+      if (idx == state[kDecEos]) state[kDecStop] = 1;
+    }
+    state[kDecPos] = state[kDecPos] + 1;
   }
 }
 
-__global__ void set_state_kernel(int* state, int pos, int tok, int step) {
-  state[0] = pos;
-  state[1] = tok;
-  if (step >= 0) state[2] = step;
+__global__ __launch_bounds__(CN_BLOCK) void silu_mul_kernel(const float* g, const float* u, float* h, int n) {
+  const int i = blockIdx.x * CN_BLOCK + threadIdx.x;
+  if (i < n) {
+    const float gv = g[i];
+    h[i] = (gv / (1.0f + expf(-gv))) * u[i];
+  }
+}
+
+__global__ void set_state_kernel(int* state, int pos, int tok, int step, int eos) {
+  state[kDecPos] = pos;
+  state[kDecTok] = tok;
+  if (step >= 0) {
+    state[kDecStep] = step;
+    state[kDecStop] = 0;
+    state[kDecEos] = eos;
+  }
 }
 
 // Heads per wave and pass for a group of kv_mul query heads (four waves split
@@ -476,7 +496,13 @@ hipError_t argmax_launch(const float* logits, int n, int* state, int* out_tokens
   return hipGetLastError();
 }
 
-hipError_t set_state_launch(int* state, int pos, int tok, int step, hipStream_t st) {
-  hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(1), 0, st, state, pos, tok, step);
+hipError_t set_state_launch(int* state, int pos, int tok, int step, hipStream_t st, int eos) {
+  hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(1), 0, st, state, pos, tok, step, eos);
+  return hipGetLastError();
+}
+
+hipError_t silu_mul_launch(const float* g, const float* u, float* h, int n, hipStream_t st) {
+  if (n <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((n + CN_BLOCK - 1) / CN_BLOCK), dim3(CN_BLOCK), 0, st, g, u, h, n);
   return hipGetLastError();
 }

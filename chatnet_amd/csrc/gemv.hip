@@ -29,6 +29,7 @@
 //   QKV     RoPE on q/k pairs + K/V cache write  (TensorMath.ApplyRoPE :408-458, LlamaModel.cs:146-153)
 //   SWIGLU  h[r] = silu(gate[r]) * up[r]         (TensorMath.SiluElementwiseMul :253-286)
 #include "device_common.h"
+#include "gemv_common.h"
 #include "kernels.h"
 
 namespace {
@@ -87,97 +88,6 @@ constexpr int XD_UNIT_DW = 44;
 // sum_d 16^d E_d = X + 0x88888, so the nibbles of (X + 0x88888) are the E_d and
 // XOR 8 turns each into D_d = E_d - 8 as a signed nibble.  Valid for
 // X in [-0x88888, 0x77777], which |X| <= 2^18 satisfies.
-
-// x read from the decode attention's per-chunk partials (ADD_MERGE): element
-// i belongs to head i / hd; each active chunk c (c < s_eff) holds the running
-// max M_c, sum L_c and unnormalised output O_c of its positions, and
-//   x = sum_c O_c e^(M_c - M) / sum_c L_c e^(M_c - M),  M = max_c M_c
-// (attn_merge_kernel's combination).  Every chunk's loads are issued (their
-// addresses do not depend on the position); inactive ones are masked.  The
-// weights e^(M_c - M) and the sum depend on the head only: the base-256
-// staging (16-element groups of one head) computes them once per group.
-struct MergeSrc {
-  const float* o;
-  const float* ml;
-  int hd, splits, s_eff;
-};
-
-// Elements i .. i+3 combined in one round trip: every chunk's (max, sum) and
-// outputs are loaded together, then folded.  Used by the base-16 staging,
-// whose items (two float4 of one head) gain nothing from sharing the weights.
-__device__ __forceinline__ float4 merged_x4(const MergeSrc& m, int i) {
-  const int h = i / m.hd, d = i - h * m.hd;
-  const size_t base = (size_t)h * m.splits;
-  float2 ml[kFoldMaxSplits];
-  float4 oc[kFoldMaxSplits];
-  float M = -INFINITY;
-#pragma unroll
-  for (int c = 0; c < kFoldMaxSplits; c++) {
-    const bool in = c < m.splits;
-    ml[c] = in ? *reinterpret_cast<const float2*>(m.ml + 2 * (base + c)) : make_float2(0.f, 0.f);
-    oc[c] = in ? *reinterpret_cast<const float4*>(m.o + (base + c) * m.hd + d) : make_float4(0.f, 0.f, 0.f, 0.f);
-    if (c >= m.s_eff) ml[c].y = 0.f;
-    if (ml[c].y > 0.f) M = fmaxf(M, ml[c].x);
-  }
-  float L = 0.f;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-  for (int c = 0; c < kFoldMaxSplits; c++) {
-    if (ml[c].y > 0.f) {
-      const float f = expf(ml[c].x - M);
-      L += ml[c].y * f;
-      acc.x += oc[c].x * f;
-      acc.y += oc[c].y * f;
-      acc.z += oc[c].z * f;
-      acc.w += oc[c].w * f;
-    }
-  }
-  return make_float4(acc.x / L, acc.y / L, acc.z / L, acc.w / L);
-}
-
-// Chunk weights of head h: f[c] = e^(M_c - M) for active chunks that hold
-// positions (0 otherwise) and their sum L = sum_c L_c f[c].
-struct MergeW {
-  float f[kFoldMaxSplits];
-  float L;
-};
-
-__device__ __forceinline__ MergeW merge_weights(const MergeSrc& m, int h) {
-  const size_t base = (size_t)h * m.splits;
-  float2 ml[kFoldMaxSplits];
-  float M = -INFINITY;
-#pragma unroll
-  for (int c = 0; c < kFoldMaxSplits; c++) {
-    ml[c] = c < m.splits ? *reinterpret_cast<const float2*>(m.ml + 2 * (base + c)) : make_float2(0.f, 0.f);
-    if (c >= m.s_eff) ml[c].y = 0.f;
-    if (ml[c].y > 0.f) M = fmaxf(M, ml[c].x);
-  }
-  MergeW w;
-  w.L = 0.f;
-#pragma unroll
-  for (int c = 0; c < kFoldMaxSplits; c++) {
-    w.f[c] = ml[c].y > 0.f ? expf(ml[c].x - M) : 0.f;
-    w.L += ml[c].y * w.f[c];
-  }
-  return w;
-}
-
-// Elements d .. d+3 of head h combined with the chunk weights.
-__device__ __forceinline__ float4 merge_apply(const MergeSrc& m, const MergeW& w, int h, int d) {
-  const size_t base = (size_t)h * m.splits;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-  for (int c = 0; c < kFoldMaxSplits; c++) {
-    if (c < m.splits) {
-      const float4 o = *reinterpret_cast<const float4*>(m.o + (base + c) * m.hd + d);
-      acc.x += o.x * w.f[c];
-      acc.y += o.y * w.f[c];
-      acc.z += o.z * w.f[c];
-      acc.w += o.w * w.f[c];
-    }
-  }
-  return make_float4(acc.x / w.L, acc.y / w.L, acc.z / w.L, acc.w / w.L);
-}
 
 // x (and the RMSNorm weight) of the MAXT work items a thread stages.
 // Work item t = (block t/4, dword k = t%4) holds x[32b+4k..+3] and
@@ -775,135 +685,6 @@ __device__ __forceinline__ void dot_unit_k45_dig8(const uint32_t (*w)[QTraits<QT
   }
 }
 
-// Segment base pointer and row count by run-time segment index, chosen with
-// masks: indexing the kernel-argument arrays (or a select chain, which the
-// compiler turns into a table) would copy them to scratch, and a scratch load
-// waits on every vector-memory operation in flight.
-__device__ __forceinline__ const uint8_t* seg_w(const GemvArgs& a, int seg) {
-  const uintptr_t w0 = reinterpret_cast<uintptr_t>(a.w[0]);
-  const uintptr_t w1 = reinterpret_cast<uintptr_t>(a.w[1]);
-  const uintptr_t w2 = reinterpret_cast<uintptr_t>(a.w[2]);
-  const uintptr_t m1 = 0 - (uintptr_t)(seg == 1), m2 = 0 - (uintptr_t)(seg == 2);
-  return reinterpret_cast<const uint8_t*>(w0 ^ ((w0 ^ w1) & m1) ^ ((w0 ^ w2) & m2));
-}
-__device__ __forceinline__ int seg_n(const GemvArgs& a, int seg) {
-  return seg == 0 ? a.seg_rows[0] : (seg == 1 ? a.seg_rows[1] : a.seg_rows[2]);
-}
-
-// Virtual row -> (segment, row-in-segment).
-template <int EPI>
-__device__ __forceinline__ void map_row(const GemvArgs& a, int vr, int& seg, int& r) {
-  if constexpr (EPI == GEMV_EPI_SWIGLU) {
-    seg = vr & 1;
-    r = vr >> 1;
-  } else if constexpr (EPI == GEMV_EPI_QKV) {
-    if (vr < a.seg_rows[0]) { seg = 0; r = vr; }
-    else if (vr < a.seg_rows[0] + a.seg_rows[1]) { seg = 1; r = vr - a.seg_rows[0]; }
-    else { seg = 2; r = vr - a.seg_rows[0] - a.seg_rows[1]; }
-  } else {
-    seg = 0;
-    r = vr;
-  }
-}
-
-// What an epilogue reads besides the dot products, loaded by the lane that
-// finishes the rows together with the weights of the same iteration, so the
-// epilogue does not wait on a load issued behind the next iteration's weights:
-//   ADD: the residual rows;
-//   QKV: (cos, sin) of each q/k row pair at position pos from the RoPE table
-//        (TensorMath.ApplyRoPE's angle, TensorMath.cs:418-432), the pair index
-//        being the row's offset within its head, in res[0..RPW); with a bias
-//        (QwenModel.cs:104-120) the rows' biases in res[RPW..2*RPW).
-template <int EPI, int RPW>
-constexpr int res_count() { return EPI == GEMV_EPI_QKV ? 2 * RPW : RPW; }
-
-template <int EPI, int RPW, int NR>
-__device__ __forceinline__ void load_residual(const GemvArgs& a, int vr0, int li, int pos, float (&res)[NR]) {
-#pragma unroll
-  for (int i = 0; i < NR; i++) res[i] = 0.f;
-  if (li != 0) return;
-  if constexpr (EPI == GEMV_EPI_ADD || EPI == GEMV_EPI_ADD_MERGE) {
-#pragma unroll
-    for (int i = 0; i < RPW; i++) {
-      const int vr = vr0 + i;
-      if (vr < a.n_vrows) res[i] = a.out[0][vr];
-    }
-  } else if constexpr (EPI == GEMV_EPI_QKV) {
-#pragma unroll
-    for (int i = 0; i < RPW; i += 2) {
-      const int vr = vr0 + i;
-      int seg, r;
-      map_row<EPI>(a, vr, seg, r);
-      if (vr < a.n_vrows && seg < 2) {
-        const float2 cs = a.rope[(size_t)pos * (a.head_dim / 2) + (r % a.head_dim) / 2];
-        res[i] = cs.x;
-        res[i + 1] = cs.y;
-      }
-      if (vr < a.n_vrows && a.bias) {
-        const float2 b = *reinterpret_cast<const float2*>(a.bias + vr);
-        res[RPW + i] = b.x;
-        res[RPW + i + 1] = b.y;
-      }
-    }
-  }
-}
-
-// pos: the device-side position (QKV), read at kernel start; res: what
-// load_residual fetched for these rows.
-template <int EPI, int RPW>
-__device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, const float* v, const float* res, int pos) {
-#pragma unroll
-  for (int i = 0; i < RPW; i += 2) {
-    const int vr = vr0 + i;
-    if (vr >= a.n_vrows) return;
-    int seg, r;
-    map_row<EPI>(a, vr, seg, r);
-    if constexpr (EPI == GEMV_EPI_STORE || EPI == GEMV_EPI_LOGITS) {
-      a.out[0][r] = v[i];
-      if (vr + 1 < a.n_vrows) a.out[0][r + 1] = v[i + 1];
-    } else if constexpr (EPI == GEMV_EPI_ADD || EPI == GEMV_EPI_ADD_MERGE) {
-      a.out[0][r] = res[i] + v[i];
-      if (vr + 1 < a.n_vrows) a.out[0][r + 1] = res[i + 1] + v[i + 1];
-    } else if constexpr (EPI == GEMV_EPI_SWIGLU) {
-      const float g = v[i], u = v[i + 1];
-      a.out[0][r] = (g / (1.0f + expf(-g))) * u;
-    } else {  // QKV
-      float x0 = v[i], x1 = v[i + 1];
-      if (a.bias) {  // q/k/v += bias before RoPE (QwenModel.cs:104-125)
-        x0 += res[RPW + i];
-        x1 += res[RPW + i + 1];
-      }
-      if (seg < 2) {
-        const float c = res[i], s = res[i + 1];
-        const float y0 = x0 * c - x1 * s;
-        const float y1 = x0 * s + x1 * c;
-        x0 = y0;
-        x1 = y1;
-      }
-      if (seg == 0) {
-        a.out[0][r] = x0;
-        a.out[0][r + 1] = x1;
-      } else {
-        const size_t off = (size_t)pos * a.kv_dim + r;
-        // K or V cache base chosen arithmetically: a select of the two pointer
-        // arguments compiles to a scratch table whose load waits on every
-        // vector-memory operation in flight
-        const uintptr_t kb = reinterpret_cast<uintptr_t>(a.kcache), vb = reinterpret_cast<uintptr_t>(a.vcache);
-        const uintptr_t base = vb + ((kb - vb) & (uintptr_t)(0 - (uintptr_t)(seg == 1)));
-        if (a.kv_f16) {
-          _Float16* dst = reinterpret_cast<_Float16*>(base) + off;
-          dst[0] = (_Float16)x0;
-          dst[1] = (_Float16)x1;
-        } else {
-          float* dst = reinterpret_cast<float*>(base) + off;
-          dst[0] = x0;
-          dst[1] = x1;
-        }
-      }
-    }
-  }
-}
-
 // Issues the loads of one wave iteration: RPW rows x NU units per lane.
 template <int QT, int RPW, int LPR, int NU, int EPI>
 __device__ __forceinline__ void issue_loads(const GemvArgs& a, int it, int sub, int li, int nunits, size_t bpr,
@@ -959,6 +740,8 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
   constexpr int NR = res_count<EPI, RPW>();
   float res[NR];
   const int pos = EPI == GEMV_EPI_QKV ? *a.pos : 0;
+  // read with the first loads, tested after staging (uniform across the grid)
+  const int stopped = a.stop ? *a.stop : 0;
   constexpr bool MERGE = EPI == GEMV_EPI_ADD_MERGE;
   MergeSrc ms{};
   if constexpr (MERGE) {
@@ -1014,6 +797,7 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int v = 0; v < NWV; v++) ss += xred[v];
     const float rms = NORM ? 1.0f / sqrtf(ss / (float)K + a.eps) : 1.0f;
+    if (stopped) return;
     while (it < n_iters) {
       float acc[RPW];
 #pragma unroll
@@ -1165,17 +949,32 @@ GemvShape pick_shape(int K, int n_vrows, int num_cus, bool allow8, bool isolated
   return s;
 }
 
+// One instantiation's launch.  The base-256 digit records of rows longer than
+// 15872 take more than 64 KB of LDS, which must be allowed explicitly (once
+// per kernel).
+template <int QT, int RPW, int LPR, int NU, int EPI, int BS>
+hipError_t launch_one(const GemvArgs& a, int grid, size_t smem, hipStream_t st) {
+  const auto kern = &gemv_kernel<QT, RPW, LPR, NU, EPI, BS>;
+  if (smem > 65536) {
+    static bool lds_set = false;
+    if (!lds_set) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+      if (e != hipSuccess) return e;
+      lds_set = true;
+    }
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(BS), smem, st, a);
+  return hipGetLastError();
+}
+
 template <int QT, int RPW, int NU, int EPI, int BS>
 hipError_t launch_k(const GemvArgs& a, int lpr, int grid, size_t smem, hipStream_t st) {
   if constexpr (QT != QT_Q4_0) {
-    if (lpr == 16) {
-      hipLaunchKernelGGL((gemv_kernel<QT, RPW, 16, NU, EPI, BS>), dim3(grid), dim3(BS), smem, st, a);
-      return hipGetLastError();
-    }
+    if (lpr == 16) return launch_one<QT, RPW, 16, NU, EPI, BS>(a, grid, smem, st);
   }
-  if (lpr == 32) hipLaunchKernelGGL((gemv_kernel<QT, RPW, 32, NU, EPI, BS>), dim3(grid), dim3(BS), smem, st, a);
-  else hipLaunchKernelGGL((gemv_kernel<QT, RPW, 64, NU, EPI, BS>), dim3(grid), dim3(BS), smem, st, a);
-  return hipGetLastError();
+  if (lpr == 32) return launch_one<QT, RPW, 32, NU, EPI, BS>(a, grid, smem, st);
+  return launch_one<QT, RPW, 64, NU, EPI, BS>(a, grid, smem, st);
 }
 
 template <int QT, int RPW, int NU, int EPI>
@@ -1214,6 +1013,7 @@ __global__ __launch_bounds__(BS) void gemv_ks_kernel(GemvArgs a) {
 
   uint32_t w[RPW][9];
   float res[NR];
+  const int stopped = a.stop ? *a.stop : 0;
   auto load = [&](int itn) {
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
@@ -1237,6 +1037,7 @@ __global__ __launch_bounds__(BS) void gemv_ks_kernel(GemvArgs a) {
   float* part = xred + 16;  // [NRG][KS-1][RPW]
   stage_digitize<MAXT, false, BS>(st, K, xd, xred);
   __syncthreads();
+  if (stopped) return;
   while (base < n_iters) {
     float acc[RPW];
 #pragma unroll
@@ -1352,6 +1153,8 @@ size_t gemv_lds_bytes(int qtype, int K) {
 // The launch shapes cover rows of up to 256 lanes x units: K <= 16384.
 bool gemv_supports(int qtype, int K) {
   switch (qtype) {
+    case 0:  // F32 and F16 rows (gemv_float.hip): K floats of x in LDS
+    case 1:
     case QT_Q4_0:
     case QT_Q8_0: return K > 0 && K % 64 == 0 && K <= 16384;
     case QT_Q4_K:
@@ -1362,6 +1165,7 @@ bool gemv_supports(int qtype, int K) {
 }
 
 hipError_t gemv_launch(int qtype, int epi, const GemvArgs& a, int num_cus, hipStream_t st) {
+  if (qtype == 0 || qtype == 1) return gemv_float_launch(qtype, epi, a, num_cus, st);
   switch (epi) {
     case GEMV_EPI_STORE: return launch_epi<GEMV_EPI_STORE>(qtype, a, num_cus, st);
     case GEMV_EPI_ADD: return launch_epi<GEMV_EPI_ADD>(qtype, a, num_cus, st);

@@ -1,0 +1,232 @@
+// gemv_common.h — device pieces shared by the GEMV kernels of gemv.hip
+// (quantized weights) and gemv_float.hip (F32 / F16 weights): the virtual-row
+// map of a fused launch, the epilogues, and the attention-partial merge that
+// the O projection folds into its x staging.
+#pragma once
+
+#include "device_common.h"
+#include "kernels.h"
+
+namespace {
+
+// x read from the decode attention's per-chunk partials (ADD_MERGE): element
+// i belongs to head i / hd; each active chunk c (c < s_eff) holds the running
+// max M_c, sum L_c and unnormalised output O_c of its positions, and
+//   x = sum_c O_c e^(M_c - M) / sum_c L_c e^(M_c - M),  M = max_c M_c
+// (attn_merge_kernel's combination).  Every chunk's loads are issued (their
+// addresses do not depend on the position); inactive ones are masked.  The
+// weights e^(M_c - M) and the sum depend on the head only: the base-256
+// staging (16-element groups of one head) computes them once per group.
+struct MergeSrc {
+  const float* o;
+  const float* ml;
+  int hd, splits, s_eff;
+};
+
+// Elements i .. i+3 combined in one round trip: every chunk's (max, sum) and
+// outputs are loaded together, then folded.  Used by the base-16 staging,
+// whose items (two float4 of one head) gain nothing from sharing the weights.
+__device__ __forceinline__ float4 merged_x4(const MergeSrc& m, int i) {
+  const int h = i / m.hd, d = i - h * m.hd;
+  const size_t base = (size_t)h * m.splits;
+  float2 ml[kFoldMaxSplits];
+  float4 oc[kFoldMaxSplits];
+  float M = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < kFoldMaxSplits; c++) {
+    const bool in = c < m.splits;
+    ml[c] = in ? *reinterpret_cast<const float2*>(m.ml + 2 * (base + c)) : make_float2(0.f, 0.f);
+    oc[c] = in ? *reinterpret_cast<const float4*>(m.o + (base + c) * m.hd + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (c >= m.s_eff) ml[c].y = 0.f;
+    if (ml[c].y > 0.f) M = fmaxf(M, ml[c].x);
+  }
+  float L = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int c = 0; c < kFoldMaxSplits; c++) {
+    if (ml[c].y > 0.f) {
+      const float f = expf(ml[c].x - M);
+      L += ml[c].y * f;
+      acc.x += oc[c].x * f;
+      acc.y += oc[c].y * f;
+      acc.z += oc[c].z * f;
+      acc.w += oc[c].w * f;
+    }
+  }
+  return make_float4(acc.x / L, acc.y / L, acc.z / L, acc.w / L);
+}
+
+// Chunk weights of head h: f[c] = e^(M_c - M) for active chunks that hold
+// positions (0 otherwise) and their sum L = sum_c L_c f[c].
+struct MergeW {
+  float f[kFoldMaxSplits];
+  float L;
+};
+
+__device__ __forceinline__ MergeW merge_weights(const MergeSrc& m, int h) {
+  const size_t base = (size_t)h * m.splits;
+  float2 ml[kFoldMaxSplits];
+  float M = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < kFoldMaxSplits; c++) {
+    ml[c] = c < m.splits ? *reinterpret_cast<const float2*>(m.ml + 2 * (base + c)) : make_float2(0.f, 0.f);
+    if (c >= m.s_eff) ml[c].y = 0.f;
+    if (ml[c].y > 0.f) M = fmaxf(M, ml[c].x);
+  }
+  MergeW w;
+  w.L = 0.f;
+#pragma unroll
+  for (int c = 0; c < kFoldMaxSplits; c++) {
+    w.f[c] = ml[c].y > 0.f ? expf(ml[c].x - M) : 0.f;
+    w.L += ml[c].y * w.f[c];
+  }
+  return w;
+}
+
+// Elements d .. d+3 of head h combined with the chunk weights.
+__device__ __forceinline__ float4 merge_apply(const MergeSrc& m, const MergeW& w, int h, int d) {
+  const size_t base = (size_t)h * m.splits;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int c = 0; c < kFoldMaxSplits; c++) {
+    if (c < m.splits) {
+      const float4 o = *reinterpret_cast<const float4*>(m.o + (base + c) * m.hd + d);
+      acc.x += o.x * w.f[c];
+      acc.y += o.y * w.f[c];
+      acc.z += o.z * w.f[c];
+      acc.w += o.w * w.f[c];
+    }
+  }
+  return make_float4(acc.x / w.L, acc.y / w.L, acc.z / w.L, acc.w / w.L);
+}
+
+// Segment base pointer and row count by run-time segment index, chosen with
+// masks: indexing the kernel-argument arrays (or a select chain, which the
+// compiler turns into a table) would copy them to scratch, and a scratch load
+// waits on every vector-memory operation in flight.
+__device__ __forceinline__ const uint8_t* seg_w(const GemvArgs& a, int seg) {
+  const uintptr_t w0 = reinterpret_cast<uintptr_t>(a.w[0]);
+  const uintptr_t w1 = reinterpret_cast<uintptr_t>(a.w[1]);
+  const uintptr_t w2 = reinterpret_cast<uintptr_t>(a.w[2]);
+  const uintptr_t m1 = 0 - (uintptr_t)(seg == 1), m2 = 0 - (uintptr_t)(seg == 2);
+  return reinterpret_cast<const uint8_t*>(w0 ^ ((w0 ^ w1) & m1) ^ ((w0 ^ w2) & m2));
+}
+__device__ __forceinline__ int seg_n(const GemvArgs& a, int seg) {
+  return seg == 0 ? a.seg_rows[0] : (seg == 1 ? a.seg_rows[1] : a.seg_rows[2]);
+}
+
+// Virtual row -> (segment, row-in-segment).
+template <int EPI>
+__device__ __forceinline__ void map_row(const GemvArgs& a, int vr, int& seg, int& r) {
+  if constexpr (EPI == GEMV_EPI_SWIGLU) {
+    seg = vr & 1;
+    r = vr >> 1;
+  } else if constexpr (EPI == GEMV_EPI_QKV) {
+    if (vr < a.seg_rows[0]) { seg = 0; r = vr; }
+    else if (vr < a.seg_rows[0] + a.seg_rows[1]) { seg = 1; r = vr - a.seg_rows[0]; }
+    else { seg = 2; r = vr - a.seg_rows[0] - a.seg_rows[1]; }
+  } else {
+    seg = 0;
+    r = vr;
+  }
+}
+
+// What an epilogue reads besides the dot products, loaded by the lane that
+// finishes the rows together with the weights of the same iteration, so the
+// epilogue does not wait on a load issued behind the next iteration's weights:
+//   ADD: the residual rows;
+//   QKV: (cos, sin) of each q/k row pair at position pos from the RoPE table
+//        (TensorMath.ApplyRoPE's angle, TensorMath.cs:418-432), the pair index
+//        being the row's offset within its head, in res[0..RPW); with a bias
+//        (QwenModel.cs:104-120) the rows' biases in res[RPW..2*RPW).
+template <int EPI, int RPW>
+constexpr int res_count() { return EPI == GEMV_EPI_QKV ? 2 * RPW : RPW; }
+
+template <int EPI, int RPW, int NR>
+__device__ __forceinline__ void load_residual(const GemvArgs& a, int vr0, int li, int pos, float (&res)[NR]) {
+#pragma unroll
+  for (int i = 0; i < NR; i++) res[i] = 0.f;
+  if (li != 0) return;
+  if constexpr (EPI == GEMV_EPI_ADD || EPI == GEMV_EPI_ADD_MERGE) {
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      const int vr = vr0 + i;
+      if (vr < a.n_vrows) res[i] = a.out[0][vr];
+    }
+  } else if constexpr (EPI == GEMV_EPI_QKV) {
+#pragma unroll
+    for (int i = 0; i < RPW; i += 2) {
+      const int vr = vr0 + i;
+      int seg, r;
+      map_row<EPI>(a, vr, seg, r);
+      if (vr < a.n_vrows && seg < 2) {
+        const float2 cs = a.rope[(size_t)pos * (a.head_dim / 2) + (r % a.head_dim) / 2];
+        res[i] = cs.x;
+        res[i + 1] = cs.y;
+      }
+      if (vr < a.n_vrows && a.bias) {
+        const float2 b = *reinterpret_cast<const float2*>(a.bias + vr);
+        res[RPW + i] = b.x;
+        res[RPW + i + 1] = b.y;
+      }
+    }
+  }
+}
+
+// pos: the device-side position (QKV), read at kernel start; res: what
+// load_residual fetched for these rows.
+template <int EPI, int RPW>
+__device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, const float* v, const float* res, int pos) {
+#pragma unroll
+  for (int i = 0; i < RPW; i += 2) {
+    const int vr = vr0 + i;
+    if (vr >= a.n_vrows) return;
+    int seg, r;
+    map_row<EPI>(a, vr, seg, r);
+    if constexpr (EPI == GEMV_EPI_STORE || EPI == GEMV_EPI_LOGITS) {
+      a.out[0][r] = v[i];
+      if (vr + 1 < a.n_vrows) a.out[0][r + 1] = v[i + 1];
+    } else if constexpr (EPI == GEMV_EPI_ADD || EPI == GEMV_EPI_ADD_MERGE) {
+      a.out[0][r] = res[i] + v[i];
+      if (vr + 1 < a.n_vrows) a.out[0][r + 1] = res[i + 1] + v[i + 1];
+    } else if constexpr (EPI == GEMV_EPI_SWIGLU) {
+      const float g = v[i], u = v[i + 1];
+      a.out[0][r] = (g / (1.0f + expf(-g))) * u;
+    } else {  // QKV
+      float x0 = v[i], x1 = v[i + 1];
+      if (a.bias) {  // q/k/v += bias before RoPE (QwenModel.cs:104-125)
+        x0 += res[RPW + i];
+        x1 += res[RPW + i + 1];
+      }
+      if (seg < 2) {
+        const float c = res[i], s = res[i + 1];
+        const float y0 = x0 * c - x1 * s;
+        const float y1 = x0 * s + x1 * c;
+        x0 = y0;
+        x1 = y1;
+      }
+      if (seg == 0) {
+        a.out[0][r] = x0;
+        a.out[0][r + 1] = x1;
+      } else {
+        const size_t off = (size_t)pos * a.kv_dim + r;
+        // K or V cache base chosen arithmetically: a select of the two pointer
+        // arguments compiles to a scratch table whose load waits on every
+        // vector-memory operation in flight
+        const uintptr_t kb = reinterpret_cast<uintptr_t>(a.kcache), vb = reinterpret_cast<uintptr_t>(a.vcache);
+        const uintptr_t base = vb + ((kb - vb) & (uintptr_t)(0 - (uintptr_t)(seg == 1)));
+        if (a.kv_f16) {
+          _Float16* dst = reinterpret_cast<_Float16*>(base) + off;
+          dst[0] = (_Float16)x0;
+          dst[1] = (_Float16)x1;
+        } else {
+          float* dst = reinterpret_cast<float*>(base) + off;
+          dst[0] = x0;
+          dst[1] = x1;
+        }
+      }
+    }
+  }
+}
+
+}  // namespace

@@ -1,0 +1,188 @@
+// gemv_float.hip — GEMV for F32 and F16 weight matrices on gfx950.
+//
+// Replaces the two float branches of LlamaModel.MatVecMulByType
+// (src/ChatNet.Core/Models/Llama/LlamaModel.cs:470-567):
+//   F32  TensorMath.MatVecMul (TensorMath.cs:527-540): y[r] = dot(W[r], x)
+//   F16  LlamaModel.MatVecMulF16 (LlamaModel.cs:570-598): every half of the
+//        row converted exactly (DequantQ4_0.HalfToFloat), then the dot.
+// Rows are independent (TensorMath.cs:47-51); the GPU sums in its own order
+// with fp32 FMAs, within the GEMV tolerance of the reference's order.
+//
+// x (times the RMSNorm weight when one is fused) is staged once per
+// workgroup in LDS as fp32; 1/rms is applied to the finished dots, as in the
+// quantized GEMV.  A wave owns RPW consecutive rows at a time: lane l reads
+// the 16-byte pieces l, l+64, ... of each row (1 KB per wave and row per
+// step, fully coalesced), U steps of all RPW rows issued before any FMA, and
+// the row sums are reduced across the wave.  The epilogues are the quantized
+// GEMV's (gemv_common.h): store, residual add, QKV + RoPE + KV-cache write,
+// SiLU(gate)*up on interleaved rows, LM head, and the attention merge folded
+// into the O projection's x staging.
+#include "device_common.h"
+#include "gemv_common.h"
+#include "kernels.h"
+
+namespace {
+
+constexpr int WT_F32 = 0, WT_F16 = 1;
+
+// 16-byte pieces of a row: 4 F32 or 8 F16 weights.
+template <int WT>
+constexpr int piece_elems() { return WT == WT_F32 ? 4 : 8; }
+
+template <int WT>
+__device__ __forceinline__ float piece_dot(const cn_u32x4& w, const float* xs) {
+  if constexpr (WT == WT_F32) {
+    const float4 xv = *reinterpret_cast<const float4*>(xs);
+    float t = __uint_as_float(w.x) * xv.x;
+    t = fmaf(__uint_as_float(w.y), xv.y, t);
+    t = fmaf(__uint_as_float(w.z), xv.z, t);
+    return fmaf(__uint_as_float(w.w), xv.w, t);
+  } else {
+    const float4 x0 = *reinterpret_cast<const float4*>(xs);
+    const float4 x1 = *reinterpret_cast<const float4*>(xs + 4);
+    float t = cn_h2f(w.x) * x0.x;
+    t = fmaf(cn_h2f(w.x >> 16), x0.y, t);
+    t = fmaf(cn_h2f(w.y), x0.z, t);
+    t = fmaf(cn_h2f(w.y >> 16), x0.w, t);
+    t = fmaf(cn_h2f(w.z), x1.x, t);
+    t = fmaf(cn_h2f(w.z >> 16), x1.y, t);
+    t = fmaf(cn_h2f(w.w), x1.z, t);
+    return fmaf(cn_h2f(w.w >> 16), x1.w, t);
+  }
+}
+
+template <int WT, int RPW, int EPI, int U>
+__global__ __launch_bounds__(CN_BLOCK) void gemv_f_kernel(GemvArgs a) {
+  constexpr int NWV = CN_BLOCK / CN_WAVE;
+  constexpr int PE = piece_elems<WT>();
+  constexpr int NR = res_count<EPI, RPW>();
+  constexpr bool NORM = EPI == GEMV_EPI_QKV || EPI == GEMV_EPI_SWIGLU || EPI == GEMV_EPI_LOGITS;
+  constexpr bool MERGE = EPI == GEMV_EPI_ADD_MERGE;
+  extern __shared__ float smem[];  // [K] staged x, then NWV partial sums of squares
+  const int K = a.K;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int pos = EPI == GEMV_EPI_QKV ? *a.pos : 0;
+  const int stopped = a.stop ? *a.stop : 0;
+  float* red = smem + K;
+
+  // ---- stage x * g as fp32 (sum of squares of x for the RMS factor) ----
+  MergeSrc ms{};
+  if constexpr (MERGE) {
+    ms.o = a.part_o;
+    ms.ml = a.part_ml;
+    ms.hd = a.head_dim;
+    ms.splits = a.msplits;
+    ms.s_eff = min(a.msplits, (*a.pos + a.mchunk) / a.mchunk);
+  }
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < (K >> 2); c += CN_BLOCK) {
+    float4 v;
+    if constexpr (MERGE) v = merged_x4(ms, 4 * c);
+    else v = reinterpret_cast<const float4*>(a.x)[c];
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    if constexpr (NORM) {
+      const float4 g = reinterpret_cast<const float4*>(a.norm_w)[c];
+      v.x *= g.x;
+      v.y *= g.y;
+      v.z *= g.z;
+      v.w *= g.w;
+    }
+    reinterpret_cast<float4*>(smem)[c] = v;
+  }
+  ss = cn_wave_sum(ss);
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  float sst = 0.f;
+#pragma unroll
+  for (int w = 0; w < NWV; w++) sst += red[w];
+  const float rms = NORM ? 1.0f / sqrtf(sst / (float)K + a.eps) : 1.0f;
+  if (stopped) return;
+
+  const size_t row_bytes = (size_t)K * (WT == WT_F32 ? 4 : 2);
+  const int npieces = K / PE;  // 16-byte pieces per row
+  const int n_iters = (a.n_vrows + RPW - 1) / RPW;
+  for (int it = blockIdx.x * NWV + wave; it < n_iters; it += gridDim.x * NWV) {
+    const int vr0 = it * RPW;
+    const uint8_t* rp[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      const int vr = vr0 + i < a.n_vrows ? vr0 + i : a.n_vrows - 1;  // rows past the end re-read the last
+      int seg, r;
+      map_row<EPI>(a, vr, seg, r);
+      rp[i] = seg_w(a, seg) + (size_t)r * row_bytes;
+    }
+    float res[NR];
+    load_residual<EPI, RPW, NR>(a, vr0, lane, pos, res);
+    float acc[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) acc[i] = 0.f;
+    for (int p0 = 0; p0 < npieces; p0 += CN_WAVE * U) {
+      cn_u32x4 w[U][RPW];
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const int p = p0 + CN_WAVE * u + lane;
+#pragma unroll
+        for (int i = 0; i < RPW; i++)
+          w[u][i] = p < npieces ? *reinterpret_cast<const cn_u32x4*>(rp[i] + (size_t)p * 16) : cn_u32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const int p = p0 + CN_WAVE * u + lane;
+        if (p < npieces) {
+#pragma unroll
+          for (int i = 0; i < RPW; i++) acc[i] += piece_dot<WT>(w[u][i], smem + (size_t)p * PE);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; i++) acc[i] = cn_wave_sum(acc[i]) * rms;
+    if (lane == 0) epilogue<EPI, RPW>(a, vr0, acc, res, pos);
+  }
+}
+
+size_t gemv_f_smem(int K) { return sizeof(float) * ((size_t)K + 16); }
+
+template <int WT, int EPI>
+hipError_t launch_wt(const GemvArgs& a, int num_cus, hipStream_t st) {
+  constexpr int RPW = 2, U = 4;
+  const size_t smem = gemv_f_smem(a.K);
+  const auto kern = &gemv_f_kernel<WT, RPW, EPI, U>;
+  if (smem > 65536) {  // more than 64 KB of dynamic LDS must be allowed explicitly (once)
+    static bool lds_set = false;
+    if (!lds_set) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+      if (e != hipSuccess) return e;
+      lds_set = true;
+    }
+  }
+  const int n_iters = (a.n_vrows + RPW - 1) / RPW;
+  int grid = (n_iters + 3) / 4;
+  if (grid > 4 * num_cus) grid = 4 * num_cus;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(CN_BLOCK), smem, st, a);
+  return hipGetLastError();
+}
+
+template <int EPI>
+hipError_t launch_f_epi(int qtype, const GemvArgs& a, int num_cus, hipStream_t st) {
+  if (qtype == 0) return launch_wt<WT_F32, EPI>(a, num_cus, st);
+  return launch_wt<WT_F16, EPI>(a, num_cus, st);
+}
+
+}  // namespace
+
+hipError_t gemv_float_launch(int qtype, int epi, const GemvArgs& a, int num_cus, hipStream_t st) {
+  if ((qtype != 0 && qtype != 1) || a.K <= 0 || a.K % 64 != 0 || a.K > 16384) return hipErrorInvalidValue;
+  switch (epi) {
+    case GEMV_EPI_STORE: return launch_f_epi<GEMV_EPI_STORE>(qtype, a, num_cus, st);
+    case GEMV_EPI_ADD: return launch_f_epi<GEMV_EPI_ADD>(qtype, a, num_cus, st);
+    case GEMV_EPI_QKV: return launch_f_epi<GEMV_EPI_QKV>(qtype, a, num_cus, st);
+    case GEMV_EPI_SWIGLU: return launch_f_epi<GEMV_EPI_SWIGLU>(qtype, a, num_cus, st);
+    case GEMV_EPI_LOGITS: return launch_f_epi<GEMV_EPI_LOGITS>(qtype, a, num_cus, st);
+    case GEMV_EPI_ADD_MERGE:
+      if (a.msplits < 2 || a.msplits > kFoldMaxSplits || a.mchunk < 1 || a.head_dim % 32 != 0)
+        return hipErrorInvalidValue;
+      return launch_f_epi<GEMV_EPI_ADD_MERGE>(qtype, a, num_cus, st);
+    default: return hipErrorInvalidValue;
+  }
+}

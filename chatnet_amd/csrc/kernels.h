@@ -40,11 +40,18 @@ struct GemvArgs {
   const float* part_o;
   const float* part_ml;
   int msplits, mchunk;
+  // Decode loops: the stop flag of the device decode state (kDecStop); when it
+  // is set the launch returns after staging x, writing nothing.  nullptr
+  // elsewhere.
+  const int* stop;
 };
 
+// Weight types: Q4_0, Q8_0 (K % 64 == 0), Q4_K, Q5_K, Q6_K (K % 256 == 0), and
+// F32 / F16 (K % 64 == 0, gemv_float.hip); K <= 16384.
 bool gemv_supports(int qtype, int K);
 size_t gemv_lds_bytes(int qtype, int K);
 hipError_t gemv_launch(int qtype, int epi, const GemvArgs& a, int num_cus, hipStream_t st);
+hipError_t gemv_float_launch(int qtype, int epi, const GemvArgs& a, int num_cus, hipStream_t st);
 
 // Batched quantized GEMM on the matrix cores (gemm.hip):
 //   acc[n][vr] = sum_k W_vr[k] * xb[n][k],  0 <= n < N, 0 <= vr < M
@@ -126,14 +133,25 @@ struct AttnArgs {
   int splits;         // position chunks of the launch (<= 64), one workgroup per kv head each
   int chunk;          // positions per chunk: chunk c covers [c*chunk, (c+1)*chunk) below pos+1
   int fold;           // splits > 1: leave the partials for the O GEMV (GEMV_EPI_ADD_MERGE)
+  const int* stop;    // decode loops: return at once while *stop is set (nullptr: never)
 };
 hipError_t attn_decode_launch(const AttnArgs& a, hipStream_t st);
 // Positions one decode-attention workgroup covers per round of wave steps.
 int attn_decode_round(int head_dim, int kv_mul);
 
+// Device decode state, kDecWords ints: the position of the token being
+// forwarded, that token, the picks made so far in the current decode loop, a
+// stop flag (set by a pick that returns the EOS token; the decode-step kernels
+// then exit early, so the cache and logits stay as InferenceEngine.Generate
+// leaves them when it breaks before forwarding EOS, InferenceEngine.cs:258-261)
+// and the EOS token id of the loop (-1: none).
+enum { kDecPos = 0, kDecTok = 1, kDecStep = 2, kDecStop = 3, kDecEos = 4, kDecWords = 8 };
+
 // Greedy argmax (GreedySampler.Sample, GreedySampler.cs:13-26); writes the
-// winner to state[1] and appends it to out_tokens[state[2]++], and advances
-// state[0] (the position) by one.
+// winner to state[kDecTok] and advances state[kDecPos] (the position) by one.
+// With out_tokens (a decode loop) it also appends the winner to
+// out_tokens[state[kDecStep]++], does nothing while state[kDecStop] is set,
+// and sets it when the winner is state[kDecEos].
 hipError_t argmax_launch(const float* logits, int n, int* state, int* out_tokens, int out_cap,
                          hipStream_t st);
 
@@ -165,5 +183,10 @@ class NetRandom {
   int inext_, inextp_;
 };
 
-// Sets state[0] = pos, state[1] = tok and, when step >= 0, state[2] = step.
-hipError_t set_state_launch(int* state, int pos, int tok, int step, hipStream_t st);
+// h[i] = silu(g[i]) * u[i] (TensorMath.SiluElementwiseMul, TensorMath.cs:253-286).
+hipError_t silu_mul_launch(const float* g, const float* u, float* h, int n, hipStream_t st);
+
+// Sets state[kDecPos] = pos, state[kDecTok] = tok and, when step >= 0 (the
+// start of a decode loop), state[kDecStep] = step, clears the stop flag and
+// sets state[kDecEos] = eos.
+hipError_t set_state_launch(int* state, int pos, int tok, int step, hipStream_t st, int eos = -1);

@@ -73,6 +73,7 @@ __global__ __launch_bounds__(kST) void sample_kernel(const float* __restrict__ l
   __shared__ float cp[kSampleMaxK];
   __shared__ int ci[kSampleMaxK];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (out_tokens && state[kDecStop]) return;  // the decode loop stopped at EOS
   const float inv_temp = prm->inv_temp;
   const float top_p = prm->top_p;
   const int k = prm->top_k < n ? prm->top_k : n;
@@ -265,7 +266,7 @@ __global__ __launch_bounds__(kST) void sample_kernel(const float* __restrict__ l
     float sum = 0.f;
     for (int i = 0; i < cutoff; i++) sum += cp[i];
     const float inv = 1.0f / sum;
-    const int step = state[2];
+    const int step = state[kDecStep];
     const float r = draws ? draws[step] : prm->draw;
     float acc = 0.f;
     int tok = ci[cutoff - 1];
@@ -276,10 +277,13 @@ __global__ __launch_bounds__(kST) void sample_kernel(const float* __restrict__ l
         break;
       }
     }
-    state[1] = tok;
-    if (out_tokens && step < out_cap) out_tokens[step] = tok;
-    state[2] = step + 1;
-    state[0] = state[0] + 1;
+    state[kDecTok] = tok;
+    if (out_tokens) {
+      if (step < out_cap) out_tokens[step] = tok;
+      state[kDecStep] = step + 1;
+      if (tok == state[kDecEos]) state[kDecStop] = 1;
+    }
+    state[kDecPos] = state[kDecPos] + 1;
   }
 }
 #pragma clang diagnostic pop

@@ -36,6 +36,14 @@ MIXES = {
     # Q5_K_M-style: Q5_K attention and ffn_gate/up, Q6_K ffn_down and output
     "q5_k_m": {"attn": _native.GGML_Q5_K, "gate_up": _native.GGML_Q5_K, "down": _native.GGML_Q6_K,
                "output": _native.GGML_Q6_K},
+    # unquantized matrices (TensorMath.MatVecMul / LlamaModel.MatVecMulF16)
+    "f32": {"attn": _native.GGML_F32, "gate_up": _native.GGML_F32, "down": _native.GGML_F32,
+            "output": _native.GGML_F32},
+    "f16": {"attn": _native.GGML_F16, "gate_up": _native.GGML_F16, "down": _native.GGML_F16,
+            "output": _native.GGML_F16},
+    # every matrix dispatched on its own type, ffn_gate and ffn_up differing
+    "mixed": {"attn": _native.GGML_Q8_0, "gate": _native.GGML_Q4_0, "up": _native.GGML_F16,
+              "down": _native.GGML_Q4_K, "output": _native.GGML_F32},
 }
 
 
@@ -83,6 +91,8 @@ def tensor(ggml_type: int, seed: int, name: str, rows: int, cols: int, sigma: fl
     n = rows * cols
     if ggml_type == _native.GGML_F32:
         data = normal(seed, name, n, sigma).view(np.uint8)
+    elif ggml_type == _native.GGML_F16:  # round to nearest even, as System.Half's conversion
+        data = normal(seed, name, n, sigma).astype(np.float16).view(np.uint8)
     else:
         nbytes = _native.tensor_nbytes(ggml_type, n)
         data = np.empty(nbytes, dtype=np.uint8)
@@ -128,8 +138,10 @@ def llama_checkpoint(cfg: LlamaConfig, seed: int = 1234, mix: str = "q4_0",
         ck[p + "attn_k.weight"] = tensor(q["attn"], seed, p + "attn_k.weight", kvd, cfg.dim)
         ck[p + "attn_v.weight"] = tensor(q["attn"], seed, p + "attn_v.weight", kvd, cfg.dim)
         ck[p + "attn_output.weight"] = tensor(q["attn"], seed, p + "attn_output.weight", cfg.dim, cfg.dim)
-        ck[p + "ffn_gate.weight"] = tensor(q["gate_up"], seed, p + "ffn_gate.weight", cfg.hidden_dim, cfg.dim)
-        ck[p + "ffn_up.weight"] = tensor(q["gate_up"], seed, p + "ffn_up.weight", cfg.hidden_dim, cfg.dim)
+        ck[p + "ffn_gate.weight"] = tensor(q.get("gate", q.get("gate_up")), seed, p + "ffn_gate.weight",
+                                           cfg.hidden_dim, cfg.dim)
+        ck[p + "ffn_up.weight"] = tensor(q.get("up", q.get("gate_up")), seed, p + "ffn_up.weight",
+                                         cfg.hidden_dim, cfg.dim)
         ck[p + "ffn_down.weight"] = tensor(q["down"], seed, p + "ffn_down.weight", cfg.dim, cfg.hidden_dim)
         if qkv_bias:
             for nm, n in (("attn_q.bias", cfg.dim), ("attn_k.bias", kvd), ("attn_v.bias", kvd)):

@@ -110,10 +110,12 @@ CHATNET_API int chatnet_create(const chatnet_config* cfg, int device, chatnet_mo
  * blk.{l}.{attn_norm,ffn_norm,attn_q,attn_k,attn_v,attn_output,
  * ffn_gate,ffn_up,ffn_down}.weight, plus for CHATNET_ARCH_QWEN2 the optional
  * F32 biases blk.{l}.{attn_q,attn_k,attn_v}.bias (QwenWeights.cs:158-170: a
- * layer that has the q bias must have all three).  Without output.weight the
- * LM head is token_embd.weight (the tied fallback of LlamaWeights.cs:89-98
- * and QwenWeights.cs:102-112), which must then be Q4_0 or Q8_0.  Embeddings
- * may be F32, F16, Q4_0 or Q8_0.  `dims` is GGUF order (ne0 = inner).
+ * layer that has the q bias must have all three).  Weight matrices may be
+ * F32, F16, Q4_0, Q8_0, Q4_K, Q5_K or Q6_K, each dispatched on its own type
+ * (LlamaModel.MatVecMulByType, LlamaModel.cs:470-567).  Without output.weight
+ * the LM head is token_embd.weight, of whatever type (the tied fallback of
+ * LlamaWeights.cs:89-98 and QwenWeights.cs:102-112).  Embeddings may be F32,
+ * F16, Q4_0 or Q8_0.  `dims` is GGUF order (ne0 = inner).
  * `nbytes` must equal GgufTensorInfo.ByteSize (GgufTensorInfo.cs:30-113).
  * Replaces MemoryMappedWeights.GetTensorPointer (MemoryMappedWeights.cs:76-84)
  * as the source of weight bytes for the forward pass. */
@@ -138,15 +140,20 @@ CHATNET_API int chatnet_forward(chatnet_model* m, const int32_t* tokens, int n, 
 CHATNET_API int chatnet_argmax(chatnet_model* m, int32_t* out_token);
 
 /* Greedy generation loop of InferenceEngine.Generate
- * (src/ChatNet.Core/InferenceEngine.cs:234-307) with the tokenizer, EOS and
+ * (src/ChatNet.Core/InferenceEngine.cs:234-307) with the tokenizer and
  * stop-string checks left to the caller: forwards the prompt at positions
  * 0..n_prompt-1, then emits up to max_tokens greedy tokens, feeding each back
- * at the next position; stops early when the next position would reach
- * context_length - 1 (InferenceEngine.cs:295-298).  The decode loop stays on
- * the device (one HIP graph per step, token fed back through device memory).
- * Output stops before the first `eos_token` (InferenceEngine.cs:258-261);
- * eos_token < 0 disables the check.  Writes the generated ids to out_tokens
- * (room for max_tokens ids) and their count to *n_out. */
+ * at the next position.  As in the reference, a token is emitted before the
+ * context check, so the loop stops after emitting the token at position
+ * context_length - 1 without forwarding it (InferenceEngine.cs:295-298), and a
+ * prompt that fills the context still yields one token.  The loop stops before
+ * the first `eos_token` and never forwards it (InferenceEngine.cs:258-261):
+ * the cache, the position and the logits stay those of the last token before
+ * it, so a later chatnet_decode_greedy continues from there.  eos_token < 0
+ * disables the check.  The decode loop stays on the device (one HIP graph per
+ * step, token fed back through device memory; the steps after an EOS return
+ * at once).  Writes the generated ids to out_tokens (room for max_tokens ids)
+ * and their count to *n_out. */
 CHATNET_API int chatnet_generate_greedy(chatnet_model* m, const int32_t* prompt, int n_prompt,
                             int max_tokens, int32_t eos_token, int32_t* out_tokens,
                             int* n_out);
@@ -191,19 +198,24 @@ CHATNET_API int chatnet_net_random(int32_t seed, int n, double* out);
 /* Copies the device logits of the last forward to the host (vocab_size floats). */
 CHATNET_API int chatnet_get_logits(chatnet_model* m, float* logits_host);
 
-/* Quantized matrix product on caller-owned device buffers, the batched form of
- * TensorMath.MatVecMulQ4_0 / MatVecMulQ6K / MatVecMulGeneric
- * (TensorMath.cs:548-656) as dispatched by LlamaModel.MatVecMulByType
- * (LlamaModel.cs:470-567):
+/* Matrix product on caller-owned device buffers, the batched form of
+ * TensorMath.MatVecMulQ4_0 / MatVecMulQ6K / MatVecMulGeneric / MatVecMul and
+ * LlamaModel.MatVecMulF16 (TensorMath.cs:527-656, LlamaModel.cs:570-598) as
+ * dispatched by LlamaModel.MatVecMulByType (LlamaModel.cs:470-567):
  *   y[n][m] = sum_k W[m][k] * x[n][k],  0 <= n < N, 0 <= m < M
  * W is M rows of raw GGUF blocks (row stride K/block*bytes_per_block), x is
- * N x K fp32 row-major, y is N x M fp32 row-major.  Types Q4_0, Q8_0 and K %
- * 64 == 0, or Q4_K, Q5_K, Q6_K and K % 256 == 0, with K <= 16384.  N >= 8 with
- * Q4_0 runs the dequant-to-LDS bf16 MFMA GEMM (x rounded to bf16); any
- * other call runs the fused dequant-GEMV once per column.  The GEMM's
- * workspace is allocated on first use per (device, stream) and kept.
- * `stream` is a hipStream_t (NULL = default stream).  Asynchronous on
- * `stream`. */
+ * N x K fp32 row-major, y is N x M fp32 row-major; w_dev and x_dev 16-byte
+ * aligned.  Types F32, F16, Q4_0, Q8_0 and K % 64 == 0, or Q4_K, Q5_K, Q6_K
+ * and K % 256 == 0, with K <= 16384.  N >= 8 with Q4_0 runs the
+ * dequant-to-LDS bf16 MFMA GEMM (x rounded to bf16); any other call runs the
+ * fused GEMV once per column.  The GEMM's workspace is allocated on first use
+ * per (device, stream) and kept until the process ends (a buffer it outgrows
+ * is retired, not freed, since a captured graph may still read it).  A call
+ * on a stream under HIP graph capture cannot allocate: it fails with
+ * CHATNET_ERR_INVALID_ARG if the stream's workspace is too small, so a
+ * capturing caller first makes one uncaptured call of the largest size.
+ * `stream` is a hipStream_t (NULL = default
+ * stream).  Asynchronous on `stream`. */
 CHATNET_API int chatnet_matmul(uint32_t ggml_type, const void* w_dev, const float* x_dev,
                    float* y_dev, int M, int K, int N, void* stream);
 

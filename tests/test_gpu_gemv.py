@@ -118,3 +118,15 @@ def test_batched_columns_match_per_column_gemv(N):
         r = oracle.matvec(2, t.data, x[n], M, K)
         assert normwise(y[n], r) <= 1e-2
 
+
+
+# F32 and F16 weight matrices (TensorMath.MatVecMul, TensorMath.cs:527-540, and
+# LlamaModel.MatVecMulF16, LlamaModel.cs:570-598), including ragged row counts,
+# the longest rows (K = 16384: 64 KB of staged x) and the LM-head shape.
+@pytest.mark.parametrize("qtype,M,K", [
+    (0, 2048, 2048), (0, 256, 2048), (0, 4096, 4096), (0, 2048, 5632), (0, 32000, 2048),
+    (1, 2048, 2048), (1, 256, 2048), (1, 4096, 11008), (1, 11008, 4096), (1, 32000, 4096),
+    (0, 1, 64), (0, 7, 192), (0, 33, 16384), (1, 1, 64), (1, 5, 320), (1, 9, 16384),
+])
+def test_float_weight_gemv_shapes(qtype, M, K):
+    run_case(qtype, M, K, seed=7)
