@@ -1,0 +1,54 @@
+"""GPU parity at the full end-to-end workloads (chatnet_amd.workloads) against
+the oracle's committed expected outputs (tests/golden/workload_<name>.npz,
+written by tests/golden/make_workload_fixtures.py).
+
+For each workload: the checkpoint is regenerated from its seed on this
+machine (its sample digest must equal the fixture's), the prompt is forwarded
+as one chatnet_forward span (the batched MFMA path where the weight types
+allow it, token by token otherwise), then the device greedy loop runs every
+decode step of the workload.  Bars (LlamaModel.Forward, LlamaModel.cs:93-238;
+InferenceEngine.Generate, InferenceEngine.cs:234-307):
+  - logits after the prompt within 1e-2 of the oracle's (max abs);
+  - every greedy token identical to the oracle's; a step whose oracle
+    top-1/top-2 margin is below 1e-3 may differ and is then teacher-forced
+    (the oracle's token forwarded at that position), so the comparison runs to
+    the last step;
+  - logits after the last decode token within 1e-2.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from chatnet_amd import HipLlamaModel
+from chatnet_amd.workloads import WORKLOADS, checkpoint_sample_digest
+from gpu_util import announce, greedy_against_expected
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+LOGIT_TOL = 1e-2
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("name", list(WORKLOADS))
+def test_workload_matches_oracle_fixture(name):
+    w = WORKLOADS[name]
+    fx = np.load(os.path.join(GOLDEN, f"workload_{name}.npz"))
+    announce(f"workload {name}: regenerating the checkpoint")
+    ck = w.checkpoint()
+    assert checkpoint_sample_digest(ck) == str(fx["digest"]), "this machine regenerates a different checkpoint"
+    prompt = w.prompt()
+    assert np.array_equal(prompt, fx["prompt"])
+    announce(f"workload {name}: {w.n_prompt}-token prompt + {w.n_decode} greedy steps on the gpu")
+    with HipLlamaModel(w.config, ck) as m:
+        ck.clear()  # the device holds its own copy
+        lp = m.forward(prompt, 0).copy()
+        e0 = float(np.max(np.abs(lp - fx["logits_prompt"])))
+        print(f"[workload] {name}: prompt logits max-abs err {e0:.3g}", flush=True)
+        assert e0 <= LOGIT_TOL, (name, "prompt logits", e0)
+        forced = greedy_against_expected(m, fx["tokens"], fx["margins"], w.n_prompt, name)
+        lf = m.get_logits()
+    e1 = float(np.max(np.abs(lf - fx["logits_final"])))
+    print(f"[workload] {name}: final logits max-abs err {e1:.3g}, {forced} near-tie steps teacher-forced", flush=True)
+    assert e1 <= LOGIT_TOL, (name, "final logits", e1)
