@@ -141,6 +141,10 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.c_uint32, _P, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P],
     ),
+    "chatnet_matmul_noalloc": (
+        ctypes.c_int,
+        [ctypes.c_uint32, _P, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P],
+    ),
     "chatnet_tensor_nbytes": (ctypes.c_uint64, [ctypes.c_uint32, ctypes.c_uint64]),
     "chatnet_destroy": (None, [_P]),
     "chatnet_last_error": (ctypes.c_char_p, []),

@@ -96,7 +96,7 @@ int matmul_workspace(int dev, hipStream_t st, size_t bytes, char** out) {
     if (cs != hipStreamCaptureStatusNone)
       return fail(CHATNET_ERR_INVALID_ARG,
                   "chatnet_matmul: the stream is capturing and its workspace (%zu bytes) is smaller than the %zu "
-                  "this call needs; make one uncaptured call of this size first",
+                  "this call needs; make one uncaptured call of this size first, or use chatnet_matmul_noalloc",
                   e.second, bytes);
     char* p = nullptr;
     if (hipMalloc((void**)&p, bytes) != hipSuccess)
@@ -105,6 +105,32 @@ int matmul_workspace(int dev, hipStream_t st, size_t bytes, char** out) {
     e = {p, bytes};
   }
   *out = e.first;
+  return CHATNET_OK;
+}
+
+// Scratch of chatnet_matmul_noalloc: a fixed array in the library's code
+// object, so every device the library runs on holds its own copy from module
+// load to process exit and no call allocates.  Host code never uses the
+// array's name as an address (on the host it names a stand-in, not device
+// memory): the device address comes from hipGetSymbolAddress, taken once per
+// device with that device current, and is passed to the kernels.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+std::mutex g_scratch_mu;
+constexpr int kMaxDevices = 64;
+char* g_scratch_dev[kMaxDevices] = {};
+
+int noalloc_scratch(int dev, char** out) {
+  if (dev < 0 || dev >= kMaxDevices) return fail(CHATNET_ERR_NO_DEVICE, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(CHATNET_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_dev[dev] = static_cast<char*>(p);
+  }
+  *out = g_scratch_dev[dev];
   return CHATNET_OK;
 }
 
@@ -906,10 +932,11 @@ int run_prompt(chatnet_model* m, const int32_t* tokens, int n, int position) {
   return CHATNET_OK;
 }
 
-// chatnet_matmul: the batched path's scratch (bf16 x, then the K-split
-// partials) comes from the per-stream workspace.
-int matmul_impl(uint32_t type, const void* w_dev, const float* x_dev, float* y_dev, int M, int K, int N,
-                void* stream) {
+// chatnet_matmul and chatnet_matmul_noalloc: the same kernels; the batched
+// path's scratch (bf16 x, then the K-split partials) comes from the per-stream
+// workspace, or with `noalloc` from the fixed per-device scratch array.
+int matmul_impl(uint32_t type, const void* w_dev, const float* x_dev, float* y_dev, int M, int K, int N, void* stream,
+                bool noalloc) {
   if (!w_dev || !x_dev || !y_dev) return fail(CHATNET_ERR_INVALID_ARG, "null device pointer");
   if (M <= 0 || K <= 0 || N <= 0) return fail(CHATNET_ERR_INVALID_ARG, "M, K, N must be positive");
   if (!is_matrix_type(type)) return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "matmul type %u not supported", type);
@@ -927,7 +954,15 @@ int matmul_impl(uint32_t type, const void* w_dev, const float* x_dev, float* y_d
     const size_t part_bytes = gemm_workspace_bytes(M, N, K, cus, false);
     char* ws = nullptr;
     int rc;
-    rc = matmul_workspace(dev, st, xb_bytes + part_bytes, &ws);
+    if (noalloc) {
+      if (xb_bytes + part_bytes > kNoAllocScratchBytes)
+        return fail(CHATNET_ERR_INVALID_ARG,
+                    "chatnet_matmul_noalloc: M=%d K=%d N=%d needs %zu bytes of scratch, more than its %zu", M, K, N,
+                    xb_bytes + part_bytes, kNoAllocScratchBytes);
+      rc = noalloc_scratch(dev, &ws);
+    } else {
+      rc = matmul_workspace(dev, st, xb_bytes + part_bytes, &ws);
+    }
     if (rc) return rc;
     HIP_TRY(to_bf16_launch(x_dev, (uint16_t*)ws, (size_t)N * K, st));
     GemmArgs g;
@@ -1187,7 +1222,12 @@ int chatnet_net_random(int32_t seed, int n, double* out) {
 
 int chatnet_matmul(uint32_t type, const void* w_dev, const float* x_dev, float* y_dev, int M, int K, int N,
                    void* stream) {
-  return matmul_impl(type, w_dev, x_dev, y_dev, M, K, N, stream);
+  return matmul_impl(type, w_dev, x_dev, y_dev, M, K, N, stream, false);
+}
+
+int chatnet_matmul_noalloc(uint32_t type, const void* w_dev, const float* x_dev, float* y_dev, int M, int K, int N,
+                           void* stream) {
+  return matmul_impl(type, w_dev, x_dev, y_dev, M, K, N, stream, true);
 }
 
 }  // extern "C"

@@ -213,11 +213,25 @@ CHATNET_API int chatnet_get_logits(chatnet_model* m, float* logits_host);
  * is retired, not freed, since a captured graph may still read it).  A call
  * on a stream under HIP graph capture cannot allocate: it fails with
  * CHATNET_ERR_INVALID_ARG if the stream's workspace is too small, so a
- * capturing caller first makes one uncaptured call of the largest size.
- * `stream` is a hipStream_t (NULL = default
+ * capturing caller first makes one uncaptured call of the largest size, or
+ * uses chatnet_matmul_noalloc.  `stream` is a hipStream_t (NULL = default
  * stream).  Asynchronous on `stream`. */
 CHATNET_API int chatnet_matmul(uint32_t ggml_type, const void* w_dev, const float* x_dev,
                    float* y_dev, int M, int K, int N, void* stream);
+
+/* chatnet_matmul without any allocation, for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc.  No counterpart in the reference.  Same arguments,
+ * kernels and results as chatnet_matmul; the batched path's scratch (bf16 x
+ * and the K-split partials) lives in a fixed 64 MiB array per device, held by
+ * the library from load to process exit, instead of a per-stream workspace.
+ * Calls needing more scratch than that (N*K*2 bytes of x, rounded up to 256,
+ * plus the partials) fail with CHATNET_ERR_INVALID_ARG before launching
+ * anything.  Every call on one device shares that device's array: calls that
+ * may overlap on one device (different streams, threads) race and must be
+ * serialized by the caller. */
+CHATNET_API int chatnet_matmul_noalloc(uint32_t ggml_type, const void* w_dev, const float* x_dev,
+                                       float* y_dev, int M, int K, int N, void* stream);
 
 /* Bytes of one GGUF tensor of `ggml_type` with `n_elements` elements, per
  * GgufTensorInfo.ByteSize (GgufTensorInfo.cs:30-113); 0 for an unknown type. */

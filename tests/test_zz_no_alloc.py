@@ -1,0 +1,57 @@
+"""chatnet_matmul_noalloc (the allocation-free variant of chatnet_matmul: its
+scratch is the library's fixed per-device array) against chatnet_matmul on
+the same inputs, through the C ABI: two calls in a row, the second smaller,
+so the second runs on scratch the first left behind.  Bar: the batched MFMA
+GEMM's 1e-2 normwise (the same kernels run, so the outputs are expected to be
+identical), and the GEMV path's 1e-3."""
+import numpy as np
+import pytest
+
+from chatnet_amd import _native, hiprt, synth
+from gpu_util import announce, normwise
+
+pytestmark = pytest.mark.gpu
+
+
+def _call(fn_name, qtype, w_d, x_d, M, K, N, stream):
+    lib = _native.hip_lib()
+    y = hiprt.DeviceBuffer(4 * M * N)
+    y.fill(0xFF)  # NaN pattern: anything left unwritten stays NaN
+    _native.check(getattr(lib, fn_name)(qtype, w_d.ptr, x_d.ptr, y.ptr, M, K, N, stream))
+    hiprt.synchronize()
+    out = y.to_numpy(np.float32, M * N).reshape(N, M)
+    y.free()
+    return out
+
+
+@pytest.mark.parametrize("first,second", [
+    ((11008, 4096, 512), (4096, 4096, 64)),   # K-split partials, then a smaller split
+    ((2048, 5632, 512), (256, 2048, 8)),
+    ((4096, 4096, 64), (2048, 2048, 3)),       # then the GEMV path (no scratch)
+])
+def test_noalloc_matches_matmul_on_two_calls(first, second):
+    stream = hiprt.Stream()
+    for (M, K, N) in (first, second):
+        announce(f"noalloc M={M} K={K} N={N}")
+        t = synth.tensor(2, 3, f"na{M}x{K}", M, K)
+        x = synth.normal(3, f"nax{N}x{K}", N * K, 1.0)
+        w_d = hiprt.DeviceBuffer.from_numpy(t.data, pad=256)
+        x_d = hiprt.DeviceBuffer.from_numpy(x)
+        ref = _call("chatnet_matmul", 2, w_d, x_d, M, K, N, stream.h)
+        got = _call("chatnet_matmul_noalloc", 2, w_d, x_d, M, K, N, stream.h)
+        w_d.free()
+        x_d.free()
+        assert np.all(np.isfinite(got))
+        err = normwise(got, ref)
+        print(f"noalloc M={M} K={K} N={N}: normwise {err:.3g}, identical {bool(np.array_equal(got, ref))}",
+              flush=True)
+        assert err <= (1e-2 if N >= 8 else 1e-3)
+    stream.synchronize()
+
+
+def test_noalloc_refuses_more_scratch_than_it_has():
+    # N*K*2 = 128 MiB of bf16 x alone: refused before anything is launched
+    M, K, N = 256, 16384, 4096
+    lib = _native.hip_lib()
+    with pytest.raises(_native.ChatnetArgumentError):
+        _native.check(lib.chatnet_matmul_noalloc(2, 16, 16, 16, M, K, N, None))
