@@ -635,6 +635,7 @@ int launch_token(chatnet_model* m, bool lm_head, int cap, bool decode = false) {
     // a few chunks are combined by the O GEMV as it stages x (no merge launch)
     at.fold = plan.splits > 1 && plan.splits <= kFoldMaxSplits;
     at.stop = a.stop;
+    at.hsplit = attn_decode_hsplit(c.n_kv_heads, at.kv_mul, plan.splits, m->num_cus);
     HIP_TRY(attn_decode_launch(at, st));
 
     GemvArgs o = base_args(m, decode);

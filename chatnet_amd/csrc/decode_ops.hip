@@ -5,6 +5,9 @@
 
 namespace {
 
+// The stop flag of launches outside a decode loop (never set).
+static __device__ int g_never_stop = 0;
+
 // LlamaModel.LoadEmbedding (LlamaModel.cs:365-394): F32 row copy, F16
 // per-element conversion, Q4_0 row dequantization (DequantQ4_0.cs:28-58).
 __global__ __launch_bounds__(CN_BLOCK) void embed_kernel(const void* emb, int type, int dim,
@@ -121,61 +124,73 @@ __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
   constexpr int EPL = HD / 16;   // head elements per lane
   constexpr int NW = CN_BLOCK / CN_WAVE;
   constexpr int SP = 4 * PG;     // positions per wave step
-  const int kvh = blockIdx.x / a.splits;
+  // workgroup (kv head, head group, split): a.hsplit workgroups share a kv
+  // head, each taking kvm = kv_mul / hsplit of its query heads
   const int split = blockIdx.x % a.splits;
+  const int hs = (blockIdx.x / a.splits) % a.hsplit;
+  const int kvh = blockIdx.x / (a.splits * a.hsplit);
+  const int kvm = a.kv_mul / a.hsplit;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row = lane >> 4, col = lane & 15;
-  const int WH = a.kv_mul >= 4 ? 4 : (a.kv_mul >= 2 ? 2 : 1);
+  const int WH = kvm >= 4 ? 4 : (kvm >= 2 ? 2 : 1);
   const int WP = NW / WH;
   const int hw = wave % WH, pw = wave / WH;
-  const int h0 = kvh * a.kv_mul;
+  const int h0 = kvh * a.kv_mul + hs * kvm;
   const int p0 = split * a.chunk;
-  const int pcap = min(p0 + a.chunk, a.ctx);  // this split's positions, all inside the cache
+  const int pcap = min(p0 + a.chunk, a.ctx);  // this split's positions, all inside the cache (p0 < ctx)
   const size_t koff = (size_t)kvh * HD + col * EPL;
   __shared__ float so[NW * HPW * HD];
   __shared__ float sml[NW * HPW * 2];
-  const int seq = *a.pos + 1;
-  if (a.stop && *a.stop) return;
+  // position and stop flag: vector loads consumed after the first K/V loads
+  // are issued (a scalar read would be waited for before them)
+  const int pos_v = cn_load_late(a.pos);
+  const int stop_v = cn_load_late(a.stop ? a.stop : &g_never_stop);
+  bool first_pass = true;
 
-  for (int jg = 0; jg < a.kv_mul; jg += WH * HPW) {
+  for (int jg = 0; jg < kvm; jg += WH * HPW) {
     const int jb = jg + hw * HPW;                      // the wave's first head of this pass
-    const int nj = max(0, min(HPW, a.kv_mul - jb));    // its heads in this pass
+    const int nj = max(0, min(HPW, kvm - jb));         // its heads in this pass
     float q[HPW][EPL], m[HPW], l[HPW], o[HPW][EPL];
 #pragma unroll
     for (int j = 0; j < HPW; j++) {
-      if (j < nj) {
-        kv_load_n<false, EPL>(a.q, (size_t)(h0 + jb + j) * HD + col * EPL, q[j]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < EPL; e++) q[j][e] = 0.f;
-      }
+      // straight-line loads: heads past the wave's last re-read a valid head, unused
+      const int hq = h0 + min(jb + j, kvm - 1);
+      kv_load_n<false, EPL>(a.q, (size_t)hq * HD + col * EPL, q[j]);
       m[j] = -INFINITY;
       l[j] = 0.f;
 #pragma unroll
       for (int e = 0; e < EPL; e++) o[j][e] = 0.f;
     }
+    // K/V rows of a wave step starting at position pb: rows past the chunk
+    // re-read its last position (masked below), so every load is issued
+    auto load_step = [&](int pb, float (&kr)[PG][EPL], float (&vr)[PG][EPL]) {
+#pragma unroll
+      for (int g = 0; g < PG; g++) {
+        const int p = min(pb + 4 * g + row, pcap - 1);
+        kv_load_n<F16, EPL>(a.kc, (size_t)p * a.kv_dim + koff, kr[g]);
+        kv_load_n<F16, EPL>(a.vc, (size_t)p * a.kv_dim + koff, vr[g]);
+      }
+    };
     // first step: positions below pcap regardless of seq
     int pb = p0 + pw * SP;
     float kr[PG][EPL], vr[PG][EPL];
-#pragma unroll
-    for (int g = 0; g < PG; g++) {
-      const int p = pb + 4 * g + row;
-      if (nj > 0 && p < pcap) {
-        kv_load_n<F16, EPL>(a.kc, (size_t)p * a.kv_dim + koff, kr[g]);
-        kv_load_n<F16, EPL>(a.vc, (size_t)p * a.kv_dim + koff, vr[g]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < EPL; e++) kr[g][e] = vr[g][e] = 0.f;
-      }
+    load_step(pb, kr, vr);
+    if (first_pass) {
+      if (__builtin_amdgcn_readfirstlane(stop_v)) return;  // uniform: before any barrier
+      first_pass = false;
     }
+    const int seq = __builtin_amdgcn_readfirstlane(pos_v) + 1;
     const int p1 = nj > 0 ? min(seq, pcap) : 0;
     while (pb < p1) {  // uniform across the wave
+      // the next step's loads go out before this step is computed
+      float kn[PG][EPL], vn[PG][EPL];
+      load_step(pb + WP * SP, kn, vn);
       float sc[PG][HPW];
 #pragma unroll
       for (int g = 0; g < PG; g++) {
         const bool on = pb + 4 * g + row < p1;
-        // rows past the sequence may hold anything the speculative first loads
-        // found: their scores become -inf and their V rows 0 by selection
+        // rows past the sequence hold re-read or stale rows: their scores
+        // become -inf and their V rows 0 by selection
 #pragma unroll
         for (int e = 0; e < EPL; e++) vr[g][e] = on ? vr[g][e] : 0.f;
 #pragma unroll
@@ -214,18 +229,13 @@ __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
         m[j] = mn;
       }
       pb += WP * SP;
-      if (pb >= p1) break;
 #pragma unroll
-      for (int g = 0; g < PG; g++) {
-        const int p = pb + 4 * g + row;
-        if (p < p1) {
-          kv_load_n<F16, EPL>(a.kc, (size_t)p * a.kv_dim + koff, kr[g]);
-          kv_load_n<F16, EPL>(a.vc, (size_t)p * a.kv_dim + koff, vr[g]);
-        } else {
+      for (int g = 0; g < PG; g++)
 #pragma unroll
-          for (int e = 0; e < EPL; e++) kr[g][e] = vr[g][e] = 0.f;
+        for (int e = 0; e < EPL; e++) {
+          kr[g][e] = kn[g][e];
+          vr[g][e] = vn[g][e];
         }
-      }
     }
     // rows -> wave: sums and o add across the 4 rows (common running max)
 #pragma unroll
@@ -267,7 +277,7 @@ __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
     __syncthreads();
     for (int i = threadIdx.x; i < WH * HPW * HD; i += CN_BLOCK) {
       const int d = i % HD, jj = (i / HD) % HPW, hh = i / (HD * HPW);  // head jg + hh*HPW + jj
-      if (jg + hh * HPW + jj >= a.kv_mul) continue;
+      if (jg + hh * HPW + jj >= kvm) continue;
       float M = -INFINITY;
       for (int w = 0; w < WP; w++) {
         const int sl = (w * WH + hh) * HPW + jj;
@@ -451,13 +461,13 @@ constexpr int attn_pg(int hd, int hpw) {
 template <int HD, bool F16, int HPW>
 void attn_launch_k(const AttnArgs& a, hipStream_t st) {
   const int n_kv = a.n_heads / a.kv_mul;
-  hipLaunchKernelGGL((attn_decode_kernel<HD, F16, HPW, attn_pg(HD, HPW)>), dim3(n_kv * a.splits), dim3(CN_BLOCK), 0,
-                     st, a);
+  hipLaunchKernelGGL((attn_decode_kernel<HD, F16, HPW, attn_pg(HD, HPW)>), dim3(n_kv * a.hsplit * a.splits),
+                     dim3(CN_BLOCK), 0, st, a);
 }
 
 template <int HD, bool F16>
 hipError_t attn_launch_t(const AttnArgs& a, hipStream_t st) {
-  const int hpw = attn_hpw(a.kv_mul);
+  const int hpw = attn_hpw(a.kv_mul / a.hsplit);
   if (hpw == 1) attn_launch_k<HD, F16, 1>(a, st);
   else if (hpw == 2 || HD > 128) attn_launch_k<HD, F16, 2>(a, st);
   else attn_launch_k<HD, F16, 4>(a, st);
@@ -474,6 +484,14 @@ hipError_t embed_launch(const void* emb, int type, int dim, const int* tok, floa
   return hipGetLastError();
 }
 
+int attn_decode_hsplit(int n_kv_heads, int kv_mul, int splits, int num_cus) {
+  // split a kv head's query heads over workgroups while the launch stays within
+  // one workgroup per CU and every workgroup keeps at least two heads
+  int hs = 1;
+  while (kv_mul % (2 * hs) == 0 && kv_mul / (2 * hs) >= 2 && n_kv_heads * 2 * hs * splits <= num_cus) hs *= 2;
+  return hs;
+}
+
 int attn_decode_round(int head_dim, int kv_mul) {
   const int wh = kv_mul >= 4 ? 4 : (kv_mul >= 2 ? 2 : 1);
   int hpw = attn_hpw(kv_mul);
@@ -482,7 +500,9 @@ int attn_decode_round(int head_dim, int kv_mul) {
 }
 
 hipError_t attn_decode_launch(const AttnArgs& a, hipStream_t st) {
-  if (a.splits < 1 || a.splits > 64 || a.chunk < 1 || a.head_dim % 16 != 0) return hipErrorInvalidValue;
+  if (a.splits < 1 || a.splits > 64 || a.chunk < 1 || a.head_dim % 16 != 0 || a.hsplit < 1 ||
+      a.kv_mul % a.hsplit != 0)
+    return hipErrorInvalidValue;
   if (a.head_dim == 64) return a.kv_f16 ? attn_launch_t<64, true>(a, st) : attn_launch_t<64, false>(a, st);
   if (a.head_dim == 128) return a.kv_f16 ? attn_launch_t<128, true>(a, st) : attn_launch_t<128, false>(a, st);
   if (a.head_dim == 32) return a.kv_f16 ? attn_launch_t<32, true>(a, st) : attn_launch_t<32, false>(a, st);

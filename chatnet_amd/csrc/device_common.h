@@ -6,8 +6,42 @@
 
 typedef uint32_t cn_u32x4 __attribute__((ext_vector_type(4)));
 
+// Global-memory address space.  A pointer rebuilt from integers (a segment
+// chosen with masks, a realigned address) is generic to the compiler, and
+// generic ("flat") loads count against both the vector-memory and the
+// LDS/scalar wait counters, so every LDS or scalar wait would also wait for
+// the weight stream in flight.  Weight rows are read through pointers cast
+// back to this address space, which compiles to global loads.
+#define CN_GLOBAL __attribute__((address_space(1)))
+typedef CN_GLOBAL const uint8_t cn_gbyte;
+
 #define CN_WAVE 64
 #define CN_BLOCK 256
+
+// A zero the compiler cannot see through.  Indexing a uniform address with it
+// makes the load a vector load, which is issued with the loads around it and
+// waited for only where its value is used; a scalar load of the same word is
+// waited for at the first scalar wait of the kernel, before any later load is
+// issued.  (A register move only; no memory is touched.)
+__device__ __forceinline__ int cn_opaque_zero() {
+  int z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return z;
+}
+
+// *p read as a vector load that the kernel consumes late (see cn_opaque_zero);
+// the value is uniform, so __builtin_amdgcn_readfirstlane recovers it.
+__device__ __forceinline__ int cn_load_late(const int* p) { return p[cn_opaque_zero()]; }
+
+// RoPE (cos, sin) of the pair at even element i of a head at position pos:
+// theta = pos * exp(i * (1/hd) * (-ln base)), TensorMath.ApplyRoPE's angle
+// (TensorMath.cs:418-432), evaluated exactly as the span kernels' table.
+__device__ __forceinline__ float2 cn_rope_cs(int pos, int i, float dim_inv, float neg_log_base) {
+  const float theta = (float)pos * expf((float)i * dim_inv * neg_log_base);
+  float s, c;
+  sincosf(theta, &s, &c);
+  return make_float2(c, s);
+}
 
 // Exact IEEE binary16 -> binary32 (v_cvt_f32_f16 keeps f16 subnormals; the
 // reference's System.Half conversion, DequantQ4_0.cs:190-194, is exact too).

@@ -105,7 +105,11 @@ struct XStage<MAXT, false> {
 // Issues every load of the staged x before the caller issues its weight
 // loads: vector-memory counters retire in order, so loads issued after the
 // weight stream could not be consumed before the whole stream had landed.
-// BS threads stage the K/8 items, item t on thread t % BS.
+// Every load is issued unconditionally (threads past the last item re-read
+// the last one; stage_digitize ignores them): a load issued on only some paths leaves
+// the compiler unable to count the loads after x, and it then waits for all
+// of them, weights included.  BS threads stage the K/8 items, item t on
+// thread t % BS.
 template <int MAXT, bool NORM, int BS, bool MERGE = false>
 __device__ __forceinline__ void stage_load(const float* __restrict__ x, const float* __restrict__ norm_w, int K,
                                            XStage<MAXT, NORM>& st, const MergeSrc& ms = MergeSrc{}) {
@@ -113,20 +117,17 @@ __device__ __forceinline__ void stage_load(const float* __restrict__ x, const fl
 #pragma unroll
   for (int j = 0; j < MAXT; j++) {
     const int t = threadIdx.x + BS * j;
-    const int b = t >> 2, k = t & 3;
+    const bool on = t < ntask;
+    const int tc = on ? t : ntask - 1;
+    const int b = tc >> 2, k = tc & 3;
     float4 lo = make_float4(0.f, 0.f, 0.f, 0.f), hi = lo, glo = lo, ghi = lo;
-    if (t < ntask) {
-      if constexpr (MERGE) {
-        lo = merged_x4(ms, 32 * b + 4 * k);
-        hi = merged_x4(ms, 32 * b + 16 + 4 * k);
-      } else {
-        lo = *reinterpret_cast<const float4*>(x + 32 * b + 4 * k);
-        hi = *reinterpret_cast<const float4*>(x + 32 * b + 16 + 4 * k);
-      }
-      if constexpr (NORM) {
-        glo = *reinterpret_cast<const float4*>(norm_w + 32 * b + 4 * k);
-        ghi = *reinterpret_cast<const float4*>(norm_w + 32 * b + 16 + 4 * k);
-      }
+    if constexpr (!MERGE) {  // merged x: stage_merge_load / stage_merge
+      lo = *reinterpret_cast<const float4*>(x + 32 * b + 4 * k);
+      hi = *reinterpret_cast<const float4*>(x + 32 * b + 16 + 4 * k);
+    }
+    if constexpr (NORM) {
+      glo = *reinterpret_cast<const float4*>(norm_w + 32 * b + 4 * k);
+      ghi = *reinterpret_cast<const float4*>(norm_w + 32 * b + 16 + 4 * k);
     }
     st.x[j][0] = lo.x; st.x[j][1] = lo.y; st.x[j][2] = lo.z; st.x[j][3] = lo.w;
     st.x[j][4] = hi.x; st.x[j][5] = hi.y; st.x[j][6] = hi.z; st.x[j][7] = hi.w;
@@ -134,6 +135,66 @@ __device__ __forceinline__ void stage_load(const float* __restrict__ x, const fl
       st.g[j][0] = glo.x; st.g[j][1] = glo.y; st.g[j][2] = glo.z; st.g[j][3] = glo.w;
       st.g[j][4] = ghi.x; st.g[j][5] = ghi.y; st.g[j][6] = ghi.z; st.g[j][7] = ghi.w;
     }
+  }
+}
+
+// x of the base-16 staging read from the decode attention's chunk partials
+// (ADD_MERGE), in two phases so the weight loads need not wait for them:
+// stage_merge_load issues the loads of every chunk's (max, sum) and outputs
+// for the thread's items (the two float4 of an item lie in one head: 32-element
+// blocks never straddle a head), then, after the caller has issued its weight
+// loads, stage_merge combines them as merged_x4 does.
+template <int MAXT>
+struct XMerge {
+  float2 ml[MAXT][kFoldMaxSplits];
+  float4 lo[MAXT][kFoldMaxSplits], hi[MAXT][kFoldMaxSplits];
+};
+
+template <int MAXT, int BS>
+__device__ __forceinline__ void stage_merge_load(const MergeSrc& m, int K, XMerge<MAXT>& r) {
+  const int ntask = K >> 3;
+#pragma unroll
+  for (int j = 0; j < MAXT; j++) {
+    const int t = threadIdx.x + BS * j;
+    const int tc = t < ntask ? t : ntask - 1;
+    const int i = 32 * (tc >> 2) + 4 * (tc & 3);  // first element of the item's low float4
+    const int h = i / m.hd, d = i - h * m.hd;
+    const size_t base = (size_t)h * m.splits;
+#pragma unroll
+    for (int c = 0; c < kFoldMaxSplits; c++) {  // chunks past splits re-read the last one, weight 0
+      const size_t s = base + (c < m.splits ? c : m.splits - 1);
+      r.ml[j][c] = *reinterpret_cast<const float2*>(m.ml + 2 * s);
+      r.lo[j][c] = *reinterpret_cast<const float4*>(m.o + s * m.hd + d);
+      r.hi[j][c] = *reinterpret_cast<const float4*>(m.o + s * m.hd + d + 16);
+    }
+  }
+}
+
+template <int MAXT, bool NORM>
+__device__ __forceinline__ void stage_merge(const MergeSrc& m, const XMerge<MAXT>& r, XStage<MAXT, NORM>& st) {
+#pragma unroll
+  for (int j = 0; j < MAXT; j++) {
+    float2 ml[kFoldMaxSplits];
+    float M = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < kFoldMaxSplits; c++) {
+      ml[c] = r.ml[j][c];
+      if (c >= m.s_eff) ml[c].y = 0.f;
+      if (ml[c].y > 0.f) M = fmaxf(M, ml[c].x);
+    }
+    float L = 0.f;
+    float4 lo = make_float4(0.f, 0.f, 0.f, 0.f), hi = lo;
+#pragma unroll
+    for (int c = 0; c < kFoldMaxSplits; c++) {
+      if (ml[c].y > 0.f) {
+        const float f = expf(ml[c].x - M);
+        L += ml[c].y * f;
+        lo.x += r.lo[j][c].x * f; lo.y += r.lo[j][c].y * f; lo.z += r.lo[j][c].z * f; lo.w += r.lo[j][c].w * f;
+        hi.x += r.hi[j][c].x * f; hi.y += r.hi[j][c].y * f; hi.z += r.hi[j][c].z * f; hi.w += r.hi[j][c].w * f;
+      }
+    }
+    st.x[j][0] = lo.x / L; st.x[j][1] = lo.y / L; st.x[j][2] = lo.z / L; st.x[j][3] = lo.w / L;
+    st.x[j][4] = hi.x / L; st.x[j][5] = hi.y / L; st.x[j][6] = hi.z / L; st.x[j][7] = hi.w / L;
   }
 }
 
@@ -156,7 +217,7 @@ __device__ __forceinline__ void stage_digitize(const XStage<MAXT, NORM>& st, int
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       v[i] = st.x[j][i];
-      ss += v[i] * v[i];
+      ss += on ? v[i] * v[i] : 0.f;  // threads past the last item hold a re-read item
     }
     if constexpr (NORM) {
 #pragma unroll
@@ -262,21 +323,21 @@ __device__ __forceinline__ void stage_load16(const float* __restrict__ x, const 
 #pragma unroll
   for (int j = 0; j < MAXT; j++) {
     const int t = threadIdx.x + BS * j;
+    const bool on = t < ngroups;
+    const int tc = on ? t : ngroups - 1;  // loads issued unconditionally (see stage_load)
     MergeW mw{};
     int mh = 0, md = 0;
     if constexpr (MERGE) {  // the group's 16 elements lie in one head
-      mh = (16 * t) / ms.hd;
-      md = 16 * t - mh * ms.hd;
-      if (t < ngroups) mw = merge_weights(ms, mh);
+      mh = (16 * tc) / ms.hd;
+      md = 16 * tc - mh * ms.hd;
+      mw = merge_weights(ms, mh);
     }
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f), g = v;
-      if (t < ngroups) {
-        if constexpr (MERGE) v = merge_apply(ms, mw, mh, md + 4 * c);
-        else v = *reinterpret_cast<const float4*>(x + 16 * t + 4 * c);
-        if constexpr (NORM) g = *reinterpret_cast<const float4*>(norm_w + 16 * t + 4 * c);
-      }
+      float4 v, g = make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (MERGE) v = merge_apply(ms, mw, mh, md + 4 * c);
+      else v = *reinterpret_cast<const float4*>(x + 16 * tc + 4 * c);
+      if constexpr (NORM) g = *reinterpret_cast<const float4*>(norm_w + 16 * tc + 4 * c);
       st.x[j][4 * c + 0] = v.x; st.x[j][4 * c + 1] = v.y; st.x[j][4 * c + 2] = v.z; st.x[j][4 * c + 3] = v.w;
       if constexpr (NORM) {
         st.g[j][4 * c + 0] = g.x; st.g[j][4 * c + 1] = g.y; st.g[j][4 * c + 2] = g.z; st.g[j][4 * c + 3] = g.w;
@@ -295,10 +356,11 @@ __device__ __forceinline__ void stage_digitize16(const XStage16<MAXT, NORM>& st,
   for (int j = 0; j < MAXT; j++) {
     const int t = threadIdx.x + BS * j;
     float v[16];
+    const bool on = t < ngroups;  // threads past the last group hold a re-read group
 #pragma unroll
     for (int i = 0; i < 16; i++) {
       v[i] = st.x[j][i];
-      ss += v[i] * v[i];
+      ss += on ? v[i] * v[i] : 0.f;
     }
     if constexpr (NORM) {
 #pragma unroll
@@ -319,7 +381,7 @@ __device__ __forceinline__ void stage_digitize16(const XStage16<MAXT, NORM>& st,
       sum += X;
       U[i] = (uint32_t)(X + 0x808080);
     }
-    if (t < ngroups) {
+    if (on) {
       uint32_t* rec = xd + (t >> 3) * XD6_UNIT_DW + 16 * (t & 7);
       uint32_t P[3][4];
 #pragma unroll
@@ -347,17 +409,17 @@ __device__ __forceinline__ void stage_digitize16(const XStage16<MAXT, NORM>& st,
 // Unit loads
 // ---------------------------------------------------------------------------
 template <int QT>
-__device__ __forceinline__ void load_unit(const uint8_t* row, int u, uint32_t* w);
+__device__ __forceinline__ void load_unit(const cn_gbyte* row, int u, uint32_t* w);
 
 template <>
-__device__ __forceinline__ void load_unit<QT_Q4_0>(const uint8_t* row, int u, uint32_t* w) {
-  const uint32_t* p = reinterpret_cast<const uint32_t*>(row + (size_t)u * 36);
+__device__ __forceinline__ void load_unit<QT_Q4_0>(const cn_gbyte* row, int u, uint32_t* w) {
+  const CN_GLOBAL uint32_t* p = (const CN_GLOBAL uint32_t*)(row + (size_t)u * 36);
 #pragma unroll
   for (int k = 0; k < 9; k++) w[k] = p[k];
 }
 
-__device__ __forceinline__ void load_u32x4(const uint8_t* p, uint32_t* w) {
-  const cn_u32x4 t = *reinterpret_cast<const cn_u32x4*>(p);
+__device__ __forceinline__ void load_u32x4(const cn_gbyte* p, uint32_t* w) {
+  const cn_u32x4 t = *(const CN_GLOBAL cn_u32x4*)p;
   w[0] = t.x;
   w[1] = t.y;
   w[2] = t.z;
@@ -367,8 +429,8 @@ __device__ __forceinline__ void load_u32x4(const uint8_t* p, uint32_t* w) {
 // Half h = u & 1 of Q4_K super-block u >> 1 (144 bytes, 16-byte aligned):
 // w[0..3] = d, dmin and the 12 scale bytes, w[4..19] = qs[64h .. 64h+63].
 template <>
-__device__ __forceinline__ void load_unit<QT_Q4_K>(const uint8_t* row, int u, uint32_t* w) {
-  const uint8_t* sb = row + (size_t)(u >> 1) * 144;
+__device__ __forceinline__ void load_unit<QT_Q4_K>(const cn_gbyte* row, int u, uint32_t* w) {
+  const cn_gbyte* sb = row + (size_t)(u >> 1) * 144;
   const int h = u & 1;
   load_u32x4(sb, w);
 #pragma unroll
@@ -378,8 +440,8 @@ __device__ __forceinline__ void load_unit<QT_Q4_K>(const uint8_t* row, int u, ui
 // Two Q8_0 blocks, 68 bytes: rows hold whole pairs (K % 64 == 0), so a unit
 // starts on a 4-byte boundary.
 template <>
-__device__ __forceinline__ void load_unit<QT_Q8_0>(const uint8_t* row, int u, uint32_t* w) {
-  const uint32_t* p = reinterpret_cast<const uint32_t*>(row + (size_t)u * 68);
+__device__ __forceinline__ void load_unit<QT_Q8_0>(const cn_gbyte* row, int u, uint32_t* w) {
+  const CN_GLOBAL uint32_t* p = (const CN_GLOBAL uint32_t*)(row + (size_t)u * 68);
 #pragma unroll
   for (int k = 0; k < 17; k++) w[k] = p[k];
 }
@@ -388,8 +450,8 @@ __device__ __forceinline__ void load_unit<QT_Q8_0>(const uint8_t* row, int u, ui
 // w[0..3] = d, dmin and the scales, w[4..7] = qh[16h .. 16h+15] (the fifth
 // bits of elements 128h ..), w[8..23] = qs[64h .. 64h+63].
 template <>
-__device__ __forceinline__ void load_unit<QT_Q5_K>(const uint8_t* row, int u, uint32_t* w) {
-  const uint8_t* sb = row + (size_t)(u >> 1) * 176;
+__device__ __forceinline__ void load_unit<QT_Q5_K>(const cn_gbyte* row, int u, uint32_t* w) {
+  const cn_gbyte* sb = row + (size_t)(u >> 1) * 176;
   const int h = u & 1;
   load_u32x4(sb, w);
   load_u32x4(sb + 16 + 16 * h, w + 4);
@@ -407,12 +469,12 @@ __device__ __forceinline__ void load_unit<QT_Q5_K>(const uint8_t* row, int u, ui
 // sh = 2 (it then ends at byte 209), and d is a 16-bit load, so nothing past
 // the super-block is read.
 template <>
-__device__ __forceinline__ void load_unit<QT_Q6_K>(const uint8_t* row, int u, uint32_t* w) {
-  const uint8_t* sb = row + (size_t)(u >> 1) * 210;
+__device__ __forceinline__ void load_unit<QT_Q6_K>(const cn_gbyte* row, int u, uint32_t* w) {
+  const cn_gbyte* sb = row + (size_t)(u >> 1) * 210;
   const int h = u & 1;
   const uintptr_t base = reinterpret_cast<uintptr_t>(sb);
   const uint32_t sh = (uint32_t)(base & 3);  // 0 or 2
-  const uint32_t* q = reinterpret_cast<const uint32_t*>(base & ~(uintptr_t)3);
+  const CN_GLOBAL uint32_t* q = (const CN_GLOBAL uint32_t*)(base & ~(uintptr_t)3);
   uint32_t r[17], t[9], c[3];
 #pragma unroll
   for (int k = 0; k < 17; k++) r[k] = q[16 * h + k];
@@ -427,7 +489,7 @@ __device__ __forceinline__ void load_unit<QT_Q6_K>(const uint8_t* row, int u, ui
   for (int k = 0; k < 8; k++) w[16 + k] = __builtin_amdgcn_alignbyte(t[k + 1], t[k], sh);
   w[24] = __builtin_amdgcn_alignbyte(c[1], c[0], sh);
   w[25] = __builtin_amdgcn_alignbyte(c[2], c[1], sh);
-  w[26] = *reinterpret_cast<const uint16_t*>(sb + 208);
+  w[26] = *(const CN_GLOBAL uint16_t*)(sb + 208);
 }
 
 // ---------------------------------------------------------------------------
@@ -686,6 +748,11 @@ __device__ __forceinline__ void dot_unit_k45_dig8(const uint32_t (*w)[QTraits<QT
 }
 
 // Issues the loads of one wave iteration: RPW rows x NU units per lane.
+// Every load is issued (a row past n_vrows re-reads the last row, a unit past
+// the row's end the last unit) so the loads are straight-line code: the
+// caller discards those rows (the epilogue skips them) and units (the dot
+// skips them), and the compiler can count exactly how many loads follow the
+// staged x (a load on a conditional path makes it wait for all of them).
 template <int QT, int RPW, int LPR, int NU, int EPI>
 __device__ __forceinline__ void issue_loads(const GemvArgs& a, int it, int sub, int li, int nunits, size_t bpr,
                                             uint32_t (&w)[RPW][NU][QTraits<QT>::NDW]) {
@@ -693,20 +760,14 @@ __device__ __forceinline__ void issue_loads(const GemvArgs& a, int it, int sub, 
   const int vr0 = it * RW + sub * RPW;
 #pragma unroll
   for (int i = 0; i < RPW; i++) {
-    const int vr = vr0 + i;
-    const bool ok = vr < a.n_vrows;
+    const int vr = vr0 + i < a.n_vrows ? vr0 + i : a.n_vrows - 1;
     int seg, r;
-    map_row<EPI>(a, ok ? vr : 0, seg, r);
-    const uint8_t* rp = seg_w(a, seg) + (size_t)r * bpr;
+    map_row<EPI>(a, vr, seg, r);
+    const cn_gbyte* rp = seg_w(a, seg) + (size_t)r * bpr;
 #pragma unroll
     for (int n = 0; n < NU; n++) {
       const int u = li + LPR * n;
-      if (ok && u < nunits) {
-        load_unit<QT>(rp, u, w[i][n]);
-      } else {
-#pragma unroll
-        for (int k = 0; k < QTraits<QT>::NDW; k++) w[i][n][k] = 0;
-      }
+      load_unit<QT>(rp, u < nunits ? u : nunits - 1, w[i][n]);
     }
   }
 }
@@ -739,17 +800,22 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
   uint32_t w[RPW][NU][T::NDW];
   constexpr int NR = res_count<EPI, RPW>();
   float res[NR];
-  const int pos = EPI == GEMV_EPI_QKV ? *a.pos : 0;
-  // read with the first loads, tested after staging (uniform across the grid)
-  const int stopped = a.stop ? *a.stop : 0;
+  // The stop flag and the position are read as vector loads issued ahead of
+  // x and consumed late (after staging, in the epilogue), so no scalar wait
+  // for them stalls the loads at the start.
   constexpr bool MERGE = EPI == GEMV_EPI_ADD_MERGE;
+  const int stop_v = cn_load_late(stop_flag(a));
+  const int pos_v = (EPI == GEMV_EPI_QKV || MERGE) ? cn_load_late(a.pos) : 0;
+  constexpr bool kDig8 = QT == QT_Q8_0 || QT == QT_Q6_K || QT == QT_Q5_K || (QT == QT_Q4_K && LPR > 32);
   MergeSrc ms{};
   if constexpr (MERGE) {
     ms.o = a.part_o;
     ms.ml = a.part_ml;
     ms.hd = a.head_dim;
     ms.splits = a.msplits;
-    ms.s_eff = min(a.msplits, (*a.pos + a.mchunk) / a.mchunk);  // chunks below pos + 1
+    // the base-256 staging merges while it loads: it needs the position now
+    if constexpr (kDig8)
+      ms.s_eff = min(a.msplits, (__builtin_amdgcn_readfirstlane(pos_v) + a.mchunk) / a.mchunk);
   }
 
   // ---- prologue: stage x (optionally RMS-normalised) into LDS ----
@@ -757,7 +823,6 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
   // up to K = 4096 (the register budget of the staged x at 16 items per
   // half-super-block lane); base-256 digits on v_dot4_i32_i8 for Q8_0, Q6_K,
   // Q5_K and the longer Q4_K rows.
-  constexpr bool kDig8 = QT == QT_Q8_0 || QT == QT_Q6_K || QT == QT_Q5_K || (QT == QT_Q4_K && LPR > 32);
   {
     constexpr bool NORM = EPI == GEMV_EPI_QKV || EPI == GEMV_EPI_SWIGLU || EPI == GEMV_EPI_LOGITS;
     uint32_t* xd = reinterpret_cast<uint32_t*>(smem);
@@ -773,22 +838,29 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
       constexpr bool kLate = NU >= 2;
       if constexpr (!kLate) {
         issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
-        load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, pos, res);
+        load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, 0, res);
       }
       xred = reinterpret_cast<float*>(smem) + (size_t)((K + 127) >> 7) * XD6_UNIT_DW;
       stage_digitize16<MAXT, NORM, BS>(st, K, xd, xred);
       if constexpr (kLate) {
         issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
-        load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, pos, res);
+        load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, 0, res);
       }
     } else {
       // items per thread: K <= UNIT * LPR * NU, so K/8 <= (UNIT/8) * LPR * NU items over BS threads
       constexpr int MAXT = ((UNIT / 8) * LPR * NU + BS - 1) / BS;
       XStage<MAXT, NORM> st;
       stage_load<MAXT, NORM, BS, MERGE>(a.x, a.norm_w, K, st, ms);
-      // rows past n_vrows come back as zeros, so idle waves need no branch here
+      XMerge<MERGE ? MAXT : 1> mr;
+      if constexpr (MERGE) stage_merge_load<MAXT, BS>(ms, K, mr);
+      // rows past n_vrows are loaded (re-reading the last row) and skipped
       issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
-      load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, pos, res);
+      load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, 0, res);
+      if constexpr (MERGE) {
+        // chunks below pos + 1 (the position arrives with the partials)
+        ms.s_eff = min(a.msplits, (__builtin_amdgcn_readfirstlane(pos_v) + a.mchunk) / a.mchunk);
+        stage_merge<MAXT, NORM>(ms, mr, st);
+      }
       xred = reinterpret_cast<float*>(smem) + (size_t)(K >> 6) * XD_UNIT_DW;
       stage_digitize<MAXT, NORM, BS, QT == QT_Q4_K>(st, K, xd, xred);
     }
@@ -797,8 +869,10 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int v = 0; v < NWV; v++) ss += xred[v];
     const float rms = NORM ? 1.0f / sqrtf(ss / (float)K + a.eps) : 1.0f;
-    if (stopped) return;
+    if (__builtin_amdgcn_readfirstlane(stop_v)) return;
+    const int pos = __builtin_amdgcn_readfirstlane(pos_v);
     while (it < n_iters) {
+      load_rope<EPI, RPW, NR>(a, it * RW + sub * RPW, pos, res);
       float acc[RPW];
 #pragma unroll
       for (int i = 0; i < RPW; i++) acc[i] = 0.f;
@@ -825,7 +899,7 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
       it += wstride;
       if (it < n_iters) {
         issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
-        load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, pos, res);
+        load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, 0, res);
       }
 #pragma unroll
       for (int i = 0; i < RPW; i++) {
@@ -1013,17 +1087,12 @@ __global__ __launch_bounds__(BS) void gemv_ks_kernel(GemvArgs a) {
 
   uint32_t w[RPW][9];
   float res[NR];
-  const int stopped = a.stop ? *a.stop : 0;
-  auto load = [&](int itn) {
+  const int stop_v = cn_load_late(stop_flag(a));  // consumed after staging
+  auto load = [&](int itn) {  // straight-line loads, as issue_loads
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
-      const int vr = itn * RPW + i;
-      if (vr < a.n_vrows && u < nunits) {
-        load_unit<QT_Q4_0>(a.w[0] + (size_t)vr * bpr, u, w[i]);
-      } else {
-#pragma unroll
-        for (int k = 0; k < 9; k++) w[i][k] = 0;
-      }
+      const int vr = itn * RPW + i < a.n_vrows ? itn * RPW + i : a.n_vrows - 1;
+      load_unit<QT_Q4_0>((const cn_gbyte*)a.w[0] + (size_t)vr * bpr, u < nunits ? u : nunits - 1, w[i]);
     }
   };
   // items per thread: K/8 <= 8 * 64 * KS items over BS = 64 * KS * NRG threads
@@ -1037,7 +1106,7 @@ __global__ __launch_bounds__(BS) void gemv_ks_kernel(GemvArgs a) {
   float* part = xred + 16;  // [NRG][KS-1][RPW]
   stage_digitize<MAXT, false, BS>(st, K, xd, xred);
   __syncthreads();
-  if (stopped) return;
+  if (__builtin_amdgcn_readfirstlane(stop_v)) return;
   while (base < n_iters) {
     float acc[RPW];
 #pragma unroll

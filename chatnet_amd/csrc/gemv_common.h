@@ -9,6 +9,11 @@
 
 namespace {
 
+// The stop flag of launches outside a decode loop (never set).
+static __device__ int cn_never_stop = 0;
+
+__device__ __forceinline__ const int* stop_flag(const GemvArgs& a) { return a.stop ? a.stop : &cn_never_stop; }
+
 // x read from the decode attention's per-chunk partials (ADD_MERGE): element
 // i belongs to head i / hd; each active chunk c (c < s_eff) holds the running
 // max M_c, sum L_c and unnormalised output O_c of its positions, and
@@ -33,10 +38,10 @@ __device__ __forceinline__ float4 merged_x4(const MergeSrc& m, int i) {
   float4 oc[kFoldMaxSplits];
   float M = -INFINITY;
 #pragma unroll
-  for (int c = 0; c < kFoldMaxSplits; c++) {
-    const bool in = c < m.splits;
-    ml[c] = in ? *reinterpret_cast<const float2*>(m.ml + 2 * (base + c)) : make_float2(0.f, 0.f);
-    oc[c] = in ? *reinterpret_cast<const float4*>(m.o + (base + c) * m.hd + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int c = 0; c < kFoldMaxSplits; c++) {  // straight-line loads: chunks past splits re-read the last
+    const int cc = c < m.splits ? c : m.splits - 1;
+    ml[c] = *reinterpret_cast<const float2*>(m.ml + 2 * (base + cc));
+    oc[c] = *reinterpret_cast<const float4*>(m.o + (base + cc) * m.hd + d);
     if (c >= m.s_eff) ml[c].y = 0.f;
     if (ml[c].y > 0.f) M = fmaxf(M, ml[c].x);
   }
@@ -68,8 +73,8 @@ __device__ __forceinline__ MergeW merge_weights(const MergeSrc& m, int h) {
   float2 ml[kFoldMaxSplits];
   float M = -INFINITY;
 #pragma unroll
-  for (int c = 0; c < kFoldMaxSplits; c++) {
-    ml[c] = c < m.splits ? *reinterpret_cast<const float2*>(m.ml + 2 * (base + c)) : make_float2(0.f, 0.f);
+  for (int c = 0; c < kFoldMaxSplits; c++) {  // straight-line loads: chunks past splits re-read the last
+    ml[c] = *reinterpret_cast<const float2*>(m.ml + 2 * (base + (c < m.splits ? c : m.splits - 1)));
     if (c >= m.s_eff) ml[c].y = 0.f;
     if (ml[c].y > 0.f) M = fmaxf(M, ml[c].x);
   }
@@ -89,13 +94,13 @@ __device__ __forceinline__ float4 merge_apply(const MergeSrc& m, const MergeW& w
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int c = 0; c < kFoldMaxSplits; c++) {
-    if (c < m.splits) {
-      const float4 o = *reinterpret_cast<const float4*>(m.o + (base + c) * m.hd + d);
-      acc.x += o.x * w.f[c];
-      acc.y += o.y * w.f[c];
-      acc.z += o.z * w.f[c];
-      acc.w += o.w * w.f[c];
-    }
+    // chunks past splits re-read the last one (finite: every chunk of the
+    // launch is written each step) with weight 0
+    const float4 o = *reinterpret_cast<const float4*>(m.o + (base + (c < m.splits ? c : m.splits - 1)) * m.hd + d);
+    acc.x += o.x * w.f[c];
+    acc.y += o.y * w.f[c];
+    acc.z += o.z * w.f[c];
+    acc.w += o.w * w.f[c];
   }
   return make_float4(acc.x / w.L, acc.y / w.L, acc.z / w.L, acc.w / w.L);
 }
@@ -104,12 +109,12 @@ __device__ __forceinline__ float4 merge_apply(const MergeSrc& m, const MergeW& w
 // masks: indexing the kernel-argument arrays (or a select chain, which the
 // compiler turns into a table) would copy them to scratch, and a scratch load
 // waits on every vector-memory operation in flight.
-__device__ __forceinline__ const uint8_t* seg_w(const GemvArgs& a, int seg) {
+__device__ __forceinline__ const cn_gbyte* seg_w(const GemvArgs& a, int seg) {
   const uintptr_t w0 = reinterpret_cast<uintptr_t>(a.w[0]);
   const uintptr_t w1 = reinterpret_cast<uintptr_t>(a.w[1]);
   const uintptr_t w2 = reinterpret_cast<uintptr_t>(a.w[2]);
   const uintptr_t m1 = 0 - (uintptr_t)(seg == 1), m2 = 0 - (uintptr_t)(seg == 2);
-  return reinterpret_cast<const uint8_t*>(w0 ^ ((w0 ^ w1) & m1) ^ ((w0 ^ w2) & m2));
+  return (const cn_gbyte*)(w0 ^ ((w0 ^ w1) & m1) ^ ((w0 ^ w2) & m2));
 }
 __device__ __forceinline__ int seg_n(const GemvArgs& a, int seg) {
   return seg == 0 ? a.seg_rows[0] : (seg == 1 ? a.seg_rows[1] : a.seg_rows[2]);
@@ -135,40 +140,56 @@ __device__ __forceinline__ void map_row(const GemvArgs& a, int vr, int& seg, int
 // finishes the rows together with the weights of the same iteration, so the
 // epilogue does not wait on a load issued behind the next iteration's weights:
 //   ADD: the residual rows;
-//   QKV: (cos, sin) of each q/k row pair at position pos from the RoPE table
-//        (TensorMath.ApplyRoPE's angle, TensorMath.cs:418-432), the pair index
-//        being the row's offset within its head, in res[0..RPW); with a bias
-//        (QwenModel.cs:104-120) the rows' biases in res[RPW..2*RPW).
+//   QKV: with a bias (QwenModel.cs:104-120) the rows' biases in
+//        res[RPW..2*RPW); the (cos, sin) of the row pairs go to res[0..RPW)
+//        once the position is known (load_rope).
 template <int EPI, int RPW>
 constexpr int res_count() { return EPI == GEMV_EPI_QKV ? 2 * RPW : RPW; }
 
+// Loaded by every lane (the lanes of a row group read the same addresses),
+// rows past n_vrows clamped to the last one: straight-line loads, so the
+// compiler's count of loads in flight stays exact (see issue_loads).
 template <int EPI, int RPW, int NR>
 __device__ __forceinline__ void load_residual(const GemvArgs& a, int vr0, int li, int pos, float (&res)[NR]) {
+  (void)li;
 #pragma unroll
   for (int i = 0; i < NR; i++) res[i] = 0.f;
-  if (li != 0) return;
   if constexpr (EPI == GEMV_EPI_ADD || EPI == GEMV_EPI_ADD_MERGE) {
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
-      const int vr = vr0 + i;
-      if (vr < a.n_vrows) res[i] = a.out[0][vr];
+      const int vr = vr0 + i < a.n_vrows ? vr0 + i : a.n_vrows - 1;
+      res[i] = a.out[0][vr];
     }
   } else if constexpr (EPI == GEMV_EPI_QKV) {
+    (void)pos;
 #pragma unroll
     for (int i = 0; i < RPW; i += 2) {
-      const int vr = vr0 + i;
-      int seg, r;
-      map_row<EPI>(a, vr, seg, r);
-      if (vr < a.n_vrows && seg < 2) {
-        const float2 cs = a.rope[(size_t)pos * (a.head_dim / 2) + (r % a.head_dim) / 2];
-        res[i] = cs.x;
-        res[i + 1] = cs.y;
-      }
-      if (vr < a.n_vrows && a.bias) {
+      const int vr = vr0 + i < a.n_vrows ? vr0 + i : a.n_vrows - 2;
+      if (a.bias) {
         const float2 b = *reinterpret_cast<const float2*>(a.bias + vr);
         res[RPW + i] = b.x;
         res[RPW + i + 1] = b.y;
       }
+    }
+  }
+}
+
+// QKV: (cos, sin) of each q/k row pair at position pos from the RoPE table
+// (TensorMath.ApplyRoPE's angle, TensorMath.cs:418-432; the pair index is the
+// row's offset within its head) into res[0..RPW).  Issued once the position
+// is known, after x is staged, so the table loads (cache hits) are covered by
+// the dot product; v rows (segment 2) read an entry they do not use.
+template <int EPI, int RPW, int NR>
+__device__ __forceinline__ void load_rope(const GemvArgs& a, int vr0, int pos, float (&res)[NR]) {
+  if constexpr (EPI == GEMV_EPI_QKV) {
+#pragma unroll
+    for (int i = 0; i < RPW; i += 2) {
+      const int vr = vr0 + i < a.n_vrows ? vr0 + i : a.n_vrows - 2;
+      int seg, r;
+      map_row<EPI>(a, vr, seg, r);
+      const float2 cs = a.rope[(size_t)pos * (a.head_dim / 2) + (r % a.head_dim) / 2];
+      res[i] = cs.x;
+      res[i + 1] = cs.y;
     }
   }
 }
@@ -198,7 +219,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, const float
         x0 += res[RPW + i];
         x1 += res[RPW + i + 1];
       }
-      if (seg < 2) {
+      if (seg < 2) {  // RoPE of the pair (TensorMath.cs:408-458), (cos, sin) from load_rope
         const float c = res[i], s = res[i + 1];
         const float y0 = x0 * c - x1 * s;
         const float y1 = x0 * s + x1 * c;
@@ -216,11 +237,11 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, const float
         const uintptr_t kb = reinterpret_cast<uintptr_t>(a.kcache), vb = reinterpret_cast<uintptr_t>(a.vcache);
         const uintptr_t base = vb + ((kb - vb) & (uintptr_t)(0 - (uintptr_t)(seg == 1)));
         if (a.kv_f16) {
-          _Float16* dst = reinterpret_cast<_Float16*>(base) + off;
+          CN_GLOBAL _Float16* dst = (CN_GLOBAL _Float16*)base + off;
           dst[0] = (_Float16)x0;
           dst[1] = (_Float16)x1;
         } else {
-          float* dst = reinterpret_cast<float*>(base) + off;
+          CN_GLOBAL float* dst = (CN_GLOBAL float*)base + off;
           dst[0] = x0;
           dst[1] = x1;
         }

@@ -61,8 +61,8 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_f_kernel(GemvArgs a) {
   extern __shared__ float smem[];  // [K] staged x, then NWV partial sums of squares
   const int K = a.K;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int pos = EPI == GEMV_EPI_QKV ? *a.pos : 0;
-  const int stopped = a.stop ? *a.stop : 0;
+  const int pos_v = (EPI == GEMV_EPI_QKV || EPI == GEMV_EPI_ADD_MERGE) ? cn_load_late(a.pos) : 0;
+  const int stop_v = cn_load_late(stop_flag(a));
   float* red = smem + K;
 
   // ---- stage x * g as fp32 (sum of squares of x for the RMS factor) ----
@@ -72,7 +72,7 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_f_kernel(GemvArgs a) {
     ms.ml = a.part_ml;
     ms.hd = a.head_dim;
     ms.splits = a.msplits;
-    ms.s_eff = min(a.msplits, (*a.pos + a.mchunk) / a.mchunk);
+    ms.s_eff = min(a.msplits, (__builtin_amdgcn_readfirstlane(pos_v) + a.mchunk) / a.mchunk);
   }
   float ss = 0.f;
   for (int c = threadIdx.x; c < (K >> 2); c += CN_BLOCK) {
@@ -96,14 +96,15 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_f_kernel(GemvArgs a) {
 #pragma unroll
   for (int w = 0; w < NWV; w++) sst += red[w];
   const float rms = NORM ? 1.0f / sqrtf(sst / (float)K + a.eps) : 1.0f;
-  if (stopped) return;
+  if (__builtin_amdgcn_readfirstlane(stop_v)) return;
+  const int pos = __builtin_amdgcn_readfirstlane(pos_v);
 
   const size_t row_bytes = (size_t)K * (WT == WT_F32 ? 4 : 2);
   const int npieces = K / PE;  // 16-byte pieces per row
   const int n_iters = (a.n_vrows + RPW - 1) / RPW;
   for (int it = blockIdx.x * NWV + wave; it < n_iters; it += gridDim.x * NWV) {
     const int vr0 = it * RPW;
-    const uint8_t* rp[RPW];
+    const cn_gbyte* rp[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
       const int vr = vr0 + i < a.n_vrows ? vr0 + i : a.n_vrows - 1;  // rows past the end re-read the last
@@ -113,6 +114,7 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_f_kernel(GemvArgs a) {
     }
     float res[NR];
     load_residual<EPI, RPW, NR>(a, vr0, lane, pos, res);
+    load_rope<EPI, RPW, NR>(a, vr0, pos, res);
     float acc[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; i++) acc[i] = 0.f;
@@ -123,7 +125,7 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_f_kernel(GemvArgs a) {
         const int p = p0 + CN_WAVE * u + lane;
 #pragma unroll
         for (int i = 0; i < RPW; i++)
-          w[u][i] = p < npieces ? *reinterpret_cast<const cn_u32x4*>(rp[i] + (size_t)p * 16) : cn_u32x4{0, 0, 0, 0};
+          w[u][i] = p < npieces ? *(const CN_GLOBAL cn_u32x4*)(rp[i] + (size_t)p * 16) : cn_u32x4{0, 0, 0, 0};
       }
 #pragma unroll
       for (int u = 0; u < U; u++) {

@@ -133,11 +133,15 @@ struct AttnArgs {
   int splits;         // position chunks of the launch (<= 64), one workgroup per kv head each
   int chunk;          // positions per chunk: chunk c covers [c*chunk, (c+1)*chunk) below pos+1
   int fold;           // splits > 1: leave the partials for the O GEMV (GEMV_EPI_ADD_MERGE)
+  int hsplit;         // workgroups per kv head, each taking kv_mul / hsplit query heads
   const int* stop;    // decode loops: return at once while *stop is set (nullptr: never)
 };
 hipError_t attn_decode_launch(const AttnArgs& a, hipStream_t st);
-// Positions one decode-attention workgroup covers per round of wave steps.
+// Positions one decode-attention workgroup covers per round of wave steps
+// (kv_mul: the query heads the workgroup takes).
 int attn_decode_round(int head_dim, int kv_mul);
+// Workgroups per kv head for a launch of `splits` position chunks.
+int attn_decode_hsplit(int n_kv_heads, int kv_mul, int splits, int num_cus);
 
 // Device decode state, kDecWords ints: the position of the token being
 // forwarded, that token, the picks made so far in the current decode loop, a

@@ -18,10 +18,7 @@ __global__ __launch_bounds__(CN_BLOCK) void rope_table_kernel(float2* tab, int c
   const int idx = blockIdx.x * CN_BLOCK + threadIdx.x;
   if (idx >= ctx * half) return;
   const int pos = idx / half, i = 2 * (idx % half);
-  const float theta = (float)pos * expf((float)i * dim_inv * neg_log_base);
-  float s, c;
-  sincosf(theta, &s, &c);
-  tab[idx] = make_float2(c, s);
+  tab[idx] = cn_rope_cs(pos, i, dim_inv, neg_log_base);
 }
 
 // RoPE of the pair (x0, x1) with the table entry cs = (cos, sin).
