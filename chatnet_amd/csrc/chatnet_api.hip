@@ -51,6 +51,9 @@ struct DevTensor {
   uint32_t type = 0;
   uint64_t nbytes = 0;
   uint64_t ne0 = 0, ne1 = 1;  // GGUF dims: ne0 = inner (K), ne1 = rows (M)
+  // The matrix re-encoded for the batched GEMM (gemm_pack_launch), made by the
+  // first span that needs it and dropped when the tensor is uploaded again.
+  void* pk = nullptr;
 };
 
 struct Layer {
@@ -416,6 +419,7 @@ void chatnet_destroy(chatnet_model* m) {
   for (auto& l : m->layers) {
     fr(l.attn_norm.ptr); fr(l.ffn_norm.ptr); fr(l.wq.ptr); fr(l.wk.ptr); fr(l.wv.ptr);
     fr(l.wo.ptr); fr(l.wg.ptr); fr(l.wu.ptr); fr(l.wd.ptr); fr(l.bias);
+    fr(l.wq.pk); fr(l.wk.pk); fr(l.wv.pk); fr(l.wo.pk); fr(l.wg.pk); fr(l.wu.pk); fr(l.wd.pk);
   }
   fr(m->kcache); fr(m->vcache); fr(m->x); fr(m->q); fr(m->att); fr(m->h); fr(m->gu); fr(m->logits);
   fr(m->state); fr(m->out_tokens);
@@ -499,6 +503,8 @@ int chatnet_upload_tensor(chatnet_model* m, const char* name, uint32_t type, con
     HIP_TRY(hipStreamSynchronize(m->stream));
     (void)hipFree(slot->ptr);
     slot->ptr = nullptr;
+    if (slot->pk) (void)hipFree(slot->pk);
+    slot->pk = nullptr;
   }
   // 256 bytes of tail padding keep every vector load of the kernels in bounds.
   if (hipMalloc(&slot->ptr, nbytes + 256) != hipSuccess)
@@ -722,19 +728,53 @@ int ensure_out_tokens(chatnet_model* m, int cap) {
 constexpr int kSpanMin = 8;
 constexpr int kSpanCap = 512;
 
-bool span_batchable(const chatnet_model* m, int n) {
-  if (n < kSpanMin) return false;
+// The seven projection matrices of a layer.
+struct LayerMats {
+  DevTensor* t[7];
+};
+LayerMats layer_mats(Layer& L) { return {{&L.wq, &L.wk, &L.wv, &L.wo, &L.wg, &L.wu, &L.wd}}; }
+
+// How a span's projections read their weights: raw Q4_0 blocks when every
+// matrix is Q4_0, else packed units of every matrix (any packable types, mixed
+// freely); SPAN_NONE when some matrix can be neither (F32 / F16) and the span
+// runs token by token.
+enum SpanMode { SPAN_NONE = 0, SPAN_RAW_Q4_0 = 1, SPAN_PACKED = 2 };
+
+SpanMode span_mode(chatnet_model* m, int n) {
+  if (n < kSpanMin) return SPAN_NONE;
   const char* e = getenv("CHATNET_SPAN_BATCH");  // "0": per-token schedule for every span
-  if (e && e[0] == '0') return false;
+  if (e && e[0] == '0') return SPAN_NONE;
   const chatnet_config& c = m->cfg;
-  if (!attn_prefill_supports(c.head_dim, c.n_heads / c.n_kv_heads)) return false;
-  if (!gemm_supports(CHATNET_GGML_Q4_0, c.dim) || !gemm_supports(CHATNET_GGML_Q4_0, c.hidden_dim)) return false;
-  for (const Layer& L : m->layers) {
-    const DevTensor* ts[] = {&L.wq, &L.wk, &L.wv, &L.wo, &L.wg, &L.wu, &L.wd};
-    for (const DevTensor* t : ts)
-      if (t->type != CHATNET_GGML_Q4_0) return false;
+  if (!attn_prefill_supports(c.head_dim, c.n_heads / c.n_kv_heads)) return SPAN_NONE;
+  bool all_q4_0 = true, packable = true;
+  for (Layer& L : m->layers) {
+    const LayerMats lm = layer_mats(L);
+    for (int i = 0; i < 7; i++) {
+      const DevTensor* t = lm.t[i];
+      if (t->type != CHATNET_GGML_Q4_0 || !gemm_supports(CHATNET_GGML_Q4_0, (int)t->ne0)) all_q4_0 = false;
+      if (!gemm_pack_supports((int)t->type, (int)t->ne0)) packable = false;
+    }
   }
-  return true;
+  if (all_q4_0) return SPAN_RAW_Q4_0;
+  return packable ? SPAN_PACKED : SPAN_NONE;
+}
+
+// Packs every projection matrix not yet packed (once per upload).
+int ensure_span_packs(chatnet_model* m) {
+  for (Layer& L : m->layers) {
+    const LayerMats lm = layer_mats(L);
+    for (int i = 0; i < 7; i++) {
+      DevTensor* t = lm.t[i];
+      if (t->pk) continue;
+      const size_t bytes = gemm_pack_bytes((int)t->ne1, (int)t->ne0);
+      if (hipMalloc(&t->pk, bytes) != hipSuccess) {
+        t->pk = nullptr;
+        return fail(CHATNET_ERR_OUT_OF_MEMORY, "hipMalloc of %zu bytes (packed weights) failed", bytes);
+      }
+      HIP_TRY(gemm_pack_launch((int)t->type, t->ptr, (int)t->ne1, (int)t->ne0, t->pk, m->stream));
+    }
+  }
+  return CHATNET_OK;
 }
 
 int ensure_span_buffers(chatnet_model* m) {
@@ -774,11 +814,15 @@ int span_gemm(chatnet_model* m, GemmArgs& g) {
 
 // LlamaModel.Forward (LlamaModel.cs:93-238) over tokens[0..n) at positions
 // position.. as batches of up to span_cap tokens: every projection is one
-// MFMA GEMM over the batch, attention is causal over the cache, and the LM
-// head runs for the last token only (LlamaModel.cs:207).
-int run_span(chatnet_model* m, const int32_t* tokens, int n, int position) {
+// MFMA GEMM over the batch (raw Q4_0 blocks, or every matrix packed), attention
+// is causal over the cache, and the LM head runs for the last token only
+// (LlamaModel.cs:207).
+int run_span(chatnet_model* m, const int32_t* tokens, int n, int position, SpanMode mode) {
   int rc = ensure_span_buffers(m);
   if (rc) return rc;
+  const bool packed = mode == SPAN_PACKED;
+  if (packed && (rc = ensure_span_packs(m))) return rc;
+  auto wsrc = [packed](const DevTensor& t) { return (const uint8_t*)(packed ? t.pk : t.ptr); };
   const chatnet_config& c = m->cfg;
   hipStream_t st = m->stream;
   const int kvd = m->kv_dim, qkv_ld = c.dim + 2 * kvd;
@@ -800,9 +844,10 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position) {
       GemmArgs g;
       memset(&g, 0, sizeof(g));
       g.qtype = CHATNET_GGML_Q4_0;
-      g.w[0] = (const uint8_t*)L.wq.ptr;
-      g.w[1] = (const uint8_t*)L.wk.ptr;
-      g.w[2] = (const uint8_t*)L.wv.ptr;
+      g.packed = packed;
+      g.w[0] = wsrc(L.wq);
+      g.w[1] = wsrc(L.wk);
+      g.w[2] = wsrc(L.wv);
       g.seg_rows[0] = c.dim;
       g.seg_rows[1] = kvd;
       g.seg_rows[2] = kvd;
@@ -854,7 +899,8 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position) {
       GemmArgs o;
       memset(&o, 0, sizeof(o));
       o.qtype = CHATNET_GGML_Q4_0;
-      o.w[0] = (const uint8_t*)L.wo.ptr;
+      o.packed = packed;
+      o.w[0] = wsrc(L.wo);
       o.seg_rows[0] = c.dim;
       o.M = c.dim;
       o.K = c.dim;
@@ -871,8 +917,9 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position) {
       GemmArgs gu;
       memset(&gu, 0, sizeof(gu));
       gu.qtype = CHATNET_GGML_Q4_0;
-      gu.w[0] = (const uint8_t*)L.wg.ptr;
-      gu.w[1] = (const uint8_t*)L.wu.ptr;
+      gu.packed = packed;
+      gu.w[0] = wsrc(L.wg);
+      gu.w[1] = wsrc(L.wu);
       gu.seg_rows[0] = c.hidden_dim;
       gu.seg_rows[1] = c.hidden_dim;
       gu.seg_mode = GEMM_SEG_INTERLEAVE;
@@ -890,7 +937,8 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position) {
       GemmArgs d;
       memset(&d, 0, sizeof(d));
       d.qtype = CHATNET_GGML_Q4_0;
-      d.w[0] = (const uint8_t*)L.wd.ptr;
+      d.packed = packed;
+      d.w[0] = wsrc(L.wd);
       d.seg_rows[0] = c.dim;
       d.M = c.dim;
       d.K = c.hidden_dim;
@@ -921,7 +969,8 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position) {
 }
 
 int run_prompt(chatnet_model* m, const int32_t* tokens, int n, int position) {
-  if (span_batchable(m, n)) return run_span(m, tokens, n, position);
+  const SpanMode mode = span_mode(m, n);
+  if (mode != SPAN_NONE) return run_span(m, tokens, n, position, mode);
   for (int t = 0; t < n; t++) {
     HIP_TRY(set_state_launch(m->state, position + t, tokens[t], -1, m->stream));
     int rc = launch_token(m, t == n - 1, bucket_cap(m, position + t + 1));
@@ -949,27 +998,37 @@ int matmul_impl(uint32_t type, const void* w_dev, const float* x_dev, float* y_d
   HIP_TRY(hipGetDevice(&dev));
   const int cus = device_cus(dev);
   hipStream_t st = (hipStream_t)stream;
-  if (N >= 8 && gemm_supports((int)type, K)) {
-    // x -> bf16 into the scratch, then the MFMA GEMM (K-split partials after x).
+  // Q4_0 reads its raw blocks; the other block types (not in the no-allocation
+  // variant) are packed into the workspace first, one pass over W.
+  const bool raw = gemm_supports((int)type, K);
+  const bool pack = !raw && !noalloc && gemm_pack_supports((int)type, K);
+  if (N >= 8 && (raw || pack)) {
+    // x -> bf16 into the scratch, then the MFMA GEMM (K-split partials after x,
+    // packed W after those).
     const size_t xb_bytes = ((size_t)N * K * sizeof(uint16_t) + 255) & ~(size_t)255;
-    const size_t part_bytes = gemm_workspace_bytes(M, N, K, cus, false);
+    const size_t part_bytes = (gemm_workspace_bytes(M, N, K, cus, false) + 255) & ~(size_t)255;
+    const size_t pack_bytes = pack ? gemm_pack_bytes(M, K) : 0;
+    const size_t need = xb_bytes + part_bytes + pack_bytes;
     char* ws = nullptr;
     int rc;
     if (noalloc) {
-      if (xb_bytes + part_bytes > kNoAllocScratchBytes)
+      if (need > kNoAllocScratchBytes)
         return fail(CHATNET_ERR_INVALID_ARG,
                     "chatnet_matmul_noalloc: M=%d K=%d N=%d needs %zu bytes of scratch, more than its %zu", M, K, N,
-                    xb_bytes + part_bytes, kNoAllocScratchBytes);
+                    need, kNoAllocScratchBytes);
       rc = noalloc_scratch(dev, &ws);
     } else {
-      rc = matmul_workspace(dev, st, xb_bytes + part_bytes, &ws);
+      rc = matmul_workspace(dev, st, need, &ws);
     }
     if (rc) return rc;
     HIP_TRY(to_bf16_launch(x_dev, (uint16_t*)ws, (size_t)N * K, st));
+    if (pack) HIP_TRY(gemm_pack_launch((int)type, w_dev, M, K, ws + xb_bytes + part_bytes, st));
     GemmArgs g;
     memset(&g, 0, sizeof(g));
     g.qtype = (int)type;
-    g.w[0] = g.w[1] = g.w[2] = (const uint8_t*)w_dev;
+    g.packed = pack;
+    const uint8_t* wp = pack ? (const uint8_t*)(ws + xb_bytes + part_bytes) : (const uint8_t*)w_dev;
+    g.w[0] = g.w[1] = g.w[2] = wp;
     g.seg_rows[0] = M;
     g.seg_mode = GEMM_SEG_SINGLE;
     g.M = M;

@@ -5,7 +5,9 @@
 // that chatnet_matmul with N >= 8 and a multi-token LlamaModel.Forward span
 // (LlamaModel.cs:93-238) need.
 //
-// W stays in its raw Q4_0 blocks in HBM; x arrives as bf16 [N][K] (one
+// W is read either as raw Q4_0 blocks or as packed units (gemm_pack_kernel:
+// any of Q4_0, Q8_0, Q4_K, Q5_K, Q6_K re-encoded once as u8 codes with an fp32
+// scale and offset per 16 weights); x arrives as bf16 [N][K] (one
 // plane, or hi + lo planes for the exact-weight variant) from the producer
 // kernel (conversion, RMSNorm, attention or the SwiGLU epilogue).  W bytes
 // and x tiles stream through an LDS ring by direct global->LDS loads; each
@@ -22,8 +24,6 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-constexpr int Q4_0_UNIT_DW = 9;  // two Q4_0 blocks = 64 weights = 36 bytes
 
 // W rows of the virtual row `vr`: single matrix, three concatenated (q|k|v)
 // or two interleaved (gate even, up odd).
@@ -134,6 +134,27 @@ __device__ __forceinline__ void dequant_w16(uint32_t q0, uint32_t q1, float d, b
   }
 }
 
+// 8 packed weights fmaf(code, sc, of) as bf16 (hi, and lo = bf16(w - hi) when
+// `precise`); the codes are the bytes of c0 then c1.
+__device__ __forceinline__ void dequant_u8x8(uint32_t c0, uint32_t c1, float sc, float of, bool precise, bf16x8& hi,
+                                             bf16x8& lo) {
+  float w[8];
+  w[0] = fmaf(cn_ubyte<0>(c0), sc, of);
+  w[1] = fmaf(cn_ubyte<1>(c0), sc, of);
+  w[2] = fmaf(cn_ubyte<2>(c0), sc, of);
+  w[3] = fmaf(cn_ubyte<3>(c0), sc, of);
+  w[4] = fmaf(cn_ubyte<0>(c1), sc, of);
+  w[5] = fmaf(cn_ubyte<1>(c1), sc, of);
+  w[6] = fmaf(cn_ubyte<2>(c1), sc, of);
+  w[7] = fmaf(cn_ubyte<3>(c1), sc, of);
+#pragma unroll
+  for (int t = 0; t < 8; t++) {
+    const __bf16 b = (__bf16)w[t];
+    hi[t] = b;
+    if (precise) lo[t] = (__bf16)(w[t] - (float)b);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Pipelined 32x32 tile kernel: raw W bytes and the x tile stream into an
 // S-stage LDS ring through direct global->LDS loads (global_load_lds_dwordx4,
@@ -177,24 +198,27 @@ __device__ __forceinline__ void wg_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <bool PRECISE, int TM, int TN, int S>
+template <bool PRECISE, int TM, int TN, int S, bool PK>
 struct PipeCfg {
   static constexpr int PL = PRECISE ? 2 : 1;
   static constexpr int BM = 128 * TM, BN = 32 * TN;
+  static constexpr int UNIT = PK ? kGemmPackUnit : 36;  // global bytes per row and chunk
+  static constexpr int WP = PK ? 6 : 3;        // 16-byte pieces per row and chunk
+  static constexpr int WROW = 16 * WP;         // LDS bytes per row and chunk
   static constexpr int XB = BN * 128;          // bytes per x plane per stage
-  static constexpr int WB = BM * 48;           // bytes of W per stage
+  static constexpr int WB = BM * WROW;         // bytes of W per stage
   static constexpr int STAGE = PL * XB + WB;
   static constexpr int XPW = BN * 8 / 4;       // x pieces (16 B) per wave per plane
   static constexpr int XI = XPW / 64;
-  static constexpr int WPW = BM * 3 / 4;       // W pieces per wave
+  static constexpr int WPW = BM * WP / 4;      // W pieces per wave
   static constexpr int WI = (WPW + 63) / 64;
   static constexpr int VPS = PL * XI + WI;     // vector-memory instructions per stage per wave
   static_assert(XPW % 64 == 0, "x pieces per wave must fill whole instructions");
 };
 
-template <bool PRECISE, int TM, int TN, int S>
+template <bool PRECISE, int TM, int TN, int S, bool PK>
 __global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
-  using C = PipeCfg<PRECISE, TM, TN, S>;
+  using C = PipeCfg<PRECISE, TM, TN, S, PK>;
   extern __shared__ __attribute__((aligned(16))) char lds[];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -214,7 +238,7 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
   const int cps = (nchunks + a.splits - 1) / a.splits;
   const int c_begin = ks * cps;
   const int c_end = min(nchunks, c_begin + cps);
-  const int row_dw = a.K / 64 * Q4_0_UNIT_DW;
+  const int row_dw = a.K / 64 * (C::UNIT / 4);
 
   // Per-lane source pointers of the stage loads (chunk-independent parts).
   const uint16_t* xsrc[C::PL][C::XI];
@@ -235,10 +259,11 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
     const int q = 64 * j + lane;
     wact[j] = q < C::WPW;
     const int piece = wave * C::WPW + (wact[j] ? q : 0);
-    const int row = piece / 3, part = piece % 3;
+    const int row = piece / C::WP, part = piece % C::WP;
     const int vr = min(m0 + row, a.M - 1);
-    // pieces at unit bytes 0, 16 and 20: exactly the 36 bytes, no read past the unit
-    wsrc[j] = reinterpret_cast<const char*>(gemm_row_ptr(a, vr, row_dw)) + (part == 2 ? 20 : 16 * part);
+    // Q4_0: pieces at unit bytes 0, 16 and 20, exactly the 36 bytes, no read
+    // past the unit; packed: the 6 pieces of the 96-byte unit
+    wsrc[j] = reinterpret_cast<const char*>(gemm_row_ptr(a, vr, row_dw)) + (!PK && part == 2 ? 20 : 16 * part);
   }
 
   auto issue = [&](int c, int slot) {
@@ -251,7 +276,7 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < C::WI; j++)
       if (wact[j])
-        lds_dma16(wsrc[j] + c * 36, st + C::PL * C::XB + (wave * C::WPW + 64 * j) * 16);
+        lds_dma16(wsrc[j] + c * C::UNIT, st + C::PL * C::XB + (wave * C::WPW + 64 * j) * 16);
     asm volatile("" ::: "memory");
   };
 
@@ -265,19 +290,45 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
 
   if (c_begin < c_end) {
     auto slot_of = [&](int c) { return lds + ((c - c_begin) % S) * C::STAGE; };
-    // The 5 dwords of a lane's W block from a stage slot: the slot holds unit
-    // bytes [0,16) [16,32) [20,36): block A's d + qs at dwords 0..4, block B's
-    // d in the high half of dword 4 and its qs at dwords 8..11.
-    auto wraw = [&](const char* st, int r, uint32_t (&w)[5]) {
-      const uint32_t* wb = reinterpret_cast<const uint32_t*>(st + C::PL * C::XB + (wave * 32 * TM + 32 * r + li) * 48);
-      w[0] = wb[8 * h];
-      w[1] = wb[8 * h + 1];
-      w[2] = wb[8 * h + 2];
-      w[3] = wb[8 * h + 3];
-      w[4] = wb[4];
+    // The dwords of a lane's W slice from a stage slot.  Q4_0 (5 dwords): the
+    // slot holds unit bytes [0,16) [16,32) [20,36): block A's d + qs at dwords
+    // 0..4, block B's d in the high half of dword 4 and its qs at dwords
+    // 8..11.  Packed (12 dwords): codes 32h..32h+31 (dwords 8h..8h+7), then
+    // scales 2h, 2h+1 (unit bytes 64 + 8h) and offsets 2h, 2h+1 (80 + 8h).
+    constexpr int WD = PK ? 12 : 5;
+    auto wraw = [&](const char* st, int r, uint32_t (&w)[WD]) {
+      const uint32_t* wb =
+          reinterpret_cast<const uint32_t*>(st + C::PL * C::XB + (wave * 32 * TM + 32 * r + li) * C::WROW);
+      if constexpr (PK) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) w[i] = wb[8 * h + i];
+        w[8] = wb[16 + 2 * h];
+        w[9] = wb[17 + 2 * h];
+        w[10] = wb[20 + 2 * h];
+        w[11] = wb[21 + 2 * h];
+      } else {
+        w[0] = wb[8 * h];
+        w[1] = wb[8 * h + 1];
+        w[2] = wb[8 * h + 2];
+        w[3] = wb[8 * h + 3];
+        w[4] = wb[4];
+      }
     };
-    // half 0: steps 0 and 2 (low/high nibbles of qs[0..7]); half 1: steps 1 and 3
-    auto deq = [&](const uint32_t (&w)[5], int half, bf16x8 (&fh)[4], bf16x8 (&fl)[4]) {
+    // Q4_0: half 0 gives steps 0 and 2 (low/high nibbles of qs[0..7]), half 1
+    // steps 1 and 3.  Packed: half 0 gives steps 0 and 1 (codes 0..15 of the
+    // lane, scale 2h), half 1 steps 2 and 3 (codes 16..31, scale 2h+1).
+    auto deq = [&](const uint32_t (&w)[WD], int half, bf16x8 (&fh)[4], bf16x8 (&fl)[4]) {
+      if constexpr (PK) {
+        const float sc = __uint_as_float(w[8 + half]), of = __uint_as_float(w[10 + half]);
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+          bf16x8 th, tl;
+          dequant_u8x8(w[4 * half + 2 * t], w[4 * half + 2 * t + 1], sc, of, PRECISE, th, tl);
+          fh[2 * half + t] = th;
+          if constexpr (PRECISE) fl[2 * half + t] = tl;
+        }
+        return;
+      }
       const uint32_t sh = h ? 0u : 2u;
       const float d = cn_h2f(h ? (w[4] >> 16) : w[0]);
       const uint32_t qa = __builtin_amdgcn_alignbyte(half ? w[3] : w[1], half ? w[2] : w[0], sh);
@@ -316,7 +367,7 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
     bf16x8 wh[TM][4], wl[TM][4];
 #pragma unroll
     for (int r = 0; r < TM; r++) {
-      uint32_t w[5];
+      uint32_t w[WD];
       wraw(slot_of(c_begin), r, w);
       deq(w, 0, wh[r], wl[r]);
       deq(w, 1, wh[r], wl[r]);
@@ -334,7 +385,7 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
       }
       // Unconditional (branch-free, so it interleaves with the MFMAs): on the
       // last chunk this reads a stale slot whose result is never used.
-      uint32_t nw[TM][5];
+      uint32_t nw[TM][WD];
 #pragma unroll
       for (int r = 0; r < TM; r++) wraw(slot_of(c + 1), r, nw[r]);
       bf16x8 nwh[TM][4], nwl[TM][4];
@@ -414,9 +465,9 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
   }
 }
 
-template <bool PRECISE, int TM, int TN, int S>
+template <bool PRECISE, int TM, int TN, int S, bool PK>
 constexpr size_t gemm_p_lds() {
-  return (size_t)S * PipeCfg<PRECISE, TM, TN, S>::STAGE;
+  return (size_t)S * PipeCfg<PRECISE, TM, TN, S, PK>::STAGE;
 }
 
 // Sums the K-split partials [splits][N][M] and applies the epilogue; one
@@ -488,6 +539,113 @@ __global__ __launch_bounds__(CN_BLOCK) void rmsnorm_bf16_kernel(const float* __r
   }
 }
 
+// ---------------------------------------------------------------------------
+// Packing: one thread re-encodes the 64 weights of chunk c of row r as a
+// 96-byte unit: 64 u8 codes in K order, then scale[4] and offset[4] (fp32,
+// one pair per 16 weights).  Each block type's dequantized value is
+// fmaf(code, scale, offset) with one rounding, as the reference rounds it:
+//   Q4_0 (DequantQ4_0.cs)  code q,      scale d,        offset -8d
+//   Q8_0 (DequantQ8_0.cs)  code q+128,  scale d,        offset -128d
+//   Q4_K (DequantQ4K.cs)   code q,      scale d*sc[s],  offset -(dmin*m[s])
+//   Q5_K (DequantQ5K.cs)   code q5,     scale d*sc[s],  offset -(dmin*m[s])
+//   Q6_K (DequantQ6K.cs)   code q+32,   scale d*sc[i],  offset -32*d*sc[i]
+// (d*sc, dmin*m and the power-of-two multiples are exact in fp32, and so is
+// code*scale for Q4_0, Q8_0, Q4_K and Q5_K; Q6_K's (d*sc)*q is rounded once
+// either way).  Sub-block layouts: Q4_K / Q5_K sub-block s of a super-block
+// holds its 32 weights in the reference's order (elements 0..15 are the
+// low nibbles of qs[16s..16s+15], 16..31 the high ones), Q6_K as
+// DequantQ6K.Dequantize (DequantQ6K.cs:37-88).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float h2f_at(const uint8_t* p) { return cn_h2f((uint32_t)p[0] | ((uint32_t)p[1] << 8)); }
+
+// Q4_K / Q5_K 6-bit scale and min of sub-block j (DequantQ4K.cs:218-264).
+__device__ __forceinline__ void k4_scale_min(const uint8_t* q, int j, int& sc, int& mn) {
+  if (j < 4) {
+    sc = q[j] & 63;
+    mn = q[j + 4] & 63;
+  } else {
+    sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+    mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+  }
+}
+
+__global__ __launch_bounds__(CN_BLOCK) void gemm_pack_kernel(int qtype, const uint8_t* __restrict__ w,
+                                                            size_t row_bytes, int M, int nchunks,
+                                                            uint8_t* __restrict__ dst) {
+  const long long t = (long long)blockIdx.x * CN_BLOCK + threadIdx.x;
+  if (t >= (long long)M * nchunks) return;
+  const int r = (int)(t / nchunks), c = (int)(t % nchunks);
+  const uint8_t* row = w + (size_t)r * row_bytes;
+  uint32_t code[16];
+  float sc[4], of[4];
+  auto put = [&](int k, uint32_t v) {
+    if ((k & 3) == 0) code[k >> 2] = 0;
+    code[k >> 2] |= (v & 0xFFu) << (8 * (k & 3));
+  };
+  if (qtype == 2 || qtype == 8) {  // Q4_0 / Q8_0: blocks 2c and 2c+1 of 32
+    const int bb = qtype == 2 ? 18 : 34;
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+      const uint8_t* blk = row + (size_t)(2 * c + b) * bb;
+      const float d = h2f_at(blk);
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
+        uint32_t v;
+        if (qtype == 2) v = j < 16 ? (blk[2 + j] & 15u) : (uint32_t)(blk[2 + j - 16] >> 4);
+        else v = (uint32_t)blk[2 + j] ^ 0x80u;
+        put(32 * b + j, v);
+      }
+      sc[2 * b] = sc[2 * b + 1] = d;
+      of[2 * b] = of[2 * b + 1] = (qtype == 2 ? -8.0f : -128.0f) * d;
+    }
+  } else if (qtype == 12 || qtype == 13) {  // Q4_K / Q5_K: sub-blocks 2(c%4), 2(c%4)+1
+    const int sbb = qtype == 12 ? 144 : 176;
+    const uint8_t* blk = row + (size_t)(c >> 2) * sbb;
+    const float d = h2f_at(blk), dmin = h2f_at(blk + 2);
+    const uint8_t* qs0 = blk + (qtype == 12 ? 16 : 48);
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+      const int s = 2 * (c & 3) + b;
+      int sv, mv;
+      k4_scale_min(blk + 4, s, sv, mv);
+      const uint8_t* qs = qs0 + 16 * s;
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
+        uint32_t v = j < 16 ? (qs[j] & 15u) : (uint32_t)(qs[j - 16] >> 4);
+        if (qtype == 13) {
+          const int e = 32 * s + j;
+          v |= (uint32_t)((blk[16 + e / 8] >> (e % 8)) & 1) << 4;
+        }
+        put(32 * b + j, v);
+      }
+      sc[2 * b] = sc[2 * b + 1] = d * (float)sv;
+      of[2 * b] = of[2 * b + 1] = -(dmin * (float)mv);
+    }
+  } else {  // Q6_K: elements 64(c%4) .. +63 of the super-block
+    const uint8_t* blk = row + (size_t)(c >> 2) * 210;
+    const float d = h2f_at(blk + 208);
+    const int8_t* scl = reinterpret_cast<const int8_t*>(blk + 192);
+#pragma unroll
+    for (int j = 0; j < 64; j++) {
+      const int e = 64 * (c & 3) + j, hh = e >> 7, e2 = e & 127, qq = e2 >> 5, l = e2 & 31;
+      const uint8_t qlb = blk[64 * hh + l + 32 * (qq & 1)];
+      const uint32_t nib = qq >= 2 ? (uint32_t)(qlb >> 4) : (qlb & 15u);
+      const uint32_t hb = (blk[128 + 32 * hh + l] >> (2 * qq)) & 3u;
+      put(j, nib | (hb << 4));
+      if ((j & 15) == 0) {
+        const float s = d * (float)scl[8 * hh + l / 16 + 2 * qq];
+        sc[j >> 4] = s;
+        of[j >> 4] = -32.0f * s;
+      }
+    }
+  }
+  uint4* o = reinterpret_cast<uint4*>(dst + ((size_t)r * nchunks + c) * kGemmPackUnit);
+#pragma unroll
+  for (int i = 0; i < 4; i++) o[i] = make_uint4(code[4 * i], code[4 * i + 1], code[4 * i + 2], code[4 * i + 3]);
+  o[4] = make_uint4(__float_as_uint(sc[0]), __float_as_uint(sc[1]), __float_as_uint(sc[2]), __float_as_uint(sc[3]));
+  o[5] = make_uint4(__float_as_uint(of[0]), __float_as_uint(of[1]), __float_as_uint(of[2]), __float_as_uint(of[3]));
+}
+
 // Column tile by batch size (32, 64 or 128 columns per workgroup, 128 rows);
 // K is split while the tile grid covers fewer than two workgroups per CU,
 // keeping at least 8 chunks of 64 per split so the LDS ring stays full.
@@ -507,32 +665,65 @@ GemmShape pick_gemm(int M, int N, int K, int num_cus) {
 
 constexpr int kStages = 3;
 
-template <bool PRECISE, int TN>
+template <bool PRECISE, int TN, bool PK>
 hipError_t launch_p(const GemmArgs& a, int grid, hipStream_t st) {
-  constexpr size_t lds = gemm_p_lds<PRECISE, 1, TN, kStages>();
+  constexpr size_t lds = gemm_p_lds<PRECISE, 1, TN, kStages, PK>();
+  static_assert(lds <= 160 * 1024, "LDS ring exceeds the CU's 160 KB");
   // Dynamic LDS above 64 KB must be allowed per kernel; every caller sets the
   // same value, so a race on the flag is harmless.
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_p_kernel<PRECISE, 1, TN, kStages>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_p_kernel<PRECISE, 1, TN, kStages, PK>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((gemm_p_kernel<PRECISE, 1, TN, kStages>), dim3(grid), dim3(CN_BLOCK), lds, st, a);
+  hipLaunchKernelGGL((gemm_p_kernel<PRECISE, 1, TN, kStages, PK>), dim3(grid), dim3(CN_BLOCK), lds, st, a);
   return hipGetLastError();
 }
 
-template <bool PRECISE>
+template <bool PRECISE, bool PK>
 hipError_t launch_tn(const GemmArgs& a, int tn, int grid, hipStream_t st) {
-  if (tn == 1) return launch_p<PRECISE, 1>(a, grid, st);
-  if (tn == 2) return launch_p<PRECISE, 2>(a, grid, st);
-  return launch_p<PRECISE, 4>(a, grid, st);
+  if (tn == 1) return launch_p<PRECISE, 1, PK>(a, grid, st);
+  if (tn == 2) return launch_p<PRECISE, 2, PK>(a, grid, st);
+  return launch_p<PRECISE, 4, PK>(a, grid, st);
+}
+
+template <bool PRECISE>
+hipError_t launch_fmt(const GemmArgs& a, int tn, int grid, hipStream_t st) {
+  return a.packed ? launch_tn<PRECISE, true>(a, tn, grid, st) : launch_tn<PRECISE, false>(a, tn, grid, st);
 }
 
 }  // namespace
 
 bool gemm_supports(int qtype, int K) { return qtype == 2 && K > 0 && K % 64 == 0; }
+
+bool gemm_pack_supports(int qtype, int K) {
+  if (K <= 0) return false;
+  if (qtype == 2 || qtype == 8) return K % 64 == 0;
+  if (qtype == 12 || qtype == 13 || qtype == 14) return K % 256 == 0;
+  return false;
+}
+
+size_t gemm_pack_bytes(int M, int K) { return (size_t)M * (size_t)(K / 64) * kGemmPackUnit; }
+
+hipError_t gemm_pack_launch(int qtype, const void* w, int M, int K, void* dst, hipStream_t st) {
+  if (!gemm_pack_supports(qtype, K) || M <= 0 || !w || !dst) return hipErrorInvalidValue;
+  size_t row_bytes;
+  switch (qtype) {
+    case 2: row_bytes = (size_t)K / 32 * 18; break;
+    case 8: row_bytes = (size_t)K / 32 * 34; break;
+    case 12: row_bytes = (size_t)K / 256 * 144; break;
+    case 13: row_bytes = (size_t)K / 256 * 176; break;
+    default: row_bytes = (size_t)K / 256 * 210; break;
+  }
+  const long long n = (long long)M * (K / 64);
+  const long long blocks = (n + CN_BLOCK - 1) / CN_BLOCK;
+  if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(gemm_pack_kernel, dim3((unsigned)blocks), dim3(CN_BLOCK), 0, st, qtype,
+                     static_cast<const uint8_t*>(w), row_bytes, M, K / 64, static_cast<uint8_t*>(dst));
+  return hipGetLastError();
+}
 
 size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool /*precise*/) {
   const GemmShape s = pick_gemm(M, N, K, num_cus);
@@ -540,7 +731,8 @@ size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool /*precise*/) 
 }
 
 hipError_t gemm_launch(const GemmArgs& a_in, int num_cus, hipStream_t st) {
-  if (!gemm_supports(a_in.qtype, a_in.K) || a_in.M <= 0 || a_in.N <= 0) return hipErrorInvalidValue;
+  const bool k_ok = a_in.packed ? (a_in.K > 0 && a_in.K % 64 == 0) : gemm_supports(a_in.qtype, a_in.K);
+  if (!k_ok || a_in.M <= 0 || a_in.N <= 0) return hipErrorInvalidValue;
   const bool precise = a_in.precise != 0;
   if (precise && !a_in.xb_lo) return hipErrorInvalidValue;
   const GemmShape s = pick_gemm(a_in.M, a_in.N, a_in.K, num_cus);
@@ -549,7 +741,7 @@ hipError_t gemm_launch(const GemmArgs& a_in, int num_cus, hipStream_t st) {
   if (s.splits > 1 && !a.part) return hipErrorInvalidValue;
   const long long grid = (long long)((a.M + 127) / 128) * ((a.N + 32 * s.tn - 1) / (32 * s.tn)) * s.splits;
   if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
-  hipError_t e = precise ? launch_tn<true>(a, s.tn, (int)grid, st) : launch_tn<false>(a, s.tn, (int)grid, st);
+  hipError_t e = precise ? launch_fmt<true>(a, s.tn, (int)grid, st) : launch_fmt<false>(a, s.tn, (int)grid, st);
   if (e != hipSuccess || s.splits == 1) return e;
   const long long work = (long long)((a.M + 3) / 4) * a.N;
   hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((work + CN_BLOCK - 1) / CN_BLOCK)), dim3(CN_BLOCK), 0, st, a);

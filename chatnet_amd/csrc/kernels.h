@@ -60,6 +60,7 @@ hipError_t gemv_float_launch(int qtype, int epi, const GemvArgs& a, int num_cus,
 enum { GEMM_SEG_SINGLE = 0, GEMM_SEG_CONCAT = 1, GEMM_SEG_INTERLEAVE = 2 };
 struct GemmArgs {
   int qtype;
+  int packed;             // 1: w holds gemm_pack_launch units (any packable type), 0: raw Q4_0 blocks
   const uint8_t* w[3];
   int seg_rows[3];
   int seg_mode;
@@ -77,6 +78,15 @@ struct GemmArgs {
   int splits;             // set by gemm_launch
 };
 bool gemm_supports(int qtype, int K);
+// Packed weights: every 64 weights of a row become one 96-byte unit of 64 u8
+// codes, 4 fp32 scales and 4 fp32 offsets (one pair per 16 weights), with
+// weight k = fmaf(code[k], scale[k/16], offset[k/16]) equal to the block
+// type's own dequantized value.  Types Q4_0, Q8_0 (K % 64 == 0) and Q4_K,
+// Q5_K, Q6_K (K % 256 == 0).
+constexpr int kGemmPackUnit = 96;
+bool gemm_pack_supports(int qtype, int K);
+size_t gemm_pack_bytes(int M, int K);
+hipError_t gemm_pack_launch(int qtype, const void* w, int M, int K, void* dst, hipStream_t st);
 size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool precise);
 hipError_t gemm_launch(const GemmArgs& a, int num_cus, hipStream_t st);
 hipError_t to_bf16_launch(const float* x, uint16_t* xb, size_t n, hipStream_t st);

@@ -108,7 +108,9 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
 // p0+t, query head h, kv head h / kv_mul,
 //   out[t][h] = softmax_p<=p0+t( q . K[p] * scale ) . V[p].
 // A workgroup owns 64 rows = QB consecutive tokens x the kv_mul query heads of
-// one kv head (QB = 64 / kv_mul); wave w owns rows 16w..16w+15, lane l the
+// one kv head (QB = floor(64 / kv_mul); when kv_mul does not divide 64 the
+// last 64 - QB*kv_mul rows are padding that is never written); wave w owns
+// rows 16w..16w+15, lane l the
 // row 16w + l%16.  K/V are walked in chunks of 64 positions, staged in LDS as
 // bf16 high and low parts (K row-major, V transposed), and both products run
 // on v_mfma_f32_16x16x32_bf16 with three passes (hi*hi + hi*lo + lo*hi):
@@ -158,7 +160,8 @@ __global__ __launch_bounds__(kSpanThreads) void attn_prefill_kernel(PrefillAttnA
   const int t0 = (gridDim.y - 1 - blockIdx.y) * QB;  // longest key ranges dispatched first
   const int r = 16 * w + c;
   const int t = t0 + r / a.kv_mul, hh = kvh * a.kv_mul + r % a.kv_mul;
-  const int qpos = t < a.n ? a.p0 + t : -1;  // -1: padding row, every key masked
+  const bool real = r < QB * a.kv_mul && t < a.n;
+  const int qpos = real ? a.p0 + t : -1;  // -1: padding row, every key masked
   const int t_last = min(a.n, t0 + QB) - 1;
   const int kend = a.p0 + t_last + 1;        // keys [0, kend)
 
@@ -167,7 +170,7 @@ __global__ __launch_bounds__(kSpanThreads) void attn_prefill_kernel(PrefillAttnA
 #pragma unroll
   for (int s = 0; s < NS; s++) {
     qr[s][0] = qr[s][1] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (t < a.n) {
+    if (real) {
       const float* qp = a.qkv + (size_t)t * a.ld + hh * HD + 32 * s + 8 * g;
       qr[s][0] = *reinterpret_cast<const float4*>(qp);
       qr[s][1] = *reinterpret_cast<const float4*>(qp + 4);
@@ -356,7 +359,7 @@ __global__ __launch_bounds__(kSpanThreads) void attn_prefill_kernel(PrefillAttnA
     }
   }
   __syncthreads();
-  if (grp == 1 || t >= a.n) return;
+  if (grp == 1 || !real) return;
   // group 0 scored key 0 of every real row, so m is finite; a row group 1 never
   // scored has m1 = -inf and weight 0
   const float m1 = xm[r], l1 = xm[64 + r];
@@ -402,7 +405,7 @@ hipError_t attn_prefill_t(const PrefillAttnArgs& a, hipStream_t st) {
 }  // namespace
 
 bool attn_prefill_supports(int head_dim, int kv_mul) {
-  return (head_dim == 64 || head_dim == 128) && kv_mul >= 1 && kv_mul <= 64 && (64 % kv_mul) == 0;
+  return (head_dim == 64 || head_dim == 128) && kv_mul >= 1 && kv_mul <= 64;
 }
 
 hipError_t attn_prefill_launch(const PrefillAttnArgs& a, hipStream_t st) {

@@ -44,6 +44,9 @@ MIXES = {
     # every matrix dispatched on its own type, ffn_gate and ffn_up differing
     "mixed": {"attn": _native.GGML_Q8_0, "gate": _native.GGML_Q4_0, "up": _native.GGML_F16,
               "down": _native.GGML_Q4_K, "output": _native.GGML_F32},
+    # block types only, each matrix on its own type and ffn_gate/up differing
+    "mixed_blocks": {"attn": _native.GGML_Q8_0, "gate": _native.GGML_Q4_0, "up": _native.GGML_Q5_K,
+                     "down": _native.GGML_Q6_K, "output": _native.GGML_Q4_K},
 }
 
 

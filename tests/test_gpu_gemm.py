@@ -1,7 +1,8 @@
 """GPU parity of the batched quantized GEMM (chatnet_matmul with N >= 8: Q4_0
-blocks dequantized into bf16 MFMA operands, fp32 accumulation) against the
-oracle's dequantize-then-dot (DequantQ4_0.Dequantize, DequantQ4_0.cs:28-58,
-followed by an exact float64 product) for every column.
+blocks, or Q8_0 / Q4_K / Q5_K / Q6_K packed units, dequantized into bf16 MFMA
+operands, fp32 accumulation) against the oracle's dequantize-then-dot
+(DequantQ4_0.Dequantize, DequantQ4_0.cs:28-58, and the other types'
+Dequantize, followed by an exact float64 product) for every column.
 
 Bar: normwise error max|y-r|/max|r| <= 1e-2 per column (bf16 operands)."""
 import numpy as np
@@ -63,13 +64,24 @@ def test_gemm_columns_match_gemv():
         assert normwise(y[n], g) <= TOL
 
 
-def test_k_quant_batches_use_the_gemv_path():
-    """Q4_K / Q6_K batches run one fused GEMV per column (fp32 bar 1e-3)."""
-    for qtype, M, K in ((12, 64, 512), (14, 64, 512)):
-        t = synth.tensor(qtype, 9, f"kq-batch{qtype}", M, K)
-        x = synth.normal(9, f"kq-batch-x{qtype}", 8 * K, 1.0).reshape(8, K)
-        announce(f"k-quant batch type={qtype}")
-        y = gpu_matmul(qtype, t.data, x, M, K)
-        for n in range(8):
-            r = oracle.matvec(qtype, t.data, x[n], M, K)
-            assert normwise(y[n], r) <= 1e-3
+# Other block types: W is packed once per call into u8 codes with an fp32
+# scale and offset per 16 weights (each weight bit-equal to the type's own
+# dequantized value), then the same MFMA GEMM runs.
+PACKED = {8: "q8_0", 12: "q4_k", 13: "q5_k", 14: "q6_k"}
+
+
+@pytest.mark.parametrize("M,K,N", [
+    (4096, 4096, 64), (2048, 2048, 512), (11008, 4096, 8), (4096, 11008, 33), (80, 256, 17), (130, 512, 9),
+])
+@pytest.mark.parametrize("qtype", sorted(PACKED))
+def test_packed_block_types_gemm(qtype, M, K, N):
+    announce(f"gemm {PACKED[qtype]} M={M} K={K} N={N}")
+    t = synth.tensor(qtype, 9, f"packed{qtype}-{M}x{K}", M, K)
+    x = synth.normal(9, f"packed-x{qtype}-{N}x{K}", N * K, 1.0).reshape(N, K)
+    y = gpu_matmul(qtype, t.data, x, M, K)
+    assert np.all(np.isfinite(y))
+    w = oracle.dequant(qtype, t.data, M * K).reshape(M, K).astype(np.float64)
+    r = x.astype(np.float64) @ w.T
+    errs = [normwise(y[n], r[n]) for n in range(N)]
+    worst = int(np.argmax(errs))
+    assert errs[worst] <= TOL, (qtype, M, K, N, worst, errs[worst])

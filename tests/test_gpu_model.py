@@ -368,12 +368,26 @@ SPAN_SMALL = TINY_TEST.replace(dim=256, hidden_dim=512, n_heads=4, n_kv_heads=2,
                                context_length=1100)
 
 
-def span_case(cfg, seed, n_prompt, n_next=8):
-    ck = synth.llama_checkpoint(cfg, seed=seed, mix="q4_0")
+def span_case(cfg, seed, n_prompt, n_next=8, mix="q4_0", ck=None, check_batched=False):
+    """A span of n_prompt tokens and a continuing span of n_next, logits
+    against the oracle.  check_batched: the same prompt on the per-token
+    schedule must give different bits (the batched GEMM rounds differently),
+    i.e. the span really ran batched."""
+    if ck is None:
+        ck = synth.llama_checkpoint(cfg, seed=seed, mix=mix)
     toks = synth.tokens(seed, "prompt", n_prompt + n_next, cfg.vocab_size)
     with HipLlamaModel(cfg, ck) as m:
-        g = m.forward(toks[:n_prompt], 0)
+        g = m.forward(toks[:n_prompt], 0).copy()
         g2 = m.forward(toks[n_prompt:], n_prompt)  # a second span continuing the sequence
+    if check_batched:
+        import os
+        os.environ["CHATNET_SPAN_BATCH"] = "0"
+        try:
+            with HipLlamaModel(cfg, ck) as m:
+                h = m.forward(toks[:n_prompt], 0).copy()
+        finally:
+            del os.environ["CHATNET_SPAN_BATCH"]
+        assert not np.array_equal(g, h), "the span ran on the per-token schedule"
     ora = oracle.OracleLlama(cfg, ck)
     r = ora.forward(toks[:n_prompt], 0)
     r2 = ora.forward(toks[n_prompt:], n_prompt)
@@ -421,11 +435,42 @@ def test_span_longer_than_batch_cap_matches_oracle_and_token_schedule(monkeypatc
     compare_greedy(list(gt), o, margins, "span 600 tokens, greedy 16")
 
 
+@pytest.mark.parametrize("mix", ["q4_k_m", "q5_k_m", "q8_0", "q6_k", "q4_k", "mixed_blocks"])
+def test_span_block_type_mixes_match_oracle(mix):
+    """Spans of models with other block types run batched on packed weights
+    (every matrix re-encoded once, types mixed freely, ffn_gate and ffn_up of
+    different types in mixed_blocks)."""
+    announce(f"span: mix {mix}, 40 + 8 tokens")
+    span_case(SPAN_SMALL.replace(context_length=96), 39, 40, mix=mix, check_batched=True)
+
+
+def test_span_q4_k_m_llama7b_layer_matches_oracle():
+    """A 7B-shaped Q4_K_M layer (Q4_K attention and gate/up, Q6_K down, Q6_K
+    LM head) as a 16-token span."""
+    from chatnet_amd import LLAMA2_7B
+    announce("span: llama-7b-shaped q4_k_m layer, 16 + 8 tokens")
+    span_case(LLAMA2_7B.replace(n_layers=1, context_length=64), 40, 16, mix="q4_k_m", check_batched=True)
+
+
+def test_span_qwen2_0_5b_layer_matches_oracle():
+    """Qwen2-0.5B-shaped layer (14 query heads over 2 kv heads: kv_mul 7, 9
+    tokens x 7 heads per span-attention workgroup, one padding row) with Q8_0
+    weights, biases and the tied Q8_0 embedding, as a 40-token span."""
+    from chatnet_amd import QWEN2_0_5B
+    cfg = QWEN2_0_5B.replace(n_layers=1, context_length=64)
+    ck = synth.llama_checkpoint(cfg, seed=47, mix="q8_0", with_output=False, embedding=_native.GGML_Q8_0)
+    announce("span: qwen2-0.5b layer, 40 + 8 tokens")
+    span_case(cfg, 47, 40, ck=ck, check_batched=True)
+
+
 @pytest.mark.parametrize("head_dim,n_heads,n_kv,kv", [
     (64, 8, 2, _native.KV_F32),    # kv_mul 4: 16 tokens per workgroup
     (64, 16, 1, _native.KV_F32),   # kv_mul 16: 4 tokens per workgroup
     (128, 4, 4, _native.KV_F32),   # head_dim 128 without grouping
     (128, 8, 2, _native.KV_F16),   # head_dim 128, kv_mul 4, fp16 cache
+    (64, 14, 2, _native.KV_F32),   # kv_mul 7: 9 tokens per workgroup, one padding row
+    (128, 12, 4, _native.KV_F16),  # kv_mul 3: 21 tokens per workgroup, one padding row
+    (64, 10, 2, _native.KV_F32),   # kv_mul 5: 12 tokens per workgroup, four padding rows
 ])
 def test_span_attention_layouts_match_oracle(head_dim, n_heads, n_kv, kv):
     """Causal span attention across GQA ratios and head sizes: a 150-token
