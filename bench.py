@@ -39,6 +39,9 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16
 METRIC = "decode tok/s bs1 (1.1B & 7B Q4_0); Q4_0 GEMV achieved HBM GB/s vs peak"
 SWEEP = [(2048, 2048), (256, 2048), (5632, 2048), (2048, 5632), (32000, 2048), (4096, 4096), (11008, 4096)]
 ROOF_SHAPE = (11008, 4096)
+# legs --only can select
+LEGS = ("gemv_sweep", "roofline", "kquant", "gemm_sweep", "gemm_counters", "llama7b_decode", "tinyllama_decode",
+        "prefill")
 # Q4_K_M-style mix on Llama-2-7B shapes: Q4_K attention + gate/up, Q6_K down + output
 KQ4_SHAPES = [(4096, 4096), (11008, 4096)]
 KQ6_SHAPES = [(4096, 11008), (32000, 4096)]
@@ -194,6 +197,7 @@ def gemv_sweep(shapes, replays=2, rotate_bytes=ROTATE_BYTES, qtype=2):
         res[f"{M}x{K}"] = {"us": round(us, 3), "GB/s": round(alg / us / 1e3, 1),
                            "frac": round(alg / us / 1e3 / HBM_PEAK_GBS, 4), "alg_bytes": alg,
                            "launches": copies, "rotated_MB": round(copies * stride / 1e6, 1)}
+        log(f"  gemv type {qtype} {M}x{K}: {res[f'{M}x{K}']['us']} us")
         for b in (pool, x, y):
             b.free()
     return res
@@ -240,8 +244,27 @@ def gemm_sweep(shapes, ns, rotate_bytes=ROTATE_BYTES):
             x.free()
             y.free()
         res[f"{M}x{K}"] = per
+        log(f"  gemm {M}x{K}: {json.dumps(per)}")
         pool.free()
     return res
+
+
+def gemm_counters(shapes, ns=(64, 512)):
+    """One chatnet_matmul call per shape and N (warm weights), for counter
+    collection, where every dispatch is serialized by the profiler."""
+    from chatnet_amd import hiprt, ops, synth
+
+    for (M, K) in shapes:
+        w = hiprt.DeviceBuffer.from_numpy(synth.tensor(2, 7, f"ctr{M}x{K}", M, K).data, pad=256)
+        for N in ns:
+            x = hiprt.DeviceBuffer.from_numpy(synth.normal(99, f"gemmx{N}x{K}", N * K, 1.0))
+            y = hiprt.DeviceBuffer(4 * M * N)
+            ops.matmul_ptr(2, w.ptr, x.ptr, y.ptr, M, K, N, 0)
+            hiprt.synchronize()
+            x.free()
+            y.free()
+            log(f"  counters: {M}x{K} N={N} done")
+        w.free()
 
 
 def copy_rate(nbytes=512 << 20, reps=5):
@@ -382,7 +405,11 @@ def main():
     ap.add_argument("--no-gemm", action="store_true", help="skip the batched GEMM sweep")
     ap.add_argument("--no-kquant", action="store_true", help="skip the Q4_K / Q6_K / Q8_0 / Q5_K legs")
     ap.add_argument("--roofline-only", action="store_true", help="only the isolated GEMV legs")
+    ap.add_argument("--only", choices=LEGS, help="run this one leg (for profiling); the line carries what it measured")
     args = ap.parse_args()
+
+    def want(leg: str) -> bool:
+        return args.only is None or args.only == leg
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); "
               "multi-GPU sharding is design-only", file=sys.stderr)
@@ -395,12 +422,18 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
 
-    copy_gbs = copy_rate()
-    log(f"device-to-device copy: {copy_gbs} GB/s (read + write)")
-    log("gemv sweep (cold: one launch per weight copy, >= 1 GiB of copies per shape)")
-    sweep = gemv_sweep(SWEEP)
-    roof = sweep[f"{ROOF_SHAPE[0]}x{ROOF_SHAPE[1]}"]
-    log(f"sweep: {json.dumps(sweep)}")
+    copy_gbs = sweep = None
+    roof = {}
+    if args.only == "roofline":  # the roofline shape alone (counter runs)
+        sweep = gemv_sweep([ROOF_SHAPE])
+        roof = sweep[f"{ROOF_SHAPE[0]}x{ROOF_SHAPE[1]}"]
+    if want("gemv_sweep"):
+        copy_gbs = copy_rate()
+        log(f"device-to-device copy: {copy_gbs} GB/s (read + write)")
+        log("gemv sweep (cold: one launch per weight copy, >= 1 GiB of copies per shape)")
+        sweep = gemv_sweep(SWEEP)
+        roof = sweep[f"{ROOF_SHAPE[0]}x{ROOF_SHAPE[1]}"]
+        log(f"sweep: {json.dumps(sweep)}")
 
     value = ms = None
     cpu = None
@@ -412,7 +445,7 @@ def main():
     qwen = None
     fp16kv = None
     par = {}
-    if not args.roofline_only and not args.no_kquant:
+    if not args.roofline_only and not args.no_kquant and want("kquant"):
         log("Q4_K / Q6_K / Q8_0 / Q5_K / F16 gemv (cold) and 7B Q4_K_M-style 64-token decode")
         kq = {"gemv_q4_k_cold": gemv_sweep(KQ4_SHAPES, qtype=12),
               "gemv_q6_k_cold": gemv_sweep(KQ6_SHAPES, qtype=14),
@@ -427,11 +460,14 @@ def main():
         par[wk.name] = parity(wk.name, tk, lpk)
         del ckk
         log(f"  {json.dumps(kq)}")
-    if not args.roofline_only and not args.no_gemm:
+    if args.only == "gemm_counters":
+        log("gemm counter leg: one call per shape, N = 64 and 512")
+        gemm_counters(SWEEP)
+    if not args.roofline_only and not args.no_gemm and want("gemm_sweep"):
         log("gemm sweep N = 8, 64, 512 (cold)")
         gsweep = gemm_sweep(SWEEP, (8, 64, 512))
         log(f"gemm sweep: {json.dumps(gsweep)}")
-    if not args.roofline_only:
+    if not args.roofline_only and want("llama7b_decode"):
         w7 = WORKLOADS["llama2_7b_q4_0_decode"]
         cfg7 = w7.config
         log("generating Llama-2-7B-shaped Q4_0 checkpoint")
@@ -449,25 +485,30 @@ def main():
         fp16kv = round(args.steps / dt16, 1)
         log(f"  fp16 KV cache: {fp16kv} tok/s")
         w1 = WORKLOADS["tinyllama_q4_0_decode"]
-        ck1 = w1.checkpoint() if not args.no_tinyllama or not args.no_cpu else None
-        if not args.no_cpu:
+        if not args.no_cpu and args.only is None:
             log("cpu baseline (oracle on host cores)")
-            cpu = cpu_baseline(cfg7, ck7, w1.config, ck1)
+            cpu = cpu_baseline(cfg7, ck7, w1.config, w1.checkpoint())
             log(f"  {cpu['value']} tok/s on {cpu['cores']} threads; {json.dumps(cpu['legs'])}")
         del ck7
-        if not args.no_tinyllama:
+    if not args.roofline_only and not args.no_tinyllama:
+        if want("tinyllama_decode"):
+            w1 = WORKLOADS["tinyllama_q4_0_decode"]
+            ck1 = w1.checkpoint()
             rate1, toks1, lp1 = short_decode_run(w1.config, ck1, w1.prompt(), w1.n_decode, 20)
             tiny = round(rate1, 1)
             par[w1.name] = parity(w1.name, toks1, lp1)
             log(f"TinyLlama decode ({w1.n_prompt}-token prompt, {w1.n_decode} tokens, context "
                 f"{w1.config.context_length}): {tiny} tok/s; parity {json.dumps(par[w1.name])}")
-            tiny_sampled = sampled_run(w1.config.replace(context_length=2048), ck1, w1.prompt(), 128)
-            log(f"TinyLlama decode, temperature sampler on the device: {tiny_sampled} tok/s")
+            if args.only is None:
+                tiny_sampled = sampled_run(w1.config.replace(context_length=2048), ck1, w1.prompt(), 128)
+                log(f"TinyLlama decode, temperature sampler on the device: {tiny_sampled} tok/s")
+            del ck1
+        if want("prefill"):
             w2 = WORKLOADS["tinyllama_q4_0_prefill"]
             log(f"TinyLlama {w2.n_prompt}-token prefill + {w2.n_decode} decode")
-            del ck1
             prefill = prefill_run(w2, w2.checkpoint())
             log(f"  {json.dumps(prefill)}")
+        if args.only is None:
             cfgq = QWEN2_0_5B.replace(context_length=2048)
             ckq = synth.llama_checkpoint(cfgq, seed=5, mix="q8_0", with_output=False, embedding=_native.GGML_Q8_0)
             pq = synth.tokens(5, "prompt", 16, cfgq.vocab_size)
@@ -514,13 +555,13 @@ def main():
         "tinyllama_q4_0_prefill": prefill,
         "llama2_7b_q4_k_m": kq,
         "qwen2_0_5b_q8_0": qwen,
-        "roofline": {"bound": "hbm", "achieved": roof["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": roof["frac"],
+        "roofline": {"bound": "hbm", "achieved": roof.get("GB/s"), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": roof.get("frac"),
                      "traffic": profile_figure("gemv_q4_0_sweep_roofline.md",
                                                f"traffic_bytes_per_launch {ROOF_SHAPE[0]}x{ROOF_SHAPE[1]}"),
                      "traffic_source": "profiles/gemv_q4_0_sweep_roofline.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
                      "kernel": "gemv_kernel<Q4_0> (chatnet_matmul N=1) at 11008x4096, cold",
-                     "alg_bytes_per_launch": roof["alg_bytes"], "avg_launch_us": roof["us"],
+                     "alg_bytes_per_launch": roof.get("alg_bytes"), "avg_launch_us": roof.get("us"),
                      "measured_copy_GBs": copy_gbs,
                      "measured_copy_note": "512 MiB device-to-device copy, read + write bytes per second"},
         "cpu_baseline": cpu,

@@ -189,8 +189,9 @@ struct chatnet_model {
 
 namespace {
 
-// Most decode-attention chunks per kv head: up to two workgroups per CU over
-// the kv heads, at most 64.
+// Most decode-attention chunks per kv head the CUs call for: up to two
+// workgroups per CU over the kv heads, at most 64 (the model then caps it by
+// what the O projection folds).
 int attn_max_splits(int n_kv_heads, int num_cus) {
   int s = 1;
   while (s < 64 && s * 2 * n_kv_heads <= 2 * num_cus) s *= 2;
@@ -363,6 +364,14 @@ int chatnet_create(const chatnet_config* cfg, int device, chatnet_model** out) {
   m->layers.resize(c.n_layers);
   const size_t kv_bytes = (size_t)c.n_layers * c.context_length * m->kv_dim * m->kv_elt;
   m->attn_splits_max = attn_max_splits(c.n_kv_heads, m->num_cus);
+  {
+    // Every workgroup of the O projection reads all chunk partials while it
+    // stages x (n_heads * splits * head_dim floats): at most 64 KB of them,
+    // and never more chunks than it can fold, so no merge launch is needed.
+    int fold_cap = (int)((64 << 10) / ((size_t)c.n_heads * c.head_dim * sizeof(float)));
+    fold_cap = fold_cap < 2 ? 2 : (fold_cap > kFoldMaxSplits ? kFoldMaxSplits : fold_cap);
+    if (m->attn_splits_max > fold_cap) m->attn_splits_max = fold_cap;
+  }
   const size_t attn_slots = (size_t)c.n_heads * m->attn_splits_max;
   auto cleanup = [m]() { chatnet_destroy(m); };
   if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) {
@@ -638,8 +647,6 @@ int launch_token(chatnet_model* m, bool lm_head, int cap, bool decode = false) {
     at.chunk = plan.chunk;
     at.part_o = m->attn_part_o;
     at.part_ml = m->attn_part_ml;
-    // a few chunks are combined by the O GEMV as it stages x (no merge launch)
-    at.fold = plan.splits > 1 && plan.splits <= kFoldMaxSplits;
     at.stop = a.stop;
     at.hsplit = attn_decode_hsplit(c.n_kv_heads, at.kv_mul, plan.splits, m->num_cus);
     HIP_TRY(attn_decode_launch(at, st));
@@ -651,13 +658,14 @@ int launch_token(chatnet_model* m, bool lm_head, int cap, bool decode = false) {
     o.seg_rows[0] = c.dim;
     o.n_vrows = c.dim;
     o.out[0] = m->x;
-    if (at.fold) {
+    const bool fold = plan.splits > 1;  // the O GEMV combines the chunks as it stages x
+    if (fold) {
       o.part_o = m->attn_part_o;
       o.part_ml = m->attn_part_ml;
       o.msplits = plan.splits;
       o.mchunk = plan.chunk;
     }
-    HIP_TRY(gemv_launch((int)L.wo.type, at.fold ? GEMV_EPI_ADD_MERGE : GEMV_EPI_ADD, o, m->num_cus, st));
+    HIP_TRY(gemv_launch((int)L.wo.type, fold ? GEMV_EPI_ADD_MERGE : GEMV_EPI_ADD, o, m->num_cus, st));
 
     GemvArgs g = base_args(m, decode);
     g.K = c.dim;

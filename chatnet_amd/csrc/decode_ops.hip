@@ -35,13 +35,6 @@ __global__ __launch_bounds__(CN_BLOCK) void embed_kernel(const void* emb, int ty
   }
 }
 
-// Splits that carry positions at sequence length seq: the launch covers
-// a.splits fixed chunks of a.chunk positions, and chunk c is active while
-// c * chunk < seq.
-__device__ __forceinline__ int attn_active_splits(const AttnArgs& a, int seq) {
-  return min(a.splits, (seq + a.chunk - 1) / a.chunk);
-}
-
 // n consecutive floats of a K/V cache row (fp32 or fp16) starting at idx.
 template <bool F16, int N>
 __device__ __forceinline__ void kv_load_n(const void* base, size_t idx, float* out) {
@@ -118,7 +111,8 @@ __device__ __forceinline__ void attn_put(const AttnArgs& a, int h, int split, in
 // only on the chunk, so they are in flight before the position arrives.  With
 // WP = 1 each wave holds its heads' complete result for the chunk; otherwise
 // the WP waves of a head fold through LDS.  A launch of one chunk writes the
-// output itself; more chunks leave partials for attn_merge_kernel.
+// output itself; more chunks (at most kFoldMaxSplits) leave partials that the
+// O projection combines as it stages its x (GEMV_EPI_ADD_MERGE).
 template <int HD, bool F16, int HPW, int PG>
 __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
   constexpr int EPL = HD / 16;   // head elements per lane
@@ -299,80 +293,6 @@ __global__ __launch_bounds__(CN_BLOCK) void attn_decode_kernel(AttnArgs a) {
   }
 }
 
-// Merges the active split partials of one query head (grid = n_heads,
-// block = CN_BLOCK = G groups of HD threads):
-//   M = max_c m_c,  L = sum_c l_c e^(m_c - M),  out = sum_c o_c e^(m_c - M) / L,
-// empty splits (l_c = 0) contributing nothing.  Group g takes splits
-// g, g+G, ... in rounds of R (all loads of a round in flight together, the
-// running (M, L, acc) rescaled when a round raises the maximum), so up to G*R
-// splits cost one memory round trip; the G group states are then combined the
-// same way through LDS.
-template <int HD>
-__global__ __launch_bounds__(CN_BLOCK) void attn_merge_kernel(AttnArgs a) {
-  constexpr int R = 16;
-  constexpr int G = CN_BLOCK / HD;
-  __shared__ float sm[G][HD], sl[G], so[G][HD];
-  const int h = blockIdx.x, d = threadIdx.x % HD, g = threadIdx.x / HD;
-  if (a.stop && *a.stop) return;
-  const int s_eff = attn_active_splits(a, *a.pos + 1);
-  const size_t base = (size_t)h * a.splits;
-  float M = -INFINITY, L = 0.f, acc = 0.f;
-  // The loads cover every split of the launch (their addresses do not depend
-  // on the position), so they are in flight before s_eff is known; inactive
-  // splits hold stale values and are masked out.
-  for (int c0 = g; c0 < a.splits; c0 += G * R) {
-    float mc[R], lc[R], oc[R];
-#pragma unroll
-    for (int c = 0; c < R; c++) {
-      const int cs = c0 + G * c;
-      const bool in = cs < a.splits;
-      const float mr = in ? a.part_ml[2 * (base + cs)] : 0.f;
-      const float lr = in ? a.part_ml[2 * (base + cs) + 1] : 0.f;
-      const float orr = in ? a.part_o[(base + cs) * HD + d] : 0.f;
-      const bool on = cs < s_eff;
-      mc[c] = on ? mr : 0.f;
-      lc[c] = on ? lr : 0.f;
-      oc[c] = on ? orr : 0.f;
-    }
-    float Mn = M;
-#pragma unroll
-    for (int c = 0; c < R; c++)
-      if (lc[c] > 0.f) Mn = fmaxf(Mn, mc[c]);
-    if (Mn == -INFINITY) continue;  // nothing in this round or before it
-    const float r = (M == -INFINITY) ? 0.f : expf(M - Mn);
-    L *= r;
-    acc *= r;
-#pragma unroll
-    for (int c = 0; c < R; c++) {
-      if (lc[c] > 0.f) {
-        const float f = expf(mc[c] - Mn);
-        L += lc[c] * f;
-        acc += oc[c] * f;
-      }
-    }
-    M = Mn;
-  }
-  sm[g][d] = M;
-  so[g][d] = acc;
-  if (d == 0) sl[g] = L;
-  __syncthreads();
-  if (g != 0) return;
-  float Mt = -INFINITY;
-#pragma unroll
-  for (int k = 0; k < G; k++)
-    if (sl[k] > 0.f) Mt = fmaxf(Mt, sm[k][d]);
-  float Lt = 0.f, at = 0.f;
-#pragma unroll
-  for (int k = 0; k < G; k++) {
-    if (sl[k] > 0.f) {
-      const float f = expf(sm[k][d] - Mt);
-      Lt += sl[k] * f;
-      at += so[k][d] * f;
-    }
-  }
-  a.out[(size_t)h * HD + d] = at / Lt;
-}
-
 // GreedySampler.Sample: strict '>' scan => the lowest index of the maximum;
 // NaN never wins unless it sits at index 0, in which case the answer is 0.
 // A decode-loop pick (out_tokens given) does nothing once the loop has
@@ -471,7 +391,6 @@ hipError_t attn_launch_t(const AttnArgs& a, hipStream_t st) {
   if (hpw == 1) attn_launch_k<HD, F16, 1>(a, st);
   else if (hpw == 2 || HD > 128) attn_launch_k<HD, F16, 2>(a, st);
   else attn_launch_k<HD, F16, 4>(a, st);
-  if (a.splits > 1 && !a.fold) hipLaunchKernelGGL((attn_merge_kernel<HD>), dim3(a.n_heads), dim3(CN_BLOCK), 0, st, a);
   return hipGetLastError();
 }
 
@@ -500,7 +419,7 @@ int attn_decode_round(int head_dim, int kv_mul) {
 }
 
 hipError_t attn_decode_launch(const AttnArgs& a, hipStream_t st) {
-  if (a.splits < 1 || a.splits > 64 || a.chunk < 1 || a.head_dim % 16 != 0 || a.hsplit < 1 ||
+  if (a.splits < 1 || a.splits > kFoldMaxSplits || a.chunk < 1 || a.head_dim % 16 != 0 || a.hsplit < 1 ||
       a.kv_mul % a.hsplit != 0)
     return hipErrorInvalidValue;
   if (a.head_dim == 64) return a.kv_f16 ? attn_launch_t<64, true>(a, st) : attn_launch_t<64, false>(a, st);

@@ -140,9 +140,8 @@ struct AttnArgs {
   float scale;
   float* part_o;      // split partials: [n_heads][splits][head_dim]
   float* part_ml;     // [n_heads][splits][2] (max, sum)
-  int splits;         // position chunks of the launch (<= 64), one workgroup per kv head each
+  int splits;         // position chunks of the launch (<= kFoldMaxSplits), one workgroup per kv head each
   int chunk;          // positions per chunk: chunk c covers [c*chunk, (c+1)*chunk) below pos+1
-  int fold;           // splits > 1: leave the partials for the O GEMV (GEMV_EPI_ADD_MERGE)
   int hsplit;         // workgroups per kv head, each taking kv_mul / hsplit query heads
   const int* stop;    // decode loops: return at once while *stop is set (nullptr: never)
 };

@@ -206,9 +206,12 @@ CHATNET_API int chatnet_get_logits(chatnet_model* m, float* logits_host);
  * W is M rows of raw GGUF blocks (row stride K/block*bytes_per_block), x is
  * N x K fp32 row-major, y is N x M fp32 row-major; w_dev and x_dev 16-byte
  * aligned.  Types F32, F16, Q4_0, Q8_0 and K % 64 == 0, or Q4_K, Q5_K, Q6_K
- * and K % 256 == 0, with K <= 16384.  N >= 8 with Q4_0 runs the
- * dequant-to-LDS bf16 MFMA GEMM (x rounded to bf16); any other call runs the
- * fused GEMV once per column.  The GEMM's workspace is allocated on first use
+ * and K % 256 == 0, with K <= 16384.  N >= 8 with Q4_0, Q8_0, Q4_K, Q5_K or
+ * Q6_K runs the dequant-to-LDS bf16 MFMA GEMM (x rounded to bf16; Q4_0 read as
+ * raw blocks, the other types first re-encoded into the workspace as u8 codes
+ * with an fp32 scale and offset per 16 weights, M*(K/64)*96 bytes, giving the
+ * same dequantized values); any other call (N < 8, F32, F16) runs the fused
+ * GEMV once per column.  The GEMM's workspace is allocated on first use
  * per (device, stream) and kept until the process ends (a buffer it outgrows
  * is retired, not freed, since a captured graph may still read it).  A call
  * on a stream under HIP graph capture cannot allocate: it fails with
@@ -222,8 +225,10 @@ CHATNET_API int chatnet_matmul(uint32_t ggml_type, const void* w_dev, const floa
 /* chatnet_matmul without any allocation, for callers that cannot allocate
  * device memory: code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc.  No counterpart in the reference.  Same arguments,
- * kernels and results as chatnet_matmul; the batched path's scratch (bf16 x
- * and the K-split partials) lives in a fixed 64 MiB array per device, held by
+ * kernels and results as chatnet_matmul for Q4_0; the other types run the
+ * fused GEMV once per column (their packed copy of W would need the scratch).
+ * The batched path's scratch (bf16 x and the K-split partials) lives in a
+ * fixed 64 MiB array per device, held by
  * the library from load to process exit, instead of a per-stream workspace.
  * Calls needing more scratch than that (N*K*2 bytes of x, rounded up to 256,
  * plus the partials) fail with CHATNET_ERR_INVALID_ARG before launching
