@@ -2,6 +2,8 @@
 
     lib/libchatnet_hip.so    HIP kernels + C ABI for gfx950 (hipcc)
     lib/libchatnet_synth.so  host-only synthetic weight generator (gcc)
+    lib/probe_chain_floor    stand-alone measurement of a dependent-kernel
+                             chain's floor in a HIP graph (not the library)
 
 Run as `python -m chatnet_amd.build_lib` or through __graft_entry__.build().
 """
@@ -91,8 +93,22 @@ def build_synth(verbose: bool = False) -> str:
     return out
 
 
+def build_probe(verbose: bool = False) -> str:
+    hipcc = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
+    os.makedirs(LIBDIR, exist_ok=True)
+    out = os.path.join(LIBDIR, "probe_chain_floor")
+    tmp = out + ".tmp"
+    flags = [f for f in HIPCC_FLAGS if f not in ("-shared", "-fPIC", "-fvisibility=hidden")]
+    cmd = [hipcc, *flags, os.path.join(CSRC, "probe_chain_floor.hip"), "-o", tmp]
+    if verbose:
+        print(" ".join(cmd))
+    _run(cmd)
+    os.replace(tmp, out)
+    return out
+
+
 def build_all(verbose: bool = False) -> list[str]:
-    return [build_synth(verbose), build_hip(verbose)]
+    return [build_synth(verbose), build_hip(verbose), build_probe(verbose)]
 
 
 if __name__ == "__main__":
