@@ -301,16 +301,47 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, int n
                                                       int* out_tokens, int out_cap) {
   __shared__ float bv[16];
   __shared__ int bi[16];
-  if (out_tokens && state[kDecStop]) return;
+  // Every logit load of a round is issued before the first comparison (one
+  // memory latency per round instead of one per element); the decode
+  // loop's stop flag is read as a vector load behind them.
+  constexpr int U = 8;  // float4 per thread per round
+  const int tid = threadIdx.x;
+  const int n4 = n >> 2;
+  const float4* l4 = reinterpret_cast<const float4*>(logits);
   float best = -INFINITY;
   int idx = 0x7FFFFFFF;
-  for (int i = threadIdx.x; i < n; i += 1024) {
-    const float v = logits[i];
-    if (v > best) {
-      best = v;
+  for (int base = 0; base < n4; base += 1024 * U) {
+    float4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int j = base + u * 1024 + tid;
+      v[u] = l4[j < n4 ? j : n4 - 1];
+    }
+    // a thread's elements come in increasing index order, so the strict '>'
+    // keeps the lowest index of its maximum
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int j = base + u * 1024 + tid;
+      if (j < n4) {
+        const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+          if (e[k] > best) {
+            best = e[k];
+            idx = 4 * j + k;
+          }
+      }
+    }
+  }
+  if (tid < (n & 3)) {
+    const int i = 4 * n4 + tid;
+    const float e = logits[i];
+    if (e > best) {  // above every element this thread has seen: all have lower indices
+      best = e;
       idx = i;
     }
   }
+  const int stop = out_tokens ? cn_load_late(state + kDecStop) : 0;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
     const float ov = __shfl_xor(best, off, 64);
@@ -320,13 +351,13 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, int n
       idx = oi;
     }
   }
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = tid & 63, wave = tid >> 6;
   if (lane == 0) {
     bv[wave] = best;
     bi[wave] = idx;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (tid == 0 && !stop) {
     best = bv[0];
     idx = bi[0];
     for (int w = 1; w < 16; w++)

@@ -171,14 +171,16 @@ def test_weight_and_embedding_types_match_oracle(mix, emb, tied):
     compare_greedy(gt, o, margins, f"types mix={mix} embedding={emb} tied={tied}")
 
 
-@pytest.mark.parametrize("tie_rows,nan_rows,expect", [
-    ((7, 1030, 1031, 3000, 4095), (), 7),     # ties across threads and waves: lowest index wins
-    ((1024, 2048, 9), (), 9),                 # same thread (stride 1024) and across waves
-    ((7, 3000), (0,), 0),                     # NaN at index 0 never loses (GreedySampler.cs:16-24)
-    ((7, 3000), (5, 2999), 7),                # NaN elsewhere never wins
+@pytest.mark.parametrize("tie_rows,nan_rows,expect,vocab", [
+    ((7, 1030, 1031, 3000, 4095), (), 7, 4096),  # ties across threads and waves: lowest index wins
+    ((1024, 2048, 9), (), 9, 4096),              # same thread (stride 1024) and across waves
+    ((7, 3000), (0,), 0, 4096),                  # NaN at index 0 never loses (GreedySampler.cs:16-24)
+    ((7, 3000), (5, 2999), 7, 4096),             # NaN elsewhere never wins
+    ((40002, 32769, 40001), (), 32769, 40003),   # second round of loads, the 3 tail elements
+    ((40002,), (1,), 40002, 40003),              # the maximum in the tail only
 ])
-def test_device_argmax_ties_and_nan(tie_rows, nan_rows, expect):
-    cfg = TINY_TEST.replace(vocab_size=4096)
+def test_device_argmax_ties_and_nan(tie_rows, nan_rows, expect, vocab):
+    cfg = TINY_TEST.replace(vocab_size=vocab)
     ck = synth.llama_checkpoint(cfg, seed=28)
     prompt = [3, 1, 4, 1, 5]
     bpr = cfg.dim // 32 * 18
