@@ -805,7 +805,7 @@ int ensure_span_buffers(chatnet_model* m) {
 
 int span_gemm(chatnet_model* m, GemmArgs& g) {
   g.precise = 1;
-  const size_t need = gemm_workspace_bytes(g.M, g.N, g.K, m->num_cus, true);
+  const size_t need = gemm_workspace_bytes(g.M, g.N, g.K, m->num_cus, true, g.packed != 0);
   if (need > m->sp_part_bytes) {
     HIP_TRY(hipStreamSynchronize(m->stream));
     if (m->sp_part) (void)hipFree(m->sp_part);
@@ -1014,7 +1014,7 @@ int matmul_impl(uint32_t type, const void* w_dev, const float* x_dev, float* y_d
     // x -> bf16 into the scratch, then the MFMA GEMM (K-split partials after x,
     // packed W after those).
     const size_t xb_bytes = ((size_t)N * K * sizeof(uint16_t) + 255) & ~(size_t)255;
-    const size_t part_bytes = (gemm_workspace_bytes(M, N, K, cus, false) + 255) & ~(size_t)255;
+    const size_t part_bytes = (gemm_workspace_bytes(M, N, K, cus, false, pack) + 255) & ~(size_t)255;
     const size_t pack_bytes = pack ? gemm_pack_bytes(M, K) : 0;
     const size_t need = xb_bytes + part_bytes + pack_bytes;
     char* ws = nullptr;

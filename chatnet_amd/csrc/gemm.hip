@@ -648,14 +648,19 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_pack_kernel(int qtype, const ui
 
 // Column tile by batch size (32, 64 or 128 columns per workgroup, 128 rows);
 // K is split while the tile grid covers fewer than two workgroups per CU,
-// keeping at least 8 chunks of 64 per split so the LDS ring stays full.
+// keeping at least 8 chunks of 64 per split so the LDS ring stays full.  The
+// two-plane kernel on raw Q4_0 blocks takes 64-column tiles at any N > 32:
+// its ring is then 66 KB, so two workgroups share a CU and one's pipeline
+// fill and epilogue overlap the other's MFMAs (measured per GEMM of 22
+// TinyLlama layers at N = 512: 5.28 -> 4.89 ms; 7B shapes at N = 128: 2.13 ->
+// 1.91 ms).  128-column tiles of packed weights would not fit twice either way.
 struct GemmShape {
   int tn, splits;
 };
 
-GemmShape pick_gemm(int M, int N, int K, int num_cus) {
+GemmShape pick_gemm(int M, int N, int K, int num_cus, bool precise, bool packed) {
   GemmShape s;
-  s.tn = N <= 32 ? 1 : (N <= 64 ? 2 : 4);
+  s.tn = N <= 32 ? 1 : (N <= 64 || (precise && !packed) ? 2 : 4);
   const long long tiles = (long long)((M + 127) / 128) * ((N + 32 * s.tn - 1) / (32 * s.tn));
   const int nchunks = K / 64;
   s.splits = 1;
@@ -725,8 +730,8 @@ hipError_t gemm_pack_launch(int qtype, const void* w, int M, int K, void* dst, h
   return hipGetLastError();
 }
 
-size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool /*precise*/) {
-  const GemmShape s = pick_gemm(M, N, K, num_cus);
+size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool precise, bool packed) {
+  const GemmShape s = pick_gemm(M, N, K, num_cus, precise, packed);
   return s.splits > 1 ? (size_t)s.splits * N * M * sizeof(float) : 0;
 }
 
@@ -735,7 +740,7 @@ hipError_t gemm_launch(const GemmArgs& a_in, int num_cus, hipStream_t st) {
   if (!k_ok || a_in.M <= 0 || a_in.N <= 0) return hipErrorInvalidValue;
   const bool precise = a_in.precise != 0;
   if (precise && !a_in.xb_lo) return hipErrorInvalidValue;
-  const GemmShape s = pick_gemm(a_in.M, a_in.N, a_in.K, num_cus);
+  const GemmShape s = pick_gemm(a_in.M, a_in.N, a_in.K, num_cus, precise, a_in.packed != 0);
   GemmArgs a = a_in;
   a.splits = s.splits;
   if (s.splits > 1 && !a.part) return hipErrorInvalidValue;

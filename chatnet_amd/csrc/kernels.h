@@ -87,7 +87,7 @@ constexpr int kGemmPackUnit = 96;
 bool gemm_pack_supports(int qtype, int K);
 size_t gemm_pack_bytes(int M, int K);
 hipError_t gemm_pack_launch(int qtype, const void* w, int M, int K, void* dst, hipStream_t st);
-size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool precise);
+size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool precise, bool packed);
 hipError_t gemm_launch(const GemmArgs& a, int num_cus, hipStream_t st);
 hipError_t to_bf16_launch(const float* x, uint16_t* xb, size_t n, hipStream_t st);
 // xb = bf16(RMSNorm(x) * g) per row; with xb_lo also the low parts.
