@@ -144,14 +144,14 @@ __device__ __forceinline__ void stage_load(const float* __restrict__ x, const fl
 // for the thread's items (the two float4 of an item lie in one head: 32-element
 // blocks never straddle a head), then, after the caller has issued its weight
 // loads, stage_merge combines them as merged_x4 does.
-template <int MAXT>
+template <int MAXT, int NS>
 struct XMerge {
-  float2 ml[MAXT][kFoldMaxSplits];
-  float4 lo[MAXT][kFoldMaxSplits], hi[MAXT][kFoldMaxSplits];
+  float2 ml[MAXT][NS];
+  float4 lo[MAXT][NS], hi[MAXT][NS];
 };
 
-template <int MAXT, int BS>
-__device__ __forceinline__ void stage_merge_load(const MergeSrc& m, int K, XMerge<MAXT>& r) {
+template <int MAXT, int BS, int NS>
+__device__ __forceinline__ void stage_merge_load(const MergeSrc& m, int K, XMerge<MAXT, NS>& r) {
   const int ntask = K >> 3;
 #pragma unroll
   for (int j = 0; j < MAXT; j++) {
@@ -161,7 +161,7 @@ __device__ __forceinline__ void stage_merge_load(const MergeSrc& m, int K, XMerg
     const int h = i / m.hd, d = i - h * m.hd;
     const size_t base = (size_t)h * m.splits;
 #pragma unroll
-    for (int c = 0; c < kFoldMaxSplits; c++) {  // chunks past splits re-read the last one, weight 0
+    for (int c = 0; c < NS; c++) {  // chunks past splits re-read the last one, weight 0
       const size_t s = base + (c < m.splits ? c : m.splits - 1);
       r.ml[j][c] = *reinterpret_cast<const float2*>(m.ml + 2 * s);
       r.lo[j][c] = *reinterpret_cast<const float4*>(m.o + s * m.hd + d);
@@ -170,14 +170,14 @@ __device__ __forceinline__ void stage_merge_load(const MergeSrc& m, int K, XMerg
   }
 }
 
-template <int MAXT, bool NORM>
-__device__ __forceinline__ void stage_merge(const MergeSrc& m, const XMerge<MAXT>& r, XStage<MAXT, NORM>& st) {
+template <int MAXT, bool NORM, int NS>
+__device__ __forceinline__ void stage_merge(const MergeSrc& m, const XMerge<MAXT, NS>& r, XStage<MAXT, NORM>& st) {
 #pragma unroll
   for (int j = 0; j < MAXT; j++) {
-    float2 ml[kFoldMaxSplits];
+    float2 ml[NS];
     float M = -INFINITY;
 #pragma unroll
-    for (int c = 0; c < kFoldMaxSplits; c++) {
+    for (int c = 0; c < NS; c++) {
       ml[c] = r.ml[j][c];
       if (c >= m.s_eff) ml[c].y = 0.f;
       if (ml[c].y > 0.f) M = fmaxf(M, ml[c].x);
@@ -185,7 +185,7 @@ __device__ __forceinline__ void stage_merge(const MergeSrc& m, const XMerge<MAXT
     float L = 0.f;
     float4 lo = make_float4(0.f, 0.f, 0.f, 0.f), hi = lo;
 #pragma unroll
-    for (int c = 0; c < kFoldMaxSplits; c++) {
+    for (int c = 0; c < NS; c++) {
       if (ml[c].y > 0.f) {
         const float f = expf(ml[c].x - M);
         L += ml[c].y * f;
@@ -316,7 +316,7 @@ struct XStage16<MAXT, false> {
 
 // Group t of x (and of the RMSNorm weight) on thread t % BS, loads issued
 // before the caller's weight loads (see stage_load).
-template <int MAXT, bool NORM, int BS, bool MERGE = false>
+template <int MAXT, bool NORM, int BS, bool MERGE = false, int NS = kFoldMaxSplits>
 __device__ __forceinline__ void stage_load16(const float* __restrict__ x, const float* __restrict__ norm_w, int K,
                                              XStage16<MAXT, NORM>& st, const MergeSrc& ms = MergeSrc{}) {
   const int ngroups = K >> 4;
@@ -325,12 +325,12 @@ __device__ __forceinline__ void stage_load16(const float* __restrict__ x, const 
     const int t = threadIdx.x + BS * j;
     const bool on = t < ngroups;
     const int tc = on ? t : ngroups - 1;  // loads issued unconditionally (see stage_load)
-    MergeW mw{};
+    MergeW<NS> mw{};
     int mh = 0, md = 0;
     if constexpr (MERGE) {  // the group's 16 elements lie in one head
       mh = (16 * tc) / ms.hd;
       md = 16 * tc - mh * ms.hd;
-      mw = merge_weights(ms, mh);
+      mw = merge_weights<NS>(ms, mh);
     }
 #pragma unroll
     for (int c = 0; c < 4; c++) {
@@ -803,7 +803,8 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
   // The stop flag and the position are read as vector loads issued ahead of
   // x and consumed late (after staging, in the epilogue), so no scalar wait
   // for them stalls the loads at the start.
-  constexpr bool MERGE = EPI == GEMV_EPI_ADD_MERGE;
+  constexpr bool MERGE = is_merge(EPI);
+  constexpr int NS = merge_slots(EPI);
   const int stop_v = cn_load_late(stop_flag(a));
   const int pos_v = (EPI == GEMV_EPI_QKV || MERGE) ? cn_load_late(a.pos) : 0;
   constexpr bool kDig8 = QT == QT_Q8_0 || QT == QT_Q6_K || QT == QT_Q5_K || (QT == QT_Q4_K && LPR > 32);
@@ -831,7 +832,7 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
       // groups per thread: K <= UNIT * LPR * NU, so K/16 <= (UNIT/16) * LPR * NU groups over BS threads
       constexpr int MAXT = ((UNIT / 16) * LPR * NU + BS - 1) / BS;
       XStage16<MAXT, NORM> st;
-      stage_load16<MAXT, NORM, BS, MERGE>(a.x, a.norm_w, K, st, ms);
+      stage_load16<MAXT, NORM, BS, MERGE, NS>(a.x, a.norm_w, K, st, ms);
       // Two units per lane: the staged x would sit beside twice the weight
       // registers (2 waves per SIMD), so it is digitized before the weight
       // loads are issued.
@@ -851,15 +852,15 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
       constexpr int MAXT = ((UNIT / 8) * LPR * NU + BS - 1) / BS;
       XStage<MAXT, NORM> st;
       stage_load<MAXT, NORM, BS, MERGE>(a.x, a.norm_w, K, st, ms);
-      XMerge<MERGE ? MAXT : 1> mr;
-      if constexpr (MERGE) stage_merge_load<MAXT, BS>(ms, K, mr);
+      XMerge<MERGE ? MAXT : 1, MERGE ? NS : 1> mr;
+      if constexpr (MERGE) stage_merge_load<MAXT, BS, NS>(ms, K, mr);
       // rows past n_vrows are loaded (re-reading the last row) and skipped
       issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
       load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, 0, res);
       if constexpr (MERGE) {
         // chunks below pos + 1 (the position arrives with the partials)
         ms.s_eff = min(a.msplits, (__builtin_amdgcn_readfirstlane(pos_v) + a.mchunk) / a.mchunk);
-        stage_merge<MAXT, NORM>(ms, mr, st);
+        stage_merge<MAXT, NORM, NS>(ms, mr, st);
       }
       xred = reinterpret_cast<float*>(smem) + (size_t)(K >> 6) * XD_UNIT_DW;
       stage_digitize<MAXT, NORM, BS, QT == QT_Q4_K>(st, K, xd, xred);
@@ -1244,6 +1245,8 @@ hipError_t gemv_launch(int qtype, int epi, const GemvArgs& a, int num_cus, hipSt
     case GEMV_EPI_ADD_MERGE:
       if (a.msplits < 2 || a.msplits > kFoldMaxSplits || a.mchunk < 1 || a.head_dim % 32 != 0)
         return hipErrorInvalidValue;
+      if (merge_epi(a.msplits) == kEpiMerge2) return launch_epi<kEpiMerge2>(qtype, a, num_cus, st);
+      if (merge_epi(a.msplits) == kEpiMerge4) return launch_epi<kEpiMerge4>(qtype, a, num_cus, st);
       return launch_epi<GEMV_EPI_ADD_MERGE>(qtype, a, num_cus, st);
     default: return hipErrorInvalidValue;
   }

@@ -28,17 +28,27 @@ struct MergeSrc {
   int hd, splits, s_eff;
 };
 
+// ADD_MERGE instances by chunk slots: the epilogue value a launch passes
+// (GEMV_EPI_ADD_MERGE, up to kFoldMaxSplits chunks) is dispatched to the
+// instance with the fewest slots that hold its chunks, so a launch of 2 or 4
+// chunks issues 2 or 4 chunks' loads per element, not kFoldMaxSplits.
+constexpr int kEpiMerge4 = 6, kEpiMerge2 = 7;
+constexpr bool is_merge(int epi) { return epi == GEMV_EPI_ADD_MERGE || epi == kEpiMerge4 || epi == kEpiMerge2; }
+constexpr int merge_slots(int epi) { return epi == kEpiMerge2 ? 2 : (epi == kEpiMerge4 ? 4 : kFoldMaxSplits); }
+constexpr int merge_epi(int splits) { return splits <= 2 ? kEpiMerge2 : (splits <= 4 ? kEpiMerge4 : GEMV_EPI_ADD_MERGE); }
+
 // Elements i .. i+3 combined in one round trip: every chunk's (max, sum) and
 // outputs are loaded together, then folded.  Used by the base-16 staging,
 // whose items (two float4 of one head) gain nothing from sharing the weights.
+template <int NS>
 __device__ __forceinline__ float4 merged_x4(const MergeSrc& m, int i) {
   const int h = i / m.hd, d = i - h * m.hd;
   const size_t base = (size_t)h * m.splits;
-  float2 ml[kFoldMaxSplits];
-  float4 oc[kFoldMaxSplits];
+  float2 ml[NS];
+  float4 oc[NS];
   float M = -INFINITY;
 #pragma unroll
-  for (int c = 0; c < kFoldMaxSplits; c++) {  // straight-line loads: chunks past splits re-read the last
+  for (int c = 0; c < NS; c++) {  // straight-line loads: chunks past splits re-read the last
     const int cc = c < m.splits ? c : m.splits - 1;
     ml[c] = *reinterpret_cast<const float2*>(m.ml + 2 * (base + cc));
     oc[c] = *reinterpret_cast<const float4*>(m.o + (base + cc) * m.hd + d);
@@ -48,7 +58,7 @@ __device__ __forceinline__ float4 merged_x4(const MergeSrc& m, int i) {
   float L = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (int c = 0; c < kFoldMaxSplits; c++) {
+  for (int c = 0; c < NS; c++) {
     if (ml[c].y > 0.f) {
       const float f = expf(ml[c].x - M);
       L += ml[c].y * f;
@@ -63,25 +73,27 @@ __device__ __forceinline__ float4 merged_x4(const MergeSrc& m, int i) {
 
 // Chunk weights of head h: f[c] = e^(M_c - M) for active chunks that hold
 // positions (0 otherwise) and their sum L = sum_c L_c f[c].
+template <int NS>
 struct MergeW {
-  float f[kFoldMaxSplits];
+  float f[NS];
   float L;
 };
 
-__device__ __forceinline__ MergeW merge_weights(const MergeSrc& m, int h) {
+template <int NS>
+__device__ __forceinline__ MergeW<NS> merge_weights(const MergeSrc& m, int h) {
   const size_t base = (size_t)h * m.splits;
-  float2 ml[kFoldMaxSplits];
+  float2 ml[NS];
   float M = -INFINITY;
 #pragma unroll
-  for (int c = 0; c < kFoldMaxSplits; c++) {  // straight-line loads: chunks past splits re-read the last
+  for (int c = 0; c < NS; c++) {  // straight-line loads: chunks past splits re-read the last
     ml[c] = *reinterpret_cast<const float2*>(m.ml + 2 * (base + (c < m.splits ? c : m.splits - 1)));
     if (c >= m.s_eff) ml[c].y = 0.f;
     if (ml[c].y > 0.f) M = fmaxf(M, ml[c].x);
   }
-  MergeW w;
+  MergeW<NS> w;
   w.L = 0.f;
 #pragma unroll
-  for (int c = 0; c < kFoldMaxSplits; c++) {
+  for (int c = 0; c < NS; c++) {
     w.f[c] = ml[c].y > 0.f ? expf(ml[c].x - M) : 0.f;
     w.L += ml[c].y * w.f[c];
   }
@@ -89,11 +101,12 @@ __device__ __forceinline__ MergeW merge_weights(const MergeSrc& m, int h) {
 }
 
 // Elements d .. d+3 of head h combined with the chunk weights.
-__device__ __forceinline__ float4 merge_apply(const MergeSrc& m, const MergeW& w, int h, int d) {
+template <int NS>
+__device__ __forceinline__ float4 merge_apply(const MergeSrc& m, const MergeW<NS>& w, int h, int d) {
   const size_t base = (size_t)h * m.splits;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (int c = 0; c < kFoldMaxSplits; c++) {
+  for (int c = 0; c < NS; c++) {
     // chunks past splits re-read the last one (finite: every chunk of the
     // launch is written each step) with weight 0
     const float4 o = *reinterpret_cast<const float4*>(m.o + (base + (c < m.splits ? c : m.splits - 1)) * m.hd + d);
@@ -154,7 +167,7 @@ __device__ __forceinline__ void load_residual(const GemvArgs& a, int vr0, int li
   (void)li;
 #pragma unroll
   for (int i = 0; i < NR; i++) res[i] = 0.f;
-  if constexpr (EPI == GEMV_EPI_ADD || EPI == GEMV_EPI_ADD_MERGE) {
+  if constexpr (EPI == GEMV_EPI_ADD || is_merge(EPI)) {
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
       const int vr = vr0 + i < a.n_vrows ? vr0 + i : a.n_vrows - 1;
@@ -207,7 +220,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, const float
     if constexpr (EPI == GEMV_EPI_STORE || EPI == GEMV_EPI_LOGITS) {
       a.out[0][r] = v[i];
       if (vr + 1 < a.n_vrows) a.out[0][r + 1] = v[i + 1];
-    } else if constexpr (EPI == GEMV_EPI_ADD || EPI == GEMV_EPI_ADD_MERGE) {
+    } else if constexpr (EPI == GEMV_EPI_ADD || is_merge(EPI)) {
       a.out[0][r] = res[i] + v[i];
       if (vr + 1 < a.n_vrows) a.out[0][r + 1] = res[i + 1] + v[i + 1];
     } else if constexpr (EPI == GEMV_EPI_SWIGLU) {

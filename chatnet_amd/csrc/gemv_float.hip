@@ -77,7 +77,7 @@ __global__ __launch_bounds__(CN_BLOCK) void gemv_f_kernel(GemvArgs a) {
   float ss = 0.f;
   for (int c = threadIdx.x; c < (K >> 2); c += CN_BLOCK) {
     float4 v;
-    if constexpr (MERGE) v = merged_x4(ms, 4 * c);
+    if constexpr (MERGE) v = merged_x4<kFoldMaxSplits>(ms, 4 * c);
     else v = reinterpret_cast<const float4*>(a.x)[c];
     ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
     if constexpr (NORM) {
