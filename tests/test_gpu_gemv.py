@@ -68,6 +68,8 @@ def test_generic_type_gemv_shapes(qtype, M, K):
     # Q4_0 rows of 65..128 units: K split over two waves (65: the second wave
     # holds one unit; 128: both full)
     (2, 5, 4160), (2, 3, 8192), (2, 1, 8192),
+    # Q4_0 rows of 129..192 units: one row per lane, three units each
+    (2, 1, 8256), (2, 5, 12288), (2, 4097, 11008),
     (12, 3, 16384), (13, 3, 16384), (14, 3, 16384), (8, 9, 16320),
 ])
 def test_ragged_and_misaligned_shapes(qtype, M, K):
