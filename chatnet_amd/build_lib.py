@@ -4,6 +4,8 @@
     lib/libchatnet_synth.so  host-only synthetic weight generator (gcc)
     lib/probe_chain_floor    stand-alone measurement of a dependent-kernel
                              chain's floor in a HIP graph (not the library)
+    lib/probe_grid_handoff   stand-alone measurement of a grid-wide handoff
+                             inside one persistent kernel (not the library)
 
 Run as `python -m chatnet_amd.build_lib` or through __graft_entry__.build().
 """
@@ -21,6 +23,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIP_SOURCES = ["chatnet_api.hip", "gemv.hip", "gemv_float.hip", "gemm.hip", "prefill.hip", "decode_ops.hip", "sample.hip"]
 HIP_HEADERS = ["device_common.h", "gemv_common.h", "kernels.h"]
+PROBES = ["probe_chain_floor", "probe_grid_handoff"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -93,13 +96,13 @@ def build_synth(verbose: bool = False) -> str:
     return out
 
 
-def build_probe(verbose: bool = False) -> str:
+def build_probe(name: str, verbose: bool = False) -> str:
     hipcc = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
     os.makedirs(LIBDIR, exist_ok=True)
-    out = os.path.join(LIBDIR, "probe_chain_floor")
+    out = os.path.join(LIBDIR, name)
     tmp = out + ".tmp"
     flags = [f for f in HIPCC_FLAGS if f not in ("-shared", "-fPIC", "-fvisibility=hidden")]
-    cmd = [hipcc, *flags, os.path.join(CSRC, "probe_chain_floor.hip"), "-o", tmp]
+    cmd = [hipcc, *flags, os.path.join(CSRC, name + ".hip"), "-o", tmp]
     if verbose:
         print(" ".join(cmd))
     _run(cmd)
@@ -108,7 +111,7 @@ def build_probe(verbose: bool = False) -> str:
 
 
 def build_all(verbose: bool = False) -> list[str]:
-    return [build_synth(verbose), build_hip(verbose), build_probe(verbose)]
+    return [build_synth(verbose), build_hip(verbose)] + [build_probe(n, verbose) for n in PROBES]
 
 
 if __name__ == "__main__":
