@@ -803,7 +803,7 @@ int ensure_span_buffers(chatnet_model* m) {
   return CHATNET_OK;
 }
 
-int span_gemm(chatnet_model* m, GemmArgs& g) {
+int span_gemm(chatnet_model* m, GemmArgs& g, int* splits_left = nullptr) {
   g.precise = 1;
   const size_t need = gemm_workspace_bytes(g.M, g.N, g.K, m->num_cus, true, g.packed != 0);
   if (need > m->sp_part_bytes) {
@@ -816,7 +816,7 @@ int span_gemm(chatnet_model* m, GemmArgs& g) {
     m->sp_part_bytes = need;
   }
   g.part = m->sp_part;
-  HIP_TRY(gemm_launch(g, m->num_cus, m->stream));
+  HIP_TRY(gemm_launch(g, m->num_cus, m->stream, splits_left));
   return CHATNET_OK;
 }
 
@@ -837,6 +837,8 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position, SpanM
   uint16_t* xb_lo = m->sp_xb + (size_t)m->span_cap * c.dim;
   uint16_t* hb_lo = m->sp_hb + (size_t)m->span_cap * c.hidden_dim;
   int last_rows = 0;
+  int pending = 0;  // K splits of a residual-add GEMM whose partials the next norm folds in
+  int* defer = c.dim <= 4096 ? &pending : nullptr;  // the fold's register budget
   for (int s0 = 0; s0 < n; s0 += m->span_cap) {
     const int cn = n - s0 < m->span_cap ? n - s0 : m->span_cap;
     const int p0 = position + s0;
@@ -847,8 +849,11 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position, SpanM
       const size_t loff = (size_t)l * c.context_length * kvd * m->kv_elt;
       void* kc = (char*)m->kcache + loff;
       void* vc = (char*)m->vcache + loff;
-      HIP_TRY(rmsnorm_bf16_launch(m->sp_x, (const float*)L.attn_norm.ptr, c.rms_norm_eps, m->sp_xb, xb_lo, cn, c.dim,
-                                  st));
+      // the previous layer's down projection may have left its K-split
+      // partials: the residual add completes here, with the norm
+      HIP_TRY(add_rmsnorm_bf16_launch(m->sp_x, m->sp_part, pending, (const float*)L.attn_norm.ptr, c.rms_norm_eps,
+                                      m->sp_xb, xb_lo, cn, c.dim, st));
+      pending = 0;
       GemmArgs g;
       memset(&g, 0, sizeof(g));
       g.qtype = CHATNET_GGML_Q4_0;
@@ -868,7 +873,8 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position, SpanM
       g.epi = GEMV_EPI_STORE;
       g.y = m->sp_qkv;
       g.ldy = qkv_ld;
-      if ((rc = span_gemm(m, g))) return rc;
+      int qkv_splits = 0;  // partials the RoPE/KV kernel sums itself
+      if ((rc = span_gemm(m, g, &qkv_splits))) return rc;
 
       RopeKvArgs r;
       memset(&r, 0, sizeof(r));
@@ -883,6 +889,8 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position, SpanM
       r.vcache = vc;
       r.kv_f16 = c.kv_dtype == CHATNET_KV_F16;
       r.bias = L.bias_have ? L.bias : nullptr;
+      r.part = m->sp_part;
+      r.splits = qkv_splits;
       HIP_TRY(rope_kv_launch(r, cn, st));
 
       PrefillAttnArgs at;
@@ -918,10 +926,11 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position, SpanM
       o.epi = GEMV_EPI_ADD;
       o.y = m->sp_x;
       o.ldy = c.dim;
-      if ((rc = span_gemm(m, o))) return rc;
+      if ((rc = span_gemm(m, o, defer))) return rc;
 
-      HIP_TRY(rmsnorm_bf16_launch(m->sp_x, (const float*)L.ffn_norm.ptr, c.rms_norm_eps, m->sp_xb, xb_lo, cn, c.dim,
-                                  st));
+      HIP_TRY(add_rmsnorm_bf16_launch(m->sp_x, m->sp_part, pending, (const float*)L.ffn_norm.ptr, c.rms_norm_eps,
+                                      m->sp_xb, xb_lo, cn, c.dim, st));
+      pending = 0;
       GemmArgs gu;
       memset(&gu, 0, sizeof(gu));
       gu.qtype = CHATNET_GGML_Q4_0;
@@ -956,7 +965,8 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position, SpanM
       d.epi = GEMV_EPI_ADD;
       d.y = m->sp_x;
       d.ldy = c.dim;
-      if ((rc = span_gemm(m, d))) return rc;
+      // the last layer's residual add completes here (the LM head reads x)
+      if ((rc = span_gemm(m, d, l + 1 < c.n_layers ? defer : nullptr))) return rc;
     }
     last_rows = cn;
   }

@@ -505,34 +505,76 @@ __global__ __launch_bounds__(CN_BLOCK) void to_bf16_kernel(const float* __restri
 }
 
 // RMSNorm of each row (TensorMath.RmsNorm, TensorMath.cs:97-165) written as
-// bf16 for the next GEMM: xb[r] = bf16((x[r] * rms_r) * g).  One workgroup per row.
-__global__ __launch_bounds__(CN_BLOCK) void rmsnorm_bf16_kernel(const float* __restrict__ x,
-                                                               const float* __restrict__ g, float eps,
-                                                               uint16_t* __restrict__ xb,
-                                                               uint16_t* __restrict__ xb_lo, int dim) {
+// bf16 for the next GEMM: xb[r] = bf16((x[r] * rms_r) * g), with xb_lo the low
+// parts.  One workgroup per row, the row held in registers between the sum of
+// squares and the scaling (one pass over memory).  With `part` (splits > 0)
+// the row is first completed as a residual add of the preceding GEMM's K-split
+// partials [splits][rows][dim], summed in split order exactly as
+// gemm_reduce_kernel does (x += ((0 + p0) + p1) + ...), and written back to x.
+template <int V, int SPL>
+__global__ __launch_bounds__(CN_BLOCK) void add_rmsnorm_bf16_kernel(float* __restrict__ x,
+                                                                   const float* __restrict__ part, int splits,
+                                                                   const float* __restrict__ g, float eps,
+                                                                   uint16_t* __restrict__ xb,
+                                                                   uint16_t* __restrict__ xb_lo, int rows, int dim) {
   __shared__ float red[4];
-  const float* xr = x + (size_t)blockIdx.x * dim;
-  uint16_t* o = xb + (size_t)blockIdx.x * dim;
-  float ss = 0.f;
-  for (int i = threadIdx.x * 4; i < dim; i += CN_BLOCK * 4) {
-    const float4 v = *reinterpret_cast<const float4*>(xr + i);
-    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  const size_t row = blockIdx.x;
+  float* xr = x + row * dim;
+  f32x4 v[V];
+#pragma unroll
+  for (int j = 0; j < V; j++) {
+    const int i = (threadIdx.x + CN_BLOCK * j) * 4;
+    v[j] = i < dim ? *reinterpret_cast<const f32x4*>(xr + i) : f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  if constexpr (SPL > 0) {
+    // every partial's loads issued before the first add (SPL >= splits;
+    // slots past splits are not read)
+    f32x4 pv[SPL][V];
+#pragma unroll
+    for (int k = 0; k < SPL; k++) {
+      const float* pr = part + ((size_t)(k < splits ? k : 0) * rows + row) * dim;
+#pragma unroll
+      for (int j = 0; j < V; j++) {
+        const int i = (threadIdx.x + CN_BLOCK * j) * 4;
+        pv[k][j] = (i < dim && k < splits) ? *reinterpret_cast<const f32x4*>(pr + i) : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+    f32x4 sum[V];
+#pragma unroll
+    for (int j = 0; j < V; j++) sum[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < SPL; k++)
+#pragma unroll
+      for (int j = 0; j < V; j++)
+        if (k < splits) sum[j] += pv[k][j];
+#pragma unroll
+    for (int j = 0; j < V; j++) {
+      const int i = (threadIdx.x + CN_BLOCK * j) * 4;
+      v[j] = v[j] + sum[j];
+      if (i < dim) *reinterpret_cast<f32x4*>(xr + i) = v[j];
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < V; j++) ss += v[j][0] * v[j][0] + v[j][1] * v[j][1] + v[j][2] * v[j][2] + v[j][3] * v[j][3];
   ss = cn_block_sum(ss, red);
   const float rms = 1.0f / sqrtf(ss / (float)dim + eps);
-  for (int i = threadIdx.x * 4; i < dim; i += CN_BLOCK * 4) {
-    const float4 v = *reinterpret_cast<const float4*>(xr + i);
+  uint16_t* o = xb + row * dim;
+#pragma unroll
+  for (int j = 0; j < V; j++) {
+    const int i = (threadIdx.x + CN_BLOCK * j) * 4;
+    if (i >= dim) continue;
     const float4 w = *reinterpret_cast<const float4*>(g + i);
-    const float y0 = v.x * rms * w.x, y1 = v.y * rms * w.y, y2 = v.z * rms * w.z, y3 = v.w * rms * w.w;
+    const float y0 = v[j][0] * rms * w.x, y1 = v[j][1] * rms * w.y, y2 = v[j][2] * rms * w.z, y3 = v[j][3] * rms * w.w;
     if (xb_lo) {
-      uint16_t h[4], l[4];
-      split_bf16(y0, h[0], l[0]);
-      split_bf16(y1, h[1], l[1]);
-      split_bf16(y2, h[2], l[2]);
-      split_bf16(y3, h[3], l[3]);
-      *reinterpret_cast<uint2*>(o + i) = make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
-      *reinterpret_cast<uint2*>(xb_lo + (size_t)blockIdx.x * dim + i) =
-          make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
+      uint16_t hh[4], ll[4];
+      split_bf16(y0, hh[0], ll[0]);
+      split_bf16(y1, hh[1], ll[1]);
+      split_bf16(y2, hh[2], ll[2]);
+      split_bf16(y3, hh[3], ll[3]);
+      *reinterpret_cast<uint2*>(o + i) = make_uint2(hh[0] | ((uint32_t)hh[1] << 16), hh[2] | ((uint32_t)hh[3] << 16));
+      *reinterpret_cast<uint2*>(xb_lo + row * dim + i) =
+          make_uint2(ll[0] | ((uint32_t)ll[1] << 16), ll[2] | ((uint32_t)ll[3] << 16));
     } else {
       *reinterpret_cast<uint2*>(o + i) = make_uint2(pack2_bf16(y0, y1), pack2_bf16(y2, y3));
     }
@@ -735,7 +777,7 @@ size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool precise, bool
   return s.splits > 1 ? (size_t)s.splits * N * M * sizeof(float) : 0;
 }
 
-hipError_t gemm_launch(const GemmArgs& a_in, int num_cus, hipStream_t st) {
+hipError_t gemm_launch(const GemmArgs& a_in, int num_cus, hipStream_t st, int* splits_left) {
   const bool k_ok = a_in.packed ? (a_in.K > 0 && a_in.K % 64 == 0) : gemm_supports(a_in.qtype, a_in.K);
   if (!k_ok || a_in.M <= 0 || a_in.N <= 0) return hipErrorInvalidValue;
   const bool precise = a_in.precise != 0;
@@ -747,7 +789,12 @@ hipError_t gemm_launch(const GemmArgs& a_in, int num_cus, hipStream_t st) {
   const long long grid = (long long)((a.M + 127) / 128) * ((a.N + 32 * s.tn - 1) / (32 * s.tn)) * s.splits;
   if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
   hipError_t e = precise ? launch_fmt<true>(a, s.tn, (int)grid, st) : launch_fmt<false>(a, s.tn, (int)grid, st);
+  if (splits_left) *splits_left = 0;
   if (e != hipSuccess || s.splits == 1) return e;
+  if (splits_left) {  // the caller folds the partials into its next kernel
+    *splits_left = s.splits;
+    return hipSuccess;
+  }
   const long long work = (long long)((a.M + 3) / 4) * a.N;
   hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((work + CN_BLOCK - 1) / CN_BLOCK)), dim3(CN_BLOCK), 0, st, a);
   return hipGetLastError();
@@ -760,9 +807,39 @@ hipError_t to_bf16_launch(const float* x, uint16_t* xb, size_t n, hipStream_t st
   return hipGetLastError();
 }
 
+template <int V>
+void add_rmsnorm_v(float* x, const float* part, int splits, const float* g, float eps, uint16_t* xb, uint16_t* xb_lo,
+                   int rows, int dim, hipStream_t st) {
+  const dim3 grid(rows), block(CN_BLOCK);
+  if (V > 4 || splits <= 0) {  // wide rows: the norm alone (no partials folded)
+    hipLaunchKernelGGL((add_rmsnorm_bf16_kernel<V, 0>), grid, block, 0, st, x, part, 0, g, eps, xb, xb_lo, rows, dim);
+    return;
+  }
+  if constexpr (V <= 4) {
+  if (splits <= 0) hipLaunchKernelGGL((add_rmsnorm_bf16_kernel<V, 0>), grid, block, 0, st, x, part, 0, g, eps, xb, xb_lo, rows, dim);
+  else if (splits <= 2) hipLaunchKernelGGL((add_rmsnorm_bf16_kernel<V, 2>), grid, block, 0, st, x, part, splits, g, eps, xb, xb_lo, rows, dim);
+  else if (splits <= 4) hipLaunchKernelGGL((add_rmsnorm_bf16_kernel<V, 4>), grid, block, 0, st, x, part, splits, g, eps, xb, xb_lo, rows, dim);
+  else if (splits <= 8) hipLaunchKernelGGL((add_rmsnorm_bf16_kernel<V, 8>), grid, block, 0, st, x, part, splits, g, eps, xb, xb_lo, rows, dim);
+  else hipLaunchKernelGGL((add_rmsnorm_bf16_kernel<V, 16>), grid, block, 0, st, x, part, splits, g, eps, xb, xb_lo, rows, dim);
+  }
+}
+
+hipError_t add_rmsnorm_bf16_launch(float* x, const float* part, int splits, const float* g, float eps, uint16_t* xb,
+                                   uint16_t* xb_lo, int rows, int dim, hipStream_t st) {
+  if (dim % 4 || dim <= 0 || rows <= 0 || splits > 16 || (splits > 0 && !part)) return hipErrorInvalidValue;
+  const int v = (dim + 4 * CN_BLOCK - 1) / (4 * CN_BLOCK);  // float4 per thread
+  // at most 4 float4 per thread when partials are folded (the register budget of
+  // 16 splits x 4 float4), 16 for the norm alone
+  if (splits > 0 && v > 4) return hipErrorInvalidValue;
+  if (v > 16) return hipErrorInvalidValue;
+  if (v <= 2) add_rmsnorm_v<2>(x, part, splits, g, eps, xb, xb_lo, rows, dim, st);
+  else if (v <= 4) add_rmsnorm_v<4>(x, part, splits, g, eps, xb, xb_lo, rows, dim, st);
+  else if (v <= 8) add_rmsnorm_v<8>(x, part, 0, g, eps, xb, xb_lo, rows, dim, st);
+  else add_rmsnorm_v<16>(x, part, 0, g, eps, xb, xb_lo, rows, dim, st);
+  return hipGetLastError();
+}
+
 hipError_t rmsnorm_bf16_launch(const float* x, const float* g, float eps, uint16_t* xb, uint16_t* xb_lo, int rows,
                                int dim, hipStream_t st) {
-  if (dim % 4) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(rmsnorm_bf16_kernel, dim3(rows), dim3(CN_BLOCK), 0, st, x, g, eps, xb, xb_lo, dim);
-  return hipGetLastError();
+  return add_rmsnorm_bf16_launch(const_cast<float*>(x), nullptr, 0, g, eps, xb, xb_lo, rows, dim, st);
 }

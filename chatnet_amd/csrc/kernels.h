@@ -88,11 +88,20 @@ bool gemm_pack_supports(int qtype, int K);
 size_t gemm_pack_bytes(int M, int K);
 hipError_t gemm_pack_launch(int qtype, const void* w, int M, int K, void* dst, hipStream_t st);
 size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool precise, bool packed);
-hipError_t gemm_launch(const GemmArgs& a, int num_cus, hipStream_t st);
+// With splits_left, a launch whose K is split leaves its partial tiles in
+// a.part ([splits][N][M]) unreduced and reports the split count there (0 when
+// the epilogue ran): the caller folds them into its next kernel
+// (add_rmsnorm_bf16_launch for a residual add).
+hipError_t gemm_launch(const GemmArgs& a, int num_cus, hipStream_t st, int* splits_left = nullptr);
 hipError_t to_bf16_launch(const float* x, uint16_t* xb, size_t n, hipStream_t st);
 // xb = bf16(RMSNorm(x) * g) per row; with xb_lo also the low parts.
 hipError_t rmsnorm_bf16_launch(const float* x, const float* g, float eps, uint16_t* xb, uint16_t* xb_lo, int rows,
                                int dim, hipStream_t st);
+// x[r] += the K-split partials part[0..splits)[r] (summed as the GEMM's reduce
+// does), then xb / xb_lo = RMSNorm(x[r]) * g as rmsnorm_bf16_launch; splits 0:
+// the norm alone.  dim <= 16384, and dim <= 4096 with splits (at most 16).
+hipError_t add_rmsnorm_bf16_launch(float* x, const float* part, int splits, const float* g, float eps, uint16_t* xb,
+                                   uint16_t* xb_lo, int rows, int dim, hipStream_t st);
 
 // Span kernels (prefill.hip).  qkv is [n][ld] fp32 with q | k | v columns.
 struct RopeKvArgs {
@@ -103,6 +112,11 @@ struct RopeKvArgs {
   void* vcache;
   int kv_f16;
   const float* bias;  // optional [dim | kv_dim | kv_dim] added to q | k | v before RoPE
+  // optional: the QKV GEMM's unreduced K-split partials [splits][n][ld]
+  // (splits <= 16), read instead of qkv; q is written back to qkv either way
+  const float* part;
+  int splits;
+  int n;  // set by rope_kv_launch
 };
 hipError_t rope_kv_launch(const RopeKvArgs& a, int n, hipStream_t st);
 // Fills tab[p][j] = (cos, sin) of theta = p * exp(2j * dim_inv * neg_log_base),

@@ -33,6 +33,30 @@ __device__ __forceinline__ void rope_pair(float& x0, float& x1, float2 cs) {
 // One thread per (token, pair): q pairs rotated in place, k pairs rotated and
 // stored at cache row p0+t, v pairs copied there (LlamaModel.cs:137-153); with
 // a bias, q/k/v get it added first (QwenModel.cs:104-125).
+// Pair i of row t: from the row itself, or (SPL > 0) as the sum in split
+// order of the QKV GEMM's K-split partials [splits][n][ld], exactly as the
+// GEMM's reduce would have stored it (((0 + p0) + p1) + ...).
+template <int SPL>
+__device__ __forceinline__ float2 qkv_pair(const RopeKvArgs& a, int t, int col) {
+  if constexpr (SPL == 0) {
+    return *reinterpret_cast<const float2*>(a.qkv + (size_t)t * a.ld + col);
+  } else {
+    float2 pv[SPL];
+#pragma unroll
+    for (int k = 0; k < SPL; k++)
+      pv[k] = *reinterpret_cast<const float2*>(a.part + ((size_t)(k < a.splits ? k : 0) * a.n + t) * a.ld + col);
+    float2 s = make_float2(0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < SPL; k++)
+      if (k < a.splits) {
+        s.x += pv[k].x;
+        s.y += pv[k].y;
+      }
+    return s;
+  }
+}
+
+template <int SPL>
 __global__ __launch_bounds__(CN_BLOCK) void rope_kv_kernel(RopeKvArgs a) {
   const int t = blockIdx.y;
   const int pairs_q = a.dim / 2, pairs_kv = a.kv_dim / 2;
@@ -44,7 +68,7 @@ __global__ __launch_bounds__(CN_BLOCK) void rope_kv_kernel(RopeKvArgs a) {
   if (a.bias) b = reinterpret_cast<const float2*>(a.bias)[i];
   if (i < pairs_q) {
     float2* p = reinterpret_cast<float2*>(row) + i;
-    float2 v = *p;
+    float2 v = qkv_pair<SPL>(a, t, 2 * i);
     if (a.bias) { v.x += b.x; v.y += b.y; }
     rope_pair(v.x, v.y, a.rope[(size_t)pos * (a.head_dim / 2) + i % (a.head_dim / 2)]);
     *p = v;
@@ -52,7 +76,7 @@ __global__ __launch_bounds__(CN_BLOCK) void rope_kv_kernel(RopeKvArgs a) {
   }
   const bool is_k = i < pairs_q + pairs_kv;
   const int j = is_k ? i - pairs_q : i - pairs_q - pairs_kv;  // pair index within k or v
-  float2 v = reinterpret_cast<const float2*>(row + a.dim + (is_k ? 0 : a.kv_dim))[j];
+  float2 v = qkv_pair<SPL>(a, t, a.dim + (is_k ? 0 : a.kv_dim) + 2 * j);
   if (a.bias) { v.x += b.x; v.y += b.y; }
   if (is_k) rope_pair(v.x, v.y, a.rope[(size_t)pos * (a.head_dim / 2) + j % (a.head_dim / 2)]);
   const size_t off = (size_t)pos * a.kv_dim + 2 * j;
@@ -425,6 +449,17 @@ hipError_t rope_table_launch(float2* tab, int ctx, int head_dim, float dim_inv, 
 hipError_t rope_kv_launch(const RopeKvArgs& a, int n, hipStream_t st) {
   if (n <= 0 || (a.dim & 1) || (a.kv_dim & 1)) return hipErrorInvalidValue;
   const int pairs = a.dim / 2 + a.kv_dim;
-  hipLaunchKernelGGL(rope_kv_kernel, dim3((pairs + CN_BLOCK - 1) / CN_BLOCK, n), dim3(CN_BLOCK), 0, st, a);
+  const dim3 grid((pairs + CN_BLOCK - 1) / CN_BLOCK, n);
+  if (a.splits > 16 || (a.splits > 0 && !a.part)) return hipErrorInvalidValue;
+  if (a.splits > 0) {
+    RopeKvArgs b = a;
+    b.n = n;
+    if (a.splits <= 2) hipLaunchKernelGGL(rope_kv_kernel<2>, grid, dim3(CN_BLOCK), 0, st, b);
+    else if (a.splits <= 4) hipLaunchKernelGGL(rope_kv_kernel<4>, grid, dim3(CN_BLOCK), 0, st, b);
+    else if (a.splits <= 8) hipLaunchKernelGGL(rope_kv_kernel<8>, grid, dim3(CN_BLOCK), 0, st, b);
+    else hipLaunchKernelGGL(rope_kv_kernel<16>, grid, dim3(CN_BLOCK), 0, st, b);
+  } else {
+    hipLaunchKernelGGL(rope_kv_kernel<0>, grid, dim3(CN_BLOCK), 0, st, a);
+  }
   return hipGetLastError();
 }
