@@ -782,6 +782,9 @@ hipError_t gemm_launch(const GemmArgs& a_in, int num_cus, hipStream_t st, int* s
   if (!k_ok || a_in.M <= 0 || a_in.N <= 0) return hipErrorInvalidValue;
   const bool precise = a_in.precise != 0;
   if (precise && !a_in.xb_lo) return hipErrorInvalidValue;
+  // partials can be left only for a store or a residual add (the folding
+  // kernels apply no other epilogue)
+  if (splits_left && a_in.epi != GEMV_EPI_STORE && a_in.epi != GEMV_EPI_ADD) return hipErrorInvalidValue;
   const GemmShape s = pick_gemm(a_in.M, a_in.N, a_in.K, num_cus, precise, a_in.packed != 0);
   GemmArgs a = a_in;
   a.splits = s.splits;
