@@ -56,6 +56,28 @@ __device__ __forceinline__ float cn_ubyte(uint32_t v) {
   return (float)((v >> (8 * B)) & 0xFFu);
 }
 
+// Inputs of the exact-weight span GEMM (x of every projection in a span) are
+// two fp16 planes, hi = fp16(x) and lo = fp16(x - hi) (about 22 significant
+// bits while |x| stays in fp16's normal range), with each 32-element block
+// stored in the order its Q4_0 weight dwords deliver the elements: groups of
+// four, G0 G4 G1 G5 G2 G6 G3 G7 (group g = elements 4g..4g+3).  Position of
+// element k in a row (every row length is a multiple of 32):
+__host__ __device__ __forceinline__ int cn_span_pos(int k) {
+  const int g = (k >> 2) & 7;
+  return (k & ~31) + 4 * (g < 4 ? 2 * g : 2 * g - 7) + (k & 3);
+}
+
+typedef _Float16 cn_half2 __attribute__((ext_vector_type(2)));
+typedef float cn_float2 __attribute__((ext_vector_type(2)));
+
+// (a, b) as packed fp16 high parts and packed fp16 low parts.
+__device__ __forceinline__ void cn_split_f16x2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  const cn_half2 h = __builtin_convertvector((cn_float2){a, b}, cn_half2);
+  const cn_half2 l = __builtin_convertvector((cn_float2){a - (float)h[0], b - (float)h[1]}, cn_half2);
+  hi = __builtin_bit_cast(uint32_t, h);
+  lo = __builtin_bit_cast(uint32_t, l);
+}
+
 __device__ __forceinline__ float cn_wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, CN_WAVE);

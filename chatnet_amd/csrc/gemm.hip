@@ -7,16 +7,18 @@
 //
 // W is read either as raw Q4_0 blocks or as packed units (gemm_pack_kernel:
 // any of Q4_0, Q8_0, Q4_K, Q5_K, Q6_K re-encoded once as u8 codes with an fp32
-// scale and offset per 16 weights); x arrives as bf16 [N][K] (one
-// plane, or hi + lo planes for the exact-weight variant) from the producer
-// kernel (conversion, RMSNorm, attention or the SwiGLU epilogue).  W bytes
-// and x tiles stream through an LDS ring by direct global->LDS loads; each
-// wave dequantizes its W rows into v_mfma_f32_32x32x16_bf16 operands in
-// registers and accumulates in fp32.  When the tile grid leaves the chip
+// scale and offset per 16 weights); x arrives from the producer kernel
+// (conversion, RMSNorm, attention or the SwiGLU epilogue) either as one bf16
+// plane [N][K] (chatnet_matmul) or, for the exact-weight variant the spans
+// run, as fp16 hi + lo planes in the cn_span_pos order.  W bytes and x tiles
+// stream through an LDS ring by direct global->LDS loads; each wave
+// dequantizes its W rows into v_mfma_f32_32x32x16_bf16 (one plane) or
+// v_mfma_f32_32x32x16_f16 (exact-weight) operands in registers and
+// accumulates in fp32.  When the tile grid leaves the chip
 // under-filled the K range is split and gemm_reduce_kernel sums the partial
 // tiles and applies the epilogue.  Epilogues: STORE y = acc, ADD y += acc
 // (residual), SWIGLU (rows interleave gate/up; h = silu(gate)*up is written
-// as bf16 (hi + lo) for the next GEMM).
+// in the next GEMM's input format).
 #include "device_common.h"
 #include "kernels.h"
 
@@ -55,24 +57,17 @@ __device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
   return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
-// v as bf16 hi + bf16 lo (hi + lo carries ~16 significant bits of v).
-__device__ __forceinline__ void split_bf16(float v, uint16_t& hi, uint16_t& lo) {
-  const __bf16 h = (__bf16)v;
-  const __bf16 l = (__bf16)(v - (float)h);
-  hi = __builtin_bit_cast(uint16_t, h);
-  lo = __builtin_bit_cast(uint16_t, l);
-}
-
-// h[n][j] = silu(gate) * up, as bf16 (and its low part when hb_lo is set).
+// h[n][j] = silu(gate) * up: bf16 in natural order (one plane), or fp16 hi +
+// lo planes in the span order (cn_span_pos) when hb_lo is set.
 __device__ __forceinline__ void write_h(const GemmArgs& a, int n, int j, float v) {
-  const size_t i = (size_t)n * a.ldh + j;
   if (a.hb_lo) {
-    uint16_t hi, lo;
-    split_bf16(v, hi, lo);
-    a.hb[i] = hi;
-    a.hb_lo[i] = lo;
+    const size_t i = (size_t)n * a.ldh + cn_span_pos(j);
+    uint32_t hi, lo;
+    cn_split_f16x2(v, 0.f, hi, lo);
+    a.hb[i] = (uint16_t)hi;
+    a.hb_lo[i] = (uint16_t)lo;
   } else {
-    a.hb[i] = __builtin_bit_cast(uint16_t, (__bf16)v);
+    a.hb[(size_t)n * a.ldh + j] = __builtin_bit_cast(uint16_t, (__bf16)v);
   }
 }
 
@@ -82,12 +77,20 @@ __device__ __forceinline__ void write_out4(const GemmArgs& a, int epi, int n, in
   const bool full = (m + 3 < a.M) && ((a.ldy & 3) == 0);
   if (epi == GEMV_EPI_SWIGLU) {
     // rows (m, m+1) and (m+2, m+3) are (gate, up) pairs of h[m/2], h[m/2+1]
-    if (m + 3 < a.M && !a.hb_lo) {
-      uint16_t* h = a.hb + (size_t)n * a.ldh + (m >> 1);
-      *reinterpret_cast<uint32_t*>(h) = pack2_bf16(silu_mul(v[0], v[1]), silu_mul(v[2], v[3]));
+    // (m/2 even: the two stay adjacent in the span order too)
+    if (m + 3 < a.M) {
+      const float h0 = silu_mul(v[0], v[1]), h1 = silu_mul(v[2], v[3]);
+      if (a.hb_lo) {
+        const size_t i = (size_t)n * a.ldh + cn_span_pos(m >> 1);
+        uint32_t hi, lo;
+        cn_split_f16x2(h0, h1, hi, lo);
+        *reinterpret_cast<uint32_t*>(a.hb + i) = hi;
+        *reinterpret_cast<uint32_t*>(a.hb_lo + i) = lo;
+      } else {
+        *reinterpret_cast<uint32_t*>(a.hb + (size_t)n * a.ldh + (m >> 1)) = pack2_bf16(h0, h1);
+      }
     } else {
       write_h(a, n, m >> 1, silu_mul(v[0], v[1]));
-      if (m + 3 < a.M) write_h(a, n, (m >> 1) + 1, silu_mul(v[2], v[3]));
     }
     return;
   }
@@ -102,13 +105,19 @@ __device__ __forceinline__ void write_out4(const GemmArgs& a, int epi, int n, in
 }
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-// 16 weights d*(q-8) of one lane as bf16: 8 per MFMA step (low nibbles of
-// q0/q1 for the first, high nibbles for the second).  w = d*(q-8) is exact in
-// fp32 (at most 14 significant bits); `hi` is bf16(w) and, when `precise`,
-// `lo` = bf16(w - hi) makes hi + lo == w exactly.
-__device__ __forceinline__ void dequant_w16(uint32_t q0, uint32_t q1, float d, bool precise, bf16x8 (&hi)[2],
-                                            bf16x8 (&lo)[2]) {
+__device__ __forceinline__ f32x16 mma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mma32(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// One-plane kernel (chatnet_matmul, bf16 x): 16 weights d*(q-8) of one lane as
+// bf16, 8 per MFMA step (low nibbles of q0/q1 for the first, high nibbles for
+// the second).
+__device__ __forceinline__ void dequant_w16(uint32_t q0, uint32_t q1, float d, bf16x8 (&hi)[2]) {
   const float nd = -8.0f * d;
   uint32_t n[2][2] = {{q0 & 0x0F0F0F0Fu, q1 & 0x0F0F0F0Fu}, {(q0 >> 4) & 0x0F0F0F0Fu, (q1 >> 4) & 0x0F0F0F0Fu}};
   // Opaque to the optimizer: without this it folds the masks into one
@@ -116,43 +125,80 @@ __device__ __forceinline__ void dequant_w16(uint32_t q0, uint32_t q1, float d, b
   asm volatile("" : "+v"(n[0][0]), "+v"(n[0][1]), "+v"(n[1][0]), "+v"(n[1][1]));
 #pragma unroll
   for (int s = 0; s < 2; s++) {
-    float w[8];
-    w[0] = fmaf(cn_ubyte<0>(n[s][0]), d, nd);
-    w[1] = fmaf(cn_ubyte<1>(n[s][0]), d, nd);
-    w[2] = fmaf(cn_ubyte<2>(n[s][0]), d, nd);
-    w[3] = fmaf(cn_ubyte<3>(n[s][0]), d, nd);
-    w[4] = fmaf(cn_ubyte<0>(n[s][1]), d, nd);
-    w[5] = fmaf(cn_ubyte<1>(n[s][1]), d, nd);
-    w[6] = fmaf(cn_ubyte<2>(n[s][1]), d, nd);
-    w[7] = fmaf(cn_ubyte<3>(n[s][1]), d, nd);
-#pragma unroll
-    for (int t = 0; t < 8; t++) {
-      const __bf16 b = (__bf16)w[t];
-      hi[s][t] = b;
-      if (precise) lo[s][t] = (__bf16)(w[t] - (float)b);
-    }
+    hi[s][0] = (__bf16)fmaf(cn_ubyte<0>(n[s][0]), d, nd);
+    hi[s][1] = (__bf16)fmaf(cn_ubyte<1>(n[s][0]), d, nd);
+    hi[s][2] = (__bf16)fmaf(cn_ubyte<2>(n[s][0]), d, nd);
+    hi[s][3] = (__bf16)fmaf(cn_ubyte<3>(n[s][0]), d, nd);
+    hi[s][4] = (__bf16)fmaf(cn_ubyte<0>(n[s][1]), d, nd);
+    hi[s][5] = (__bf16)fmaf(cn_ubyte<1>(n[s][1]), d, nd);
+    hi[s][6] = (__bf16)fmaf(cn_ubyte<2>(n[s][1]), d, nd);
+    hi[s][7] = (__bf16)fmaf(cn_ubyte<3>(n[s][1]), d, nd);
   }
 }
 
-// 8 packed weights fmaf(code, sc, of) as bf16 (hi, and lo = bf16(w - hi) when
-// `precise`); the codes are the bytes of c0 then c1.
-__device__ __forceinline__ void dequant_u8x8(uint32_t c0, uint32_t c1, float sc, float of, bool precise, bf16x8& hi,
-                                             bf16x8& lo) {
+// One-plane kernel, packed units: 8 weights fmaf(code, sc, of) as bf16; the
+// codes are the bytes of c0 then c1.
+__device__ __forceinline__ void dequant_u8x8(uint32_t c0, uint32_t c1, float sc, float of, bf16x8& hi) {
+  hi[0] = (__bf16)fmaf(cn_ubyte<0>(c0), sc, of);
+  hi[1] = (__bf16)fmaf(cn_ubyte<1>(c0), sc, of);
+  hi[2] = (__bf16)fmaf(cn_ubyte<2>(c0), sc, of);
+  hi[3] = (__bf16)fmaf(cn_ubyte<3>(c0), sc, of);
+  hi[4] = (__bf16)fmaf(cn_ubyte<0>(c1), sc, of);
+  hi[5] = (__bf16)fmaf(cn_ubyte<1>(c1), sc, of);
+  hi[6] = (__bf16)fmaf(cn_ubyte<2>(c1), sc, of);
+  hi[7] = (__bf16)fmaf(cn_ubyte<3>(c1), sc, of);
+}
+
+// Exact-weight (span) kernel, raw Q4_0, fp16 operands.  One MFMA step of a
+// lane takes one qs dword of its block; wp holds its bytes in the order
+// b0 b2 b1 b3, so that the elements (4s, 4s+1) sit in the low nibbles at bits
+// 0-3 / 16-19, (4s+2, 4s+3) at bits 8-11 / 24-27, (16+4s, 16+4s+1) in the
+// high nibbles at bits 4-7 / 20-23 and (16+4s+2, 16+4s+3) at 12-15 / 28-31:
+// the element order cn_span_pos stores x in.  A pair (q_a, q_b) becomes two
+// fp16 halves 0x6400 | q = 1024 + q (or 0x6400 | q << 4 = 1024 + 16q), and a
+// packed fp16 add (fma) turns each into q - 8 exactly.  The weight d*(q-8)
+// then splits exactly as Wa = (q-8)*dh + Wb = (q-8)*dl, dh = d with its three
+// low mantissa bits cleared, dl = d - dh: (q-8) has at most 3 significant
+// bits, dh at most 8 and dl at most 3, so both products are fp16 values for
+// |d| < 4096 (fp16 subnormals included) and need no rounding.  `magic` holds
+// 0x64006400 in a register (v_and_or_b32 takes no two literals).
+__device__ __forceinline__ void dequant_q4_f16(uint32_t wp, uint32_t magic, cn_half2 dh, cn_half2 dl, f16x8& wa,
+                                               f16x8& wb) {
+  const uint32_t u = wp >> 8;
+  const cn_half2 t0 = __builtin_bit_cast(cn_half2, (wp & 0x000F000Fu) | magic);
+  const cn_half2 t1 = __builtin_bit_cast(cn_half2, (u & 0x000F000Fu) | magic);
+  const cn_half2 t2 = __builtin_bit_cast(cn_half2, (wp & 0x00F000F0u) | magic);
+  const cn_half2 t3 = __builtin_bit_cast(cn_half2, (u & 0x00F000F0u) | magic);
+  const cn_half2 m1032 = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+  const cn_half2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const cn_half2 m72 = {(_Float16)-72.0f, (_Float16)-72.0f};
+  const cn_half2 p0 = t0 + m1032, p1 = t1 + m1032;
+  const cn_half2 p2 = t2 * s16 + m72, p3 = t3 * s16 + m72;
+  const cn_half2 a0 = p0 * dh, a1 = p1 * dh, a2 = p2 * dh, a3 = p3 * dh;
+  const cn_half2 b0 = p0 * dl, b1 = p1 * dl, b2 = p2 * dl, b3 = p3 * dl;
+  wa = (f16x8){a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+  wb = (f16x8){b0[0], b0[1], b1[0], b1[1], b2[0], b2[1], b3[0], b3[1]};
+}
+
+// Exact-weight kernel, packed units: the 8 weights of one MFMA step, codes of
+// ca with (sc0, of0) then codes of cb with (sc1, of1), as fp16 hi + lo
+// (w = fmaf(code, sc, of) carries up to 24 bits; hi + lo keep ~22).
+__device__ __forceinline__ void dequant_u8_f16(uint32_t ca, uint32_t cb, float sc0, float of0, float sc1, float of1,
+                                               f16x8& wa, f16x8& wb) {
   float w[8];
-  w[0] = fmaf(cn_ubyte<0>(c0), sc, of);
-  w[1] = fmaf(cn_ubyte<1>(c0), sc, of);
-  w[2] = fmaf(cn_ubyte<2>(c0), sc, of);
-  w[3] = fmaf(cn_ubyte<3>(c0), sc, of);
-  w[4] = fmaf(cn_ubyte<0>(c1), sc, of);
-  w[5] = fmaf(cn_ubyte<1>(c1), sc, of);
-  w[6] = fmaf(cn_ubyte<2>(c1), sc, of);
-  w[7] = fmaf(cn_ubyte<3>(c1), sc, of);
+  w[0] = fmaf(cn_ubyte<0>(ca), sc0, of0);
+  w[1] = fmaf(cn_ubyte<1>(ca), sc0, of0);
+  w[2] = fmaf(cn_ubyte<2>(ca), sc0, of0);
+  w[3] = fmaf(cn_ubyte<3>(ca), sc0, of0);
+  w[4] = fmaf(cn_ubyte<0>(cb), sc1, of1);
+  w[5] = fmaf(cn_ubyte<1>(cb), sc1, of1);
+  w[6] = fmaf(cn_ubyte<2>(cb), sc1, of1);
+  w[7] = fmaf(cn_ubyte<3>(cb), sc1, of1);
+  uint32_t hi[4], lo[4];
 #pragma unroll
-  for (int t = 0; t < 8; t++) {
-    const __bf16 b = (__bf16)w[t];
-    hi[t] = b;
-    if (precise) lo[t] = (__bf16)(w[t] - (float)b);
-  }
+  for (int t = 0; t < 4; t++) cn_split_f16x2(w[2 * t], w[2 * t + 1], hi[t], lo[t]);
+  wa = __builtin_bit_cast(f16x8, make_uint4(hi[0], hi[1], hi[2], hi[3]));
+  wb = __builtin_bit_cast(f16x8, make_uint4(lo[0], lo[1], lo[2], lo[3]));
 }
 
 // ---------------------------------------------------------------------------
@@ -163,20 +209,24 @@ __device__ __forceinline__ void dequant_u8x8(uint32_t c0, uint32_t c1, float sc,
 // (s_waitcnt vmcnt(n) + a bare s_barrier), not for the whole queue.
 //
 // Per chunk (one 36-byte Q4_0 unit per W row) lane half h of row li takes
-// block h of the unit: its 8 k of MFMA step s are the low (s < 2) or high
-// nibbles of qs[8(s&1) .. +7], i.e. k = 32h + 8s .. +7 of the chunk.  The
-// x fragment of the same lane reads exactly those k, so the K order inside a
-// chunk is permuted consistently for both operands.
+// block h of the unit, and the x fragment of the same lane reads the same 8 k
+// of every MFMA step, so the K order inside a chunk is permuted consistently
+// for both operands.  One-plane kernel (bf16, x in natural order): step s
+// takes the low (s < 2) or high nibbles of qs[8(s&1) .. +7], i.e. k = 32h +
+// 8s .. +7 of the chunk.  Exact-weight kernel (fp16, x in the cn_span_pos
+// order): step s takes qs dword s (dequant_q4_f16).  Packed units: step s
+// takes codes 32h + 8s .. +7 (one plane) or 32h + 4s .. +3 and 32h + 16 + 4s
+// .. +3 (exact-weight, the span order).
 // LDS layout per stage: x planes [BN rows][8 x 16 B] with the 16-byte chunk
 // of logical index c of row r stored at c ^ ((r >> 1) & 7) (reads of 32 rows
 // stay 2-way per bank), then W [BM rows][48 B] holding unit bytes [0,16),
 // [16,32) and [20,36).
 // A wave owns 32*TM W rows x 32*TN columns; the 4 waves stack along M and
-// share the x tile.  PRECISE (spans of the forward pass) runs three MFMAs per
-// step, Wh*xh + Wh*xl + Wl*xh, with W = Wh + Wl exact and x = xh + xl to
-// ~2^-17; the dropped Wl*xl term is below 2^-16 relative.  Output layout of a
-// 32x32 tile: lane l, accumulator v holds row 8*(v/4) + 4*(l/32) + v%4,
-// column l%32.
+// share the x tile.  PRECISE (spans of the forward pass) runs three fp16 MFMAs
+// per step, Wa*xh + Wa*xl + Wb*xh, with W = Wa + Wb exact (raw Q4_0; ~22 bits
+// for packed units) and x = xh + xl to ~2^-22; the dropped Wb*xl term is
+// below 2^-19 relative.  Output layout of a 32x32 tile: lane l, accumulator v
+// holds row 8*(v/4) + 4*(l/32) + v%4, column l%32.
 // ---------------------------------------------------------------------------
 // 16 bytes from global memory straight into LDS: lane i of the wave writes
 // lds_wave_base + 16*i (lds_wave_base must be the same for the whole wave).
@@ -216,12 +266,25 @@ struct PipeCfg {
   static_assert(XPW % 64 == 0, "x pieces per wave must fill whole instructions");
 };
 
+template <bool PRECISE>
+struct GemmOp;
+template <>
+struct GemmOp<false> {
+  typedef bf16x8 T;
+};
+template <>
+struct GemmOp<true> {
+  typedef f16x8 T;
+};
+
 template <bool PRECISE, int TM, int TN, int S, bool PK>
 __global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
   using C = PipeCfg<PRECISE, TM, TN, S, PK>;
+  using OP = typename GemmOp<PRECISE>::T;
   extern __shared__ __attribute__((aligned(16))) char lds[];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = lane >> 5, li = lane & 31;
 
   const int n_nt = (a.N + C::BN - 1) / C::BN;
@@ -314,32 +377,58 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
         w[4] = wb[4];
       }
     };
-    // Q4_0: half 0 gives steps 0 and 2 (low/high nibbles of qs[0..7]), half 1
-    // steps 1 and 3.  Packed: half 0 gives steps 0 and 1 (codes 0..15 of the
-    // lane, scale 2h), half 1 steps 2 and 3 (codes 16..31, scale 2h+1).
-    auto deq = [&](const uint32_t (&w)[WD], int half, bf16x8 (&fh)[4], bf16x8 (&fl)[4]) {
-      if constexpr (PK) {
-        const float sc = __uint_as_float(w[8 + half]), of = __uint_as_float(w[10 + half]);
+    // One-plane kernel.  Q4_0: half 0 gives steps 0 and 2 (low/high nibbles
+    // of qs[0..7]), half 1 steps 1 and 3.  Packed: half 0 gives steps 0 and
+    // 1 (codes 0..15 of the lane, scale 2h), half 1 steps 2 and 3 (codes
+    // 16..31, scale 2h+1).
+    auto deq_half = [&](const uint32_t (&w)[WD], int half, OP (&fh)[4]) {
+      if constexpr (!PRECISE) {
+        if constexpr (PK) {
+          const float sc = __uint_as_float(w[8 + half]), of = __uint_as_float(w[10 + half]);
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
-          bf16x8 th, tl;
-          dequant_u8x8(w[4 * half + 2 * t], w[4 * half + 2 * t + 1], sc, of, PRECISE, th, tl);
-          fh[2 * half + t] = th;
-          if constexpr (PRECISE) fl[2 * half + t] = tl;
+          for (int t = 0; t < 2; t++) dequant_u8x8(w[4 * half + 2 * t], w[4 * half + 2 * t + 1], sc, of, fh[2 * half + t]);
+        } else {
+          const uint32_t sh = h ? 0u : 2u;
+          const float d = cn_h2f(h ? (w[4] >> 16) : w[0]);
+          const uint32_t qa = __builtin_amdgcn_alignbyte(half ? w[3] : w[1], half ? w[2] : w[0], sh);
+          const uint32_t qb = __builtin_amdgcn_alignbyte(half ? w[4] : w[2], half ? w[3] : w[1], sh);
+          bf16x8 th[2];
+          dequant_w16(qa, qb, d, th);
+          fh[half] = th[0];
+          fh[half + 2] = th[1];
         }
-        return;
       }
-      const uint32_t sh = h ? 0u : 2u;
-      const float d = cn_h2f(h ? (w[4] >> 16) : w[0]);
-      const uint32_t qa = __builtin_amdgcn_alignbyte(half ? w[3] : w[1], half ? w[2] : w[0], sh);
-      const uint32_t qb = __builtin_amdgcn_alignbyte(half ? w[4] : w[2], half ? w[3] : w[1], sh);
-      bf16x8 th[2], tl[2];
-      dequant_w16(qa, qb, d, PRECISE, th, tl);
-      fh[half] = th[0];
-      fh[half + 2] = th[1];
+    };
+    // Exact-weight kernel: the (dh, dl) split of the lane's block scale
+    // (Q4_0), then step s of the chunk as Wa, Wb.  v_perm_b32 selectors take
+    // qs dword s of the lane's block (2 bytes into the unit for block A) as
+    // bytes b0 b2 b1 b3.
+    const uint32_t psel = h ? 0x03010200u : 0x05030402u;
+    uint32_t magic = 0x64006400u;
+    asm volatile("" : "+v"(magic));
+    struct Dsc {
+      cn_half2 dh, dl;
+    };
+    auto dsplit = [&](const uint32_t (&w)[WD]) {
+      Dsc r{};
+      if constexpr (PRECISE && !PK) {
+        const uint32_t d16 = h ? (w[4] >> 16) : (w[0] & 0xFFFFu);
+        const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)d16);
+        const _Float16 dh = __builtin_bit_cast(_Float16, (uint16_t)(d16 & 0xFFF8u));
+        const _Float16 dl = d - dh;
+        r.dh = (cn_half2){dh, dh};
+        r.dl = (cn_half2){dl, dl};
+      }
+      return r;
+    };
+    auto deq_step = [&](const uint32_t (&w)[WD], const Dsc& ds, int s, OP& fa, OP& fb) {
       if constexpr (PRECISE) {
-        fl[half] = tl[0];
-        fl[half + 2] = tl[1];
+        if constexpr (PK) {
+          dequant_u8_f16(w[s], w[4 + s], __uint_as_float(w[8]), __uint_as_float(w[10]), __uint_as_float(w[9]),
+                         __uint_as_float(w[11]), fa, fb);
+        } else {
+          dequant_q4_f16(__builtin_amdgcn_perm(w[s + 1], w[s], psel), magic, ds.dh, ds.dl, fa, fb);
+        }
       }
     };
     // Waits until stage t has landed, given that stages up to `issued` are in flight.
@@ -364,13 +453,19 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
       }
     wait_stage(c_begin, issued);
     wg_barrier();
-    bf16x8 wh[TM][4], wl[TM][4];
+    OP wa[TM][4], wb[TM][4];
 #pragma unroll
     for (int r = 0; r < TM; r++) {
       uint32_t w[WD];
       wraw(slot_of(c_begin), r, w);
-      deq(w, 0, wh[r], wl[r]);
-      deq(w, 1, wh[r], wl[r]);
+      if constexpr (PRECISE) {
+        const Dsc ds = dsplit(w);
+#pragma unroll
+        for (int s = 0; s < 4; s++) deq_step(w, ds, s, wa[r][s], wb[r][s]);
+      } else {
+        deq_half(w, 0, wa[r]);
+        deq_half(w, 1, wa[r]);
+      }
     }
 
     for (int c = c_begin; c < c_end; c++) {
@@ -386,20 +481,24 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
       // Unconditional (branch-free, so it interleaves with the MFMAs): on the
       // last chunk this reads a stale slot whose result is never used.
       uint32_t nw[TM][WD];
+      Dsc nds[TM];
 #pragma unroll
-      for (int r = 0; r < TM; r++) wraw(slot_of(c + 1), r, nw[r]);
-      bf16x8 nwh[TM][4], nwl[TM][4];
+      for (int r = 0; r < TM; r++) {
+        wraw(slot_of(c + 1), r, nw[r]);
+        nds[r] = dsplit(nw[r]);
+      }
+      OP nwa[TM][4], nwb[TM][4];
 
       const char* st = slot_of(c);
-      bf16x8 xh[2][TN], xl[2][TN];
+      OP xh[2][TN], xl[2][TN];
       auto load_x = [&](int s, int b) {
 #pragma unroll
         for (int cc = 0; cc < TN; cc++) {
           const int xrow = 32 * cc + li;
           const int phys = (4 * h + s) ^ ((xrow >> 1) & 7);
           const char* xp = st + xrow * 128 + phys * 16;
-          xh[b][cc] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(xp));
-          if constexpr (PRECISE) xl[b][cc] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(xp + C::XB));
+          xh[b][cc] = __builtin_bit_cast(OP, *reinterpret_cast<const uint4*>(xp));
+          if constexpr (PRECISE) xl[b][cc] = __builtin_bit_cast(OP, *reinterpret_cast<const uint4*>(xp + C::XB));
         }
       };
       load_x(0, 0);
@@ -411,32 +510,30 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
 #pragma unroll
         for (int cc = 0; cc < TN; cc++)
 #pragma unroll
-          for (int r = 0; r < TM; r++)
-            acc[r][cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wh[r][s], xh[s & 1][cc], acc[r][cc], 0, 0, 0);
+          for (int r = 0; r < TM; r++) acc[r][cc] = mma32(wa[r][s], xh[s & 1][cc], acc[r][cc]);
         if constexpr (PRECISE) {
 #pragma unroll
           for (int cc = 0; cc < TN; cc++)
 #pragma unroll
-            for (int r = 0; r < TM; r++)
-              acc[r][cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wh[r][s], xl[s & 1][cc], acc[r][cc], 0, 0, 0);
+            for (int r = 0; r < TM; r++) acc[r][cc] = mma32(wa[r][s], xl[s & 1][cc], acc[r][cc]);
 #pragma unroll
           for (int cc = 0; cc < TN; cc++)
 #pragma unroll
-            for (int r = 0; r < TM; r++)
-              acc[r][cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wl[r][s], xh[s & 1][cc], acc[r][cc], 0, 0, 0);
-        }
-        // the next chunk's W is dequantized while these MFMAs run
-        if (s == 0 || s == 2) {
+            for (int r = 0; r < TM; r++) acc[r][cc] = mma32(wb[r][s], xh[s & 1][cc], acc[r][cc]);
+          // the next chunk's step s is dequantized while these MFMAs run
 #pragma unroll
-          for (int r = 0; r < TM; r++) deq(nw[r], s >> 1, nwh[r], nwl[r]);
+          for (int r = 0; r < TM; r++) deq_step(nw[r], nds[r], s, nwa[r][s], nwb[r][s]);
+        } else if (s == 0 || s == 2) {
+#pragma unroll
+          for (int r = 0; r < TM; r++) deq_half(nw[r], s >> 1, nwa[r]);
         }
       }
 #pragma unroll
       for (int r = 0; r < TM; r++)
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-          wh[r][s] = nwh[r][s];
-          if constexpr (PRECISE) wl[r][s] = nwl[r][s];
+          wa[r][s] = nwa[r][s];
+          if constexpr (PRECISE) wb[r][s] = nwb[r][s];
         }
     }
   }
@@ -504,9 +601,9 @@ __global__ __launch_bounds__(CN_BLOCK) void to_bf16_kernel(const float* __restri
   }
 }
 
-// RMSNorm of each row (TensorMath.RmsNorm, TensorMath.cs:97-165) written as
-// bf16 for the next GEMM: xb[r] = bf16((x[r] * rms_r) * g), with xb_lo the low
-// parts.  One workgroup per row, the row held in registers between the sum of
+// RMSNorm of each row (TensorMath.RmsNorm, TensorMath.cs:97-165) written for
+// the next GEMM: xb[r] = bf16((x[r] * rms_r) * g) in natural order, or with
+// xb_lo the span GEMM's two fp16 planes in the cn_span_pos order.  One workgroup per row, the row held in registers between the sum of
 // squares and the scaling (one pass over memory).  With `part` (splits > 0)
 // the row is first completed as a residual add of the preceding GEMM's K-split
 // partials [splits][rows][dim], summed in split order exactly as
@@ -567,14 +664,13 @@ __global__ __launch_bounds__(CN_BLOCK) void add_rmsnorm_bf16_kernel(float* __res
     const float4 w = *reinterpret_cast<const float4*>(g + i);
     const float y0 = v[j][0] * rms * w.x, y1 = v[j][1] * rms * w.y, y2 = v[j][2] * rms * w.z, y3 = v[j][3] * rms * w.w;
     if (xb_lo) {
-      uint16_t hh[4], ll[4];
-      split_bf16(y0, hh[0], ll[0]);
-      split_bf16(y1, hh[1], ll[1]);
-      split_bf16(y2, hh[2], ll[2]);
-      split_bf16(y3, hh[3], ll[3]);
-      *reinterpret_cast<uint2*>(o + i) = make_uint2(hh[0] | ((uint32_t)hh[1] << 16), hh[2] | ((uint32_t)hh[3] << 16));
-      *reinterpret_cast<uint2*>(xb_lo + row * dim + i) =
-          make_uint2(ll[0] | ((uint32_t)ll[1] << 16), ll[2] | ((uint32_t)ll[3] << 16));
+      // the four elements stay adjacent in the span order
+      const int pos = cn_span_pos(i);
+      uint2 hh, ll;
+      cn_split_f16x2(y0, y1, hh.x, ll.x);
+      cn_split_f16x2(y2, y3, hh.y, ll.y);
+      *reinterpret_cast<uint2*>(o + pos) = hh;
+      *reinterpret_cast<uint2*>(xb_lo + row * dim + pos) = ll;
     } else {
       *reinterpret_cast<uint2*>(o + i) = make_uint2(pack2_bf16(y0, y1), pack2_bf16(y2, y3));
     }
@@ -830,6 +926,7 @@ void add_rmsnorm_v(float* x, const float* part, int splits, const float* g, floa
 hipError_t add_rmsnorm_bf16_launch(float* x, const float* part, int splits, const float* g, float eps, uint16_t* xb,
                                    uint16_t* xb_lo, int rows, int dim, hipStream_t st) {
   if (dim % 4 || dim <= 0 || rows <= 0 || splits > 16 || (splits > 0 && !part)) return hipErrorInvalidValue;
+  if (xb_lo && dim % 32) return hipErrorInvalidValue;  // the span order permutes blocks of 32
   const int v = (dim + 4 * CN_BLOCK - 1) / (4 * CN_BLOCK);  // float4 per thread
   // at most 4 float4 per thread when partials are folded (the register budget of
   // 16 splits x 4 float4), 16 for the norm alone

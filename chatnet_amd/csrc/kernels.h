@@ -65,14 +65,14 @@ struct GemmArgs {
   int seg_rows[3];
   int seg_mode;
   int M, K, N;            // M = virtual rows
-  const uint16_t* xb;     // N x K bf16, row stride K
-  const uint16_t* xb_lo;  // precise: low parts, x = xb + xb_lo
+  const uint16_t* xb;     // N x K, row stride K: bf16, or the fp16 high parts when precise
+  const uint16_t* xb_lo;  // precise: fp16 low parts, x = xb + xb_lo, both in the cn_span_pos order
   int precise;            // exact-weight two-plane kernel
   int epi;
   float* y;               // STORE / ADD target
   int ldy;
-  uint16_t* hb;           // SWIGLU target (bf16)
-  uint16_t* hb_lo;        // optional low parts of h
+  uint16_t* hb;           // SWIGLU target: bf16, or fp16 high parts with hb_lo
+  uint16_t* hb_lo;        // optional fp16 low parts of h (then both planes in the cn_span_pos order)
   int ldh;
   float* part;            // K-split partials, gemm_workspace_bytes() bytes
   int splits;             // set by gemm_launch
@@ -94,7 +94,8 @@ size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool precise, bool
 // (add_rmsnorm_bf16_launch for a residual add).
 hipError_t gemm_launch(const GemmArgs& a, int num_cus, hipStream_t st, int* splits_left = nullptr);
 hipError_t to_bf16_launch(const float* x, uint16_t* xb, size_t n, hipStream_t st);
-// xb = bf16(RMSNorm(x) * g) per row; with xb_lo also the low parts.
+// xb = bf16(RMSNorm(x) * g) per row; with xb_lo the span GEMM's input instead
+// (fp16 hi + lo planes in the cn_span_pos order, dim % 32 == 0).
 hipError_t rmsnorm_bf16_launch(const float* x, const float* g, float eps, uint16_t* xb, uint16_t* xb_lo, int rows,
                                int dim, hipStream_t st);
 // x[r] += the K-split partials part[0..splits)[r] (summed as the GEMM's reduce
@@ -128,8 +129,8 @@ struct PrefillAttnArgs {
   int ld;
   const void* kc;    // layer base, [ctx][kv_dim]
   const void* vc;
-  uint16_t* out;     // bf16 [n][ldo]
-  uint16_t* out_lo;  // optional low parts
+  uint16_t* out;     // [n][ldo]: bf16, or fp16 high parts with out_lo
+  uint16_t* out_lo;  // optional fp16 low parts (then both planes in the cn_span_pos order)
   int ldo;
   int n, p0, n_heads, kv_mul, head_dim, kv_dim, kv_f16;
   float scale;

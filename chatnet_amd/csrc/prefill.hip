@@ -151,8 +151,9 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
 // each SIMD and the chain of chunks per group is half as long; group 1 hands
 // its softmax state and unnormalised output to group 0 through LDS at the end.
 // Each group's next chunk is loaded into registers while it computes the
-// current one.  The output is written as bf16 (and its low part, when out_lo
-// is given) for the O-projection GEMM.
+// current one.  The output is written for the O-projection GEMM: bf16 in
+// natural order, or with out_lo the span GEMM's fp16 hi + lo planes in the
+// cn_span_pos order.
 constexpr int kSpanThreads = 512;
 
 template <int HD>
@@ -391,15 +392,24 @@ __global__ __launch_bounds__(kSpanThreads) void attn_prefill_kernel(PrefillAttnA
   const float a0 = __builtin_amdgcn_exp2f(m_run - m), a1 = __builtin_amdgcn_exp2f(m1 - m);
   const float inv = 1.0f / (l * a0 + l1 * a1);
   const float s0 = a0 * inv, s1 = a1 * inv;
-  const size_t base = (size_t)t * a.ldo + hh * HD + 4 * g;
+  const size_t row = (size_t)t * a.ldo;
 #pragma unroll
   for (int i = 0; i < NT; i++) {
     const float4 o1 = *reinterpret_cast<const float4*>(&xs[4 * ((4 * i + g) * 64 + r)]);
-    uint2 hi, lo;
-    split4(o[i][0] * s0 + o1.x * s1, o[i][1] * s0 + o1.y * s1, o[i][2] * s0 + o1.z * s1,
-           o[i][3] * s0 + o1.w * s1, hi, lo);
-    *reinterpret_cast<uint2*>(a.out + base + 16 * i) = hi;
-    if (a.out_lo) *reinterpret_cast<uint2*>(a.out_lo + base + 16 * i) = lo;
+    const float v0 = o[i][0] * s0 + o1.x * s1, v1 = o[i][1] * s0 + o1.y * s1, v2 = o[i][2] * s0 + o1.z * s1,
+                v3 = o[i][3] * s0 + o1.w * s1;
+    const int e = hh * HD + 4 * g + 16 * i;  // four adjacent elements, also in the span order
+    if (a.out_lo) {
+      uint2 hi, lo;
+      cn_split_f16x2(v0, v1, hi.x, lo.x);
+      cn_split_f16x2(v2, v3, hi.y, lo.y);
+      *reinterpret_cast<uint2*>(a.out + row + cn_span_pos(e)) = hi;
+      *reinterpret_cast<uint2*>(a.out_lo + row + cn_span_pos(e)) = lo;
+    } else {
+      uint2 hi, lo;
+      split4(v0, v1, v2, v3, hi, lo);
+      *reinterpret_cast<uint2*>(a.out + row + e) = hi;
+    }
   }
 }
 
