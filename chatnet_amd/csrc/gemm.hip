@@ -19,6 +19,8 @@
 // tiles and applies the epilogue.  Epilogues: STORE y = acc, ADD y += acc
 // (residual), SWIGLU (rows interleave gate/up; h = silu(gate)*up is written
 // in the next GEMM's input format).
+#include <algorithm>
+
 #include "device_common.h"
 #include "kernels.h"
 
@@ -50,7 +52,13 @@ __device__ __forceinline__ const uint32_t* gemm_row_ptr(const GemmArgs& a, int v
   return reinterpret_cast<const uint32_t*>(w) + (size_t)r * row_dw;
 }
 
-__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+// silu(g) * u = g * u / (1 + e^-g) (TensorMath.SiluElementwiseMul,
+// TensorMath.cs:253-286) with the hardware exp2 and reciprocal: about 1e-7
+// relative, below the resolution of the fp16 hi + lo planes h is stored in
+// (the span epilogue runs it for every h element of the tile).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return g * u * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));
+}
 
 __device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
   const __bf16 a = (__bf16)lo, b = (__bf16)hi;
@@ -202,31 +210,23 @@ __device__ __forceinline__ void dequant_u8_f16(uint32_t ca, uint32_t cb, float s
 }
 
 // ---------------------------------------------------------------------------
-// Pipelined 32x32 tile kernel: raw W bytes and the x tile stream into an
-// S-stage LDS ring through direct global->LDS loads (global_load_lds_dwordx4,
-// no registers held), so S-1 chunks of 64 K are in flight while one is
-// computed.  A workgroup waits only for the chunk it needs
+// Pipelined 32x32 tile kernels (gemm_p_kernel, gemm_s_kernel): raw W bytes
+// and the x tile stream into an LDS ring through direct global->LDS loads
+// (global_load_lds_dwordx4, no registers held), so later chunks of 64 K are in
+// flight while one is computed; a workgroup waits only for the chunk it needs
 // (s_waitcnt vmcnt(n) + a bare s_barrier), not for the whole queue.
 //
 // Per chunk (one 36-byte Q4_0 unit per W row) lane half h of row li takes
 // block h of the unit, and the x fragment of the same lane reads the same 8 k
 // of every MFMA step, so the K order inside a chunk is permuted consistently
-// for both operands.  One-plane kernel (bf16, x in natural order): step s
-// takes the low (s < 2) or high nibbles of qs[8(s&1) .. +7], i.e. k = 32h +
-// 8s .. +7 of the chunk.  Exact-weight kernel (fp16, x in the cn_span_pos
-// order): step s takes qs dword s (dequant_q4_f16).  Packed units: step s
-// takes codes 32h + 8s .. +7 (one plane) or 32h + 4s .. +3 and 32h + 16 + 4s
-// .. +3 (exact-weight, the span order).
+// for both operands (each kernel's comment gives its order).
 // LDS layout per stage: x planes [BN rows][8 x 16 B] with the 16-byte chunk
 // of logical index c of row r stored at c ^ ((r >> 1) & 7) (reads of 32 rows
-// stay 2-way per bank), then W [BM rows][48 B] holding unit bytes [0,16),
-// [16,32) and [20,36).
-// A wave owns 32*TM W rows x 32*TN columns; the 4 waves stack along M and
-// share the x tile.  PRECISE (spans of the forward pass) runs three fp16 MFMAs
-// per step, Wa*xh + Wa*xl + Wb*xh, with W = Wa + Wb exact (raw Q4_0; ~22 bits
-// for packed units) and x = xh + xl to ~2^-22; the dropped Wb*xl term is
-// below 2^-19 relative.  Output layout of a 32x32 tile: lane l, accumulator v
-// holds row 8*(v/4) + 4*(l/32) + v%4, column l%32.
+// stay 2-way per bank), then W [128 rows][48 B] holding unit bytes [0,16),
+// [16,32) and [20,36) (packed units: [128 rows][96 B]).
+// A wave owns 32 W rows x 32*TN columns; the 4 waves stack along M and share
+// the x tile.  Output layout of a 32x32 tile: lane l, accumulator v holds row
+// 8*(v/4) + 4*(l/32) + v%4, column l%32.
 // ---------------------------------------------------------------------------
 // 16 bytes from global memory straight into LDS: lane i of the wave writes
 // lds_wave_base + 16*i (lds_wave_base must be the same for the whole wave).
@@ -248,89 +248,77 @@ __device__ __forceinline__ void wg_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <bool PRECISE, int TM, int TN, int S, bool PK>
+template <bool PRECISE, int TN, int S, bool PK>
 struct PipeCfg {
   static constexpr int PL = PRECISE ? 2 : 1;
-  static constexpr int BM = 128 * TM, BN = 32 * TN;
+  static constexpr int BM = 128, BN = 32 * TN;
   static constexpr int UNIT = PK ? kGemmPackUnit : 36;  // global bytes per row and chunk
   static constexpr int WP = PK ? 6 : 3;        // 16-byte pieces per row and chunk
   static constexpr int WROW = 16 * WP;         // LDS bytes per row and chunk
   static constexpr int XB = BN * 128;          // bytes per x plane per stage
   static constexpr int WB = BM * WROW;         // bytes of W per stage
   static constexpr int STAGE = PL * XB + WB;
+  static constexpr int LDS = S * STAGE;        // the ring
   static constexpr int XPW = BN * 8 / 4;       // x pieces (16 B) per wave per plane
   static constexpr int XI = XPW / 64;
   static constexpr int WPW = BM * WP / 4;      // W pieces per wave
   static constexpr int WI = (WPW + 63) / 64;
   static constexpr int VPS = PL * XI + WI;     // vector-memory instructions per stage per wave
+  static constexpr int WD = PK ? 12 : 5;       // W dwords a lane reads per chunk
+  static constexpr bool PACKED = PK;
   static_assert(XPW % 64 == 0, "x pieces per wave must fill whole instructions");
 };
 
-template <bool PRECISE>
-struct GemmOp;
-template <>
-struct GemmOp<false> {
-  typedef bf16x8 T;
-};
-template <>
-struct GemmOp<true> {
-  typedef f16x8 T;
-};
-
-template <bool PRECISE, int TM, int TN, int S, bool PK>
-__global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
-  using C = PipeCfg<PRECISE, TM, TN, S, PK>;
-  using OP = typename GemmOp<PRECISE>::T;
-  extern __shared__ __attribute__((aligned(16))) char lds[];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int h = lane >> 5, li = lane & 31;
-
-  const int n_nt = (a.N + C::BN - 1) / C::BN;
-  int bid = blockIdx.x;
-  const int ks = bid % a.splits;
-  bid /= a.splits;
-  const int nt = bid % n_nt;
-  const int mt = bid / n_nt;
-  const int m0 = mt * C::BM;
-  const int n0 = nt * C::BN;
-  const int m_wave = m0 + wave * 32 * TM;
-
-  const int nchunks = a.K / 64;
-  const int cps = (nchunks + a.splits - 1) / a.splits;
-  const int c_begin = ks * cps;
-  const int c_end = min(nchunks, c_begin + cps);
-  const int row_dw = a.K / 64 * (C::UNIT / 4);
-
-  // Per-lane source pointers of the stage loads (chunk-independent parts).
+// Tile coordinates, K range and stage loads of one workgroup (both kernels).
+template <class C>
+struct TileIO {
+  int lane, wave, h, li, ks, m0, n0, c_begin, c_end;
   const uint16_t* xsrc[C::PL][C::XI];
-#pragma unroll
-  for (int p = 0; p < C::PL; p++)
-#pragma unroll
-    for (int j = 0; j < C::XI; j++) {
-      const int piece = wave * C::XPW + 64 * j + lane;
-      const int row = piece >> 3, ch = piece & 7;
-      const int n = min(n0 + row, a.N - 1);
-      const int logical = ch ^ ((row >> 1) & 7);
-      xsrc[p][j] = (p ? a.xb_lo : a.xb) + (size_t)n * a.K + 8 * logical;
-    }
   const char* wsrc[C::WI];
   bool wact[C::WI];
+
+  __device__ __forceinline__ explicit TileIO(const GemmArgs& a) {
+    lane = threadIdx.x & 63;
+    wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    h = lane >> 5;
+    li = lane & 31;
+    const int n_nt = (a.N + C::BN - 1) / C::BN;
+    int bid = blockIdx.x;
+    ks = bid % a.splits;
+    bid /= a.splits;
+    m0 = (bid / n_nt) * C::BM;
+    n0 = (bid % n_nt) * C::BN;
+    const int nchunks = a.K / 64;
+    const int cps = (nchunks + a.splits - 1) / a.splits;
+    c_begin = ks * cps;
+    c_end = min(nchunks, c_begin + cps);
+    const int row_dw = a.K / 64 * (C::UNIT / 4);
 #pragma unroll
-  for (int j = 0; j < C::WI; j++) {
-    const int q = 64 * j + lane;
-    wact[j] = q < C::WPW;
-    const int piece = wave * C::WPW + (wact[j] ? q : 0);
-    const int row = piece / C::WP, part = piece % C::WP;
-    const int vr = min(m0 + row, a.M - 1);
-    // Q4_0: pieces at unit bytes 0, 16 and 20, exactly the 36 bytes, no read
-    // past the unit; packed: the 6 pieces of the 96-byte unit
-    wsrc[j] = reinterpret_cast<const char*>(gemm_row_ptr(a, vr, row_dw)) + (!PK && part == 2 ? 20 : 16 * part);
+    for (int p = 0; p < C::PL; p++)
+#pragma unroll
+      for (int j = 0; j < C::XI; j++) {
+        const int piece = wave * C::XPW + 64 * j + lane;
+        const int row = piece >> 3, ch = piece & 7;
+        const int n = min(n0 + row, a.N - 1);
+        const int logical = ch ^ ((row >> 1) & 7);
+        xsrc[p][j] = (p ? a.xb_lo : a.xb) + (size_t)n * a.K + 8 * logical;
+      }
+#pragma unroll
+    for (int j = 0; j < C::WI; j++) {
+      const int q = 64 * j + lane;
+      wact[j] = q < C::WPW;
+      const int piece = wave * C::WPW + (wact[j] ? q : 0);
+      const int row = piece / C::WP, part = piece % C::WP;
+      const int vr = min(m0 + row, a.M - 1);
+      // Q4_0: pieces at unit bytes 0, 16 and 20, exactly the 36 bytes, no read
+      // past the unit; packed: the 6 pieces of the 96-byte unit
+      wsrc[j] = reinterpret_cast<const char*>(gemm_row_ptr(a, vr, row_dw)) + (!C::PACKED && part == 2 ? 20 : 16 * part);
+    }
   }
 
-  auto issue = [&](int c, int slot) {
-    char* st = lds + slot * C::STAGE;
+  // Chunk c's x planes and W rows into stage `st` (C::VPS vector-memory
+  // instructions per wave).
+  __device__ __forceinline__ void issue(int c, char* st) const {
 #pragma unroll
     for (int p = 0; p < C::PL; p++)
 #pragma unroll
@@ -338,97 +326,104 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
         lds_dma16(xsrc[p][j] + c * 64, st + p * C::XB + (wave * C::XPW + 64 * j) * 16);
 #pragma unroll
     for (int j = 0; j < C::WI; j++)
-      if (wact[j])
-        lds_dma16(wsrc[j] + c * C::UNIT, st + C::PL * C::XB + (wave * C::WPW + 64 * j) * 16);
+      if (wact[j]) lds_dma16(wsrc[j] + c * C::UNIT, st + C::PL * C::XB + (wave * C::WPW + 64 * j) * 16);
     asm volatile("" ::: "memory");
-  };
+  }
 
-  f32x16 acc[TM][TN];
+  // The dwords of the lane's W slice in stage `st`.  Q4_0 (5 dwords): the
+  // stage holds unit bytes [0,16) [16,32) [20,36): block A's d + qs at dwords
+  // 0..4, block B's d in the high half of dword 4 and its qs at dwords
+  // 8..11.  Packed (12 dwords): codes 32h..32h+31 (dwords 8h..8h+7), then
+  // scales 2h, 2h+1 (unit bytes 64 + 8h) and offsets 2h, 2h+1 (80 + 8h).
+  __device__ __forceinline__ void wraw(const char* st, uint32_t (&w)[C::WD]) const {
+    const uint32_t* wb = reinterpret_cast<const uint32_t*>(st + C::PL * C::XB + (wave * 32 + li) * C::WROW);
+    if constexpr (C::PACKED) {
 #pragma unroll
-  for (int r = 0; r < TM; r++)
-#pragma unroll
-    for (int cc = 0; cc < TN; cc++)
-#pragma unroll
-      for (int v = 0; v < 16; v++) acc[r][cc][v] = 0.f;
+      for (int i = 0; i < 8; i++) w[i] = wb[8 * h + i];
+      w[8] = wb[16 + 2 * h];
+      w[9] = wb[17 + 2 * h];
+      w[10] = wb[20 + 2 * h];
+      w[11] = wb[21 + 2 * h];
+    } else {
+      w[0] = wb[8 * h];
+      w[1] = wb[8 * h + 1];
+      w[2] = wb[8 * h + 2];
+      w[3] = wb[8 * h + 3];
+      w[4] = wb[4];
+    }
+  }
 
+  // The 16-byte x fragment of MFMA step s, column tile cc, plane p.
+  __device__ __forceinline__ uint4 xfrag(const char* st, int p, int s, int cc) const {
+    const int xrow = 32 * cc + li;
+    const int phys = (4 * h + s) ^ ((xrow >> 1) & 7);
+    return *reinterpret_cast<const uint4*>(st + p * C::XB + xrow * 128 + phys * 16);
+  }
+
+  // Final tiles: K-split partials [splits][N][M] or the epilogue.
+  template <int TN>
+  __device__ __forceinline__ void store(const GemmArgs& a, const f32x16 (&acc)[TN]) const {
+#pragma unroll
+    for (int cc = 0; cc < TN; cc++) {
+      const int n = n0 + 32 * cc + li;
+#pragma unroll
+      for (int v4 = 0; v4 < 4; v4++) {
+        const int m = m0 + wave * 32 + 8 * v4 + 4 * h;
+        const f32x4 v = {acc[cc][4 * v4], acc[cc][4 * v4 + 1], acc[cc][4 * v4 + 2], acc[cc][4 * v4 + 3]};
+        if (a.splits > 1) {
+          if (n < a.N && m < a.M) {
+            float* p = a.part + ((size_t)ks * a.N + n) * a.M + m;
+            if (m + 3 < a.M && (a.M & 3) == 0) *reinterpret_cast<f32x4*>(p) = v;
+            else
+              for (int i = 0; i < 4 && m + i < a.M; i++) p[i] = v[i];
+          }
+        } else {
+          write_out4(a, a.epi, n, m, v);
+        }
+      }
+    }
+  }
+};
+
+// One-plane kernel (chatnet_matmul: bf16 x in natural order).  An S-stage
+// ring with S-1 chunks in flight; each chunk's W is dequantized during the
+// previous chunk's MFMAs.  Q4_0: lane half h of row li takes block h of the
+// unit, and MFMA step s the low (s < 2) or high nibbles of qs[8(s&1) .. +7],
+// i.e. k = 32h + 8s .. +7 of the chunk, the same 8 k its x fragment reads.
+// Packed: step s takes codes 32h + 8s .. +7.
+template <int TN, int S, bool PK>
+__global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
+  using C = PipeCfg<false, TN, S, PK>;
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  const TileIO<C> io(a);
+  const int h = io.h;
+
+  f32x16 acc[TN];
+#pragma unroll
+  for (int cc = 0; cc < TN; cc++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[cc][v] = 0.f;
+
+  const int c_begin = io.c_begin, c_end = io.c_end;
   if (c_begin < c_end) {
     auto slot_of = [&](int c) { return lds + ((c - c_begin) % S) * C::STAGE; };
-    // The dwords of a lane's W slice from a stage slot.  Q4_0 (5 dwords): the
-    // slot holds unit bytes [0,16) [16,32) [20,36): block A's d + qs at dwords
-    // 0..4, block B's d in the high half of dword 4 and its qs at dwords
-    // 8..11.  Packed (12 dwords): codes 32h..32h+31 (dwords 8h..8h+7), then
-    // scales 2h, 2h+1 (unit bytes 64 + 8h) and offsets 2h, 2h+1 (80 + 8h).
-    constexpr int WD = PK ? 12 : 5;
-    auto wraw = [&](const char* st, int r, uint32_t (&w)[WD]) {
-      const uint32_t* wb =
-          reinterpret_cast<const uint32_t*>(st + C::PL * C::XB + (wave * 32 * TM + 32 * r + li) * C::WROW);
+    // Q4_0: half 0 gives steps 0 and 2 (low/high nibbles of qs[0..7]), half 1
+    // steps 1 and 3.  Packed: half 0 gives steps 0 and 1 (codes 0..15 of the
+    // lane, scale 2h), half 1 steps 2 and 3 (codes 16..31, scale 2h+1).
+    auto deq_half = [&](const uint32_t (&w)[C::WD], int half, bf16x8 (&fh)[4]) {
       if constexpr (PK) {
+        const float sc = __uint_as_float(w[8 + half]), of = __uint_as_float(w[10 + half]);
 #pragma unroll
-        for (int i = 0; i < 8; i++) w[i] = wb[8 * h + i];
-        w[8] = wb[16 + 2 * h];
-        w[9] = wb[17 + 2 * h];
-        w[10] = wb[20 + 2 * h];
-        w[11] = wb[21 + 2 * h];
+        for (int t = 0; t < 2; t++) dequant_u8x8(w[4 * half + 2 * t], w[4 * half + 2 * t + 1], sc, of, fh[2 * half + t]);
       } else {
-        w[0] = wb[8 * h];
-        w[1] = wb[8 * h + 1];
-        w[2] = wb[8 * h + 2];
-        w[3] = wb[8 * h + 3];
-        w[4] = wb[4];
-      }
-    };
-    // One-plane kernel.  Q4_0: half 0 gives steps 0 and 2 (low/high nibbles
-    // of qs[0..7]), half 1 steps 1 and 3.  Packed: half 0 gives steps 0 and
-    // 1 (codes 0..15 of the lane, scale 2h), half 1 steps 2 and 3 (codes
-    // 16..31, scale 2h+1).
-    auto deq_half = [&](const uint32_t (&w)[WD], int half, OP (&fh)[4]) {
-      if constexpr (!PRECISE) {
-        if constexpr (PK) {
-          const float sc = __uint_as_float(w[8 + half]), of = __uint_as_float(w[10 + half]);
-#pragma unroll
-          for (int t = 0; t < 2; t++) dequant_u8x8(w[4 * half + 2 * t], w[4 * half + 2 * t + 1], sc, of, fh[2 * half + t]);
-        } else {
-          const uint32_t sh = h ? 0u : 2u;
-          const float d = cn_h2f(h ? (w[4] >> 16) : w[0]);
-          const uint32_t qa = __builtin_amdgcn_alignbyte(half ? w[3] : w[1], half ? w[2] : w[0], sh);
-          const uint32_t qb = __builtin_amdgcn_alignbyte(half ? w[4] : w[2], half ? w[3] : w[1], sh);
-          bf16x8 th[2];
-          dequant_w16(qa, qb, d, th);
-          fh[half] = th[0];
-          fh[half + 2] = th[1];
-        }
-      }
-    };
-    // Exact-weight kernel: the (dh, dl) split of the lane's block scale
-    // (Q4_0), then step s of the chunk as Wa, Wb.  v_perm_b32 selectors take
-    // qs dword s of the lane's block (2 bytes into the unit for block A) as
-    // bytes b0 b2 b1 b3.
-    const uint32_t psel = h ? 0x03010200u : 0x05030402u;
-    uint32_t magic = 0x64006400u;
-    asm volatile("" : "+v"(magic));
-    struct Dsc {
-      cn_half2 dh, dl;
-    };
-    auto dsplit = [&](const uint32_t (&w)[WD]) {
-      Dsc r{};
-      if constexpr (PRECISE && !PK) {
-        const uint32_t d16 = h ? (w[4] >> 16) : (w[0] & 0xFFFFu);
-        const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)d16);
-        const _Float16 dh = __builtin_bit_cast(_Float16, (uint16_t)(d16 & 0xFFF8u));
-        const _Float16 dl = d - dh;
-        r.dh = (cn_half2){dh, dh};
-        r.dl = (cn_half2){dl, dl};
-      }
-      return r;
-    };
-    auto deq_step = [&](const uint32_t (&w)[WD], const Dsc& ds, int s, OP& fa, OP& fb) {
-      if constexpr (PRECISE) {
-        if constexpr (PK) {
-          dequant_u8_f16(w[s], w[4 + s], __uint_as_float(w[8]), __uint_as_float(w[10]), __uint_as_float(w[9]),
-                         __uint_as_float(w[11]), fa, fb);
-        } else {
-          dequant_q4_f16(__builtin_amdgcn_perm(w[s + 1], w[s], psel), magic, ds.dh, ds.dl, fa, fb);
-        }
+        const uint32_t sh = h ? 0u : 2u;
+        const float d = cn_h2f(h ? (w[4] >> 16) : w[0]);
+        const uint32_t qa = __builtin_amdgcn_alignbyte(half ? w[3] : w[1], half ? w[2] : w[0], sh);
+        const uint32_t qb = __builtin_amdgcn_alignbyte(half ? w[4] : w[2], half ? w[3] : w[1], sh);
+        bf16x8 th[2];
+        dequant_w16(qa, qb, d, th);
+        fh[half] = th[0];
+        fh[half + 2] = th[1];
       }
     };
     // Waits until stage t has landed, given that stages up to `issued` are in flight.
@@ -448,24 +443,17 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < S - 1; i++)
       if (c_begin + i < c_end) {
-        issue(c_begin + i, i);
+        io.issue(c_begin + i, lds + i * C::STAGE);
         issued = c_begin + i;
       }
     wait_stage(c_begin, issued);
     wg_barrier();
-    OP wa[TM][4], wb[TM][4];
-#pragma unroll
-    for (int r = 0; r < TM; r++) {
-      uint32_t w[WD];
-      wraw(slot_of(c_begin), r, w);
-      if constexpr (PRECISE) {
-        const Dsc ds = dsplit(w);
-#pragma unroll
-        for (int s = 0; s < 4; s++) deq_step(w, ds, s, wa[r][s], wb[r][s]);
-      } else {
-        deq_half(w, 0, wa[r]);
-        deq_half(w, 1, wa[r]);
-      }
+    bf16x8 wh[4];
+    {
+      uint32_t w[C::WD];
+      io.wraw(slot_of(c_begin), w);
+      deq_half(w, 0, wh);
+      deq_half(w, 1, wh);
     }
 
     for (int c = c_begin; c < c_end; c++) {
@@ -475,96 +463,123 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
       wait_stage(has_next ? c + 1 : c, issued);
       wg_barrier();
       if (c + S - 1 < c_end) {
-        issue(c + S - 1, (c + S - 1 - c_begin) % S);
+        io.issue(c + S - 1, slot_of(c + S - 1));
         issued = c + S - 1;
       }
       // Unconditional (branch-free, so it interleaves with the MFMAs): on the
       // last chunk this reads a stale slot whose result is never used.
-      uint32_t nw[TM][WD];
-      Dsc nds[TM];
-#pragma unroll
-      for (int r = 0; r < TM; r++) {
-        wraw(slot_of(c + 1), r, nw[r]);
-        nds[r] = dsplit(nw[r]);
-      }
-      OP nwa[TM][4], nwb[TM][4];
+      uint32_t nw[C::WD];
+      io.wraw(slot_of(c + 1), nw);
+      bf16x8 nwh[4];
 
       const char* st = slot_of(c);
-      OP xh[2][TN], xl[2][TN];
+      bf16x8 xh[2][TN];
       auto load_x = [&](int s, int b) {
 #pragma unroll
-        for (int cc = 0; cc < TN; cc++) {
-          const int xrow = 32 * cc + li;
-          const int phys = (4 * h + s) ^ ((xrow >> 1) & 7);
-          const char* xp = st + xrow * 128 + phys * 16;
-          xh[b][cc] = __builtin_bit_cast(OP, *reinterpret_cast<const uint4*>(xp));
-          if constexpr (PRECISE) xl[b][cc] = __builtin_bit_cast(OP, *reinterpret_cast<const uint4*>(xp + C::XB));
-        }
+        for (int cc = 0; cc < TN; cc++) xh[b][cc] = __builtin_bit_cast(bf16x8, io.xfrag(st, 0, s, cc));
       };
       load_x(0, 0);
 #pragma unroll
       for (int s = 0; s < 4; s++) {
         if (s < 3) load_x(s + 1, (s + 1) & 1);  // next step's fragments in flight during this step
-        // one pass over all accumulators per product, so consecutive MFMAs
-        // never wait on each other's result
 #pragma unroll
-        for (int cc = 0; cc < TN; cc++)
-#pragma unroll
-          for (int r = 0; r < TM; r++) acc[r][cc] = mma32(wa[r][s], xh[s & 1][cc], acc[r][cc]);
-        if constexpr (PRECISE) {
-#pragma unroll
-          for (int cc = 0; cc < TN; cc++)
-#pragma unroll
-            for (int r = 0; r < TM; r++) acc[r][cc] = mma32(wa[r][s], xl[s & 1][cc], acc[r][cc]);
-#pragma unroll
-          for (int cc = 0; cc < TN; cc++)
-#pragma unroll
-            for (int r = 0; r < TM; r++) acc[r][cc] = mma32(wb[r][s], xh[s & 1][cc], acc[r][cc]);
-          // the next chunk's step s is dequantized while these MFMAs run
-#pragma unroll
-          for (int r = 0; r < TM; r++) deq_step(nw[r], nds[r], s, nwa[r][s], nwb[r][s]);
-        } else if (s == 0 || s == 2) {
-#pragma unroll
-          for (int r = 0; r < TM; r++) deq_half(nw[r], s >> 1, nwa[r]);
-        }
+        for (int cc = 0; cc < TN; cc++) acc[cc] = mma32(wh[s], xh[s & 1][cc], acc[cc]);
+        if (s == 0 || s == 2) deq_half(nw, s >> 1, nwh);
       }
 #pragma unroll
-      for (int r = 0; r < TM; r++)
-#pragma unroll
-        for (int s = 0; s < 4; s++) {
-          wa[r][s] = nwa[r][s];
-          if constexpr (PRECISE) wb[r][s] = nwb[r][s];
-        }
+      for (int s = 0; s < 4; s++) wh[s] = nwh[s];
     }
   }
-
-#pragma unroll
-  for (int r = 0; r < TM; r++) {
-#pragma unroll
-    for (int cc = 0; cc < TN; cc++) {
-      const int n = n0 + 32 * cc + li;
-#pragma unroll
-      for (int v4 = 0; v4 < 4; v4++) {
-        const int m = m_wave + 32 * r + 8 * v4 + 4 * h;
-        const f32x4 v = {acc[r][cc][4 * v4], acc[r][cc][4 * v4 + 1], acc[r][cc][4 * v4 + 2], acc[r][cc][4 * v4 + 3]};
-        if (a.splits > 1) {
-          if (n < a.N && m < a.M) {
-            float* p = a.part + ((size_t)ks * a.N + n) * a.M + m;
-            if (m + 3 < a.M && (a.M & 3) == 0) *reinterpret_cast<f32x4*>(p) = v;
-            else
-              for (int i = 0; i < 4 && m + i < a.M; i++) p[i] = v[i];
-          }
-        } else {
-          write_out4(a, a.epi, n, m, v);
-        }
-      }
-    }
-  }
+  io.template store<TN>(a, acc);
 }
 
-template <bool PRECISE, int TM, int TN, int S, bool PK>
-constexpr size_t gemm_p_lds() {
-  return (size_t)S * PipeCfg<PRECISE, TM, TN, S, PK>::STAGE;
+// Span kernel (the exact-weight product of the forward pass's spans: fp16 x
+// hi + lo planes in the cn_span_pos order).  An S-stage ring (S = 2 or 3): at
+// the start of chunk c every wave has landed its part of the chunk and finished
+// chunk c-1, chunk c+S-1 is issued into the freed stage, and chunk c's W is
+// dequantized step by step just ahead of its MFMAs.  Two stages take 44 KB of
+// LDS (raw Q4_0, 64 columns), so three workgroups share a CU and one's VALU
+// work and waits overlap the others' MFMAs; three stages keep two chunks in
+// flight for grids of at most two workgroups per CU.  Step s of lane half h:
+// Q4_0 qs dword s of block h (dequant_q4_f16), packed codes 32h + 4s .. +3
+// and 32h + 16 + 4s .. +3 with the scale/offset pairs 2h and 2h+1.  Three
+// fp16 MFMAs per step: Wa*xh + Wa*xl + Wb*xh, W = Wa + Wb exact for Q4_0 (~22
+// bits for packed units), x = xh + xl to ~2^-22; the dropped Wb*xl term is
+// below 2^-19 relative.
+template <int TN, int S, bool PK>
+__global__ __launch_bounds__(CN_BLOCK) void gemm_s_kernel(GemmArgs a) {
+  using C = PipeCfg<true, TN, S, PK>;
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  const TileIO<C> io(a);
+  const int h = io.h;
+
+  f32x16 acc[TN];
+#pragma unroll
+  for (int cc = 0; cc < TN; cc++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[cc][v] = 0.f;
+
+  // v_perm_b32 selectors: qs dword s of the lane's block (2 bytes into the
+  // unit for block A) as bytes b0 b2 b1 b3; 0x64006400 kept in a register
+  // so each nibble pair takes one v_and_or_b32
+  const uint32_t psel = h ? 0x03010200u : 0x05030402u;
+  uint32_t magic = 0x64006400u;
+  asm volatile("" : "+v"(magic));
+
+  const int c_begin = io.c_begin, c_end = io.c_end;
+  if (c_begin < c_end) {
+    auto slot_of = [&](int c) { return lds + ((c - c_begin) % S) * C::STAGE; };
+#pragma unroll
+    for (int i = 0; i < S - 1; i++)
+      if (c_begin + i < c_end) io.issue(c_begin + i, lds + i * C::STAGE);
+    for (int c = c_begin; c < c_end; c++) {
+      char* st = slot_of(c);
+      // this wave's part of chunk c (chunk c+1 may stay in flight with three stages)
+      if (S >= 3 && c + 1 < c_end) vm_wait<C::VPS>();
+      else vm_wait<0>();
+      wg_barrier();  // every wave's part landed, every wave done with chunk c-1
+      if (c + S - 1 < c_end) io.issue(c + S - 1, slot_of(c + S - 1));
+      uint32_t w[C::WD];
+      io.wraw(st, w);
+      cn_half2 dh2 = {}, dl2 = {};
+      if constexpr (!PK) {
+        // d = dh + dl: dh keeps the top 8 significant bits of the fp16 scale
+        const uint32_t d16 = h ? (w[4] >> 16) : (w[0] & 0xFFFFu);
+        const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)d16);
+        const _Float16 dh = __builtin_bit_cast(_Float16, (uint16_t)(d16 & 0xFFF8u));
+        const _Float16 dl = d - dh;
+        dh2 = (cn_half2){dh, dh};
+        dl2 = (cn_half2){dl, dl};
+      }
+      f16x8 xh[2][TN], xl[2][TN];
+      auto load_x = [&](int s, int b) {
+#pragma unroll
+        for (int cc = 0; cc < TN; cc++) {
+          xh[b][cc] = __builtin_bit_cast(f16x8, io.xfrag(st, 0, s, cc));
+          xl[b][cc] = __builtin_bit_cast(f16x8, io.xfrag(st, 1, s, cc));
+        }
+      };
+      load_x(0, 0);
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        if (s < 3) load_x(s + 1, (s + 1) & 1);
+        f16x8 wa, wb;
+        if constexpr (PK) {
+          dequant_u8_f16(w[s], w[4 + s], __uint_as_float(w[8]), __uint_as_float(w[10]), __uint_as_float(w[9]),
+                         __uint_as_float(w[11]), wa, wb);
+        } else {
+          dequant_q4_f16(__builtin_amdgcn_perm(w[s + 1], w[s], psel), magic, dh2, dl2, wa, wb);
+        }
+#pragma unroll
+        for (int cc = 0; cc < TN; cc++) acc[cc] = mma32(wa, xh[s & 1][cc], acc[cc]);
+#pragma unroll
+        for (int cc = 0; cc < TN; cc++) acc[cc] = mma32(wa, xl[s & 1][cc], acc[cc]);
+#pragma unroll
+        for (int cc = 0; cc < TN; cc++) acc[cc] = mma32(wb, xh[s & 1][cc], acc[cc]);
+      }
+    }
+  }
+  io.template store<TN>(a, acc);
 }
 
 // Sums the K-split partials [splits][N][M] and applies the epilogue; one
@@ -784,57 +799,103 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_pack_kernel(int qtype, const ui
   o[5] = make_uint4(__float_as_uint(of[0]), __float_as_uint(of[1]), __float_as_uint(of[2]), __float_as_uint(of[3]));
 }
 
-// Column tile by batch size (32, 64 or 128 columns per workgroup, 128 rows);
-// K is split while the tile grid covers fewer than two workgroups per CU,
-// keeping at least 8 chunks of 64 per split so the LDS ring stays full.  The
-// two-plane kernel on raw Q4_0 blocks takes 64-column tiles at any N > 32:
-// its ring is then 66 KB, so two workgroups share a CU and one's pipeline
-// fill and epilogue overlap the other's MFMAs (measured per GEMM of 22
-// TinyLlama layers at N = 512: 5.28 -> 4.89 ms; 7B shapes at N = 128: 2.13 ->
-// 1.91 ms).  128-column tiles of packed weights would not fit twice either way.
+// Column tile by batch size and kernel.  One-plane kernel: 32, 64 or 128
+// columns per workgroup, a 3-stage ring, K split while the tile grid covers
+// fewer than two workgroups per CU (at least 8 chunks of 64 per split).  Span
+// kernel: 32 or 64 columns; a tile grid of more than two workgroups per CU
+// takes the 2-stage ring (44 KB for raw Q4_0 at 64 columns, three workgroups
+// per CU; 56 KB for packed units, two), a smaller one the 3-stage ring (two
+// per CU) and a K split into the largest count that keeps the grid within one
+// round of resident workgroups with at least 8 chunks per split (a grid just
+// over a round would run a second round on a few CUs).
 struct GemmShape {
-  int tn, splits;
+  int tn, splits, stages;
 };
-
-GemmShape pick_gemm(int M, int N, int K, int num_cus, bool precise, bool packed) {
-  GemmShape s;
-  s.tn = N <= 32 ? 1 : (N <= 64 || (precise && !packed) ? 2 : 4);
-  const long long tiles = (long long)((M + 127) / 128) * ((N + 32 * s.tn - 1) / (32 * s.tn));
-  const int nchunks = K / 64;
-  s.splits = 1;
-  while (tiles * s.splits < 2LL * num_cus && nchunks / (s.splits * 2) >= 8 && s.splits < 16) s.splits *= 2;
-  return s;
-}
 
 constexpr int kStages = 3;
 
-template <bool PRECISE, int TN, bool PK>
-hipError_t launch_p(const GemmArgs& a, int grid, hipStream_t st) {
-  constexpr size_t lds = gemm_p_lds<PRECISE, 1, TN, kStages, PK>();
-  static_assert(lds <= 160 * 1024, "LDS ring exceeds the CU's 160 KB");
-  // Dynamic LDS above 64 KB must be allowed per kernel; every caller sets the
-  // same value, so a race on the flag is harmless.
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_p_kernel<PRECISE, 1, TN, kStages, PK>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    attr_set = true;
+template <bool PRECISE, int TN, int S, bool PK>
+constexpr int ring_bytes() {
+  return PipeCfg<PRECISE, TN, S, PK>::LDS;
+}
+
+int span_ring_bytes(int tn, int stages, bool packed) {
+  if (stages == 2) {
+    if (tn == 1) return packed ? ring_bytes<true, 1, 2, true>() : ring_bytes<true, 1, 2, false>();
+    return packed ? ring_bytes<true, 2, 2, true>() : ring_bytes<true, 2, 2, false>();
   }
-  hipLaunchKernelGGL((gemm_p_kernel<PRECISE, 1, TN, kStages, PK>), dim3(grid), dim3(CN_BLOCK), lds, st, a);
+  if (tn == 1) return packed ? ring_bytes<true, 1, 3, true>() : ring_bytes<true, 1, 3, false>();
+  return packed ? ring_bytes<true, 2, 3, true>() : ring_bytes<true, 2, 3, false>();
+}
+
+GemmShape pick_gemm(int M, int N, int K, int num_cus, bool precise, bool packed) {
+  GemmShape s;
+  const int nchunks = K / 64;
+  s.splits = 1;
+  s.stages = kStages;
+  if (precise) {
+    s.tn = N <= 32 ? 1 : 2;
+    const long long tiles = (long long)((M + 127) / 128) * ((N + 32 * s.tn - 1) / (32 * s.tn));
+    s.stages = tiles > 2LL * num_cus ? 2 : 3;
+    const int per_cu = std::min(3, 160 * 1024 / span_ring_bytes(s.tn, s.stages, packed));
+    const long long slots = (long long)per_cu * num_cus;
+    while (s.splits < 16 && tiles * (s.splits + 1) <= slots && nchunks / (s.splits + 1) >= 8) s.splits++;
+  } else {
+    s.tn = N <= 32 ? 1 : (N <= 64 ? 2 : 4);
+    const long long tiles = (long long)((M + 127) / 128) * ((N + 32 * s.tn - 1) / (32 * s.tn));
+    while (tiles * s.splits < 2LL * num_cus && nchunks / (s.splits * 2) >= 8 && s.splits < 16) s.splits *= 2;
+  }
+  return s;
+}
+
+// Dynamic LDS above 64 KB must be allowed per kernel; every caller sets the
+// same value, so a race on the flag is harmless.
+template <class F>
+hipError_t allow_lds(F* kernel, int bytes, bool& done) {
+  if (done || bytes <= 64 * 1024) return hipSuccess;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     bytes);
+  if (e == hipSuccess) done = true;
+  return e;
+}
+
+template <int TN, bool PK>
+hipError_t launch_p(const GemmArgs& a, int grid, hipStream_t st) {
+  constexpr int lds = PipeCfg<false, TN, kStages, PK>::LDS;
+  static_assert(lds <= 160 * 1024, "LDS ring exceeds the CU's 160 KB");
+  static bool attr_set = false;
+  hipError_t e = allow_lds(&gemm_p_kernel<TN, kStages, PK>, lds, attr_set);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((gemm_p_kernel<TN, kStages, PK>), dim3(grid), dim3(CN_BLOCK), lds, st, a);
   return hipGetLastError();
 }
 
-template <bool PRECISE, bool PK>
-hipError_t launch_tn(const GemmArgs& a, int tn, int grid, hipStream_t st) {
-  if (tn == 1) return launch_p<PRECISE, 1, PK>(a, grid, st);
-  if (tn == 2) return launch_p<PRECISE, 2, PK>(a, grid, st);
-  return launch_p<PRECISE, 4, PK>(a, grid, st);
+template <int TN, int S, bool PK>
+hipError_t launch_s(const GemmArgs& a, int grid, hipStream_t st) {
+  constexpr int lds = PipeCfg<true, TN, S, PK>::LDS;
+  static_assert(lds <= 160 * 1024, "LDS ring exceeds the CU's 160 KB");
+  static bool attr_set = false;
+  hipError_t e = allow_lds(&gemm_s_kernel<TN, S, PK>, lds, attr_set);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((gemm_s_kernel<TN, S, PK>), dim3(grid), dim3(CN_BLOCK), lds, st, a);
+  return hipGetLastError();
 }
 
-template <bool PRECISE>
-hipError_t launch_fmt(const GemmArgs& a, int tn, int grid, hipStream_t st) {
-  return a.packed ? launch_tn<PRECISE, true>(a, tn, grid, st) : launch_tn<PRECISE, false>(a, tn, grid, st);
+template <int TN, bool PK>
+hipError_t launch_s_ring(const GemmArgs& a, int stages, int grid, hipStream_t st) {
+  return stages == 2 ? launch_s<TN, 2, PK>(a, grid, st) : launch_s<TN, 3, PK>(a, grid, st);
+}
+
+hipError_t launch_kernel(const GemmArgs& a, const GemmShape& s, bool precise, int grid, hipStream_t st) {
+  const bool pk = a.packed != 0;
+  const int tn = s.tn;
+  if (precise) {
+    if (tn == 1) return pk ? launch_s_ring<1, true>(a, s.stages, grid, st) : launch_s_ring<1, false>(a, s.stages, grid, st);
+    return pk ? launch_s_ring<2, true>(a, s.stages, grid, st) : launch_s_ring<2, false>(a, s.stages, grid, st);
+  }
+  if (tn == 1) return pk ? launch_p<1, true>(a, grid, st) : launch_p<1, false>(a, grid, st);
+  if (tn == 2) return pk ? launch_p<2, true>(a, grid, st) : launch_p<2, false>(a, grid, st);
+  return pk ? launch_p<4, true>(a, grid, st) : launch_p<4, false>(a, grid, st);
 }
 
 }  // namespace
@@ -887,7 +948,7 @@ hipError_t gemm_launch(const GemmArgs& a_in, int num_cus, hipStream_t st, int* s
   if (s.splits > 1 && !a.part) return hipErrorInvalidValue;
   const long long grid = (long long)((a.M + 127) / 128) * ((a.N + 32 * s.tn - 1) / (32 * s.tn)) * s.splits;
   if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
-  hipError_t e = precise ? launch_fmt<true>(a, s.tn, (int)grid, st) : launch_fmt<false>(a, s.tn, (int)grid, st);
+  hipError_t e = launch_kernel(a, s, precise, (int)grid, st);
   if (splits_left) *splits_left = 0;
   if (e != hipSuccess || s.splits == 1) return e;
   if (splits_left) {  // the caller folds the partials into its next kernel
