@@ -23,7 +23,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIP_SOURCES = ["chatnet_api.hip", "gemv.hip", "gemv_float.hip", "gemm.hip", "prefill.hip", "decode_ops.hip", "sample.hip"]
 HIP_HEADERS = ["device_common.h", "gemv_common.h", "kernels.h"]
-PROBES = ["probe_chain_floor", "probe_grid_handoff"]
+PROBES = ["probe_chain_floor", "probe_grid_handoff", "probe_span_gemm"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
