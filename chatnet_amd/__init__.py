@@ -1,7 +1,9 @@
 """chatnet_amd — MI355X-native quantized Llama forward pass for ChatNet.
 
-The hot path of ChatNet (LlamaModel.Forward with the Q4_0 / Q8_0 / Q4_K /
-Q5_K / Q6_K dequant-matvecs, and the Mistral and Qwen2 variants of it) as hand-written gfx950 HIP kernels behind a C ABI
+The hot path of ChatNet (LlamaModel.Forward with the dequant-matvecs of every
+weight type it dispatches, F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0 and Q2_K ..
+Q8_K, and the Mistral and Qwen2 variants of it) as hand-written gfx950 HIP
+kernels behind a C ABI
 (libchatnet_hip.so, include/chatnet_hip.h).  Python here is a thin host:
 ctypes bindings, the IModel-shaped wrapper and the synthetic-weight tools.
 """

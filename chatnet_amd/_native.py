@@ -28,6 +28,12 @@ GGML_Q8_0 = 8
 GGML_Q4_K = 12
 GGML_Q5_K = 13
 GGML_Q6_K = 14
+GGML_Q4_1 = 3
+GGML_Q5_0 = 6
+GGML_Q5_1 = 7
+GGML_Q2_K = 10
+GGML_Q3_K = 11
+GGML_Q8_K = 15
 
 KV_F32 = 0
 KV_F16 = 1

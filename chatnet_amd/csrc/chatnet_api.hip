@@ -73,11 +73,29 @@ int device_cus(int dev) {
   return p.multiProcessorCount;
 }
 
-// Weight types the GEMV serves (LlamaModel.MatVecMulByType, LlamaModel.cs:470-567).
+// Weight types the GEMV serves (LlamaModel.MatVecMulByType, LlamaModel.cs:470-567):
+// F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K from the stored blocks, and Q4_1,
+// Q5_0, Q5_1, Q2_K, Q3_K, Q8_K (the reference's MatVecMulGeneric branches,
+// LlamaModel.cs:488-511, 517-528) from packed units made at upload.
 bool is_matrix_type(uint32_t t) {
   return t == CHATNET_GGML_F32 || t == CHATNET_GGML_F16 || t == CHATNET_GGML_Q4_0 || t == CHATNET_GGML_Q8_0 ||
-         t == CHATNET_GGML_Q4_K || t == CHATNET_GGML_Q5_K || t == CHATNET_GGML_Q6_K;
+         t == CHATNET_GGML_Q4_K || t == CHATNET_GGML_Q5_K || t == CHATNET_GGML_Q6_K || gemv_needs_pack((int)t);
 }
+
+// Embedding rows read in their stored form; every other block type is
+// gathered from packed units made at upload.
+bool embed_raw_type(uint32_t t) {
+  return t == CHATNET_GGML_F32 || t == CHATNET_GGML_F16 || t == CHATNET_GGML_Q4_0 || t == CHATNET_GGML_Q8_0;
+}
+
+// A matrix as the GEMV reads it: its packed units for the types the GEMV
+// takes only in that form, else the stored blocks.
+int gemv_qt(const DevTensor& t) { return gemv_needs_pack((int)t.type) ? kGemvPacked : (int)t.type; }
+const uint8_t* gemv_w(const DevTensor& t) {
+  return (const uint8_t*)(gemv_needs_pack((int)t.type) ? t.pk : t.ptr);
+}
+int embed_qt(const DevTensor& t) { return embed_raw_type(t.type) ? (int)t.type : kGemvPacked; }
+const void* embed_w(const DevTensor& t) { return embed_raw_type(t.type) ? t.ptr : t.pk; }
 
 // Workspace of chatnet_matmul's batched path (bf16 copy of x + K-split
 // partials), one per (device, stream): work queued on one stream runs in
@@ -424,7 +442,7 @@ void chatnet_destroy(chatnet_model* m) {
   if (m->stream) (void)hipStreamSynchronize(m->stream);
   drop_graphs(m);
   auto fr = [](void* p) { if (p) (void)hipFree(p); };
-  fr(m->emb.ptr); fr(m->out.ptr); fr(m->out_norm.ptr);
+  fr(m->emb.ptr); fr(m->out.ptr); fr(m->out_norm.ptr); fr(m->emb.pk); fr(m->out.pk);
   for (auto& l : m->layers) {
     fr(l.attn_norm.ptr); fr(l.ffn_norm.ptr); fr(l.wq.ptr); fr(l.wk.ptr); fr(l.wv.ptr);
     fr(l.wo.ptr); fr(l.wg.ptr); fr(l.wu.ptr); fr(l.wd.ptr); fr(l.bias);
@@ -462,9 +480,10 @@ int chatnet_upload_tensor(chatnet_model* m, const char* name, uint32_t type, con
   char suffix[64] = {0};
   if (!strcmp(name, "token_embd.weight")) {
     slot = &m->emb; want0 = c.dim; want1 = c.vocab_size; matrix = false;
-    if (type != CHATNET_GGML_F32 && type != CHATNET_GGML_F16 && type != CHATNET_GGML_Q4_0 && type != CHATNET_GGML_Q8_0)
-      return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "token_embd.weight: type %u not supported (F32, F16, Q4_0, Q8_0)",
-                  type);
+    if (!embed_raw_type(type) && !gemm_pack_supports((int)type, 256))
+      return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "token_embd.weight: type %u not supported", type);
+    if (!embed_raw_type(type) && !gemm_pack_supports((int)type, c.dim))
+      return fail(CHATNET_ERR_INVALID_ARG, "token_embd.weight: dim %d not a multiple of the type's block", c.dim);
     if ((type == CHATNET_GGML_Q4_0 || type == CHATNET_GGML_Q8_0) && c.dim % 32 != 0)
       return fail(CHATNET_ERR_INVALID_ARG, "token_embd.weight: dim %d not a multiple of 32", c.dim);
   } else if (!strcmp(name, "output.weight")) {
@@ -500,7 +519,9 @@ int chatnet_upload_tensor(chatnet_model* m, const char* name, uint32_t type, con
   if (matrix) {
     if (!is_matrix_type(type))
       return fail(CHATNET_ERR_UNSUPPORTED_TYPE,
-                  "tensor %s: weight type %u not supported (F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K)", name, type);
+                  "tensor %s: weight type %u not supported (F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, "
+                  "Q4_K, Q5_K, Q6_K, Q8_K)",
+                  name, type);
     if (!gemv_supports((int)type, (int)ne0))
       return fail(CHATNET_ERR_INVALID_ARG, "tensor %s: inner dim %llu not a multiple of the block", name,
                   (unsigned long long)ne0);
@@ -534,6 +555,18 @@ int chatnet_upload_tensor(chatnet_model* m, const char* name, uint32_t type, con
   slot->nbytes = nbytes;
   slot->ne0 = ne0;
   slot->ne1 = ne1;
+  // Types the GEMV (or the embedding gather) reads only as packed units are
+  // packed now, one pass over the uploaded rows; the stored blocks stay for
+  // the other readers.
+  if ((matrix && gemv_needs_pack((int)type)) || (slot == &m->emb && !embed_raw_type(type))) {
+    const size_t pk_bytes = gemm_pack_bytes((int)ne1, (int)ne0);
+    if (hipMalloc(&slot->pk, pk_bytes) != hipSuccess) {
+      slot->pk = nullptr;
+      return fail(CHATNET_ERR_OUT_OF_MEMORY, "hipMalloc of %zu bytes (packed %s) failed", pk_bytes, name);
+    }
+    HIP_TRY(gemm_pack_launch((int)type, slot->ptr, (int)ne1, (int)ne0, slot->pk, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+  }
   drop_graphs(m);
   g_err.clear();
   return CHATNET_OK;
@@ -593,7 +626,7 @@ int launch_token(chatnet_model* m, bool lm_head, int cap, bool decode = false) {
   const chatnet_config& c = m->cfg;
   hipStream_t st = m->stream;
   const int kvd = m->kv_dim;
-  HIP_TRY(embed_launch(m->emb.ptr, (int)m->emb.type, c.dim, m->state + 1, m->x, st));
+  HIP_TRY(embed_launch(embed_w(m->emb), embed_qt(m->emb), c.dim, m->state + 1, m->x, st));
   for (int l = 0; l < c.n_layers; l++) {
     const Layer& L = m->layers[l];
     const size_t loff = (size_t)l * c.context_length * kvd * m->kv_elt;
@@ -606,26 +639,26 @@ int launch_token(chatnet_model* m, bool lm_head, int cap, bool decode = false) {
     a.vcache = (char*)m->vcache + loff;
     a.bias = L.bias_have ? L.bias : nullptr;  // QwenModel.cs:104-120
     if (L.wq.type == L.wk.type && L.wk.type == L.wv.type) {
-      a.w[0] = (const uint8_t*)L.wq.ptr;
-      a.w[1] = (const uint8_t*)L.wk.ptr;
-      a.w[2] = (const uint8_t*)L.wv.ptr;
+      a.w[0] = gemv_w(L.wq);
+      a.w[1] = gemv_w(L.wk);
+      a.w[2] = gemv_w(L.wv);
       a.seg_rows[0] = c.dim;
       a.seg_rows[1] = kvd;
       a.seg_rows[2] = kvd;
       a.n_vrows = c.dim + 2 * kvd;
-      HIP_TRY(gemv_launch((int)L.wq.type, GEMV_EPI_QKV, a, m->num_cus, st));
+      HIP_TRY(gemv_launch(gemv_qt(L.wq), GEMV_EPI_QKV, a, m->num_cus, st));
     } else {
       const DevTensor* ts[3] = {&L.wq, &L.wk, &L.wv};
       const int rows[3] = {c.dim, kvd, kvd};
       for (int s = 0; s < 3; s++) {
         GemvArgs b = a;
-        b.w[0] = b.w[1] = b.w[2] = (const uint8_t*)ts[s]->ptr;
+        b.w[0] = b.w[1] = b.w[2] = gemv_w(*ts[s]);
         b.seg_rows[0] = s == 0 ? rows[0] : 0;
         b.seg_rows[1] = s == 1 ? rows[1] : 0;
         b.seg_rows[2] = s == 2 ? rows[2] : 0;
         b.n_vrows = rows[s];
         if (b.bias) b.bias += s == 0 ? 0 : c.dim + (s == 2 ? kvd : 0);
-        HIP_TRY(gemv_launch((int)ts[s]->type, GEMV_EPI_QKV, b, m->num_cus, st));
+        HIP_TRY(gemv_launch(gemv_qt(*ts[s]), GEMV_EPI_QKV, b, m->num_cus, st));
       }
     }
     AttnArgs at;
@@ -654,7 +687,7 @@ int launch_token(chatnet_model* m, bool lm_head, int cap, bool decode = false) {
     GemvArgs o = base_args(m, decode);
     o.K = c.dim;
     o.x = m->att;
-    o.w[0] = (const uint8_t*)L.wo.ptr;
+    o.w[0] = gemv_w(L.wo);
     o.seg_rows[0] = c.dim;
     o.n_vrows = c.dim;
     o.out[0] = m->x;
@@ -665,31 +698,31 @@ int launch_token(chatnet_model* m, bool lm_head, int cap, bool decode = false) {
       o.msplits = plan.splits;
       o.mchunk = plan.chunk;
     }
-    HIP_TRY(gemv_launch((int)L.wo.type, fold ? GEMV_EPI_ADD_MERGE : GEMV_EPI_ADD, o, m->num_cus, st));
+    HIP_TRY(gemv_launch(gemv_qt(L.wo), fold ? GEMV_EPI_ADD_MERGE : GEMV_EPI_ADD, o, m->num_cus, st));
 
     GemvArgs g = base_args(m, decode);
     g.K = c.dim;
     g.x = m->x;
     g.norm_w = (const float*)L.ffn_norm.ptr;
     if (L.wg.type == L.wu.type) {  // one launch, gate and up rows interleaved
-      g.w[0] = (const uint8_t*)L.wg.ptr;
-      g.w[1] = (const uint8_t*)L.wu.ptr;
+      g.w[0] = gemv_w(L.wg);
+      g.w[1] = gemv_w(L.wu);
       g.seg_rows[0] = c.hidden_dim;
       g.seg_rows[1] = c.hidden_dim;
       g.n_vrows = 2 * c.hidden_dim;
       g.out[0] = m->h;
-      HIP_TRY(gemv_launch((int)L.wg.type, GEMV_EPI_SWIGLU, g, m->num_cus, st));
+      HIP_TRY(gemv_launch(gemv_qt(L.wg), GEMV_EPI_SWIGLU, g, m->num_cus, st));
     } else {
       // gate and up of different types (each dispatched on its own type,
       // LlamaModel.cs:175-179): two normed GEMVs, then SiLU(gate) * up
       const DevTensor* ts[2] = {&L.wg, &L.wu};
       for (int s = 0; s < 2; s++) {
         GemvArgs b = g;
-        b.w[0] = b.w[1] = b.w[2] = (const uint8_t*)ts[s]->ptr;
+        b.w[0] = b.w[1] = b.w[2] = gemv_w(*ts[s]);
         b.seg_rows[0] = c.hidden_dim;
         b.n_vrows = c.hidden_dim;
         b.out[0] = m->gu + (size_t)s * c.hidden_dim;
-        HIP_TRY(gemv_launch((int)ts[s]->type, GEMV_EPI_LOGITS, b, m->num_cus, st));
+        HIP_TRY(gemv_launch(gemv_qt(*ts[s]), GEMV_EPI_LOGITS, b, m->num_cus, st));
       }
       HIP_TRY(silu_mul_launch(m->gu, m->gu + c.hidden_dim, m->h, c.hidden_dim, st));
     }
@@ -697,22 +730,22 @@ int launch_token(chatnet_model* m, bool lm_head, int cap, bool decode = false) {
     GemvArgs d = base_args(m, decode);
     d.K = c.hidden_dim;
     d.x = m->h;
-    d.w[0] = (const uint8_t*)L.wd.ptr;
+    d.w[0] = gemv_w(L.wd);
     d.seg_rows[0] = c.dim;
     d.n_vrows = c.dim;
     d.out[0] = m->x;
-    HIP_TRY(gemv_launch((int)L.wd.type, GEMV_EPI_ADD, d, m->num_cus, st));
+    HIP_TRY(gemv_launch(gemv_qt(L.wd), GEMV_EPI_ADD, d, m->num_cus, st));
   }
   if (lm_head) {
     GemvArgs o = base_args(m, decode);  // final RMSNorm fused (LlamaModel.cs:203-213)
     o.K = c.dim;
     o.x = m->x;
     o.norm_w = (const float*)m->out_norm.ptr;
-    o.w[0] = (const uint8_t*)lm_head_tensor(m).ptr;
+    o.w[0] = gemv_w(lm_head_tensor(m));
     o.seg_rows[0] = c.vocab_size;
     o.n_vrows = c.vocab_size;
     o.out[0] = m->logits;
-    HIP_TRY(gemv_launch((int)lm_head_tensor(m).type, GEMV_EPI_LOGITS, o, m->num_cus, st));
+    HIP_TRY(gemv_launch(gemv_qt(lm_head_tensor(m)), GEMV_EPI_LOGITS, o, m->num_cus, st));
   }
   return CHATNET_OK;
 }
@@ -843,7 +876,7 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position, SpanM
     const int cn = n - s0 < m->span_cap ? n - s0 : m->span_cap;
     const int p0 = position + s0;
     HIP_TRY(hipMemcpyAsync(m->sp_tok, tokens + s0, sizeof(int) * cn, hipMemcpyHostToDevice, st));
-    HIP_TRY(embed_launch(m->emb.ptr, (int)m->emb.type, c.dim, m->sp_tok, m->sp_x, st, cn));
+    HIP_TRY(embed_launch(embed_w(m->emb), embed_qt(m->emb), c.dim, m->sp_tok, m->sp_x, st, cn));
     for (int l = 0; l < c.n_layers; l++) {
       const Layer& L = m->layers[l];
       const size_t loff = (size_t)l * c.context_length * kvd * m->kv_elt;
@@ -975,11 +1008,11 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position, SpanM
   o.K = c.dim;
   o.x = m->sp_x + (size_t)(last_rows - 1) * c.dim;
   o.norm_w = (const float*)m->out_norm.ptr;
-  o.w[0] = (const uint8_t*)lm_head_tensor(m).ptr;
+  o.w[0] = gemv_w(lm_head_tensor(m));
   o.seg_rows[0] = c.vocab_size;
   o.n_vrows = c.vocab_size;
   o.out[0] = m->logits;
-  HIP_TRY(gemv_launch((int)lm_head_tensor(m).type, GEMV_EPI_LOGITS, o, m->num_cus, st));
+  HIP_TRY(gemv_launch(gemv_qt(lm_head_tensor(m)), GEMV_EPI_LOGITS, o, m->num_cus, st));
   m->have_logits = true;
   m->next_pos = position + n;
   m->last_tok = tokens[n - 1];
@@ -1017,14 +1050,19 @@ int matmul_impl(uint32_t type, const void* w_dev, const float* x_dev, float* y_d
   const int cus = device_cus(dev);
   hipStream_t st = (hipStream_t)stream;
   // Q4_0 reads its raw blocks; the other block types (not in the no-allocation
-  // variant) are packed into the workspace first, one pass over W.
+  // variant) are packed into the workspace first, one pass over W.  The types
+  // the GEMV reads only as packed units are packed for every N, in both
+  // variants.
   const bool raw = gemm_supports((int)type, K);
-  const bool pack = !raw && !noalloc && gemm_pack_supports((int)type, K);
-  if (N >= 8 && (raw || pack)) {
-    // x -> bf16 into the scratch, then the MFMA GEMM (K-split partials after x,
-    // packed W after those).
-    const size_t xb_bytes = ((size_t)N * K * sizeof(uint16_t) + 255) & ~(size_t)255;
-    const size_t part_bytes = (gemm_workspace_bytes(M, N, K, cus, false, pack) + 255) & ~(size_t)255;
+  const bool must_pack = gemv_needs_pack((int)type);
+  const bool batched = N >= 8 && (raw || must_pack || (!noalloc && gemm_pack_supports((int)type, K)));
+  const bool pack = must_pack || (batched && !raw);
+  const uint8_t* wp = (const uint8_t*)w_dev;
+  if (batched || pack) {
+    // [bf16 x | K-split partials | packed W], the first two for the batched path only
+    const size_t xb_bytes = batched ? ((size_t)N * K * sizeof(uint16_t) + 255) & ~(size_t)255 : 0;
+    const size_t part_bytes =
+        batched ? (gemm_workspace_bytes(M, N, K, cus, false, pack) + 255) & ~(size_t)255 : 0;
     const size_t pack_bytes = pack ? gemm_pack_bytes(M, K) : 0;
     const size_t need = xb_bytes + part_bytes + pack_bytes;
     char* ws = nullptr;
@@ -1039,38 +1077,44 @@ int matmul_impl(uint32_t type, const void* w_dev, const float* x_dev, float* y_d
       rc = matmul_workspace(dev, st, need, &ws);
     }
     if (rc) return rc;
-    HIP_TRY(to_bf16_launch(x_dev, (uint16_t*)ws, (size_t)N * K, st));
-    if (pack) HIP_TRY(gemm_pack_launch((int)type, w_dev, M, K, ws + xb_bytes + part_bytes, st));
-    GemmArgs g;
-    memset(&g, 0, sizeof(g));
-    g.qtype = (int)type;
-    g.packed = pack;
-    const uint8_t* wp = pack ? (const uint8_t*)(ws + xb_bytes + part_bytes) : (const uint8_t*)w_dev;
-    g.w[0] = g.w[1] = g.w[2] = wp;
-    g.seg_rows[0] = M;
-    g.seg_mode = GEMM_SEG_SINGLE;
-    g.M = M;
-    g.K = K;
-    g.N = N;
-    g.xb = (const uint16_t*)ws;
-    g.epi = GEMV_EPI_STORE;
-    g.y = y_dev;
-    g.ldy = M;
-    g.part = part_bytes ? (float*)(ws + xb_bytes) : nullptr;
-    HIP_TRY(gemm_launch(g, cus, st));
-    g_err.clear();
-    return CHATNET_OK;
+    if (pack) {
+      HIP_TRY(gemm_pack_launch((int)type, w_dev, M, K, ws + xb_bytes + part_bytes, st));
+      wp = (const uint8_t*)(ws + xb_bytes + part_bytes);
+    }
+    if (batched) {
+      // x -> bf16 into the scratch, then the MFMA GEMM
+      HIP_TRY(to_bf16_launch(x_dev, (uint16_t*)ws, (size_t)N * K, st));
+      GemmArgs g;
+      memset(&g, 0, sizeof(g));
+      g.qtype = (int)type;
+      g.packed = pack;
+      g.w[0] = g.w[1] = g.w[2] = wp;
+      g.seg_rows[0] = M;
+      g.seg_mode = GEMM_SEG_SINGLE;
+      g.M = M;
+      g.K = K;
+      g.N = N;
+      g.xb = (const uint16_t*)ws;
+      g.epi = GEMV_EPI_STORE;
+      g.y = y_dev;
+      g.ldy = M;
+      g.part = part_bytes ? (float*)(ws + xb_bytes) : nullptr;
+      HIP_TRY(gemm_launch(g, cus, st));
+      g_err.clear();
+      return CHATNET_OK;
+    }
   }
-  for (int n = 0; n < N; n++) {  // one fused GEMV per column, no scratch
+  const int qt = pack ? kGemvPacked : (int)type;
+  for (int n = 0; n < N; n++) {  // one fused GEMV per column
     GemvArgs a;
     memset(&a, 0, sizeof(a));
-    a.w[0] = a.w[1] = a.w[2] = (const uint8_t*)w_dev;
+    a.w[0] = a.w[1] = a.w[2] = wp;
     a.seg_rows[0] = M;
     a.n_vrows = M;
     a.K = K;
     a.x = x_dev + (size_t)n * K;
     a.out[0] = y_dev + (size_t)n * M;
-    HIP_TRY(gemv_launch((int)type, GEMV_EPI_STORE, a, cus, st));
+    HIP_TRY(gemv_launch(qt, GEMV_EPI_STORE, a, cus, st));
   }
   g_err.clear();
   return CHATNET_OK;

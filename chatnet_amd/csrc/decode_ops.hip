@@ -9,14 +9,22 @@ namespace {
 static __device__ int g_never_stop = 0;
 
 // LlamaModel.LoadEmbedding (LlamaModel.cs:365-394): F32 row copy, F16
-// per-element conversion, Q4_0 row dequantization (DequantQ4_0.cs:28-58).
+// per-element conversion, Q4_0 / Q8_0 row dequantization (DequantQ4_0.cs:28-58,
+// DequantQ8_0.cs:19-41), and every other block type through its packed units
+// (type kGemvPacked: fmaf(code, scale, offset), the type's dequantized value,
+// the generic branch at LlamaModel.cs:384-393).
 __global__ __launch_bounds__(CN_BLOCK) void embed_kernel(const void* emb, int type, int dim,
                                                          const int* tok, float* x) {
   const int t = tok[blockIdx.y];
   x += (size_t)blockIdx.y * dim;
   const int i = blockIdx.x * CN_BLOCK + threadIdx.x;
   if (i >= dim) return;
-  if (type == 0) {
+  if (type == kGemvPacked) {
+    const uint8_t* u = reinterpret_cast<const uint8_t*>(emb) + ((size_t)t * (dim / 64) + i / 64) * kGemmPackUnit;
+    const float* sc = reinterpret_cast<const float*>(u + 64);
+    const int g = (i & 63) >> 4;
+    x[i] = fmaf((float)u[i & 63], sc[g], sc[4 + g]);
+  } else if (type == 0) {
     x[i] = reinterpret_cast<const float*>(emb)[(size_t)t * dim + i];
   } else if (type == 1) {
     const uint16_t* e = reinterpret_cast<const uint16_t*>(emb);

@@ -698,13 +698,22 @@ __global__ __launch_bounds__(CN_BLOCK) void add_rmsnorm_bf16_kernel(float* __res
 // one pair per 16 weights).  Each block type's dequantized value is
 // fmaf(code, scale, offset) with one rounding, as the reference rounds it:
 //   Q4_0 (DequantQ4_0.cs)  code q,      scale d,        offset -8d
+//   Q4_1 (DequantQ4_1.cs)  code q,      scale d,        offset m
+//   Q5_0 (DequantQ5_0.cs)  code q5,     scale d,        offset -16d
+//   Q5_1 (DequantQ5_1.cs)  code q5,     scale d,        offset m
 //   Q8_0 (DequantQ8_0.cs)  code q+128,  scale d,        offset -128d
+//   Q2_K (DequantQ2K.cs)   code q,      scale d*sc,     offset -(dmin*m)
+//   Q3_K (DequantQ3K.cs)   code q3,     scale d*sc,     offset -4*d*sc
 //   Q4_K (DequantQ4K.cs)   code q,      scale d*sc[s],  offset -(dmin*m[s])
 //   Q5_K (DequantQ5K.cs)   code q5,     scale d*sc[s],  offset -(dmin*m[s])
 //   Q6_K (DequantQ6K.cs)   code q+32,   scale d*sc[i],  offset -32*d*sc[i]
+//   Q8_K (DequantQ8K.cs)   code q+128,  scale d (fp32), offset -128d
 // (d*sc, dmin*m and the power-of-two multiples are exact in fp32, and so is
-// code*scale for Q4_0, Q8_0, Q4_K and Q5_K; Q6_K's (d*sc)*q is rounded once
-// either way).  Sub-block layouts: Q4_K / Q5_K sub-block s of a super-block
+// code*scale for the fp16-scaled types, so their one rounding is the
+// reference's final add (or none); Q6_K's (d*sc)*q and Q8_K's q*d are rounded
+// once either way).  Q2_K and Q3_K elements follow the reference's layouts
+// (DequantQ2K.cs:55-82: element 128g + 32t + 16h + l is bits 2t.. of qs[32g +
+// 16h + l] with scale byte 8g + 2t + h; DequantQ3K.cs:52-63, :122-150).  Sub-block layouts: Q4_K / Q5_K sub-block s of a super-block
 // holds its 32 weights in the reference's order (elements 0..15 are the
 // low nibbles of qs[16s..16s+15], 16..31 the high ones), Q6_K as
 // DequantQ6K.Dequantize (DequantQ6K.cs:37-88).
@@ -773,6 +782,67 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_pack_kernel(int qtype, const ui
       }
       sc[2 * b] = sc[2 * b + 1] = d * (float)sv;
       of[2 * b] = of[2 * b + 1] = -(dmin * (float)mv);
+    }
+  } else if (qtype == 3 || qtype == 6 || qtype == 7) {  // Q4_1 / Q5_0 / Q5_1: blocks 2c and 2c+1 of 32
+    const int bb = qtype == 3 ? 20 : (qtype == 6 ? 22 : 24);
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+      const uint8_t* blk = row + (size_t)(2 * c + b) * bb;
+      const float d = h2f_at(blk);
+      const uint8_t* qs = blk + bb - 16;
+      uint32_t qh = 0;
+      if (qtype != 3) {
+        const uint8_t* h = blk + (qtype == 6 ? 2 : 4);
+        qh = (uint32_t)h[0] | ((uint32_t)h[1] << 8) | ((uint32_t)h[2] << 16) | ((uint32_t)h[3] << 24);
+      }
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
+        const uint32_t nib = j < 16 ? (qs[j] & 15u) : (uint32_t)(qs[j - 16] >> 4);
+        put(32 * b + j, nib | (((qh >> j) & 1u) << 4));
+      }
+      sc[2 * b] = sc[2 * b + 1] = d;
+      of[2 * b] = of[2 * b + 1] = qtype == 6 ? -16.0f * d : (qtype == 3 || qtype == 7 ? h2f_at(blk + 2) : 0.f);
+    }
+  } else if (qtype == 10) {  // Q2_K: elements 64(c%4) .. +63 of the super-block
+    const uint8_t* blk = row + (size_t)(c >> 2) * 84;
+    const float d = h2f_at(blk + 80), dmin = h2f_at(blk + 82);
+#pragma unroll
+    for (int j = 0; j < 64; j++) {
+      const int e = 64 * (c & 3) + j, g = e >> 7, t = (e & 127) >> 5, h = (e & 31) >> 4, l = e & 15;
+      put(j, (uint32_t)(blk[16 + 32 * g + 16 * h + l] >> (2 * t)) & 3u);
+      if ((j & 15) == 0) {
+        const uint8_t sb = blk[8 * g + 2 * t + h];
+        sc[j >> 4] = d * (float)(sb & 15);
+        of[j >> 4] = -(dmin * (float)(sb >> 4));
+      }
+    }
+  } else if (qtype == 11) {  // Q3_K: elements 64(c%4) .. +63 of the super-block
+    const uint8_t* blk = row + (size_t)(c >> 2) * 110;
+    const float d = h2f_at(blk + 108);
+    const uint8_t* s = blk + 96;
+#pragma unroll
+    for (int j = 0; j < 64; j++) {
+      const int e = 64 * (c & 3) + j;
+      const uint32_t q2 = (blk[32 + e / 4] >> (2 * (e % 4))) & 3u, hb = (blk[e / 8] >> (e % 8)) & 1u;
+      put(j, q2 | (hb << 2));
+      if ((j & 15) == 0) {
+        const int i = e >> 4;  // the sub-block's 6-bit scale, stored + 32
+        const int lo = i < 8 ? (s[i] & 15) : (s[i - 8] >> 4);
+        const int v = (lo | (((s[8 + (i & 3)] >> (2 * (i >> 2))) & 3) << 4)) - 32;
+        sc[j >> 4] = d * (float)v;
+        of[j >> 4] = -4.0f * sc[j >> 4];
+      }
+    }
+  } else if (qtype == 15) {  // Q8_K: elements 64(c%4) .. +63 of the super-block
+    const uint8_t* blk = row + (size_t)(c >> 2) * 292;
+    float d;
+    __builtin_memcpy(&d, blk, 4);
+#pragma unroll
+    for (int j = 0; j < 64; j++) put(j, (uint32_t)blk[4 + 64 * (c & 3) + j] ^ 0x80u);
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      sc[g] = d;
+      of[g] = -128.0f * d;
     }
   } else {  // Q6_K: elements 64(c%4) .. +63 of the super-block
     const uint8_t* blk = row + (size_t)(c >> 2) * 210;
@@ -904,8 +974,8 @@ bool gemm_supports(int qtype, int K) { return qtype == 2 && K > 0 && K % 64 == 0
 
 bool gemm_pack_supports(int qtype, int K) {
   if (K <= 0) return false;
-  if (qtype == 2 || qtype == 8) return K % 64 == 0;
-  if (qtype == 12 || qtype == 13 || qtype == 14) return K % 256 == 0;
+  if (qtype == 2 || qtype == 3 || qtype == 6 || qtype == 7 || qtype == 8) return K % 64 == 0;
+  if (qtype == 10 || qtype == 11 || qtype == 12 || qtype == 13 || qtype == 14 || qtype == 15) return K % 256 == 0;
   return false;
 }
 
@@ -916,9 +986,15 @@ hipError_t gemm_pack_launch(int qtype, const void* w, int M, int K, void* dst, h
   size_t row_bytes;
   switch (qtype) {
     case 2: row_bytes = (size_t)K / 32 * 18; break;
+    case 3: row_bytes = (size_t)K / 32 * 20; break;
+    case 6: row_bytes = (size_t)K / 32 * 22; break;
+    case 7: row_bytes = (size_t)K / 32 * 24; break;
     case 8: row_bytes = (size_t)K / 32 * 34; break;
+    case 10: row_bytes = (size_t)K / 256 * 84; break;
+    case 11: row_bytes = (size_t)K / 256 * 110; break;
     case 12: row_bytes = (size_t)K / 256 * 144; break;
     case 13: row_bytes = (size_t)K / 256 * 176; break;
+    case 15: row_bytes = (size_t)K / 256 * 292; break;
     default: row_bytes = (size_t)K / 256 * 210; break;
   }
   const long long n = (long long)M * (K / 64);

@@ -1242,12 +1242,25 @@ bool gemv_supports(int qtype, int K) {
     case QT_Q4_K:
     case QT_Q5_K:
     case QT_Q6_K: return K > 0 && K % 256 == 0 && K <= 16384;
+    // served as packed units (gemv_launch with kGemvPacked)
+    case 3:   // Q4_1
+    case 6:   // Q5_0
+    case 7: return K > 0 && K % 64 == 0 && K <= 16384;  // Q5_1
+    case 10:  // Q2_K
+    case 11:  // Q3_K
+    case 15: return K > 0 && K % 256 == 0 && K <= 16384;  // Q8_K
     default: return false;
   }
 }
 
+bool gemv_needs_pack(int qtype) {
+  return qtype == 3 || qtype == 6 || qtype == 7 || qtype == 10 || qtype == 11 || qtype == 15;
+}
+
 hipError_t gemv_launch(int qtype, int epi, const GemvArgs& a, int num_cus, hipStream_t st) {
-  if (qtype == 0 || qtype == 1) return gemv_float_launch(qtype, epi, a, num_cus, st);
+  if (qtype == 0 || qtype == 1 || qtype == kGemvPacked) return gemv_float_launch(qtype, epi, a, num_cus, st);
+  if (qtype != QT_Q4_0 && qtype != QT_Q8_0 && qtype != QT_Q4_K && qtype != QT_Q5_K && qtype != QT_Q6_K)
+    return hipErrorInvalidValue;  // the packed-unit types are launched as kGemvPacked
   switch (epi) {
     case GEMV_EPI_STORE: return launch_epi<GEMV_EPI_STORE>(qtype, a, num_cus, st);
     case GEMV_EPI_ADD: return launch_epi<GEMV_EPI_ADD>(qtype, a, num_cus, st);

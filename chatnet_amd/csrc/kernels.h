@@ -47,8 +47,13 @@ struct GemvArgs {
 };
 
 // Weight types: Q4_0, Q8_0 (K % 64 == 0), Q4_K, Q5_K, Q6_K (K % 256 == 0), and
-// F32 / F16 (K % 64 == 0, gemv_float.hip); K <= 16384.
+// F32 / F16 (K % 64 == 0, gemv_float.hip); K <= 16384.  gemv_float_launch
+// also takes kGemvPacked: w[] holding packed units (gemm_pack_launch), how the
+// model runs Q4_1, Q5_0, Q5_1 (K % 64 == 0), Q2_K, Q3_K and Q8_K (K % 256 == 0).
+constexpr int kGemvPacked = -1;
 bool gemv_supports(int qtype, int K);
+// True for the types gemv_supports accepts only as packed units.
+bool gemv_needs_pack(int qtype);
 size_t gemv_lds_bytes(int qtype, int K);
 hipError_t gemv_launch(int qtype, int epi, const GemvArgs& a, int num_cus, hipStream_t st);
 hipError_t gemv_float_launch(int qtype, int epi, const GemvArgs& a, int num_cus, hipStream_t st);
@@ -139,7 +144,9 @@ bool attn_prefill_supports(int head_dim, int kv_mul);
 hipError_t attn_prefill_launch(const PrefillAttnArgs& a, hipStream_t st);
 
 // Embedding row gather (LlamaModel.LoadEmbedding, LlamaModel.cs:365-394) of
-// n tokens read from device memory: x[i] = row tok[i].
+// n tokens read from device memory: x[i] = row tok[i].  type: F32, F16, Q4_0,
+// Q8_0 on the stored rows, or kGemvPacked on the packed units of any other
+// block type (dim % 64 == 0).
 hipError_t embed_launch(const void* emb, int type, int dim, const int* tok, float* x, hipStream_t st,
                         int n = 1);
 

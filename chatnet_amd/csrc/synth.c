@@ -309,6 +309,175 @@ static void quant_block_q5_k(const float* w, uint8_t* out) {
   }
 }
 
+/* Q4_1: d = (max - min) / 15, m = min (both fp16), q = round((w - m) / d)
+ * clamped to [0, 15]; element j < 16 in the low nibble of qs[j], 16 + j in the
+ * high nibble. */
+static void quant_block_q4_1(const float* w, uint8_t* out) {
+  float lo = w[0], hi = w[0];
+  for (int j = 1; j < 32; j++) {
+    if (w[j] < lo) lo = w[j];
+    if (w[j] > hi) hi = w[j];
+  }
+  uint16_t dh = chatnet_float_to_half((hi - lo) / 15.0f), mh = chatnet_float_to_half(lo);
+  float d = half_to_float(dh), m = half_to_float(mh), id = d != 0.f ? 1.0f / d : 0.f;
+  put16(out, dh);
+  put16(out + 2, mh);
+  for (int j = 0; j < 16; j++) {
+    int q0 = nearest_int((w[j] - m) * id), q1 = nearest_int((w[16 + j] - m) * id);
+    q0 = q0 < 0 ? 0 : (q0 > 15 ? 15 : q0);
+    q1 = q1 < 0 ? 0 : (q1 > 15 ? 15 : q1);
+    out[4 + j] = (uint8_t)(q0 | (q1 << 4));
+  }
+}
+
+/* Q5_0 / Q5_1: 5-bit quants, the low nibble in qs (Q4_0's order) and bit 4
+ * of element j in bit j of the little-endian qh word.  Q5_0: d = amax / -16
+ * (sign of the largest-magnitude element kept), q = round(w/d) + 16 in
+ * [0, 31]; Q5_1: d = (max - min) / 31, m = min, q = round((w - m) / d). */
+static void put_q5(const int* q, uint8_t* qh, uint8_t* qs) {
+  uint32_t h = 0;
+  for (int j = 0; j < 16; j++) qs[j] = (uint8_t)((q[j] & 0xF) | ((q[16 + j] & 0xF) << 4));
+  for (int j = 0; j < 32; j++) h |= (uint32_t)((q[j] >> 4) & 1) << j;
+  qh[0] = (uint8_t)h;
+  qh[1] = (uint8_t)(h >> 8);
+  qh[2] = (uint8_t)(h >> 16);
+  qh[3] = (uint8_t)(h >> 24);
+}
+
+static void quant_block_q5_0(const float* w, uint8_t* out) {
+  float amax = 0.f, mx = 0.f;
+  for (int j = 0; j < 32; j++)
+    if (fabsf(w[j]) > amax) { amax = fabsf(w[j]); mx = w[j]; }
+  uint16_t dh = chatnet_float_to_half(mx / -16.0f);
+  float d = half_to_float(dh), id = d != 0.f ? 1.0f / d : 0.f;
+  int q[32];
+  for (int j = 0; j < 32; j++) {
+    int v = nearest_int(w[j] * id) + 16;
+    q[j] = v < 0 ? 0 : (v > 31 ? 31 : v);
+  }
+  put16(out, dh);
+  put_q5(q, out + 2, out + 6);
+}
+
+static void quant_block_q5_1(const float* w, uint8_t* out) {
+  float lo = w[0], hi = w[0];
+  for (int j = 1; j < 32; j++) {
+    if (w[j] < lo) lo = w[j];
+    if (w[j] > hi) hi = w[j];
+  }
+  uint16_t dh = chatnet_float_to_half((hi - lo) / 31.0f), mh = chatnet_float_to_half(lo);
+  float d = half_to_float(dh), m = half_to_float(mh), id = d != 0.f ? 1.0f / d : 0.f;
+  int q[32];
+  for (int j = 0; j < 32; j++) {
+    int v = nearest_int((w[j] - m) * id);
+    q[j] = v < 0 ? 0 : (v > 31 ? 31 : v);
+  }
+  put16(out, dh);
+  put16(out + 2, mh);
+  put_q5(q, out + 4, out + 8);
+}
+
+/* Q2_K (the reference's layout, DequantQ2K.cs:15-20, :55-82): per 16-element
+ * sub-block sb, scale (max - min) / 3 and offset -min(0, min), both 4-bit
+ * against fp16 d / dmin; element 128g + 32t + 16h + l is bits 2t..2t+1 of
+ * qs[32g + 16h + l] with scale byte sb = 8g + 2t + h (low nibble scale, high
+ * nibble min). */
+static void quant_block_q2_k(const float* w, uint8_t* out) {
+  float scale[16], mins[16], ms = 0.f, mm = 0.f;
+  for (int sb = 0; sb < 16; sb++) {
+    int g = sb / 8, t = (sb % 8) / 2, h = sb % 2, e0 = 128 * g + 32 * t + 16 * h;
+    float lo = 0.f, hi = w[e0];
+    for (int l = 0; l < 16; l++) {
+      if (w[e0 + l] < lo) lo = w[e0 + l];
+      if (w[e0 + l] > hi) hi = w[e0 + l];
+    }
+    if (hi < lo) hi = lo;
+    scale[sb] = (hi - lo) / 3.0f;
+    mins[sb] = -lo;
+    if (scale[sb] > ms) ms = scale[sb];
+    if (mins[sb] > mm) mm = mins[sb];
+  }
+  uint16_t dh = chatnet_float_to_half(ms / 15.0f), mh = chatnet_float_to_half(mm / 15.0f);
+  float d = half_to_float(dh), dmin = half_to_float(mh);
+  memset(out, 0, 84);
+  for (int sb = 0; sb < 16; sb++) {
+    int sc = d > 0.f ? nearest_int(scale[sb] / d) : 0, m = dmin > 0.f ? nearest_int(mins[sb] / dmin) : 0;
+    sc = sc < 0 ? 0 : (sc > 15 ? 15 : sc);
+    m = m < 0 ? 0 : (m > 15 ? 15 : m);
+    out[sb] = (uint8_t)(sc | (m << 4));
+    int g = sb / 8, t = (sb % 8) / 2, h = sb % 2, e0 = 128 * g + 32 * t + 16 * h;
+    float dl = d * (float)sc, ml = dmin * (float)m;
+    for (int l = 0; l < 16; l++) {
+      int q = dl > 0.f ? nearest_int((w[e0 + l] + ml) / dl) : 0;
+      q = q < 0 ? 0 : (q > 3 ? 3 : q);
+      out[16 + 32 * g + 16 * h + l] |= (uint8_t)(q << (2 * t));
+    }
+  }
+  put16(out + 80, dh);
+  put16(out + 82, mh);
+}
+
+/* Q3_K (the reference's layout, DequantQ3K.cs:9-21, :52-63): per 16-element
+ * sub-block a signed 6-bit scale sc = round(-amax / 4 / d) (d = max|scale| /
+ * 31 as fp16), q3 = round(w / (d*sc)) + 4 in [0, 7]; element i keeps bits 0-1
+ * in qs[i/4] at 2(i%4) and bit 2 in hmask[i/8] bit i%8; scales stored + 32,
+ * low nibbles in bytes 0..7 (sc 0..7 low, 8..15 high), two high bits per
+ * scale in bytes 8..11. */
+static void quant_block_q3_k(const float* w, uint8_t* out) {
+  float scale[16], amax_all = 0.f;
+  for (int sb = 0; sb < 16; sb++) {
+    float amax = 0.f, mx = 0.f;
+    for (int l = 0; l < 16; l++)
+      if (fabsf(w[16 * sb + l]) > amax) { amax = fabsf(w[16 * sb + l]); mx = w[16 * sb + l]; }
+    scale[sb] = -mx / 4.0f;
+    if (fabsf(scale[sb]) > amax_all) amax_all = fabsf(scale[sb]);
+  }
+  uint16_t dh = chatnet_float_to_half(amax_all / 31.0f);
+  float d = half_to_float(dh);
+  memset(out, 0, 110);
+  int sc[16];
+  for (int sb = 0; sb < 16; sb++) {
+    int v = d > 0.f ? nearest_int(scale[sb] / d) : 0;
+    sc[sb] = v < -32 ? -32 : (v > 31 ? 31 : v);
+  }
+  for (int i = 0; i < 256; i++) {
+    float den = d * (float)sc[i / 16];
+    int q = den != 0.f ? nearest_int(w[i] / den) + 4 : 4;
+    q = q < 0 ? 0 : (q > 7 ? 7 : q);
+    out[32 + i / 4] |= (uint8_t)((q & 3) << (2 * (i % 4)));
+    out[i / 8] |= (uint8_t)(((q >> 2) & 1) << (i % 8));
+  }
+  uint8_t* s = out + 96;
+  for (int i = 0; i < 16; i++) {
+    int u = sc[i] + 32;
+    if (i < 8) s[i] |= (uint8_t)(u & 0xF);
+    else s[i - 8] |= (uint8_t)((u & 0xF) << 4);
+    s[8 + i % 4] |= (uint8_t)(((u >> 4) & 3) << (2 * (i / 4)));
+  }
+  put16(out + 108, dh);
+}
+
+/* Q8_K: fp32 d = max|w| / 127, q = round(w / d) in [-127, 127], then the 16
+ * int16 block sums the format carries. */
+static void quant_block_q8_k(const float* w, uint8_t* out) {
+  float amax = 0.f;
+  for (int i = 0; i < 256; i++)
+    if (fabsf(w[i]) > amax) amax = fabsf(w[i]);
+  float d = amax / 127.0f, id = d != 0.f ? 1.0f / d : 0.f;
+  memcpy(out, &d, 4);
+  for (int g = 0; g < 16; g++) {
+    int sum = 0;
+    for (int l = 0; l < 16; l++) {
+      int q = nearest_int(w[16 * g + l] * id);
+      q = q < -127 ? -127 : (q > 127 ? 127 : q);
+      out[4 + 16 * g + l] = (uint8_t)(int8_t)q;
+      sum += q;
+    }
+    out[260 + 2 * g] = (uint8_t)(sum & 0xFF);
+    out[261 + 2 * g] = (uint8_t)((sum >> 8) & 0xFF);
+  }
+}
+
 static int block_info(uint32_t type, int* blk, int* bytes) {
   switch (type) {
     case 2: *blk = 32; *bytes = 18; return 0;
@@ -316,6 +485,12 @@ static int block_info(uint32_t type, int* blk, int* bytes) {
     case 12: *blk = 256; *bytes = 144; return 0;
     case 13: *blk = 256; *bytes = 176; return 0;
     case 14: *blk = 256; *bytes = 210; return 0;
+    case 3: *blk = 32; *bytes = 20; return 0;
+    case 6: *blk = 32; *bytes = 22; return 0;
+    case 7: *blk = 32; *bytes = 24; return 0;
+    case 10: *blk = 256; *bytes = 84; return 0;
+    case 11: *blk = 256; *bytes = 110; return 0;
+    case 15: *blk = 256; *bytes = 292; return 0;
     default: return -1;
   }
 }
@@ -326,6 +501,12 @@ static void quant_block(uint32_t type, const float* src, uint8_t* dst) {
     case 8: quant_block_q8_0(src, dst); break;
     case 12: quant_block_q4_k(src, dst); break;
     case 13: quant_block_q5_k(src, dst); break;
+    case 3: quant_block_q4_1(src, dst); break;
+    case 6: quant_block_q5_0(src, dst); break;
+    case 7: quant_block_q5_1(src, dst); break;
+    case 10: quant_block_q2_k(src, dst); break;
+    case 11: quant_block_q3_k(src, dst); break;
+    case 15: quant_block_q8_k(src, dst); break;
     default: quant_block_q6_k(src, dst); break;
   }
 }

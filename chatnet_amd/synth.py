@@ -47,6 +47,14 @@ MIXES = {
     # block types only, each matrix on its own type and ffn_gate/up differing
     "mixed_blocks": {"attn": _native.GGML_Q8_0, "gate": _native.GGML_Q4_0, "up": _native.GGML_Q5_K,
                      "down": _native.GGML_Q6_K, "output": _native.GGML_Q4_K},
+    # the types served through packed units (LlamaModel.MatVecMulByType's
+    # generic branches): legacy 32-blocks, then the small K-quants
+    "legacy_blocks": {"attn": _native.GGML_Q4_1, "gate": _native.GGML_Q5_0, "up": _native.GGML_Q5_1,
+                      "down": _native.GGML_Q5_0, "output": _native.GGML_Q4_1},
+    "q3_k_m": {"attn": _native.GGML_Q3_K, "gate_up": _native.GGML_Q3_K, "down": _native.GGML_Q4_K,
+               "output": _native.GGML_Q6_K},
+    "q2_k": {"attn": _native.GGML_Q2_K, "gate_up": _native.GGML_Q2_K, "down": _native.GGML_Q3_K,
+             "output": _native.GGML_Q8_K},
 }
 
 

@@ -387,6 +387,256 @@ float oracle_dot_q5_k(const uint8_t* row, const float* x, int n) {
   return sum;
 }
 
+/* ---------------------------------------------------------------------------
+ * Q4_1 (DequantQ4_1.cs): fp16 d, fp16 m, qs[16]; value = q*d + m (q unsigned
+ * nibble, elements 0..15 low nibbles, 16..31 high nibbles).
+ * ------------------------------------------------------------------------- */
+static inline int nib32(const uint8_t* qs, int j) { return j < 16 ? (qs[j] & 0x0F) : ((qs[j - 16] >> 4) & 0x0F); }
+
+/* DequantQ4_1.Dequantize (DequantQ4_1.cs:24-55), partial last block included. */
+void oracle_dequant_q4_1(const uint8_t* src, float* out, int n) {
+  int blocks = (n + 31) / 32;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = src + (size_t)b * 20;
+    float d = h2f(blk), m = h2f(blk + 2);
+    int count = n - 32 * b < 32 ? n - 32 * b : 32;
+    for (int j = 0; j < count; j++) out[32 * b + j] = (float)nib32(blk + 4, j) * d + m;
+  }
+}
+
+/* DequantQ4_1.DotProductVec128 (DequantQ4_1.cs:66-127): per block two 4-lane
+ * accumulators (lanes of elements 0..3 / 8..11 / 16..19 / 24..27 into the
+ * first, 4..7 / 12..15 / 20..23 / 28..31 into the second), each term
+ * (q*d + m) * x, added to the row accumulators after the block. */
+float oracle_dot_q4_1(const uint8_t* row, const float* x, int n) {
+  int blocks = n / 32;
+  float acc0[4] = {0, 0, 0, 0}, acc1[4] = {0, 0, 0, 0};
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = row + (size_t)b * 20;
+    const float* in = x + (size_t)b * 32;
+    float d = h2f(blk), m = h2f(blk + 2);
+    float b0[4] = {0, 0, 0, 0}, b1[4] = {0, 0, 0, 0};
+    for (int g = 0; g < 32; g += 8)
+      for (int l = 0; l < 4; l++) {
+        b0[l] = b0[l] + ((float)nib32(blk + 4, g + l) * d + m) * in[g + l];
+        b1[l] = b1[l] + ((float)nib32(blk + 4, g + 4 + l) * d + m) * in[g + 4 + l];
+      }
+    for (int l = 0; l < 4; l++) {
+      acc0[l] = acc0[l] + b0[l];
+      acc1[l] = acc1[l] + b1[l];
+    }
+  }
+  float s[4];
+  for (int l = 0; l < 4; l++) s[l] = acc0[l] + acc1[l];
+  return vsum4(s);
+}
+
+/* ---------------------------------------------------------------------------
+ * Q5_0 / Q5_1 (DequantQ5_0.cs, DequantQ5_1.cs): q5 = nibble | bit j of the
+ * little-endian qh word << 4; Q5_0 value = (q5 - 16) * d, Q5_1 q5 * d + m.
+ * ------------------------------------------------------------------------- */
+static inline int q5_32(const uint8_t* qh, const uint8_t* qs, int j) {
+  uint32_t h = (uint32_t)qh[0] | ((uint32_t)qh[1] << 8) | ((uint32_t)qh[2] << 16) | ((uint32_t)qh[3] << 24);
+  return nib32(qs, j) | (int)(((h >> j) & 1u) << 4);
+}
+
+/* DequantQ5_0.Dequantize (DequantQ5_0.cs:28-70). */
+void oracle_dequant_q5_0(const uint8_t* src, float* out, int n) {
+  int blocks = (n + 31) / 32;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = src + (size_t)b * 22;
+    float d = h2f(blk);
+    int count = n - 32 * b < 32 ? n - 32 * b : 32;
+    for (int j = 0; j < count; j++) out[32 * b + j] = (float)(q5_32(blk + 2, blk + 6, j) - 16) * d;
+  }
+}
+
+/* DequantQ5_0.DotProductScalar (DequantQ5_0.cs:79-118): the block's integer
+ * (q5 - 16) * x terms summed in order, then sum += blockSum * d. */
+float oracle_dot_q5_0(const uint8_t* row, const float* x, int n) {
+  int blocks = n / 32;
+  float sum = 0.0f;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = row + (size_t)b * 22;
+    const float* in = x + (size_t)b * 32;
+    float d = h2f(blk), bs = 0.0f;
+    for (int j = 0; j < 32; j++) bs = bs + (float)(q5_32(blk + 2, blk + 6, j) - 16) * in[j];
+    sum = sum + bs * d;
+  }
+  return sum;
+}
+
+/* DequantQ5_1.Dequantize (DequantQ5_1.cs:30-70). */
+void oracle_dequant_q5_1(const uint8_t* src, float* out, int n) {
+  int blocks = (n + 31) / 32;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = src + (size_t)b * 24;
+    float d = h2f(blk), m = h2f(blk + 2);
+    int count = n - 32 * b < 32 ? n - 32 * b : 32;
+    for (int j = 0; j < count; j++) out[32 * b + j] = (float)q5_32(blk + 4, blk + 8, j) * d + m;
+  }
+}
+
+/* DequantQ5_1.DotProductScalar (DequantQ5_1.cs:78-118): sum += blockSum * d +
+ * inputSum * m per block, blockSum = sum of q5 * x, inputSum = sum of x. */
+float oracle_dot_q5_1(const uint8_t* row, const float* x, int n) {
+  int blocks = n / 32;
+  float sum = 0.0f;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = row + (size_t)b * 24;
+    const float* in = x + (size_t)b * 32;
+    float d = h2f(blk), m = h2f(blk + 2), bs = 0.0f, is = 0.0f;
+    for (int j = 0; j < 32; j++) {
+      bs = bs + (float)q5_32(blk + 4, blk + 8, j) * in[j];
+      is = is + in[j];
+    }
+    sum = sum + (bs * d + is * m); /* the right side first: sum += a + b */
+  }
+  return sum;
+}
+
+/* ---------------------------------------------------------------------------
+ * Q2_K (DequantQ2K.cs): scales[16] @0 (low nibble scale, high nibble min per
+ * 16 elements), qs[64] @16, d @80, dmin @82.  Element 128g + 32t + 16h + l
+ * (g, h in {0,1}, t in 0..3, l < 16) is bits 2t..2t+1 of qs[32g + 16h + l]
+ * with scale byte 8g + 2t + h; value = (d*sc) * q - dmin*m.
+ * ------------------------------------------------------------------------- */
+static inline void q2k_elem(const uint8_t* blk, int e, int* q, int* sb) {
+  int g = e / 128, t = (e % 128) / 32, h = (e % 32) / 16, l = e % 16;
+  *q = (blk[16 + 32 * g + 16 * h + l] >> (2 * t)) & 3;
+  *sb = 8 * g + 2 * t + h;
+}
+
+/* DequantQ2K.Dequantize (DequantQ2K.cs:33-86). */
+void oracle_dequant_q2_k(const uint8_t* src, float* out, int n) {
+  int blocks = n / 256;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = src + (size_t)b * 84;
+    float d = h2f(blk + 80), dmin = h2f(blk + 82);
+    for (int e = 0; e < 256; e++) {
+      int q, sb;
+      q2k_elem(blk, e, &q, &sb);
+      float dl = d * (float)(blk[sb] & 0x0F), ml = dmin * (float)((blk[sb] >> 4) & 0x0F);
+      out[(size_t)b * 256 + e] = dl * (float)q - ml;
+    }
+  }
+}
+
+/* DequantQ2K.DotProductScalar (DequantQ2K.cs:95-155): one sequential sum of
+ * (dl*q - ml) * x per super-block in element order, added to the row sum. */
+float oracle_dot_q2_k(const uint8_t* row, const float* x, int n) {
+  int blocks = n / 256;
+  float sum = 0.0f;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = row + (size_t)b * 84;
+    const float* in = x + (size_t)b * 256;
+    float d = h2f(blk + 80), dmin = h2f(blk + 82), bs = 0.0f;
+    for (int e = 0; e < 256; e++) {
+      int q, sb;
+      q2k_elem(blk, e, &q, &sb);
+      float dl = d * (float)(blk[sb] & 0x0F), ml = dmin * (float)((blk[sb] >> 4) & 0x0F);
+      bs = bs + (dl * (float)q - ml) * in[e];
+    }
+    sum = sum + bs;
+  }
+  return sum;
+}
+
+/* ---------------------------------------------------------------------------
+ * Q3_K (DequantQ3K.cs): hmask[32] @0, qs[64] @32, scales[12] @96, d @108.
+ * Element i: q3 = (bits 2(i%4).. of qs[i/4]) | (bit i%8 of hmask[i/8]) << 2;
+ * value = d * sc[i/16] * (q3 - 4), sc the signed 6-bit scales (low nibbles
+ * of bytes 0..7 for 0..7, high nibbles for 8..15, two more bits from bytes
+ * 8..11, minus 32).
+ * ------------------------------------------------------------------------- */
+static void q3k_scales(const uint8_t* p, int* sc) {
+  for (int i = 0; i < 8; i++) {
+    sc[i] = p[i] & 0x0F;
+    sc[i + 8] = (p[i] >> 4) & 0x0F;
+  }
+  for (int i = 0; i < 4; i++) {
+    int hb = p[8 + i];
+    sc[i] |= (hb & 3) << 4;
+    sc[i + 4] |= ((hb >> 2) & 3) << 4;
+    sc[i + 8] |= ((hb >> 4) & 3) << 4;
+    sc[i + 12] |= ((hb >> 6) & 3) << 4;
+  }
+  for (int i = 0; i < 16; i++) sc[i] -= 32;
+}
+
+static inline int q3k_q(const uint8_t* blk, int i) {
+  return ((blk[32 + i / 4] >> (2 * (i % 4))) & 3) | (((blk[i / 8] >> (i % 8)) & 1) << 2);
+}
+
+/* DequantQ3K.Dequantize (DequantQ3K.cs:35-70, DecodeScales :122-150). */
+void oracle_dequant_q3_k(const uint8_t* src, float* out, int n) {
+  int blocks = n / 256;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = src + (size_t)b * 110;
+    float d = h2f(blk + 108);
+    int sc[16];
+    q3k_scales(blk + 96, sc);
+    for (int i = 0; i < 256; i++) out[(size_t)b * 256 + i] = d * (float)sc[i / 16] * (float)(q3k_q(blk, i) - 4);
+  }
+}
+
+/* DequantQ3K.DotProductScalar (DequantQ3K.cs:79-117): blockSum of the integer
+ * sc * (q3 - 4) times x in element order, then sum += d * blockSum. */
+float oracle_dot_q3_k(const uint8_t* row, const float* x, int n) {
+  int blocks = n / 256;
+  float sum = 0.0f;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = row + (size_t)b * 110;
+    const float* in = x + (size_t)b * 256;
+    float d = h2f(blk + 108), bs = 0.0f;
+    int sc[16];
+    q3k_scales(blk + 96, sc);
+    for (int i = 0; i < 256; i++) bs = bs + (float)(sc[i / 16] * (q3k_q(blk, i) - 4)) * in[i];
+    sum = sum + d * bs;
+  }
+  return sum;
+}
+
+/* ---------------------------------------------------------------------------
+ * Q8_K (DequantQ8K.cs): fp32 d @0, int8 qs[256] @4, int16 bsums[16] @260
+ * (not read); value = (sbyte)q * d.
+ * ------------------------------------------------------------------------- */
+static inline float f32_at(const uint8_t* p) {
+  float f;
+  memcpy(&f, p, 4);
+  return f;
+}
+
+/* DequantQ8K.Dequantize (DequantQ8K.cs:26-51). */
+void oracle_dequant_q8_k(const uint8_t* src, float* out, int n) {
+  int blocks = n / 256;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = src + (size_t)b * 292;
+    float d = f32_at(blk);
+    for (int i = 0; i < 256; i++) out[(size_t)b * 256 + i] = (float)(int8_t)blk[4 + i] * d;
+  }
+}
+
+/* DequantQ8K.DotProductVec128 (DequantQ8K.cs:62-101): lanes of elements
+ * 8k..8k+3 into acc0, 8k+4..8k+7 into acc1, each term (q * d) * x. */
+float oracle_dot_q8_k(const uint8_t* row, const float* x, int n) {
+  int blocks = n / 256;
+  float acc0[4] = {0, 0, 0, 0}, acc1[4] = {0, 0, 0, 0};
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = row + (size_t)b * 292;
+    const float* in = x + (size_t)b * 256;
+    float d = f32_at(blk);
+    for (int i = 0; i < 256; i += 8)
+      for (int l = 0; l < 4; l++) {
+        acc0[l] = acc0[l] + ((float)(int8_t)blk[4 + i + l] * d) * in[i + l];
+        acc1[l] = acc1[l] + ((float)(int8_t)blk[4 + i + 4 + l] * d) * in[i + 4 + l];
+      }
+  }
+  float s[4];
+  for (int l = 0; l < 4; l++) s[l] = acc0[l] + acc1[l];
+  return vsum4(s);
+}
+
 /* TensorMath.MatVecMulQ4_0 / MatVecMulQ6K / MatVecMulGeneric / MatVecMul
  * (TensorMath.cs:527-656) dispatched as LlamaModel.MatVecMulByType
  * (LlamaModel.cs:470-567).  Rows are independent (TensorMath.cs:47-51), so the
@@ -401,6 +651,12 @@ int oracle_matvec(uint32_t type, const void* W, const float* x, float* y, int M,
     case ORACLE_Q6_K: bpr = (size_t)(K / 256) * 210; dot = oracle_dot_q6_k; break;
     case ORACLE_Q8_0: bpr = (size_t)(K / 32) * 34; dot = oracle_dot_q8_0; break;
     case ORACLE_Q5_K: bpr = (size_t)(K / 256) * 176; dot = oracle_dot_q5_k; break;
+    case ORACLE_Q4_1: bpr = (size_t)(K / 32) * 20; dot = oracle_dot_q4_1; break;
+    case ORACLE_Q5_0: bpr = (size_t)(K / 32) * 22; dot = oracle_dot_q5_0; break;
+    case ORACLE_Q5_1: bpr = (size_t)(K / 32) * 24; dot = oracle_dot_q5_1; break;
+    case ORACLE_Q2_K: bpr = (size_t)(K / 256) * 84; dot = oracle_dot_q2_k; break;
+    case ORACLE_Q3_K: bpr = (size_t)(K / 256) * 110; dot = oracle_dot_q3_k; break;
+    case ORACLE_Q8_K: bpr = (size_t)(K / 256) * 292; dot = oracle_dot_q8_k; break;
     case ORACLE_F32: {
       const float* wf = (const float*)W;
       for (int r = 0; r < M; r++) y[r] = oracle_dot_f32(wf + (size_t)r * K, x, K);
@@ -789,7 +1045,9 @@ int oracle_llama_set_tensor(oracle_llama* m, const char* name, uint32_t type, co
   return -2;
 }
 
-/* LlamaModel.LoadEmbedding (LlamaModel.cs:365-394) for F32 / F16 / Q4_0 / Q8_0. */
+/* LlamaModel.LoadEmbedding (LlamaModel.cs:365-394): F32 copy, F16 per
+ * element, any quantized type through its Dequantize (GetDequantInfo,
+ * LlamaModel.cs:399-467) on the token's row. */
 static int load_embedding(oracle_llama* m, int token, float* out) {
   int dim = m->c.dim;
   const uint8_t* e = (const uint8_t*)m->emb.data;
@@ -800,6 +1058,15 @@ static int load_embedding(oracle_llama* m, int token, float* out) {
       return 0;
     case ORACLE_Q4_0: oracle_dequant_q4_0(e + (size_t)token * (dim / 32) * 18, out, dim); return 0;
     case ORACLE_Q8_0: oracle_dequant_q8_0(e + (size_t)token * (dim / 32) * 34, out, dim); return 0;
+    case ORACLE_Q4_1: oracle_dequant_q4_1(e + (size_t)token * (dim / 32) * 20, out, dim); return 0;
+    case ORACLE_Q5_0: oracle_dequant_q5_0(e + (size_t)token * (dim / 32) * 22, out, dim); return 0;
+    case ORACLE_Q5_1: oracle_dequant_q5_1(e + (size_t)token * (dim / 32) * 24, out, dim); return 0;
+    case ORACLE_Q2_K: oracle_dequant_q2_k(e + (size_t)token * (dim / 256) * 84, out, dim); return 0;
+    case ORACLE_Q3_K: oracle_dequant_q3_k(e + (size_t)token * (dim / 256) * 110, out, dim); return 0;
+    case ORACLE_Q4_K: oracle_dequant_q4_k(e + (size_t)token * (dim / 256) * 144, out, dim); return 0;
+    case ORACLE_Q5_K: oracle_dequant_q5_k(e + (size_t)token * (dim / 256) * 176, out, dim); return 0;
+    case ORACLE_Q6_K: oracle_dequant_q6_k(e + (size_t)token * (dim / 256) * 210, out, dim); return 0;
+    case ORACLE_Q8_K: oracle_dequant_q8_k(e + (size_t)token * (dim / 256) * 292, out, dim); return 0;
     default: return -3;
   }
 }

@@ -53,8 +53,9 @@
 extern "C" {
 #endif
 
-enum { ORACLE_F32 = 0, ORACLE_F16 = 1, ORACLE_Q4_0 = 2, ORACLE_Q8_0 = 8, ORACLE_Q4_K = 12, ORACLE_Q5_K = 13,
-       ORACLE_Q6_K = 14 };
+enum { ORACLE_F32 = 0, ORACLE_F16 = 1, ORACLE_Q4_0 = 2, ORACLE_Q4_1 = 3, ORACLE_Q5_0 = 6, ORACLE_Q5_1 = 7,
+       ORACLE_Q8_0 = 8, ORACLE_Q2_K = 10, ORACLE_Q3_K = 11, ORACLE_Q4_K = 12, ORACLE_Q5_K = 13, ORACLE_Q6_K = 14,
+       ORACLE_Q8_K = 15 };
 
 void oracle_set_threads(int n);
 int oracle_get_threads(void);
@@ -71,6 +72,18 @@ void oracle_dequant_q8_0(const uint8_t* src, float* out, int n);
 float oracle_dot_q8_0(const uint8_t* row, const float* x, int n);
 void oracle_dequant_q5_k(const uint8_t* src, float* out, int n);
 float oracle_dot_q5_k(const uint8_t* row, const float* x, int n);
+void oracle_dequant_q4_1(const uint8_t* src, float* out, int n);
+float oracle_dot_q4_1(const uint8_t* row, const float* x, int n);
+void oracle_dequant_q5_0(const uint8_t* src, float* out, int n);
+float oracle_dot_q5_0(const uint8_t* row, const float* x, int n);
+void oracle_dequant_q5_1(const uint8_t* src, float* out, int n);
+float oracle_dot_q5_1(const uint8_t* row, const float* x, int n);
+void oracle_dequant_q2_k(const uint8_t* src, float* out, int n);
+float oracle_dot_q2_k(const uint8_t* row, const float* x, int n);
+void oracle_dequant_q3_k(const uint8_t* src, float* out, int n);
+float oracle_dot_q3_k(const uint8_t* row, const float* x, int n);
+void oracle_dequant_q8_k(const uint8_t* src, float* out, int n);
+float oracle_dot_q8_k(const uint8_t* row, const float* x, int n);
 float oracle_dot_f32(const float* a, const float* b, int n);
 
 /* y[m] = dot(W row m, x) for m < M (MatVecMulByType semantics). Returns 0 or -3

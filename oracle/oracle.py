@@ -16,7 +16,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(HERE, "liboracle.so")
 
 F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 2, 8, 12, 13, 14
-_NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q5_K: "q5_k", Q6_K: "q6_k"}
+Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q8_K = 3, 6, 7, 10, 11, 15
+_NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q5_K: "q5_k", Q6_K: "q6_k", Q4_1: "q4_1", Q5_0: "q5_0",
+          Q5_1: "q5_1", Q2_K: "q2_k", Q3_K: "q3_k", Q8_K: "q8_k"}
 _P = ctypes.c_void_p
 _lib = None
 
@@ -43,7 +45,7 @@ def lib() -> ctypes.CDLL:
         L.oracle_get_threads.restype = ctypes.c_int
         L.oracle_half_to_float.restype = ctypes.c_float
         L.oracle_half_to_float.argtypes = [ctypes.c_uint16]
-        for q in ("q4_0", "q4_k", "q6_k", "q8_0", "q5_k"):
+        for q in _NAMES.values():
             getattr(L, f"oracle_dequant_{q}").argtypes = [_P, _P, ctypes.c_int]
             getattr(L, f"oracle_dequant_{q}").restype = None
             getattr(L, f"oracle_dot_{q}").argtypes = [_P, _P, ctypes.c_int]

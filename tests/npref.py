@@ -84,7 +84,75 @@ def dequant_q5_k(raw: np.ndarray, n: int) -> np.ndarray:
     return val.reshape(-1)[:n]
 
 
-DEQUANT = {2: dequant_q4_0, 8: dequant_q8_0, 12: dequant_q4_k, 13: dequant_q5_k, 14: dequant_q6_k}
+def _h(b, i):
+    return half(b[:, i].astype(np.uint16) | (b[:, i + 1].astype(np.uint16) << 8))
+
+
+def _nibbles32(qs):  # elements 0..15 low nibbles, 16..31 high nibbles (DequantQ4_1.cs:14-16)
+    return np.concatenate([qs & 0x0F, qs >> 4], axis=1).astype(np.float64)
+
+
+def dequant_q4_1(raw: np.ndarray, n: int) -> np.ndarray:  # DequantQ4_1.cs:24-55
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, 20)
+    return (_nibbles32(b[:, 4:]) * _h(b, 0)[:, None] + _h(b, 2)[:, None]).ravel()[:n]
+
+
+def _q5(qh4, qs16):  # bit j of the little-endian qh word is element j's fifth bit
+    hb = np.unpackbits(qh4, axis=1, bitorder="little").astype(np.float64)  # [blk, 32]
+    return _nibbles32(qs16) + 16.0 * hb
+
+
+def dequant_q5_0(raw: np.ndarray, n: int) -> np.ndarray:  # DequantQ5_0.cs:28-70
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, 22)
+    return ((_q5(b[:, 2:6], b[:, 6:]) - 16.0) * _h(b, 0)[:, None]).ravel()[:n]
+
+
+def dequant_q5_1(raw: np.ndarray, n: int) -> np.ndarray:  # DequantQ5_1.cs:30-70
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, 24)
+    return (_q5(b[:, 4:8], b[:, 8:]) * _h(b, 0)[:, None] + _h(b, 2)[:, None]).ravel()[:n]
+
+
+def dequant_q2_k(raw: np.ndarray, n: int) -> np.ndarray:  # DequantQ2K.cs:33-86
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, 84)
+    d, dmin = _h(b, 80), _h(b, 82)
+    out = np.zeros((b.shape[0], 256))
+    for g in range(2):
+        for t in range(4):
+            for hh in range(2):
+                sb = 8 * g + 2 * t + hh
+                q = (b[:, 16 + 32 * g + 16 * hh: 16 + 32 * g + 16 * hh + 16] >> (2 * t)) & 3
+                sc, m = (b[:, sb] & 0x0F).astype(np.float64), (b[:, sb] >> 4).astype(np.float64)
+                e0 = 128 * g + 32 * t + 16 * hh
+                out[:, e0:e0 + 16] = (d * sc)[:, None] * q - (dmin * m)[:, None]
+    return out.ravel()[:n]
+
+
+def q3k_scales(s12: np.ndarray) -> np.ndarray:  # DequantQ3K.cs:122-150
+    s = np.asarray(s12, dtype=np.int64).reshape(-1, 12)
+    lo = np.concatenate([s[:, 0:8] & 0x0F, s[:, 0:8] >> 4], axis=1)  # sc 0..7 low, 8..15 high nibbles
+    hi = np.concatenate([(s[:, 8:12] >> (2 * k)) & 3 for k in range(4)], axis=1)  # sc 4k+i from byte 8+i
+    return (lo | (hi << 4)) - 32
+
+
+def dequant_q3_k(raw: np.ndarray, n: int) -> np.ndarray:  # DequantQ3K.cs:35-70
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, 110)
+    d = _h(b, 108)
+    sc = q3k_scales(b[:, 96:108]).astype(np.float64)
+    i = np.arange(256)
+    q2 = (b[:, 32 + i // 4] >> (2 * (i % 4))) & 3
+    hb = (b[:, i // 8] >> (i % 8)) & 1
+    q3 = (q2 | (hb << 2)).astype(np.float64)
+    return (d[:, None] * sc[:, i // 16] * (q3 - 4.0)).ravel()[:n]
+
+
+def dequant_q8_k(raw: np.ndarray, n: int) -> np.ndarray:  # DequantQ8K.cs:26-51
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, 292)
+    d = b[:, 0:4].copy().view("<f4").astype(np.float64).ravel()
+    return (b[:, 4:260].view(np.int8).astype(np.float64) * d[:, None]).ravel()[:n]
+
+
+DEQUANT = {2: dequant_q4_0, 8: dequant_q8_0, 12: dequant_q4_k, 13: dequant_q5_k, 14: dequant_q6_k,
+           3: dequant_q4_1, 6: dequant_q5_0, 7: dequant_q5_1, 10: dequant_q2_k, 11: dequant_q3_k, 15: dequant_q8_k}
 
 
 def matrix(t) -> np.ndarray:

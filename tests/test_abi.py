@@ -76,9 +76,14 @@ def test_matmul_rejects_bad_arguments_before_launch():
     lib = _native.hip_lib()
     assert lib.chatnet_matmul(2, None, None, None, 4, 64, 1, None) == _native.ERR_INVALID_ARG
     fake = ctypes.c_void_p(16)
-    assert lib.chatnet_matmul(3, fake, fake, fake, 4, 64, 1, None) == _native.ERR_UNSUPPORTED_TYPE
+    # Q8_1 (9) is not a weight type MatVecMulByType dispatches (LlamaModel.cs:474-566)
+    assert lib.chatnet_matmul(9, fake, fake, fake, 4, 64, 1, None) == _native.ERR_UNSUPPORTED_TYPE
     assert lib.chatnet_matmul(2, fake, fake, fake, 4, 48, 1, None) == _native.ERR_INVALID_ARG
     assert lib.chatnet_matmul(12, fake, fake, fake, 4, 128, 1, None) == _native.ERR_INVALID_ARG
+    # block multiples of the types read as packed units: 64 for Q4_1/Q5_0/Q5_1, 256 for Q2_K/Q3_K/Q8_K
+    assert lib.chatnet_matmul(3, fake, fake, fake, 4, 96, 1, None) == _native.ERR_INVALID_ARG
+    assert lib.chatnet_matmul(10, fake, fake, fake, 4, 128, 1, None) == _native.ERR_INVALID_ARG
+    assert lib.chatnet_matmul(15, fake, fake, fake, 4, 16640, 1, None) == _native.ERR_INVALID_ARG
 
 
 def test_greedy_sampler_host_mirror():

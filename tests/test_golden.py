@@ -11,13 +11,14 @@ import oracle
 from chatnet_amd import TINY_TEST, synth
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+TAGS = ["q4_0", "q4_k", "q6_k", "q8_0", "q5_k", "q4_1", "q5_0", "q5_1", "q2_k", "q3_k", "q8_k"]
 
 
 def load(name):
     return np.load(os.path.join(GOLD, name), allow_pickle=False)
 
 
-@pytest.mark.parametrize("tag", ["q4_0", "q4_k", "q6_k", "q8_0", "q5_k"])
+@pytest.mark.parametrize("tag", TAGS)
 def test_block_fixtures_reproduce(tag):
     g = load(f"blocks_{tag}.npz")
     qtype, rows, K = int(g["ggml_type"]), int(g["rows"]), int(g["K"])
@@ -52,7 +53,7 @@ def test_tiny_model_fixture_reproduces():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("tag", ["q4_0", "q4_k", "q6_k", "q8_0", "q5_k"])
+@pytest.mark.parametrize("tag", TAGS)
 def test_gpu_matches_block_fixtures(tag):
     from gpu_util import announce, gpu_matmul, normwise
 

@@ -67,7 +67,8 @@ def test_gemm_columns_match_gemv():
 # Other block types: W is packed once per call into u8 codes with an fp32
 # scale and offset per 16 weights (each weight bit-equal to the type's own
 # dequantized value), then the same MFMA GEMM runs.
-PACKED = {8: "q8_0", 12: "q4_k", 13: "q5_k", 14: "q6_k"}
+PACKED = {3: "q4_1", 6: "q5_0", 7: "q5_1", 8: "q8_0", 10: "q2_k", 11: "q3_k", 12: "q4_k", 13: "q5_k", 14: "q6_k",
+          15: "q8_k"}
 
 
 @pytest.mark.parametrize("M,K,N", [

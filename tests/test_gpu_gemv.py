@@ -132,3 +132,24 @@ def test_batched_columns_match_per_column_gemv(N):
 ])
 def test_float_weight_gemv_shapes(qtype, M, K):
     run_case(qtype, M, K, seed=7)
+
+
+# The types the GEMV reads as packed units (re-encoded on the device first:
+# u8 codes with an fp32 scale and offset per 16 weights, each weight equal to
+# the type's dequantized value): Q4_1, Q5_0, Q5_1 and Q2_K, Q3_K, Q8_K, the
+# MatVecMulGeneric branches of LlamaModel.MatVecMulByType (LlamaModel.cs:488-528).
+PACKED_ONLY = {3: "q4_1", 6: "q5_0", 7: "q5_1", 10: "q2_k", 11: "q3_k", 15: "q8_k"}
+
+
+@pytest.mark.parametrize("M,K", [(4096, 4096), (11008, 4096), (4096, 11008), (32000, 2048)])
+@pytest.mark.parametrize("qtype", sorted(PACKED_ONLY))
+def test_packed_unit_types_gemv_shapes(qtype, M, K):
+    run_case(qtype, M, K, seed=11)
+
+
+@pytest.mark.parametrize("qtype,M,K", [
+    (3, 1, 64), (6, 3, 128), (7, 17, 192), (3, 33, 2048), (6, 5, 16384), (7, 130, 5632),
+    (10, 1, 256), (11, 9, 768), (15, 40, 2816), (10, 7, 5632), (11, 3, 16384), (15, 5, 16384),
+])
+def test_packed_unit_types_ragged_shapes(qtype, M, K):
+    run_case(qtype, M, K, seed=13)

@@ -154,6 +154,11 @@ def test_qwen2_upload_rules():
     ("q8_0", _native.GGML_Q8_0, True), ("f32", _native.GGML_F32, False), ("f32", _native.GGML_F32, True),
     ("f16", _native.GGML_F16, False), ("f16", _native.GGML_F16, True), ("mixed", _native.GGML_Q8_0, False),
     ("mixed", _native.GGML_F32, True), ("q4_k_m", _native.GGML_F16, True),
+    # the types read as packed units, as matrices, embeddings and tied LM heads
+    ("legacy_blocks", _native.GGML_Q5_1, False), ("legacy_blocks", _native.GGML_Q4_1, True),
+    ("q3_k_m", _native.GGML_Q3_K, False), ("q3_k_m", _native.GGML_Q5_0, True),
+    ("q2_k", _native.GGML_Q2_K, True), ("q2_k", _native.GGML_Q8_K, False),
+    ("q4_k_m", _native.GGML_Q4_K, True), ("q4_0", _native.GGML_Q6_K, False), ("q8_0", _native.GGML_Q5_K, True),
 ])
 def test_weight_and_embedding_types_match_oracle(mix, emb, tied):
     cfg = TINY_TEST
@@ -437,7 +442,8 @@ def test_span_longer_than_batch_cap_matches_oracle_and_token_schedule(monkeypatc
     compare_greedy(list(gt), o, margins, "span 600 tokens, greedy 16")
 
 
-@pytest.mark.parametrize("mix", ["q4_k_m", "q5_k_m", "q8_0", "q6_k", "q4_k", "mixed_blocks"])
+@pytest.mark.parametrize("mix", ["q4_k_m", "q5_k_m", "q8_0", "q6_k", "q4_k", "mixed_blocks", "legacy_blocks",
+                                 "q3_k_m", "q2_k"])
 def test_span_block_type_mixes_match_oracle(mix):
     """Spans of models with other block types run batched on packed weights
     (every matrix re-encoded once, types mixed freely, ffn_gate and ffn_up of

@@ -354,3 +354,122 @@ def test_argmax_tie_rule():  # GreedySampler.cs:13-26
     assert oracle.argmax(np.array([np.nan, 5, 9], np.float32)) == 0
     assert oracle.argmax(np.array([1, np.nan, 9, 9], np.float32)) == 2
     assert oracle.argmax(np.array([-np.inf, -np.inf], np.float32)) == 0
+
+
+# ---------------------------------------------------------------- Q4_1 / Q5_0 / Q5_1
+def test_q4_1_dequantize_and_dot():  # QuantizationTests.cs:93-135
+    blk = np.frombuffer(h16(2.0) + h16(1.0) + bytes(16), np.uint8)
+    assert np.all(oracle.dequant(oracle.Q4_1, blk, 32) == 1.0)  # 0 * 2 + 1
+    blk = np.frombuffer(h16(1.0) + h16(0.5) + bytes([0x55] * 16), np.uint8)
+    assert oracle.dot(oracle.Q4_1, blk, np.ones(32, np.float32)) == 32 * 5.5
+
+
+def test_q4_1_nibble_positions():
+    qs = bytearray(16)
+    qs[3] = 0xA7  # element 3 gets 7, element 19 gets 10
+    deq = oracle.dequant(oracle.Q4_1, np.frombuffer(h16(1.0) + h16(-1.0) + bytes(qs), np.uint8), 32)
+    want = np.full(32, -1.0, np.float32)
+    want[3], want[19] = 6.0, 9.0
+    assert np.array_equal(deq, want)
+
+
+def test_q5_0_dequantize_and_dot():  # QuantizationTests.cs:140-184
+    blk = np.frombuffer(h16(1.0) + bytes(20), np.uint8)
+    assert np.all(oracle.dequant(oracle.Q5_0, blk, 32) == -16.0)
+    # qh = 0x0000FFFF: elements 0..15 get the fifth bit; qs nibbles 0xA
+    blk = np.frombuffer(h16(0.5) + bytes([0xFF, 0xFF, 0, 0]) + bytes([0xAA] * 16), np.uint8)
+    deq = oracle.dequant(oracle.Q5_0, blk, 32)
+    assert np.all(deq[:16] == 5.0) and np.all(deq[16:] == -3.0)  # (26 - 16) / 2, (10 - 16) / 2
+    assert oracle.dot(oracle.Q5_0, blk, np.full(32, 0.5, np.float32)) == 16.0
+
+
+def test_q5_1_dequantize_and_dot():  # QuantizationTests.cs:189-232
+    blk = np.frombuffer(h16(1.0) + h16(2.0) + bytes(20), np.uint8)
+    assert np.all(oracle.dequant(oracle.Q5_1, blk, 32) == 2.0)
+    blk = np.frombuffer(h16(0.25) + h16(0.5) + bytes(4) + bytes([0x33] * 16), np.uint8)
+    assert oracle.dot(oracle.Q5_1, blk, np.ones(32, np.float32)) == 32 * 1.25
+
+
+@pytest.mark.parametrize("qtype,head", [(6, 2), (7, 4)])
+def test_q5_high_bit_positions(qtype, head):
+    # bit j of the little-endian qh word is element j's fifth bit (DequantQ5_0.cs:36-62)
+    raw = bytearray(h16(1.0) + (h16(0.0) if qtype == 7 else b"") + bytes(20))
+    qh = (1 << 5) | (1 << 20)
+    raw[head:head + 4] = qh.to_bytes(4, "little")
+    deq = oracle.dequant(qtype, np.frombuffer(bytes(raw), np.uint8), 32)
+    base = -16.0 if qtype == 6 else 0.0
+    want = np.full(32, base, np.float32)
+    want[5] += 16.0
+    want[20] += 16.0
+    assert np.array_equal(deq, want)
+
+
+# ---------------------------------------------------------------- Q2_K / Q3_K / Q8_K
+def q2k_block(d, dmin, scale_byte, qs_byte):
+    return np.frombuffer(bytes([scale_byte] * 16) + bytes([qs_byte] * 64) + h16(d) + h16(dmin), np.uint8)
+
+
+def test_q2_k_closed_forms():  # QuantizationTests.cs:351-394
+    assert np.all(oracle.dequant(oracle.Q2_K, q2k_block(1.0, 0.5, 0x21, 0), 256) == -1.0)  # 0 - 0.5 * 2
+    # q = 1 everywhere (0x55), scale 1, min 1: 0.5 * 1 - 0.25 = 0.25 per element
+    assert oracle.dot(oracle.Q2_K, q2k_block(0.5, 0.25, 0x11, 0x55), np.ones(256, np.float32)) == 64.0
+
+
+def test_q2_k_element_positions():
+    # element 128g + 32t + 16h + l = bits 2t.. of qs[32g + 16h + l], scale byte 8g + 2t + h
+    raw = bytearray(q2k_block(1.0, 1.0, 0x00, 0).tobytes())
+    raw[16 + 32 * 1 + 16 * 1 + 7] = 0b11 << 4  # g=1, h=1, l=7, t=2 -> element 128+64+16+7 = 215
+    raw[8 + 2 * 2 + 1] = 0x35  # its scale byte: scale 5, min 3
+    deq = oracle.dequant(oracle.Q2_K, np.frombuffer(bytes(raw), np.uint8), 256)
+    want = np.zeros(256, np.float32)
+    want[208:224] = -3.0  # the sub-block's min applies to all 16 of its elements
+    want[215] = 5.0 * 3 - 3.0
+    assert np.array_equal(deq, want)
+
+
+def test_q3_k_closed_forms():  # QuantizationTests.cs:399-438
+    zero = np.frombuffer(bytes(108) + h16(1.0), np.uint8)  # scales 0 - 32, q3 0: 1 * -32 * -4
+    assert np.all(oracle.dequant(oracle.Q3_K, zero, 256) == 128.0)
+    blk = np.frombuffer(bytes(32) + bytes([0x55] * 64) + bytes(12) + h16(0.1), np.uint8)
+    d = float(np.float16(0.1))
+    deq = oracle.dequant(oracle.Q3_K, blk, 256)
+    assert np.all(deq == np.float32(np.float32(d) * np.float32(-32.0)) * np.float32(-3.0))
+    y = oracle.dot(oracle.Q3_K, blk, np.ones(256, np.float32))
+    assert abs(y - 256 * 96 * d) < 1e-3  # sum of sc * (q3 - 4) = 256 * 96, times d
+
+
+def test_q3_k_scale_decode_and_positions():
+    s = bytearray(12)
+    s[2] = 0x9C  # sc[2] low nibble 0xC, sc[10] low nibble 0x9
+    s[8 + 2] = 0b11_01_10_01  # sc[2] += 1 << 4, sc[6] += 2 << 4, sc[10] += 1 << 4, sc[14] += 3 << 4
+    sc = npref.q3k_scales(np.frombuffer(bytes(s), np.uint8))[0]
+    assert sc[2] == 0x1C - 32 and sc[6] == 0x20 - 32 and sc[10] == 0x19 - 32 and sc[14] == 0x30 - 32
+    raw = bytearray(bytes(32) + bytes(64) + bytes(s) + h16(1.0))
+    raw[32 + 170 // 4] = 0b10 << (2 * (170 % 4))  # element 170: q2 = 2
+    raw[170 // 8] = 1 << (170 % 8)  # its high bit: q3 = 6
+    deq = oracle.dequant(oracle.Q3_K, np.frombuffer(bytes(raw), np.uint8), 256)
+    assert deq[170] == (0x19 - 32) * (6 - 4)  # sub-block 10
+    assert deq[169] == (0x19 - 32) * (0 - 4) and deq[32] == (0x1C - 32) * -4
+
+
+def test_q8_k_closed_forms():  # QuantizationTests.cs:544-586
+    blk = np.frombuffer(np.float32(0.5).tobytes() + bytes([10] * 256) + bytes(32), np.uint8)
+    assert np.all(oracle.dequant(oracle.Q8_K, blk, 256) == 5.0)
+    q = bytes([(i % 20) for i in range(4, 260)])
+    blk = np.frombuffer(np.float32(0.25).tobytes() + q + bytes(32), np.uint8)
+    assert oracle.dot(oracle.Q8_K, blk, np.ones(256, np.float32)) == 0.25 * sum(q)
+    neg = np.frombuffer(np.float32(2.0).tobytes() + bytes([0xFF] + [0] * 255) + bytes(32), np.uint8)
+    assert oracle.dequant(oracle.Q8_K, neg, 256)[0] == -2.0  # sbyte
+
+
+@pytest.mark.parametrize("qtype", [3, 6, 7, 10, 11, 15])
+def test_packed_types_match_float64_restatement(qtype):
+    rows, K = 48, 512
+    t = synth.tensor(qtype, 11, f"pk{qtype}", rows, K)
+    x = synth.normal(12, "pk-x", K, 1.0)
+    W64 = npref.matrix(t)
+    np.testing.assert_allclose(oracle.dequant(qtype, t.data, rows * K).reshape(rows, K), W64, rtol=1e-6,
+                               atol=1e-12)
+    y = oracle.matvec(qtype, t.data, x, rows, K)
+    ref = W64 @ x.astype(np.float64)
+    assert np.max(np.abs(y - ref)) / np.max(np.abs(ref)) < 1e-5

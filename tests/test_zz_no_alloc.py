@@ -55,3 +55,33 @@ def test_noalloc_refuses_more_scratch_than_it_has():
     lib = _native.hip_lib()
     with pytest.raises(_native.ChatnetArgumentError):
         _native.check(lib.chatnet_matmul_noalloc(2, 16, 16, 16, M, K, N, None))
+
+
+@pytest.mark.parametrize("qtype,first,second", [
+    (11, (2048, 2048, 64), (1024, 1024, 2)),   # Q3_K: packed W in the scratch, GEMM then GEMV
+    (3, (4096, 4096, 1), (512, 2048, 16)),     # Q4_1: GEMV then GEMM
+])
+def test_noalloc_packed_unit_types_match_matmul(qtype, first, second):
+    stream = hiprt.Stream()
+    for (M, K, N) in (first, second):
+        announce(f"noalloc type={qtype} M={M} K={K} N={N}")
+        t = synth.tensor(qtype, 5, f"nap{qtype}-{M}x{K}", M, K)
+        x = synth.normal(5, f"napx{N}x{K}", N * K, 1.0)
+        w_d = hiprt.DeviceBuffer.from_numpy(t.data, pad=256)
+        x_d = hiprt.DeviceBuffer.from_numpy(x)
+        ref = _call("chatnet_matmul", qtype, w_d, x_d, M, K, N, stream.h)
+        got = _call("chatnet_matmul_noalloc", qtype, w_d, x_d, M, K, N, stream.h)
+        w_d.free()
+        x_d.free()
+        assert np.all(np.isfinite(got))
+        err = normwise(got, ref)
+        print(f"noalloc type={qtype} M={M} K={K} N={N}: normwise {err:.3g}", flush=True)
+        assert err <= (1e-2 if N >= 8 else 1e-3)
+    stream.synchronize()
+
+
+def test_noalloc_refuses_a_packed_copy_larger_than_its_scratch():
+    # Q2_K 11008 x 4096 packs into 11008 * 64 * 96 bytes (64.5 MiB)
+    lib = _native.hip_lib()
+    with pytest.raises(_native.ChatnetArgumentError):
+        _native.check(lib.chatnet_matmul_noalloc(10, 16, 16, 16, 11008, 4096, 1, None))
