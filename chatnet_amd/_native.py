@@ -34,6 +34,15 @@ GGML_Q5_1 = 7
 GGML_Q2_K = 10
 GGML_Q3_K = 11
 GGML_Q8_K = 15
+GGML_IQ2_XXS = 16
+GGML_IQ2_XS = 17
+GGML_IQ3_XXS = 18
+GGML_IQ1_S = 19
+GGML_IQ4_NL = 20
+GGML_IQ3_S = 21
+GGML_IQ2_S = 22
+GGML_IQ4_XS = 23
+GGML_IQ1_M = 29
 
 KV_F32 = 0
 KV_F16 = 1

@@ -75,8 +75,9 @@ int device_cus(int dev) {
 
 // Weight types the GEMV serves (LlamaModel.MatVecMulByType, LlamaModel.cs:470-567):
 // F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K from the stored blocks, and Q4_1,
-// Q5_0, Q5_1, Q2_K, Q3_K, Q8_K (the reference's MatVecMulGeneric branches,
-// LlamaModel.cs:488-511, 517-528) from packed units made at upload.
+// Q5_0, Q5_1, Q2_K, Q3_K, Q8_K and the nine IQ types (the reference's
+// MatVecMulGeneric branches, LlamaModel.cs:488-562) from packed units made at
+// upload.
 bool is_matrix_type(uint32_t t) {
   return t == CHATNET_GGML_F32 || t == CHATNET_GGML_F16 || t == CHATNET_GGML_Q4_0 || t == CHATNET_GGML_Q8_0 ||
          t == CHATNET_GGML_Q4_K || t == CHATNET_GGML_Q5_K || t == CHATNET_GGML_Q6_K || gemv_needs_pack((int)t);
@@ -482,6 +483,10 @@ int chatnet_upload_tensor(chatnet_model* m, const char* name, uint32_t type, con
     slot = &m->emb; want0 = c.dim; want1 = c.vocab_size; matrix = false;
     if (!embed_raw_type(type) && !gemm_pack_supports((int)type, 256))
       return fail(CHATNET_ERR_UNSUPPORTED_TYPE, "token_embd.weight: type %u not supported", type);
+    if (type == CHATNET_GGML_IQ3_S)  // IQ3S.Dequantize indexes past the row it is given (DequantIQ.cs:266, :280)
+      return fail(CHATNET_ERR_OUT_OF_RANGE,
+                  "token_embd.weight: IQ3_S rows cannot be dequantized one at a time (the reference's "
+                  "IQ3S.Dequantize reads 28 bytes past the row and throws IndexOutOfRangeException)");
     if (!embed_raw_type(type) && !gemm_pack_supports((int)type, c.dim))
       return fail(CHATNET_ERR_INVALID_ARG, "token_embd.weight: dim %d not a multiple of the type's block", c.dim);
     if ((type == CHATNET_GGML_Q4_0 || type == CHATNET_GGML_Q8_0) && c.dim % 32 != 0)
@@ -520,7 +525,7 @@ int chatnet_upload_tensor(chatnet_model* m, const char* name, uint32_t type, con
     if (!is_matrix_type(type))
       return fail(CHATNET_ERR_UNSUPPORTED_TYPE,
                   "tensor %s: weight type %u not supported (F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, "
-                  "Q4_K, Q5_K, Q6_K, Q8_K)",
+                  "Q4_K, Q5_K, Q6_K, Q8_K, IQ2_XXS, IQ2_XS, IQ3_XXS, IQ1_S, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS, IQ1_M)",
                   name, type);
     if (!gemv_supports((int)type, (int)ne0))
       return fail(CHATNET_ERR_INVALID_ARG, "tensor %s: inner dim %llu not a multiple of the block", name,
@@ -541,7 +546,13 @@ int chatnet_upload_tensor(chatnet_model* m, const char* name, uint32_t type, con
     return fail(CHATNET_ERR_OUT_OF_MEMORY, "hipMalloc of %llu bytes for %s failed", (unsigned long long)nbytes, name);
   const bool neox_rows = c.arch == CHATNET_ARCH_QWEN2 && layer >= 0 &&
                          (slot == &m->layers[layer].wq || slot == &m->layers[layer].wk);
-  if (neox_rows) {
+  // Types the GEMV (or the embedding gather) reads only as packed units are
+  // packed below, one pass over the uploaded rows; the stored blocks stay for
+  // the other readers.  Their stored rows keep the file's order even where the
+  // Qwen2 row order applies (an IQ3_S row reads into the row after it in the
+  // file, DequantIQ.cs:255-283): the packed rows are put in that order instead.
+  const bool pack_now = (matrix && gemv_needs_pack((int)type)) || (slot == &m->emb && !embed_raw_type(type));
+  if (neox_rows && !pack_now) {
     const size_t bpr = (size_t)(nbytes / ne1);
     std::vector<uint8_t> rows(nbytes);
     for (uint64_t r = 0; r < ne1; r++)
@@ -555,17 +566,30 @@ int chatnet_upload_tensor(chatnet_model* m, const char* name, uint32_t type, con
   slot->nbytes = nbytes;
   slot->ne0 = ne0;
   slot->ne1 = ne1;
-  // Types the GEMV (or the embedding gather) reads only as packed units are
-  // packed now, one pass over the uploaded rows; the stored blocks stay for
-  // the other readers.
-  if ((matrix && gemv_needs_pack((int)type)) || (slot == &m->emb && !embed_raw_type(type))) {
+  if (pack_now) {
     const size_t pk_bytes = gemm_pack_bytes((int)ne1, (int)ne0);
     if (hipMalloc(&slot->pk, pk_bytes) != hipSuccess) {
       slot->pk = nullptr;
       return fail(CHATNET_ERR_OUT_OF_MEMORY, "hipMalloc of %zu bytes (packed %s) failed", pk_bytes, name);
     }
-    HIP_TRY(gemm_pack_launch((int)type, slot->ptr, (int)ne1, (int)ne0, slot->pk, m->stream));
-    HIP_TRY(hipStreamSynchronize(m->stream));
+    if (neox_rows) {
+      void* tmp = nullptr;
+      if (hipMalloc(&tmp, pk_bytes) != hipSuccess)
+        return fail(CHATNET_ERR_OUT_OF_MEMORY, "hipMalloc of %zu bytes (packed %s) failed", pk_bytes, name);
+      const size_t prow = pk_bytes / ne1;
+      hipError_t e = gemm_pack_launch((int)type, slot->ptr, (int)ne1, (int)ne0, tmp, m->stream);
+      for (uint64_t r = 0; r < ne1 && e == hipSuccess; r++)
+        e = hipMemcpyAsync((char*)slot->pk + r * prow,
+                           (const char*)tmp + (size_t)neox_source_row((int)r, c.head_dim) * prow, prow,
+                           hipMemcpyDeviceToDevice, m->stream);
+      const hipError_t es = hipStreamSynchronize(m->stream);
+      (void)hipFree(tmp);
+      HIP_TRY(e);
+      HIP_TRY(es);
+    } else {
+      HIP_TRY(gemm_pack_launch((int)type, slot->ptr, (int)ne1, (int)ne0, slot->pk, m->stream));
+      HIP_TRY(hipStreamSynchronize(m->stream));
+    }
   }
   drop_graphs(m);
   g_err.clear();

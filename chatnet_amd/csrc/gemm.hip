@@ -708,6 +708,13 @@ __global__ __launch_bounds__(CN_BLOCK) void add_rmsnorm_bf16_kernel(float* __res
 //   Q5_K (DequantQ5K.cs)   code q5,     scale d*sc[s],  offset -(dmin*m[s])
 //   Q6_K (DequantQ6K.cs)   code q+32,   scale d*sc[i],  offset -32*d*sc[i]
 //   Q8_K (DequantQ8K.cs)   code q+128,  scale d (fp32), offset -128d
+//   IQ4_NL, IQ4_XS (DequantIQ.cs)  code table[q]+128, scale d or d*sc, offset -128*scale
+//   IQ3_S    code +-(sc*q3)+128, scale d, offset -128d (sc folded into the code)
+//   IQ3_XXS  code q3, scale d, offset -4d
+//   IQ2_XXS, IQ2_XS  code q, scale d or d*sc, offset -scale
+//   IQ2_S    code +-q+128, scale d*sc, offset -128*scale
+//   IQ1_S, IQ1_M  code 128+t (t in -1..1; IQ1_M 128+t*2 at full scale), scale d
+//            (IQ1_M d/2), offset -128*scale
 // (d*sc, dmin*m and the power-of-two multiples are exact in fp32, and so is
 // code*scale for the fp16-scaled types, so their one rounding is the
 // reference's final add (or none); Q6_K's (d*sc)*q and Q8_K's q*d are rounded
@@ -731,8 +738,12 @@ __device__ __forceinline__ void k4_scale_min(const uint8_t* q, int j, int& sc, i
   }
 }
 
+// IQ4_NL's table (DequantIQ.IQ4NL_Table, DequantIQ.cs:29-33) plus 128: the
+// packed code of each index.
+__constant__ uint8_t cn_iq4nl_code[16] = {1, 24, 45, 63, 79, 93, 106, 118, 129, 141, 153, 166, 181, 197, 217, 241};
+
 __global__ __launch_bounds__(CN_BLOCK) void gemm_pack_kernel(int qtype, const uint8_t* __restrict__ w,
-                                                            size_t row_bytes, int M, int nchunks,
+                                                            size_t row_bytes, size_t w_bytes, int M, int nchunks,
                                                             uint8_t* __restrict__ dst) {
   const long long t = (long long)blockIdx.x * CN_BLOCK + threadIdx.x;
   if (t >= (long long)M * nchunks) return;
@@ -843,6 +854,120 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_pack_kernel(int qtype, const ui
     for (int g = 0; g < 4; g++) {
       sc[g] = d;
       of[g] = -128.0f * d;
+    }
+  } else if (qtype == 20) {  // IQ4_NL: blocks 2c and 2c+1 of 32 (DequantIQ.cs:46-76)
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+      const uint8_t* blk = row + (size_t)(2 * c + b) * 18;
+      const float d = h2f_at(blk);
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        put(32 * b + j, cn_iq4nl_code[blk[2 + j] & 15]);
+        put(32 * b + 16 + j, cn_iq4nl_code[blk[2 + j] >> 4]);
+      }
+      sc[2 * b] = sc[2 * b + 1] = d;
+      of[2 * b] = of[2 * b + 1] = -128.0f * d;
+    }
+  } else if (qtype == 23) {  // IQ4_XS: sub-blocks 2(c%4), 2(c%4)+1 (DequantIQ.cs:139-176)
+    const uint8_t* blk = row + (size_t)(c >> 2) * 136;
+    const float d = h2f_at(blk);
+    const int sh = blk[2] | (blk[3] << 8);
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+      const int s = 2 * (c & 3) + b;
+      // low scale bits from byte 4+s (bytes 8..11 are sub-block 0's first quants)
+      const int scv = ((blk[4 + s] & 0x3F) | (((sh >> (2 * s)) & 3) << 6)) - 32;
+      const uint8_t* qs = blk + 8 + 16 * s;
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        put(32 * b + j, cn_iq4nl_code[qs[j] & 15]);
+        put(32 * b + 16 + j, cn_iq4nl_code[qs[j] >> 4]);
+      }
+      sc[2 * b] = sc[2 * b + 1] = d * (float)scv;
+      of[2 * b] = of[2 * b + 1] = -128.0f * sc[2 * b];
+    }
+  } else if (qtype == 21) {  // IQ3_S: elements 64(c%4) .. +63 (DequantIQ.cs:244-290)
+    // sign bytes 98..129 and scale bytes 130..137 reach up to 28 bytes into the
+    // next block; past the end of w they read as zero (the tail a model's
+    // upload pads with)
+    const size_t base = (size_t)r * row_bytes + (size_t)(c >> 2) * 110;
+    auto at = [&](int off) -> uint32_t { return base + off < w_bytes ? w[base + off] : 0u; };
+    const float d = h2f_at(w + base);
+#pragma unroll
+    for (int j = 0; j < 64; j++) {
+      const int idx = 64 * (c & 3) + j, sub = idx >> 3;
+      const int q3 = (int)(((at(2 + idx / 4) >> (2 * (idx % 4))) & 3u) | (((at(66 + idx / 8) >> (idx % 8)) & 1u) << 2));
+      const int scv = (int)((at(130 + sub / 4) >> (2 * (sub % 4))) & 3u) + 1;
+      const int v = ((at(98 + sub) >> (idx & 7)) & 1u) ? -scv * q3 : scv * q3;
+      put(j, (uint32_t)(v + 128));
+    }
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      sc[g] = d;
+      of[g] = -128.0f * d;
+    }
+  } else if (qtype == 18) {  // IQ3_XXS: d * (q3 - 4) (DequantIQ.cs:364-399)
+    const uint8_t* blk = row + (size_t)(c >> 2) * 98;
+    const float d = h2f_at(blk);
+#pragma unroll
+    for (int j = 0; j < 64; j++) {
+      const int idx = 64 * (c & 3) + j;
+      const uint8_t* p = blk + 2 + 3 * (idx >> 3);
+      const uint32_t word = (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16);
+      put(j, (word >> (3 * (idx & 7))) & 7u);
+    }
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      sc[g] = d;
+      of[g] = -4.0f * d;
+    }
+  } else if (qtype == 16 || qtype == 17 || qtype == 22) {  // IQ2_XXS / IQ2_XS / IQ2_S: sub-blocks 4(c%4) ..
+    const int bb = qtype == 16 ? 66 : (qtype == 17 ? 74 : 82);
+    const uint8_t* blk = row + (size_t)(c >> 2) * bb;
+    const float d = h2f_at(blk);
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const int sub = 4 * (c & 3) + g;
+      const uint8_t* qs = blk + 2 + 4 * sub;
+      if (qtype == 22) {  // (d * (low nibble + 1)) * q, elements 0..3 signed (DequantIQ.cs:656-696)
+        const uint32_t qh = blk[66 + sub];
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const int q = (qs[e >> 2] >> (2 * (e & 3))) & 3;
+          const bool neg = e < 4 && ((qh >> (4 + e)) & 1u);
+          put(16 * g + e, (uint32_t)((neg ? -q : q) + 128));
+        }
+        sc[g] = d * (float)((qh & 15u) + 1);
+        of[g] = -128.0f * sc[g];
+      } else {  // d * (q - 1) or (d * sc) * (q - 1), sc a signed nibble - 8 (DequantIQ.cs:456-598)
+#pragma unroll
+        for (int e = 0; e < 16; e++) put(16 * g + e, (qs[e >> 2] >> (2 * (e & 3))) & 3u);
+        float dsc = d;
+        if (qtype == 17) {
+          const int raw = (int8_t)blk[66 + sub / 2];
+          dsc = d * (float)(((sub & 1) ? (raw >> 4) & 15 : raw & 15) - 8);
+        }
+        sc[g] = dsc;
+        of[g] = -dsc;
+      }
+    }
+  } else if (qtype == 19 || qtype == 29) {  // IQ1_S / IQ1_M: ternary (DequantIQ.cs:767-805, :869-914)
+    const int bb = qtype == 19 ? 50 : 56;
+    const uint8_t* blk = row + (size_t)(c >> 2) * bb;
+    const float d = h2f_at(blk);
+#pragma unroll
+    for (int j = 0; j < 64; j++) {
+      const int idx = 64 * (c & 3) + j, sub = idx >> 3, e = idx & 7;
+      const int tv = ((blk[2 + sub] >> e) & 1) ? 1 : (((blk[34 + sub / 2] >> ((sub & 1) * 4 + e / 2)) & 1) ? -1 : 0);
+      // IQ1_M: d * sc with sc 1 or 0.5 (bit sub%8 of byte 50 + sub/8) as (d/2) * (2 or 1)
+      const int m = qtype == 19 ? 1 : (((blk[50 + sub / 8] >> (sub & 7)) & 1) ? 2 : 1);
+      put(j, (uint32_t)(128 + tv * m));
+    }
+    const float step = qtype == 19 ? d : 0.5f * d;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      sc[g] = step;
+      of[g] = -128.0f * step;
     }
   } else {  // Q6_K: elements 64(c%4) .. +63 of the super-block
     const uint8_t* blk = row + (size_t)(c >> 2) * 210;
@@ -974,8 +1099,8 @@ bool gemm_supports(int qtype, int K) { return qtype == 2 && K > 0 && K % 64 == 0
 
 bool gemm_pack_supports(int qtype, int K) {
   if (K <= 0) return false;
-  if (qtype == 2 || qtype == 3 || qtype == 6 || qtype == 7 || qtype == 8) return K % 64 == 0;
-  if (qtype == 10 || qtype == 11 || qtype == 12 || qtype == 13 || qtype == 14 || qtype == 15) return K % 256 == 0;
+  if (qtype == 2 || qtype == 3 || qtype == 6 || qtype == 7 || qtype == 8 || qtype == 20) return K % 64 == 0;
+  if ((qtype >= 10 && qtype <= 19) || (qtype >= 21 && qtype <= 23) || qtype == 29) return K % 256 == 0;
   return false;
 }
 
@@ -995,13 +1120,23 @@ hipError_t gemm_pack_launch(int qtype, const void* w, int M, int K, void* dst, h
     case 12: row_bytes = (size_t)K / 256 * 144; break;
     case 13: row_bytes = (size_t)K / 256 * 176; break;
     case 15: row_bytes = (size_t)K / 256 * 292; break;
+    case 16: row_bytes = (size_t)K / 256 * 66; break;
+    case 17: row_bytes = (size_t)K / 256 * 74; break;
+    case 18: row_bytes = (size_t)K / 256 * 98; break;
+    case 19: row_bytes = (size_t)K / 256 * 50; break;
+    case 20: row_bytes = (size_t)K / 32 * 18; break;
+    case 21: row_bytes = (size_t)K / 256 * 110; break;
+    case 22: row_bytes = (size_t)K / 256 * 82; break;
+    case 23: row_bytes = (size_t)K / 256 * 136; break;
+    case 29: row_bytes = (size_t)K / 256 * 56; break;
     default: row_bytes = (size_t)K / 256 * 210; break;
   }
   const long long n = (long long)M * (K / 64);
   const long long blocks = (n + CN_BLOCK - 1) / CN_BLOCK;
   if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
   hipLaunchKernelGGL(gemm_pack_kernel, dim3((unsigned)blocks), dim3(CN_BLOCK), 0, st, qtype,
-                     static_cast<const uint8_t*>(w), row_bytes, M, K / 64, static_cast<uint8_t*>(dst));
+                     static_cast<const uint8_t*>(w), row_bytes, (size_t)M * row_bytes, M, K / 64,
+                     static_cast<uint8_t*>(dst));
   return hipGetLastError();
 }
 

@@ -1246,15 +1246,25 @@ bool gemv_supports(int qtype, int K) {
     case 3:   // Q4_1
     case 6:   // Q5_0
     case 7: return K > 0 && K % 64 == 0 && K <= 16384;  // Q5_1
+    case 20: return K > 0 && K % 64 == 0 && K <= 16384;  // IQ4_NL
     case 10:  // Q2_K
     case 11:  // Q3_K
-    case 15: return K > 0 && K % 256 == 0 && K <= 16384;  // Q8_K
+    case 15:  // Q8_K
+    case 16:  // IQ2_XXS
+    case 17:  // IQ2_XS
+    case 18:  // IQ3_XXS
+    case 19:  // IQ1_S
+    case 21:  // IQ3_S
+    case 22:  // IQ2_S
+    case 23:  // IQ4_XS
+    case 29: return K > 0 && K % 256 == 0 && K <= 16384;  // IQ1_M
     default: return false;
   }
 }
 
 bool gemv_needs_pack(int qtype) {
-  return qtype == 3 || qtype == 6 || qtype == 7 || qtype == 10 || qtype == 11 || qtype == 15;
+  return qtype == 3 || qtype == 6 || qtype == 7 || qtype == 10 || qtype == 11 || qtype == 15 ||
+         (qtype >= 16 && qtype <= 23) || qtype == 29;
 }
 
 hipError_t gemv_launch(int qtype, int epi, const GemvArgs& a, int num_cus, hipStream_t st) {

@@ -15,12 +15,16 @@
  *   Q5_K  DequantQ5K.cs:7-34,58-83 fp16 d, fp16 dmin, 12 B scales/mins, qh[32]
  *                                  (bit e%8 of qh[e/8] = bit 4 of element e),
  *                                  qs[128] in Q4_K's nibble order
+ *   Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q8_K and the IQ family as the reference's
+ *                                  dequantizers read them (DequantQ4_1.cs ..
+ *                                  DequantQ8K.cs, DequantIQ.cs)
  * Every element is a pure function of (seed, stream, index): a splitmix64
  * counter hash feeds a Box-Muller transform, so any tensor can be regenerated
  * bit-identically, in any order, on any number of threads.
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #define EXPORT __attribute__((visibility("default")))
@@ -478,6 +482,259 @@ static void quant_block_q8_k(const float* w, uint8_t* out) {
   }
 }
 
+/* ---------------------------------------------------------------------------
+ * The IQ family as the reference decodes it (DequantIQ.cs: bit fields, no
+ * codebooks).  Each encoder picks, per weight, the nearest value the decoder
+ * can produce under the fields it has already fixed.
+ * ------------------------------------------------------------------------- */
+static const float kIQ4NL[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+static int nearest_iq4(float v, float dsc) {
+  int best = 0;
+  float be = INFINITY;
+  for (int q = 0; q < 16; q++) {
+    float e = fabsf(dsc * kIQ4NL[q] - v);
+    if (e < be) { be = e; best = q; }
+  }
+  return best;
+}
+
+static float signed_amax(const float* w, int n) {
+  float a = 0.f;
+  for (int i = 0; i < n; i++)
+    if (fabsf(w[i]) > fabsf(a)) a = w[i];
+  return a;
+}
+
+/* IQ4_NL (DequantIQ.cs:46-76): d = -amax/127, so the largest weight lands on
+ * table[0]; elements j<16 low nibbles, 16+j high nibbles of qs[j]. */
+static void quant_block_iq4_nl(const float* w, uint8_t* out) {
+  uint16_t dh = chatnet_float_to_half(-signed_amax(w, 32) / 127.0f);
+  float d = half_to_float(dh);
+  put16(out, dh);
+  for (int j = 0; j < 16; j++)
+    out[2 + j] = (uint8_t)(nearest_iq4(w[j], d) | (nearest_iq4(w[16 + j], d) << 4));
+}
+
+/* IQ4_XS (DequantIQ.cs:139-176): sub-block s's scale is (byte 4+s & 63 |
+ * 2 bits of scales_h << 6) - 32, and bytes 8..11 are also the first quants of
+ * sub-block 0.  Sub-blocks 0..3 get their scale freely; sub-block 0 is
+ * quantized next, which fixes the low 6 bits of the scales of 4..7, whose
+ * high bits are then chosen nearest to the wanted scale. */
+static void quant_block_iq4_xs(const float* w, uint8_t* out) {
+  float amax = 0.f, want[8];
+  for (int s = 0; s < 8; s++) {
+    want[s] = fabsf(signed_amax(w + 32 * s, 32));
+    if (want[s] > amax) amax = want[s];
+  }
+  uint16_t dh = chatnet_float_to_half(amax / (113.0f * 190.0f));
+  float d = half_to_float(dh);
+  memset(out, 0, 136);
+  put16(out, dh);
+  int sh = 0;
+  for (int s = 0; s < 8; s++) {
+    /* positive scales: the table's end on the largest weight's side (113 or -127) meets it */
+    float sa = signed_amax(w + 32 * s, 32);
+    int sc = d > 0.f ? nearest_int(fabsf(sa) / (sa > 0.f ? 113.0f : 127.0f) / d) : 0;
+    if (s < 4) {
+      int v = sc + 32;
+      v = v < 0 ? 0 : (v > 255 ? 255 : v);
+      out[4 + s] = (uint8_t)(v & 63);
+      sh |= (v >> 6) << (2 * s);
+    } else {
+      int low = out[4 + s] & 63, best = 0, be = 1 << 30;
+      for (int hi = 0; hi < 4; hi++) {
+        int e = abs((low | (hi << 6)) - 32 - sc);
+        if (e < be) { be = e; best = hi; }
+      }
+      sh |= best << (2 * s);
+    }
+    put16(out + 2, (uint16_t)sh);
+    int scv = ((out[4 + s] & 63) | (((sh >> (2 * s)) & 3) << 6)) - 32;
+    float dsc = d * (float)scv;
+    for (int j = 0; j < 16; j++) {
+      int lo = nearest_iq4(w[32 * s + j], dsc), hi = nearest_iq4(w[32 * s + 16 + j], dsc);
+      out[8 + 16 * s + j] = (uint8_t)(lo | (hi << 4));
+    }
+  }
+}
+
+/* IQ3_S (DequantIQ.cs:244-290): value +-(d*sc)*q3; the signs of sub-blocks
+ * 12..31 and all eight scale bytes are bytes 0..27 of the next block (`next`,
+ * zeros past the tensor), fixed before this block is encoded; own sign bytes
+ * (sub-blocks 0..11) follow the weights. */
+static void quant_block_iq3_s(const float* w, uint8_t* out, const uint8_t* next) {
+  int sc[32];
+  float need = 0.f;
+  for (int s = 0; s < 32; s++) {
+    sc[s] = ((next[20 + s / 4] >> (2 * (s % 4))) & 3) + 1;
+    float a = fabsf(signed_amax(w + 8 * s, 8)) / (7.0f * (float)sc[s]);
+    if (a > need) need = a;
+  }
+  uint16_t dh = chatnet_float_to_half(need);
+  float d = half_to_float(dh);
+  memset(out, 0, 110);
+  put16(out, dh);
+  for (int s = 0; s < 32; s++) {
+    uint8_t sb;
+    if (s < 12) {
+      sb = 0;
+      for (int j = 0; j < 8; j++) sb |= (uint8_t)((w[8 * s + j] < 0.f) << j);
+      out[98 + s] = sb;
+    } else {
+      sb = next[s - 12];
+    }
+    float dsc = d * (float)sc[s];
+    for (int j = 0; j < 8; j++) {
+      int idx = 8 * s + j, neg = (sb >> j) & 1;
+      float v = w[idx];
+      int q = 0;
+      if (dsc > 0.f && ((v < 0.f) == (neg != 0))) {
+        q = nearest_int(fabsf(v) / dsc);
+        q = q > 7 ? 7 : q;
+      }
+      out[2 + idx / 4] |= (uint8_t)((q & 3) << (2 * (idx % 4)));
+      out[66 + idx / 8] |= (uint8_t)(((q >> 2) & 1) << (idx % 8));
+    }
+  }
+}
+
+/* IQ3_XXS (DequantIQ.cs:364-399): d*(q3-4), 3-bit fields of a 24-bit word
+ * per 8 elements. */
+static void quant_block_iq3_xxs(const float* w, uint8_t* out) {
+  uint16_t dh = chatnet_float_to_half(-signed_amax(w, 256) / 4.0f);
+  float d = half_to_float(dh);
+  memset(out, 0, 98);
+  put16(out, dh);
+  for (int s = 0; s < 32; s++) {
+    uint32_t packed = 0;
+    for (int j = 0; j < 8; j++) {
+      int q = d != 0.f ? nearest_int(w[8 * s + j] / d) + 4 : 4;
+      q = q < 0 ? 0 : (q > 7 ? 7 : q);
+      packed |= (uint32_t)q << (3 * j);
+    }
+    out[2 + 3 * s] = (uint8_t)packed;
+    out[3 + 3 * s] = (uint8_t)(packed >> 8);
+    out[4 + 3 * s] = (uint8_t)(packed >> 16);
+  }
+}
+
+/* The 2-bit fields of IQ2_XS / IQ2_XXS / IQ2_S: element e of sub-block s at
+ * bits 2(e%4) of byte 2 + 4s + e/4. */
+static inline void put_iq2(uint8_t* out, int s, int e, int q) { out[2 + 4 * s + e / 4] |= (uint8_t)((q & 3) << (2 * (e % 4))); }
+
+/* IQ2_XS (DequantIQ.cs:456-496): (d*sc)*(q-1), sc a nibble - 8 per 16
+ * elements; scales kept positive, q-1 spans -1..2. */
+static void quant_block_iq2_xs(const float* w, uint8_t* out) {
+  float amax = 0.f;
+  for (int i = 0; i < 256; i++) amax = fabsf(w[i]) > amax ? fabsf(w[i]) : amax;
+  uint16_t dh = chatnet_float_to_half(amax / 14.0f);
+  float d = half_to_float(dh);
+  memset(out, 0, 74);
+  put16(out, dh);
+  for (int s = 0; s < 16; s++) {
+    float a = fabsf(signed_amax(w + 16 * s, 16));
+    int sc = d > 0.f ? nearest_int(a / 2.0f / d) : 1;
+    sc = sc < 1 ? 1 : (sc > 7 ? 7 : sc);
+    out[66 + s / 2] |= (uint8_t)((sc + 8) << (4 * (s & 1)));
+    float dsc = d * (float)sc;
+    for (int e = 0; e < 16; e++) {
+      int q = dsc > 0.f ? nearest_int(w[16 * s + e] / dsc) + 1 : 1;
+      put_iq2(out, s, e, q < 0 ? 0 : (q > 3 ? 3 : q));
+    }
+  }
+}
+
+/* IQ2_XXS (DequantIQ.cs:568-598): d*(q-1). */
+static void quant_block_iq2_xxs(const float* w, uint8_t* out) {
+  float amax = 0.f;
+  for (int i = 0; i < 256; i++) amax = fabsf(w[i]) > amax ? fabsf(w[i]) : amax;
+  uint16_t dh = chatnet_float_to_half(amax / 2.0f);
+  float d = half_to_float(dh);
+  memset(out, 0, 66);
+  put16(out, dh);
+  for (int i = 0; i < 256; i++) {
+    int q = d > 0.f ? nearest_int(w[i] / d) + 1 : 1;
+    put_iq2(out, i / 16, i % 16, q < 0 ? 0 : (q > 3 ? 3 : q));
+  }
+}
+
+/* IQ2_S (DequantIQ.cs:656-696): (d*sc)*q, q 0..3, sc = low nibble + 1; only
+ * elements 0..3 of a sub-block can be negative (sign nibble). */
+static void quant_block_iq2_s(const float* w, uint8_t* out) {
+  float amax = 0.f;
+  for (int i = 0; i < 256; i++) amax = fabsf(w[i]) > amax ? fabsf(w[i]) : amax;
+  uint16_t dh = chatnet_float_to_half(amax / 48.0f);
+  float d = half_to_float(dh);
+  memset(out, 0, 82);
+  put16(out, dh);
+  for (int s = 0; s < 16; s++) {
+    float a = fabsf(signed_amax(w + 16 * s, 16));
+    int sc = d > 0.f ? nearest_int(a / 3.0f / d) : 1;
+    sc = sc < 1 ? 1 : (sc > 16 ? 16 : sc);
+    int sign = 0;
+    float dsc = d * (float)sc;
+    for (int e = 0; e < 16; e++) {
+      float v = w[16 * s + e];
+      if (e < 4 && v < 0.f) sign |= 1 << e;
+      int q = (dsc > 0.f && (v >= 0.f || e < 4)) ? nearest_int(fabsf(v) / dsc) : 0;
+      put_iq2(out, s, e, q > 3 ? 3 : q);
+    }
+    out[66 + s] = (uint8_t)((sc - 1) | (sign << 4));
+  }
+}
+
+/* IQ1_S / IQ1_M (DequantIQ.cs:767-805, :869-914): element j of sub-block s is
+ * +1 with bit j of qs[s], else -1 with bit (s%2)*4 + j/2 of qh[s/2] (shared by
+ * two elements), else 0; times d (IQ1_S) or d*sc, sc = 1 or 0.5 (IQ1_M).  The
+ * shared bit is set where it lowers the pair's error. */
+static float iq1_encode_sub(const float* w, float step, uint8_t* qs, uint8_t* qh, int s, int write) {
+  float err = 0.f;
+  uint8_t bits = 0, hb = 0;
+  for (int p = 0; p < 4; p++) {
+    float e0 = 0.f, e1 = 0.f;  /* pair error without / with the shared -1 bit */
+    uint8_t b0 = 0, b1 = 0;
+    for (int k = 0; k < 2; k++) {
+      int j = 2 * p + k;
+      float v = w[j];
+      float zero = fabsf(v), plus = fabsf(v - step), minus = fabsf(v + step);
+      if (plus < zero) { e0 += plus; b0 |= (uint8_t)(1 << j); } else e0 += zero;
+      if (plus < minus) { e1 += plus; b1 |= (uint8_t)(1 << j); } else e1 += minus;
+    }
+    if (e1 < e0) { err += e1; bits |= b1; hb |= (uint8_t)(1 << p); } else { err += e0; bits |= b0; }
+  }
+  if (write) {
+    qs[s] = bits;
+    qh[s / 2] |= (uint8_t)(hb << ((s % 2) * 4));
+  }
+  return err;
+}
+
+static void quant_block_iq1_s(const float* w, uint8_t* out) {
+  float mean = 0.f;
+  for (int i = 0; i < 256; i++) mean += fabsf(w[i]);
+  uint16_t dh = chatnet_float_to_half(1.5f * mean / 256.0f);
+  float d = half_to_float(dh);
+  memset(out, 0, 50);
+  put16(out, dh);
+  for (int s = 0; s < 32; s++) iq1_encode_sub(w + 8 * s, d, out + 2, out + 34, s, 1);
+}
+
+static void quant_block_iq1_m(const float* w, uint8_t* out) {
+  float mean = 0.f;
+  for (int i = 0; i < 256; i++) mean += fabsf(w[i]);
+  uint16_t dh = chatnet_float_to_half(2.0f * mean / 256.0f);
+  float d = half_to_float(dh);
+  memset(out, 0, 56);
+  put16(out, dh);
+  for (int s = 0; s < 32; s++) {
+    int full = iq1_encode_sub(w + 8 * s, d, out + 2, out + 34, s, 0) <=
+               iq1_encode_sub(w + 8 * s, 0.5f * d, out + 2, out + 34, s, 0);
+    iq1_encode_sub(w + 8 * s, full ? d : 0.5f * d, out + 2, out + 34, s, 1);
+    if (full) out[50 + s / 8] |= (uint8_t)(1 << (s % 8));
+  }
+}
+
 static int block_info(uint32_t type, int* blk, int* bytes) {
   switch (type) {
     case 2: *blk = 32; *bytes = 18; return 0;
@@ -491,6 +748,15 @@ static int block_info(uint32_t type, int* blk, int* bytes) {
     case 10: *blk = 256; *bytes = 84; return 0;
     case 11: *blk = 256; *bytes = 110; return 0;
     case 15: *blk = 256; *bytes = 292; return 0;
+    case 16: *blk = 256; *bytes = 66; return 0;
+    case 17: *blk = 256; *bytes = 74; return 0;
+    case 18: *blk = 256; *bytes = 98; return 0;
+    case 19: *blk = 256; *bytes = 50; return 0;
+    case 20: *blk = 32; *bytes = 18; return 0;
+    case 21: *blk = 256; *bytes = 110; return 0;
+    case 22: *blk = 256; *bytes = 82; return 0;
+    case 23: *blk = 256; *bytes = 136; return 0;
+    case 29: *blk = 256; *bytes = 56; return 0;
     default: return -1;
   }
 }
@@ -507,6 +773,14 @@ static void quant_block(uint32_t type, const float* src, uint8_t* dst) {
     case 10: quant_block_q2_k(src, dst); break;
     case 11: quant_block_q3_k(src, dst); break;
     case 15: quant_block_q8_k(src, dst); break;
+    case 16: quant_block_iq2_xxs(src, dst); break;
+    case 17: quant_block_iq2_xs(src, dst); break;
+    case 18: quant_block_iq3_xxs(src, dst); break;
+    case 19: quant_block_iq1_s(src, dst); break;
+    case 20: quant_block_iq4_nl(src, dst); break;
+    case 22: quant_block_iq2_s(src, dst); break;
+    case 23: quant_block_iq4_xs(src, dst); break;
+    case 29: quant_block_iq1_m(src, dst); break;
     default: quant_block_q6_k(src, dst); break;
   }
 }
@@ -517,6 +791,13 @@ EXPORT uint64_t chatnet_synth_quantize(uint32_t type, const float* w, uint64_t n
   if (block_info(type, &blk, &bytes) || n % (uint64_t)blk) return 0;
   uint64_t nb = n / (uint64_t)blk;
   uint8_t* o = (uint8_t*)out;
+  if (type == 21) {  /* IQ3_S: each block reads 28 bytes of the next, so encode back to front */
+    static const uint8_t zeros[28] = {0};
+    for (int64_t b = (int64_t)nb - 1; b >= 0; b--)
+      quant_block_iq3_s(w + (uint64_t)b * blk, o + (uint64_t)b * bytes,
+                        b + 1 < (int64_t)nb ? o + (uint64_t)(b + 1) * bytes : zeros);
+    return nb * (uint64_t)bytes;
+  }
 #pragma omp parallel for schedule(static)
   for (int64_t b = 0; b < (int64_t)nb; b++) {
     const float* src = w + (uint64_t)b * blk;
@@ -540,6 +821,21 @@ EXPORT uint64_t chatnet_synth_tensor(uint32_t type, uint64_t seed, uint64_t stre
   uint64_t nb = n / (uint64_t)blk;
   uint64_t key = stream_key(seed, stream);
   uint8_t* o = (uint8_t*)out;
+  if (type == 21) {  /* IQ3_S: back to front, as chatnet_synth_quantize */
+    static const uint8_t zeros[28] = {0};
+    for (int64_t b = (int64_t)nb - 1; b >= 0; b--) {
+      float w[256];
+      uint64_t e0 = (uint64_t)b * blk;
+      for (int j = 0; j < blk; j += 2) {
+        double z0, z1;
+        normal_pair(key, (e0 + j) >> 1, &z0, &z1);
+        w[j] = (float)(z0 * sigma);
+        w[j + 1] = (float)(z1 * sigma);
+      }
+      quant_block_iq3_s(w, o + (uint64_t)b * bytes, b + 1 < (int64_t)nb ? o + (uint64_t)(b + 1) * bytes : zeros);
+    }
+    return nb * (uint64_t)bytes;
+  }
 #pragma omp parallel for schedule(static)
   for (int64_t b = 0; b < (int64_t)nb; b++) {
     float w[256];

@@ -55,6 +55,11 @@ MIXES = {
                "output": _native.GGML_Q6_K},
     "q2_k": {"attn": _native.GGML_Q2_K, "gate_up": _native.GGML_Q2_K, "down": _native.GGML_Q3_K,
              "output": _native.GGML_Q8_K},
+    # the IQ family as DequantIQ.cs decodes it, every type in one of two mixes
+    "iq_a": {"attn": _native.GGML_IQ4_XS, "gate": _native.GGML_IQ3_XXS, "up": _native.GGML_IQ2_XS,
+             "down": _native.GGML_IQ4_NL, "output": _native.GGML_IQ1_M},
+    "iq_b": {"attn": _native.GGML_IQ3_S, "gate_up": _native.GGML_IQ2_S, "down": _native.GGML_IQ2_XXS,
+             "output": _native.GGML_IQ1_S},
 }
 
 

@@ -63,7 +63,16 @@ enum {
   CHATNET_GGML_Q4_K = 12,
   CHATNET_GGML_Q5_K = 13,
   CHATNET_GGML_Q6_K = 14,
-  CHATNET_GGML_Q8_K = 15
+  CHATNET_GGML_Q8_K = 15,
+  CHATNET_GGML_IQ2_XXS = 16,
+  CHATNET_GGML_IQ2_XS = 17,
+  CHATNET_GGML_IQ3_XXS = 18,
+  CHATNET_GGML_IQ1_S = 19,
+  CHATNET_GGML_IQ4_NL = 20,
+  CHATNET_GGML_IQ3_S = 21,
+  CHATNET_GGML_IQ2_S = 22,
+  CHATNET_GGML_IQ4_XS = 23,
+  CHATNET_GGML_IQ1_M = 29
 };
 
 /* KV-cache element type. */
@@ -117,16 +126,22 @@ CHATNET_API int chatnet_create(const chatnet_config* cfg, int device, chatnet_mo
  * ffn_gate,ffn_up,ffn_down}.weight, plus for CHATNET_ARCH_QWEN2 the optional
  * F32 biases blk.{l}.{attn_q,attn_k,attn_v}.bias (QwenWeights.cs:158-170: a
  * layer that has the q bias must have all three).  Weight matrices may be
- * F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K or
- * Q8_K, each dispatched on its own type (LlamaModel.MatVecMulByType,
- * LlamaModel.cs:470-567); Q4_1, Q5_0, Q5_1, Q2_K, Q3_K and Q8_K are also
- * re-encoded on the device at upload (u8 codes with an fp32 scale and offset
- * per 16 weights, M*(K/64)*96 bytes beside the stored blocks), the form the
- * GEMV reads them in.  Without output.weight the LM head is
- * token_embd.weight, of whatever type (the tied fallback of
- * LlamaWeights.cs:89-98 and QwenWeights.cs:102-112).  Embeddings may be of any
- * of those types (LlamaModel.LoadEmbedding, LlamaModel.cs:365-394); a block
- * type other than Q4_0 and Q8_0 is re-encoded the same way at upload.
+ * of every type LlamaModel.MatVecMulByType dispatches (LlamaModel.cs:470-567):
+ * F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K
+ * and IQ2_XXS, IQ2_XS, IQ3_XXS, IQ1_S, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS, IQ1_M
+ * (as DequantIQ.cs decodes them), each dispatched on its own type.  Q4_1,
+ * Q5_0, Q5_1, Q2_K, Q3_K, Q8_K and the IQ types are also re-encoded on the
+ * device at upload (u8 codes with an fp32 scale and offset per 16 weights,
+ * M*(K/64)*96 bytes beside the stored blocks), the form the GEMV reads them
+ * in.  An IQ3_S row's last block reads 28 bytes past the row, as the
+ * reference does (DequantIQ.cs:255-283): the next row's first bytes, or for
+ * the last row zeros (the reference reads whatever follows the tensor in the
+ * file).  Without output.weight the LM head is token_embd.weight, of whatever
+ * type (the tied fallback of LlamaWeights.cs:89-98 and QwenWeights.cs:102-112).
+ * Embeddings may be of any of those types but IQ3_S (LlamaModel.LoadEmbedding,
+ * LlamaModel.cs:365-394; the reference's IQ3_S row dequantize throws,
+ * CHATNET_ERR_OUT_OF_RANGE); a block type other than Q4_0 and Q8_0 is
+ * re-encoded the same way at upload.
  * `dims` is GGUF order (ne0 = inner).
  * `nbytes` must equal GgufTensorInfo.ByteSize (GgufTensorInfo.cs:30-113).
  * Replaces MemoryMappedWeights.GetTensorPointer (MemoryMappedWeights.cs:76-84)
@@ -217,15 +232,17 @@ CHATNET_API int chatnet_get_logits(chatnet_model* m, float* logits_host);
  *   y[n][m] = sum_k W[m][k] * x[n][k],  0 <= n < N, 0 <= m < M
  * W is M rows of raw GGUF blocks (row stride K/block*bytes_per_block), x is
  * N x K fp32 row-major, y is N x M fp32 row-major; w_dev and x_dev 16-byte
- * aligned.  Types F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0 and K % 64 == 0, or
- * Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K and K % 256 == 0, with K <= 16384.
+ * aligned.  Types F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, IQ4_NL and
+ * K % 64 == 0, or Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K and the other IQ types
+ * and K % 256 == 0, with K <= 16384 (IQ3_S: bytes past W's last row read as
+ * zero).
  * N >= 8 with a block type runs the dequant-to-LDS bf16 MFMA GEMM (x rounded
  * to bf16; Q4_0 read as raw blocks, the other types first re-encoded into the
  * workspace as u8 codes with an fp32 scale and offset per 16 weights,
  * M*(K/64)*96 bytes, giving the same dequantized values); any other call
  * (N < 8, F32, F16) runs the fused GEMV once per column, which reads Q4_1,
- * Q5_0, Q5_1, Q2_K, Q3_K and Q8_K from that same re-encoded copy, made in the
- * workspace first.  The GEMM's workspace is allocated on first use
+ * Q5_0, Q5_1, Q2_K, Q3_K, Q8_K and the IQ types from that same re-encoded
+ * copy, made in the workspace first.  The GEMM's workspace is allocated on first use
  * per (device, stream) and kept until the process ends (a buffer it outgrows
  * is retired, not freed, since a captured graph may still read it).  A call
  * on a stream under HIP graph capture cannot allocate: it fails with
@@ -239,17 +256,18 @@ CHATNET_API int chatnet_matmul(uint32_t ggml_type, const void* w_dev, const floa
 /* chatnet_matmul without any allocation, for callers that cannot allocate
  * device memory: code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc.  No counterpart in the reference.  Same arguments,
- * kernels and results as chatnet_matmul for Q4_0 and for the six types read
- * only as packed units (Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q8_K, whose packed copy
- * of W, M*(K/64)*96 bytes, goes into the scratch); Q8_0, Q4_K, Q5_K and Q6_K
- * run the fused GEMV once per column on their stored blocks.  The scratch
- * (bf16 x, the K-split partials and the packed W) lives in a fixed 64 MiB
- * array per device, held by the library from load to process exit, instead of
- * a per-stream workspace.  Calls needing more scratch than that (N*K*2 bytes
- * of x for N >= 8, rounded up to 256, plus the partials, plus the packed W)
- * fail with CHATNET_ERR_INVALID_ARG before launching anything.  Every call on one device shares that device's array: calls that
- * may overlap on one device (different streams, threads) race and must be
- * serialized by the caller. */
+ * kernels and results as chatnet_matmul for Q4_0 and for the types read
+ * only as packed units (Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q8_K and the IQ types,
+ * whose packed copy of W, M*(K/64)*96 bytes, goes into the scratch); Q8_0,
+ * Q4_K, Q5_K and Q6_K run the fused GEMV once per column on their stored
+ * blocks.  The scratch (bf16 x, the K-split partials and the packed W) lives
+ * in a fixed 64 MiB array per device, held by the library from load to
+ * process exit, instead of a per-stream workspace.  Calls needing more
+ * scratch than that (N*K*2 bytes of x for N >= 8, rounded up to 256, plus the
+ * partials, plus the packed W) fail with CHATNET_ERR_INVALID_ARG before
+ * launching anything.  Every call on one device shares that device's array:
+ * calls that may overlap on one device (different streams, threads) race and
+ * must be serialized by the caller. */
 CHATNET_API int chatnet_matmul_noalloc(uint32_t ggml_type, const void* w_dev, const float* x_dev,
                                        float* y_dev, int M, int K, int N, void* stream);
 

@@ -637,6 +637,367 @@ float oracle_dot_q8_k(const uint8_t* row, const float* x, int n) {
   return vsum4(s);
 }
 
+/* ---------------------------------------------------------------------------
+ * IQ family (DequantIQ.cs).  The reference's own decoders: bit fields with
+ * small scales and no codebook grids (they do not decode llama.cpp's IQ
+ * files).  Restated as written, their quirks included:
+ *   IQ4_XS takes the low scale of sub-block s from byte 4+s (s < 8: bytes 8..11
+ *     are the first quants), masked to 6 bits, and 2 more bits from scales_h
+ *     placed at bits 6..7 (DequantIQ.cs:155-159);
+ *   IQ3_S reads its sign bytes at 98..129 and its scale bytes at 130..137 of a
+ *     110-byte block (DequantIQ.cs:255-283): a row's last block reads the first
+ *     28 bytes of the next row, and the tensor's last block 28 bytes past its
+ *     end (the wrapper in oracle.py appends zeros there, as the device copy's
+ *     tail padding holds); its Dequantize over one embedding row therefore
+ *     indexes past the row's span, which the reference reports as an
+ *     IndexOutOfRangeException (load_embedding returns -5);
+ *   IQ2_S negates only elements 0..3 of a 16-element sub-block (:677-678).
+ * ------------------------------------------------------------------------- */
+
+/* DequantIQ.IQ4NL_Table (DequantIQ.cs:29-33). */
+static const float kIQ4NL[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+/* IQ4NL.Dequantize (DequantIQ.cs:46-76), partial last block included. */
+void oracle_dequant_iq4_nl(const uint8_t* src, float* out, int n) {
+  int blocks = (n + 31) / 32;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = src + (size_t)b * 18;
+    float d = h2f(blk);
+    int rem = n - 32 * b;
+    for (int j = 0; j < 16 && j < rem; j++) out[32 * b + j] = d * kIQ4NL[blk[2 + j] & 0x0F];
+    for (int j = 0; j < 16 && 16 + j < rem; j++) out[32 * b + 16 + j] = d * kIQ4NL[(blk[2 + j] >> 4) & 0x0F];
+  }
+}
+
+/* IQ4NL.DotProductScalar (DequantIQ.cs:85-125): the low nibbles' terms, then
+ * the high nibbles', into one block sum; sum += blockSum * scale. */
+float oracle_dot_iq4_nl(const uint8_t* row, const float* x, int n) {
+  int blocks = n / 32;
+  float sum = 0.0f;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = row + (size_t)b * 18;
+    const float* in = x + (size_t)b * 32;
+    float d = h2f(blk), bs = 0.0f;
+    for (int j = 0; j < 16; j++) bs = bs + kIQ4NL[blk[2 + j] & 0x0F] * in[j];
+    for (int j = 0; j < 16; j++) bs = bs + kIQ4NL[(blk[2 + j] >> 4) & 0x0F] * in[16 + j];
+    sum = sum + bs * d;
+  }
+  return sum;
+}
+
+static inline int iq4xs_scale(const uint8_t* blk, int sub) {
+  int sh = blk[2] | (blk[3] << 8);
+  return ((blk[4 + sub] & 0x3F) | (((sh >> (2 * sub)) & 3) << 6)) - 32;
+}
+
+/* IQ4XS.Dequantize (DequantIQ.cs:139-176). */
+void oracle_dequant_iq4_xs(const uint8_t* src, float* out, int n) {
+  int blocks = n / 256;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = src + (size_t)b * 136;
+    float d = h2f(blk);
+    for (int sub = 0; sub < 8; sub++) {
+      float dsc = d * (float)iq4xs_scale(blk, sub);
+      for (int j = 0; j < 16; j++) {
+        uint8_t q = blk[8 + 16 * sub + j];
+        out[(size_t)b * 256 + 32 * sub + j] = dsc * kIQ4NL[q & 0x0F];
+        out[(size_t)b * 256 + 32 * sub + j + 16] = dsc * kIQ4NL[(q >> 4) & 0x0F];
+      }
+    }
+  }
+}
+
+/* IQ4XS.DotProductScalar (DequantIQ.cs:184-234): per sub-block the low and
+ * high nibble terms alternate; blockSum += dsc * subSum; sum += blockSum. */
+float oracle_dot_iq4_xs(const uint8_t* row, const float* x, int n) {
+  int blocks = n / 256;
+  float sum = 0.0f;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = row + (size_t)b * 136;
+    const float* in = x + (size_t)b * 256;
+    float d = h2f(blk), bs = 0.0f;
+    for (int sub = 0; sub < 8; sub++) {
+      float dsc = d * (float)iq4xs_scale(blk, sub), ss = 0.0f;
+      for (int j = 0; j < 16; j++) {
+        uint8_t q = blk[8 + 16 * sub + j];
+        ss = ss + kIQ4NL[q & 0x0F] * in[32 * sub + j];
+        ss = ss + kIQ4NL[(q >> 4) & 0x0F] * in[32 * sub + j + 16];
+      }
+      bs = bs + dsc * ss;
+    }
+    sum = sum + bs;
+  }
+  return sum;
+}
+
+/* IQ3_S element idx of the block at blk: the unsigned 3-bit magnitude and the
+ * sign bit (byte 98 + idx/8, bit idx%8), the scale (byte 130 + idx/32) . */
+static inline int iq3s_q(const uint8_t* blk, int idx) {
+  return ((blk[2 + idx / 4] >> (2 * (idx % 4))) & 3) | (((blk[66 + idx / 8] >> (idx % 8)) & 1) << 2);
+}
+static inline int iq3s_sc(const uint8_t* blk, int sub) { return ((blk[130 + sub / 4] >> (2 * (sub % 4))) & 3) + 1; }
+
+/* IQ3S.Dequantize (DequantIQ.cs:244-290). */
+void oracle_dequant_iq3_s(const uint8_t* src, float* out, int n) {
+  int blocks = n / 256;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = src + (size_t)b * 110;
+    float d = h2f(blk);
+    for (int sub = 0; sub < 32; sub++) {
+      float dsc = d * (float)iq3s_sc(blk, sub);
+      uint8_t sb = blk[98 + sub];
+      for (int j = 0; j < 8; j++) {
+        int idx = 8 * sub + j;
+        float val = dsc * (float)iq3s_q(blk, idx);
+        if ((sb >> j) & 1) val = -val;
+        out[(size_t)b * 256 + idx] = val;
+      }
+    }
+  }
+}
+
+/* IQ3S.DotProductScalar (DequantIQ.cs:299-349). */
+float oracle_dot_iq3_s(const uint8_t* row, const float* x, int n) {
+  int blocks = n / 256;
+  float sum = 0.0f;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = row + (size_t)b * 110;
+    const float* in = x + (size_t)b * 256;
+    float d = h2f(blk), bs = 0.0f;
+    for (int sub = 0; sub < 32; sub++) {
+      float dsc = d * (float)iq3s_sc(blk, sub), ss = 0.0f;
+      uint8_t sb = blk[98 + sub];
+      for (int j = 0; j < 8; j++) {
+        float val = (float)iq3s_q(blk, 8 * sub + j);
+        if ((sb >> j) & 1) val = -val;
+        ss = ss + val * in[8 * sub + j];
+      }
+      bs = bs + dsc * ss;
+    }
+    sum = sum + bs;
+  }
+  return sum;
+}
+
+static inline int iq3xxs_q(const uint8_t* blk, int idx) {
+  const uint8_t* p = blk + 2 + 3 * (idx / 8);
+  uint32_t packed = (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16);
+  return (int)((packed >> (3 * (idx % 8))) & 7);
+}
+
+/* IQ3XXS.Dequantize (DequantIQ.cs:364-399): d * (q3 - 4). */
+void oracle_dequant_iq3_xxs(const uint8_t* src, float* out, int n) {
+  int blocks = n / 256;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = src + (size_t)b * 98;
+    float d = h2f(blk);
+    for (int i = 0; i < 256; i++) out[(size_t)b * 256 + i] = d * (float)(iq3xxs_q(blk, i) - 4);
+  }
+}
+
+/* IQ3XXS.DotProductScalar (DequantIQ.cs:408-447). */
+float oracle_dot_iq3_xxs(const uint8_t* row, const float* x, int n) {
+  int blocks = n / 256;
+  float sum = 0.0f;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = row + (size_t)b * 98;
+    const float* in = x + (size_t)b * 256;
+    float d = h2f(blk), bs = 0.0f;
+    for (int i = 0; i < 256; i++) bs = bs + (float)(iq3xxs_q(blk, i) - 4) * in[i];
+    sum = sum + d * bs;
+  }
+  return sum;
+}
+
+/* IQ2 element e of a 16-element sub-block sub: bits 2(e%4) of qs[4 sub + e/4]. */
+static inline int iq2_q(const uint8_t* blk, int sub, int e) { return (blk[2 + 4 * sub + e / 4] >> (2 * (e % 4))) & 3; }
+static inline int iq2xs_sc(const uint8_t* blk, int sub) {
+  int raw = (int8_t)blk[66 + sub / 2];
+  return (sub & 1) == 0 ? (raw & 0x0F) - 8 : ((raw >> 4) & 0x0F) - 8;
+}
+
+/* IQ2XS.Dequantize (DequantIQ.cs:456-496): dsc * (q - 1). */
+void oracle_dequant_iq2_xs(const uint8_t* src, float* out, int n) {
+  int blocks = n / 256;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = src + (size_t)b * 74;
+    float d = h2f(blk);
+    for (int sub = 0; sub < 16; sub++) {
+      float dsc = d * (float)iq2xs_sc(blk, sub);
+      for (int e = 0; e < 16; e++) out[(size_t)b * 256 + 16 * sub + e] = dsc * (float)(iq2_q(blk, sub, e) - 1);
+    }
+  }
+}
+
+/* IQ2XS.DotProductScalar (DequantIQ.cs:505-559). */
+float oracle_dot_iq2_xs(const uint8_t* row, const float* x, int n) {
+  int blocks = n / 256;
+  float sum = 0.0f;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = row + (size_t)b * 74;
+    const float* in = x + (size_t)b * 256;
+    float d = h2f(blk), bs = 0.0f;
+    for (int sub = 0; sub < 16; sub++) {
+      float dsc = d * (float)iq2xs_sc(blk, sub), ss = 0.0f;
+      for (int e = 0; e < 16; e++) ss = ss + (float)(iq2_q(blk, sub, e) - 1) * in[16 * sub + e];
+      bs = bs + dsc * ss;
+    }
+    sum = sum + bs;
+  }
+  return sum;
+}
+
+/* IQ2XXS.Dequantize (DequantIQ.cs:568-598): d * (q - 1). */
+void oracle_dequant_iq2_xxs(const uint8_t* src, float* out, int n) {
+  int blocks = n / 256;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = src + (size_t)b * 66;
+    float d = h2f(blk);
+    for (int sub = 0; sub < 16; sub++)
+      for (int e = 0; e < 16; e++) out[(size_t)b * 256 + 16 * sub + e] = d * (float)(iq2_q(blk, sub, e) - 1);
+  }
+}
+
+/* IQ2XXS.DotProductScalar (DequantIQ.cs:607-647). */
+float oracle_dot_iq2_xxs(const uint8_t* row, const float* x, int n) {
+  int blocks = n / 256;
+  float sum = 0.0f;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = row + (size_t)b * 66;
+    const float* in = x + (size_t)b * 256;
+    float d = h2f(blk), bs = 0.0f;
+    for (int sub = 0; sub < 16; sub++)
+      for (int e = 0; e < 16; e++) bs = bs + (float)(iq2_q(blk, sub, e) - 1) * in[16 * sub + e];
+    sum = sum + d * bs;
+  }
+  return sum;
+}
+
+/* IQ2S.Dequantize (DequantIQ.cs:656-696): dsc * q, elements 0..3 of a
+ * sub-block negated by the sign nibble of qh[sub]. */
+void oracle_dequant_iq2_s(const uint8_t* src, float* out, int n) {
+  int blocks = n / 256;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = src + (size_t)b * 82;
+    float d = h2f(blk);
+    for (int sub = 0; sub < 16; sub++) {
+      uint8_t qh = blk[66 + sub];
+      float dsc = d * (float)((qh & 0x0F) + 1);
+      int sign = (qh >> 4) & 0x0F;
+      for (int e = 0; e < 16; e++) {
+        float val = dsc * (float)iq2_q(blk, sub, e);
+        if (e < 4 && ((sign >> e) & 1)) val = -val;
+        out[(size_t)b * 256 + 16 * sub + e] = val;
+      }
+    }
+  }
+}
+
+/* IQ2S.DotProductScalar (DequantIQ.cs:705-758). */
+float oracle_dot_iq2_s(const uint8_t* row, const float* x, int n) {
+  int blocks = n / 256;
+  float sum = 0.0f;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = row + (size_t)b * 82;
+    const float* in = x + (size_t)b * 256;
+    float d = h2f(blk), bs = 0.0f;
+    for (int sub = 0; sub < 16; sub++) {
+      uint8_t qh = blk[66 + sub];
+      float dsc = d * (float)((qh & 0x0F) + 1), ss = 0.0f;
+      int sign = (qh >> 4) & 0x0F;
+      for (int e = 0; e < 16; e++) {
+        float val = (float)iq2_q(blk, sub, e);
+        if (e < 4 && ((sign >> e) & 1)) val = -val;
+        ss = ss + val * in[16 * sub + e];
+      }
+      bs = bs + dsc * ss;
+    }
+    sum = sum + bs;
+  }
+  return sum;
+}
+
+/* IQ1 ternary element j of 8-element sub-block sub: +1 if bit j of qs[sub],
+ * else -1 if bit (sub%2)*4 + j/2 of qh[sub/2], else 0. */
+static inline int iq1_t(const uint8_t* blk, int sub, int j) {
+  if ((blk[2 + sub] >> j) & 1) return 1;
+  return ((blk[34 + sub / 2] >> ((sub % 2) * 4 + j / 2)) & 1) ? -1 : 0;
+}
+
+/* IQ1S.Dequantize (DequantIQ.cs:767-805): d, -d or 0. */
+void oracle_dequant_iq1_s(const uint8_t* src, float* out, int n) {
+  int blocks = n / 256;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = src + (size_t)b * 50;
+    float d = h2f(blk);
+    for (int sub = 0; sub < 32; sub++)
+      for (int j = 0; j < 8; j++) {
+        int t = iq1_t(blk, sub, j);
+        out[(size_t)b * 256 + 8 * sub + j] = t == 1 ? d : (t == -1 ? -d : 0.0f);
+      }
+  }
+}
+
+/* IQ1S.DotProductScalar (DequantIQ.cs:814-860). */
+float oracle_dot_iq1_s(const uint8_t* row, const float* x, int n) {
+  int blocks = n / 256;
+  float sum = 0.0f;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = row + (size_t)b * 50;
+    const float* in = x + (size_t)b * 256;
+    float d = h2f(blk), bs = 0.0f;
+    for (int sub = 0; sub < 32; sub++)
+      for (int j = 0; j < 8; j++) bs = bs + (float)iq1_t(blk, sub, j) * in[8 * sub + j];
+    sum = sum + d * bs;
+  }
+  return sum;
+}
+
+/* IQ1_M sub-block scale: bit sub%8 of scales[sub/8] selects 1 or 0.5
+ * (DequantIQ.cs:884-890; sub/8 < 4 < 6 always). */
+static inline float iq1m_sc(const uint8_t* blk, int sub) {
+  int idx = sub / 8;
+  if (idx >= 6) return 1.0f;
+  return ((blk[50 + idx] >> (sub % 8)) & 1) ? 1.0f : 0.5f;
+}
+
+/* IQ1M.Dequantize (DequantIQ.cs:869-914): d*sc, -d*sc or 0. */
+void oracle_dequant_iq1_m(const uint8_t* src, float* out, int n) {
+  int blocks = n / 256;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = src + (size_t)b * 56;
+    float d = h2f(blk);
+    for (int sub = 0; sub < 32; sub++) {
+      float sc = iq1m_sc(blk, sub);
+      for (int j = 0; j < 8; j++) {
+        int t = iq1_t(blk, sub, j);
+        out[(size_t)b * 256 + 8 * sub + j] = t == 1 ? d * sc : (t == -1 ? -d * sc : 0.0f);
+      }
+    }
+  }
+}
+
+/* IQ1M.DotProductScalar (DequantIQ.cs:923-975). */
+float oracle_dot_iq1_m(const uint8_t* row, const float* x, int n) {
+  int blocks = n / 256;
+  float sum = 0.0f;
+  for (int b = 0; b < blocks; b++) {
+    const uint8_t* blk = row + (size_t)b * 56;
+    const float* in = x + (size_t)b * 256;
+    float d = h2f(blk), bs = 0.0f;
+    for (int sub = 0; sub < 32; sub++) {
+      float sc = iq1m_sc(blk, sub);
+      for (int j = 0; j < 8; j++) {
+        int t = iq1_t(blk, sub, j);
+        float w = t == 1 ? sc : (t == -1 ? -sc : 0.0f);
+        bs = bs + w * in[8 * sub + j];
+      }
+    }
+    sum = sum + d * bs;
+  }
+  return sum;
+}
+
 /* TensorMath.MatVecMulQ4_0 / MatVecMulQ6K / MatVecMulGeneric / MatVecMul
  * (TensorMath.cs:527-656) dispatched as LlamaModel.MatVecMulByType
  * (LlamaModel.cs:470-567).  Rows are independent (TensorMath.cs:47-51), so the
@@ -657,6 +1018,15 @@ int oracle_matvec(uint32_t type, const void* W, const float* x, float* y, int M,
     case ORACLE_Q2_K: bpr = (size_t)(K / 256) * 84; dot = oracle_dot_q2_k; break;
     case ORACLE_Q3_K: bpr = (size_t)(K / 256) * 110; dot = oracle_dot_q3_k; break;
     case ORACLE_Q8_K: bpr = (size_t)(K / 256) * 292; dot = oracle_dot_q8_k; break;
+    case ORACLE_IQ2_XXS: bpr = (size_t)(K / 256) * 66; dot = oracle_dot_iq2_xxs; break;
+    case ORACLE_IQ2_XS: bpr = (size_t)(K / 256) * 74; dot = oracle_dot_iq2_xs; break;
+    case ORACLE_IQ3_XXS: bpr = (size_t)(K / 256) * 98; dot = oracle_dot_iq3_xxs; break;
+    case ORACLE_IQ1_S: bpr = (size_t)(K / 256) * 50; dot = oracle_dot_iq1_s; break;
+    case ORACLE_IQ4_NL: bpr = (size_t)(K / 32) * 18; dot = oracle_dot_iq4_nl; break;
+    case ORACLE_IQ3_S: bpr = (size_t)(K / 256) * 110; dot = oracle_dot_iq3_s; break;
+    case ORACLE_IQ2_S: bpr = (size_t)(K / 256) * 82; dot = oracle_dot_iq2_s; break;
+    case ORACLE_IQ4_XS: bpr = (size_t)(K / 256) * 136; dot = oracle_dot_iq4_xs; break;
+    case ORACLE_IQ1_M: bpr = (size_t)(K / 256) * 56; dot = oracle_dot_iq1_m; break;
     case ORACLE_F32: {
       const float* wf = (const float*)W;
       for (int r = 0; r < M; r++) y[r] = oracle_dot_f32(wf + (size_t)r * K, x, K);
@@ -1067,6 +1437,15 @@ static int load_embedding(oracle_llama* m, int token, float* out) {
     case ORACLE_Q5_K: oracle_dequant_q5_k(e + (size_t)token * (dim / 256) * 176, out, dim); return 0;
     case ORACLE_Q6_K: oracle_dequant_q6_k(e + (size_t)token * (dim / 256) * 210, out, dim); return 0;
     case ORACLE_Q8_K: oracle_dequant_q8_k(e + (size_t)token * (dim / 256) * 292, out, dim); return 0;
+    case ORACLE_IQ2_XXS: oracle_dequant_iq2_xxs(e + (size_t)token * (dim / 256) * 66, out, dim); return 0;
+    case ORACLE_IQ2_XS: oracle_dequant_iq2_xs(e + (size_t)token * (dim / 256) * 74, out, dim); return 0;
+    case ORACLE_IQ3_XXS: oracle_dequant_iq3_xxs(e + (size_t)token * (dim / 256) * 98, out, dim); return 0;
+    case ORACLE_IQ1_S: oracle_dequant_iq1_s(e + (size_t)token * (dim / 256) * 50, out, dim); return 0;
+    case ORACLE_IQ4_NL: oracle_dequant_iq4_nl(e + (size_t)token * (dim / 32) * 18, out, dim); return 0;
+    case ORACLE_IQ2_S: oracle_dequant_iq2_s(e + (size_t)token * (dim / 256) * 82, out, dim); return 0;
+    case ORACLE_IQ4_XS: oracle_dequant_iq4_xs(e + (size_t)token * (dim / 256) * 136, out, dim); return 0;
+    case ORACLE_IQ1_M: oracle_dequant_iq1_m(e + (size_t)token * (dim / 256) * 56, out, dim); return 0;
+    case ORACLE_IQ3_S: return -5; /* IQ3S.Dequantize indexes past the row's span (DequantIQ.cs:266, :280) */
     default: return -3;
   }
 }

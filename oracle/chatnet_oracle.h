@@ -26,6 +26,21 @@
  *                     brute force.
  *   q5_k dequant/dot  reference KAT QuantizationTests.cs:513-537 (dot 5184),
  *                     a hand-derived high-bit position KAT, float64 brute force.
+ *   q4_1 q5_0 q5_1 q8_k  reference exact-value KATs QuantizationTests.cs:
+ *                     93-110, 141-157, 189-205, 544-562, hand-derived position
+ *                     KATs (high-bit words, nibble halves), float64 brute force.
+ *   q2_k q3_k         hand-derived element/scale position KATs (each element's
+ *                     bit field and scale byte set alone), closed forms
+ *                     (uniform fields), float64 brute force.
+ *   iq4_nl            reference KATs QuantizationTests.cs:594-635 (table
+ *                     lookups, dot = dequantize-then-dot), float64 brute force.
+ *   iq4_xs iq3_s iq3_xxs iq2_xs iq2_xxs iq2_s iq1_s iq1_m  hand-derived
+ *                     position KATs for every bit field (one field set at a
+ *                     time; the quirks above: IQ4_XS scale bytes 4..11, IQ3_S
+ *                     signs/scales read from the next block, IQ2_S signs on
+ *                     elements 0..3 only), closed forms, float64 brute force.
+ *                     Sign of a zero weight (the reference's -0.0 for a negated
+ *                     zero magnitude): parity unpinned (no test distinguishes).
  *   rope_neox         closed form at hd 4, identity at pos 0, pair norms, and
  *                     the exact identity neox = P^-1 . rope . P with P the
  *                     split-half -> interleaved permutation of each head.
@@ -55,7 +70,8 @@ extern "C" {
 
 enum { ORACLE_F32 = 0, ORACLE_F16 = 1, ORACLE_Q4_0 = 2, ORACLE_Q4_1 = 3, ORACLE_Q5_0 = 6, ORACLE_Q5_1 = 7,
        ORACLE_Q8_0 = 8, ORACLE_Q2_K = 10, ORACLE_Q3_K = 11, ORACLE_Q4_K = 12, ORACLE_Q5_K = 13, ORACLE_Q6_K = 14,
-       ORACLE_Q8_K = 15 };
+       ORACLE_Q8_K = 15, ORACLE_IQ2_XXS = 16, ORACLE_IQ2_XS = 17, ORACLE_IQ3_XXS = 18, ORACLE_IQ1_S = 19,
+       ORACLE_IQ4_NL = 20, ORACLE_IQ3_S = 21, ORACLE_IQ2_S = 22, ORACLE_IQ4_XS = 23, ORACLE_IQ1_M = 29 };
 
 void oracle_set_threads(int n);
 int oracle_get_threads(void);
@@ -84,6 +100,24 @@ void oracle_dequant_q3_k(const uint8_t* src, float* out, int n);
 float oracle_dot_q3_k(const uint8_t* row, const float* x, int n);
 void oracle_dequant_q8_k(const uint8_t* src, float* out, int n);
 float oracle_dot_q8_k(const uint8_t* row, const float* x, int n);
+void oracle_dequant_iq4_nl(const uint8_t* src, float* out, int n);
+float oracle_dot_iq4_nl(const uint8_t* row, const float* x, int n);
+void oracle_dequant_iq4_xs(const uint8_t* src, float* out, int n);
+float oracle_dot_iq4_xs(const uint8_t* row, const float* x, int n);
+void oracle_dequant_iq3_s(const uint8_t* src, float* out, int n);
+float oracle_dot_iq3_s(const uint8_t* row, const float* x, int n);
+void oracle_dequant_iq3_xxs(const uint8_t* src, float* out, int n);
+float oracle_dot_iq3_xxs(const uint8_t* row, const float* x, int n);
+void oracle_dequant_iq2_xs(const uint8_t* src, float* out, int n);
+float oracle_dot_iq2_xs(const uint8_t* row, const float* x, int n);
+void oracle_dequant_iq2_xxs(const uint8_t* src, float* out, int n);
+float oracle_dot_iq2_xxs(const uint8_t* row, const float* x, int n);
+void oracle_dequant_iq2_s(const uint8_t* src, float* out, int n);
+float oracle_dot_iq2_s(const uint8_t* row, const float* x, int n);
+void oracle_dequant_iq1_s(const uint8_t* src, float* out, int n);
+float oracle_dot_iq1_s(const uint8_t* row, const float* x, int n);
+void oracle_dequant_iq1_m(const uint8_t* src, float* out, int n);
+float oracle_dot_iq1_m(const uint8_t* row, const float* x, int n);
 float oracle_dot_f32(const float* a, const float* b, int n);
 
 /* y[m] = dot(W row m, x) for m < M (MatVecMulByType semantics). Returns 0 or -3

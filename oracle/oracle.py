@@ -17,8 +17,21 @@ LIB = os.path.join(HERE, "liboracle.so")
 
 F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 2, 8, 12, 13, 14
 Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q8_K = 3, 6, 7, 10, 11, 15
+IQ2_XXS, IQ2_XS, IQ3_XXS, IQ1_S, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS, IQ1_M = 16, 17, 18, 19, 20, 21, 22, 23, 29
 _NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q5_K: "q5_k", Q6_K: "q6_k", Q4_1: "q4_1", Q5_0: "q5_0",
-          Q5_1: "q5_1", Q2_K: "q2_k", Q3_K: "q3_k", Q8_K: "q8_k"}
+          Q5_1: "q5_1", Q2_K: "q2_k", Q3_K: "q3_k", Q8_K: "q8_k", IQ2_XXS: "iq2_xxs", IQ2_XS: "iq2_xs",
+          IQ3_XXS: "iq3_xxs", IQ1_S: "iq1_s", IQ4_NL: "iq4_nl", IQ3_S: "iq3_s", IQ2_S: "iq2_s", IQ4_XS: "iq4_xs",
+          IQ1_M: "iq1_m"}
+# IQ3_S reads 28 bytes past a tensor's last block (DequantIQ.cs:255-283): its
+# buffers get this many zero bytes appended, as the device copy's tail holds.
+IQ3_S_TAIL = 32
+
+
+def _padded(qtype: int, data: np.ndarray) -> np.ndarray:
+    d = np.ascontiguousarray(data).view(np.uint8).ravel()
+    if qtype == IQ3_S:
+        d = np.concatenate([d, np.zeros(IQ3_S_TAIL, np.uint8)])
+    return d
 _P = ctypes.c_void_p
 _lib = None
 
@@ -94,21 +107,21 @@ def half_to_float(h: int) -> float:
 def dequant(qtype: int, data: np.ndarray, n: int) -> np.ndarray:
     out = np.empty(n, dtype=np.float32)
     name = _NAMES[qtype]
-    d = np.ascontiguousarray(data, dtype=np.uint8)
+    d = _padded(qtype, np.ascontiguousarray(data, dtype=np.uint8))
     getattr(lib(), f"oracle_dequant_{name}")(d.ctypes.data, out.ctypes.data, n)
     return out
 
 
 def dot(qtype: int, row: np.ndarray, x: np.ndarray) -> float:
     name = _NAMES[qtype]
-    r = np.ascontiguousarray(row, dtype=np.uint8)
+    r = _padded(qtype, np.ascontiguousarray(row, dtype=np.uint8))
     xx = _f32(x)
     return float(getattr(lib(), f"oracle_dot_{name}")(r.ctypes.data, xx.ctypes.data, xx.size))
 
 
 def matvec(qtype: int, w: np.ndarray, x: np.ndarray, M: int, K: int) -> np.ndarray:
     y = np.empty(M, dtype=np.float32)
-    ww = np.ascontiguousarray(w)
+    ww = _padded(qtype, w) if qtype == IQ3_S else np.ascontiguousarray(w)
     xx = _f32(x)
     rc = lib().oracle_matvec(qtype, ww.ctypes.data, xx.ctypes.data, y.ctypes.data, M, K)
     if rc:
@@ -191,7 +204,7 @@ class OracleLlama:
             raise MemoryError("oracle_llama_create failed")
         self._keep = []
         for name, t in checkpoint.items():
-            arr = np.ascontiguousarray(t.data)
+            arr = _padded(t.type, t.data) if t.type == IQ3_S else np.ascontiguousarray(t.data)
             self._keep.append(arr)
             rc = lib().oracle_llama_set_tensor(self._h, name.encode(), t.type, arr.ctypes.data)
             if rc:

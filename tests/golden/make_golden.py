@@ -1,7 +1,8 @@
 """Writes the golden fixtures of tests/golden/ (run from the repository root).
 
 Fixtures are data only: seeded inputs and the CPU oracle's outputs for them.
-  blocks_{q4_0,q4_1,q5_0,q5_1,q8_0,q2_k,q3_k,q4_k,q5_k,q6_k,q8_k}.npz
+  blocks_{q4_0,q4_1,q5_0,q5_1,q8_0,q2_k,q3_k,q4_k,q5_k,q6_k,q8_k}.npz and
+  blocks_{iq2_xxs,iq2_xs,iq3_xxs,iq1_s,iq4_nl,iq3_s,iq2_s,iq4_xs,iq1_m}.npz
       raw blocks of 16 rows x 512 weights, an x vector, and the oracle's
       dequantized rows and row dots (DequantQ*.Dequantize / DotProduct).
   tiny_llama_q4_0.npz
@@ -39,7 +40,10 @@ def main():
     force = "--force" in sys.argv[1:]
     for qtype, tag in ((oracle.Q4_0, "q4_0"), (oracle.Q4_K, "q4_k"), (oracle.Q6_K, "q6_k"), (oracle.Q8_0, "q8_0"),
                        (oracle.Q5_K, "q5_k"), (oracle.Q4_1, "q4_1"), (oracle.Q5_0, "q5_0"), (oracle.Q5_1, "q5_1"),
-                       (oracle.Q2_K, "q2_k"), (oracle.Q3_K, "q3_k"), (oracle.Q8_K, "q8_k")):
+                       (oracle.Q2_K, "q2_k"), (oracle.Q3_K, "q3_k"), (oracle.Q8_K, "q8_k"),
+                       (oracle.IQ2_XXS, "iq2_xxs"), (oracle.IQ2_XS, "iq2_xs"), (oracle.IQ3_XXS, "iq3_xxs"),
+                       (oracle.IQ1_S, "iq1_s"), (oracle.IQ4_NL, "iq4_nl"), (oracle.IQ3_S, "iq3_s"),
+                       (oracle.IQ2_S, "iq2_s"), (oracle.IQ4_XS, "iq4_xs"), (oracle.IQ1_M, "iq1_m")):
         if os.path.exists(os.path.join(OUT, f"blocks_{tag}.npz")) and not force:
             continue
         rows, K = 16, 512

@@ -151,8 +151,93 @@ def dequant_q8_k(raw: np.ndarray, n: int) -> np.ndarray:  # DequantQ8K.cs:26-51
     return (b[:, 4:260].view(np.int8).astype(np.float64) * d[:, None]).ravel()[:n]
 
 
+# The IQ family as DequantIQ.cs decodes it (bit fields, no codebooks).
+IQ4NL = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.float64)
+
+
+def _bits(b, lo, hi, width):
+    """Fields of `width` bits, least significant first, of bytes lo..hi-1 of each block."""
+    bits = np.unpackbits(np.ascontiguousarray(b[:, lo:hi]), axis=1, bitorder="little")
+    w = bits.reshape(b.shape[0], -1, width)
+    return (w * (1 << np.arange(width))).sum(axis=2)
+
+
+def dequant_iq4_nl(raw: np.ndarray, n: int) -> np.ndarray:  # DequantIQ.cs:46-76
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, 18)
+    q = _nibbles32(b[:, 2:]).astype(np.int64)
+    return (_h(b, 0)[:, None] * IQ4NL[q]).ravel()[:n]
+
+
+def dequant_iq4_xs(raw: np.ndarray, n: int) -> np.ndarray:  # DequantIQ.cs:139-176
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, 136)
+    sh = b[:, 2].astype(np.int64) | (b[:, 3].astype(np.int64) << 8)
+    sub = np.arange(8)
+    sc = ((b[:, 4:12] & 0x3F).astype(np.int64) | (((sh[:, None] >> (2 * sub)) & 3) << 6)) - 32  # bytes 4..11
+    qs = b[:, 8:136].reshape(-1, 8, 16)
+    q = np.concatenate([qs & 0x0F, qs >> 4], axis=2).astype(np.int64)  # [blk, sub, 32]
+    return (_h(b, 0)[:, None, None] * sc[:, :, None] * IQ4NL[q]).ravel()[:n]
+
+
+def dequant_iq3_s(raw: np.ndarray, n: int) -> np.ndarray:  # DequantIQ.cs:244-290
+    flat = np.concatenate([np.asarray(raw, dtype=np.uint8).ravel(), np.zeros(32, np.uint8)])
+    nb = (flat.size - 32) // 110
+    # each block's window reaches 28 bytes into the next (signs at 98..129, scales at 130..137)
+    win = np.stack([flat[110 * k: 110 * k + 138] for k in range(nb)])
+    q3 = _bits(win, 2, 66, 2) | (_bits(win, 66, 98, 1) << 2)   # [blk, 256]
+    neg = _bits(win, 98, 130, 1)                                # bit j of byte 98+sub: element 8 sub + j
+    sc = _bits(win, 130, 138, 2) + 1                            # [blk, 32]: sub-block 4i+k at bits 2k of byte 130+i
+    v = _h(win, 0)[:, None] * np.repeat(sc, 8, axis=1) * q3
+    return np.where(neg == 1, -v, v).ravel()[:n]
+
+
+def dequant_iq3_xxs(raw: np.ndarray, n: int) -> np.ndarray:  # DequantIQ.cs:364-399
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, 98)
+    return (_h(b, 0)[:, None] * (_bits(b, 2, 98, 3) - 4)).ravel()[:n]
+
+
+def dequant_iq2_xs(raw: np.ndarray, n: int) -> np.ndarray:  # DequantIQ.cs:456-496
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, 74)
+    sc = _bits(b, 66, 74, 4) - 8            # sub-block 2i low nibble, 2i+1 high nibble of byte 66+i
+    return (_h(b, 0)[:, None] * np.repeat(sc, 16, axis=1) * (_bits(b, 2, 66, 2) - 1)).ravel()[:n]
+
+
+def dequant_iq2_xxs(raw: np.ndarray, n: int) -> np.ndarray:  # DequantIQ.cs:568-598
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, 66)
+    return (_h(b, 0)[:, None] * (_bits(b, 2, 66, 2) - 1)).ravel()[:n]
+
+
+def dequant_iq2_s(raw: np.ndarray, n: int) -> np.ndarray:  # DequantIQ.cs:656-696
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, 82)
+    qh = b[:, 66:82].astype(np.int64)
+    v = _h(b, 0)[:, None] * np.repeat((qh & 0x0F) + 1, 16, axis=1) * _bits(b, 2, 66, 2)
+    sign = np.zeros((b.shape[0], 16, 16), np.int64)
+    sign[:, :, :4] = (qh[:, :, None] >> (4 + np.arange(4))) & 1   # elements 0..3 of each sub-block only
+    return np.where(sign.reshape(-1, 256) == 1, -v, v).ravel()[:n]
+
+
+def _iq1_ternary(b):
+    bit = _bits(b, 2, 34, 1)                                    # [blk, 256]: element 8 sub + j
+    e = np.arange(256)
+    sub, j = e // 8, e % 8
+    hbit = (b[:, 34 + sub // 2] >> ((sub % 2) * 4 + j // 2)) & 1
+    return np.where(bit == 1, 1, np.where(hbit == 1, -1, 0))
+
+
+def dequant_iq1_s(raw: np.ndarray, n: int) -> np.ndarray:  # DequantIQ.cs:767-805
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, 50)
+    return (_h(b, 0)[:, None] * _iq1_ternary(b)).ravel()[:n]
+
+
+def dequant_iq1_m(raw: np.ndarray, n: int) -> np.ndarray:  # DequantIQ.cs:869-914
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, 56)
+    sc = np.where(_bits(b, 50, 54, 1) == 1, 1.0, 0.5)          # sub-block s: bit s%8 of byte 50 + s/8
+    return (_h(b, 0)[:, None] * np.repeat(sc, 8, axis=1) * _iq1_ternary(b)).ravel()[:n]
+
+
 DEQUANT = {2: dequant_q4_0, 8: dequant_q8_0, 12: dequant_q4_k, 13: dequant_q5_k, 14: dequant_q6_k,
-           3: dequant_q4_1, 6: dequant_q5_0, 7: dequant_q5_1, 10: dequant_q2_k, 11: dequant_q3_k, 15: dequant_q8_k}
+           3: dequant_q4_1, 6: dequant_q5_0, 7: dequant_q5_1, 10: dequant_q2_k, 11: dequant_q3_k, 15: dequant_q8_k,
+           16: dequant_iq2_xxs, 17: dequant_iq2_xs, 18: dequant_iq3_xxs, 19: dequant_iq1_s, 20: dequant_iq4_nl,
+           21: dequant_iq3_s, 22: dequant_iq2_s, 23: dequant_iq4_xs, 29: dequant_iq1_m}
 
 
 def matrix(t) -> np.ndarray:

@@ -11,7 +11,8 @@ import oracle
 from chatnet_amd import TINY_TEST, synth
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
-TAGS = ["q4_0", "q4_k", "q6_k", "q8_0", "q5_k", "q4_1", "q5_0", "q5_1", "q2_k", "q3_k", "q8_k"]
+TAGS = ["q4_0", "q4_k", "q6_k", "q8_0", "q5_k", "q4_1", "q5_0", "q5_1", "q2_k", "q3_k", "q8_k", "iq2_xxs", "iq2_xs",
+        "iq3_xxs", "iq1_s", "iq4_nl", "iq3_s", "iq2_s", "iq4_xs", "iq1_m"]
 
 
 def load(name):

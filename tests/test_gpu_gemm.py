@@ -86,3 +86,23 @@ def test_packed_block_types_gemm(qtype, M, K, N):
     errs = [normwise(y[n], r[n]) for n in range(N)]
     worst = int(np.argmax(errs))
     assert errs[worst] <= TOL, (qtype, M, K, N, worst, errs[worst])
+
+
+# The IQ family (DequantIQ.cs decoders) through the same packed GEMM.
+IQ = {16: "iq2_xxs", 17: "iq2_xs", 18: "iq3_xxs", 19: "iq1_s", 20: "iq4_nl", 21: "iq3_s", 22: "iq2_s",
+      23: "iq4_xs", 29: "iq1_m"}
+
+
+@pytest.mark.parametrize("M,K,N", [(4096, 4096, 64), (2048, 2048, 512), (130, 512, 9)])
+@pytest.mark.parametrize("qtype", sorted(IQ))
+def test_iq_types_gemm(qtype, M, K, N):
+    announce(f"gemm {IQ[qtype]} M={M} K={K} N={N}")
+    t = synth.tensor(qtype, 21, f"iqg{qtype}-{M}x{K}", M, K)
+    x = synth.normal(21, f"iqg-x{qtype}-{N}x{K}", N * K, 1.0).reshape(N, K)
+    y = gpu_matmul(qtype, t.data, x, M, K)
+    assert np.all(np.isfinite(y))
+    w = oracle.dequant(qtype, t.data, M * K).reshape(M, K).astype(np.float64)
+    r = x.astype(np.float64) @ w.T
+    errs = [normwise(y[n], r[n]) for n in range(N)]
+    worst = int(np.argmax(errs))
+    assert errs[worst] <= TOL, (qtype, M, K, N, worst, errs[worst])

@@ -139,6 +139,9 @@ def test_float_weight_gemv_shapes(qtype, M, K):
 # the type's dequantized value): Q4_1, Q5_0, Q5_1 and Q2_K, Q3_K, Q8_K, the
 # MatVecMulGeneric branches of LlamaModel.MatVecMulByType (LlamaModel.cs:488-528).
 PACKED_ONLY = {3: "q4_1", 6: "q5_0", 7: "q5_1", 10: "q2_k", 11: "q3_k", 15: "q8_k"}
+# The IQ family (DequantIQ.cs), read the same way.
+IQ = {16: "iq2_xxs", 17: "iq2_xs", 18: "iq3_xxs", 19: "iq1_s", 20: "iq4_nl", 21: "iq3_s", 22: "iq2_s",
+      23: "iq4_xs", 29: "iq1_m"}
 
 
 @pytest.mark.parametrize("M,K", [(4096, 4096), (11008, 4096), (4096, 11008), (32000, 2048)])
@@ -153,3 +156,17 @@ def test_packed_unit_types_gemv_shapes(qtype, M, K):
 ])
 def test_packed_unit_types_ragged_shapes(qtype, M, K):
     run_case(qtype, M, K, seed=13)
+
+
+@pytest.mark.parametrize("M,K", [(4096, 4096), (4096, 11008)])
+@pytest.mark.parametrize("qtype", sorted(IQ))
+def test_iq_types_gemv_shapes(qtype, M, K):
+    run_case(qtype, M, K, seed=17)
+
+
+@pytest.mark.parametrize("qtype,M,K", [
+    (20, 1, 64), (20, 17, 192), (20, 5, 16384), (21, 1, 256), (21, 9, 768), (21, 3, 16384),
+    (16, 7, 5632), (17, 40, 2816), (18, 1, 256), (19, 5, 768), (22, 33, 2048), (23, 9, 16384), (29, 130, 1280),
+])
+def test_iq_types_ragged_shapes(qtype, M, K):
+    run_case(qtype, M, K, seed=19)

@@ -101,6 +101,25 @@ def test_qwen2_span_and_greedy_match_oracle():
     compare_greedy(gt, o, margins, "qwen2 span 40+8, greedy 32")
 
 
+def test_qwen2_iq3_s_rows_keep_the_file_order():
+    """IQ3_S q/k matrices of a Qwen2 model: each row's last block reads the
+    next row of the file (DequantIQ.cs:255-283), while the device keeps q/k in
+    its per-head pair order; decode and a span against the oracle."""
+    cfg = SPAN_SMALL.replace(arch=_native.ARCH_QWEN2, rope_freq_base=1e6, context_length=64)
+    ck = synth.llama_checkpoint(cfg, seed=45, mix="iq_b")
+    toks = synth.tokens(45, "prompt", 20, cfg.vocab_size)
+    announce("qwen2 iq_b: 12-token span + 8 decode steps")
+    ora = oracle.OracleLlama(cfg, ck)
+    with HipLlamaModel(cfg, ck) as m:
+        g = m.forward(toks[:12], 0)
+        r = ora.forward(toks[:12], 0)
+        assert np.max(np.abs(g - r)) <= LOGIT_TOL
+        for i, t in enumerate(toks[12:]):
+            g = m.forward([t], 12 + i)
+            r = ora.forward([t], 12 + i)
+            assert np.max(np.abs(g - r)) <= LOGIT_TOL, (i, float(np.max(np.abs(g - r))))
+
+
 def test_qwen2_from_gguf_matches_uploaded_checkpoint(tmp_path):
     from chatnet_amd import gguf
     cfg = TINY_QWEN
@@ -159,6 +178,10 @@ def test_qwen2_upload_rules():
     ("q3_k_m", _native.GGML_Q3_K, False), ("q3_k_m", _native.GGML_Q5_0, True),
     ("q2_k", _native.GGML_Q2_K, True), ("q2_k", _native.GGML_Q8_K, False),
     ("q4_k_m", _native.GGML_Q4_K, True), ("q4_0", _native.GGML_Q6_K, False), ("q8_0", _native.GGML_Q5_K, True),
+    # the IQ family (DequantIQ.cs decoders)
+    ("iq_a", _native.GGML_IQ4_NL, False), ("iq_a", _native.GGML_IQ4_XS, True), ("iq_b", _native.GGML_IQ2_S, False),
+    ("iq_b", _native.GGML_IQ1_M, True), ("iq_a", _native.GGML_IQ3_XXS, False), ("iq_b", _native.GGML_IQ2_XS, True),
+    ("iq_a", _native.GGML_IQ2_XXS, True), ("iq_b", _native.GGML_IQ1_S, False),
 ])
 def test_weight_and_embedding_types_match_oracle(mix, emb, tied):
     cfg = TINY_TEST
@@ -357,8 +380,11 @@ def test_error_paths():
             m.upload_tensor("blk.0.attn_q.weight", t.type, t.dims, t.data[:-18])
         with pytest.raises(_native.ChatnetSizeMismatch):
             m.upload_tensor("blk.0.attn_q.weight", t.type, (cfg.dim, cfg.dim // 2), t.data[: t.data.size // 2])
-        with pytest.raises(_native.ChatnetNotSupported):
-            m.upload_tensor("blk.0.attn_q.weight", 6, t.dims, np.zeros(cfg.dim * cfg.dim // 32 * 22, np.uint8))  # Q5_0
+        with pytest.raises(_native.ChatnetNotSupported):  # Q8_1: no MatVecMulByType branch
+            m.upload_tensor("blk.0.attn_q.weight", 9, t.dims, np.zeros(cfg.dim * cfg.dim // 32 * 36, np.uint8))
+        with pytest.raises(_native.ChatnetOutOfRange):  # IQ3S.Dequantize reads past an embedding row
+            m.upload_tensor("token_embd.weight", _native.GGML_IQ3_S, (cfg.dim, cfg.vocab_size),
+                            np.zeros(cfg.vocab_size * cfg.dim // 256 * 110, np.uint8))
         with pytest.raises(_native.ChatnetKeyNotFound):
             m.upload_tensor("blk.9.attn_q.weight", t.type, t.dims, t.data)
         for name, tt in ck.items():
@@ -443,7 +469,7 @@ def test_span_longer_than_batch_cap_matches_oracle_and_token_schedule(monkeypatc
 
 
 @pytest.mark.parametrize("mix", ["q4_k_m", "q5_k_m", "q8_0", "q6_k", "q4_k", "mixed_blocks", "legacy_blocks",
-                                 "q3_k_m", "q2_k"])
+                                 "q3_k_m", "q2_k", "iq_a", "iq_b"])
 def test_span_block_type_mixes_match_oracle(mix):
     """Spans of models with other block types run batched on packed weights
     (every matrix re-encoded once, types mixed freely, ffn_gate and ffn_up of

@@ -473,3 +473,153 @@ def test_packed_types_match_float64_restatement(qtype):
     y = oracle.matvec(qtype, t.data, x, rows, K)
     ref = W64 @ x.astype(np.float64)
     assert np.max(np.abs(y - ref)) / np.max(np.abs(ref)) < 1e-5
+
+
+# ---------------------------------------------------------------- IQ family
+# DequantIQ.cs: the reference's own bit-field decoders (no codebooks).
+IQ4NL = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
+
+
+def test_iq4_nl_reference_kats():  # QuantizationTests.cs:594-635
+    blk = bytearray(h16(1.0) + bytes(16))
+    blk[2] = 0x80  # element 0: index 0, element 16: index 8
+    deq = oracle.dequant(oracle.IQ4_NL, np.frombuffer(bytes(blk), np.uint8), 32)
+    assert deq[0] == -127.0 and deq[16] == 1.0
+    q = np.frombuffer(h16(0.01) + bytes([0x88] * 16), np.uint8)
+    d = float(np.float16(0.01))
+    dq = oracle.dequant(oracle.IQ4_NL, q, 32)
+    assert np.all(dq == np.float32(d))
+    assert abs(oracle.dot(oracle.IQ4_NL, q, np.ones(32, np.float32)) - float(np.sum(dq))) < 1e-5
+
+
+def test_iq4_nl_table_positions():
+    raw = bytearray(h16(2.0) + bytes(16))
+    for j in range(16):
+        raw[2 + j] = j | ((15 - j) << 4)
+    deq = oracle.dequant(oracle.IQ4_NL, np.frombuffer(bytes(raw), np.uint8), 32)
+    assert list(deq[:16]) == [2.0 * v for v in IQ4NL]
+    assert list(deq[16:]) == [2.0 * v for v in IQ4NL[::-1]]
+
+
+def test_iq4_xs_scale_bytes_and_positions():
+    # all-zero fields: every scale (0 | 0 << 6) - 32, every index 0 (-127)
+    zero = np.frombuffer(h16(1.0) + bytes(134), np.uint8)
+    assert np.all(oracle.dequant(oracle.IQ4_XS, zero, 256) == 4064.0)
+    raw = bytearray(h16(0.5) + bytes(134))
+    raw[4 + 5] = 0xFF                      # low scale of sub-block 5: 0x3F (bits 6, 7 dropped)
+    raw[2] = 0b10 << (2 * 1)               # scales_h bits for sub-block 1 -> (0 | 2 << 6) - 32 = 96
+    raw[3] = 0b01 << (2 * (5 - 4))         # scales_h bits for sub-block 5 -> (63 | 1 << 6) - 32 = 95
+    raw[8 + 16 * 5 + 3] = 0x0F             # sub-block 5: element 3 -> index 15, element 19 -> index 0
+    raw[8 + 16 * 1 + 9] = 0xA0             # sub-block 1: element 9 -> index 0, element 25 -> index 10
+    deq = oracle.dequant(oracle.IQ4_XS, np.frombuffer(bytes(raw), np.uint8), 256)
+    assert deq[32 * 5 + 3] == np.float32(0.5 * 95) * 113 and deq[32 * 5 + 19] == np.float32(0.5 * 95) * -127
+    assert deq[32 * 1 + 9] == np.float32(0.5 * 96) * -127 and deq[32 * 1 + 25] == np.float32(0.5 * 96) * 25
+    # the scale of sub-block 4 is byte 8: sub-block 0's first quant byte
+    raw2 = bytearray(h16(1.0) + bytes(134))
+    raw2[8] = 0x25                         # sub-block 0: element 0 index 5, element 16 index 2
+    deq = oracle.dequant(oracle.IQ4_XS, np.frombuffer(bytes(raw2), np.uint8), 256)
+    assert deq[0] == -32.0 * IQ4NL[5] and deq[16] == -32.0 * IQ4NL[2]
+    assert np.all(deq[128:160] == (0x25 - 32) * -127.0)   # sub-block 4: scale 0x25 - 32 = 5, index 0
+
+
+def test_iq3_s_reads_signs_and_scales_from_the_next_block():
+    # one block: signs of sub-blocks 12..31 and every scale come from the
+    # (zero) tail: scale 1, positive
+    blk = bytearray(h16(1.0) + bytes(108))
+    blk[2 + 5 // 4] = 0b11 << (2 * (5 % 4))  # element 5: q2 = 3
+    blk[66 + 0] = 1 << 5                      # element 5: high bit -> q3 = 7
+    blk[98 + 0] = 1 << 5                      # sub-block 0 sign byte: element 5 negated
+    blk[2 + 200 // 4] = 0b10 << (2 * (200 % 4))  # element 200 (sub-block 25): q3 = 2, sign from the tail
+    deq = oracle.dequant(oracle.IQ3_S, np.frombuffer(bytes(blk), np.uint8), 256)
+    want = np.zeros(256, np.float32)
+    want[5], want[200] = -7.0, 2.0
+    assert np.array_equal(deq, want)
+    # two blocks: block 0's sub-block 25 takes sign byte 98 + 25 = 123 = block 1's byte 13 and
+    # scale byte 130 + 25 // 4 = 136 = block 1's byte 26
+    nxt = bytearray(h16(1.0) + bytes(108))
+    nxt[13] = 1 << 0                                  # element 200 = sub-block 25, j = 0: negated
+    nxt[26] = 0b10 << (2 * (25 % 4))                  # sub-block 25 scale 2 + 1 = 3
+    two = np.frombuffer(bytes(blk) + bytes(nxt), np.uint8)
+    deq = oracle.dequant(oracle.IQ3_S, two, 512)
+    assert deq[200] == -6.0 and deq[5] == -7.0
+    np.testing.assert_array_equal(npref.dequant_iq3_s(two, 512), deq)
+    x = np.zeros(512, np.float32)
+    x[200], x[5] = 1.0, 2.0
+    assert oracle.dot(oracle.IQ3_S, two, x) == -20.0
+
+
+def test_iq3_xxs_fields():
+    zero = np.frombuffer(h16(0.5) + bytes(96), np.uint8)
+    assert np.all(oracle.dequant(oracle.IQ3_XXS, zero, 256) == -2.0)  # 0.5 * (0 - 4)
+    raw = bytearray(zero.tobytes())
+    word = 6 << (3 * 5)  # element 77 = sub-block 9, j = 5: q3 = 6
+    for k in range(3):
+        raw[2 + 3 * 9 + k] = (word >> (8 * k)) & 0xFF
+    deq = oracle.dequant(oracle.IQ3_XXS, np.frombuffer(bytes(raw), np.uint8), 256)
+    assert deq[77] == 1.0 and np.sum(deq != -2.0) == 1
+    assert oracle.dot(oracle.IQ3_XXS, np.frombuffer(bytes(raw), np.uint8), np.ones(256, np.float32)) == 0.5 * (
+        255 * -4 + 2)
+
+
+def test_iq2_xs_scale_nibbles_and_fields():
+    raw = bytearray(h16(1.0) + bytes(72))
+    raw[66 + 5 // 2] = 0xB0            # sub-block 5 (odd: high nibble of a negative sbyte): 11 - 8 = 3
+    raw[2 + 4 * 5 + 6 // 4] = 0b11 << (2 * (6 % 4))  # sub-block 5, element 6: q = 3
+    deq = oracle.dequant(oracle.IQ2_XS, np.frombuffer(bytes(raw), np.uint8), 256)
+    assert deq[16 * 5 + 6] == 6.0                       # 3 * (3 - 1)
+    assert np.all(np.delete(deq[80:96], 6) == -3.0)     # 3 * (0 - 1)
+    assert deq[16 * 4] == 8.0                           # sub-block 4: low nibble 0 - 8 = -8, q = 0
+    np.testing.assert_array_equal(npref.dequant_iq2_xs(np.frombuffer(bytes(raw), np.uint8), 256), deq)
+
+
+def test_iq2_xxs_fields():
+    raw = bytearray(h16(0.25) + bytes(64))
+    raw[2 + 4 * 7 + 13 // 4] = 0b10 << (2 * (13 % 4))  # element 7 * 16 + 13: q = 2
+    deq = oracle.dequant(oracle.IQ2_XXS, np.frombuffer(bytes(raw), np.uint8), 256)
+    assert deq[125] == 0.25 and np.all(np.delete(deq, 125) == -0.25)
+
+
+def test_iq2_s_signs_only_on_the_first_four_elements():
+    raw = bytearray(h16(1.0) + bytes(80))
+    for j in range(4):
+        raw[2 + 4 * 3 + j] = 0xFF          # sub-block 3: every q = 3
+    raw[66 + 3] = 0b1011_0101              # scale 5 + 1 = 6, sign nibble 0b1011
+    deq = oracle.dequant(oracle.IQ2_S, np.frombuffer(bytes(raw), np.uint8), 256)
+    assert list(deq[48:52]) == [-18.0, -18.0, 18.0, -18.0]
+    assert np.all(deq[52:64] == 18.0)
+    assert np.all(deq[:48] == 0.0) and np.all(deq[64:] == 0.0)
+
+
+@pytest.mark.parametrize("qtype,size", [(19, 50), (29, 56)])
+def test_iq1_ternary_fields(qtype, size):
+    raw = bytearray(h16(2.0) + bytes(size - 2))
+    raw[2 + 5] = 1 << 3                    # sub-block 5, element 3: +1
+    raw[34 + 5 // 2] = 1 << ((5 % 2) * 4 + 6 // 2)  # sub-block 5, elements 6 and 7: -1
+    raw[2 + 5] |= 1 << 7                   # ... but element 7's qs bit wins: +1
+    deq = oracle.dequant(qtype, np.frombuffer(bytes(raw), np.uint8), 256)
+    sc = 1.0 if qtype == 19 else 0.5       # IQ1_M: scale bit 5 of byte 50 clear -> 0.5
+    want = np.zeros(256, np.float32)
+    want[43], want[46], want[47] = 2.0 * sc, -2.0 * sc, 2.0 * sc
+    assert np.array_equal(deq, want)
+    if qtype == 29:
+        raw[50] = 1 << 5                   # sub-block 5 full scale
+        deq = oracle.dequant(qtype, np.frombuffer(bytes(raw), np.uint8), 256)
+        assert deq[43] == 2.0 and deq[46] == -2.0
+
+
+def test_iq1_s_dot_closed_form():
+    blk = np.frombuffer(h16(0.5) + bytes([0xFF] * 32) + bytes(16), np.uint8)
+    assert oracle.dot(oracle.IQ1_S, blk, np.ones(256, np.float32)) == 128.0
+
+
+@pytest.mark.parametrize("qtype", [16, 17, 18, 19, 20, 21, 22, 23, 29])
+def test_iq_types_match_float64_restatement(qtype):
+    rows, K = 24, 512
+    t = synth.tensor(qtype, 13, f"iq{qtype}", rows, K)
+    x = synth.normal(14, "iq-x", K, 1.0)
+    W64 = npref.matrix(t)
+    np.testing.assert_allclose(oracle.dequant(qtype, t.data, rows * K).reshape(rows, K), W64, rtol=1e-6,
+                               atol=1e-12)
+    y = oracle.matvec(qtype, t.data, x, rows, K)
+    ref = W64 @ x.astype(np.float64)
+    assert np.max(np.abs(y - ref)) / np.max(np.abs(ref)) < 1e-5
