@@ -170,3 +170,18 @@ def test_iq_types_gemv_shapes(qtype, M, K):
 ])
 def test_iq_types_ragged_shapes(qtype, M, K):
     run_case(qtype, M, K, seed=19)
+
+
+@pytest.mark.parametrize("N", [1, 16])
+def test_iq3_s_ignores_bytes_after_the_matrix(N):
+    # IQ3_S's last block of a row reads 28 bytes past it (DequantIQ.cs:255-283);
+    # past the matrix's end the library reads zeros whatever memory follows
+    M, K = 9, 512
+    t = synth.tensor(21, 23, "iq3s-tail", M, K)
+    x = synth.normal(23, "iq3s-tail-x", N * K, 1.0).reshape(N, K)
+    announce(f"iq3_s tail N={N}")
+    garbage = np.concatenate([t.data, np.full(256, 0xFF, np.uint8)])
+    y = gpu_matmul(21, garbage, x, M, K)
+    for n in range(N):
+        r = oracle.matvec(21, t.data, x[n], M, K)  # the oracle appends zeros
+        assert normwise(y[n], r) <= (TOL if N == 1 else 1e-2)
