@@ -204,9 +204,11 @@ def gemv_sweep(shapes, replays=2, rotate_bytes=ROTATE_BYTES, qtype=2):
 
 
 def gemm_sweep(shapes, ns, rotate_bytes=ROTATE_BYTES):
-    """Batched chatnet_matmul (x fp32 -> bf16, MFMA GEMM, split-K reduce when
-    used) per call, cold weights as in gemv_sweep (one call per weight copy);
-    HIP events on the stream the calls are captured on."""
+    """Batched chatnet_matmul per call: the multi-column GEMV for few columns
+    of smaller matrices, else x fp32 -> bf16, the MFMA GEMM and the split-K
+    reduce when used; cold
+    weights as in gemv_sweep (one call per weight copy); HIP events on the
+    stream the calls are captured on."""
     from chatnet_amd import hiprt, ops, synth
 
     res = {}
@@ -239,8 +241,12 @@ def gemm_sweep(shapes, ns, rotate_bytes=ROTATE_BYTES):
             stream.synchronize()
             alg = nb + 4 * K * N + 4 * M * N
             tflops = 2.0 * M * N * K / us / 1e6
-            per[str(N)] = {"us": round(us, 2), "GB/s": round(alg / us / 1e3, 1), "TFLOP/s": round(tflops, 1),
-                           "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "launches": copies}
+            gemv = N < 8 or (N <= 16 and M * K * N <= 8 * 4096 * 4096)  # the library's choice
+            per[str(N)] = {"path": "multi-column GEMV" if gemv else "MFMA GEMM", "us": round(us, 2),
+                           "GB/s": round(alg / us / 1e3, 1), "hbm_frac": round(alg / us / 1e3 / HBM_PEAK_GBS, 4),
+                           "TFLOP/s": round(tflops, 1),
+                           "mfma_frac": None if gemv else round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                           "launches": copies}
             x.free()
             y.free()
         res[f"{M}x{K}"] = per

@@ -1077,6 +1077,17 @@ int matmul_impl(uint32_t type, const void* w_dev, const float* x_dev, float* y_d
   // variant) are packed into the workspace first, one pass over W.  The types
   // the GEMV reads only as packed units are packed for every N, in both
   // variants.
+  // Q4_0 with a few columns: the GEMV over all of them at once, one pass over W.
+  // Its digit dots cost ALU and LDS time per column, so from 8 columns on it
+  // is taken only up to the size where it measured faster than the MFMA GEMM
+  // (8 columns of a 4096 x 4096 matrix: 14.8 against 17.2 us; 11008 x 4096:
+  // 27.6 against 23.4 us).
+  if (type == CHATNET_GGML_Q4_0 && N >= 2 && gemv_cols_max(K) >= 2 &&
+      (N < 8 || (N <= 16 && (long long)M * K * N <= 8LL * 4096 * 4096))) {
+    HIP_TRY(gemv_cols_launch(w_dev, x_dev, y_dev, M, K, N, cus, st));
+    g_err.clear();
+    return CHATNET_OK;
+  }
   const bool raw = gemm_supports((int)type, K);
   const bool must_pack = gemv_needs_pack((int)type);
   const bool batched = N >= 8 && (raw || must_pack || (!noalloc && gemm_pack_supports((int)type, K)));

@@ -28,6 +28,8 @@
 //   ADD     y[r] += dot                          (O / down + residual, TensorMath.Add :712-733)
 //   QKV     RoPE on q/k pairs + K/V cache write  (TensorMath.ApplyRoPE :408-458, LlamaModel.cs:146-153)
 //   SWIGLU  h[r] = silu(gate[r]) * up[r]         (TensorMath.SiluElementwiseMul :253-286)
+#include <cstring>
+
 #include "device_common.h"
 #include "gemv_common.h"
 #include "kernels.h"
@@ -913,6 +915,128 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
   }
 }
 
+// Several columns of x against the same Q4_0 rows (chatnet_matmul with
+// 2 <= N <= 16): gemv_kernel's digit path with the digit records of ncols
+// columns staged in LDS (column c at c * cstride dwords) and each lane's units,
+// loaded once, dotted with every column.  y[c * M + row] = dot(W[row], x[c]) in
+// gemv_kernel's exact arithmetic (the same records, the same reduction order),
+// so a column's result equals the single-column GEMV's bit for bit wherever
+// that runs gemv_kernel (not gemv_ks_kernel's two-wave K split, 4096 < K <= 8192,
+// which sums in another order).
+template <int NC, int RPW, int LPR, int NU, int BS>
+__global__ __launch_bounds__(BS) void gemv_cols_kernel(GemvArgs a, int ncols) {
+  using T = QTraits<QT_Q4_0>;
+  constexpr int NWV = BS / CN_WAVE;
+  constexpr int RW = RPW * (CN_WAVE / LPR);
+  constexpr int MAXT = ((T::UNIT / 8) * LPR * NU + BS - 1) / BS;
+  // columns whose x loads are issued together before any is digitized
+  constexpr int CB = MAXT <= 1 ? 8 : (MAXT <= 2 ? 4 : 2);
+  extern __shared__ float smem[];
+  const int K = a.K, M = a.n_vrows;
+  const int nunits = K / T::UNIT;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane / LPR, li = lane % LPR;
+  const int n_iters = (M + RW - 1) / RW;
+  const size_t bpr = (size_t)(K / T::BLOCK) * T::BLOCK_BYTES;
+  const int wstride = gridDim.x * NWV;
+  const int cstride = nunits * XD_UNIT_DW;
+  int it = blockIdx.x * NWV + wave;
+  uint32_t* xd = reinterpret_cast<uint32_t*>(smem);
+  float* red = smem + (size_t)NC * cstride;  // sums of squares, unused
+
+  uint32_t w[RPW][NU][T::NDW];
+  issue_loads<QT_Q4_0, RPW, LPR, NU, GEMV_EPI_STORE>(a, it, sub, li, nunits, bpr, w);
+  for (int c0 = 0; c0 < ncols; c0 += CB) {
+    XStage<MAXT, false> st[CB];
+#pragma unroll
+    for (int j = 0; j < CB; j++)  // columns past ncols re-read the last
+      stage_load<MAXT, false, BS>(a.x + (size_t)min(c0 + j, ncols - 1) * K, nullptr, K, st[j]);
+#pragma unroll
+    for (int j = 0; j < CB; j++)
+      if (c0 + j < ncols) stage_digitize<MAXT, false, BS>(st[j], K, xd + (size_t)(c0 + j) * cstride, red);
+  }
+  __syncthreads();
+  while (it < n_iters) {
+    float acc[NC][RPW];
+#pragma unroll
+    for (int c = 0; c < NC; c++)
+#pragma unroll
+      for (int i = 0; i < RPW; i++) acc[c][i] = 0.f;
+#pragma unroll
+    for (int n = 0; n < NU; n++) {
+      const int u = li + LPR * n;
+      if (u < nunits) {
+        uint32_t wu[RPW][T::NDW];
+#pragma unroll
+        for (int i = 0; i < RPW; i++)
+#pragma unroll
+          for (int k = 0; k < T::NDW; k++) wu[i][k] = w[i][n][k];
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+          if (c < ncols) dot_unit_q4_0_dig<RPW>(wu, xd + (size_t)c * cstride + u * XD_UNIT_DW, acc[c]);
+      }
+    }
+    const int cur = it;
+    it += wstride;
+    if (it < n_iters) issue_loads<QT_Q4_0, RPW, LPR, NU, GEMV_EPI_STORE>(a, it, sub, li, nunits, bpr, w);
+#pragma unroll
+    for (int c = 0; c < NC; c++)
+#pragma unroll
+      for (int i = 0; i < RPW; i++)
+#pragma unroll
+        for (int off = LPR / 2; off > 0; off >>= 1) acc[c][i] += __shfl_xor(acc[c][i], off, CN_WAVE);
+    if (li == 0) {
+#pragma unroll
+      for (int c = 0; c < NC; c++)
+#pragma unroll
+        for (int i = 0; i < RPW; i++) {
+          const int row = cur * RW + sub * RPW + i;
+          if (c < ncols && row < M) a.out[0][(size_t)c * M + row] = acc[c][i];
+        }
+    }
+  }
+}
+
+template <int NC, int RPW, int LPR, int NU>
+hipError_t launch_cols_k(const GemvArgs& a, int ncols, int num_cus, hipStream_t st) {
+  constexpr int BS = 512, RW = RPW * (CN_WAVE / LPR);
+  const size_t smem = ((size_t)NC * (a.K / 64) * XD_UNIT_DW + 16) * sizeof(float);
+  const auto kern = &gemv_cols_kernel<NC, RPW, LPR, NU, BS>;
+  static bool lds_set = false;  // every caller sets the same maximum
+  if (!lds_set) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    lds_set = true;
+  }
+  const int per_cu = (int)((160 * 1024) / smem) < 2 ? 1 : 2;
+  const int waves = (a.n_vrows + RW - 1) / RW;
+  int grid = (waves + BS / CN_WAVE - 1) / (BS / CN_WAVE);
+  if (grid > per_cu * num_cus) grid = per_cu * num_cus;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(BS), smem, st, a, ncols);
+  return hipGetLastError();
+}
+
+// Two rows per lane while that still gives every CU a workgroup, else one.
+template <int NC, int LPR, int NU>
+hipError_t launch_cols_rows(const GemvArgs& a, int ncols, int num_cus, hipStream_t st) {
+  if constexpr (NU <= 2) {
+    const int wg2 = (a.n_vrows + 2 * (CN_WAVE / LPR) * 8 - 1) / (2 * (CN_WAVE / LPR) * 8);
+    if (wg2 >= num_cus) return launch_cols_k<NC, 2, LPR, NU>(a, ncols, num_cus, st);
+  }
+  return launch_cols_k<NC, 1, LPR, NU>(a, ncols, num_cus, st);
+}
+
+template <int NC>
+hipError_t launch_cols_nc(const GemvArgs& a, int ncols, int num_cus, hipStream_t st) {
+  const int nunits = a.K / 64;
+  if (nunits <= 32) return launch_cols_rows<NC, 32, 1>(a, ncols, num_cus, st);
+  if (nunits <= 64) return launch_cols_rows<NC, 64, 1>(a, ncols, num_cus, st);
+  if (nunits <= 128) return launch_cols_rows<NC, 64, 2>(a, ncols, num_cus, st);
+  if (nunits <= 192) return launch_cols_rows<NC, 64, 3>(a, ncols, num_cus, st);
+  return launch_cols_rows<NC, 64, 4>(a, ncols, num_cus, st);
+}
+
 template <int QT>
 size_t gemv_smem_bytes(int K) {
   using T = QTraits<QT>;
@@ -1260,6 +1384,37 @@ bool gemv_supports(int qtype, int K) {
     case 29: return K > 0 && K % 256 == 0 && K <= 16384;  // IQ1_M
     default: return false;
   }
+}
+
+int gemv_cols_max(int K) {
+  if (K <= 0 || K % 64 != 0 || K > 16384) return 0;
+  const size_t per_col = (size_t)(K / 64) * XD_UNIT_DW * sizeof(float);
+  const int n = (int)((150 * 1024) / per_col);
+  return n >= 16 ? 16 : (n >= 8 ? 8 : (n >= 4 ? 4 : (n >= 2 ? 2 : 1)));
+}
+
+hipError_t gemv_cols_launch(const void* w, const float* x, float* y, int M, int K, int N, int num_cus,
+                            hipStream_t st) {
+  const int g = gemv_cols_max(K);
+  if (g < 2 || M <= 0 || N < 1 || !w || !x || !y) return hipErrorInvalidValue;
+  for (int c0 = 0; c0 < N; c0 += g) {
+    const int nc = N - c0 < g ? N - c0 : g;
+    GemvArgs a;
+    memset(&a, 0, sizeof(a));
+    a.w[0] = a.w[1] = a.w[2] = static_cast<const uint8_t*>(w);
+    a.seg_rows[0] = M;
+    a.n_vrows = M;
+    a.K = K;
+    a.x = x + (size_t)c0 * K;
+    a.out[0] = y + (size_t)c0 * M;
+    hipError_t e;
+    if (nc <= 2) e = launch_cols_nc<2>(a, nc, num_cus, st);
+    else if (nc <= 4) e = launch_cols_nc<4>(a, nc, num_cus, st);
+    else if (nc <= 8) e = launch_cols_nc<8>(a, nc, num_cus, st);
+    else e = launch_cols_nc<16>(a, nc, num_cus, st);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 bool gemv_needs_pack(int qtype) {

@@ -55,6 +55,12 @@ constexpr int kGemvPacked = -1;
 bool gemv_supports(int qtype, int K);
 // True for the types gemv_supports accepts only as packed units.
 bool gemv_needs_pack(int qtype);
+// Q4_0 rows against N columns of x (N x K fp32, row-major) in launches of up to
+// gemv_cols_max(K) columns: y (N x M) column c = the single-column GEMV of x[c]
+// (bit for bit outside 4096 < K <= 8192).  K % 64 == 0, K <= 16384.
+int gemv_cols_max(int K);
+hipError_t gemv_cols_launch(const void* w, const float* x, float* y, int M, int K, int N, int num_cus,
+                            hipStream_t st);
 size_t gemv_lds_bytes(int qtype, int K);
 hipError_t gemv_launch(int qtype, int epi, const GemvArgs& a, int num_cus, hipStream_t st);
 hipError_t gemv_float_launch(int qtype, int epi, const GemvArgs& a, int num_cus, hipStream_t st);

@@ -236,9 +236,11 @@ CHATNET_API int chatnet_get_logits(chatnet_model* m, float* logits_host);
  * K % 64 == 0, or Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K and the other IQ types
  * and K % 256 == 0, with K <= 16384 (IQ3_S: bytes past W's last row read as
  * zero).
- * N >= 8 with a block type runs the dequant-to-LDS bf16 MFMA GEMM (x rounded
- * to bf16; Q4_0 read as raw blocks, the other types first re-encoded into the
- * workspace as u8 codes with an fp32 scale and offset per 16 weights,
+ * Q4_0 with 2 <= N < 8, or N <= 16 with M*K*N <= 8*4096*4096, runs one
+ * multi-column GEMV (each column the N = 1 product's exact arithmetic).  Other
+ * calls with N >= 8 and a block type run the dequant-to-LDS bf16 MFMA GEMM (x
+ * rounded to bf16; Q4_0 read as raw blocks, the other types first re-encoded
+ * into the workspace as u8 codes with an fp32 scale and offset per 16 weights,
  * M*(K/64)*96 bytes, giving the same dequantized values); any other call
  * (N < 8, F32, F16) runs the fused GEMV once per column, which reads Q4_1,
  * Q5_0, Q5_1, Q2_K, Q3_K, Q8_K and the IQ types from that same re-encoded

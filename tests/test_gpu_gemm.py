@@ -1,10 +1,14 @@
-"""GPU parity of the batched quantized GEMM (chatnet_matmul with N >= 8: Q4_0
-blocks, or Q8_0 / Q4_K / Q5_K / Q6_K packed units, dequantized into bf16 MFMA
-operands, fp32 accumulation) against the oracle's dequantize-then-dot
-(DequantQ4_0.Dequantize, DequantQ4_0.cs:28-58, and the other types'
-Dequantize, followed by an exact float64 product) for every column.
+"""GPU parity of the batched quantized products of chatnet_matmul against the
+oracle's dequantize-then-dot (DequantQ4_0.Dequantize, DequantQ4_0.cs:28-58,
+and the other types' Dequantize, followed by an exact float64 product) for
+every column: the MFMA GEMM (N >= 8 for block types, Q4_0 blocks
+dequantized into bf16 operands, the other types' packed units, fp32
+accumulation) and, for Q4_0 with N < 8, or N <= 16 on matrices up to
+8 * 4096 * 4096 / N weights, the multi-column GEMV.
 
-Bar: normwise error max|y-r|/max|r| <= 1e-2 per column (bf16 operands)."""
+Bar: normwise error max|y-r|/max|r| <= 1e-2 per column (bf16 operands); the
+multi-column GEMV equals the single-column GEMV bit for bit (within 1e-6 for
+4096 < K <= 8192, where the single column splits K over two waves)."""
 import numpy as np
 import pytest
 
@@ -38,15 +42,37 @@ def gemm_case(M, K, N, seed):
     return max(errs)
 
 
-@pytest.mark.parametrize("N", [8, 64, 512])
+@pytest.mark.parametrize("N", [8, 24, 64, 512])
 @pytest.mark.parametrize("M,K", SWEEP)
 def test_q4_0_gemm_sweep_shapes(M, K, N):
     gemm_case(M, K, N, seed=3)
 
 
+# Q4_0 with few columns (N < 8, or up to 16 on smaller matrices): one GEMV
+# launch per group of columns whose digit records fit in LDS (16 at K <= 2048,
+# 8 at 4096, 4 at 11008, 2 at 16384).
+@pytest.mark.parametrize("M,K,N", [
+    (2048, 2048, 2), (2048, 2048, 16), (5632, 2048, 8), (2048, 5632, 11), (4096, 4096, 8), (11008, 4096, 5),
+    (4096, 11008, 7), (33, 16384, 5), (1, 64, 3), (7, 192, 16), (130, 8256, 9), (32000, 2048, 3),
+])
+def test_q4_0_multi_column_gemv_equals_single_column(M, K, N):
+    announce(f"multi-column gemv q4_0 M={M} K={K} N={N}")
+    t = synth.tensor(Q4_0, 6, f"cols{M}x{K}", M, K)
+    x = synth.normal(6, f"colsx{N}x{K}", N * K, 1.0).reshape(N, K)
+    y = gpu_matmul(Q4_0, t.data, x, M, K)
+    assert y.shape == (N, M) and np.all(np.isfinite(y))
+    for n in sorted({0, N // 2, N - 1}):
+        one = gpu_matmul(Q4_0, t.data, x[n], M, K)[0]
+        if 4096 < K <= 8192:  # the single column splits K over two waves: another summation order
+            assert normwise(y[n], one) <= 1e-6
+        else:
+            assert np.array_equal(y[n], one), (n, float(np.max(np.abs(y[n] - one))))
+        assert normwise(y[n], oracle.matvec(Q4_0, t.data, x[n], M, K)) <= 1e-3
+
+
 @pytest.mark.parametrize("M,K,N", [
     (1, 64, 8), (3, 64, 9), (80, 128, 17), (130, 5632, 33), (256, 2048, 100), (67, 192, 300),
-    (2048, 11008, 8), (4096, 64, 513),
+    (2048, 11008, 8), (4096, 64, 513), (2048, 11008, 20), (5, 512, 17),
 ])
 def test_q4_0_gemm_ragged_shapes(M, K, N):
     gemm_case(M, K, N, seed=4)
@@ -54,12 +80,12 @@ def test_q4_0_gemm_ragged_shapes(M, K, N):
 
 def test_gemm_columns_match_gemv():
     """Each GEMM column is the N=1 product of that column (same weights)."""
-    M, K, N = 2048, 2048, 16
+    M, K, N = 2048, 2048, 24
     t = synth.tensor(Q4_0, 8, "gemm-vs-gemv", M, K)
     x = synth.normal(8, "gemm-vs-gemv-x", N * K, 1.0).reshape(N, K)
     announce("gemm columns vs gemv")
     y = gpu_matmul(Q4_0, t.data, x, M, K)
-    for n in (0, 7, 15):
+    for n in (0, 11, 23):
         g = gpu_matmul(Q4_0, t.data, x[n], M, K)[0]
         assert normwise(y[n], g) <= TOL
 
