@@ -1105,6 +1105,16 @@ GemvShape pick_shape(int K, int n_vrows, int num_cus, bool allow8, bool isolated
     s.rpw = 2;
     s.lpr = nunits <= 16 ? 16 : (nunits <= 32 ? 32 : 64);
     s.nu = (nunits + s.lpr - 1) / s.lpr;
+    if (QT == QT_Q5_K && nunits > 64 && nunits <= 96) {
+      // 65..96 half super-blocks (8192 < K <= 12288, the 7B down projection):
+      // 32 lanes x 3 units fill 96 slots where 64 x 2 would leave a third idle;
+      // one row per lane keeps the three units' registers in budget (4096 x
+      // 11008 cold: 13.6 -> 12.0 us; Q6_K measured 14.9 -> 15.3, so it keeps
+      // 64 x 2)
+      s.rpw = 1;
+      s.lpr = 32;
+      s.nu = 3;
+    }
   }
   if (QT == QT_Q4_0 && s.nu == 3) {
     // Rows of 129..192 units (8192 < K <= 12288): one row per lane, so the
@@ -1327,6 +1337,9 @@ hipError_t launch_qt(const GemvArgs& a, int num_cus, hipStream_t st) {
     return launch_k<QT, 2, 4, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
   } else {
     if (s.nu == 1) return launch_k<QT, 2, 1, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
+    if constexpr (QT == QT_Q5_K) {
+      if (s.nu == 3) return launch_one<QT, 1, 32, 3, EPI, CN_BLOCK>(a, s.grid, smem, st);
+    }
     return launch_k<QT, 2, 2, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
   }
 }

@@ -71,6 +71,8 @@ def test_generic_type_gemv_shapes(qtype, M, K):
     # Q4_0 rows of 129..192 units: one row per lane, three units each
     (2, 1, 8256), (2, 5, 12288), (2, 4097, 11008),
     (12, 3, 16384), (13, 3, 16384), (14, 3, 16384), (8, 9, 16320),
+    # Q5_K rows of 65..96 half super-blocks: one row per lane, 32 lanes x 3 units
+    (13, 5, 8448), (13, 7, 12288), (13, 66, 11008),
 ])
 def test_ragged_and_misaligned_shapes(qtype, M, K):
     run_case(qtype, M, K, seed=5)
