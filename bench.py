@@ -452,11 +452,12 @@ def main():
     fp16kv = None
     par = {}
     if not args.roofline_only and not args.no_kquant and want("kquant"):
-        log("Q4_K / Q6_K / Q8_0 / Q5_K / F16 gemv (cold), 7B Q4_K_M- and Q3_K_M-style 64-token decodes")
+        log("Q4_K / Q6_K / Q8_0 / Q5_K / Q3_K / F16 gemv (cold), 7B Q4_K_M- and Q3_K_M-style 64-token decodes")
         kq = {"gemv_q4_k_cold": gemv_sweep(KQ4_SHAPES, qtype=12),
               "gemv_q6_k_cold": gemv_sweep(KQ6_SHAPES, qtype=14),
               "gemv_q8_0_cold": gemv_sweep(GENERIC_SHAPES, qtype=8),
               "gemv_q5_k_cold": gemv_sweep(GENERIC_SHAPES, qtype=13),
+              "gemv_q3_k_cold": gemv_sweep(GENERIC_SHAPES, qtype=11),
               "gemv_f16_cold": gemv_sweep(GENERIC_SHAPES[:2], qtype=1)}
         wk = WORKLOADS["llama2_7b_q4_k_m_decode"]
         ckk = wk.checkpoint()
@@ -465,8 +466,8 @@ def main():
         kq["weights_GB"] = round(synth.checkpoint_bytes(ckk) / 1e9, 3)
         par[wk.name] = parity(wk.name, tk, lpk)
         del ckk
-        # the same shape and prompt in a mix served through packed units made at
-        # upload: Q3_K attention and gate/up, Q4_K down, Q6_K head (Q3_K_M-style);
+        # the same shape and prompt in a Q3_K_M-style mix, every matrix read from
+        # its stored blocks: Q3_K attention and gate/up, Q4_K down, Q6_K head;
         # no committed fixture for it (its parity is the GPU tests' at small shapes)
         ck3 = synth.llama_checkpoint(wk.config, seed=wk.seed, mix="q3_k_m")
         dt3, _, _ = decode_run(wk.config, ck3, wk.prompt(), wk.n_decode, 4)

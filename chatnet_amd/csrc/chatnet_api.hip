@@ -74,13 +74,14 @@ int device_cus(int dev) {
 }
 
 // Weight types the GEMV serves (LlamaModel.MatVecMulByType, LlamaModel.cs:470-567):
-// F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K from the stored blocks, and Q4_1,
-// Q5_0, Q5_1, Q2_K, Q3_K, Q8_K and the nine IQ types (the reference's
+// F32, F16, Q4_0, Q8_0, Q3_K, Q4_K, Q5_K, Q6_K from the stored blocks, and
+// Q4_1, Q5_0, Q5_1, Q2_K, Q8_K and the nine IQ types (the reference's
 // MatVecMulGeneric branches, LlamaModel.cs:488-562) from packed units made at
 // upload.
 bool is_matrix_type(uint32_t t) {
   return t == CHATNET_GGML_F32 || t == CHATNET_GGML_F16 || t == CHATNET_GGML_Q4_0 || t == CHATNET_GGML_Q8_0 ||
-         t == CHATNET_GGML_Q4_K || t == CHATNET_GGML_Q5_K || t == CHATNET_GGML_Q6_K || gemv_needs_pack((int)t);
+         t == CHATNET_GGML_Q3_K || t == CHATNET_GGML_Q4_K || t == CHATNET_GGML_Q5_K || t == CHATNET_GGML_Q6_K ||
+         gemv_needs_pack((int)t);
 }
 
 // Embedding rows read in their stored form; every other block type is

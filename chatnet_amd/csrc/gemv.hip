@@ -36,7 +36,7 @@
 
 namespace {
 
-constexpr int QT_Q4_0 = 2, QT_Q8_0 = 8, QT_Q4_K = 12, QT_Q5_K = 13, QT_Q6_K = 14;
+constexpr int QT_Q4_0 = 2, QT_Q8_0 = 8, QT_Q3_K = 11, QT_Q4_K = 12, QT_Q5_K = 13, QT_Q6_K = 14;
 
 template <int QT> struct QTraits;
 template <> struct QTraits<QT_Q4_0> {
@@ -53,6 +53,10 @@ template <> struct QTraits<QT_Q4_K> {
 template <> struct QTraits<QT_Q6_K> {
   static constexpr int UNIT = 128, NDW = 27;
   static constexpr int BLOCK_BYTES = 210, BLOCK = 256;
+};
+template <> struct QTraits<QT_Q3_K> {
+  static constexpr int UNIT = 128, NDW = 16;
+  static constexpr int BLOCK_BYTES = 110, BLOCK = 256;
 };
 template <> struct QTraits<QT_Q8_0> {
   static constexpr int UNIT = 64, NDW = 17;  // two 34-byte blocks
@@ -350,7 +354,10 @@ __device__ __forceinline__ void stage_load16(const float* __restrict__ x, const 
 
 // Writes the base-256 digit records of x * norm_w (x alone without NORM) and,
 // as stage_digitize, leaves each wave's share of sum x^2 in red[wave].
-template <int MAXT, bool NORM, int BS>
+// TR (Q3_K): record dword w, byte b holds element 4b + w of the group instead
+// of element 4w + b, the order in which Q3_K's 2-bit fields come out of a qs
+// dword (shift by 2w, mask 0x03030303).
+template <int MAXT, bool NORM, int BS, bool TR = false>
 __device__ __forceinline__ void stage_digitize16(const XStage16<MAXT, NORM>& st, int K, uint32_t* xd, float* red) {
   const int ngroups = K >> 4;
   float ss = 0.f;
@@ -388,10 +395,13 @@ __device__ __forceinline__ void stage_digitize16(const XStage16<MAXT, NORM>& st,
       uint32_t P[3][4];
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        const uint32_t a01 = __builtin_amdgcn_perm(U[4 * k + 1], U[4 * k], 0x05010400u);  // U0.b0 U1.b0 U0.b1 U1.b1
-        const uint32_t a23 = __builtin_amdgcn_perm(U[4 * k + 3], U[4 * k + 2], 0x05010400u);
-        const uint32_t c01 = __builtin_amdgcn_perm(U[4 * k + 1], U[4 * k], 0x00000602u);  // U0.b2 U1.b2
-        const uint32_t c23 = __builtin_amdgcn_perm(U[4 * k + 3], U[4 * k + 2], 0x00000602u);
+        // the four elements of record dword k, in byte order
+        const uint32_t u0 = U[TR ? k : 4 * k], u1 = U[TR ? 4 + k : 4 * k + 1];
+        const uint32_t u2 = U[TR ? 8 + k : 4 * k + 2], u3 = U[TR ? 12 + k : 4 * k + 3];
+        const uint32_t a01 = __builtin_amdgcn_perm(u1, u0, 0x05010400u);  // U0.b0 U1.b0 U0.b1 U1.b1
+        const uint32_t a23 = __builtin_amdgcn_perm(u3, u2, 0x05010400u);
+        const uint32_t c01 = __builtin_amdgcn_perm(u1, u0, 0x00000602u);  // U0.b2 U1.b2
+        const uint32_t c23 = __builtin_amdgcn_perm(u3, u2, 0x00000602u);
         P[0][k] = __builtin_amdgcn_perm(a23, a01, 0x05040100u) ^ 0x80808080u;
         P[1][k] = __builtin_amdgcn_perm(a23, a01, 0x07060302u) ^ 0x80808080u;
         P[2][k] = __builtin_amdgcn_perm(c23, c01, 0x05040100u) ^ 0x80808080u;
@@ -492,6 +502,39 @@ __device__ __forceinline__ void load_unit<QT_Q6_K>(const cn_gbyte* row, int u, u
   w[24] = __builtin_amdgcn_alignbyte(c[1], c[0], sh);
   w[25] = __builtin_amdgcn_alignbyte(c[2], c[1], sh);
   w[26] = *(const CN_GLOBAL uint16_t*)(sb + 208);
+}
+
+// Q3_K half super-block h = u & 1 (DequantQ3K.cs: hmask[32] @0, qs[64] @32,
+// scales[12] @96, fp16 d @108; 110 bytes, so super-blocks start on 2-byte
+// boundaries): w[0..7] = qs[32h .. 32h+31], w[8..11] = hmask[16h .. 16h+15],
+// w[12..14] = the 12 scale bytes, w[15] = d (low half).  As for Q6_K, each
+// piece is read as the dword-aligned window that covers it and realigned by
+// sh = 0 or 2 bytes; the qs and hmask windows end inside the super-block (at
+// byte 99 at most), the scales' window takes its fourth dword only when sh = 2
+// (it then ends at byte 109), and d is a 16-bit load, so nothing past the
+// super-block is read.
+template <>
+__device__ __forceinline__ void load_unit<QT_Q3_K>(const cn_gbyte* row, int u, uint32_t* w) {
+  const cn_gbyte* sb = row + (size_t)(u >> 1) * 110;
+  const int h = u & 1;
+  const uintptr_t base = reinterpret_cast<uintptr_t>(sb);
+  const uint32_t sh = (uint32_t)(base & 3);  // 0 or 2
+  const CN_GLOBAL uint32_t* q = (const CN_GLOBAL uint32_t*)(base & ~(uintptr_t)3);
+  uint32_t r[9], t[5], c[4];
+#pragma unroll
+  for (int k = 0; k < 9; k++) r[k] = q[8 + 8 * h + k];
+#pragma unroll
+  for (int k = 0; k < 5; k++) t[k] = q[4 * h + k];
+#pragma unroll
+  for (int k = 0; k < 3; k++) c[k] = q[24 + k];
+  c[3] = sh ? q[27] : 0u;
+#pragma unroll
+  for (int k = 0; k < 8; k++) w[k] = __builtin_amdgcn_alignbyte(r[k + 1], r[k], sh);
+#pragma unroll
+  for (int k = 0; k < 4; k++) w[8 + k] = __builtin_amdgcn_alignbyte(t[k + 1], t[k], sh);
+#pragma unroll
+  for (int k = 0; k < 3; k++) w[12 + k] = __builtin_amdgcn_alignbyte(c[k + 1], c[k], sh);
+  w[15] = *(const CN_GLOBAL uint16_t*)(sb + 108);
 }
 
 // ---------------------------------------------------------------------------
@@ -657,6 +700,59 @@ __device__ __forceinline__ void dot_unit_q6_k_dig(const uint32_t (*w)[27], const
   for (int i = 0; i < RPW; i++) acc[i] += cn_h2f(w[i][26]) * part[i];
 }
 
+// Q3_K half super-block h (DequantQ3K.cs:35-70, DecodeScales :122-150): element
+// l of the half is q3 = (qs byte l/4 >> 2(l%4)) & 3 | (hmask bit l) << 2,
+// value d*sc*(q3 - 4) with sc the 6-bit scale of group 8h + l/16 (low nibble
+// of byte i or high nibble of byte i-8, two bits of byte 8 + i%4 above it,
+// minus 32).  Group g's qs are dword g; shifted by 2w and masked they give the
+// 2-bit fields of elements 4b + w in bytes b, which meet the transposed digit
+// records (stage_digitize16 with TR).  Its 16 hmask bits are spread one nibble
+// per byte (bit 4b + w -> bit 8b + w) and bit w of each byte moved to bit 2.
+template <int RPW>
+__device__ __forceinline__ void dot_unit_q3_k_dig(const uint32_t (*w)[16], const uint32_t* xd, int h, float* acc) {
+  float part[RPW];
+#pragma unroll
+  for (int i = 0; i < RPW; i++) part[i] = 0.f;
+#pragma unroll
+  for (int g = 0; g < 8; g++) {
+    const uint32_t* rec = xd + 16 * g;
+    uint32_t D[3][4];
+#pragma unroll
+    for (int d = 0; d < 3; d++) {
+      const uint4 t = *reinterpret_cast<const uint4*>(rec + 4 * d);
+      D[d][0] = t.x; D[d][1] = t.y; D[d][2] = t.z; D[d][3] = t.w;
+    }
+    const int xsum = (int)rec[12];
+    const int e = (int)rec[13];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      const uint32_t qw = w[i][g];
+      uint32_t hs = (w[i][8 + (g >> 1)] >> (16 * (g & 1))) & 0xFFFFu;
+      hs = (hs | (hs << 8)) & 0x00FF00FFu;
+      hs = (hs | (hs << 4)) & 0x0F0F0F0Fu;
+      uint32_t q[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const uint32_t hb = k < 3 ? (hs << (2 - k)) : (hs >> 1);
+        q[k] = ((qw >> (2 * k)) & 0x03030303u) | (hb & 0x04040404u);
+      }
+      int t = 0;
+#pragma unroll
+      for (int d = 2; d >= 0; d--) {
+        if (d < 2) t <<= 8;
+#pragma unroll
+        for (int k = 0; k < 4; k++) t = __builtin_amdgcn_sdot4((int)q[k], (int)D[d][k], t, false);
+      }
+      const uint32_t lob = (w[i][12 + (g >> 2)] >> (8 * (g & 3))) >> (4 * h);
+      const uint32_t hib = w[i][14] >> (8 * (g & 3) + 4 * h + 2 * (g >> 2));
+      const int scv = (int)((lob & 15u) | ((hib & 3u) << 4)) - 32;
+      part[i] += ldexpf((float)(t - 4 * xsum) * (float)scv, -e);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RPW; i++) acc[i] += cn_h2f(w[i][15]) * part[i];
+}
+
 // Q8_0 pair of blocks (DequantQ8_0.cs:51-90) against the base-256 digit
 // records of its four 16-element groups: block A is unit bytes 0..33 (d, then
 // 32 int8; its qs realigned with alignbyte), block B bytes 34..67 (d in the
@@ -809,7 +905,8 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
   constexpr int NS = merge_slots(EPI);
   const int stop_v = cn_load_late(stop_flag(a));
   const int pos_v = (EPI == GEMV_EPI_QKV || MERGE) ? cn_load_late(a.pos) : 0;
-  constexpr bool kDig8 = QT == QT_Q8_0 || QT == QT_Q6_K || QT == QT_Q5_K || (QT == QT_Q4_K && LPR > 32);
+  constexpr bool kDig8 =
+      QT == QT_Q8_0 || QT == QT_Q3_K || QT == QT_Q6_K || QT == QT_Q5_K || (QT == QT_Q4_K && LPR > 32);
   MergeSrc ms{};
   if constexpr (MERGE) {
     ms.o = a.part_o;
@@ -844,7 +941,7 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
         load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, 0, res);
       }
       xred = reinterpret_cast<float*>(smem) + (size_t)((K + 127) >> 7) * XD6_UNIT_DW;
-      stage_digitize16<MAXT, NORM, BS>(st, K, xd, xred);
+      stage_digitize16<MAXT, NORM, BS, QT == QT_Q3_K>(st, K, xd, xred);
       if constexpr (kLate) {
         issue_loads<QT, RPW, LPR, NU, EPI>(a, it, sub, li, nunits, bpr, w);
         load_residual<EPI, RPW, NR>(a, it * RW + sub * RPW, li, 0, res);
@@ -891,6 +988,7 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
           if constexpr (QT == QT_Q4_0) dot_unit_q4_0_dig<RPW>(wu, xd + u * XD_UNIT_DW, acc);
           else if constexpr (QT == QT_Q8_0) dot_unit_q8_0_dig8<RPW>(wu, xd + (u >> 1) * XD6_UNIT_DW + 64 * (u & 1), acc);
           else if constexpr (QT == QT_Q6_K) dot_unit_q6_k_dig<RPW>(wu, xd + u * XD6_UNIT_DW, acc);
+          else if constexpr (QT == QT_Q3_K) dot_unit_q3_k_dig<RPW>(wu, xd + u * XD6_UNIT_DW, u & 1, acc);
           else if constexpr (kDig8) dot_unit_k45_dig8<QT, RPW>(wu, xd + u * XD6_UNIT_DW, u & 1, acc);
           else dot_unit_q4_k_dig<RPW>(wu, xd + 2 * u * XD_UNIT_DW, u & 1, acc);
         }
@@ -1163,8 +1261,8 @@ GemvShape pick_shape(int K, int n_vrows, int num_cus, bool allow8, bool isolated
   // per CU (32000x4096 29.2 -> 28.0 us), two-unit K-quant lanes (~160 VGPRs,
   // x digitized before the weight loads) at three, Q4_K and Q5_K one-unit
   // lanes at two
-  const bool kq = QT == QT_Q4_K || QT == QT_Q5_K || QT == QT_Q6_K;
-  const int per_cu = QT == QT_Q6_K && s.nu == 1 ? 4 : (kq && s.nu >= 2 ? 3 : 2);
+  const bool kq = QT == QT_Q3_K || QT == QT_Q4_K || QT == QT_Q5_K || QT == QT_Q6_K;
+  const int per_cu = (QT == QT_Q6_K || QT == QT_Q3_K) && s.nu == 1 ? 4 : (kq && s.nu >= 2 ? 3 : 2);
   if (s.grid > per_cu * num_cus) s.grid = per_cu * num_cus;
   if (s.grid < 1) s.grid = 1;
   return s;
@@ -1350,6 +1448,7 @@ hipError_t launch_epi(int qtype, const GemvArgs& a, int num_cus, hipStream_t st)
     case QT_Q4_0: return launch_qt<QT_Q4_0, EPI>(a, num_cus, st);
     case QT_Q4_K: return launch_qt<QT_Q4_K, EPI>(a, num_cus, st);
     case QT_Q6_K: return launch_qt<QT_Q6_K, EPI>(a, num_cus, st);
+    case QT_Q3_K: return launch_qt<QT_Q3_K, EPI>(a, num_cus, st);
     case QT_Q8_0: return launch_qt<QT_Q8_0, EPI>(a, num_cus, st);
     case QT_Q5_K: return launch_qt<QT_Q5_K, EPI>(a, num_cus, st);
     default: return hipErrorInvalidValue;
@@ -1363,6 +1462,7 @@ size_t gemv_lds_bytes(int qtype, int K) {
     case QT_Q4_0: return gemv_smem_bytes<QT_Q4_0>(K);
     case QT_Q4_K: return gemv_smem_bytes<QT_Q4_K>(K);
     case QT_Q6_K: return gemv_smem_bytes<QT_Q6_K>(K);
+    case QT_Q3_K: return gemv_smem_bytes<QT_Q3_K>(K);
     case QT_Q8_0: return gemv_smem_bytes<QT_Q8_0>(K);
     case QT_Q5_K: return gemv_smem_bytes<QT_Q5_K>(K);
     default: return 0;
@@ -1376,6 +1476,7 @@ bool gemv_supports(int qtype, int K) {
     case 1:
     case QT_Q4_0:
     case QT_Q8_0: return K > 0 && K % 64 == 0 && K <= 16384;
+    case QT_Q3_K:
     case QT_Q4_K:
     case QT_Q5_K:
     case QT_Q6_K: return K > 0 && K % 256 == 0 && K <= 16384;
@@ -1385,7 +1486,6 @@ bool gemv_supports(int qtype, int K) {
     case 7: return K > 0 && K % 64 == 0 && K <= 16384;  // Q5_1
     case 20: return K > 0 && K % 64 == 0 && K <= 16384;  // IQ4_NL
     case 10:  // Q2_K
-    case 11:  // Q3_K
     case 15:  // Q8_K
     case 16:  // IQ2_XXS
     case 17:  // IQ2_XS
@@ -1431,13 +1531,14 @@ hipError_t gemv_cols_launch(const void* w, const float* x, float* y, int M, int 
 }
 
 bool gemv_needs_pack(int qtype) {
-  return qtype == 3 || qtype == 6 || qtype == 7 || qtype == 10 || qtype == 11 || qtype == 15 ||
-         (qtype >= 16 && qtype <= 23) || qtype == 29;
+  return qtype == 3 || qtype == 6 || qtype == 7 || qtype == 10 || qtype == 15 || (qtype >= 16 && qtype <= 23) ||
+         qtype == 29;
 }
 
 hipError_t gemv_launch(int qtype, int epi, const GemvArgs& a, int num_cus, hipStream_t st) {
   if (qtype == 0 || qtype == 1 || qtype == kGemvPacked) return gemv_float_launch(qtype, epi, a, num_cus, st);
-  if (qtype != QT_Q4_0 && qtype != QT_Q8_0 && qtype != QT_Q4_K && qtype != QT_Q5_K && qtype != QT_Q6_K)
+  if (qtype != QT_Q4_0 && qtype != QT_Q8_0 && qtype != QT_Q3_K && qtype != QT_Q4_K && qtype != QT_Q5_K &&
+      qtype != QT_Q6_K)
     return hipErrorInvalidValue;  // the packed-unit types are launched as kGemvPacked
   switch (epi) {
     case GEMV_EPI_STORE: return launch_epi<GEMV_EPI_STORE>(qtype, a, num_cus, st);

@@ -49,8 +49,8 @@ struct GemvArgs {
 // Weight types: Q4_0, Q8_0 (K % 64 == 0), Q4_K, Q5_K, Q6_K (K % 256 == 0), and
 // F32 / F16 (K % 64 == 0, gemv_float.hip); K <= 16384.  gemv_float_launch
 // also takes kGemvPacked: w[] holding packed units (gemm_pack_launch), how the
-// model runs Q4_1, Q5_0, Q5_1, IQ4_NL (K % 64 == 0), Q2_K, Q3_K, Q8_K and the
-// other IQ types (K % 256 == 0).
+// model runs Q4_1, Q5_0, Q5_1, IQ4_NL (K % 64 == 0), Q2_K, Q8_K and the other
+// IQ types (K % 256 == 0).
 constexpr int kGemvPacked = -1;
 bool gemv_supports(int qtype, int K);
 // True for the types gemv_supports accepts only as packed units.

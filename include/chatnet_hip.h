@@ -130,7 +130,7 @@ CHATNET_API int chatnet_create(const chatnet_config* cfg, int device, chatnet_mo
  * F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K
  * and IQ2_XXS, IQ2_XS, IQ3_XXS, IQ1_S, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS, IQ1_M
  * (as DequantIQ.cs decodes them), each dispatched on its own type.  Q4_1,
- * Q5_0, Q5_1, Q2_K, Q3_K, Q8_K and the IQ types are also re-encoded on the
+ * Q5_0, Q5_1, Q2_K, Q8_K and the IQ types are also re-encoded on the
  * device at upload (u8 codes with an fp32 scale and offset per 16 weights,
  * M*(K/64)*96 bytes beside the stored blocks), the form the GEMV reads them
  * in.  An IQ3_S row's last block reads 28 bytes past the row, as the
@@ -243,7 +243,7 @@ CHATNET_API int chatnet_get_logits(chatnet_model* m, float* logits_host);
  * into the workspace as u8 codes with an fp32 scale and offset per 16 weights,
  * M*(K/64)*96 bytes, giving the same dequantized values); any other call
  * (N < 8, F32, F16) runs the fused GEMV once per column, which reads Q4_1,
- * Q5_0, Q5_1, Q2_K, Q3_K, Q8_K and the IQ types from that same re-encoded
+ * Q5_0, Q5_1, Q2_K, Q8_K and the IQ types from that same re-encoded
  * copy, made in the workspace first.  The GEMM's workspace is allocated on first use
  * per (device, stream) and kept until the process ends (a buffer it outgrows
  * is retired, not freed, since a captured graph may still read it).  A call
@@ -259,9 +259,9 @@ CHATNET_API int chatnet_matmul(uint32_t ggml_type, const void* w_dev, const floa
  * device memory: code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc.  No counterpart in the reference.  Same arguments,
  * kernels and results as chatnet_matmul for Q4_0 and for the types read
- * only as packed units (Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q8_K and the IQ types,
+ * only as packed units (Q4_1, Q5_0, Q5_1, Q2_K, Q8_K and the IQ types,
  * whose packed copy of W, M*(K/64)*96 bytes, goes into the scratch); Q8_0,
- * Q4_K, Q5_K and Q6_K run the fused GEMV once per column on their stored
+ * Q3_K, Q4_K, Q5_K and Q6_K run the fused GEMV once per column on their stored
  * blocks.  The scratch (bf16 x, the K-split partials and the packed W) lives
  * in a fixed 64 MiB array per device, held by the library from load to
  * process exit, instead of a per-stream workspace.  Calls needing more

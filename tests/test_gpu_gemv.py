@@ -136,10 +136,11 @@ def test_float_weight_gemv_shapes(qtype, M, K):
     run_case(qtype, M, K, seed=7)
 
 
-# The types the GEMV reads as packed units (re-encoded on the device first:
-# u8 codes with an fp32 scale and offset per 16 weights, each weight equal to
-# the type's dequantized value): Q4_1, Q5_0, Q5_1 and Q2_K, Q3_K, Q8_K, the
-# MatVecMulGeneric branches of LlamaModel.MatVecMulByType (LlamaModel.cs:488-528).
+# The MatVecMulGeneric branches of LlamaModel.MatVecMulByType (LlamaModel.cs:488-528):
+# Q4_1, Q5_0, Q5_1, Q2_K and Q8_K the GEMV reads as packed units (re-encoded on
+# the device first: u8 codes with an fp32 scale and offset per 16 weights, each
+# weight equal to the type's dequantized value); Q3_K it reads from the stored
+# 110-byte blocks (rows of an odd number of blocks start 2 bytes off a dword).
 PACKED_ONLY = {3: "q4_1", 6: "q5_0", 7: "q5_1", 10: "q2_k", 11: "q3_k", 15: "q8_k"}
 # The IQ family (DequantIQ.cs), read the same way.
 IQ = {16: "iq2_xxs", 17: "iq2_xs", 18: "iq3_xxs", 19: "iq1_s", 20: "iq4_nl", 21: "iq3_s", 22: "iq2_s",
@@ -155,6 +156,7 @@ def test_packed_unit_types_gemv_shapes(qtype, M, K):
 @pytest.mark.parametrize("qtype,M,K", [
     (3, 1, 64), (6, 3, 128), (7, 17, 192), (3, 33, 2048), (6, 5, 16384), (7, 130, 5632),
     (10, 1, 256), (11, 9, 768), (15, 40, 2816), (10, 7, 5632), (11, 3, 16384), (15, 5, 16384),
+    (11, 1, 256), (11, 7, 256), (11, 65, 1280), (11, 130, 5632), (11, 257, 4352),
 ])
 def test_packed_unit_types_ragged_shapes(qtype, M, K):
     run_case(qtype, M, K, seed=13)

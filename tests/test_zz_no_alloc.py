@@ -58,7 +58,8 @@ def test_noalloc_refuses_more_scratch_than_it_has():
 
 
 @pytest.mark.parametrize("qtype,first,second", [
-    (11, (2048, 2048, 64), (1024, 1024, 2)),   # Q3_K: packed W in the scratch, GEMM then GEMV
+    (10, (2048, 2048, 64), (1024, 1024, 2)),   # Q2_K: packed W in the scratch, GEMM then GEMV
+    (11, (2048, 2048, 64), (1024, 1024, 2)),   # Q3_K: GEMV over the stored blocks per column
     (3, (4096, 4096, 1), (512, 2048, 16)),     # Q4_1: GEMV then GEMM
 ])
 def test_noalloc_packed_unit_types_match_matmul(qtype, first, second):
