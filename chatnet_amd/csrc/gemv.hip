@@ -1165,7 +1165,7 @@ struct GemvShape {
 // of two covering the row (min 16), 256 threads, at most two workgroups per CU.
 // Q8_0: Q4_0's (LPR, NU) with 2 rows per lane and 256 threads.
 template <int QT>
-GemvShape pick_shape(int K, int n_vrows, int num_cus, bool allow8, bool isolated) {
+GemvShape pick_shape(int K, int n_vrows, int num_cus, bool allow8, bool isolated, bool paired) {
   using T = QTraits<QT>;
   const int nunits = K / T::UNIT;
   GemvShape s{64, 1, 2, CN_BLOCK, 1};
@@ -1203,7 +1203,7 @@ GemvShape pick_shape(int K, int n_vrows, int num_cus, bool allow8, bool isolated
     s.rpw = 2;
     s.lpr = nunits <= 16 ? 16 : (nunits <= 32 ? 32 : 64);
     s.nu = (nunits + s.lpr - 1) / s.lpr;
-    if (QT == QT_Q5_K && nunits > 64 && nunits <= 96) {
+    if (QT == QT_Q5_K && nunits > 64 && nunits <= 96 && !paired) {
       // 65..96 half super-blocks (8192 < K <= 12288, the 7B down projection):
       // 32 lanes x 3 units fill 96 slots where 64 x 2 would leave a third idle;
       // one row per lane keeps the three units' registers in budget (4096 x
@@ -1214,7 +1214,7 @@ GemvShape pick_shape(int K, int n_vrows, int num_cus, bool allow8, bool isolated
       s.nu = 3;
     }
   }
-  if (QT == QT_Q4_0 && s.nu == 3) {
+  if (QT == QT_Q4_0 && s.nu == 3 && !paired) {
     // Rows of 129..192 units (8192 < K <= 12288): one row per lane, so the
     // launch has twice the waves and each finishes its three units sooner
     // (7B down projection 4096x11008 in the decode graph: 723 -> 730 tok/s),
@@ -1412,7 +1412,9 @@ hipError_t launch_qt(const GemvArgs& a, int num_cus, hipStream_t st) {
     const int nunits = a.K >> 6;
     if (nunits > 64 && nunits <= 128) return launch_ks<2, EPI>(a, st);
   }
-  const GemvShape s = pick_shape<QT>(a.K, a.n_vrows, num_cus, kAllow8, EPI == GEMV_EPI_STORE);
+  // the QKV and SwiGLU epilogues take a lane's rows in pairs: never one row per lane
+  constexpr bool kPaired = EPI == GEMV_EPI_QKV || EPI == GEMV_EPI_SWIGLU;
+  const GemvShape s = pick_shape<QT>(a.K, a.n_vrows, num_cus, kAllow8, EPI == GEMV_EPI_STORE, kPaired);
   const size_t smem = gemv_smem_bytes<QT>(a.K);
   if constexpr (QT == QT_Q4_0) {
     if (s.nu == 1) {
@@ -1426,7 +1428,10 @@ hipError_t launch_qt(const GemvArgs& a, int num_cus, hipStream_t st) {
       if (s.rpw == 4) return launch_bs<QT, 4, 2, EPI>(a, s, smem, st);
       return launch_bs<QT, 2, 2, EPI>(a, s, smem, st);
     }
-    if (s.nu == 3) return launch_bs<QT, 1, 3, EPI>(a, s, smem, st);
+    if (s.nu == 3) {
+      if constexpr (kPaired) return launch_bs<QT, 2, 3, EPI>(a, s, smem, st);
+      else return launch_bs<QT, 1, 3, EPI>(a, s, smem, st);
+    }
     return launch_bs<QT, 2, 4, EPI>(a, s, smem, st);
   } else if constexpr (QT == QT_Q8_0) {
     if (s.nu == 1) return launch_k<QT, 2, 1, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
@@ -1435,7 +1440,7 @@ hipError_t launch_qt(const GemvArgs& a, int num_cus, hipStream_t st) {
     return launch_k<QT, 2, 4, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
   } else {
     if (s.nu == 1) return launch_k<QT, 2, 1, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
-    if constexpr (QT == QT_Q5_K) {
+    if constexpr (QT == QT_Q5_K && !kPaired) {
       if (s.nu == 3) return launch_one<QT, 1, 32, 3, EPI, CN_BLOCK>(a, s.grid, smem, st);
     }
     return launch_k<QT, 2, 2, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);

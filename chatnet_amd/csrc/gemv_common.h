@@ -209,8 +209,12 @@ __device__ __forceinline__ void load_rope(const GemvArgs& a, int vr0, int pos, f
 
 // pos: the device-side position (QKV), read at kernel start; res: what
 // load_residual fetched for these rows.
+// QKV (RoPE pairs) and SwiGLU (gate/up pairs) take the rows of a lane two at a
+// time and need an even RPW; the store and add forms also take one row.
 template <int EPI, int RPW>
 __device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, const float* v, const float* res, int pos) {
+  static_assert(RPW % 2 == 0 || (EPI != GEMV_EPI_QKV && EPI != GEMV_EPI_SWIGLU),
+                "the QKV and SwiGLU epilogues take rows in pairs");
 #pragma unroll
   for (int i = 0; i < RPW; i += 2) {
     const int vr = vr0 + i;
@@ -219,10 +223,14 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int vr0, const float
     map_row<EPI>(a, vr, seg, r);
     if constexpr (EPI == GEMV_EPI_STORE || EPI == GEMV_EPI_LOGITS) {
       a.out[0][r] = v[i];
-      if (vr + 1 < a.n_vrows) a.out[0][r + 1] = v[i + 1];
+      if constexpr (RPW >= 2) {
+        if (vr + 1 < a.n_vrows) a.out[0][r + 1] = v[i + 1];
+      }
     } else if constexpr (EPI == GEMV_EPI_ADD || is_merge(EPI)) {
       a.out[0][r] = res[i] + v[i];
-      if (vr + 1 < a.n_vrows) a.out[0][r + 1] = res[i + 1] + v[i + 1];
+      if constexpr (RPW >= 2) {
+        if (vr + 1 < a.n_vrows) a.out[0][r + 1] = res[i + 1] + v[i + 1];
+      }
     } else if constexpr (EPI == GEMV_EPI_SWIGLU) {
       const float g = v[i], u = v[i + 1];
       a.out[0][r] = (g / (1.0f + expf(-g))) * u;

@@ -605,3 +605,24 @@ def test_llama7b_layer_decode_matches_oracle():
     if n == 8:
         r = oracle.OracleLlama(cfg, ck).forward(list(prompt) + list(o), 0)
         assert np.max(np.abs(lg - r)) <= LOGIT_TOL
+
+
+@pytest.mark.parametrize("mix", ["q4_0", "q5_k_m"])
+def test_wide_rows_in_paired_epilogues_match_oracle(mix):
+    """dim 8448: the QKV and gate/up GEMVs read rows of 8192 < K <= 12288,
+    where the store and add launches run one row per lane; the RoPE and SwiGLU
+    epilogues take a lane's rows in pairs and keep two rows per lane."""
+    cfg = TINY_TEST.replace(dim=8448, hidden_dim=512, n_layers=1, n_heads=66, n_kv_heads=66, head_dim=128,
+                            context_length=32)
+    ck = synth.llama_checkpoint(cfg, seed=38, mix=mix)
+    prompt = synth.tokens(38, "prompt", 4, cfg.vocab_size)
+    announce(f"wide rows mix={mix}")
+    with HipLlamaModel(cfg, ck) as m:
+        m.forward(prompt, 0)
+        g = m.decode_greedy(4)
+        lg = m.get_logits()
+    o, margins = oracle.OracleLlama(cfg, ck).generate_greedy(list(prompt), 4)
+    n = compare_greedy(list(g), o, margins, f"wide rows mix={mix}, greedy 4")
+    if n == 4:
+        r = oracle.OracleLlama(cfg, ck).forward(list(prompt) + list(o), 0)
+        assert np.max(np.abs(lg - r)) <= LOGIT_TOL
