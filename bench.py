@@ -466,13 +466,14 @@ def main():
         kq["weights_GB"] = round(synth.checkpoint_bytes(ckk) / 1e9, 3)
         par[wk.name] = parity(wk.name, tk, lpk)
         del ckk
-        # the same shape and prompt in a Q3_K_M-style mix, every matrix read from
-        # its stored blocks: Q3_K attention and gate/up, Q4_K down, Q6_K head;
-        # no committed fixture for it (its parity is the GPU tests' at small shapes)
-        ck3 = synth.llama_checkpoint(wk.config, seed=wk.seed, mix="q3_k_m")
-        dt3, _, _ = decode_run(wk.config, ck3, wk.prompt(), wk.n_decode, 4)
-        kq["llama2_7b_q3_k_m_decode_tok_s"] = round(wk.n_decode / dt3, 1)
+        # the same shape in a Q3_K_M-style mix, every matrix read from its
+        # stored blocks: Q3_K attention and gate/up, Q4_K down, Q6_K head
+        w3 = WORKLOADS["llama2_7b_q3_k_m_decode"]
+        ck3 = w3.checkpoint()
+        dt3, t3, lp3 = decode_run(w3.config, ck3, w3.prompt(), w3.n_decode, 4)
+        kq["llama2_7b_q3_k_m_decode_tok_s"] = round(w3.n_decode / dt3, 1)
         kq["q3_k_m_weights_GB"] = round(synth.checkpoint_bytes(ck3) / 1e9, 3)
+        par[w3.name] = parity(w3.name, t3, lp3)
         del ck3
         log(f"  {json.dumps(kq)}")
     if args.only == "gemm_counters":

@@ -2,10 +2,6 @@
 
     lib/libchatnet_hip.so    HIP kernels + C ABI for gfx950 (hipcc)
     lib/libchatnet_synth.so  host-only synthetic weight generator (gcc)
-    lib/probe_chain_floor    stand-alone measurement of a dependent-kernel
-                             chain's floor in a HIP graph (not the library)
-    lib/probe_grid_handoff   stand-alone measurement of a grid-wide handoff
-                             inside one persistent kernel (not the library)
 
 Run as `python -m chatnet_amd.build_lib` or through __graft_entry__.build().
 """
@@ -23,7 +19,6 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIP_SOURCES = ["chatnet_api.hip", "gemv.hip", "gemv_float.hip", "gemm.hip", "prefill.hip", "decode_ops.hip", "sample.hip"]
 HIP_HEADERS = ["device_common.h", "gemv_common.h", "kernels.h"]
-PROBES = ["probe_chain_floor", "probe_grid_handoff", "probe_span_gemm"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -96,22 +91,8 @@ def build_synth(verbose: bool = False) -> str:
     return out
 
 
-def build_probe(name: str, verbose: bool = False) -> str:
-    hipcc = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
-    os.makedirs(LIBDIR, exist_ok=True)
-    out = os.path.join(LIBDIR, name)
-    tmp = out + ".tmp"
-    flags = [f for f in HIPCC_FLAGS if f not in ("-shared", "-fPIC", "-fvisibility=hidden")]
-    cmd = [hipcc, *flags, os.path.join(CSRC, name + ".hip"), "-o", tmp]
-    if verbose:
-        print(" ".join(cmd))
-    _run(cmd)
-    os.replace(tmp, out)
-    return out
-
-
 def build_all(verbose: bool = False) -> list[str]:
-    return [build_synth(verbose), build_hip(verbose)] + [build_probe(n, verbose) for n in PROBES]
+    return [build_synth(verbose), build_hip(verbose)]
 
 
 if __name__ == "__main__":

@@ -11,6 +11,7 @@
 // then the LM head (final RMSNorm fused) only for the last token of a span.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstdarg>
@@ -64,12 +65,17 @@ struct Layer {
   unsigned bias_have = 0;
 };
 
+// CU count per device ordinal, cached (threads may race to fill an entry; they
+// store the same value).
 int device_cus(int dev) {
-  static int cache[64] = {0};
-  if (dev >= 0 && dev < 64 && cache[dev]) return cache[dev];
+  static std::atomic<int> cache[64];
+  if (dev >= 0 && dev < 64) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c) return c;
+  }
   hipDeviceProp_t p;
   if (hipGetDeviceProperties(&p, dev) != hipSuccess) return 256;
-  if (dev >= 0 && dev < 64) cache[dev] = p.multiProcessorCount;
+  if (dev >= 0 && dev < 64) cache[dev].store(p.multiProcessorCount, std::memory_order_relaxed);
   return p.multiProcessorCount;
 }
 
@@ -99,7 +105,7 @@ const uint8_t* gemv_w(const DevTensor& t) {
 int embed_qt(const DevTensor& t) { return embed_raw_type(t.type) ? (int)t.type : kGemvPacked; }
 const void* embed_w(const DevTensor& t) { return embed_raw_type(t.type) ? t.ptr : t.pk; }
 
-// Workspace of chatnet_matmul's batched path (bf16 copy of x + K-split
+// Workspace of chatnet_matmul's batched path (fp16 copy of x + K-split
 // partials), one per (device, stream): work queued on one stream runs in
 // order, so calls sharing a stream can share it.  Grown on demand and kept
 // until the process ends; a buffer it outgrows is retired, not freed, because
@@ -198,7 +204,7 @@ struct chatnet_model {
   // up to span_cap tokens per pass.
   int span_cap = 0;
   float* sp_x = nullptr;       // [cap][dim] residual stream
-  // GEMM inputs as bf16 hi + lo planes (x = hi + lo to ~2^-17)
+  // GEMM inputs as fp16 hi + lo planes in the span order (x = hi + lo to ~2^-22)
   uint16_t* sp_xb = nullptr;   // [2][cap][dim]: normed x, then attention output
   uint16_t* sp_hb = nullptr;   // [2][cap][hidden]: silu(gate)*up
   float* sp_qkv = nullptr;     // [cap][dim + 2*kv_dim]
@@ -1059,7 +1065,7 @@ int run_prompt(chatnet_model* m, const int32_t* tokens, int n, int position) {
 }
 
 // chatnet_matmul and chatnet_matmul_noalloc: the same kernels; the batched
-// path's scratch (bf16 x, then the K-split partials) comes from the per-stream
+// path's scratch (fp16 x and its column scales, then the K-split partials) comes from the per-stream
 // workspace, or with `noalloc` from the fixed per-device scratch array.
 int matmul_impl(uint32_t type, const void* w_dev, const float* x_dev, float* y_dev, int M, int K, int N, void* stream,
                 bool noalloc) {
@@ -1095,8 +1101,10 @@ int matmul_impl(uint32_t type, const void* w_dev, const float* x_dev, float* y_d
   const bool pack = must_pack || (batched && !raw);
   const uint8_t* wp = (const uint8_t*)w_dev;
   if (batched || pack) {
-    // [bf16 x | K-split partials | packed W], the first two for the batched path only
-    const size_t xb_bytes = batched ? ((size_t)N * K * sizeof(uint16_t) + 255) & ~(size_t)255 : 0;
+    // [fp16 x | per-column x scales | K-split partials | packed W], the first three
+    // for the batched path only
+    const size_t xh_bytes = batched ? ((size_t)N * K * sizeof(uint16_t) + 255) & ~(size_t)255 : 0;
+    const size_t xb_bytes = batched ? xh_bytes + (((size_t)N * sizeof(float) + 255) & ~(size_t)255) : 0;
     const size_t part_bytes =
         batched ? (gemm_workspace_bytes(M, N, K, cus, false, pack) + 255) & ~(size_t)255 : 0;
     const size_t pack_bytes = pack ? gemm_pack_bytes(M, K) : 0;
@@ -1118,8 +1126,8 @@ int matmul_impl(uint32_t type, const void* w_dev, const float* x_dev, float* y_d
       wp = (const uint8_t*)(ws + xb_bytes + part_bytes);
     }
     if (batched) {
-      // x -> bf16 into the scratch, then the MFMA GEMM
-      HIP_TRY(to_bf16_launch(x_dev, (uint16_t*)ws, (size_t)N * K, st));
+      // x -> per-column scaled fp16 into the scratch, then the MFMA GEMM
+      HIP_TRY(to_f16_scaled_launch(x_dev, (uint16_t*)ws, (float*)(ws + xh_bytes), N, K, st));
       GemmArgs g;
       memset(&g, 0, sizeof(g));
       g.qtype = (int)type;
@@ -1131,6 +1139,7 @@ int matmul_impl(uint32_t type, const void* w_dev, const float* x_dev, float* y_d
       g.K = K;
       g.N = N;
       g.xb = (const uint16_t*)ws;
+      g.xinv = (const float*)(ws + xh_bytes);
       g.epi = GEMV_EPI_STORE;
       g.y = y_dev;
       g.ldy = M;

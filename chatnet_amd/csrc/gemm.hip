@@ -26,7 +26,6 @@
 
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // W rows of the virtual row `vr`: single matrix, three concatenated (q|k|v)
@@ -115,46 +114,8 @@ __device__ __forceinline__ void write_out4(const GemmArgs& a, int epi, int n, in
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-__device__ __forceinline__ f32x16 mma32(bf16x8 a, bf16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
 __device__ __forceinline__ f32x16 mma32(f16x8 a, f16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-}
-
-// One-plane kernel (chatnet_matmul, bf16 x): 16 weights d*(q-8) of one lane as
-// bf16, 8 per MFMA step (low nibbles of q0/q1 for the first, high nibbles for
-// the second).
-__device__ __forceinline__ void dequant_w16(uint32_t q0, uint32_t q1, float d, bf16x8 (&hi)[2]) {
-  const float nd = -8.0f * d;
-  uint32_t n[2][2] = {{q0 & 0x0F0F0F0Fu, q1 & 0x0F0F0F0Fu}, {(q0 >> 4) & 0x0F0F0F0Fu, (q1 >> 4) & 0x0F0F0F0Fu}};
-  // Opaque to the optimizer: without this it folds the masks into one
-  // bit-field extract per element instead of v_cvt_f32_ubyte{0..3}.
-  asm volatile("" : "+v"(n[0][0]), "+v"(n[0][1]), "+v"(n[1][0]), "+v"(n[1][1]));
-#pragma unroll
-  for (int s = 0; s < 2; s++) {
-    hi[s][0] = (__bf16)fmaf(cn_ubyte<0>(n[s][0]), d, nd);
-    hi[s][1] = (__bf16)fmaf(cn_ubyte<1>(n[s][0]), d, nd);
-    hi[s][2] = (__bf16)fmaf(cn_ubyte<2>(n[s][0]), d, nd);
-    hi[s][3] = (__bf16)fmaf(cn_ubyte<3>(n[s][0]), d, nd);
-    hi[s][4] = (__bf16)fmaf(cn_ubyte<0>(n[s][1]), d, nd);
-    hi[s][5] = (__bf16)fmaf(cn_ubyte<1>(n[s][1]), d, nd);
-    hi[s][6] = (__bf16)fmaf(cn_ubyte<2>(n[s][1]), d, nd);
-    hi[s][7] = (__bf16)fmaf(cn_ubyte<3>(n[s][1]), d, nd);
-  }
-}
-
-// One-plane kernel, packed units: 8 weights fmaf(code, sc, of) as bf16; the
-// codes are the bytes of c0 then c1.
-__device__ __forceinline__ void dequant_u8x8(uint32_t c0, uint32_t c1, float sc, float of, bf16x8& hi) {
-  hi[0] = (__bf16)fmaf(cn_ubyte<0>(c0), sc, of);
-  hi[1] = (__bf16)fmaf(cn_ubyte<1>(c0), sc, of);
-  hi[2] = (__bf16)fmaf(cn_ubyte<2>(c0), sc, of);
-  hi[3] = (__bf16)fmaf(cn_ubyte<3>(c0), sc, of);
-  hi[4] = (__bf16)fmaf(cn_ubyte<0>(c1), sc, of);
-  hi[5] = (__bf16)fmaf(cn_ubyte<1>(c1), sc, of);
-  hi[6] = (__bf16)fmaf(cn_ubyte<2>(c1), sc, of);
-  hi[7] = (__bf16)fmaf(cn_ubyte<3>(c1), sc, of);
 }
 
 // Exact-weight (span) kernel, raw Q4_0, fp16 operands.  One MFMA step of a
@@ -207,6 +168,38 @@ __device__ __forceinline__ void dequant_u8_f16(uint32_t ca, uint32_t cb, float s
   for (int t = 0; t < 4; t++) cn_split_f16x2(w[2 * t], w[2 * t + 1], hi[t], lo[t]);
   wa = __builtin_bit_cast(f16x8, make_uint4(hi[0], hi[1], hi[2], hi[3]));
   wb = __builtin_bit_cast(f16x8, make_uint4(lo[0], lo[1], lo[2], lo[3]));
+}
+
+// One-plane kernel (chatnet_matmul), raw Q4_0: the 8 weights of one MFMA step
+// as fp16(d * (q - 8)), one rounding each.  The nibble pairs of wp (bytes b0 b2
+// b1 b3 of a qs dword, as dequant_q4_f16 takes them) become q - 8 exactly as
+// there, and one packed fp16 multiply by d rounds each product once (|d| <
+// 8188 keeps every product finite).
+__device__ __forceinline__ f16x8 dequant_q4_h(uint32_t wp, uint32_t magic, cn_half2 d2) {
+  const uint32_t u = wp >> 8;
+  const cn_half2 t0 = __builtin_bit_cast(cn_half2, (wp & 0x000F000Fu) | magic);
+  const cn_half2 t1 = __builtin_bit_cast(cn_half2, (u & 0x000F000Fu) | magic);
+  const cn_half2 t2 = __builtin_bit_cast(cn_half2, (wp & 0x00F000F0u) | magic);
+  const cn_half2 t3 = __builtin_bit_cast(cn_half2, (u & 0x00F000F0u) | magic);
+  const cn_half2 m1032 = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+  const cn_half2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const cn_half2 m72 = {(_Float16)-72.0f, (_Float16)-72.0f};
+  const cn_half2 a0 = (t0 + m1032) * d2, a1 = (t1 + m1032) * d2;
+  const cn_half2 a2 = (t2 * s16 + m72) * d2, a3 = (t3 * s16 + m72) * d2;
+  return (f16x8){a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+}
+
+// One-plane kernel, packed units: the 8 weights of one MFMA step, codes of ca
+// with (sc0, of0) then codes of cb with (sc1, of1), each fmaf(code, sc, of) in
+// fp32 (the type's value) rounded once to fp16.
+__device__ __forceinline__ f16x8 dequant_u8_h(uint32_t ca, uint32_t cb, float sc0, float of0, float sc1, float of1) {
+  const cn_float2 w0 = {fmaf(cn_ubyte<0>(ca), sc0, of0), fmaf(cn_ubyte<1>(ca), sc0, of0)};
+  const cn_float2 w1 = {fmaf(cn_ubyte<2>(ca), sc0, of0), fmaf(cn_ubyte<3>(ca), sc0, of0)};
+  const cn_float2 w2 = {fmaf(cn_ubyte<0>(cb), sc1, of1), fmaf(cn_ubyte<1>(cb), sc1, of1)};
+  const cn_float2 w3 = {fmaf(cn_ubyte<2>(cb), sc1, of1), fmaf(cn_ubyte<3>(cb), sc1, of1)};
+  const cn_half2 h0 = __builtin_convertvector(w0, cn_half2), h1 = __builtin_convertvector(w1, cn_half2);
+  const cn_half2 h2 = __builtin_convertvector(w2, cn_half2), h3 = __builtin_convertvector(w3, cn_half2);
+  return (f16x8){h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
 }
 
 // ---------------------------------------------------------------------------
@@ -366,10 +359,12 @@ struct TileIO {
 #pragma unroll
     for (int cc = 0; cc < TN; cc++) {
       const int n = n0 + 32 * cc + li;
+      // one-plane kernel: x of column n was scaled by 1 / xinv[n] (a power of two)
+      const float sc = a.xinv ? a.xinv[n < a.N ? n : a.N - 1] : 1.0f;
 #pragma unroll
       for (int v4 = 0; v4 < 4; v4++) {
         const int m = m0 + wave * 32 + 8 * v4 + 4 * h;
-        const f32x4 v = {acc[cc][4 * v4], acc[cc][4 * v4 + 1], acc[cc][4 * v4 + 2], acc[cc][4 * v4 + 3]};
+        const f32x4 v = f32x4{acc[cc][4 * v4], acc[cc][4 * v4 + 1], acc[cc][4 * v4 + 2], acc[cc][4 * v4 + 3]} * sc;
         if (a.splits > 1) {
           if (n < a.N && m < a.M) {
             float* p = a.part + ((size_t)ks * a.N + n) * a.M + m;
@@ -385,12 +380,15 @@ struct TileIO {
   }
 };
 
-// One-plane kernel (chatnet_matmul: bf16 x in natural order).  An S-stage
-// ring with S-1 chunks in flight; each chunk's W is dequantized during the
-// previous chunk's MFMAs.  Q4_0: lane half h of row li takes block h of the
-// unit, and MFMA step s the low (s < 2) or high nibbles of qs[8(s&1) .. +7],
-// i.e. k = 32h + 8s .. +7 of the chunk, the same 8 k its x fragment reads.
-// Packed: step s takes codes 32h + 8s .. +7.
+// One-plane kernel (chatnet_matmul): x as one fp16 plane in the cn_span_pos
+// order, each column scaled by a power of two (to_f16_scaled_launch) that
+// store() undoes.  The ring and the step order are the span kernel's (below):
+// at the start of chunk c every wave has landed its part of the chunk and
+// finished chunk c-1, chunk c+S-1 is issued into the freed stage, and each
+// step's 8 weights are dequantized into one fp16 operand just ahead of its
+// TN MFMAs (one v_mfma_f32_32x32x16_f16 per column tile).  Step s of lane
+// half h: Q4_0 qs dword s of block h; packed codes 32h + 4s .. +3 and
+// 32h + 16 + 4s .. +3 with the scale/offset pairs 2h and 2h+1.
 template <int TN, int S, bool PK>
 __global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
   using C = PipeCfg<false, TN, S, PK>;
@@ -404,90 +402,48 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
 #pragma unroll
     for (int v = 0; v < 16; v++) acc[cc][v] = 0.f;
 
+  const uint32_t psel = h ? 0x03010200u : 0x05030402u;
+  uint32_t magic = 0x64006400u;
+  asm volatile("" : "+v"(magic));
+
   const int c_begin = io.c_begin, c_end = io.c_end;
   if (c_begin < c_end) {
     auto slot_of = [&](int c) { return lds + ((c - c_begin) % S) * C::STAGE; };
-    // Q4_0: half 0 gives steps 0 and 2 (low/high nibbles of qs[0..7]), half 1
-    // steps 1 and 3.  Packed: half 0 gives steps 0 and 1 (codes 0..15 of the
-    // lane, scale 2h), half 1 steps 2 and 3 (codes 16..31, scale 2h+1).
-    auto deq_half = [&](const uint32_t (&w)[C::WD], int half, bf16x8 (&fh)[4]) {
-      if constexpr (PK) {
-        const float sc = __uint_as_float(w[8 + half]), of = __uint_as_float(w[10 + half]);
-#pragma unroll
-        for (int t = 0; t < 2; t++) dequant_u8x8(w[4 * half + 2 * t], w[4 * half + 2 * t + 1], sc, of, fh[2 * half + t]);
-      } else {
-        const uint32_t sh = h ? 0u : 2u;
-        const float d = cn_h2f(h ? (w[4] >> 16) : w[0]);
-        const uint32_t qa = __builtin_amdgcn_alignbyte(half ? w[3] : w[1], half ? w[2] : w[0], sh);
-        const uint32_t qb = __builtin_amdgcn_alignbyte(half ? w[4] : w[2], half ? w[3] : w[1], sh);
-        bf16x8 th[2];
-        dequant_w16(qa, qb, d, th);
-        fh[half] = th[0];
-        fh[half + 2] = th[1];
-      }
-    };
-    // Waits until stage t has landed, given that stages up to `issued` are in flight.
-    auto wait_stage = [&](int t, int issued) {
-      const int later = issued - t;
-      if constexpr (S >= 4) {
-        if (later >= 2) vm_wait<2 * C::VPS>();
-        else if (later == 1) vm_wait<C::VPS>();
-        else vm_wait<0>();
-      } else {
-        if (later >= 1) vm_wait<C::VPS>();
-        else vm_wait<0>();
-      }
-    };
-
-    int issued = c_begin - 1;
 #pragma unroll
     for (int i = 0; i < S - 1; i++)
-      if (c_begin + i < c_end) {
-        io.issue(c_begin + i, lds + i * C::STAGE);
-        issued = c_begin + i;
-      }
-    wait_stage(c_begin, issued);
-    wg_barrier();
-    bf16x8 wh[4];
-    {
-      uint32_t w[C::WD];
-      io.wraw(slot_of(c_begin), w);
-      deq_half(w, 0, wh);
-      deq_half(w, 1, wh);
-    }
-
+      if (c_begin + i < c_end) io.issue(c_begin + i, lds + i * C::STAGE);
     for (int c = c_begin; c < c_end; c++) {
-      const bool has_next = c + 1 < c_end;
-      // Stage c+1 (whose W is dequantized during this chunk) must have landed,
-      // and every wave must be done with chunk c-1 before its slot is reused.
-      wait_stage(has_next ? c + 1 : c, issued);
+      char* st = slot_of(c);
+      if (S >= 3 && c + 1 < c_end) vm_wait<C::VPS>();
+      else vm_wait<0>();
       wg_barrier();
-      if (c + S - 1 < c_end) {
-        io.issue(c + S - 1, slot_of(c + S - 1));
-        issued = c + S - 1;
+      if (c + S - 1 < c_end) io.issue(c + S - 1, slot_of(c + S - 1));
+      uint32_t w[C::WD];
+      io.wraw(st, w);
+      cn_half2 d2 = {};
+      if constexpr (!PK) {
+        const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(h ? (w[4] >> 16) : (w[0] & 0xFFFFu)));
+        d2 = (cn_half2){d, d};
       }
-      // Unconditional (branch-free, so it interleaves with the MFMAs): on the
-      // last chunk this reads a stale slot whose result is never used.
-      uint32_t nw[C::WD];
-      io.wraw(slot_of(c + 1), nw);
-      bf16x8 nwh[4];
-
-      const char* st = slot_of(c);
-      bf16x8 xh[2][TN];
+      f16x8 xh[2][TN];
       auto load_x = [&](int s, int b) {
 #pragma unroll
-        for (int cc = 0; cc < TN; cc++) xh[b][cc] = __builtin_bit_cast(bf16x8, io.xfrag(st, 0, s, cc));
+        for (int cc = 0; cc < TN; cc++) xh[b][cc] = __builtin_bit_cast(f16x8, io.xfrag(st, 0, s, cc));
       };
       load_x(0, 0);
 #pragma unroll
       for (int s = 0; s < 4; s++) {
-        if (s < 3) load_x(s + 1, (s + 1) & 1);  // next step's fragments in flight during this step
+        if (s < 3) load_x(s + 1, (s + 1) & 1);
+        f16x8 wa;
+        if constexpr (PK) {
+          wa = dequant_u8_h(w[s], w[4 + s], __uint_as_float(w[8]), __uint_as_float(w[10]), __uint_as_float(w[9]),
+                            __uint_as_float(w[11]));
+        } else {
+          wa = dequant_q4_h(__builtin_amdgcn_perm(w[s + 1], w[s], psel), magic, d2);
+        }
 #pragma unroll
-        for (int cc = 0; cc < TN; cc++) acc[cc] = mma32(wh[s], xh[s & 1][cc], acc[cc]);
-        if (s == 0 || s == 2) deq_half(nw, s >> 1, nwh);
+        for (int cc = 0; cc < TN; cc++) acc[cc] = mma32(wa, xh[s & 1][cc], acc[cc]);
       }
-#pragma unroll
-      for (int s = 0; s < 4; s++) wh[s] = nwh[s];
     }
   }
   io.template store<TN>(a, acc);
@@ -601,18 +557,47 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_reduce_kernel(GemmArgs a) {
   write_out4(a, a.epi, n, m, s);
 }
 
-// fp32 -> bf16 (round to nearest even), 4 elements per thread.
-__global__ __launch_bounds__(CN_BLOCK) void to_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ xb,
-                                                          size_t n) {
-  const size_t i = ((size_t)blockIdx.x * CN_BLOCK + threadIdx.x) * 4;
-  if (i + 3 < n) {
-    const float4 v = *reinterpret_cast<const float4*>(x + i);
-    uint2 o;
-    o.x = pack2_bf16(v.x, v.y);
-    o.y = pack2_bf16(v.z, v.w);
-    *reinterpret_cast<uint2*>(xb + i) = o;
-  } else {
-    for (size_t j = i; j < n; j++) xb[j] = __builtin_bit_cast(uint16_t, (__bf16)x[j]);
+// x [N][K] fp32 -> the one-plane kernel's input: per column n a power of two
+// 2^e_n that brings max|x[n]| into [2^14, 2^15) (so every element stays
+// inside fp16's range and as far above its subnormals as the column allows;
+// e_n in [-125, 125]; 0 for a column that is all zero or holds an infinity),
+// xh[n][cn_span_pos(k)] = fp16(x[n][k] * 2^e_n) (the scaling is exact, one
+// rounding to nearest even) and xinv[n] = 2^-e_n.  One workgroup per column,
+// the column held in registers between the max and the conversion.
+template <int V>
+__global__ __launch_bounds__(CN_BLOCK) void to_f16_scaled_kernel(const float* __restrict__ x,
+                                                                uint16_t* __restrict__ xh,
+                                                                float* __restrict__ xinv, int K) {
+  __shared__ float red[4];
+  const size_t n = blockIdx.x;
+  const float* xr = x + n * K;
+  f32x4 v[V];
+  float mx = 0.f;
+#pragma unroll
+  for (int j = 0; j < V; j++) {
+    const int i = (threadIdx.x + CN_BLOCK * j) * 4;
+    v[j] = i < K ? *reinterpret_cast<const f32x4*>(xr + i) : f32x4{0.f, 0.f, 0.f, 0.f};
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[j][0]), fabsf(v[j][1])), fmaxf(fabsf(v[j][2]), fabsf(v[j][3]))));
+  }
+  mx = cn_block_max(mx, red);
+  int e = 0;
+  if (mx > 0.f && mx <= 3.402823466e38f) {
+    int E;
+    (void)frexpf(mx, &E);  // mx = f * 2^E, f in [0.5, 1)
+    e = min(125, max(-125, 15 - E));
+  }
+  if (threadIdx.x == 0) xinv[n] = ldexpf(1.0f, -e);
+  const float sc = ldexpf(1.0f, e);
+  uint16_t* o = xh + n * K;
+#pragma unroll
+  for (int j = 0; j < V; j++) {
+    const int i = (threadIdx.x + CN_BLOCK * j) * 4;
+    if (i >= K) continue;
+    const f32x4 y = v[j] * sc;  // 2^e is a normal float for e in [-125, 125]
+    const cn_half2 a = __builtin_convertvector((cn_float2){y[0], y[1]}, cn_half2);
+    const cn_half2 b = __builtin_convertvector((cn_float2){y[2], y[3]}, cn_half2);
+    *reinterpret_cast<uint2*>(o + cn_span_pos(i)) =
+        make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
   }
 }
 
@@ -1043,24 +1028,15 @@ GemmShape pick_gemm(int M, int N, int K, int num_cus, bool precise, bool packed)
   return s;
 }
 
-// Dynamic LDS above 64 KB must be allowed per kernel; every caller sets the
-// same value, so a race on the flag is harmless.
-template <class F>
-hipError_t allow_lds(F* kernel, int bytes, bool& done) {
-  if (done || bytes <= 64 * 1024) return hipSuccess;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     bytes);
-  if (e == hipSuccess) done = true;
-  return e;
-}
-
 template <int TN, bool PK>
 hipError_t launch_p(const GemmArgs& a, int grid, hipStream_t st) {
   constexpr int lds = PipeCfg<false, TN, kStages, PK>::LDS;
   static_assert(lds <= 160 * 1024, "LDS ring exceeds the CU's 160 KB");
-  static bool attr_set = false;
-  hipError_t e = allow_lds(&gemm_p_kernel<TN, kStages, PK>, lds, attr_set);
-  if (e != hipSuccess) return e;
+  static std::atomic<uint64_t> lds_done{0};
+  if (lds > 64 * 1024) {
+    const hipError_t e = allow_full_lds(reinterpret_cast<const void*>(&gemm_p_kernel<TN, kStages, PK>), lds_done);
+    if (e != hipSuccess) return e;
+  }
   hipLaunchKernelGGL((gemm_p_kernel<TN, kStages, PK>), dim3(grid), dim3(CN_BLOCK), lds, st, a);
   return hipGetLastError();
 }
@@ -1069,9 +1045,11 @@ template <int TN, int S, bool PK>
 hipError_t launch_s(const GemmArgs& a, int grid, hipStream_t st) {
   constexpr int lds = PipeCfg<true, TN, S, PK>::LDS;
   static_assert(lds <= 160 * 1024, "LDS ring exceeds the CU's 160 KB");
-  static bool attr_set = false;
-  hipError_t e = allow_lds(&gemm_s_kernel<TN, S, PK>, lds, attr_set);
-  if (e != hipSuccess) return e;
+  static std::atomic<uint64_t> lds_done{0};
+  if (lds > 64 * 1024) {
+    const hipError_t e = allow_full_lds(reinterpret_cast<const void*>(&gemm_s_kernel<TN, S, PK>), lds_done);
+    if (e != hipSuccess) return e;
+  }
   hipLaunchKernelGGL((gemm_s_kernel<TN, S, PK>), dim3(grid), dim3(CN_BLOCK), lds, st, a);
   return hipGetLastError();
 }
@@ -1171,10 +1149,14 @@ hipError_t gemm_launch(const GemmArgs& a_in, int num_cus, hipStream_t st, int* s
   return hipGetLastError();
 }
 
-hipError_t to_bf16_launch(const float* x, uint16_t* xb, size_t n, hipStream_t st) {
-  const size_t threads = (n + 3) / 4;
-  hipLaunchKernelGGL(to_bf16_kernel, dim3((unsigned)((threads + CN_BLOCK - 1) / CN_BLOCK)), dim3(CN_BLOCK), 0, st,
-                     x, xb, n);
+hipError_t to_f16_scaled_launch(const float* x, uint16_t* xh, float* xinv, int N, int K, hipStream_t st) {
+  if (N <= 0 || K <= 0 || K % 32 || K > 16384) return hipErrorInvalidValue;
+  const int v = (K + 4 * CN_BLOCK - 1) / (4 * CN_BLOCK);  // float4 per thread
+  const dim3 grid(N), block(CN_BLOCK);
+  if (v <= 2) hipLaunchKernelGGL((to_f16_scaled_kernel<2>), grid, block, 0, st, x, xh, xinv, K);
+  else if (v <= 4) hipLaunchKernelGGL((to_f16_scaled_kernel<4>), grid, block, 0, st, x, xh, xinv, K);
+  else if (v <= 8) hipLaunchKernelGGL((to_f16_scaled_kernel<8>), grid, block, 0, st, x, xh, xinv, K);
+  else hipLaunchKernelGGL((to_f16_scaled_kernel<16>), grid, block, 0, st, x, xh, xinv, K);
   return hipGetLastError();
 }
 

@@ -1100,13 +1100,9 @@ hipError_t launch_cols_k(const GemvArgs& a, int ncols, int num_cus, hipStream_t 
   constexpr int BS = 512, RW = RPW * (CN_WAVE / LPR);
   const size_t smem = ((size_t)NC * (a.K / 64) * XD_UNIT_DW + 16) * sizeof(float);
   const auto kern = &gemv_cols_kernel<NC, RPW, LPR, NU, BS>;
-  static bool lds_set = false;  // every caller sets the same maximum
-  if (!lds_set) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (e != hipSuccess) return e;
-    lds_set = true;
-  }
+  static std::atomic<uint64_t> lds_done{0};
+  const hipError_t e = allow_full_lds(reinterpret_cast<const void*>(kern), lds_done);
+  if (e != hipSuccess) return e;
   const int per_cu = (int)((160 * 1024) / smem) < 2 ? 1 : 2;
   const int waves = (a.n_vrows + RW - 1) / RW;
   int grid = (waves + BS / CN_WAVE - 1) / (BS / CN_WAVE);
@@ -1270,18 +1266,14 @@ GemvShape pick_shape(int K, int n_vrows, int num_cus, bool allow8, bool isolated
 
 // One instantiation's launch.  The base-256 digit records of rows longer than
 // 15872 take more than 64 KB of LDS, which must be allowed explicitly (once
-// per kernel).
+// per kernel and device, for the CU's whole LDS).
 template <int QT, int RPW, int LPR, int NU, int EPI, int BS>
 hipError_t launch_one(const GemvArgs& a, int grid, size_t smem, hipStream_t st) {
   const auto kern = &gemv_kernel<QT, RPW, LPR, NU, EPI, BS>;
   if (smem > 65536) {
-    static bool lds_set = false;
-    if (!lds_set) {
-      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-      if (e != hipSuccess) return e;
-      lds_set = true;
-    }
+    static std::atomic<uint64_t> lds_done{0};
+    const hipError_t e = allow_full_lds(reinterpret_cast<const void*>(kern), lds_done);
+    if (e != hipSuccess) return e;
   }
   hipLaunchKernelGGL(kern, dim3(grid), dim3(BS), smem, st, a);
   return hipGetLastError();

@@ -282,14 +282,10 @@ hipError_t launch_pk(const GemvArgs& a, int num_cus, hipStream_t st) {
   constexpr int RPW = 2;
   const size_t smem = gemv_pk_smem(a.K);
   const auto kern = &gemv_pk_kernel<RPW, EPI>;
-  if (smem > 65536) {  // more than 64 KB of dynamic LDS must be allowed explicitly (once)
-    static bool lds_set = false;
-    if (!lds_set) {
-      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-      if (e != hipSuccess) return e;
-      lds_set = true;
-    }
+  if (smem > 65536) {  // more than 64 KB of dynamic LDS must be allowed (once per device)
+    static std::atomic<uint64_t> lds_done{0};
+    const hipError_t e = allow_full_lds(reinterpret_cast<const void*>(kern), lds_done);
+    if (e != hipSuccess) return e;
   }
   const int n_iters = (a.n_vrows + RPW - 1) / RPW;
   int grid = (n_iters + 3) / 4;
@@ -303,14 +299,10 @@ hipError_t launch_wt(const GemvArgs& a, int num_cus, hipStream_t st) {
   constexpr int RPW = 2, U = 4;
   const size_t smem = gemv_f_smem(a.K);
   const auto kern = &gemv_f_kernel<WT, RPW, EPI, U>;
-  if (smem > 65536) {  // more than 64 KB of dynamic LDS must be allowed explicitly (once)
-    static bool lds_set = false;
-    if (!lds_set) {
-      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-      if (e != hipSuccess) return e;
-      lds_set = true;
-    }
+  if (smem > 65536) {  // more than 64 KB of dynamic LDS must be allowed (once per device)
+    static std::atomic<uint64_t> lds_done{0};
+    const hipError_t e = allow_full_lds(reinterpret_cast<const void*>(kern), lds_done);
+    if (e != hipSuccess) return e;
   }
   const int n_iters = (a.n_vrows + RPW - 1) / RPW;
   int grid = (n_iters + 3) / 4;

@@ -5,6 +5,26 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <atomic>
+
+// A kernel may use more than 64 KB of dynamic LDS only after its maximum was
+// raised, per device.  allow_full_lds raises it to the CU's whole 160 KB (so
+// every later launch of the kernel fits, whatever its size) the first time a
+// device launches the kernel; `done` holds one bit per device ordinal < 64
+// (higher ordinals set the attribute on every call).  Concurrent first calls
+// both set the same value.
+constexpr int kCuLdsBytes = 160 * 1024;
+inline hipError_t allow_full_lds(const void* kern, std::atomic<uint64_t>& done) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = dev >= 0 && dev < 64 ? 1ull << dev : 0;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+  e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, kCuLdsBytes);
+  if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_acq_rel);
+  return e;
+}
+
 // STORE and LOGITS write y = W x; LOGITS is the LM-head instance (a separate
 // kernel so its launches are told apart from stand-alone GEMVs in profiles).
 // GEMV_EPI_ADD_MERGE: GEMV_EPI_ADD whose x is the decode attention's output,
@@ -77,8 +97,10 @@ struct GemmArgs {
   int seg_rows[3];
   int seg_mode;
   int M, K, N;            // M = virtual rows
-  const uint16_t* xb;     // N x K, row stride K: bf16, or the fp16 high parts when precise
-  const uint16_t* xb_lo;  // precise: fp16 low parts, x = xb + xb_lo, both in the cn_span_pos order
+  const uint16_t* xb;     // N x K, row stride K, fp16 in the cn_span_pos order: one plane scaled per
+                          // column (one-plane kernel, to_f16_scaled_launch), or the high parts when precise
+  const uint16_t* xb_lo;  // precise: fp16 low parts, x = xb + xb_lo
+  const float* xinv;      // one-plane kernel: per-column 2^-e undoing the scale of xb (nullptr: 1)
   int precise;            // exact-weight two-plane kernel
   int epi;
   float* y;               // STORE / ADD target
@@ -105,7 +127,10 @@ size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool precise, bool
 // the epilogue ran): the caller folds them into its next kernel
 // (add_rmsnorm_bf16_launch for a residual add).
 hipError_t gemm_launch(const GemmArgs& a, int num_cus, hipStream_t st, int* splits_left = nullptr);
-hipError_t to_bf16_launch(const float* x, uint16_t* xb, size_t n, hipStream_t st);
+// x [N][K] fp32 -> the one-plane GEMM's input: xh[n] = fp16(x[n] * 2^e_n) in
+// the cn_span_pos order, 2^e_n bringing max|x[n]| into [2^14, 2^15), and
+// xinv[n] = 2^-e_n.  K % 32 == 0, K <= 16384.
+hipError_t to_f16_scaled_launch(const float* x, uint16_t* xh, float* xinv, int N, int K, hipStream_t st);
 // xb = bf16(RMSNorm(x) * g) per row; with xb_lo the span GEMM's input instead
 // (fp16 hi + lo planes in the cn_span_pos order, dim % 32 == 0).
 hipError_t rmsnorm_bf16_launch(const float* x, const float* g, float eps, uint16_t* xb, uint16_t* xb_lo, int rows,

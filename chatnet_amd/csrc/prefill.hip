@@ -425,13 +425,9 @@ template <int HD, bool F16>
 hipError_t attn_prefill_t(const PrefillAttnArgs& a, hipStream_t st) {
   const int QB = 64 / a.kv_mul;
   const dim3 grid(a.n_heads / a.kv_mul, (a.n + QB - 1) / QB);
-  static bool lds_set = false;  // > 64 KB of dynamic LDS must be allowed explicitly
-  if (!lds_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_prefill_kernel<HD, F16>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)prefill_lds_bytes<HD>());
-    if (e != hipSuccess) return e;
-    lds_set = true;
-  }
+  static std::atomic<uint64_t> lds_done{0};  // > 64 KB of dynamic LDS must be allowed (once per device)
+  const hipError_t e = allow_full_lds(reinterpret_cast<const void*>(&attn_prefill_kernel<HD, F16>), lds_done);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((attn_prefill_kernel<HD, F16>), grid, dim3(kSpanThreads), prefill_lds_bytes<HD>(), st, a);
   return hipGetLastError();
 }

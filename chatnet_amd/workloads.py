@@ -13,6 +13,8 @@ chatnet_amd.synth, and the prompt of (seed, prompt_stream, n_prompt).
                             span, 256 greedy tokens, context 2048
     llama2_7b_q4_k_m_decode Llama-2-7B shape, Q4_K attention + gate/up, Q6_K
                             down + output, 16-token prompt, 64 greedy tokens
+    llama2_7b_q3_k_m_decode Llama-2-7B shape, Q3_K attention + gate/up, Q4_K
+                            down, Q6_K output, 16-token prompt, 64 greedy tokens
 """
 from __future__ import annotations
 
@@ -46,19 +48,20 @@ WORKLOADS = {w.name: w for w in (
     Workload("tinyllama_q4_0_prefill", TINYLLAMA_1B.replace(context_length=2048), 77, "q4_0", "prefill", 512, 128),
     Workload("llama2_7b_q4_0_decode", LLAMA2_7B.replace(context_length=2048), 7, "q4_0", "prompt", 128, 256),
     Workload("llama2_7b_q4_k_m_decode", LLAMA2_7B.replace(context_length=2048), 11, "q4_k_m", "prompt", 16, 64),
+    Workload("llama2_7b_q3_k_m_decode", LLAMA2_7B.replace(context_length=2048), 13, "q3_k_m", "prompt", 16, 64),
 )}
 
 
-def checkpoint_sample_digest(ck: dict, head: int = 1 << 16) -> str:
-    """SHA-256 over every tensor's name, byte count and first `head` bytes:
-    enough to tell whether a machine regenerates the same checkpoint, at a
-    fraction of the cost of hashing every byte."""
-    import hashlib
+def checkpoint_digest(ck: dict) -> str:
+    """XXH3-128 over every tensor's name, byte count and every byte, in name
+    order: tells whether a machine regenerates exactly the same checkpoint
+    (about 0.1 s per GB)."""
+    import xxhash
 
-    h = hashlib.sha256()
+    h = xxhash.xxh3_128()
     for name in sorted(ck):
         data = np.ascontiguousarray(ck[name].data).view(np.uint8).ravel()
         h.update(name.encode())
         h.update(str(data.size).encode())
-        h.update(data[:head].tobytes())
+        h.update(memoryview(data))
     return h.hexdigest()

@@ -154,11 +154,16 @@ CHATNET_API int chatnet_upload_tensor(chatnet_model* m, const char* name, uint32
  * (IModel.cs:18, LlamaModel.cs:93-238).  Processes tokens[0..n) at positions
  * position..position+n-1, writing their K/V into the cache; logits of the last
  * token stay on the device and are copied to `logits_host` (vocab_size
- * floats) when it is non-NULL.  Spans of 8 or more tokens (Q4_0 weights,
- * head_dim 64 or 128, n_heads/n_kv_heads dividing 64) run as batches of up
- * to 512 tokens: exact-weight MFMA
- * GEMMs over two-plane bf16 activations and causal attention over the cache;
- * shorter spans run token by token. */
+ * floats) when it is non-NULL.  Spans of 8 or more tokens run as batches of
+ * up to 512 tokens when head_dim is 64 or 128, n_heads / n_kv_heads is at
+ * most 64 and every projection matrix is of a block type (Q4_0 read from its
+ * stored blocks when all seven matrices of every layer are Q4_0; otherwise
+ * every matrix, of any block type but F32 / F16, re-encoded once into packed
+ * units kept for the model's lifetime): MFMA GEMMs on fp16 operands (each
+ * weight exact as two fp16 planes for Q4_0, ~22 bits for packed units;
+ * activations as fp16 hi + lo planes; three products per step) and causal
+ * attention over the cache.  Shorter spans, and models with F32 / F16
+ * projection matrices, run token by token. */
 CHATNET_API int chatnet_forward(chatnet_model* m, const int32_t* tokens, int n, int position,
                     float* logits_host);
 

@@ -46,6 +46,54 @@ def record_greedy(case: str, same: int, steps: int, forced: int = 0, min_margin:
     GREEDY_RECORDS.append((case, same, steps, forced, min_margin))
 
 
+def _continue(resume, prefix, k):
+    """The oracle's k greedy tokens (and margins) after the prompt + prefix."""
+    if callable(resume):
+        return resume(prefix, k)
+    import oracle
+
+    cfg, ck, prompt = resume
+    return oracle.OracleLlama(cfg, ck).generate_greedy(list(prompt) + list(prefix), k)
+
+
+def compare_greedy(gpu_tokens, ora_tokens, margins, case="greedy", resume=None):
+    """Compares the GPU's greedy tokens with the oracle's, every step.  A
+    difference fails unless the oracle's top-1/top-2 margin at that step is
+    below NEAR_TIE (either token is then a valid pick); the oracle is then
+    teacher-forced onto the GPU's pick: `resume` = (cfg, checkpoint, prompt)
+    regenerates the oracle's greedy continuation after the prompt and the
+    GPU's tokens so far (or a callable (prefix, k) -> (tokens, margins) does),
+    and the remaining steps are compared against it.
+    Returns the number of leading steps identical without forcing (callers
+    compare final logits only when that is every step).  The result is
+    recorded for the terminal summary either way."""
+    gpu = [int(t) for t in gpu_tokens]
+    exp = [int(t) for t in ora_tokens]
+    mar = [float(m) for m in margins[:len(exp)]]
+    first, forced, i = len(exp), 0, 0
+    while i < len(exp):
+        if i >= len(gpu):
+            break
+        if gpu[i] != exp[i]:
+            if not mar[i] < NEAR_TIE:
+                record_greedy(case, i, len(exp), forced, float(np.min(mar)))
+                raise AssertionError(f"{case}: {i}/{len(exp)} greedy tokens identical; step {i}: gpu {gpu[i]} vs "
+                                     f"oracle {exp[i]}, margin {mar[i]:.3g}")
+            assert resume is not None, f"{case}: near-tie at step {i} but no oracle continuation given"
+            print(f"[greedy] {case}: near-tie at step {i} (margin {mar[i]:.3g}), oracle teacher-forced", flush=True)
+            forced += 1
+            first = min(first, i)
+            rest, rm = [], []
+            if i + 1 < len(exp):
+                rest, rm = _continue(resume, gpu[:i + 1], len(exp) - i - 1)
+            exp = exp[:i] + [gpu[i]] + [int(t) for t in rest]
+            mar = mar[:i + 1] + [float(m) for m in rm[:len(rest)]]
+        i += 1
+    assert len(gpu) == len(exp), f"{case}: {len(gpu)} tokens, oracle {len(exp)}"
+    record_greedy(case, len(exp) - forced, len(exp), forced, float(np.min(mar)) if mar else float("nan"))
+    return first
+
+
 def greedy_against_expected(model, expected, margins, p0: int, case: str):
     """Runs the device greedy loop (chatnet_decode_greedy) after a forward of
     positions < p0 and compares every token with `expected` (the oracle's).

@@ -41,6 +41,17 @@ def run_case(qtype, M, K, seed=1):
     return err
 
 
+@pytest.mark.parametrize("qtype", [0, 1, 2, 8, 11, 12, 13, 14, 3, 23])
+def test_growing_k_past_64kb_of_lds_in_one_process(qtype):
+    """Rows of K > 15872 stage x in more than 64 KB of LDS, which a kernel may
+    use only once its maximum was raised.  The same type and epilogue at
+    K = 16128 and then K = 16384 (a larger staging area for the same kernel
+    instance) must both run and match the oracle.  Placed first in this file so
+    the K = 16128 launch is the instance's first above 64 KB in the process."""
+    for K in (16128, 16384):
+        run_case(qtype, 5, K, seed=23)
+
+
 @pytest.mark.parametrize("M,K", Q4_0_SHAPES)
 def test_q4_0_gemv_sweep_shapes(M, K):
     run_case(2, M, K)

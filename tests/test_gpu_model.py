@@ -10,7 +10,7 @@ import pytest
 import oracle
 from chatnet_amd import TINY_TEST, TINYLLAMA_1B, HipLlamaModel, _native, synth
 from chatnet_amd.engine import GreedySampler, generate
-from gpu_util import NEAR_TIE, announce, record_greedy
+from gpu_util import announce, compare_greedy
 
 pytestmark = pytest.mark.gpu
 
@@ -22,25 +22,6 @@ def _threads():
     oracle.set_threads(16)
     yield
     oracle.set_threads(1)
-
-
-def compare_greedy(gpu_tokens, ora_tokens, margins, case="greedy"):
-    """Number of leading greedy tokens the GPU and the oracle agree on.  A
-    difference fails unless the oracle's top-1/top-2 margin at that step is
-    below NEAR_TIE (then either token is a valid pick and the sequences part
-    there); the result is recorded for the terminal summary either way."""
-    n = len(ora_tokens)
-    assert len(gpu_tokens) == n, f"{case}: {len(gpu_tokens)} tokens, oracle {n}"
-    mm = float(np.min(margins[:n])) if n else float("nan")
-    for i, (g, o) in enumerate(zip(gpu_tokens, ora_tokens)):
-        if g != o:
-            record_greedy(case, i, n, 0, mm)
-            assert margins[i] < NEAR_TIE, \
-                f"{case}: {i}/{n} greedy tokens identical; step {i}: gpu {g} vs oracle {o}, margin {margins[i]:.3g}"
-            print(f"[greedy] {case}: {i}/{n} identical, near-tie at step {i} (margin {margins[i]:.3g})", flush=True)
-            return i
-    record_greedy(case, n, n, 0, mm)
-    return n
 
 
 @pytest.mark.parametrize("mix,kv", [("q4_0", _native.KV_F32), ("q4_k_m", _native.KV_F32),
@@ -98,7 +79,7 @@ def test_qwen2_span_and_greedy_match_oracle():
     r2 = ora.forward(toks[40:], 40)
     assert np.max(np.abs(g - r)) <= LOGIT_TOL and np.max(np.abs(g2 - r2)) <= LOGIT_TOL
     o, margins = oracle.OracleLlama(cfg, ck).generate_greedy(list(toks), 32)
-    compare_greedy(gt, o, margins, "qwen2 span 40+8, greedy 32")
+    compare_greedy(gt, o, margins, "qwen2 span 40+8, greedy 32", resume=(cfg, ck, list(toks)))
 
 
 def test_qwen2_iq3_s_rows_keep_the_file_order():
@@ -196,7 +177,7 @@ def test_weight_and_embedding_types_match_oracle(mix, emb, tied):
             assert np.max(np.abs(g - r)) <= LOGIT_TOL, (pos, float(np.max(np.abs(g - r))))
         gt = list(m.decode_greedy(16))
     o, margins = oracle.OracleLlama(cfg, ck).generate_greedy(list(toks), 16)
-    compare_greedy(gt, o, margins, f"types mix={mix} embedding={emb} tied={tied}")
+    compare_greedy(gt, o, margins, f"types mix={mix} embedding={emb} tied={tied}", resume=(cfg, ck, list(toks)))
 
 
 @pytest.mark.parametrize("tie_rows,nan_rows,expect,vocab", [
@@ -262,7 +243,7 @@ def test_eos_stops_before_forwarding_and_a_continued_decode_resumes():
     r = oracle.OracleLlama(cfg, ck).forward(list(prompt) + full[:k], 0)
     assert np.max(np.abs(lg - r)) <= LOGIT_TOL
     o, margins = oracle.OracleLlama(cfg, ck).generate_greedy(list(prompt), 30)
-    compare_greedy(full, o[:30], margins, "eos run, uninterrupted 6+30")
+    compare_greedy(full, o[:30], margins, "eos run, uninterrupted 6+30", resume=(cfg, ck, list(prompt)))
 
 
 @pytest.mark.parametrize("n_prompt,expect_len", [(12, 1), (11, 1), (10, 2), (4, 8)])
@@ -278,7 +259,7 @@ def test_prompt_filling_the_context(n_prompt, expect_len):
         h = generate(m, prompt, 5 if n_prompt > 4 else 100, GreedySampler())
     assert len(g) == expect_len and list(h) == g
     o, margins = oracle.OracleLlama(cfg, ck).generate_greedy(list(prompt), 5 if n_prompt > 4 else 100)
-    compare_greedy(g, o, margins, f"context fill {n_prompt}/12")
+    compare_greedy(g, o, margins, f"context fill {n_prompt}/12", resume=(cfg, ck, list(prompt)))
 
 
 def test_span_forward_matches_oracle_span():
@@ -306,7 +287,7 @@ def test_tiny_greedy_generation_matches_oracle():
         # the host loop over IModel.Forward gives the same tokens as the device loop
         h = generate(m, prompt, 32, GreedySampler())
     o, margins = oracle.OracleLlama(cfg, ck).generate_greedy(list(prompt), 32)
-    compare_greedy(list(g), o, margins, "tiny greedy 8+32")
+    compare_greedy(list(g), o, margins, "tiny greedy 8+32", resume=(cfg, ck, list(prompt)))
     assert list(g) == list(h)
 
 
@@ -358,7 +339,7 @@ def test_tinyllama_q4_0_greedy_32_steps_match_oracle():
         g = m.generate_greedy(prompt, 32)
         logits_g = m.get_logits()
     o, margins = oracle.OracleLlama(cfg, ck).generate_greedy(list(prompt), 32)
-    n = compare_greedy(list(g), o, margins, "tinyllama 16+32 (live oracle)")
+    n = compare_greedy(list(g), o, margins, "tinyllama 16+32 (live oracle)", resume=(cfg, ck, list(prompt)))
     print(f"tinyllama: {n}/32 greedy tokens identical; min margin {min(margins):.3g}", flush=True)
     if n == 32:
         # the last decode step forwarded token 32 at position 16+31; compare its logits
@@ -465,7 +446,7 @@ def test_span_longer_than_batch_cap_matches_oracle_and_token_schedule(monkeypatc
     assert np.max(np.abs(g - r)) <= LOGIT_TOL
     assert np.max(np.abs(h - r)) <= LOGIT_TOL
     o, margins = oracle.OracleLlama(cfg, ck).generate_greedy(list(toks), 16)
-    compare_greedy(list(gt), o, margins, "span 600 tokens, greedy 16")
+    compare_greedy(list(gt), o, margins, "span 600 tokens, greedy 16", resume=(cfg, ck, list(toks)))
 
 
 @pytest.mark.parametrize("mix", ["q4_k_m", "q5_k_m", "q8_0", "q6_k", "q4_k", "mixed_blocks", "legacy_blocks",
@@ -528,7 +509,7 @@ def test_long_context_decode_attention_matches_oracle():
         gt = m.decode_greedy(8)
         logits_g = m.get_logits()
     o, margins = oracle.OracleLlama(cfg, ck).generate_greedy(list(toks), 8)
-    n = compare_greedy(list(gt), o, margins, "2000-token context, greedy 8")
+    n = compare_greedy(list(gt), o, margins, "2000-token context, greedy 8", resume=(cfg, ck, list(toks)))
     if n == 8:
         # the 8th decode step forwarded the 8th token at position 2007
         r = oracle.OracleLlama(cfg, ck).forward(list(toks) + list(o), 0)
@@ -560,7 +541,7 @@ def test_decode_attention_layouts_match_oracle(head_dim, n_heads, n_kv, kv):
         g = m.decode_greedy(80)
         logits_g = m.get_logits()
     o, margins = oracle.OracleLlama(cfg, ck).generate_greedy(list(prompt), 80)
-    n = compare_greedy(list(g), o, margins, f"decode attention hd={head_dim} heads={n_heads} kv={n_kv} kvtype={kv}")
+    n = compare_greedy(list(g), o, margins, f"decode attention hd={head_dim} heads={n_heads} kv={n_kv} kvtype={kv}", resume=(cfg, ck, list(prompt)))
     if n == 80:
         r = oracle.OracleLlama(cfg, ck).forward(list(prompt) + list(o), 0)
         tol = LOGIT_TOL if kv == _native.KV_F32 else 2 * LOGIT_TOL
@@ -581,7 +562,7 @@ def test_qwen2_0_5b_layer_decode_matches_oracle():
         g = m.decode_greedy(8)
         lg = m.get_logits()
     o, margins = oracle.OracleLlama(cfg, ck).generate_greedy(list(prompt), 8)
-    n = compare_greedy(list(g), o, margins, "qwen2-0.5b layer, greedy 8")
+    n = compare_greedy(list(g), o, margins, "qwen2-0.5b layer, greedy 8", resume=(cfg, ck, list(prompt)))
     if n == 8:
         r = oracle.OracleLlama(cfg, ck).forward(list(prompt) + list(o), 0)
         assert np.max(np.abs(lg - r)) <= LOGIT_TOL
@@ -601,7 +582,7 @@ def test_llama7b_layer_decode_matches_oracle():
         g = m.decode_greedy(8)
         lg = m.get_logits()
     o, margins = oracle.OracleLlama(cfg, ck).generate_greedy(list(prompt), 8)
-    n = compare_greedy(list(g), o, margins, "7b layer, greedy 8")
+    n = compare_greedy(list(g), o, margins, "7b layer, greedy 8", resume=(cfg, ck, list(prompt)))
     if n == 8:
         r = oracle.OracleLlama(cfg, ck).forward(list(prompt) + list(o), 0)
         assert np.max(np.abs(lg - r)) <= LOGIT_TOL
@@ -622,7 +603,7 @@ def test_wide_rows_in_paired_epilogues_match_oracle(mix):
         g = m.decode_greedy(4)
         lg = m.get_logits()
     o, margins = oracle.OracleLlama(cfg, ck).generate_greedy(list(prompt), 4)
-    n = compare_greedy(list(g), o, margins, f"wide rows mix={mix}, greedy 4")
+    n = compare_greedy(list(g), o, margins, f"wide rows mix={mix}, greedy 4", resume=(cfg, ck, list(prompt)))
     if n == 4:
         r = oracle.OracleLlama(cfg, ck).forward(list(prompt) + list(o), 0)
         assert np.max(np.abs(lg - r)) <= LOGIT_TOL

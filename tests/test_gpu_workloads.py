@@ -3,7 +3,7 @@ the oracle's committed expected outputs (tests/golden/workload_<name>.npz,
 written by tests/golden/make_workload_fixtures.py).
 
 For each workload: the checkpoint is regenerated from its seed on this
-machine (its sample digest must equal the fixture's), the prompt is forwarded
+machine (its digest of every byte must equal the fixture's), the prompt is forwarded
 as one chatnet_forward span (the batched MFMA path where the weight types
 allow it, token by token otherwise), then the device greedy loop runs every
 decode step of the workload.  Bars (LlamaModel.Forward, LlamaModel.cs:93-238;
@@ -21,7 +21,7 @@ import numpy as np
 import pytest
 
 from chatnet_amd import HipLlamaModel
-from chatnet_amd.workloads import WORKLOADS, checkpoint_sample_digest
+from chatnet_amd.workloads import WORKLOADS, checkpoint_digest
 from gpu_util import announce, greedy_against_expected
 
 pytestmark = pytest.mark.gpu
@@ -37,7 +37,7 @@ def test_workload_matches_oracle_fixture(name):
     fx = np.load(os.path.join(GOLDEN, f"workload_{name}.npz"))
     announce(f"workload {name}: regenerating the checkpoint")
     ck = w.checkpoint()
-    assert checkpoint_sample_digest(ck) == str(fx["digest"]), "this machine regenerates a different checkpoint"
+    assert checkpoint_digest(ck) == str(fx["digest"]), "this machine regenerates a different checkpoint"
     prompt = w.prompt()
     assert np.array_equal(prompt, fx["prompt"])
     announce(f"workload {name}: {w.n_prompt}-token prompt + {w.n_decode} greedy steps on the gpu")

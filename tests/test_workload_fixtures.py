@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle
-from chatnet_amd.workloads import WORKLOADS, checkpoint_sample_digest
+from chatnet_amd.workloads import WORKLOADS, checkpoint_digest
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
@@ -38,7 +38,7 @@ def test_oracle_reproduces_tinyllama_decode_fixture():
     w = WORKLOADS["tinyllama_q4_0_decode"]
     fx = load(w.name)
     ck = w.checkpoint()
-    assert checkpoint_sample_digest(ck) == str(fx["digest"])
+    assert checkpoint_digest(ck) == str(fx["digest"])
     oracle.set_threads(os.cpu_count() or 1)
     try:
         ora = oracle.OracleLlama(w.config, ck)
