@@ -223,10 +223,18 @@ __device__ __forceinline__ f16x8 dequant_u8_h(uint32_t ca, uint32_t cb, float sc
 // ---------------------------------------------------------------------------
 // 16 bytes from global memory straight into LDS: lane i of the wave writes
 // lds_wave_base + 16*i (lds_wave_base must be the same for the whole wave).
-// The builtin exists only for the device; the host pass sees an empty body.
+// Issued as inline assembly: the compiler treats its own LDS-DMA builtin as
+// a write to all of LDS and waits for every load in flight (vmcnt(0)) before
+// the next LDS read, which would drain the ring at every chunk; the kernels
+// instead wait for the chunk they read with vm_wait and a barrier.  The
+// compiler's own waits stay correct with these loads in flight (vector-memory
+// counters retire in order, so a wait for one of its loads can only wait
+// longer).
 __device__ __forceinline__ void lds_dma16(const void* g, void* lds_wave_base) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0, 0);
+  const uint32_t m = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_wave_base);
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(m) : "memory");
 #endif
 }
 
@@ -239,6 +247,40 @@ __device__ __forceinline__ void wg_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+}
+
+// LDS reads issued as inline assembly, so that the compiler neither sinks them
+// next to their first use nor waits for them itself: a chunk's reads are all
+// issued at its start and each step waits (lds_wait) only for the reads it
+// consumes.  LDS reads of one wave retire in order.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+__device__ __forceinline__ cn_u32x4 lds_read128(uint32_t addr) {
+  cn_u32x4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint2 lds_read64(uint32_t addr) {
+  uint2 v;
+  asm volatile("ds_read_b64 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t lds_read32(uint32_t addr) {
+  uint32_t v;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+// Waits until at most N of this wave's LDS reads are outstanding.  A value
+// read by lds_read* must pass through reg_fence after the wait that covers it,
+// so that its uses stay behind that wait.
+template <int N>
+__device__ __forceinline__ void lds_wait() {
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
+}
+template <class T>
+__device__ __forceinline__ void reg_fence(T& r) {
+  asm volatile("" : "+v"(r));
 }
 
 template <bool PRECISE, int TN, int S, bool PK>
@@ -346,6 +388,13 @@ struct TileIO {
     }
   }
 
+  // Where the 16-byte x fragment of MFMA step s, column tile cc, plane p lies.
+  __device__ __forceinline__ const char* xfrag_ptr(const char* st, int p, int s, int cc) const {
+    const int xrow = 32 * cc + li;
+    const int phys = (4 * h + s) ^ ((xrow >> 1) & 7);
+    return st + p * C::XB + xrow * 128 + phys * 16;
+  }
+
   // The 16-byte x fragment of MFMA step s, column tile cc, plane p.
   __device__ __forceinline__ uint4 xfrag(const char* st, int p, int s, int cc) const {
     const int xrow = 32 * cc + li;
@@ -390,7 +439,7 @@ struct TileIO {
 // half h: Q4_0 qs dword s of block h; packed codes 32h + 4s .. +3 and
 // 32h + 16 + 4s .. +3 with the scale/offset pairs 2h and 2h+1.
 template <int TN, int S, bool PK>
-__global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
+__global__ __launch_bounds__(CN_BLOCK) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_p_kernel(GemmArgs a) {
   using C = PipeCfg<false, TN, S, PK>;
   extern __shared__ __attribute__((aligned(16))) char lds[];
   const TileIO<C> io(a);
@@ -414,26 +463,69 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
       if (c_begin + i < c_end) io.issue(c_begin + i, lds + i * C::STAGE);
     for (int c = c_begin; c < c_end; c++) {
       char* st = slot_of(c);
-      if (S >= 3 && c + 1 < c_end) vm_wait<C::VPS>();
-      else vm_wait<0>();
+      // chunks c+1 .. c+S-2 may stay in flight
+      const int later = min(S - 2, c_end - 1 - c);
+      if constexpr (S >= 5) {
+        if (later >= 3) vm_wait<3 * C::VPS>();
+        else if (later == 2) vm_wait<2 * C::VPS>();
+        else if (later == 1) vm_wait<C::VPS>();
+        else vm_wait<0>();
+      } else if constexpr (S == 4) {
+        if (later >= 2) vm_wait<2 * C::VPS>();
+        else if (later == 1) vm_wait<C::VPS>();
+        else vm_wait<0>();
+      } else {
+        if (later >= 1) vm_wait<C::VPS>();
+        else vm_wait<0>();
+      }
       wg_barrier();
       if (c + S - 1 < c_end) io.issue(c + S - 1, slot_of(c + S - 1));
+      // the lane's W dwords (as wraw), then every x fragment of the chunk, all
+      // issued at once; step s waits for its own fragments only
       uint32_t w[C::WD];
-      io.wraw(st, w);
-      cn_half2 d2 = {};
-      if constexpr (!PK) {
-        const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(h ? (w[4] >> 16) : (w[0] & 0xFFFFu)));
-        d2 = (cn_half2){d, d};
+      {
+        const uint32_t wb = lds_addr(st + C::PL * C::XB + (io.wave * 32 + io.li) * C::WROW);
+        if constexpr (PK) {
+          const cn_u32x4 c0 = lds_read128(wb + 32 * h), c1 = lds_read128(wb + 32 * h + 16);
+          const uint2 sc = lds_read64(wb + 64 + 8 * h), of = lds_read64(wb + 80 + 8 * h);
+          w[0] = c0[0], w[1] = c0[1], w[2] = c0[2], w[3] = c0[3];
+          w[4] = c1[0], w[5] = c1[1], w[6] = c1[2], w[7] = c1[3];
+          w[8] = sc.x, w[9] = sc.y, w[10] = of.x, w[11] = of.y;
+        } else {
+          const cn_u32x4 q = lds_read128(wb + 32 * h);
+          const uint32_t t = lds_read32(wb + 16);
+          w[0] = q[0], w[1] = q[1], w[2] = q[2], w[3] = q[3], w[4] = t;
+        }
       }
-      f16x8 xh[2][TN];
-      auto load_x = [&](int s, int b) {
+      cn_u32x4 xr[4][TN];
 #pragma unroll
-        for (int cc = 0; cc < TN; cc++) xh[b][cc] = __builtin_bit_cast(f16x8, io.xfrag(st, 0, s, cc));
-      };
-      load_x(0, 0);
+      for (int s = 0; s < 4; s++)
+#pragma unroll
+        for (int cc = 0; cc < TN; cc++) xr[s][cc] = lds_read128(lds_addr(io.xfrag_ptr(st, 0, s, cc)));
 #pragma unroll
       for (int s = 0; s < 4; s++) {
-        if (s < 3) load_x(s + 1, (s + 1) & 1);
+        // reads issued after step s's fragments: those of steps s+1 .. 3
+        if (s == 0) {
+          lds_wait<(3 * TN > 15 ? 15 : 3 * TN)>();
+#pragma unroll
+          for (int i = 0; i < C::WD; i++) reg_fence(w[i]);
+        } else if (s == 1) {
+          lds_wait<2 * TN>();
+        } else if (s == 2) {
+          lds_wait<TN>();
+        } else {
+          lds_wait<0>();
+        }
+#pragma unroll
+        for (int cc = 0; cc < TN; cc++) reg_fence(xr[s][cc]);
+        cn_half2 d2 = {};
+        if constexpr (!PK) {
+          const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(h ? (w[4] >> 16) : (w[0] & 0xFFFFu)));
+          d2 = (cn_half2){d, d};
+        }
+        f16x8 xh[TN];
+#pragma unroll
+        for (int cc = 0; cc < TN; cc++) xh[cc] = __builtin_bit_cast(f16x8, xr[s][cc]);
         f16x8 wa;
         if constexpr (PK) {
           wa = dequant_u8_h(w[s], w[4 + s], __uint_as_float(w[8]), __uint_as_float(w[10]), __uint_as_float(w[9]),
@@ -442,7 +534,8 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_p_kernel(GemmArgs a) {
           wa = dequant_q4_h(__builtin_amdgcn_perm(w[s + 1], w[s], psel), magic, d2);
         }
 #pragma unroll
-        for (int cc = 0; cc < TN; cc++) acc[cc] = mma32(wa, xh[s & 1][cc], acc[cc]);
+        for (int cc = 0; cc < TN; cc++) acc[cc] = mma32(wa, xh[cc], acc[cc]);
+        __builtin_amdgcn_sched_barrier(0);  // the next step's wait stays behind these MFMAs
       }
     }
   }
@@ -979,10 +1072,8 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_pack_kernel(int qtype, const ui
   o[5] = make_uint4(__float_as_uint(of[0]), __float_as_uint(of[1]), __float_as_uint(of[2]), __float_as_uint(of[3]));
 }
 
-// Column tile by batch size and kernel.  One-plane kernel: 32, 64 or 128
-// columns per workgroup, a 3-stage ring, K split while the tile grid covers
-// fewer than two workgroups per CU (at least 8 chunks of 64 per split).  Span
-// kernel: 32 or 64 columns; a tile grid of more than two workgroups per CU
+// Column tile by batch size and kernel.  One-plane kernel: see pick_gemm
+// (at least 8 chunks of 64 per split).  Span kernel: 32 or 64 columns; a tile grid of more than two workgroups per CU
 // takes the 2-stage ring (44 KB for raw Q4_0 at 64 columns, three workgroups
 // per CU; 56 KB for packed units, two), a smaller one the 3-stage ring (two
 // per CU) and a K split into the largest count that keeps the grid within one
@@ -1021,24 +1112,46 @@ GemmShape pick_gemm(int M, int N, int K, int num_cus, bool precise, bool packed)
     const long long slots = (long long)per_cu * num_cus;
     while (s.splits < 16 && tiles * (s.splits + 1) <= slots && nchunks / (s.splits + 1) >= 8) s.splits++;
   } else {
+    // 32, 64 or 128 columns per workgroup.  Tiles of 64 and 128 columns run
+    // the 2-stage ring (44 KB of LDS for raw Q4_0 at 128 columns: three
+    // workgroups per CU, which hide each other's waits better than a deeper
+    // ring with fewer workgroups) and split K only while the tile grid is
+    // smaller than the CU count (a split's partials cost a reduce pass over
+    // N x M x splits floats); 32-column tiles (N <= 32, HBM-bound) keep the
+    // 3-stage ring and split K while the grid covers fewer than two
+    // workgroups per CU.  Measured, 11008 x 4096 at N = 512: 93.6 us per
+    // call with 3 stages and the wider split, 81.4 us with this rule.
     s.tn = N <= 32 ? 1 : (N <= 64 ? 2 : 4);
+    s.stages = s.tn == 1 ? 3 : 2;
     const long long tiles = (long long)((M + 127) / 128) * ((N + 32 * s.tn - 1) / (32 * s.tn));
-    while (tiles * s.splits < 2LL * num_cus && nchunks / (s.splits * 2) >= 8 && s.splits < 16) s.splits *= 2;
+    const long long want = s.tn == 1 ? 2LL * num_cus : (long long)num_cus;
+    while (tiles * s.splits < want && nchunks / (s.splits * 2) >= 8 && s.splits < 16) s.splits *= 2;
   }
   return s;
 }
 
-template <int TN, bool PK>
+template <int TN, int S, bool PK>
 hipError_t launch_p(const GemmArgs& a, int grid, hipStream_t st) {
-  constexpr int lds = PipeCfg<false, TN, kStages, PK>::LDS;
+  constexpr int lds = PipeCfg<false, TN, S, PK>::LDS;
   static_assert(lds <= 160 * 1024, "LDS ring exceeds the CU's 160 KB");
   static std::atomic<uint64_t> lds_done{0};
   if (lds > 64 * 1024) {
-    const hipError_t e = allow_full_lds(reinterpret_cast<const void*>(&gemm_p_kernel<TN, kStages, PK>), lds_done);
+    const hipError_t e = allow_full_lds(reinterpret_cast<const void*>(&gemm_p_kernel<TN, S, PK>), lds_done);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((gemm_p_kernel<TN, kStages, PK>), dim3(grid), dim3(CN_BLOCK), lds, st, a);
+  hipLaunchKernelGGL((gemm_p_kernel<TN, S, PK>), dim3(grid), dim3(CN_BLOCK), lds, st, a);
   return hipGetLastError();
+}
+
+template <int TN, bool PK>
+hipError_t launch_p_ring(const GemmArgs& a, int stages, int grid, hipStream_t st) {
+  if constexpr (TN == 1) {
+    (void)stages;
+    return launch_p<TN, 3, PK>(a, grid, st);
+  } else {
+    (void)stages;
+    return launch_p<TN, 2, PK>(a, grid, st);
+  }
 }
 
 template <int TN, int S, bool PK>
@@ -1066,9 +1179,9 @@ hipError_t launch_kernel(const GemmArgs& a, const GemmShape& s, bool precise, in
     if (tn == 1) return pk ? launch_s_ring<1, true>(a, s.stages, grid, st) : launch_s_ring<1, false>(a, s.stages, grid, st);
     return pk ? launch_s_ring<2, true>(a, s.stages, grid, st) : launch_s_ring<2, false>(a, s.stages, grid, st);
   }
-  if (tn == 1) return pk ? launch_p<1, true>(a, grid, st) : launch_p<1, false>(a, grid, st);
-  if (tn == 2) return pk ? launch_p<2, true>(a, grid, st) : launch_p<2, false>(a, grid, st);
-  return pk ? launch_p<4, true>(a, grid, st) : launch_p<4, false>(a, grid, st);
+  if (tn == 1) return pk ? launch_p_ring<1, true>(a, s.stages, grid, st) : launch_p_ring<1, false>(a, s.stages, grid, st);
+  if (tn == 2) return pk ? launch_p_ring<2, true>(a, s.stages, grid, st) : launch_p_ring<2, false>(a, s.stages, grid, st);
+  return pk ? launch_p_ring<4, true>(a, s.stages, grid, st) : launch_p_ring<4, false>(a, s.stages, grid, st);
 }
 
 }  // namespace
