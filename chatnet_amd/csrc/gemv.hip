@@ -37,6 +37,9 @@
 namespace {
 
 constexpr int QT_Q4_0 = 2, QT_Q8_0 = 8, QT_Q3_K = 11, QT_Q4_K = 12, QT_Q5_K = 13, QT_Q6_K = 14;
+// Q6_K rows read in quarter super-blocks (64 weights per lane unit): the
+// launch shape of rows of 65..96 half super-blocks (8192 < K <= 12288).
+constexpr int QT_Q6_KQ = 114;
 
 template <int QT> struct QTraits;
 template <> struct QTraits<QT_Q4_0> {
@@ -52,6 +55,10 @@ template <> struct QTraits<QT_Q4_K> {
 };
 template <> struct QTraits<QT_Q6_K> {
   static constexpr int UNIT = 128, NDW = 27;
+  static constexpr int BLOCK_BYTES = 210, BLOCK = 256;
+};
+template <> struct QTraits<QT_Q6_KQ> {
+  static constexpr int UNIT = 64, NDW = 15;
   static constexpr int BLOCK_BYTES = 210, BLOCK = 256;
 };
 template <> struct QTraits<QT_Q3_K> {
@@ -504,6 +511,41 @@ __device__ __forceinline__ void load_unit<QT_Q6_K>(const cn_gbyte* row, int u, u
   w[26] = *(const CN_GLOBAL uint16_t*)(sb + 208);
 }
 
+// Quarter q = u & 1 of half h = (u >> 1) & 1 of Q6_K super-block u >> 2: the
+// 64 elements 128h + l + 32i (l in [16q, 16q + 16), i < 4).  w[0..3] =
+// ql[64h + 16q .. +15] (low nibbles: i = 0, high: i = 2), w[4..7] =
+// ql[64h + 32 + 16q .. +15] (i = 1, 3), w[8..11] = qh[32h + 16q .. +15] (bits
+// 2i), w[12..13] = the half's 8 scale bytes (group q + 2i), w[14] = d.  Each
+// piece is read as its dword-aligned window and realigned as load_unit<Q6_K>
+// does; every window lies inside the super-block or the bytes before it.
+template <>
+__device__ __forceinline__ void load_unit<QT_Q6_KQ>(const cn_gbyte* row, int u, uint32_t* w) {
+  const cn_gbyte* sb = row + (size_t)(u >> 2) * 210;
+  const int h = (u >> 1) & 1, q = u & 1;
+  const uintptr_t base = reinterpret_cast<uintptr_t>(sb);
+  const uint32_t sh = (uint32_t)(base & 3);  // 0 or 2
+  const CN_GLOBAL uint32_t* p = (const CN_GLOBAL uint32_t*)(base & ~(uintptr_t)3);
+  uint32_t a[5], b[5], c[5], e[3];
+#pragma unroll
+  for (int k = 0; k < 5; k++) {
+    a[k] = p[16 * h + 4 * q + k];
+    b[k] = p[16 * h + 8 + 4 * q + k];
+    c[k] = p[32 + 8 * h + 4 * q + k];
+  }
+  e[0] = p[48 + 2 * h];
+  e[1] = p[49 + 2 * h];
+  e[2] = sh ? p[50 + 2 * h] : 0u;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    w[k] = __builtin_amdgcn_alignbyte(a[k + 1], a[k], sh);
+    w[4 + k] = __builtin_amdgcn_alignbyte(b[k + 1], b[k], sh);
+    w[8 + k] = __builtin_amdgcn_alignbyte(c[k + 1], c[k], sh);
+  }
+  w[12] = __builtin_amdgcn_alignbyte(e[1], e[0], sh);
+  w[13] = __builtin_amdgcn_alignbyte(e[2], e[1], sh);
+  w[14] = *(const CN_GLOBAL uint16_t*)(sb + 208);
+}
+
 // Q3_K half super-block h = u & 1 (DequantQ3K.cs: hmask[32] @0, qs[64] @32,
 // scales[12] @96, fp16 d @108; 110 bytes, so super-blocks start on 2-byte
 // boundaries): w[0..7] = qs[32h .. 32h+31], w[8..11] = hmask[16h .. 16h+15],
@@ -698,6 +740,50 @@ __device__ __forceinline__ void dot_unit_q6_k_dig(const uint32_t (*w)[27], const
   }
 #pragma unroll
   for (int i = 0; i < RPW; i++) acc[i] += cn_h2f(w[i][26]) * part[i];
+}
+
+// Q6_K quarter q of a half super-block (load_unit<QT_Q6_KQ>) against the
+// half's digit records (groups q, q + 2, q + 4, q + 6): dot_unit_q6_k_dig's
+// arithmetic for those four groups.
+template <int RPW>
+__device__ __forceinline__ void dot_unit_q6_kq_dig(const uint32_t (*w)[15], const uint32_t* xd, int q, float* acc) {
+  float part[RPW];
+#pragma unroll
+  for (int i = 0; i < RPW; i++) part[i] = 0.f;
+#pragma unroll
+  for (int qi = 0; qi < 4; qi++) {
+    const int g = 2 * qi + q;  // local group: scale 8h + g of the super-block
+    const uint32_t* rec = xd + 16 * g;
+    uint32_t D[3][4];
+#pragma unroll
+    for (int d = 0; d < 3; d++) {
+      const uint4 t = *reinterpret_cast<const uint4*>(rec + 4 * d);
+      D[d][0] = t.x; D[d][1] = t.y; D[d][2] = t.z; D[d][3] = t.w;
+    }
+    const int xsum = (int)rec[12];
+    const int e = (int)rec[13];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      uint32_t qv[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const uint32_t qlw = (qi & 1) ? w[i][4 + k] : w[i][k];
+        const uint32_t nib = (qi < 2) ? (qlw & 0x0F0F0F0Fu) : ((qlw >> 4) & 0x0F0F0F0Fu);
+        qv[k] = nib | (((w[i][8 + k] >> (2 * qi)) & 0x03030303u) << 4);
+      }
+      int t = 0;
+#pragma unroll
+      for (int d = 2; d >= 0; d--) {
+        if (d < 2) t <<= 8;
+#pragma unroll
+        for (int k = 0; k < 4; k++) t = __builtin_amdgcn_sdot4((int)qv[k], (int)D[d][k], t, false);
+      }
+      const int8_t scv = (int8_t)((w[i][12 + (g >> 2)] >> (8 * (g & 3))) & 0xFF);
+      part[i] += ldexpf((float)(t - 32 * xsum) * (float)scv, -e);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RPW; i++) acc[i] += cn_h2f(w[i][14]) * part[i];
 }
 
 // Q3_K half super-block h (DequantQ3K.cs:35-70, DecodeScales :122-150): element
@@ -906,7 +992,7 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
   const int stop_v = cn_load_late(stop_flag(a));
   const int pos_v = (EPI == GEMV_EPI_QKV || MERGE) ? cn_load_late(a.pos) : 0;
   constexpr bool kDig8 =
-      QT == QT_Q8_0 || QT == QT_Q3_K || QT == QT_Q6_K || QT == QT_Q5_K || (QT == QT_Q4_K && LPR > 32);
+      QT == QT_Q8_0 || QT == QT_Q3_K || QT == QT_Q6_K || QT == QT_Q6_KQ || QT == QT_Q5_K || (QT == QT_Q4_K && LPR > 32);
   MergeSrc ms{};
   if constexpr (MERGE) {
     ms.o = a.part_o;
@@ -988,6 +1074,7 @@ __global__ __launch_bounds__(BS) void gemv_kernel(GemvArgs a) {
           if constexpr (QT == QT_Q4_0) dot_unit_q4_0_dig<RPW>(wu, xd + u * XD_UNIT_DW, acc);
           else if constexpr (QT == QT_Q8_0) dot_unit_q8_0_dig8<RPW>(wu, xd + (u >> 1) * XD6_UNIT_DW + 64 * (u & 1), acc);
           else if constexpr (QT == QT_Q6_K) dot_unit_q6_k_dig<RPW>(wu, xd + u * XD6_UNIT_DW, acc);
+          else if constexpr (QT == QT_Q6_KQ) dot_unit_q6_kq_dig<RPW>(wu, xd + (u >> 1) * XD6_UNIT_DW, u & 1, acc);
           else if constexpr (QT == QT_Q3_K) dot_unit_q3_k_dig<RPW>(wu, xd + u * XD6_UNIT_DW, u & 1, acc);
           else if constexpr (kDig8) dot_unit_k45_dig8<QT, RPW>(wu, xd + u * XD6_UNIT_DW, u & 1, acc);
           else dot_unit_q4_k_dig<RPW>(wu, xd + 2 * u * XD_UNIT_DW, u & 1, acc);
@@ -1257,7 +1344,7 @@ GemvShape pick_shape(int K, int n_vrows, int num_cus, bool allow8, bool isolated
   // per CU (32000x4096 29.2 -> 28.0 us), two-unit K-quant lanes (~160 VGPRs,
   // x digitized before the weight loads) at three, Q4_K and Q5_K one-unit
   // lanes at two
-  const bool kq = QT == QT_Q3_K || QT == QT_Q4_K || QT == QT_Q5_K || QT == QT_Q6_K;
+  const bool kq = QT == QT_Q3_K || QT == QT_Q4_K || QT == QT_Q5_K || QT == QT_Q6_K || QT == QT_Q6_KQ;
   const int per_cu = (QT == QT_Q6_K || QT == QT_Q3_K) && s.nu == 1 ? 4 : (kq && s.nu >= 2 ? 3 : 2);
   if (s.grid > per_cu * num_cus) s.grid = per_cu * num_cus;
   if (s.grid < 1) s.grid = 1;
@@ -1392,6 +1479,13 @@ hipError_t launch_ks(const GemvArgs& a, hipStream_t st) {
 
 template <int QT, int EPI>
 hipError_t launch_qt(const GemvArgs& a, int num_cus, hipStream_t st) {
+  if constexpr (QT == QT_Q6_K && (EPI == GEMV_EPI_STORE || EPI == GEMV_EPI_ADD)) {
+    // Rows of 65..96 half super-blocks (the 7B down projection, 86): 64 lanes
+    // x 2 half super-blocks leave a third of the slots idle, 64 lanes x 3
+    // quarters a tenth
+    const int halves = a.K / 128;
+    if (halves > 64 && halves <= 96) return launch_qt<QT_Q6_KQ, EPI>(a, num_cus, st);
+  }
   // 8 rows per lane only for the norm-fused epilogues (the wide QKV, gate/up
   // and LM-head launches); hipcc 7.2 fails to compile the 8-row STORE/ADD forms.
   constexpr bool kAllow8 = EPI == GEMV_EPI_QKV || EPI == GEMV_EPI_SWIGLU || EPI == GEMV_EPI_LOGITS;
@@ -1430,6 +1524,8 @@ hipError_t launch_qt(const GemvArgs& a, int num_cus, hipStream_t st) {
     if (s.nu == 2) return launch_k<QT, 2, 2, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
     if (s.nu == 3) return launch_k<QT, 2, 3, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
     return launch_k<QT, 2, 4, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
+  } else if constexpr (QT == QT_Q6_KQ) {
+    return launch_one<QT, 2, 64, 3, EPI, CN_BLOCK>(a, s.grid, smem, st);  // 129..192 quarters per row
   } else {
     if (s.nu == 1) return launch_k<QT, 2, 1, EPI, CN_BLOCK>(a, s.lpr, s.grid, smem, st);
     if constexpr (QT == QT_Q5_K && !kPaired) {

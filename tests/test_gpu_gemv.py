@@ -84,6 +84,9 @@ def test_generic_type_gemv_shapes(qtype, M, K):
     (12, 3, 16384), (13, 3, 16384), (14, 3, 16384), (8, 9, 16320),
     # Q5_K rows of 65..96 half super-blocks: one row per lane, 32 lanes x 3 units
     (13, 5, 8448), (13, 7, 12288), (13, 66, 11008),
+    # Q6_K rows of 65..96 half super-blocks: quarter super-blocks, 64 lanes x 3
+    # (rows start 2 bytes off a dword on every other row)
+    (14, 5, 8448), (14, 7, 12288), (14, 131, 11008), (14, 1, 11008),
 ])
 def test_ragged_and_misaligned_shapes(qtype, M, K):
     run_case(qtype, M, K, seed=5)
