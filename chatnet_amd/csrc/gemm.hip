@@ -283,10 +283,13 @@ __device__ __forceinline__ void reg_fence(T& r) {
   asm volatile("" : "+v"(r));
 }
 
-template <bool PRECISE, int TN, int S, bool PK>
+// MT: 32-row tiles per wave (the waves stack along M, BM = 128 * MT rows per
+// workgroup); each x fragment read from LDS feeds MT MFMAs.
+template <bool PRECISE, int TN, int S, bool PK, int MT = 1>
 struct PipeCfg {
   static constexpr int PL = PRECISE ? 2 : 1;
-  static constexpr int BM = 128, BN = 32 * TN;
+  static constexpr int MTILES = MT;
+  static constexpr int BM = 128 * MT, BN = 32 * TN;
   static constexpr int UNIT = PK ? kGemmPackUnit : 36;  // global bytes per row and chunk
   static constexpr int WP = PK ? 6 : 3;        // 16-byte pieces per row and chunk
   static constexpr int WROW = 16 * WP;         // LDS bytes per row and chunk
@@ -370,8 +373,9 @@ struct TileIO {
   // 0..4, block B's d in the high half of dword 4 and its qs at dwords
   // 8..11.  Packed (12 dwords): codes 32h..32h+31 (dwords 8h..8h+7), then
   // scales 2h, 2h+1 (unit bytes 64 + 8h) and offsets 2h, 2h+1 (80 + 8h).
-  __device__ __forceinline__ void wraw(const char* st, uint32_t (&w)[C::WD]) const {
-    const uint32_t* wb = reinterpret_cast<const uint32_t*>(st + C::PL * C::XB + (wave * 32 + li) * C::WROW);
+  __device__ __forceinline__ void wraw(const char* st, uint32_t (&w)[C::WD], int mt = 0) const {
+    const uint32_t* wb =
+        reinterpret_cast<const uint32_t*>(st + C::PL * C::XB + (wave * 32 * C::MTILES + 32 * mt + li) * C::WROW);
     if constexpr (C::PACKED) {
 #pragma unroll
       for (int i = 0; i < 8; i++) w[i] = wb[8 * h + i];
@@ -404,7 +408,7 @@ struct TileIO {
 
   // Final tiles: K-split partials [splits][N][M] or the epilogue.
   template <int TN>
-  __device__ __forceinline__ void store(const GemmArgs& a, const f32x16 (&acc)[TN]) const {
+  __device__ __forceinline__ void store(const GemmArgs& a, const f32x16 (&acc)[TN], int mt = 0) const {
 #pragma unroll
     for (int cc = 0; cc < TN; cc++) {
       const int n = n0 + 32 * cc + li;
@@ -412,7 +416,7 @@ struct TileIO {
       const float sc = a.xinv ? a.xinv[n < a.N ? n : a.N - 1] : 1.0f;
 #pragma unroll
       for (int v4 = 0; v4 < 4; v4++) {
-        const int m = m0 + wave * 32 + 8 * v4 + 4 * h;
+        const int m = m0 + wave * 32 * C::MTILES + 32 * mt + 8 * v4 + 4 * h;
         const f32x4 v = f32x4{acc[cc][4 * v4], acc[cc][4 * v4 + 1], acc[cc][4 * v4 + 2], acc[cc][4 * v4 + 3]} * sc;
         if (a.splits > 1) {
           if (n < a.N && m < a.M) {
@@ -438,18 +442,20 @@ struct TileIO {
 // TN MFMAs (one v_mfma_f32_32x32x16_f16 per column tile).  Step s of lane
 // half h: Q4_0 qs dword s of block h; packed codes 32h + 4s .. +3 and
 // 32h + 16 + 4s .. +3 with the scale/offset pairs 2h and 2h+1.
-template <int TN, int S, bool PK>
+template <int TN, int S, bool PK, int MT>
 __global__ __launch_bounds__(CN_BLOCK) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_p_kernel(GemmArgs a) {
-  using C = PipeCfg<false, TN, S, PK>;
+  using C = PipeCfg<false, TN, S, PK, MT>;
   extern __shared__ __attribute__((aligned(16))) char lds[];
   const TileIO<C> io(a);
   const int h = io.h;
 
-  f32x16 acc[TN];
+  f32x16 acc[MT][TN];
 #pragma unroll
-  for (int cc = 0; cc < TN; cc++)
+  for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-    for (int v = 0; v < 16; v++) acc[cc][v] = 0.f;
+    for (int cc = 0; cc < TN; cc++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) acc[mt][cc][v] = 0.f;
 
   const uint32_t psel = h ? 0x03010200u : 0x05030402u;
   uint32_t magic = 0x64006400u;
@@ -482,19 +488,20 @@ __global__ __launch_bounds__(CN_BLOCK) __attribute__((amdgpu_waves_per_eu(1, 2))
       if (c + S - 1 < c_end) io.issue(c + S - 1, slot_of(c + S - 1));
       // the lane's W dwords (as wraw), then every x fragment of the chunk, all
       // issued at once; step s waits for its own fragments only
-      uint32_t w[C::WD];
-      {
-        const uint32_t wb = lds_addr(st + C::PL * C::XB + (io.wave * 32 + io.li) * C::WROW);
+      uint32_t w[MT][C::WD];
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++) {
+        const uint32_t wb = lds_addr(st + C::PL * C::XB + (io.wave * 32 * MT + 32 * mt + io.li) * C::WROW);
         if constexpr (PK) {
           const cn_u32x4 c0 = lds_read128(wb + 32 * h), c1 = lds_read128(wb + 32 * h + 16);
           const uint2 sc = lds_read64(wb + 64 + 8 * h), of = lds_read64(wb + 80 + 8 * h);
-          w[0] = c0[0], w[1] = c0[1], w[2] = c0[2], w[3] = c0[3];
-          w[4] = c1[0], w[5] = c1[1], w[6] = c1[2], w[7] = c1[3];
-          w[8] = sc.x, w[9] = sc.y, w[10] = of.x, w[11] = of.y;
+          w[mt][0] = c0[0], w[mt][1] = c0[1], w[mt][2] = c0[2], w[mt][3] = c0[3];
+          w[mt][4] = c1[0], w[mt][5] = c1[1], w[mt][6] = c1[2], w[mt][7] = c1[3];
+          w[mt][8] = sc.x, w[mt][9] = sc.y, w[mt][10] = of.x, w[mt][11] = of.y;
         } else {
           const cn_u32x4 q = lds_read128(wb + 32 * h);
           const uint32_t t = lds_read32(wb + 16);
-          w[0] = q[0], w[1] = q[1], w[2] = q[2], w[3] = q[3], w[4] = t;
+          w[mt][0] = q[0], w[mt][1] = q[1], w[mt][2] = q[2], w[mt][3] = q[3], w[mt][4] = t;
         }
       }
       cn_u32x4 xr[4][TN];
@@ -508,7 +515,9 @@ __global__ __launch_bounds__(CN_BLOCK) __attribute__((amdgpu_waves_per_eu(1, 2))
         if (s == 0) {
           lds_wait<(3 * TN > 15 ? 15 : 3 * TN)>();
 #pragma unroll
-          for (int i = 0; i < C::WD; i++) reg_fence(w[i]);
+          for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int i = 0; i < C::WD; i++) reg_fence(w[mt][i]);
         } else if (s == 1) {
           lds_wait<2 * TN>();
         } else if (s == 2) {
@@ -518,28 +527,29 @@ __global__ __launch_bounds__(CN_BLOCK) __attribute__((amdgpu_waves_per_eu(1, 2))
         }
 #pragma unroll
         for (int cc = 0; cc < TN; cc++) reg_fence(xr[s][cc]);
-        cn_half2 d2 = {};
-        if constexpr (!PK) {
-          const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(h ? (w[4] >> 16) : (w[0] & 0xFFFFu)));
-          d2 = (cn_half2){d, d};
-        }
         f16x8 xh[TN];
 #pragma unroll
         for (int cc = 0; cc < TN; cc++) xh[cc] = __builtin_bit_cast(f16x8, xr[s][cc]);
-        f16x8 wa;
-        if constexpr (PK) {
-          wa = dequant_u8_h(w[s], w[4 + s], __uint_as_float(w[8]), __uint_as_float(w[10]), __uint_as_float(w[9]),
-                            __uint_as_float(w[11]));
-        } else {
-          wa = dequant_q4_h(__builtin_amdgcn_perm(w[s + 1], w[s], psel), magic, d2);
-        }
 #pragma unroll
-        for (int cc = 0; cc < TN; cc++) acc[cc] = mma32(wa, xh[cc], acc[cc]);
+        for (int mt = 0; mt < MT; mt++) {
+          f16x8 wa;
+          if constexpr (PK) {
+            wa = dequant_u8_h(w[mt][s], w[mt][4 + s], __uint_as_float(w[mt][8]), __uint_as_float(w[mt][10]),
+                              __uint_as_float(w[mt][9]), __uint_as_float(w[mt][11]));
+          } else {
+            const _Float16 d =
+                __builtin_bit_cast(_Float16, (uint16_t)(h ? (w[mt][4] >> 16) : (w[mt][0] & 0xFFFFu)));
+            wa = dequant_q4_h(__builtin_amdgcn_perm(w[mt][s + 1], w[mt][s], psel), magic, (cn_half2){d, d});
+          }
+#pragma unroll
+          for (int cc = 0; cc < TN; cc++) acc[mt][cc] = mma32(wa, xh[cc], acc[mt][cc]);
+        }
         __builtin_amdgcn_sched_barrier(0);  // the next step's wait stays behind these MFMAs
       }
     }
   }
-  io.template store<TN>(a, acc);
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++) io.template store<TN>(a, acc[mt], mt);
 }
 
 // Span kernel (the exact-weight product of the forward pass's spans: fp16 x
@@ -1080,7 +1090,7 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_pack_kernel(int qtype, const ui
 // round of resident workgroups with at least 8 chunks per split (a grid just
 // over a round would run a second round on a few CUs).
 struct GemmShape {
-  int tn, splits, stages;
+  int tn, splits, stages, mt = 1;
 };
 
 constexpr int kStages = 3;
@@ -1123,34 +1133,41 @@ GemmShape pick_gemm(int M, int N, int K, int num_cus, bool precise, bool packed)
     // call with 3 stages and the wider split, 81.4 us with this rule.
     s.tn = N <= 32 ? 1 : (N <= 64 ? 2 : 4);
     s.stages = s.tn == 1 ? 3 : 2;
-    const long long tiles = (long long)((M + 127) / 128) * ((N + 32 * s.tn - 1) / (32 * s.tn));
+    // Two 32-row tiles per wave (256-row workgroups, each x fragment read
+    // from LDS feeding two MFMAs) where that still leaves a tile per CU:
+    // 32000 x 2048 at N = 512, 96.7 -> 85.3 us per call; 11008 x 4096 (172
+    // such tiles) went 79.3 -> 88.3 us and keeps one.
+    if (s.tn == 4 && (long long)((M + 255) / 256) * ((N + 127) / 128) >= num_cus) s.mt = 2;
+    const long long tiles = (long long)((M + 128 * s.mt - 1) / (128 * s.mt)) * ((N + 32 * s.tn - 1) / (32 * s.tn));
     const long long want = s.tn == 1 ? 2LL * num_cus : (long long)num_cus;
     while (tiles * s.splits < want && nchunks / (s.splits * 2) >= 8 && s.splits < 16) s.splits *= 2;
   }
   return s;
 }
 
-template <int TN, int S, bool PK>
+template <int TN, int S, bool PK, int MT>
 hipError_t launch_p(const GemmArgs& a, int grid, hipStream_t st) {
-  constexpr int lds = PipeCfg<false, TN, S, PK>::LDS;
+  constexpr int lds = PipeCfg<false, TN, S, PK, MT>::LDS;
   static_assert(lds <= 160 * 1024, "LDS ring exceeds the CU's 160 KB");
   static std::atomic<uint64_t> lds_done{0};
   if (lds > 64 * 1024) {
-    const hipError_t e = allow_full_lds(reinterpret_cast<const void*>(&gemm_p_kernel<TN, S, PK>), lds_done);
+    const hipError_t e = allow_full_lds(reinterpret_cast<const void*>(&gemm_p_kernel<TN, S, PK, MT>), lds_done);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((gemm_p_kernel<TN, S, PK>), dim3(grid), dim3(CN_BLOCK), lds, st, a);
+  hipLaunchKernelGGL((gemm_p_kernel<TN, S, PK, MT>), dim3(grid), dim3(CN_BLOCK), lds, st, a);
   return hipGetLastError();
 }
 
 template <int TN, bool PK>
-hipError_t launch_p_ring(const GemmArgs& a, int stages, int grid, hipStream_t st) {
+hipError_t launch_p_ring(const GemmArgs& a, int stages, int mt, int grid, hipStream_t st) {
+  (void)stages;
   if constexpr (TN == 1) {
-    (void)stages;
-    return launch_p<TN, 3, PK>(a, grid, st);
+    return launch_p<TN, 3, PK, 1>(a, grid, st);
+  } else if constexpr (TN == 4) {
+    if (mt == 2) return launch_p<TN, 2, PK, 2>(a, grid, st);
+    return launch_p<TN, 2, PK, 1>(a, grid, st);
   } else {
-    (void)stages;
-    return launch_p<TN, 2, PK>(a, grid, st);
+    return launch_p<TN, 2, PK, 1>(a, grid, st);
   }
 }
 
@@ -1179,9 +1196,9 @@ hipError_t launch_kernel(const GemmArgs& a, const GemmShape& s, bool precise, in
     if (tn == 1) return pk ? launch_s_ring<1, true>(a, s.stages, grid, st) : launch_s_ring<1, false>(a, s.stages, grid, st);
     return pk ? launch_s_ring<2, true>(a, s.stages, grid, st) : launch_s_ring<2, false>(a, s.stages, grid, st);
   }
-  if (tn == 1) return pk ? launch_p_ring<1, true>(a, s.stages, grid, st) : launch_p_ring<1, false>(a, s.stages, grid, st);
-  if (tn == 2) return pk ? launch_p_ring<2, true>(a, s.stages, grid, st) : launch_p_ring<2, false>(a, s.stages, grid, st);
-  return pk ? launch_p_ring<4, true>(a, s.stages, grid, st) : launch_p_ring<4, false>(a, s.stages, grid, st);
+  if (tn == 1) return pk ? launch_p_ring<1, true>(a, s.stages, 1, grid, st) : launch_p_ring<1, false>(a, s.stages, 1, grid, st);
+  if (tn == 2) return pk ? launch_p_ring<2, true>(a, s.stages, 1, grid, st) : launch_p_ring<2, false>(a, s.stages, 1, grid, st);
+  return pk ? launch_p_ring<4, true>(a, s.stages, s.mt, grid, st) : launch_p_ring<4, false>(a, s.stages, s.mt, grid, st);
 }
 
 }  // namespace
@@ -1248,7 +1265,8 @@ hipError_t gemm_launch(const GemmArgs& a_in, int num_cus, hipStream_t st, int* s
   GemmArgs a = a_in;
   a.splits = s.splits;
   if (s.splits > 1 && !a.part) return hipErrorInvalidValue;
-  const long long grid = (long long)((a.M + 127) / 128) * ((a.N + 32 * s.tn - 1) / (32 * s.tn)) * s.splits;
+  const long long grid =
+      (long long)((a.M + 128 * s.mt - 1) / (128 * s.mt)) * ((a.N + 32 * s.tn - 1) / (32 * s.tn)) * s.splits;
   if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
   hipError_t e = launch_kernel(a, s, precise, (int)grid, st);
   if (splits_left) *splits_left = 0;
