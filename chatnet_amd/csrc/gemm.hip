@@ -243,6 +243,19 @@ __device__ __forceinline__ void vm_wait() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Waits until only the `later` chunks issued after the needed one (at most
+// K, VPS vector-memory instructions each) may still be in flight.
+template <int VPS, int K>
+__device__ __forceinline__ void vm_wait_later(int later) {
+  if constexpr (K == 0 || K * VPS > 63) {
+    if constexpr (K == 0) vm_wait<0>();
+    else vm_wait_later<VPS, K - 1>(later);
+  } else {
+    if (later >= K) vm_wait<K * VPS>();
+    else vm_wait_later<VPS, K - 1>(later);
+  }
+}
+
 __device__ __forceinline__ void wg_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
@@ -470,20 +483,7 @@ __global__ __launch_bounds__(CN_BLOCK) __attribute__((amdgpu_waves_per_eu(1, 2))
     for (int c = c_begin; c < c_end; c++) {
       char* st = slot_of(c);
       // chunks c+1 .. c+S-2 may stay in flight
-      const int later = min(S - 2, c_end - 1 - c);
-      if constexpr (S >= 5) {
-        if (later >= 3) vm_wait<3 * C::VPS>();
-        else if (later == 2) vm_wait<2 * C::VPS>();
-        else if (later == 1) vm_wait<C::VPS>();
-        else vm_wait<0>();
-      } else if constexpr (S == 4) {
-        if (later >= 2) vm_wait<2 * C::VPS>();
-        else if (later == 1) vm_wait<C::VPS>();
-        else vm_wait<0>();
-      } else {
-        if (later >= 1) vm_wait<C::VPS>();
-        else vm_wait<0>();
-      }
+      vm_wait_later<C::VPS, S - 2>(min(S - 2, c_end - 1 - c));
       wg_barrier();
       if (c + S - 1 < c_end) io.issue(c + S - 1, slot_of(c + S - 1));
       // the lane's W dwords (as wraw), then every x fragment of the chunk, all
@@ -1127,19 +1127,21 @@ GemmShape pick_gemm(int M, int N, int K, int num_cus, bool precise, bool packed)
     // workgroups per CU, which hide each other's waits better than a deeper
     // ring with fewer workgroups) and split K only while the tile grid is
     // smaller than the CU count (a split's partials cost a reduce pass over
-    // N x M x splits floats); 32-column tiles (N <= 32, HBM-bound) keep the
-    // 3-stage ring and split K while the grid covers fewer than two
-    // workgroups per CU.  Measured, 11008 x 4096 at N = 512: 93.6 us per
-    // call with 3 stages and the wider split, 81.4 us with this rule.
+    // N x M x splits floats); 32-column tiles (N <= 32, HBM-bound) run a
+    // 4-stage ring (40 KB) under the same split rule.  Measured per call,
+    // 11008 x 4096 at N = 512: 93.6 us with 3 stages and splits up to two
+    // workgroups per CU, 81.4 us with this rule; at N = 8: 20.4 us with 3
+    // stages and that wider split, 17.8 us with this rule (6 and 8 stages:
+    // 18.4, 18.9).
     s.tn = N <= 32 ? 1 : (N <= 64 ? 2 : 4);
-    s.stages = s.tn == 1 ? 3 : 2;
+    s.stages = s.tn == 1 ? 4 : 2;
     // Two 32-row tiles per wave (256-row workgroups, each x fragment read
     // from LDS feeding two MFMAs) where that still leaves a tile per CU:
     // 32000 x 2048 at N = 512, 96.7 -> 85.3 us per call; 11008 x 4096 (172
     // such tiles) went 79.3 -> 88.3 us and keeps one.
     if (s.tn == 4 && (long long)((M + 255) / 256) * ((N + 127) / 128) >= num_cus) s.mt = 2;
     const long long tiles = (long long)((M + 128 * s.mt - 1) / (128 * s.mt)) * ((N + 32 * s.tn - 1) / (32 * s.tn));
-    const long long want = s.tn == 1 ? 2LL * num_cus : (long long)num_cus;
+    const long long want = num_cus;
     while (tiles * s.splits < want && nchunks / (s.splits * 2) >= 8 && s.splits < 16) s.splits *= 2;
   }
   return s;
@@ -1162,7 +1164,7 @@ template <int TN, bool PK>
 hipError_t launch_p_ring(const GemmArgs& a, int stages, int mt, int grid, hipStream_t st) {
   (void)stages;
   if constexpr (TN == 1) {
-    return launch_p<TN, 3, PK, 1>(a, grid, st);
+    return launch_p<TN, 4, PK, 1>(a, grid, st);
   } else if constexpr (TN == 4) {
     if (mt == 2) return launch_p<TN, 2, PK, 2>(a, grid, st);
     return launch_p<TN, 2, PK, 1>(a, grid, st);
