@@ -330,16 +330,25 @@ def prefill_run(w, ck):
             "decode_tok_s": round(w.n_decode / (t2 - t1), 1), "parity": parity(w.name, toks, lp)}
 
 
-def profile_figure(path: str, key: str):
-    """A number recorded as `key: value` in a committed profiles/ summary."""
+def profile_value(path: str, key: str):
+    """The text after `key:` on its line in a committed profiles/ summary."""
     try:
         with open(os.path.join(ROOT, "profiles", path)) as f:
             for line in f:
                 if line.startswith(key + ":"):
-                    return float(line.split(":", 1)[1].split()[0])
-    except (OSError, ValueError):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
         pass
     return None
+
+
+def profile_figure(path: str, key: str):
+    """A number recorded as `key: value` in a committed profiles/ summary."""
+    v = profile_value(path, key)
+    try:
+        return float(v.split()[0]) if v else None
+    except ValueError:
+        return None
 
 
 def cpu_model() -> str:
@@ -353,10 +362,12 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(cfg7, ck7, cfg1, ck1):
+def cpu_baseline(cfg7, ck7, w1, ck1):
     """The oracle (C restatement of the reference's CPU path) on the host
     cores, bounded samples: the 7B decode (headline unit), the TinyLlama
-    decode at all threads and at one thread, and the isolated Q4_0 GEMV."""
+    workload (its 16-token prompt and 32 greedy tokens) at all threads and a
+    shorter sample at one thread, and the isolated Q4_0 GEMV at the seven
+    sweep shapes (N = 1; the reference has no batched product)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
     from chatnet_amd import synth
@@ -376,28 +387,55 @@ def cpu_baseline(cfg7, ck7, cfg1, ck1):
         ora.close()
         return decode / dt
 
+    def workload_rate(w, ck, threads):
+        """The workload's prompt token by token, then its greedy decode
+        (InferenceEngine.Generate's loop); decode tok/s and the tokens."""
+        oracle.set_threads(threads)
+        ora = oracle.OracleLlama(w.config, ck)
+        logits = None
+        for i, tk in enumerate(w.prompt()):
+            logits = ora.forward([int(tk)], i)
+        toks = []
+        t0 = time.perf_counter()
+        pos = w.n_prompt
+        for _ in range(w.n_decode):
+            tok = oracle.argmax(logits)
+            toks.append(tok)
+            logits = ora.forward([tok], pos)
+            pos += 1
+        dt = time.perf_counter() - t0
+        ora.close()
+        return w.n_decode / dt, toks
+
     v7 = decode_rate(cfg7, ck7, 4, 8, cores)
     legs = {"cpu_model": cpu_model(), "host_threads_visible": os.cpu_count(), "threads_used": cores}
-    if cfg1 is not None:
-        legs["tinyllama_q4_0_decode_tok_s"] = round(decode_rate(cfg1, ck1, 4, 16, cores), 3)
-        legs["tinyllama_q4_0_decode_tok_s_1_thread"] = round(decode_rate(cfg1, ck1, 2, 4, 1), 3)
-    M, K = ROOF_SHAPE
-    t = synth.tensor(2, 99, f"sweep{M}x{K}", M, K)
-    x = synth.normal(99, f"sweepx{K}", K, 1.0)
+    if w1 is not None:
+        r1, toks1 = workload_rate(w1, ck1, cores)
+        legs["tinyllama_q4_0_decode_tok_s"] = round(r1, 3)
+        legs["tinyllama_q4_0_decode_workload"] = f"{w1.n_prompt}-token prompt, {w1.n_decode} greedy tokens timed"
+        fx = fixture(w1.name)
+        legs["tinyllama_q4_0_decode_tokens_match_fixture"] = (
+            None if fx is None else [int(t) for t in fx["tokens"]] == [int(t) for t in toks1])
+        legs["tinyllama_q4_0_decode_tok_s_1_thread"] = round(decode_rate(w1.config, ck1, 2, 4, 1), 3)
     oracle.set_threads(cores)
-    oracle.matvec(2, t.data, x, M, K)
-    reps = 10
-    t0 = time.perf_counter()
-    for _ in range(reps):
+    reps = 5
+    gbs = {}
+    for (M, K) in SWEEP:
+        t = synth.tensor(2, 99, f"sweep{M}x{K}", M, K)
+        x = synth.normal(99, f"sweepx{K}", K, 1.0)
         oracle.matvec(2, t.data, x, M, K)
-    dt = (time.perf_counter() - t0) / reps
-    legs[f"gemv_q4_0_{M}x{K}_GBs"] = round(gemv_algorithmic_bytes(M, K) / dt / 1e9, 2)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            oracle.matvec(2, t.data, x, M, K)
+        dt = (time.perf_counter() - t0) / reps
+        gbs[f"{M}x{K}"] = round(gemv_algorithmic_bytes(M, K) / dt / 1e9, 2)
+    legs["gemv_q4_0_n1_GBs"] = gbs
     oracle.set_threads(1)
     return {"value": round(v7, 3), "unit": "tok/s", "cores": cores, "kind": "port",
             "sample": f"oracle LlamaModel.Forward restatement, {cfg7.n_layers}-layer {cfg7.dim}-dim Q4_0, "
                       f"4-token prompt then 8 greedy decode tokens timed, row-parallel over {cores} threads; "
-                      f"legs: TinyLlama-shaped decode (16 tokens at {cores} threads, 4 at 1 thread) and "
-                      f"{reps} isolated {M}x{K} Q4_0 GEMVs",
+                      f"legs: the TinyLlama-shaped 16+32 workload at {cores} threads (4 tokens at 1 thread) "
+                      f"and {reps} isolated Q4_0 GEMVs per sweep shape",
             "legs": legs}
 
 
@@ -503,7 +541,7 @@ def main():
         w1 = WORKLOADS["tinyllama_q4_0_decode"]
         if not args.no_cpu and args.only is None:
             log("cpu baseline (oracle on host cores)")
-            cpu = cpu_baseline(cfg7, ck7, w1.config, w1.checkpoint())
+            cpu = cpu_baseline(cfg7, ck7, w1, w1.checkpoint())
             log(f"  {cpu['value']} tok/s on {cpu['cores']} threads; {json.dumps(cpu['legs'])}")
         del ck7
     if not args.roofline_only and not args.no_tinyllama:
@@ -565,7 +603,9 @@ def main():
             "gemv_us_per_token": tiny_gemv_us,
             "gemv_frac_of_hbm_peak": (round(tiny_gemv_bytes / (tiny_gemv_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
                                       if tiny_gemv_us else None),
-            "gemv_source": "profiles/tinyllama_q4_0_decode_kernels.md (rocprofv3 kernel trace of the workload)"},
+            "gemv_source": "profiles/tinyllama_q4_0_decode_kernels.md (rocprofv3 kernel trace of the workload, "
+                           "read from the committed summary, not measured by this run)",
+            "gemv_source_commit": profile_value("tinyllama_q4_0_decode_kernels.md", "commit")},
         "gemv_sweep_q4_0_n1_cold": sweep,
         "gemm_sweep_q4_0_cold": gsweep,
         "tinyllama_q4_0_prefill": prefill,
@@ -576,6 +616,7 @@ def main():
                      "traffic": profile_figure("gemv_q4_0_sweep_roofline.md",
                                                f"traffic_bytes_per_launch {ROOF_SHAPE[0]}x{ROOF_SHAPE[1]}"),
                      "traffic_source": "profiles/gemv_q4_0_sweep_roofline.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
+                     "traffic_source_commit": profile_value("gemv_q4_0_sweep_roofline.md", "commit"),
                      "kernel": "gemv_kernel<Q4_0> (chatnet_matmul N=1) at 11008x4096, cold",
                      "alg_bytes_per_launch": roof.get("alg_bytes"), "avg_launch_us": roof.get("us"),
                      "measured_copy_GBs": copy_gbs,
