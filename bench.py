@@ -40,8 +40,13 @@ METRIC = "decode tok/s bs1 (1.1B & 7B Q4_0); Q4_0 GEMV achieved HBM GB/s vs peak
 SWEEP = [(2048, 2048), (256, 2048), (5632, 2048), (2048, 5632), (32000, 2048), (4096, 4096), (11008, 4096)]
 ROOF_SHAPE = (11008, 4096)
 # legs --only can select
-LEGS = ("gemv_sweep", "roofline", "kquant", "gemm_sweep", "gemm_counters", "llama7b_decode", "tinyllama_decode",
-        "prefill")
+LEGS = ("gemv_sweep", "roofline", "kquant", "gemm_sweep", "gemm_counters", "gemv_counters", "llama7b_decode",
+        "tinyllama_decode", "prefill")
+# one N = 1 chatnet_matmul per (type, M, K) for counter runs: the 7B shapes of
+# the Q4_0 and K-quant decodes
+COUNTER_GEMVS = [(2, 11008, 4096), (2, 4096, 11008), (12, 4096, 4096), (12, 11008, 4096), (14, 4096, 11008),
+                 (14, 32000, 4096), (11, 4096, 4096), (11, 11008, 4096), (11, 4096, 11008), (13, 11008, 4096),
+                 (8, 11008, 4096)]
 # Q4_K_M-style mix on Llama-2-7B shapes: Q4_K attention + gate/up, Q6_K down + output
 KQ4_SHAPES = [(4096, 4096), (11008, 4096)]
 KQ6_SHAPES = [(4096, 11008), (32000, 4096)]
@@ -271,6 +276,22 @@ def gemm_counters(shapes, ns=(64, 512)):
             y.free()
             log(f"  counters: {M}x{K} N={N} done")
         w.free()
+
+
+def gemv_counters(cases=COUNTER_GEMVS):
+    """One N = 1 chatnet_matmul per (type, M, K), direct launches, each on its
+    own freshly uploaded weights, for counter collection."""
+    from chatnet_amd import hiprt, ops, synth
+
+    for (qt, M, K) in cases:
+        w = hiprt.DeviceBuffer.from_numpy(synth.tensor(qt, 7, f"gctr{qt}-{M}x{K}", M, K).data, pad=256)
+        x = hiprt.DeviceBuffer.from_numpy(synth.normal(99, f"gctrx{K}", K, 1.0))
+        y = hiprt.DeviceBuffer(4 * M)
+        ops.matmul_ptr(qt, w.ptr, x.ptr, y.ptr, M, K, 1, 0)
+        hiprt.synchronize()
+        for b in (w, x, y):
+            b.free()
+        log(f"  counters: type {qt} {M}x{K} done")
 
 
 def copy_rate(nbytes=512 << 20, reps=5):
@@ -517,6 +538,9 @@ def main():
     if args.only == "gemm_counters":
         log("gemm counter leg: one call per shape, N = 64 and 512")
         gemm_counters(SWEEP)
+    if args.only == "gemv_counters":
+        log("gemv counter leg: one N = 1 call per type and shape")
+        gemv_counters()
     if not args.roofline_only and not args.no_gemm and want("gemm_sweep"):
         log("gemm sweep N = 8, 64, 512 (cold)")
         gsweep = gemm_sweep(SWEEP, (8, 64, 512))
