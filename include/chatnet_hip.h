@@ -243,8 +243,10 @@ CHATNET_API int chatnet_get_logits(chatnet_model* m, float* logits_host);
  * zero).
  * Q4_0 with 2 <= N < 8, or N <= 16 with M*K*N <= 8*4096*4096, runs one
  * multi-column GEMV (each column the N = 1 product's exact arithmetic).  Other
- * calls with N >= 8 and a block type run the dequant-to-LDS bf16 MFMA GEMM (x
- * rounded to bf16; Q4_0 read as raw blocks, the other types first re-encoded
+ * calls with N >= 8 and a block type run the dequant-to-LDS fp16 MFMA GEMM (x
+ * rounded to fp16 after scaling each column by a power of two that keeps it
+ * inside fp16's range, each weight rounded once to fp16; Q4_0 read as raw
+ * blocks, the other types first re-encoded
  * into the workspace as u8 codes with an fp32 scale and offset per 16 weights,
  * M*(K/64)*96 bytes, giving the same dequantized values); any other call
  * (N < 8, F32, F16) runs the fused GEMV once per column, which reads Q4_1,
@@ -267,11 +269,12 @@ CHATNET_API int chatnet_matmul(uint32_t ggml_type, const void* w_dev, const floa
  * only as packed units (Q4_1, Q5_0, Q5_1, Q2_K, Q8_K and the IQ types,
  * whose packed copy of W, M*(K/64)*96 bytes, goes into the scratch); Q8_0,
  * Q3_K, Q4_K, Q5_K and Q6_K run the fused GEMV once per column on their stored
- * blocks.  The scratch (bf16 x, the K-split partials and the packed W) lives
+ * blocks.  The scratch (fp16 x, its per-column scales, the K-split partials
+ * and the packed W) lives
  * in a fixed 64 MiB array per device, held by the library from load to
  * process exit, instead of a per-stream workspace.  Calls needing more
- * scratch than that (N*K*2 bytes of x for N >= 8, rounded up to 256, plus the
- * partials, plus the packed W) fail with CHATNET_ERR_INVALID_ARG before
+ * scratch than that (N*K*2 bytes of x for N >= 8 and N*4 bytes of scales,
+ * each rounded up to 256, plus the partials, plus the packed W) fail with CHATNET_ERR_INVALID_ARG before
  * launching anything.  Every call on one device shares that device's array:
  * calls that may overlap on one device (different streams, threads) race and
  * must be serialized by the caller. */
