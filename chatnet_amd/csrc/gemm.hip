@@ -269,20 +269,37 @@ __device__ __forceinline__ void wg_barrier() {
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
 }
+// OFF: a constant byte offset carried in the instruction's offset field (no
+// address arithmetic for it).
+template <int OFF = 0>
 __device__ __forceinline__ cn_u32x4 lds_read128(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field is 16 bits");
   cn_u32x4 v;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
   return v;
 }
+template <int OFF = 0>
 __device__ __forceinline__ uint2 lds_read64(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field is 16 bits");
   uint2 v;
-  asm volatile("ds_read_b64 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+  asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
   return v;
 }
+template <int OFF = 0>
 __device__ __forceinline__ uint32_t lds_read32(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field is 16 bits");
   uint32_t v;
-  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+  asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
   return v;
+}
+// The x fragments of one MFMA step for column tiles CC .. TN-1: tile cc lies
+// 32 x-rows (4096 bytes) after tile cc-1, at the same swizzled chunk.
+template <int CC, int TN>
+__device__ __forceinline__ void lds_read_xtiles(uint32_t base, cn_u32x4 (&xr)[TN]) {
+  if constexpr (CC < TN) {
+    xr[CC] = lds_read128<CC * 4096>(base);
+    lds_read_xtiles<CC + 1, TN>(base, xr);
+  }
 }
 // Waits until at most N of this wave's LDS reads are outstanding.  A value
 // read by lds_read* must pass through reg_fence after the wait that covers it,
@@ -296,13 +313,16 @@ __device__ __forceinline__ void reg_fence(T& r) {
   asm volatile("" : "+v"(r));
 }
 
-// MT: 32-row tiles per wave (the waves stack along M, BM = 128 * MT rows per
-// workgroup); each x fragment read from LDS feeds MT MFMAs.
-template <bool PRECISE, int TN, int S, bool PK, int MT = 1>
+// MT: 32-row tiles per wave, TN: 32-column tiles per wave; each x fragment
+// read from LDS feeds MT MFMAs, each dequantized W fragment TN.  WNC: waves
+// along N (1: the four waves stack along M, BM = 128 * MT; 2: a 2 x 2 grid of
+// waves, BM = 64 * MT, BN = 64 * TN, each wave reading half the x tile).
+template <bool PRECISE, int TN, int S, bool PK, int MT = 1, int WNC = 1>
 struct PipeCfg {
   static constexpr int PL = PRECISE ? 2 : 1;
   static constexpr int MTILES = MT;
-  static constexpr int BM = 128 * MT, BN = 32 * TN;
+  static constexpr int WN = WNC, WM = 4 / WNC;  // waves along N and M
+  static constexpr int BM = 32 * WM * MT, BN = 32 * TN * WN;
   static constexpr int UNIT = PK ? kGemmPackUnit : 36;  // global bytes per row and chunk
   static constexpr int WP = PK ? 6 : 3;        // 16-byte pieces per row and chunk
   static constexpr int WROW = 16 * WP;         // LDS bytes per row and chunk
@@ -317,13 +337,14 @@ struct PipeCfg {
   static constexpr int VPS = PL * XI + WI;     // vector-memory instructions per stage per wave
   static constexpr int WD = PK ? 12 : 5;       // W dwords a lane reads per chunk
   static constexpr bool PACKED = PK;
+  static constexpr int TNW = TN;                // column tiles per wave
   static_assert(XPW % 64 == 0, "x pieces per wave must fill whole instructions");
 };
 
 // Tile coordinates, K range and stage loads of one workgroup (both kernels).
 template <class C>
 struct TileIO {
-  int lane, wave, h, li, ks, m0, n0, c_begin, c_end;
+  int lane, wave, wm, wn, h, li, ks, m0, n0, c_begin, c_end;
   const uint16_t* xsrc[C::PL][C::XI];
   const char* wsrc[C::WI];
   bool wact[C::WI];
@@ -331,6 +352,8 @@ struct TileIO {
   __device__ __forceinline__ explicit TileIO(const GemmArgs& a) {
     lane = threadIdx.x & 63;
     wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    wm = wave % C::WM;
+    wn = wave / C::WM;
     h = lane >> 5;
     li = lane & 31;
     const int n_nt = (a.N + C::BN - 1) / C::BN;
@@ -388,7 +411,7 @@ struct TileIO {
   // scales 2h, 2h+1 (unit bytes 64 + 8h) and offsets 2h, 2h+1 (80 + 8h).
   __device__ __forceinline__ void wraw(const char* st, uint32_t (&w)[C::WD], int mt = 0) const {
     const uint32_t* wb =
-        reinterpret_cast<const uint32_t*>(st + C::PL * C::XB + (wave * 32 * C::MTILES + 32 * mt + li) * C::WROW);
+        reinterpret_cast<const uint32_t*>(st + C::PL * C::XB + (wm * 32 * C::MTILES + 32 * mt + li) * C::WROW);
     if constexpr (C::PACKED) {
 #pragma unroll
       for (int i = 0; i < 8; i++) w[i] = wb[8 * h + i];
@@ -407,14 +430,14 @@ struct TileIO {
 
   // Where the 16-byte x fragment of MFMA step s, column tile cc, plane p lies.
   __device__ __forceinline__ const char* xfrag_ptr(const char* st, int p, int s, int cc) const {
-    const int xrow = 32 * cc + li;
+    const int xrow = wn * 32 * C::TNW + 32 * cc + li;
     const int phys = (4 * h + s) ^ ((xrow >> 1) & 7);
     return st + p * C::XB + xrow * 128 + phys * 16;
   }
 
   // The 16-byte x fragment of MFMA step s, column tile cc, plane p.
   __device__ __forceinline__ uint4 xfrag(const char* st, int p, int s, int cc) const {
-    const int xrow = 32 * cc + li;
+    const int xrow = wn * 32 * C::TNW + 32 * cc + li;
     const int phys = (4 * h + s) ^ ((xrow >> 1) & 7);
     return *reinterpret_cast<const uint4*>(st + p * C::XB + xrow * 128 + phys * 16);
   }
@@ -424,12 +447,12 @@ struct TileIO {
   __device__ __forceinline__ void store(const GemmArgs& a, const f32x16 (&acc)[TN], int mt = 0) const {
 #pragma unroll
     for (int cc = 0; cc < TN; cc++) {
-      const int n = n0 + 32 * cc + li;
+      const int n = n0 + wn * 32 * C::TNW + 32 * cc + li;
       // one-plane kernel: x of column n was scaled by 1 / xinv[n] (a power of two)
       const float sc = a.xinv ? a.xinv[n < a.N ? n : a.N - 1] : 1.0f;
 #pragma unroll
       for (int v4 = 0; v4 < 4; v4++) {
-        const int m = m0 + wave * 32 * C::MTILES + 32 * mt + 8 * v4 + 4 * h;
+        const int m = m0 + wm * 32 * C::MTILES + 32 * mt + 8 * v4 + 4 * h;
         const f32x4 v = f32x4{acc[cc][4 * v4], acc[cc][4 * v4 + 1], acc[cc][4 * v4 + 2], acc[cc][4 * v4 + 3]} * sc;
         if (a.splits > 1) {
           if (n < a.N && m < a.M) {
@@ -455,9 +478,9 @@ struct TileIO {
 // TN MFMAs (one v_mfma_f32_32x32x16_f16 per column tile).  Step s of lane
 // half h: Q4_0 qs dword s of block h; packed codes 32h + 4s .. +3 and
 // 32h + 16 + 4s .. +3 with the scale/offset pairs 2h and 2h+1.
-template <int TN, int S, bool PK, int MT>
+template <int TN, int S, bool PK, int MT, int WNC>
 __global__ __launch_bounds__(CN_BLOCK) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_p_kernel(GemmArgs a) {
-  using C = PipeCfg<false, TN, S, PK, MT>;
+  using C = PipeCfg<false, TN, S, PK, MT, WNC>;
   extern __shared__ __attribute__((aligned(16))) char lds[];
   const TileIO<C> io(a);
   const int h = io.h;
@@ -491,58 +514,77 @@ __global__ __launch_bounds__(CN_BLOCK) __attribute__((amdgpu_waves_per_eu(1, 2))
       uint32_t w[MT][C::WD];
 #pragma unroll
       for (int mt = 0; mt < MT; mt++) {
-        const uint32_t wb = lds_addr(st + C::PL * C::XB + (io.wave * 32 * MT + 32 * mt + io.li) * C::WROW);
+        // the W rows follow the x planes in the stage (offset WO)
+        constexpr int WO = C::PL * C::XB;
+        const uint32_t wb = lds_addr(st + (io.wm * 32 * MT + 32 * mt + io.li) * C::WROW);
         if constexpr (PK) {
-          const cn_u32x4 c0 = lds_read128(wb + 32 * h), c1 = lds_read128(wb + 32 * h + 16);
-          const uint2 sc = lds_read64(wb + 64 + 8 * h), of = lds_read64(wb + 80 + 8 * h);
+          const uint32_t wc = wb + 32 * h, ws = wb + 8 * h;
+          const cn_u32x4 c0 = lds_read128<WO>(wc), c1 = lds_read128<WO + 16>(wc);
+          const uint2 sc = lds_read64<WO + 64>(ws), of = lds_read64<WO + 80>(ws);
           w[mt][0] = c0[0], w[mt][1] = c0[1], w[mt][2] = c0[2], w[mt][3] = c0[3];
           w[mt][4] = c1[0], w[mt][5] = c1[1], w[mt][6] = c1[2], w[mt][7] = c1[3];
           w[mt][8] = sc.x, w[mt][9] = sc.y, w[mt][10] = of.x, w[mt][11] = of.y;
         } else {
-          const cn_u32x4 q = lds_read128(wb + 32 * h);
-          const uint32_t t = lds_read32(wb + 16);
+          const cn_u32x4 q = lds_read128<WO>(wb + 32 * h);
+          const uint32_t t = lds_read32<WO + 16>(wb);
           w[mt][0] = q[0], w[mt][1] = q[1], w[mt][2] = q[2], w[mt][3] = q[3], w[mt][4] = t;
         }
       }
       cn_u32x4 xr[4][TN];
 #pragma unroll
-      for (int s = 0; s < 4; s++)
+      for (int s = 0; s < 4; s++) lds_read_xtiles<0, TN>(lds_addr(io.xfrag_ptr(st, 0, s, 0)), xr[s]);
+      // Step s's W operands are dequantized during step s-1 (step 0's before
+      // the first MFMA) and interleaved with its MFMAs: one wave issues in
+      // order, so VALU work placed after a run of MFMAs waits behind them
+      // while the matrix pipe drains; between them it runs in their shadow.
+      auto dequant = [&](int s, int mt) -> f16x8 {
+        if constexpr (PK) {
+          return dequant_u8_h(w[mt][s], w[mt][4 + s], __uint_as_float(w[mt][8]), __uint_as_float(w[mt][10]),
+                              __uint_as_float(w[mt][9]), __uint_as_float(w[mt][11]));
+        } else {
+          const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(h ? (w[mt][4] >> 16) : (w[mt][0] & 0xFFFFu)));
+          return dequant_q4_h(__builtin_amdgcn_perm(w[mt][s + 1], w[mt][s], psel), magic, (cn_half2){d, d});
+        }
+      };
+      // the W dwords and step 0's fragments: reads issued after them are
+      // those of steps 1 .. 3
+      lds_wait<(3 * TN > 15 ? 15 : 3 * TN)>();
 #pragma unroll
-        for (int cc = 0; cc < TN; cc++) xr[s][cc] = lds_read128(lds_addr(io.xfrag_ptr(st, 0, s, cc)));
+      for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int i = 0; i < C::WD; i++) reg_fence(w[mt][i]);
+      f16x8 wa[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++) wa[mt] = dequant(0, mt);
 #pragma unroll
       for (int s = 0; s < 4; s++) {
-        // reads issued after step s's fragments: those of steps s+1 .. 3
-        if (s == 0) {
-          lds_wait<(3 * TN > 15 ? 15 : 3 * TN)>();
-#pragma unroll
-          for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-            for (int i = 0; i < C::WD; i++) reg_fence(w[mt][i]);
-        } else if (s == 1) {
-          lds_wait<2 * TN>();
-        } else if (s == 2) {
-          lds_wait<TN>();
-        } else {
-          lds_wait<0>();
-        }
+        if (s == 1) lds_wait<2 * TN>();
+        else if (s == 2) lds_wait<TN>();
+        else if (s == 3) lds_wait<0>();
 #pragma unroll
         for (int cc = 0; cc < TN; cc++) reg_fence(xr[s][cc]);
         f16x8 xh[TN];
 #pragma unroll
         for (int cc = 0; cc < TN; cc++) xh[cc] = __builtin_bit_cast(f16x8, xr[s][cc]);
+        f16x8 wn[MT];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
-          f16x8 wa;
-          if constexpr (PK) {
-            wa = dequant_u8_h(w[mt][s], w[mt][4 + s], __uint_as_float(w[mt][8]), __uint_as_float(w[mt][10]),
-                              __uint_as_float(w[mt][9]), __uint_as_float(w[mt][11]));
-          } else {
-            const _Float16 d =
-                __builtin_bit_cast(_Float16, (uint16_t)(h ? (w[mt][4] >> 16) : (w[mt][0] & 0xFFFFu)));
-            wa = dequant_q4_h(__builtin_amdgcn_perm(w[mt][s + 1], w[mt][s], psel), magic, (cn_half2){d, d});
+#pragma unroll
+          for (int cc = 0; cc < TN; cc++) acc[mt][cc] = mma32(wa[mt], xh[cc], acc[mt][cc]);
+        }
+        if (s < 3) {
+#pragma unroll
+          for (int mt = 0; mt < MT; mt++) wn[mt] = dequant(s + 1, mt);
+          // one MFMA, then a share of the next step's dequantization, ...
+          constexpr int kDequantValu = PK ? 24 : 14;  // VALU instructions per dequantized operand
+          constexpr int kPer = (kDequantValu * MT + MT * TN - 1) / (MT * TN);
+#pragma unroll
+          for (int i = 0; i < MT * TN; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, kPer, 0);
           }
 #pragma unroll
-          for (int cc = 0; cc < TN; cc++) acc[mt][cc] = mma32(wa, xh[cc], acc[mt][cc]);
+          for (int mt = 0; mt < MT; mt++) wa[mt] = wn[mt];
         }
         __builtin_amdgcn_sched_barrier(0);  // the next step's wait stays behind these MFMAs
       }
@@ -1147,16 +1189,16 @@ GemmShape pick_gemm(int M, int N, int K, int num_cus, bool precise, bool packed)
   return s;
 }
 
-template <int TN, int S, bool PK, int MT>
+template <int TN, int S, bool PK, int MT, int WNC = 1>
 hipError_t launch_p(const GemmArgs& a, int grid, hipStream_t st) {
-  constexpr int lds = PipeCfg<false, TN, S, PK, MT>::LDS;
+  constexpr int lds = PipeCfg<false, TN, S, PK, MT, WNC>::LDS;
   static_assert(lds <= 160 * 1024, "LDS ring exceeds the CU's 160 KB");
   static std::atomic<uint64_t> lds_done{0};
   if (lds > 64 * 1024) {
-    const hipError_t e = allow_full_lds(reinterpret_cast<const void*>(&gemm_p_kernel<TN, S, PK, MT>), lds_done);
+    const hipError_t e = allow_full_lds(reinterpret_cast<const void*>(&gemm_p_kernel<TN, S, PK, MT, WNC>), lds_done);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((gemm_p_kernel<TN, S, PK, MT>), dim3(grid), dim3(CN_BLOCK), lds, st, a);
+  hipLaunchKernelGGL((gemm_p_kernel<TN, S, PK, MT, WNC>), dim3(grid), dim3(CN_BLOCK), lds, st, a);
   return hipGetLastError();
 }
 
