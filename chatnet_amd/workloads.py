@@ -15,6 +15,20 @@ chatnet_amd.synth, and the prompt of (seed, prompt_stream, n_prompt).
                             down + output, 16-token prompt, 64 greedy tokens
     llama2_7b_q3_k_m_decode Llama-2-7B shape, Q3_K attention + gate/up, Q4_K
                             down, Q6_K output, 16-token prompt, 64 greedy tokens
+
+and, at the same 7B shape with a 16-token prompt and 16 greedy tokens, one
+workload per mix of the types the device reads as packed units (the
+reference's MatVecMulGeneric branches, LlamaModel.cs:488-562), so that each
+of them is checked at full depth and width:
+
+    llama2_7b_legacy_blocks_decode  Q4_1 attention and output, Q5_0 gate and
+                                    down, Q5_1 up
+    llama2_7b_q2_k_decode           Q2_K attention + gate/up, Q3_K down, Q8_K
+                                    output
+    llama2_7b_iq_a_decode           IQ4_XS attention, IQ3_XXS gate, IQ2_XS up,
+                                    IQ4_NL down, IQ1_M output
+    llama2_7b_iq_b_decode           IQ3_S attention, IQ2_S gate/up, IQ2_XXS
+                                    down, IQ1_S output
 """
 from __future__ import annotations
 
@@ -49,6 +63,11 @@ WORKLOADS = {w.name: w for w in (
     Workload("llama2_7b_q4_0_decode", LLAMA2_7B.replace(context_length=2048), 7, "q4_0", "prompt", 128, 256),
     Workload("llama2_7b_q4_k_m_decode", LLAMA2_7B.replace(context_length=2048), 11, "q4_k_m", "prompt", 16, 64),
     Workload("llama2_7b_q3_k_m_decode", LLAMA2_7B.replace(context_length=2048), 13, "q3_k_m", "prompt", 16, 64),
+    Workload("llama2_7b_legacy_blocks_decode", LLAMA2_7B.replace(context_length=2048), 21, "legacy_blocks", "prompt",
+             16, 16),
+    Workload("llama2_7b_q2_k_decode", LLAMA2_7B.replace(context_length=2048), 22, "q2_k", "prompt", 16, 16),
+    Workload("llama2_7b_iq_a_decode", LLAMA2_7B.replace(context_length=2048), 23, "iq_a", "prompt", 16, 16),
+    Workload("llama2_7b_iq_b_decode", LLAMA2_7B.replace(context_length=2048), 24, "iq_b", "prompt", 16, 16),
 )}
 
 
