@@ -915,7 +915,7 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position, SpanM
       void* vc = (char*)m->vcache + loff;
       // the previous layer's down projection may have left its K-split
       // partials: the residual add completes here, with the norm
-      HIP_TRY(add_rmsnorm_bf16_launch(m->sp_x, m->sp_part, pending, (const float*)L.attn_norm.ptr, c.rms_norm_eps,
+      HIP_TRY(add_rmsnorm_span_launch(m->sp_x, m->sp_part, pending, (const float*)L.attn_norm.ptr, c.rms_norm_eps,
                                       m->sp_xb, xb_lo, cn, c.dim, st));
       pending = 0;
       GemmArgs g;
@@ -992,7 +992,7 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position, SpanM
       o.ldy = c.dim;
       if ((rc = span_gemm(m, o, defer))) return rc;
 
-      HIP_TRY(add_rmsnorm_bf16_launch(m->sp_x, m->sp_part, pending, (const float*)L.ffn_norm.ptr, c.rms_norm_eps,
+      HIP_TRY(add_rmsnorm_span_launch(m->sp_x, m->sp_part, pending, (const float*)L.ffn_norm.ptr, c.rms_norm_eps,
                                       m->sp_xb, xb_lo, cn, c.dim, st));
       pending = 0;
       GemmArgs gu;

@@ -6,15 +6,15 @@
 // (LlamaModel.cs:93-238) need.
 //
 // W is read either as raw Q4_0 blocks or as packed units (gemm_pack_kernel:
-// any of Q4_0, Q8_0, Q4_K, Q5_K, Q6_K re-encoded once as u8 codes with an fp32
-// scale and offset per 16 weights); x arrives from the producer kernel
-// (conversion, RMSNorm, attention or the SwiGLU epilogue) either as one bf16
-// plane [N][K] (chatnet_matmul) or, for the exact-weight variant the spans
-// run, as fp16 hi + lo planes in the cn_span_pos order.  W bytes and x tiles
-// stream through an LDS ring by direct global->LDS loads; each wave
-// dequantizes its W rows into v_mfma_f32_32x32x16_bf16 (one plane) or
-// v_mfma_f32_32x32x16_f16 (exact-weight) operands in registers and
-// accumulates in fp32.  When the tile grid leaves the chip
+// the other block types re-encoded as u8 codes with an fp32 scale and offset
+// per 16 weights); x arrives from the producer kernel in the cn_span_pos
+// order, either as one fp16 plane scaled per column by a power of two
+// (to_f16_scaled_kernel, chatnet_matmul) or, for the exact-weight variant the
+// spans run, as fp16 hi + lo planes (conversion, RMSNorm, attention or the
+// SwiGLU epilogue).  W bytes and x tiles stream through an LDS ring by direct
+// global->LDS loads; each wave dequantizes its W rows into
+// v_mfma_f32_32x32x16_f16 operands in registers (one rounded plane, or two
+// exact planes) and accumulates in fp32.  When the tile grid leaves the chip
 // under-filled the K range is split and gemm_reduce_kernel sums the partial
 // tiles and applies the epilogue.  Epilogues: STORE y = acc, ADD y += acc
 // (residual), SWIGLU (rows interleave gate/up; h = silu(gate)*up is written
@@ -59,23 +59,14 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * u * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));
 }
 
-__device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
-  const __bf16 a = (__bf16)lo, b = (__bf16)hi;
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
-}
-
-// h[n][j] = silu(gate) * up: bf16 in natural order (one plane), or fp16 hi +
-// lo planes in the span order (cn_span_pos) when hb_lo is set.
+// h[n][j] = silu(gate) * up as the next span GEMM's input: fp16 hi + lo
+// planes in the span order (cn_span_pos).
 __device__ __forceinline__ void write_h(const GemmArgs& a, int n, int j, float v) {
-  if (a.hb_lo) {
-    const size_t i = (size_t)n * a.ldh + cn_span_pos(j);
-    uint32_t hi, lo;
-    cn_split_f16x2(v, 0.f, hi, lo);
-    a.hb[i] = (uint16_t)hi;
-    a.hb_lo[i] = (uint16_t)lo;
-  } else {
-    a.hb[(size_t)n * a.ldh + j] = __builtin_bit_cast(uint16_t, (__bf16)v);
-  }
+  const size_t i = (size_t)n * a.ldh + cn_span_pos(j);
+  uint32_t hi, lo;
+  cn_split_f16x2(v, 0.f, hi, lo);
+  a.hb[i] = (uint16_t)hi;
+  a.hb_lo[i] = (uint16_t)lo;
 }
 
 // Final write of 4 consecutive rows m..m+3 of column n.
@@ -87,15 +78,11 @@ __device__ __forceinline__ void write_out4(const GemmArgs& a, int epi, int n, in
     // (m/2 even: the two stay adjacent in the span order too)
     if (m + 3 < a.M) {
       const float h0 = silu_mul(v[0], v[1]), h1 = silu_mul(v[2], v[3]);
-      if (a.hb_lo) {
-        const size_t i = (size_t)n * a.ldh + cn_span_pos(m >> 1);
-        uint32_t hi, lo;
-        cn_split_f16x2(h0, h1, hi, lo);
-        *reinterpret_cast<uint32_t*>(a.hb + i) = hi;
-        *reinterpret_cast<uint32_t*>(a.hb_lo + i) = lo;
-      } else {
-        *reinterpret_cast<uint32_t*>(a.hb + (size_t)n * a.ldh + (m >> 1)) = pack2_bf16(h0, h1);
-      }
+      const size_t i = (size_t)n * a.ldh + cn_span_pos(m >> 1);
+      uint32_t hi, lo;
+      cn_split_f16x2(h0, h1, hi, lo);
+      *reinterpret_cast<uint32_t*>(a.hb + i) = hi;
+      *reinterpret_cast<uint32_t*>(a.hb_lo + i) = lo;
     } else {
       write_h(a, n, m >> 1, silu_mul(v[0], v[1]));
     }
@@ -746,15 +733,15 @@ __global__ __launch_bounds__(CN_BLOCK) void to_f16_scaled_kernel(const float* __
   }
 }
 
-// RMSNorm of each row (TensorMath.RmsNorm, TensorMath.cs:97-165) written for
-// the next GEMM: xb[r] = bf16((x[r] * rms_r) * g) in natural order, or with
-// xb_lo the span GEMM's two fp16 planes in the cn_span_pos order.  One workgroup per row, the row held in registers between the sum of
+// RMSNorm of each row (TensorMath.RmsNorm, TensorMath.cs:97-165) written as
+// the next span GEMM's input: (x[r] * rms_r) * g as fp16 hi + lo planes
+// (xb, xb_lo) in the cn_span_pos order.  One workgroup per row, the row held in registers between the sum of
 // squares and the scaling (one pass over memory).  With `part` (splits > 0)
 // the row is first completed as a residual add of the preceding GEMM's K-split
 // partials [splits][rows][dim], summed in split order exactly as
 // gemm_reduce_kernel does (x += ((0 + p0) + p1) + ...), and written back to x.
 template <int V, int SPL>
-__global__ __launch_bounds__(CN_BLOCK) void add_rmsnorm_bf16_kernel(float* __restrict__ x,
+__global__ __launch_bounds__(CN_BLOCK) void add_rmsnorm_span_kernel(float* __restrict__ x,
                                                                    const float* __restrict__ part, int splits,
                                                                    const float* __restrict__ g, float eps,
                                                                    uint16_t* __restrict__ xb,
@@ -808,17 +795,13 @@ __global__ __launch_bounds__(CN_BLOCK) void add_rmsnorm_bf16_kernel(float* __res
     if (i >= dim) continue;
     const float4 w = *reinterpret_cast<const float4*>(g + i);
     const float y0 = v[j][0] * rms * w.x, y1 = v[j][1] * rms * w.y, y2 = v[j][2] * rms * w.z, y3 = v[j][3] * rms * w.w;
-    if (xb_lo) {
-      // the four elements stay adjacent in the span order
-      const int pos = cn_span_pos(i);
-      uint2 hh, ll;
-      cn_split_f16x2(y0, y1, hh.x, ll.x);
-      cn_split_f16x2(y2, y3, hh.y, ll.y);
-      *reinterpret_cast<uint2*>(o + pos) = hh;
-      *reinterpret_cast<uint2*>(xb_lo + row * dim + pos) = ll;
-    } else {
-      *reinterpret_cast<uint2*>(o + i) = make_uint2(pack2_bf16(y0, y1), pack2_bf16(y2, y3));
-    }
+    // the four elements stay adjacent in the span order
+    const int pos = cn_span_pos(i);
+    uint2 hh, ll;
+    cn_split_f16x2(y0, y1, hh.x, ll.x);
+    cn_split_f16x2(y2, y3, hh.y, ll.y);
+    *reinterpret_cast<uint2*>(o + pos) = hh;
+    *reinterpret_cast<uint2*>(xb_lo + row * dim + pos) = ll;
   }
 }
 
@@ -1305,6 +1288,7 @@ hipError_t gemm_launch(const GemmArgs& a_in, int num_cus, hipStream_t st, int* s
   // partials can be left only for a store or a residual add (the folding
   // kernels apply no other epilogue)
   if (splits_left && a_in.epi != GEMV_EPI_STORE && a_in.epi != GEMV_EPI_ADD) return hipErrorInvalidValue;
+  if (a_in.epi == GEMV_EPI_SWIGLU && (!a_in.hb || !a_in.hb_lo)) return hipErrorInvalidValue;
   const GemmShape s = pick_gemm(a_in.M, a_in.N, a_in.K, num_cus, precise, a_in.packed != 0);
   GemmArgs a = a_in;
   a.splits = s.splits;
@@ -1340,22 +1324,22 @@ void add_rmsnorm_v(float* x, const float* part, int splits, const float* g, floa
                    int rows, int dim, hipStream_t st) {
   const dim3 grid(rows), block(CN_BLOCK);
   if (V > 4 || splits <= 0) {  // wide rows: the norm alone (no partials folded)
-    hipLaunchKernelGGL((add_rmsnorm_bf16_kernel<V, 0>), grid, block, 0, st, x, part, 0, g, eps, xb, xb_lo, rows, dim);
+    hipLaunchKernelGGL((add_rmsnorm_span_kernel<V, 0>), grid, block, 0, st, x, part, 0, g, eps, xb, xb_lo, rows, dim);
     return;
   }
   if constexpr (V <= 4) {
-  if (splits <= 0) hipLaunchKernelGGL((add_rmsnorm_bf16_kernel<V, 0>), grid, block, 0, st, x, part, 0, g, eps, xb, xb_lo, rows, dim);
-  else if (splits <= 2) hipLaunchKernelGGL((add_rmsnorm_bf16_kernel<V, 2>), grid, block, 0, st, x, part, splits, g, eps, xb, xb_lo, rows, dim);
-  else if (splits <= 4) hipLaunchKernelGGL((add_rmsnorm_bf16_kernel<V, 4>), grid, block, 0, st, x, part, splits, g, eps, xb, xb_lo, rows, dim);
-  else if (splits <= 8) hipLaunchKernelGGL((add_rmsnorm_bf16_kernel<V, 8>), grid, block, 0, st, x, part, splits, g, eps, xb, xb_lo, rows, dim);
-  else hipLaunchKernelGGL((add_rmsnorm_bf16_kernel<V, 16>), grid, block, 0, st, x, part, splits, g, eps, xb, xb_lo, rows, dim);
+  if (splits <= 0) hipLaunchKernelGGL((add_rmsnorm_span_kernel<V, 0>), grid, block, 0, st, x, part, 0, g, eps, xb, xb_lo, rows, dim);
+  else if (splits <= 2) hipLaunchKernelGGL((add_rmsnorm_span_kernel<V, 2>), grid, block, 0, st, x, part, splits, g, eps, xb, xb_lo, rows, dim);
+  else if (splits <= 4) hipLaunchKernelGGL((add_rmsnorm_span_kernel<V, 4>), grid, block, 0, st, x, part, splits, g, eps, xb, xb_lo, rows, dim);
+  else if (splits <= 8) hipLaunchKernelGGL((add_rmsnorm_span_kernel<V, 8>), grid, block, 0, st, x, part, splits, g, eps, xb, xb_lo, rows, dim);
+  else hipLaunchKernelGGL((add_rmsnorm_span_kernel<V, 16>), grid, block, 0, st, x, part, splits, g, eps, xb, xb_lo, rows, dim);
   }
 }
 
-hipError_t add_rmsnorm_bf16_launch(float* x, const float* part, int splits, const float* g, float eps, uint16_t* xb,
+hipError_t add_rmsnorm_span_launch(float* x, const float* part, int splits, const float* g, float eps, uint16_t* xb,
                                    uint16_t* xb_lo, int rows, int dim, hipStream_t st) {
   if (dim % 4 || dim <= 0 || rows <= 0 || splits > 16 || (splits > 0 && !part)) return hipErrorInvalidValue;
-  if (xb_lo && dim % 32) return hipErrorInvalidValue;  // the span order permutes blocks of 32
+  if (!xb || !xb_lo || dim % 32) return hipErrorInvalidValue;  // the span order permutes blocks of 32
   const int v = (dim + 4 * CN_BLOCK - 1) / (4 * CN_BLOCK);  // float4 per thread
   // at most 4 float4 per thread when partials are folded (the register budget of
   // 16 splits x 4 float4), 16 for the norm alone
@@ -1368,7 +1352,3 @@ hipError_t add_rmsnorm_bf16_launch(float* x, const float* part, int splits, cons
   return hipGetLastError();
 }
 
-hipError_t rmsnorm_bf16_launch(const float* x, const float* g, float eps, uint16_t* xb, uint16_t* xb_lo, int rows,
-                               int dim, hipStream_t st) {
-  return add_rmsnorm_bf16_launch(const_cast<float*>(x), nullptr, 0, g, eps, xb, xb_lo, rows, dim, st);
-}

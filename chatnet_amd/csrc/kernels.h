@@ -88,7 +88,8 @@ hipError_t gemv_float_launch(int qtype, int epi, const GemvArgs& a, int num_cus,
 // Batched quantized GEMM on the matrix cores (gemm.hip):
 //   acc[n][vr] = sum_k W_vr[k] * xb[n][k],  0 <= n < N, 0 <= vr < M
 // epilogue `epi`: GEMV_EPI_STORE y[n*ldy+vr] = acc, GEMV_EPI_ADD y += acc,
-// GEMV_EPI_SWIGLU hb[n*ldh+vr/2] = bf16(silu(acc[vr even]) * acc[vr odd]).
+// GEMV_EPI_SWIGLU h[n][vr/2] = silu(acc[vr even]) * acc[vr odd] as fp16 hi + lo
+// planes (hb, hb_lo) in the cn_span_pos order.
 enum { GEMM_SEG_SINGLE = 0, GEMM_SEG_CONCAT = 1, GEMM_SEG_INTERLEAVE = 2 };
 struct GemmArgs {
   int qtype;
@@ -105,8 +106,8 @@ struct GemmArgs {
   int epi;
   float* y;               // STORE / ADD target
   int ldy;
-  uint16_t* hb;           // SWIGLU target: bf16, or fp16 high parts with hb_lo
-  uint16_t* hb_lo;        // optional fp16 low parts of h (then both planes in the cn_span_pos order)
+  uint16_t* hb;           // SWIGLU target: fp16 high parts of h (cn_span_pos order)
+  uint16_t* hb_lo;        // SWIGLU target: fp16 low parts of h
   int ldh;
   float* part;            // K-split partials, gemm_workspace_bytes() bytes
   int splits;             // set by gemm_launch
@@ -125,20 +126,17 @@ size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool precise, bool
 // With splits_left, a launch whose K is split leaves its partial tiles in
 // a.part ([splits][N][M]) unreduced and reports the split count there (0 when
 // the epilogue ran): the caller folds them into its next kernel
-// (add_rmsnorm_bf16_launch for a residual add).
+// (add_rmsnorm_span_launch for a residual add).
 hipError_t gemm_launch(const GemmArgs& a, int num_cus, hipStream_t st, int* splits_left = nullptr);
 // x [N][K] fp32 -> the one-plane GEMM's input: xh[n] = fp16(x[n] * 2^e_n) in
 // the cn_span_pos order, 2^e_n bringing max|x[n]| into [2^14, 2^15), and
 // xinv[n] = 2^-e_n.  K % 32 == 0, K <= 16384.
 hipError_t to_f16_scaled_launch(const float* x, uint16_t* xh, float* xinv, int N, int K, hipStream_t st);
-// xb = bf16(RMSNorm(x) * g) per row; with xb_lo the span GEMM's input instead
-// (fp16 hi + lo planes in the cn_span_pos order, dim % 32 == 0).
-hipError_t rmsnorm_bf16_launch(const float* x, const float* g, float eps, uint16_t* xb, uint16_t* xb_lo, int rows,
-                               int dim, hipStream_t st);
 // x[r] += the K-split partials part[0..splits)[r] (summed as the GEMM's reduce
-// does), then xb / xb_lo = RMSNorm(x[r]) * g as rmsnorm_bf16_launch; splits 0:
-// the norm alone.  dim <= 16384, and dim <= 4096 with splits (at most 16).
-hipError_t add_rmsnorm_bf16_launch(float* x, const float* part, int splits, const float* g, float eps, uint16_t* xb,
+// does), then xb / xb_lo = RMSNorm(x[r]) * g as the span GEMM's input (fp16 hi
+// + lo planes in the cn_span_pos order); splits 0: the norm alone.  dim % 32
+// == 0, dim <= 16384, and dim <= 4096 with splits (at most 16).
+hipError_t add_rmsnorm_span_launch(float* x, const float* part, int splits, const float* g, float eps, uint16_t* xb,
                                    uint16_t* xb_lo, int rows, int dim, hipStream_t st);
 
 // Span kernels (prefill.hip).  qkv is [n][ld] fp32 with q | k | v columns.
@@ -166,8 +164,8 @@ struct PrefillAttnArgs {
   int ld;
   const void* kc;    // layer base, [ctx][kv_dim]
   const void* vc;
-  uint16_t* out;     // [n][ldo]: bf16, or fp16 high parts with out_lo
-  uint16_t* out_lo;  // optional fp16 low parts (then both planes in the cn_span_pos order)
+  uint16_t* out;     // [n][ldo]: fp16 high parts, cn_span_pos order
+  uint16_t* out_lo;  // [n][ldo]: fp16 low parts
   int ldo;
   int n, p0, n_heads, kv_mul, head_dim, kv_dim, kv_f16;
   float scale;

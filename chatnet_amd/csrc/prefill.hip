@@ -151,9 +151,8 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
 // each SIMD and the chain of chunks per group is half as long; group 1 hands
 // its softmax state and unnormalised output to group 0 through LDS at the end.
 // Each group's next chunk is loaded into registers while it computes the
-// current one.  The output is written for the O-projection GEMM: bf16 in
-// natural order, or with out_lo the span GEMM's fp16 hi + lo planes in the
-// cn_span_pos order.
+// current one.  The output is written for the O-projection span GEMM: fp16
+// hi + lo planes (out, out_lo) in the cn_span_pos order.
 constexpr int kSpanThreads = 512;
 
 template <int HD>
@@ -399,17 +398,11 @@ __global__ __launch_bounds__(kSpanThreads) void attn_prefill_kernel(PrefillAttnA
     const float v0 = o[i][0] * s0 + o1.x * s1, v1 = o[i][1] * s0 + o1.y * s1, v2 = o[i][2] * s0 + o1.z * s1,
                 v3 = o[i][3] * s0 + o1.w * s1;
     const int e = hh * HD + 4 * g + 16 * i;  // four adjacent elements, also in the span order
-    if (a.out_lo) {
-      uint2 hi, lo;
-      cn_split_f16x2(v0, v1, hi.x, lo.x);
-      cn_split_f16x2(v2, v3, hi.y, lo.y);
-      *reinterpret_cast<uint2*>(a.out + row + cn_span_pos(e)) = hi;
-      *reinterpret_cast<uint2*>(a.out_lo + row + cn_span_pos(e)) = lo;
-    } else {
-      uint2 hi, lo;
-      split4(v0, v1, v2, v3, hi, lo);
-      *reinterpret_cast<uint2*>(a.out + row + e) = hi;
-    }
+    uint2 hi, lo;
+    cn_split_f16x2(v0, v1, hi.x, lo.x);
+    cn_split_f16x2(v2, v3, hi.y, lo.y);
+    *reinterpret_cast<uint2*>(a.out + row + cn_span_pos(e)) = hi;
+    *reinterpret_cast<uint2*>(a.out_lo + row + cn_span_pos(e)) = lo;
   }
 }
 
@@ -439,7 +432,7 @@ bool attn_prefill_supports(int head_dim, int kv_mul) {
 }
 
 hipError_t attn_prefill_launch(const PrefillAttnArgs& a, hipStream_t st) {
-  if (!attn_prefill_supports(a.head_dim, a.kv_mul) || a.n <= 0) return hipErrorInvalidValue;
+  if (!attn_prefill_supports(a.head_dim, a.kv_mul) || a.n <= 0 || !a.out || !a.out_lo) return hipErrorInvalidValue;
   if (a.head_dim == 64) return a.kv_f16 ? attn_prefill_t<64, true>(a, st) : attn_prefill_t<64, false>(a, st);
   return a.kv_f16 ? attn_prefill_t<128, true>(a, st) : attn_prefill_t<128, false>(a, st);
 }
