@@ -429,14 +429,26 @@ struct TileIO {
     return *reinterpret_cast<const uint4*>(st + p * C::XB + xrow * 128 + phys * 16);
   }
 
-  // Final tiles: K-split partials [splits][N][M] or the epilogue.
+  // The output scale of each of the lane's columns: the one-plane kernel's x
+  // of column n was scaled by 1 / xinv[n] (a power of two); 1 otherwise.
+  // Loaded at the kernel's start, so the epilogue does not wait for it.
   template <int TN>
-  __device__ __forceinline__ void store(const GemmArgs& a, const f32x16 (&acc)[TN], int mt = 0) const {
+  __device__ __forceinline__ void load_scales(const GemmArgs& a, float (&sc)[TN]) const {
 #pragma unroll
     for (int cc = 0; cc < TN; cc++) {
       const int n = n0 + wn * 32 * C::TNW + 32 * cc + li;
-      // one-plane kernel: x of column n was scaled by 1 / xinv[n] (a power of two)
-      const float sc = a.xinv ? a.xinv[n < a.N ? n : a.N - 1] : 1.0f;
+      sc[cc] = a.xinv ? a.xinv[n < a.N ? n : a.N - 1] : 1.0f;
+    }
+  }
+
+  // Final tiles: K-split partials [splits][N][M] or the epilogue.
+  template <int TN>
+  __device__ __forceinline__ void store(const GemmArgs& a, const f32x16 (&acc)[TN], const float (&scl)[TN],
+                                        int mt = 0) const {
+#pragma unroll
+    for (int cc = 0; cc < TN; cc++) {
+      const int n = n0 + wn * 32 * C::TNW + 32 * cc + li;
+      const float sc = scl[cc];
 #pragma unroll
       for (int v4 = 0; v4 < 4; v4++) {
         const int m = m0 + wm * 32 * C::MTILES + 32 * mt + 8 * v4 + 4 * h;
@@ -471,6 +483,8 @@ __global__ __launch_bounds__(CN_BLOCK) __attribute__((amdgpu_waves_per_eu(1, 2))
   extern __shared__ __attribute__((aligned(16))) char lds[];
   const TileIO<C> io(a);
   const int h = io.h;
+  float xsc[TN];
+  io.template load_scales<TN>(a, xsc);
 
   f32x16 acc[MT][TN];
 #pragma unroll
@@ -578,7 +592,7 @@ __global__ __launch_bounds__(CN_BLOCK) __attribute__((amdgpu_waves_per_eu(1, 2))
     }
   }
 #pragma unroll
-  for (int mt = 0; mt < MT; mt++) io.template store<TN>(a, acc[mt], mt);
+  for (int mt = 0; mt < MT; mt++) io.template store<TN>(a, acc[mt], xsc, mt);
 }
 
 // Span kernel (the exact-weight product of the forward pass's spans: fp16 x
@@ -667,7 +681,9 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_s_kernel(GemmArgs a) {
       }
     }
   }
-  io.template store<TN>(a, acc);
+  float sc[TN];
+  io.template load_scales<TN>(a, sc);
+  io.template store<TN>(a, acc, sc);
 }
 
 // Sums the K-split partials [splits][N][M] and applies the epilogue; one
