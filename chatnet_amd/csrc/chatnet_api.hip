@@ -806,38 +806,63 @@ struct LayerMats {
 };
 LayerMats layer_mats(Layer& L) { return {{&L.wq, &L.wk, &L.wv, &L.wo, &L.wg, &L.wu, &L.wd}}; }
 
-// How a span's projections read their weights: raw Q4_0 blocks when every
-// matrix is Q4_0, else packed units of every matrix (any packable types, mixed
-// freely); SPAN_NONE when some matrix can be neither (F32 / F16) and the span
-// runs token by token.
-enum SpanMode { SPAN_NONE = 0, SPAN_RAW_Q4_0 = 1, SPAN_PACKED = 2 };
+// How a span's projections read their weights, per GEMM of the layer (QKV,
+// O, gate/up, down): F16 and F32 matrices as their own rows (GEMM_W_F16 /
+// GEMM_W_F32), block types as raw Q4_0 blocks when every block-typed
+// projection is Q4_0, else as packed units (types mixed freely).  The
+// matrices one GEMM concatenates (q|k|v) or interleaves (gate/up) must share
+// that format; a span whose layers cannot (ffn_gate Q4_0 with ffn_up F16, a
+// type neither packable nor float) runs token by token.
+enum { SG_QKV = 0, SG_O = 1, SG_GU = 2, SG_D = 3 };
+struct SpanPlan {
+  bool ok = false;
+  int fmt[4] = {};
+};
 
-SpanMode span_mode(chatnet_model* m, int n) {
-  if (n < kSpanMin) return SPAN_NONE;
+SpanPlan span_plan(chatnet_model* m, int n) {
+  SpanPlan p;
+  if (n < kSpanMin) return p;
   const char* e = getenv("CHATNET_SPAN_BATCH");  // "0": per-token schedule for every span
-  if (e && e[0] == '0') return SPAN_NONE;
+  if (e && e[0] == '0') return p;
   const chatnet_config& c = m->cfg;
-  if (!attn_prefill_supports(c.head_dim, c.n_heads / c.n_kv_heads)) return SPAN_NONE;
-  bool all_q4_0 = true, packable = true;
+  if (!attn_prefill_supports(c.head_dim, c.n_heads / c.n_kv_heads)) return p;
+  // the class of a matrix: a float format, 1 for any block type, -1 for none
+  auto cls = [](const DevTensor* t) -> int {
+    if (t->type == CHATNET_GGML_F16) return GEMM_W_F16;
+    if (t->type == CHATNET_GGML_F32) return GEMM_W_F32;
+    if (t->ne0 % 64 == 0 && gemm_pack_supports((int)t->type, (int)t->ne0)) return GEMM_W_PACKED;
+    return -1;
+  };
+  const int group_of[7] = {SG_QKV, SG_QKV, SG_QKV, SG_O, SG_GU, SG_GU, SG_D};
+  int gcls[4] = {0, 0, 0, 0};  // 0: not seen yet
+  bool all_q4_0 = true;
   for (Layer& L : m->layers) {
     const LayerMats lm = layer_mats(L);
     for (int i = 0; i < 7; i++) {
       const DevTensor* t = lm.t[i];
-      if (t->type != CHATNET_GGML_Q4_0 || !gemm_supports(CHATNET_GGML_Q4_0, (int)t->ne0)) all_q4_0 = false;
-      if (!gemm_pack_supports((int)t->type, (int)t->ne0)) packable = false;
+      const int k = cls(t);
+      if (k < 0) return p;
+      int& g = gcls[group_of[i]];
+      if (g == 0) g = k;
+      else if (g != k) return p;
+      if (k == GEMM_W_PACKED && (t->type != CHATNET_GGML_Q4_0 || !gemm_supports(CHATNET_GGML_Q4_0, (int)t->ne0)))
+        all_q4_0 = false;
     }
   }
-  if (all_q4_0) return SPAN_RAW_Q4_0;
-  return packable ? SPAN_PACKED : SPAN_NONE;
+  for (int g = 0; g < 4; g++) p.fmt[g] = gcls[g] == GEMM_W_PACKED ? (all_q4_0 ? GEMM_W_Q4_0 : GEMM_W_PACKED) : gcls[g];
+  p.ok = true;
+  return p;
 }
 
-// Packs every projection matrix not yet packed (once per upload).
-int ensure_span_packs(chatnet_model* m) {
+// Packs every projection matrix of a packed-unit GEMM not yet packed (once
+// per upload).
+int ensure_span_packs(chatnet_model* m, const SpanPlan& plan) {
+  const int group_of[7] = {SG_QKV, SG_QKV, SG_QKV, SG_O, SG_GU, SG_GU, SG_D};
   for (Layer& L : m->layers) {
     const LayerMats lm = layer_mats(L);
     for (int i = 0; i < 7; i++) {
       DevTensor* t = lm.t[i];
-      if (t->pk) continue;
+      if (t->pk || plan.fmt[group_of[i]] != GEMM_W_PACKED) continue;
       const size_t bytes = gemm_pack_bytes((int)t->ne1, (int)t->ne0);
       if (hipMalloc(&t->pk, bytes) != hipSuccess) {
         t->pk = nullptr;
@@ -869,7 +894,7 @@ int ensure_span_buffers(chatnet_model* m) {
 
 int span_gemm(chatnet_model* m, GemmArgs& g, int* splits_left = nullptr) {
   g.precise = 1;
-  const size_t need = gemm_workspace_bytes(g.M, g.N, g.K, m->num_cus, true, g.packed != 0);
+  const size_t need = gemm_workspace_bytes(g.M, g.N, g.K, m->num_cus, true, g.packed);
   if (need > m->sp_part_bytes) {
     HIP_TRY(hipStreamSynchronize(m->stream));
     if (m->sp_part) (void)hipFree(m->sp_part);
@@ -886,15 +911,16 @@ int span_gemm(chatnet_model* m, GemmArgs& g, int* splits_left = nullptr) {
 
 // LlamaModel.Forward (LlamaModel.cs:93-238) over tokens[0..n) at positions
 // position.. as batches of up to span_cap tokens: every projection is one
-// MFMA GEMM over the batch (raw Q4_0 blocks, or every matrix packed), attention
+// MFMA GEMM over the batch (its weights read as `plan` says), attention
 // is causal over the cache, and the LM head runs for the last token only
 // (LlamaModel.cs:207).
-int run_span(chatnet_model* m, const int32_t* tokens, int n, int position, SpanMode mode) {
+int run_span(chatnet_model* m, const int32_t* tokens, int n, int position, const SpanPlan& plan) {
   int rc = ensure_span_buffers(m);
   if (rc) return rc;
-  const bool packed = mode == SPAN_PACKED;
-  if (packed && (rc = ensure_span_packs(m))) return rc;
-  auto wsrc = [packed](const DevTensor& t) { return (const uint8_t*)(packed ? t.pk : t.ptr); };
+  if ((rc = ensure_span_packs(m, plan))) return rc;
+  auto wsrc = [&plan](const DevTensor& t, int grp) {
+    return (const uint8_t*)(plan.fmt[grp] == GEMM_W_PACKED ? t.pk : t.ptr);
+  };
   const chatnet_config& c = m->cfg;
   hipStream_t st = m->stream;
   const int kvd = m->kv_dim, qkv_ld = c.dim + 2 * kvd;
@@ -921,10 +947,10 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position, SpanM
       GemmArgs g;
       memset(&g, 0, sizeof(g));
       g.qtype = CHATNET_GGML_Q4_0;
-      g.packed = packed;
-      g.w[0] = wsrc(L.wq);
-      g.w[1] = wsrc(L.wk);
-      g.w[2] = wsrc(L.wv);
+      g.packed = plan.fmt[SG_QKV];
+      g.w[0] = wsrc(L.wq, SG_QKV);
+      g.w[1] = wsrc(L.wk, SG_QKV);
+      g.w[2] = wsrc(L.wv, SG_QKV);
       g.seg_rows[0] = c.dim;
       g.seg_rows[1] = kvd;
       g.seg_rows[2] = kvd;
@@ -979,8 +1005,8 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position, SpanM
       GemmArgs o;
       memset(&o, 0, sizeof(o));
       o.qtype = CHATNET_GGML_Q4_0;
-      o.packed = packed;
-      o.w[0] = wsrc(L.wo);
+      o.packed = plan.fmt[SG_O];
+      o.w[0] = wsrc(L.wo, SG_O);
       o.seg_rows[0] = c.dim;
       o.M = c.dim;
       o.K = c.dim;
@@ -998,9 +1024,9 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position, SpanM
       GemmArgs gu;
       memset(&gu, 0, sizeof(gu));
       gu.qtype = CHATNET_GGML_Q4_0;
-      gu.packed = packed;
-      gu.w[0] = wsrc(L.wg);
-      gu.w[1] = wsrc(L.wu);
+      gu.packed = plan.fmt[SG_GU];
+      gu.w[0] = wsrc(L.wg, SG_GU);
+      gu.w[1] = wsrc(L.wu, SG_GU);
       gu.seg_rows[0] = c.hidden_dim;
       gu.seg_rows[1] = c.hidden_dim;
       gu.seg_mode = GEMM_SEG_INTERLEAVE;
@@ -1018,8 +1044,8 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position, SpanM
       GemmArgs d;
       memset(&d, 0, sizeof(d));
       d.qtype = CHATNET_GGML_Q4_0;
-      d.packed = packed;
-      d.w[0] = wsrc(L.wd);
+      d.packed = plan.fmt[SG_D];
+      d.w[0] = wsrc(L.wd, SG_D);
       d.seg_rows[0] = c.dim;
       d.M = c.dim;
       d.K = c.hidden_dim;
@@ -1051,8 +1077,8 @@ int run_span(chatnet_model* m, const int32_t* tokens, int n, int position, SpanM
 }
 
 int run_prompt(chatnet_model* m, const int32_t* tokens, int n, int position) {
-  const SpanMode mode = span_mode(m, n);
-  if (mode != SPAN_NONE) return run_span(m, tokens, n, position, mode);
+  const SpanPlan plan = span_plan(m, n);
+  if (plan.ok) return run_span(m, tokens, n, position, plan);
   for (int t = 0; t < n; t++) {
     HIP_TRY(set_state_launch(m->state, position + t, tokens[t], -1, m->stream));
     int rc = launch_token(m, t == n - 1, bucket_cap(m, position + t + 1));

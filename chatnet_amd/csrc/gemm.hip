@@ -304,14 +304,20 @@ __device__ __forceinline__ void reg_fence(T& r) {
 // read from LDS feeds MT MFMAs, each dequantized W fragment TN.  WNC: waves
 // along N (1: the four waves stack along M, BM = 128 * MT; 2: a 2 x 2 grid of
 // waves, BM = 64 * MT, BN = 64 * TN, each wave reading half the x tile).
-template <bool PRECISE, int TN, int S, bool PK, int MT = 1, int WNC = 1>
+// WF: how W is stored (GemmArgs::packed): GEMM_W_Q4_0 raw blocks,
+// GEMM_W_PACKED units, GEMM_W_F16 / GEMM_W_F32 rows of the float type; the
+// float rows' 16-byte pieces are XOR-swizzled in LDS as the x rows are.
+template <bool PRECISE, int TN, int S, int WF, int MT = 1, int WNC = 1>
 struct PipeCfg {
   static constexpr int PL = PRECISE ? 2 : 1;
   static constexpr int MTILES = MT;
   static constexpr int WN = WNC, WM = 4 / WNC;  // waves along N and M
   static constexpr int BM = 32 * WM * MT, BN = 32 * TN * WN;
-  static constexpr int UNIT = PK ? kGemmPackUnit : 36;  // global bytes per row and chunk
-  static constexpr int WP = PK ? 6 : 3;        // 16-byte pieces per row and chunk
+  static constexpr bool PK = WF == GEMM_W_PACKED;
+  static constexpr bool FLT = WF == GEMM_W_F16 || WF == GEMM_W_F32;
+  // global bytes per row and chunk of 64
+  static constexpr int UNIT = WF == GEMM_W_F32 ? 256 : (WF == GEMM_W_F16 ? 128 : (PK ? kGemmPackUnit : 36));
+  static constexpr int WP = FLT ? UNIT / 16 : (PK ? 6 : 3);  // 16-byte pieces per row and chunk
   static constexpr int WROW = 16 * WP;         // LDS bytes per row and chunk
   static constexpr int XB = BN * 128;          // bytes per x plane per stage
   static constexpr int WB = BM * WROW;         // bytes of W per stage
@@ -322,7 +328,7 @@ struct PipeCfg {
   static constexpr int WPW = BM * WP / 4;      // W pieces per wave
   static constexpr int WI = (WPW + 63) / 64;
   static constexpr int VPS = PL * XI + WI;     // vector-memory instructions per stage per wave
-  static constexpr int WD = PK ? 12 : 5;       // W dwords a lane reads per chunk
+  static constexpr int WD = FLT ? UNIT / 8 : (PK ? 12 : 5);  // W dwords a lane reads per chunk
   static constexpr bool PACKED = PK;
   static constexpr int TNW = TN;                // column tiles per wave
   static_assert(XPW % 64 == 0, "x pieces per wave must fill whole instructions");
@@ -372,8 +378,10 @@ struct TileIO {
       const int row = piece / C::WP, part = piece % C::WP;
       const int vr = min(m0 + row, a.M - 1);
       // Q4_0: pieces at unit bytes 0, 16 and 20, exactly the 36 bytes, no read
-      // past the unit; packed: the 6 pieces of the 96-byte unit
-      wsrc[j] = reinterpret_cast<const char*>(gemm_row_ptr(a, vr, row_dw)) + (!C::PACKED && part == 2 ? 20 : 16 * part);
+      // past the unit; packed: the 6 pieces of the 96-byte unit; float rows:
+      // LDS slot `part` holds the row's piece part ^ ((row >> 1) & 7)
+      const int off = C::FLT ? 16 * (part ^ ((row >> 1) & 7)) : (!C::PACKED && part == 2 ? 20 : 16 * part);
+      wsrc[j] = reinterpret_cast<const char*>(gemm_row_ptr(a, vr, row_dw)) + off;
     }
   }
 
@@ -399,7 +407,18 @@ struct TileIO {
   __device__ __forceinline__ void wraw(const char* st, uint32_t (&w)[C::WD], int mt = 0) const {
     const uint32_t* wb =
         reinterpret_cast<const uint32_t*>(st + C::PL * C::XB + (wm * 32 * C::MTILES + 32 * mt + li) * C::WROW);
-    if constexpr (C::PACKED) {
+    if constexpr (C::FLT) {
+      // the lane's block h: logical pieces P*h .. P*h+P-1 of the row (P = 4
+      // for F16, 8 for F32), each in its swizzled slot
+      constexpr int P = C::WP / 2;
+      const int sw = (li >> 1) & 7;
+#pragma unroll
+      for (int q = 0; q < P; q++) {
+        const uint32_t* pc = wb + 4 * ((P * h + q) ^ sw);
+#pragma unroll
+        for (int i = 0; i < 4; i++) w[4 * q + i] = pc[i];
+      }
+    } else if constexpr (C::PACKED) {
 #pragma unroll
       for (int i = 0; i < 8; i++) w[i] = wb[8 * h + i];
       w[8] = wb[16 + 2 * h];
@@ -608,9 +627,10 @@ __global__ __launch_bounds__(CN_BLOCK) __attribute__((amdgpu_waves_per_eu(1, 2))
 // fp16 MFMAs per step: Wa*xh + Wa*xl + Wb*xh, W = Wa + Wb exact for Q4_0 (~22
 // bits for packed units), x = xh + xl to ~2^-22; the dropped Wb*xl term is
 // below 2^-19 relative.
-template <int TN, int S, bool PK>
+template <int TN, int S, int WF>
 __global__ __launch_bounds__(CN_BLOCK) void gemm_s_kernel(GemmArgs a) {
-  using C = PipeCfg<true, TN, S, PK>;
+  using C = PipeCfg<true, TN, S, WF>;
+  constexpr bool PK = C::PK;
   extern __shared__ __attribute__((aligned(16))) char lds[];
   const TileIO<C> io(a);
   const int h = io.h;
@@ -644,7 +664,7 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_s_kernel(GemmArgs a) {
       uint32_t w[C::WD];
       io.wraw(st, w);
       cn_half2 dh2 = {}, dl2 = {};
-      if constexpr (!PK) {
+      if constexpr (WF == GEMM_W_Q4_0) {
         // d = dh + dl: dh keeps the top 8 significant bits of the fp16 scale
         const uint32_t d16 = h ? (w[4] >> 16) : (w[0] & 0xFFFFu);
         const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)d16);
@@ -666,7 +686,23 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_s_kernel(GemmArgs a) {
       for (int s = 0; s < 4; s++) {
         if (s < 3) load_x(s + 1, (s + 1) & 1);
         f16x8 wa, wb;
-        if constexpr (PK) {
+        if constexpr (WF == GEMM_W_F16) {
+          // elements 4s..4s+3 and 16+4s..16+4s+3 of the lane's block, already
+          // fp16: W * (xh + xl), exact products
+          wa = __builtin_bit_cast(f16x8, (cn_u32x4){w[2 * s], w[2 * s + 1], w[8 + 2 * s], w[9 + 2 * s]});
+        } else if constexpr (WF == GEMM_W_F32) {
+          // the same elements as fp32, split as W = Wa + Wb in fp16 (one
+          // rounding each, ~22 bits together)
+          uint32_t hi[4], lo[4];
+#pragma unroll
+          for (int k = 0; k < 2; k++) {
+            cn_split_f16x2(__uint_as_float(w[4 * s + 2 * k]), __uint_as_float(w[4 * s + 2 * k + 1]), hi[k], lo[k]);
+            cn_split_f16x2(__uint_as_float(w[16 + 4 * s + 2 * k]), __uint_as_float(w[16 + 4 * s + 2 * k + 1]),
+                           hi[2 + k], lo[2 + k]);
+          }
+          wa = __builtin_bit_cast(f16x8, (cn_u32x4){hi[0], hi[1], hi[2], hi[3]});
+          wb = __builtin_bit_cast(f16x8, (cn_u32x4){lo[0], lo[1], lo[2], lo[3]});
+        } else if constexpr (PK) {
           dequant_u8_f16(w[s], w[4 + s], __uint_as_float(w[8]), __uint_as_float(w[10]), __uint_as_float(w[9]),
                          __uint_as_float(w[11]), wa, wb);
         } else {
@@ -676,8 +712,10 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_s_kernel(GemmArgs a) {
         for (int cc = 0; cc < TN; cc++) acc[cc] = mma32(wa, xh[s & 1][cc], acc[cc]);
 #pragma unroll
         for (int cc = 0; cc < TN; cc++) acc[cc] = mma32(wa, xl[s & 1][cc], acc[cc]);
+        if constexpr (WF != GEMM_W_F16) {
 #pragma unroll
-        for (int cc = 0; cc < TN; cc++) acc[cc] = mma32(wb, xh[s & 1][cc], acc[cc]);
+          for (int cc = 0; cc < TN; cc++) acc[cc] = mma32(wb, xh[s & 1][cc], acc[cc]);
+        }
       }
     }
   }
@@ -1136,21 +1174,27 @@ struct GemmShape {
 
 constexpr int kStages = 3;
 
-template <bool PRECISE, int TN, int S, bool PK>
+template <bool PRECISE, int TN, int S, int WF>
 constexpr int ring_bytes() {
-  return PipeCfg<PRECISE, TN, S, PK>::LDS;
+  return PipeCfg<PRECISE, TN, S, WF>::LDS;
 }
 
-int span_ring_bytes(int tn, int stages, bool packed) {
-  if (stages == 2) {
-    if (tn == 1) return packed ? ring_bytes<true, 1, 2, true>() : ring_bytes<true, 1, 2, false>();
-    return packed ? ring_bytes<true, 2, 2, true>() : ring_bytes<true, 2, 2, false>();
+template <int WF>
+int span_ring_bytes_t(int tn, int stages) {
+  if (stages == 2) return tn == 1 ? ring_bytes<true, 1, 2, WF>() : ring_bytes<true, 2, 2, WF>();
+  return tn == 1 ? ring_bytes<true, 1, 3, WF>() : ring_bytes<true, 2, 3, WF>();
+}
+
+int span_ring_bytes(int tn, int stages, int wf) {
+  switch (wf) {
+    case GEMM_W_PACKED: return span_ring_bytes_t<GEMM_W_PACKED>(tn, stages);
+    case GEMM_W_F16: return span_ring_bytes_t<GEMM_W_F16>(tn, stages);
+    case GEMM_W_F32: return span_ring_bytes_t<GEMM_W_F32>(tn, stages);
+    default: return span_ring_bytes_t<GEMM_W_Q4_0>(tn, stages);
   }
-  if (tn == 1) return packed ? ring_bytes<true, 1, 3, true>() : ring_bytes<true, 1, 3, false>();
-  return packed ? ring_bytes<true, 2, 3, true>() : ring_bytes<true, 2, 3, false>();
 }
 
-GemmShape pick_gemm(int M, int N, int K, int num_cus, bool precise, bool packed) {
+GemmShape pick_gemm(int M, int N, int K, int num_cus, bool precise, int wf) {
   GemmShape s;
   const int nchunks = K / 64;
   s.splits = 1;
@@ -1159,7 +1203,7 @@ GemmShape pick_gemm(int M, int N, int K, int num_cus, bool precise, bool packed)
     s.tn = N <= 32 ? 1 : 2;
     const long long tiles = (long long)((M + 127) / 128) * ((N + 32 * s.tn - 1) / (32 * s.tn));
     s.stages = tiles > 2LL * num_cus ? 2 : 3;
-    const int per_cu = std::min(3, 160 * 1024 / span_ring_bytes(s.tn, s.stages, packed));
+    const int per_cu = std::max(1, std::min(3, 160 * 1024 / span_ring_bytes(s.tn, s.stages, wf)));
     const long long slots = (long long)per_cu * num_cus;
     while (s.splits < 16 && tiles * (s.splits + 1) <= slots && nchunks / (s.splits + 1) >= 8) s.splits++;
   } else {
@@ -1214,31 +1258,38 @@ hipError_t launch_p_ring(const GemmArgs& a, int stages, int mt, int grid, hipStr
   }
 }
 
-template <int TN, int S, bool PK>
+template <int TN, int S, int WF>
 hipError_t launch_s(const GemmArgs& a, int grid, hipStream_t st) {
-  constexpr int lds = PipeCfg<true, TN, S, PK>::LDS;
+  constexpr int lds = PipeCfg<true, TN, S, WF>::LDS;
   static_assert(lds <= 160 * 1024, "LDS ring exceeds the CU's 160 KB");
   static std::atomic<uint64_t> lds_done{0};
   if (lds > 64 * 1024) {
-    const hipError_t e = allow_full_lds(reinterpret_cast<const void*>(&gemm_s_kernel<TN, S, PK>), lds_done);
+    const hipError_t e = allow_full_lds(reinterpret_cast<const void*>(&gemm_s_kernel<TN, S, WF>), lds_done);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((gemm_s_kernel<TN, S, PK>), dim3(grid), dim3(CN_BLOCK), lds, st, a);
+  hipLaunchKernelGGL((gemm_s_kernel<TN, S, WF>), dim3(grid), dim3(CN_BLOCK), lds, st, a);
   return hipGetLastError();
 }
 
-template <int TN, bool PK>
+template <int TN, int WF>
 hipError_t launch_s_ring(const GemmArgs& a, int stages, int grid, hipStream_t st) {
-  return stages == 2 ? launch_s<TN, 2, PK>(a, grid, st) : launch_s<TN, 3, PK>(a, grid, st);
+  return stages == 2 ? launch_s<TN, 2, WF>(a, grid, st) : launch_s<TN, 3, WF>(a, grid, st);
+}
+
+template <int TN>
+hipError_t launch_s_fmt(const GemmArgs& a, int stages, int grid, hipStream_t st) {
+  switch (a.packed) {
+    case GEMM_W_PACKED: return launch_s_ring<TN, GEMM_W_PACKED>(a, stages, grid, st);
+    case GEMM_W_F16: return launch_s_ring<TN, GEMM_W_F16>(a, stages, grid, st);
+    case GEMM_W_F32: return launch_s_ring<TN, GEMM_W_F32>(a, stages, grid, st);
+    default: return launch_s_ring<TN, GEMM_W_Q4_0>(a, stages, grid, st);
+  }
 }
 
 hipError_t launch_kernel(const GemmArgs& a, const GemmShape& s, bool precise, int grid, hipStream_t st) {
   const bool pk = a.packed != 0;
   const int tn = s.tn;
-  if (precise) {
-    if (tn == 1) return pk ? launch_s_ring<1, true>(a, s.stages, grid, st) : launch_s_ring<1, false>(a, s.stages, grid, st);
-    return pk ? launch_s_ring<2, true>(a, s.stages, grid, st) : launch_s_ring<2, false>(a, s.stages, grid, st);
-  }
+  if (precise) return tn == 1 ? launch_s_fmt<1>(a, s.stages, grid, st) : launch_s_fmt<2>(a, s.stages, grid, st);
   if (tn == 1) return pk ? launch_p_ring<1, true>(a, s.stages, 1, grid, st) : launch_p_ring<1, false>(a, s.stages, 1, grid, st);
   if (tn == 2) return pk ? launch_p_ring<2, true>(a, s.stages, 1, grid, st) : launch_p_ring<2, false>(a, s.stages, 1, grid, st);
   return pk ? launch_p_ring<4, true>(a, s.stages, s.mt, grid, st) : launch_p_ring<4, false>(a, s.stages, s.mt, grid, st);
@@ -1291,12 +1342,14 @@ hipError_t gemm_pack_launch(int qtype, const void* w, int M, int K, void* dst, h
   return hipGetLastError();
 }
 
-size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool precise, bool packed) {
-  const GemmShape s = pick_gemm(M, N, K, num_cus, precise, packed);
+size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool precise, int wfmt) {
+  const GemmShape s = pick_gemm(M, N, K, num_cus, precise, wfmt);
   return s.splits > 1 ? (size_t)s.splits * N * M * sizeof(float) : 0;
 }
 
 hipError_t gemm_launch(const GemmArgs& a_in, int num_cus, hipStream_t st, int* splits_left) {
+  if (a_in.packed < GEMM_W_Q4_0 || a_in.packed > GEMM_W_F32 || (a_in.packed > GEMM_W_PACKED && !a_in.precise))
+    return hipErrorInvalidValue;  // float rows only in the span kernel
   const bool k_ok = a_in.packed ? (a_in.K > 0 && a_in.K % 64 == 0) : gemm_supports(a_in.qtype, a_in.K);
   if (!k_ok || a_in.M <= 0 || a_in.N <= 0) return hipErrorInvalidValue;
   const bool precise = a_in.precise != 0;
@@ -1305,7 +1358,7 @@ hipError_t gemm_launch(const GemmArgs& a_in, int num_cus, hipStream_t st, int* s
   // kernels apply no other epilogue)
   if (splits_left && a_in.epi != GEMV_EPI_STORE && a_in.epi != GEMV_EPI_ADD) return hipErrorInvalidValue;
   if (a_in.epi == GEMV_EPI_SWIGLU && (!a_in.hb || !a_in.hb_lo)) return hipErrorInvalidValue;
-  const GemmShape s = pick_gemm(a_in.M, a_in.N, a_in.K, num_cus, precise, a_in.packed != 0);
+  const GemmShape s = pick_gemm(a_in.M, a_in.N, a_in.K, num_cus, precise, a_in.packed);
   GemmArgs a = a_in;
   a.splits = s.splits;
   if (s.splits > 1 && !a.part) return hipErrorInvalidValue;

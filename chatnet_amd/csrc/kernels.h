@@ -91,9 +91,12 @@ hipError_t gemv_float_launch(int qtype, int epi, const GemvArgs& a, int num_cus,
 // GEMV_EPI_SWIGLU h[n][vr/2] = silu(acc[vr even]) * acc[vr odd] as fp16 hi + lo
 // planes (hb, hb_lo) in the cn_span_pos order.
 enum { GEMM_SEG_SINGLE = 0, GEMM_SEG_CONCAT = 1, GEMM_SEG_INTERLEAVE = 2 };
+// How W is stored (GemmArgs::packed): raw Q4_0 blocks, gemm_pack_launch units
+// (any packable type), or rows of F16 / F32 values (the span kernel only).
+enum { GEMM_W_Q4_0 = 0, GEMM_W_PACKED = 1, GEMM_W_F16 = 2, GEMM_W_F32 = 3 };
 struct GemmArgs {
   int qtype;
-  int packed;             // 1: w holds gemm_pack_launch units (any packable type), 0: raw Q4_0 blocks
+  int packed;             // GEMM_W_*: how w is stored
   const uint8_t* w[3];
   int seg_rows[3];
   int seg_mode;
@@ -122,7 +125,7 @@ constexpr int kGemmPackUnit = 96;
 bool gemm_pack_supports(int qtype, int K);
 size_t gemm_pack_bytes(int M, int K);
 hipError_t gemm_pack_launch(int qtype, const void* w, int M, int K, void* dst, hipStream_t st);
-size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool precise, bool packed);
+size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool precise, int wfmt);
 // With splits_left, a launch whose K is split leaves its partial tiles in
 // a.part ([splits][N][M]) unreduced and reports the split count there (0 when
 // the epilogue ran): the caller folds them into its next kernel

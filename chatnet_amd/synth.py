@@ -55,6 +55,10 @@ MIXES = {
                "output": _native.GGML_Q6_K},
     "q2_k": {"attn": _native.GGML_Q2_K, "gate_up": _native.GGML_Q2_K, "down": _native.GGML_Q3_K,
              "output": _native.GGML_Q8_K},
+    # float and block projections side by side: F16 attention, Q4_0 gate/up,
+    # F32 down (each GEMM of a span on its own weight format)
+    "float_mix": {"attn": _native.GGML_F16, "gate_up": _native.GGML_Q4_0, "down": _native.GGML_F32,
+                  "output": _native.GGML_Q4_K},
     # the IQ family as DequantIQ.cs decodes it, every type in one of two mixes
     "iq_a": {"attn": _native.GGML_IQ4_XS, "gate": _native.GGML_IQ3_XXS, "up": _native.GGML_IQ2_XS,
              "down": _native.GGML_IQ4_NL, "output": _native.GGML_IQ1_M},

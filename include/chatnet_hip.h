@@ -155,15 +155,17 @@ CHATNET_API int chatnet_upload_tensor(chatnet_model* m, const char* name, uint32
  * position..position+n-1, writing their K/V into the cache; logits of the last
  * token stay on the device and are copied to `logits_host` (vocab_size
  * floats) when it is non-NULL.  Spans of 8 or more tokens run as batches of
- * up to 512 tokens when head_dim is 64 or 128, n_heads / n_kv_heads is at
- * most 64 and every projection matrix is of a block type (Q4_0 read from its
- * stored blocks when all seven matrices of every layer are Q4_0; otherwise
- * every matrix, of any block type but F32 / F16, re-encoded once into packed
- * units kept for the model's lifetime): MFMA GEMMs on fp16 operands (each
- * weight exact as two fp16 planes for Q4_0, ~22 bits for packed units;
- * activations as fp16 hi + lo planes; three products per step) and causal
- * attention over the cache.  Shorter spans, and models with F32 / F16
- * projection matrices, run token by token. */
+ * up to 512 tokens when head_dim is 64 or 128 and n_heads / n_kv_heads is at
+ * most 64: MFMA GEMMs on fp16 operands (activations as fp16 hi + lo planes)
+ * and causal attention over the cache.  Each GEMM of a layer (q|k|v, o,
+ * gate|up, down) reads its matrices in one format: F16 rows as stored (two
+ * products per step, exact weights), F32 rows split into fp16 hi + lo as
+ * read (three products, ~22 bits), block types from their stored Q4_0
+ * blocks when every block-typed projection of the model is Q4_0 (each weight
+ * exact as two fp16 planes), otherwise re-encoded once into packed units kept
+ * for the model's lifetime (~22 bits).  Shorter spans, and models whose
+ * layers give one GEMM matrices of both a float and a block type (ffn_gate
+ * Q4_0 with ffn_up F16), run token by token. */
 CHATNET_API int chatnet_forward(chatnet_model* m, const int32_t* tokens, int n, int position,
                     float* logits_host);
 

@@ -459,6 +459,24 @@ def test_span_block_type_mixes_match_oracle(mix):
     span_case(SPAN_SMALL.replace(context_length=96), 39, 40, mix=mix, check_batched=True)
 
 
+@pytest.mark.parametrize("mix", ["f16", "f32", "float_mix"])
+def test_span_float_weight_mixes_match_oracle(mix):
+    """Spans of models with F16 or F32 projections run batched: F16 rows meet
+    x's fp16 hi + lo planes directly (two products per step, exact weights),
+    F32 rows are split into fp16 hi + lo as they are read (three products);
+    float_mix runs F16 attention, Q4_0 gate/up and an F32 down projection in
+    one span, each GEMM on its own weight format."""
+    announce(f"span: float mix {mix}, 40 + 8 tokens")
+    span_case(SPAN_SMALL.replace(context_length=96), 41, 40, mix=mix, check_batched=True)
+
+
+def test_span_f16_llama7b_layer_matches_oracle():
+    """A 7B-shaped layer with F16 projections as a 16-token span."""
+    from chatnet_amd import LLAMA2_7B
+    announce("span: llama-7b-shaped f16 layer, 16 + 8 tokens")
+    span_case(LLAMA2_7B.replace(n_layers=1, context_length=64), 42, 16, mix="f16", check_batched=True)
+
+
 def test_span_q4_k_m_llama7b_layer_matches_oracle():
     """A 7B-shaped Q4_K_M layer (Q4_K attention and gate/up, Q6_K down, Q6_K
     LM head) as a 16-token span."""
