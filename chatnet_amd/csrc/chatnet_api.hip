@@ -808,11 +808,13 @@ LayerMats layer_mats(Layer& L) { return {{&L.wq, &L.wk, &L.wv, &L.wo, &L.wg, &L.
 
 // How a span's projections read their weights, per GEMM of the layer (QKV,
 // O, gate/up, down): F16 and F32 matrices as their own rows (GEMM_W_F16 /
-// GEMM_W_F32), block types as raw Q4_0 blocks when every block-typed
-// projection is Q4_0, else as packed units (types mixed freely).  The
-// matrices one GEMM concatenates (q|k|v) or interleaves (gate/up) must share
-// that format; a span whose layers cannot (ffn_gate Q4_0 with ffn_up F16, a
-// type neither packable nor float) runs token by token.
+// GEMM_W_F32), block types from their stored blocks when every matrix of that
+// GEMM in every layer is Q4_0 (GEMM_W_Q4_0) or every one is Q4_K
+// (GEMM_W_Q4_K), else as packed units (block types mixed freely, made once
+// per model).  The matrices one GEMM concatenates (q|k|v) or interleaves
+// (gate/up) must share a class (float type or block type); a span whose layers
+// cannot (ffn_gate Q4_0 with ffn_up F16, a type neither packable nor float)
+// runs token by token.
 enum { SG_QKV = 0, SG_O = 1, SG_GU = 2, SG_D = 3 };
 struct SpanPlan {
   bool ok = false;
@@ -835,21 +837,24 @@ SpanPlan span_plan(chatnet_model* m, int n) {
   };
   const int group_of[7] = {SG_QKV, SG_QKV, SG_QKV, SG_O, SG_GU, SG_GU, SG_D};
   int gcls[4] = {0, 0, 0, 0};  // 0: not seen yet
-  bool all_q4_0 = true;
+  bool all_q4_0[4] = {true, true, true, true}, all_q4_k[4] = {true, true, true, true};
   for (Layer& L : m->layers) {
     const LayerMats lm = layer_mats(L);
     for (int i = 0; i < 7; i++) {
       const DevTensor* t = lm.t[i];
-      const int k = cls(t);
+      const int k = cls(t), gi = group_of[i];
       if (k < 0) return p;
-      int& g = gcls[group_of[i]];
+      int& g = gcls[gi];
       if (g == 0) g = k;
       else if (g != k) return p;
-      if (k == GEMM_W_PACKED && (t->type != CHATNET_GGML_Q4_0 || !gemm_supports(CHATNET_GGML_Q4_0, (int)t->ne0)))
-        all_q4_0 = false;
+      if (t->type != CHATNET_GGML_Q4_0 || !gemm_supports(CHATNET_GGML_Q4_0, (int)t->ne0)) all_q4_0[gi] = false;
+      if (t->type != CHATNET_GGML_Q4_K || t->ne0 % 256) all_q4_k[gi] = false;
     }
   }
-  for (int g = 0; g < 4; g++) p.fmt[g] = gcls[g] == GEMM_W_PACKED ? (all_q4_0 ? GEMM_W_Q4_0 : GEMM_W_PACKED) : gcls[g];
+  for (int g = 0; g < 4; g++) {
+    if (gcls[g] != GEMM_W_PACKED) p.fmt[g] = gcls[g];
+    else p.fmt[g] = all_q4_0[g] ? GEMM_W_Q4_0 : (all_q4_k[g] ? GEMM_W_Q4_K : GEMM_W_PACKED);
+  }
   p.ok = true;
   return p;
 }

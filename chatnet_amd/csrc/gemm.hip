@@ -305,8 +305,10 @@ __device__ __forceinline__ void reg_fence(T& r) {
 // along N (1: the four waves stack along M, BM = 128 * MT; 2: a 2 x 2 grid of
 // waves, BM = 64 * MT, BN = 64 * TN, each wave reading half the x tile).
 // WF: how W is stored (GemmArgs::packed): GEMM_W_Q4_0 raw blocks,
-// GEMM_W_PACKED units, GEMM_W_F16 / GEMM_W_F32 rows of the float type; the
-// float rows' 16-byte pieces are XOR-swizzled in LDS as the x rows are.
+// GEMM_W_PACKED units, GEMM_W_F16 / GEMM_W_F32 rows of the float type (their
+// 16-byte pieces XOR-swizzled in LDS as the x rows are), GEMM_W_Q4_K raw
+// super-blocks (per chunk of 64: the 16-byte header, then the 32 qs bytes of
+// the chunk's two sub-blocks).
 template <bool PRECISE, int TN, int S, int WF, int MT = 1, int WNC = 1>
 struct PipeCfg {
   static constexpr int PL = PRECISE ? 2 : 1;
@@ -315,6 +317,7 @@ struct PipeCfg {
   static constexpr int BM = 32 * WM * MT, BN = 32 * TN * WN;
   static constexpr bool PK = WF == GEMM_W_PACKED;
   static constexpr bool FLT = WF == GEMM_W_F16 || WF == GEMM_W_F32;
+  static constexpr bool Q4K = WF == GEMM_W_Q4_K;
   // global bytes per row and chunk of 64
   static constexpr int UNIT = WF == GEMM_W_F32 ? 256 : (WF == GEMM_W_F16 ? 128 : (PK ? kGemmPackUnit : 36));
   static constexpr int WP = FLT ? UNIT / 16 : (PK ? 6 : 3);  // 16-byte pieces per row and chunk
@@ -328,7 +331,7 @@ struct PipeCfg {
   static constexpr int WPW = BM * WP / 4;      // W pieces per wave
   static constexpr int WI = (WPW + 63) / 64;
   static constexpr int VPS = PL * XI + WI;     // vector-memory instructions per stage per wave
-  static constexpr int WD = FLT ? UNIT / 8 : (PK ? 12 : 5);  // W dwords a lane reads per chunk
+  static constexpr int WD = FLT ? UNIT / 8 : (PK ? 12 : (Q4K ? 8 : 5));  // W dwords a lane reads per chunk
   static constexpr bool PACKED = PK;
   static constexpr int TNW = TN;                // column tiles per wave
   static_assert(XPW % 64 == 0, "x pieces per wave must fill whole instructions");
@@ -340,6 +343,7 @@ struct TileIO {
   int lane, wave, wm, wn, h, li, ks, m0, n0, c_begin, c_end;
   const uint16_t* xsrc[C::PL][C::XI];
   const char* wsrc[C::WI];
+  int wstep[C::WI];  // Q4_K: bytes the piece moves per chunk within a super-block
   bool wact[C::WI];
 
   __device__ __forceinline__ explicit TileIO(const GemmArgs& a) {
@@ -380,8 +384,9 @@ struct TileIO {
       // Q4_0: pieces at unit bytes 0, 16 and 20, exactly the 36 bytes, no read
       // past the unit; packed: the 6 pieces of the 96-byte unit; float rows:
       // LDS slot `part` holds the row's piece part ^ ((row >> 1) & 7)
-      const int off = C::FLT ? 16 * (part ^ ((row >> 1) & 7)) : (!C::PACKED && part == 2 ? 20 : 16 * part);
+      const int off = C::FLT ? 16 * (part ^ ((row >> 1) & 7)) : (!C::PACKED && !C::Q4K && part == 2 ? 20 : 16 * part);
       wsrc[j] = reinterpret_cast<const char*>(gemm_row_ptr(a, vr, row_dw)) + off;
+      wstep[j] = part ? 32 : 0;  // Q4_K: the header stays, the qs window moves
     }
   }
 
@@ -394,8 +399,11 @@ struct TileIO {
       for (int j = 0; j < C::XI; j++)
         lds_dma16(xsrc[p][j] + c * 64, st + p * C::XB + (wave * C::XPW + 64 * j) * 16);
 #pragma unroll
-    for (int j = 0; j < C::WI; j++)
-      if (wact[j]) lds_dma16(wsrc[j] + c * C::UNIT, st + C::PL * C::XB + (wave * C::WPW + 64 * j) * 16);
+    for (int j = 0; j < C::WI; j++) {
+      // Q4_K: super-block c / 4 (144 bytes), qs of its sub-blocks 2(c%4), 2(c%4)+1
+      const char* src = C::Q4K ? wsrc[j] + (size_t)(c >> 2) * 144 + (c & 3) * wstep[j] : wsrc[j] + c * C::UNIT;
+      if (wact[j]) lds_dma16(src, st + C::PL * C::XB + (wave * C::WPW + 64 * j) * 16);
+    }
     asm volatile("" ::: "memory");
   }
 
@@ -407,7 +415,13 @@ struct TileIO {
   __device__ __forceinline__ void wraw(const char* st, uint32_t (&w)[C::WD], int mt = 0) const {
     const uint32_t* wb =
         reinterpret_cast<const uint32_t*>(st + C::PL * C::XB + (wm * 32 * C::MTILES + 32 * mt + li) * C::WROW);
-    if constexpr (C::FLT) {
+    if constexpr (C::Q4K) {
+      // the header (d | dmin, 12 scale bytes), then the qs of sub-block h of the chunk
+#pragma unroll
+      for (int i = 0; i < 4; i++) w[i] = wb[i];
+#pragma unroll
+      for (int i = 0; i < 4; i++) w[4 + i] = wb[4 + 4 * h + i];
+    } else if constexpr (C::FLT) {
       // the lane's block h: logical pieces P*h .. P*h+P-1 of the row (P = 4
       // for F16, 8 for F32), each in its swizzled slot
       constexpr int P = C::WP / 2;
@@ -664,6 +678,24 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_s_kernel(GemmArgs a) {
       uint32_t w[C::WD];
       io.wraw(st, w);
       cn_half2 dh2 = {}, dl2 = {};
+      float ksc = 0.f, kof = 0.f;
+      if constexpr (C::Q4K) {
+        // sub-block sb of the super-block (DequantQ4K.DecodeScales,
+        // DequantQ4K.cs:218-264): its weights are d*sc*q - dmin*m, and both
+        // products are exact in fp32 (11 x 6 bits)
+        const int sb = 2 * (c & 3) + h;
+        auto qb = [&](int i) { return (w[1 + (i >> 2)] >> (8 * (i & 3))) & 0xFFu; };
+        uint32_t sc, mm;
+        if (sb < 4) {
+          sc = qb(sb) & 63u;
+          mm = qb(sb + 4) & 63u;
+        } else {
+          sc = (qb(sb + 4) & 0xFu) | ((qb(sb - 4) >> 6) << 4);
+          mm = (qb(sb + 4) >> 4) | ((qb(sb) >> 6) << 4);
+        }
+        ksc = cn_h2f(w[0]) * (float)sc;
+        kof = -(cn_h2f(w[0] >> 16) * (float)mm);
+      }
       if constexpr (WF == GEMM_W_Q4_0) {
         // d = dh + dl: dh keeps the top 8 significant bits of the fp16 scale
         const uint32_t d16 = h ? (w[4] >> 16) : (w[0] & 0xFFFFu);
@@ -702,6 +734,11 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_s_kernel(GemmArgs a) {
           }
           wa = __builtin_bit_cast(f16x8, (cn_u32x4){hi[0], hi[1], hi[2], hi[3]});
           wb = __builtin_bit_cast(f16x8, (cn_u32x4){lo[0], lo[1], lo[2], lo[3]});
+        } else if constexpr (C::Q4K) {
+          // qs dword s of the sub-block: low nibbles are elements 4s..4s+3,
+          // high nibbles 16+4s..16+4s+3 (DequantQ4K.cs:59-72), the order x is stored in
+          const uint32_t q = w[4 + s];
+          dequant_u8_f16(q & 0x0F0F0F0Fu, (q >> 4) & 0x0F0F0F0Fu, ksc, kof, ksc, kof, wa, wb);
         } else if constexpr (PK) {
           dequant_u8_f16(w[s], w[4 + s], __uint_as_float(w[8]), __uint_as_float(w[10]), __uint_as_float(w[9]),
                          __uint_as_float(w[11]), wa, wb);
@@ -1190,6 +1227,7 @@ int span_ring_bytes(int tn, int stages, int wf) {
     case GEMM_W_PACKED: return span_ring_bytes_t<GEMM_W_PACKED>(tn, stages);
     case GEMM_W_F16: return span_ring_bytes_t<GEMM_W_F16>(tn, stages);
     case GEMM_W_F32: return span_ring_bytes_t<GEMM_W_F32>(tn, stages);
+    case GEMM_W_Q4_K: return span_ring_bytes_t<GEMM_W_Q4_K>(tn, stages);
     default: return span_ring_bytes_t<GEMM_W_Q4_0>(tn, stages);
   }
 }
@@ -1282,6 +1320,7 @@ hipError_t launch_s_fmt(const GemmArgs& a, int stages, int grid, hipStream_t st)
     case GEMM_W_PACKED: return launch_s_ring<TN, GEMM_W_PACKED>(a, stages, grid, st);
     case GEMM_W_F16: return launch_s_ring<TN, GEMM_W_F16>(a, stages, grid, st);
     case GEMM_W_F32: return launch_s_ring<TN, GEMM_W_F32>(a, stages, grid, st);
+    case GEMM_W_Q4_K: return launch_s_ring<TN, GEMM_W_Q4_K>(a, stages, grid, st);
     default: return launch_s_ring<TN, GEMM_W_Q4_0>(a, stages, grid, st);
   }
 }
@@ -1348,9 +1387,11 @@ size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool precise, int 
 }
 
 hipError_t gemm_launch(const GemmArgs& a_in, int num_cus, hipStream_t st, int* splits_left) {
-  if (a_in.packed < GEMM_W_Q4_0 || a_in.packed > GEMM_W_F32 || (a_in.packed > GEMM_W_PACKED && !a_in.precise))
-    return hipErrorInvalidValue;  // float rows only in the span kernel
-  const bool k_ok = a_in.packed ? (a_in.K > 0 && a_in.K % 64 == 0) : gemm_supports(a_in.qtype, a_in.K);
+  if (a_in.packed < GEMM_W_Q4_0 || a_in.packed > GEMM_W_Q4_K || (a_in.packed > GEMM_W_PACKED && !a_in.precise))
+    return hipErrorInvalidValue;  // float rows and raw Q4_K only in the span kernel
+  const bool k_ok = a_in.packed == GEMM_W_Q4_K ? (a_in.K > 0 && a_in.K % 256 == 0)
+                    : a_in.packed                ? (a_in.K > 0 && a_in.K % 64 == 0)
+                                                 : gemm_supports(a_in.qtype, a_in.K);
   if (!k_ok || a_in.M <= 0 || a_in.N <= 0) return hipErrorInvalidValue;
   const bool precise = a_in.precise != 0;
   if (precise && !a_in.xb_lo) return hipErrorInvalidValue;

@@ -92,8 +92,9 @@ hipError_t gemv_float_launch(int qtype, int epi, const GemvArgs& a, int num_cus,
 // planes (hb, hb_lo) in the cn_span_pos order.
 enum { GEMM_SEG_SINGLE = 0, GEMM_SEG_CONCAT = 1, GEMM_SEG_INTERLEAVE = 2 };
 // How W is stored (GemmArgs::packed): raw Q4_0 blocks, gemm_pack_launch units
-// (any packable type), or rows of F16 / F32 values (the span kernel only).
-enum { GEMM_W_Q4_0 = 0, GEMM_W_PACKED = 1, GEMM_W_F16 = 2, GEMM_W_F32 = 3 };
+// (any packable type), or (the span kernel only) rows of F16 / F32 values or
+// raw Q4_K super-blocks.
+enum { GEMM_W_Q4_0 = 0, GEMM_W_PACKED = 1, GEMM_W_F16 = 2, GEMM_W_F32 = 3, GEMM_W_Q4_K = 4 };
 struct GemmArgs {
   int qtype;
   int packed;             // GEMM_W_*: how w is stored

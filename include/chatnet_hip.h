@@ -160,10 +160,10 @@ CHATNET_API int chatnet_upload_tensor(chatnet_model* m, const char* name, uint32
  * and causal attention over the cache.  Each GEMM of a layer (q|k|v, o,
  * gate|up, down) reads its matrices in one format: F16 rows as stored (two
  * products per step, exact weights), F32 rows split into fp16 hi + lo as
- * read (three products, ~22 bits), block types from their stored Q4_0
- * blocks when every block-typed projection of the model is Q4_0 (each weight
- * exact as two fp16 planes), otherwise re-encoded once into packed units kept
- * for the model's lifetime (~22 bits).  Shorter spans, and models whose
+ * read (three products, ~22 bits), block types from their stored blocks when
+ * every matrix of that GEMM is Q4_0 (each weight exact as two fp16 planes) or
+ * every one is Q4_K (~22 bits), otherwise re-encoded once into packed units
+ * kept for the model's lifetime (~22 bits).  Shorter spans, and models whose
  * layers give one GEMM matrices of both a float and a block type (ffn_gate
  * Q4_0 with ffn_up F16), run token by token. */
 CHATNET_API int chatnet_forward(chatnet_model* m, const int32_t* tokens, int n, int position,
