@@ -116,9 +116,15 @@ std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, std::pair<char*, size_t>> g_ws;
 std::vector<char*> g_ws_retired;
 
+// The first kMatmulCounterBytes of a stream's workspace are the one-plane
+// GEMM's stream-K tile counters: zeroed when the workspace is allocated, and
+// every launch leaves them zero.
+constexpr size_t kMatmulCounterBytes = (size_t)kGemmTileCounters * sizeof(unsigned);
+
 int matmul_workspace(int dev, hipStream_t st, size_t bytes, char** out) {
   std::lock_guard<std::mutex> lk(g_ws_mu);
   auto& e = g_ws[{dev, st}];
+  bytes = std::max(bytes, kMatmulCounterBytes);
   if (e.second < bytes) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     HIP_TRY(hipStreamIsCapturing(st, &cs));
@@ -130,6 +136,11 @@ int matmul_workspace(int dev, hipStream_t st, size_t bytes, char** out) {
     char* p = nullptr;
     if (hipMalloc((void**)&p, bytes) != hipSuccess)
       return fail(CHATNET_ERR_OUT_OF_MEMORY, "hipMalloc of %zu bytes (matmul workspace) failed", bytes);
+    const hipError_t z = hipMemsetAsync(p, 0, kMatmulCounterBytes, st);
+    if (z != hipSuccess) {
+      (void)hipFree(p);
+      return fail(CHATNET_ERR_HIP, "hipMemsetAsync of the matmul workspace's counters: %s", hipGetErrorString(z));
+    }
     if (e.first) g_ws_retired.push_back(e.first);
     e = {p, bytes};
   }
@@ -1132,12 +1143,15 @@ int matmul_impl(uint32_t type, const void* w_dev, const float* x_dev, float* y_d
   const bool pack = must_pack || (batched && !raw);
   const uint8_t* wp = (const uint8_t*)w_dev;
   if (batched || pack) {
-    // [fp16 x | per-column x scales | K-split partials | packed W], the first three
-    // for the batched path only
-    const size_t xh_bytes = batched ? ((size_t)N * K * sizeof(uint16_t) + 255) & ~(size_t)255 : 0;
-    const size_t xb_bytes = batched ? xh_bytes + (((size_t)N * sizeof(float) + 255) & ~(size_t)255) : 0;
+    // [stream-K tile counters | fp16 x | per-column x scales | K-split or
+    // stream-K partials | packed W]: the counters in the per-stream workspace
+    // only (the no-allocation variant runs no stream-K launch), the next
+    // three for the batched path only
+    const size_t cnt_bytes = noalloc ? 0 : kMatmulCounterBytes;
+    const size_t xh_bytes = cnt_bytes + (batched ? ((size_t)N * K * sizeof(uint16_t) + 255) & ~(size_t)255 : 0);
+    const size_t xb_bytes = batched ? xh_bytes + (((size_t)N * sizeof(float) + 255) & ~(size_t)255) : cnt_bytes;
     const size_t part_bytes =
-        batched ? (gemm_workspace_bytes(M, N, K, cus, false, pack) + 255) & ~(size_t)255 : 0;
+        batched ? (gemm_workspace_bytes(M, N, K, cus, false, pack, !noalloc) + 255) & ~(size_t)255 : 0;
     const size_t pack_bytes = pack ? gemm_pack_bytes(M, K) : 0;
     const size_t need = xb_bytes + part_bytes + pack_bytes;
     char* ws = nullptr;
@@ -1158,7 +1172,7 @@ int matmul_impl(uint32_t type, const void* w_dev, const float* x_dev, float* y_d
     }
     if (batched) {
       // x -> per-column scaled fp16 into the scratch, then the MFMA GEMM
-      HIP_TRY(to_f16_scaled_launch(x_dev, (uint16_t*)ws, (float*)(ws + xh_bytes), N, K, st));
+      HIP_TRY(to_f16_scaled_launch(x_dev, (uint16_t*)(ws + cnt_bytes), (float*)(ws + xh_bytes), N, K, st));
       GemmArgs g;
       memset(&g, 0, sizeof(g));
       g.qtype = (int)type;
@@ -1169,12 +1183,13 @@ int matmul_impl(uint32_t type, const void* w_dev, const float* x_dev, float* y_d
       g.M = M;
       g.K = K;
       g.N = N;
-      g.xb = (const uint16_t*)ws;
+      g.xb = (const uint16_t*)(ws + cnt_bytes);
       g.xinv = (const float*)(ws + xh_bytes);
       g.epi = GEMV_EPI_STORE;
       g.y = y_dev;
       g.ldy = M;
       g.part = part_bytes ? (float*)(ws + xb_bytes) : nullptr;
+      g.tile_cnt = noalloc ? nullptr : (unsigned*)ws;
       HIP_TRY(gemm_launch(g, cus, st));
       g_err.clear();
       return CHATNET_OK;

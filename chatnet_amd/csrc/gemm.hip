@@ -346,6 +346,8 @@ struct TileIO {
   int wstep[C::WI];  // Q4_K: bytes the piece moves per chunk within a super-block
   bool wact[C::WI];
 
+  // The tile and K range of blockIdx.x (tile-major, K split innermost); a
+  // stream-K launch (a.sk_wgs > 0) sets each of its segments with set_tile.
   __device__ __forceinline__ explicit TileIO(const GemmArgs& a) {
     lane = threadIdx.x & 63;
     wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -353,16 +355,22 @@ struct TileIO {
     wn = wave / C::WM;
     h = lane >> 5;
     li = lane & 31;
-    const int n_nt = (a.N + C::BN - 1) / C::BN;
+    if (a.sk_wgs > 0) return;
     int bid = blockIdx.x;
     ks = bid % a.splits;
     bid /= a.splits;
-    m0 = (bid / n_nt) * C::BM;
-    n0 = (bid % n_nt) * C::BN;
     const int nchunks = a.K / 64;
     const int cps = (nchunks + a.splits - 1) / a.splits;
-    c_begin = ks * cps;
-    c_end = min(nchunks, c_begin + cps);
+    set_tile(a, bid, ks * cps, min(nchunks, ks * cps + cps));
+  }
+
+  // Tile `tile` (row tile tile / n_nt, column tile tile % n_nt), chunks [cb, ce).
+  __device__ __forceinline__ void set_tile(const GemmArgs& a, int tile, int cb, int ce) {
+    const int n_nt = (a.N + C::BN - 1) / C::BN;
+    m0 = (tile / n_nt) * C::BM;
+    n0 = (tile % n_nt) * C::BN;
+    c_begin = cb;
+    c_end = ce;
     const int row_dw = a.K / 64 * (C::UNIT / 4);
 #pragma unroll
     for (int p = 0; p < C::PL; p++)
@@ -510,122 +518,225 @@ struct TileIO {
 // TN MFMAs (one v_mfma_f32_32x32x16_f16 per column tile).  Step s of lane
 // half h: Q4_0 qs dword s of block h; packed codes 32h + 4s .. +3 and
 // 32h + 16 + 4s .. +3 with the scale/offset pairs 2h and 2h+1.
-template <int TN, int S, bool PK, int MT, int WNC>
-__global__ __launch_bounds__(CN_BLOCK) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_p_kernel(GemmArgs a) {
+template <int TN, int S, bool PK, int MT, int WNC, bool SK>
+__global__ __launch_bounds__(CN_BLOCK) __attribute__((amdgpu_waves_per_eu(SK ? 2 : 1, 2))) void gemm_p_kernel(GemmArgs a) {
   using C = PipeCfg<false, TN, S, PK, MT, WNC>;
   extern __shared__ __attribute__((aligned(16))) char lds[];
-  const TileIO<C> io(a);
+  __shared__ int sk_last;
+  TileIO<C> io(a);
   const int h = io.h;
-  float xsc[TN];
-  io.template load_scales<TN>(a, xsc);
-
-  f32x16 acc[MT][TN];
-#pragma unroll
-  for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-    for (int cc = 0; cc < TN; cc++)
-#pragma unroll
-      for (int v = 0; v < 16; v++) acc[mt][cc][v] = 0.f;
-
   const uint32_t psel = h ? 0x03010200u : 0x05030402u;
   uint32_t magic = 0x64006400u;
   asm volatile("" : "+v"(magic));
 
-  const int c_begin = io.c_begin, c_end = io.c_end;
-  if (c_begin < c_end) {
-    auto slot_of = [&](int c) { return lds + ((c - c_begin) % S) * C::STAGE; };
+  // Stream-K (SK): the launch's tiles x chunks of 64 as one sequence
+  // (tile-major).  Workgroups 0 .. D-1 take tiles 0 .. D-1 whole; the other
+  // G2 share the remaining tiles' chunks in equal ranges, each covering the
+  // end of one tile and the start of the next at most.  Otherwise one
+  // segment: the tile and K range of blockIdx.x.
+  const int nc = a.K / 64;
+  const long long units = (long long)a.sk_tiles * nc;
+  constexpr bool sk = SK;
+  const int D = a.sk_dp, G2 = a.sk_wgs - a.sk_dp;
+  const long long u0 = (long long)D * nc, units2 = units - u0;
+  auto lo_of = [&](int g) -> long long { return g < D ? (long long)g * nc : u0 + units2 * (g - D) / G2; };
+  long long u = sk ? lo_of(blockIdx.x) : 0;
+  const long long u_end = sk ? lo_of(blockIdx.x + 1) : 1;
+  for (bool first = true; u < u_end; first = false) {
+    int tile = 0;
+    if constexpr (sk) {
+      tile = (int)(u / nc);
+      const int cb = (int)(u % nc);
+      const int ce = (int)min((long long)nc, cb + (u_end - u));
+      io.set_tile(a, tile, cb, ce);
+      u += ce - cb;
+      if (!first) __syncthreads();  // every wave is done with the previous segment's ring
+    } else {
+      u = u_end;
+    }
+    float xsc[TN];
+    io.template load_scales<TN>(a, xsc);
+
+    f32x16 acc[MT][TN];
 #pragma unroll
-    for (int i = 0; i < S - 1; i++)
-      if (c_begin + i < c_end) io.issue(c_begin + i, lds + i * C::STAGE);
-    for (int c = c_begin; c < c_end; c++) {
-      char* st = slot_of(c);
-      // chunks c+1 .. c+S-2 may stay in flight
-      vm_wait_later<C::VPS, S - 2>(min(S - 2, c_end - 1 - c));
-      wg_barrier();
-      if (c + S - 1 < c_end) io.issue(c + S - 1, slot_of(c + S - 1));
-      // the lane's W dwords (as wraw), then every x fragment of the chunk, all
-      // issued at once; step s waits for its own fragments only
-      uint32_t w[MT][C::WD];
+    for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-      for (int mt = 0; mt < MT; mt++) {
-        // the W rows follow the x planes in the stage (offset WO)
-        constexpr int WO = C::PL * C::XB;
-        const uint32_t wb = lds_addr(st + (io.wm * 32 * MT + 32 * mt + io.li) * C::WROW);
-        if constexpr (PK) {
-          const uint32_t wc = wb + 32 * h, ws = wb + 8 * h;
-          const cn_u32x4 c0 = lds_read128<WO>(wc), c1 = lds_read128<WO + 16>(wc);
-          const uint2 sc = lds_read64<WO + 64>(ws), of = lds_read64<WO + 80>(ws);
-          w[mt][0] = c0[0], w[mt][1] = c0[1], w[mt][2] = c0[2], w[mt][3] = c0[3];
-          w[mt][4] = c1[0], w[mt][5] = c1[1], w[mt][6] = c1[2], w[mt][7] = c1[3];
-          w[mt][8] = sc.x, w[mt][9] = sc.y, w[mt][10] = of.x, w[mt][11] = of.y;
-        } else {
-          const cn_u32x4 q = lds_read128<WO>(wb + 32 * h);
-          const uint32_t t = lds_read32<WO + 16>(wb);
-          w[mt][0] = q[0], w[mt][1] = q[1], w[mt][2] = q[2], w[mt][3] = q[3], w[mt][4] = t;
+      for (int cc = 0; cc < TN; cc++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[mt][cc][v] = 0.f;
+
+    const int c_begin = io.c_begin, c_end = io.c_end;
+    if (c_begin < c_end) {
+      auto slot_of = [&](int c) { return lds + ((c - c_begin) % S) * C::STAGE; };
+#pragma unroll
+      for (int i = 0; i < S - 1; i++)
+        if (c_begin + i < c_end) io.issue(c_begin + i, lds + i * C::STAGE);
+      for (int c = c_begin; c < c_end; c++) {
+        char* st = slot_of(c);
+        // chunks c+1 .. c+S-2 may stay in flight
+        vm_wait_later<C::VPS, S - 2>(min(S - 2, c_end - 1 - c));
+        wg_barrier();
+        if (c + S - 1 < c_end) io.issue(c + S - 1, slot_of(c + S - 1));
+        // the lane's W dwords (as wraw), then every x fragment of the chunk, all
+        // issued at once; step s waits for its own fragments only
+        uint32_t w[MT][C::WD];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+          // the W rows follow the x planes in the stage (offset WO)
+          constexpr int WO = C::PL * C::XB;
+          const uint32_t wb = lds_addr(st + (io.wm * 32 * MT + 32 * mt + io.li) * C::WROW);
+          if constexpr (PK) {
+            const uint32_t wc = wb + 32 * h, ws = wb + 8 * h;
+            const cn_u32x4 c0 = lds_read128<WO>(wc), c1 = lds_read128<WO + 16>(wc);
+            const uint2 sc = lds_read64<WO + 64>(ws), of = lds_read64<WO + 80>(ws);
+            w[mt][0] = c0[0], w[mt][1] = c0[1], w[mt][2] = c0[2], w[mt][3] = c0[3];
+            w[mt][4] = c1[0], w[mt][5] = c1[1], w[mt][6] = c1[2], w[mt][7] = c1[3];
+            w[mt][8] = sc.x, w[mt][9] = sc.y, w[mt][10] = of.x, w[mt][11] = of.y;
+          } else {
+            const cn_u32x4 q = lds_read128<WO>(wb + 32 * h);
+            const uint32_t t = lds_read32<WO + 16>(wb);
+            w[mt][0] = q[0], w[mt][1] = q[1], w[mt][2] = q[2], w[mt][3] = q[3], w[mt][4] = t;
+          }
+        }
+        cn_u32x4 xr[4][TN];
+#pragma unroll
+        for (int s = 0; s < 4; s++) lds_read_xtiles<0, TN>(lds_addr(io.xfrag_ptr(st, 0, s, 0)), xr[s]);
+        // Step s's W operands are dequantized during step s-1 (step 0's before
+        // the first MFMA) and interleaved with its MFMAs: one wave issues in
+        // order, so VALU work placed after a run of MFMAs waits behind them
+        // while the matrix pipe drains; between them it runs in their shadow.
+        auto dequant = [&](int s, int mt) -> f16x8 {
+          if constexpr (PK) {
+            return dequant_u8_h(w[mt][s], w[mt][4 + s], __uint_as_float(w[mt][8]), __uint_as_float(w[mt][10]),
+                                __uint_as_float(w[mt][9]), __uint_as_float(w[mt][11]));
+          } else {
+            const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(h ? (w[mt][4] >> 16) : (w[mt][0] & 0xFFFFu)));
+            return dequant_q4_h(__builtin_amdgcn_perm(w[mt][s + 1], w[mt][s], psel), magic, (cn_half2){d, d});
+          }
+        };
+        // the W dwords and step 0's fragments: reads issued after them are
+        // those of steps 1 .. 3
+        lds_wait<(3 * TN > 15 ? 15 : 3 * TN)>();
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+          for (int i = 0; i < C::WD; i++) reg_fence(w[mt][i]);
+        f16x8 wa[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) wa[mt] = dequant(0, mt);
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+          if (s == 1) lds_wait<2 * TN>();
+          else if (s == 2) lds_wait<TN>();
+          else if (s == 3) lds_wait<0>();
+#pragma unroll
+          for (int cc = 0; cc < TN; cc++) reg_fence(xr[s][cc]);
+          f16x8 xh[TN];
+#pragma unroll
+          for (int cc = 0; cc < TN; cc++) xh[cc] = __builtin_bit_cast(f16x8, xr[s][cc]);
+          f16x8 wn[MT];
+#pragma unroll
+          for (int mt = 0; mt < MT; mt++) {
+#pragma unroll
+            for (int cc = 0; cc < TN; cc++) acc[mt][cc] = mma32(wa[mt], xh[cc], acc[mt][cc]);
+          }
+          if (s < 3) {
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) wn[mt] = dequant(s + 1, mt);
+            // one MFMA, then a share of the next step's dequantization, ...
+            constexpr int kDequantValu = PK ? 24 : 14;  // VALU instructions per dequantized operand
+            constexpr int kPer = (kDequantValu * MT + MT * TN - 1) / (MT * TN);
+#pragma unroll
+            for (int i = 0; i < MT * TN; i++) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+              __builtin_amdgcn_sched_group_barrier(0x002, kPer, 0);
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) wa[mt] = wn[mt];
+          }
+          __builtin_amdgcn_sched_barrier(0);  // the next step's wait stays behind these MFMAs
         }
       }
-      cn_u32x4 xr[4][TN];
+    }
+    if (!sk || (io.c_begin == 0 && io.c_end == nc)) {
 #pragma unroll
-      for (int s = 0; s < 4; s++) lds_read_xtiles<0, TN>(lds_addr(io.xfrag_ptr(st, 0, s, 0)), xr[s]);
-      // Step s's W operands are dequantized during step s-1 (step 0's before
-      // the first MFMA) and interleaved with its MFMAs: one wave issues in
-      // order, so VALU work placed after a run of MFMAs waits behind them
-      // while the matrix pipe drains; between them it runs in their shadow.
-      auto dequant = [&](int s, int mt) -> f16x8 {
-        if constexpr (PK) {
-          return dequant_u8_h(w[mt][s], w[mt][4 + s], __uint_as_float(w[mt][8]), __uint_as_float(w[mt][10]),
-                              __uint_as_float(w[mt][9]), __uint_as_float(w[mt][11]));
-        } else {
-          const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(h ? (w[mt][4] >> 16) : (w[mt][0] & 0xFFFFu)));
-          return dequant_q4_h(__builtin_amdgcn_perm(w[mt][s + 1], w[mt][s], psel), magic, (cn_half2){d, d});
-        }
+      for (int mt = 0; mt < MT; mt++) io.template store<TN>(a, acc[mt], xsc, mt);
+      continue;
+    }
+    // A tile shared by the workgroups gf .. gl (K order).  Each writes its
+    // scaled part to a slot of its own (2g for its range's first segment,
+    // 2g + 1 for its last; float j of thread t at j * CN_BLOCK + t) with
+    // device-scope stores, waits for them, then arrives on the tile's counter.
+    // The last to arrive reads the parts back with device-scope loads (its
+    // own too, so that no accumulator stays live), sums them in K order as
+    // the K-split reduce does (((0 + p_gf) + ...) + p_gl, whatever the
+    // arrival order), applies the epilogue and sets the counter back to zero
+    // for the next launch.  Device-scope accesses go past the XCD's L2 copy
+    // without the L2-wide writeback and invalidation of a device fence (which
+    // would empty the L2 under every other workgroup of the XCD).  No
+    // workgroup waits for another.
+    if constexpr (SK) {
+      constexpr int NF = MT * TN * 16;  // floats per thread
+      auto wg_of = [&](long long unit) {  // the workgroup whose range holds chunk `unit`
+        return unit < u0 ? (int)(unit / nc) : D + (int)(((unit - u0 + 1) * G2 - 1) / units2);
       };
-      // the W dwords and step 0's fragments: reads issued after them are
-      // those of steps 1 .. 3
-      lds_wait<(3 * TN > 15 ? 15 : 3 * TN)>();
+      auto slot = [&](int g) {
+        const bool first_seg = lo_of(g) >= (long long)tile * nc;
+        return a.part + (size_t)(2 * g + (first_seg ? 0 : 1)) * NF * CN_BLOCK + threadIdx.x;
+      };
+      const int gf = wg_of((long long)tile * nc), gl = wg_of((long long)tile * nc + nc - 1);
+      float* mine = slot(blockIdx.x);
 #pragma unroll
       for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-        for (int i = 0; i < C::WD; i++) reg_fence(w[mt][i]);
-      f16x8 wa[MT];
+        for (int cc = 0; cc < TN; cc++)
 #pragma unroll
-      for (int mt = 0; mt < MT; mt++) wa[mt] = dequant(0, mt);
+          for (int v = 0; v < 16; v++)
+            __hip_atomic_store(mine + ((mt * TN + cc) * 16 + v) * CN_BLOCK, acc[mt][cc][v] * xsc[cc], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the part has reached device scope
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        const unsigned arrived = __hip_atomic_fetch_add(a.tile_cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sk_last = arrived == (unsigned)(gl - gf);
+        if (sk_last) __hip_atomic_store(a.tile_cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+      if (sk_last) {
+        // B contributors' parts per batch, every load of a batch in flight
+        // together (one device-scope round trip per batch), added in K order
+        constexpr int B = NF >= 64 ? 1 : 64 / NF;
+        float sum[NF];
 #pragma unroll
-      for (int s = 0; s < 4; s++) {
-        if (s == 1) lds_wait<2 * TN>();
-        else if (s == 2) lds_wait<TN>();
-        else if (s == 3) lds_wait<0>();
+        for (int j = 0; j < NF; j++) sum[j] = 0.f;
+        for (int g0 = gf; g0 <= gl; g0 += B) {
+          float v[B][NF];
 #pragma unroll
-        for (int cc = 0; cc < TN; cc++) reg_fence(xr[s][cc]);
-        f16x8 xh[TN];
+          for (int b = 0; b < B; b++) {
+            const float* p = slot(min(g0 + b, gl));
 #pragma unroll
-        for (int cc = 0; cc < TN; cc++) xh[cc] = __builtin_bit_cast(f16x8, xr[s][cc]);
-        f16x8 wn[MT];
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-#pragma unroll
-          for (int cc = 0; cc < TN; cc++) acc[mt][cc] = mma32(wa[mt], xh[cc], acc[mt][cc]);
-        }
-        if (s < 3) {
-#pragma unroll
-          for (int mt = 0; mt < MT; mt++) wn[mt] = dequant(s + 1, mt);
-          // one MFMA, then a share of the next step's dequantization, ...
-          constexpr int kDequantValu = PK ? 24 : 14;  // VALU instructions per dequantized operand
-          constexpr int kPer = (kDequantValu * MT + MT * TN - 1) / (MT * TN);
-#pragma unroll
-          for (int i = 0; i < MT * TN; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, kPer, 0);
+            for (int j = 0; j < NF; j++) v[b][j] = __hip_atomic_load(p + j * CN_BLOCK, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           }
 #pragma unroll
-          for (int mt = 0; mt < MT; mt++) wa[mt] = wn[mt];
+          for (int b = 0; b < B; b++)
+            if (g0 + b <= gl)
+#pragma unroll
+              for (int j = 0; j < NF; j++) sum[j] += v[b][j];
         }
-        __builtin_amdgcn_sched_barrier(0);  // the next step's wait stays behind these MFMAs
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+          for (int cc = 0; cc < TN; cc++)
+#pragma unroll
+            for (int v4 = 0; v4 < 4; v4++) {
+              const int j = (mt * TN + cc) * 16 + 4 * v4;
+              write_out4(a, a.epi, io.n0 + io.wn * 32 * TN + 32 * cc + io.li,
+                         io.m0 + io.wm * 32 * MT + 32 * mt + 8 * v4 + 4 * h,
+                         f32x4{sum[j], sum[j + 1], sum[j + 2], sum[j + 3]});
+            }
       }
     }
   }
-#pragma unroll
-  for (int mt = 0; mt < MT; mt++) io.template store<TN>(a, acc[mt], xsc, mt);
 }
 
 // Span kernel (the exact-weight product of the forward pass's spans: fp16 x
@@ -1207,6 +1318,8 @@ __global__ __launch_bounds__(CN_BLOCK) void gemm_pack_kernel(int qtype, const ui
 // over a round would run a second round on a few CUs).
 struct GemmShape {
   int tn, splits, stages, mt = 1;
+  int sk_wgs = 0, sk_dp = 0;  // one-plane kernel: stream-K workgroups (0: none), of them whole-tile ones
+  long long tiles = 0;
 };
 
 constexpr int kStages = 3;
@@ -1232,7 +1345,7 @@ int span_ring_bytes(int tn, int stages, int wf) {
   }
 }
 
-GemmShape pick_gemm(int M, int N, int K, int num_cus, bool precise, int wf) {
+GemmShape pick_gemm(int M, int N, int K, int num_cus, bool precise, int wf, bool stream_k = false) {
   GemmShape s;
   const int nchunks = K / 64;
   s.splits = 1;
@@ -1262,38 +1375,56 @@ GemmShape pick_gemm(int M, int N, int K, int num_cus, bool precise, int wf) {
     // from LDS feeding two MFMAs) where that still leaves a tile per CU:
     // 32000 x 2048 at N = 512, 96.7 -> 85.3 us per call; 11008 x 4096 (172
     // such tiles) went 79.3 -> 88.3 us and keeps one.
+    // Stream-K for a grid of 128-row tiles just over one per CU (a partial
+    // second round: 11008 x 4096 at N = 512 has 344 tiles, and 88 CUs ran
+    // two while the rest idled): one whole tile per CU, and a second
+    // workgroup per CU takes an equal share (at least 8 chunks) of the
+    // remaining tiles' chunks.  Measured per call (same box, alternating
+    // builds): 11008 x 4096 N = 512 74.4 -> 71.2 us, N = 480 74.2 -> 70.6;
+    // at 448 tiles (14336 x 4096) 82.1 -> 87.1, so only up to 1.4 tiles per
+    // CU.  Sharing every tile of a smaller grid this way instead of splitting
+    // K measured slower than the split and its reduce pass (4096 x 4096 N =
+    // 512 41.5 -> 46.3 us, N = 8 11008 x 4096 18.7 -> 21.0): a shared tile's
+    // parts cost device-scope round trips (store, arrival, reads).
+    const long long tiles1 = (long long)((M + 127) / 128) * ((N + 32 * s.tn - 1) / (32 * s.tn));
+    if (stream_k && tiles1 > num_cus && tiles1 <= kGemmTileCounters && tiles1 * 5 <= 7LL * num_cus &&
+        (tiles1 - num_cus) * nchunks / num_cus >= 8) {
+      s.tiles = tiles1;
+      s.sk_dp = num_cus;
+      s.sk_wgs = 2 * num_cus;
+      return s;
+    }
     if (s.tn == 4 && (long long)((M + 255) / 256) * ((N + 127) / 128) >= num_cus) s.mt = 2;
     const long long tiles = (long long)((M + 128 * s.mt - 1) / (128 * s.mt)) * ((N + 32 * s.tn - 1) / (32 * s.tn));
+    s.tiles = tiles;
     const long long want = num_cus;
     while (tiles * s.splits < want && nchunks / (s.splits * 2) >= 8 && s.splits < 16) s.splits *= 2;
   }
   return s;
 }
 
-template <int TN, int S, bool PK, int MT, int WNC = 1>
+template <int TN, int S, bool PK, int MT, bool SK = false>
 hipError_t launch_p(const GemmArgs& a, int grid, hipStream_t st) {
-  constexpr int lds = PipeCfg<false, TN, S, PK, MT, WNC>::LDS;
+  constexpr int lds = PipeCfg<false, TN, S, PK, MT, 1>::LDS;
   static_assert(lds <= 160 * 1024, "LDS ring exceeds the CU's 160 KB");
   static std::atomic<uint64_t> lds_done{0};
   if (lds > 64 * 1024) {
-    const hipError_t e = allow_full_lds(reinterpret_cast<const void*>(&gemm_p_kernel<TN, S, PK, MT, WNC>), lds_done);
+    const hipError_t e = allow_full_lds(reinterpret_cast<const void*>(&gemm_p_kernel<TN, S, PK, MT, 1, SK>), lds_done);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((gemm_p_kernel<TN, S, PK, MT, WNC>), dim3(grid), dim3(CN_BLOCK), lds, st, a);
+  hipLaunchKernelGGL((gemm_p_kernel<TN, S, PK, MT, 1, SK>), dim3(grid), dim3(CN_BLOCK), lds, st, a);
   return hipGetLastError();
 }
 
+// Stream-K launches run one-row-tile (MT = 1) instances.
 template <int TN, bool PK>
-hipError_t launch_p_ring(const GemmArgs& a, int stages, int mt, int grid, hipStream_t st) {
-  (void)stages;
-  if constexpr (TN == 1) {
-    return launch_p<TN, 4, PK, 1>(a, grid, st);
-  } else if constexpr (TN == 4) {
-    if (mt == 2) return launch_p<TN, 2, PK, 2>(a, grid, st);
-    return launch_p<TN, 2, PK, 1>(a, grid, st);
-  } else {
-    return launch_p<TN, 2, PK, 1>(a, grid, st);
+hipError_t launch_p_ring(const GemmArgs& a, int mt, int grid, hipStream_t st) {
+  constexpr int S = TN == 1 ? 4 : 2;
+  if (a.sk_wgs > 0) return launch_p<TN, S, PK, 1, true>(a, grid, st);
+  if constexpr (TN == 4) {
+    if (mt == 2) return launch_p<TN, S, PK, 2>(a, grid, st);
   }
+  return launch_p<TN, S, PK, 1>(a, grid, st);
 }
 
 template <int TN, int S, int WF>
@@ -1329,9 +1460,9 @@ hipError_t launch_kernel(const GemmArgs& a, const GemmShape& s, bool precise, in
   const bool pk = a.packed != 0;
   const int tn = s.tn;
   if (precise) return tn == 1 ? launch_s_fmt<1>(a, s.stages, grid, st) : launch_s_fmt<2>(a, s.stages, grid, st);
-  if (tn == 1) return pk ? launch_p_ring<1, true>(a, s.stages, 1, grid, st) : launch_p_ring<1, false>(a, s.stages, 1, grid, st);
-  if (tn == 2) return pk ? launch_p_ring<2, true>(a, s.stages, 1, grid, st) : launch_p_ring<2, false>(a, s.stages, 1, grid, st);
-  return pk ? launch_p_ring<4, true>(a, s.stages, s.mt, grid, st) : launch_p_ring<4, false>(a, s.stages, s.mt, grid, st);
+  if (tn == 1) return pk ? launch_p_ring<1, true>(a, 1, grid, st) : launch_p_ring<1, false>(a, 1, grid, st);
+  if (tn == 2) return pk ? launch_p_ring<2, true>(a, 1, grid, st) : launch_p_ring<2, false>(a, 1, grid, st);
+  return pk ? launch_p_ring<4, true>(a, s.mt, grid, st) : launch_p_ring<4, false>(a, s.mt, grid, st);
 }
 
 }  // namespace
@@ -1381,8 +1512,9 @@ hipError_t gemm_pack_launch(int qtype, const void* w, int M, int K, void* dst, h
   return hipGetLastError();
 }
 
-size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool precise, int wfmt) {
-  const GemmShape s = pick_gemm(M, N, K, num_cus, precise, wfmt);
+size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool precise, int wfmt, bool stream_k) {
+  const GemmShape s = pick_gemm(M, N, K, num_cus, precise, wfmt, stream_k && !precise);
+  if (s.sk_wgs > 0) return (size_t)2 * s.sk_wgs * (128 * s.mt) * (32 * s.tn) * sizeof(float);
   return s.splits > 1 ? (size_t)s.splits * N * M * sizeof(float) : 0;
 }
 
@@ -1399,12 +1531,17 @@ hipError_t gemm_launch(const GemmArgs& a_in, int num_cus, hipStream_t st, int* s
   // kernels apply no other epilogue)
   if (splits_left && a_in.epi != GEMV_EPI_STORE && a_in.epi != GEMV_EPI_ADD) return hipErrorInvalidValue;
   if (a_in.epi == GEMV_EPI_SWIGLU && (!a_in.hb || !a_in.hb_lo)) return hipErrorInvalidValue;
-  const GemmShape s = pick_gemm(a_in.M, a_in.N, a_in.K, num_cus, precise, a_in.packed);
+  const GemmShape s =
+      pick_gemm(a_in.M, a_in.N, a_in.K, num_cus, precise, a_in.packed, a_in.tile_cnt != nullptr && !precise);
   GemmArgs a = a_in;
   a.splits = s.splits;
-  if (s.splits > 1 && !a.part) return hipErrorInvalidValue;
-  const long long grid =
-      (long long)((a.M + 128 * s.mt - 1) / (128 * s.mt)) * ((a.N + 32 * s.tn - 1) / (32 * s.tn)) * s.splits;
+  a.sk_wgs = s.sk_wgs;
+  a.sk_dp = s.sk_dp;
+  a.sk_tiles = (int)s.tiles;
+  if ((s.splits > 1 || s.sk_wgs > 0) && !a.part) return hipErrorInvalidValue;
+  const long long grid = s.sk_wgs > 0 ? s.sk_wgs
+                                      : (long long)((a.M + 128 * s.mt - 1) / (128 * s.mt)) *
+                                            ((a.N + 32 * s.tn - 1) / (32 * s.tn)) * s.splits;
   if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
   hipError_t e = launch_kernel(a, s, precise, (int)grid, st);
   if (splits_left) *splits_left = 0;

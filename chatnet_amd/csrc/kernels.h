@@ -113,9 +113,16 @@ struct GemmArgs {
   uint16_t* hb;           // SWIGLU target: fp16 high parts of h (cn_span_pos order)
   uint16_t* hb_lo;        // SWIGLU target: fp16 low parts of h
   int ldh;
-  float* part;            // K-split partials, gemm_workspace_bytes() bytes
+  float* part;            // K-split partials (stream-K: each workgroup's two part slots),
+                          // gemm_workspace_bytes() bytes
+  unsigned* tile_cnt;     // one-plane kernel: kGemmTileCounters arrival counters, zero before the
+                          // launch and left zero by it; nullptr: no stream-K launch
   int splits;             // set by gemm_launch
+  int sk_wgs, sk_dp;      // set by gemm_launch: stream-K workgroups (0: none), of them whole-tile ones
+  int sk_tiles;           // set by gemm_launch: the stream-K launch's tiles
 };
+// Arrival counters a stream-K launch may use (one per tile).
+constexpr int kGemmTileCounters = 1024;
 bool gemm_supports(int qtype, int K);
 // Packed weights: every 64 weights of a row become one 96-byte unit of 64 u8
 // codes, 4 fp32 scales and 4 fp32 offsets (one pair per 16 weights), with
@@ -126,7 +133,9 @@ constexpr int kGemmPackUnit = 96;
 bool gemm_pack_supports(int qtype, int K);
 size_t gemm_pack_bytes(int M, int K);
 hipError_t gemm_pack_launch(int qtype, const void* w, int M, int K, void* dst, hipStream_t st);
-size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool precise, int wfmt);
+// stream_k: the caller passes GemmArgs::tile_cnt (the one-plane kernel may
+// then share the tiles past one per CU between workgroups).
+size_t gemm_workspace_bytes(int M, int N, int K, int num_cus, bool precise, int wfmt, bool stream_k = false);
 // With splits_left, a launch whose K is split leaves its partial tiles in
 // a.part ([splits][N][M]) unreduced and reports the split count there (0 when
 // the epilogue ran): the caller folds them into its next kernel

@@ -110,6 +110,38 @@ def test_gemm_columns_of_very_different_magnitudes():
         assert normwise(y[n], r[n]) <= 5e-3, (n, mags[n], normwise(y[n], r[n]))
 
 
+@pytest.mark.parametrize("qtype,shapes", [
+    (Q4_0, [(11008, 4096, 512), (4096, 4096, 64), (11008, 4096, 480), (11008, 4096, 512)]),
+    (Q4_0, [(10240, 4096, 512), (2048, 11008, 8), (10240, 4096, 512)]),
+    (12, [(11008, 4096, 512), (11008, 4096, 512)]),   # Q4_K: packed units
+])
+def test_stream_k_calls_in_a_row_repeat_bit_for_bit(qtype, shapes):
+    """Tile grids just over one tile per CU (344 and 320 tiles of 128 x 128
+    here) are stream-K launches: one whole tile per CU, and a second
+    workgroup per CU takes an equal share of the remaining tiles' K chunks; a
+    tile shared by several is summed by the last of them to arrive, in K
+    order, from the parts each wrote.  Calls in a row on one stream (each
+    must leave its tile counters at zero for the next, other shapes between)
+    match the oracle, and a repeated call is bit-identical to the first
+    whatever the arrival order."""
+    seen = {}
+    for (M, K, N) in shapes:
+        announce(f"stream-k type={qtype} M={M} K={K} N={N}")
+        t = synth.tensor(qtype, 15, f"sk{qtype}-{M}x{K}", M, K)
+        x = synth.normal(15, f"skx{N}x{K}", N * K, 1.0).reshape(N, K)
+        y = gpu_matmul(qtype, t.data, x, M, K)
+        assert np.all(np.isfinite(y))
+        key = (M, K, N)
+        if key in seen:
+            assert np.array_equal(seen[key], y), (key, float(np.max(np.abs(seen[key] - y))))
+            continue
+        w = oracle.dequant(qtype, t.data, M * K).reshape(M, K).astype(np.float64)
+        r = x.astype(np.float64) @ w.T
+        worst = max(normwise(y[n], r[n]) for n in range(N))
+        assert worst <= TOL, (key, worst)
+        seen[key] = y
+
+
 def test_gemm_columns_match_gemv():
     """Each GEMM column is the N=1 product of that column (same weights)."""
     M, K, N = 2048, 2048, 24

@@ -2,8 +2,11 @@
 scratch is the library's fixed per-device array) against chatnet_matmul on
 the same inputs, through the C ABI: two calls in a row, the second smaller,
 so the second runs on scratch the first left behind.  Bar: the batched MFMA
-GEMM's 1e-2 normwise (the same kernels run, so the outputs are expected to be
-identical), and the GEMV path's 1e-3."""
+GEMM's 1e-2 normwise, and the GEMV path's 1e-3.  The outputs are identical
+where both run the same launch; for 11008 x 4096 at N = 512 chatnet_matmul
+shares the tiles past one per CU between workgroups (stream-K, summed in
+another order) and the no-allocation variant, which keeps no tile counters,
+runs the plain tile grid."""
 import numpy as np
 import pytest
 
