@@ -142,6 +142,50 @@ def test_stream_k_calls_in_a_row_repeat_bit_for_bit(qtype, shapes):
         seen[key] = y
 
 
+@pytest.mark.parametrize("M,K,N", [(11008, 4096, 512), (4096, 4096, 512), (11008, 4096, 8)])
+def test_captured_matmul_replays_match_eager(M, K, N):
+    """chatnet_matmul captured into a HIP graph, after an uncaptured call of
+    the same size has grown the stream's workspace: every replay, with other
+    eager work on the stream between replays, writes the eager call's output
+    bit for bit.  The stream-K launch (11008 x 4096 at N = 512) must leave
+    its tile counters at zero for the next replay, and the K-split launches
+    (4096 x 4096 at N = 512, 11008 x 4096 at N = 8) rewrite their partials
+    and reduce them again."""
+    from chatnet_amd import hiprt, ops
+
+    announce(f"captured matmul q4_0 M={M} K={K} N={N}")
+    t = synth.tensor(Q4_0, 16, f"graph{M}x{K}", M, K)
+    x = synth.normal(16, f"graphx{N}x{K}", N * K, 1.0)
+    w_d = hiprt.DeviceBuffer.from_numpy(t.data, pad=256)
+    x_d = hiprt.DeviceBuffer.from_numpy(x)
+    y_eager, y_graph = hiprt.DeviceBuffer(4 * N * M), hiprt.DeviceBuffer(4 * N * M)
+    # other work for the stream between replays: a smaller product on the
+    # same workspace (it does not regrow it)
+    M2, K2, N2 = 2048, 2048, 64
+    t2 = synth.tensor(Q4_0, 17, "graph-other", M2, K2)
+    w2_d = hiprt.DeviceBuffer.from_numpy(t2.data, pad=256)
+    x2_d = hiprt.DeviceBuffer.from_numpy(synth.normal(17, "graph-other-x", N2 * K2, 1.0))
+    y2_d = hiprt.DeviceBuffer(4 * N2 * M2)
+    stream = hiprt.Stream()
+    ops.matmul_ptr(Q4_0, w_d.ptr, x_d.ptr, y_eager.ptr, M, K, N, stream.h)
+    stream.synchronize()
+    ref = y_eager.to_numpy(np.float32, N * M)
+    assert np.all(np.isfinite(ref))
+    graph = hiprt.Graph(stream, lambda: ops.matmul_ptr(Q4_0, w_d.ptr, x_d.ptr, y_graph.ptr, M, K, N, stream.h))
+    for rep in range(3):
+        y_graph.fill(0xFF)  # NaN pattern: a replay that writes nothing fails
+        hiprt.synchronize()
+        graph.launch()
+        stream.synchronize()
+        got = y_graph.to_numpy(np.float32, N * M)
+        assert np.array_equal(got, ref), (rep, float(np.nanmax(np.abs(got - ref))))
+        ops.matmul_ptr(Q4_0, w2_d.ptr, x2_d.ptr, y2_d.ptr, M2, K2, N2, stream.h)
+        stream.synchronize()
+    del graph
+    for b in (w_d, x_d, y_eager, y_graph, w2_d, x2_d, y2_d):
+        b.free()
+
+
 def test_gemm_columns_match_gemv():
     """Each GEMM column is the N=1 product of that column (same weights)."""
     M, K, N = 2048, 2048, 24
