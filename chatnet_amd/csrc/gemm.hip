@@ -355,7 +355,8 @@ struct TileIO {
     wn = wave / C::WM;
     h = lane >> 5;
     li = lane & 31;
-    if (a.sk_wgs > 0) return;
+    ks = 0;
+    if (a.sk_wgs > 0) return;  // stream-K launches do not split K (a.splits == 1)
     int bid = blockIdx.x;
     ks = bid % a.splits;
     bid /= a.splits;
