@@ -114,6 +114,9 @@ def test_gemm_columns_of_very_different_magnitudes():
     (Q4_0, [(11008, 4096, 512), (4096, 4096, 64), (11008, 4096, 480), (11008, 4096, 512)]),
     (Q4_0, [(10240, 4096, 512), (2048, 11008, 8), (10240, 4096, 512)]),
     (12, [(11008, 4096, 512), (11008, 4096, 512)]),   # Q4_K: packed units
+    # ragged: a partial last row tile (11000 rows), a partial last column tile
+    # (500 columns) and 65 chunks per tile (K = 4160), still 344 tiles
+    (Q4_0, [(11000, 4160, 500), (11000, 4160, 500)]),
 ])
 def test_stream_k_calls_in_a_row_repeat_bit_for_bit(qtype, shapes):
     """Tile grids just over one tile per CU (344 and 320 tiles of 128 x 128
