@@ -253,7 +253,12 @@ CHATNET_API int chatnet_get_logits(chatnet_model* m, float* logits_host);
  * M*(K/64)*96 bytes, giving the same dequantized values); any other call
  * (N < 8, F32, F16) runs the fused GEMV once per column, which reads Q4_1,
  * Q5_0, Q5_1, Q2_K, Q8_K and the IQ types from that same re-encoded
- * copy, made in the workspace first.  The GEMM's workspace is allocated on first use
+ * copy, made in the workspace first.  A GEMM whose grid of 128 x 128 tiles
+ * is just over one tile per CU (e.g. 11008 x 4096 at N = 512) runs as a
+ * stream-K launch: one whole tile per CU, the other tiles' K chunks shared
+ * out evenly, a shared tile summed in K order by its last contributor (the
+ * result does not depend on arrival order) with arrival counters kept at the
+ * start of the workspace.  The GEMM's workspace is allocated on first use
  * per (device, stream) and kept until the process ends (a buffer it outgrows
  * is retired, not freed, since a captured graph may still read it).  A call
  * on a stream under HIP graph capture cannot allocate: it fails with
@@ -269,7 +274,9 @@ CHATNET_API int chatnet_matmul(uint32_t ggml_type, const void* w_dev, const floa
  * that forbid hipMalloc.  No counterpart in the reference.  Same arguments,
  * kernels and results as chatnet_matmul for Q4_0 and for the types read
  * only as packed units (Q4_1, Q5_0, Q5_1, Q2_K, Q8_K and the IQ types,
- * whose packed copy of W, M*(K/64)*96 bytes, goes into the scratch); Q8_0,
+ * whose packed copy of W, M*(K/64)*96 bytes, goes into the scratch), except
+ * that it runs no stream-K launch: where chatnet_matmul shares tiles it runs
+ * the plain tile grid, the same product summed in another order.  Q8_0,
  * Q3_K, Q4_K, Q5_K and Q6_K run the fused GEMV once per column on their stored
  * blocks.  The scratch (fp16 x, its per-column scales, the K-split partials
  * and the packed W) lives
