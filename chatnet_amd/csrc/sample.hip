@@ -9,15 +9,19 @@
 //   cutoff = first i with sum(p[0..i]) >= top_p, else k         (:70-80)
 //   renormalise the cutoff tokens, first i with r < acc         (:83-106)
 // The reference finds the top k by quickselect and insertion sort; here a
-// 4-pass radix select on the float bit patterns (p >= 0, so they order like
-// the values) finds the k-th largest key, the keys at or above it are
-// gathered (an index-ordered scan instead when more than 1024 tie with it),
-// and a bitonic sort in LDS orders them by (p descending, index ascending),
-// the first k being the winners.  Equal probabilities may therefore come out in another order
-// than the reference's quickselect leaves them.  The softmax sum is a tree
-// here and a left-to-right sum in the reference (a few ulps apart); the
-// top-p, renormalisation and draw loops run on one thread in the reference's
-// order, with products kept apart from the sums as the reference rounds them.
+// radix select on the float bit patterns (p >= 0, so they order like the
+// values), a byte per pass, narrows the keys down to the k-th largest, or
+// stops early once at most 64 keys lie at or above the selected bin.  The
+// keys at or above that bound are gathered (an index-ordered scan instead
+// when more than 1024 tie with the k-th), and a bitonic sort orders them by
+// (p descending, index ascending), the first k being the winners: across
+// the lanes of one wave for at most 64 keys, in LDS for more.  Equal
+// probabilities may therefore come out in another order than the
+// reference's quickselect leaves them.  The softmax sum is a tree here and
+// a left-to-right sum in the reference (a few ulps apart); the top-p,
+// renormalisation and draw loops run in the reference's order on one list
+// (wave 0's lanes or LDS), with products kept apart from the sums as the
+// reference rounds them.
 #include "device_common.h"
 #include "kernels.h"
 
@@ -68,12 +72,16 @@ __global__ __launch_bounds__(kST) void sample_kernel(const float* __restrict__ l
                                                      int* out_tokens, int out_cap, float* __restrict__ p) {
   __shared__ float red[kSW];
   __shared__ int hist[256 * 8];
-  __shared__ int sel[2];
+  __shared__ int sel[3];
   __shared__ int wcnt[2][kSW];
   __shared__ float cp[kSampleMaxK];
   __shared__ int ci[kSampleMaxK];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (out_tokens && state[kDecStop]) return;  // the decode loop stopped at EOS
+  // the decode loop's stop flag (set at EOS) and step: vector loads consumed
+  // at the end, so the logits loads go out without waiting for them; a
+  // stopped loop's launch computes and writes nothing
+  const int stop_v = out_tokens ? cn_load_late(state + kDecStop) : 0;
+  const int step_v = cn_load_late(state + kDecStep);
   const float inv_temp = prm->inv_temp;
   const float top_p = prm->top_p;
   const int k = prm->top_k < n ? prm->top_k : n;
@@ -88,12 +96,17 @@ __global__ __launch_bounds__(kST) void sample_kernel(const float* __restrict__ l
     else p[tid + kST * j] = x;
   };
 
-  // temperature and softmax
+  // temperature and softmax (REG: every logits load issued before the first
+  // use of the parameters)
   float mx = -INFINITY;
+  if constexpr (REG) {
+#pragma unroll
+    for (int j = 0; j < nj; j++) rv[j] = tid + kST * j < n ? logits[tid + kST * j] : 0.f;
+  }
 #pragma unroll
   for (int j = 0; j < nj; j++) {
     const int i = tid + kST * j;
-    const float v = i < n ? __fmul_rn(logits[i], inv_temp) : -INFINITY;
+    const float v = i < n ? __fmul_rn(REG ? rv[j] : logits[i], inv_temp) : -INFINITY;
     if (REG || i < n) put(j, v);
     mx = fmaxf(mx, v);
   }
@@ -157,16 +170,24 @@ __global__ __launch_bounds__(kST) void sample_kernel(const float* __restrict__ l
         }
         sel[0] = 255 - 4 * lane - j;
         sel[1] = remaining - cum;
+        sel[2] = c[j];
       }
     }
     __syncthreads();
     prefix |= (uint32_t)sel[0] << shift;
     pmask |= 255u << shift;
     remaining = sel[1];
+    // keys at or above the selected bin's lower bound: the k - remaining
+    // taken before it and the whole bin.  At most a wave's worth: gather them
+    // all now, the sort below still leaves the same k first.
+    const int at_or_above = k - sel[1] + sel[2];
     __syncthreads();
+    if (at_or_above <= CN_WAVE) break;
   }
-  // keys above `prefix` are all taken; of those equal to it, the first
-  // `remaining` in index order
+  // after all four passes `prefix` is the k-th largest key: keys above it are
+  // all taken, of those equal to it the first `remaining` in index order;
+  // after an early exit it is the lower bound of a bin, with at most a wave's
+  // worth of keys at or above it
 
   // Gather every key >= prefix in any order: the sort below orders them by
   // (p descending, index ascending), so its first k entries are the winners.
@@ -226,61 +247,95 @@ __global__ __launch_bounds__(kST) void sample_kernel(const float* __restrict__ l
     m = k;
   }
 
-  // bitonic sort of the gathered keys: p descending, then index ascending
-  int k2 = 1;
-  while (k2 < m) k2 <<= 1;
-  for (int j = m + tid; j < k2; j += kST) {
-    cp[j] = -1.0f;
-    ci[j] = 0x7FFFFFFF;
-  }
-  __syncthreads();
-  for (int size = 2; size <= k2; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      const int o = tid ^ stride;
-      if (tid < k2 && o > tid) {
-        const bool first = (tid & size) == 0;
-        const float pa = cp[tid], pb = cp[o];
-        const int ia = ci[tid], ib = ci[o];
-        const bool b_first = pb > pa || (pb == pa && ib < ia);
-        if (b_first == first) {
-          cp[tid] = pb;
-          cp[o] = pa;
-          ci[tid] = ib;
-          ci[o] = ia;
-        }
-      }
-      __syncthreads();
-    }
-  }
-
-  if (tid == 0) {
+  // TemperatureSampler.cs:70-106 in the reference's order on the sorted list
+  // (entry i through P(i) and I(i)): the top-p cutoff, the renormalising sum
+  // and the draw, products kept apart from the sums as the reference rounds
+  // them
+  auto decide = [&](auto P, auto I) -> int {
     float cumulative = 0.f;
     int cutoff = k;
     for (int i = 0; i < k; i++) {
-      cumulative += cp[i];
+      cumulative += P(i);
       if (cumulative >= top_p) {
         cutoff = i + 1;
         break;
       }
     }
     float sum = 0.f;
-    for (int i = 0; i < cutoff; i++) sum += cp[i];
+    for (int i = 0; i < cutoff; i++) sum += P(i);
     const float inv = 1.0f / sum;
-    const int step = state[kDecStep];
-    const float r = draws ? draws[step] : prm->draw;
+    const float r = draws ? draws[step_v] : prm->draw;
     float acc = 0.f;
-    int tok = ci[cutoff - 1];
+    int t = I(cutoff - 1);
     for (int i = 0; i < cutoff; i++) {
-      acc += __fmul_rn(cp[i], inv);
+      acc += __fmul_rn(P(i), inv);
       if (r < acc) {
-        tok = ci[i];
+        t = I(i);
         break;
       }
     }
+    return t;
+  };
+  int tok = 0;
+  if (m <= CN_WAVE) {
+    // at most a wave's worth of keys: wave 0 sorts them across its lanes with
+    // the block sort's network and test below (p descending, then index
+    // ascending; lanes past m hold keys that sort last), then runs the loops
+    // on them, every lane the same values, entry i read from lane i
+    if (wave == 0) {
+      float pv = lane < m ? cp[lane] : -1.0f;
+      int iv = lane < m ? ci[lane] : 0x7FFFFFFF;
+      for (int size = 2; size <= CN_WAVE; size <<= 1)
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+          const float po = __shfl_xor(pv, stride, CN_WAVE);
+          const int io = __shfl_xor(iv, stride, CN_WAVE);
+          const bool lo = (lane & stride) == 0;  // the pair's lower lane holds a, the upper b
+          const float pa = lo ? pv : po, pb = lo ? po : pv;
+          const int ia = lo ? iv : io, ib = lo ? io : iv;
+          const bool b_first = pb > pa || (pb == pa && ib < ia);
+          if (b_first == ((lane & size) == 0)) {
+            pv = po;
+            iv = io;
+          }
+        }
+      tok = decide([&](int i) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pv), i)); },
+                   [&](int i) { return __builtin_amdgcn_readlane(iv, i); });
+    }
+  } else {
+    // bitonic sort of the gathered keys: p descending, then index ascending
+    int k2 = 1;
+    while (k2 < m) k2 <<= 1;
+    for (int j = m + tid; j < k2; j += kST) {
+      cp[j] = -1.0f;
+      ci[j] = 0x7FFFFFFF;
+    }
+    __syncthreads();
+    for (int size = 2; size <= k2; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        const int o = tid ^ stride;
+        if (tid < k2 && o > tid) {
+          const bool first = (tid & size) == 0;
+          const float pa = cp[tid], pb = cp[o];
+          const int ia = ci[tid], ib = ci[o];
+          const bool b_first = pb > pa || (pb == pa && ib < ia);
+          if (b_first == first) {
+            cp[tid] = pb;
+            cp[o] = pa;
+            ci[tid] = ib;
+            ci[o] = ia;
+          }
+        }
+        __syncthreads();
+      }
+    }
+    if (tid == 0) tok = decide([&](int i) { return cp[i]; }, [&](int i) { return ci[i]; });
+  }
+
+  if (tid == 0 && !stop_v) {
     state[kDecTok] = tok;
     if (out_tokens) {
-      if (step < out_cap) out_tokens[step] = tok;
-      state[kDecStep] = step + 1;
+      if (step_v < out_cap) out_tokens[step_v] = tok;
+      state[kDecStep] = step_v + 1;
       if (tok == state[kDecEos]) state[kDecStop] = 1;
     }
     state[kDecPos] = state[kDecPos] + 1;
