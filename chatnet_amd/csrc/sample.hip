@@ -103,6 +103,9 @@ __global__ __launch_bounds__(kST) void sample_kernel(const float* __restrict__ l
 #pragma unroll
     for (int j = 0; j < nj; j++) rv[j] = tid + kST * j < n ? logits[tid + kST * j] : 0.f;
   }
+  // this step's draw, loaded while the logits arrive (it waits for the step
+  // only, which was loaded first)
+  const float r_draw = draws ? draws[step_v] : prm->draw;
 #pragma unroll
   for (int j = 0; j < nj; j++) {
     const int i = tid + kST * j;
@@ -248,9 +251,9 @@ __global__ __launch_bounds__(kST) void sample_kernel(const float* __restrict__ l
   }
 
   // TemperatureSampler.cs:70-106 in the reference's order on the sorted list
-  // (entry i through P(i) and I(i)): the top-p cutoff, the renormalising sum
-  // and the draw, products kept apart from the sums as the reference rounds
-  // them
+  // in LDS (entry i through P(i) and I(i)): the top-p cutoff, the
+  // renormalising sum and the draw, products kept apart from the sums as the
+  // reference rounds them
   auto decide = [&](auto P, auto I) -> int {
     float cumulative = 0.f;
     int cutoff = k;
@@ -264,7 +267,7 @@ __global__ __launch_bounds__(kST) void sample_kernel(const float* __restrict__ l
     float sum = 0.f;
     for (int i = 0; i < cutoff; i++) sum += P(i);
     const float inv = 1.0f / sum;
-    const float r = draws ? draws[step_v] : prm->draw;
+    const float r = r_draw;
     float acc = 0.f;
     int t = I(cutoff - 1);
     for (int i = 0; i < cutoff; i++) {
@@ -280,8 +283,8 @@ __global__ __launch_bounds__(kST) void sample_kernel(const float* __restrict__ l
   if (m <= CN_WAVE) {
     // at most a wave's worth of keys: wave 0 sorts them across its lanes with
     // the block sort's network and test below (p descending, then index
-    // ascending; lanes past m hold keys that sort last), then runs the loops
-    // on them, every lane the same values, entry i read from lane i
+    // ascending; lanes past m hold keys that sort last), then makes decide's
+    // choice on them, entry i in lane i
     if (wave == 0) {
       float pv = lane < m ? cp[lane] : -1.0f;
       int iv = lane < m ? ci[lane] : 0x7FFFFFFF;
@@ -298,8 +301,29 @@ __global__ __launch_bounds__(kST) void sample_kernel(const float* __restrict__ l
             iv = io;
           }
         }
-      tok = decide([&](int i) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pv), i)); },
-                   [&](int i) { return __builtin_amdgcn_readlane(iv, i); });
+      // decide's three loops without a branch per entry: running sums in list
+      // order, one add per entry as the reference rounds them, each lane
+      // keeping the value after its own entry.  The cutoff is the first lane
+      // (below k) whose running sum reaches top_p; the renormalising sum over
+      // entries [0, cutoff) is the same sequence of adds, so it is the running
+      // sum at cutoff - 1; the draw takes the first lane (below cutoff) whose
+      // running sum of products exceeds it, else entry cutoff - 1.
+      auto running = [&](float v) {
+        float a = 0.f, mine = 0.f;
+#pragma unroll
+        for (int i = 0; i < CN_WAVE; i++) {
+          a += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
+          mine = lane == i ? a : mine;
+        }
+        return mine;
+      };
+      const float cum = running(pv);
+      const uint64_t over = __ballot(lane < k && cum >= top_p);
+      const int cutoff = over ? __ffsll((unsigned long long)over) : k;
+      const float inv = 1.0f / __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cum), cutoff - 1));
+      const float acc = running(__fmul_rn(pv, inv));
+      const uint64_t hit = __ballot(lane < cutoff && r_draw < acc);
+      tok = __builtin_amdgcn_readlane(iv, hit ? __ffsll((unsigned long long)hit) - 1 : cutoff - 1);
     }
   } else {
     // bitonic sort of the gathered keys: p descending, then index ascending
