@@ -43,10 +43,13 @@ def test_sample_matches_oracle(cfg_name):
             # the raw logits of a random-weight model are nearly flat; scale
             # the temperature so the distributions range from peaked to flat
             spread = float(np.std(logits))
+            # k = 64 and 65: the largest top-k sorted across one wave's lanes and
+            # the smallest sorted in LDS
             for j, (t, k, p) in enumerate([(0.05, 40, 0.9), (0.3, 40, 0.9), (1.0, 40, 0.95), (1.0, 1, 0.9),
-                                           (0.5, 1024, 1.0), (2.0, 7, 0.5), (0.2, 300, 0.99)]):
+                                           (0.5, 1024, 1.0), (2.0, 7, 0.5), (0.2, 300, 0.99), (1.0, 64, 1.0),
+                                           (1.0, 65, 1.0)]):
                 t = t * spread
-                draw = float(draws[(pos * 7 + j) % draws.size])
+                draw = float(draws[(pos * 9 + j) % draws.size])
                 got = m.sample(t, k, p, draw)
                 agree += _check(got, logits, t, k, p, draw, f"pos {pos} T {t:.3g} k {k} p {p}")
                 total += 1
