@@ -41,7 +41,7 @@ SWEEP = [(2048, 2048), (256, 2048), (5632, 2048), (2048, 5632), (32000, 2048), (
 ROOF_SHAPE = (11008, 4096)
 # legs --only can select
 LEGS = ("gemv_sweep", "roofline", "kquant", "gemm_sweep", "gemm_counters", "gemv_counters", "llama7b_decode",
-        "tinyllama_decode", "prefill")
+        "tinyllama_decode", "prefill", "sampled")
 # one N = 1 chatnet_matmul per (type, M, K) for counter runs: the 7B shapes of
 # the Q4_0 and K-quant decodes
 COUNTER_GEMVS = [(2, 11008, 4096), (2, 4096, 11008), (12, 4096, 4096), (12, 11008, 4096), (14, 4096, 11008),
@@ -581,6 +581,10 @@ def main():
                 tiny_sampled = sampled_run(w1.config.replace(context_length=2048), ck1, w1.prompt(), 128)
                 log(f"TinyLlama decode, temperature sampler on the device: {tiny_sampled} tok/s")
             del ck1
+        if args.only == "sampled":  # the sampled decode alone (for profiling)
+            w1 = WORKLOADS["tinyllama_q4_0_decode"]
+            tiny_sampled = sampled_run(w1.config.replace(context_length=2048), w1.checkpoint(), w1.prompt(), 128)
+            log(f"TinyLlama decode, temperature sampler on the device: {tiny_sampled} tok/s")
         if want("prefill"):
             w2 = WORKLOADS["tinyllama_q4_0_prefill"]
             log(f"TinyLlama {w2.n_prompt}-token prefill + {w2.n_decode} decode")
